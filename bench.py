@@ -1,0 +1,383 @@
+"""Benchmark of the MI355X hot path on one GPU; prints ONE JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only attn,lut,kv,gemm]
+
+Headline (`value`): int8-KV GQA decode attention
+(B=32, H=32, Hkv=8, D=128, ragged L_b ~ U[512, 32768], bucket 32768, Q bf16,
+cache filled by the int8 quantize+append op) in tokens/s = B / step time.
+A step is one DecodeAttentionI8 dispatch over the whole batch, inputs
+resident in HBM. The other configs are reported under "components":
+LUT Gelem/s (config 1), GEMM TFLOP/s (config 2), KV append (config 3).
+Every number comes from HIP events on the stream the kernels run on.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0      # dense bf16 MFMA
+FP32_PEAK_TFLOPS = 157.3       # fp32 matrix
+METRIC = "int8-KV decode attn tok/s & HBM GB/s; bf16 LUT Gelem/s; GEMM TFLOP/s"
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--only", default="attn,lut,kv,gemm")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--seed", type=int, default=1234)
+    return p.parse_args()
+
+
+class Timer:
+    """HIP events recorded on the backend's stream around each timed dispatch."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.pairs = []
+
+    def __enter__(self):
+        s = self.torch.cuda.Event(enable_timing=True)
+        s.record()
+        self._s = s
+        return self
+
+    def __exit__(self, *exc):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.pairs.append((self._s, e))
+
+    def mean_ms(self):
+        self.torch.cuda.synchronize()
+        return sum(s.elapsed_time(e) for s, e in self.pairs) / max(1, len(self.pairs))
+
+
+def bf16_normal(torch, shape, gen, outlier_frac=0.0):
+    x = torch.randn(shape, generator=gen, device="cuda", dtype=torch.float32)
+    if outlier_frac > 0:
+        d = shape[-1]
+        nout = max(1, math.ceil(outlier_frac * d))
+        ch = torch.randperm(d, generator=gen, device="cuda")[:nout]
+        x[..., ch] *= 20.0
+    return x.to(torch.bfloat16)
+
+
+# --------------------------------------------------------------- config 4 ----
+def bench_attn(torch, be, args, rep):
+    import numpy as np
+    from hologram_amd import (DTYPE_BF16, BufferRef, DecodeAttentionI8Call, DeviceWorkspace,
+                              KernelCall, KvQuantAppendCall)
+    B, H, Hkv, D, bucket = 32, 32, 8, 128, 32768
+    rng = np.random.default_rng(args.seed)
+    lens = rng.integers(512, 32769, size=B).astype(np.uint32)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed)
+    planes = B * Hkv
+    ws = DeviceWorkspace()
+    kq = torch.empty(planes * bucket * D, dtype=torch.int8, device="cuda")
+    vq = torch.empty_like(kq)
+    ks = torch.empty(planes * bucket, dtype=torch.float32, device="cuda")
+    vs = torch.empty_like(ks)
+    pos0 = torch.zeros(1, dtype=torch.int32, device="cuda")
+    # fill both caches through the int8 quantize+append op (config 3's scheme)
+    for cq, cs in ((kq, ks), (vq, vs)):
+        for p0 in range(0, planes, 32):       # 32 planes (256 MiB of bf16) per call
+            src = bf16_normal(torch, (32, bucket, D), gen, 0.02)
+            fill = DeviceWorkspace()
+            fill.bind(0, src)
+            fill.bind(1, pos0)
+            fill.bind(2, cq)
+            fill.bind(3, cs)
+            off_q, off_s = p0 * bucket * D, p0 * bucket * 4
+            call = KernelCall.KvQuantAppend(KvQuantAppendCall(
+                BufferRef(0), BufferRef(1), BufferRef(2, off_q, 32 * bucket * D),
+                BufferRef(3, off_s, 32 * bucket * 4), BufferRef(2, off_q, 32 * bucket * D),
+                BufferRef(3, off_s, 32 * bucket * 4), 32, bucket, bucket, D, DTYPE_BF16))
+            be.dispatch(call, fill)
+            be.synchronize()
+            del src
+    nq = 4   # rotate fresh queries every step
+    qs = [bf16_normal(torch, (B * H * D,), gen) for _ in range(nq)]
+    out = torch.empty(B * H * D, dtype=torch.bfloat16, device="cuda")
+    lens_t = torch.from_numpy(lens.astype(np.int32)).cuda()
+    for s, t in enumerate([qs[0], kq, vq, ks, vs, lens_t, out]):
+        ws.bind(s, t)
+    for i in range(1, nq):
+        ws.bind(7 + i, qs[i])
+    calls = []
+    for i in range(nq):
+        qslot = 0 if i == 0 else 7 + i
+        calls.append(KernelCall.DecodeAttentionI8(DecodeAttentionI8Call(
+            BufferRef(qslot), *[BufferRef(s) for s in range(1, 7)], B, H, Hkv, bucket, D, 0,
+            DTYPE_BF16)))
+    for i in range(args.warmup):
+        be.dispatch(calls[i % nq], ws)
+    be.synchronize()
+    timer = Timer(torch)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        with timer:
+            be.dispatch(calls[i % nq], ws)
+    be.synchronize()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = timer.mean_ms()
+    sum_l = int(lens.sum())
+    kv_bytes = sum_l * Hkv * (2 * D + 8)          # int8 K and V rows + two f32 scales
+    alg_bytes = kv_bytes + B * H * D * 2 * 2 + B * 4
+    flops = 4.0 * D * H * sum_l
+    res = {
+        "tok_s": B / (ms / 1e3), "ms": ms, "wall_ms_per_step": wall * 1e3 / args.steps,
+        "hbm_gbs": alg_bytes / (ms / 1e3) / 1e9, "alg_bytes": alg_bytes, "sum_len": sum_l,
+        "gflops": flops / 1e9, "lens_seed": args.seed,
+    }
+    rep["attn"] = res
+    if not args.no_cpu:
+        rep["attn_cpu"] = cpu_attn(torch, kq, ks, vq, vs, qs[0], lens, B, H, Hkv, bucket, D)
+    return res
+
+
+def cpu_attn(torch, kq, ks, vq, vs, q, lens, B, H, Hkv, bucket, D):
+    """Oracle-side C++ restatement of the reference CPU path on a bounded sample:
+    the first sequences of the batch until ~8 MiB-row of keys, all host threads."""
+    import numpy as np
+    import oracle
+    take, acc = 0, 0
+    while take < B and (acc < 400_000 or take == 0):
+        acc += int(lens[take])
+        take += 1
+    planes = take * Hkv
+    kq_h = kq[: planes * bucket * D].cpu().numpy()
+    vq_h = vq[: planes * bucket * D].cpu().numpy()
+    ks_h = ks[: planes * bucket].cpu().numpy()
+    vs_h = vs[: planes * bucket].cpu().numpy()
+    q_h = q.float().cpu().numpy()[: take * H * D].copy()
+    l_h = lens[:take].astype(np.uint32).copy()
+    out = np.zeros(take * H * D, np.float32)
+    th = oracle.host_threads()
+    lib = oracle.lib()
+    p = lambda a: a.ctypes.data
+    t0 = time.perf_counter()
+    lib.cb_decode_attention_i8(p(q_h), p(kq_h), p(ks_h), p(vq_h), p(vs_h), p(l_h), p(out), take, H,
+                               Hkv, bucket, D, oracle.attn_scale(D), th)
+    dt = time.perf_counter() - t0
+    full = float(lens.sum())
+    t_full = dt * full / float(acc)
+    return {"value": B / t_full, "unit": "tok/s", "cores": th, "kind": "port",
+            "sample": f"{take} of {B} sequences ({acc} of {int(full)} keys), one pass, scaled "
+                      f"by key count to the full batch; {dt:.2f} s",
+            "seconds": dt}
+
+
+# --------------------------------------------------------------- config 1 ----
+def bench_lut(torch, be, args, rep):
+    import numpy as np
+    from hologram_amd import DTYPE_BF16, BufferRef, DeviceWorkspace, KernelCall, UnaryCall
+    n = 16_777_216
+    nbuf = 8                                   # 8 x (32 + 32) MiB = 512 MiB rotation
+    ws = DeviceWorkspace()
+    ins, outs = [], []
+    for i in range(nbuf):
+        x = torch.randint(0, 65536, (n,), dtype=torch.int32, device="cuda").to(torch.int16)
+        ins.append(x)
+        outs.append(torch.empty(n, dtype=torch.int16, device="cuda"))
+        ws.bind(2 * i, ins[-1])
+        ws.bind(2 * i + 1, outs[-1])
+    res = {}
+    for name in ("Gelu", "Silu", "Exp"):
+        ctor = getattr(KernelCall, name)
+        calls = [ctor(UnaryCall(BufferRef(2 * i), BufferRef(2 * i + 1), n, 16, DTYPE_BF16))
+                 for i in range(nbuf)]
+        for i in range(max(args.warmup, 1)):
+            be.dispatch(calls[i % nbuf], ws)
+        be.synchronize()
+        timer = Timer(torch)
+        for i in range(args.steps * 4):
+            with timer:
+                be.dispatch(calls[i % nbuf], ws)
+        be.synchronize()
+        ms = timer.mean_ms()
+        res[name.lower()] = {"gelem_s": n / (ms / 1e3) / 1e9, "us": ms * 1e3,
+                             "hbm_gbs": 4 * n / (ms / 1e3) / 1e9}
+    rep["lut"] = res
+    if not args.no_cpu:
+        import oracle
+        tab = oracle.build_table(2, DTYPE_BF16)
+        xs = ins[0].cpu().numpy().view(np.uint16)
+        o = np.empty_like(xs)
+        th = oracle.host_threads()
+        t0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < 3.0:
+            oracle.lib().cb_lut(tab.ctypes.data, xs.ctypes.data, o.ctypes.data, n, th)
+            reps += 1
+        dt = (time.perf_counter() - t0) / reps
+        rep["lut_cpu"] = {"value": n / dt / 1e9, "unit": "Gelem/s", "cores": th, "kind": "port",
+                          "sample": f"GELU gather of the 16,777,216 elements x{reps}"}
+    return res
+
+
+# --------------------------------------------------------------- config 3 ----
+def bench_kv(torch, be, args, rep):
+    from hologram_amd import DTYPE_BF16, BufferRef, DeviceWorkspace, KernelCall, KvQuantAppendCall
+    planes, bucket, D = 16 * 8, 4096, 128
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed + 3)
+    ws = DeviceWorkspace()
+    cq = torch.randint(-127, 128, (planes * bucket * D,), dtype=torch.int8, device="cuda",
+                       generator=gen)
+    cs = torch.rand(planes * bucket, device="cuda", generator=gen)
+    oq, os_ = torch.empty_like(cq), torch.empty_like(cs)
+    news = [bf16_normal(torch, (planes, 1, D), gen, 0.02) for _ in range(4)]
+    pos = torch.tensor([4095], dtype=torch.int32, device="cuda")
+    for s, t in enumerate([pos, cq, cs, oq, os_] + news):
+        ws.bind(s, t)
+    res = {}
+    for form in ("in_place", "copy"):
+        out_q, out_s = (BufferRef(1), BufferRef(2)) if form == "in_place" else (BufferRef(3), BufferRef(4))
+        calls = [KernelCall.KvQuantAppend(KvQuantAppendCall(
+            BufferRef(5 + i), BufferRef(0), BufferRef(1), BufferRef(2), out_q, out_s, planes,
+            bucket, 1, D, DTYPE_BF16)) for i in range(4)]
+        for i in range(max(args.warmup, 1)):
+            be.dispatch(calls[i % 4], ws)
+        be.synchronize()
+        timer = Timer(torch)
+        for i in range(args.steps * 4):
+            with timer:
+                be.dispatch(calls[i % 4], ws)
+        be.synchronize()
+        ms = timer.mean_ms()
+        if form == "in_place":
+            alg = planes * D * 2 + planes * D + planes * 4 + 4
+        else:
+            alg = 2 * (planes * bucket * D + planes * bucket * 4) + planes * D * 2
+        res[form] = {"us": ms * 1e3, "alg_bytes": alg, "hbm_gbs": alg / (ms / 1e3) / 1e9}
+    rep["kv"] = res
+    return res
+
+
+# --------------------------------------------------------------- config 2 ----
+def bench_gemm(torch, be, args, rep):
+    from hologram_amd import DTYPE_BF16, DTYPE_F32, BufferRef, DeviceWorkspace, KernelCall, MatMulCall
+    shapes = [(1024, 1024, 1024), (4096, 4096, 4096), (8192, 8192, 8192), (16, 4096, 4096)]
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed + 2)
+    res = {}
+    for dt, tdt, peak in ((DTYPE_BF16, torch.bfloat16, BF16_PEAK_TFLOPS),
+                          (DTYPE_F32, torch.float32, FP32_PEAK_TFLOPS)):
+        for (m, n, k) in shapes:
+            es = 2 if dt == DTYPE_BF16 else 4
+            nbuf = max(1, min(4, (512 << 20) // ((m * k + k * n + m * n) * es)))
+            ws = DeviceWorkspace()
+            calls = []
+            for i in range(nbuf):
+                a = (torch.randn(m * k, generator=gen, device="cuda") / math.sqrt(k)).to(tdt)
+                b = (torch.randn(k * n, generator=gen, device="cuda") / math.sqrt(k)).to(tdt)
+                c = torch.empty(m * n, dtype=tdt, device="cuda")
+                ws.bind(3 * i, a)
+                ws.bind(3 * i + 1, b)
+                ws.bind(3 * i + 2, c)
+                calls.append(KernelCall.MatMul(MatMulCall(BufferRef(3 * i), BufferRef(3 * i + 1),
+                                                          BufferRef(3 * i + 2), m, k, n, dt)))
+            for i in range(max(args.warmup, 1)):
+                be.dispatch(calls[i % nbuf], ws)
+            be.synchronize()
+            timer = Timer(torch)
+            steps = args.steps if m * n * k < 8192 ** 3 else max(3, args.steps // 4)
+            for i in range(steps):
+                with timer:
+                    be.dispatch(calls[i % nbuf], ws)
+            be.synchronize()
+            ms = timer.mean_ms()
+            tf = 2.0 * m * n * k / (ms / 1e3) / 1e12
+            key = f"{'bf16' if dt == DTYPE_BF16 else 'f32'}_{m}x{n}x{k}"
+            res[key] = {"tflops": tf, "ms": ms, "frac_peak": tf / peak,
+                        "hbm_gbs": (m * k + k * n + m * n) * es / (ms / 1e3) / 1e9}
+            del ws, calls
+    rep["gemm"] = res
+    return res
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    from hologram_amd import HipBackend
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no HIP device"}))
+        sys.exit(1)
+    be = HipBackend(0, torch.cuda.current_stream().cuda_stream)
+    only = set(args.only.split(","))
+    rep = {}
+    t_all = time.perf_counter()
+    if "attn" in only:
+        bench_attn(torch, be, args, rep)
+        torch.cuda.empty_cache()
+    if "lut" in only:
+        bench_lut(torch, be, args, rep)
+        torch.cuda.empty_cache()
+    if "kv" in only:
+        bench_kv(torch, be, args, rep)
+        torch.cuda.empty_cache()
+    if "gemm" in only:
+        bench_gemm(torch, be, args, rep)
+    be.close()
+
+    attn = rep.get("attn")
+    line = {
+        "metric": METRIC,
+        "value": attn["tok_s"] if attn else None,
+        "unit": "tok/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": attn["ms"] if attn else None,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 KV, bf16 Q/out, fp32 softmax",
+        "data": "synthetic (seeded N(0,1) K/V with 2% x20 outlier channels, quantized by the "
+                "int8 append op; seeded ragged lengths)",
+        "config": {"workload": "config 4: GQA decode attention over int8 KV", "batch": 32,
+                   "heads": 32, "kv_heads": 8, "head_dim": 128, "bucket": 32768,
+                   "len_dist": "U[512, 32768]", "sum_len": attn["sum_len"] if attn else None},
+    }
+    if attn:
+        line["roofline"] = {"bound": "hbm", "achieved": attn["hbm_gbs"], "peak": HBM_PEAK_GBS,
+                            "unit": "GB/s", "frac": attn["hbm_gbs"] / HBM_PEAK_GBS,
+                            "traffic": None}
+    if "attn_cpu" in rep:
+        c = rep["attn_cpu"]
+        line["cpu_baseline"] = {k: c[k] for k in ("value", "unit", "cores", "kind", "sample")}
+    comps = {}
+    if "lut" in rep:
+        comps["lut_bf16_16M"] = {k: {"gelem_s": v["gelem_s"], "us": v["us"],
+                                     "roofline_frac": v["hbm_gbs"] / HBM_PEAK_GBS}
+                                 for k, v in rep["lut"].items()}
+        if "lut_cpu" in rep:
+            comps["lut_bf16_16M"]["cpu_baseline"] = rep["lut_cpu"]
+    if "kv" in rep:
+        comps["kv_quant_append"] = rep["kv"]
+    if "gemm" in rep:
+        comps["gemm"] = rep["gemm"]
+    if attn:
+        comps["decode_attn_i8"] = {k: attn[k] for k in ("tok_s", "hbm_gbs", "ms", "gflops",
+                                                        "wall_ms_per_step")}
+    line["components"] = comps
+    line["bench_wall_s"] = time.perf_counter() - t_all
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,613 @@
+// holo_backend.cpp — the C ABI of include/holo_hip.h: the Backend::dispatch
+// boundary (crates/hologram-compute/src/backend.rs:8-15) over device-resident
+// slots, with the reference CPU kernels' refusals reproduced before any
+// device work.
+#include "holo_hip.h"
+
+#include <hip/hip_runtime.h>
+#include <string.h>
+
+#include <cmath>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "holo_kernels.h"
+
+namespace holo {
+bool build_lut_table(int act, bool f16, uint16_t *t);
+}
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string &msg) {
+    g_last_error = msg;
+    return code;
+}
+
+struct Range {
+    uint8_t *ptr = nullptr;
+    uint64_t bytes = 0;
+};
+
+// A resolved operand: [base, base + bytes) in device memory.
+struct View {
+    uint8_t *base = nullptr;
+    uint64_t bytes = 0;
+    uint64_t key = 0;  // 0: compare device addresses; else the slot a size-only check saw
+};
+
+}  // namespace
+
+struct holo_backend {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::map<uint32_t, Range> slots;
+    uint16_t *lut_dev[5][2] = {};       // [act][0 = f16, 1 = bf16], uploaded once
+    void *scratch = nullptr;            // split-K partials of decode attention
+    size_t scratch_bytes = 0;
+};
+
+namespace {
+
+// Slot-size source for validation: a live backend's slot table, or the plain
+// slot_bytes array of holo_hip_validate (no device memory behind it).
+struct SlotTable {
+    const holo_backend *be = nullptr;
+    const uint64_t *sizes = nullptr;
+    uint32_t nsizes = 0;
+
+    bool lookup(uint32_t slot, uint8_t **ptr, uint64_t *bytes, uint64_t *key) const {
+        if (be) {
+            auto it = be->slots.find(slot);
+            if (it == be->slots.end()) return false;
+            *ptr = it->second.ptr;
+            *bytes = it->second.bytes;
+            *key = 0;
+            return true;
+        }
+        if (slot >= nsizes) return false;
+        // Size-only check: slots are distinct buffers, ranges are offsets.
+        *ptr = nullptr;
+        *bytes = sizes[slot];
+        *key = uint64_t(slot) + 1;
+        return true;
+    }
+};
+
+// BufferArena::buf_range (crates/hologram-exec/src/buffer.rs:312-335):
+// start = min(offset, len); end = length == 0 ? len : min(start + length, len).
+bool resolve(const SlotTable &st, const holo_buffer_ref &r, View *v) {
+    uint8_t *p;
+    uint64_t len, key;
+    if (!st.lookup(r.slot, &p, &len, &key)) return false;
+    const uint64_t start = r.offset < len ? r.offset : len;
+    const uint64_t end = r.length == 0 ? len : (start + r.length < len ? start + r.length : len);
+    v->base = p + start;
+    v->bytes = end - start;
+    v->key = key;
+    return true;
+}
+
+bool overlaps(const View &a, const View &b) {
+    if (a.key != b.key) return false;
+    return a.base < b.base + b.bytes && b.base < a.base + a.bytes;
+}
+
+// split_borrow (buffer.rs:974-998): every read resolves and no read range
+// overlaps the write range; a refusal is SlotOutOfRange(write slot).
+int split_borrow(const SlotTable &st, const holo_buffer_ref *reads, View *rv, int nreads,
+                 const holo_buffer_ref &write, View *wv, const char *op) {
+    if (!resolve(st, write, wv))
+        return fail(HOLO_ERR_SLOT_OUT_OF_RANGE,
+                    std::string(op) + ": output slot " + std::to_string(write.slot) + " unbound");
+    for (int i = 0; i < nreads; ++i) {
+        if (!resolve(st, reads[i], &rv[i]))
+            return fail(HOLO_ERR_SLOT_OUT_OF_RANGE, std::string(op) + ": input slot " +
+                                                        std::to_string(reads[i].slot) + " unbound");
+        if (overlaps(rv[i], *wv))
+            return fail(HOLO_ERR_SLOT_OUT_OF_RANGE,
+                        std::string(op) + ": input overlaps output slot " +
+                            std::to_string(write.slot));
+    }
+    return HOLO_OK;
+}
+
+int need(const View &v, uint64_t bytes, uint32_t slot, const char *op, const char *what) {
+    if (v.bytes < bytes)
+        return fail(HOLO_ERR_SLOT_OUT_OF_RANGE,
+                    std::string(op) + ": " + what + " (slot " + std::to_string(slot) + ") holds " +
+                        std::to_string(v.bytes) + " bytes, needs " + std::to_string(bytes));
+    return HOLO_OK;
+}
+
+#define HOLO_TRY(expr)                    \
+    do {                                  \
+        int _rc = (expr);                 \
+        if (_rc != HOLO_OK) return _rc;   \
+    } while (0)
+
+int launched(hipError_t e, const char *op) {
+    if (e != hipSuccess)
+        return fail(HOLO_ERR_DISPATCH, std::string(op) + ": launch failed: " + hipGetErrorString(e));
+    return HOLO_OK;
+}
+
+int lut_act_of(uint32_t tag) {
+    switch (tag) {
+        case HOLO_OP_SIGMOID: return HOLO_ACT_SIGMOID;
+        case HOLO_OP_TANH: return HOLO_ACT_TANH;
+        case HOLO_OP_GELU: return HOLO_ACT_GELU;
+        case HOLO_OP_SILU: return HOLO_ACT_SILU;
+        case HOLO_OP_EXP: return HOLO_ACT_EXP;
+        default: return -1;
+    }
+}
+
+size_t dtype_size(uint8_t dt) {
+    switch (dt) {
+        case HOLO_DTYPE_I8: return 1;
+        case HOLO_DTYPE_F16:
+        case HOLO_DTYPE_BF16: return 2;
+        case HOLO_DTYPE_F32: return 4;
+        default: return 0;
+    }
+}
+
+// ---------------------------------------------------------------- LUT ----
+// unary_act -> unary_lut (src/cpu/kernels.rs:1586-1598, src/cpu/lut.rs:76-98).
+int do_unary(holo_backend *be, const SlotTable &st, uint32_t tag, const holo_unary_call &c) {
+    const char *op = "unary_lut";
+    const int act = lut_act_of(tag);
+    if (c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F16)
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    "unary_lut: the device path serves bf16/f16 (the 65536-entry table); "
+                    "route other dtypes to the CPU backend");
+    if (c.element_count == 0) return HOLO_OK;
+    View in, out;
+    HOLO_TRY(split_borrow(st, &c.input, &in, 1, c.output, &out, op));
+    const uint64_t bytes = c.element_count * 2;
+    HOLO_TRY(need(in, bytes, c.input.slot, op, "input"));
+    HOLO_TRY(need(out, bytes, c.output.slot, op, "output"));
+    if (!be) return HOLO_OK;
+    const int di = c.dtype == HOLO_DTYPE_BF16 ? 1 : 0;
+    uint16_t *&tab = be->lut_dev[act][di];
+    if (!tab) {
+        std::vector<uint16_t> host(65536);
+        holo::build_lut_table(act, di == 0, host.data());
+        void *d = nullptr;
+        hipError_t e = hipMalloc(&d, 65536 * 2);
+        if (e != hipSuccess) return fail(HOLO_ERR_INIT, "unary_lut: table allocation failed");
+        e = hipMemcpy(d, host.data(), 65536 * 2, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            (void)hipFree(d);
+            return fail(HOLO_ERR_INIT, "unary_lut: table upload failed");
+        }
+        tab = static_cast<uint16_t *>(d);
+    }
+    return launched(holo::launch_lut_u16(tab, reinterpret_cast<const uint16_t *>(in.base),
+                                         reinterpret_cast<uint16_t *>(out.base), c.element_count,
+                                         be->stream),
+                    op);
+}
+
+// ------------------------------------------------------------- MatMul ----
+// matmul_float (src/cpu/float_kernels.rs:298-399).
+int do_matmul(holo_backend *be, const SlotTable &st, const holo_matmul_call &c) {
+    const char *op = "matmul";
+    if (c.m == 0 || c.k == 0 || c.n == 0) return HOLO_OK;
+    if (c.dtype != HOLO_DTYPE_F32 && c.dtype != HOLO_DTYPE_BF16)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "matmul: the device path serves f32 and bf16");
+    if (c.b_packed)
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    "matmul: panel-packed B (b_packed) is a CPU layout; bind the row-major weight");
+    const uint64_t es = dtype_size(c.dtype);
+    holo_buffer_ref reads[2] = {c.a, c.b};
+    View rv[2], out;
+    HOLO_TRY(split_borrow(st, reads, rv, 2, c.output, &out, op));
+    HOLO_TRY(need(rv[0], uint64_t(c.m) * c.k * es, c.a.slot, op, "a"));
+    HOLO_TRY(need(rv[1], uint64_t(c.k) * c.n * es, c.b.slot, op, "b"));
+    HOLO_TRY(need(out, uint64_t(c.m) * c.n * es, c.output.slot, op, "output"));
+    if (!be) return HOLO_OK;
+    return launched(holo::launch_matmul(rv[0].base, rv[1].base, out.base, c.m, c.k, c.n, c.dtype,
+                                        be->stream),
+                    op);
+}
+
+// ------------------------------------------------------- KvCacheWrite ----
+// kv_cache_write (src/cpu/kernels.rs:455-501): honest copy + ring rows.
+int do_kv_write(holo_backend *be, const SlotTable &st, const holo_kv_cache_write_call &c) {
+    const char *op = "kv_cache_write";
+    if (c.bucket_rows == 0 || c.row_bytes == 0)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "kv_cache_write: bucket_rows and row_bytes must be >= 1");
+    if (c.new_rows > c.bucket_rows)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "kv_cache_write: new_rows exceeds bucket_rows");
+    holo_buffer_ref reads[3] = {c.cache, c.new_rows_buf, c.pos};
+    View rv[3], out;
+    HOLO_TRY(split_borrow(st, reads, rv, 3, c.output, &out, op));
+    const uint64_t plane = uint64_t(c.bucket_rows) * c.row_bytes;
+    const uint64_t total = plane * c.planes;
+    if (rv[0].bytes < total || rv[1].bytes < uint64_t(c.planes) * c.new_rows * c.row_bytes ||
+        rv[2].bytes < 4 || out.bytes < total)
+        return fail(HOLO_ERR_SLOT_OUT_OF_RANGE,
+                    "kv_cache_write: an operand is shorter than the declared geometry (slot " +
+                        std::to_string(c.output.slot) + ")");
+    if (!be) return HOLO_OK;
+    HOLO_TRY(launched(holo::launch_copy_bytes(rv[0].base, out.base, total, be->stream), op));
+    if (c.planes == 0 || c.new_rows == 0) return HOLO_OK;
+    return launched(holo::launch_kv_place_rows(rv[1].base,
+                                               reinterpret_cast<const uint32_t *>(rv[2].base),
+                                               out.base, c.planes, c.bucket_rows, c.new_rows,
+                                               c.row_bytes, be->stream),
+                    op);
+}
+
+// ------------------------------------------------------ KvQuantAppend ----
+int do_kv_quant(holo_backend *be, const SlotTable &st, const holo_kv_quant_append_call &c) {
+    const char *op = "kv_quant_append";
+    if (c.bucket_rows == 0 || c.head_dim == 0)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "kv_quant_append: bucket_rows and head_dim must be >= 1");
+    if (c.new_rows > c.bucket_rows)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "kv_quant_append: new_rows exceeds bucket_rows");
+    if (c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F16 && c.dtype != HOLO_DTYPE_F32)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "kv_quant_append: new rows must be bf16, f16 or f32");
+    if (c.head_dim > 8192)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "kv_quant_append: head_dim above 8192");
+    const bool in_place = c.output.slot == c.cache.slot && c.output.offset == c.cache.offset &&
+                          c.output_scales.slot == c.cache_scales.slot &&
+                          c.output_scales.offset == c.cache_scales.offset;
+    const uint64_t qbytes = uint64_t(c.planes) * c.bucket_rows * c.head_dim;
+    const uint64_t sbytes = uint64_t(c.planes) * c.bucket_rows * 4;
+    const uint64_t nbytes = uint64_t(c.planes) * c.new_rows * c.head_dim * dtype_size(c.dtype);
+    View nw, pos, cq, cs, oq, os;
+    if (in_place) {
+        // The move form: the new rows and pos must not alias the cache.
+        holo_buffer_ref reads[2] = {c.new_rows_buf, c.pos};
+        View rv[2];
+        HOLO_TRY(split_borrow(st, reads, rv, 2, c.output, &oq, op));
+        HOLO_TRY(split_borrow(st, reads, rv, 2, c.output_scales, &os, op));
+        nw = rv[0];
+        pos = rv[1];
+        if (overlaps(oq, os))
+            return fail(HOLO_ERR_SLOT_OUT_OF_RANGE, "kv_quant_append: int8 cache overlaps scales");
+    } else {
+        holo_buffer_ref reads[4] = {c.new_rows_buf, c.pos, c.cache, c.cache_scales};
+        View rv[4];
+        HOLO_TRY(split_borrow(st, reads, rv, 4, c.output, &oq, op));
+        HOLO_TRY(split_borrow(st, reads, rv, 4, c.output_scales, &os, op));
+        if (overlaps(oq, os))
+            return fail(HOLO_ERR_SLOT_OUT_OF_RANGE, "kv_quant_append: outputs overlap");
+        nw = rv[0];
+        pos = rv[1];
+        cq = rv[2];
+        cs = rv[3];
+        HOLO_TRY(need(cq, qbytes, c.cache.slot, op, "cache"));
+        HOLO_TRY(need(cs, sbytes, c.cache_scales.slot, op, "cache_scales"));
+    }
+    HOLO_TRY(need(nw, nbytes, c.new_rows_buf.slot, op, "new rows"));
+    HOLO_TRY(need(pos, 4, c.pos.slot, op, "pos"));
+    HOLO_TRY(need(oq, qbytes, c.output.slot, op, "output"));
+    HOLO_TRY(need(os, sbytes, c.output_scales.slot, op, "output_scales"));
+    if (!be) return HOLO_OK;
+    if (!in_place) {
+        HOLO_TRY(launched(holo::launch_copy_bytes(cq.base, oq.base, qbytes, be->stream), op));
+        HOLO_TRY(launched(holo::launch_copy_bytes(cs.base, os.base, sbytes, be->stream), op));
+    }
+    if (c.planes == 0 || c.new_rows == 0) return HOLO_OK;
+    return launched(holo::launch_kv_quant_append(nw.base, c.dtype,
+                                                 reinterpret_cast<const uint32_t *>(pos.base),
+                                                 reinterpret_cast<int8_t *>(oq.base),
+                                                 reinterpret_cast<float *>(os.base), c.planes,
+                                                 c.bucket_rows, c.new_rows, c.head_dim, be->stream),
+                    op);
+}
+
+// ---------------------------------------------------- DecodeAttnI8 -------
+// Refusals follow decode_attention_valid_float (src/cpu/float_kernels.rs:4192-4220).
+int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attention_i8_call &c) {
+    const char *op = "decode_attention_i8";
+    if (c.batch == 0 || c.heads == 0 || c.head_dim == 0) return HOLO_OK;
+    const uint32_t hkv = c.kv_heads == 0 ? c.heads : c.kv_heads;
+    if (c.heads % hkv != 0)
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    "decode_attention_i8: heads must be a multiple of kv_heads (grouped-query)");
+    if (c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F32)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "decode_attention_i8: q/output must be bf16 or f32");
+    if (!holo::attn_i8_supported(c.heads, hkv, c.head_dim))
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    "decode_attention_i8: head_dim must be 64 or 128 and heads/kv_heads one of "
+                    "1, 2, 4, 8");
+    const uint64_t es = dtype_size(c.dtype);
+    const uint64_t qn = uint64_t(c.batch) * c.heads * c.head_dim;
+    const uint64_t rows = uint64_t(c.batch) * hkv * c.bucket_rows;
+    holo_buffer_ref reads[6] = {c.q, c.k_cache, c.v_cache, c.k_scales, c.v_scales, c.lens};
+    View rv[6], out;
+    HOLO_TRY(split_borrow(st, reads, rv, 6, c.output, &out, op));
+    HOLO_TRY(need(rv[0], qn * es, c.q.slot, op, "q"));
+    HOLO_TRY(need(rv[1], rows * c.head_dim, c.k_cache.slot, op, "k_cache"));
+    HOLO_TRY(need(rv[2], rows * c.head_dim, c.v_cache.slot, op, "v_cache"));
+    HOLO_TRY(need(rv[3], rows * 4, c.k_scales.slot, op, "k_scales"));
+    HOLO_TRY(need(rv[4], rows * 4, c.v_scales.slot, op, "v_scales"));
+    HOLO_TRY(need(rv[5], uint64_t(c.batch) * 4, c.lens.slot, op, "lens"));
+    HOLO_TRY(need(out, qn * es, c.output.slot, op, "output"));
+    if (!be) return HOLO_OK;
+    // score divisor (float_kernels.rs:4256-4266)
+    float dflt = std::sqrt(static_cast<float>(c.head_dim));
+    if (dflt < 1.0f) dflt = 1.0f;
+    float scale = dflt;
+    if (c.scale_bits != 0) {
+        float sm;
+        memcpy(&sm, &c.scale_bits, 4);
+        scale = sm > 0.0f ? 1.0f / sm : dflt;
+    }
+    const size_t need_scratch = holo::attn_i8_scratch_bytes(c.batch, c.heads, c.bucket_rows, c.head_dim);
+    if (need_scratch > be->scratch_bytes) {
+        if (be->scratch) {
+            (void)hipStreamSynchronize(be->stream);
+            (void)hipFree(be->scratch);
+            be->scratch = nullptr;
+            be->scratch_bytes = 0;
+        }
+        if (hipMalloc(&be->scratch, need_scratch) != hipSuccess)
+            return fail(HOLO_ERR_INIT, "decode_attention_i8: scratch allocation failed");
+        be->scratch_bytes = need_scratch;
+    }
+    holo::AttnI8Args a;
+    a.q = rv[0].base;
+    a.kq = reinterpret_cast<const int8_t *>(rv[1].base);
+    a.vq = reinterpret_cast<const int8_t *>(rv[2].base);
+    a.ks = reinterpret_cast<const float *>(rv[3].base);
+    a.vs = reinterpret_cast<const float *>(rv[4].base);
+    a.lens = reinterpret_cast<const uint32_t *>(rv[5].base);
+    a.out = out.base;
+    a.B = c.batch;
+    a.H = c.heads;
+    a.Hkv = hkv;
+    a.bucket = c.bucket_rows;
+    a.D = c.head_dim;
+    a.score_scale = scale;
+    a.dtype = c.dtype;
+    if (c.bucket_rows == 0) {
+        // No key can be visible: the pinned zero vector (pinned_semantics.rs).
+        return launched(holo::launch_fill_zero(out.base, qn * es, be->stream), op);
+    }
+    return launched(holo::launch_attn_i8(a, be->scratch, be->stream), op);
+}
+
+int dispatch_impl(holo_backend *be, const SlotTable &st, const holo_kernel_call *call) {
+    if (!call) return fail(HOLO_ERR_DISPATCH, "dispatch: null call");
+    switch (call->tag) {
+        case HOLO_OP_SIGMOID:
+        case HOLO_OP_TANH:
+        case HOLO_OP_GELU:
+        case HOLO_OP_SILU:
+        case HOLO_OP_EXP: return do_unary(be, st, call->tag, call->u.unary);
+        case HOLO_OP_MATMUL: return do_matmul(be, st, call->u.matmul);
+        case HOLO_OP_KV_CACHE_WRITE: return do_kv_write(be, st, call->u.kv_write);
+        case HOLO_OP_KV_QUANT_APPEND: return do_kv_quant(be, st, call->u.kv_quant_append);
+        case HOLO_OP_DECODE_ATTN_I8: return do_attn_i8(be, st, call->u.attn_i8);
+        default:
+            return fail(HOLO_ERR_UNSUPPORTED_OP,
+                        "dispatch: kernel call tag " + std::to_string(call->tag) +
+                            " has no device kernel in this backend");
+    }
+}
+
+// -------------------------------------------------------- wire codec ----
+// crates/hologram-archive/src/kernel_codec.rs:557-813 (LE fields).
+struct Reader {
+    const uint8_t *p;
+    size_t len, at = 0;
+    bool ok = true;
+    template <class T>
+    T get() {
+        T v{};
+        if (at + sizeof(T) > len) {
+            ok = false;
+            return v;
+        }
+        memcpy(&v, p + at, sizeof(T));
+        at += sizeof(T);
+        return v;
+    }
+    holo_buffer_ref buf() {
+        holo_buffer_ref b;
+        b.slot = get<uint32_t>();
+        b.offset = get<uint64_t>();
+        b.length = get<uint64_t>();
+        return b;
+    }
+};
+
+int decode_impl(const uint8_t *wire, size_t len, holo_kernel_call *out, size_t *consumed) {
+    if (!wire || !out) return fail(HOLO_ERR_DISPATCH, "decode_call: null argument");
+    Reader r{wire, len};
+    memset(out, 0, sizeof(*out));
+    out->tag = r.get<uint16_t>();
+    switch (out->tag) {
+        case HOLO_OP_SIGMOID:
+        case HOLO_OP_TANH:
+        case HOLO_OP_GELU:
+        case HOLO_OP_SILU:
+        case HOLO_OP_EXP: {  // put_unary :575-581
+            auto &c = out->u.unary;
+            c.input = r.buf();
+            c.output = r.buf();
+            c.element_count = r.get<uint64_t>();
+            c.witt_bits = r.get<uint16_t>();
+            c.dtype = r.get<uint8_t>();
+            break;
+        }
+        case HOLO_OP_MATMUL: {  // put_matmul :590-599
+            auto &c = out->u.matmul;
+            c.a = r.buf();
+            c.b = r.buf();
+            c.output = r.buf();
+            c.m = r.get<uint32_t>();
+            c.k = r.get<uint32_t>();
+            c.n = r.get<uint32_t>();
+            c.dtype = r.get<uint8_t>();
+            c.b_packed = r.get<uint8_t>();
+            break;
+        }
+        case HOLO_OP_KV_CACHE_WRITE: {  // put_kvwr :804-813
+            auto &c = out->u.kv_write;
+            c.cache = r.buf();
+            c.new_rows_buf = r.buf();
+            c.pos = r.buf();
+            c.output = r.buf();
+            c.planes = r.get<uint32_t>();
+            c.bucket_rows = r.get<uint32_t>();
+            c.new_rows = r.get<uint32_t>();
+            c.row_bytes = r.get<uint32_t>();
+            break;
+        }
+        case HOLO_OP_KV_QUANT_APPEND: {  // field order of holo_kv_quant_append_call
+            auto &c = out->u.kv_quant_append;
+            c.new_rows_buf = r.buf();
+            c.pos = r.buf();
+            c.cache = r.buf();
+            c.cache_scales = r.buf();
+            c.output = r.buf();
+            c.output_scales = r.buf();
+            c.planes = r.get<uint32_t>();
+            c.bucket_rows = r.get<uint32_t>();
+            c.new_rows = r.get<uint32_t>();
+            c.head_dim = r.get<uint32_t>();
+            c.dtype = r.get<uint8_t>();
+            break;
+        }
+        case HOLO_OP_DECODE_ATTN_I8: {  // field order of holo_decode_attention_i8_call
+            auto &c = out->u.attn_i8;
+            c.q = r.buf();
+            c.k_cache = r.buf();
+            c.v_cache = r.buf();
+            c.k_scales = r.buf();
+            c.v_scales = r.buf();
+            c.lens = r.buf();
+            c.output = r.buf();
+            c.batch = r.get<uint32_t>();
+            c.heads = r.get<uint32_t>();
+            c.kv_heads = r.get<uint32_t>();
+            c.bucket_rows = r.get<uint32_t>();
+            c.head_dim = r.get<uint32_t>();
+            c.scale_bits = r.get<uint32_t>();
+            c.dtype = r.get<uint8_t>();
+            break;
+        }
+        default:
+            if (!r.ok) return fail(HOLO_ERR_DISPATCH, "decode_call: truncated discriminant");
+            return fail(HOLO_ERR_UNSUPPORTED_OP,
+                        "decode_call: discriminant " + std::to_string(out->tag) +
+                            " has no device kernel in this backend");
+    }
+    if (!r.ok) return fail(HOLO_ERR_DISPATCH, "decode_call: truncated payload");
+    if (consumed) *consumed = r.at;
+    return HOLO_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int holo_hip_backend_create(int device, void *stream, holo_backend **out) {
+    if (!out) return fail(HOLO_ERR_INIT, "backend_create: null out");
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0)
+        return fail(HOLO_ERR_INIT, "backend_create: no HIP device visible");
+    if (device < 0 || device >= count)
+        return fail(HOLO_ERR_INIT, "backend_create: device index out of range");
+    if (hipSetDevice(device) != hipSuccess) return fail(HOLO_ERR_INIT, "backend_create: hipSetDevice failed");
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess)
+        return fail(HOLO_ERR_INIT, "backend_create: device query failed");
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(HOLO_ERR_INIT, std::string("backend_create: built for gfx950, device is ") +
+                                       prop.gcnArchName);
+    auto *be = new holo_backend();
+    be->device = device;
+    be->stream = static_cast<hipStream_t>(stream);
+    *out = be;
+    return HOLO_OK;
+}
+
+int holo_hip_backend_destroy(holo_backend *be) {
+    if (!be) return HOLO_OK;
+    (void)hipSetDevice(be->device);
+    (void)hipStreamSynchronize(be->stream);
+    for (auto &row : be->lut_dev)
+        for (auto *t : row)
+            if (t) (void)hipFree(t);
+    if (be->scratch) (void)hipFree(be->scratch);
+    delete be;
+    return HOLO_OK;
+}
+
+int holo_hip_set_stream(holo_backend *be, void *stream) {
+    if (!be) return fail(HOLO_ERR_INIT, "set_stream: null backend");
+    be->stream = static_cast<hipStream_t>(stream);
+    return HOLO_OK;
+}
+
+int holo_hip_slot_bind(holo_backend *be, uint32_t slot, void *ptr, uint64_t bytes) {
+    if (!be) return fail(HOLO_ERR_INIT, "slot_bind: null backend");
+    if (slot == HOLO_SLOT_ABSENT) return fail(HOLO_ERR_SLOT_OUT_OF_RANGE, "slot_bind: reserved slot id");
+    if (!ptr && bytes) return fail(HOLO_ERR_SLOT_OUT_OF_RANGE, "slot_bind: null pointer");
+    be->slots[slot] = Range{static_cast<uint8_t *>(ptr), bytes};
+    return HOLO_OK;
+}
+
+int holo_hip_slot_unbind(holo_backend *be, uint32_t slot) {
+    if (!be) return fail(HOLO_ERR_INIT, "slot_unbind: null backend");
+    be->slots.erase(slot);
+    return HOLO_OK;
+}
+
+int holo_hip_dispatch(holo_backend *be, const holo_kernel_call *call) {
+    if (!be) return fail(HOLO_ERR_INIT, "dispatch: null backend");
+    SlotTable st;
+    st.be = be;
+    return dispatch_impl(be, st, call);
+}
+
+int holo_hip_dispatch_encoded(holo_backend *be, const uint8_t *wire, size_t len, size_t *consumed) {
+    holo_kernel_call c;
+    HOLO_TRY(decode_impl(wire, len, &c, consumed));
+    return holo_hip_dispatch(be, &c);
+}
+
+int holo_hip_synchronize(holo_backend *be) {
+    if (!be) return fail(HOLO_ERR_INIT, "synchronize: null backend");
+    hipError_t e = hipStreamSynchronize(be->stream);
+    if (e != hipSuccess) return fail(HOLO_ERR_DISPATCH, std::string("synchronize: ") + hipGetErrorString(e));
+    return HOLO_OK;
+}
+
+int holo_hip_validate(const holo_kernel_call *call, const uint64_t *slot_bytes, uint32_t nslots) {
+    SlotTable st;
+    st.sizes = slot_bytes;
+    st.nsizes = slot_bytes ? nslots : 0;
+    return dispatch_impl(nullptr, st, call);
+}
+
+int holo_hip_decode_call(const uint8_t *wire, size_t len, holo_kernel_call *out, size_t *consumed) {
+    return decode_impl(wire, len, out, consumed);
+}
+
+int holo_hip_lut_table(int act, int dtype, uint16_t *out65536) {
+    if (!out65536) return fail(HOLO_ERR_DISPATCH, "lut_table: null output");
+    if (dtype != HOLO_DTYPE_BF16 && dtype != HOLO_DTYPE_F16)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "lut_table: dtype must be bf16 or f16");
+    if (!holo::build_lut_table(act, dtype == HOLO_DTYPE_F16, out65536))
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "lut_table: no table for this activation id");
+    return HOLO_OK;
+}
+
+const char *holo_hip_last_error_message(void) { return g_last_error.c_str(); }
+
+}  // extern "C"

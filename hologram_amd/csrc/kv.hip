@@ -1,0 +1,211 @@
+// kv.hip — KV-cache kernels: the honest-copy byte stream, KvCacheWrite's ring
+// row placement (crates/hologram-compute/src/cpu/kernels.rs:455-501), and the
+// int8 quantize+append that applies quantize_row_i8
+// (src/cpu/simd.rs:4755-4785) to each appended row on the device.
+//
+// The write position `pos` is content: a device-resident 4-byte u32 read by
+// the kernels themselves, so a decode step never syncs to the host for it.
+#include <hip/hip_runtime.h>
+
+#include "holo_device.h"
+#include "holo_kernels.h"
+
+namespace holo {
+namespace {
+
+constexpr int kCopyThreads = 256;
+
+__global__ __launch_bounds__(kCopyThreads) void copy16_kernel(const u32x4 *__restrict__ src,
+                                                             u32x4 *__restrict__ dst, uint64_t nvec) {
+    const uint64_t stride = uint64_t(gridDim.x) * kCopyThreads;
+    uint64_t i = uint64_t(blockIdx.x) * kCopyThreads + threadIdx.x;
+    for (; i + 3 * stride < nvec; i += 4 * stride) {
+        const u32x4 a = ld_stream(&src[i]);
+        const u32x4 b = ld_stream(&src[i + stride]);
+        const u32x4 c = ld_stream(&src[i + 2 * stride]);
+        const u32x4 d = ld_stream(&src[i + 3 * stride]);
+        st_stream(a, &dst[i]);
+        st_stream(b, &dst[i + stride]);
+        st_stream(c, &dst[i + 2 * stride]);
+        st_stream(d, &dst[i + 3 * stride]);
+    }
+    for (; i < nvec; i += stride) dst[i] = src[i];
+}
+
+__global__ __launch_bounds__(kCopyThreads) void copy1_kernel(const uint8_t *__restrict__ src,
+                                                            uint8_t *__restrict__ dst, uint64_t n) {
+    const uint64_t stride = uint64_t(gridDim.x) * kCopyThreads;
+    for (uint64_t i = uint64_t(blockIdx.x) * kCopyThreads + threadIdx.x; i < n; i += stride)
+        dst[i] = src[i];
+}
+
+__global__ __launch_bounds__(kCopyThreads) void zero1_kernel(uint8_t *__restrict__ dst, uint64_t n) {
+    const uint64_t stride = uint64_t(gridDim.x) * kCopyThreads;
+    for (uint64_t i = uint64_t(blockIdx.x) * kCopyThreads + threadIdx.x; i < n; i += stride) dst[i] = 0;
+}
+
+unsigned copy_blocks(uint64_t items) {
+    uint64_t b = (items + kCopyThreads - 1) / kCopyThreads;
+    const uint64_t cap = 256 * 16;  // 16 workgroups per CU, grid-stride beyond
+    if (b > cap) b = cap;
+    return unsigned(b ? b : 1);
+}
+
+// One workgroup per (plane, new row): out[p][(pos + j) % bucket] = new[p][j].
+__global__ __launch_bounds__(kCopyThreads) void place_rows_kernel(const uint8_t *__restrict__ nw,
+                                                                 const uint32_t *__restrict__ posp,
+                                                                 uint8_t *__restrict__ out,
+                                                                 uint32_t bucket, uint32_t new_rows,
+                                                                 uint32_t row_bytes) {
+    const uint32_t p = blockIdx.x / new_rows, j = blockIdx.x % new_rows;
+    const uint64_t pos = *posp % bucket;
+    const uint64_t dst = (uint64_t(p) * bucket + (pos + j) % bucket) * row_bytes;
+    const uint64_t src = (uint64_t(p) * new_rows + j) * row_bytes;
+    for (uint32_t c = threadIdx.x; c < row_bytes; c += kCopyThreads) out[dst + c] = nw[src + c];
+}
+
+__device__ __forceinline__ float widen(const void *base, uint8_t dtype, uint64_t i) {
+    if (dtype == 8) return reinterpret_cast<const float *>(base)[i];
+    const uint32_t b = reinterpret_cast<const uint16_t *>(base)[i];
+    if (dtype == 7) return __uint_as_float(b << 16);
+    // f16 -> f32 by bits, as src/cpu/dtype.rs:94-118 (exact; NaN payload kept)
+    const uint32_t s = (b >> 15) << 31, e = (b >> 10) & 0x1fu, m = b & 0x3ffu;
+    if (e == 0x1fu) return __uint_as_float(s | 0x7f800000u | (m << 13));
+    if (e != 0) return __uint_as_float(s | ((e + 112u) << 23) | (m << 13));
+    if (m == 0) return __uint_as_float(s);
+    const int sh = __clz(m) - 21;  // left shifts until the implicit bit (0x400) is set
+    return __uint_as_float(s | (uint32_t(113 - sh) << 23) | (((m << sh) & 0x3ffu) << 13));
+}
+
+// Rust's `f32 as i32` then clamp(-127, 127): NaN -> 0; any out-of-range value
+// saturates, so clamping in the float domain first gives the same integer.
+__device__ __forceinline__ int8_t to_q(float r) {
+    if (r != r) return 0;
+    r = r < -127.0f ? -127.0f : (r > 127.0f ? 127.0f : r);
+    return static_cast<int8_t>(static_cast<int32_t>(r));
+}
+
+// One wavefront per (plane, new row). The row max is a wave reduction of
+// |x| (NaN never wins a `>` comparison, as in the reference's scan; max is
+// exact, so the order of the reduction does not matter). Divisions are the
+// correctly rounded IEEE ones and the file is built without contraction, so
+// t = x * inv and t +- 0.5 round exactly as the reference's two steps.
+template <int kMaxPerLane>
+__global__ __launch_bounds__(256) void quant_append_kernel(const void *__restrict__ nw, uint8_t dtype,
+                                                          const uint32_t *__restrict__ posp,
+                                                          int8_t *__restrict__ cq,
+                                                          float *__restrict__ cs, uint32_t planes,
+                                                          uint32_t bucket, uint32_t new_rows,
+                                                          uint32_t d) {
+    const uint32_t wave = (blockIdx.x * 256u + threadIdx.x) >> 6;
+    const uint32_t lane = threadIdx.x & 63u;
+    if (wave >= planes * new_rows) return;
+    const uint32_t p = wave / new_rows, j = wave % new_rows;
+    const uint64_t pos = *posp % bucket;
+    const uint64_t row = uint64_t(p) * bucket + (pos + j) % bucket;
+    const uint64_t src = (uint64_t(p) * new_rows + j) * d;
+
+    float x[kMaxPerLane];
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kMaxPerLane; ++e) {
+        const uint32_t c = lane + 64u * e;
+        x[e] = c < d ? widen(nw, dtype, src + c) : 0.0f;
+        const float v = x[e];
+        const float av = v < 0.0f ? -v : v;
+        if (av > amax) amax = av;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float o = __shfl_xor(amax, off, 64);
+        if (o > amax) amax = o;
+    }
+    int8_t *dst = cq + row * d;
+    if (amax == 0.0f) {
+#pragma unroll
+        for (int e = 0; e < kMaxPerLane; ++e) {
+            const uint32_t c = lane + 64u * e;
+            if (c < d) dst[c] = 0;
+        }
+        if (lane == 0) cs[row] = 0.0f;
+        return;
+    }
+    const float inv = 127.0f / amax;
+#pragma unroll
+    for (int e = 0; e < kMaxPerLane; ++e) {
+        const uint32_t c = lane + 64u * e;
+        if (c < d) {
+            const float t = x[e] * inv;
+            const float r = t >= 0.0f ? truncf(t + 0.5f) : truncf(t - 0.5f);
+            dst[c] = to_q(r);
+        }
+    }
+    if (lane == 0) cs[row] = amax / 127.0f;
+}
+
+}  // namespace
+
+hipError_t launch_copy_bytes(const void *src, void *dst, uint64_t bytes, hipStream_t stream) {
+    if (bytes == 0) return hipSuccess;
+    const bool aligned =
+        ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0;
+    if (aligned) {
+        const uint64_t nvec = bytes / 16, tail = bytes - nvec * 16;
+        if (nvec)
+            hipLaunchKernelGGL(copy16_kernel, dim3(copy_blocks(nvec)), dim3(kCopyThreads), 0, stream,
+                               static_cast<const u32x4 *>(src), static_cast<u32x4 *>(dst), nvec);
+        if (tail)
+            hipLaunchKernelGGL(copy1_kernel, dim3(1), dim3(kCopyThreads), 0, stream,
+                               static_cast<const uint8_t *>(src) + nvec * 16,
+                               static_cast<uint8_t *>(dst) + nvec * 16, tail);
+    } else {
+        hipLaunchKernelGGL(copy1_kernel, dim3(copy_blocks(bytes)), dim3(kCopyThreads), 0, stream,
+                           static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), bytes);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_zero(void *dst, uint64_t bytes, hipStream_t stream) {
+    if (bytes == 0) return hipSuccess;
+    hipLaunchKernelGGL(zero1_kernel, dim3(copy_blocks(bytes)), dim3(kCopyThreads), 0, stream,
+                       static_cast<uint8_t *>(dst), bytes);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_place_rows(const uint8_t *nw, const uint32_t *pos, uint8_t *out, uint32_t planes,
+                                uint32_t bucket, uint32_t new_rows, uint32_t row_bytes,
+                                hipStream_t stream) {
+    const uint64_t blocks = uint64_t(planes) * new_rows;
+    if (blocks == 0) return hipSuccess;
+    if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(place_rows_kernel, dim3(unsigned(blocks)), dim3(kCopyThreads), 0, stream, nw,
+                       pos, out, bucket, new_rows, row_bytes);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_quant_append(const void *nw, uint8_t dtype, const uint32_t *pos, int8_t *cq,
+                                  float *cs, uint32_t planes, uint32_t bucket, uint32_t new_rows,
+                                  uint32_t d, hipStream_t stream) {
+    const uint64_t waves = uint64_t(planes) * new_rows;
+    if (waves == 0) return hipSuccess;
+    const uint64_t blocks = (waves + 3) / 4;
+    if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
+    const dim3 g{unsigned(blocks), 1, 1}, b{256, 1, 1};
+    if (d <= 128)
+        hipLaunchKernelGGL(quant_append_kernel<2>, g, b, 0, stream, nw, dtype, pos, cq, cs, planes,
+                           bucket, new_rows, d);
+    else if (d <= 512)
+        hipLaunchKernelGGL(quant_append_kernel<8>, g, b, 0, stream, nw, dtype, pos, cq, cs, planes,
+                           bucket, new_rows, d);
+    else if (d <= 2048)
+        hipLaunchKernelGGL(quant_append_kernel<32>, g, b, 0, stream, nw, dtype, pos, cq, cs, planes,
+                           bucket, new_rows, d);
+    else if (d <= 8192)
+        hipLaunchKernelGGL(quant_append_kernel<128>, g, b, 0, stream, nw, dtype, pos, cq, cs, planes,
+                           bucket, new_rows, d);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+}  // namespace holo

@@ -1,0 +1,246 @@
+"""KernelCall: the reference's closed kernel-call surface, for the hot ops.
+
+Mirrors crates/hologram-compute/src/kernel_call.rs (field names, order and
+widths) for the variants this backend executes, plus the two new int8-KV
+capabilities, which take new archive discriminants (122, 123) as the
+reference's codec rule requires (crates/hologram-archive/src/kernel_codec.rs:124-128).
+`KernelCall.encode()` writes the archive wire form (u16 LE discriminant + LE
+payload, kernel_codec.rs:557-813).
+"""
+from __future__ import annotations
+
+import ctypes
+import struct
+from dataclasses import dataclass, field
+
+from . import _ffi
+
+# dtype tags, crates/hologram-types/src/dtype_id.rs:52-61
+DTYPE_I8 = 2
+DTYPE_F16 = 6
+DTYPE_BF16 = 7
+DTYPE_F32 = 8
+
+
+class lut_act:  # noqa: N801 - the reference's module name (kernel_call.rs:877-885)
+    SIGMOID = 0
+    TANH = 1
+    GELU = 2
+    SILU = 3
+    EXP = 4
+    ERF = 5
+    COUNT = 6
+
+
+# archive discriminants, kernel_codec.rs:18-128
+D_SIGMOID = 12
+D_TANH = 13
+D_GELU = 14
+D_SILU = 15
+D_EXP = 18
+D_MATMUL = 46
+D_KVWR = 120
+D_DAVL = 121
+D_KVQA = 122   # new: int8 quantize + append
+D_DAI8 = 123   # new: decode attention over an int8 cache
+
+SLOT_ABSENT = 0xFFFFFFFF
+
+
+@dataclass(frozen=True)
+class BufferRef:
+    """crates/hologram-compute/src/workspace.rs:16-24 (length 0 = whole slot)."""
+    slot: int
+    offset: int = 0
+    length: int = 0
+
+    def c(self) -> _ffi.BufferRefC:
+        return _ffi.BufferRefC(self.slot, self.offset, self.length)
+
+    def wire(self) -> bytes:
+        return struct.pack("<IQQ", self.slot, self.offset, self.length)
+
+
+@dataclass(frozen=True)
+class UnaryCall:
+    """kernel_call.rs:28-36."""
+    input: BufferRef
+    output: BufferRef
+    element_count: int
+    witt_bits: int = 16
+    dtype: int = DTYPE_BF16
+
+    def wire(self) -> bytes:  # put_unary, kernel_codec.rs:575-581
+        return (self.input.wire() + self.output.wire()
+                + struct.pack("<QHB", self.element_count, self.witt_bits, self.dtype))
+
+
+@dataclass(frozen=True)
+class MatMulCall:
+    """kernel_call.rs:49-65."""
+    a: BufferRef
+    b: BufferRef
+    output: BufferRef
+    m: int
+    k: int
+    n: int
+    dtype: int = DTYPE_F32
+    b_packed: bool = False
+
+    def wire(self) -> bytes:  # put_matmul, kernel_codec.rs:590-599
+        return (self.a.wire() + self.b.wire() + self.output.wire()
+                + struct.pack("<IIIBB", self.m, self.k, self.n, self.dtype, int(self.b_packed)))
+
+
+@dataclass(frozen=True)
+class KvCacheWriteCall:
+    """kernel_call.rs:742-759."""
+    cache: BufferRef
+    new: BufferRef
+    pos: BufferRef
+    output: BufferRef
+    planes: int
+    bucket_rows: int
+    new_rows: int
+    row_bytes: int
+
+    def wire(self) -> bytes:  # put_kvwr, kernel_codec.rs:804-813
+        return (self.cache.wire() + self.new.wire() + self.pos.wire() + self.output.wire()
+                + struct.pack("<IIII", self.planes, self.bucket_rows, self.new_rows,
+                              self.row_bytes))
+
+
+@dataclass(frozen=True)
+class KvQuantAppendCall:
+    """New (discriminant 122): int8 quantize + ring append (include/holo_hip.h)."""
+    new: BufferRef
+    pos: BufferRef
+    cache: BufferRef
+    cache_scales: BufferRef
+    output: BufferRef
+    output_scales: BufferRef
+    planes: int
+    bucket_rows: int
+    new_rows: int
+    head_dim: int
+    dtype: int = DTYPE_BF16
+
+    def wire(self) -> bytes:
+        return (self.new.wire() + self.pos.wire() + self.cache.wire() + self.cache_scales.wire()
+                + self.output.wire() + self.output_scales.wire()
+                + struct.pack("<IIIIB", self.planes, self.bucket_rows, self.new_rows,
+                              self.head_dim, self.dtype))
+
+
+@dataclass(frozen=True)
+class DecodeAttentionI8Call:
+    """New (discriminant 123): GQA decode over an int8 cache (include/holo_hip.h)."""
+    q: BufferRef
+    k_cache: BufferRef
+    v_cache: BufferRef
+    k_scales: BufferRef
+    v_scales: BufferRef
+    lens: BufferRef
+    output: BufferRef
+    batch: int
+    heads: int
+    kv_heads: int
+    bucket_rows: int
+    head_dim: int
+    scale_bits: int = 0
+    dtype: int = DTYPE_BF16
+
+    def wire(self) -> bytes:
+        return (self.q.wire() + self.k_cache.wire() + self.v_cache.wire() + self.k_scales.wire()
+                + self.v_scales.wire() + self.lens.wire() + self.output.wire()
+                + struct.pack("<IIIIIIB", self.batch, self.heads, self.kv_heads,
+                              self.bucket_rows, self.head_dim, self.scale_bits, self.dtype))
+
+
+_NAMES = {D_SIGMOID: "Sigmoid", D_TANH: "Tanh", D_GELU: "Gelu", D_SILU: "Silu", D_EXP: "Exp",
+          D_MATMUL: "MatMul", D_KVWR: "KvCacheWrite", D_KVQA: "KvQuantAppend",
+          D_DAI8: "DecodeAttentionI8"}
+
+
+@dataclass(frozen=True)
+class KernelCall:
+    """One variant of the closed KernelCall enum: discriminant + payload."""
+    tag: int
+    payload: object = field(repr=True)
+
+    # constructors named after the Rust variants (kernel_call.rs:1146-1276)
+    @classmethod
+    def Sigmoid(cls, c: UnaryCall) -> "KernelCall":  # noqa: N802
+        return cls(D_SIGMOID, c)
+
+    @classmethod
+    def Tanh(cls, c: UnaryCall) -> "KernelCall":  # noqa: N802
+        return cls(D_TANH, c)
+
+    @classmethod
+    def Gelu(cls, c: UnaryCall) -> "KernelCall":  # noqa: N802
+        return cls(D_GELU, c)
+
+    @classmethod
+    def Silu(cls, c: UnaryCall) -> "KernelCall":  # noqa: N802
+        return cls(D_SILU, c)
+
+    @classmethod
+    def Exp(cls, c: UnaryCall) -> "KernelCall":  # noqa: N802
+        return cls(D_EXP, c)
+
+    @classmethod
+    def MatMul(cls, c: MatMulCall) -> "KernelCall":  # noqa: N802
+        return cls(D_MATMUL, c)
+
+    @classmethod
+    def KvCacheWrite(cls, c: KvCacheWriteCall) -> "KernelCall":  # noqa: N802
+        return cls(D_KVWR, c)
+
+    @classmethod
+    def KvQuantAppend(cls, c: KvQuantAppendCall) -> "KernelCall":  # noqa: N802
+        return cls(D_KVQA, c)
+
+    @classmethod
+    def DecodeAttentionI8(cls, c: DecodeAttentionI8Call) -> "KernelCall":  # noqa: N802
+        return cls(D_DAI8, c)
+
+    @property
+    def name(self) -> str:
+        return _NAMES.get(self.tag, f"op{self.tag}")
+
+    def encode(self) -> bytes:
+        """Archive wire form of this one call (kernel_codec.rs encode_one)."""
+        return struct.pack("<H", self.tag) + self.payload.wire()
+
+    def to_c(self) -> _ffi.KernelCallC:
+        kc = _ffi.KernelCallC()
+        kc.tag = self.tag
+        p = self.payload
+        if isinstance(p, UnaryCall):
+            kc.u.unary = _ffi.UnaryCallC(p.input.c(), p.output.c(), p.element_count,
+                                         p.witt_bits, p.dtype)
+        elif isinstance(p, MatMulCall):
+            kc.u.matmul = _ffi.MatMulCallC(p.a.c(), p.b.c(), p.output.c(), p.m, p.k, p.n,
+                                           p.dtype, int(p.b_packed))
+        elif isinstance(p, KvCacheWriteCall):
+            kc.u.kv_write = _ffi.KvCacheWriteCallC(p.cache.c(), p.new.c(), p.pos.c(),
+                                                   p.output.c(), p.planes, p.bucket_rows,
+                                                   p.new_rows, p.row_bytes)
+        elif isinstance(p, KvQuantAppendCall):
+            kc.u.kv_quant_append = _ffi.KvQuantAppendCallC(
+                p.new.c(), p.pos.c(), p.cache.c(), p.cache_scales.c(), p.output.c(),
+                p.output_scales.c(), p.planes, p.bucket_rows, p.new_rows, p.head_dim, p.dtype)
+        elif isinstance(p, DecodeAttentionI8Call):
+            kc.u.attn_i8 = _ffi.DecodeAttentionI8CallC(
+                p.q.c(), p.k_cache.c(), p.v_cache.c(), p.k_scales.c(), p.v_scales.c(),
+                p.lens.c(), p.output.c(), p.batch, p.heads, p.kv_heads, p.bucket_rows,
+                p.head_dim, p.scale_bits, p.dtype)
+        else:
+            raise TypeError(f"no C form for payload {type(p).__name__}")
+        return kc
+
+
+def encode_calls(calls: list[KernelCall]) -> bytes:
+    """kernel_codec.rs:130-137: u32 LE count, then each call."""
+    return struct.pack("<I", len(calls)) + b"".join(c.encode() for c in calls)

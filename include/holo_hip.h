@@ -1,0 +1,206 @@
+/*
+ * holo_hip.h — C ABI of the MI355X (gfx950) compute backend for Hologram.
+ *
+ * The reference's operator API is the Rust trait
+ *     Backend::dispatch(&mut self, &KernelCall, &mut Workspace) -> Result<(), BackendError>
+ * (crates/hologram-compute/src/backend.rs:8-15). This header is that boundary as
+ * a C ABI: a Rust `Backend` impl binds these functions one to one (the shim is
+ * in INTEGRATION.md). Buffers are device-resident: the caller's content-addressed
+ * pool (crates/hologram-exec/src/buffer.rs:149-207) binds each slot to a device
+ * allocation it owns, and kernels read/write the slots in place — no per-call
+ * host round trip.
+ *
+ * All entry points return a holo_status; on failure a human-readable message is
+ * available from holo_hip_last_error_message() on the same thread
+ * (the convention of crates/hologram-ffi/src/lib.rs:47-48).
+ */
+#ifndef HOLO_HIP_H
+#define HOLO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* BackendError, crates/hologram-compute/src/error.rs:6-20 (0 = Ok). */
+typedef enum holo_status {
+    HOLO_OK = 0,
+    HOLO_ERR_SLOT_OUT_OF_RANGE = 1, /* BackendError::SlotOutOfRange(slot) */
+    HOLO_ERR_SHAPE_MISMATCH = 2,    /* BackendError::ShapeMismatch        */
+    HOLO_ERR_UNSUPPORTED_OP = 3,    /* BackendError::UnsupportedOp(..)    */
+    HOLO_ERR_INIT = 4,              /* BackendError::Init(..)             */
+    HOLO_ERR_DISPATCH = 5           /* BackendError::Dispatch(..)         */
+} holo_status;
+
+/* dtype tags, crates/hologram-types/src/dtype_id.rs:52-61 */
+#define HOLO_DTYPE_I8 2u
+#define HOLO_DTYPE_F16 6u
+#define HOLO_DTYPE_BF16 7u
+#define HOLO_DTYPE_F32 8u
+
+/* lut_act ids, crates/hologram-compute/src/kernel_call.rs:877-885 */
+#define HOLO_ACT_SIGMOID 0
+#define HOLO_ACT_TANH 1
+#define HOLO_ACT_GELU 2
+#define HOLO_ACT_SILU 3
+#define HOLO_ACT_EXP 4
+
+/* KernelCall tags = the archive wire discriminants,
+ * crates/hologram-archive/src/kernel_codec.rs:18-128. 122 and 123 are new
+ * capabilities and take new discriminants (kernel_codec.rs:124-128). */
+#define HOLO_OP_SIGMOID 12u
+#define HOLO_OP_TANH 13u
+#define HOLO_OP_GELU 14u
+#define HOLO_OP_SILU 15u
+#define HOLO_OP_EXP 18u
+#define HOLO_OP_MATMUL 46u
+#define HOLO_OP_KV_CACHE_WRITE 120u
+#define HOLO_OP_KV_QUANT_APPEND 122u      /* new: int8 quantize + ring append   */
+#define HOLO_OP_DECODE_ATTN_I8 123u       /* new: GQA decode over an int8 cache */
+
+/* BufferRef, crates/hologram-compute/src/workspace.rs:16-24.
+ * length == 0 means "to the end of the slot"; slot == HOLO_SLOT_ABSENT marks an
+ * absent operand (kernel_call.rs:217-228). */
+typedef struct holo_buffer_ref {
+    uint32_t slot;
+    uint64_t offset;
+    uint64_t length;
+} holo_buffer_ref;
+#define HOLO_SLOT_ABSENT 0xFFFFFFFFu
+
+/* UnaryCall, kernel_call.rs:28-36. Sigmoid/Tanh/Gelu/Silu/Exp over bf16/f16
+ * run as a gather through the 65536-entry table (src/cpu/lut.rs:76-98). */
+typedef struct holo_unary_call {
+    holo_buffer_ref input;
+    holo_buffer_ref output;
+    uint64_t element_count;
+    uint16_t witt_bits;
+    uint8_t dtype;
+} holo_unary_call;
+
+/* MatMulCall, kernel_call.rs:49-65. Row-major A[m,k] * B[k,n] -> C[m,n];
+ * f32 or bf16 (fp32 accumulation, bf16 result narrowed by truncation,
+ * src/cpu/float_kernels.rs:368-392). b_packed = 1 is refused (UnsupportedOp). */
+typedef struct holo_matmul_call {
+    holo_buffer_ref a;
+    holo_buffer_ref b;
+    holo_buffer_ref output;
+    uint32_t m, k, n;
+    uint8_t dtype;
+    uint8_t b_packed;
+} holo_matmul_call;
+
+/* KvCacheWriteCall, kernel_call.rs:742-759 (byte rows, honest copy:
+ * src/cpu/kernels.rs:455-501). `pos` is a device-resident 4-byte LE u32. */
+typedef struct holo_kv_cache_write_call {
+    holo_buffer_ref cache;
+    holo_buffer_ref new_rows_buf;
+    holo_buffer_ref pos;
+    holo_buffer_ref output;
+    uint32_t planes, bucket_rows, new_rows, row_bytes;
+} holo_kv_cache_write_call;
+
+/* New (tag 122): int8 KV quantize + append. Each new row (head_dim values of
+ * `dtype` in {bf16, f16, f32}) is quantized with the reference's per-row
+ * symmetric scheme (src/cpu/simd.rs:4755-4785: scale = max|x|/127,
+ * q = clamp(round-half-away(x * (127/max|x|)), -127, 127); an all-zero row is
+ * q = 0, scale = 0) and placed at ring row (pos + j) % bucket_rows of plane p,
+ * as KvCacheWrite places rows. Caches: int8 [planes, bucket_rows, head_dim] and
+ * f32 scales [planes, bucket_rows].
+ *   output == cache and output_scales == cache_scales (same slot and offset):
+ *       in-place form (the executor's O(new_rows) move, session.rs:1313-1370);
+ *   otherwise: honest-copy form, outputs must not overlap any input. */
+typedef struct holo_kv_quant_append_call {
+    holo_buffer_ref new_rows_buf;
+    holo_buffer_ref pos;
+    holo_buffer_ref cache;
+    holo_buffer_ref cache_scales;
+    holo_buffer_ref output;
+    holo_buffer_ref output_scales;
+    uint32_t planes, bucket_rows, new_rows, head_dim;
+    uint8_t dtype;
+} holo_kv_quant_append_call;
+
+/* New (tag 123): single-token GQA decode attention over int8 K/V caches laid
+ * out as holo_kv_quant_append_call writes them. For sequence b the visible keys
+ * are rows [0, min(lens[b], bucket_rows)) of each kv-head plane; query head h
+ * reads kv head h / (heads / kv_heads) (kernel_call.rs:691-716). Scores are
+ * dot(q, k_dequant) / scale with scale = sqrtf(head_dim) (or 1/f32(scale_bits)),
+ * fp32 softmax; the result equals the reference DecodeAttentionValid
+ * {b=1, past=L-1, valid=L-1, q_rows=new=1} over the dequantized rows
+ * (src/cpu/float_kernels.rs:4192-4307) within tolerance. A sequence with no
+ * visible key produces the exact zero vector. q/output dtype: bf16 or f32
+ * ([batch, heads, head_dim]); lens: u32 [batch], device-resident. */
+typedef struct holo_decode_attention_i8_call {
+    holo_buffer_ref q;
+    holo_buffer_ref k_cache;
+    holo_buffer_ref v_cache;
+    holo_buffer_ref k_scales;
+    holo_buffer_ref v_scales;
+    holo_buffer_ref lens;
+    holo_buffer_ref output;
+    uint32_t batch, heads, kv_heads, bucket_rows, head_dim, scale_bits;
+    uint8_t dtype;
+} holo_decode_attention_i8_call;
+
+/* KernelCall (kernel_call.rs:1146-1276): tag + the variant's payload. */
+typedef struct holo_kernel_call {
+    uint32_t tag;
+    union {
+        holo_unary_call unary;
+        holo_matmul_call matmul;
+        holo_kv_cache_write_call kv_write;
+        holo_kv_quant_append_call kv_quant_append;
+        holo_decode_attention_i8_call attn_i8;
+    } u;
+} holo_kernel_call;
+
+typedef struct holo_backend holo_backend;
+
+/* Create a backend on HIP device `device`, enqueueing on `stream` (a
+ * hipStream_t; NULL = the device's null stream). Replaces CpuBackend::new()
+ * (crates/hologram-compute/src/cpu.rs:55-87). */
+int holo_hip_backend_create(int device, void *stream, holo_backend **out);
+int holo_hip_backend_destroy(holo_backend *be);
+/* Change the stream later dispatches enqueue on. */
+int holo_hip_set_stream(holo_backend *be, void *stream);
+
+/* Bind slot -> device range (pool-owned memory; the backend never frees it).
+ * The slot table is the device form of BufferArena's binding table
+ * (crates/hologram-exec/src/buffer.rs:312-335). */
+int holo_hip_slot_bind(holo_backend *be, uint32_t slot, void *device_ptr, uint64_t bytes);
+int holo_hip_slot_unbind(holo_backend *be, uint32_t slot);
+
+/* Backend::dispatch (backend.rs:8-15): validate, then enqueue the call's
+ * kernels on the backend's stream. Asynchronous: call holo_hip_synchronize
+ * before the host reads any output. Unsupported tags return
+ * HOLO_ERR_UNSUPPORTED_OP so the caller can route the call elsewhere, as the
+ * reference's GPU backends do (src/metal_backend/mod.rs:172-180). */
+int holo_hip_dispatch(holo_backend *be, const holo_kernel_call *call);
+/* Same, from one call in the archive wire format (u16 LE discriminant + LE
+ * payload, crates/hologram-archive/src/kernel_codec.rs:130-137, 557-813).
+ * *consumed receives the encoded length. */
+int holo_hip_dispatch_encoded(holo_backend *be, const uint8_t *wire, size_t len,
+                              size_t *consumed);
+int holo_hip_synchronize(holo_backend *be);
+
+/* Host-side checks of one call against slot sizes, with no device work
+ * (the refusals of src/cpu/kernels.rs, float_kernels.rs; split_borrow's
+ * overlap rule, buffer.rs:974-998). slot_bytes[i] = size of slot i. */
+int holo_hip_validate(const holo_kernel_call *call, const uint64_t *slot_bytes, uint32_t nslots);
+/* Decode one wire-format call into *out (no device work). */
+int holo_hip_decode_call(const uint8_t *wire, size_t len, holo_kernel_call *out, size_t *consumed);
+
+/* The 65536-entry table the backend stages in LDS for (act, dtype):
+ * T[b] = narrow(f(widen(b))), src/cpu/lut.rs:43-67. */
+int holo_hip_lut_table(int act, int dtype, uint16_t *out65536);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *holo_hip_last_error_message(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

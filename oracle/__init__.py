@@ -1,0 +1,182 @@
+"""Python binding of the CPU oracle (oracle/libholo_oracle.so).
+
+TEST INFRASTRUCTURE: imported only by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker and the timed CPU baseline. The
+product (hologram_amd/) never imports it. Build with `make -C oracle`.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libholo_oracle.so"
+
+DTYPE_I8, DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 2, 6, 7, 8
+ACT_SIGMOID, ACT_TANH, ACT_GELU, ACT_SILU, ACT_EXP = 0, 1, 2, 3, 4
+
+_P = ctypes.c_void_p
+_S = ctypes.c_size_t
+_U32 = ctypes.c_uint32
+_F = ctypes.c_float
+_SIGS = {
+    "or_bf16_to_f32": (_F, [ctypes.c_uint16]),
+    "or_f32_to_bf16": (ctypes.c_uint16, [_F]),
+    "or_f16_to_f32": (_F, [ctypes.c_uint16]),
+    "or_f32_to_f16": (ctypes.c_uint16, [_F]),
+    "or_exp_f32_det": (_F, [_F]),
+    "or_libm_expf": (_F, [_F]),
+    "or_sigmoid_f": (_F, [_F]),
+    "or_tanh_f": (_F, [_F]),
+    "or_gelu_f": (_F, [_F]),
+    "or_silu_f": (_F, [_F]),
+    "or_lut_act_ref": (_F, [ctypes.c_int, _F]),
+    "or_build_table": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _P]),
+    "or_unary_lut": (None, [_P, _P, _P, _S]),
+    "or_quantize_row_i8": (_F, [_P, _P, _S]),
+    "or_matmul_i8_pc_omajor": (None, [_P, _P, _P, _P, _S, _S, _S]),
+    "or_fnv1a_f32": (ctypes.c_uint64, [_P, _S]),
+    "or_kv_cache_write": (ctypes.c_int, [_P, _P, _U32, _P, _U32, _U32, _U32, _U32]),
+    "or_kv_quant_append": (ctypes.c_int, [_P, ctypes.c_int, _U32, _P, _P, _U32, _U32, _U32,
+                                          _U32]),
+    "or_dequant_i8": (None, [_P, _P, _P, _S, _S]),
+    "or_attn_scale": (_F, [_U32, _U32]),
+    "or_decode_attention_valid_f32": (None, [_P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32,
+                                             _U32, _U32, _U32, _F, _U32]),
+    "or_decode_attention_i8": (None, [_P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32,
+                                      _F]),
+    "or_matmul_ref_f64": (None, [_P, _P, _P, _S, _S, _S]),
+    "or_max_rel_err": (ctypes.c_double, [_P, _P, _S]),
+    # cpu_baseline.c (timing engines)
+    "cb_lut": (None, [_P, _P, _P, _S, ctypes.c_int]),
+    "cb_matmul_f32": (None, [_P, _P, _P, _S, _S, _S, ctypes.c_int]),
+    "cb_matmul_bf16": (None, [_P, _P, _P, _S, _S, _S, ctypes.c_int]),
+    "cb_kv_quant_append_copy": (ctypes.c_int, [_P, ctypes.c_int, _U32, _P, _P, _P, _P, _U32,
+                                               _U32, _U32, _U32, ctypes.c_int]),
+    "cb_decode_attention_i8": (None, [_P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32,
+                                      _F, ctypes.c_int]),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} missing: run `make -C oracle`")
+        h = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(h, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = h
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def build_table(act: int, dtype: int = DTYPE_BF16) -> np.ndarray:
+    t = np.zeros(65536, np.uint16)
+    if lib().or_build_table(act, dtype, _p(t)) != 0:
+        raise ValueError("no oracle table for this activation/dtype")
+    return t
+
+
+def unary_lut(table: np.ndarray, x: np.ndarray) -> np.ndarray:
+    out = np.empty_like(x)
+    lib().or_unary_lut(_p(table), _p(x), _p(out), x.size)
+    return out
+
+
+def quantize_row_i8(a: np.ndarray) -> tuple:
+    a = np.ascontiguousarray(a, np.float32)
+    q = np.zeros(a.size, np.int8)
+    s = lib().or_quantize_row_i8(_p(a), _p(q), a.size)
+    return q, np.float32(s)
+
+
+def matmul_i8_pc_omajor(a, bq, scales, m, k, n) -> np.ndarray:
+    out = np.zeros(m * n, np.float32)
+    lib().or_matmul_i8_pc_omajor(_p(a), _p(bq), _p(scales), _p(out), m, k, n)
+    return out
+
+
+def fnv1a_f32(v: np.ndarray) -> int:
+    v = np.ascontiguousarray(v, np.float32)
+    return lib().or_fnv1a_f32(_p(v), v.size)
+
+
+def kv_cache_write(cache: np.ndarray, new: np.ndarray, pos: int, planes: int, bucket: int,
+                   new_rows: int, row_bytes: int) -> np.ndarray:
+    out = np.empty_like(cache)
+    rc = lib().or_kv_cache_write(_p(cache), _p(new), pos, _p(out), planes, bucket, new_rows,
+                                 row_bytes)
+    if rc != 0:
+        raise ValueError(f"kv_cache_write refused ({rc})")
+    return out
+
+
+def kv_quant_append(new: np.ndarray, dtype: int, pos: int, cache_q: np.ndarray,
+                    cache_s: np.ndarray, planes: int, bucket: int, new_rows: int,
+                    head_dim: int) -> tuple:
+    """Copy-form quantize+append: returns (new int8 cache, new scale cache)."""
+    oq, os_ = cache_q.copy(), cache_s.copy()
+    rc = lib().or_kv_quant_append(_p(new), dtype, pos, _p(oq), _p(os_), planes, bucket,
+                                  new_rows, head_dim)
+    if rc != 0:
+        raise ValueError(f"kv_quant_append refused ({rc})")
+    return oq, os_
+
+
+def dequant_i8(q: np.ndarray, scales: np.ndarray, row_len: int) -> np.ndarray:
+    rows = q.size // row_len
+    out = np.empty(rows * row_len, np.float32)
+    lib().or_dequant_i8(_p(q), _p(scales), _p(out), rows, row_len)
+    return out
+
+
+def attn_scale(head_dim: int, scale_bits: int = 0) -> float:
+    return lib().or_attn_scale(head_dim, scale_bits)
+
+
+def decode_attention_valid_f32(q, kp, vp, kn, vn, b, h, hkv, m, past, new, d, scale,
+                               vis_past) -> np.ndarray:
+    out = np.zeros(b * h * m * d, np.float32)
+    lib().or_decode_attention_valid_f32(_p(q), _p(kp), _p(vp), _p(kn), _p(vn), _p(out), b, h,
+                                        hkv, m, past, new, d, scale, vis_past)
+    return out
+
+
+def decode_attention_i8(q, kq, ks, vq, vs, lens, B, H, Hkv, bucket, D, scale) -> np.ndarray:
+    out = np.zeros(B * H * D, np.float32)
+    lib().or_decode_attention_i8(_p(q), _p(kq), _p(ks), _p(vq), _p(vs), _p(lens), _p(out), B,
+                                 H, Hkv, bucket, D, scale)
+    return out
+
+
+def matmul_ref_f64(a, b, m, k, n) -> np.ndarray:
+    out = np.zeros(m * n, np.float32)
+    lib().or_matmul_ref_f64(_p(a), _p(b), _p(out), m, k, n)
+    return out
+
+
+def max_rel_err(got, want) -> float:
+    got = np.ascontiguousarray(got, np.float32)
+    want = np.ascontiguousarray(want, np.float32)
+    return lib().or_max_rel_err(_p(got), _p(want), got.size)
+
+
+def host_threads() -> int:
+    """Threads for the CPU baseline: this process's CPU share, at most 16."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))

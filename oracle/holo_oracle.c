@@ -1,0 +1,482 @@
+/*
+ * holo_oracle.c — CPU restatement of the reference hot path (TEST INFRASTRUCTURE).
+ *
+ * Loaded only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg, as the checker. Build: oracle/Makefile (-O2 -ffp-contract=off
+ * -fno-fast-math, x86-64 SSE2). Each function cites the reference file:line it
+ * restates (paths under crates/hologram-compute/ unless stated). The pins that
+ * check each function are listed in holo_oracle.h.
+ */
+#include "holo_oracle.h"
+
+#include <math.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* bit helpers                                                              */
+/* ------------------------------------------------------------------------ */
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* Rust's `f32 as i32`: truncate toward zero, saturate, NaN -> 0. */
+static inline int32_t rust_f32_as_i32(float t)
+{
+    if (t != t) return 0;
+    if (t >= 2147483648.0f) return INT32_MAX;
+    if (t <= -2147483904.0f) return INT32_MIN;
+    return (int32_t)t;
+}
+
+/* ------------------------------------------------------------------------ */
+/* codecs: src/cpu/dtype.rs:69-153                                          */
+/* ------------------------------------------------------------------------ */
+float or_bf16_to_f32(uint16_t b) { return u2f((uint32_t)b << 16); }          /* :69-73 */
+uint16_t or_f32_to_bf16(float v) { return (uint16_t)(f2u(v) >> 16); }        /* :75-79 */
+
+float or_f16_to_f32(uint16_t bits)                                            /* :94-118 */
+{
+    uint32_t sign = (bits >> 15) & 1u, ex = (bits >> 10) & 0x1fu, mant = bits & 0x3ffu;
+    uint32_t out;
+    if (ex == 0) {
+        if (mant == 0) {
+            out = sign << 31;
+        } else {
+            uint32_t m = mant;
+            int32_t e = 1;
+            while ((m & 0x400u) == 0) { m <<= 1; e -= 1; }
+            out = (sign << 31) | ((uint32_t)(127 - 15 + e) << 23) | ((m & 0x3ffu) << 13);
+        }
+    } else if (ex == 0x1f) {
+        out = (sign << 31) | (0xffu << 23) | (mant << 13);
+    } else {
+        out = (sign << 31) | ((ex + 127 - 15) << 23) | (mant << 13);
+    }
+    return u2f(out);
+}
+
+uint16_t or_f32_to_f16(float v)                                               /* :121-153 */
+{
+    uint32_t bits = f2u(v);
+    uint16_t sign = (uint16_t)((bits >> 31) & 1u);
+    int32_t ex = (int32_t)((bits >> 23) & 0xffu);
+    uint32_t mant = bits & 0x7fffffu;
+    if (ex == 0xff) {
+        uint16_t nan_bit = mant != 0 ? 0x200 : 0;
+        return (uint16_t)((sign << 15) | (0x1f << 10) | nan_bit);
+    }
+    int32_t ne = ex - 127 + 15;
+    if (ne >= 0x1f) return (uint16_t)((sign << 15) | (0x1f << 10));
+    if (ne <= 0) {
+        if (ne < -10) return (uint16_t)(sign << 15);
+        uint32_t m = mant | 0x800000u;
+        uint32_t shift = (uint32_t)(1 - ne) + 13;
+        uint32_t rounded = (m + (1u << (shift - 1))) >> shift;
+        return (uint16_t)((sign << 15) | (uint16_t)rounded);
+    }
+    uint16_t rm = (uint16_t)((mant + 0x1000u) >> 13);
+    if (rm & 0x400) {
+        int32_t be = ne + 1;
+        if (be >= 0x1f) return (uint16_t)((sign << 15) | (0x1f << 10));
+        return (uint16_t)((sign << 15) | ((uint16_t)be << 10));
+    }
+    return (uint16_t)((sign << 15) | ((uint16_t)ne << 10) | (rm & 0x3ff));
+}
+
+/* ------------------------------------------------------------------------ */
+/* deterministic exp: src/cpu/simd.rs:4191-4239                             */
+/* ------------------------------------------------------------------------ */
+float or_exp_f32_det(float x)
+{
+    const float LO = -87.33654f, HI = 88.0f;
+    const float LOG2E = 1.44269504088896340736f;     /* core::f32::consts::LOG2_E */
+    const float LN2_HI = u2f(0x3F318000u);
+    const float LN2_LO = -2.1219444e-4f;
+    const float C6 = 1.0f / 720.0f, C5 = 1.0f / 120.0f, C4 = 1.0f / 24.0f,
+                C3 = 1.0f / 6.0f, C2 = 0.5f;
+    if (x != x || x < LO) return 0.0f;
+    if (x > HI) x = HI;
+    float t = x * LOG2E;
+    int32_t k = t >= 0.0f ? rust_f32_as_i32(t + 0.5f) : rust_f32_as_i32(t - 0.5f);
+    float kf = (float)k;
+    float r = (x - kf * LN2_HI) - kf * LN2_LO;
+    float p = C6;
+    p = p * r + C5;
+    p = p * r + C4;
+    p = p * r + C3;
+    p = p * r + C2;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    uint32_t sb = (uint32_t)(k + 127) << 23;
+    if (sb > 0x7f000000u) sb = 0x7f000000u;
+    return p * u2f(sb);
+}
+
+/* ------------------------------------------------------------------------ */
+/* libm 0.2.16 `expf` (Cargo.lock:2471-2473; call site float_kernels.rs:3498-3500).
+ * The crate is not vendored in the reference. Its expf is the published
+ * FreeBSD msun e_expf.c algorithm (as carried by musl): special-case cutoffs,
+ * ln2 hi/lo reduction with k = trunc(x/ln2 +- 1/2), the degree-2 rational
+ * remez form y = 1 + (x*c/(2-c) - lo + hi), then scalbnf. Restated here from
+ * that published algorithm; pinned against a correctly rounded exp.        */
+/* ------------------------------------------------------------------------ */
+static float or_scalbnf(float x, int32_t n)
+{
+    const float x1p127 = u2f(0x7f000000u), x1p_126 = u2f(0x00800000u), x1p24 = u2f(0x4b800000u);
+    if (n > 127) {
+        x *= x1p127;
+        n -= 127;
+        if (n > 127) {
+            x *= x1p127;
+            n -= 127;
+            if (n > 127) n = 127;
+        }
+    } else if (n < -126) {
+        x *= x1p_126 * x1p24;
+        n += 126 - 24;
+        if (n < -126) {
+            x *= x1p_126 * x1p24;
+            n += 126 - 24;
+            if (n < -126) n = -126;
+        }
+    }
+    return x * u2f((uint32_t)(0x7f + n) << 23);
+}
+
+float or_libm_expf(float x)
+{
+    const float HALF[2] = {0.5f, -0.5f};
+    const float LN2_HI = 6.9314575195e-01f;  /* 0x3f317200 */
+    const float LN2_LO = 1.4286067653e-06f;  /* 0x35bfbe8e */
+    const float INV_LN2 = 1.4426950216e+00f; /* 0x3fb8aa3b */
+    const float P1 = 1.6666625440e-1f;       /* 0xaaaa8f.0p-26 */
+    const float P2 = -2.7667332906e-3f;      /* -0xb55215.0p-32 */
+    const float x1p127 = u2f(0x7f000000u);
+    uint32_t hx = f2u(x);
+    int32_t sign = (int32_t)(hx >> 31);
+    hx &= 0x7fffffffu;
+    if (hx >= 0x42aeac50u) {                 /* |x| >= 87.33655 or NaN */
+        if (hx > 0x7f800000u) return x;      /* NaN: returned unchanged */
+        if (hx >= 0x42b17218u && !sign) return x * x1p127;   /* overflow */
+        if (sign && hx >= 0x42cff1b5u) return 0.0f;          /* x <= -103.97 */
+    }
+    int32_t k;
+    float hi, lo;
+    if (hx > 0x3eb17218u) {                  /* |x| > 0.5 ln2 */
+        if (hx > 0x3f851592u)                /* |x| > 1.5 ln2 */
+            k = rust_f32_as_i32(INV_LN2 * x + HALF[sign]);
+        else
+            k = 1 - sign - sign;
+        float kf = (float)k;
+        hi = x - kf * LN2_HI;
+        lo = kf * LN2_LO;
+        x = hi - lo;
+    } else if (hx > 0x39000000u) {           /* |x| > 2^-14 */
+        k = 0;
+        hi = x;
+        lo = 0.0f;
+    } else {
+        return 1.0f + x;
+    }
+    float xx = x * x;
+    float c = x - xx * (P1 + xx * P2);
+    float y = 1.0f + (((x * c) / (2.0f - c) - lo) + hi);
+    return k == 0 ? y : or_scalbnf(y, k);
+}
+
+/* ------------------------------------------------------------------------ */
+/* activations: src/cpu/float_kernels.rs:3537-3566, op order kept, no FMA   */
+/* ------------------------------------------------------------------------ */
+float or_sigmoid_f(float x) { return 1.0f / (1.0f + or_exp_f32_det(-x)); }
+float or_tanh_f(float x)
+{
+    float e = or_exp_f32_det(2.0f * x);
+    return (e - 1.0f) / (e + 1.0f);
+}
+float or_gelu_f(float x)
+{
+    /* 0.5 * x * (1.0 + tanh_f(0.797_884_6 * (x + 0.044_715 * x * x * x))) */
+    float cube = ((0.044715f * x) * x) * x;
+    float u = 0.7978846f * (x + cube);
+    return (0.5f * x) * (1.0f + or_tanh_f(u));
+}
+float or_silu_f(float x) { return x * or_sigmoid_f(x); }
+
+float or_lut_act_ref(int act, float x)
+{
+    switch (act) {
+    case OR_ACT_SIGMOID: return or_sigmoid_f(x);
+    case OR_ACT_TANH: return or_tanh_f(x);
+    case OR_ACT_GELU: return or_gelu_f(x);
+    case OR_ACT_SILU: return or_silu_f(x);
+    case OR_ACT_EXP: return or_libm_expf(x);
+    default: return NAN;
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* LUT build / gather: src/cpu/lut.rs:43-67, 76-98                          */
+/* ------------------------------------------------------------------------ */
+int or_build_table(int act, int dtype, uint16_t *t)
+{
+    if (act < 0 || act > OR_ACT_EXP) return -1;
+    if (dtype != OR_DTYPE_BF16 && dtype != OR_DTYPE_F16) return -1;
+    for (uint32_t bits = 0; bits < 65536u; ++bits) {
+        float x = dtype == OR_DTYPE_F16 ? or_f16_to_f32((uint16_t)bits)
+                                        : or_bf16_to_f32((uint16_t)bits);
+        float y = or_lut_act_ref(act, x);
+        t[bits] = dtype == OR_DTYPE_F16 ? or_f32_to_f16(y) : or_f32_to_bf16(y);
+    }
+    return 0;
+}
+
+void or_unary_lut(const uint16_t *t, const uint16_t *in, uint16_t *out, size_t n)
+{
+    for (size_t i = 0; i < n; ++i) out[i] = t[in[i]];
+}
+
+/* ------------------------------------------------------------------------ */
+/* int8 scheme: src/cpu/simd.rs:4755-4785                                   */
+/* ------------------------------------------------------------------------ */
+float or_quantize_row_i8(const float *a, int8_t *q, size_t k)
+{
+    float amax = 0.0f;
+    for (size_t i = 0; i < k; ++i) {
+        float v = a[i];
+        float av = v < 0.0f ? -v : v;
+        if (av > amax) amax = av;
+    }
+    if (amax == 0.0f) return 0.0f;           /* q left untouched, as the reference */
+    float inv = 127.0f / amax;
+    for (size_t i = 0; i < k; ++i) {
+        float t = a[i] * inv;
+        int32_t r = t >= 0.0f ? rust_f32_as_i32(t + 0.5f) : rust_f32_as_i32(t - 0.5f);
+        if (r < -127) r = -127;
+        if (r > 127) r = 127;
+        q[i] = (int8_t)r;
+    }
+    return amax / 127.0f;
+}
+
+/* simd.rs:5295-5480 with the portable inner of :5203-5215: exact i32 dot,
+ * out = (acc as f32) * (scale_a * scales[j]); an all-zero row writes zeros. */
+void or_matmul_i8_pc_omajor(const float *a, const int8_t *bq, const float *scales,
+                            float *out, size_t m, size_t k, size_t n)
+{
+    int8_t q[4096];
+    if (k > sizeof q) return;
+    for (size_t i = 0; i < m; ++i) {
+        memset(q, 0, k);
+        float sa = or_quantize_row_i8(a + i * k, q, k);
+        if (sa == 0.0f) {
+            for (size_t j = 0; j < n; ++j) out[i * n + j] = 0.0f;
+            continue;
+        }
+        for (size_t j = 0; j < n; ++j) {
+            const int8_t *row = bq + j * k;
+            int32_t acc = 0;
+            for (size_t kk = 0; kk < k; ++kk) acc += (int32_t)q[kk] * (int32_t)row[kk];
+            out[i * n + j] = (float)acc * (sa * scales[j]);
+        }
+    }
+}
+
+/* FNV-1a over the LE bytes of each f32 (simd.rs:8237-8246). */
+uint64_t or_fnv1a_f32(const float *v, size_t n)
+{
+    uint64_t h = 0xcbf29ce484222325ull;
+    for (size_t i = 0; i < n; ++i) {
+        uint32_t u = f2u(v[i]);
+        for (int b = 0; b < 4; ++b) {
+            h ^= (u >> (8 * b)) & 0xffu;
+            h *= 0x100000001b3ull;
+        }
+    }
+    return h;
+}
+
+/* ------------------------------------------------------------------------ */
+/* KV write: src/cpu/kernels.rs:455-501                                     */
+/* ------------------------------------------------------------------------ */
+int or_kv_cache_write(const uint8_t *cache, const uint8_t *nw, uint32_t posv, uint8_t *out,
+                      uint32_t planes, uint32_t bucket, uint32_t new_rows, uint32_t row)
+{
+    if (bucket == 0 || row == 0) return 3;   /* UnsupportedOp */
+    if (new_rows > bucket) return 3;
+    size_t plane_bytes = (size_t)bucket * row;
+    size_t pos = (size_t)posv % bucket;
+    memcpy(out, cache, (size_t)planes * plane_bytes);
+    for (size_t p = 0; p < planes; ++p) {
+        size_t ob = p * plane_bytes, nb = p * (size_t)new_rows * row;
+        for (size_t j = 0; j < new_rows; ++j) {
+            size_t dst = ob + ((pos + j) % bucket) * row;
+            memcpy(out + dst, nw + nb + j * row, row);
+        }
+    }
+    return 0;
+}
+
+static float widen(const void *base, int dtype, size_t i)
+{
+    if (dtype == OR_DTYPE_BF16) return or_bf16_to_f32(((const uint16_t *)base)[i]);
+    if (dtype == OR_DTYPE_F16) return or_f16_to_f32(((const uint16_t *)base)[i]);
+    return ((const float *)base)[i];
+}
+
+int or_kv_quant_append(const void *nw, int dtype, uint32_t posv, int8_t *cq, float *cs,
+                       uint32_t planes, uint32_t bucket, uint32_t new_rows, uint32_t d)
+{
+    float row[8192];
+    if (bucket == 0 || d == 0 || d > 8192) return 3;
+    if (new_rows > bucket) return 3;
+    if (dtype != OR_DTYPE_BF16 && dtype != OR_DTYPE_F16 && dtype != OR_DTYPE_F32) return 3;
+    size_t pos = (size_t)posv % bucket;
+    for (size_t p = 0; p < planes; ++p) {
+        for (size_t j = 0; j < new_rows; ++j) {
+            size_t src = (p * new_rows + j) * (size_t)d;
+            for (size_t c = 0; c < d; ++c) row[c] = widen(nw, dtype, src + c);
+            size_t r = p * (size_t)bucket + (pos + j) % bucket;
+            int8_t *dst = cq + r * d;
+            memset(dst, 0, d);                 /* all-zero row: q defined as 0 */
+            cs[r] = or_quantize_row_i8(row, dst, d);
+        }
+    }
+    return 0;
+}
+
+void or_dequant_i8(const int8_t *q, const float *scales, float *out, size_t rows, size_t len)
+{
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t c = 0; c < len; ++c)
+            out[r * len + c] = (float)q[r * len + c] * scales[r];   /* kernels.rs:270 */
+}
+
+/* ------------------------------------------------------------------------ */
+/* decode attention: src/cpu/float_kernels.rs:3834-3957, 4192-4307          */
+/* ------------------------------------------------------------------------ */
+float or_attn_scale(uint32_t d, uint32_t scale_bits)             /* :4256-4266 */
+{
+    float dflt = sqrtf((float)d);
+    if (dflt < 1.0f) dflt = 1.0f;
+    if (scale_bits == 0) return dflt;
+    float sm = u2f(scale_bits);
+    return sm > 0.0f ? 1.0f / sm : dflt;
+}
+
+/* one (b, h, q-row): :3834-3883. The dot is a sequential scalar sum here; the
+ * reference's SIMD lane order differs in the last bits (tolerance metric). */
+static void valid_row(const float *q, const float *kp, const float *vp, const float *kn,
+                      const float *vn, float *out, size_t vis_past, size_t new_vis, size_t d,
+                      float scale, float *sc)
+{
+    size_t vis = vis_past + new_vis;
+    for (size_t c = 0; c < d; ++c) out[c] = 0.0f;
+    if (vis == 0) return;
+    for (size_t j = 0; j < vis; ++j) {
+        const float *kr = j < vis_past ? kp + j * d : kn + (j - vis_past) * d;
+        float s = 0.0f;
+        for (size_t c = 0; c < d; ++c) s += q[c] * kr[c];
+        sc[j] = s / scale;
+    }
+    float mx = -INFINITY;
+    for (size_t j = 0; j < vis; ++j) mx = fmaxf(mx, sc[j]);
+    for (size_t j = 0; j < vis; ++j) sc[j] = or_exp_f32_det(sc[j] - mx);
+    float sum = 0.0f;
+    for (size_t j = 0; j < vis; ++j) sum += sc[j];
+    float denom = sum > 1e-30f ? sum : 1e-30f;
+    for (size_t j = 0; j < vis; ++j) {
+        float p = sc[j] / denom;
+        const float *vr = j < vis_past ? vp + j * d : vn + (j - vis_past) * d;
+        for (size_t c = 0; c < d; ++c) out[c] += p * vr[c];
+    }
+}
+
+#include <stdlib.h>
+void or_decode_attention_valid_f32(const float *q, const float *kp, const float *vp,
+                                   const float *kn, const float *vn, float *out,
+                                   uint32_t b, uint32_t h, uint32_t hkv, uint32_t m,
+                                   uint32_t past, uint32_t nnew, uint32_t d, float scale,
+                                   uint32_t vis_past)
+{
+    /* :3899-3957: row r -> (bi, hi, qi); kvh = bi*hkv + hi/group */
+    if (hkv == 0) hkv = h;
+    size_t group = h / hkv;
+    if (vis_past > past) vis_past = past;
+    float *sc = (float *)malloc(sizeof(float) * ((size_t)past + nnew + 1));
+    size_t rows = (size_t)b * h * m;
+    for (size_t r = 0; r < rows; ++r) {
+        size_t bi = r / ((size_t)h * m), hi = (r / m) % h, qi = r % m;
+        size_t kvh = bi * hkv + hi / group;
+        size_t new_vis = qi + 1 < nnew ? qi + 1 : nnew;
+        valid_row(q + r * d, kp + kvh * (size_t)past * d, vp + kvh * (size_t)past * d,
+                  kn + kvh * (size_t)nnew * d, vn + kvh * (size_t)nnew * d, out + r * d,
+                  vis_past, new_vis, d, scale, sc);
+    }
+    free(sc);
+}
+
+void or_decode_attention_i8(const float *q, const int8_t *kq, const float *ks,
+                            const int8_t *vq, const float *vs, const uint32_t *lens,
+                            float *out, uint32_t B, uint32_t H, uint32_t Hkv,
+                            uint32_t bucket, uint32_t D, float scale)
+{
+    size_t group = H / Hkv;
+    float *kd = (float *)malloc(sizeof(float) * (size_t)bucket * D);
+    float *vd = (float *)malloc(sizeof(float) * (size_t)bucket * D);
+    float *sc = (float *)malloc(sizeof(float) * ((size_t)bucket + 1));
+    for (size_t b = 0; b < B; ++b) {
+        size_t L = lens[b] < bucket ? lens[b] : bucket;
+        for (size_t kh = 0; kh < Hkv; ++kh) {
+            size_t plane = b * Hkv + kh;
+            or_dequant_i8(kq + plane * (size_t)bucket * D, ks + plane * (size_t)bucket, kd, L, D);
+            or_dequant_i8(vq + plane * (size_t)bucket * D, vs + plane * (size_t)bucket, vd, L, D);
+            for (size_t g = 0; g < group; ++g) {
+                size_t hh = kh * group + g;
+                const float *qr = q + (b * H + hh) * D;
+                float *orow = out + (b * H + hh) * D;
+                if (L == 0) {
+                    for (size_t c = 0; c < D; ++c) orow[c] = 0.0f;
+                    continue;
+                }
+                /* past = L-1 dequantized rows, new = the last row (q_rows = new = 1) */
+                valid_row(qr, kd, vd, kd + (L - 1) * D, vd + (L - 1) * D, orow, L - 1, 1, D,
+                          scale, sc);
+            }
+        }
+    }
+    free(kd);
+    free(vd);
+    free(sc);
+}
+
+/* ------------------------------------------------------------------------ */
+/* MatMul reference: tests/conformance.rs:100-112, metric :138-144          */
+/* ------------------------------------------------------------------------ */
+void or_matmul_ref_f64(const float *a, const float *b, float *out, size_t m, size_t k, size_t n)
+{
+    double *acc = (double *)malloc(sizeof(double) * n);
+    for (size_t i = 0; i < m; ++i) {
+        for (size_t j = 0; j < n; ++j) acc[j] = 0.0;
+        for (size_t p = 0; p < k; ++p) {
+            double av = (double)a[i * k + p];
+            const float *br = b + p * n;
+            for (size_t j = 0; j < n; ++j) acc[j] += av * (double)br[j];
+        }
+        for (size_t j = 0; j < n; ++j) out[i * n + j] = (float)acc[j];
+    }
+    free(acc);
+}
+
+double or_max_rel_err(const float *got, const float *want, size_t n)
+{
+    double scale = 0.0, worst = 0.0;
+    for (size_t i = 0; i < n; ++i) {
+        double w = fabs((double)want[i]);
+        if (w > scale) scale = w;
+    }
+    scale += 1e-9;
+    for (size_t i = 0; i < n; ++i) {
+        double e = fabs((double)got[i] - (double)want[i]) / scale;
+        if (e > worst || e != e) worst = e != e ? INFINITY : e;
+    }
+    return worst;
+}

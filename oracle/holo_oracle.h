@@ -1,0 +1,107 @@
+/*
+ * holo_oracle.h — CPU restatement of the Hologram reference's hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker that the HIP backend
+ * (hologram_amd/) is compared against, and the CPU baseline bench.py times
+ * beside it. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load it. The product never links, loads or calls anything here.
+ *
+ * Every function restates one reference function (Rust, crates/hologram-compute)
+ * in plain C with the same IEEE-754 binary32 operation order, built with
+ * -ffp-contract=off -fno-fast-math on x86-64 SSE2 (no x87, no FMA), which is
+ * the target the reference's LUT tables are defined against.
+ *
+ * Parity pins (what checks each function; see tests/test_oracle_pins.py):
+ *   bf16/f16 codecs ............ closed form (exhaustive round trips, RNE rules)
+ *   or_exp_f32_det ............. closed form (|rel err| <= 2e-6 vs long double)
+ *   or_gelu/silu/sigmoid/tanh .. reference test tolerances (tests/lut.rs:67-132)
+ *                                 and f64 closed forms within 1 bf16 ulp
+ *   or_libm_expf ............... correctly-rounded exp (<= 1 ulp everywhere,
+ *                                 bit-equal on all non-fragile bf16 entries)
+ *   or_quantize_row_i8 ......... reference golden FNV 0x787ccdc172029f9b
+ *                                 (simd.rs:8236-8259) through or_matmul_i8_pc_omajor
+ *   or_kv_cache_write .......... closed form (ring placement, brute force)
+ *   or_decode_attention_* ...... f64 softmax closed form, zero-visible row = 0
+ *   or_matmul_ref_f64 .......... closed form (identity / permutation products)
+ */
+#ifndef HOLO_ORACLE_H
+#define HOLO_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype tags: crates/hologram-types/src/dtype_id.rs:52-61 */
+enum { OR_DTYPE_I8 = 2, OR_DTYPE_F16 = 6, OR_DTYPE_BF16 = 7, OR_DTYPE_F32 = 8 };
+/* lut_act ids: crates/hologram-compute/src/kernel_call.rs:877-885 */
+enum { OR_ACT_SIGMOID = 0, OR_ACT_TANH = 1, OR_ACT_GELU = 2, OR_ACT_SILU = 3, OR_ACT_EXP = 4 };
+
+/* ---- codecs: src/cpu/dtype.rs:69-153 ---- */
+float    or_bf16_to_f32(uint16_t b);
+uint16_t or_f32_to_bf16(float v);          /* truncation, NaN payload kept */
+float    or_f16_to_f32(uint16_t b);
+uint16_t or_f32_to_f16(float v);           /* the reference's own rounding */
+
+/* ---- transcendental restatements ---- */
+float or_exp_f32_det(float x);             /* src/cpu/simd.rs:4217-4239 */
+float or_libm_expf(float x);               /* libm 0.2.16 expf (FreeBSD e_expf.c) */
+float or_sigmoid_f(float x);               /* src/cpu/float_kernels.rs:3549-3551 */
+float or_tanh_f(float x);                  /* :3553-3558 */
+float or_gelu_f(float x);                  /* :3560-3562 */
+float or_silu_f(float x);                  /* :3564-3566 */
+float or_lut_act_ref(int act, float x);    /* :3628-3638 (Erf not restated) */
+
+/* ---- LUT: src/cpu/lut.rs:43-67 (build) and :76-98 (gather) ---- */
+int  or_build_table(int act, int dtype, uint16_t *table /* [65536] */);
+void or_unary_lut(const uint16_t *table, const uint16_t *in, uint16_t *out, size_t n);
+
+/* ---- int8 scheme: src/cpu/simd.rs:4755-4785 ---- */
+float or_quantize_row_i8(const float *a, int8_t *q, size_t k);
+/* W8A8 output-major GEMV, simd.rs:5295-5480 (golden carrier, simd.rs:8236-8259) */
+void or_matmul_i8_pc_omajor(const float *a, const int8_t *bq, const float *scales,
+                            float *out, size_t m, size_t k, size_t n);
+uint64_t or_fnv1a_f32(const float *v, size_t n);
+
+/* ---- KV write: src/cpu/kernels.rs:455-501 (honest copy) ---- */
+int or_kv_cache_write(const uint8_t *cache, const uint8_t *newrows, uint32_t pos,
+                      uint8_t *out, uint32_t planes, uint32_t bucket_rows,
+                      uint32_t new_rows, uint32_t row_bytes);
+/* int8 quantize+append (new op): widen each new row (dtype of `newrows`),
+ * quantize it with or_quantize_row_i8, place the int8 row and its f32 scale at
+ * ring row (pos + j) % bucket of the int8 cache and the scale cache. Writes in
+ * place into cache_q / cache_s (the caller copies first for the copy form). */
+int or_kv_quant_append(const void *newrows, int dtype, uint32_t pos,
+                       int8_t *cache_q, float *cache_s, uint32_t planes,
+                       uint32_t bucket_rows, uint32_t new_rows, uint32_t head_dim);
+/* dequantize: src/cpu/kernels.rs:246-271, symmetric zp = 0 */
+void or_dequant_i8(const int8_t *q, const float *scales, float *out,
+                   size_t rows, size_t row_len);
+
+/* ---- decode attention: src/cpu/float_kernels.rs:3834-3957, 4192-4307 ---- */
+float or_attn_scale(uint32_t head_dim, uint32_t scale_bits);
+void or_decode_attention_valid_f32(const float *q, const float *k_past, const float *v_past,
+                                   const float *k_new, const float *v_new, float *out,
+                                   uint32_t b, uint32_t h, uint32_t hkv, uint32_t m,
+                                   uint32_t past, uint32_t nnew, uint32_t d, float scale,
+                                   uint32_t vis_past);
+/* int8-cache decode attention (new op), stated as the reference's per-sequence
+ * DecodeAttentionValid{b=1, past=L-1, valid=L-1, q=new=1} over the dequantized
+ * rows.  q: [B,H,D] f32 (widened), caches [B,Hkv,bucket,D] int8 + [B,Hkv,bucket]
+ * f32 scales, lens[B] (clamped to bucket), out [B,H,D] f32. */
+void or_decode_attention_i8(const float *q, const int8_t *kq, const float *ks,
+                            const int8_t *vq, const float *vs, const uint32_t *lens,
+                            float *out, uint32_t B, uint32_t H, uint32_t Hkv,
+                            uint32_t bucket, uint32_t D, float scale);
+
+/* ---- MatMul references: tests/conformance.rs:100-144 ---- */
+void or_matmul_ref_f64(const float *a, const float *b, float *out,
+                       size_t m, size_t k, size_t n);
+double or_max_rel_err(const float *got, const float *want, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

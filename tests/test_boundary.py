@@ -1,0 +1,190 @@
+"""CPU tests of the drop-in boundary: the C-ABI library loads and exports every
+function include/holo_hip.h declares; the host-side refusals mirror the
+reference CPU kernels' (src/cpu/kernels.rs, float_kernels.rs, buffer.rs); the
+wire codec agrees with kernel_codec.rs; the host-built tables equal the
+oracle's. No device work."""
+import ctypes
+import re
+import struct
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import ROOT
+from hologram_amd import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, BufferRef, DecodeAttentionI8Call,
+                          KernelCall, KvCacheWriteCall, KvQuantAppendCall, MatMulCall,
+                          SlotOutOfRange, UnaryCall, UnsupportedOp, decode_call, lut_table,
+                          validate)
+from hologram_amd import _ffi
+
+
+def declared_functions():
+    text = (ROOT / "include" / "holo_hip.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(holo_hip_\w+)\s*\(", text,
+                                 re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _ffi.lib()
+    names = declared_functions()
+    assert len(names) >= 12
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared but not exported"
+        assert name in _ffi.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_no_device_backend_create_fails_loudly():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a device is present")
+    from hologram_amd import HipBackend, InitError
+    with pytest.raises(InitError):
+        HipBackend(0)
+
+
+@pytest.mark.parametrize("act", range(5))
+@pytest.mark.parametrize("dtype", [DTYPE_BF16, DTYPE_F16])
+def test_host_tables_equal_oracle(act, dtype):
+    assert np.array_equal(lut_table(act, dtype), oracle.build_table(act, dtype))
+
+
+def test_erf_table_not_built():
+    with pytest.raises(UnsupportedOp):
+        lut_table(5, DTYPE_BF16)
+
+
+# ---- refusals (validate = dispatch's host checks, no device) -----------------
+
+def unary(n, dtype=DTYPE_BF16, inp=BufferRef(0), out=BufferRef(1)):
+    return KernelCall.Gelu(UnaryCall(inp, out, n, 16, dtype))
+
+
+def test_unary_sizes():
+    validate(unary(8), [16, 16])
+    with pytest.raises(SlotOutOfRange):
+        validate(unary(9), [16, 18])        # input short
+    with pytest.raises(SlotOutOfRange):
+        validate(unary(8), [16, 15])        # output short
+    with pytest.raises(SlotOutOfRange):
+        validate(unary(8), [16])            # output slot unbound
+    with pytest.raises(UnsupportedOp):
+        validate(unary(8, DTYPE_F32), [64, 64])
+    validate(unary(0), [])                  # empty is a no-op before any lookup
+
+
+def test_split_borrow_overlap_rule():
+    # same slot, disjoint ranges: allowed (buffer.rs:974-998)
+    validate(unary(4, inp=BufferRef(0, 0, 8), out=BufferRef(0, 8, 8)), [16])
+    with pytest.raises(SlotOutOfRange):
+        validate(unary(4, inp=BufferRef(0, 0, 8), out=BufferRef(0, 4, 8)), [16])
+
+
+def test_view_offsets_clamp_like_buf_range():
+    # offset past the end resolves to an empty view -> too short
+    with pytest.raises(SlotOutOfRange):
+        validate(unary(1, inp=BufferRef(0, 100)), [16, 16])
+
+
+def test_matmul_refusals():
+    mm = lambda **kw: KernelCall.MatMul(MatMulCall(BufferRef(0), BufferRef(1), BufferRef(2),
+                                                   **kw))
+    validate(mm(m=2, k=3, n=4, dtype=DTYPE_F32), [24, 48, 32])
+    with pytest.raises(SlotOutOfRange):
+        validate(mm(m=2, k=3, n=4, dtype=DTYPE_F32), [24, 47, 32])
+    with pytest.raises(UnsupportedOp):
+        validate(mm(m=2, k=3, n=4, dtype=DTYPE_F16), [24, 48, 32])
+    with pytest.raises(UnsupportedOp):
+        validate(mm(m=2, k=3, n=4, dtype=DTYPE_F32, b_packed=True), [24, 48, 32])
+    validate(mm(m=0, k=3, n=4, dtype=DTYPE_F32), [])
+
+
+def test_kv_write_refusals():
+    kw = lambda **k: KernelCall.KvCacheWrite(KvCacheWriteCall(
+        BufferRef(0), BufferRef(1), BufferRef(2), BufferRef(3), **k))
+    validate(kw(planes=2, bucket_rows=4, new_rows=1, row_bytes=8), [64, 16, 4, 64])
+    with pytest.raises(UnsupportedOp):
+        validate(kw(planes=2, bucket_rows=4, new_rows=5, row_bytes=8), [64, 80, 4, 64])
+    with pytest.raises(UnsupportedOp):
+        validate(kw(planes=2, bucket_rows=0, new_rows=0, row_bytes=8), [64, 16, 4, 64])
+    with pytest.raises(SlotOutOfRange):
+        validate(kw(planes=2, bucket_rows=4, new_rows=1, row_bytes=8), [64, 16, 3, 64])
+
+
+def test_kv_quant_append_forms():
+    def call(out_q, out_s, **k):
+        return KernelCall.KvQuantAppend(KvQuantAppendCall(
+            BufferRef(0), BufferRef(1), BufferRef(2), BufferRef(3), out_q, out_s, **k))
+    geo = dict(planes=2, bucket_rows=4, new_rows=1, head_dim=8, dtype=DTYPE_BF16)
+    sizes = [32, 4, 64, 32, 64, 32]
+    validate(call(BufferRef(4), BufferRef(5), **geo), sizes)          # copy form
+    validate(call(BufferRef(2), BufferRef(3), **geo), sizes)          # in-place form
+    with pytest.raises(SlotOutOfRange):                              # output aliases new rows
+        validate(call(BufferRef(0), BufferRef(5), **geo), [64, 4, 64, 32, 64, 32])
+    with pytest.raises(UnsupportedOp):
+        validate(call(BufferRef(4), BufferRef(5), **{**geo, "dtype": 2}), sizes)
+
+
+def test_attn_refusals():
+    def call(**k):
+        return KernelCall.DecodeAttentionI8(DecodeAttentionI8Call(
+            *[BufferRef(s) for s in range(7)], **k))
+    B, H, Hkv, bucket, D = 2, 8, 2, 16, 128
+    rows = B * Hkv * bucket
+    sizes = [B * H * D * 2, rows * D, rows * D, rows * 4, rows * 4, B * 4, B * H * D * 2]
+    validate(call(batch=B, heads=H, kv_heads=Hkv, bucket_rows=bucket, head_dim=D), sizes)
+    with pytest.raises(UnsupportedOp):
+        validate(call(batch=B, heads=H, kv_heads=3, bucket_rows=bucket, head_dim=D), sizes)
+    with pytest.raises(UnsupportedOp):
+        validate(call(batch=B, heads=H, kv_heads=Hkv, bucket_rows=bucket, head_dim=96), sizes)
+    with pytest.raises(SlotOutOfRange):
+        short = list(sizes)
+        short[5] = 4
+        validate(call(batch=B, heads=H, kv_heads=Hkv, bucket_rows=bucket, head_dim=D), short)
+
+
+def test_unknown_tag_is_unsupported():
+    kc = _ffi.KernelCallC()
+    kc.tag = 64   # Softmax: no device kernel here
+    with pytest.raises(UnsupportedOp):
+        from hologram_amd.backend import check
+        check(_ffi.lib().holo_hip_validate(ctypes.byref(kc), None, 0))
+
+
+# ---- wire codec ---------------------------------------------------------------
+
+def test_codec_layout_matches_kernel_codec():
+    c = KernelCall.MatMul(MatMulCall(BufferRef(1, 2, 3), BufferRef(4), BufferRef(5, 6), 7, 8, 9,
+                                     DTYPE_BF16))
+    wire = c.encode()
+    # u16 discriminant 46, three (u32, u64, u64) refs, three u32, two u8
+    assert len(wire) == 2 + 3 * 20 + 12 + 2
+    assert struct.unpack_from("<H", wire)[0] == 46
+    kc, used = decode_call(wire)
+    assert used == len(wire)
+    m = kc.u.matmul
+    assert (m.a.slot, m.a.offset, m.a.length) == (1, 2, 3)
+    assert (m.m, m.k, m.n, m.dtype, m.b_packed) == (7, 8, 9, DTYPE_BF16, 0)
+
+
+@pytest.mark.parametrize("call", [
+    KernelCall.Exp(UnaryCall(BufferRef(3), BufferRef(4, 16, 32), 99, 16, DTYPE_F16)),
+    KernelCall.KvCacheWrite(KvCacheWriteCall(BufferRef(0), BufferRef(1), BufferRef(2),
+                                             BufferRef(3), 5, 6, 1, 128)),
+    KernelCall.KvQuantAppend(KvQuantAppendCall(*[BufferRef(i) for i in range(6)], 128, 4096, 1,
+                                               128, DTYPE_BF16)),
+    KernelCall.DecodeAttentionI8(DecodeAttentionI8Call(*[BufferRef(i) for i in range(7)], 32, 32,
+                                                       8, 32768, 128, 0, DTYPE_BF16)),
+])
+def test_codec_round_trip(call):
+    wire = call.encode()
+    kc, used = decode_call(wire + b"\xff\xff")     # trailing bytes belong to the next call
+    assert used == len(wire)
+    assert bytes(kc) == bytes(call.to_c())
+
+
+def test_codec_truncated_payload():
+    from hologram_amd import DispatchError
+    wire = KernelCall.Gelu(UnaryCall(BufferRef(0), BufferRef(1), 5)).encode()
+    with pytest.raises(DispatchError):
+        decode_call(wire[:-1])

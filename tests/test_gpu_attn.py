@@ -1,0 +1,103 @@
+"""GPU parity: int8-KV GQA decode attention (new op 123) vs the oracle's
+per-sequence DecodeAttentionValid over dequantized rows
+(src/cpu/float_kernels.rs:3834-3957). Tolerance: normalized max error
+max|got - want| / max|want| <= 1e-2 (bf16 output is narrowed by truncation)."""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import from_dev, to_dev
+from hologram_amd import (DTYPE_BF16, DTYPE_F32, BufferRef, DecodeAttentionI8Call,
+                          DeviceWorkspace, KernelCall, UnsupportedOp)
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+
+
+def make_cache(rng, B, Hkv, bucket, D):
+    """Fill every row through the oracle quantizer (config 3's scheme)."""
+    planes = B * Hkv
+    x = rng.standard_normal((planes, bucket, D)).astype(np.float32)
+    ch = rng.choice(D, size=max(1, int(np.ceil(0.02 * D))), replace=False)
+    x[..., ch] *= 20.0
+    cq = np.zeros(planes * bucket * D, np.int8)
+    cs = np.zeros(planes * bucket, np.float32)
+    return oracle.kv_quant_append(x, DTYPE_F32, 0, cq, cs, planes, bucket, bucket, D)
+
+
+def run_case(torch, backend, B, H, Hkv, D, bucket, lens, dtype, seed, scale_bits=0):
+    rng = np.random.default_rng(seed)
+    kq, ks = make_cache(rng, B, Hkv, bucket, D)
+    vq, vs = make_cache(rng, B, Hkv, bucket, D)
+    q32 = rng.standard_normal(B * H * D).astype(np.float32)
+    if dtype == DTYPE_BF16:
+        qbits = (q32.view(np.uint32) >> 16).astype(np.uint16)
+        q32 = (qbits.astype(np.uint32) << 16).view(np.float32)
+        qdev = qbits
+    else:
+        qdev = q32
+    lens = np.asarray(lens, np.uint32)
+    es = 2 if dtype == DTYPE_BF16 else 4
+    out = torch.zeros(B * H * D * es, dtype=torch.uint8, device="cuda")
+    ws = DeviceWorkspace()
+    for s, arr in enumerate([qdev, kq, vq, ks, vs, lens]):
+        ws.bind(s, to_dev(torch, arr))
+    ws.bind(6, out)
+    call = KernelCall.DecodeAttentionI8(DecodeAttentionI8Call(
+        *[BufferRef(s) for s in range(7)], B, H, Hkv, bucket, D, scale_bits, dtype))
+    backend.dispatch(call, ws)
+    backend.synchronize()
+    if dtype == DTYPE_BF16:
+        got = (from_dev(out, np.uint16).astype(np.uint32) << 16).view(np.float32)
+    else:
+        got = from_dev(out, np.float32)
+    want = oracle.decode_attention_i8(q32, kq, ks, vq, vs, lens, B, H, Hkv, bucket, D,
+                                      oracle.attn_scale(D, scale_bits))
+    return got.reshape(B, H, D), want.reshape(B, H, D), lens
+
+
+def norm_err(got, want):
+    return float(np.max(np.abs(got - want)) / (np.max(np.abs(want)) + 1e-9))
+
+
+@pytest.mark.parametrize("dtype", [DTYPE_BF16, DTYPE_F32])
+@pytest.mark.parametrize("H,Hkv,D", [(32, 8, 128), (8, 8, 128), (16, 8, 64), (16, 2, 128),
+                                     (8, 1, 64)])
+def test_ragged_gqa(torch_cuda, backend, H, Hkv, D, dtype):
+    B, bucket = 5, 1300
+    lens = [1, 256, 257, 1299, 5000]          # last one clamps to the bucket
+    got, want, _ = run_case(torch_cuda, backend, B, H, Hkv, D, bucket, lens, dtype, seed=H * D)
+    assert np.all(np.isfinite(got))
+    for b in range(B):
+        assert norm_err(got[b], want[b]) <= TOL, f"sequence {b} (len {lens[b]})"
+
+
+def test_zero_length_is_exact_zero(torch_cuda, backend):
+    got, want, _ = run_case(torch_cuda, backend, 3, 8, 2, 128, 64, [0, 64, 0], DTYPE_F32, seed=1)
+    assert np.all(got[0] == 0) and np.all(got[2] == 0)
+    assert norm_err(got[1], want[1]) <= TOL
+
+
+def test_scale_bits(torch_cuda, backend):
+    sb = int(np.float32(0.05).view(np.uint32))
+    got, want, _ = run_case(torch_cuda, backend, 2, 8, 2, 128, 600, [600, 333], DTYPE_F32,
+                            seed=7, scale_bits=sb)
+    assert norm_err(got, want) <= TOL
+
+
+def test_config4_shape_subset(torch_cuda, backend):
+    """B=8 of config 4's 32, H=32/8, D=128, ragged L up to 8192."""
+    rng = np.random.default_rng(44)
+    lens = rng.integers(512, 8193, size=8)
+    got, want, _ = run_case(torch_cuda, backend, 8, 32, 8, 128, 8192, lens, DTYPE_BF16, seed=4)
+    for b in range(8):
+        assert norm_err(got[b], want[b]) <= TOL
+
+
+def test_refusals(torch_cuda, backend):
+    ws = DeviceWorkspace()
+    for s in range(7):
+        ws.bind(s, torch_cuda.zeros(1 << 16, dtype=torch_cuda.uint8, device="cuda"))
+    with pytest.raises(UnsupportedOp):   # heads not a multiple of kv_heads
+        backend.dispatch(KernelCall.DecodeAttentionI8(DecodeAttentionI8Call(
+            *[BufferRef(s) for s in range(7)], 1, 6, 4, 16, 128)), ws)

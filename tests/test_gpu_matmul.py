@@ -1,0 +1,77 @@
+"""GPU parity: MatMul (f32, bf16) vs the f64 reference of tests/conformance.rs:100-144
+on the same (bf16-quantized) inputs. Normalized error bound: 1e-5 (f32), 1e-2 (bf16)."""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import from_dev, to_dev
+from hologram_amd import (DTYPE_BF16, DTYPE_F32, BufferRef, DeviceWorkspace, KernelCall,
+                          MatMulCall, UnsupportedOp)
+
+pytestmark = pytest.mark.gpu
+
+
+def run_mm(torch, backend, m, k, n, dtype, seed):
+    rng = np.random.default_rng(seed)
+    a = (rng.standard_normal(m * k) / np.sqrt(k)).astype(np.float32)
+    b = (rng.standard_normal(k * n) / np.sqrt(k)).astype(np.float32)
+    if dtype == DTYPE_BF16:
+        ab = (a.view(np.uint32) >> 16).astype(np.uint16)
+        bb = (b.view(np.uint32) >> 16).astype(np.uint16)
+        a = (ab.astype(np.uint32) << 16).view(np.float32)
+        b = (bb.astype(np.uint32) << 16).view(np.float32)
+        da, db, es = ab, bb, 2
+    else:
+        da, db, es = a, b, 4
+    out = torch.zeros(m * n * es, dtype=torch.uint8, device="cuda")
+    ws = DeviceWorkspace()
+    ws.bind(0, to_dev(torch, da))
+    ws.bind(1, to_dev(torch, db))
+    ws.bind(2, out)
+    backend.dispatch(KernelCall.MatMul(MatMulCall(BufferRef(0), BufferRef(1), BufferRef(2), m, k,
+                                                  n, dtype)), ws)
+    backend.synchronize()
+    if dtype == DTYPE_BF16:
+        got = (from_dev(out, np.uint16).astype(np.uint32) << 16).view(np.float32)
+    else:
+        got = from_dev(out, np.float32)
+    return got, oracle.matmul_ref_f64(a, b, m, k, n)
+
+
+@pytest.mark.parametrize("dtype,tol", [(DTYPE_F32, 1e-5), (DTYPE_BF16, 1e-2)])
+@pytest.mark.parametrize("m,k,n", [(1024, 1024, 1024), (16, 4096, 4096), (128, 64, 128),
+                                   (1, 1, 1), (77, 131, 45), (300, 1000, 257), (16, 4096, 1000)])
+def test_matmul_parity(torch_cuda, backend, m, k, n, dtype, tol):
+    got, want = run_mm(torch_cuda, backend, m, k, n, dtype, seed=m * 7 + n)
+    err = oracle.max_rel_err(got, want)
+    assert err <= tol, f"normalized error {err:.3g}"
+
+
+def test_bf16_truncates(torch_cuda, backend):
+    """bf16 narrowing is truncation (write_bf16, src/cpu/dtype.rs:75-79): the exact
+    sum 1 + 2^-8 + 2^-9 = 0x3F818000 narrows to 0x3F81 (rounding would give 0x3F82)."""
+    k = 64
+    a = np.zeros(k, np.float32)
+    a[:3] = 1.0
+    b = np.zeros(k, np.float32)
+    b[:3] = [1.0, 2.0 ** -8, 2.0 ** -9]
+    ab = (a.view(np.uint32) >> 16).astype(np.uint16)
+    bb = (b.view(np.uint32) >> 16).astype(np.uint16)
+    out = torch_cuda.zeros(2, dtype=torch_cuda.uint8, device="cuda")
+    ws = DeviceWorkspace()
+    ws.bind(0, to_dev(torch_cuda, ab))
+    ws.bind(1, to_dev(torch_cuda, bb))
+    ws.bind(2, out)
+    backend.dispatch(KernelCall.MatMul(MatMulCall(BufferRef(0), BufferRef(1), BufferRef(2), 1, k,
+                                                  1, DTYPE_BF16)), ws)
+    backend.synchronize()
+    assert int(from_dev(out, np.uint16)[0]) == 0x3F81
+
+
+def test_packed_b_refused(torch_cuda, backend):
+    ws = DeviceWorkspace()
+    for s in range(3):
+        ws.bind(s, torch_cuda.zeros(4096, dtype=torch_cuda.uint8, device="cuda"))
+    with pytest.raises(UnsupportedOp):
+        backend.dispatch(KernelCall.MatMul(MatMulCall(BufferRef(0), BufferRef(1), BufferRef(2),
+                                                      4, 4, 4, DTYPE_F32, True)), ws)

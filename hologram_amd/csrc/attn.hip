@@ -6,266 +6,485 @@
 // which is the reference's DecodeAttentionValid row
 // (crates/hologram-compute/src/cpu/float_kernels.rs:3834-3883) over the
 // dequantized rows (kernels.rs:270). Softmax is fp32 (exp2 of log2e-scaled
-// scores, online across chunks); no key with j >= L_b is ever read.
+// scores, online); no key with j >= L_b contributes.
 //
-// Structure (split-K flash decoding):
-//   attn_chunk_kernel  grid (chunks, Hkv, B), 256 threads. One workgroup
-//                      owns one (b, kh, 256-key chunk) and all G query heads
-//                      of the group, so each K/V byte is read from HBM once
-//                      for the whole group. Pass 1 scores the chunk (int8 K
-//                      dequantized in registers), the chunk max and sum are
-//                      taken in LDS, pass 2 accumulates p * v. It writes the
-//                      partial (m, l, acc[D]) per head.
-//   attn_combine_kernel grid (H, B), D threads: merges the chunk partials of
-//                      one (b, h) and writes the output row (bf16 by
-//                      truncation, as the reference narrows, or f32).
-// Workgroups whose chunk starts at or beyond L_b exit at once, so the
-// ragged batch costs only the keys that exist.
+// Split-K flash decoding on MFMA:
+//   attn_mfma_kernel   grid (chunks, Hkv, B), 4 wavefronts. A workgroup owns a
+//                      (b, kh, kChunk-key) chunk and all G <= 16 query heads of
+//                      the group, so each K/V byte is read from HBM once. Each
+//                      wavefront takes every 4th 32-key block of the chunk:
+//     S^T[32 keys x 16 heads] = K . Q^T   v_mfma_i32_16x16x64_i8 on the raw K
+//                                         bytes; Q as exact int8 hi/lo halves
+//     online softmax over the block       fp32, per head = per lane column
+//     O^T[D x 16] += V^T . P^T            the same MFMA; P^T is exactly the
+//                                         lane's own 8 scores, V^T is gathered
+//                                         byte-transposed from 8 key rows
+//   The four wavefront states merge in LDS into one partial (m, l, O[D]) per
+//   head; a plane with a single chunk writes its output rows directly.
+//   Chunks starting at or beyond L_b exit at once.
+//   attn_combine_kernel grid (Hkv, B): merges the chunk partials of a plane and
+//   writes the G output rows: bf16 (truncated, as the reference narrows) or
+//   f32. (The kernel boundary makes every partial visible across the XCDs'
+//   separate L2s; a same-kernel merge would need agent-scope fences per
+//   workgroup, which write back and invalidate L2.)
+//
+// Exactness: Q is scaled by a power of two per head so its largest |q| sits in
+// [2^13, 2^14), rounded to an integer q_s (relative error <= 2^-14 of the
+// head's max) and split q_s = 256 qh + ql with int8 halves, so the int32 QK
+// dot products are exact. For PV, an int8 v is the f16 1152 + (v ^ 0x80) - 1152
+// built by byte placement under the f16 exponent of 1024 (every integer
+// -128..127 is an exact f16); P' = p * vscale / 2^ve with 2^ve
+// >= every vscale seen so far keeps P' in [0, 1] (ve is tracked online per
+// wavefront and the accumulator rescaled when it grows). MFMA products are
+// exact and accumulate in fp32.
 #include <hip/hip_runtime.h>
 
+#include <math.h>
+
+#include "holo_device.h"
 #include "holo_kernels.h"
 
 namespace holo {
 namespace {
 
-constexpr int kChunk = 256;   // keys per workgroup
-constexpr int kThreads = 256;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kChunk = 1024;   // keys per workgroup
+constexpr int kMaxChunks = 256; // bucket_rows <= kChunk * kMaxChunks
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kBlock = 32;     // keys per wavefront step
 constexpr float kLog2e = 1.4426950408889634f;
 
-__device__ __forceinline__ float load_q(const void *q, uint8_t dtype, uint64_t i) {
-    if (dtype == 8) return reinterpret_cast<const float *>(q)[i];
-    return __uint_as_float(uint32_t(reinterpret_cast<const uint16_t *>(q)[i]) << 16);
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// V^T operand of the PV MFMA: dim t of the lane's 4-byte segment, for the
+// lane's 8 keys (words w[0..7], bytes already xor 0x80), as 8 exact f16.
+// Two byte permutes interleave a key pair, two more place each byte under the
+// f16 exponent of 1024 (0x64xx = 1024 + byte), and one packed subtract of
+// 1152 leaves the signed int8 value.
+__device__ __forceinline__ void pair_dims(uint32_t a, uint32_t b, uint32_t *f4) {
+    const uint32_t kMagic = 0x64646464u;
+    const uint32_t x01 = __builtin_amdgcn_perm(b, a, 0x05010400u);   // a0 b0 a1 b1
+    const uint32_t x23 = __builtin_amdgcn_perm(b, a, 0x07030602u);   // a2 b2 a3 b3
+    f4[0] = __builtin_amdgcn_perm(kMagic, x01, 0x04010400u);         // a0 64 b0 64
+    f4[1] = __builtin_amdgcn_perm(kMagic, x01, 0x04030402u);         // a1 64 b1 64
+    f4[2] = __builtin_amdgcn_perm(kMagic, x23, 0x04010400u);
+    f4[3] = __builtin_amdgcn_perm(kMagic, x23, 0x04030402u);
 }
 
-// 4 int8 in a 32-bit word -> 4 floats (sign-extending byte extracts).
-__device__ __forceinline__ void i8x4_to_f32(uint32_t w, float *f) {
-    f[0] = static_cast<float>(static_cast<int32_t>(w << 24) >> 24);
-    f[1] = static_cast<float>(static_cast<int32_t>(w << 16) >> 24);
-    f[2] = static_cast<float>(static_cast<int32_t>(w << 8) >> 24);
-    f[3] = static_cast<float>(static_cast<int32_t>(w) >> 24);
+__device__ __forceinline__ f16x8 words_to_f16(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
+    u32x4 m;
+    m.x = w0;
+    m.y = w1;
+    m.z = w2;
+    m.w = w3;
+    return __builtin_bit_cast(f16x8, m) - (f16x8)(_Float16)1152.0f;
 }
 
-template <int DPT>
-__device__ __forceinline__ void load_row(const int8_t *p, float *f) {
-    if constexpr (DPT == 16) {
-        const uint4 v = *reinterpret_cast<const uint4 *>(p);
-        i8x4_to_f32(v.x, f);
-        i8x4_to_f32(v.y, f + 4);
-        i8x4_to_f32(v.z, f + 8);
-        i8x4_to_f32(v.w, f + 12);
-    } else {
-        const uint2 v = *reinterpret_cast<const uint2 *>(p);
-        i8x4_to_f32(v.x, f);
-        i8x4_to_f32(v.y, f + 4);
-    }
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, int(bytes), 0x00020000);
 }
 
-// D: head_dim; G: query heads per kv head; DPT: dims per thread.
-template <int D, int G, int DPT>
-__global__ __launch_bounds__(kThreads) void attn_chunk_kernel(
-    const void *__restrict__ q, uint8_t dtype, const int8_t *__restrict__ kq,
-    const int8_t *__restrict__ vq, const float *__restrict__ ks, const float *__restrict__ vs,
-    const uint32_t *__restrict__ lens, float *__restrict__ part, uint32_t H, uint32_t Hkv,
-    uint32_t bucket, uint32_t nchunks, float inv_scale_log2e) {
-    constexpr int TPK = D / DPT;          // threads cooperating on one key row
-    constexpr int KPP = kThreads / TPK;   // keys per pass of the workgroup
-    static_assert(64 % TPK == 0, "a key's threads must share a wavefront");
+// D: head_dim (64 or 128); kF32Q: q/out are f32 (else bf16). G (query heads per
+// kv head) is <= 16 at run time.
+template <int D, bool kF32Q>
+__global__ __launch_bounds__(kThreads) void attn_mfma_kernel(
+    const void *__restrict__ q, const int8_t *__restrict__ kq, const int8_t *__restrict__ vq,
+    const float *__restrict__ ks, const float *__restrict__ vs, const uint32_t *__restrict__ lens,
+    float *__restrict__ part, void *__restrict__ out, uint32_t H, uint32_t Hkv, uint32_t G,
+    uint32_t bucket, uint32_t nchunks, float log2e_over_scale) {
+    constexpr int KB = D / 4;          // K bytes per lane per key row (QK k-slots)
+    constexpr int NKS = D / 64;        // i8 MFMA k-steps (64 dims each)
+    constexpr int NDB = D / 16;        // 16-row dim blocks of O^T
+    constexpr int VW = NDB / 4;        // V u32 words per lane per key row
 
-    __shared__ float sc[G][kChunk];       // scores, then probabilities
-    __shared__ float red[G][D];           // p.v accumulation across key slots
-    __shared__ float stat[G][2];          // chunk max, chunk sum
+    __shared__ float red_m[kWaves][16], red_l[kWaves][16];
+    __shared__ float red_o[kWaves][16][D];
 
     const uint32_t b = blockIdx.z, kh = blockIdx.y, chunk = blockIdx.x;
     uint32_t L = lens[b];
     if (L > bucket) L = bucket;
     const uint32_t c0 = chunk * kChunk;
-    if (c0 >= L) return;
-    const uint32_t nk = L - c0 < uint32_t(kChunk) ? L - c0 : uint32_t(kChunk);
-
-    const int tid = threadIdx.x;
-    const int dg = tid % TPK;             // dim group
-    const int slot = tid / TPK;           // key slot
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    if (c0 >= L) {
+        if (L == 0 && chunk == 0) {       // no visible key: the exact zero rows
+            for (uint32_t idx = tid; idx < G * D; idx += kThreads) {
+                const uint64_t oi = (uint64_t(b) * H + kh * G) * D + idx;
+                if constexpr (kF32Q)
+                    static_cast<float *>(out)[oi] = 0.0f;
+                else
+                    static_cast<uint16_t *>(out)[oi] = 0;
+            }
+        }
+        return;
+    }
+    const uint32_t c1 = L - c0 < uint32_t(kChunk) ? L : c0 + kChunk;
+    const int r = lane & 15, g = lane >> 4;
+    // the wavefront index is uniform: keep block offsets in scalar registers
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
     const uint64_t plane = uint64_t(b) * Hkv + kh;
-    const int8_t *kbase = kq + (plane * bucket + c0) * D + dg * DPT;
-    const int8_t *vbase = vq + (plane * bucket + c0) * D + dg * DPT;
-    const float *ksb = ks + plane * bucket + c0;
-    const float *vsb = vs + plane * bucket + c0;
+    // One buffer resource per plane: uniform base, 32-bit lane offsets, and
+    // hardware range checking (reads past the plane return 0).
+    const auto rk = rsrc(kq + plane * bucket * D, bucket * D);
+    const auto rv = rsrc(vq + plane * bucket * D, bucket * D);
+    const auto rks = rsrc(ks + plane * bucket, bucket * 4);
+    const auto rvs = rsrc(vs + plane * bucket, bucket * 4);
 
-    for (int i = tid; i < G * D; i += kThreads) (&red[0][0])[i] = 0.0f;
+    // Per-lane byte offsets inside a 32-key block; the block base is a uniform
+    // soffset. K rows 16mb + r (KB bytes at KB*g); V rows
+    // kappa(g, j) = 16(j/4) + 4g + j%4 (NDB bytes at NDB*r).
+    uint32_t koff[2], voff[8];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) koff[mb] = (16 * mb + r) * D + KB * g;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) voff[j] = (16 * (j >> 2) + 4 * g + (j & 3)) * D + NDB * r;
 
-    float qr[G][DPT];
+    struct Blk {
+        u32x4 k[2][NKS];
+        uint32_t v[8][VW];
+        float ksc[8], vsc[8];
+    };
+    auto load = [&](uint32_t blk, Blk &o) {
+        const int kvs = int(blk * D), ss = int(blk * 4);
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+        for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int e = 0; e < DPT; ++e)
-            qr[g][e] = load_q(q, dtype, (uint64_t(b) * H + kh * G + g) * D + dg * DPT + e);
-
-    // pass 1: s2 = (q . k_int) * kscale * log2e / scale
-    for (uint32_t kk = slot; kk < nk; kk += KPP) {
-        float kf[DPT];
-        load_row<DPT>(kbase + uint64_t(kk) * D, kf);
-        float dot[G];
+            for (int s = 0; s < NKS; ++s)
+                o.k[mb][s] = __builtin_amdgcn_raw_buffer_load_b128(rk, int(koff[mb]) + 16 * s, kvs, 0);
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float a = 0.0f;
-#pragma unroll
-            for (int e = 0; e < DPT; ++e) a = fmaf(qr[g][e], kf[e], a);
-            dot[g] = a;
+        for (int j = 0; j < 8; ++j) {
+            if constexpr (VW == 2) {
+                const auto w = __builtin_amdgcn_raw_buffer_load_b64(rv, int(voff[j]), kvs, 0);
+                o.v[j][0] = w[0];
+                o.v[j][1] = w[1];
+            } else {
+                o.v[j][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, int(voff[j]), kvs, 0);
+            }
         }
 #pragma unroll
-        for (int off = TPK / 2; off >= 1; off >>= 1)
-#pragma unroll
-            for (int g = 0; g < G; ++g) dot[g] += __shfl_xor(dot[g], off, 64);
-        if (dg == 0) {
-            const float kscale = ksb[kk];
-#pragma unroll
-            for (int g = 0; g < G; ++g) sc[g][kk] = (dot[g] * kscale) * inv_scale_log2e;
+        for (int h = 0; h < 2; ++h) {
+            const u32x4 k4 = __builtin_amdgcn_raw_buffer_load_b128(rks, (16 * h + 4 * g) * 4, ss, 0);
+            const u32x4 v4 = __builtin_amdgcn_raw_buffer_load_b128(rvs, (16 * h + 4 * g) * 4, ss, 0);
+            o.ksc[4 * h] = __uint_as_float(k4.x);
+            o.ksc[4 * h + 1] = __uint_as_float(k4.y);
+            o.ksc[4 * h + 2] = __uint_as_float(k4.z);
+            o.ksc[4 * h + 3] = __uint_as_float(k4.w);
+            o.vsc[4 * h] = __uint_as_float(v4.x);
+            o.vsc[4 * h + 1] = __uint_as_float(v4.y);
+            o.vsc[4 * h + 2] = __uint_as_float(v4.z);
+            o.vsc[4 * h + 3] = __uint_as_float(v4.w);
         }
-    }
-    __syncthreads();
+    };
 
-    // chunk max and sum per head: wavefront w takes heads w, w + 4, ...
+    // Q loads first, then the first block's: the Q set-up below waits only for Q.
+    // Lanes of padding heads (r >= G) read head 0 and zero it.
+    float qv[KB];
+    const bool live = uint32_t(r) < G;
     {
-        const int w = tid >> 6, lane = tid & 63;
-        for (int g = w; g < G; g += kThreads / 64) {
-            float m = -INFINITY;
-            for (uint32_t j = lane; j < nk; j += 64) m = fmaxf(m, sc[g][j]);
+        const uint64_t qi = (uint64_t(b) * H + kh * G + (live ? r : 0)) * D + KB * g;
+        if constexpr (kF32Q) {
+            const u32x4 *src = reinterpret_cast<const u32x4 *>(static_cast<const float *>(q) + qi);
 #pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-            float l = 0.0f;
-            for (uint32_t j = lane; j < nk; j += 64) {
-                const float p = exp2f(sc[g][j] - m);
-                sc[g][j] = p;
-                l += p;
+            for (int w = 0; w < KB / 4; ++w) {
+                const u32x4 v = src[w];
+                qv[4 * w] = __uint_as_float(v.x);
+                qv[4 * w + 1] = __uint_as_float(v.y);
+                qv[4 * w + 2] = __uint_as_float(v.z);
+                qv[4 * w + 3] = __uint_as_float(v.w);
             }
+        } else {
+            const u32x4 *src = reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(q) + qi);
 #pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off, 64);
-            if (lane == 0) {
-                stat[g][0] = m;
-                stat[g][1] = l;
+            for (int w = 0; w < KB / 8; ++w) {
+                const u32x4 v = src[w];
+                const uint32_t e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    qv[8 * w + 2 * t] = __uint_as_float(e[t] << 16);
+                    qv[8 * w + 2 * t + 1] = __uint_as_float(e[t] & 0xFFFF0000u);
+                }
             }
         }
+#pragma unroll
+        for (int e = 0; e < KB; ++e) qv[e] = live ? qv[e] : 0.0f;
     }
-    __syncthreads();
+    const uint32_t first = c0 + wv * kBlock;
+    Blk cur;
+    if (first < c1) load(first, cur);
 
-    // pass 2: acc[g][dims] += p_g * vscale * v_int
-    float acc[G][DPT];
+    // Q as a 15-bit integer per head, q * 2^qe with max |.| in [2^13, 2^14),
+    // split exactly into int8 halves: q_s = 256 qh + ql, ql in [-128, 127].
+    float qmax = 0.0f;
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int e = 0; e < KB; ++e) qmax = fmaxf(qmax, fabsf(qv[e]));
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 16, 64));
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
+    int qe = 0;
+    if (qmax > 0.0f && qmax <= 3.0e38f) {
+        (void)frexpf(qmax, &qe);          // qmax < 2^qe
+        qe = 14 - qe;
+    }
+    i32x4 qh[NKS], ql[NKS];
 #pragma unroll
-        for (int e = 0; e < DPT; ++e) acc[g][e] = 0.0f;
-    for (uint32_t kk = slot; kk < nk; kk += KPP) {
-        float vf[DPT];
-        load_row<DPT>(vbase + uint64_t(kk) * D, vf);
-        const float vscale = vsb[kk];
+    for (int s = 0; s < NKS; ++s)
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float pw = sc[g][kk] * vscale;
+        for (int w = 0; w < 4; ++w) {
+            uint32_t hw = 0, lw = 0;
 #pragma unroll
-            for (int e = 0; e < DPT; ++e) acc[g][e] = fmaf(pw, vf[e], acc[g][e]);
+            for (int t = 0; t < 4; ++t) {
+                const int qs = int(rintf(ldexpf(qv[16 * s + 4 * w + t], qe)));
+                const int hi = (qs + 128) >> 8;
+                const int lo = qs - hi * 256;
+                hw |= uint32_t(hi & 0xFF) << (8 * t);
+                lw |= uint32_t(lo & 0xFF) << (8 * t);
+            }
+            qh[s][w] = int(hw);
+            ql[s][w] = int(lw);
         }
+    const float score_mul = log2e_over_scale * ldexpf(1.0f, -qe);
+
+    f32x4 acc_o[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) acc_o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.0f;
+    int ve = -200;                         // 2^ve bounds every vscale seen (unset)
+    float v_unscale = 0.0f;
+
+    for (uint32_t blk = first; blk < c1; blk += kWaves * kBlock) {
+        // prefetch the next block of this wavefront before computing this one
+        const uint32_t nb = blk + kWaves * kBlock;
+        Blk nxt;
+        if (nb < c1) load(nb, nxt);
+        const bool full = blk + kBlock <= c1;
+
+        // -- S^T = K . Q^T on the int8 MFMA, exact in int32: lane holds keys
+        //    16mb + 4g + i for head r
+        float sc[8];
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+            i32x4 ah = {0, 0, 0, 0}, al = {0, 0, 0, 0};
+#pragma unroll
+            for (int s = 0; s < NKS; ++s) {
+                const i32x4 kf = __builtin_bit_cast(i32x4, cur.k[mb][s]);
+                ah = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, qh[s], ah, 0, 0, 0);
+                al = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, ql[s], al, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[4 * mb + i] = float(ah[i] * 256 + al[i]);
+        }
+        float m_blk = -INFINITY, vb = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t key = blk + 16 * (j >> 2) + 4 * g + (j & 3);
+            const bool vis = full || key < c1;
+            sc[j] = vis ? (sc[j] * cur.ksc[j]) * score_mul : -INFINITY;
+            m_blk = fmaxf(m_blk, sc[j]);
+            vb = vis ? fmaxf(vb, cur.vsc[j]) : vb;
+        }
+        m_blk = fmaxf(m_blk, __shfl_xor(m_blk, 16, 64));
+        m_blk = fmaxf(m_blk, __shfl_xor(m_blk, 32, 64));
+        vb = fmaxf(vb, __shfl_xor(vb, 16, 64));
+        vb = fmaxf(vb, __shfl_xor(vb, 32, 64));
+        if (__any(m_blk > m_run)) {        // rescale only when some head's max grew
+            const float m_new = fmaxf(m_run, m_blk);
+            const float alpha = exp2f(m_run - m_new);
+            m_run = m_new;
+            l_run *= alpha;
+#pragma unroll
+            for (int i = 0; i < NDB; ++i) acc_o[i] *= alpha;
+        }
+        // keep every P' = p * vscale / 2^ve in [0, 1]  (vb is wave-uniform)
+        if (vb > ldexpf(1.0f, ve) && vb <= 3.0e38f) {
+            int ve_new;
+            (void)frexpf(vb, &ve_new);                     // vb < 2^ve_new
+            const float shrink = ldexpf(1.0f, ve - ve_new);
+#pragma unroll
+            for (int i = 0; i < NDB; ++i) acc_o[i] *= shrink;
+            ve = ve_new;
+            v_unscale = ldexpf(1.0f, -ve);
+        }
+        f16x8 pf;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float p = exp2f(sc[j] - m_run);           // masked keys: exp2(-inf) = 0
+            l_run += p;
+            const float pw = p * (cur.vsc[j] * v_unscale);
+            pf[j] = (_Float16)(p > 0.0f ? pw : 0.0f);       // never 0 * garbage scale
+        }
+
+        // -- O^T += V^T . P^T : dim block mb = 4w + t, row m holds dim NDB*m + mb
+#pragma unroll
+        for (int w = 0; w < VW; ++w) {
+            uint32_t f[4][4];   // [dim t][key pair]
+#pragma unroll
+            for (int pr = 0; pr < 4; ++pr) {
+                uint32_t f4[4];
+                pair_dims(cur.v[2 * pr][w] ^ 0x80808080u, cur.v[2 * pr + 1][w] ^ 0x80808080u, f4);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) f[t][pr] = f4[t];
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                acc_o[4 * w + t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    words_to_f16(f[t][0], f[t][1], f[t][2], f[t][3]), pf, acc_o[4 * w + t], 0, 0, 0);
+        }
+        cur = nxt;
     }
-    // fold the key slots of one wavefront (lanes dg, dg+TPK, ...), then LDS
-#pragma unroll
-    for (int off = TPK; off < 64; off <<= 1)
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int e = 0; e < DPT; ++e) acc[g][e] += __shfl_xor(acc[g][e], off, 64);
-    if ((tid & 63) < TPK) {
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int e = 0; e < DPT; ++e) atomicAdd(&red[g][dg * DPT + e], acc[g][e]);
+
+    // ---- wavefront state -> LDS, merge the four wavefronts per head
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+    if (g == 0) {
+        red_m[wave][r] = m_run;
+        red_l[wave][r] = l_run;
     }
+    const float v_rescale = ldexpf(1.0f, ve);   // 2^-200 is 0: an idle wave adds nothing
+#pragma unroll
+    for (int mb = 0; mb < NDB; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            red_o[wave][r][NDB * (4 * g + i) + mb] = acc_o[mb][i] * v_rescale;
     __syncthreads();
 
-    float *dst = part + ((plane * nchunks + chunk) * G) * (D + 2);
-    for (int i = tid; i < G * D; i += kThreads) {
-        const int g = i / D, d = i % D;
-        dst[g * (D + 2) + 2 + d] = red[g][d];
-    }
-    if (tid < G) {
-        dst[tid * (D + 2)] = stat[tid][0];
-        dst[tid * (D + 2) + 1] = stat[tid][1];
+    // One chunk: the merged state is the answer. Several: write this chunk's partial.
+    const uint32_t nch = (L + kChunk - 1) / kChunk;
+    float *dst = part + (plane * nchunks + chunk) * G * (D + 2);
+    for (uint32_t idx = tid; idx < G * D; idx += kThreads) {
+        const uint32_t h = idx / D, d = idx % D;
+        float m = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) m = fmaxf(m, red_m[w][h]);
+        float o = 0.0f, l = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float sc = red_m[w][h] == -INFINITY ? 0.0f : exp2f(red_m[w][h] - m);
+            o = fmaf(red_o[w][h][d], sc, o);
+            l = fmaf(red_l[w][h], sc, l);
+        }
+        if (nch == 1) {
+            const uint64_t oi = (uint64_t(b) * H + kh * G + h) * D + d;
+            if constexpr (kF32Q)
+                static_cast<float *>(out)[oi] = o / l;
+            else
+                static_cast<uint16_t *>(out)[oi] = uint16_t(__float_as_uint(o / l) >> 16);
+            continue;
+        }
+        dst[h * (D + 2) + 2 + d] = o;
+        if (d == 0) {
+            dst[h * (D + 2)] = m;
+            dst[h * (D + 2) + 1] = l;
+        }
     }
 }
 
-template <int D, int G>
-__global__ __launch_bounds__(D) void attn_combine_kernel(const float *__restrict__ part,
-                                                        const uint32_t *__restrict__ lens,
-                                                        void *__restrict__ out, uint8_t dtype,
-                                                        uint32_t H, uint32_t Hkv, uint32_t bucket,
-                                                        uint32_t nchunks) {
-    const uint32_t h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-    const uint32_t kh = h / G, g = h % G;
+// Merge the chunk partials of one (b, kh) plane (only planes with more than one
+// chunk; single-chunk planes were written directly): 256 threads, the
+// per-(chunk, head) weights first, then each (head, dim) output as one
+// weighted sum whose loads are issued eight at a time.
+template <int D, bool kF32Q>
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restrict__ part,
+                                                          const uint32_t *__restrict__ lens,
+                                                          void *__restrict__ out, uint32_t H,
+                                                          uint32_t Hkv, uint32_t G,
+                                                          uint32_t bucket, uint32_t nchunks) {
+    __shared__ float wgt[kMaxChunks][16];
+    __shared__ float inv_l[16];
+    const uint32_t kh = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
     uint32_t L = lens[b];
     if (L > bucket) L = bucket;
     const uint32_t nch = (L + kChunk - 1) / kChunk;
-    const float *src = part + ((uint64_t(b) * Hkv + kh) * nchunks * G + g) * (D + 2);
-    const uint64_t stride = uint64_t(G) * (D + 2);
-    float m = -INFINITY;
-    for (uint32_t c = 0; c < nch; ++c) m = fmaxf(m, src[c * stride]);
-    float l = 0.0f, o = 0.0f;
-    for (uint32_t c = 0; c < nch; ++c) {
-        const float w = exp2f(src[c * stride] - m);
-        l = fmaf(src[c * stride + 1], w, l);
-        o = fmaf(src[c * stride + 2 + d], w, o);
+    if (nch <= 1) return;
+    const uint64_t plane = uint64_t(b) * Hkv + kh;
+    const float *src = part + plane * nchunks * G * (D + 2);
+    const uint64_t cstride = uint64_t(G) * (D + 2);
+    // per head: M = max_c m_c; wgt[c] = 2^(m_c - M); 1 / sum_c wgt[c] l_c
+    if (tid < 64) {
+        const uint32_t h = tid & 15, c4 = tid >> 4;    // 4 chunk lanes per head
+        float m = -INFINITY;
+        if (h < G)
+            for (uint32_t c = c4; c < nch; c += 4) m = fmaxf(m, src[c * cstride + h * (D + 2)]);
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        float l = 0.0f;
+        if (h < G)
+            for (uint32_t c = c4; c < nch; c += 4) {
+                const float w = exp2f(src[c * cstride + h * (D + 2)] - m);
+                wgt[c][h] = w;
+                l = fmaf(src[c * cstride + h * (D + 2) + 1], w, l);
+            }
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        if (c4 == 0 && h < G) inv_l[h] = 1.0f / l;
     }
-    const float r = nch ? o / l : 0.0f;   // no visible key: the exact zero row
-    const uint64_t oi = (uint64_t(b) * H + h) * D + d;
-    if (dtype == 8)
-        reinterpret_cast<float *>(out)[oi] = r;
-    else
-        reinterpret_cast<uint16_t *>(out)[oi] = uint16_t(__float_as_uint(r) >> 16);
+    __syncthreads();
+    for (uint32_t idx = tid; idx < G * D; idx += 256) {
+        const uint32_t h = idx / D, d = idx % D;
+        const float *ph = src + h * (D + 2) + 2 + d;
+        float o = 0.0f;
+        for (uint32_t c0 = 0; c0 < nch; c0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t c = c0 + u < nch ? c0 + u : nch - 1;
+                v[u] = ph[c * cstride];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (c0 + u < nch) o = fmaf(v[u], wgt[c0 + u][h], o);
+        }
+        const float res = o * inv_l[h];
+        const uint64_t oi = (uint64_t(b) * H + kh * G + h) * D + d;
+        if constexpr (kF32Q)
+            static_cast<float *>(out)[oi] = res;
+        else
+            static_cast<uint16_t *>(out)[oi] = uint16_t(__float_as_uint(res) >> 16);
+    }
 }
 
 uint32_t chunks_of(uint32_t bucket) { return (bucket + kChunk - 1) / kChunk; }
 
-}  // namespace
-
-size_t attn_i8_scratch_bytes(uint32_t B, uint32_t H, uint32_t bucket, uint32_t D) {
-    return size_t(B) * H * chunks_of(bucket) * (D + 2) * sizeof(float);
-}
-
-bool attn_i8_supported(uint32_t H, uint32_t Hkv, uint32_t D) {
-    if (Hkv == 0 || H % Hkv) return false;
-    const uint32_t G = H / Hkv;
-    return (D == 64 || D == 128) && (G == 1 || G == 2 || G == 4 || G == 8);
-}
-
-template <int D, int G, int DPT>
-static hipError_t run(const AttnI8Args &a, float *part, hipStream_t stream) {
+template <int D>
+hipError_t run(const AttnI8Args &a, void *scratch, hipStream_t stream) {
     const uint32_t nch = chunks_of(a.bucket);
-    const float inv_scale_log2e = kLog2e / a.score_scale;
-    hipLaunchKernelGGL((attn_chunk_kernel<D, G, DPT>), dim3(nch, a.Hkv, a.B), dim3(kThreads), 0,
-                       stream, a.q, a.dtype, a.kq, a.vq, a.ks, a.vs, a.lens, part, a.H, a.Hkv,
-                       a.bucket, nch, inv_scale_log2e);
+    const uint32_t G = a.H / a.Hkv;
+    float *part = static_cast<float *>(scratch);
+    const dim3 grid(nch, a.Hkv, a.B);
+    const float mul = kLog2e / a.score_scale;
+    if (a.dtype == 8)
+        hipLaunchKernelGGL((attn_mfma_kernel<D, true>), grid, dim3(kThreads), 0, stream, a.q, a.kq,
+                           a.vq, a.ks, a.vs, a.lens, part, a.out, a.H, a.Hkv, G, a.bucket, nch, mul);
+    else
+        hipLaunchKernelGGL((attn_mfma_kernel<D, false>), grid, dim3(kThreads), 0, stream, a.q,
+                           a.kq, a.vq, a.ks, a.vs, a.lens, part, a.out, a.H, a.Hkv, G, a.bucket,
+                           nch, mul);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((attn_combine_kernel<D, G>), dim3(a.H, a.B), dim3(D), 0, stream, part,
-                       a.lens, a.out, a.dtype, a.H, a.Hkv, a.bucket, nch);
+    if (e != hipSuccess || nch == 1) return e;
+    if (a.dtype == 8)
+        hipLaunchKernelGGL((attn_combine_kernel<D, true>), dim3(a.Hkv, a.B), dim3(256), 0, stream,
+                           part, a.lens, a.out, a.H, a.Hkv, G, a.bucket, nch);
+    else
+        hipLaunchKernelGGL((attn_combine_kernel<D, false>), dim3(a.Hkv, a.B), dim3(256), 0, stream,
+                           part, a.lens, a.out, a.H, a.Hkv, G, a.bucket, nch);
     return hipGetLastError();
 }
 
+}  // namespace
+
+size_t attn_i8_scratch_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t bucket, uint32_t D) {
+    (void)Hkv;
+    return size_t(B) * H * chunks_of(bucket) * (D + 2) * sizeof(float);
+}
+
+bool attn_i8_supported(uint32_t H, uint32_t Hkv, uint32_t D, uint32_t bucket) {
+    if (Hkv == 0 || H % Hkv) return false;
+    return (D == 64 || D == 128) && H / Hkv <= 16 && chunks_of(bucket) <= uint32_t(kMaxChunks);
+}
+
 hipError_t launch_attn_i8(const AttnI8Args &a, void *scratch, hipStream_t stream) {
-    float *part = static_cast<float *>(scratch);
-    const uint32_t G = a.H / a.Hkv;
-    if (a.D == 128) {
-        switch (G) {
-            case 1: return run<128, 1, 16>(a, part, stream);
-            case 2: return run<128, 2, 16>(a, part, stream);
-            case 4: return run<128, 4, 16>(a, part, stream);
-            case 8: return run<128, 8, 8>(a, part, stream);
-        }
-    } else if (a.D == 64) {
-        switch (G) {
-            case 1: return run<64, 1, 16>(a, part, stream);
-            case 2: return run<64, 2, 16>(a, part, stream);
-            case 4: return run<64, 4, 16>(a, part, stream);
-            case 8: return run<64, 8, 8>(a, part, stream);
-        }
-    }
+    if (a.D == 128) return run<128>(a, scratch, stream);
+    if (a.D == 64) return run<64>(a, scratch, stream);
     return hipErrorInvalidValue;
 }
 

@@ -117,6 +117,12 @@ int split_borrow(const SlotTable &st, const holo_buffer_ref *reads, View *rv, in
     return HOLO_OK;
 }
 
+// Device address alignment of a resolved view (offsets included). A size-only
+// validation has no addresses; its views are checked by offset alone.
+bool aligned(const View &v, uint64_t a) {
+    return (reinterpret_cast<uintptr_t>(v.base) % a) == 0;
+}
+
 int need(const View &v, uint64_t bytes, uint32_t slot, const char *op, const char *what) {
     if (v.bytes < bytes)
         return fail(HOLO_ERR_SLOT_OUT_OF_RANGE,
@@ -173,6 +179,8 @@ int do_unary(holo_backend *be, const SlotTable &st, uint32_t tag, const holo_una
     const uint64_t bytes = c.element_count * 2;
     HOLO_TRY(need(in, bytes, c.input.slot, op, "input"));
     HOLO_TRY(need(out, bytes, c.output.slot, op, "output"));
+    if (!aligned(in, 2) || !aligned(out, 2))
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "unary_lut: operands must be 2-byte aligned");
     if (!be) return HOLO_OK;
     const int di = c.dtype == HOLO_DTYPE_BF16 ? 1 : 0;
     uint16_t *&tab = be->lut_dev[act][di];
@@ -212,6 +220,10 @@ int do_matmul(holo_backend *be, const SlotTable &st, const holo_matmul_call &c) 
     HOLO_TRY(need(rv[0], uint64_t(c.m) * c.k * es, c.a.slot, op, "a"));
     HOLO_TRY(need(rv[1], uint64_t(c.k) * c.n * es, c.b.slot, op, "b"));
     HOLO_TRY(need(out, uint64_t(c.m) * c.n * es, c.output.slot, op, "output"));
+    if (!aligned(rv[0], es) || !aligned(rv[1], es) || !aligned(out, es))
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "matmul: operands must be element-aligned");
+    if ((uint64_t(c.m) + 127) / 128 > 65535)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "matmul: m above 8388480");
     if (!be) return HOLO_OK;
     return launched(holo::launch_matmul(rv[0].base, rv[1].base, out.base, c.m, c.k, c.n, c.dtype,
                                         be->stream),
@@ -292,6 +304,13 @@ int do_kv_quant(holo_backend *be, const SlotTable &st, const holo_kv_quant_appen
     HOLO_TRY(need(pos, 4, c.pos.slot, op, "pos"));
     HOLO_TRY(need(oq, qbytes, c.output.slot, op, "output"));
     HOLO_TRY(need(os, sbytes, c.output_scales.slot, op, "output_scales"));
+    if (!aligned(os, 4) || !aligned(nw, dtype_size(c.dtype)) || !aligned(pos, 4) ||
+        (!in_place && !aligned(cs, 4)))
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    "kv_quant_append: scales and pos must be 4-byte aligned, new rows "
+                    "element-aligned");
+    if (uint64_t(c.planes) * c.new_rows > 0xffffffffull / 64)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "kv_quant_append: planes * new_rows too large");
     if (!be) return HOLO_OK;
     if (!in_place) {
         HOLO_TRY(launched(holo::launch_copy_bytes(cq.base, oq.base, qbytes, be->stream), op));
@@ -317,10 +336,10 @@ int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attentio
                     "decode_attention_i8: heads must be a multiple of kv_heads (grouped-query)");
     if (c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F32)
         return fail(HOLO_ERR_UNSUPPORTED_OP, "decode_attention_i8: q/output must be bf16 or f32");
-    if (!holo::attn_i8_supported(c.heads, hkv, c.head_dim))
+    if (!holo::attn_i8_supported(c.heads, hkv, c.head_dim, c.bucket_rows))
         return fail(HOLO_ERR_UNSUPPORTED_OP,
-                    "decode_attention_i8: head_dim must be 64 or 128 and heads/kv_heads one of "
-                    "1, 2, 4, 8");
+                    "decode_attention_i8: head_dim must be 64 or 128, heads/kv_heads at most 16 "
+                    "and bucket_rows at most 262144");
     const uint64_t es = dtype_size(c.dtype);
     const uint64_t qn = uint64_t(c.batch) * c.heads * c.head_dim;
     const uint64_t rows = uint64_t(c.batch) * hkv * c.bucket_rows;
@@ -334,6 +353,15 @@ int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attentio
     HOLO_TRY(need(rv[4], rows * 4, c.v_scales.slot, op, "v_scales"));
     HOLO_TRY(need(rv[5], uint64_t(c.batch) * 4, c.lens.slot, op, "lens"));
     HOLO_TRY(need(out, qn * es, c.output.slot, op, "output"));
+    // launch-shape limits of the kernels: grid (chunks, kv_heads, batch)
+    if (c.batch > 65535 || hkv > 65535)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "decode_attention_i8: batch and kv_heads must be <= 65535");
+    // vector loads: 16-byte K/V rows, 4-byte scales/lens, element-aligned q/out
+    if (!aligned(rv[1], 16) || !aligned(rv[2], 16) || !aligned(rv[3], 4) || !aligned(rv[4], 4) ||
+        !aligned(rv[5], 4) || !aligned(rv[0], es) || !aligned(out, es))
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    "decode_attention_i8: caches must be 16-byte aligned, scales/lens 4-byte, "
+                    "q/output element-aligned");
     if (!be) return HOLO_OK;
     // score divisor (float_kernels.rs:4256-4266)
     float dflt = std::sqrt(static_cast<float>(c.head_dim));
@@ -344,7 +372,8 @@ int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attentio
         memcpy(&sm, &c.scale_bits, 4);
         scale = sm > 0.0f ? 1.0f / sm : dflt;
     }
-    const size_t need_scratch = holo::attn_i8_scratch_bytes(c.batch, c.heads, c.bucket_rows, c.head_dim);
+    const size_t need_scratch =
+        holo::attn_i8_scratch_bytes(c.batch, c.heads, hkv, c.bucket_rows, c.head_dim);
     if (need_scratch > be->scratch_bytes) {
         if (be->scratch) {
             (void)hipStreamSynchronize(be->stream);

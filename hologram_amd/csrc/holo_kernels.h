@@ -30,7 +30,8 @@ hipError_t launch_kv_quant_append(const void *nw, uint8_t dtype, const uint32_t 
                                   hipStream_t stream);
 
 // attn.hip — int8-KV GQA decode attention. `scratch` holds the split-K
-// partials; attn_i8_scratch_bytes() gives the size it needs.
+// partials; attn_i8_scratch_bytes() gives its size. Calls sharing one scratch
+// must not overlap.
 struct AttnI8Args {
     const void *q;          // [B, H, D] bf16 or f32
     const int8_t *kq, *vq;  // [B, Hkv, bucket, D]
@@ -41,8 +42,8 @@ struct AttnI8Args {
     float score_scale;      // the divisor: sqrtf(D) or 1/scale_multiplier
     uint8_t dtype;
 };
-size_t attn_i8_scratch_bytes(uint32_t B, uint32_t H, uint32_t bucket, uint32_t D);
-bool attn_i8_supported(uint32_t H, uint32_t Hkv, uint32_t D);
+size_t attn_i8_scratch_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t bucket, uint32_t D);
+bool attn_i8_supported(uint32_t H, uint32_t Hkv, uint32_t D, uint32_t bucket);
 hipError_t launch_attn_i8(const AttnI8Args &a, void *scratch, hipStream_t stream);
 
 // gemm.hip — C = A*B row-major, fp32 accumulation. dtype f32 or bf16 (bf16

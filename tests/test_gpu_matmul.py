@@ -48,15 +48,13 @@ def test_matmul_parity(torch_cuda, backend, m, k, n, dtype, tol):
 
 
 def test_bf16_truncates(torch_cuda, backend):
-    """bf16 narrowing is truncation (write_bf16, src/cpu/dtype.rs:75-79): the exact
-    sum 1 + 2^-8 + 2^-9 = 0x3F818000 narrows to 0x3F81 (rounding would give 0x3F82)."""
+    """bf16 narrowing is truncation (write_bf16, src/cpu/dtype.rs:75-79): the single
+    exact product (1 + 2^-7) * 1.5 = 0x3FC18000 narrows to 0x3FC1, where rounding to
+    nearest-even would give 0x3FC2."""
     k = 64
-    a = np.zeros(k, np.float32)
-    a[:3] = 1.0
-    b = np.zeros(k, np.float32)
-    b[:3] = [1.0, 2.0 ** -8, 2.0 ** -9]
-    ab = (a.view(np.uint32) >> 16).astype(np.uint16)
-    bb = (b.view(np.uint32) >> 16).astype(np.uint16)
+    ab = np.zeros(k, np.uint16)
+    bb = np.zeros(k, np.uint16)
+    ab[5], bb[5] = 0x3F81, 0x3FC0
     out = torch_cuda.zeros(2, dtype=torch_cuda.uint8, device="cuda")
     ws = DeviceWorkspace()
     ws.bind(0, to_dev(torch_cuda, ab))
@@ -65,7 +63,7 @@ def test_bf16_truncates(torch_cuda, backend):
     backend.dispatch(KernelCall.MatMul(MatMulCall(BufferRef(0), BufferRef(1), BufferRef(2), 1, k,
                                                   1, DTYPE_BF16)), ws)
     backend.synchronize()
-    assert int(from_dev(out, np.uint16)[0]) == 0x3F81
+    assert int(from_dev(out, np.uint16)[0]) == 0x3FC1
 
 
 def test_packed_b_refused(torch_cuda, backend):

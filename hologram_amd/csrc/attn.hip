@@ -40,6 +40,7 @@
 #include <hip/hip_runtime.h>
 
 #include <math.h>
+#include <stdlib.h>
 
 #include "holo_device.h"
 #include "holo_kernels.h"
@@ -50,8 +51,8 @@ namespace {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kChunk = 1024;   // keys per workgroup
-constexpr int kMaxChunks = 256; // bucket_rows <= kChunk * kMaxChunks
+constexpr int kMaxChunks = 256; // chunks per plane (bucket_rows <= chunk * kMaxChunks)
+constexpr int kWps = 3;  // wavefronts per SIMD the registers are budgeted for
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBlock = 32;     // keys per wavefront step
@@ -88,13 +89,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_
 }
 
 // D: head_dim (64 or 128); kF32Q: q/out are f32 (else bf16). G (query heads per
-// kv head) is <= 16 at run time.
+// kv head) is <= 16 at run time. Registers are budgeted for three wavefronts per
+// SIMD (measured best: more waves spill, fewer leave the loads too thin).
 template <int D, bool kF32Q>
-__global__ __launch_bounds__(kThreads) void attn_mfma_kernel(
+__global__ __launch_bounds__(kThreads, kWps) void attn_mfma_kernel(
     const void *__restrict__ q, const int8_t *__restrict__ kq, const int8_t *__restrict__ vq,
     const float *__restrict__ ks, const float *__restrict__ vs, const uint32_t *__restrict__ lens,
     float *__restrict__ part, void *__restrict__ out, uint32_t H, uint32_t Hkv, uint32_t G,
-    uint32_t bucket, uint32_t nchunks, float log2e_over_scale) {
+    uint32_t bucket, uint32_t kChunk, uint32_t nchunks, float log2e_over_scale) {
     constexpr int KB = D / 4;          // K bytes per lane per key row (QK k-slots)
     constexpr int NKS = D / 64;        // i8 MFMA k-steps (64 dims each)
     constexpr int NDB = D / 16;        // 16-row dim blocks of O^T
@@ -102,6 +104,7 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(
 
     __shared__ float red_m[kWaves][16], red_l[kWaves][16];
     __shared__ float red_o[kWaves][16][D];
+    __shared__ float4 blk_sc[kWaves][16];   // the current block's 32 k- and 32 v-scales
 
     const uint32_t b = blockIdx.z, kh = blockIdx.y, chunk = blockIdx.x;
     uint32_t L = lens[b];
@@ -120,7 +123,7 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(
         }
         return;
     }
-    const uint32_t c1 = L - c0 < uint32_t(kChunk) ? L : c0 + kChunk;
+    const uint32_t c1 = L - c0 < kChunk ? L : c0 + kChunk;
     const int r = lane & 15, g = lane >> 4;
     // the wavefront index is uniform: keep block offsets in scalar registers
     const int wv = __builtin_amdgcn_readfirstlane(wave);
@@ -133,18 +136,17 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(
     const auto rvs = rsrc(vs + plane * bucket, bucket * 4);
 
     // Per-lane byte offsets inside a 32-key block; the block base is a uniform
-    // soffset. K rows 16mb + r (KB bytes at KB*g); V rows
-    // kappa(g, j) = 16(j/4) + 4g + j%4 (NDB bytes at NDB*r).
-    uint32_t koff[2], voff[8];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) koff[mb] = (16 * mb + r) * D + KB * g;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) voff[j] = (16 * (j >> 2) + 4 * g + (j & 3)) * D + NDB * r;
+    // soffset and the per-row parts are instruction immediates. K rows 16mb + r
+    // (KB bytes at KB*g); V rows kappa(g, j) = 16(j/4) + 4g + j%4 (NDB bytes at
+    // NDB*r); scales: lane l < 32 takes kscale[l], lane l >= 32 vscale[l - 32].
+    const int koff = r * D + KB * g;
+    const int voff = 4 * g * D + NDB * r;
+    const int soff = 4 * lane;
 
     struct Blk {
         u32x4 k[2][NKS];
         uint32_t v[8][VW];
-        float ksc[8], vsc[8];
+        float sc;                           // one key or value scale per lane
     };
     auto load = [&](uint32_t blk, Blk &o) {
         const int kvs = int(blk * D), ss = int(blk * 4);
@@ -152,30 +154,20 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(
         for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
             for (int s = 0; s < NKS; ++s)
-                o.k[mb][s] = __builtin_amdgcn_raw_buffer_load_b128(rk, int(koff[mb]) + 16 * s, kvs, 0);
+                o.k[mb][s] = __builtin_amdgcn_raw_buffer_load_b128(rk, koff + 16 * mb * D + 16 * s, kvs, 0);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
+            const int row = (16 * (j >> 2) + (j & 3)) * D;
             if constexpr (VW == 2) {
-                const auto w = __builtin_amdgcn_raw_buffer_load_b64(rv, int(voff[j]), kvs, 0);
+                const auto w = __builtin_amdgcn_raw_buffer_load_b64(rv, voff + row, kvs, 0);
                 o.v[j][0] = w[0];
                 o.v[j][1] = w[1];
             } else {
-                o.v[j][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, int(voff[j]), kvs, 0);
+                o.v[j][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, voff + row, kvs, 0);
             }
         }
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const u32x4 k4 = __builtin_amdgcn_raw_buffer_load_b128(rks, (16 * h + 4 * g) * 4, ss, 0);
-            const u32x4 v4 = __builtin_amdgcn_raw_buffer_load_b128(rvs, (16 * h + 4 * g) * 4, ss, 0);
-            o.ksc[4 * h] = __uint_as_float(k4.x);
-            o.ksc[4 * h + 1] = __uint_as_float(k4.y);
-            o.ksc[4 * h + 2] = __uint_as_float(k4.z);
-            o.ksc[4 * h + 3] = __uint_as_float(k4.w);
-            o.vsc[4 * h] = __uint_as_float(v4.x);
-            o.vsc[4 * h + 1] = __uint_as_float(v4.y);
-            o.vsc[4 * h + 2] = __uint_as_float(v4.z);
-            o.vsc[4 * h + 3] = __uint_as_float(v4.w);
-        }
+        o.sc = __uint_as_float(lane < 32 ? __builtin_amdgcn_raw_buffer_load_b32(rks, soff, ss, 0)
+                                         : __builtin_amdgcn_raw_buffer_load_b32(rvs, soff - 128, ss, 0));
     };
 
     // Q loads first, then the first block's: the Q set-up below waits only for Q.
@@ -210,6 +202,9 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(
 #pragma unroll
         for (int e = 0; e < KB; ++e) qv[e] = live ? qv[e] : 0.0f;
     }
+    // Wavefront wv takes every fourth 32-key block of the chunk; one block is
+    // in flight (prefetched into registers) while the previous is computed.
+    constexpr uint32_t kStride = kWaves * kBlock;
     const uint32_t first = c0 + wv * kBlock;
     Blk cur;
     if (first < c1) load(first, cur);
@@ -252,12 +247,23 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(
     int ve = -200;                         // 2^ve bounds every vscale seen (unset)
     float v_unscale = 0.0f;
 
-    for (uint32_t blk = first; blk < c1; blk += kWaves * kBlock) {
-        // prefetch the next block of this wavefront before computing this one
-        const uint32_t nb = blk + kWaves * kBlock;
+    for (uint32_t blk = first; blk < c1; blk += kStride) {
+        const uint32_t nb = blk + kStride;
         Blk nxt;
         if (nb < c1) load(nb, nxt);
         const bool full = blk + kBlock <= c1;
+        // this block's scales through the wavefront's LDS slot: keys 16h + 4g + i
+        reinterpret_cast<float *>(blk_sc[wv])[lane] = cur.sc;
+        __builtin_amdgcn_wave_barrier();
+        float ksc[8], vsc[8];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float4 k4 = blk_sc[wv][4 * h + g];
+            const float4 v4 = blk_sc[wv][8 + 4 * h + g];
+            ksc[4 * h] = k4.x; ksc[4 * h + 1] = k4.y; ksc[4 * h + 2] = k4.z; ksc[4 * h + 3] = k4.w;
+            vsc[4 * h] = v4.x; vsc[4 * h + 1] = v4.y; vsc[4 * h + 2] = v4.z; vsc[4 * h + 3] = v4.w;
+        }
+        __builtin_amdgcn_wave_barrier();
 
         // -- S^T = K . Q^T on the int8 MFMA, exact in int32: lane holds keys
         //    16mb + 4g + i for head r
@@ -279,9 +285,9 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(
         for (int j = 0; j < 8; ++j) {
             const uint32_t key = blk + 16 * (j >> 2) + 4 * g + (j & 3);
             const bool vis = full || key < c1;
-            sc[j] = vis ? (sc[j] * cur.ksc[j]) * score_mul : -INFINITY;
+            sc[j] = vis ? (sc[j] * ksc[j]) * score_mul : -INFINITY;
             m_blk = fmaxf(m_blk, sc[j]);
-            vb = vis ? fmaxf(vb, cur.vsc[j]) : vb;
+            vb = vis ? fmaxf(vb, vsc[j]) : vb;
         }
         m_blk = fmaxf(m_blk, __shfl_xor(m_blk, 16, 64));
         m_blk = fmaxf(m_blk, __shfl_xor(m_blk, 32, 64));
@@ -310,7 +316,7 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(
         for (int j = 0; j < 8; ++j) {
             const float p = exp2f(sc[j] - m_run);           // masked keys: exp2(-inf) = 0
             l_run += p;
-            const float pw = p * (cur.vsc[j] * v_unscale);
+            const float pw = p * (vsc[j] * v_unscale);
             pf[j] = (_Float16)(p > 0.0f ? pw : 0.0f);       // never 0 * garbage scale
         }
 
@@ -388,7 +394,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restri
                                                           const uint32_t *__restrict__ lens,
                                                           void *__restrict__ out, uint32_t H,
                                                           uint32_t Hkv, uint32_t G,
-                                                          uint32_t bucket, uint32_t nchunks) {
+                                                          uint32_t bucket, uint32_t kChunk,
+                                                          uint32_t nchunks) {
     __shared__ float wgt[kMaxChunks][16];
     __shared__ float inv_l[16];
     const uint32_t kh = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
@@ -443,30 +450,48 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restri
     }
 }
 
-uint32_t chunks_of(uint32_t bucket) { return (bucket + kChunk - 1) / kChunk; }
+// Keys per workgroup: a multiple of the 128 keys one pass of the four
+// wavefronts covers. HOLO_ATTN_CHUNK overrides it (tuning sweeps).
+uint32_t chunk_keys(uint32_t bucket) {
+    static const uint32_t forced = [] {
+        const char *e = getenv("HOLO_ATTN_CHUNK");
+        const long v = e ? strtol(e, nullptr, 10) : 0;
+        return v >= 128 && v % 128 == 0 ? uint32_t(v) : 0u;
+    }();
+    uint32_t c = forced ? forced : 2048;
+    while ((bucket + c - 1) / c > uint32_t(kMaxChunks)) c *= 2;
+    return c;
+}
+
+uint32_t chunks_of(uint32_t bucket) {
+    const uint32_t c = chunk_keys(bucket);
+    return (bucket + c - 1) / c;
+}
 
 template <int D>
 hipError_t run(const AttnI8Args &a, void *scratch, hipStream_t stream) {
+    const uint32_t ck = chunk_keys(a.bucket);
     const uint32_t nch = chunks_of(a.bucket);
     const uint32_t G = a.H / a.Hkv;
     float *part = static_cast<float *>(scratch);
     const dim3 grid(nch, a.Hkv, a.B);
     const float mul = kLog2e / a.score_scale;
     if (a.dtype == 8)
-        hipLaunchKernelGGL((attn_mfma_kernel<D, true>), grid, dim3(kThreads), 0, stream, a.q, a.kq,
-                           a.vq, a.ks, a.vs, a.lens, part, a.out, a.H, a.Hkv, G, a.bucket, nch, mul);
+        hipLaunchKernelGGL((attn_mfma_kernel<D, true>), grid, dim3(kThreads), 0,
+                           stream, a.q, a.kq, a.vq, a.ks, a.vs, a.lens, part, a.out, a.H, a.Hkv, G,
+                           a.bucket, ck, nch, mul);
     else
-        hipLaunchKernelGGL((attn_mfma_kernel<D, false>), grid, dim3(kThreads), 0, stream, a.q,
-                           a.kq, a.vq, a.ks, a.vs, a.lens, part, a.out, a.H, a.Hkv, G, a.bucket,
-                           nch, mul);
+        hipLaunchKernelGGL((attn_mfma_kernel<D, false>), grid, dim3(kThreads), 0,
+                           stream, a.q, a.kq, a.vq, a.ks, a.vs, a.lens, part, a.out, a.H, a.Hkv, G,
+                           a.bucket, ck, nch, mul);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || nch == 1) return e;
     if (a.dtype == 8)
         hipLaunchKernelGGL((attn_combine_kernel<D, true>), dim3(a.Hkv, a.B), dim3(256), 0, stream,
-                           part, a.lens, a.out, a.H, a.Hkv, G, a.bucket, nch);
+                           part, a.lens, a.out, a.H, a.Hkv, G, a.bucket, ck, nch);
     else
         hipLaunchKernelGGL((attn_combine_kernel<D, false>), dim3(a.Hkv, a.B), dim3(256), 0, stream,
-                           part, a.lens, a.out, a.H, a.Hkv, G, a.bucket, nch);
+                           part, a.lens, a.out, a.H, a.Hkv, G, a.bucket, ck, nch);
     return hipGetLastError();
 }
 
@@ -479,7 +504,7 @@ size_t attn_i8_scratch_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t buck
 
 bool attn_i8_supported(uint32_t H, uint32_t Hkv, uint32_t D, uint32_t bucket) {
     if (Hkv == 0 || H % Hkv) return false;
-    return (D == 64 || D == 128) && H / Hkv <= 16 && chunks_of(bucket) <= uint32_t(kMaxChunks);
+    return (D == 64 || D == 128) && H / Hkv <= 16 && bucket <= (1u << 30) / D;
 }
 
 hipError_t launch_attn_i8(const AttnI8Args &a, void *scratch, hipStream_t stream) {

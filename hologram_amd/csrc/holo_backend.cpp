@@ -339,7 +339,7 @@ int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attentio
     if (!holo::attn_i8_supported(c.heads, hkv, c.head_dim, c.bucket_rows))
         return fail(HOLO_ERR_UNSUPPORTED_OP,
                     "decode_attention_i8: head_dim must be 64 or 128, heads/kv_heads at most 16 "
-                    "and bucket_rows at most 262144");
+                    "and bucket_rows * head_dim at most 2^30");
     const uint64_t es = dtype_size(c.dtype);
     const uint64_t qn = uint64_t(c.batch) * c.heads * c.head_dim;
     const uint64_t rows = uint64_t(c.batch) * hkv * c.bucket_rows;

@@ -1,22 +1,22 @@
 // lut.hip — bf16/f16 activation as a gather through the 65536-entry table
 // (the device form of unary_lut, crates/hologram-compute/src/cpu/lut.rs:76-98).
 //
-// Every workgroup first stages the whole 128 KiB table in LDS (gfx950 gives a
-// workgroup up to 160 KiB), then streams the input with 16-byte loads and
-// stores: 8 patterns per load, 8 LDS lookups, one 16-byte store. The grid is
-// one workgroup per CU, persistent, so the table is staged 256 times (32 MiB
-// of L2/MALL reads) for any n. HBM traffic is 2 bytes read + 2 bytes written
-// per element.
+// One persistent workgroup per CU holds the whole 128 KiB table in LDS (gfx950
+// gives a workgroup up to 160 KiB). Each thread first issues the 16-byte loads
+// of its first input vectors, then helps stage the table, so the table's L2
+// reads overlap the HBM reads; after the barrier it looks up 8 patterns per
+// vector in LDS and streams the results out. A workgroup's vectors are one
+// contiguous span per pass (DRAM page locality). HBM traffic: 2 bytes read +
+// 2 bytes written per element; the table adds one 128 KiB L2 read per CU.
 #include <hip/hip_runtime.h>
+
+#include <stdlib.h>
 
 #include "holo_device.h"
 #include "holo_kernels.h"
 
 namespace holo {
 namespace {
-
-constexpr int kThreads = 1024;
-constexpr int kUnroll = 4;  // 16-byte vectors in flight per thread
 
 __device__ __forceinline__ uint32_t look2(const uint16_t *t, uint32_t w) {
     return static_cast<uint32_t>(t[w & 0xffffu]) | (static_cast<uint32_t>(t[w >> 16]) << 16);
@@ -31,36 +31,77 @@ __device__ __forceinline__ u32x4 look8(const uint16_t *t, u32x4 v) {
     return r;
 }
 
-// nvec: number of 16-byte vectors handled by the vector loop (0 when the
-// pointers are not both 16-byte aligned); elements [nvec*8, n) take the
-// scalar loop.
-__global__ __launch_bounds__(kThreads) void lut_gather_kernel(const uint16_t *__restrict__ table,
-                                                             const uint16_t *__restrict__ in,
-                                                             uint16_t *__restrict__ out,
-                                                             uint64_t n, uint64_t nvec) {
+// TPB threads, VPT 16-byte vectors per thread per pass. nvec: vectors handled
+// by the vector path (0 when the pointers are not both 16-byte aligned);
+// elements [nvec*8, n) take the scalar tail.
+template <int TPB, int VPT>
+__global__ __launch_bounds__(TPB) void lut_gather_kernel(const uint16_t *__restrict__ table,
+                                                        const uint16_t *__restrict__ in,
+                                                        uint16_t *__restrict__ out, uint64_t n,
+                                                        uint64_t nvec) {
     __shared__ u32x4 lds4[65536 * 2 / 16];
+    const u32x4 *in4 = reinterpret_cast<const u32x4 *>(in);
+    u32x4 *out4 = reinterpret_cast<u32x4 *>(out);
+    constexpr uint64_t kSpan = uint64_t(TPB) * VPT;          // vectors per workgroup pass
+    const uint64_t pass = uint64_t(gridDim.x) * kSpan;
+
+    uint64_t base = blockIdx.x * kSpan + threadIdx.x;
+    u32x4 v[VPT];
+#pragma unroll
+    for (int u = 0; u < VPT; ++u) {
+        const uint64_t i = base + uint64_t(u) * TPB;
+        if (i < nvec) v[u] = ld_stream(&in4[i]);
+    }
     const u32x4 *tab4 = reinterpret_cast<const u32x4 *>(table);
 #pragma unroll
-    for (int i = 0; i < 65536 * 2 / 16 / kThreads; ++i)
-        lds4[threadIdx.x + i * kThreads] = tab4[threadIdx.x + i * kThreads];
+    for (int i = 0; i < 65536 * 2 / 16 / TPB; ++i) lds4[threadIdx.x + i * TPB] = tab4[threadIdx.x + i * TPB];
     __syncthreads();
     const uint16_t *t = reinterpret_cast<const uint16_t *>(lds4);
 
-    const u32x4 *in4 = reinterpret_cast<const u32x4 *>(in);
-    u32x4 *out4 = reinterpret_cast<u32x4 *>(out);
-    const uint64_t stride = uint64_t(gridDim.x) * kThreads;
-    uint64_t i = uint64_t(blockIdx.x) * kThreads + threadIdx.x;
-    // main loop: kUnroll independent 16-byte loads before any lookup
-    for (; i + (kUnroll - 1) * stride < nvec; i += kUnroll * stride) {
-        u32x4 v[kUnroll];
+    while (base < nvec) {
+        const uint64_t next = base + pass;
+        u32x4 w[VPT];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) v[u] = ld_stream(&in4[i + u * stride]);
+        for (int u = 0; u < VPT; ++u) {   // next pass's loads go out before this pass's stores
+            const uint64_t i = next + uint64_t(u) * TPB;
+            if (i < nvec) w[u] = ld_stream(&in4[i]);
+        }
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) st_stream(look8(t, v[u]), &out4[i + u * stride]);
+        for (int u = 0; u < VPT; ++u) {
+            const uint64_t i = base + uint64_t(u) * TPB;
+            if (i < nvec) st_stream(look8(t, v[u]), &out4[i]);
+        }
+#pragma unroll
+        for (int u = 0; u < VPT; ++u) v[u] = w[u];
+        base = next;
     }
-    for (; i < nvec; i += stride) out4[i] = look8(t, in4[i]);
-    for (uint64_t e = nvec * 8 + uint64_t(blockIdx.x) * kThreads + threadIdx.x; e < n; e += stride)
+    for (uint64_t e = nvec * 8 + uint64_t(blockIdx.x) * TPB + threadIdx.x; e < n;
+         e += uint64_t(gridDim.x) * TPB)
         out[e] = t[in[e]];
+}
+
+int cu_count() {
+    static const int cus = [] {
+        int dev = 0, c = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
+            c = 256;
+        return c;
+    }();
+    return cus;
+}
+
+template <int TPB, int VPT>
+hipError_t launch(const uint16_t *table, const uint16_t *in, uint16_t *out, uint64_t n,
+                  uint64_t nvec, hipStream_t stream) {
+    // one workgroup per CU at most (the table fills the CU's LDS)
+    const uint64_t work = nvec ? (nvec + uint64_t(TPB) * VPT - 1) / (uint64_t(TPB) * VPT)
+                               : (n + TPB - 1) / TPB;
+    uint64_t blocks = work < uint64_t(cu_count()) ? work : uint64_t(cu_count());
+    if (blocks == 0) blocks = 1;
+    hipLaunchKernelGGL((lut_gather_kernel<TPB, VPT>), dim3(unsigned(blocks)), dim3(TPB), 0, stream,
+                       table, in, out, n, nvec);
+    return hipGetLastError();
 }
 
 }  // namespace
@@ -70,17 +111,21 @@ hipError_t launch_lut_u16(const uint16_t *table, const uint16_t *in, uint16_t *o
     if (n == 0) return hipSuccess;
     const bool aligned = ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
     const uint64_t nvec = aligned ? n / 8 : 0;
-    int dev = 0, cus = 256;
-    (void)hipGetDevice(&dev);
-    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    // one persistent workgroup per CU; fewer when n is small
-    const uint64_t work = aligned ? nvec : n;
-    uint64_t blocks = (work + kThreads - 1) / kThreads;
-    if (blocks > uint64_t(cus)) blocks = cus;
-    if (blocks == 0) blocks = 1;
-    hipLaunchKernelGGL(lut_gather_kernel, dim3(unsigned(blocks)), dim3(kThreads), 0, stream, table,
-                       in, out, n, nvec);
-    return hipGetLastError();
+    // HOLO_LUT_CFG selects a launch shape for tuning sweeps (0 = default).
+    static const int cfg = [] {
+        const char *e = getenv("HOLO_LUT_CFG");
+        return e ? atoi(e) : 0;
+    }();
+    switch (cfg) {
+        case 1: return launch<1024, 1>(table, in, out, n, nvec, stream);
+        case 2: return launch<1024, 2>(table, in, out, n, nvec, stream);
+        case 3: return launch<512, 2>(table, in, out, n, nvec, stream);
+        case 4: return launch<512, 4>(table, in, out, n, nvec, stream);
+        case 5: return launch<256, 4>(table, in, out, n, nvec, stream);
+        case 6: return launch<512, 16>(table, in, out, n, nvec, stream);
+        case 7: return launch<1024, 4>(table, in, out, n, nvec, stream);
+        default: return launch<1024, 8>(table, in, out, n, nvec, stream);
+    }
 }
 
 }  // namespace holo

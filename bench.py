@@ -29,6 +29,26 @@ FP32_PEAK_TFLOPS = 157.3       # fp32 matrix
 METRIC = "int8-KV decode attn tok/s & HBM GB/s; bf16 LUT Gelem/s; GEMM TFLOP/s"
 
 
+def profiled_traffic(key):
+    """HBM bytes per launch measured by rocprofv3 counters (profiles/traffic.txt)."""
+    f = ROOT / "profiles" / "traffic.txt"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        parts = line.split()
+        if len(parts) >= 3 and parts[0] == key:
+            return int(parts[1]) + int(parts[2])
+    return None
+
+
+def roofline(bound, achieved, peak, unit, traffic=None, kernel=None):
+    r = {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
+         "frac": achieved / peak, "traffic": traffic}
+    if kernel:
+        r["kernel"] = kernel
+    return r
+
+
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -259,7 +279,9 @@ def bench_kv(torch, be, args, rep):
             alg = planes * D * 2 + planes * D + planes * 4 + 4
         else:
             alg = 2 * (planes * bucket * D + planes * bucket * 4) + planes * D * 2
-        res[form] = {"us": ms * 1e3, "alg_bytes": alg, "hbm_gbs": alg / (ms / 1e3) / 1e9}
+        gbs = alg / (ms / 1e3) / 1e9
+        res[form] = {"us": ms * 1e3, "alg_bytes": alg, "hbm_gbs": gbs,
+                     "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
     rep["kv"] = res
     return res
 
@@ -299,8 +321,12 @@ def bench_gemm(torch, be, args, rep):
             ms = timer.mean_ms()
             tf = 2.0 * m * n * k / (ms / 1e3) / 1e12
             key = f"{'bf16' if dt == DTYPE_BF16 else 'f32'}_{m}x{n}x{k}"
-            res[key] = {"tflops": tf, "ms": ms, "frac_peak": tf / peak,
-                        "hbm_gbs": (m * k + k * n + m * n) * es / (ms / 1e3) / 1e9}
+            gbs = (m * k + k * n + m * n) * es / (ms / 1e3) / 1e9
+            if m <= 64:   # skinny: bandwidth-bound on B
+                rl = roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")
+            else:
+                rl = roofline("mfma", tf, peak, "TFLOP/s")
+            res[key] = {"tflops": tf, "ms": ms, "hbm_gbs": gbs, "roofline": rl}
             del ws, calls
     rep["gemm"] = res
     return res
@@ -350,17 +376,21 @@ def main():
                    "len_dist": "U[512, 32768]", "sum_len": attn["sum_len"] if attn else None},
     }
     if attn:
-        line["roofline"] = {"bound": "hbm", "achieved": attn["hbm_gbs"], "peak": HBM_PEAK_GBS,
-                            "unit": "GB/s", "frac": attn["hbm_gbs"] / HBM_PEAK_GBS,
-                            "traffic": None}
+        line["roofline"] = roofline(
+            "hbm", attn["hbm_gbs"], HBM_PEAK_GBS, "GB/s", profiled_traffic("decode_attn_i8_config4"),
+            "attn_mfma_kernel + attn_combine_kernel (one DecodeAttentionI8 dispatch); "
+            f"algorithmic bytes {attn['alg_bytes']}")
     if "attn_cpu" in rep:
         c = rep["attn_cpu"]
         line["cpu_baseline"] = {k: c[k] for k in ("value", "unit", "cores", "kind", "sample")}
     comps = {}
     if "lut" in rep:
-        comps["lut_bf16_16M"] = {k: {"gelem_s": v["gelem_s"], "us": v["us"],
-                                     "roofline_frac": v["hbm_gbs"] / HBM_PEAK_GBS}
-                                 for k, v in rep["lut"].items()}
+        comps["lut_bf16_16M"] = {
+            k: {"gelem_s": v["gelem_s"], "us": v["us"],
+                "roofline": roofline("hbm", v["hbm_gbs"], HBM_PEAK_GBS, "GB/s",
+                                     profiled_traffic("lut_gather_bf16_16M"),
+                                     "lut_gather_kernel; algorithmic bytes 67108864")}
+            for k, v in rep["lut"].items()}
         if "lut_cpu" in rep:
             comps["lut_bf16_16M"]["cpu_baseline"] = rep["lut_cpu"]
     if "kv" in rep:

@@ -1,0 +1,285 @@
+"""CPU tests that pin the oracle (oracle/holo_oracle.c) to the reference.
+
+Each oracle function is checked against something other than its own formula:
+the reference's golden vector, the reference's own test tolerances, a closed
+form or a brute force on tiny inputs. Where a plausible mistake would slip
+through one check, a second check is chosen to catch it (a planted mistake is
+computed here on the CPU and shown to fail).
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+
+BF16, F16, F32 = oracle.DTYPE_BF16, oracle.DTYPE_F16, oracle.DTYPE_F32
+L = oracle.lib()
+
+
+def bf16_values():
+    bits = np.arange(65536, dtype=np.uint32) << 16
+    return bits.view(np.float32)
+
+
+def golden_inputs():
+    """The generators of integer_gemv_bits_are_the_cross_lane_golden (simd.rs:8247-8256)."""
+    m, k, n = 3, 64, 24
+    a = (np.array([(i * 37) % 91 for i in range(m * k)], np.float32) - np.float32(45.0)) * np.float32(0.031)
+    scales = (np.float32(0.011) + np.arange(n, dtype=np.float32) * np.float32(0.0007)).astype(np.float32)
+    bq = np.array([((i * 31) % 255) - 127 for i in range(k * n)], dtype=np.int8)
+    return a.astype(np.float32), bq, scales, m, k, n
+
+
+# ---------------------------------------------------------------- golden ----
+
+def test_int8_quantizer_reproduces_reference_golden():
+    """FNV-1a of matmul_i8_pc_omajor(3, 64, 24) == 0x787ccdc172029f9b (simd.rs:8259)."""
+    a, bq, scales, m, k, n = golden_inputs()
+    out = oracle.matmul_i8_pc_omajor(a, bq, scales, m, k, n)
+    assert oracle.fnv1a_f32(out) == 0x787CCDC172029F9B
+
+
+def _golden_with(quantize):
+    """The golden's arithmetic with a substitute quantizer (numpy, CPU only)."""
+    a, bq, scales, m, k, n = golden_inputs()
+    out = np.zeros(m * n, np.float32)
+    for i in range(m):
+        row = a[i * k:(i + 1) * k]
+        q, s = quantize(row)
+        for j in range(n):
+            acc = int(np.dot(q.astype(np.int64), bq[j * k:(j + 1) * k].astype(np.int64)))
+            out[i * n + j] = np.float32(acc) * (np.float32(s) * scales[j])
+    return oracle.fnv1a_f32(out)
+
+
+def test_golden_discriminates_quantizer_mistakes():
+    """The golden catches a truncating quantizer and a scale computed as 1/inv
+    instead of amax/127. Its inputs never hit an exact .5 tie, so it does NOT
+    tell half-away-from-zero from half-to-even: the tie rule is pinned by the
+    exact-tie closed form in test_quantizer_closed_forms."""
+    def quant(row, rnd, scale_from_inv=False):
+        amax = np.float32(np.max(np.abs(row)))
+        inv = np.float32(127.0) / amax
+        t = (row * inv).astype(np.float32)
+        q = np.clip(rnd(t), -127, 127).astype(np.int8)
+        s = np.float32(1.0) / inv if scale_from_inv else amax / np.float32(127.0)
+        return q, s
+
+    away = lambda t: np.where(t >= 0, np.trunc(t + np.float32(0.5)), np.trunc(t - np.float32(0.5)))
+    assert _golden_with(lambda r: quant(r, away)) == 0x787CCDC172029F9B
+    assert _golden_with(lambda r: quant(r, np.rint)) == 0x787CCDC172029F9B   # no ties here
+    assert _golden_with(lambda r: quant(r, np.trunc)) != 0x787CCDC172029F9B
+    assert _golden_with(lambda r: quant(r, away, scale_from_inv=True)) != 0x787CCDC172029F9B
+
+
+def test_quantizer_closed_forms():
+    # all-zero row: scale 0 and q untouched (the oracle's caller zeroes q)
+    q, s = oracle.quantize_row_i8(np.zeros(8, np.float32))
+    assert s == 0.0 and not q.any()
+    # amax = 127 makes inv exactly 1, so x.5 values are exact ties: they round
+    # away from zero (half-to-even would give 2, -2, 0, 0)
+    row = np.array([127.0, 2.5, -2.5, 0.5, -0.5, -127.0], np.float32)
+    q, s = oracle.quantize_row_i8(row)
+    assert s == np.float32(1.0)
+    assert list(q) == [127, 3, -3, 1, -1, -127]
+    # NaN is ignored by the max and quantizes to 0; Inf gives scale Inf, q 0 / NaN -> 0
+    q, s = oracle.quantize_row_i8(np.array([np.nan, 1.0, -0.5], np.float32))
+    assert q[0] == 0 and q[1] == 127 and s == np.float32(1.0) / np.float32(127.0)
+    q, s = oracle.quantize_row_i8(np.array([np.inf, 3.0], np.float32))
+    assert math.isinf(s) and not q.any()
+
+
+# ---------------------------------------------------------------- exp -------
+
+def test_exp_det_error_bound_and_cutoffs():
+    xs = np.linspace(-87.3, 88.0, 200_001, dtype=np.float32)
+    got = np.array([L.or_exp_f32_det(float(x)) for x in xs[::50]], np.float64)
+    want = np.exp(xs[::50].astype(np.longdouble)).astype(np.float64)
+    rel = np.abs(got - want) / want
+    assert rel.max() <= 2e-6
+    assert L.or_exp_f32_det(0.0) == 1.0
+    assert L.or_exp_f32_det(-100.0) == 0.0
+    assert L.or_exp_f32_det(float("nan")) == 0.0
+    big = L.or_exp_f32_det(float("inf"))
+    assert big == L.or_exp_f32_det(88.0) and 1.6e38 < big < 1.7e38
+
+
+def test_libm_expf_within_one_ulp_of_correctly_rounded_on_every_bf16_input():
+    xs = bf16_values()
+    fin = np.isfinite(xs)
+    got = np.array([L.or_libm_expf(float(x)) for x in xs], np.float32)
+    with np.errstate(over="ignore", under="ignore", invalid="ignore"):
+        cr = np.exp(xs.astype(np.longdouble)).astype(np.float32)
+    gu, cu = got.view(np.uint32).astype(np.int64), cr.view(np.uint32).astype(np.int64)
+    assert np.abs(gu - cu)[fin].max() <= 1
+    # the bf16 Exp table equals the truncated correctly rounded value everywhere
+    assert np.array_equal((gu >> 16)[fin], (cu >> 16)[fin])
+    assert int(np.float32(L.or_libm_expf(1.0)).view(np.uint32)) == 0x402DF854
+    assert L.or_libm_expf(float("-inf")) == 0.0 and math.isinf(L.or_libm_expf(100.0))
+
+
+# ---------------------------------------------------------------- tables ----
+
+def gelu_f64(x):
+    c = math.sqrt(2.0 / math.pi)
+    return 0.5 * x * (1.0 + math.tanh(c * (x + 0.044715 * x ** 3)))
+
+
+def test_reference_lut_tests_hold():
+    """tests/lut.rs:67-132: GELU within 0.02 + 0.02|want|, Sigmoid within 0.01."""
+    tg = oracle.build_table(oracle.ACT_GELU, BF16)
+    ts = oracle.build_table(oracle.ACT_SIGMOID, BF16)
+    to_bits = lambda v: int(np.float32(v).view(np.uint32)) >> 16
+    widen = lambda b: float((np.uint32(b) << np.uint32(16)).view(np.float32))
+    for i in range(64):
+        b = to_bits(i * 0.25 - 8.0)
+        x, got = widen(b), widen(tg[b])
+        assert abs(got - gelu_f64(x)) <= 0.02 + 0.02 * abs(gelu_f64(x))
+    for i in range(48):
+        b = to_bits(i * 0.4 - 9.0)
+        x, got = widen(b), widen(ts[b])
+        assert abs(got - 1.0 / (1.0 + math.exp(-x))) <= 0.01
+
+
+@pytest.mark.parametrize("act,ref,floor", [
+    (oracle.ACT_GELU, gelu_f64, 0.0),
+    (oracle.ACT_SILU, lambda x: x / (1.0 + math.exp(-x)) if x > -700 else 0.0, 0.0),
+    (oracle.ACT_SIGMOID, lambda x: 1.0 / (1.0 + math.exp(-x)) if x > -700 else 0.0, 0.0),
+    # tanh_f = (e - 1)/(e + 1): e - 1 cancels, an absolute error of ~ulp(1)/2
+    (oracle.ACT_TANH, math.tanh, 2.0 ** -23),
+])
+def test_tables_track_the_f64_function_on_every_finite_pattern(act, ref, floor):
+    """Each bf16 entry is within one bf16 ulp (truncation) of the f64 function,
+    plus the f32 rounding of the cancelling term 1 + tanh/exp (|x| * 2^-22, or
+    the absolute floor of tanh's e - 1)."""
+    t = oracle.build_table(act, BF16)
+    xs = bf16_values()
+    got = (t.astype(np.uint32) << 16).view(np.float32)
+    for b in range(0, 65536, 7):
+        x = float(xs[b])
+        if not math.isfinite(x) or abs(x) > 80:
+            continue
+        want = ref(x)
+        tol = abs(want) * 2.0 ** -7 + abs(x) * 2.0 ** -22 + floor + 1e-38
+        assert abs(float(got[b]) - want) <= tol, (hex(b), x, float(got[b]), want)
+
+
+def test_table_special_values_follow_x86_semantics():
+    g = oracle.build_table(oracle.ACT_GELU, BF16)
+    s = oracle.build_table(oracle.ACT_SILU, BF16)
+    assert g[0xFF80] == 0xFFC0          # GELU(-Inf) = (-Inf) * 0: x86 default NaN
+    assert g[0x7F80] == 0x7F80          # GELU(+Inf) = +Inf
+    assert s[0x7F80] == 0x7F80 and s[0xFF80] == 0xFF80
+    assert g[0x7FC1] == 0x7FC1          # quiet NaN input propagates
+    assert s[0x7F81] == 0x7FC1          # signaling NaN is quieted (IEEE)
+    e = oracle.build_table(oracle.ACT_EXP, BF16)
+    assert e[0x0000] == 0x3F80 and e[0x8000] == 0x3F80   # exp(+-0) = 1
+    assert e[0x7F81] == 0x7F81          # libm returns a NaN input unchanged
+
+
+# ---------------------------------------------------------------- codecs ----
+
+def test_f16_codec_round_trip_and_rounding_rule():
+    for b in range(65536):
+        if (b & 0x7C00) == 0x7C00 and (b & 0x3FF):
+            continue   # NaNs
+        assert L.or_f32_to_f16(L.or_f16_to_f32(b)) == b
+    # ties: the reference adds half an ulp and truncates (half-up), not RNE
+    assert L.or_f32_to_f16(1.0 + 2.0 ** -11) == 0x3C01            # RNE would give 0x3C00
+    assert L.or_f32_to_f16(70000.0) == 0x7C00                      # overflow -> Inf
+    assert L.or_f32_to_f16(float("nan")) in (0x7E00, 0xFE00)
+    # bf16 narrowing is truncation
+    assert L.or_f32_to_bf16(float(np.float32(1.0 + 2.0 ** -8 + 2.0 ** -9))) == 0x3F80
+
+
+# ---------------------------------------------------------------- KV write --
+
+@pytest.mark.parametrize("pos,new_rows", [(0, 1), (3, 2), (4, 3), (2**32 - 1, 5), (7, 5)])
+def test_kv_cache_write_ring_placement_brute_force(pos, new_rows):
+    planes, bucket, row = 3, 5, 4
+    rng = np.random.default_rng(pos % 1000)
+    cache = rng.integers(0, 256, size=planes * bucket * row, dtype=np.uint8)
+    new = rng.integers(0, 256, size=planes * new_rows * row, dtype=np.uint8)
+    got = oracle.kv_cache_write(cache, new, pos, planes, bucket, new_rows, row)
+    want = cache.reshape(planes, bucket, row).copy()
+    for p in range(planes):
+        for j in range(new_rows):
+            want[p, (pos + j) % bucket] = new.reshape(planes, new_rows, row)[p, j]
+    assert np.array_equal(got, want.reshape(-1))
+
+
+def test_kv_cache_write_refusals():
+    with pytest.raises(ValueError):
+        oracle.kv_cache_write(np.zeros(8, np.uint8), np.zeros(48, np.uint8), 0, 1, 2, 3, 4)
+
+
+# ---------------------------------------------------------------- attention -
+
+def softmax_attention_f64(q, k, v, scale):
+    s = (k.astype(np.float64) @ q.astype(np.float64)) / scale
+    p = np.exp(s - s.max())
+    p /= p.sum()
+    return p @ v.astype(np.float64)
+
+
+def test_decode_attention_matches_f64_softmax_and_gqa_map():
+    rng = np.random.default_rng(0)
+    B, H, Hkv, D, bucket = 2, 4, 2, 16, 37
+    lens = np.array([37, 5], np.uint32)
+    x = rng.standard_normal((B * Hkv, bucket, D)).astype(np.float32)
+    kq, ks = oracle.kv_quant_append(x, F32, 0, np.zeros(x.size, np.int8),
+                                    np.zeros(B * Hkv * bucket, np.float32), B * Hkv, bucket,
+                                    bucket, D)
+    y = rng.standard_normal((B * Hkv, bucket, D)).astype(np.float32)
+    vq, vs = oracle.kv_quant_append(y, F32, 0, np.zeros(y.size, np.int8),
+                                    np.zeros(B * Hkv * bucket, np.float32), B * Hkv, bucket,
+                                    bucket, D)
+    q = rng.standard_normal(B * H * D).astype(np.float32)
+    scale = oracle.attn_scale(D)
+    assert scale == np.float32(4.0)
+    got = oracle.decode_attention_i8(q, kq, ks, vq, vs, lens, B, H, Hkv, bucket, D, scale)
+    kd = oracle.dequant_i8(kq, ks, D).reshape(B * Hkv, bucket, D)
+    vd = oracle.dequant_i8(vq, vs, D).reshape(B * Hkv, bucket, D)
+    for b in range(B):
+        for h in range(H):
+            plane = b * Hkv + h // (H // Hkv)          # GQA: kv head h / group
+            Lb = int(lens[b])
+            want = softmax_attention_f64(q[(b * H + h) * D:(b * H + h + 1) * D],
+                                         kd[plane, :Lb], vd[plane, :Lb], scale)
+            np.testing.assert_allclose(got[(b * H + h) * D:(b * H + h + 1) * D], want,
+                                       rtol=1e-5, atol=1e-6)
+
+
+def test_decode_attention_zero_and_single_key():
+    D, bucket = 8, 4
+    kq = np.ones(bucket * D, np.int8)
+    ks = np.ones(bucket, np.float32)
+    vq = np.arange(bucket * D, dtype=np.int8)
+    vs = np.full(bucket, 0.5, np.float32)
+    q = np.ones(D, np.float32)
+    out0 = oracle.decode_attention_i8(q, kq, ks, vq, vs, np.array([0], np.uint32), 1, 1, 1,
+                                      bucket, D, 1.0)
+    assert not out0.any()
+    out1 = oracle.decode_attention_i8(q, kq, ks, vq, vs, np.array([1], np.uint32), 1, 1, 1,
+                                      bucket, D, 1.0)
+    np.testing.assert_array_equal(out1, vq[:D].astype(np.float32) * 0.5)
+
+
+# ---------------------------------------------------------------- matmul ----
+
+def test_matmul_reference_closed_forms():
+    rng = np.random.default_rng(3)
+    m, k = 5, 7
+    a = rng.standard_normal(m * k).astype(np.float32)
+    eye = np.eye(k, dtype=np.float32).reshape(-1)
+    assert np.array_equal(oracle.matmul_ref_f64(a, eye, m, k, k), a)
+    perm = np.eye(k, dtype=np.float32)[::-1].copy().reshape(-1)
+    assert np.array_equal(oracle.matmul_ref_f64(a, perm, m, k, k),
+                          a.reshape(m, k)[:, ::-1].reshape(-1))
+    b = rng.standard_normal(k * 3).astype(np.float32)
+    want = a.reshape(m, k).astype(np.float64) @ b.reshape(k, 3).astype(np.float64)
+    np.testing.assert_allclose(oracle.matmul_ref_f64(a, b, m, k, 3),
+                               want.astype(np.float32).reshape(-1), rtol=1e-6)
+    assert oracle.max_rel_err(np.array([1.0, 2.0], np.float32),
+                              np.array([1.0, 4.0], np.float32)) == pytest.approx(0.5)

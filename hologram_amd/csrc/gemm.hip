@@ -10,6 +10,7 @@
 // are issued before the current slab's MFMAs.
 #include <hip/hip_runtime.h>
 
+#include "holo_device.h"
 #include "holo_kernels.h"
 
 namespace holo {
@@ -260,6 +261,154 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(const float *__restr
             }
 }
 
+
+// ------------------------------------------------------ bf16, large tiles ----
+// 256x256 workgroup tile, K slabs of 64, four wavefronts of 128x128 on
+// v_mfma_f32_32x32x16_bf16 (4x4 tiles, 256 fp32 accumulators per lane). B is
+// row-major [K, N]; the MFMA B operand wants 8 consecutive k per lane, so each
+// thread loads an 8(k) x 8(n) block, transposes it in registers with byte
+// permutes and stores it n-major (Bt[n][k]) into LDS: both operands are then
+// 16-byte, k-contiguous LDS reads. LDS rows are padded to 72 elements (144 B)
+// so the 32 rows one fragment read touches fall on distinct banks. The next
+// slab's global loads are issued before the current slab's MFMAs.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+constexpr int kBigM = 256, kBigN = 256, kBigK = 64, kLdk = kBigK + 8;
+
+__device__ __forceinline__ void tile_coords(uint32_t wg, uint32_t nwg, uint32_t tiles_m,
+                                            uint32_t tiles_n, uint32_t *tm, uint32_t *tn) {
+    // Workgroups are dispatched round-robin over the 8 XCDs (wg % 8). Give each
+    // XCD a contiguous run of tile ids, so neighbouring tiles share its L2.
+    const uint32_t tile = nwg % 8 == 0 ? (wg % 8) * (nwg / 8) + wg / 8 : wg;
+    // Grouped order: 8 tile rows per group, columns walked within the group.
+    constexpr uint32_t kGroup = 8;
+    const uint32_t per_group = kGroup * tiles_n;
+    const uint32_t first_m = (tile / per_group) * kGroup;
+    const uint32_t gsize = tiles_m - first_m < kGroup ? tiles_m - first_m : kGroup;
+    const uint32_t in_group = tile % per_group;
+    *tm = first_m + in_group % gsize;
+    *tn = in_group / gsize;
+}
+
+__global__ __launch_bounds__(256, 1) void gemm_bf16_big_kernel(const uint16_t *__restrict__ A,
+                                                              const uint16_t *__restrict__ B,
+                                                              uint16_t *__restrict__ C, uint32_t M,
+                                                              uint32_t N, uint32_t K) {
+    __shared__ uint16_t lds[2][2][kBigM][kLdk];   // [stage][A | Bt][row][k]
+    const uint32_t tiles_m = M / kBigM, tiles_n = N / kBigN;
+    uint32_t tm, tn;
+    tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, &tm, &tn);
+    const uint32_t m0 = tm * kBigM, n0 = tn * kBigN;
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
+    const int lr = lane & 31, lg = lane >> 5;
+
+    // global -> register slab loads
+    const int arow = tid >> 3, akc = (tid & 7) * 8;           // A: 8 threads per 128-byte row
+    // B: an 8x8 block (k 8bkb.., n 8bnb..). kb varies fastest, so the 8 lanes an
+    // LDS store cycle serves write 8 different 16-byte chunks of one Bt row
+    // (rows 8 apart share banks once rows are 16-byte aligned).
+    const int bkb = tid & 7, bnb = tid >> 3;
+    const uint16_t *ag = A + uint64_t(m0 + arow) * K + akc;
+    const uint16_t *bg = B + uint64_t(8 * bkb) * N + n0 + 8 * bnb;
+    u32x4 ra[8], rb[8];
+    auto gload = [&](uint32_t k0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(ag + uint64_t(32 * i) * K + k0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) rb[j] = *reinterpret_cast<const u32x4 *>(bg + uint64_t(k0 + j) * N);
+    };
+    auto lstore = [&](int st) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4 *>(&lds[st][0][arow + 32 * i][akc]) = ra[i];
+        // transpose the 8x8 block: column c gets (k 0..7) as 4 dwords of k pairs
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+            u32x4 o;
+            o.x = __builtin_amdgcn_perm(rb[1][c >> 1], rb[0][c >> 1], sel);
+            o.y = __builtin_amdgcn_perm(rb[3][c >> 1], rb[2][c >> 1], sel);
+            o.z = __builtin_amdgcn_perm(rb[5][c >> 1], rb[4][c >> 1], sel);
+            o.w = __builtin_amdgcn_perm(rb[7][c >> 1], rb[6][c >> 1], sel);
+            *reinterpret_cast<u32x4 *>(&lds[st][1][8 * bnb + c][8 * bkb]) = o;
+        }
+    };
+
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // Software pipeline per 64-deep slab s (LDS buffer s & 1), k-steps kk = 0..3:
+    //   start of slab: global loads of slab s+1 into registers
+    //   each kk:       LDS fragments of kk+1 are read before kk's 16 MFMAs issue
+    //   kk == 2:       slab s+1 goes into the other LDS buffer (its last readers
+    //                  passed the previous slab's barrier)
+    //   kk == 3:       barrier, then slab s+1's kk = 0 fragments are read while
+    //                  kk = 3's MFMAs run
+    bf16x8 af[2][4], bfr[2][4];
+    auto fload = [&](int st, int kk, int fb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            af[fb][i] = *reinterpret_cast<const bf16x8 *>(&lds[st][0][wm + 32 * i + lr][kk + 8 * lg]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            bfr[fb][j] = *reinterpret_cast<const bf16x8 *>(&lds[st][1][wn + 32 * j + lr][kk + 8 * lg]);
+    };
+    auto mfmas = [&](int fb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[fb][i], bfr[fb][j], acc[i][j], 0, 0, 0);
+    };
+
+    const uint32_t nk = K / kBigK;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    fload(0, 0, 0);
+    for (uint32_t s = 0; s < nk; ++s) {
+        const int cur = s & 1;
+        const bool more = s + 1 < nk;
+        if (more) gload((s + 1) * kBigK);
+        // kk = 0, 1, 2: fragments of the next k-step, then this k-step's MFMAs
+        fload(cur, 16, 1);
+        mfmas(0);
+        __builtin_amdgcn_sched_barrier(0);
+        fload(cur, 32, 0);
+        mfmas(1);
+        __builtin_amdgcn_sched_barrier(0);
+        fload(cur, 48, 1);
+        mfmas(0);
+        if (more) lstore(cur ^ 1);
+        __builtin_amdgcn_sched_barrier(0);
+        // kk = 3
+        __syncthreads();
+        if (more) fload(cur ^ 1, 0, 0);
+        mfmas(1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // 32x32 D layout: acc[r] is row 8(r/4) + 4*lg + r%4, column lr. One base
+    // pointer per lane; the scheduling barrier keeps each tile's addresses local
+    // (hoisting all 256 of them would spill).
+    uint16_t *cbase = C + uint64_t(m0 + wm + 4 * lg) * N + n0 + wn + lr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint16_t *ct = cbase + uint64_t(32 * i) * N + 32 * j;
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                ct[uint64_t(8 * (r >> 2) + (r & 3)) * N] = uint16_t(__float_as_uint(acc[i][j][r]) >> 16);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+}
+
 }  // namespace
 
 hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint32_t k, uint32_t n,
@@ -268,6 +417,14 @@ hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint
     const uintptr_t al = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b);
     if (dtype == 7) {
         const bool fast = (al & 15) == 0 && k % BK16 == 0 && n % 8 == 0;
+        // large aligned problems: 256x256 tiles, at least one tile per CU
+        if ((al & 15) == 0 && m % kBigM == 0 && n % kBigN == 0 && k % kBigK == 0 &&
+            uint64_t(m / kBigM) * (n / kBigN) >= 256) {
+            hipLaunchKernelGGL(gemm_bf16_big_kernel, dim3((m / kBigM) * (n / kBigN)), dim3(256), 0,
+                               stream, static_cast<const uint16_t *>(a),
+                               static_cast<const uint16_t *>(b), static_cast<uint16_t *>(c), m, n, k);
+            return hipGetLastError();
+        }
         if (fast)
             hipLaunchKernelGGL(gemm_bf16_kernel<true>, grid, dim3(kThreads), 0, stream,
                                static_cast<const uint16_t *>(a), static_cast<const uint16_t *>(b),

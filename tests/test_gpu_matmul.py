@@ -73,3 +73,34 @@ def test_packed_b_refused(torch_cuda, backend):
     with pytest.raises(UnsupportedOp):
         backend.dispatch(KernelCall.MatMul(MatMulCall(BufferRef(0), BufferRef(1), BufferRef(2),
                                                       4, 4, 4, DTYPE_F32, True)), ws)
+
+
+def run_mm_rows(torch, backend, m, k, n, seed, rows):
+    """bf16 MatMul on the device; f64 reference only on the sampled rows."""
+    g = torch.Generator().manual_seed(seed)
+    a = (torch.randn(m, k, generator=g) / np.sqrt(k)).to(torch.bfloat16)
+    b = (torch.randn(k, n, generator=g) / np.sqrt(k)).to(torch.bfloat16)
+    ad, bd = a.cuda(), b.cuda()
+    out = torch.zeros(m, n, dtype=torch.bfloat16, device="cuda")
+    ws = DeviceWorkspace()
+    ws.bind(0, ad)
+    ws.bind(1, bd)
+    ws.bind(2, out)
+    backend.dispatch(KernelCall.MatMul(MatMulCall(BufferRef(0), BufferRef(1), BufferRef(2), m, k, n,
+                                                  DTYPE_BF16)), ws)
+    backend.synchronize()
+    got = out[rows].float().cpu().numpy().reshape(-1)
+    a32 = a[rows].float().numpy().reshape(-1).copy()
+    b32 = b.float().numpy().reshape(-1).copy()
+    want = oracle.matmul_ref_f64(a32, b32, len(rows), k, n)
+    return got, want
+
+
+@pytest.mark.parametrize("m,k,n", [(4096, 256, 4096), (8192, 8192, 8192), (2048, 1024, 8192)])
+def test_matmul_large_tiles_sampled_rows(torch_cuda, backend, m, k, n):
+    """The 256x256-tile path: every 256-row tile and every row residue mod 32
+    appears among the sampled rows."""
+    rows = sorted({(t * 256 + (t * 37) % 256) % m for t in range(m // 256)} | set(range(0, 64)))
+    got, want = run_mm_rows(torch_cuda, backend, m, k, n, seed=m + n + k, rows=rows)
+    err = oracle.max_rel_err(got, want)
+    assert err <= 1e-2, f"normalized error {err:.3g}"

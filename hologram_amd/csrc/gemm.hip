@@ -10,6 +10,8 @@
 // are issued before the current slab's MFMAs.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "holo_device.h"
 #include "holo_kernels.h"
 
@@ -309,27 +311,38 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_big_kernel(const uint16_t *_
     // LDS store cycle serves write 8 different 16-byte chunks of one Bt row
     // (rows 8 apart share banks once rows are 16-byte aligned).
     const int bkb = tid & 7, bnb = tid >> 3;
-    const uint16_t *ag = A + uint64_t(m0 + arow) * K + akc;
-    const uint16_t *bg = B + uint64_t(8 * bkb) * N + n0 + 8 * bnb;
-    u32x4 ra[8], rb[8];
-    auto gload = [&](uint32_t k0) {
+    // Buffer loads against a resource re-based at every slab: one VGPR offset
+    // per operand, row strides as scalar offsets, 32-bit offsets for any
+    // matrix size (the launcher keeps 256 rows of A and 64 rows of B below 2 GiB).
+    const uint32_t a_voff = (uint32_t(arow) * K + akc) * 2u;
+    const uint32_t b_voff = (uint32_t(8 * bkb) * N + 8 * bnb) * 2u;
+    // two register sets: set t & 1 stages slab t
+    u32x4 ra[2][8], rb[2][8];
+    auto gload = [&](int set, uint32_t k0) {
+        const auto rsa = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t *>(A + uint64_t(m0) * K + k0), 0, int(512u * K), 0x00020000);
+        const auto rsb = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t *>(B + uint64_t(k0) * N + n0), 0, int(128u * N), 0x00020000);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(ag + uint64_t(32 * i) * K + k0);
+        for (int i = 0; i < 8; ++i)
+            ra[set][i] = __builtin_amdgcn_raw_buffer_load_b128(rsa, a_voff, int(64u * K) * i, 0);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) rb[j] = *reinterpret_cast<const u32x4 *>(bg + uint64_t(k0 + j) * N);
+        for (int j = 0; j < 8; ++j)
+            rb[set][j] = __builtin_amdgcn_raw_buffer_load_b128(rsb, b_voff, int(2u * N) * j, 0);
     };
-    auto lstore = [&](int st) {
+    auto lstore = [&](int st, int set) {
+        const u32x4 *xb = rb[set];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4 *>(&lds[st][0][arow + 32 * i][akc]) = ra[i];
+        for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4 *>(&lds[st][0][arow + 32 * i][akc]) = ra[set][i];
         // transpose the 8x8 block: column c gets (k 0..7) as 4 dwords of k pairs
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
             const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
             u32x4 o;
-            o.x = __builtin_amdgcn_perm(rb[1][c >> 1], rb[0][c >> 1], sel);
-            o.y = __builtin_amdgcn_perm(rb[3][c >> 1], rb[2][c >> 1], sel);
-            o.z = __builtin_amdgcn_perm(rb[5][c >> 1], rb[4][c >> 1], sel);
-            o.w = __builtin_amdgcn_perm(rb[7][c >> 1], rb[6][c >> 1], sel);
+            o.x = __builtin_amdgcn_perm(xb[1][c >> 1], xb[0][c >> 1], sel);
+            o.y = __builtin_amdgcn_perm(xb[3][c >> 1], xb[2][c >> 1], sel);
+            o.z = __builtin_amdgcn_perm(xb[5][c >> 1], xb[4][c >> 1], sel);
+            o.w = __builtin_amdgcn_perm(xb[7][c >> 1], xb[6][c >> 1], sel);
             *reinterpret_cast<u32x4 *>(&lds[st][1][8 * bnb + c][8 * bkb]) = o;
         }
     };
@@ -342,13 +355,21 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_big_kernel(const uint16_t *_
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    // Software pipeline per 64-deep slab s (LDS buffer s & 1), k-steps kk = 0..3:
-    //   start of slab: global loads of slab s+1 into registers
-    //   each kk:       LDS fragments of kk+1 are read before kk's 16 MFMAs issue
-    //   kk == 2:       slab s+1 goes into the other LDS buffer (its last readers
-    //                  passed the previous slab's barrier)
-    //   kk == 3:       barrier, then slab s+1's kk = 0 fragments are read while
-    //                  kk = 3's MFMAs run
+    // Software pipeline per 64-deep slab s (LDS buffer s & 1), k-steps kk = 0..3.
+    // When slab s starts, register set (s+1) & 1 holds slab s+1 and set s & 1
+    // is receiving slab s+2. With one wave per SIMD nothing else fills the MFMA
+    // pipe, so every other instruction is placed in the shadow of a running
+    // MFMA (sched_group_barrier: 0x008 MFMA, 0x100 LDS read, 0x200 LDS write,
+    // 0x020 global read, 0x002 VALU):
+    //   kk = 0, 1: LDS fragments of kk+1, one read between MFMAs
+    //   kk = 2:    fragments of kk = 3, then slab s+1 goes into the other LDS
+    //              buffer (its last readers passed the previous barrier), its
+    //              stores spread over the first 12 MFMAs so the last 4 cover
+    //              their completion
+    //   barrier
+    //   kk = 3:    fragments of slab s+1's kk = 0, and the global loads of slab
+    //              s+3 into the set just stored (two slabs of MFMAs to land),
+    //              between the MFMAs
     bf16x8 af[2][4], bfr[2][4];
     auto fload = [&](int st, int kk, int fb) {
 #pragma unroll
@@ -365,33 +386,92 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_big_kernel(const uint16_t *_
             for (int j = 0; j < 4; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[fb][i], bfr[fb][j], acc[i][j], 0, 0, 0);
     };
+    // one fragment read after each of the first 8 MFMAs
+    auto mix_reads = [] {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    };
 
-    const uint32_t nk = K / kBigK;
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    fload(0, 0, 0);
-    for (uint32_t s = 0; s < nk; ++s) {
+    // One slab. set: (s+1) & 1 as a constant. store: slab s+1 exists (store
+    // it, read its first fragments); load: slab s+3 exists (issue its global
+    // loads). In the main loop all three are constants, so the body is one
+    // basic block, which the interleaving needs.
+    auto slab = [&](uint32_t s, auto set, auto store, auto load) {
+        constexpr int kSet = decltype(set)::value;
         const int cur = s & 1;
-        const bool more = s + 1 < nk;
-        if (more) gload((s + 1) * kBigK);
-        // kk = 0, 1, 2: fragments of the next k-step, then this k-step's MFMAs
         fload(cur, 16, 1);
         mfmas(0);
+        mix_reads();
         __builtin_amdgcn_sched_barrier(0);
         fload(cur, 32, 0);
         mfmas(1);
+        mix_reads();
         __builtin_amdgcn_sched_barrier(0);
         fload(cur, 48, 1);
         mfmas(0);
-        if (more) lstore(cur ^ 1);
+        if (store) {
+            lstore(cur ^ 1, kSet);
+            // 8 reads up front; A stores (plain) after MFMAs 1-4, B stores (4
+            // perms each) after MFMAs 5-12; MFMAs 13-16 cover completion
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+                __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        }
         __builtin_amdgcn_sched_barrier(0);
-        // kk = 3
-        __syncthreads();
-        if (more) fload(cur ^ 1, 0, 0);
+        if (store) {
+            __syncthreads();
+            fload(cur ^ 1, 0, 0);
+        }
         mfmas(1);
+        if (load) {
+            gload(kSet, (s + 3) * kBigK);
+            // 8 fragment reads then 16 global loads, two per MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+        }
         __builtin_amdgcn_sched_barrier(0);
+    };
+    using yes = std::integral_constant<bool, true>;
+    using no = std::integral_constant<bool, false>;
+    using set0 = std::integral_constant<int, 0>;
+    using set1 = std::integral_constant<int, 1>;
+
+    const uint32_t nk = K / kBigK;   // even, >= 4
+    gload(0, 0);
+    gload(1, kBigK);
+    lstore(0, 0);
+    gload(0, 2 * kBigK);
+    __syncthreads();
+    fload(0, 0, 0);
+    uint32_t s = 0;
+    for (; s + 4 < nk; s += 2) {
+        slab(s, set1{}, yes{}, yes{});
+        slab(s + 1, set0{}, yes{}, yes{});
     }
+    // the last four slabs (nk is even and >= 4, so s = nk - 4)
+    slab(s, set1{}, yes{}, yes{});
+    slab(s + 1, set0{}, yes{}, no{});
+    slab(s + 2, set1{}, yes{}, no{});
+    slab(s + 3, set0{}, no{}, no{});
 
     // 32x32 D layout: acc[r] is row 8(r/4) + 4*lg + r%4, column lr. One base
     // pointer per lane; the scheduling barrier keeps each tile's addresses local
@@ -417,8 +497,11 @@ hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint
     const uintptr_t al = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b);
     if (dtype == 7) {
         const bool fast = (al & 15) == 0 && k % BK16 == 0 && n % 8 == 0;
-        // large aligned problems: 256x256 tiles, at least one tile per CU
-        if ((al & 15) == 0 && m % kBigM == 0 && n % kBigN == 0 && k % kBigK == 0 &&
+        // large aligned problems: 256x256 tiles, at least one tile per CU, an
+        // even number (>= 4) of 64-deep slabs, and 256 rows of A / 64 rows of
+        // B within a 32-bit buffer range
+        if ((al & 15) == 0 && m % kBigM == 0 && n % kBigN == 0 && k % (2 * kBigK) == 0 &&
+            k >= 4 * kBigK && k < (1u << 22) && n < (1u << 24) &&
             uint64_t(m / kBigM) * (n / kBigN) >= 256) {
             hipLaunchKernelGGL(gemm_bf16_big_kernel, dim3((m / kBigM) * (n / kBigN)), dim3(256), 0,
                                stream, static_cast<const uint16_t *>(a),

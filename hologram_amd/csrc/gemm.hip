@@ -491,10 +491,17 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_big_kernel(const uint16_t *_
 
 }  // namespace
 
+size_t matmul_scratch_bytes(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype) {
+    return matmul_skinny_scratch_bytes(m, k, n, dtype);
+}
+
 hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint32_t k, uint32_t n,
-                         uint8_t dtype, hipStream_t stream) {
+                         uint8_t dtype, void *scratch, hipStream_t stream) {
     const dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM);
     const uintptr_t al = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b);
+    // few rows: stream B once (16-byte aligned operands, output included)
+    if (((al | reinterpret_cast<uintptr_t>(c)) & 15) == 0 && matmul_skinny_applies(m, k, n, dtype))
+        return launch_matmul_skinny(a, b, c, m, k, n, dtype, scratch, stream);
     if (dtype == 7) {
         const bool fast = (al & 15) == 0 && k % BK16 == 0 && n % 8 == 0;
         // large aligned problems: 256x256 tiles, at least one tile per CU, an

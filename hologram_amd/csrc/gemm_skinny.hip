@@ -1,0 +1,344 @@
+// gemm_skinny.hip — C = A * B for a few rows of A (M <= 64), the decode-shaped
+// MatMul (one token's activations against a weight): B's K*N elements are the
+// whole cost, so the kernels are built to stream B once at HBM rate.
+//
+// Same arithmetic contract as the tiled kernels (matmul_float,
+// crates/hologram-compute/src/cpu/float_kernels.rs:298-399): fp32 accumulate,
+// bf16 results narrowed by truncation (src/cpu/dtype.rs:75-79).
+//
+// Work split. A workgroup owns a strip of columns (128 for bf16, 64 for f32)
+// and a K range of KC rows; its four wavefronts interleave over that range in
+// k steps, each wave issuing all of its steps' B loads up front (about 128 KiB
+// in flight per workgroup). The waves' partial tiles are summed through LDS in
+// a fixed order. With more than one K range the workgroups write fp32 partials
+// [ks][M][N] and a second kernel sums them in ks order, so the result does not
+// depend on scheduling.
+//
+// B operand without LDS. B is row-major, the MFMA B operand wants consecutive
+// k per lane. A lane loads an 8 (k) x 8 (n) bf16 block as eight 16-byte rows
+// and transposes it with byte permutes into eight k-vectors, one per column;
+// MFMA number c then covers columns 8j + c of the strip (j = lane % 16), so the
+// accumulators of one lane hold 8 consecutive columns. f32 does the same with
+// 4 x 4 blocks and 16x16x4 MFMAs, with the k order chosen so the A operand of
+// four MFMAs is one 16-byte load.
+#include <hip/hip_runtime.h>
+
+#include "holo_device.h"
+#include "holo_kernels.h"
+
+namespace holo {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 4;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, int(bytes), 0x00020000);
+}
+
+// Column c (0..7) of an 8x8 bf16 block held as 8 rows of 4 dwords: the 8 k
+// values as 4 dwords of k pairs.
+__device__ __forceinline__ u32x4 column8(const u32x4 *rows, int c) {
+    const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+    u32x4 o;
+    o.x = __builtin_amdgcn_perm(rows[1][c >> 1], rows[0][c >> 1], sel);
+    o.y = __builtin_amdgcn_perm(rows[3][c >> 1], rows[2][c >> 1], sel);
+    o.z = __builtin_amdgcn_perm(rows[5][c >> 1], rows[4][c >> 1], sel);
+    o.w = __builtin_amdgcn_perm(rows[7][c >> 1], rows[6][c >> 1], sel);
+    return o;
+}
+
+// ---------------------------------------------------------------- bf16 ----
+// MT 16-row tiles of A, STEPS 32-deep k steps per wave: KC = 4 * STEPS * 32.
+template <int MT, int STEPS>
+__global__ __launch_bounds__(256) void skinny_bf16_kernel(const uint16_t *__restrict__ A,
+                                                          const uint16_t *__restrict__ B,
+                                                          uint16_t *__restrict__ C,
+                                                          float *__restrict__ P, uint32_t M,
+                                                          uint32_t N, uint32_t K) {
+    constexpr uint32_t KC = kWaves * STEPS * 32;
+    __shared__ f32x4 red[kWaves - 1][MT][8][64];
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, g = lane >> 4, q = lane & 15;
+    const uint32_t n0 = blockIdx.x * 128 + 8 * q;
+    const uint32_t kb0 = blockIdx.y * KC;
+    const uint32_t krows = K - kb0 < KC ? K - kb0 : KC;
+    // This workgroup's rows of B as one buffer range; columns past N are sent
+    // out of range, where buffer loads return zero.
+    const auto rb = rsrc(B + uint64_t(kb0) * N, krows * N * 2u);
+    const auto ra = rsrc(A, M * K * 2u);   // rows >= M read zero
+    const uint32_t bcol = n0 < N ? n0 * 2u : 0x80000000u;
+
+    u32x4 b[STEPS][8], a[STEPS][MT];
+#pragma unroll
+    for (int t = 0; t < STEPS; ++t) {
+        const uint32_t kr = uint32_t(t * kWaves + w) * 32;   // step start within the range
+        if (kr < krows) {
+            const uint32_t vo = bcol + (kr + 8 * g) * N * 2u;
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+                b[t][r] = __builtin_amdgcn_raw_buffer_load_b128(rb, vo, int(N * 2u) * r, 0);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+                a[t][mt] = __builtin_amdgcn_raw_buffer_load_b128(
+                    ra, ((mt * 16 + q) * K + kb0 + kr + 8 * g) * 2u, 0, 0);
+        }
+    }
+    f32x4 acc[MT][8];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[mt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < STEPS; ++t) {
+        if (uint32_t(t * kWaves + w) * 32 < krows) {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const u32x4 o = column8(b[t], c);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    acc[mt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8, a[t][mt]), __builtin_bit_cast(bf16x8, o),
+                        acc[mt][c], 0, 0, 0);
+            }
+        }
+    }
+
+    // waves 1..3 hand their partials to wave 0 (lane-contiguous, conflict-free)
+    if (w > 0) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) red[w - 1][mt][c][lane] = acc[mt][c];
+    }
+    __syncthreads();
+    if (w != 0) return;
+#pragma unroll
+    for (int v = 0; v < kWaves - 1; ++v)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) acc[mt][c] += red[v][mt][c][lane];
+
+    // D layout: acc[mt][c][i] is row mt*16 + 4g + i, column n0 + c
+    if (n0 >= N) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t m = mt * 16 + 4 * g + i;
+            if (m >= M) continue;
+            if (gridDim.y == 1) {
+                u32x4 o;
+#pragma unroll
+                for (int h = 0; h < 4; ++h)
+                    o[h] = (__float_as_uint(acc[mt][2 * h][i]) >> 16) |
+                           (__float_as_uint(acc[mt][2 * h + 1][i]) & 0xffff0000u);
+                *reinterpret_cast<u32x4 *>(C + uint64_t(m) * N + n0) = o;
+            } else {
+                float *p = P + (uint64_t(blockIdx.y) * M + m) * N + n0;
+                *reinterpret_cast<f32x4 *>(p) =
+                    f32x4{acc[mt][0][i], acc[mt][1][i], acc[mt][2][i], acc[mt][3][i]};
+                *reinterpret_cast<f32x4 *>(p + 4) =
+                    f32x4{acc[mt][4][i], acc[mt][5][i], acc[mt][6][i], acc[mt][7][i]};
+            }
+        }
+}
+
+// ----------------------------------------------------------------- f32 ----
+// MT 16-row tiles of A, STEPS 16-deep k steps per wave: KC = 4 * STEPS * 16.
+// Lane (g, q) of a step loads rows kr + 4g + r (r = 0..3), columns 4q..4q+3 of
+// the strip, and A[m][kr + 4g .. kr + 4g + 3]; MFMA (r, c) pairs k-group g with
+// row kr + 4g + r in both operands.
+template <int MT, int STEPS>
+__global__ __launch_bounds__(256) void skinny_f32_kernel(const float *__restrict__ A,
+                                                         const float *__restrict__ B,
+                                                         float *__restrict__ C,
+                                                         float *__restrict__ P, uint32_t M,
+                                                         uint32_t N, uint32_t K) {
+    constexpr uint32_t KC = kWaves * STEPS * 16;
+    __shared__ f32x4 red[kWaves - 1][MT][4][64];
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, g = lane >> 4, q = lane & 15;
+    const uint32_t n0 = blockIdx.x * 64 + 4 * q;
+    const uint32_t kb0 = blockIdx.y * KC;
+    const uint32_t krows = K - kb0 < KC ? K - kb0 : KC;
+    const auto rb = rsrc(B + uint64_t(kb0) * N, krows * N * 4u);
+    const auto ra = rsrc(A, M * K * 4u);
+    const uint32_t bcol = n0 < N ? n0 * 4u : 0x80000000u;
+
+    u32x4 b[STEPS][4], a[STEPS][MT];
+#pragma unroll
+    for (int t = 0; t < STEPS; ++t) {
+        const uint32_t kr = uint32_t(t * kWaves + w) * 16;
+        if (kr < krows) {
+            const uint32_t vo = bcol + (kr + 4 * g) * N * 4u;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                b[t][r] = __builtin_amdgcn_raw_buffer_load_b128(rb, vo, int(N * 4u) * r, 0);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+                a[t][mt] = __builtin_amdgcn_raw_buffer_load_b128(
+                    ra, ((mt * 16 + q) * K + kb0 + kr + 4 * g) * 4u, 0, 0);
+        }
+    }
+    f32x4 acc[MT][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[mt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < STEPS; ++t) {
+        if (uint32_t(t * kWaves + w) * 16 < krows) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+                        acc[mt][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                            __uint_as_float(a[t][mt][r]), __uint_as_float(b[t][r][c]), acc[mt][c],
+                            0, 0, 0);
+        }
+    }
+
+    if (w > 0) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) red[w - 1][mt][c][lane] = acc[mt][c];
+    }
+    __syncthreads();
+    if (w != 0) return;
+#pragma unroll
+    for (int v = 0; v < kWaves - 1; ++v)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[mt][c] += red[v][mt][c][lane];
+
+    if (n0 >= N) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t m = mt * 16 + 4 * g + i;
+            if (m >= M) continue;
+            float *dst = gridDim.y == 1 ? C + uint64_t(m) * N + n0
+                                        : P + (uint64_t(blockIdx.y) * M + m) * N + n0;
+            *reinterpret_cast<f32x4 *>(dst) =
+                f32x4{acc[mt][0][i], acc[mt][1][i], acc[mt][2][i], acc[mt][3][i]};
+        }
+}
+
+// Sum of the ks partials in ks order; 4 consecutive outputs per thread.
+template <bool kBf16>
+__global__ __launch_bounds__(256) void skinny_reduce_kernel(const float *__restrict__ P,
+                                                            void *__restrict__ C, uint32_t M,
+                                                            uint32_t N, uint32_t KS) {
+    const uint64_t quads = uint64_t(M) * N / 4;
+    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= quads) return;
+    const uint64_t plane = uint64_t(M) * N;
+    const f32x4 *p = reinterpret_cast<const f32x4 *>(P + 4 * i);
+    const uint64_t step = plane / 4;
+    f32x4 s = p[0];
+    uint32_t ks = 1;
+    for (; ks + 4 <= KS; ks += 4) {   // four loads in flight, added in ks order
+        const f32x4 v0 = p[ks * step], v1 = p[(ks + 1) * step], v2 = p[(ks + 2) * step],
+                    v3 = p[(ks + 3) * step];
+        s += v0;
+        s += v1;
+        s += v2;
+        s += v3;
+    }
+    for (; ks < KS; ++ks) s += p[ks * step];
+    if (kBf16) {
+        uint2 o;
+        o.x = (__float_as_uint(s[0]) >> 16) | (__float_as_uint(s[1]) & 0xffff0000u);
+        o.y = (__float_as_uint(s[2]) >> 16) | (__float_as_uint(s[3]) & 0xffff0000u);
+        reinterpret_cast<uint2 *>(C)[i] = o;
+    } else {
+        reinterpret_cast<f32x4 *>(C)[i] = s;
+    }
+}
+
+struct SkinnyPlan {
+    int mt = 0, steps = 0;
+    uint32_t kc = 0, ks = 0, strips = 0;
+};
+
+// mt = 0: the skinny kernels do not apply.
+SkinnyPlan plan(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype) {
+    SkinnyPlan p;
+    if (m == 0 || m > 64 || k == 0 || n == 0) return p;
+    const bool bf16 = dtype == 7;
+    if (dtype != 7 && dtype != 8) return p;
+    const uint32_t es = bf16 ? 2 : 4;
+    if (bf16 ? (n % 8 != 0 || k % 32 != 0) : (n % 4 != 0 || k % 16 != 0)) return p;
+    p.mt = m <= 16 ? 1 : m <= 32 ? 2 : 4;
+    p.steps = bf16 ? (p.mt == 4 ? 2 : 4) : (p.mt == 4 ? 4 : 8);
+    p.kc = kWaves * p.steps * (bf16 ? 32 : 16);
+    // 32-bit buffer ranges: all of A, and KC rows of B (plus the out-of-range
+    // column offset 2^31 on top of a row offset)
+    if (uint64_t(m) * k * es >= (1ull << 31) || uint64_t(p.kc) * n * es >= (1ull << 31)) {
+        p.mt = 0;
+        return p;
+    }
+    p.ks = (k + p.kc - 1) / p.kc;
+    p.strips = (n + (bf16 ? 127 : 63)) / (bf16 ? 128 : 64);
+    if (p.ks > 65535 || p.strips > (1u << 31)) p.mt = 0;
+    return p;
+}
+
+}  // namespace
+
+size_t matmul_skinny_scratch_bytes(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype) {
+    const SkinnyPlan p = plan(m, k, n, dtype);
+    if (p.mt == 0 || p.ks <= 1) return 0;
+    return size_t(p.ks) * m * n * 4;
+}
+
+bool matmul_skinny_applies(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype) {
+    return plan(m, k, n, dtype).mt != 0;
+}
+
+hipError_t launch_matmul_skinny(const void *a, const void *b, void *c, uint32_t m, uint32_t k,
+                                uint32_t n, uint8_t dtype, void *scratch, hipStream_t stream) {
+    const SkinnyPlan p = plan(m, k, n, dtype);
+    if (p.mt == 0 || (p.ks > 1 && scratch == nullptr)) return hipErrorInvalidValue;
+    const dim3 grid(p.strips, p.ks), block(256);
+    float *P = static_cast<float *>(scratch);
+    if (dtype == 7) {
+        const auto *A = static_cast<const uint16_t *>(a);
+        const auto *B = static_cast<const uint16_t *>(b);
+        auto *C = static_cast<uint16_t *>(c);
+        switch (p.mt) {
+            case 1: hipLaunchKernelGGL((skinny_bf16_kernel<1, 4>), grid, block, 0, stream, A, B, C, P, m, n, k); break;
+            case 2: hipLaunchKernelGGL((skinny_bf16_kernel<2, 4>), grid, block, 0, stream, A, B, C, P, m, n, k); break;
+            default: hipLaunchKernelGGL((skinny_bf16_kernel<4, 2>), grid, block, 0, stream, A, B, C, P, m, n, k); break;
+        }
+    } else {
+        const auto *A = static_cast<const float *>(a);
+        const auto *B = static_cast<const float *>(b);
+        auto *C = static_cast<float *>(c);
+        switch (p.mt) {
+            case 1: hipLaunchKernelGGL((skinny_f32_kernel<1, 8>), grid, block, 0, stream, A, B, C, P, m, n, k); break;
+            case 2: hipLaunchKernelGGL((skinny_f32_kernel<2, 8>), grid, block, 0, stream, A, B, C, P, m, n, k); break;
+            default: hipLaunchKernelGGL((skinny_f32_kernel<4, 4>), grid, block, 0, stream, A, B, C, P, m, n, k); break;
+        }
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || p.ks <= 1) return e;
+    const uint64_t quads = uint64_t(m) * n / 4;
+    const dim3 rgrid(unsigned((quads + 255) / 256));
+    if (dtype == 7)
+        hipLaunchKernelGGL(skinny_reduce_kernel<true>, rgrid, block, 0, stream, P, c, m, n, p.ks);
+    else
+        hipLaunchKernelGGL(skinny_reduce_kernel<false>, rgrid, block, 0, stream, P, c, m, n, p.ks);
+    return hipGetLastError();
+}
+
+}  // namespace holo

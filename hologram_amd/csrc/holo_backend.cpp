@@ -48,7 +48,7 @@ struct holo_backend {
     hipStream_t stream = nullptr;
     std::map<uint32_t, Range> slots;
     uint16_t *lut_dev[5][2] = {};       // [act][0 = f16, 1 = bf16], uploaded once
-    void *scratch = nullptr;            // split-K partials of decode attention
+    void *scratch = nullptr;            // split-K partials (decode attention, few-row MatMul)
     size_t scratch_bytes = 0;
 };
 
@@ -203,6 +203,22 @@ int do_unary(holo_backend *be, const SlotTable &st, uint32_t tag, const holo_una
                     op);
 }
 
+// The backend's split-K scratch grows to the largest request; the old buffer
+// is released only after the stream has drained (kernels may still read it).
+int ensure_scratch(holo_backend *be, size_t bytes, const char *op) {
+    if (bytes <= be->scratch_bytes) return HOLO_OK;
+    if (be->scratch) {
+        (void)hipStreamSynchronize(be->stream);
+        (void)hipFree(be->scratch);
+        be->scratch = nullptr;
+        be->scratch_bytes = 0;
+    }
+    if (hipMalloc(&be->scratch, bytes) != hipSuccess)
+        return fail(HOLO_ERR_INIT, std::string(op) + ": scratch allocation failed");
+    be->scratch_bytes = bytes;
+    return HOLO_OK;
+}
+
 // ------------------------------------------------------------- MatMul ----
 // matmul_float (src/cpu/float_kernels.rs:298-399).
 int do_matmul(holo_backend *be, const SlotTable &st, const holo_matmul_call &c) {
@@ -225,8 +241,9 @@ int do_matmul(holo_backend *be, const SlotTable &st, const holo_matmul_call &c) 
     if ((uint64_t(c.m) + 127) / 128 > 65535)
         return fail(HOLO_ERR_UNSUPPORTED_OP, "matmul: m above 8388480");
     if (!be) return HOLO_OK;
+    HOLO_TRY(ensure_scratch(be, holo::matmul_scratch_bytes(c.m, c.k, c.n, c.dtype), op));
     return launched(holo::launch_matmul(rv[0].base, rv[1].base, out.base, c.m, c.k, c.n, c.dtype,
-                                        be->stream),
+                                        be->scratch, be->stream),
                     op);
 }
 
@@ -372,19 +389,8 @@ int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attentio
         memcpy(&sm, &c.scale_bits, 4);
         scale = sm > 0.0f ? 1.0f / sm : dflt;
     }
-    const size_t need_scratch =
-        holo::attn_i8_scratch_bytes(c.batch, c.heads, hkv, c.bucket_rows, c.head_dim);
-    if (need_scratch > be->scratch_bytes) {
-        if (be->scratch) {
-            (void)hipStreamSynchronize(be->stream);
-            (void)hipFree(be->scratch);
-            be->scratch = nullptr;
-            be->scratch_bytes = 0;
-        }
-        if (hipMalloc(&be->scratch, need_scratch) != hipSuccess)
-            return fail(HOLO_ERR_INIT, "decode_attention_i8: scratch allocation failed");
-        be->scratch_bytes = need_scratch;
-    }
+    HOLO_TRY(ensure_scratch(
+        be, holo::attn_i8_scratch_bytes(c.batch, c.heads, hkv, c.bucket_rows, c.head_dim), op));
     holo::AttnI8Args a;
     a.q = rv[0].base;
     a.kq = reinterpret_cast<const int8_t *>(rv[1].base);

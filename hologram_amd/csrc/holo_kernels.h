@@ -47,8 +47,18 @@ bool attn_i8_supported(uint32_t H, uint32_t Hkv, uint32_t D, uint32_t bucket);
 hipError_t launch_attn_i8(const AttnI8Args &a, void *scratch, hipStream_t stream);
 
 // gemm.hip — C = A*B row-major, fp32 accumulation. dtype f32 or bf16 (bf16
-// result narrowed by truncation).
+// result narrowed by truncation). `scratch` holds split-K partials of the
+// few-row path, matmul_scratch_bytes() bytes (0: none needed). Calls sharing
+// one scratch must not overlap.
+size_t matmul_scratch_bytes(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype);
 hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint32_t k,
-                         uint32_t n, uint8_t dtype, hipStream_t stream);
+                         uint32_t n, uint8_t dtype, void *scratch, hipStream_t stream);
+
+// gemm_skinny.hip — the few-row (m <= 64) path that launch_matmul takes when
+// it applies (16-byte aligned operands required by the caller).
+bool matmul_skinny_applies(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype);
+size_t matmul_skinny_scratch_bytes(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype);
+hipError_t launch_matmul_skinny(const void *a, const void *b, void *c, uint32_t m, uint32_t k,
+                                uint32_t n, uint8_t dtype, void *scratch, hipStream_t stream);
 
 }  // namespace holo

@@ -105,3 +105,88 @@ def test_matmul_large_tiles_sampled_rows(torch_cuda, backend, m, k, n):
     got, want = run_mm_rows(torch_cuda, backend, m, k, n, seed=m + n + k, rows=rows)
     err = oracle.max_rel_err(got, want)
     assert err <= 1e-2, f"normalized error {err:.3g}"
+
+
+SKINNY = [(1, 4096, 4096), (7, 96, 136), (16, 512, 256), (16, 544, 264), (17, 1024, 512),
+          (33, 2048, 384), (64, 4096, 1024), (5, 48, 68)]
+
+
+def run_mm_guarded(torch, backend, m, k, n, dtype, a, b):
+    """MatMul into an output slot followed by 256 guard bytes; returns (C, guard)."""
+    es = 2 if dtype == DTYPE_BF16 else 4
+    out = torch.full((m * n * es + 256,), 0xAB, dtype=torch.uint8, device="cuda")
+    ws = DeviceWorkspace()
+    ws.bind(0, to_dev(torch, a))
+    ws.bind(1, to_dev(torch, b))
+    ws.bind(2, out)
+    backend.dispatch(KernelCall.MatMul(MatMulCall(BufferRef(0), BufferRef(1),
+                                                  BufferRef(2, 0, m * n * es), m, k, n, dtype)), ws)
+    backend.synchronize()
+    raw = out.cpu().numpy()
+    body = raw[:m * n * es]
+    if dtype == DTYPE_BF16:
+        got = (body.view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+    else:
+        got = body.view(np.float32).copy()
+    return got, raw[m * n * es:]
+
+
+def inputs(m, k, n, dtype, seed):
+    rng = np.random.default_rng(seed)
+    a = (rng.standard_normal(m * k) / np.sqrt(k)).astype(np.float32)
+    b = (rng.standard_normal(k * n) / np.sqrt(k)).astype(np.float32)
+    if dtype == DTYPE_BF16:
+        ab = (a.view(np.uint32) >> 16).astype(np.uint16)
+        bb = (b.view(np.uint32) >> 16).astype(np.uint16)
+        return ab, bb, (ab.astype(np.uint32) << 16).view(np.float32), \
+            (bb.astype(np.uint32) << 16).view(np.float32)
+    return a, b, a, b
+
+
+@pytest.mark.parametrize("dtype,tol", [(DTYPE_F32, 1e-5), (DTYPE_BF16, 1e-2)])
+@pytest.mark.parametrize("m,k,n", SKINNY)
+def test_matmul_skinny(torch_cuda, backend, m, k, n, dtype, tol):
+    """The few-row path (m <= 64): 1, 2 and 4 row tiles, partial column strips,
+    one K range (direct store) and several (partials + ordered sum); nothing is
+    written past the output."""
+    da, db, a, b = inputs(m, k, n, dtype, seed=m * 31 + k + n)
+    got, guard = run_mm_guarded(torch_cuda, backend, m, k, n, dtype, da, db)
+    assert (guard == 0xAB).all()
+    err = oracle.max_rel_err(got, oracle.matmul_ref_f64(a, b, m, k, n))
+    assert err <= tol, f"normalized error {err:.3g}"
+
+
+@pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_BF16])
+def test_matmul_skinny_nonfinite_row_isolated(torch_cuda, backend, dtype):
+    """An Inf in one row of A makes that row non-finite (B has no zeros) and
+    leaves every other row exact to tolerance; rows past m inside the last
+    16-row tile are computed but never stored."""
+    m, k, n = 7, 1024, 256
+    da, db, a, b = inputs(m, k, n, dtype, seed=5)
+    if dtype == DTYPE_BF16:
+        da = da.copy()
+        da[3 * k + 17] = 0x7F80
+    else:
+        da = da.copy()
+        da[3 * k + 17] = np.inf
+    a = a.copy()
+    a[3 * k + 17] = np.inf
+    got, guard = run_mm_guarded(torch_cuda, backend, m, k, n, dtype, da, db)
+    assert (guard == 0xAB).all()
+    got = got.reshape(m, n)
+    assert not np.isfinite(got[3]).any()
+    keep = [r for r in range(m) if r != 3]
+    want = oracle.matmul_ref_f64(a.reshape(m, k)[keep].reshape(-1).copy(), b, len(keep), k, n)
+    assert oracle.max_rel_err(got[keep].reshape(-1).copy(), want) <= (1e-2 if dtype == DTYPE_BF16 else 1e-5)
+
+
+def test_matmul_skinny_deterministic_and_scratch_growth(torch_cuda, backend):
+    """Split-K partials are summed in a fixed order: repeated calls agree
+    bitwise, also after the scratch has grown for a larger call in between."""
+    m, k, n = 16, 2048, 512
+    da, db, _, _ = inputs(m, k, n, DTYPE_BF16, seed=9)
+    first, _ = run_mm_guarded(torch_cuda, backend, m, k, n, DTYPE_BF16, da, db)
+    ea, eb, _, _ = inputs(64, 8192, 1024, DTYPE_F32, seed=10)   # larger scratch
+    run_mm_guarded(torch_cuda, backend, 64, 8192, 1024, DTYPE_F32, ea, eb)
+    again, _ = run_mm_guarded(torch_cuda, backend, m, k, n, DTYPE_BF16, da, db)
+    assert first.view(np.uint32).tolist() == again.view(np.uint32).tolist()

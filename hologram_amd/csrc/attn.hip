@@ -8,25 +8,31 @@
 // dequantized rows (kernels.rs:270). Softmax is fp32 (exp2 of log2e-scaled
 // scores, online); no key with j >= L_b contributes.
 //
-// Split-K flash decoding on MFMA:
-//   attn_mfma_kernel   grid (chunks, Hkv, B), 4 wavefronts. A workgroup owns a
-//                      (b, kh, kChunk-key) chunk and all G <= 16 query heads of
-//                      the group, so each K/V byte is read from HBM once. Each
-//                      wavefront takes every 4th 32-key block of the chunk:
+// Work split (balanced form, the default): the planes' keys, in 128-key quads,
+// are laid end to end and cut into as many equal shares as the GPU holds
+// workgroups at once, so a ragged batch (lengths 512..32768) runs as a single
+// round with every workgroup streaming the same number of bytes. A share may
+// end inside a plane or span several; each (plane, share) segment leaves a
+// partial (m, l, O[D]) per head unless it is the whole plane, and
+// attn_merge_kernel merges a plane's partials in a fixed order. The quad
+// offsets are scanned from `lens` on the device, so a decode step never waits
+// on the host. Batches beyond the scan's LDS use the grid form: one workgroup
+// per 2048-key chunk of each plane, merged by attn_combine_kernel.
+//
+// Inside a segment (attn_segment), four wavefronts own all G <= 16 query heads
+// of the group, so each K/V byte is read from HBM once. Each wavefront takes
+// every 4th 32-key block:
 //     S^T[32 keys x 16 heads] = K . Q^T   v_mfma_i32_16x16x64_i8 on the raw K
 //                                         bytes; Q as exact int8 hi/lo halves
 //     online softmax over the block       fp32, per head = per lane column
-//     O^T[D x 16] += V^T . P^T            the same MFMA; P^T is exactly the
-//                                         lane's own 8 scores, V^T is gathered
-//                                         byte-transposed from 8 key rows
-//   The four wavefront states merge in LDS into one partial (m, l, O[D]) per
-//   head; a plane with a single chunk writes its output rows directly.
-//   Chunks starting at or beyond L_b exit at once.
-//   attn_combine_kernel grid (Hkv, B): merges the chunk partials of a plane and
-//   writes the G output rows: bf16 (truncated, as the reference narrows) or
-//   f32. (The kernel boundary makes every partial visible across the XCDs'
-//   separate L2s; a same-kernel merge would need agent-scope fences per
-//   workgroup, which write back and invalidate L2.)
+//     O^T[D x 16] += V^T . P^T            v_mfma_f32_16x16x32_f16; P^T is
+//                                         exactly the lane's own 8 scores, V^T
+//                                         is gathered byte-transposed from 8
+//                                         key rows
+// and the four wavefront states merge in LDS. (Merging across workgroups is a
+// second kernel: the kernel boundary makes every partial visible across the
+// XCDs' separate L2s; a same-kernel merge would need agent-scope fences per
+// workgroup, which write back and invalidate L2.)
 //
 // Exactness: Q is scaled by a power of two per head so its largest |q| sits in
 // [2^13, 2^14), rounded to an integer q_s (relative error <= 2^-14 of the
@@ -41,6 +47,9 @@
 
 #include <math.h>
 #include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
 
 #include "holo_device.h"
 #include "holo_kernels.h"
@@ -51,11 +60,11 @@ namespace {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kMaxChunks = 256; // chunks per plane (bucket_rows <= chunk * kMaxChunks)
 constexpr int kWps = 3;  // wavefronts per SIMD the registers are budgeted for
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBlock = 32;     // keys per wavefront step
+constexpr uint32_t kQuad = kWaves * kBlock;   // keys per pass of the four wavefronts
 constexpr float kLog2e = 1.4426950408889634f;
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -84,46 +93,46 @@ __device__ __forceinline__ f16x8 words_to_f16(uint32_t w0, uint32_t w1, uint32_t
     return __builtin_bit_cast(f16x8, m) - (f16x8)(_Float16)1152.0f;
 }
 
+// A value every lane holds alike, moved to a scalar register.
+__device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, int(bytes), 0x00020000);
 }
 
-// D: head_dim (64 or 128); kF32Q: q/out are f32 (else bf16). G (query heads per
-// kv head) is <= 16 at run time. Registers are budgeted for three wavefronts per
-// SIMD (measured best: more waves spill, fewer leave the loads too thin).
+
+// The exact zero rows of plane (b, kh): no visible key (pinned_semantics.rs).
+template <bool kF32Q>
+__device__ __forceinline__ void zero_rows(void *out, uint32_t b, uint32_t kh, uint32_t H,
+                                          uint32_t G, uint32_t D, uint32_t tid, uint32_t nthreads) {
+    for (uint32_t idx = tid; idx < G * D; idx += nthreads) {
+        const uint64_t oi = (uint64_t(b) * H + kh * G) * D + idx;
+        if constexpr (kF32Q)
+            static_cast<float *>(out)[oi] = 0.0f;
+        else
+            static_cast<uint16_t *>(out)[oi] = 0;
+    }
+}
+
+// One wavefront group's share of a plane: keys [c0, c1) of plane (b, kh) with
+// c0 a multiple of 128 and c0 < c1 <= L_b, for all G query heads of the group.
+// `single`: the range is the whole plane, so the merged state is the answer and
+// goes to `out`; otherwise it is a partial (m, l, O[D]) per head at `dst`.
+// b, kh, c0, c1 and single must be uniform over the workgroup; every wavefront
+// of the workgroup calls this together (it synchronises through LDS).
 template <int D, bool kF32Q>
-__global__ __launch_bounds__(kThreads, kWps) void attn_mfma_kernel(
+__device__ __forceinline__ void attn_segment(
     const void *__restrict__ q, const int8_t *__restrict__ kq, const int8_t *__restrict__ vq,
-    const float *__restrict__ ks, const float *__restrict__ vs, const uint32_t *__restrict__ lens,
-    float *__restrict__ part, void *__restrict__ out, uint32_t H, uint32_t Hkv, uint32_t G,
-    uint32_t bucket, uint32_t kChunk, uint32_t nchunks, float log2e_over_scale) {
+    const float *__restrict__ ks, const float *__restrict__ vs, float *__restrict__ dst,
+    void *__restrict__ out, uint32_t b, uint32_t kh, uint32_t c0, uint32_t c1, bool single,
+    uint32_t H, uint32_t Hkv, uint32_t G, uint32_t bucket, float log2e_over_scale,
+    float (&red_m)[kWaves][16], float (&red_l)[kWaves][16], float (&red_o)[kWaves][16][D],
+    float4 (&blk_sc)[kWaves][16]) {
     constexpr int KB = D / 4;          // K bytes per lane per key row (QK k-slots)
     constexpr int NKS = D / 64;        // i8 MFMA k-steps (64 dims each)
     constexpr int NDB = D / 16;        // 16-row dim blocks of O^T
     constexpr int VW = NDB / 4;        // V u32 words per lane per key row
-
-    __shared__ float red_m[kWaves][16], red_l[kWaves][16];
-    __shared__ float red_o[kWaves][16][D];
-    __shared__ float4 blk_sc[kWaves][16];   // the current block's 32 k- and 32 v-scales
-
-    const uint32_t b = blockIdx.z, kh = blockIdx.y, chunk = blockIdx.x;
-    uint32_t L = lens[b];
-    if (L > bucket) L = bucket;
-    const uint32_t c0 = chunk * kChunk;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    if (c0 >= L) {
-        if (L == 0 && chunk == 0) {       // no visible key: the exact zero rows
-            for (uint32_t idx = tid; idx < G * D; idx += kThreads) {
-                const uint64_t oi = (uint64_t(b) * H + kh * G) * D + idx;
-                if constexpr (kF32Q)
-                    static_cast<float *>(out)[oi] = 0.0f;
-                else
-                    static_cast<uint16_t *>(out)[oi] = 0;
-            }
-        }
-        return;
-    }
-    const uint32_t c1 = L - c0 < kChunk ? L : c0 + kChunk;
     const int r = lane & 15, g = lane >> 4;
     // the wavefront index is uniform: keep block offsets in scalar registers
     const int wv = __builtin_amdgcn_readfirstlane(wave);
@@ -354,9 +363,7 @@ __global__ __launch_bounds__(kThreads, kWps) void attn_mfma_kernel(
             red_o[wave][r][NDB * (4 * g + i) + mb] = acc_o[mb][i] * v_rescale;
     __syncthreads();
 
-    // One chunk: the merged state is the answer. Several: write this chunk's partial.
-    const uint32_t nch = (L + kChunk - 1) / kChunk;
-    float *dst = part + (plane * nchunks + chunk) * G * (D + 2);
+    // The whole plane: the merged state is the answer. Otherwise write the partial.
     for (uint32_t idx = tid; idx < G * D; idx += kThreads) {
         const uint32_t h = idx / D, d = idx % D;
         float m = -INFINITY;
@@ -369,7 +376,7 @@ __global__ __launch_bounds__(kThreads, kWps) void attn_mfma_kernel(
             o = fmaf(red_o[w][h][d], sc, o);
             l = fmaf(red_l[w][h], sc, l);
         }
-        if (nch == 1) {
+        if (single) {
             const uint64_t oi = (uint64_t(b) * H + kh * G + h) * D + d;
             if constexpr (kF32Q)
                 static_cast<float *>(out)[oi] = o / l;
@@ -383,41 +390,175 @@ __global__ __launch_bounds__(kThreads, kWps) void attn_mfma_kernel(
             dst[h * (D + 2) + 1] = l;
         }
     }
+    __syncthreads();   // the caller may reuse red_* and blk_sc next
 }
 
-// Merge the chunk partials of one (b, kh) plane (only planes with more than one
-// chunk; single-chunk planes were written directly): 256 threads, the
-// per-(chunk, head) weights first, then each (head, dim) output as one
-// weighted sum whose loads are issued eight at a time.
+// Grid form for very large batches: grid (chunks, Hkv, B), one workgroup per
+// kChunk-key chunk of a plane; chunks at or beyond L_b exit at once, and chunk
+// 0 of a plane with no visible key writes the exact zero rows. Partial of
+// (plane, chunk) at index plane * nchunks + chunk.
 template <int D, bool kF32Q>
-__global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restrict__ part,
-                                                          const uint32_t *__restrict__ lens,
-                                                          void *__restrict__ out, uint32_t H,
-                                                          uint32_t Hkv, uint32_t G,
-                                                          uint32_t bucket, uint32_t kChunk,
-                                                          uint32_t nchunks) {
-    __shared__ float wgt[kMaxChunks][16];
-    __shared__ float inv_l[16];
-    const uint32_t kh = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+__global__ __launch_bounds__(kThreads, kWps) void attn_chunk_kernel(
+    const void *__restrict__ q, const int8_t *__restrict__ kq, const int8_t *__restrict__ vq,
+    const float *__restrict__ ks, const float *__restrict__ vs, const uint32_t *__restrict__ lens,
+    float *__restrict__ part, void *__restrict__ out, uint32_t H, uint32_t Hkv, uint32_t G,
+    uint32_t bucket, uint32_t kChunk, uint32_t nchunks, float log2e_over_scale) {
+    __shared__ float red_m[kWaves][16], red_l[kWaves][16];
+    __shared__ float red_o[kWaves][16][D];
+    __shared__ float4 blk_sc[kWaves][16];
+    const uint32_t b = blockIdx.z, kh = blockIdx.y, chunk = blockIdx.x;
     uint32_t L = lens[b];
     if (L > bucket) L = bucket;
-    const uint32_t nch = (L + kChunk - 1) / kChunk;
-    if (nch <= 1) return;
+    const uint32_t c0 = chunk * kChunk;
+    if (c0 >= L) {
+        if (L == 0 && chunk == 0) zero_rows<kF32Q>(out, b, kh, H, G, D, threadIdx.x, kThreads);
+        return;
+    }
+    const uint32_t c1 = L - c0 < kChunk ? L : c0 + kChunk;
     const uint64_t plane = uint64_t(b) * Hkv + kh;
-    const float *src = part + plane * nchunks * G * (D + 2);
+    float *dst = part + (plane * nchunks + chunk) * G * (D + 2);
+    attn_segment<D, kF32Q>(q, kq, vq, ks, vs, dst, out, b, kh, c0, c1, L <= kChunk, H, Hkv, G,
+                           bucket, log2e_over_scale, red_m, red_l, red_o, blk_sc);
+}
+
+// Balanced form: the planes' 128-key quads laid end to end, plane (b, kh) in
+// (b, kh) order, and cut into `P` equal shares, one per workgroup (P is the
+// number of workgroups the GPU holds at once, so the whole batch is one round
+// with no tail). Each workgroup first scans ceil(L_b / 128) into quad offsets
+// (in LDS; workgroup 0 also stores them for the merge), then walks the planes
+// its share touches. Segment (plane p, workgroup w) has partial index p + w,
+// which is unique because along the quad line either p or w grows at every
+// segment boundary; a plane's partials are contiguous. Shares are at least
+// kMinQuads quads, so a small batch uses fewer workgroups.
+constexpr uint32_t kScanMax = 1024;   // sequences the balanced form scans in LDS
+constexpr uint32_t kMinQuads = 4;
+constexpr uint32_t kMaxSplit = 1024;  // workgroups of the balanced form
+
+__device__ __forceinline__ uint32_t split_count(uint64_t quads, uint32_t P) {
+    const uint64_t cap = (quads + kMinQuads - 1) / kMinQuads;
+    return uint32_t(cap < P ? (cap ? cap : 1) : P);
+}
+
+template <int D, bool kF32Q>
+__global__ __launch_bounds__(kThreads, kWps) void attn_split_kernel(
+    const void *__restrict__ q, const int8_t *__restrict__ kq, const int8_t *__restrict__ vq,
+    const float *__restrict__ ks, const float *__restrict__ vs, const uint32_t *__restrict__ lens,
+    float *__restrict__ part, uint32_t *__restrict__ qoff_out, void *__restrict__ out, uint32_t B,
+    uint32_t H, uint32_t Hkv, uint32_t G, uint32_t bucket, uint32_t P, float log2e_over_scale) {
+    __shared__ float red_m[kWaves][16], red_l[kWaves][16];
+    __shared__ float red_o[kWaves][16][D];
+    __shared__ float4 blk_sc[kWaves][16];
+    __shared__ uint32_t qoff[kScanMax + 1];
+    __shared__ uint32_t wsum[kWaves];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    // quads of sequence i = ceil(min(lens[i], bucket) / 128); each thread owns
+    // four consecutive sequences, then a workgroup-wide exclusive scan
+    uint32_t nq[4], t = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const uint32_t i = 4 * tid + u;
+        uint32_t L = i < B ? lens[i] : 0u;
+        L = L > bucket ? bucket : L;
+        nq[u] = (L + kQuad - 1) / kQuad;
+        t += nq[u];
+    }
+    uint32_t incl = t;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t v = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += v;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    uint32_t ex = incl - t, total = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        ex += w < wave ? wsum[w] : 0u;
+        total += wsum[w];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const uint32_t i = 4 * tid + u;
+        if (i < B) qoff[i] = ex;
+        ex += nq[u];
+    }
+    if (tid == 0) qoff[B] = total;
+    __syncthreads();
+    if (blockIdx.x == 0)
+        for (uint32_t i = tid; i <= B; i += kThreads) qoff_out[i] = qoff[i];
+
+    // Everything below is uniform: keep it in scalar registers (the segment's
+    // inner loop needs the vector registers).
+    const uint32_t tot = uni(total);
+    const uint64_t qt = uint64_t(Hkv) * tot;
+    const uint32_t Pe = split_count(qt, P);
+    const uint32_t w = blockIdx.x;
+    if (w >= Pe) return;
+    uint64_t x = uint64_t(w) * qt / Pe;
+    const uint64_t x1 = uint64_t(w + 1) * qt / Pe;
+    if (x >= x1) return;
+    // the sequence holding quad x: the largest b with Hkv * qoff[b] <= x
+    uint32_t lo = 0, hi = B;
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (uint64_t(Hkv) * uni(qoff[mid]) <= x) lo = mid; else hi = mid;
+    }
+    uint32_t b = lo;
+    uint32_t q0 = uni(qoff[b]), q1 = uni(qoff[b + 1]);
+    uint32_t kh = uint32_t((x - uint64_t(Hkv) * q0) / (q1 - q0));
+    while (x < x1) {
+        const uint32_t nqb = q1 - q0;
+        const uint64_t ps = uint64_t(Hkv) * q0 + uint64_t(kh) * nqb, pe = ps + nqb;
+        const uint64_t se = x1 < pe ? x1 : pe;
+        uint32_t L = lens[b];
+        L = L > bucket ? bucket : L;
+        const uint32_t c0 = uint32_t(x - ps) * kQuad;
+        const uint32_t c1e = uint32_t(se - ps) * kQuad;
+        const uint32_t c1 = c1e < L ? c1e : L;
+        const bool single = x == ps && se == pe;
+        const uint64_t p = uint64_t(b) * Hkv + kh;
+        float *dst = part + (p + w) * G * (D + 2);
+        attn_segment<D, kF32Q>(q, kq, vq, ks, vs, dst, out, b, kh, c0, c1, single, H, Hkv, G,
+                               bucket, log2e_over_scale, red_m, red_l, red_o, blk_sc);
+        x = se;
+        if (++kh == Hkv) {
+            kh = 0;
+            do {
+                ++b;
+                q0 = q1;
+                q1 = b < B ? uni(qoff[b + 1]) : q0;
+            } while (b < B && q1 == q0);
+        }
+    }
+}
+
+// Merge `nseg` consecutive partials (m, l, O[D]) per head at `src` into the G
+// output rows of plane (b, kh): 256 threads, the per-(segment, head) weights
+// first, then each (head, dim) output as one weighted sum whose loads are
+// issued eight at a time. nseg <= kMaxSeg.
+constexpr uint32_t kMaxSeg = 1024;
+
+template <int D, bool kF32Q>
+__device__ __forceinline__ void merge_partials(const float *__restrict__ src, uint32_t nseg,
+                                               void *__restrict__ out, uint32_t b, uint32_t kh,
+                                               uint32_t H, uint32_t G, float (&wgt)[kMaxSeg][16],
+                                               float (&inv_l)[16]) {
+    const uint32_t tid = threadIdx.x;
     const uint64_t cstride = uint64_t(G) * (D + 2);
     // per head: M = max_c m_c; wgt[c] = 2^(m_c - M); 1 / sum_c wgt[c] l_c
     if (tid < 64) {
-        const uint32_t h = tid & 15, c4 = tid >> 4;    // 4 chunk lanes per head
+        const uint32_t h = tid & 15, c4 = tid >> 4;    // 4 segment lanes per head
         float m = -INFINITY;
         if (h < G)
-            for (uint32_t c = c4; c < nch; c += 4) m = fmaxf(m, src[c * cstride + h * (D + 2)]);
+            for (uint32_t c = c4; c < nseg; c += 4) m = fmaxf(m, src[c * cstride + h * (D + 2)]);
         m = fmaxf(m, __shfl_xor(m, 16, 64));
         m = fmaxf(m, __shfl_xor(m, 32, 64));
         float l = 0.0f;
         if (h < G)
-            for (uint32_t c = c4; c < nch; c += 4) {
-                const float w = exp2f(src[c * cstride + h * (D + 2)] - m);
+            for (uint32_t c = c4; c < nseg; c += 4) {
+                const float mc = src[c * cstride + h * (D + 2)];
+                const float w = mc == -INFINITY ? 0.0f : exp2f(mc - m);
                 wgt[c][h] = w;
                 l = fmaf(src[c * cstride + h * (D + 2) + 1], w, l);
             }
@@ -430,16 +571,16 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restri
         const uint32_t h = idx / D, d = idx % D;
         const float *ph = src + h * (D + 2) + 2 + d;
         float o = 0.0f;
-        for (uint32_t c0 = 0; c0 < nch; c0 += 8) {
+        for (uint32_t c0 = 0; c0 < nseg; c0 += 8) {
             float v[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                const uint32_t c = c0 + u < nch ? c0 + u : nch - 1;
+                const uint32_t c = c0 + u < nseg ? c0 + u : nseg - 1;
                 v[u] = ph[c * cstride];
             }
 #pragma unroll
             for (int u = 0; u < 8; ++u)
-                if (c0 + u < nch) o = fmaf(v[u], wgt[c0 + u][h], o);
+                if (c0 + u < nseg) o = fmaf(v[u], wgt[c0 + u][h], o);
         }
         const float res = o * inv_l[h];
         const uint64_t oi = (uint64_t(b) * H + kh * G + h) * D + d;
@@ -450,16 +591,62 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restri
     }
 }
 
-// Keys per workgroup: a multiple of the 128 keys one pass of the four
-// wavefronts covers. HOLO_ATTN_CHUNK overrides it (tuning sweeps).
+// Merge for the grid form: grid (Hkv, B); planes of one chunk were written directly.
+template <int D, bool kF32Q>
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restrict__ part,
+                                                          const uint32_t *__restrict__ lens,
+                                                          void *__restrict__ out, uint32_t H,
+                                                          uint32_t Hkv, uint32_t G,
+                                                          uint32_t bucket, uint32_t kChunk,
+                                                          uint32_t nchunks) {
+    __shared__ float wgt[kMaxSeg][16];
+    __shared__ float inv_l[16];
+    const uint32_t kh = blockIdx.x, b = blockIdx.y;
+    uint32_t L = lens[b];
+    if (L > bucket) L = bucket;
+    const uint32_t nch = (L + kChunk - 1) / kChunk;
+    if (nch <= 1) return;
+    const uint64_t plane = uint64_t(b) * Hkv + kh;
+    merge_partials<D, kF32Q>(part + plane * nchunks * G * (D + 2), nch, out, b, kh, H, G, wgt,
+                             inv_l);
+}
+
+// Merge for the balanced form: grid (Hkv, B). A plane with no visible key gets
+// the exact zero rows; a plane inside one workgroup's share was written
+// directly; otherwise its partials p + wa .. p + wb are merged.
+template <int D, bool kF32Q>
+__global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict__ part,
+                                                        const uint32_t *__restrict__ qoff,
+                                                        const uint32_t *__restrict__ lens,
+                                                        void *__restrict__ out, uint32_t B,
+                                                        uint32_t H, uint32_t Hkv, uint32_t G,
+                                                        uint32_t bucket, uint32_t P) {
+    __shared__ float wgt[kMaxSeg][16];
+    __shared__ float inv_l[16];
+    const uint32_t kh = blockIdx.x, b = blockIdx.y;
+    const uint32_t L = lens[b];
+    if (L == 0 || bucket == 0) {
+        zero_rows<kF32Q>(out, b, kh, H, G, D, threadIdx.x, 256);
+        return;
+    }
+    const uint64_t qt = uint64_t(Hkv) * qoff[B];
+    const uint32_t Pe = split_count(qt, P);
+    const uint32_t nqb = qoff[b + 1] - qoff[b];
+    const uint64_t ps = uint64_t(Hkv) * qoff[b] + uint64_t(kh) * nqb, pe = ps + nqb;
+    // workgroup holding quad x: ((x + 1) * Pe - 1) / qt
+    const uint32_t wa = uint32_t(((ps + 1) * Pe - 1) / qt);
+    const uint32_t wb = uint32_t((pe * Pe - 1) / qt);
+    if (wa == wb) return;
+    const uint64_t p = uint64_t(b) * Hkv + kh;
+    merge_partials<D, kF32Q>(part + (p + wa) * G * (D + 2), wb - wa + 1, out, b, kh, H, G, wgt,
+                             inv_l);
+}
+
+// Keys per workgroup of the grid form: a multiple of the 128 keys one pass of
+// the four wavefronts covers.
 uint32_t chunk_keys(uint32_t bucket) {
-    static const uint32_t forced = [] {
-        const char *e = getenv("HOLO_ATTN_CHUNK");
-        const long v = e ? strtol(e, nullptr, 10) : 0;
-        return v >= 128 && v % 128 == 0 ? uint32_t(v) : 0u;
-    }();
-    uint32_t c = forced ? forced : 2048;
-    while ((bucket + c - 1) / c > uint32_t(kMaxChunks)) c *= 2;
+    uint32_t c = 2048;
+    while ((bucket + c - 1) / c > kMaxSeg) c *= 2;
     return c;
 }
 
@@ -468,38 +655,98 @@ uint32_t chunks_of(uint32_t bucket) {
     return (bucket + c - 1) / c;
 }
 
-template <int D>
-hipError_t run(const AttnI8Args &a, void *scratch, hipStream_t stream) {
-    const uint32_t ck = chunk_keys(a.bucket);
-    const uint32_t nch = chunks_of(a.bucket);
+int cu_count() {
+    static const int cus = [] {
+        int dev = 0, c = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
+            c = 256;
+        return c;
+    }();
+    return cus;
+}
+
+// Workgroups of the balanced form: as many as the GPU runs at once (CUs x
+// resident workgroups per CU of this kernel), at most kMaxSplit.
+template <int D, bool kF32Q>
+uint32_t split_wgs() {
+    static const uint32_t n = [] {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &per_cu, reinterpret_cast<const void *>(&attn_split_kernel<D, kF32Q>), kThreads, 0) !=
+                hipSuccess || per_cu <= 0)
+            per_cu = 1;
+        const uint64_t v = uint64_t(per_cu) * cu_count();
+        return uint32_t(v < kMaxSplit ? v : kMaxSplit);
+    }();
+    return n;
+}
+
+// HOLO_ATTN_FORM=grid forces the grid form (tuning and tests); the default
+// takes the balanced form whenever the batch fits its LDS scan.
+bool use_split(uint32_t B) {
+    static const bool grid_forced = [] {
+        const char *e = getenv("HOLO_ATTN_FORM");
+        return e && strcmp(e, "grid") == 0;
+    }();
+    return !grid_forced && B <= kScanMax;
+}
+
+// scratch: partials first, then (balanced form) the B + 1 quad offsets
+size_t split_part_floats(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t D, uint32_t P) {
+    return (size_t(B) * Hkv + P) * (H / Hkv) * (D + 2);
+}
+
+template <int D, bool kF32Q>
+hipError_t run_t(const AttnI8Args &a, void *scratch, hipStream_t stream) {
     const uint32_t G = a.H / a.Hkv;
     float *part = static_cast<float *>(scratch);
-    const dim3 grid(nch, a.Hkv, a.B);
     const float mul = kLog2e / a.score_scale;
-    if (a.dtype == 8)
-        hipLaunchKernelGGL((attn_mfma_kernel<D, true>), grid, dim3(kThreads), 0,
-                           stream, a.q, a.kq, a.vq, a.ks, a.vs, a.lens, part, a.out, a.H, a.Hkv, G,
-                           a.bucket, ck, nch, mul);
-    else
-        hipLaunchKernelGGL((attn_mfma_kernel<D, false>), grid, dim3(kThreads), 0,
-                           stream, a.q, a.kq, a.vq, a.ks, a.vs, a.lens, part, a.out, a.H, a.Hkv, G,
-                           a.bucket, ck, nch, mul);
+    if (use_split(a.B)) {
+        const uint32_t P = split_wgs<D, kF32Q>();
+        uint32_t *qoff = reinterpret_cast<uint32_t *>(part + split_part_floats(a.B, a.H, a.Hkv, D, P));
+        hipLaunchKernelGGL((attn_split_kernel<D, kF32Q>), dim3(P), dim3(kThreads), 0, stream, a.q,
+                           a.kq, a.vq, a.ks, a.vs, a.lens, part, qoff, a.out, a.B, a.H, a.Hkv, G,
+                           a.bucket, P, mul);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL((attn_merge_kernel<D, kF32Q>), dim3(a.Hkv, a.B), dim3(256), 0, stream,
+                           part, qoff, a.lens, a.out, a.B, a.H, a.Hkv, G, a.bucket, P);
+        return hipGetLastError();
+    }
+    const uint32_t ck = chunk_keys(a.bucket);
+    const uint32_t nch = chunks_of(a.bucket);
+    hipLaunchKernelGGL((attn_chunk_kernel<D, kF32Q>), dim3(nch, a.Hkv, a.B), dim3(kThreads), 0,
+                       stream, a.q, a.kq, a.vq, a.ks, a.vs, a.lens, part, a.out, a.H, a.Hkv, G,
+                       a.bucket, ck, nch, mul);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || nch == 1) return e;
-    if (a.dtype == 8)
-        hipLaunchKernelGGL((attn_combine_kernel<D, true>), dim3(a.Hkv, a.B), dim3(256), 0, stream,
-                           part, a.lens, a.out, a.H, a.Hkv, G, a.bucket, ck, nch);
-    else
-        hipLaunchKernelGGL((attn_combine_kernel<D, false>), dim3(a.Hkv, a.B), dim3(256), 0, stream,
-                           part, a.lens, a.out, a.H, a.Hkv, G, a.bucket, ck, nch);
+    hipLaunchKernelGGL((attn_combine_kernel<D, kF32Q>), dim3(a.Hkv, a.B), dim3(256), 0, stream,
+                       part, a.lens, a.out, a.H, a.Hkv, G, a.bucket, ck, nch);
     return hipGetLastError();
+}
+
+template <int D>
+hipError_t run(const AttnI8Args &a, void *scratch, hipStream_t stream) {
+    return a.dtype == 8 ? run_t<D, true>(a, scratch, stream) : run_t<D, false>(a, scratch, stream);
+}
+
+template <int D, bool kF32Q>
+size_t scratch_t(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t bucket) {
+    if (use_split(B))
+        return split_part_floats(B, H, Hkv, D, split_wgs<D, kF32Q>()) * sizeof(float) +
+               size_t(B + 1) * sizeof(uint32_t);
+    return size_t(B) * H * chunks_of(bucket) * (D + 2) * sizeof(float);
 }
 
 }  // namespace
 
 size_t attn_i8_scratch_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t bucket, uint32_t D) {
-    (void)Hkv;
-    return size_t(B) * H * chunks_of(bucket) * (D + 2) * sizeof(float);
+    // the larger of the bf16 and f32 instantiations' needs (their occupancy may differ)
+    size_t n = 0;
+    if (D == 128) n = std::max(scratch_t<128, false>(B, H, Hkv, bucket), scratch_t<128, true>(B, H, Hkv, bucket));
+    if (D == 64) n = std::max(scratch_t<64, false>(B, H, Hkv, bucket), scratch_t<64, true>(B, H, Hkv, bucket));
+    return n;
 }
 
 bool attn_i8_supported(uint32_t H, uint32_t Hkv, uint32_t D, uint32_t bucket) {

@@ -104,9 +104,9 @@ def test_refusals(torch_cuda, backend):
 
 
 def test_repeat_calls_are_bitwise_identical(torch_cuda, backend):
-    """The split-K merge order is fixed (chunks merged in index order), and each
-    call leaves the per-plane tickets at zero: back-to-back calls, and a call on
-    a different batch shape in between, give identical bits."""
+    """The split-K merge order is fixed (a plane's partials merged in index
+    order): back-to-back calls, and a call on a different batch shape in
+    between (which reuses the scratch), give identical bits."""
     B, H, Hkv, D, bucket = 4, 16, 4, 128, 5000
     rng = np.random.default_rng(9)
     kq, ks = make_cache(rng, B, Hkv, bucket, D)
@@ -128,3 +128,30 @@ def test_repeat_calls_are_bitwise_identical(torch_cuda, backend):
         if i == 1:   # a differently shaped call in between reuses the scratch
             run_case(torch_cuda, backend, 2, 8, 8, 64, 3000, [2999, 1500], DTYPE_F32, seed=3)
     assert np.array_equal(runs[0], runs[1]) and np.array_equal(runs[1], runs[2])
+
+
+def test_shares_cross_planes(torch_cuda, backend):
+    """Lengths that make the balanced split cut planes at odd places: single-key
+    planes, a plane of exactly one 128-key quad, zero-length sequences between
+    long ones, and lengths beyond the bucket."""
+    lens = [3000, 0, 1, 128, 129, 0, 0, 2047, 4096, 5000, 7, 0]
+    B, H, Hkv, D, bucket = len(lens), 16, 4, 128, 4096
+    got, want, _ = run_case(torch_cuda, backend, B, H, Hkv, D, bucket, lens, DTYPE_F32, seed=21)
+    for b in range(B):
+        if lens[b] == 0:
+            assert np.all(got[b] == 0), f"sequence {b} must be exact zeros"
+        else:
+            assert norm_err(got[b], want[b]) <= TOL, f"sequence {b} (len {lens[b]})"
+
+
+def test_large_batch_grid_form(torch_cuda, backend):
+    """More sequences than the balanced form scans in LDS (1024): the grid form."""
+    B, H, Hkv, D, bucket = 1030, 4, 2, 64, 96
+    rng = np.random.default_rng(5)
+    lens = rng.integers(0, 120, size=B)
+    got, want, _ = run_case(torch_cuda, backend, B, H, Hkv, D, bucket, lens, DTYPE_BF16, seed=6)
+    for b in range(B):
+        if lens[b] == 0:
+            assert np.all(got[b] == 0)
+        else:
+            assert norm_err(got[b], want[b]) <= TOL, f"sequence {b} (len {lens[b]})"

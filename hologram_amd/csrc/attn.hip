@@ -114,24 +114,46 @@ __device__ __forceinline__ void zero_rows(void *out, uint32_t b, uint32_t kh, ui
     }
 }
 
-// One wavefront group's share of a plane: keys [c0, c1) of plane (b, kh) with
+// LDS of one workgroup's segment: the wavefront merge and the super-block
+// scale buffers. k-scales are stored pre-multiplied by log2(e)/scale.
+constexpr uint32_t kSuper = 4 * kQuad;   // keys per scale super-block (512)
+
+template <int D>
+struct SegLds {
+    float red_m[kWaves][16], red_l[kWaves][16];
+    float red_o[kWaves][16][D];
+    float sk[2][kSuper], sv[2][kSuper];
+    float svmax[2][2];
+    i32x4 qop[2][D / 64][64];   // Q int8 hi/lo MFMA operands, per lane of a wavefront
+    float smul[16];             // 2^-qe per head
+};
+
+// One workgroup's share of a plane: keys [c0, c1) of plane (b, kh) with
 // c0 a multiple of 128 and c0 < c1 <= L_b, for all G query heads of the group.
 // `single`: the range is the whole plane, so the merged state is the answer and
 // goes to `out`; otherwise it is a partial (m, l, O[D]) per head at `dst`.
 // b, kh, c0, c1 and single must be uniform over the workgroup; every wavefront
 // of the workgroup calls this together (it synchronises through LDS).
+//
+// Per 512-key super-block the workgroup loads the k- and v-scales in one
+// 16-byte load per thread (one load ahead, staged through registers into a
+// double buffer in LDS), so the scales travel as large requests rather than
+// one 128-byte line per block and stream; invisible keys get scale 0. The
+// super-block's largest v-scale sets ve, shared by the four wavefronts:
+// P' = p * vscale / 2^ve <= 1 is fed to the f16 MFMA, and the softmax state is
+// kept in units of 2^-ve (p' = exp2(s - m - ve), l' = sum p').
 template <int D, bool kF32Q>
 __device__ __forceinline__ void attn_segment(
     const void *__restrict__ q, const int8_t *__restrict__ kq, const int8_t *__restrict__ vq,
     const float *__restrict__ ks, const float *__restrict__ vs, float *__restrict__ dst,
     void *__restrict__ out, uint32_t b, uint32_t kh, uint32_t c0, uint32_t c1, bool single,
     uint32_t H, uint32_t Hkv, uint32_t G, uint32_t bucket, float log2e_over_scale,
-    float (&red_m)[kWaves][16], float (&red_l)[kWaves][16], float (&red_o)[kWaves][16][D],
-    float4 (&blk_sc)[kWaves][16]) {
+    SegLds<D> &lds) {
     constexpr int KB = D / 4;          // K bytes per lane per key row (QK k-slots)
     constexpr int NKS = D / 64;        // i8 MFMA k-steps (64 dims each)
     constexpr int NDB = D / 16;        // 16-row dim blocks of O^T
     constexpr int VW = NDB / 4;        // V u32 words per lane per key row
+    constexpr int kVeMin = -100;       // 2^ve floor: keeps l' = sum p' finite
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int r = lane & 15, g = lane >> 4;
     // the wavefront index is uniform: keep block offsets in scalar registers
@@ -147,43 +169,68 @@ __device__ __forceinline__ void attn_segment(
     // Per-lane byte offsets inside a 32-key block; the block base is a uniform
     // soffset and the per-row parts are instruction immediates. K rows 16mb + r
     // (KB bytes at KB*g); V rows kappa(g, j) = 16(j/4) + 4g + j%4 (NDB bytes at
-    // NDB*r); scales: lane l < 32 takes kscale[l], lane l >= 32 vscale[l - 32].
+    // NDB*r).
     const int koff = r * D + KB * g;
     const int voff = 4 * g * D + NDB * r;
-    const int soff = 4 * lane;
 
     struct Blk {
         u32x4 k[2][NKS];
         uint32_t v[8][VW];
-        float sc;                           // one key or value scale per lane
     };
+    // The per-row constants ride in the scalar offset: only koff and voff stay
+    // in vector registers across the loop.
     auto load = [&](uint32_t blk, Blk &o) {
-        const int kvs = int(blk * D), ss = int(blk * 4);
+        const int kvs = int(blk * D);
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
             for (int s = 0; s < NKS; ++s)
-                o.k[mb][s] = __builtin_amdgcn_raw_buffer_load_b128(rk, koff + 16 * mb * D + 16 * s, kvs, 0);
+                o.k[mb][s] = __builtin_amdgcn_raw_buffer_load_b128(rk, koff, kvs + 16 * mb * D + 16 * s, 0);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int row = (16 * (j >> 2) + (j & 3)) * D;
             if constexpr (VW == 2) {
-                const auto w = __builtin_amdgcn_raw_buffer_load_b64(rv, voff + row, kvs, 0);
+                const auto w = __builtin_amdgcn_raw_buffer_load_b64(rv, voff, kvs + row, 0);
                 o.v[j][0] = w[0];
                 o.v[j][1] = w[1];
             } else {
-                o.v[j][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, voff + row, kvs, 0);
+                o.v[j][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, voff, kvs + row, 0);
             }
         }
-        o.sc = __uint_as_float(lane < 32 ? __builtin_amdgcn_raw_buffer_load_b32(rks, soff, ss, 0)
-                                         : __builtin_amdgcn_raw_buffer_load_b32(rvs, soff - 128, ss, 0));
+    };
+    // Super-block scales: wavefronts 0-1 load the 512 k-scales, 2-3 the
+    // v-scales, four keys per thread.
+    const uint32_t st = uint32_t(tid) & 127u;
+    auto load_sc = [&](uint32_t sb) -> u32x4 {
+        const int so = int((c0 + sb * kSuper) * 4);
+        return wv < 2 ? __builtin_amdgcn_raw_buffer_load_b128(rks, int(16 * st), so, 0)
+                      : __builtin_amdgcn_raw_buffer_load_b128(rvs, int(16 * st), so, 0);
+    };
+    auto store_sc = [&](uint32_t sb, u32x4 v) {
+        const uint32_t key0 = c0 + sb * kSuper + 4 * st;
+        float f[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) f[t] = key0 + t < c1 ? __uint_as_float(v[t]) : 0.0f;
+        if (wv < 2) {
+            *reinterpret_cast<float4 *>(&lds.sk[sb & 1][4 * st]) =
+                float4{f[0] * log2e_over_scale, f[1] * log2e_over_scale,
+                       f[2] * log2e_over_scale, f[3] * log2e_over_scale};
+        } else {
+            *reinterpret_cast<float4 *>(&lds.sv[sb & 1][4 * st]) = float4{f[0], f[1], f[2], f[3]};
+            float m = fmaxf(fmaxf(f[0], f[1]), fmaxf(f[2], f[3]));
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            if (lane == 0) lds.svmax[sb & 1][wv - 2] = m;
+        }
     };
 
-    // Q loads first, then the first block's: the Q set-up below waits only for Q.
-    // Lanes of padding heads (r >= G) read head 0 and zero it.
-    float qv[KB];
-    const bool live = uint32_t(r) < G;
-    {
+    // Wavefront 0 turns Q into the MFMA operands (in LDS, shared by the four
+    // wavefronts); its loads go out first. Lanes of padding heads (r >= G)
+    // read head 0 and zero it.
+    const uint32_t nsb = (c1 - c0 + kSuper - 1) / kSuper;
+    if (wv == 0) {
+        float qv[KB];
+        const bool live = uint32_t(r) < G;
         const uint64_t qi = (uint64_t(b) * H + kh * G + (live ? r : 0)) * D + KB * g;
         if constexpr (kF32Q) {
             const u32x4 *src = reinterpret_cast<const u32x4 *>(static_cast<const float *>(q) + qi);
@@ -210,125 +257,113 @@ __device__ __forceinline__ void attn_segment(
         }
 #pragma unroll
         for (int e = 0; e < KB; ++e) qv[e] = live ? qv[e] : 0.0f;
+        // Q as a 15-bit integer per head, q * 2^qe with max |.| in [2^13, 2^14),
+        // split exactly into int8 halves: q_s = 256 qh + ql, ql in [-128, 127].
+        float qmax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < KB; ++e) qmax = fmaxf(qmax, fabsf(qv[e]));
+        qmax = fmaxf(qmax, __shfl_xor(qmax, 16, 64));
+        qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
+        int qe = 0;
+        if (qmax > 0.0f && qmax <= 3.0e38f) {
+            (void)frexpf(qmax, &qe);          // qmax < 2^qe
+            qe = 14 - qe;
+        }
+#pragma unroll
+        for (int s = 0; s < NKS; ++s) {
+            i32x4 qh, ql;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                uint32_t hw = 0, lw = 0;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int qs = int(rintf(ldexpf(qv[16 * s + 4 * w + t], qe)));
+                    const int hi = (qs + 128) >> 8;
+                    const int lo = qs - hi * 256;
+                    hw |= uint32_t(hi & 0xFF) << (8 * t);
+                    lw |= uint32_t(lo & 0xFF) << (8 * t);
+                }
+                qh[w] = int(hw);
+                ql[w] = int(lw);
+            }
+            lds.qop[0][s][lane] = qh;
+            lds.qop[1][s][lane] = ql;
+        }
+        if (g == 0) lds.smul[r] = ldexpf(1.0f, -qe);   // the k-scales carry log2(e)/scale
     }
-    // Wavefront wv takes every fourth 32-key block of the chunk; one block is
+    u32x4 sreg = load_sc(0);
+    // Wavefront wv takes every fourth 32-key block of the segment; one block is
     // in flight (prefetched into registers) while the previous is computed.
-    constexpr uint32_t kStride = kWaves * kBlock;
     const uint32_t first = c0 + wv * kBlock;
     Blk cur;
     if (first < c1) load(first, cur);
 
-    // Q as a 15-bit integer per head, q * 2^qe with max |.| in [2^13, 2^14),
-    // split exactly into int8 halves: q_s = 256 qh + ql, ql in [-128, 127].
-    float qmax = 0.0f;
-#pragma unroll
-    for (int e = 0; e < KB; ++e) qmax = fmaxf(qmax, fabsf(qv[e]));
-    qmax = fmaxf(qmax, __shfl_xor(qmax, 16, 64));
-    qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
-    int qe = 0;
-    if (qmax > 0.0f && qmax <= 3.0e38f) {
-        (void)frexpf(qmax, &qe);          // qmax < 2^qe
-        qe = 14 - qe;
-    }
-    i32x4 qh[NKS], ql[NKS];
-#pragma unroll
-    for (int s = 0; s < NKS; ++s)
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            uint32_t hw = 0, lw = 0;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int qs = int(rintf(ldexpf(qv[16 * s + 4 * w + t], qe)));
-                const int hi = (qs + 128) >> 8;
-                const int lo = qs - hi * 256;
-                hw |= uint32_t(hi & 0xFF) << (8 * t);
-                lw |= uint32_t(lo & 0xFF) << (8 * t);
-            }
-            qh[s][w] = int(hw);
-            ql[s][w] = int(lw);
-        }
-    const float score_mul = log2e_over_scale * ldexpf(1.0f, -qe);
-
     f32x4 acc_o[NDB];
 #pragma unroll
     for (int i = 0; i < NDB; ++i) acc_o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_run = 0.0f;
-    int ve = -200;                         // 2^ve bounds every vscale seen (unset)
-    float v_unscale = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f, mv = -INFINITY;   // mv = m_run + ve
+    int ve = kVeMin;
 
-    for (uint32_t blk = first; blk < c1; blk += kStride) {
-        const uint32_t nb = blk + kStride;
-        Blk nxt;
-        if (nb < c1) load(nb, nxt);
-        const bool full = blk + kBlock <= c1;
-        // this block's scales through the wavefront's LDS slot: keys 16h + 4g + i
-        reinterpret_cast<float *>(blk_sc[wv])[lane] = cur.sc;
-        __builtin_amdgcn_wave_barrier();
+    store_sc(0, sreg);
+    __syncthreads();
+    const float smul = lds.smul[r];
+
+    // One 32-key block: lane (r, g) holds keys 16mb + 4g + i for head r.
+    // masked: keys at or beyond c1 are invisible (the segment's last block;
+    // wave-uniform, so the masking is a branch the full blocks skip).
+    auto block = [&](bool masked, const Blk &cb, uint32_t blk, const float *skp,
+                     const float *svp) __attribute__((always_inline)) {
         float ksc[8], vsc[8];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const float4 k4 = blk_sc[wv][4 * h + g];
-            const float4 v4 = blk_sc[wv][8 + 4 * h + g];
+            const float4 k4 = *reinterpret_cast<const float4 *>(skp + 16 * h + 4 * g);
+            const float4 v4 = *reinterpret_cast<const float4 *>(svp + 16 * h + 4 * g);
             ksc[4 * h] = k4.x; ksc[4 * h + 1] = k4.y; ksc[4 * h + 2] = k4.z; ksc[4 * h + 3] = k4.w;
             vsc[4 * h] = v4.x; vsc[4 * h + 1] = v4.y; vsc[4 * h + 2] = v4.z; vsc[4 * h + 3] = v4.w;
         }
-        __builtin_amdgcn_wave_barrier();
-
-        // -- S^T = K . Q^T on the int8 MFMA, exact in int32: lane holds keys
-        //    16mb + 4g + i for head r
+        // -- S^T = K . Q^T on the int8 MFMA, exact in int32
         float sc[8];
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) {
             i32x4 ah = {0, 0, 0, 0}, al = {0, 0, 0, 0};
 #pragma unroll
             for (int s = 0; s < NKS; ++s) {
-                const i32x4 kf = __builtin_bit_cast(i32x4, cur.k[mb][s]);
-                ah = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, qh[s], ah, 0, 0, 0);
-                al = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, ql[s], al, 0, 0, 0);
+                const i32x4 kf = __builtin_bit_cast(i32x4, cb.k[mb][s]);
+                ah = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, lds.qop[0][s][lane], ah, 0, 0, 0);
+                al = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, lds.qop[1][s][lane], al, 0, 0, 0);
             }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sc[4 * mb + i] = float(ah[i] * 256 + al[i]);
+            for (int i = 0; i < 4; ++i) sc[4 * mb + i] = (float(ah[i] * 256 + al[i]) * ksc[4 * mb + i]) * smul;
         }
-        float m_blk = -INFINITY, vb = 0.0f;
+        if (masked) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t key = blk + 16 * (j >> 2) + 4 * g + (j & 3);
-            const bool vis = full || key < c1;
-            sc[j] = vis ? (sc[j] * ksc[j]) * score_mul : -INFINITY;
-            m_blk = fmaxf(m_blk, sc[j]);
-            vb = vis ? fmaxf(vb, vsc[j]) : vb;
+            for (int j = 0; j < 8; ++j)
+                if (blk + 16 * (j >> 2) + 4 * g + (j & 3) >= c1) sc[j] = -INFINITY;
         }
-        m_blk = fmaxf(m_blk, __shfl_xor(m_blk, 16, 64));
-        m_blk = fmaxf(m_blk, __shfl_xor(m_blk, 32, 64));
-        vb = fmaxf(vb, __shfl_xor(vb, 16, 64));
-        vb = fmaxf(vb, __shfl_xor(vb, 32, 64));
+        float m_blk = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
+                            fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+        {   // across the four key groups g: lanes r, r+16, r+32, r+48
+            const auto x16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m_blk), __float_as_uint(m_blk), false, false);
+            m_blk = fmaxf(__uint_as_float(x16[0]), __uint_as_float(x16[1]));
+            const auto x32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m_blk), __float_as_uint(m_blk), false, false);
+            m_blk = fmaxf(__uint_as_float(x32[0]), __uint_as_float(x32[1]));
+        }
         if (__any(m_blk > m_run)) {        // rescale only when some head's max grew
             const float m_new = fmaxf(m_run, m_blk);
             const float alpha = exp2f(m_run - m_new);
             m_run = m_new;
+            mv = m_run + float(ve);
             l_run *= alpha;
 #pragma unroll
             for (int i = 0; i < NDB; ++i) acc_o[i] *= alpha;
         }
-        // keep every P' = p * vscale / 2^ve in [0, 1]  (vb is wave-uniform)
-        if (vb > ldexpf(1.0f, ve) && vb <= 3.0e38f) {
-            int ve_new;
-            (void)frexpf(vb, &ve_new);                     // vb < 2^ve_new
-            const float shrink = ldexpf(1.0f, ve - ve_new);
-#pragma unroll
-            for (int i = 0; i < NDB; ++i) acc_o[i] *= shrink;
-            ve = ve_new;
-            v_unscale = ldexpf(1.0f, -ve);
-        }
         f16x8 pf;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float p = exp2f(sc[j] - m_run);           // masked keys: exp2(-inf) = 0
+            const float p = exp2f(sc[j] - mv);   // p * 2^-ve; masked keys: exp2(-inf) = 0
             l_run += p;
-            const float pw = p * (vsc[j] * v_unscale);
-            pf[j] = (_Float16)(p > 0.0f ? pw : 0.0f);       // never 0 * garbage scale
+            pf[j] = (_Float16)(p * vsc[j]);      // invisible keys carry scale 0
         }
-
         // -- O^T += V^T . P^T : dim block mb = 4w + t, row m holds dim NDB*m + mb
 #pragma unroll
         for (int w = 0; w < VW; ++w) {
@@ -336,7 +371,7 @@ __device__ __forceinline__ void attn_segment(
 #pragma unroll
             for (int pr = 0; pr < 4; ++pr) {
                 uint32_t f4[4];
-                pair_dims(cur.v[2 * pr][w] ^ 0x80808080u, cur.v[2 * pr + 1][w] ^ 0x80808080u, f4);
+                pair_dims(cb.v[2 * pr][w] ^ 0x80808080u, cb.v[2 * pr + 1][w] ^ 0x80808080u, f4);
 #pragma unroll
                 for (int t = 0; t < 4; ++t) f[t][pr] = f4[t];
             }
@@ -345,36 +380,71 @@ __device__ __forceinline__ void attn_segment(
                 acc_o[4 * w + t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                     words_to_f16(f[t][0], f[t][1], f[t][2], f[t][3]), pf, acc_o[4 * w + t], 0, 0, 0);
         }
-        cur = nxt;
+    };
+
+    // Every wavefront walks the same 4 * nsb quads (the barriers must match);
+    // its block of a quad past c1 is skipped.
+    for (uint32_t it = 0; it < 4 * nsb; ++it) {
+        const uint32_t sb = it >> 2;
+        if ((it & 3) == 0) {
+            if (sb + 1 < nsb) sreg = load_sc(sb + 1);
+            // 2^ve bounds every v-scale of this super-block (all wavefronts alike)
+            const float vb = fmaxf(lds.svmax[sb & 1][0], lds.svmax[sb & 1][1]);
+            if (vb > ldexpf(1.0f, ve) && vb <= 3.0e38f) {
+                int ve_new;
+                (void)frexpf(vb, &ve_new);                     // vb < 2^ve_new
+                const float shrink = ldexpf(1.0f, ve - ve_new);
+                l_run *= shrink;
+#pragma unroll
+                for (int i = 0; i < NDB; ++i) acc_o[i] *= shrink;
+                ve = ve_new;
+                mv = m_run + float(ve);
+            }
+        }
+        const uint32_t blk = c0 + it * kQuad + wv * kBlock;
+        if (blk < c1) {
+            const uint32_t nb = blk + kQuad;
+            Blk nxt;
+            if (nb < c1) load(nb, nxt);
+            const uint32_t so = (it & 3) * kQuad + wv * kBlock;
+            const float *skp = lds.sk[sb & 1] + so, *svp = lds.sv[sb & 1] + so;
+            block(blk + kBlock > c1, cur, blk, skp, svp);
+            cur = nxt;
+        }
+        if ((it & 3) == 3) {
+            if (sb + 1 < nsb) store_sc(sb + 1, sreg);
+            __syncthreads();
+        }
     }
 
     // ---- wavefront state -> LDS, merge the four wavefronts per head
     l_run += __shfl_xor(l_run, 16, 64);
     l_run += __shfl_xor(l_run, 32, 64);
     if (g == 0) {
-        red_m[wave][r] = m_run;
-        red_l[wave][r] = l_run;
+        lds.red_m[wave][r] = m_run;
+        lds.red_l[wave][r] = l_run;
     }
-    const float v_rescale = ldexpf(1.0f, ve);   // 2^-200 is 0: an idle wave adds nothing
 #pragma unroll
     for (int mb = 0; mb < NDB; ++mb)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            red_o[wave][r][NDB * (4 * g + i) + mb] = acc_o[mb][i] * v_rescale;
+            lds.red_o[wave][r][NDB * (4 * g + i) + mb] = acc_o[mb][i];
     __syncthreads();
 
-    // The whole plane: the merged state is the answer. Otherwise write the partial.
+    // The whole plane: the merged state is the answer (o / l does not depend on
+    // the common 2^ve). Otherwise write the partial, scaled back by 2^ve.
+    const float v_rescale = ldexpf(1.0f, ve);
     for (uint32_t idx = tid; idx < G * D; idx += kThreads) {
         const uint32_t h = idx / D, d = idx % D;
         float m = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) m = fmaxf(m, red_m[w][h]);
+        for (int w = 0; w < kWaves; ++w) m = fmaxf(m, lds.red_m[w][h]);
         float o = 0.0f, l = 0.0f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
-            const float sc = red_m[w][h] == -INFINITY ? 0.0f : exp2f(red_m[w][h] - m);
-            o = fmaf(red_o[w][h][d], sc, o);
-            l = fmaf(red_l[w][h], sc, l);
+            const float sc = lds.red_m[w][h] == -INFINITY ? 0.0f : exp2f(lds.red_m[w][h] - m);
+            o = fmaf(lds.red_o[w][h][d], sc, o);
+            l = fmaf(lds.red_l[w][h], sc, l);
         }
         if (single) {
             const uint64_t oi = (uint64_t(b) * H + kh * G + h) * D + d;
@@ -384,13 +454,13 @@ __device__ __forceinline__ void attn_segment(
                 static_cast<uint16_t *>(out)[oi] = uint16_t(__float_as_uint(o / l) >> 16);
             continue;
         }
-        dst[h * (D + 2) + 2 + d] = o;
+        dst[h * (D + 2) + 2 + d] = o * v_rescale;
         if (d == 0) {
             dst[h * (D + 2)] = m;
-            dst[h * (D + 2) + 1] = l;
+            dst[h * (D + 2) + 1] = l * v_rescale;
         }
     }
-    __syncthreads();   // the caller may reuse red_* and blk_sc next
+    __syncthreads();   // the caller may reuse the LDS next
 }
 
 // Grid form for very large batches: grid (chunks, Hkv, B), one workgroup per
@@ -403,9 +473,7 @@ __global__ __launch_bounds__(kThreads, kWps) void attn_chunk_kernel(
     const float *__restrict__ ks, const float *__restrict__ vs, const uint32_t *__restrict__ lens,
     float *__restrict__ part, void *__restrict__ out, uint32_t H, uint32_t Hkv, uint32_t G,
     uint32_t bucket, uint32_t kChunk, uint32_t nchunks, float log2e_over_scale) {
-    __shared__ float red_m[kWaves][16], red_l[kWaves][16];
-    __shared__ float red_o[kWaves][16][D];
-    __shared__ float4 blk_sc[kWaves][16];
+    __shared__ SegLds<D> lds;
     const uint32_t b = blockIdx.z, kh = blockIdx.y, chunk = blockIdx.x;
     uint32_t L = lens[b];
     if (L > bucket) L = bucket;
@@ -418,7 +486,7 @@ __global__ __launch_bounds__(kThreads, kWps) void attn_chunk_kernel(
     const uint64_t plane = uint64_t(b) * Hkv + kh;
     float *dst = part + (plane * nchunks + chunk) * G * (D + 2);
     attn_segment<D, kF32Q>(q, kq, vq, ks, vs, dst, out, b, kh, c0, c1, L <= kChunk, H, Hkv, G,
-                           bucket, log2e_over_scale, red_m, red_l, red_o, blk_sc);
+                           bucket, log2e_over_scale, lds);
 }
 
 // Balanced form: the planes' 128-key quads laid end to end, plane (b, kh) in
@@ -445,9 +513,7 @@ __global__ __launch_bounds__(kThreads, kWps) void attn_split_kernel(
     const float *__restrict__ ks, const float *__restrict__ vs, const uint32_t *__restrict__ lens,
     float *__restrict__ part, uint32_t *__restrict__ qoff_out, void *__restrict__ out, uint32_t B,
     uint32_t H, uint32_t Hkv, uint32_t G, uint32_t bucket, uint32_t P, float log2e_over_scale) {
-    __shared__ float red_m[kWaves][16], red_l[kWaves][16];
-    __shared__ float red_o[kWaves][16][D];
-    __shared__ float4 blk_sc[kWaves][16];
+    __shared__ SegLds<D> lds;
     __shared__ uint32_t qoff[kScanMax + 1];
     __shared__ uint32_t wsum[kWaves];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -520,7 +586,7 @@ __global__ __launch_bounds__(kThreads, kWps) void attn_split_kernel(
         const uint64_t p = uint64_t(b) * Hkv + kh;
         float *dst = part + (p + w) * G * (D + 2);
         attn_segment<D, kF32Q>(q, kq, vq, ks, vs, dst, out, b, kh, c0, c1, single, H, Hkv, G,
-                               bucket, log2e_over_scale, red_m, red_l, red_o, blk_sc);
+                               bucket, log2e_over_scale, lds);
         x = se;
         if (++kh == Hkv) {
             kh = 0;

@@ -40,8 +40,8 @@
 // dot products are exact. For PV, an int8 v is the f16 1152 + (v ^ 0x80) - 1152
 // built by byte placement under the f16 exponent of 1024 (every integer
 // -128..127 is an exact f16); P' = p * vscale / 2^ve with 2^ve
-// >= every vscale seen so far keeps P' in [0, 1] (ve is tracked online per
-// wavefront and the accumulator rescaled when it grows). MFMA products are
+// >= every vscale seen so far keeps P' in [0, 1] (ve is tracked per 512-key
+// super-block and the accumulator rescaled when it grows). MFMA products are
 // exact and accumulate in fp32.
 #include <hip/hip_runtime.h>
 

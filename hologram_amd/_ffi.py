@@ -28,6 +28,38 @@ class UnaryCallC(ctypes.Structure):
                 ("witt_bits", ctypes.c_uint16), ("dtype", ctypes.c_uint8)]
 
 
+class BinaryCallC(ctypes.Structure):
+    _fields_ = [("a", BufferRefC), ("b", BufferRefC), ("output", BufferRefC),
+                ("element_count", ctypes.c_uint64), ("witt_bits", ctypes.c_uint16),
+                ("dtype", ctypes.c_uint8)]
+
+
+class NormCallC(ctypes.Structure):
+    _fields_ = [("x", BufferRefC), ("gamma", BufferRefC), ("beta", BufferRefC),
+                ("residual", BufferRefC), ("output", BufferRefC), ("batch", ctypes.c_uint32),
+                ("feature", ctypes.c_uint32), ("channels", ctypes.c_uint32),
+                ("num_groups", ctypes.c_uint32), ("epsilon_bits", ctypes.c_uint64),
+                ("dtype", ctypes.c_uint8)]
+
+
+class RopeCallC(ctypes.Structure):
+    _fields_ = [("x", BufferRefC), ("cos", BufferRefC), ("sin", BufferRefC),
+                ("output", BufferRefC), ("head_dim", ctypes.c_uint32),
+                ("element_count", ctypes.c_uint64), ("dtype", ctypes.c_uint8)]
+
+
+class GatherCallC(ctypes.Structure):
+    _fields_ = [("data", BufferRefC), ("indices", BufferRefC), ("output", BufferRefC),
+                ("outer", ctypes.c_uint64), ("axis_dim", ctypes.c_uint64),
+                ("inner", ctypes.c_uint64), ("num_indices", ctypes.c_uint64),
+                ("idx_dtype", ctypes.c_uint8), ("dtype", ctypes.c_uint8)]
+
+
+class ArgMaxCallC(ctypes.Structure):
+    _fields_ = [("input", BufferRefC), ("output", BufferRefC), ("rows", ctypes.c_uint32),
+                ("cols", ctypes.c_uint32), ("dtype", ctypes.c_uint8)]
+
+
 class MatMulCallC(ctypes.Structure):
     _fields_ = [("a", BufferRefC), ("b", BufferRefC), ("output", BufferRefC),
                 ("m", ctypes.c_uint32), ("k", ctypes.c_uint32), ("n", ctypes.c_uint32),
@@ -59,7 +91,9 @@ class DecodeAttentionI8CallC(ctypes.Structure):
 
 
 class CallUnion(ctypes.Union):
-    _fields_ = [("unary", UnaryCallC), ("matmul", MatMulCallC), ("kv_write", KvCacheWriteCallC),
+    _fields_ = [("unary", UnaryCallC), ("binary", BinaryCallC), ("norm", NormCallC),
+                ("rope", RopeCallC), ("gather", GatherCallC), ("argmax", ArgMaxCallC),
+                ("matmul", MatMulCallC), ("kv_write", KvCacheWriteCallC),
                 ("kv_quant_append", KvQuantAppendCallC), ("attn_i8", DecodeAttentionI8CallC)]
 
 
@@ -85,6 +119,27 @@ SIGNATURES = {
                                             ctypes.POINTER(KernelCallC),
                                             ctypes.POINTER(ctypes.c_size_t)]),
     "holo_hip_lut_table": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _P]),
+    "holo_hip_session_load": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.c_size_t,
+                                             ctypes.POINTER(_P)]),
+    "holo_hip_session_close": (ctypes.c_int, [_P]),
+    "holo_hip_session_info": (ctypes.c_int, [_P] + [ctypes.POINTER(ctypes.c_uint32)] * 4),
+    "holo_hip_session_port": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_uint32,
+                                             ctypes.POINTER(ctypes.c_uint32),
+                                             ctypes.POINTER(ctypes.c_uint64),
+                                             ctypes.POINTER(ctypes.c_uint8),
+                                             ctypes.POINTER(ctypes.c_uint64)]),
+    "holo_hip_session_fingerprint": (ctypes.c_int, [_P, ctypes.c_char_p]),
+    "holo_hip_session_bind_input": (ctypes.c_int, [_P, ctypes.c_uint32, _P, ctypes.c_uint64]),
+    "holo_hip_session_write_input": (ctypes.c_int, [_P, ctypes.c_uint32, _P, ctypes.c_uint64]),
+    "holo_hip_session_execute": (ctypes.c_int, [_P]),
+    "holo_hip_session_capture": (ctypes.c_int, [_P]),
+    "holo_hip_session_replay": (ctypes.c_int, [_P]),
+    "holo_hip_session_synchronize": (ctypes.c_int, [_P]),
+    "holo_hip_session_stream": (ctypes.c_int, [_P, ctypes.POINTER(_P)]),
+    "holo_hip_session_output": (ctypes.c_int, [_P, ctypes.c_uint32, ctypes.POINTER(_P),
+                                               ctypes.POINTER(ctypes.c_uint64)]),
+    "holo_hip_session_read_output": (ctypes.c_int, [_P, ctypes.c_uint32, _P, ctypes.c_uint64]),
+    "holo_hip_blake3": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_size_t, ctypes.c_char_p]),
     "holo_hip_last_error_message": (ctypes.c_char_p, []),
 }
 

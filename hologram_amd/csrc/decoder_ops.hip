@@ -1,0 +1,264 @@
+// decoder_ops.hip — the remaining ops of a Llama-style decode step on the
+// device: Add / Mul, RmsNorm, rotary embedding, Gather (embedding rows) and
+// ArgMax (the greedy pick). Each is memory-bound at decode shapes; each keeps
+// the reference's per-element arithmetic (widen to f32, the same IEEE
+// operations in the same order, narrow bf16 by truncation), so Add, Mul, RoPE
+// and Gather are bit-exact with the reference CPU kernels, and RmsNorm differs
+// only by the order of its sum of squares (a tree here, sequential there).
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+
+#include "holo_device.h"
+#include "holo_kernels.h"
+
+namespace holo {
+namespace {
+
+__device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
+__device__ __forceinline__ uint16_t f2bf(float f) { return uint16_t(__float_as_uint(f) >> 16); }
+
+template <bool kBf16>
+__device__ __forceinline__ float ld(const void *p, uint64_t i) {
+    if constexpr (kBf16)
+        return bf2f(static_cast<const uint16_t *>(p)[i]);
+    else
+        return static_cast<const float *>(p)[i];
+}
+
+template <bool kBf16>
+__device__ __forceinline__ void st(void *p, uint64_t i, float v) {
+    if constexpr (kBf16)
+        static_cast<uint16_t *>(p)[i] = f2bf(v);
+    else
+        static_cast<float *>(p)[i] = v;
+}
+
+constexpr int kOpAdd = 0, kOpMul = 1;
+
+template <int kOp>
+__device__ __forceinline__ float bin(float a, float b) {
+    return kOp == kOpAdd ? a + b : a * b;
+}
+
+// Add / Mul: 16-byte vectors (8 bf16 or 4 f32 per lane) when every operand is
+// 16-byte aligned, element tail after; grid-stride.
+template <bool kBf16, int kOp>
+__global__ __launch_bounds__(256) void binary_kernel(const void *__restrict__ a,
+                                                     const void *__restrict__ b,
+                                                     void *__restrict__ out, uint64_t n,
+                                                     uint64_t nvec) {
+    constexpr int E = kBf16 ? 8 : 4;
+    const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
+    const u32x4 *a4 = static_cast<const u32x4 *>(a);
+    const u32x4 *b4 = static_cast<const u32x4 *>(b);
+    u32x4 *o4 = static_cast<u32x4 *>(out);
+    for (uint64_t v = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; v < nvec; v += stride) {
+        const u32x4 x = a4[v], y = b4[v];
+        u32x4 r;
+        if constexpr (kBf16) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float lo = bin<kOp>(__uint_as_float(x[w] << 16), __uint_as_float(y[w] << 16));
+                const float hi = bin<kOp>(__uint_as_float(x[w] & 0xFFFF0000u),
+                                          __uint_as_float(y[w] & 0xFFFF0000u));
+                r[w] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+            }
+        } else {
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+                r[w] = __float_as_uint(bin<kOp>(__uint_as_float(x[w]), __uint_as_float(y[w])));
+        }
+        o4[v] = r;
+    }
+    for (uint64_t i = nvec * E + uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+        st<kBf16>(out, i, bin<kOp>(ld<kBf16>(a, i), ld<kBf16>(b, i)));
+}
+
+// RmsNorm: one workgroup per row. Sum of squares in f32 (tree order), then
+// out = (x * inv_rms) * gamma as the reference evaluates it.
+template <bool kBf16>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const void *__restrict__ x,
+                                                      const void *__restrict__ gamma,
+                                                      void *__restrict__ out, uint32_t feature,
+                                                      float eps) {
+    __shared__ float part[8];
+    const uint64_t row = uint64_t(blockIdx.x) * feature;
+    float ss = 0.0f;
+    for (uint32_t j = threadIdx.x; j < feature; j += 256) {
+        const float v = ld<kBf16>(x, row + j);
+        ss = fmaf(v, v, ss);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float sumsq = part[0] + part[1] + part[2] + part[3];
+    const float inv = 1.0f / sqrtf(sumsq / float(feature) + eps);
+    for (uint32_t j = threadIdx.x; j < feature; j += 256) {
+        float v = ld<kBf16>(x, row + j) * inv;
+        if (gamma) v = v * ld<kBf16>(gamma, j);
+        st<kBf16>(out, row + j, v);
+    }
+}
+
+// Rotary embedding, rotate-half form over heads of head_dim elements.
+template <bool kBf16>
+__global__ __launch_bounds__(256) void rope_kernel(const void *__restrict__ x,
+                                                   const void *__restrict__ cs,
+                                                   const void *__restrict__ sn,
+                                                   void *__restrict__ out, uint32_t head_dim,
+                                                   uint64_t n) {
+    const uint32_t half = head_dim / 2;
+    for (uint64_t e = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; e < n;
+         e += uint64_t(gridDim.x) * blockDim.x) {
+        const uint32_t pos = uint32_t(e % head_dim);
+        const float xe = ld<kBf16>(x, e), ce = ld<kBf16>(cs, e), se = ld<kBf16>(sn, e);
+        float v;
+        if (pos < half)
+            v = xe * ce - ld<kBf16>(x, e + half) * se;
+        else
+            v = xe * ce + ld<kBf16>(x, e - half) * se;
+        st<kBf16>(out, e, v);
+    }
+}
+
+// Gather rows of `row_bytes` (a multiple of 4 when `words`): one workgroup per
+// (outer, index) row. An index outside [-axis_dim, axis_dim) zeroes its row
+// and raises *err.
+template <bool kI64>
+__global__ __launch_bounds__(256) void gather_kernel(const uint8_t *__restrict__ data,
+                                                     const void *__restrict__ idx,
+                                                     uint8_t *__restrict__ out, uint64_t axis_dim,
+                                                     uint64_t num_idx, uint64_t row_bytes,
+                                                     int *__restrict__ err) {
+    const uint64_t o = blockIdx.y, k = blockIdx.x;
+    int64_t i = kI64 ? static_cast<const int64_t *>(idx)[k] : static_cast<const int32_t *>(idx)[k];
+    if (i < 0) i += int64_t(axis_dim);
+    uint8_t *dst = out + (o * num_idx + k) * row_bytes;
+    const bool ok = i >= 0 && uint64_t(i) < axis_dim;
+    if (!ok && threadIdx.x == 0) atomicOr(err, 1);
+    const uint8_t *src = data + (o * axis_dim + (ok ? uint64_t(i) : 0)) * row_bytes;
+    if ((row_bytes & 15) == 0 && ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0) {
+        const u32x4 *s4 = reinterpret_cast<const u32x4 *>(src);
+        u32x4 *d4 = reinterpret_cast<u32x4 *>(dst);
+        for (uint64_t w = threadIdx.x; w < row_bytes / 16; w += 256)
+            d4[w] = ok ? s4[w] : u32x4{0, 0, 0, 0};
+    } else {
+        for (uint64_t w = threadIdx.x; w < row_bytes; w += 256) dst[w] = ok ? src[w] : uint8_t(0);
+    }
+}
+
+// ArgMax per row: one workgroup per row; each thread keeps the first index of
+// its largest value, then a (value, index) reduction that prefers the lower
+// index on equal values. NaN never compares greater.
+template <bool kBf16>
+__global__ __launch_bounds__(256) void argmax_kernel(const void *__restrict__ in,
+                                                     int32_t *__restrict__ out, uint32_t cols) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const uint64_t row = uint64_t(blockIdx.x) * cols;
+    float best = -INFINITY;
+    int bi = -1;
+    for (uint32_t j = threadIdx.x; j < cols; j += 256) {
+        const float v = ld<kBf16>(in, row + j);
+        if (v > best || (bi < 0 && v == best)) {
+            best = v;
+            bi = int(j);
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (oi >= 0 && (bi < 0 || ov > best || (ov == best && oi < bi))) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = best;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w)
+            if (si[w] >= 0 && (bi < 0 || sv[w] > best || (sv[w] == best && si[w] < bi))) {
+                best = sv[w];
+                bi = si[w];
+            }
+        out[blockIdx.x] = bi < 0 ? 0 : bi;
+    }
+}
+
+unsigned grid_for(uint64_t work, unsigned cap = 4096) {
+    const uint64_t g = (work + 255) / 256;
+    return unsigned(g == 0 ? 1 : (g < cap ? g : cap));
+}
+
+}  // namespace
+
+hipError_t launch_binary(int op, const void *a, const void *b, void *out, uint64_t n, bool bf16,
+                         hipStream_t stream) {
+    const bool vec = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+                       reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+    const uint64_t nvec = vec ? n / (bf16 ? 8 : 4) : 0;
+    const unsigned grid = grid_for(nvec ? nvec : n);
+    if (bf16) {
+        if (op == 0)
+            hipLaunchKernelGGL((binary_kernel<true, kOpAdd>), dim3(grid), dim3(256), 0, stream, a, b, out, n, nvec);
+        else
+            hipLaunchKernelGGL((binary_kernel<true, kOpMul>), dim3(grid), dim3(256), 0, stream, a, b, out, n, nvec);
+    } else {
+        if (op == 0)
+            hipLaunchKernelGGL((binary_kernel<false, kOpAdd>), dim3(grid), dim3(256), 0, stream, a, b, out, n, nvec);
+        else
+            hipLaunchKernelGGL((binary_kernel<false, kOpMul>), dim3(grid), dim3(256), 0, stream, a, b, out, n, nvec);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm(const void *x, const void *gamma, void *out, uint32_t batch,
+                          uint32_t feature, float eps, bool bf16, hipStream_t stream) {
+    if (bf16)
+        hipLaunchKernelGGL((rmsnorm_kernel<true>), dim3(batch), dim3(256), 0, stream, x, gamma, out, feature, eps);
+    else
+        hipLaunchKernelGGL((rmsnorm_kernel<false>), dim3(batch), dim3(256), 0, stream, x, gamma, out, feature, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(const void *x, const void *cs, const void *sn, void *out, uint32_t head_dim,
+                       uint64_t n, bool bf16, hipStream_t stream) {
+    const unsigned grid = grid_for(n);
+    if (bf16)
+        hipLaunchKernelGGL((rope_kernel<true>), dim3(grid), dim3(256), 0, stream, x, cs, sn, out, head_dim, n);
+    else
+        hipLaunchKernelGGL((rope_kernel<false>), dim3(grid), dim3(256), 0, stream, x, cs, sn, out, head_dim, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather(const void *data, const void *idx, void *out, uint64_t outer,
+                         uint64_t axis_dim, uint64_t num_idx, uint64_t row_bytes, bool i64,
+                         int *err, hipStream_t stream) {
+    const dim3 grid{unsigned(num_idx), unsigned(outer), 1u};
+    if (i64)
+        hipLaunchKernelGGL((gather_kernel<true>), grid, dim3(256), 0, stream,
+                           static_cast<const uint8_t *>(data), idx, static_cast<uint8_t *>(out),
+                           axis_dim, num_idx, row_bytes, err);
+    else
+        hipLaunchKernelGGL((gather_kernel<false>), grid, dim3(256), 0, stream,
+                           static_cast<const uint8_t *>(data), idx, static_cast<uint8_t *>(out),
+                           axis_dim, num_idx, row_bytes, err);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const void *in, int32_t *out, uint32_t rows, uint32_t cols, bool bf16,
+                         hipStream_t stream) {
+    if (bf16)
+        hipLaunchKernelGGL((argmax_kernel<true>), dim3(rows), dim3(256), 0, stream, in, out, cols);
+    else
+        hipLaunchKernelGGL((argmax_kernel<false>), dim3(rows), dim3(256), 0, stream, in, out, cols);
+    return hipGetLastError();
+}
+
+}  // namespace holo

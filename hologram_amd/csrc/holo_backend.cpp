@@ -14,6 +14,7 @@
 #include <string>
 #include <vector>
 
+#include "holo_internal.h"
 #include "holo_kernels.h"
 
 namespace holo {
@@ -23,6 +24,7 @@ bool build_lut_table(int act, bool f16, uint16_t *t);
 namespace {
 
 thread_local std::string g_last_error;
+const int kZero = 0;
 
 int fail(int code, const std::string &msg) {
     g_last_error = msg;
@@ -50,6 +52,7 @@ struct holo_backend {
     uint16_t *lut_dev[5][2] = {};       // [act][0 = f16, 1 = bf16], uploaded once
     void *scratch = nullptr;            // split-K partials (decode attention, few-row MatMul)
     size_t scratch_bytes = 0;
+    int *dev_err = nullptr;             // device-side refusals (Gather's index range), read at sync
 };
 
 namespace {
@@ -60,8 +63,16 @@ struct SlotTable {
     const holo_backend *be = nullptr;
     const uint64_t *sizes = nullptr;
     uint32_t nsizes = 0;
+    const std::vector<holo::SlotRange> *vec = nullptr;   // a session's slot table
 
     bool lookup(uint32_t slot, uint8_t **ptr, uint64_t *bytes, uint64_t *key) const {
+        if (vec) {
+            if (slot >= vec->size() || !(*vec)[slot].ptr) return false;
+            *ptr = (*vec)[slot].ptr;
+            *bytes = (*vec)[slot].bytes;
+            *key = 0;
+            return true;
+        }
         if (be) {
             auto it = be->slots.find(slot);
             if (it == be->slots.end()) return false;
@@ -255,9 +266,13 @@ int do_kv_write(holo_backend *be, const SlotTable &st, const holo_kv_cache_write
         return fail(HOLO_ERR_UNSUPPORTED_OP, "kv_cache_write: bucket_rows and row_bytes must be >= 1");
     if (c.new_rows > c.bucket_rows)
         return fail(HOLO_ERR_UNSUPPORTED_OP, "kv_cache_write: new_rows exceeds bucket_rows");
-    holo_buffer_ref reads[3] = {c.cache, c.new_rows_buf, c.pos};
-    View rv[3], out;
-    HOLO_TRY(split_borrow(st, reads, rv, 3, c.output, &out, op));
+    // output == cache (same slot and offset): the executor's in-place move
+    // (session.rs:1313-1370) — only the new rows are written.
+    const bool in_place = c.output.slot == c.cache.slot && c.output.offset == c.cache.offset;
+    holo_buffer_ref reads[3] = {c.new_rows_buf, c.pos, c.cache};
+    View rv3[3], out;
+    HOLO_TRY(split_borrow(st, reads, rv3, in_place ? 2 : 3, c.output, &out, op));
+    View rv[3] = {in_place ? out : rv3[2], rv3[0], rv3[1]};
     const uint64_t plane = uint64_t(c.bucket_rows) * c.row_bytes;
     const uint64_t total = plane * c.planes;
     if (rv[0].bytes < total || rv[1].bytes < uint64_t(c.planes) * c.new_rows * c.row_bytes ||
@@ -266,7 +281,7 @@ int do_kv_write(holo_backend *be, const SlotTable &st, const holo_kv_cache_write
                     "kv_cache_write: an operand is shorter than the declared geometry (slot " +
                         std::to_string(c.output.slot) + ")");
     if (!be) return HOLO_OK;
-    HOLO_TRY(launched(holo::launch_copy_bytes(rv[0].base, out.base, total, be->stream), op));
+    if (!in_place) HOLO_TRY(launched(holo::launch_copy_bytes(rv[0].base, out.base, total, be->stream), op));
     if (c.planes == 0 || c.new_rows == 0) return HOLO_OK;
     return launched(holo::launch_kv_place_rows(rv[1].base,
                                                reinterpret_cast<const uint32_t *>(rv[2].base),
@@ -413,6 +428,146 @@ int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attentio
     return launched(holo::launch_attn_i8(a, be->scratch, be->stream), op);
 }
 
+// ------------------------------------------------------- Add / Mul -----
+// binary_float (src/cpu/float_kernels.rs:238-300).
+int do_binary(holo_backend *be, const SlotTable &st, uint32_t tag, const holo_binary_call &c) {
+    const char *op = tag == HOLO_OP_ADD ? "add" : "mul";
+    if (c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F32)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, std::string(op) + ": the device path serves bf16 and f32");
+    if (c.element_count == 0) return HOLO_OK;
+    const uint64_t es = dtype_size(c.dtype), bytes = c.element_count * es;
+    holo_buffer_ref reads[2] = {c.a, c.b};
+    View rv[2], out;
+    HOLO_TRY(split_borrow(st, reads, rv, 2, c.output, &out, op));
+    HOLO_TRY(need(rv[0], bytes, c.a.slot, op, "a"));
+    HOLO_TRY(need(rv[1], bytes, c.b.slot, op, "b"));
+    HOLO_TRY(need(out, bytes, c.output.slot, op, "output"));
+    if (!aligned(rv[0], es) || !aligned(rv[1], es) || !aligned(out, es))
+        return fail(HOLO_ERR_UNSUPPORTED_OP, std::string(op) + ": operands must be element-aligned");
+    if (!be) return HOLO_OK;
+    return launched(holo::launch_binary(tag == HOLO_OP_ADD ? 0 : 1, rv[0].base, rv[1].base, out.base,
+                                        c.element_count, c.dtype == HOLO_DTYPE_BF16, be->stream),
+                    op);
+}
+
+// ------------------------------------------------------------ RmsNorm ----
+// rms_norm_float (src/cpu/float_kernels.rs:1683-1755); epsilon rule :1324-1336.
+int do_rmsnorm(holo_backend *be, const SlotTable &st, const holo_norm_call &c) {
+    const char *op = "rms_norm";
+    if (c.batch == 0 || c.feature == 0) return HOLO_OK;
+    if (c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F32)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "rms_norm: the device path serves bf16 and f32");
+    if (c.residual.slot != HOLO_SLOT_ABSENT || c.channels != 0 || c.num_groups != 0)
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    "rms_norm: residual / grouped forms are not served by the device path");
+    float eps = 1e-9f;
+    if (c.epsilon_bits != 0) {
+        const uint32_t eb = uint32_t(c.epsilon_bits);
+        memcpy(&eps, &eb, 4);
+        if (!(std::isfinite(eps) && eps > 0.0f))
+            return fail(HOLO_ERR_UNSUPPORTED_OP,
+                        "norm epsilon must be a positive finite f32 (0 selects the default)");
+    }
+    const uint64_t es = dtype_size(c.dtype), total = uint64_t(c.batch) * c.feature * es;
+    const bool has_g = c.gamma.slot != HOLO_SLOT_ABSENT;
+    holo_buffer_ref reads[2] = {c.x, c.gamma};
+    View rv[2], out;
+    HOLO_TRY(split_borrow(st, reads, rv, has_g ? 2 : 1, c.output, &out, op));
+    HOLO_TRY(need(rv[0], total, c.x.slot, op, "x"));
+    HOLO_TRY(need(out, total, c.output.slot, op, "output"));
+    // affine_operand (float_kernels.rs:39-44): an empty gamma is the identity
+    const bool use_g = has_g && rv[1].bytes > 0;
+    if (use_g) HOLO_TRY(need(rv[1], uint64_t(c.feature) * es, c.gamma.slot, op, "gamma"));
+    if (!aligned(rv[0], es) || !aligned(out, es) || (use_g && !aligned(rv[1], es)))
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "rms_norm: operands must be element-aligned");
+    if (c.batch > 0x7fffffffu) return fail(HOLO_ERR_UNSUPPORTED_OP, "rms_norm: batch too large");
+    if (!be) return HOLO_OK;
+    return launched(holo::launch_rmsnorm(rv[0].base, use_g ? rv[1].base : nullptr, out.base, c.batch,
+                                         c.feature, eps, c.dtype == HOLO_DTYPE_BF16, be->stream),
+                    op);
+}
+
+// -------------------------------------------------------------- RoPE -----
+// rope_float (src/cpu/float_kernels.rs:3123-3186).
+int do_rope(holo_backend *be, const SlotTable &st, const holo_rope_call &c) {
+    const char *op = "rope";
+    if (c.head_dim == 0 || c.head_dim % 2 != 0 || c.element_count % c.head_dim != 0)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "rope: head_dim must be even and divide the element count");
+    if (c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F32)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "rope: the device path serves bf16 and f32");
+    if (c.element_count == 0) return HOLO_OK;
+    const uint64_t es = dtype_size(c.dtype), bytes = c.element_count * es;
+    holo_buffer_ref reads[3] = {c.x, c.cos, c.sin};
+    View rv[3], out;
+    HOLO_TRY(split_borrow(st, reads, rv, 3, c.output, &out, op));
+    HOLO_TRY(need(rv[0], bytes, c.x.slot, op, "x"));
+    HOLO_TRY(need(rv[1], bytes, c.cos.slot, op, "cos"));
+    HOLO_TRY(need(rv[2], bytes, c.sin.slot, op, "sin"));
+    HOLO_TRY(need(out, bytes, c.output.slot, op, "output"));
+    if (!aligned(rv[0], es) || !aligned(rv[1], es) || !aligned(rv[2], es) || !aligned(out, es))
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "rope: operands must be element-aligned");
+    if (!be) return HOLO_OK;
+    return launched(holo::launch_rope(rv[0].base, rv[1].base, rv[2].base, out.base, c.head_dim,
+                                      c.element_count, c.dtype == HOLO_DTYPE_BF16, be->stream),
+                    op);
+}
+
+// ------------------------------------------------------------ Gather -----
+// gather (src/cpu/kernels.rs:389-447): rows copied byte for byte.
+int do_gather(holo_backend *be, const SlotTable &st, const holo_gather_call &c) {
+    const char *op = "gather";
+    const uint64_t elem = c.dtype == HOLO_DTYPE_I32 ? 4 : c.dtype == HOLO_DTYPE_I64 ? 8
+                        : c.dtype == 1 || c.dtype == HOLO_DTYPE_I8 ? 1 : dtype_size(c.dtype);
+    if (elem == 0)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "gather: sub-byte or unknown element dtype not supported");
+    uint64_t idx_w;
+    if (c.idx_dtype == HOLO_DTYPE_I32)
+        idx_w = 4;
+    else if (c.idx_dtype == HOLO_DTYPE_I64)
+        idx_w = 8;
+    else
+        return fail(HOLO_ERR_SLOT_OUT_OF_RANGE,
+                    "gather: index dtype must be i32 or i64 (slot " + std::to_string(c.indices.slot) + ")");
+    const uint64_t row = c.inner * elem;
+    holo_buffer_ref reads[2] = {c.data, c.indices};
+    View rv[2], out;
+    HOLO_TRY(split_borrow(st, reads, rv, 2, c.output, &out, op));
+    if (rv[0].bytes < c.outer * c.axis_dim * row || rv[1].bytes < c.num_indices * idx_w ||
+        out.bytes < c.outer * c.num_indices * row)
+        return fail(HOLO_ERR_SLOT_OUT_OF_RANGE,
+                    "gather: an operand is shorter than the declared geometry (slot " +
+                        std::to_string(c.output.slot) + ")");
+    if (!aligned(rv[1], idx_w)) return fail(HOLO_ERR_UNSUPPORTED_OP, "gather: indices must be aligned");
+    if (c.outer == 0 || c.num_indices == 0 || row == 0) return HOLO_OK;
+    if (c.outer > 65535 || c.num_indices > 0x7fffffffull)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "gather: outer above 65535 or too many indices");
+    if (!be) return HOLO_OK;
+    return launched(holo::launch_gather(rv[0].base, rv[1].base, out.base, c.outer, c.axis_dim,
+                                        c.num_indices, row, c.idx_dtype == HOLO_DTYPE_I64,
+                                        be->dev_err, be->stream),
+                    op);
+}
+
+// ------------------------------------------------------------ ArgMax -----
+int do_argmax(holo_backend *be, const SlotTable &st, const holo_argmax_call &c) {
+    const char *op = "argmax";
+    if (c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F32)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "argmax: input must be bf16 or f32");
+    if (c.rows == 0) return HOLO_OK;
+    const uint64_t es = dtype_size(c.dtype);
+    View in, out;
+    HOLO_TRY(split_borrow(st, &c.input, &in, 1, c.output, &out, op));
+    HOLO_TRY(need(in, uint64_t(c.rows) * c.cols * es, c.input.slot, op, "input"));
+    HOLO_TRY(need(out, uint64_t(c.rows) * 4, c.output.slot, op, "output"));
+    if (!aligned(in, es) || !aligned(out, 4))
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "argmax: operands must be element-aligned");
+    if (c.rows > 0x7fffffffu) return fail(HOLO_ERR_UNSUPPORTED_OP, "argmax: too many rows");
+    if (!be) return HOLO_OK;
+    return launched(holo::launch_argmax(in.base, reinterpret_cast<int32_t *>(out.base), c.rows,
+                                        c.cols, c.dtype == HOLO_DTYPE_BF16, be->stream),
+                    op);
+}
+
 int dispatch_impl(holo_backend *be, const SlotTable &st, const holo_kernel_call *call) {
     if (!call) return fail(HOLO_ERR_DISPATCH, "dispatch: null call");
     switch (call->tag) {
@@ -421,6 +576,12 @@ int dispatch_impl(holo_backend *be, const SlotTable &st, const holo_kernel_call 
         case HOLO_OP_GELU:
         case HOLO_OP_SILU:
         case HOLO_OP_EXP: return do_unary(be, st, call->tag, call->u.unary);
+        case HOLO_OP_ADD:
+        case HOLO_OP_MUL: return do_binary(be, st, call->tag, call->u.binary);
+        case HOLO_OP_RMS_NORM: return do_rmsnorm(be, st, call->u.norm);
+        case HOLO_OP_ROTARY: return do_rope(be, st, call->u.rope);
+        case HOLO_OP_GATHER: return do_gather(be, st, call->u.gather);
+        case HOLO_OP_ARGMAX: return do_argmax(be, st, call->u.argmax);
         case HOLO_OP_MATMUL: return do_matmul(be, st, call->u.matmul);
         case HOLO_OP_KV_CACHE_WRITE: return do_kv_write(be, st, call->u.kv_write);
         case HOLO_OP_KV_QUANT_APPEND: return do_kv_quant(be, st, call->u.kv_quant_append);
@@ -474,6 +635,65 @@ int decode_impl(const uint8_t *wire, size_t len, holo_kernel_call *out, size_t *
             c.output = r.buf();
             c.element_count = r.get<uint64_t>();
             c.witt_bits = r.get<uint16_t>();
+            c.dtype = r.get<uint8_t>();
+            break;
+        }
+        case HOLO_OP_ADD:
+        case HOLO_OP_MUL: {  // put_binary :582-589
+            auto &c = out->u.binary;
+            c.a = r.buf();
+            c.b = r.buf();
+            c.output = r.buf();
+            c.element_count = r.get<uint64_t>();
+            c.witt_bits = r.get<uint16_t>();
+            c.dtype = r.get<uint8_t>();
+            break;
+        }
+        case HOLO_OP_RMS_NORM: {  // put_norm :656-668
+            auto &c = out->u.norm;
+            c.x = r.buf();
+            c.gamma = r.buf();
+            c.beta = r.buf();
+            c.residual = r.buf();
+            c.output = r.buf();
+            c.batch = r.get<uint32_t>();
+            c.feature = r.get<uint32_t>();
+            c.channels = r.get<uint32_t>();
+            c.num_groups = r.get<uint32_t>();
+            c.epsilon_bits = r.get<uint64_t>();
+            c.dtype = r.get<uint8_t>();
+            break;
+        }
+        case HOLO_OP_ROTARY: {  // put_rope :711-719
+            auto &c = out->u.rope;
+            c.x = r.buf();
+            c.cos = r.buf();
+            c.sin = r.buf();
+            c.output = r.buf();
+            c.head_dim = r.get<uint32_t>();
+            c.element_count = r.get<uint64_t>();
+            c.dtype = r.get<uint8_t>();
+            break;
+        }
+        case HOLO_OP_GATHER: {  // put_gather :626-636
+            auto &c = out->u.gather;
+            c.data = r.buf();
+            c.indices = r.buf();
+            c.output = r.buf();
+            c.outer = r.get<uint64_t>();
+            c.axis_dim = r.get<uint64_t>();
+            c.inner = r.get<uint64_t>();
+            c.num_indices = r.get<uint64_t>();
+            c.idx_dtype = r.get<uint8_t>();
+            c.dtype = r.get<uint8_t>();
+            break;
+        }
+        case HOLO_OP_ARGMAX: {  // field order of holo_argmax_call
+            auto &c = out->u.argmax;
+            c.input = r.buf();
+            c.output = r.buf();
+            c.rows = r.get<uint32_t>();
+            c.cols = r.get<uint32_t>();
             c.dtype = r.get<uint8_t>();
             break;
         }
@@ -547,6 +767,27 @@ int decode_impl(const uint8_t *wire, size_t len, holo_kernel_call *out, size_t *
 
 }  // namespace
 
+namespace holo {
+
+int set_error(int code, const std::string &msg) { return fail(code, msg); }
+
+int dispatch_with_slots(holo_backend *be, const std::vector<SlotRange> &slots,
+                        const holo_kernel_call *call) {
+    SlotTable st;
+    st.vec = &slots;
+    return dispatch_impl(be, st, call);
+}
+
+int decode_call(const uint8_t *wire, size_t len, holo_kernel_call *out, size_t *consumed) {
+    return decode_impl(wire, len, out, consumed);
+}
+
+hipStream_t backend_stream(const holo_backend *be) { return be->stream; }
+void set_backend_stream(holo_backend *be, hipStream_t s) { be->stream = s; }
+int backend_device(const holo_backend *be) { return be->device; }
+
+}  // namespace holo
+
 extern "C" {
 
 int holo_hip_backend_create(int device, void *stream, holo_backend **out) {
@@ -567,6 +808,12 @@ int holo_hip_backend_create(int device, void *stream, holo_backend **out) {
     auto *be = new holo_backend();
     be->device = device;
     be->stream = static_cast<hipStream_t>(stream);
+    if (hipMalloc(&be->dev_err, sizeof(int)) != hipSuccess ||
+        hipMemcpy(be->dev_err, &kZero, sizeof(int), hipMemcpyHostToDevice) != hipSuccess) {
+        if (be->dev_err) (void)hipFree(be->dev_err);
+        delete be;
+        return fail(HOLO_ERR_INIT, "backend_create: device error flag allocation failed");
+    }
     *out = be;
     return HOLO_OK;
 }
@@ -579,6 +826,7 @@ int holo_hip_backend_destroy(holo_backend *be) {
         for (auto *t : row)
             if (t) (void)hipFree(t);
     if (be->scratch) (void)hipFree(be->scratch);
+    if (be->dev_err) (void)hipFree(be->dev_err);
     delete be;
     return HOLO_OK;
 }
@@ -620,6 +868,16 @@ int holo_hip_synchronize(holo_backend *be) {
     if (!be) return fail(HOLO_ERR_INIT, "synchronize: null backend");
     hipError_t e = hipStreamSynchronize(be->stream);
     if (e != hipSuccess) return fail(HOLO_ERR_DISPATCH, std::string("synchronize: ") + hipGetErrorString(e));
+    // refusals the kernels could only see on the device (a Gather index out of range)
+    int flag = 0;
+    e = hipMemcpy(&flag, be->dev_err, sizeof(int), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return fail(HOLO_ERR_DISPATCH, std::string("synchronize: ") + hipGetErrorString(e));
+    if (flag) {
+        (void)hipMemcpy(be->dev_err, &kZero, sizeof(int), hipMemcpyHostToDevice);
+        return fail(HOLO_ERR_SLOT_OUT_OF_RANGE,
+                    "gather: an index is outside [-axis_dim, axis_dim) (reported by the device; "
+                    "its output row was zeroed)");
+    }
     return HOLO_OK;
 }
 

@@ -46,6 +46,22 @@ size_t attn_i8_scratch_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t buck
 bool attn_i8_supported(uint32_t H, uint32_t Hkv, uint32_t D, uint32_t bucket);
 hipError_t launch_attn_i8(const AttnI8Args &a, void *scratch, hipStream_t stream);
 
+// decoder_ops.hip — the other ops of a decode step (bf16 or f32 operands).
+// op 0 = Add, 1 = Mul.
+hipError_t launch_binary(int op, const void *a, const void *b, void *out, uint64_t n, bool bf16,
+                         hipStream_t stream);
+// gamma == nullptr: no affine scale.
+hipError_t launch_rmsnorm(const void *x, const void *gamma, void *out, uint32_t batch,
+                          uint32_t feature, float eps, bool bf16, hipStream_t stream);
+hipError_t launch_rope(const void *x, const void *cs, const void *sn, void *out, uint32_t head_dim,
+                       uint64_t n, bool bf16, hipStream_t stream);
+// Row gather; an out-of-range index zeroes its row and sets *err (device int).
+hipError_t launch_gather(const void *data, const void *idx, void *out, uint64_t outer,
+                         uint64_t axis_dim, uint64_t num_idx, uint64_t row_bytes, bool i64,
+                         int *err, hipStream_t stream);
+hipError_t launch_argmax(const void *in, int32_t *out, uint32_t rows, uint32_t cols, bool bf16,
+                         hipStream_t stream);
+
 // gemm.hip — C = A*B row-major, fp32 accumulation. dtype f32 or bf16 (bf16
 // result narrowed by truncation). `scratch` holds split-K partials of the
 // few-row path, matmul_scratch_bytes() bytes (0: none needed). Calls sharing

@@ -1,0 +1,633 @@
+// holo_session.cpp — a `.holo` archive executed over device-resident slots:
+// the InferenceSession of crates/hologram-exec/src/session.rs with the
+// MI355X backend behind every node.
+//
+// Load (session.rs:428-797): header, version 2..=3 and the BLAKE3 footer over
+// every preceding byte (crates/hologram-archive/src/loader.rs:141-185); the
+// section table (loader.rs:220-263); KernelCalls (kernel_codec.rs wire form),
+// Inputs/Outputs ports (writer.rs decode_ports), ExecPlan levels (writer.rs
+// decode_exec_plan; absent = one level holding every call in order),
+// Constants (constant_codec.rs; a by-reference body resolves through the
+// Weights section, whose fingerprints are re-verified, writer.rs
+// decode_weights). Per-slot sizes follow session.rs:544-623: the largest
+// referencing BufferRef length, port byte count or constant body, at least 64
+// bytes, rounded up to 64. Constants are uploaded to the device once; every
+// other slot gets one device buffer for the life of the session (the
+// reference binds a fresh pool buffer per node per walk; with the graph memo
+// off, a slot's previous value is never read again, so the buffer is reused).
+//
+// Execute (session.rs:846-932 and compute_and_label :1052-1289): the levels
+// in order, each node dispatched on the backend with operands resolved
+// through the session's slot table. A KvCacheWrite / KvQuantAppend whose
+// cache operand no other node reads and that is no output port is run as the
+// in-place move (session.rs:1163-1190, 1313-1370): the call is rewritten at
+// load to write its cache operand, and its output slot aliases that buffer.
+// The whole walk can be captured once into a HIP graph and replayed, which
+// removes the per-node host cost from a decode step (the reference's ~191 ns
+// per node is per-execute host work that a GPU walk must not serialize on).
+//
+// Not carried over: κ-label derivation per node and the graph memo (the
+// benchmarks run with memo hits disabled, and labels only key reuse), load-time
+// fusion passes (the archives this backend runs carry unfused ops), paged
+// weight providers, leases and warm-start sections (WarmStart is ignored).
+#include <hip/hip_runtime.h>
+#include <string.h>
+
+#include <algorithm>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "holo_hip.h"
+#include "holo_internal.h"
+
+namespace {
+
+using holo::set_error;
+using holo::SlotRange;
+
+constexpr uint16_t kFormatVersion = 3, kMinReadVersion = 2;   // format.rs:16-21
+enum : uint8_t {
+    kSecKernelCalls = 1, kSecWeights = 3, kSecInputs = 9, kSecOutputs = 10, kSecConstants = 11,
+    kSecExecPlan = 12,
+};
+
+struct Port {
+    std::string name;
+    uint32_t slot = 0;
+    uint64_t count = 0;
+    uint8_t dtype = 0;
+    std::vector<uint64_t> shape;
+};
+
+struct Cursor {
+    const uint8_t *p;
+    size_t len, at = 0;
+    bool ok = true;
+    template <class T>
+    T get() {
+        T v{};
+        if (at + sizeof(T) > len) {
+            ok = false;
+            at = len;
+            return v;
+        }
+        memcpy(&v, p + at, sizeof(T));
+        at += sizeof(T);
+        return v;
+    }
+    const uint8_t *take(size_t n) {
+        if (at + n > len || at + n < at) {
+            ok = false;
+            at = len;
+            return nullptr;
+        }
+        const uint8_t *r = p + at;
+        at += n;
+        return r;
+    }
+};
+
+// port_bytes_per_element (session.rs): the element width of a port's dtype.
+uint64_t port_bytes(uint8_t dt) {
+    switch (dt) {
+        case 0: case 1: case HOLO_DTYPE_I8: return 1;   // bool, u8, i8
+        case HOLO_DTYPE_F16: case HOLO_DTYPE_BF16: return 2;
+        case HOLO_DTYPE_I32: case HOLO_DTYPE_F32: return 4;
+        case 3: case HOLO_DTYPE_I64: case 9: return 8;  // u64, i64, f64
+        default: return 1;
+    }
+}
+
+// The BufferRefs a call reads and writes. Writes are the call's outputs
+// (two for KvQuantAppend: the int8 cache and its scales).
+void call_operands(const holo_kernel_call &c, std::vector<holo_buffer_ref> *reads,
+                   std::vector<holo_buffer_ref> *writes) {
+    reads->clear();
+    writes->clear();
+    auto r = [&](const holo_buffer_ref &b) {
+        if (b.slot != HOLO_SLOT_ABSENT) reads->push_back(b);
+    };
+    auto w = [&](const holo_buffer_ref &b) { writes->push_back(b); };
+    switch (c.tag) {
+        case HOLO_OP_SIGMOID: case HOLO_OP_TANH: case HOLO_OP_GELU: case HOLO_OP_SILU:
+        case HOLO_OP_EXP:
+            r(c.u.unary.input); w(c.u.unary.output); break;
+        case HOLO_OP_ADD: case HOLO_OP_MUL:
+            r(c.u.binary.a); r(c.u.binary.b); w(c.u.binary.output); break;
+        case HOLO_OP_RMS_NORM:
+            r(c.u.norm.x); r(c.u.norm.gamma); r(c.u.norm.beta); r(c.u.norm.residual);
+            w(c.u.norm.output); break;
+        case HOLO_OP_ROTARY:
+            r(c.u.rope.x); r(c.u.rope.cos); r(c.u.rope.sin); w(c.u.rope.output); break;
+        case HOLO_OP_GATHER:
+            r(c.u.gather.data); r(c.u.gather.indices); w(c.u.gather.output); break;
+        case HOLO_OP_ARGMAX:
+            r(c.u.argmax.input); w(c.u.argmax.output); break;
+        case HOLO_OP_MATMUL:
+            r(c.u.matmul.a); r(c.u.matmul.b); w(c.u.matmul.output); break;
+        case HOLO_OP_KV_CACHE_WRITE:
+            r(c.u.kv_write.cache); r(c.u.kv_write.new_rows_buf); r(c.u.kv_write.pos);
+            w(c.u.kv_write.output); break;
+        case HOLO_OP_KV_QUANT_APPEND: {
+            const auto &k = c.u.kv_quant_append;
+            r(k.new_rows_buf); r(k.pos); r(k.cache); r(k.cache_scales);
+            w(k.output); w(k.output_scales); break;
+        }
+        case HOLO_OP_DECODE_ATTN_I8: {
+            const auto &a = c.u.attn_i8;
+            r(a.q); r(a.k_cache); r(a.v_cache); r(a.k_scales); r(a.v_scales); r(a.lens);
+            w(a.output); break;
+        }
+        default: break;
+    }
+}
+
+int parse_ports(const uint8_t *p, size_t n, std::vector<Port> *out) {
+    Cursor c{p, n};
+    const uint32_t count = c.get<uint32_t>();
+    for (uint32_t i = 0; i < count && c.ok; ++i) {
+        Port port;
+        const uint16_t nl = c.get<uint16_t>();
+        const uint8_t *nm = c.take(nl);
+        if (nm) port.name.assign(reinterpret_cast<const char *>(nm), nl);
+        port.slot = c.get<uint32_t>();
+        port.count = c.get<uint64_t>();
+        port.dtype = c.get<uint8_t>();
+        const uint8_t rank = c.get<uint8_t>();
+        for (uint8_t d = 0; d < rank; ++d) port.shape.push_back(c.get<uint64_t>());
+        out->push_back(port);
+    }
+    if (!c.ok) return set_error(HOLO_ERR_DISPATCH, "session_load: truncated port section");
+    return HOLO_OK;
+}
+
+}  // namespace
+
+struct holo_session {
+    holo_backend *be = nullptr;
+    hipStream_t stream = nullptr;                 // session-owned, default priority
+    std::vector<holo_kernel_call> calls;
+    std::vector<std::vector<uint32_t>> plan;
+    std::vector<Port> inputs, outputs;
+    std::vector<uint64_t> slot_bytes;             // padded size per slot
+    std::vector<SlotRange> slots;                 // current bindings
+    std::vector<SlotRange> owned;                 // the session's own buffer per slot
+    std::vector<std::pair<uint32_t, uint32_t>> aliases;   // (output slot, cache slot) moves
+    void *const_arena = nullptr, *work_arena = nullptr;
+    uint8_t fingerprint[32] = {};
+    hipGraphExec_t graph = nullptr;
+    std::vector<SlotRange> graph_slots;           // bindings the graph was captured with
+};
+
+namespace {
+
+void release(holo_session *s) {
+    if (!s) return;
+    if (s->stream) (void)hipStreamSynchronize(s->stream);
+    if (s->graph) (void)hipGraphExecDestroy(s->graph);
+    if (s->const_arena) (void)hipFree(s->const_arena);
+    if (s->work_arena) (void)hipFree(s->work_arena);
+    if (s->stream) (void)hipStreamDestroy(s->stream);
+    delete s;
+}
+
+int load_impl(holo_backend *be, const uint8_t *bytes, size_t len, holo_session **out) {
+    const char *op = "session_load";
+    // --- header + footer (loader.rs:141-185)
+    if (len < 4 + 2 + 2 + 2 + 32)
+        return set_error(HOLO_ERR_DISPATCH, "session_load: archive truncated (< 42 bytes)");
+    if (memcmp(bytes, "HOLO", 4) != 0) return set_error(HOLO_ERR_DISPATCH, "session_load: bad magic");
+    uint16_t ver;
+    memcpy(&ver, bytes + 4, 2);
+    if (ver < kMinReadVersion || ver > kFormatVersion)
+        return set_error(HOLO_ERR_DISPATCH, "session_load: unsupported .holo version " + std::to_string(ver));
+    auto s = std::unique_ptr<holo_session, void (*)(holo_session *)>(new holo_session(), release);
+    s->be = be;
+    holo::blake3_hash(bytes, len - 32, s->fingerprint);
+    if (memcmp(s->fingerprint, bytes + len - 32, 32) != 0)
+        return set_error(HOLO_ERR_DISPATCH, "session_load: footer fingerprint mismatch (BLAKE3)");
+    // --- section table (loader.rs:220-263)
+    uint16_t nsec;
+    memcpy(&nsec, bytes + 8, 2);
+    std::map<uint8_t, std::pair<const uint8_t *, size_t>> sec;
+    const size_t body_end = len - 32;
+    size_t cur = 10;
+    for (uint16_t i = 0; i < nsec; ++i) {
+        if (cur + 24 > body_end) return set_error(HOLO_ERR_DISPATCH, "session_load: section table truncated");
+        const uint8_t kind = bytes[cur];
+        if (kind < 1 || kind > 16) return set_error(HOLO_ERR_DISPATCH, "session_load: unknown section kind");
+        uint64_t off, n;
+        memcpy(&off, bytes + cur + 8, 8);
+        memcpy(&n, bytes + cur + 16, 8);
+        cur += 24;
+        if (off > body_end || n > body_end - off)
+            return set_error(HOLO_ERR_DISPATCH, "session_load: section out of range");
+        if (!sec.count(kind)) sec[kind] = {bytes + off, size_t(n)};   // first of a kind wins
+    }
+    // --- kernel calls
+    auto it = sec.find(kSecKernelCalls);
+    if (it == sec.end()) return set_error(HOLO_ERR_DISPATCH, "session_load: no KernelCalls section");
+    {
+        Cursor c{it->second.first, it->second.second};
+        const uint32_t n = c.get<uint32_t>();
+        if (!c.ok) return set_error(HOLO_ERR_DISPATCH, "session_load: truncated KernelCalls");
+        for (uint32_t i = 0; i < n; ++i) {
+            holo_kernel_call call;
+            size_t used = 0;
+            const int rc = holo::decode_call(c.p + c.at, c.len - c.at, &call, &used);
+            if (rc != HOLO_OK) return rc;
+            c.at += used;
+            s->calls.push_back(call);
+        }
+    }
+    // --- ports, plan
+    if ((it = sec.find(kSecInputs)) != sec.end()) {
+        const int rc = parse_ports(it->second.first, it->second.second, &s->inputs);
+        if (rc != HOLO_OK) return rc;
+    }
+    if ((it = sec.find(kSecOutputs)) != sec.end()) {
+        const int rc = parse_ports(it->second.first, it->second.second, &s->outputs);
+        if (rc != HOLO_OK) return rc;
+    }
+    if ((it = sec.find(kSecExecPlan)) != sec.end()) {
+        Cursor c{it->second.first, it->second.second};
+        const uint32_t nl = c.get<uint32_t>();
+        for (uint32_t l = 0; l < nl && c.ok; ++l) {
+            const uint32_t n = c.get<uint32_t>();
+            std::vector<uint32_t> lv;
+            for (uint32_t i = 0; i < n && c.ok; ++i) lv.push_back(c.get<uint32_t>());
+            s->plan.push_back(std::move(lv));
+        }
+        if (!c.ok) return set_error(HOLO_ERR_DISPATCH, "session_load: truncated ExecPlan");
+        for (auto &lv : s->plan)
+            for (uint32_t i : lv)
+                if (i >= s->calls.size())
+                    return set_error(HOLO_ERR_DISPATCH, "session_load: ExecPlan index out of range");
+    } else {
+        std::vector<uint32_t> all(s->calls.size());
+        for (size_t i = 0; i < all.size(); ++i) all[i] = uint32_t(i);
+        s->plan.push_back(std::move(all));
+    }
+    // --- weights (fingerprint -> body), constants
+    std::map<std::string, std::pair<const uint8_t *, uint64_t>> weights;
+    if ((it = sec.find(kSecWeights)) != sec.end()) {
+        Cursor c{it->second.first, it->second.second};
+        const uint32_t n = c.get<uint32_t>();
+        for (uint32_t i = 0; i < n && c.ok; ++i) {
+            const uint8_t *fp = c.take(32);
+            const uint64_t bl = c.get<uint64_t>();
+            const uint8_t *body = c.take(size_t(bl));
+            if (!c.ok) break;
+            uint8_t h[32];
+            holo::blake3_hash(body, bl, h);
+            if (memcmp(h, fp, 32) != 0)
+                return set_error(HOLO_ERR_DISPATCH, "session_load: weight body does not match its fingerprint");
+            weights[std::string(reinterpret_cast<const char *>(fp), 32)] = {body, bl};
+        }
+        if (!c.ok) return set_error(HOLO_ERR_DISPATCH, "session_load: truncated Weights section");
+    }
+    struct Const {
+        uint32_t slot;
+        const uint8_t *body;
+        uint64_t len;
+    };
+    std::vector<Const> consts;
+    if ((it = sec.find(kSecConstants)) != sec.end()) {
+        Cursor c{it->second.first, it->second.second};
+        const uint32_t n = c.get<uint32_t>();
+        for (uint32_t i = 0; i < n && c.ok; ++i) {
+            const uint8_t tag = c.get<uint8_t>();
+            const uint32_t slot = c.get<uint32_t>();
+            (void)c.get<uint8_t>();   // dtype
+            if (tag == 0) {
+                const uint32_t bl = c.get<uint32_t>();
+                const uint8_t *body = c.take(bl);
+                if (c.ok) consts.push_back({slot, body, bl});
+            } else if (tag == 1) {
+                const uint8_t *fp = c.take(32);
+                if (!c.ok) break;
+                auto w = weights.find(std::string(reinterpret_cast<const char *>(fp), 32));
+                if (w == weights.end())
+                    return set_error(HOLO_ERR_DISPATCH,
+                                     "session_load: constant references a weight the archive does not carry");
+                consts.push_back({slot, w->second.first, w->second.second});
+            } else {
+                return set_error(HOLO_ERR_DISPATCH, "session_load: unknown ConstantEntry tag");
+            }
+        }
+        if (!c.ok) return set_error(HOLO_ERR_DISPATCH, "session_load: truncated Constants section");
+    }
+    // --- per-slot sizes (session.rs:544-623)
+    size_t nslots = 0;
+    std::vector<holo_buffer_ref> rd, wr;
+    auto bump = [&](uint32_t slot) {
+        if (slot != HOLO_SLOT_ABSENT && size_t(slot) + 1 > nslots) nslots = size_t(slot) + 1;
+    };
+    for (const auto &call : s->calls) {
+        call_operands(call, &rd, &wr);
+        for (auto &b : rd) bump(b.slot);
+        for (auto &b : wr) bump(b.slot);
+    }
+    for (auto &p : s->inputs) bump(p.slot);
+    for (auto &p : s->outputs) bump(p.slot);
+    for (auto &k : consts) bump(k.slot);
+    if (nslots > (1u << 24)) return set_error(HOLO_ERR_DISPATCH, "session_load: slot ids above 2^24");
+    std::vector<uint64_t> sz(nslots, 0);
+    std::vector<uint8_t> is_const(nslots, 0), is_input(nslots, 0), is_output(nslots, 0);
+    for (const auto &call : s->calls) {
+        call_operands(call, &rd, &wr);
+        for (auto *v : {&rd, &wr})
+            for (auto &b : *v) sz[b.slot] = std::max(sz[b.slot], b.offset + b.length);
+    }
+    for (auto *ports : {&s->inputs, &s->outputs})
+        for (auto &p : *ports) sz[p.slot] = std::max(sz[p.slot], p.count * port_bytes(p.dtype));
+    for (auto &k : consts) {
+        sz[k.slot] = std::max(sz[k.slot], k.len);
+        is_const[k.slot] = 1;
+    }
+    for (auto &p : s->inputs) is_input[p.slot] = 1;
+    for (auto &p : s->outputs) is_output[p.slot] = 1;
+    for (auto &v : sz) v = std::max<uint64_t>(v, 64), v = (v + 63) / 64 * 64;
+    // --- device memory: one arena for constants, one for every other slot,
+    // each slot 256-byte aligned
+    uint64_t cbytes = 0, wbytes = 0;
+    std::vector<uint64_t> off(nslots, 0);
+    for (size_t i = 0; i < nslots; ++i) {
+        uint64_t &total = is_const[i] ? cbytes : wbytes;
+        off[i] = total;
+        total += (sz[i] + 255) / 256 * 256;
+    }
+    s->slot_bytes = sz;
+    if (!be) {   // a dry load: parse and validate only (no device)
+        s->slots.assign(nslots, SlotRange{});
+        s->owned = s->slots;
+        goto plan_moves;
+    }
+    if (hipSetDevice(holo::backend_device(be)) != hipSuccess)
+        return set_error(HOLO_ERR_INIT, "session_load: hipSetDevice failed");
+    if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess)
+        return set_error(HOLO_ERR_INIT, "session_load: stream creation failed");
+    if (cbytes && hipMalloc(&s->const_arena, cbytes) != hipSuccess)
+        return set_error(HOLO_ERR_INIT, "session_load: constant arena allocation failed (" +
+                                            std::to_string(cbytes) + " bytes)");
+    if (wbytes && hipMalloc(&s->work_arena, wbytes) != hipSuccess)
+        return set_error(HOLO_ERR_INIT, "session_load: slot arena allocation failed (" +
+                                            std::to_string(wbytes) + " bytes)");
+    s->owned.resize(nslots);
+    for (size_t i = 0; i < nslots; ++i) {
+        uint8_t *base = static_cast<uint8_t *>(is_const[i] ? s->const_arena : s->work_arena);
+        s->owned[i] = SlotRange{base + off[i], sz[i]};
+    }
+    for (auto &k : consts)
+        if (k.len && hipMemcpy(s->owned[k.slot].ptr, k.body, k.len, hipMemcpyHostToDevice) != hipSuccess)
+            return set_error(HOLO_ERR_INIT, "session_load: constant upload failed");
+    s->slots = s->owned;
+plan_moves:
+    // --- in-place KV moves (compute_stealable, session.rs:281): the cache
+    // operand has no other reader, is no output port and no constant
+    std::vector<uint32_t> readers(nslots, 0);
+    for (const auto &call : s->calls) {
+        call_operands(call, &rd, &wr);
+        for (auto &b : rd) readers[b.slot]++;
+    }
+    for (auto &call : s->calls) {
+        if (call.tag == HOLO_OP_KV_CACHE_WRITE) {
+            auto &k = call.u.kv_write;
+            const uint32_t cs = k.cache.slot, os = k.output.slot;
+            if (cs == os || readers[cs] != 1 || is_output[cs] || is_const[cs] || k.cache.offset != 0 ||
+                k.output.offset != 0)
+                continue;
+            if (k.new_rows_buf.slot == cs || k.pos.slot == cs) continue;
+            s->aliases.push_back({os, cs});
+            k.output = k.cache;
+        } else if (call.tag == HOLO_OP_KV_QUANT_APPEND) {
+            auto &k = call.u.kv_quant_append;
+            const uint32_t cq = k.cache.slot, cs = k.cache_scales.slot;
+            const uint32_t oq = k.output.slot, os = k.output_scales.slot;
+            if (cq == oq || cs == os || cq == cs || readers[cq] != 1 || readers[cs] != 1 ||
+                is_output[cq] || is_output[cs] || is_const[cq] || is_const[cs] ||
+                k.cache.offset != 0 || k.cache_scales.offset != 0 || k.output.offset != 0 ||
+                k.output_scales.offset != 0)
+                continue;
+            if (k.new_rows_buf.slot == cq || k.new_rows_buf.slot == cs || k.pos.slot == cq || k.pos.slot == cs)
+                continue;
+            s->aliases.push_back({oq, cq});
+            s->aliases.push_back({os, cs});
+            k.output = k.cache;
+            k.output_scales = k.cache_scales;
+        }
+    }
+    // every call must be one this backend runs (validated on the slot sizes)
+    for (size_t i = 0; i < s->calls.size(); ++i) {
+        const int rc = holo_hip_validate(&s->calls[i], s->slot_bytes.data(), uint32_t(nslots));
+        if (rc != HOLO_OK) {
+            std::string m = holo_hip_last_error_message();
+            return set_error(rc, std::string(op) + ": kernel call " + std::to_string(i) + " (tag " +
+                                     std::to_string(s->calls[i].tag) + "): " + m);
+        }
+    }
+    *out = s.release();
+    return HOLO_OK;
+}
+
+// One walk: each level's nodes in order on the session stream.
+int walk(holo_session *s) {
+    if (!s->be) return set_error(HOLO_ERR_INIT, "session_execute: loaded without a backend (dry load)");
+    for (auto &a : s->aliases) s->slots[a.first] = s->slots[a.second];
+    const hipStream_t saved = holo::backend_stream(s->be);
+    holo::set_backend_stream(s->be, s->stream);
+    int rc = HOLO_OK;
+    for (const auto &level : s->plan) {
+        for (uint32_t i : level) {
+            rc = holo::dispatch_with_slots(s->be, s->slots, &s->calls[i]);
+            if (rc != HOLO_OK) {
+                std::string m = holo_hip_last_error_message();
+                set_error(rc, "session_execute: kernel call " + std::to_string(i) + ": " + m);
+                break;
+            }
+        }
+        if (rc != HOLO_OK) break;
+    }
+    holo::set_backend_stream(s->be, saved);
+    return rc;
+}
+
+bool same_bindings(const std::vector<SlotRange> &a, const std::vector<SlotRange> &b) {
+    if (a.size() != b.size()) return false;
+    for (size_t i = 0; i < a.size(); ++i)
+        if (a[i].ptr != b[i].ptr || a[i].bytes != b[i].bytes) return false;
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int holo_hip_session_load(holo_backend *be, const uint8_t *bytes, size_t len, holo_session **out) {
+    if (!bytes || !out) return set_error(HOLO_ERR_INIT, "session_load: null argument");
+    *out = nullptr;
+    return load_impl(be, bytes, len, out);
+}
+
+int holo_hip_session_close(holo_session *s) {
+    release(s);
+    return HOLO_OK;
+}
+
+int holo_hip_session_info(const holo_session *s, uint32_t *n_inputs, uint32_t *n_outputs,
+                          uint32_t *n_calls, uint32_t *n_slots) {
+    if (!s) return set_error(HOLO_ERR_INIT, "session_info: null session");
+    if (n_inputs) *n_inputs = uint32_t(s->inputs.size());
+    if (n_outputs) *n_outputs = uint32_t(s->outputs.size());
+    if (n_calls) *n_calls = uint32_t(s->calls.size());
+    if (n_slots) *n_slots = uint32_t(s->slots.size());
+    return HOLO_OK;
+}
+
+int holo_hip_session_port(const holo_session *s, int is_output, uint32_t index, uint32_t *slot,
+                          uint64_t *element_count, uint8_t *dtype, uint64_t *bytes) {
+    if (!s) return set_error(HOLO_ERR_INIT, "session_port: null session");
+    const auto &ports = is_output ? s->outputs : s->inputs;
+    if (index >= ports.size()) return set_error(HOLO_ERR_SLOT_OUT_OF_RANGE, "session_port: index out of range");
+    const Port &p = ports[index];
+    if (slot) *slot = p.slot;
+    if (element_count) *element_count = p.count;
+    if (dtype) *dtype = p.dtype;
+    if (bytes) *bytes = p.count * port_bytes(p.dtype);
+    return HOLO_OK;
+}
+
+int holo_hip_session_fingerprint(const holo_session *s, uint8_t out32[32]) {
+    if (!s || !out32) return set_error(HOLO_ERR_INIT, "session_fingerprint: null argument");
+    memcpy(out32, s->fingerprint, 32);
+    return HOLO_OK;
+}
+
+int holo_hip_session_bind_input(holo_session *s, uint32_t index, void *dev_ptr, uint64_t bytes) {
+    if (!s) return set_error(HOLO_ERR_INIT, "session_bind_input: null session");
+    if (index >= s->inputs.size())
+        return set_error(HOLO_ERR_SLOT_OUT_OF_RANGE, "session_bind_input: index out of range");
+    const Port &p = s->inputs[index];
+    if (!dev_ptr) {
+        s->slots[p.slot] = s->owned[p.slot];
+        return HOLO_OK;
+    }
+    const uint64_t need = p.count * port_bytes(p.dtype);
+    if (bytes < need)
+        return set_error(HOLO_ERR_SLOT_OUT_OF_RANGE, "session_bind_input: port '" + p.name + "' needs " +
+                                                         std::to_string(need) + " bytes, got " +
+                                                         std::to_string(bytes));
+    s->slots[p.slot] = SlotRange{static_cast<uint8_t *>(dev_ptr), bytes};
+    return HOLO_OK;
+}
+
+int holo_hip_session_write_input(holo_session *s, uint32_t index, const void *host, uint64_t bytes) {
+    if (!s || !host) return set_error(HOLO_ERR_INIT, "session_write_input: null argument");
+    if (index >= s->inputs.size())
+        return set_error(HOLO_ERR_SLOT_OUT_OF_RANGE, "session_write_input: index out of range");
+    const Port &p = s->inputs[index];
+    const SlotRange &dst = s->slots[p.slot];
+    const uint64_t n = std::min<uint64_t>(bytes, p.count * port_bytes(p.dtype));
+    if (n > dst.bytes) return set_error(HOLO_ERR_SLOT_OUT_OF_RANGE, "session_write_input: too many bytes");
+    if (hipMemcpyAsync(dst.ptr, host, n, hipMemcpyHostToDevice, s->stream) != hipSuccess ||
+        hipStreamSynchronize(s->stream) != hipSuccess)
+        return set_error(HOLO_ERR_DISPATCH, "session_write_input: copy failed");
+    return HOLO_OK;
+}
+
+int holo_hip_session_execute(holo_session *s) {
+    if (!s) return set_error(HOLO_ERR_INIT, "session_execute: null session");
+    return walk(s);
+}
+
+int holo_hip_session_output(const holo_session *s, uint32_t index, void **dev_ptr, uint64_t *bytes) {
+    if (!s) return set_error(HOLO_ERR_INIT, "session_output: null session");
+    if (index >= s->outputs.size())
+        return set_error(HOLO_ERR_SLOT_OUT_OF_RANGE, "session_output: index out of range");
+    const Port &p = s->outputs[index];
+    if (dev_ptr) *dev_ptr = s->slots[p.slot].ptr;
+    if (bytes) *bytes = p.count * port_bytes(p.dtype);
+    return HOLO_OK;
+}
+
+int holo_hip_session_read_output(holo_session *s, uint32_t index, void *host, uint64_t bytes) {
+    if (!s || !host) return set_error(HOLO_ERR_INIT, "session_read_output: null argument");
+    if (index >= s->outputs.size())
+        return set_error(HOLO_ERR_SLOT_OUT_OF_RANGE, "session_read_output: index out of range");
+    const Port &p = s->outputs[index];
+    const uint64_t n = std::min<uint64_t>(bytes, p.count * port_bytes(p.dtype));
+    if (hipStreamSynchronize(s->stream) != hipSuccess ||
+        hipMemcpy(host, s->slots[p.slot].ptr, n, hipMemcpyDeviceToHost) != hipSuccess)
+        return set_error(HOLO_ERR_DISPATCH, "session_read_output: copy failed");
+    return HOLO_OK;
+}
+
+int holo_hip_session_synchronize(holo_session *s) {
+    if (!s) return set_error(HOLO_ERR_INIT, "session_synchronize: null session");
+    const hipStream_t saved = holo::backend_stream(s->be);
+    holo::set_backend_stream(s->be, s->stream);
+    const int rc = holo_hip_synchronize(s->be);
+    holo::set_backend_stream(s->be, saved);
+    return rc;
+}
+
+int holo_hip_session_stream(const holo_session *s, void **stream) {
+    if (!s || !stream) return set_error(HOLO_ERR_INIT, "session_stream: null argument");
+    *stream = s->stream;
+    return HOLO_OK;
+}
+
+int holo_hip_session_capture(holo_session *s) {
+    if (!s) return set_error(HOLO_ERR_INIT, "session_capture: null session");
+    // An eager walk first: it sizes the backend's scratch (no allocation may
+    // happen under capture) and surfaces any refusal with a message.
+    int rc = walk(s);
+    if (rc != HOLO_OK) return rc;
+    if (hipStreamSynchronize(s->stream) != hipSuccess)
+        return set_error(HOLO_ERR_DISPATCH, "session_capture: eager walk failed");
+    if (s->graph) {
+        (void)hipGraphExecDestroy(s->graph);
+        s->graph = nullptr;
+    }
+    if (hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal) != hipSuccess)
+        return set_error(HOLO_ERR_DISPATCH, "session_capture: begin capture failed");
+    rc = walk(s);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(s->stream, &g);
+    if (rc != HOLO_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess || !g) return set_error(HOLO_ERR_DISPATCH, "session_capture: end capture failed");
+    const hipError_t ie = hipGraphInstantiate(&s->graph, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (ie != hipSuccess) {
+        s->graph = nullptr;
+        return set_error(HOLO_ERR_DISPATCH, "session_capture: graph instantiation failed");
+    }
+    s->graph_slots = s->slots;
+    return HOLO_OK;
+}
+
+int holo_hip_session_replay(holo_session *s) {
+    if (!s) return set_error(HOLO_ERR_INIT, "session_replay: null session");
+    if (!s->graph) return set_error(HOLO_ERR_DISPATCH, "session_replay: no captured walk");
+    std::vector<SlotRange> now = s->slots;
+    for (auto &a : s->aliases) now[a.first] = now[a.second];
+    if (!same_bindings(now, s->graph_slots))
+        return set_error(HOLO_ERR_DISPATCH,
+                         "session_replay: an input was rebound since the capture; capture again");
+    if (hipGraphLaunch(s->graph, s->stream) != hipSuccess)
+        return set_error(HOLO_ERR_DISPATCH, "session_replay: graph launch failed");
+    return HOLO_OK;
+}
+
+int holo_hip_blake3(const void *data, size_t len, uint8_t out32[32]) {
+    if ((!data && len) || !out32) return set_error(HOLO_ERR_DISPATCH, "blake3: null argument");
+    holo::blake3_hash(data, len, out32);
+    return HOLO_OK;
+}
+
+}  // extern "C"

@@ -17,6 +17,8 @@ from . import _ffi
 
 # dtype tags, crates/hologram-types/src/dtype_id.rs:52-61
 DTYPE_I8 = 2
+DTYPE_I32 = 4
+DTYPE_I64 = 5
 DTYPE_F16 = 6
 DTYPE_BF16 = 7
 DTYPE_F32 = 8
@@ -33,16 +35,22 @@ class lut_act:  # noqa: N801 - the reference's module name (kernel_call.rs:877-8
 
 
 # archive discriminants, kernel_codec.rs:18-128
+D_ADD = 5
+D_MUL = 7
 D_SIGMOID = 12
 D_TANH = 13
 D_GELU = 14
 D_SILU = 15
 D_EXP = 18
 D_MATMUL = 46
+D_RN = 51
+D_ROTARY = 75
+D_GATHER = 114
 D_KVWR = 120
 D_DAVL = 121
 D_KVQA = 122   # new: int8 quantize + append
 D_DAI8 = 123   # new: decode attention over an int8 cache
+D_ARGMAX = 124  # new: per-row argmax (the greedy pick of a decode step)
 
 SLOT_ABSENT = 0xFFFFFFFF
 
@@ -73,6 +81,96 @@ class UnaryCall:
     def wire(self) -> bytes:  # put_unary, kernel_codec.rs:575-581
         return (self.input.wire() + self.output.wire()
                 + struct.pack("<QHB", self.element_count, self.witt_bits, self.dtype))
+
+
+@dataclass(frozen=True)
+class BinaryCall:
+    """kernel_call.rs:38-46."""
+    a: BufferRef
+    b: BufferRef
+    output: BufferRef
+    element_count: int
+    witt_bits: int = 16
+    dtype: int = DTYPE_BF16
+
+    def wire(self) -> bytes:  # put_binary, kernel_codec.rs:582-589
+        return (self.a.wire() + self.b.wire() + self.output.wire()
+                + struct.pack("<QHB", self.element_count, self.witt_bits, self.dtype))
+
+
+NO_BUFFER = BufferRef(SLOT_ABSENT)
+
+
+@dataclass(frozen=True)
+class NormCall:
+    """kernel_call.rs:422-446 (RmsNorm uses x, gamma, output; beta and
+    residual absent)."""
+    x: BufferRef
+    gamma: BufferRef
+    output: BufferRef
+    batch: int
+    feature: int
+    epsilon_bits: int = 0
+    dtype: int = DTYPE_BF16
+    beta: BufferRef = NO_BUFFER
+    residual: BufferRef = NO_BUFFER
+    channels: int = 0
+    num_groups: int = 0
+
+    def wire(self) -> bytes:  # put_norm, kernel_codec.rs:656-668
+        return (self.x.wire() + self.gamma.wire() + self.beta.wire() + self.residual.wire()
+                + self.output.wire()
+                + struct.pack("<IIIIQB", self.batch, self.feature, self.channels,
+                              self.num_groups, self.epsilon_bits, self.dtype))
+
+
+@dataclass(frozen=True)
+class RoPECall:
+    """kernel_call.rs:500-515."""
+    x: BufferRef
+    cos: BufferRef
+    sin: BufferRef
+    output: BufferRef
+    head_dim: int
+    element_count: int
+    dtype: int = DTYPE_BF16
+
+    def wire(self) -> bytes:  # put_rope, kernel_codec.rs:711-719
+        return (self.x.wire() + self.cos.wire() + self.sin.wire() + self.output.wire()
+                + struct.pack("<IQB", self.head_dim, self.element_count, self.dtype))
+
+
+@dataclass(frozen=True)
+class GatherCall:
+    """kernel_call.rs:380-404."""
+    data: BufferRef
+    indices: BufferRef
+    output: BufferRef
+    outer: int
+    axis_dim: int
+    inner: int
+    num_indices: int
+    idx_dtype: int = DTYPE_I32
+    dtype: int = DTYPE_BF16
+
+    def wire(self) -> bytes:  # put_gather, kernel_codec.rs:626-636
+        return (self.data.wire() + self.indices.wire() + self.output.wire()
+                + struct.pack("<QQQQBB", self.outer, self.axis_dim, self.inner,
+                              self.num_indices, self.idx_dtype, self.dtype))
+
+
+@dataclass(frozen=True)
+class ArgMaxCall:
+    """New (discriminant 124): per-row argmax into i32 (include/holo_hip.h)."""
+    input: BufferRef
+    output: BufferRef
+    rows: int
+    cols: int
+    dtype: int = DTYPE_BF16
+
+    def wire(self) -> bytes:
+        return self.input.wire() + self.output.wire() + struct.pack("<IIB", self.rows, self.cols,
+                                                                    self.dtype)
 
 
 @dataclass(frozen=True)
@@ -157,7 +255,8 @@ class DecodeAttentionI8Call:
                               self.bucket_rows, self.head_dim, self.scale_bits, self.dtype))
 
 
-_NAMES = {D_SIGMOID: "Sigmoid", D_TANH: "Tanh", D_GELU: "Gelu", D_SILU: "Silu", D_EXP: "Exp",
+_NAMES = {D_ADD: "Add", D_MUL: "Mul", D_RN: "RmsNorm", D_ROTARY: "RotaryEmbedding",
+          D_GATHER: "Gather", D_ARGMAX: "ArgMax", D_SIGMOID: "Sigmoid", D_TANH: "Tanh", D_GELU: "Gelu", D_SILU: "Silu", D_EXP: "Exp",
           D_MATMUL: "MatMul", D_KVWR: "KvCacheWrite", D_KVQA: "KvQuantAppend",
           D_DAI8: "DecodeAttentionI8"}
 
@@ -194,6 +293,30 @@ class KernelCall:
         return cls(D_MATMUL, c)
 
     @classmethod
+    def Add(cls, c: BinaryCall) -> "KernelCall":  # noqa: N802
+        return cls(D_ADD, c)
+
+    @classmethod
+    def Mul(cls, c: BinaryCall) -> "KernelCall":  # noqa: N802
+        return cls(D_MUL, c)
+
+    @classmethod
+    def RmsNorm(cls, c: NormCall) -> "KernelCall":  # noqa: N802
+        return cls(D_RN, c)
+
+    @classmethod
+    def RotaryEmbedding(cls, c: RoPECall) -> "KernelCall":  # noqa: N802
+        return cls(D_ROTARY, c)
+
+    @classmethod
+    def Gather(cls, c: GatherCall) -> "KernelCall":  # noqa: N802
+        return cls(D_GATHER, c)
+
+    @classmethod
+    def ArgMax(cls, c: ArgMaxCall) -> "KernelCall":  # noqa: N802
+        return cls(D_ARGMAX, c)
+
+    @classmethod
     def KvCacheWrite(cls, c: KvCacheWriteCall) -> "KernelCall":  # noqa: N802
         return cls(D_KVWR, c)
 
@@ -220,6 +343,22 @@ class KernelCall:
         if isinstance(p, UnaryCall):
             kc.u.unary = _ffi.UnaryCallC(p.input.c(), p.output.c(), p.element_count,
                                          p.witt_bits, p.dtype)
+        elif isinstance(p, BinaryCall):
+            kc.u.binary = _ffi.BinaryCallC(p.a.c(), p.b.c(), p.output.c(), p.element_count,
+                                           p.witt_bits, p.dtype)
+        elif isinstance(p, NormCall):
+            kc.u.norm = _ffi.NormCallC(p.x.c(), p.gamma.c(), p.beta.c(), p.residual.c(),
+                                       p.output.c(), p.batch, p.feature, p.channels,
+                                       p.num_groups, p.epsilon_bits, p.dtype)
+        elif isinstance(p, RoPECall):
+            kc.u.rope = _ffi.RopeCallC(p.x.c(), p.cos.c(), p.sin.c(), p.output.c(), p.head_dim,
+                                       p.element_count, p.dtype)
+        elif isinstance(p, GatherCall):
+            kc.u.gather = _ffi.GatherCallC(p.data.c(), p.indices.c(), p.output.c(), p.outer,
+                                           p.axis_dim, p.inner, p.num_indices, p.idx_dtype,
+                                           p.dtype)
+        elif isinstance(p, ArgMaxCall):
+            kc.u.argmax = _ffi.ArgMaxCallC(p.input.c(), p.output.c(), p.rows, p.cols, p.dtype)
         elif isinstance(p, MatMulCall):
             kc.u.matmul = _ffi.MatMulCallC(p.a.c(), p.b.c(), p.output.c(), p.m, p.k, p.n,
                                            p.dtype, int(p.b_packed))

@@ -1,0 +1,122 @@
+"""HipSession: a `.holo` archive executed on the MI355X backend.
+
+The host mirror of InferenceSession (crates/hologram-exec/src/session.rs):
+`load` (:399-797), `execute` with host bytes in and out (:846-932), and the
+addressed form where inputs are device buffers bound in place (:942-984).
+Everything runs in libholo_hip.so (include/holo_hip.h, holo_hip_session_*);
+this class only marshals arguments.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+from . import _ffi
+from .backend import HipBackend, check as _check
+
+
+@dataclass(frozen=True)
+class Port:
+    index: int
+    slot: int
+    element_count: int
+    dtype: int
+    nbytes: int
+
+
+class HipSession:
+    """`backend=None` loads dry: parse, size and validate every call on the host,
+    with no device (such a session reports ports and refuses to execute)."""
+
+    def __init__(self, backend: HipBackend | None, archive: bytes):
+        self._lib = _ffi.lib()
+        self.backend = backend
+        h = ctypes.c_void_p()
+        _check(self._lib.holo_hip_session_load(backend._h if backend else None, archive,
+                                               len(archive), ctypes.byref(h)))
+        self.handle = h
+        ni, no, nc, ns = (ctypes.c_uint32() for _ in range(4))
+        _check(self._lib.holo_hip_session_info(self.handle, ctypes.byref(ni), ctypes.byref(no),
+                                               ctypes.byref(nc), ctypes.byref(ns)))
+        self.n_calls, self.n_slots = nc.value, ns.value
+        self.inputs = [self._port(0, i) for i in range(ni.value)]
+        self.outputs = [self._port(1, i) for i in range(no.value)]
+
+    def _port(self, is_out: int, i: int) -> Port:
+        slot, cnt, dt, nb = ctypes.c_uint32(), ctypes.c_uint64(), ctypes.c_uint8(), ctypes.c_uint64()
+        _check(self._lib.holo_hip_session_port(self.handle, is_out, i, ctypes.byref(slot),
+                                               ctypes.byref(cnt), ctypes.byref(dt),
+                                               ctypes.byref(nb)))
+        return Port(i, slot.value, cnt.value, dt.value, nb.value)
+
+    def fingerprint(self) -> bytes:
+        out = ctypes.create_string_buffer(32)
+        _check(self._lib.holo_hip_session_fingerprint(self.handle, out))
+        return out.raw
+
+    # ---- the addressed form: device buffers bound in place
+    def bind_input(self, index: int, tensor) -> None:
+        """Bind input port `index` to a device tensor (torch) or (ptr, nbytes); None unbinds."""
+        if tensor is None:
+            _check(self._lib.holo_hip_session_bind_input(self.handle, index, None, 0))
+            return
+        ptr, nbytes = (tensor if isinstance(tensor, tuple)
+                       else (tensor.data_ptr(), tensor.numel() * tensor.element_size()))
+        _check(self._lib.holo_hip_session_bind_input(self.handle, index, ctypes.c_void_p(ptr),
+                                                     nbytes))
+
+    def output_ptr(self, index: int) -> tuple[int, int]:
+        p, n = ctypes.c_void_p(), ctypes.c_uint64()
+        _check(self._lib.holo_hip_session_output(self.handle, index, ctypes.byref(p),
+                                                 ctypes.byref(n)))
+        return p.value or 0, n.value
+
+    def run(self) -> None:
+        """One walk, enqueued on the session stream (asynchronous)."""
+        _check(self._lib.holo_hip_session_execute(self.handle))
+
+    def capture(self) -> None:
+        _check(self._lib.holo_hip_session_capture(self.handle))
+
+    def replay(self) -> None:
+        _check(self._lib.holo_hip_session_replay(self.handle))
+
+    def synchronize(self) -> None:
+        _check(self._lib.holo_hip_session_synchronize(self.handle))
+
+    def stream(self) -> int:
+        s = ctypes.c_void_p()
+        _check(self._lib.holo_hip_session_stream(self.handle, ctypes.byref(s)))
+        return s.value or 0
+
+    # ---- the byte form (execute): host bytes in, host bytes out
+    def write_input(self, index: int, data: bytes) -> None:
+        buf = ctypes.create_string_buffer(bytes(data), len(data))
+        _check(self._lib.holo_hip_session_write_input(self.handle, index, buf, len(data)))
+
+    def read_output(self, index: int) -> bytes:
+        n = self.outputs[index].nbytes
+        buf = ctypes.create_string_buffer(n)
+        _check(self._lib.holo_hip_session_read_output(self.handle, index, buf, n))
+        return buf.raw
+
+    def execute(self, inputs: list[bytes]) -> list[bytes]:
+        """session.rs execute: bytes per input port in, bytes per output port out."""
+        if len(inputs) != len(self.inputs):
+            raise ValueError(f"expected {len(self.inputs)} inputs, got {len(inputs)}")
+        for i, b in enumerate(inputs):
+            self.write_input(i, b)
+        self.run()
+        self.synchronize()
+        return [self.read_output(i) for i in range(len(self.outputs))]
+
+    def close(self) -> None:
+        if self.handle:
+            _check(self._lib.holo_hip_session_close(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -40,6 +40,9 @@ typedef enum holo_status {
 #define HOLO_DTYPE_BF16 7u
 #define HOLO_DTYPE_F32 8u
 
+#define HOLO_DTYPE_I32 4u
+#define HOLO_DTYPE_I64 5u
+
 /* lut_act ids, crates/hologram-compute/src/kernel_call.rs:877-885 */
 #define HOLO_ACT_SIGMOID 0
 #define HOLO_ACT_TANH 1
@@ -50,15 +53,21 @@ typedef enum holo_status {
 /* KernelCall tags = the archive wire discriminants,
  * crates/hologram-archive/src/kernel_codec.rs:18-128. 122 and 123 are new
  * capabilities and take new discriminants (kernel_codec.rs:124-128). */
+#define HOLO_OP_ADD 5u
+#define HOLO_OP_MUL 7u
 #define HOLO_OP_SIGMOID 12u
 #define HOLO_OP_TANH 13u
 #define HOLO_OP_GELU 14u
 #define HOLO_OP_SILU 15u
 #define HOLO_OP_EXP 18u
 #define HOLO_OP_MATMUL 46u
+#define HOLO_OP_RMS_NORM 51u
+#define HOLO_OP_ROTARY 75u
+#define HOLO_OP_GATHER 114u
 #define HOLO_OP_KV_CACHE_WRITE 120u
 #define HOLO_OP_KV_QUANT_APPEND 122u      /* new: int8 quantize + ring append   */
 #define HOLO_OP_DECODE_ATTN_I8 123u       /* new: GQA decode over an int8 cache */
+#define HOLO_OP_ARGMAX 124u               /* new: per-row argmax (greedy pick)  */
 
 /* BufferRef, crates/hologram-compute/src/workspace.rs:16-24.
  * length == 0 means "to the end of the slot"; slot == HOLO_SLOT_ABSENT marks an
@@ -79,6 +88,71 @@ typedef struct holo_unary_call {
     uint16_t witt_bits;
     uint8_t dtype;
 } holo_unary_call;
+
+/* BinaryCall, kernel_call.rs:38-46. Add / Mul over bf16 or f32: widen, one
+ * IEEE f32 operation, narrow (bf16 by truncation) — binary_float,
+ * src/cpu/float_kernels.rs:238-300. */
+typedef struct holo_binary_call {
+    holo_buffer_ref a;
+    holo_buffer_ref b;
+    holo_buffer_ref output;
+    uint64_t element_count;
+    uint16_t witt_bits;
+    uint8_t dtype;
+} holo_binary_call;
+
+/* NormCall, kernel_call.rs:422-446, as RmsNorm (src/cpu/float_kernels.rs:
+ * 1683-1755): per row of `feature` values, out = x * (1 / sqrtf(mean(x^2) +
+ * eps)) * gamma (gamma absent: 1). eps = f32(epsilon_bits), 0 selects 1e-9
+ * (float_kernels.rs:1324-1336). beta and residual must be absent; channels and
+ * num_groups must be 0. dtype bf16 or f32. */
+typedef struct holo_norm_call {
+    holo_buffer_ref x;
+    holo_buffer_ref gamma;
+    holo_buffer_ref beta;
+    holo_buffer_ref residual;
+    holo_buffer_ref output;
+    uint32_t batch, feature, channels, num_groups;
+    uint64_t epsilon_bits;
+    uint8_t dtype;
+} holo_norm_call;
+
+/* RoPECall, kernel_call.rs:500-515 (rope_float, float_kernels.rs:3123-3186):
+ * rotate-half over heads of head_dim; cos/sin tables have x's element layout. */
+typedef struct holo_rope_call {
+    holo_buffer_ref x;
+    holo_buffer_ref cos;
+    holo_buffer_ref sin;
+    holo_buffer_ref output;
+    uint32_t head_dim;
+    uint64_t element_count;
+    uint8_t dtype;
+} holo_rope_call;
+
+/* GatherCall, kernel_call.rs:380-404 (gather, src/cpu/kernels.rs:389-447):
+ * out[o][k] = data[o][idx[k]] rows of `inner` elements; i32/i64 indices with
+ * negative wrap. An index out of range is a SlotOutOfRange(indices) error; the
+ * device reports it at the next holo_hip_synchronize (its row is zeroed). */
+typedef struct holo_gather_call {
+    holo_buffer_ref data;
+    holo_buffer_ref indices;
+    holo_buffer_ref output;
+    uint64_t outer, axis_dim, inner, num_indices;
+    uint8_t idx_dtype;
+    uint8_t dtype;
+} holo_gather_call;
+
+/* New (tag 124): per-row argmax, the greedy token pick of a decode step,
+ * kept on the device so the next step's Gather reads the ids in place.
+ * out[r] = the lowest index of the largest value of row r (NaN never wins;
+ * a row with no comparable value gives 0), as i32. input bf16 or f32
+ * [rows, cols]. */
+typedef struct holo_argmax_call {
+    holo_buffer_ref input;
+    holo_buffer_ref output;
+    uint32_t rows, cols;
+    uint8_t dtype;
+} holo_argmax_call;
 
 /* MatMulCall, kernel_call.rs:49-65. Row-major A[m,k] * B[k,n] -> C[m,n];
  * f32 or bf16 (fp32 accumulation, bf16 result narrowed by truncation,
@@ -150,6 +224,11 @@ typedef struct holo_kernel_call {
     uint32_t tag;
     union {
         holo_unary_call unary;
+        holo_binary_call binary;
+        holo_norm_call norm;
+        holo_rope_call rope;
+        holo_gather_call gather;
+        holo_argmax_call argmax;
         holo_matmul_call matmul;
         holo_kv_cache_write_call kv_write;
         holo_kv_quant_append_call kv_quant_append;
@@ -196,6 +275,54 @@ int holo_hip_decode_call(const uint8_t *wire, size_t len, holo_kernel_call *out,
 /* The 65536-entry table the backend stages in LDS for (act, dtype):
  * T[b] = narrow(f(widen(b))), src/cpu/lut.rs:43-67. */
 int holo_hip_lut_table(int act, int dtype, uint16_t *out65536);
+
+/* ---- Session: a `.holo` archive run over device-resident slots ----------
+ * The InferenceSession of crates/hologram-exec/src/session.rs (load :428-797,
+ * execute :846-932, the node walk compute_and_label :1052-1289) with this
+ * backend behind every node. Load checks the header, version 2..=3 and the
+ * BLAKE3 footer (crates/hologram-archive/src/loader.rs:141-185), decodes the
+ * KernelCalls, Inputs/Outputs, ExecPlan, Constants and Weights sections,
+ * uploads every constant once, and gives every other slot a device buffer.
+ * A KV write whose cache no other node reads runs as the in-place move
+ * (session.rs:1163-1190): its output port then aliases the cache buffer. */
+typedef struct holo_session holo_session;
+
+/* be == NULL loads dry: the archive is parsed, sized and every call validated,
+ * but nothing is allocated and the session cannot execute (host-only checks). */
+int holo_hip_session_load(holo_backend *be, const uint8_t *archive, size_t len,
+                          holo_session **out);
+int holo_hip_session_close(holo_session *s);
+int holo_hip_session_info(const holo_session *s, uint32_t *n_inputs, uint32_t *n_outputs,
+                          uint32_t *n_calls, uint32_t *n_slots);
+/* Port `index` of the inputs (is_output = 0) or outputs: its slot, element
+ * count, dtype tag and byte size. */
+int holo_hip_session_port(const holo_session *s, int is_output, uint32_t index, uint32_t *slot,
+                          uint64_t *element_count, uint8_t *dtype, uint64_t *bytes);
+/* The verified 32-byte footer fingerprint (HoloLoader::fingerprint). */
+int holo_hip_session_fingerprint(const holo_session *s, uint8_t out32[32]);
+/* Bind input port `index` to caller-owned device memory (zero copy, the
+ * execute_addressed form, session.rs:942-984); NULL restores the session's
+ * own buffer. */
+int holo_hip_session_bind_input(holo_session *s, uint32_t index, void *device_ptr, uint64_t bytes);
+/* Copy host bytes into input port `index`'s current buffer (the execute form). */
+int holo_hip_session_write_input(holo_session *s, uint32_t index, const void *host, uint64_t bytes);
+/* One walk of the plan, enqueued on the session's stream (asynchronous). */
+int holo_hip_session_execute(holo_session *s);
+/* Record the walk once into a HIP graph (after one eager walk), then replay it.
+ * Replay refuses if an input was rebound since the capture. */
+int holo_hip_session_capture(holo_session *s);
+int holo_hip_session_replay(holo_session *s);
+/* Wait for the session's stream; reports device-side refusals (Gather range). */
+int holo_hip_session_synchronize(holo_session *s);
+int holo_hip_session_stream(const holo_session *s, void **stream);
+/* Device view of output port `index`, or a host copy of it (waits first). */
+int holo_hip_session_output(const holo_session *s, uint32_t index, void **device_ptr,
+                            uint64_t *bytes);
+int holo_hip_session_read_output(holo_session *s, uint32_t index, void *host, uint64_t bytes);
+
+/* BLAKE3 (default mode, 32-byte digest): the archive footer and weight
+ * fingerprint hash (crates/hologram-archive/src/weight.rs WeightFingerprint). */
+int holo_hip_blake3(const void *data, size_t len, uint8_t out32[32]);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char *holo_hip_last_error_message(void);

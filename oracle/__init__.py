@@ -48,6 +48,12 @@ _SIGS = {
                                              _U32, _U32, _U32, _F, _U32]),
     "or_decode_attention_i8": (None, [_P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32,
                                       _F]),
+    "or_binary": (None, [ctypes.c_int, _P, _P, _P, _S, ctypes.c_int]),
+    "or_rms_norm": (ctypes.c_int, [_P, _P, _P, _U32, _U32, ctypes.c_uint64, ctypes.c_int]),
+    "or_rope": (ctypes.c_int, [_P, _P, _P, _P, _U32, _S, ctypes.c_int]),
+    "or_gather": (ctypes.c_int, [_P, _P, _P, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64,
+                                 ctypes.c_uint64, ctypes.c_int]),
+    "or_argmax": (None, [_P, _P, _U32, _U32, ctypes.c_int]),
     "or_matmul_ref_f64": (None, [_P, _P, _P, _S, _S, _S]),
     "or_max_rel_err": (ctypes.c_double, [_P, _P, _S]),
     # cpu_baseline.c (timing engines)

@@ -480,3 +480,105 @@ double or_max_rel_err(const float *got, const float *want, size_t n)
     }
     return worst;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Decode-step ops. Element access widens bf16 (exact) and narrows by       */
+/* truncation, as read_float / write_float do (src/cpu/dtype.rs:69-79).     */
+static float rd(const void *p, size_t i, int dtype)
+{
+    return dtype == OR_DTYPE_BF16 ? or_bf16_to_f32(((const uint16_t *)p)[i]) : ((const float *)p)[i];
+}
+
+static void wr(void *p, size_t i, float v, int dtype)
+{
+    if (dtype == OR_DTYPE_BF16)
+        ((uint16_t *)p)[i] = or_f32_to_bf16(v);
+    else
+        ((float *)p)[i] = v;
+}
+
+/* binary_float, src/cpu/float_kernels.rs:238-300 (scalar loop :290-298) */
+void or_binary(int op, const void *a, const void *b, void *out, size_t n, int dtype)
+{
+    for (size_t i = 0; i < n; ++i) {
+        const float va = rd(a, i, dtype), vb = rd(b, i, dtype);
+        wr(out, i, op == 0 ? va + vb : va * vb, dtype);
+    }
+}
+
+/* rms_norm_float generic path, src/cpu/float_kernels.rs:1737-1754;
+ * epsilon rule :1324-1336. Returns -1 for an invalid epsilon. */
+int or_rms_norm(const void *x, const void *gamma, void *out, uint32_t batch, uint32_t feature,
+                uint64_t epsilon_bits, int dtype)
+{
+    float eps = 1e-9f;
+    if (epsilon_bits != 0) {
+        eps = u2f((uint32_t)epsilon_bits);
+        if (!(isfinite(eps) && eps > 0.0f)) return -1;
+    }
+    for (uint32_t bi = 0; bi < batch; ++bi) {
+        const size_t row = (size_t)bi * feature;
+        float sumsq = 0.0f;
+        for (uint32_t j = 0; j < feature; ++j) {
+            const float v = rd(x, row + j, dtype);
+            sumsq += v * v;
+        }
+        const float inv_rms = 1.0f / sqrtf(sumsq / (float)feature + eps);
+        for (uint32_t j = 0; j < feature; ++j) {
+            const float g = gamma ? rd(gamma, j, dtype) : 1.0f;
+            wr(out, row + j, rd(x, row + j, dtype) * inv_rms * g, dtype);
+        }
+    }
+    return 0;
+}
+
+/* rope_float scalar path, src/cpu/float_kernels.rs:3171-3184 */
+int or_rope(const void *x, const void *cs, const void *sn, void *out, uint32_t head_dim, size_t n,
+            int dtype)
+{
+    if (head_dim == 0 || head_dim % 2 != 0 || n % head_dim != 0) return -1;
+    const size_t half = head_dim / 2;
+    for (size_t e = 0; e < n; ++e) {
+        const size_t pos = e % head_dim, base = e - pos;
+        const float xe = rd(x, e, dtype), ce = rd(cs, e, dtype), se = rd(sn, e, dtype);
+        const float v = pos < half ? xe * ce - rd(x, base + pos + half, dtype) * se
+                                   : xe * ce + rd(x, base + pos - half, dtype) * se;
+        wr(out, e, v, dtype);
+    }
+    return 0;
+}
+
+/* gather, src/cpu/kernels.rs:389-447 (rows of row_bytes). 0 ok, -1 an index
+ * is out of range (the reference's SlotOutOfRange(indices)). */
+int or_gather(const uint8_t *data, const void *idx, uint8_t *out, uint64_t outer,
+              uint64_t axis_dim, uint64_t row_bytes, uint64_t num_idx, int idx_i64)
+{
+    for (uint64_t o = 0; o < outer; ++o)
+        for (uint64_t k = 0; k < num_idx; ++k) {
+            int64_t i = idx_i64 ? ((const int64_t *)idx)[k] : (int64_t)((const int32_t *)idx)[k];
+            if (i < 0) i += (int64_t)axis_dim;
+            if (i < 0 || (uint64_t)i >= axis_dim) return -1;
+            memcpy(out + (o * num_idx + k) * row_bytes, data + (o * axis_dim + (uint64_t)i) * row_bytes,
+                   row_bytes);
+        }
+    return 0;
+}
+
+/* argmax (new op 124): the lowest index of the largest value per row; NaN is
+ * never larger; a row with no comparable value gives 0. */
+void or_argmax(const void *in, int32_t *out, uint32_t rows, uint32_t cols, int dtype)
+{
+    for (uint32_t r = 0; r < rows; ++r) {
+        int best_i = -1;
+        float best = 0.0f;
+        for (uint32_t j = 0; j < cols; ++j) {
+            const float v = rd(in, (size_t)r * cols + j, dtype);
+            if (v != v) continue;
+            if (best_i < 0 || v > best) {
+                best = v;
+                best_i = (int)j;
+            }
+        }
+        out[r] = best_i < 0 ? 0 : best_i;
+    }
+}

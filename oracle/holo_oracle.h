@@ -23,6 +23,13 @@
  *   or_kv_cache_write .......... closed form (ring placement, brute force)
  *   or_decode_attention_* ...... f64 softmax closed form, zero-visible row = 0
  *   or_matmul_ref_f64 .......... closed form (identity / permutation products)
+ *   or_binary .................. closed form (f32 add/mul then truncation,
+ *                                 numpy float32 arithmetic on the same inputs)
+ *   or_rms_norm ................ f64 closed form within 2 bf16 ulp; unit rows
+ *   or_rope .................... f64 rotation of each pair (cos/sin of an angle
+ *                                 preserve the pair's norm); angle 0 = identity
+ *   or_gather .................. brute-force row indexing, negative wrap
+ *   or_argmax .................. numpy argmax (NaN-free rows), first-index ties
  */
 #ifndef HOLO_ORACLE_H
 #define HOLO_ORACLE_H
@@ -95,6 +102,21 @@ void or_decode_attention_i8(const float *q, const int8_t *kq, const float *ks,
                             const int8_t *vq, const float *vs, const uint32_t *lens,
                             float *out, uint32_t B, uint32_t H, uint32_t Hkv,
                             uint32_t bucket, uint32_t D, float scale);
+
+/* ---- decode-step ops (bf16 or f32 operands) ---- */
+/* binary_float, src/cpu/float_kernels.rs:238-300: op 0 = Add, 1 = Mul */
+void or_binary(int op, const void *a, const void *b, void *out, size_t n, int dtype);
+/* rms_norm_float generic path, float_kernels.rs:1683-1755 (gamma NULL: none) */
+int or_rms_norm(const void *x, const void *gamma, void *out, uint32_t batch, uint32_t feature,
+                uint64_t epsilon_bits, int dtype);
+/* rope_float scalar path, float_kernels.rs:3123-3186 */
+int or_rope(const void *x, const void *cs, const void *sn, void *out, uint32_t head_dim, size_t n,
+            int dtype);
+/* gather, src/cpu/kernels.rs:389-447; -1 = index out of range */
+int or_gather(const uint8_t *data, const void *idx, uint8_t *out, uint64_t outer,
+              uint64_t axis_dim, uint64_t row_bytes, uint64_t num_idx, int idx_i64);
+/* argmax (new op 124) */
+void or_argmax(const void *in, int32_t *out, uint32_t rows, uint32_t cols, int dtype);
 
 /* ---- MatMul references: tests/conformance.rs:100-144 ---- */
 void or_matmul_ref_f64(const float *a, const float *b, float *out,

@@ -1,0 +1,163 @@
+"""`.holo` archives on the host: BLAKE3, the writer, the library's reader
+(dry session load) and the oracle's independent reader, and the wire codec
+of the decode-step ops (crates/hologram-archive/src/{writer,loader,
+kernel_codec,constant_codec}.rs). No GPU needed."""
+import struct
+
+import numpy as np
+import pytest
+
+from hologram_amd import (DTYPE_BF16, DTYPE_F32, DTYPE_I32, ArgMaxCall, BinaryCall, BufferRef,
+                          ConstantEntry, GatherCall, HipSession, HoloWriter, KernelCall,
+                          MatMulCall, NormCall, PortDescriptor, RoPECall, UnsupportedOp,
+                          DispatchError, SlotOutOfRange, blake3, decode_call, validate)
+from hologram_amd.decoder_graph import DecoderConfig, build_decode_step, init_weights
+from oracle.blake3_ref import blake3 as blake3_py
+from oracle.graph import OracleSession
+
+# Known-answer vectors of the BLAKE3 specification (default hash, 32 bytes):
+# the empty input, "abc", and the official test-vector inputs (byte i = i % 251)
+# of lengths 1, 1024 (one full chunk), 1025 and 2048 (two chunks).
+KAT = {
+    b"": "af1349b9f5f9a1a6a0404dea36dcc9499bcb25c9adc112b7cc9a93cae41f3262",
+    b"abc": "6437b3ac38465133ffb63b75273a8db548c558465d79db03fd359c6cd5bd9d85",
+}
+KAT_TV = {
+    1: "2d3adedff11b61f14c886e35afa036736dcd87a74d27b5c1510225d0f592e213",
+    1024: "42214739f095a406f3fc83deb889744ac00df831c10daa55189b5d121c855af7",
+    1025: "d00278ae47eb27b34faecf67b4fe263f82d5412916c1ffd97c8cb7fb814b8444",
+    2048: "e776b6028c7cd22a4d0ba182a8bf62205d2ef576467e838ed6f2529b85fba24a",
+}
+
+
+def tv(n):
+    return bytes((np.arange(n) % 251).astype(np.uint8))
+
+
+def test_blake3_known_answers():
+    for msg, hexd in KAT.items():
+        assert blake3(msg).hex() == hexd and blake3_py(msg).hex() == hexd
+    for n, hexd in KAT_TV.items():
+        assert blake3(tv(n)).hex() == hexd and blake3_py(tv(n)).hex() == hexd
+
+
+def test_blake3_tree_fold_matches_recursive_definition():
+    """The library folds chunk values with the incremental stack (and threads);
+    the restatement uses the recursive left-complete tree. Lengths cover 1..17
+    chunks and a deep tree; a one-byte change flips the digest."""
+    rng = np.random.default_rng(3)
+    for n in list(range(0, 64 * 1024 + 1, 1024 - 7)) + [1023, 3073, 8193, 100003]:
+        data = rng.integers(0, 256, n, dtype=np.uint8).tobytes()
+        assert blake3(data) == blake3_py(data), n
+    big = rng.integers(0, 256, (4 << 20) + 1000, dtype=np.uint8)   # threaded path
+    digest = blake3(big)
+    assert digest == blake3_py(big.tobytes())
+    big[123457] ^= 1
+    assert blake3(big) != digest
+
+
+def small_archive():
+    w = HoloWriter()
+    w.inputs = [PortDescriptor("a", 0, 16, DTYPE_F32, [16])]
+    w.outputs = [PortDescriptor("out", 2, 16, DTYPE_F32, [16])]
+    body = np.arange(16, dtype=np.float32).tobytes()
+    w.constants = [ConstantEntry(1, DTYPE_F32, body, by_reference=True),
+                   ConstantEntry(3, DTYPE_F32, body, by_reference=False)]
+    w.kernel_calls = [KernelCall.Add(BinaryCall(BufferRef(0, 0, 64), BufferRef(1, 0, 64),
+                                                BufferRef(2, 0, 64), 16, 32, DTYPE_F32))]
+    w.exec_plan = [[0]]
+    return w.finish()
+
+
+def test_writer_layout_and_footer():
+    a = small_archive()
+    assert a[:4] == b"HOLO" and struct.unpack_from("<HHH", a, 4)[0] == 3
+    assert blake3(a[:-32]) == a[-32:]
+    o = OracleSession(a)
+    assert [p["name"] for p in o.inputs] == ["a"] and o.outputs[0]["slot"] == 2
+    assert o.plan == [[0]] and o.calls[0][0] == 5
+    s = HipSession(None, a)                       # the library's reader, dry
+    assert len(s.inputs) == 1 and s.outputs[0].slot == 2 and s.n_calls == 1
+    assert s.fingerprint() == a[-32:]
+    bad = bytearray(a)
+    bad[40] ^= 1
+    with pytest.raises(DispatchError):
+        HipSession(None, bytes(bad))
+    with pytest.raises(ValueError):
+        OracleSession(bytes(bad))
+
+
+def test_weights_are_deduplicated_and_checked():
+    w = HoloWriter()
+    body = bytes(range(256))
+    w.constants = [ConstantEntry(0, DTYPE_F32, body), ConstantEntry(1, DTYPE_F32, body)]
+    w.kernel_calls = [KernelCall.Add(BinaryCall(BufferRef(0, 0, 256), BufferRef(1, 0, 256),
+                                                BufferRef(2, 0, 256), 64, 32, DTYPE_F32))]
+    a = w.finish()
+    assert a.count(body) == 1                    # one Weights entry for both constants
+    HipSession(None, a)
+    # corrupt the weight body and re-seal the footer: the fingerprint check refuses
+    bad = bytearray(a[:-32])
+    i = bytes(bad).index(body)
+    bad[i] ^= 0xFF
+    with pytest.raises(DispatchError):
+        HipSession(None, bytes(bad) + blake3(bytes(bad)))
+
+
+def test_dry_session_refuses_execute():
+    s = HipSession(None, small_archive())
+    from hologram_amd import InitError
+    with pytest.raises(InitError):
+        s.run()
+
+
+def decode_step_cfg():
+    return DecoderConfig(layers=2, hidden=128, heads=4, kv_heads=2, head_dim=64, ffn=256,
+                         vocab=300, batch=2, bucket=64)
+
+
+def test_decoder_archive_loads_dry_with_in_place_caches():
+    cfg = decode_step_cfg()
+    a = build_decode_step(cfg, init_weights(cfg, seed=1))
+    s = HipSession(None, a)
+    assert len(s.inputs) == 7 + 4 * cfg.layers and len(s.outputs) == 2 + 4 * cfg.layers
+    o = OracleSession(a)
+    assert len(o.calls) == s.n_calls == 1 + 18 * cfg.layers + 3
+
+
+@pytest.mark.parametrize("call", [
+    KernelCall.Add(BinaryCall(BufferRef(1, 8, 24), BufferRef(2), BufferRef(3), 7, 16, DTYPE_BF16)),
+    KernelCall.Mul(BinaryCall(BufferRef(1), BufferRef(2), BufferRef(3), 9, 32, DTYPE_F32)),
+    KernelCall.RmsNorm(NormCall(BufferRef(1), BufferRef(2), BufferRef(3), 4, 64, 0x3727C5AC,
+                                DTYPE_BF16)),
+    KernelCall.RotaryEmbedding(RoPECall(BufferRef(1), BufferRef(2), BufferRef(3), BufferRef(4),
+                                        64, 640, DTYPE_BF16)),
+    KernelCall.Gather(GatherCall(BufferRef(1), BufferRef(2), BufferRef(3), 1, 300, 128, 2,
+                                 DTYPE_I32, DTYPE_BF16)),
+    KernelCall.ArgMax(ArgMaxCall(BufferRef(1), BufferRef(2), 2, 300, DTYPE_BF16)),
+])
+def test_wire_codec_round_trip(call):
+    wire = call.encode()
+    c, used = decode_call(wire + b"\xAA\xBB")
+    assert used == len(wire) and c.tag == call.tag
+    kc = call.to_c()
+    assert bytes(c) == bytes(kc)
+
+
+def test_decode_step_refusals():
+    sizes = [1 << 20] * 8
+    with pytest.raises(UnsupportedOp):           # odd head_dim (float_kernels.rs:3126-3131)
+        validate(KernelCall.RotaryEmbedding(RoPECall(BufferRef(1), BufferRef(2), BufferRef(3),
+                                                     BufferRef(4), 63, 630, DTYPE_BF16)), sizes)
+    with pytest.raises(UnsupportedOp):           # negative epsilon (:1324-1336)
+        validate(KernelCall.RmsNorm(NormCall(BufferRef(1), BufferRef(2), BufferRef(3), 1, 8,
+                                             0xBF800000, DTYPE_F32)), sizes)
+    with pytest.raises(SlotOutOfRange):          # index dtype (kernels.rs:399-403)
+        validate(KernelCall.Gather(GatherCall(BufferRef(1), BufferRef(2), BufferRef(3), 1, 10, 4,
+                                              2, 8, DTYPE_F32)), sizes)
+    with pytest.raises(SlotOutOfRange):          # output overlaps an input
+        validate(KernelCall.Add(BinaryCall(BufferRef(1), BufferRef(2), BufferRef(1), 8, 32,
+                                           DTYPE_F32)), sizes)
+    with pytest.raises(SlotOutOfRange):          # short operand
+        validate(KernelCall.MatMul(MatMulCall(BufferRef(1, 0, 64), BufferRef(2), BufferRef(3),
+                                              8, 8, 8, DTYPE_F32)), sizes)

@@ -1,13 +1,14 @@
 """Benchmark of the MI355X hot path on one GPU; prints ONE JSON line.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only attn,lut,kv,gemm]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only attn,lut,kv,gemm,e2e]
 
 Headline (`value`): int8-KV GQA decode attention
 (B=32, H=32, Hkv=8, D=128, ragged L_b ~ U[512, 32768], bucket 32768, Q bf16,
 cache filled by the int8 quantize+append op) in tokens/s = B / step time.
 A step is one DecodeAttentionI8 dispatch over the whole batch, inputs
 resident in HBM. The other configs are reported under "components":
-LUT Gelem/s (config 1), GEMM TFLOP/s (config 2), KV append (config 3).
+LUT Gelem/s (config 1), GEMM TFLOP/s (config 2), KV append (config 3) and the
+end-to-end decoder through the `.holo` session (config 5, decode/prefill tok/s).
 Every number comes from HIP events on the stream the kernels run on: per step
 for the headline, and around a batch of back-to-back calls for the components
 (queued_ms), whose kernels are short enough that per-call events would count
@@ -57,7 +58,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--only", default="attn,lut,kv,gemm")
+    p.add_argument("--only", default="attn,lut,kv,gemm,e2e")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--seed", type=int, default=1234)
     return p.parse_args()
@@ -339,6 +340,113 @@ def bench_gemm(torch, be, args, rep):
     return res
 
 
+# --------------------------------------------------------------- config 5 ----
+class _DevBytes:
+    """A device range as a torch uint8 tensor (CUDA array interface)."""
+
+    def __init__(self, ptr, nbytes):
+        self.__cuda_array_interface__ = {"shape": (nbytes,), "typestr": "|u1",
+                                         "data": (ptr, False), "version": 2}
+
+
+def bench_e2e(torch, be, args, rep):
+    """Config 5: the Llama-style ~1B decoder as a `.holo` decode-step archive run
+    through HipSession (memo off: every step a fresh walk), the walk captured once
+    into a HIP graph and replayed per step. Batch 8, random 512-token prompts
+    (prefilled one position per step through the same step graph), then greedy
+    decode of 256 tokens; the next-token ids never leave the device (ArgMax
+    writes the buffer the next step's Gather reads)."""
+    import numpy as np
+    from hologram_amd import HipSession
+    from hologram_amd.decoder_graph import (DecoderConfig, build_decode_step, init_weights,
+                                            rope_tables)
+    cfg = DecoderConfig()
+    prompt_len, gen_len = 512, 256
+    B, H, Hkv, Dh, V = cfg.batch, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.vocab
+    t0 = time.perf_counter()
+    archive = build_decode_step(cfg, init_weights(cfg, seed=args.seed + 5))
+    t_build = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    sess = HipSession(be, archive)
+    t_load = time.perf_counter() - t0
+    archive_bytes = len(archive)
+    del archive
+    stream = sess.stream()
+    ext = torch.cuda.ExternalStream(stream)
+    npos = prompt_len + gen_len
+    dev = lambda b: torch.frombuffer(bytearray(b), dtype=torch.uint8).cuda()
+    cq, sq = (dev(t).view(npos, -1) for t in rope_tables(cfg, np.arange(npos), H))
+    ck, sk = (dev(t).view(npos, -1) for t in rope_tables(cfg, np.arange(npos), Hkv))
+    pos_tab = torch.arange(npos, dtype=torch.int32, device="cuda").view(npos, 1)
+    lens_tab = (torch.arange(npos, dtype=torch.int32, device="cuda") + 1).view(npos, 1).repeat(1, B)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed + 6)
+    prompt = torch.randint(0, V, (prompt_len, B), generator=gen, device="cuda", dtype=torch.int32)
+    # step inputs: tokens live in the ArgMax output buffer; the rest in tensors
+    tptr, tbytes = sess.output_ptr(0)
+    tok = torch.as_tensor(_DevBytes(tptr, tbytes), device="cuda").view(torch.int32)
+    sess.bind_input(0, (tptr, tbytes))
+    bufs = [torch.empty(1, dtype=torch.int32, device="cuda"),
+            torch.empty(B, dtype=torch.int32, device="cuda"),
+            torch.empty_like(cq[0]), torch.empty_like(sq[0]), torch.empty_like(ck[0]),
+            torch.empty_like(sk[0])]
+    for i, t in enumerate(bufs):
+        sess.bind_input(1 + i, t)
+    torch.cuda.synchronize()
+
+    def set_step(p):
+        with torch.cuda.stream(ext):
+            if p < prompt_len:
+                tok.copy_(prompt[p], non_blocking=True)
+            for dst, src in zip(bufs, (pos_tab[p], lens_tab[p], cq[p], sq[p], ck[p], sk[p])):
+                dst.copy_(src, non_blocking=True)
+
+    set_step(0)
+    torch.cuda.synchronize()
+    sess.capture()                 # runs step 0 eagerly, then records the walk
+    sess.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    with torch.cuda.stream(ext):
+        ev[0].record()
+    for p in range(1, npos):
+        if p == prompt_len:
+            with torch.cuda.stream(ext):
+                ev[1].record()
+        set_step(p)
+        sess.replay()
+    with torch.cuda.stream(ext):
+        ev[2].record()
+    sess.synchronize()
+    torch.cuda.synchronize()
+    prefill_ms = ev[0].elapsed_time(ev[1])
+    decode_ms = ev[1].elapsed_time(ev[2])
+    last = tok.cpu().tolist()
+    sess.close()
+    Dm, F = cfg.hidden, cfg.ffn
+    w_bytes = 2 * (cfg.layers * (Dm * H * Dh + 2 * Dm * Hkv * Dh + H * Dh * Dm + 3 * Dm * F
+                                 + 2 * Dm) + Dm * V + Dm)
+    mean_len = prompt_len + gen_len / 2
+    kv_bytes = cfg.layers * B * Hkv * mean_len * (2 * Dh + 8)
+    step_ms = decode_ms / gen_len
+    res = {
+        "decode_tok_s": B * gen_len / (decode_ms / 1e3),
+        "prefill_tok_s": B * (prompt_len - 1) / (prefill_ms / 1e3),
+        "decode_ms_per_step": step_ms,
+        "prefill_ms_per_step": prefill_ms / (prompt_len - 1),
+        "kernels_per_step": sess.n_calls,
+        "alg_bytes_per_decode_step": int(w_bytes + kv_bytes),
+        "hbm_gbs": (w_bytes + kv_bytes) / (step_ms / 1e3) / 1e9,
+        "archive_bytes": archive_bytes, "build_s": t_build, "load_s": t_load,
+        "last_tokens": last,
+        "config": {"layers": cfg.layers, "hidden": Dm, "heads": H, "kv_heads": Hkv,
+                   "head_dim": Dh, "ffn": F, "vocab": V, "batch": B, "prompt": prompt_len,
+                   "generate": gen_len, "bucket": cfg.bucket, "kv": "int8",
+                   "weights": "bf16 ~ N(0, 0.02), seeded", "vocab_note": "32,000 assumed"},
+    }
+    rep["e2e"] = res
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -365,6 +473,9 @@ def main():
         torch.cuda.empty_cache()
     if "gemm" in only:
         bench_gemm(torch, be, args, rep)
+        torch.cuda.empty_cache()
+    if "e2e" in only:
+        bench_e2e(torch, be, args, rep)
     be.close()
 
     attn = rep.get("attn")
@@ -407,6 +518,11 @@ def main():
     if attn:
         comps["decode_attn_i8"] = {k: attn[k] for k in ("tok_s", "hbm_gbs", "ms", "gflops",
                                                         "wall_ms_per_step")}
+    if "e2e" in rep:
+        e = dict(rep["e2e"])
+        e["roofline"] = roofline("hbm", e["hbm_gbs"], HBM_PEAK_GBS, "GB/s", None,
+                                 "whole decode step (weights + int8 KV per step)")
+        comps["e2e_decoder_1b"] = e
     comps["timing"] = ("headline: HIP events per step; components: HIP events around "
                        "back-to-back calls queued behind a spin kernel (GPU time per call)")
     line["components"] = comps

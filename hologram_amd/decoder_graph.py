@@ -68,20 +68,31 @@ def bf16_bytes(a: np.ndarray) -> bytes:
 
 
 def init_weights(cfg: DecoderConfig, seed: int, std: float = 0.02) -> dict:
-    """Random-init bf16 weights ~ N(0, std) (norm gains 1), as raw bf16 bytes."""
-    rng = np.random.default_rng(seed)
+    """Random-init bf16 weights ~ N(0, std) (norm gains 1), as raw bf16 bytes.
+    Each matrix draws from its own generator spawned from `seed` (so the
+    matrices can be drawn on several threads with the same result)."""
+    from concurrent.futures import ThreadPoolExecutor
     Dm, Hd, Kd = cfg.hidden, cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
-
-    def w(*shape):
-        return bf16_bytes(rng.standard_normal(shape, dtype=np.float32) * std)
-
-    ones = bf16_bytes(np.ones(Dm, np.float32))
-    out = {"embedding": w(cfg.vocab, Dm), "final_norm": ones, "lm_head": w(Dm, cfg.vocab)}
+    shapes = [("embedding", (cfg.vocab, Dm)), ("lm_head", (Dm, cfg.vocab))]
     for layer in range(cfg.layers):
-        out[f"l{layer}"] = {
-            "attn_norm": ones, "wq": w(Dm, Hd), "wk": w(Dm, Kd), "wv": w(Dm, Kd), "wo": w(Hd, Dm),
-            "ffn_norm": ones, "wg": w(Dm, cfg.ffn), "wu": w(Dm, cfg.ffn), "wd": w(cfg.ffn, Dm),
-        }
+        shapes += [((layer, "wq"), (Dm, Hd)), ((layer, "wk"), (Dm, Kd)), ((layer, "wv"), (Dm, Kd)),
+                   ((layer, "wo"), (Hd, Dm)), ((layer, "wg"), (Dm, cfg.ffn)),
+                   ((layer, "wu"), (Dm, cfg.ffn)), ((layer, "wd"), (cfg.ffn, Dm))]
+    seeds = np.random.SeedSequence(seed).spawn(len(shapes))
+
+    def draw(i):
+        rng = np.random.default_rng(seeds[i])
+        return bf16_bytes(rng.standard_normal(shapes[i][1], dtype=np.float32) * np.float32(std))
+
+    with ThreadPoolExecutor(8) as ex:
+        mats = list(ex.map(draw, range(len(shapes))))
+    ones = bf16_bytes(np.ones(Dm, np.float32))
+    out = {"final_norm": ones}
+    for (key, _), m in zip(shapes, mats):
+        if isinstance(key, tuple):
+            out.setdefault(f"l{key[0]}", {"attn_norm": ones, "ffn_norm": ones})[key[1]] = m
+        else:
+            out[key] = m
     return out
 
 

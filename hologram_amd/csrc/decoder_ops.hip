@@ -102,6 +102,59 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const void *__restrict__ x
     }
 }
 
+// RmsNorm for bf16 rows of feature % 8 == 0, feature <= 8 * 256 * 4: one
+// workgroup per row, every 16-byte vector of x and gamma loaded once, up
+// front, and kept in registers through the reduction.
+__global__ __launch_bounds__(256) void rmsnorm_bf16_vec_kernel(const uint16_t *__restrict__ x,
+                                                               const uint16_t *__restrict__ gamma,
+                                                               uint16_t *__restrict__ out,
+                                                               uint32_t feature, float eps) {
+    constexpr int kMaxVec = 4;
+    __shared__ float part[4];
+    const uint32_t nv = feature / 8;
+    const u32x4 *xr = reinterpret_cast<const u32x4 *>(x + uint64_t(blockIdx.x) * feature);
+    const u32x4 *gr = reinterpret_cast<const u32x4 *>(gamma);
+    u32x4 xv[kMaxVec], gv[kMaxVec];
+#pragma unroll
+    for (int u = 0; u < kMaxVec; ++u) {
+        const uint32_t v = threadIdx.x + 256u * u;
+        if (v < nv) {
+            xv[u] = xr[v];
+            gv[u] = gamma ? gr[v] : u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+        }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kMaxVec; ++u)
+        if (threadIdx.x + 256u * u < nv)
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float lo = __uint_as_float(xv[u][w] << 16), hi = __uint_as_float(xv[u][w] & 0xFFFF0000u);
+                ss = fmaf(lo, lo, ss);
+                ss = fmaf(hi, hi, ss);
+            }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float inv = 1.0f / sqrtf((part[0] + part[1] + part[2] + part[3]) / float(feature) + eps);
+    u32x4 *orow = reinterpret_cast<u32x4 *>(out + uint64_t(blockIdx.x) * feature);
+#pragma unroll
+    for (int u = 0; u < kMaxVec; ++u) {
+        const uint32_t v = threadIdx.x + 256u * u;
+        if (v >= nv) continue;
+        u32x4 r;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float lo = (__uint_as_float(xv[u][w] << 16) * inv) * __uint_as_float(gv[u][w] << 16);
+            const float hi = (__uint_as_float(xv[u][w] & 0xFFFF0000u) * inv) *
+                             __uint_as_float(gv[u][w] & 0xFFFF0000u);
+            r[w] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+        }
+        orow[v] = r;
+    }
+}
+
 // Rotary embedding, rotate-half form over heads of head_dim elements.
 template <bool kBf16>
 __global__ __launch_bounds__(256) void rope_kernel(const void *__restrict__ x,
@@ -153,20 +206,44 @@ __global__ __launch_bounds__(256) void gather_kernel(const uint8_t *__restrict__
 // its largest value, then a (value, index) reduction that prefers the lower
 // index on equal values. NaN never compares greater.
 template <bool kBf16>
-__global__ __launch_bounds__(256) void argmax_kernel(const void *__restrict__ in,
-                                                     int32_t *__restrict__ out, uint32_t cols) {
-    __shared__ float sv[4];
-    __shared__ int si[4];
+__global__ __launch_bounds__(1024) void argmax_kernel(const void *__restrict__ in,
+                                                      int32_t *__restrict__ out, uint32_t cols) {
+    constexpr int kW = 16;                       // wavefronts
+    constexpr int E = kBf16 ? 8 : 4;             // elements per 16-byte vector
+    __shared__ float sv[kW];
+    __shared__ int si[kW];
     const uint64_t row = uint64_t(blockIdx.x) * cols;
     float best = -INFINITY;
     int bi = -1;
-    for (uint32_t j = threadIdx.x; j < cols; j += 256) {
-        const float v = ld<kBf16>(in, row + j);
+    auto take = [&](float v, int j) {
         if (v > best || (bi < 0 && v == best)) {
             best = v;
-            bi = int(j);
+            bi = j;
         }
+    };
+    // 16-byte vectors when the row start is aligned; each thread's vectors are
+    // ascending in index, so a strict > keeps the first index of its maximum
+    const bool vec = ((reinterpret_cast<uintptr_t>(in) + row * (kBf16 ? 2 : 4)) & 15) == 0;
+    uint32_t j0 = 0;
+    if (vec) {
+        const u32x4 *r4 = reinterpret_cast<const u32x4 *>(static_cast<const char *>(in) +
+                                                          row * (kBf16 ? 2 : 4));
+        const uint32_t nv = cols / E;
+        for (uint32_t v = threadIdx.x; v < nv; v += 1024) {
+            const u32x4 x = r4[v];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                if constexpr (kBf16) {
+                    take(__uint_as_float(x[w] << 16), int(v * E + 2 * w));
+                    take(__uint_as_float(x[w] & 0xFFFF0000u), int(v * E + 2 * w + 1));
+                } else {
+                    take(__uint_as_float(x[w]), int(v * E + w));
+                }
+            }
+        }
+        j0 = nv * E;
     }
+    for (uint32_t j = j0 + threadIdx.x; j < cols; j += 1024) take(ld<kBf16>(in, row + j), int(j));
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
         const float ov = __shfl_xor(best, o, 64);
@@ -182,7 +259,7 @@ __global__ __launch_bounds__(256) void argmax_kernel(const void *__restrict__ in
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; ++w)
+        for (int w = 1; w < kW; ++w)
             if (si[w] >= 0 && (bi < 0 || sv[w] > best || (sv[w] == best && si[w] < bi))) {
                 best = sv[w];
                 bi = si[w];
@@ -220,6 +297,15 @@ hipError_t launch_binary(int op, const void *a, const void *b, void *out, uint64
 
 hipError_t launch_rmsnorm(const void *x, const void *gamma, void *out, uint32_t batch,
                           uint32_t feature, float eps, bool bf16, hipStream_t stream) {
+    const bool vec = bf16 && feature % 8 == 0 && feature <= 8 * 256 * 4 &&
+                     ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gamma) |
+                       reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+    if (vec) {
+        hipLaunchKernelGGL(rmsnorm_bf16_vec_kernel, dim3(batch), dim3(256), 0, stream,
+                           static_cast<const uint16_t *>(x), static_cast<const uint16_t *>(gamma),
+                           static_cast<uint16_t *>(out), feature, eps);
+        return hipGetLastError();
+    }
     if (bf16)
         hipLaunchKernelGGL((rmsnorm_kernel<true>), dim3(batch), dim3(256), 0, stream, x, gamma, out, feature, eps);
     else
@@ -255,9 +341,9 @@ hipError_t launch_gather(const void *data, const void *idx, void *out, uint64_t 
 hipError_t launch_argmax(const void *in, int32_t *out, uint32_t rows, uint32_t cols, bool bf16,
                          hipStream_t stream) {
     if (bf16)
-        hipLaunchKernelGGL((argmax_kernel<true>), dim3(rows), dim3(256), 0, stream, in, out, cols);
+        hipLaunchKernelGGL((argmax_kernel<true>), dim3(rows), dim3(1024), 0, stream, in, out, cols);
     else
-        hipLaunchKernelGGL((argmax_kernel<false>), dim3(rows), dim3(256), 0, stream, in, out, cols);
+        hipLaunchKernelGGL((argmax_kernel<false>), dim3(rows), dim3(1024), 0, stream, in, out, cols);
     return hipGetLastError();
 }
 

@@ -265,6 +265,17 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float *__restr
     }
 }
 
+int skinny_cus() {
+    static const int cus = [] {
+        int dev = 0, c = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
+            c = 256;
+        return c;
+    }();
+    return cus;
+}
+
 struct SkinnyPlan {
     int mt = 0, steps = 0;
     uint32_t kc = 0, ks = 0, strips = 0;
@@ -279,8 +290,18 @@ SkinnyPlan plan(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype) {
     const uint32_t es = bf16 ? 2 : 4;
     if (bf16 ? (n % 8 != 0 || k % 32 != 0) : (n % 4 != 0 || k % 16 != 0)) return p;
     p.mt = m <= 16 ? 1 : m <= 32 ? 2 : 4;
-    p.steps = bf16 ? (p.mt == 4 ? 2 : 4) : (p.mt == 4 ? 4 : 8);
-    p.kc = kWaves * p.steps * (bf16 ? 32 : 16);
+    p.strips = (n + (bf16 ? 127 : 63)) / (bf16 ? 128 : 64);
+    // k steps per wave: the most that still gives every CU two workgroups
+    // (a long K range per workgroup keeps its loads streaming; a short one
+    // fills the GPU when B is small)
+    const int kstep = bf16 ? 32 : 16;
+    const int max_steps = bf16 ? (p.mt == 4 ? 2 : 4) : (p.mt == 4 ? 4 : 8);
+    p.steps = max_steps;
+    while (p.steps > 1 &&
+           uint64_t(p.strips) * ((k + kWaves * p.steps * kstep - 1) / (kWaves * p.steps * kstep)) <
+               2u * uint64_t(skinny_cus()))
+        p.steps /= 2;
+    p.kc = kWaves * p.steps * kstep;
     // 32-bit buffer ranges: all of A, and KC rows of B (plus the out-of-range
     // column offset 2^31 on top of a row offset)
     if (uint64_t(m) * k * es >= (1ull << 31) || uint64_t(p.kc) * n * es >= (1ull << 31)) {
@@ -288,7 +309,6 @@ SkinnyPlan plan(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype) {
         return p;
     }
     p.ks = (k + p.kc - 1) / p.kc;
-    p.strips = (n + (bf16 ? 127 : 63)) / (bf16 ? 128 : 64);
     if (p.ks > 65535 || p.strips > (1u << 31)) p.mt = 0;
     return p;
 }
@@ -315,20 +335,41 @@ hipError_t launch_matmul_skinny(const void *a, const void *b, void *c, uint32_t 
         const auto *A = static_cast<const uint16_t *>(a);
         const auto *B = static_cast<const uint16_t *>(b);
         auto *C = static_cast<uint16_t *>(c);
-        switch (p.mt) {
-            case 1: hipLaunchKernelGGL((skinny_bf16_kernel<1, 4>), grid, block, 0, stream, A, B, C, P, m, n, k); break;
-            case 2: hipLaunchKernelGGL((skinny_bf16_kernel<2, 4>), grid, block, 0, stream, A, B, C, P, m, n, k); break;
-            default: hipLaunchKernelGGL((skinny_bf16_kernel<4, 2>), grid, block, 0, stream, A, B, C, P, m, n, k); break;
+#define HOLO_SKINNY_BF16(MT, ST) hipLaunchKernelGGL((skinny_bf16_kernel<MT, ST>), grid, block, 0, stream, A, B, C, P, m, n, k)
+        if (p.mt == 1) {
+            if (p.steps == 4) HOLO_SKINNY_BF16(1, 4);
+            else if (p.steps == 2) HOLO_SKINNY_BF16(1, 2);
+            else HOLO_SKINNY_BF16(1, 1);
+        } else if (p.mt == 2) {
+            if (p.steps == 4) HOLO_SKINNY_BF16(2, 4);
+            else if (p.steps == 2) HOLO_SKINNY_BF16(2, 2);
+            else HOLO_SKINNY_BF16(2, 1);
+        } else {
+            if (p.steps == 2) HOLO_SKINNY_BF16(4, 2);
+            else HOLO_SKINNY_BF16(4, 1);
         }
+#undef HOLO_SKINNY_BF16
     } else {
         const auto *A = static_cast<const float *>(a);
         const auto *B = static_cast<const float *>(b);
         auto *C = static_cast<float *>(c);
-        switch (p.mt) {
-            case 1: hipLaunchKernelGGL((skinny_f32_kernel<1, 8>), grid, block, 0, stream, A, B, C, P, m, n, k); break;
-            case 2: hipLaunchKernelGGL((skinny_f32_kernel<2, 8>), grid, block, 0, stream, A, B, C, P, m, n, k); break;
-            default: hipLaunchKernelGGL((skinny_f32_kernel<4, 4>), grid, block, 0, stream, A, B, C, P, m, n, k); break;
+#define HOLO_SKINNY_F32(MT, ST) hipLaunchKernelGGL((skinny_f32_kernel<MT, ST>), grid, block, 0, stream, A, B, C, P, m, n, k)
+        if (p.mt == 1) {
+            if (p.steps == 8) HOLO_SKINNY_F32(1, 8);
+            else if (p.steps == 4) HOLO_SKINNY_F32(1, 4);
+            else if (p.steps == 2) HOLO_SKINNY_F32(1, 2);
+            else HOLO_SKINNY_F32(1, 1);
+        } else if (p.mt == 2) {
+            if (p.steps == 8) HOLO_SKINNY_F32(2, 8);
+            else if (p.steps == 4) HOLO_SKINNY_F32(2, 4);
+            else if (p.steps == 2) HOLO_SKINNY_F32(2, 2);
+            else HOLO_SKINNY_F32(2, 1);
+        } else {
+            if (p.steps == 4) HOLO_SKINNY_F32(4, 4);
+            else if (p.steps == 2) HOLO_SKINNY_F32(4, 2);
+            else HOLO_SKINNY_F32(4, 1);
         }
+#undef HOLO_SKINNY_F32
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.ks <= 1) return e;

@@ -1,7 +1,7 @@
 // lut.hip — bf16/f16 activation as a gather through the 65536-entry table
 // (the device form of unary_lut, crates/hologram-compute/src/cpu/lut.rs:76-98).
 //
-// One persistent workgroup per CU holds the whole 128 KiB table in LDS (gfx950
+// Large inputs: one persistent workgroup per CU holds the whole 128 KiB table in LDS (gfx950
 // gives a workgroup up to 160 KiB). Each thread first issues the 16-byte loads
 // of its first input vectors, then helps stage the table, so the table's L2
 // reads overlap the HBM reads; after the barrier it looks up 8 patterns per
@@ -80,6 +80,20 @@ __global__ __launch_bounds__(TPB) void lut_gather_kernel(const uint16_t *__restr
         out[e] = t[in[e]];
 }
 
+// Few elements: staging the 128 KiB table in LDS costs more than the whole
+// gather, and a persistent grid would be a handful of workgroups. Each thread
+// takes one 16-byte vector and looks its 8 patterns up in the table in global
+// memory (L2-resident after the first touches).
+__global__ __launch_bounds__(256) void lut_direct_kernel(const uint16_t *__restrict__ table,
+                                                         const uint16_t *__restrict__ in,
+                                                         uint16_t *__restrict__ out, uint64_t n,
+                                                         uint64_t nvec) {
+    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i < nvec) reinterpret_cast<u32x4 *>(out)[i] = look8(table, reinterpret_cast<const u32x4 *>(in)[i]);
+    const uint64_t e = nvec * 8 + i;              // the n % 8 tail, one element per thread
+    if (i < 8 && e < n) out[e] = table[in[e]];
+}
+
 int cu_count() {
     static const int cus = [] {
         int dev = 0, c = 0;
@@ -106,6 +120,9 @@ hipError_t launch(const uint16_t *table, const uint16_t *in, uint16_t *out, uint
 
 }  // namespace
 
+// Up to this many 16-byte vectors (2M elements) the direct kernel runs.
+constexpr uint64_t kDirectMaxVec = 256 * 1024;
+
 hipError_t launch_lut_u16(const uint16_t *table, const uint16_t *in, uint16_t *out, uint64_t n,
                           hipStream_t stream) {
     if (n == 0) return hipSuccess;
@@ -116,6 +133,11 @@ hipError_t launch_lut_u16(const uint16_t *table, const uint16_t *in, uint16_t *o
         const char *e = getenv("HOLO_LUT_CFG");
         return e ? atoi(e) : 0;
     }();
+    if (nvec && nvec <= kDirectMaxVec && cfg == 0) {
+        hipLaunchKernelGGL(lut_direct_kernel, dim3(unsigned((nvec + 255) / 256)), dim3(256), 0,
+                           stream, table, in, out, n, nvec);
+        return hipGetLastError();
+    }
     switch (cfg) {
         case 1: return launch<1024, 1>(table, in, out, n, nvec, stream);
         case 2: return launch<1024, 2>(table, in, out, n, nvec, stream);

@@ -14,8 +14,9 @@ from .backend import (BackendError, DeviceWorkspace, DispatchError, HipBackend, 
 from .kernel_call import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, DTYPE_I8, DTYPE_I32, DTYPE_I64,
                           NO_BUFFER, SLOT_ABSENT, ArgMaxCall, BinaryCall, BufferRef,
                           DecodeAttentionI8Call, GatherCall, KernelCall, KvCacheWriteCall,
-                          KvQuantAppendCall, MatMulCall, NormCall, RoPECall, UnaryCall,
-                          encode_calls, lut_act)
+                          KvQuantAppendCall, MatMulActivationCall, MatMulAddActivationCall,
+                          MatMulAddCall, MatMulCall, NormCall, RoPECall, UnaryCall, encode_calls,
+                          fused_activation, lut_act)
 from .archive import ConstantEntry, HoloWriter, PortDescriptor, blake3
 from .session import HipSession
 
@@ -25,6 +26,7 @@ __all__ = [
     "DTYPE_BF16", "DTYPE_F16", "DTYPE_F32", "DTYPE_I8", "DTYPE_I32", "DTYPE_I64",
     "NO_BUFFER", "SLOT_ABSENT", "ArgMaxCall", "BinaryCall", "BufferRef",
     "DecodeAttentionI8Call", "GatherCall", "KernelCall", "KvCacheWriteCall",
-    "KvQuantAppendCall", "MatMulCall", "NormCall", "RoPECall", "UnaryCall", "encode_calls",
+    "KvQuantAppendCall", "MatMulActivationCall", "MatMulAddActivationCall", "MatMulAddCall",
+    "MatMulCall", "NormCall", "RoPECall", "UnaryCall", "encode_calls", "fused_activation",
     "lut_act", "ConstantEntry", "HoloWriter", "PortDescriptor", "blake3", "HipSession",
 ]

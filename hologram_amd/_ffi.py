@@ -66,6 +66,18 @@ class MatMulCallC(ctypes.Structure):
                 ("dtype", ctypes.c_uint8), ("b_packed", ctypes.c_uint8)]
 
 
+class MatMulActCallC(ctypes.Structure):
+    _fields_ = [("mm", MatMulCallC), ("act", ctypes.c_uint8)]
+
+
+class MatMulAddCallC(ctypes.Structure):
+    _fields_ = [("mm", MatMulCallC), ("residual", BufferRefC)]
+
+
+class MatMulAddActCallC(ctypes.Structure):
+    _fields_ = [("mm", MatMulCallC), ("residual", BufferRefC), ("act", ctypes.c_uint8)]
+
+
 class KvCacheWriteCallC(ctypes.Structure):
     _fields_ = [("cache", BufferRefC), ("new_rows_buf", BufferRefC), ("pos", BufferRefC),
                 ("output", BufferRefC), ("planes", ctypes.c_uint32),
@@ -93,7 +105,9 @@ class DecodeAttentionI8CallC(ctypes.Structure):
 class CallUnion(ctypes.Union):
     _fields_ = [("unary", UnaryCallC), ("binary", BinaryCallC), ("norm", NormCallC),
                 ("rope", RopeCallC), ("gather", GatherCallC), ("argmax", ArgMaxCallC),
-                ("matmul", MatMulCallC), ("kv_write", KvCacheWriteCallC),
+                ("matmul", MatMulCallC), ("matmul_act", MatMulActCallC),
+                ("matmul_add", MatMulAddCallC), ("matmul_add_act", MatMulAddActCallC),
+                ("kv_write", KvCacheWriteCallC),
                 ("kv_quant_append", KvQuantAppendCallC), ("attn_i8", DecodeAttentionI8CallC)]
 
 
@@ -121,6 +135,10 @@ SIGNATURES = {
     "holo_hip_lut_table": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _P]),
     "holo_hip_session_load": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.c_size_t,
                                              ctypes.POINTER(_P)]),
+    "holo_hip_session_load_ex": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.c_size_t,
+                                                ctypes.c_uint32, ctypes.POINTER(_P)]),
+    "holo_hip_session_nodes": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_uint32),
+                                              ctypes.POINTER(ctypes.c_uint32)]),
     "holo_hip_session_close": (ctypes.c_int, [_P]),
     "holo_hip_session_info": (ctypes.c_int, [_P] + [ctypes.POINTER(ctypes.c_uint32)] * 4),
     "holo_hip_session_port": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_uint32,

@@ -1,0 +1,342 @@
+// epilogue.hip — the end of a few-row MatMul on the device: the fp32 split-K
+// partials of one launch (gemm_skinny.hip, launch_skinny_partials) summed in
+// ks order, narrowed, and finished per output segment with the ops that
+// consume the product in a decode step, so those ops cost no launch of their
+// own and their inputs never round-trip through HBM:
+//
+//   base      the product itself; + a residual (MatMulAdd, float_kernels.rs:
+//             846-888); an activation (MatMulActivation, :816-844; bf16 through
+//             the same 65536-entry table the standalone op uses, f32 through
+//             exp_f32_det as gelu_f/silu_f/sigmoid_f/tanh_f, :3537-3566); both
+//             (MatMulAddActivation, :890-935)
+//   rope      rotate-half rotary embedding of each head (rope_float, :3123-3186)
+//   quant     int8 quantize + ring append of each head row (quantize_row_i8,
+//             src/cpu/simd.rs:4755-4785; placement as kernels.rs:455-501)
+//   pair      the element-wise product with another segment's value
+//             (binary_float Mul, float_kernels.rs:238-300: SwiGLU's silu(g)*u)
+//
+// Every step is the same IEEE operation in the same order as the standalone
+// kernel it replaces (the partials summed sequentially in ks order as
+// skinny_reduce_kernel does, bf16 narrowed by truncation between ops), so a
+// fused walk gives the same bits as the unfused one.
+//
+// With ks == 0 the base value is read from `src` (the already-narrowed output
+// of a tiled MatMul) instead of partials: the in-place epilogue of a fused
+// MatMul call whose product took the tiled path.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+
+#include "holo_device.h"
+#include "holo_kernels.h"
+
+namespace holo {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
+__device__ __forceinline__ uint32_t f2bf(float f) { return __float_as_uint(f) >> 16; }
+
+// exp_f32_det (src/cpu/simd.rs:4191-4239): clamp, k = trunc(x*log2e +- 1/2),
+// Cody-Waite reduction, degree-6 Horner, scale by 2^k.
+__device__ float exp_det(float x) {
+    const float LO = -87.33654f, HI = 88.0f;
+    const float LOG2E = 1.44269504088896340736f;
+    const float LN2_HI = __uint_as_float(0x3F318000u);
+    const float LN2_LO = -2.1219444e-4f;
+    const float C6 = 1.0f / 720.0f, C5 = 1.0f / 120.0f, C4 = 1.0f / 24.0f, C3 = 1.0f / 6.0f,
+                C2 = 0.5f;
+    if (x != x || x < LO) return 0.0f;
+    if (x > HI) x = HI;
+    const float t = x * LOG2E;
+    const int32_t k = t >= 0.0f ? int32_t(t + 0.5f) : int32_t(t - 0.5f);
+    const float kf = float(k);
+    const float r = (x - kf * LN2_HI) - kf * LN2_LO;
+    float p = C6;
+    p = p * r + C5;
+    p = p * r + C4;
+    p = p * r + C3;
+    p = p * r + C2;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    uint32_t sb = uint32_t(k + 127) << 23;
+    if (sb > 0x7f000000u) sb = 0x7f000000u;
+    return p * __uint_as_float(sb);
+}
+
+// fused_activation ids (kernel_call.rs:861-870) served on f32.
+__device__ float act_f32(uint32_t act, float x) {
+    switch (act) {
+        case kFusedGelu: {
+            const float cube = ((0.044715f * x) * x) * x;
+            const float u = 0.7978846f * (x + cube);
+            const float e = exp_det(2.0f * u);
+            return (0.5f * x) * (1.0f + (e - 1.0f) / (e + 1.0f));
+        }
+        case kFusedSilu: return x * (1.0f / (1.0f + exp_det(-x)));
+        case kFusedSigmoid: return 1.0f / (1.0f + exp_det(-x));
+        case kFusedTanh: {
+            const float e = exp_det(2.0f * x);
+            return (e - 1.0f) / (e + 1.0f);
+        }
+        default: return x;
+    }
+}
+
+// Segment of this workgroup (workgroup-uniform, chosen with selects).
+__device__ __forceinline__ int pick(const EpiArgs &g, uint32_t *first_block) {
+    int s = 0;
+    uint32_t b0 = 0;
+#pragma unroll
+    for (int i = 1; i < kSkinnyMaxSeg; ++i)
+        if (uint32_t(i) < g.nseg && blockIdx.x >= g.blk_end[i - 1]) {
+            s = i;
+            b0 = g.blk_end[i - 1];
+        }
+    *first_block = b0;
+    return s;
+}
+
+// The product at (row m, column c) of P's column space: partials summed in
+// ks order (or the tiled output read back). Four partials in flight.
+template <bool kBf16>
+__device__ __forceinline__ float product(const EpiArgs &g, uint32_t m, uint32_t c) {
+    if (g.ks == 0) {
+        if constexpr (kBf16)
+            return bf2f(static_cast<const uint16_t *>(g.src)[uint64_t(m) * g.ntot + c]);
+        else
+            return static_cast<const float *>(g.src)[uint64_t(m) * g.ntot + c];
+    }
+    const uint64_t plane = uint64_t(g.m) * g.ntot;
+    const float *p = g.P + uint64_t(m) * g.ntot + c;
+    float s = p[0];
+    uint32_t k = 1;
+    for (; k + 4 <= g.ks; k += 4) {
+        const float v0 = p[k * plane], v1 = p[(k + 1) * plane], v2 = p[(k + 2) * plane],
+                    v3 = p[(k + 3) * plane];
+        s += v0;
+        s += v1;
+        s += v2;
+        s += v3;
+    }
+    for (; k < g.ks; ++k) s += p[k * plane];
+    return s;
+}
+
+// The same for Q*4 consecutive columns (c a multiple of 4), as 16-byte loads.
+template <bool kBf16, int Q>
+__device__ __forceinline__ void product_vec(const EpiArgs &g, uint32_t m, uint32_t c, float *v) {
+    if (g.ks == 0) {
+#pragma unroll
+        for (int j = 0; j < 4 * Q; ++j) v[j] = product<kBf16>(g, m, c + j);
+        return;
+    }
+    const uint64_t plane = uint64_t(g.m) * g.ntot / 4;
+    const f32x4 *p = reinterpret_cast<const f32x4 *>(g.P + uint64_t(m) * g.ntot + c);
+    f32x4 s[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) s[q] = p[q];
+    uint32_t k = 1;
+    for (; k + 4 <= g.ks; k += 4) {
+        f32x4 t[4][Q];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int q = 0; q < Q; ++q) t[u][q] = p[(k + u) * plane + q];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int q = 0; q < Q; ++q) s[q] += t[u][q];
+    }
+    for (; k < g.ks; ++k)
+#pragma unroll
+        for (int q = 0; q < Q; ++q) s[q] += p[k * plane + q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[4 * q + j] = s[q][j];
+}
+
+// The segment's base value from its product v (bf16: the result is a bf16
+// bit pattern widened back to f32, so later steps see exactly the stored value).
+template <bool kBf16>
+__device__ __forceinline__ float base_value(const EpiSeg &sg, float v, uint64_t e) {
+    if constexpr (kBf16) {
+        uint32_t x = f2bf(v);
+        if (sg.base == kEpiAct) x = sg.lut[x];   // f(widen(x)) narrowed: the table entry
+        if (sg.base == kEpiAdd || sg.base == kEpiAddAct) {
+            const float s = bf2f(x) + bf2f(static_cast<const uint16_t *>(sg.residual)[e]);
+            // MatMulAddActivation applies f to the f32 sum before narrowing
+            x = f2bf(sg.base == kEpiAddAct ? act_f32(sg.act, s) : s);
+        }
+        return bf2f(x);
+    } else {
+        if (sg.base == kEpiAdd || sg.base == kEpiAddAct)
+            v = v + static_cast<const float *>(sg.residual)[e];
+        if (sg.base == kEpiAct || sg.base == kEpiAddAct) v = act_f32(sg.act, v);
+        return v;
+    }
+}
+
+template <bool kBf16>
+__device__ __forceinline__ void store(void *p, uint64_t e, float v) {
+    if constexpr (kBf16)
+        static_cast<uint16_t *>(p)[e] = uint16_t(f2bf(v));
+    else
+        static_cast<float *>(p)[e] = v;
+}
+
+template <bool kBf16>
+__device__ __forceinline__ float load(const void *p, uint64_t e) {
+    if constexpr (kBf16)
+        return bf2f(static_cast<const uint16_t *>(p)[e]);
+    else
+        return static_cast<const float *>(p)[e];
+}
+
+// Rust's `f32 as i32` then clamp(-127, 127) (NaN -> 0, saturating).
+__device__ __forceinline__ int8_t to_q(float r) {
+    if (r != r) return 0;
+    r = r < -127.0f ? -127.0f : (r > 127.0f ? 127.0f : r);
+    return static_cast<int8_t>(static_cast<int32_t>(r));
+}
+
+// Element-wise segments: E consecutive columns of one row per thread.
+template <bool kBf16>
+__device__ void elem_segment(const EpiArgs &g, const EpiSeg &sg, const EpiSeg &pr, uint32_t blk) {
+    constexpr uint32_t E = kBf16 ? 8 : 4;
+    const uint64_t i = (uint64_t(blk) * 256 + threadIdx.x) * E;
+    if (i >= uint64_t(g.m) * sg.n) return;
+    const uint32_t m = uint32_t(i / sg.n), c = uint32_t(i % sg.n);
+    const uint64_t e0 = uint64_t(m) * sg.n + c;
+    float va[E], vb[E];
+    product_vec<kBf16, E / 4>(g, m, sg.col0 + c, va);
+    if (sg.pair >= 0) product_vec<kBf16, E / 4>(g, m, pr.col0 + c, vb);
+#pragma unroll
+    for (uint32_t j = 0; j < E; ++j) {
+        va[j] = base_value<kBf16>(sg, va[j], e0 + j);
+        if (sg.out) store<kBf16>(sg.out, e0 + j, va[j]);
+    }
+    if (sg.pair < 0) return;
+#pragma unroll
+    for (uint32_t j = 0; j < E; ++j) {
+        vb[j] = base_value<kBf16>(pr, vb[j], e0 + j);
+        if (pr.out) store<kBf16>(pr.out, e0 + j, vb[j]);
+        store<kBf16>(sg.mul_out, e0 + j, va[j] * vb[j]);
+    }
+}
+
+// Head-wise segments (rope and/or quant): a head of D = head_dim columns is
+// D/2 lanes, lane d holding the rotate-half pair (d, d + D/2).
+template <bool kBf16>
+__device__ void head_segment(const EpiArgs &g, const EpiSeg &sg, uint32_t blk) {
+    const uint32_t D = sg.head_dim, half = D / 2;
+    const uint32_t heads_per_block = 256 / half;
+    const uint32_t hl = threadIdx.x / half, d = threadIdx.x % half;
+    const uint32_t heads_row = sg.n / D;
+    const uint64_t head = uint64_t(blk) * heads_per_block + hl;
+    const bool live = head < uint64_t(g.m) * heads_row;
+    float x1 = 0.0f, x2 = 0.0f;
+    uint64_t e1 = 0;
+    if (live) {
+        const uint32_t m = uint32_t(head / heads_row), h = uint32_t(head % heads_row);
+        const uint32_t c1 = h * D + d;
+        e1 = uint64_t(m) * sg.n + c1;
+        x1 = base_value<kBf16>(sg, product<kBf16>(g, m, sg.col0 + c1), e1);
+        x2 = base_value<kBf16>(sg, product<kBf16>(g, m, sg.col0 + c1 + half), e1 + half);
+        if (sg.out) {
+            store<kBf16>(sg.out, e1, x1);
+            store<kBf16>(sg.out, e1 + half, x2);
+        }
+        if (sg.rope) {
+            const float c1v = load<kBf16>(sg.cos, e1), s1v = load<kBf16>(sg.sin, e1);
+            const float c2v = load<kBf16>(sg.cos, e1 + half), s2v = load<kBf16>(sg.sin, e1 + half);
+            float y1 = x1 * c1v - x2 * s1v;
+            float y2 = x2 * c2v + x1 * s2v;
+            if constexpr (kBf16) {
+                y1 = bf2f(f2bf(y1));
+                y2 = bf2f(f2bf(y2));
+            }
+            x1 = y1;
+            x2 = y2;
+            if (sg.rope_out) {
+                store<kBf16>(sg.rope_out, e1, x1);
+                store<kBf16>(sg.rope_out, e1 + half, x2);
+            }
+        }
+    }
+    if (!sg.quant) return;
+    // row max of |x| over the head's lanes (NaN never wins a `>`); exact, so
+    // the order of the reduction does not matter
+    float amax = 0.0f;
+    const float a1 = x1 < 0.0f ? -x1 : x1, a2 = x2 < 0.0f ? -x2 : x2;
+    if (a1 > amax) amax = a1;
+    if (a2 > amax) amax = a2;
+    for (uint32_t off = half / 2; off >= 1; off >>= 1) {
+        const float o = __shfl_xor(amax, int(off), 64);
+        if (o > amax) amax = o;
+    }
+    if (!live) return;
+    const uint64_t r = e1 / D;   // the row of the appended [planes, new_rows, D] block
+    const uint32_t plane = uint32_t(r / sg.new_rows), j = uint32_t(r % sg.new_rows);
+    const uint64_t pos = *sg.pos % sg.bucket;
+    const uint64_t row = uint64_t(plane) * sg.bucket + (pos + j) % sg.bucket;
+    int8_t *dst = sg.cq + row * D;
+    if (amax == 0.0f) {
+        dst[d] = 0;
+        dst[d + half] = 0;
+        if (d == 0) sg.cs[row] = 0.0f;
+        return;
+    }
+    const float inv = 127.0f / amax;
+    const float t1 = x1 * inv, t2 = x2 * inv;
+    dst[d] = to_q(t1 >= 0.0f ? truncf(t1 + 0.5f) : truncf(t1 - 0.5f));
+    dst[d + half] = to_q(t2 >= 0.0f ? truncf(t2 + 0.5f) : truncf(t2 - 0.5f));
+    if (d == 0) sg.cs[row] = amax / 127.0f;
+}
+
+template <bool kBf16>
+__global__ __launch_bounds__(256) void epilogue_kernel(const EpiArgs g) {
+    uint32_t b0;
+    const int s = pick(g, &b0);
+    const EpiSeg &sg = s == 0 ? g.seg[0] : s == 1 ? g.seg[1] : s == 2 ? g.seg[2] : g.seg[3];
+    const uint32_t blk = blockIdx.x - b0;
+    if (sg.head_dim) {
+        head_segment<kBf16>(g, sg, blk);
+    } else {
+        const int p = sg.pair < 0 ? 0 : sg.pair;
+        const EpiSeg &pr = p == 0 ? g.seg[0] : p == 1 ? g.seg[1] : p == 2 ? g.seg[2] : g.seg[3];
+        elem_segment<kBf16>(g, sg, pr, blk);
+    }
+}
+
+}  // namespace
+
+uint32_t epilogue_blocks(const EpiSeg &sg, uint32_t m, bool bf16) {
+    if (sg.skip) return 0;
+    if (sg.head_dim) {
+        const uint32_t heads_per_block = 256 / (sg.head_dim / 2);
+        const uint64_t heads = uint64_t(m) * (sg.n / sg.head_dim);
+        return uint32_t((heads + heads_per_block - 1) / heads_per_block);
+    }
+    const uint64_t threads = uint64_t(m) * sg.n / (bf16 ? 8 : 4);
+    return uint32_t((threads + 255) / 256);
+}
+
+hipError_t launch_epilogue(EpiArgs g, hipStream_t stream) {
+    if (g.nseg < 1 || g.nseg > uint32_t(kSkinnyMaxSeg)) return hipErrorInvalidValue;
+    uint32_t total = 0;
+    for (uint32_t i = 0; i < g.nseg; ++i) {
+        total += epilogue_blocks(g.seg[i], g.m, g.bf16);
+        g.blk_end[i] = total;
+    }
+    if (total == 0) return hipSuccess;
+    if (g.bf16)
+        hipLaunchKernelGGL(epilogue_kernel<true>, dim3(total), dim3(256), 0, stream, g);
+    else
+        hipLaunchKernelGGL(epilogue_kernel<false>, dim3(total), dim3(256), 0, stream, g);
+    return hipGetLastError();
+}
+
+}  // namespace holo

@@ -50,19 +50,57 @@ __device__ __forceinline__ u32x4 column8(const u32x4 *rows, int c) {
     return o;
 }
 
+// A launch covers one or more segments that share A: segment s owns its own
+// B [K, n_s] and output, and grid.x runs over the strips of every segment in
+// turn (strip_end is the running total). Partials of all segments share one
+// fp32 buffer [ks][M][ntot], segment s at columns col0_s.
+struct SkinnyArgs {
+    const void *a;
+    float *p;
+    uint32_t m, k, ntot, nseg;
+    uint32_t direct;                         // 1: one K range, narrow straight into c
+    uint32_t strip_end[kSkinnyMaxSeg];
+    const void *b[kSkinnyMaxSeg];
+    void *c[kSkinnyMaxSeg];
+    uint32_t n[kSkinnyMaxSeg], col0[kSkinnyMaxSeg];
+};
+
+// Segment of this workgroup and its first strip (workgroup-uniform, picked
+// from the kernel arguments with selects so nothing is indexed dynamically).
+struct SegPick {
+    const void *b;
+    void *c;
+    uint32_t n, col0, strip;
+};
+
+__device__ __forceinline__ SegPick pick_segment(const SkinnyArgs &g) {
+    const uint32_t bx = blockIdx.x;
+    SegPick r{g.b[0], g.c[0], g.n[0], g.col0[0], bx};
+#pragma unroll
+    for (int i = 1; i < kSkinnyMaxSeg; ++i)
+        if (uint32_t(i) < g.nseg && bx >= g.strip_end[i - 1]) {
+            r.b = g.b[i];
+            r.c = g.c[i];
+            r.n = g.n[i];
+            r.col0 = g.col0[i];
+            r.strip = bx - g.strip_end[i - 1];
+        }
+    return r;
+}
+
 // ---------------------------------------------------------------- bf16 ----
 // MT 16-row tiles of A, STEPS 32-deep k steps per wave: KC = 4 * STEPS * 32.
 template <int MT, int STEPS>
-__global__ __launch_bounds__(256) void skinny_bf16_kernel(const uint16_t *__restrict__ A,
-                                                          const uint16_t *__restrict__ B,
-                                                          uint16_t *__restrict__ C,
-                                                          float *__restrict__ P, uint32_t M,
-                                                          uint32_t N, uint32_t K) {
+__global__ __launch_bounds__(256) void skinny_bf16_kernel(const SkinnyArgs g) {
     constexpr uint32_t KC = kWaves * STEPS * 32;
     __shared__ f32x4 red[kWaves - 1][MT][8][64];
+    const SegPick sg = pick_segment(g);
+    const uint16_t *__restrict__ A = static_cast<const uint16_t *>(g.a);
+    const uint16_t *__restrict__ B = static_cast<const uint16_t *>(sg.b);
+    const uint32_t M = g.m, N = sg.n, K = g.k;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63, g = lane >> 4, q = lane & 15;
-    const uint32_t n0 = blockIdx.x * 128 + 8 * q;
+    const int lane = threadIdx.x & 63, grp = lane >> 4, q = lane & 15;
+    const uint32_t n0 = sg.strip * 128 + 8 * q;
     const uint32_t kb0 = blockIdx.y * KC;
     const uint32_t krows = K - kb0 < KC ? K - kb0 : KC;
     // This workgroup's rows of B as one buffer range; columns past N are sent
@@ -76,14 +114,14 @@ __global__ __launch_bounds__(256) void skinny_bf16_kernel(const uint16_t *__rest
     for (int t = 0; t < STEPS; ++t) {
         const uint32_t kr = uint32_t(t * kWaves + w) * 32;   // step start within the range
         if (kr < krows) {
-            const uint32_t vo = bcol + (kr + 8 * g) * N * 2u;
+            const uint32_t vo = bcol + (kr + 8 * grp) * N * 2u;
 #pragma unroll
             for (int r = 0; r < 8; ++r)
                 b[t][r] = __builtin_amdgcn_raw_buffer_load_b128(rb, vo, int(N * 2u) * r, 0);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
                 a[t][mt] = __builtin_amdgcn_raw_buffer_load_b128(
-                    ra, ((mt * 16 + q) * K + kb0 + kr + 8 * g) * 2u, 0, 0);
+                    ra, ((mt * 16 + q) * K + kb0 + kr + 8 * grp) * 2u, 0, 0);
         }
     }
     f32x4 acc[MT][8];
@@ -122,23 +160,23 @@ __global__ __launch_bounds__(256) void skinny_bf16_kernel(const uint16_t *__rest
 #pragma unroll
             for (int c = 0; c < 8; ++c) acc[mt][c] += red[v][mt][c][lane];
 
-    // D layout: acc[mt][c][i] is row mt*16 + 4g + i, column n0 + c
+    // D layout: acc[mt][c][i] is row mt*16 + 4*grp + i, column n0 + c
     if (n0 >= N) return;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t m = mt * 16 + 4 * g + i;
+            const uint32_t m = mt * 16 + 4 * grp + i;
             if (m >= M) continue;
-            if (gridDim.y == 1) {
+            if (g.direct) {
                 u32x4 o;
 #pragma unroll
                 for (int h = 0; h < 4; ++h)
                     o[h] = (__float_as_uint(acc[mt][2 * h][i]) >> 16) |
                            (__float_as_uint(acc[mt][2 * h + 1][i]) & 0xffff0000u);
-                *reinterpret_cast<u32x4 *>(C + uint64_t(m) * N + n0) = o;
+                *reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(sg.c) + uint64_t(m) * N + n0) = o;
             } else {
-                float *p = P + (uint64_t(blockIdx.y) * M + m) * N + n0;
+                float *p = g.p + (uint64_t(blockIdx.y) * M + m) * g.ntot + sg.col0 + n0;
                 *reinterpret_cast<f32x4 *>(p) =
                     f32x4{acc[mt][0][i], acc[mt][1][i], acc[mt][2][i], acc[mt][3][i]};
                 *reinterpret_cast<f32x4 *>(p + 4) =
@@ -149,20 +187,20 @@ __global__ __launch_bounds__(256) void skinny_bf16_kernel(const uint16_t *__rest
 
 // ----------------------------------------------------------------- f32 ----
 // MT 16-row tiles of A, STEPS 16-deep k steps per wave: KC = 4 * STEPS * 16.
-// Lane (g, q) of a step loads rows kr + 4g + r (r = 0..3), columns 4q..4q+3 of
-// the strip, and A[m][kr + 4g .. kr + 4g + 3]; MFMA (r, c) pairs k-group g with
-// row kr + 4g + r in both operands.
+// Lane (grp, q) of a step loads rows kr + 4*grp + r (r = 0..3), columns
+// 4q..4q+3 of the strip, and A[m][kr + 4*grp .. kr + 4*grp + 3]; MFMA (r, c)
+// pairs k-group grp with row kr + 4*grp + r in both operands.
 template <int MT, int STEPS>
-__global__ __launch_bounds__(256) void skinny_f32_kernel(const float *__restrict__ A,
-                                                         const float *__restrict__ B,
-                                                         float *__restrict__ C,
-                                                         float *__restrict__ P, uint32_t M,
-                                                         uint32_t N, uint32_t K) {
+__global__ __launch_bounds__(256) void skinny_f32_kernel(const SkinnyArgs g) {
     constexpr uint32_t KC = kWaves * STEPS * 16;
     __shared__ f32x4 red[kWaves - 1][MT][4][64];
+    const SegPick sg = pick_segment(g);
+    const float *__restrict__ A = static_cast<const float *>(g.a);
+    const float *__restrict__ B = static_cast<const float *>(sg.b);
+    const uint32_t M = g.m, N = sg.n, K = g.k;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63, g = lane >> 4, q = lane & 15;
-    const uint32_t n0 = blockIdx.x * 64 + 4 * q;
+    const int lane = threadIdx.x & 63, grp = lane >> 4, q = lane & 15;
+    const uint32_t n0 = sg.strip * 64 + 4 * q;
     const uint32_t kb0 = blockIdx.y * KC;
     const uint32_t krows = K - kb0 < KC ? K - kb0 : KC;
     const auto rb = rsrc(B + uint64_t(kb0) * N, krows * N * 4u);
@@ -174,14 +212,14 @@ __global__ __launch_bounds__(256) void skinny_f32_kernel(const float *__restrict
     for (int t = 0; t < STEPS; ++t) {
         const uint32_t kr = uint32_t(t * kWaves + w) * 16;
         if (kr < krows) {
-            const uint32_t vo = bcol + (kr + 4 * g) * N * 4u;
+            const uint32_t vo = bcol + (kr + 4 * grp) * N * 4u;
 #pragma unroll
             for (int r = 0; r < 4; ++r)
                 b[t][r] = __builtin_amdgcn_raw_buffer_load_b128(rb, vo, int(N * 4u) * r, 0);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
                 a[t][mt] = __builtin_amdgcn_raw_buffer_load_b128(
-                    ra, ((mt * 16 + q) * K + kb0 + kr + 4 * g) * 4u, 0, 0);
+                    ra, ((mt * 16 + q) * K + kb0 + kr + 4 * grp) * 4u, 0, 0);
         }
     }
     f32x4 acc[MT][4];
@@ -224,10 +262,10 @@ __global__ __launch_bounds__(256) void skinny_f32_kernel(const float *__restrict
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t m = mt * 16 + 4 * g + i;
+            const uint32_t m = mt * 16 + 4 * grp + i;
             if (m >= M) continue;
-            float *dst = gridDim.y == 1 ? C + uint64_t(m) * N + n0
-                                        : P + (uint64_t(blockIdx.y) * M + m) * N + n0;
+            float *dst = g.direct ? static_cast<float *>(sg.c) + uint64_t(m) * N + n0
+                                  : g.p + (uint64_t(blockIdx.y) * M + m) * g.ntot + sg.col0 + n0;
             *reinterpret_cast<f32x4 *>(dst) =
                 f32x4{acc[mt][0][i], acc[mt][1][i], acc[mt][2][i], acc[mt][3][i]};
         }
@@ -276,13 +314,52 @@ int skinny_cus() {
     return cus;
 }
 
-struct SkinnyPlan {
-    int mt = 0, steps = 0;
-    uint32_t kc = 0, ks = 0, strips = 0;
-};
+hipError_t launch_skinny(const SkinnyArgs &g, uint8_t dtype, int mt, int steps, uint32_t strips,
+                         uint32_t ks, hipStream_t stream) {
+    const dim3 grid(strips, ks), block(256);
+#define HOLO_SKINNY(KER, MT, ST) hipLaunchKernelGGL((KER<MT, ST>), grid, block, 0, stream, g)
+    if (dtype == 7) {
+        if (mt == 1) {
+            if (steps == 4) HOLO_SKINNY(skinny_bf16_kernel, 1, 4);
+            else if (steps == 2) HOLO_SKINNY(skinny_bf16_kernel, 1, 2);
+            else HOLO_SKINNY(skinny_bf16_kernel, 1, 1);
+        } else if (mt == 2) {
+            if (steps == 4) HOLO_SKINNY(skinny_bf16_kernel, 2, 4);
+            else if (steps == 2) HOLO_SKINNY(skinny_bf16_kernel, 2, 2);
+            else HOLO_SKINNY(skinny_bf16_kernel, 2, 1);
+        } else {
+            if (steps == 2) HOLO_SKINNY(skinny_bf16_kernel, 4, 2);
+            else HOLO_SKINNY(skinny_bf16_kernel, 4, 1);
+        }
+    } else {
+        if (mt == 1) {
+            if (steps == 8) HOLO_SKINNY(skinny_f32_kernel, 1, 8);
+            else if (steps == 4) HOLO_SKINNY(skinny_f32_kernel, 1, 4);
+            else if (steps == 2) HOLO_SKINNY(skinny_f32_kernel, 1, 2);
+            else HOLO_SKINNY(skinny_f32_kernel, 1, 1);
+        } else if (mt == 2) {
+            if (steps == 8) HOLO_SKINNY(skinny_f32_kernel, 2, 8);
+            else if (steps == 4) HOLO_SKINNY(skinny_f32_kernel, 2, 4);
+            else if (steps == 2) HOLO_SKINNY(skinny_f32_kernel, 2, 2);
+            else HOLO_SKINNY(skinny_f32_kernel, 2, 1);
+        } else {
+            if (steps == 4) HOLO_SKINNY(skinny_f32_kernel, 4, 4);
+            else if (steps == 2) HOLO_SKINNY(skinny_f32_kernel, 4, 2);
+            else HOLO_SKINNY(skinny_f32_kernel, 4, 1);
+        }
+    }
+#undef HOLO_SKINNY
+    return hipGetLastError();
+}
 
-// mt = 0: the skinny kernels do not apply.
-SkinnyPlan plan(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype) {
+}  // namespace
+
+// The split of a few-row MatMul: 16-row tiles of A, the k steps per wave and
+// the K ranges. It fixes the order of every fp32 sum of the product (within a
+// wave, across the four waves, then across K ranges in ks order), so a call
+// and a grouped launch with the same plan give the same bits. mt = 0: the
+// few-row kernels do not apply.
+SkinnyPlan matmul_skinny_plan(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype) {
     SkinnyPlan p;
     if (m == 0 || m > 64 || k == 0 || n == 0) return p;
     const bool bf16 = dtype == 7;
@@ -313,73 +390,68 @@ SkinnyPlan plan(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype) {
     return p;
 }
 
-}  // namespace
-
 size_t matmul_skinny_scratch_bytes(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype) {
-    const SkinnyPlan p = plan(m, k, n, dtype);
+    const SkinnyPlan p = matmul_skinny_plan(m, k, n, dtype);
     if (p.mt == 0 || p.ks <= 1) return 0;
     return size_t(p.ks) * m * n * 4;
 }
 
 bool matmul_skinny_applies(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype) {
-    return plan(m, k, n, dtype).mt != 0;
+    return matmul_skinny_plan(m, k, n, dtype).mt != 0;
 }
 
 hipError_t launch_matmul_skinny(const void *a, const void *b, void *c, uint32_t m, uint32_t k,
                                 uint32_t n, uint8_t dtype, void *scratch, hipStream_t stream) {
-    const SkinnyPlan p = plan(m, k, n, dtype);
+    const SkinnyPlan p = matmul_skinny_plan(m, k, n, dtype);
     if (p.mt == 0 || (p.ks > 1 && scratch == nullptr)) return hipErrorInvalidValue;
-    const dim3 grid(p.strips, p.ks), block(256);
-    float *P = static_cast<float *>(scratch);
-    if (dtype == 7) {
-        const auto *A = static_cast<const uint16_t *>(a);
-        const auto *B = static_cast<const uint16_t *>(b);
-        auto *C = static_cast<uint16_t *>(c);
-#define HOLO_SKINNY_BF16(MT, ST) hipLaunchKernelGGL((skinny_bf16_kernel<MT, ST>), grid, block, 0, stream, A, B, C, P, m, n, k)
-        if (p.mt == 1) {
-            if (p.steps == 4) HOLO_SKINNY_BF16(1, 4);
-            else if (p.steps == 2) HOLO_SKINNY_BF16(1, 2);
-            else HOLO_SKINNY_BF16(1, 1);
-        } else if (p.mt == 2) {
-            if (p.steps == 4) HOLO_SKINNY_BF16(2, 4);
-            else if (p.steps == 2) HOLO_SKINNY_BF16(2, 2);
-            else HOLO_SKINNY_BF16(2, 1);
-        } else {
-            if (p.steps == 2) HOLO_SKINNY_BF16(4, 2);
-            else HOLO_SKINNY_BF16(4, 1);
-        }
-#undef HOLO_SKINNY_BF16
-    } else {
-        const auto *A = static_cast<const float *>(a);
-        const auto *B = static_cast<const float *>(b);
-        auto *C = static_cast<float *>(c);
-#define HOLO_SKINNY_F32(MT, ST) hipLaunchKernelGGL((skinny_f32_kernel<MT, ST>), grid, block, 0, stream, A, B, C, P, m, n, k)
-        if (p.mt == 1) {
-            if (p.steps == 8) HOLO_SKINNY_F32(1, 8);
-            else if (p.steps == 4) HOLO_SKINNY_F32(1, 4);
-            else if (p.steps == 2) HOLO_SKINNY_F32(1, 2);
-            else HOLO_SKINNY_F32(1, 1);
-        } else if (p.mt == 2) {
-            if (p.steps == 8) HOLO_SKINNY_F32(2, 8);
-            else if (p.steps == 4) HOLO_SKINNY_F32(2, 4);
-            else if (p.steps == 2) HOLO_SKINNY_F32(2, 2);
-            else HOLO_SKINNY_F32(2, 1);
-        } else {
-            if (p.steps == 4) HOLO_SKINNY_F32(4, 4);
-            else if (p.steps == 2) HOLO_SKINNY_F32(4, 2);
-            else HOLO_SKINNY_F32(4, 1);
-        }
-#undef HOLO_SKINNY_F32
-    }
-    hipError_t e = hipGetLastError();
+    SkinnyArgs g{};
+    g.a = a;
+    g.p = static_cast<float *>(scratch);
+    g.m = m;
+    g.k = k;
+    g.ntot = n;
+    g.nseg = 1;
+    g.direct = p.ks <= 1;
+    g.strip_end[0] = p.strips;
+    g.b[0] = b;
+    g.c[0] = c;
+    g.n[0] = n;
+    g.col0[0] = 0;
+    hipError_t e = launch_skinny(g, dtype, p.mt, p.steps, p.strips, p.ks, stream);
     if (e != hipSuccess || p.ks <= 1) return e;
     const uint64_t quads = uint64_t(m) * n / 4;
-    const dim3 rgrid(unsigned((quads + 255) / 256));
+    const dim3 rgrid(unsigned((quads + 255) / 256)), block(256);
     if (dtype == 7)
-        hipLaunchKernelGGL(skinny_reduce_kernel<true>, rgrid, block, 0, stream, P, c, m, n, p.ks);
+        hipLaunchKernelGGL(skinny_reduce_kernel<true>, rgrid, block, 0, stream, g.p, c, m, n, p.ks);
     else
-        hipLaunchKernelGGL(skinny_reduce_kernel<false>, rgrid, block, 0, stream, P, c, m, n, p.ks);
+        hipLaunchKernelGGL(skinny_reduce_kernel<false>, rgrid, block, 0, stream, g.p, c, m, n, p.ks);
     return hipGetLastError();
+}
+
+hipError_t launch_skinny_partials(const void *a, uint32_t m, uint32_t k, uint8_t dtype,
+                                  const SkinnySegment *segs, int nseg, const SkinnyPlan &plan,
+                                  float *P, hipStream_t stream) {
+    if (plan.mt == 0 || nseg < 1 || nseg > kSkinnyMaxSeg || P == nullptr) return hipErrorInvalidValue;
+    SkinnyArgs g{};
+    g.a = a;
+    g.p = P;
+    g.m = m;
+    g.k = k;
+    g.nseg = uint32_t(nseg);
+    g.direct = 0;
+    const uint32_t sw = dtype == 7 ? 128 : 64;
+    uint32_t strips = 0, col = 0;
+    for (int i = 0; i < nseg; ++i) {
+        strips += (segs[i].n + sw - 1) / sw;
+        g.strip_end[i] = strips;
+        g.b[i] = segs[i].b;
+        g.c[i] = nullptr;
+        g.n[i] = segs[i].n;
+        g.col0[i] = col;
+        col += segs[i].n;
+    }
+    g.ntot = col;
+    return launch_skinny(g, dtype, plan.mt, plan.steps, strips, plan.ks, stream);
 }
 
 }  // namespace holo

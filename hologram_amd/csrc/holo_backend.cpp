@@ -175,6 +175,27 @@ size_t dtype_size(uint8_t dt) {
     }
 }
 
+// The device copy of the (act, dtype) table, built and uploaded on first use
+// (once per backend; a session's eager walk does this before any capture).
+int lut_table(holo_backend *be, int act, bool f16, const uint16_t **out, const char *op) {
+    uint16_t *&tab = be->lut_dev[act][f16 ? 0 : 1];
+    if (!tab) {
+        std::vector<uint16_t> host(65536);
+        holo::build_lut_table(act, f16, host.data());
+        void *d = nullptr;
+        hipError_t e = hipMalloc(&d, 65536 * 2);
+        if (e != hipSuccess) return fail(HOLO_ERR_INIT, std::string(op) + ": table allocation failed");
+        e = hipMemcpy(d, host.data(), 65536 * 2, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            (void)hipFree(d);
+            return fail(HOLO_ERR_INIT, std::string(op) + ": table upload failed");
+        }
+        tab = static_cast<uint16_t *>(d);
+    }
+    *out = tab;
+    return HOLO_OK;
+}
+
 // ---------------------------------------------------------------- LUT ----
 // unary_act -> unary_lut (src/cpu/kernels.rs:1586-1598, src/cpu/lut.rs:76-98).
 int do_unary(holo_backend *be, const SlotTable &st, uint32_t tag, const holo_unary_call &c) {
@@ -193,21 +214,8 @@ int do_unary(holo_backend *be, const SlotTable &st, uint32_t tag, const holo_una
     if (!aligned(in, 2) || !aligned(out, 2))
         return fail(HOLO_ERR_UNSUPPORTED_OP, "unary_lut: operands must be 2-byte aligned");
     if (!be) return HOLO_OK;
-    const int di = c.dtype == HOLO_DTYPE_BF16 ? 1 : 0;
-    uint16_t *&tab = be->lut_dev[act][di];
-    if (!tab) {
-        std::vector<uint16_t> host(65536);
-        holo::build_lut_table(act, di == 0, host.data());
-        void *d = nullptr;
-        hipError_t e = hipMalloc(&d, 65536 * 2);
-        if (e != hipSuccess) return fail(HOLO_ERR_INIT, "unary_lut: table allocation failed");
-        e = hipMemcpy(d, host.data(), 65536 * 2, hipMemcpyHostToDevice);
-        if (e != hipSuccess) {
-            (void)hipFree(d);
-            return fail(HOLO_ERR_INIT, "unary_lut: table upload failed");
-        }
-        tab = static_cast<uint16_t *>(d);
-    }
+    const uint16_t *tab = nullptr;
+    HOLO_TRY(lut_table(be, act, c.dtype == HOLO_DTYPE_F16, &tab, op));
     return launched(holo::launch_lut_u16(tab, reinterpret_cast<const uint16_t *>(in.base),
                                          reinterpret_cast<uint16_t *>(out.base), c.element_count,
                                          be->stream),
@@ -256,6 +264,167 @@ int do_matmul(holo_backend *be, const SlotTable &st, const holo_matmul_call &c) 
     return launched(holo::launch_matmul(rv[0].base, rv[1].base, out.base, c.m, c.k, c.n, c.dtype,
                                         be->scratch, be->stream),
                     op);
+}
+
+// ------------------------------------------------------- fused groups ----
+// Every member's product in one few-row launch (fp32 partials), then one
+// epilogue launch that finishes each segment. A one-segment group with an
+// element-wise epilogue that the few-row kernels do not serve runs the tiled
+// MatMul into its output and the epilogue in place.
+int dispatch_group_impl(holo_backend *be, const SlotTable &st, const holo::GroupDesc &g,
+                        const char *op) {
+    const size_t nseg = g.segs.size();
+    if (nseg == 0 || nseg > size_t(holo::kSkinnyMaxSeg))
+        return fail(HOLO_ERR_DISPATCH, std::string(op) + ": fused group of " + std::to_string(nseg) +
+                                           " products");
+    const bool bf16 = g.dtype == HOLO_DTYPE_BF16;
+    const uint64_t es = dtype_size(g.dtype), mk = uint64_t(g.m) * g.k;
+    auto get = [&](const holo_buffer_ref &r, uint64_t bytes, const char *what, View *v) {
+        if (!resolve(st, r, v))
+            return fail(HOLO_ERR_SLOT_OUT_OF_RANGE, std::string(op) + ": " + what + " slot " +
+                                                        std::to_string(r.slot) + " unbound");
+        return need(*v, bytes, r.slot, op, what);
+    };
+    View a;
+    HOLO_TRY(get(g.a, mk * es, "a", &a));
+    bool fast = aligned(a, 16);
+    holo::SkinnyPlan plan = holo::matmul_skinny_plan(g.m, g.k, g.segs[0].n, g.dtype);
+    holo::SkinnySegment ss[holo::kSkinnyMaxSeg];
+    holo::EpiArgs e;
+    e.m = g.m;
+    e.bf16 = bf16;
+    e.nseg = uint32_t(nseg);
+    uint32_t ntot = 0;
+    for (size_t i = 0; i < nseg; ++i) {
+        const holo::GroupSegDesc &s = g.segs[i];
+        holo::EpiSeg &d = e.seg[i];
+        const uint64_t mn = uint64_t(g.m) * s.n;
+        View v;
+        HOLO_TRY(get(s.b, uint64_t(g.k) * s.n * es, "b", &v));
+        fast = fast && aligned(v, 16);
+        ss[i] = holo::SkinnySegment{v.base, s.n};
+        const holo::SkinnyPlan p = holo::matmul_skinny_plan(g.m, g.k, s.n, g.dtype);
+        if (p.mt != plan.mt || p.steps != plan.steps || p.ks != plan.ks) fast = false;
+        d.n = s.n;
+        d.col0 = ntot;
+        ntot += s.n;
+        d.base = s.base;
+        d.act = s.act;
+        if ((s.base == holo::kEpiAct || s.base == holo::kEpiAddAct) &&
+            !holo::fused_act_supported(s.act, g.dtype, s.base == holo::kEpiAddAct))
+            return fail(HOLO_ERR_UNSUPPORTED_OP, std::string(op) + ": activation " +
+                                                     std::to_string(s.act) + " is not served");
+        if (s.base == holo::kEpiAct && bf16)
+            HOLO_TRY(lut_table(be, holo::lut_act_of_fused(s.act), false, &d.lut, op));
+        if (s.base == holo::kEpiAdd || s.base == holo::kEpiAddAct) {
+            HOLO_TRY(get(s.residual, mn * es, "residual", &v));
+            d.residual = v.base;
+        }
+        if (s.write_out) {
+            HOLO_TRY(get(s.out, mn * es, "output", &v));
+            d.out = v.base;
+        }
+        d.head_dim = s.head_dim;
+        d.rope = s.rope;
+        if (s.rope) {
+            HOLO_TRY(get(s.cos, mn * es, "cos", &v));
+            d.cos = v.base;
+            HOLO_TRY(get(s.sin, mn * es, "sin", &v));
+            d.sin = v.base;
+            if (s.write_rope) {
+                HOLO_TRY(get(s.rope_out, mn * es, "rope output", &v));
+                d.rope_out = v.base;
+            }
+        }
+        d.quant = s.quant;
+        if (s.quant) {
+            const uint64_t planes = mn / s.head_dim / s.new_rows;
+            HOLO_TRY(get(s.pos, 4, "pos", &v));
+            if (!aligned(v, 4)) return fail(HOLO_ERR_UNSUPPORTED_OP, std::string(op) + ": pos must be aligned");
+            d.pos = reinterpret_cast<const uint32_t *>(v.base);
+            HOLO_TRY(get(s.cq, planes * s.bucket * s.head_dim, "int8 cache", &v));
+            d.cq = reinterpret_cast<int8_t *>(v.base);
+            HOLO_TRY(get(s.cs, planes * s.bucket * 4, "scale cache", &v));
+            if (!aligned(v, 4)) return fail(HOLO_ERR_UNSUPPORTED_OP, std::string(op) + ": scales must be aligned");
+            d.cs = reinterpret_cast<float *>(v.base);
+            d.bucket = s.bucket;
+            d.new_rows = s.new_rows;
+        }
+        d.pair = s.pair;
+        if (s.pair >= 0) {
+            HOLO_TRY(get(s.mul_out, mn * es, "product output", &v));
+            d.mul_out = v.base;
+        }
+        d.skip = s.skip;
+    }
+    fast = fast && plan.mt != 0;
+    if (!fast) {
+        const holo::GroupSegDesc &s = g.segs[0];
+        const bool elementwise = nseg == 1 && s.write_out && !s.head_dim && s.pair < 0;
+        if (!elementwise)
+            return fail(HOLO_ERR_DISPATCH,
+                        std::string(op) + ": a fused group needs the few-row path (16-byte aligned "
+                                          "operands, one common split)");
+        // the tiled product into the output, then the epilogue in place
+        HOLO_TRY(ensure_scratch(be, holo::matmul_scratch_bytes(g.m, g.k, s.n, g.dtype), op));
+        HOLO_TRY(launched(holo::launch_matmul(a.base, ss[0].b, e.seg[0].out, g.m, g.k, s.n, g.dtype,
+                                              be->scratch, be->stream),
+                          op));
+        if (s.base == holo::kEpiStore) return HOLO_OK;
+        e.ks = 0;
+        e.src = e.seg[0].out;
+        e.ntot = s.n;
+        return launched(holo::launch_epilogue(e, be->stream), op);
+    }
+    HOLO_TRY(ensure_scratch(be, size_t(plan.ks) * g.m * ntot * 4, op));
+    e.P = static_cast<const float *>(be->scratch);
+    e.ks = plan.ks;
+    e.ntot = ntot;
+    HOLO_TRY(launched(holo::launch_skinny_partials(a.base, g.m, g.k, g.dtype, ss, int(nseg), plan,
+                                                   static_cast<float *>(be->scratch), be->stream),
+                      op));
+    return launched(holo::launch_epilogue(e, be->stream), op);
+}
+
+// ------------------------------------------------ fused MatMul epilogues ----
+// matmul_activation_float / matmul_add_float / matmul_add_activation_float
+// (src/cpu/float_kernels.rs:816-935): the product, then the epilogue over the
+// m*n results. Few-row shapes finish the product in the epilogue launch (one
+// group of one segment); the tiled path applies it in place afterwards.
+int do_matmul_fused(holo_backend *be, const SlotTable &st, uint32_t tag, const holo_matmul_call &c,
+                    const holo_buffer_ref &residual, uint32_t act) {
+    const char *op = tag == HOLO_OP_MATMUL_ACT ? "matmul_activation"
+                     : tag == HOLO_OP_MATMUL_ADD ? "matmul_add" : "matmul_add_activation";
+    const bool has_res = tag != HOLO_OP_MATMUL_ACT, has_act = tag != HOLO_OP_MATMUL_ADD;
+    if (has_act && !holo::fused_act_supported(act, c.dtype, tag == HOLO_OP_MATMUL_ADD_ACT))
+        return fail(HOLO_ERR_UNSUPPORTED_OP, std::string(op) + ": activation " + std::to_string(act) +
+                                                 " is not served on the device for this dtype");
+    HOLO_TRY(do_matmul(nullptr, st, c));   // the product's own refusals, no device work
+    if (c.m == 0 || c.k == 0 || c.n == 0) return HOLO_OK;
+    const uint64_t es = dtype_size(c.dtype), count = uint64_t(c.m) * c.n;
+    View rv[3], out;
+    if (has_res) {
+        HOLO_TRY(split_borrow(st, &residual, rv, 1, c.output, &out, op));
+        HOLO_TRY(need(rv[0], count * es, residual.slot, op, "residual"));
+        if (!aligned(rv[0], es))
+            return fail(HOLO_ERR_UNSUPPORTED_OP, std::string(op) + ": residual must be element-aligned");
+    }
+    if (!be) return HOLO_OK;
+    holo::GroupDesc g;
+    g.a = c.a;
+    g.m = c.m;
+    g.k = c.k;
+    g.dtype = c.dtype;
+    holo::GroupSegDesc s;
+    s.b = c.b;
+    s.out = c.output;
+    s.n = c.n;
+    s.base = tag == HOLO_OP_MATMUL_ACT ? holo::kEpiAct
+             : tag == HOLO_OP_MATMUL_ADD ? holo::kEpiAdd : holo::kEpiAddAct;
+    s.act = act;
+    if (has_res) s.residual = residual;
+    g.segs.push_back(s);
+    return dispatch_group_impl(be, st, g, op);
 }
 
 // ------------------------------------------------------- KvCacheWrite ----
@@ -583,6 +752,15 @@ int dispatch_impl(holo_backend *be, const SlotTable &st, const holo_kernel_call 
         case HOLO_OP_GATHER: return do_gather(be, st, call->u.gather);
         case HOLO_OP_ARGMAX: return do_argmax(be, st, call->u.argmax);
         case HOLO_OP_MATMUL: return do_matmul(be, st, call->u.matmul);
+        case HOLO_OP_MATMUL_ACT:
+            return do_matmul_fused(be, st, call->tag, call->u.matmul_act.mm, holo_buffer_ref{},
+                                   call->u.matmul_act.act);
+        case HOLO_OP_MATMUL_ADD:
+            return do_matmul_fused(be, st, call->tag, call->u.matmul_add.mm,
+                                   call->u.matmul_add.residual, 0);
+        case HOLO_OP_MATMUL_ADD_ACT:
+            return do_matmul_fused(be, st, call->tag, call->u.matmul_add_act.mm,
+                                   call->u.matmul_add_act.residual, call->u.matmul_add_act.act);
         case HOLO_OP_KV_CACHE_WRITE: return do_kv_write(be, st, call->u.kv_write);
         case HOLO_OP_KV_QUANT_APPEND: return do_kv_quant(be, st, call->u.kv_quant_append);
         case HOLO_OP_DECODE_ATTN_I8: return do_attn_i8(be, st, call->u.attn_i8);
@@ -709,6 +887,31 @@ int decode_impl(const uint8_t *wire, size_t len, holo_kernel_call *out, size_t *
             c.b_packed = r.get<uint8_t>();
             break;
         }
+        case HOLO_OP_MATMUL_ACT:
+        case HOLO_OP_MATMUL_ADD:
+        case HOLO_OP_MATMUL_ADD_ACT: {  // :509-524: put_matmul, then residual and/or act
+            holo_matmul_call mm;
+            mm.a = r.buf();
+            mm.b = r.buf();
+            mm.output = r.buf();
+            mm.m = r.get<uint32_t>();
+            mm.k = r.get<uint32_t>();
+            mm.n = r.get<uint32_t>();
+            mm.dtype = r.get<uint8_t>();
+            mm.b_packed = r.get<uint8_t>();
+            if (out->tag == HOLO_OP_MATMUL_ACT) {
+                out->u.matmul_act.mm = mm;
+                out->u.matmul_act.act = r.get<uint8_t>();
+            } else if (out->tag == HOLO_OP_MATMUL_ADD) {
+                out->u.matmul_add.mm = mm;
+                out->u.matmul_add.residual = r.buf();
+            } else {
+                out->u.matmul_add_act.mm = mm;
+                out->u.matmul_add_act.residual = r.buf();
+                out->u.matmul_add_act.act = r.get<uint8_t>();
+            }
+            break;
+        }
         case HOLO_OP_KV_CACHE_WRITE: {  // put_kvwr :804-813
             auto &c = out->u.kv_write;
             c.cache = r.buf();
@@ -780,6 +983,31 @@ int dispatch_with_slots(holo_backend *be, const std::vector<SlotRange> &slots,
 
 int decode_call(const uint8_t *wire, size_t len, holo_kernel_call *out, size_t *consumed) {
     return decode_impl(wire, len, out, consumed);
+}
+
+int dispatch_group(holo_backend *be, const std::vector<SlotRange> &slots, const GroupDesc &g) {
+    SlotTable st;
+    st.vec = &slots;
+    return dispatch_group_impl(be, st, g, "fused_group");
+}
+
+int lut_act_of_fused(uint32_t act) {
+    switch (act) {
+        case kFusedGelu: return HOLO_ACT_GELU;
+        case kFusedSilu: return HOLO_ACT_SILU;
+        case kFusedSigmoid: return HOLO_ACT_SIGMOID;
+        case kFusedTanh: return HOLO_ACT_TANH;
+        case kFusedExp: return HOLO_ACT_EXP;
+        default: return -1;
+    }
+}
+
+bool fused_act_supported(uint32_t act, uint8_t dtype, bool after_add) {
+    const bool computed = act == kFusedGelu || act == kFusedSilu || act == kFusedSigmoid ||
+                          act == kFusedTanh;
+    if (dtype == HOLO_DTYPE_BF16) return after_add ? computed : lut_act_of_fused(act) >= 0;
+    if (dtype == HOLO_DTYPE_F32) return computed;
+    return false;
 }
 
 hipStream_t backend_stream(const holo_backend *be) { return be->stream; }

@@ -31,6 +31,34 @@ int decode_call(const uint8_t *wire, size_t len, holo_kernel_call *out, size_t *
 hipStream_t backend_stream(const holo_backend *be);
 void set_backend_stream(holo_backend *be, hipStream_t s);
 int backend_device(const holo_backend *be);
+// A fused few-row MatMul group (the session's device fusion): products that
+// share A, each finished by its epilogue (holo_kernels.h EpiSeg) in one more
+// launch. Operands stay BufferRefs, resolved through the slot table at
+// dispatch, so rebinding an input needs no new plan.
+struct GroupSegDesc {
+    holo_buffer_ref b{}, out{}, residual{}, cos{}, sin{}, rope_out{}, pos{}, cq{}, cs{}, mul_out{};
+    uint32_t n = 0;
+    uint8_t base = 0;          // kEpiStore / kEpiAct / kEpiAdd / kEpiAddAct
+    uint32_t act = 0;          // fused_activation id
+    bool write_out = true;
+    uint32_t head_dim = 0;
+    bool rope = false, write_rope = true, quant = false, skip = false;
+    uint32_t bucket = 0, new_rows = 0;
+    int pair = -1;
+};
+struct GroupDesc {
+    holo_buffer_ref a{};
+    uint32_t m = 0, k = 0;
+    uint8_t dtype = 0;
+    std::vector<GroupSegDesc> segs;
+};
+int dispatch_group(holo_backend *be, const std::vector<SlotRange> &slots, const GroupDesc &g);
+// The LUT activation id of a fused_activation id (-1: no table).
+int lut_act_of_fused(uint32_t act);
+// Whether the device serves fused activation `act` for dtype (bf16 table or f32 compute);
+// `after_add`: applied to an f32 sum (MatMulAddActivation), never through a table.
+bool fused_act_supported(uint32_t act, uint8_t dtype, bool after_add);
+
 // BLAKE3 (default hash mode, 32-byte digest).
 void blake3_hash(const void *data, size_t len, uint8_t out[32]);
 

@@ -72,9 +72,65 @@ hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint
 
 // gemm_skinny.hip — the few-row (m <= 64) path that launch_matmul takes when
 // it applies (16-byte aligned operands required by the caller).
+constexpr int kSkinnyMaxSeg = 4;
+struct SkinnyPlan {
+    int mt = 0, steps = 0;             // 16-row tiles of A; k steps per wave (0: does not apply)
+    uint32_t kc = 0, ks = 0, strips = 0;   // K rows per workgroup, K ranges, column strips
+};
+SkinnyPlan matmul_skinny_plan(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype);
 bool matmul_skinny_applies(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype);
 size_t matmul_skinny_scratch_bytes(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype);
 hipError_t launch_matmul_skinny(const void *a, const void *b, void *c, uint32_t m, uint32_t k,
                                 uint32_t n, uint8_t dtype, void *scratch, hipStream_t stream);
+// One launch over up to kSkinnyMaxSeg products sharing A[m, k]: segment s is
+// B_s [k, n_s]. Every segment's fp32 partials go to P [plan.ks][m][ntot]
+// (ntot = sum of n_s), segment s at columns sum(n_0 .. n_{s-1}); `plan` must be
+// the plan each segment has on its own (the sums then match a single call).
+// epilogue.hip — the finish of a few-row MatMul group: partials summed in ks
+// order, then per segment the base value (the product, + residual, activation),
+// and optionally rotary embedding, int8 quantize + append, and the product with
+// another segment's value. The same operations in the same order as the
+// standalone kernels they stand in for.
+constexpr uint8_t kEpiStore = 0, kEpiAct = 1, kEpiAdd = 2, kEpiAddAct = 3;
+// fused_activation ids (crates/hologram-compute/src/kernel_call.rs:861-870)
+constexpr uint32_t kFusedRelu = 1, kFusedGelu = 2, kFusedSilu = 3, kFusedSigmoid = 4,
+                   kFusedTanh = 5, kFusedElu = 6, kFusedSelu = 7, kFusedExp = 8;
+struct EpiSeg {
+    uint32_t n = 0, col0 = 0;          // columns; first column in the partials' column space
+    uint8_t base = kEpiStore;
+    uint32_t act = 0;                  // f32: fused_activation id
+    const uint16_t *lut = nullptr;     // bf16: the activation's table (same as the unary op's)
+    const void *residual = nullptr;    // [m, n]
+    void *out = nullptr;               // [m, n] base value, or null (not materialized)
+    uint32_t head_dim = 0;             // > 0: head-wise (rope and/or quant), power of 2 <= 128
+    bool rope = false;
+    const void *cos = nullptr, *sin = nullptr;
+    void *rope_out = nullptr;          // null: the rotated value is not materialized
+    bool quant = false;                // in-place append of each head row
+    const uint32_t *pos = nullptr;
+    int8_t *cq = nullptr;
+    float *cs = nullptr;
+    uint32_t bucket = 0, new_rows = 0;
+    int pair = -1;                     // element-wise product with segment `pair`'s value
+    void *mul_out = nullptr;
+    bool skip = false;                 // consumed through another segment's pair; no blocks
+};
+struct EpiArgs {
+    const float *P = nullptr;          // [ks][m][ntot]
+    const void *src = nullptr;         // ks == 0: the tiled MatMul's output [m][ntot]
+    uint32_t m = 0, ks = 0, ntot = 0, nseg = 0;
+    bool bf16 = true;
+    EpiSeg seg[kSkinnyMaxSeg];
+    uint32_t blk_end[kSkinnyMaxSeg] = {};
+};
+hipError_t launch_epilogue(EpiArgs g, hipStream_t stream);
+
+struct SkinnySegment {
+    const void *b;
+    uint32_t n;
+};
+hipError_t launch_skinny_partials(const void *a, uint32_t m, uint32_t k, uint8_t dtype,
+                                  const SkinnySegment *segs, int nseg, const SkinnyPlan &plan,
+                                  float *P, hipStream_t stream);
 
 }  // namespace holo

@@ -41,6 +41,7 @@
 
 #include "holo_hip.h"
 #include "holo_internal.h"
+#include "holo_kernels.h"
 
 namespace {
 
@@ -127,6 +128,14 @@ void call_operands(const holo_kernel_call &c, std::vector<holo_buffer_ref> *read
             r(c.u.argmax.input); w(c.u.argmax.output); break;
         case HOLO_OP_MATMUL:
             r(c.u.matmul.a); r(c.u.matmul.b); w(c.u.matmul.output); break;
+        case HOLO_OP_MATMUL_ACT:
+            r(c.u.matmul_act.mm.a); r(c.u.matmul_act.mm.b); w(c.u.matmul_act.mm.output); break;
+        case HOLO_OP_MATMUL_ADD:
+            r(c.u.matmul_add.mm.a); r(c.u.matmul_add.mm.b); r(c.u.matmul_add.residual);
+            w(c.u.matmul_add.mm.output); break;
+        case HOLO_OP_MATMUL_ADD_ACT:
+            r(c.u.matmul_add_act.mm.a); r(c.u.matmul_add_act.mm.b); r(c.u.matmul_add_act.residual);
+            w(c.u.matmul_add_act.mm.output); break;
         case HOLO_OP_KV_CACHE_WRITE:
             r(c.u.kv_write.cache); r(c.u.kv_write.new_rows_buf); r(c.u.kv_write.pos);
             w(c.u.kv_write.output); break;
@@ -163,6 +172,149 @@ int parse_ports(const uint8_t *p, size_t n, std::vector<Port> *out) {
     return HOLO_OK;
 }
 
+// fused_activation id of a standalone activation call (KernelCall::
+// fused_activation, crates/hologram-compute/src/kernel_call.rs:1282-1296), or 0.
+uint32_t fused_activation(const holo_kernel_call &c) {
+    switch (c.tag) {
+        case HOLO_OP_GELU: return HOLO_FUSED_GELU;
+        case HOLO_OP_SILU: return HOLO_FUSED_SILU;
+        case HOLO_OP_SIGMOID: return HOLO_FUSED_SIGMOID;
+        case HOLO_OP_TANH: return HOLO_FUSED_TANH;
+        case HOLO_OP_EXP: return HOLO_FUSED_EXP;
+        default: return 0;
+    }
+}
+
+// fuse_matmul_epilogue (crates/hologram-exec/src/session.rs:2150-2373): a
+// MatMul whose output has one producer and one reader, and is no output port,
+// absorbs that reader when it is an activation (-> MatMulActivation) or a
+// residual Add whose other operand is ready no later than the MatMul's level
+// (-> MatMulAdd; for f32 a single activation reader of the sum is absorbed
+// too, -> MatMulAddActivation). Absorbed calls leave the call list and the
+// plan. One difference: a fusion whose activation this device does not serve
+// is skipped (the unfused calls give the same result).
+void fuse_matmul_epilogue(std::vector<holo_kernel_call> &calls,
+                          std::vector<std::vector<uint32_t>> &plan, const std::vector<Port> &outputs) {
+    const size_t n = calls.size();
+    std::map<uint32_t, uint32_t> prod_count, read_count;
+    std::map<uint32_t, size_t> read_idx;
+    std::vector<holo_buffer_ref> rd, wr;
+    for (size_t i = 0; i < n; ++i) {
+        call_operands(calls[i], &rd, &wr);
+        for (auto &r : rd) {
+            read_count[r.slot]++;
+            read_idx[r.slot] = i;
+        }
+        for (auto &w : wr)
+            if (w.slot != HOLO_SLOT_ABSENT) prod_count[w.slot]++;
+    }
+    std::vector<uint32_t> out_slots;
+    for (auto &p : outputs) out_slots.push_back(p.slot);
+    auto is_out = [&](uint32_t s) { return std::find(out_slots.begin(), out_slots.end(), s) != out_slots.end(); };
+    std::map<uint32_t, size_t> slot_level;
+    for (size_t li = 0; li < plan.size(); ++li)
+        for (uint32_t ci : plan[li]) {
+            call_operands(calls[ci], &rd, &wr);
+            if (!wr.empty() && wr.back().slot != HOLO_SLOT_ABSENT) slot_level[wr.back().slot] = li;
+        }
+    auto count = [](const std::map<uint32_t, uint32_t> &m, uint32_t s) {
+        auto it = m.find(s);
+        return it == m.end() ? 0u : it->second;
+    };
+    std::vector<bool> absorbed(n, false);
+    std::vector<holo_kernel_call> fused(calls);
+    std::vector<bool> is_fused(n, false);
+    for (size_t i = 0; i < n; ++i) {
+        if (calls[i].tag != HOLO_OP_MATMUL) continue;
+        const holo_matmul_call mm = calls[i].u.matmul;
+        if (mm.dtype != HOLO_DTYPE_F32 && mm.dtype != HOLO_DTYPE_BF16 && mm.dtype != HOLO_DTYPE_F16) continue;
+        const uint32_t s = mm.output.slot;
+        if (s == HOLO_SLOT_ABSENT || is_out(s)) continue;
+        if (count(prod_count, s) != 1 || count(read_count, s) != 1) continue;
+        const size_t j = read_idx[s];
+        if (j == i || absorbed[j]) continue;
+        std::vector<holo_buffer_ref> jins, jw;
+        call_operands(calls[j], &jins, &jw);
+        if (jw.size() != 1) continue;
+        const holo_buffer_ref jout = jw[0];
+        if (const uint32_t act = fused_activation(calls[j])) {
+            if (jins.size() != 1 || jins[0].slot != s) continue;
+            if (!holo::fused_act_supported(act, mm.dtype, false)) continue;
+            holo_kernel_call f{};
+            f.tag = HOLO_OP_MATMUL_ACT;
+            f.u.matmul_act.mm = mm;
+            f.u.matmul_act.mm.output = jout;
+            f.u.matmul_act.act = uint8_t(act);
+            fused[i] = f;
+            is_fused[i] = true;
+            absorbed[j] = true;
+        } else if (calls[j].tag == HOLO_OP_ADD) {
+            if (jins.size() != 2) continue;
+            holo_buffer_ref residual;
+            if (jins[0].slot == s) residual = jins[1];
+            else if (jins[1].slot == s) residual = jins[0];
+            else continue;
+            const auto rl = slot_level.find(residual.slot), ml = slot_level.find(s);
+            const bool ready = rl == slot_level.end() || ml == slot_level.end() || rl->second < ml->second;
+            if (!ready) continue;
+            // three-op chain matmul -> add -> activation, f32 only
+            const uint32_t add_out = jout.slot;
+            if (mm.dtype == HOLO_DTYPE_F32 && add_out != HOLO_SLOT_ABSENT && !is_out(add_out) &&
+                count(prod_count, add_out) == 1 && count(read_count, add_out) == 1) {
+                const size_t k = read_idx[add_out];
+                const uint32_t act = k != j && !absorbed[k] ? fused_activation(calls[k]) : 0;
+                std::vector<holo_buffer_ref> kins, kw;
+                call_operands(calls[k], &kins, &kw);
+                if (act && kins.size() == 1 && kins[0].slot == add_out && kw.size() == 1 &&
+                    holo::fused_act_supported(act, mm.dtype, true)) {
+                    holo_kernel_call f{};
+                    f.tag = HOLO_OP_MATMUL_ADD_ACT;
+                    f.u.matmul_add_act.mm = mm;
+                    f.u.matmul_add_act.mm.output = kw[0];
+                    f.u.matmul_add_act.residual = residual;
+                    f.u.matmul_add_act.act = uint8_t(act);
+                    fused[i] = f;
+                    is_fused[i] = true;
+                    absorbed[j] = true;
+                    absorbed[k] = true;
+                    continue;
+                }
+            }
+            holo_kernel_call f{};
+            f.tag = HOLO_OP_MATMUL_ADD;
+            f.u.matmul_add.mm = mm;
+            f.u.matmul_add.mm.output = jout;
+            f.u.matmul_add.residual = residual;
+            fused[i] = f;
+            is_fused[i] = true;
+            absorbed[j] = true;
+        }
+    }
+    if (std::find(absorbed.begin(), absorbed.end(), true) == absorbed.end()) return;
+    std::vector<holo_kernel_call> nc;
+    std::vector<uint32_t> remap(n, HOLO_SLOT_ABSENT);
+    for (size_t i = 0; i < n; ++i) {
+        if (absorbed[i]) continue;
+        remap[i] = uint32_t(nc.size());
+        nc.push_back(is_fused[i] ? fused[i] : calls[i]);
+    }
+    std::vector<std::vector<uint32_t>> np;
+    for (auto &level : plan) {
+        std::vector<uint32_t> lv;
+        for (uint32_t ci : level)
+            if (ci < n && !absorbed[ci]) lv.push_back(remap[ci]);
+        if (!lv.empty()) np.push_back(std::move(lv));
+    }
+    calls = std::move(nc);
+    plan = std::move(np);
+}
+
+// A step of the walk: one call, or a fused group (index into groups).
+struct Node {
+    int group = -1;
+    uint32_t call = 0;
+};
+
 }  // namespace
 
 struct holo_session {
@@ -179,9 +331,272 @@ struct holo_session {
     uint8_t fingerprint[32] = {};
     hipGraphExec_t graph = nullptr;
     std::vector<SlotRange> graph_slots;           // bindings the graph was captured with
+    uint32_t flags = 0;                           // HOLO_SESSION_* load options
+    std::vector<Node> nodes;                      // the walk, in order
+    std::vector<holo::GroupDesc> groups;          // fused few-row MatMul groups
 };
 
 namespace {
+
+// ------------------------------------------------------------ device fusion --
+// After the reference's passes, few-row MatMul-family calls that share their
+// A operand are gathered into one group (one launch for every product, one
+// for every epilogue), and each product's sole consumer is pulled into the
+// group's epilogue when it is a rotary embedding, an in-place int8
+// quantize+append, or an element-wise Mul with another member's product. A call
+// joins a group only if no call still in place between the group and it
+// touches what it reads or writes, and members and epilogues of one group
+// share no written slot with each other's reads; every epilogue step is the
+// standalone kernel's arithmetic, so the result is bit-identical.
+struct MmView {
+    holo_matmul_call mm{};
+    uint8_t base = holo::kEpiStore;
+    uint32_t act = 0;
+    holo_buffer_ref residual{HOLO_SLOT_ABSENT, 0, 0};
+};
+
+bool matmul_family(const holo_kernel_call &c, MmView *v) {
+    switch (c.tag) {
+        case HOLO_OP_MATMUL: v->mm = c.u.matmul; v->base = holo::kEpiStore; return true;
+        case HOLO_OP_MATMUL_ACT:
+            v->mm = c.u.matmul_act.mm; v->base = holo::kEpiAct; v->act = c.u.matmul_act.act; return true;
+        case HOLO_OP_MATMUL_ADD:
+            v->mm = c.u.matmul_add.mm; v->base = holo::kEpiAdd; v->residual = c.u.matmul_add.residual;
+            return true;
+        case HOLO_OP_MATMUL_ADD_ACT:
+            v->mm = c.u.matmul_add_act.mm; v->base = holo::kEpiAddAct;
+            v->residual = c.u.matmul_add_act.residual; v->act = c.u.matmul_add_act.act; return true;
+        default: return false;
+    }
+}
+
+bool same_ref(const holo_buffer_ref &a, const holo_buffer_ref &b) {
+    return a.slot == b.slot && a.offset == b.offset;
+}
+
+bool pow2_head(uint32_t d) { return d >= 2 && d <= 128 && (d & (d - 1)) == 0; }
+
+// Slots a segment's epilogue reads and writes (for the cross-segment check).
+void seg_slots(const holo::GroupSegDesc &s, std::vector<uint32_t> *rd, std::vector<uint32_t> *wr) {
+    rd->clear();
+    wr->clear();
+    if (s.base == holo::kEpiAdd || s.base == holo::kEpiAddAct) rd->push_back(s.residual.slot);
+    if (s.write_out) wr->push_back(s.out.slot);
+    if (s.rope) {
+        rd->push_back(s.cos.slot);
+        rd->push_back(s.sin.slot);
+        if (s.write_rope) wr->push_back(s.rope_out.slot);
+    }
+    if (s.quant) {
+        rd->push_back(s.pos.slot);
+        wr->push_back(s.cq.slot);
+        wr->push_back(s.cs.slot);
+    }
+    if (s.pair >= 0) wr->push_back(s.mul_out.slot);
+}
+
+bool segments_disjoint(const std::vector<holo::GroupSegDesc> &segs, const holo_buffer_ref &a) {
+    std::vector<std::vector<uint32_t>> rd(segs.size()), wr(segs.size());
+    for (size_t i = 0; i < segs.size(); ++i) {
+        seg_slots(segs[i], &rd[i], &wr[i]);
+        rd[i].push_back(a.slot);
+        rd[i].push_back(segs[i].b.slot);
+    }
+    for (size_t i = 0; i < segs.size(); ++i)
+        for (size_t j = 0; j < segs.size(); ++j)
+            for (uint32_t w : wr[i]) {
+                if (std::find(rd[j].begin(), rd[j].end(), w) != rd[j].end()) return false;
+                if (j != i && std::find(wr[j].begin(), wr[j].end(), w) != wr[j].end()) return false;
+            }
+    return true;
+}
+
+void device_fusion(holo_session *s, const std::vector<uint8_t> &is_output,
+                   const std::vector<uint8_t> &is_input) {
+    const auto &calls = s->calls;
+    std::vector<uint32_t> order;
+    for (auto &lv : s->plan)
+        for (uint32_t ci : lv) order.push_back(ci);
+    const size_t n = order.size(), npos = size_t(-1);
+    std::vector<std::vector<holo_buffer_ref>> R(calls.size()), W(calls.size());
+    std::vector<uint32_t> readers(is_output.size(), 0);
+    for (size_t i = 0; i < calls.size(); ++i) {
+        call_operands(calls[i], &R[i], &W[i]);
+        for (auto &r : R[i])
+            if (r.slot < readers.size()) readers[r.slot]++;
+    }
+    std::vector<bool> taken(calls.size(), false);
+    auto conflicts = [&](uint32_t x, uint32_t c) {
+        for (auto &w : W[x]) {
+            for (auto &r : R[c])
+                if (w.slot == r.slot) return true;
+            for (auto &w2 : W[c])
+                if (w.slot == w2.slot) return true;
+        }
+        for (auto &r : R[x])
+            for (auto &w2 : W[c])
+                if (r.slot == w2.slot) return true;
+        return false;
+    };
+    auto movable = [&](size_t qc, size_t p) {
+        const uint32_t c = order[qc];
+        for (size_t q = p + 1; q < qc; ++q)
+            if (!taken[order[q]] && conflicts(order[q], c)) return false;
+        return true;
+    };
+    auto sole_reader = [&](uint32_t v, size_t p) -> size_t {
+        if (v >= readers.size() || readers[v] != 1 || is_output[v]) return npos;
+        for (size_t q = p + 1; q < n; ++q) {
+            if (taken[order[q]]) continue;
+            for (auto &r : R[order[q]])
+                if (r.slot == v) return q;
+        }
+        return npos;
+    };
+    auto groupable = [&](const MmView &m) {
+        if (m.mm.dtype != HOLO_DTYPE_BF16 && m.mm.dtype != HOLO_DTYPE_F32) return false;
+        if (m.mm.b_packed || holo::matmul_skinny_plan(m.mm.m, m.mm.k, m.mm.n, m.mm.dtype).mt == 0)
+            return false;
+        if ((m.mm.a.offset | m.mm.b.offset) % 16 != 0) return false;
+        if (m.mm.a.slot >= is_input.size() || m.mm.b.slot >= is_input.size()) return false;
+        // input ports can be rebound to caller memory of any alignment
+        return !is_input[m.mm.a.slot] && !is_input[m.mm.b.slot];
+    };
+    for (size_t p = 0; p < n; ++p) {
+        const uint32_t i = order[p];
+        if (taken[i]) continue;
+        MmView mi;
+        if (!matmul_family(calls[i], &mi) || !groupable(mi)) {
+            s->nodes.push_back(Node{-1, i});
+            continue;
+        }
+        const holo::SkinnyPlan pl = holo::matmul_skinny_plan(mi.mm.m, mi.mm.k, mi.mm.n, mi.mm.dtype);
+        holo::GroupDesc g;
+        g.a = mi.mm.a;
+        g.m = mi.mm.m;
+        g.k = mi.mm.k;
+        g.dtype = mi.mm.dtype;
+        auto seg_of = [](const MmView &m) {
+            holo::GroupSegDesc d;
+            d.b = m.mm.b;
+            d.out = m.mm.output;
+            d.n = m.mm.n;
+            d.base = m.base;
+            d.act = m.act;
+            d.residual = m.residual;
+            return d;
+        };
+        g.segs.push_back(seg_of(mi));
+        std::vector<uint32_t> members{i};
+        std::vector<uint32_t> absorbed;
+        for (size_t q = p + 1; q < n && q <= p + 32 && g.segs.size() < size_t(holo::kSkinnyMaxSeg); ++q) {
+            const uint32_t j = order[q];
+            MmView mj;
+            if (taken[j] || !matmul_family(calls[j], &mj) || !groupable(mj)) continue;
+            if (!same_ref(mj.mm.a, mi.mm.a) || mj.mm.m != mi.mm.m || mj.mm.k != mi.mm.k ||
+                mj.mm.dtype != mi.mm.dtype)
+                continue;
+            const holo::SkinnyPlan pj = holo::matmul_skinny_plan(mj.mm.m, mj.mm.k, mj.mm.n, mj.mm.dtype);
+            if (pj.mt != pl.mt || pj.steps != pl.steps || pj.ks != pl.ks || !movable(q, p)) continue;
+            g.segs.push_back(seg_of(mj));
+            if (!segments_disjoint(g.segs, g.a)) {
+                g.segs.pop_back();
+                continue;
+            }
+            members.push_back(j);
+            taken[j] = true;
+        }
+        // pull each product's sole consumer into the epilogue
+        std::vector<holo_buffer_ref> value(g.segs.size());
+        std::vector<bool> done(g.segs.size(), false);
+        for (size_t t = 0; t < g.segs.size(); ++t) value[t] = g.segs[t].out;
+        for (size_t t = 0; t < g.segs.size(); ++t) {
+            while (!done[t]) {
+                const size_t qc = sole_reader(value[t].slot, p);
+                if (qc == npos || !movable(qc, p)) break;
+                const uint32_t c = order[qc];
+                const holo_kernel_call &cc = calls[c];
+                holo::GroupSegDesc trial = g.segs[t];
+                const uint64_t mn = uint64_t(g.m) * trial.n;
+                const bool free_seg = !trial.quant && trial.pair < 0 && !trial.skip;
+                std::vector<holo::GroupSegDesc> segs2 = g.segs;
+                bool ok = false, last = false;
+                int partner = -1;
+                if (cc.tag == HOLO_OP_ROTARY && free_seg && !trial.rope) {
+                    const auto &r = cc.u.rope;
+                    if (same_ref(r.x, value[t]) && r.dtype == g.dtype && pow2_head(r.head_dim) &&
+                        trial.n % r.head_dim == 0 && r.element_count == mn &&
+                        (trial.head_dim == 0 || trial.head_dim == r.head_dim)) {
+                        trial.rope = true;
+                        trial.cos = r.cos;
+                        trial.sin = r.sin;
+                        trial.rope_out = r.output;
+                        trial.head_dim = r.head_dim;
+                        trial.write_out = false;
+                        ok = true;
+                    }
+                } else if (cc.tag == HOLO_OP_KV_QUANT_APPEND && free_seg) {
+                    const auto &k = cc.u.kv_quant_append;
+                    if (same_ref(k.new_rows_buf, value[t]) && same_ref(k.output, k.cache) &&
+                        same_ref(k.output_scales, k.cache_scales) && k.dtype == g.dtype &&
+                        pow2_head(k.head_dim) && trial.n % k.head_dim == 0 &&
+                        (trial.head_dim == 0 || trial.head_dim == k.head_dim) && k.new_rows >= 1 &&
+                        k.bucket_rows >= 1 && uint64_t(k.planes) * k.new_rows * k.head_dim == mn) {
+                        trial.quant = true;
+                        trial.pos = k.pos;
+                        trial.cq = k.cache;
+                        trial.cs = k.cache_scales;
+                        trial.bucket = k.bucket_rows;
+                        trial.new_rows = k.new_rows;
+                        trial.head_dim = k.head_dim;
+                        if (trial.rope) trial.write_rope = false;
+                        else trial.write_out = false;
+                        ok = last = true;
+                    }
+                } else if (cc.tag == HOLO_OP_MUL && free_seg && !trial.rope && trial.head_dim == 0) {
+                    const auto &b = cc.u.binary;
+                    const holo_buffer_ref other = same_ref(b.a, value[t]) ? b.b
+                                                : same_ref(b.b, value[t]) ? b.a : holo_buffer_ref{HOLO_SLOT_ABSENT, 0, 0};
+                    for (size_t u = 0; u < g.segs.size() && other.slot != HOLO_SLOT_ABSENT; ++u) {
+                        const auto &su = g.segs[u];
+                        if (u == t || !same_ref(value[u], other) || su.rope || su.quant ||
+                            su.pair >= 0 || su.skip || su.head_dim || su.n != trial.n || done[u])
+                            continue;
+                        if (sole_reader(value[u].slot, p) != qc) continue;
+                        partner = int(u);
+                        break;
+                    }
+                    if (partner >= 0 && b.dtype == g.dtype && b.element_count == mn) {
+                        trial.pair = partner;
+                        trial.mul_out = b.output;
+                        trial.write_out = false;
+                        segs2[partner].skip = true;
+                        segs2[partner].write_out = false;
+                        ok = last = true;
+                    }
+                }
+                if (!ok) break;
+                segs2[t] = trial;
+                if (!segments_disjoint(segs2, g.a)) break;
+                g.segs = segs2;
+                taken[c] = true;
+                absorbed.push_back(c);
+                if (cc.tag == HOLO_OP_ROTARY) value[t] = cc.u.rope.output;
+                if (last) {
+                    done[t] = true;
+                    if (partner >= 0) done[partner] = true;
+                }
+            }
+        }
+        if (g.segs.size() == 1 && absorbed.empty()) {
+            s->nodes.push_back(Node{-1, i});
+            continue;
+        }
+        taken[i] = true;
+        s->groups.push_back(std::move(g));
+        s->nodes.push_back(Node{int(s->groups.size() - 1), i});
+    }
+}
 
 void release(holo_session *s) {
     if (!s) return;
@@ -193,7 +608,7 @@ void release(holo_session *s) {
     delete s;
 }
 
-int load_impl(holo_backend *be, const uint8_t *bytes, size_t len, holo_session **out) {
+int load_impl(holo_backend *be, const uint8_t *bytes, size_t len, uint32_t flags, holo_session **out) {
     const char *op = "session_load";
     // --- header + footer (loader.rs:141-185)
     if (len < 4 + 2 + 2 + 2 + 32)
@@ -205,6 +620,7 @@ int load_impl(holo_backend *be, const uint8_t *bytes, size_t len, holo_session *
         return set_error(HOLO_ERR_DISPATCH, "session_load: unsupported .holo version " + std::to_string(ver));
     auto s = std::unique_ptr<holo_session, void (*)(holo_session *)>(new holo_session(), release);
     s->be = be;
+    s->flags = flags;
     holo::blake3_hash(bytes, len - 32, s->fingerprint);
     if (memcmp(s->fingerprint, bytes + len - 32, 32) != 0)
         return set_error(HOLO_ERR_DISPATCH, "session_load: footer fingerprint mismatch (BLAKE3)");
@@ -270,6 +686,8 @@ int load_impl(holo_backend *be, const uint8_t *bytes, size_t len, holo_session *
         for (size_t i = 0; i < all.size(); ++i) all[i] = uint32_t(i);
         s->plan.push_back(std::move(all));
     }
+    // --- the loader's epilogue fusion (session.rs:493-509)
+    if (!(flags & HOLO_SESSION_NO_EPILOGUE_FUSION)) fuse_matmul_epilogue(s->calls, s->plan, s->outputs);
     // --- weights (fingerprint -> body), constants
     std::map<std::string, std::pair<const uint8_t *, uint64_t>> weights;
     if ((it = sec.find(kSecWeights)) != sec.end()) {
@@ -428,6 +846,13 @@ plan_moves:
                                      std::to_string(s->calls[i].tag) + "): " + m);
         }
     }
+    // --- the walk: fused groups, or every call in plan order
+    if (flags & HOLO_SESSION_NO_DEVICE_FUSION) {
+        for (auto &lv : s->plan)
+            for (uint32_t ci : lv) s->nodes.push_back(Node{-1, ci});
+    } else {
+        device_fusion(s.get(), is_output, is_input);
+    }
     *out = s.release();
     return HOLO_OK;
 }
@@ -439,16 +864,15 @@ int walk(holo_session *s) {
     const hipStream_t saved = holo::backend_stream(s->be);
     holo::set_backend_stream(s->be, s->stream);
     int rc = HOLO_OK;
-    for (const auto &level : s->plan) {
-        for (uint32_t i : level) {
-            rc = holo::dispatch_with_slots(s->be, s->slots, &s->calls[i]);
-            if (rc != HOLO_OK) {
-                std::string m = holo_hip_last_error_message();
-                set_error(rc, "session_execute: kernel call " + std::to_string(i) + ": " + m);
-                break;
-            }
+    for (const Node &nd : s->nodes) {
+        rc = nd.group >= 0 ? holo::dispatch_group(s->be, s->slots, s->groups[size_t(nd.group)])
+                           : holo::dispatch_with_slots(s->be, s->slots, &s->calls[nd.call]);
+        if (rc != HOLO_OK) {
+            std::string m = holo_hip_last_error_message();
+            set_error(rc, "session_execute: kernel call " + std::to_string(nd.call) +
+                              (nd.group >= 0 ? " (fused group)" : "") + ": " + m);
+            break;
         }
-        if (rc != HOLO_OK) break;
     }
     holo::set_backend_stream(s->be, saved);
     return rc;
@@ -468,7 +892,21 @@ extern "C" {
 int holo_hip_session_load(holo_backend *be, const uint8_t *bytes, size_t len, holo_session **out) {
     if (!bytes || !out) return set_error(HOLO_ERR_INIT, "session_load: null argument");
     *out = nullptr;
-    return load_impl(be, bytes, len, out);
+    return load_impl(be, bytes, len, 0, out);
+}
+
+int holo_hip_session_load_ex(holo_backend *be, const uint8_t *bytes, size_t len, uint32_t flags,
+                             holo_session **out) {
+    if (!bytes || !out) return set_error(HOLO_ERR_INIT, "session_load: null argument");
+    *out = nullptr;
+    return load_impl(be, bytes, len, flags, out);
+}
+
+int holo_hip_session_nodes(const holo_session *s, uint32_t *n_nodes, uint32_t *n_groups) {
+    if (!s) return set_error(HOLO_ERR_INIT, "session_nodes: null session");
+    if (n_nodes) *n_nodes = uint32_t(s->nodes.size());
+    if (n_groups) *n_groups = uint32_t(s->groups.size());
+    return HOLO_OK;
 }
 
 int holo_hip_session_close(holo_session *s) {

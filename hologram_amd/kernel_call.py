@@ -43,6 +43,9 @@ D_GELU = 14
 D_SILU = 15
 D_EXP = 18
 D_MATMUL = 46
+D_MMA = 106     # MatMulActivation (the loader's epilogue fusion)
+D_MMADD = 107   # MatMulAdd
+D_MMAA = 108    # MatMulAddActivation
 D_RN = 51
 D_ROTARY = 75
 D_GATHER = 114
@@ -53,6 +56,17 @@ D_DAI8 = 123   # new: decode attention over an int8 cache
 D_ARGMAX = 124  # new: per-row argmax (the greedy pick of a decode step)
 
 SLOT_ABSENT = 0xFFFFFFFF
+
+
+class fused_activation:  # noqa: N801 - the reference's module (kernel_call.rs:861-870)
+    RELU = 1
+    GELU = 2
+    SILU = 3
+    SIGMOID = 4
+    TANH = 5
+    ELU = 6
+    SELU = 7
+    EXP = 8
 
 
 @dataclass(frozen=True)
@@ -191,6 +205,37 @@ class MatMulCall:
 
 
 @dataclass(frozen=True)
+class MatMulActivationCall:
+    """kernel_call.rs:892-896: out = act(A*B)."""
+    mm: MatMulCall
+    act: int
+
+    def wire(self) -> bytes:  # kernel_codec.rs:509-513
+        return self.mm.wire() + struct.pack("<B", self.act)
+
+
+@dataclass(frozen=True)
+class MatMulAddCall:
+    """kernel_call.rs:906-911: out = A*B + residual."""
+    mm: MatMulCall
+    residual: BufferRef
+
+    def wire(self) -> bytes:  # kernel_codec.rs:514-518
+        return self.mm.wire() + self.residual.wire()
+
+
+@dataclass(frozen=True)
+class MatMulAddActivationCall:
+    """kernel_call.rs:923-929: out = act(A*B + residual)."""
+    mm: MatMulCall
+    residual: BufferRef
+    act: int
+
+    def wire(self) -> bytes:  # kernel_codec.rs:519-524
+        return self.mm.wire() + self.residual.wire() + struct.pack("<B", self.act)
+
+
+@dataclass(frozen=True)
 class KvCacheWriteCall:
     """kernel_call.rs:742-759."""
     cache: BufferRef
@@ -257,7 +302,8 @@ class DecodeAttentionI8Call:
 
 _NAMES = {D_ADD: "Add", D_MUL: "Mul", D_RN: "RmsNorm", D_ROTARY: "RotaryEmbedding",
           D_GATHER: "Gather", D_ARGMAX: "ArgMax", D_SIGMOID: "Sigmoid", D_TANH: "Tanh", D_GELU: "Gelu", D_SILU: "Silu", D_EXP: "Exp",
-          D_MATMUL: "MatMul", D_KVWR: "KvCacheWrite", D_KVQA: "KvQuantAppend",
+          D_MATMUL: "MatMul", D_MMA: "MatMulActivation", D_MMADD: "MatMulAdd",
+          D_MMAA: "MatMulAddActivation", D_KVWR: "KvCacheWrite", D_KVQA: "KvQuantAppend",
           D_DAI8: "DecodeAttentionI8"}
 
 
@@ -291,6 +337,18 @@ class KernelCall:
     @classmethod
     def MatMul(cls, c: MatMulCall) -> "KernelCall":  # noqa: N802
         return cls(D_MATMUL, c)
+
+    @classmethod
+    def MatMulActivation(cls, c: MatMulActivationCall) -> "KernelCall":  # noqa: N802
+        return cls(D_MMA, c)
+
+    @classmethod
+    def MatMulAdd(cls, c: MatMulAddCall) -> "KernelCall":  # noqa: N802
+        return cls(D_MMADD, c)
+
+    @classmethod
+    def MatMulAddActivation(cls, c: MatMulAddActivationCall) -> "KernelCall":  # noqa: N802
+        return cls(D_MMAA, c)
 
     @classmethod
     def Add(cls, c: BinaryCall) -> "KernelCall":  # noqa: N802
@@ -362,6 +420,12 @@ class KernelCall:
         elif isinstance(p, MatMulCall):
             kc.u.matmul = _ffi.MatMulCallC(p.a.c(), p.b.c(), p.output.c(), p.m, p.k, p.n,
                                            p.dtype, int(p.b_packed))
+        elif isinstance(p, MatMulActivationCall):
+            kc.u.matmul_act = _ffi.MatMulActCallC(_mm_c(p.mm), p.act)
+        elif isinstance(p, MatMulAddCall):
+            kc.u.matmul_add = _ffi.MatMulAddCallC(_mm_c(p.mm), p.residual.c())
+        elif isinstance(p, MatMulAddActivationCall):
+            kc.u.matmul_add_act = _ffi.MatMulAddActCallC(_mm_c(p.mm), p.residual.c(), p.act)
         elif isinstance(p, KvCacheWriteCall):
             kc.u.kv_write = _ffi.KvCacheWriteCallC(p.cache.c(), p.new.c(), p.pos.c(),
                                                    p.output.c(), p.planes, p.bucket_rows,
@@ -378,6 +442,11 @@ class KernelCall:
         else:
             raise TypeError(f"no C form for payload {type(p).__name__}")
         return kc
+
+
+def _mm_c(p: MatMulCall) -> _ffi.MatMulCallC:
+    return _ffi.MatMulCallC(p.a.c(), p.b.c(), p.output.c(), p.m, p.k, p.n, p.dtype,
+                            int(p.b_packed))
 
 
 def encode_calls(calls: list[KernelCall]) -> bytes:

@@ -24,21 +24,31 @@ class Port:
     nbytes: int
 
 
+# load options (include/holo_hip.h)
+NO_EPILOGUE_FUSION = 1   # skip the reference loader's fuse_matmul_epilogue
+NO_DEVICE_FUSION = 2     # skip this backend's grouped few-row MatMuls and epilogues
+
+
 class HipSession:
     """`backend=None` loads dry: parse, size and validate every call on the host,
-    with no device (such a session reports ports and refuses to execute)."""
+    with no device (such a session reports ports and refuses to execute).
+    `flags` turns the load-time fusions off (NO_EPILOGUE_FUSION, NO_DEVICE_FUSION);
+    fused and unfused walks give the same bits."""
 
-    def __init__(self, backend: HipBackend | None, archive: bytes):
+    def __init__(self, backend: HipBackend | None, archive: bytes, flags: int = 0):
         self._lib = _ffi.lib()
         self.backend = backend
         h = ctypes.c_void_p()
-        _check(self._lib.holo_hip_session_load(backend._h if backend else None, archive,
-                                               len(archive), ctypes.byref(h)))
+        _check(self._lib.holo_hip_session_load_ex(backend._h if backend else None, archive,
+                                                  len(archive), flags, ctypes.byref(h)))
         self.handle = h
         ni, no, nc, ns = (ctypes.c_uint32() for _ in range(4))
         _check(self._lib.holo_hip_session_info(self.handle, ctypes.byref(ni), ctypes.byref(no),
                                                ctypes.byref(nc), ctypes.byref(ns)))
         self.n_calls, self.n_slots = nc.value, ns.value
+        nn, ng = ctypes.c_uint32(), ctypes.c_uint32()
+        _check(self._lib.holo_hip_session_nodes(self.handle, ctypes.byref(nn), ctypes.byref(ng)))
+        self.n_nodes, self.n_groups = nn.value, ng.value
         self.inputs = [self._port(0, i) for i in range(ni.value)]
         self.outputs = [self._port(1, i) for i in range(no.value)]
 

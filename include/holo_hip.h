@@ -50,6 +50,17 @@ typedef enum holo_status {
 #define HOLO_ACT_SILU 3
 #define HOLO_ACT_EXP 4
 
+/* fused_activation ids of the fused MatMul epilogues,
+ * crates/hologram-compute/src/kernel_call.rs:861-870 */
+#define HOLO_FUSED_RELU 1
+#define HOLO_FUSED_GELU 2
+#define HOLO_FUSED_SILU 3
+#define HOLO_FUSED_SIGMOID 4
+#define HOLO_FUSED_TANH 5
+#define HOLO_FUSED_ELU 6
+#define HOLO_FUSED_SELU 7
+#define HOLO_FUSED_EXP 8
+
 /* KernelCall tags = the archive wire discriminants,
  * crates/hologram-archive/src/kernel_codec.rs:18-128. 122 and 123 are new
  * capabilities and take new discriminants (kernel_codec.rs:124-128). */
@@ -61,6 +72,9 @@ typedef enum holo_status {
 #define HOLO_OP_SILU 15u
 #define HOLO_OP_EXP 18u
 #define HOLO_OP_MATMUL 46u
+#define HOLO_OP_MATMUL_ACT 106u           /* MatMulActivation (kernel_codec.rs:102)    */
+#define HOLO_OP_MATMUL_ADD 107u           /* MatMulAdd (kernel_codec.rs:103)           */
+#define HOLO_OP_MATMUL_ADD_ACT 108u       /* MatMulAddActivation (kernel_codec.rs:104) */
 #define HOLO_OP_RMS_NORM 51u
 #define HOLO_OP_ROTARY 75u
 #define HOLO_OP_GATHER 114u
@@ -166,6 +180,31 @@ typedef struct holo_matmul_call {
     uint8_t b_packed;
 } holo_matmul_call;
 
+/* The fused MatMul epilogues the reference's loader produces from
+ * `matmul -> activation` and `matmul -> add(residual)` (fuse_matmul_epilogue,
+ * crates/hologram-exec/src/session.rs:2150-2373), kernel_call.rs:892-929:
+ *   MatMulActivation     out = f(A*B)           (float_kernels.rs:816-844)
+ *   MatMulAdd            out = A*B + residual   (:846-888)
+ *   MatMulAddActivation  out = f(A*B + residual) (:890-935)
+ * bf16 results are narrowed after the product (and again after the add), as
+ * the separate kernels would. Served activations: bf16 GELU/SILU/SIGMOID/TANH/
+ * EXP for MatMulActivation (through the same 65536-entry tables as the unary
+ * ops); GELU/SILU/SIGMOID/TANH otherwise (exp_f32_det); the rest return
+ * UnsupportedOp. The residual must not overlap the output (split_borrow). */
+typedef struct holo_matmul_act_call {
+    holo_matmul_call mm;
+    uint8_t act;
+} holo_matmul_act_call;
+typedef struct holo_matmul_add_call {
+    holo_matmul_call mm;
+    holo_buffer_ref residual;
+} holo_matmul_add_call;
+typedef struct holo_matmul_add_act_call {
+    holo_matmul_call mm;
+    holo_buffer_ref residual;
+    uint8_t act;
+} holo_matmul_add_act_call;
+
 /* KvCacheWriteCall, kernel_call.rs:742-759 (byte rows, honest copy:
  * src/cpu/kernels.rs:455-501). `pos` is a device-resident 4-byte LE u32. */
 typedef struct holo_kv_cache_write_call {
@@ -230,6 +269,9 @@ typedef struct holo_kernel_call {
         holo_gather_call gather;
         holo_argmax_call argmax;
         holo_matmul_call matmul;
+        holo_matmul_act_call matmul_act;
+        holo_matmul_add_call matmul_add;
+        holo_matmul_add_act_call matmul_add_act;
         holo_kv_cache_write_call kv_write;
         holo_kv_quant_append_call kv_quant_append;
         holo_decode_attention_i8_call attn_i8;
@@ -291,6 +333,19 @@ typedef struct holo_session holo_session;
  * but nothing is allocated and the session cannot execute (host-only checks). */
 int holo_hip_session_load(holo_backend *be, const uint8_t *archive, size_t len,
                           holo_session **out);
+/* Load with options. By default a load runs the reference's epilogue fusion
+ * (fuse_matmul_epilogue, session.rs:2150-2373) and then this backend's device
+ * fusion: few-row MatMuls that share their A operand run as one launch, and
+ * the ops that only consume such a product (rotary embedding, int8
+ * quantize+append, the SwiGLU product) run inside the launch that finishes
+ * it. Both give the same bits as the unfused walk; the flags turn them off. */
+#define HOLO_SESSION_NO_EPILOGUE_FUSION 1u
+#define HOLO_SESSION_NO_DEVICE_FUSION 2u
+int holo_hip_session_load_ex(holo_backend *be, const uint8_t *archive, size_t len, uint32_t flags,
+                             holo_session **out);
+/* Steps of one walk after fusion (each a call or a fused MatMul group), and
+ * how many of them are fused groups. */
+int holo_hip_session_nodes(const holo_session *s, uint32_t *n_nodes, uint32_t *n_groups);
 int holo_hip_session_close(holo_session *s);
 int holo_hip_session_info(const holo_session *s, uint32_t *n_inputs, uint32_t *n_outputs,
                           uint32_t *n_calls, uint32_t *n_slots);

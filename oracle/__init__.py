@@ -34,6 +34,7 @@ _SIGS = {
     "or_gelu_f": (_F, [_F]),
     "or_silu_f": (_F, [_F]),
     "or_lut_act_ref": (_F, [ctypes.c_int, _F]),
+    "or_fused_act_f32": (ctypes.c_int, [ctypes.c_int, _P, _P, _S]),
     "or_build_table": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _P]),
     "or_unary_lut": (None, [_P, _P, _P, _S]),
     "or_quantize_row_i8": (_F, [_P, _P, _S]),
@@ -165,6 +166,19 @@ def decode_attention_i8(q, kq, ks, vq, vs, lens, B, H, Hkv, bucket, D, scale) ->
     lib().or_decode_attention_i8(_p(q), _p(kq), _p(ks), _p(vq), _p(vs), _p(lens), _p(out), B,
                                  H, Hkv, bucket, D, scale)
     return out
+
+
+def fused_act_f32(act: int, x: np.ndarray) -> np.ndarray:
+    """fused_act_fn (float_kernels.rs:768-780) over f32 values; act is a
+    fused_activation id (kernel_call.rs:861-870)."""
+    x = np.ascontiguousarray(x, np.float32)
+    o = np.empty_like(x)
+    if lib().or_fused_act_f32(act, _p(x), _p(o), x.size) != 0:
+        raise ValueError(f"fused activation {act} is not restated")
+    return o
+
+
+FUSED_TO_LUT = {2: ACT_GELU, 3: ACT_SILU, 4: ACT_SIGMOID, 5: ACT_TANH, 8: ACT_EXP}
 
 
 def matmul_ref_f64(a, b, m, k, n) -> np.ndarray:

@@ -62,6 +62,14 @@ def _decode_call(r: _R) -> tuple:
     if tag == 46:                                    # put_matmul
         return tag, dict(a=r.buf(), b=r.buf(), output=r.buf(), m=r.u("I"), k=r.u("I"),
                          n=r.u("I"), dtype=r.u("B"), packed=r.u("B"))
+    if tag in (106, 107, 108):                       # put_matmul + epilogue (:509-524)
+        c = dict(a=r.buf(), b=r.buf(), output=r.buf(), m=r.u("I"), k=r.u("I"), n=r.u("I"),
+                 dtype=r.u("B"), packed=r.u("B"))
+        if tag != 106:
+            c["residual"] = r.buf()
+        if tag != 107:
+            c["act"] = r.u("B")
+        return tag, c
     if tag == 122:                                   # int8 quantize + append (new)
         return tag, dict(new=r.buf(), pos=r.buf(), cache=r.buf(), scales=r.buf(),
                          output=r.buf(), output_scales=r.buf(), planes=r.u("I"),
@@ -204,15 +212,23 @@ class OracleSession:
                            int(iw == 8)) != 0:
                 raise ValueError("gather: index out of range")
             self._out(c["output"], len(o))[:] = o
-        elif tag == 46:
+        elif tag in (46, 106, 107, 108):
+            # matmul_float, then the fused epilogues of float_kernels.rs:816-935
             m, k, n = c["m"], c["k"], c["n"]
-            es = DT_BYTES[c["dtype"]]
-            a = self._f32(self._view(c["a"], m * k * es), c["dtype"])
-            b = self._f32(self._view(c["b"], k * n * es), c["dtype"])
-            o = np.zeros(m * n, np.float32)
-            from . import matmul_ref_f64
-            o = matmul_ref_f64(a, b, m, k, n)
-            self._out(c["output"], m * n * es)[:] = self._narrow(o, c["dtype"])
+            dt = c["dtype"]
+            es = DT_BYTES[dt]
+            a = self._f32(self._view(c["a"], m * k * es), dt)
+            b = self._f32(self._view(c["b"], k * n * es), dt)
+            from . import FUSED_TO_LUT, build_table, fused_act_f32, matmul_ref_f64
+            v = self._f32(self._narrow(matmul_ref_f64(a, b, m, k, n), dt), dt)
+            if tag in (107, 108):
+                v = v + self._f32(self._view(c["residual"], m * n * es), dt)
+            if tag == 106 and dt == BF16:
+                t = build_table(FUSED_TO_LUT[c["act"]], dt)
+                v = self._f32(t[self._narrow(v, dt).view(np.uint16)].view(np.uint8), dt)
+            elif tag in (106, 108):
+                v = fused_act_f32(c["act"], v)
+            self._out(c["output"], m * n * es)[:] = self._narrow(v, dt)
         elif tag == 122:
             P, S, R, Dh = c["planes"], c["bucket"], c["new_rows"], c["head_dim"]
             es = DT_BYTES[c["dtype"]]

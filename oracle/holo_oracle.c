@@ -201,6 +201,24 @@ float or_gelu_f(float x)
 }
 float or_silu_f(float x) { return x * or_sigmoid_f(x); }
 
+/* fused_act_fn (src/cpu/float_kernels.rs:768-780) over a slice, the f32
+ * epilogue of MatMulActivation / MatMulAddActivation. ids: fused_activation
+ * (src/kernel_call.rs:861-870). Relu, Elu and Selu are not restated (-1). */
+int or_fused_act_f32(int act, const float *in, float *out, size_t n)
+{
+    for (size_t i = 0; i < n; ++i) {
+        switch (act) {
+        case 2: out[i] = or_gelu_f(in[i]); break;
+        case 3: out[i] = or_silu_f(in[i]); break;
+        case 4: out[i] = or_sigmoid_f(in[i]); break;
+        case 5: out[i] = or_tanh_f(in[i]); break;
+        case 8: out[i] = or_libm_expf(in[i]); break;
+        default: return -1;
+        }
+    }
+    return 0;
+}
+
 float or_lut_act_ref(int act, float x)
 {
     switch (act) {

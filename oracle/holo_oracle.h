@@ -59,6 +59,7 @@ float or_sigmoid_f(float x);               /* src/cpu/float_kernels.rs:3549-3551
 float or_tanh_f(float x);                  /* :3553-3558 */
 float or_gelu_f(float x);                  /* :3560-3562 */
 float or_silu_f(float x);                  /* :3564-3566 */
+int or_fused_act_f32(int act, const float *in, float *out, size_t n); /* fused_act_fn :768-780 */
 float or_lut_act_ref(int act, float x);    /* :3628-3638 (Erf not restated) */
 
 /* ---- LUT: src/cpu/lut.rs:43-67 (build) and :76-98 (gather) ---- */

@@ -12,6 +12,7 @@ from hologram_amd import (DTYPE_BF16, DTYPE_F32, DTYPE_I32, ArgMaxCall, BinaryCa
                           MatMulCall, NormCall, PortDescriptor, RoPECall, UnsupportedOp,
                           DispatchError, SlotOutOfRange, blake3, decode_call, validate)
 from hologram_amd.decoder_graph import DecoderConfig, build_decode_step, init_weights
+from hologram_amd.session import NO_EPILOGUE_FUSION
 from oracle.blake3_ref import blake3 as blake3_py
 from oracle.graph import OracleSession
 
@@ -122,7 +123,8 @@ def test_decoder_archive_loads_dry_with_in_place_caches():
     s = HipSession(None, a)
     assert len(s.inputs) == 7 + 4 * cfg.layers and len(s.outputs) == 2 + 4 * cfg.layers
     o = OracleSession(a)
-    assert len(o.calls) == s.n_calls == 1 + 18 * cfg.layers + 3
+    assert len(o.calls) == 1 + 18 * cfg.layers + 3
+    assert HipSession(None, a, flags=NO_EPILOGUE_FUSION).n_calls == len(o.calls)
 
 
 @pytest.mark.parametrize("call", [

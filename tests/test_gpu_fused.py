@@ -1,0 +1,149 @@
+"""GPU parity of the fused MatMul epilogues and of the fused session walk.
+
+The fused ops (MatMulActivation, MatMulAdd, MatMulAddActivation,
+src/cpu/float_kernels.rs:816-935) apply their epilogue to the product the
+unfused MatMul gives. So the check is bit for bit: the device's fused output
+equals the oracle's epilogue applied to the device's own unfused product. The
+product's accuracy is pinned separately (test_gpu_matmul.py).
+
+Both MatMul paths are covered: few rows, where the product is finished in the
+epilogue launch, and the tiled path, where the epilogue runs in place.
+
+The session is checked by stepping the same decoder archive with the fusions
+on and off. The load-time fusions must not change a single bit of any output
+(tokens, logits, int8 caches and scales).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import from_dev, to_dev
+from hologram_amd import (DTYPE_BF16, DTYPE_F32, BufferRef, DeviceWorkspace, HipSession,
+                          KernelCall, MatMulActivationCall, MatMulAddActivationCall,
+                          MatMulAddCall, MatMulCall, fused_activation)
+from hologram_amd.decoder_graph import DecoderConfig, build_decode_step, init_weights, rope_tables
+from hologram_amd.session import NO_DEVICE_FUSION, NO_EPILOGUE_FUSION
+
+pytestmark = pytest.mark.gpu
+
+FA = fused_activation
+
+
+def widen(bits, dtype):
+    if dtype == DTYPE_BF16:
+        return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+    return np.asarray(bits).view(np.float32)
+
+
+def narrow(x, dtype):
+    x = np.ascontiguousarray(x, np.float32)
+    return (x.view(np.uint32) >> 16).astype(np.uint16) if dtype == DTYPE_BF16 else x.view(np.uint32)
+
+
+CASES = [("act", FA.SILU, DTYPE_BF16), ("act", FA.GELU, DTYPE_BF16), ("act", FA.EXP, DTYPE_BF16),
+         ("act", FA.SIGMOID, DTYPE_F32), ("act", FA.TANH, DTYPE_F32), ("act", FA.SILU, DTYPE_F32),
+         ("add", 0, DTYPE_BF16), ("add", 0, DTYPE_F32),
+         ("addact", FA.GELU, DTYPE_F32), ("addact", FA.SILU, DTYPE_BF16)]
+
+
+@pytest.mark.parametrize("m", [8, 100])
+@pytest.mark.parametrize("kind,act,dtype", CASES)
+def test_fused_matmul_bit_exact(torch_cuda, backend, m, kind, act, dtype):
+    k, n = 512, 384
+    rng = np.random.default_rng(m * 31 + act)
+    a32 = (rng.standard_normal(m * k) * (3 / np.sqrt(k))).astype(np.float32)
+    b32 = rng.standard_normal(k * n).astype(np.float32)
+    r32 = rng.standard_normal(m * n).astype(np.float32)
+    a, b, r = (narrow(x, dtype) for x in (a32, b32, r32))
+    es = 2 if dtype == DTYPE_BF16 else 4
+    ws = DeviceWorkspace()
+    keep = [to_dev(torch_cuda, x) for x in (a, b, r)]
+    for s, t in enumerate(keep):
+        ws.bind(s, t)
+    prod = torch_cuda.zeros(m * n * es, dtype=torch_cuda.uint8, device="cuda")
+    fused = torch_cuda.zeros(m * n * es, dtype=torch_cuda.uint8, device="cuda")
+    ws.bind(3, prod)
+    ws.bind(4, fused)
+    mm = MatMulCall(BufferRef(0), BufferRef(1), BufferRef(3), m, k, n, dtype)
+    backend.dispatch(KernelCall.MatMul(mm), ws)
+    mmf = MatMulCall(BufferRef(0), BufferRef(1), BufferRef(4), m, k, n, dtype)
+    if kind == "act":
+        call = KernelCall.MatMulActivation(MatMulActivationCall(mmf, act))
+    elif kind == "add":
+        call = KernelCall.MatMulAdd(MatMulAddCall(mmf, BufferRef(2)))
+    else:
+        call = KernelCall.MatMulAddActivation(MatMulAddActivationCall(mmf, BufferRef(2), act))
+    backend.dispatch(call, ws)
+    backend.synchronize()
+    bits_t = np.uint16 if dtype == DTYPE_BF16 else np.uint32
+    p = from_dev(prod, bits_t)
+    got = from_dev(fused, bits_t)
+    v = widen(p, dtype)
+    if kind == "act" and dtype == DTYPE_BF16:
+        want = oracle.build_table(oracle.FUSED_TO_LUT[act], dtype)[p]
+    elif kind == "act":
+        want = narrow(oracle.fused_act_f32(act, v), dtype)
+    elif kind == "add":
+        want = narrow(v + widen(r, dtype), dtype)
+    else:
+        want = narrow(oracle.fused_act_f32(act, v + widen(r, dtype)), dtype)
+    bad = np.flatnonzero(got != want)
+    assert bad.size == 0, f"{bad.size} mismatches, first at {bad[:4]}: {got[bad[:4]]} vs {want[bad[:4]]}"
+
+
+CFG = DecoderConfig(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=1000,
+                    batch=3, bucket=64)
+
+
+def step_inputs(cfg, step, tokens):
+    cq, sq = rope_tables(cfg, np.array([step]), cfg.heads)
+    ck, sk = rope_tables(cfg, np.array([step]), cfg.kv_heads)
+    return [np.asarray(tokens, np.int32).tobytes(), np.uint32(step).tobytes(),
+            np.full(cfg.batch, step + 1, np.uint32).tobytes(), cq, sq, ck, sk]
+
+
+def walk(backend, archive, flags, steps, graph=False):
+    cfg = CFG
+    sess = HipSession(backend, archive, flags=flags)
+    P, S, Dh = cfg.planes, cfg.bucket, cfg.head_dim
+    for layer in range(cfg.layers):
+        for j, z in enumerate([bytes(P * S * Dh), bytes(P * S * 4)] * 2):
+            sess.write_input(7 + 4 * layer + j, z)
+    tokens = np.arange(cfg.batch) * 11 + 5
+    record = []
+    for step in range(steps):
+        for i, b in enumerate(step_inputs(cfg, step, tokens)):
+            sess.write_input(i, b)
+        if graph and step == 0:
+            sess.capture()            # step 0 runs eagerly, then the walk is recorded
+        elif graph:
+            sess.replay()
+        else:
+            sess.run()
+        sess.synchronize()
+        record.append([sess.read_output(o) for o in range(len(sess.outputs))])
+        tokens = np.frombuffer(record[-1][0], np.int32)
+    counts = (sess.n_calls, sess.n_nodes, sess.n_groups)
+    sess.close()
+    return record, counts
+
+
+def test_session_fusion_is_bit_identical(torch_cuda, backend):
+    archive = build_decode_step(CFG, init_weights(CFG, seed=21))
+    base, base_counts = walk(backend, archive, NO_EPILOGUE_FUSION | NO_DEVICE_FUSION, 5)
+    assert base_counts[2] == 0
+    for flags in (NO_DEVICE_FUSION, NO_EPILOGUE_FUSION, 0):
+        rec, counts = walk(backend, archive, flags, 5)
+        if not flags & NO_DEVICE_FUSION:
+            assert counts[2] > 0 and counts[1] < base_counts[1]
+        for step, (x, y) in enumerate(zip(rec, base)):
+            for o, (u, v) in enumerate(zip(x, y)):
+                assert u == v, f"flags {flags}: step {step}, output {o} differs"
+
+
+def test_fused_session_graph_replay_matches_eager(torch_cuda, backend):
+    archive = build_decode_step(CFG, init_weights(CFG, seed=23))
+    eager, _ = walk(backend, archive, 0, 6)
+    graph, _ = walk(backend, archive, 0, 6, graph=True)
+    for step, (x, y) in enumerate(zip(eager, graph)):
+        assert x == y, f"step {step}"

@@ -35,6 +35,10 @@ namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// One wavefront per workgroup: the epilogue of a decode step is a few
+// thousand threads, spread over as many CUs as possible.
+constexpr uint32_t kEpiThreads = 64;
+
 __device__ __forceinline__ float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
 __device__ __forceinline__ uint32_t f2bf(float f) { return __float_as_uint(f) >> 16; }
 
@@ -99,7 +103,27 @@ __device__ __forceinline__ int pick(const EpiArgs &g, uint32_t *first_block) {
 }
 
 // The product at (row m, column c) of P's column space: partials summed in
-// ks order (or the tiled output read back). Four partials in flight.
+// ks order (or the tiled output read back). Up to kBatch loads go out before
+// the first add, so a split of up to kBatch partials costs one memory round
+// trip; the adds keep ks order.
+constexpr uint32_t kBatch = 32;
+
+template <class T>
+__device__ __forceinline__ T sum_partials(const T *p, uint64_t plane, uint32_t ks) {
+    T s{};
+    for (uint32_t k0 = 0; k0 < ks; k0 += kBatch) {
+        T v[kBatch];
+#pragma unroll
+        for (uint32_t u = 0; u < kBatch; ++u)
+            if (k0 + u < ks) v[u] = p[(k0 + u) * plane];
+        if (k0 == 0) s = v[0];
+#pragma unroll
+        for (uint32_t u = 0; u < kBatch; ++u)
+            if (k0 + u < ks && (k0 | u) != 0) s += v[u];
+    }
+    return s;
+}
+
 template <bool kBf16>
 __device__ __forceinline__ float product(const EpiArgs &g, uint32_t m, uint32_t c) {
     if (g.ks == 0) {
@@ -108,75 +132,77 @@ __device__ __forceinline__ float product(const EpiArgs &g, uint32_t m, uint32_t 
         else
             return static_cast<const float *>(g.src)[uint64_t(m) * g.ntot + c];
     }
-    const uint64_t plane = uint64_t(g.m) * g.ntot;
-    const float *p = g.P + uint64_t(m) * g.ntot + c;
-    float s = p[0];
-    uint32_t k = 1;
-    for (; k + 4 <= g.ks; k += 4) {
-        const float v0 = p[k * plane], v1 = p[(k + 1) * plane], v2 = p[(k + 2) * plane],
-                    v3 = p[(k + 3) * plane];
-        s += v0;
-        s += v1;
-        s += v2;
-        s += v3;
-    }
-    for (; k < g.ks; ++k) s += p[k * plane];
-    return s;
+    return sum_partials(g.P + uint64_t(m) * g.ntot + c, uint64_t(g.m) * g.ntot, g.ks);
 }
 
-// The same for Q*4 consecutive columns (c a multiple of 4), as 16-byte loads.
-template <bool kBf16, int Q>
-__device__ __forceinline__ void product_vec(const EpiArgs &g, uint32_t m, uint32_t c, float *v) {
+// The same for 4 consecutive columns (c a multiple of 4), as 16-byte loads.
+template <bool kBf16>
+__device__ __forceinline__ f32x4 product4(const EpiArgs &g, uint32_t m, uint32_t c) {
+    if (g.ks == 0)
+        return f32x4{product<kBf16>(g, m, c), product<kBf16>(g, m, c + 1),
+                     product<kBf16>(g, m, c + 2), product<kBf16>(g, m, c + 3)};
+    return sum_partials(reinterpret_cast<const f32x4 *>(g.P + uint64_t(m) * g.ntot + c),
+                        uint64_t(g.m) * g.ntot / 4, g.ks);
+}
+
+// Two columns (c, c + off) of one row, their partials in flight together.
+template <bool kBf16>
+__device__ __forceinline__ void product2(const EpiArgs &g, uint32_t m, uint32_t c, uint32_t off,
+                                        float *x1, float *x2) {
     if (g.ks == 0) {
-#pragma unroll
-        for (int j = 0; j < 4 * Q; ++j) v[j] = product<kBf16>(g, m, c + j);
+        *x1 = product<kBf16>(g, m, c);
+        *x2 = product<kBf16>(g, m, c + off);
         return;
     }
-    const uint64_t plane = uint64_t(g.m) * g.ntot / 4;
-    const f32x4 *p = reinterpret_cast<const f32x4 *>(g.P + uint64_t(m) * g.ntot + c);
-    f32x4 s[Q];
+    const uint64_t plane = uint64_t(g.m) * g.ntot;
+    const float *p = g.P + uint64_t(m) * g.ntot + c;
+    float s1 = 0.0f, s2 = 0.0f;
+    for (uint32_t k0 = 0; k0 < g.ks; k0 += kBatch / 2) {
+        float v1[kBatch / 2], v2[kBatch / 2];
 #pragma unroll
-    for (int q = 0; q < Q; ++q) s[q] = p[q];
-    uint32_t k = 1;
-    for (; k + 4 <= g.ks; k += 4) {
-        f32x4 t[4][Q];
+        for (uint32_t u = 0; u < kBatch / 2; ++u)
+            if (k0 + u < g.ks) {
+                v1[u] = p[(k0 + u) * plane];
+                v2[u] = p[(k0 + u) * plane + off];
+            }
+        if (k0 == 0) {
+            s1 = v1[0];
+            s2 = v2[0];
+        }
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-            for (int q = 0; q < Q; ++q) t[u][q] = p[(k + u) * plane + q];
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-            for (int q = 0; q < Q; ++q) s[q] += t[u][q];
+        for (uint32_t u = 0; u < kBatch / 2; ++u)
+            if (k0 + u < g.ks && (k0 | u) != 0) {
+                s1 += v1[u];
+                s2 += v2[u];
+            }
     }
-    for (; k < g.ks; ++k)
-#pragma unroll
-        for (int q = 0; q < Q; ++q) s[q] += p[k * plane + q];
-#pragma unroll
-    for (int q = 0; q < Q; ++q)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[4 * q + j] = s[q][j];
+    *x1 = s1;
+    *x2 = s2;
 }
 
-// The segment's base value from its product v (bf16: the result is a bf16
-// bit pattern widened back to f32, so later steps see exactly the stored value).
+// The segment's base value from its product v and (for the add forms) the
+// residual r (bf16: the result is a bf16 bit pattern widened back to f32, so
+// later steps see exactly the stored value).
 template <bool kBf16>
-__device__ __forceinline__ float base_value(const EpiSeg &sg, float v, uint64_t e) {
+__device__ __forceinline__ float base_value(const EpiSeg &sg, float v, float r) {
     if constexpr (kBf16) {
         uint32_t x = f2bf(v);
         if (sg.base == kEpiAct) x = sg.lut[x];   // f(widen(x)) narrowed: the table entry
         if (sg.base == kEpiAdd || sg.base == kEpiAddAct) {
-            const float s = bf2f(x) + bf2f(static_cast<const uint16_t *>(sg.residual)[e]);
+            const float s = bf2f(x) + r;
             // MatMulAddActivation applies f to the f32 sum before narrowing
             x = f2bf(sg.base == kEpiAddAct ? act_f32(sg.act, s) : s);
         }
         return bf2f(x);
     } else {
-        if (sg.base == kEpiAdd || sg.base == kEpiAddAct)
-            v = v + static_cast<const float *>(sg.residual)[e];
+        if (sg.base == kEpiAdd || sg.base == kEpiAddAct) v = v + r;
         if (sg.base == kEpiAct || sg.base == kEpiAddAct) v = act_f32(sg.act, v);
         return v;
     }
+}
+
+__device__ __forceinline__ bool has_residual(const EpiSeg &sg) {
+    return sg.base == kEpiAdd || sg.base == kEpiAddAct;
 }
 
 template <bool kBf16>
@@ -202,26 +228,62 @@ __device__ __forceinline__ int8_t to_q(float r) {
     return static_cast<int8_t>(static_cast<int32_t>(r));
 }
 
-// Element-wise segments: E consecutive columns of one row per thread.
+// Element-wise segments: 4 consecutive columns of one row per thread. The
+// residual and both segments' partials are loaded before any arithmetic.
 template <bool kBf16>
 __device__ void elem_segment(const EpiArgs &g, const EpiSeg &sg, const EpiSeg &pr, uint32_t blk) {
-    constexpr uint32_t E = kBf16 ? 8 : 4;
-    const uint64_t i = (uint64_t(blk) * 256 + threadIdx.x) * E;
+    const uint64_t i = (uint64_t(blk) * kEpiThreads + threadIdx.x) * 4;
     if (i >= uint64_t(g.m) * sg.n) return;
     const uint32_t m = uint32_t(i / sg.n), c = uint32_t(i % sg.n);
     const uint64_t e0 = uint64_t(m) * sg.n + c;
-    float va[E], vb[E];
-    product_vec<kBf16, E / 4>(g, m, sg.col0 + c, va);
-    if (sg.pair >= 0) product_vec<kBf16, E / 4>(g, m, pr.col0 + c, vb);
+    float ra[4] = {0.f, 0.f, 0.f, 0.f}, rb[4] = {0.f, 0.f, 0.f, 0.f};
+    if (has_residual(sg))
 #pragma unroll
-    for (uint32_t j = 0; j < E; ++j) {
-        va[j] = base_value<kBf16>(sg, va[j], e0 + j);
+        for (uint32_t j = 0; j < 4; ++j) ra[j] = load<kBf16>(sg.residual, e0 + j);
+    const bool pair = sg.pair >= 0;
+    if (pair && has_residual(pr))
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) rb[j] = load<kBf16>(pr.residual, e0 + j);
+    f32x4 va, vb = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (g.ks == 0) {
+        va = product4<kBf16>(g, m, sg.col0 + c);
+        if (pair) vb = product4<kBf16>(g, m, pr.col0 + c);
+    } else if (!pair) {
+        va = product4<kBf16>(g, m, sg.col0 + c);
+    } else {
+        // both segments' partials in flight together
+        const uint64_t plane = uint64_t(g.m) * g.ntot / 4;
+        const f32x4 *pa = reinterpret_cast<const f32x4 *>(g.P + uint64_t(m) * g.ntot + sg.col0 + c);
+        const f32x4 *pb = reinterpret_cast<const f32x4 *>(g.P + uint64_t(m) * g.ntot + pr.col0 + c);
+        for (uint32_t k0 = 0; k0 < g.ks; k0 += kBatch / 2) {
+            f32x4 xa[kBatch / 2], xb[kBatch / 2];
+#pragma unroll
+            for (uint32_t u = 0; u < kBatch / 2; ++u)
+                if (k0 + u < g.ks) {
+                    xa[u] = pa[(k0 + u) * plane];
+                    xb[u] = pb[(k0 + u) * plane];
+                }
+            if (k0 == 0) {
+                va = xa[0];
+                vb = xb[0];
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < kBatch / 2; ++u)
+                if (k0 + u < g.ks && (k0 | u) != 0) {
+                    va += xa[u];
+                    vb += xb[u];
+                }
+        }
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+        va[j] = base_value<kBf16>(sg, va[j], ra[j]);
         if (sg.out) store<kBf16>(sg.out, e0 + j, va[j]);
     }
-    if (sg.pair < 0) return;
+    if (!pair) return;
 #pragma unroll
-    for (uint32_t j = 0; j < E; ++j) {
-        vb[j] = base_value<kBf16>(pr, vb[j], e0 + j);
+    for (uint32_t j = 0; j < 4; ++j) {
+        vb[j] = base_value<kBf16>(pr, vb[j], rb[j]);
         if (pr.out) store<kBf16>(pr.out, e0 + j, vb[j]);
         store<kBf16>(sg.mul_out, e0 + j, va[j] * vb[j]);
     }
@@ -232,7 +294,7 @@ __device__ void elem_segment(const EpiArgs &g, const EpiSeg &sg, const EpiSeg &p
 template <bool kBf16>
 __device__ void head_segment(const EpiArgs &g, const EpiSeg &sg, uint32_t blk) {
     const uint32_t D = sg.head_dim, half = D / 2;
-    const uint32_t heads_per_block = 256 / half;
+    const uint32_t heads_per_block = kEpiThreads / half;
     const uint32_t hl = threadIdx.x / half, d = threadIdx.x % half;
     const uint32_t heads_row = sg.n / D;
     const uint64_t head = uint64_t(blk) * heads_per_block + hl;
@@ -243,15 +305,28 @@ __device__ void head_segment(const EpiArgs &g, const EpiSeg &sg, uint32_t blk) {
         const uint32_t m = uint32_t(head / heads_row), h = uint32_t(head % heads_row);
         const uint32_t c1 = h * D + d;
         e1 = uint64_t(m) * sg.n + c1;
-        x1 = base_value<kBf16>(sg, product<kBf16>(g, m, sg.col0 + c1), e1);
-        x2 = base_value<kBf16>(sg, product<kBf16>(g, m, sg.col0 + c1 + half), e1 + half);
+        // side operands first: their loads overlap the partials'
+        float c1v = 0.f, s1v = 0.f, c2v = 0.f, s2v = 0.f;
+        if (sg.rope) {
+            c1v = load<kBf16>(sg.cos, e1);
+            s1v = load<kBf16>(sg.sin, e1);
+            c2v = load<kBf16>(sg.cos, e1 + half);
+            s2v = load<kBf16>(sg.sin, e1 + half);
+        }
+        float r1 = 0.f, r2 = 0.f;
+        if (has_residual(sg)) {
+            r1 = load<kBf16>(sg.residual, e1);
+            r2 = load<kBf16>(sg.residual, e1 + half);
+        }
+        float p1, p2;
+        product2<kBf16>(g, m, sg.col0 + c1, half, &p1, &p2);
+        x1 = base_value<kBf16>(sg, p1, r1);
+        x2 = base_value<kBf16>(sg, p2, r2);
         if (sg.out) {
             store<kBf16>(sg.out, e1, x1);
             store<kBf16>(sg.out, e1 + half, x2);
         }
         if (sg.rope) {
-            const float c1v = load<kBf16>(sg.cos, e1), s1v = load<kBf16>(sg.sin, e1);
-            const float c2v = load<kBf16>(sg.cos, e1 + half), s2v = load<kBf16>(sg.sin, e1 + half);
             float y1 = x1 * c1v - x2 * s1v;
             float y2 = x2 * c2v + x1 * s2v;
             if constexpr (kBf16) {
@@ -297,7 +372,7 @@ __device__ void head_segment(const EpiArgs &g, const EpiSeg &sg, uint32_t blk) {
 }
 
 template <bool kBf16>
-__global__ __launch_bounds__(256) void epilogue_kernel(const EpiArgs g) {
+__global__ __launch_bounds__(kEpiThreads) void epilogue_kernel(const EpiArgs g) {
     uint32_t b0;
     const int s = pick(g, &b0);
     const EpiSeg &sg = s == 0 ? g.seg[0] : s == 1 ? g.seg[1] : s == 2 ? g.seg[2] : g.seg[3];
@@ -313,29 +388,29 @@ __global__ __launch_bounds__(256) void epilogue_kernel(const EpiArgs g) {
 
 }  // namespace
 
-uint32_t epilogue_blocks(const EpiSeg &sg, uint32_t m, bool bf16) {
+uint32_t epilogue_blocks(const EpiSeg &sg, uint32_t m) {
     if (sg.skip) return 0;
     if (sg.head_dim) {
-        const uint32_t heads_per_block = 256 / (sg.head_dim / 2);
+        const uint32_t heads_per_block = kEpiThreads / (sg.head_dim / 2);
         const uint64_t heads = uint64_t(m) * (sg.n / sg.head_dim);
         return uint32_t((heads + heads_per_block - 1) / heads_per_block);
     }
-    const uint64_t threads = uint64_t(m) * sg.n / (bf16 ? 8 : 4);
-    return uint32_t((threads + 255) / 256);
+    const uint64_t threads = uint64_t(m) * sg.n / 4;
+    return uint32_t((threads + kEpiThreads - 1) / kEpiThreads);
 }
 
 hipError_t launch_epilogue(EpiArgs g, hipStream_t stream) {
     if (g.nseg < 1 || g.nseg > uint32_t(kSkinnyMaxSeg)) return hipErrorInvalidValue;
     uint32_t total = 0;
     for (uint32_t i = 0; i < g.nseg; ++i) {
-        total += epilogue_blocks(g.seg[i], g.m, g.bf16);
+        total += epilogue_blocks(g.seg[i], g.m);
         g.blk_end[i] = total;
     }
     if (total == 0) return hipSuccess;
     if (g.bf16)
-        hipLaunchKernelGGL(epilogue_kernel<true>, dim3(total), dim3(256), 0, stream, g);
+        hipLaunchKernelGGL(epilogue_kernel<true>, dim3(total), dim3(kEpiThreads), 0, stream, g);
     else
-        hipLaunchKernelGGL(epilogue_kernel<false>, dim3(total), dim3(256), 0, stream, g);
+        hipLaunchKernelGGL(epilogue_kernel<false>, dim3(total), dim3(kEpiThreads), 0, stream, g);
     return hipGetLastError();
 }
 

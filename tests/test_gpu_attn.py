@@ -155,3 +155,18 @@ def test_large_batch_grid_form(torch_cuda, backend):
             assert np.all(got[b] == 0)
         else:
             assert norm_err(got[b], want[b]) <= TOL, f"sequence {b} (len {lens[b]})"
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_short_contexts_one_chunk_per_plane(torch_cuda, backend, D):
+    """Many planes whose bucket fits one chunk (a decode step's shape: 8 sequences
+    x 8 kv heads, bucket 1024): one workgroup per plane, no merge launch."""
+    B, H, Hkv, bucket = 8, 32, 8, 1024
+    lens = [0, 1, 31, 128, 513, 767, 1024, 4000]
+    got, want, _ = run_case(torch_cuda, backend, B, H, Hkv, D, bucket, lens, DTYPE_BF16,
+                            seed=D + 1)
+    for b in range(B):
+        if lens[b] == 0:
+            assert np.all(got[b] == 0)
+        else:
+            assert norm_err(got[b], want[b]) <= TOL, f"sequence {b} (len {lens[b]})"

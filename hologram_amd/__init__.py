@@ -12,11 +12,12 @@ from .backend import (BackendError, DeviceWorkspace, DispatchError, HipBackend, 
                       ShapeMismatch, SlotOutOfRange, UnsupportedOp, decode_call, lut_table,
                       validate)
 from .kernel_call import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, DTYPE_I8, DTYPE_I32, DTYPE_I64,
-                          NO_BUFFER, SLOT_ABSENT, ArgMaxCall, BinaryCall, BufferRef,
+                          NO_BUFFER, SLOT_ABSENT, ArgMaxCall, AttentionI8RowsCall, BinaryCall,
+                          BufferRef,
                           DecodeAttentionI8Call, GatherCall, KernelCall, KvCacheWriteCall,
                           KvQuantAppendCall, MatMulActivationCall, MatMulAddActivationCall,
-                          MatMulAddCall, MatMulCall, NormCall, RoPECall, UnaryCall, encode_calls,
-                          fused_activation, lut_act)
+                          MatMulAddCall, MatMulCall, NormCall, RoPECall, TransposeCall, UnaryCall,
+                          encode_calls, fused_activation, lut_act)
 from .archive import ConstantEntry, HoloWriter, PortDescriptor, blake3
 from .session import HipSession
 
@@ -24,9 +25,10 @@ __all__ = [
     "BackendError", "DeviceWorkspace", "DispatchError", "HipBackend", "InitError",
     "ShapeMismatch", "SlotOutOfRange", "UnsupportedOp", "decode_call", "lut_table", "validate",
     "DTYPE_BF16", "DTYPE_F16", "DTYPE_F32", "DTYPE_I8", "DTYPE_I32", "DTYPE_I64",
-    "NO_BUFFER", "SLOT_ABSENT", "ArgMaxCall", "BinaryCall", "BufferRef",
+    "NO_BUFFER", "SLOT_ABSENT", "ArgMaxCall", "AttentionI8RowsCall", "BinaryCall", "BufferRef",
     "DecodeAttentionI8Call", "GatherCall", "KernelCall", "KvCacheWriteCall",
     "KvQuantAppendCall", "MatMulActivationCall", "MatMulAddActivationCall", "MatMulAddCall",
-    "MatMulCall", "NormCall", "RoPECall", "UnaryCall", "encode_calls", "fused_activation",
+    "MatMulCall", "NormCall", "RoPECall", "TransposeCall", "UnaryCall", "encode_calls",
+    "fused_activation",
     "lut_act", "ConstantEntry", "HoloWriter", "PortDescriptor", "blake3", "HipSession",
 ]

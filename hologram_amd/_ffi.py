@@ -102,13 +102,24 @@ class DecodeAttentionI8CallC(ctypes.Structure):
                 ("dtype", ctypes.c_uint8)]
 
 
+class AttentionI8RowsCallC(ctypes.Structure):
+    _fields_ = [("attn", DecodeAttentionI8CallC), ("q_rows", ctypes.c_uint32)]
+
+
+class TransposeCallC(ctypes.Structure):
+    _fields_ = [("input", BufferRefC), ("output", BufferRefC), ("rank", ctypes.c_uint8),
+                ("dims", ctypes.c_uint32 * 8), ("perm", ctypes.c_uint8 * 8),
+                ("dtype", ctypes.c_uint8)]
+
+
 class CallUnion(ctypes.Union):
     _fields_ = [("unary", UnaryCallC), ("binary", BinaryCallC), ("norm", NormCallC),
                 ("rope", RopeCallC), ("gather", GatherCallC), ("argmax", ArgMaxCallC),
                 ("matmul", MatMulCallC), ("matmul_act", MatMulActCallC),
                 ("matmul_add", MatMulAddCallC), ("matmul_add_act", MatMulAddActCallC),
                 ("kv_write", KvCacheWriteCallC),
-                ("kv_quant_append", KvQuantAppendCallC), ("attn_i8", DecodeAttentionI8CallC)]
+                ("kv_quant_append", KvQuantAppendCallC), ("attn_i8", DecodeAttentionI8CallC),
+                ("attn_i8_rows", AttentionI8RowsCallC), ("transpose", TransposeCallC)]
 
 
 class KernelCallC(ctypes.Structure):

@@ -146,8 +146,8 @@ template <int D, bool kF32Q>
 __device__ __forceinline__ void attn_segment(
     const void *__restrict__ q, const int8_t *__restrict__ kq, const int8_t *__restrict__ vq,
     const float *__restrict__ ks, const float *__restrict__ vs, float *__restrict__ dst,
-    void *__restrict__ out, uint32_t b, uint32_t kh, uint32_t c0, uint32_t c1, bool single,
-    uint32_t H, uint32_t Hkv, uint32_t G, uint32_t bucket, float log2e_over_scale,
+    void *__restrict__ out, uint32_t b, uint32_t qrow, uint32_t kh, uint32_t c0, uint32_t c1,
+    bool single, uint32_t H, uint32_t Hkv, uint32_t G, uint32_t bucket, float log2e_over_scale,
     SegLds<D> &lds) {
     constexpr int KB = D / 4;          // K bytes per lane per key row (QK k-slots)
     constexpr int NKS = D / 64;        // i8 MFMA k-steps (64 dims each)
@@ -231,7 +231,7 @@ __device__ __forceinline__ void attn_segment(
     if (wv == 0) {
         float qv[KB];
         const bool live = uint32_t(r) < G;
-        const uint64_t qi = (uint64_t(b) * H + kh * G + (live ? r : 0)) * D + KB * g;
+        const uint64_t qi = (uint64_t(qrow) * H + kh * G + (live ? r : 0)) * D + KB * g;
         if constexpr (kF32Q) {
             const u32x4 *src = reinterpret_cast<const u32x4 *>(static_cast<const float *>(q) + qi);
 #pragma unroll
@@ -447,7 +447,7 @@ __device__ __forceinline__ void attn_segment(
             l = fmaf(lds.red_l[w][h], sc, l);
         }
         if (single) {
-            const uint64_t oi = (uint64_t(b) * H + kh * G + h) * D + d;
+            const uint64_t oi = (uint64_t(qrow) * H + kh * G + h) * D + d;
             if constexpr (kF32Q)
                 static_cast<float *>(out)[oi] = o / l;
             else
@@ -463,6 +463,14 @@ __device__ __forceinline__ void attn_segment(
     __syncthreads();   // the caller may reuse the LDS next
 }
 
+// Keys visible to a query row `back` rows before the last of its sequence:
+// the sequence's visible length less `back` (none if that is not positive),
+// at most the bucket.
+__device__ __forceinline__ uint32_t visible_keys(uint32_t len, uint32_t back, uint32_t bucket) {
+    const uint32_t L = len > back ? len - back : 0u;
+    return L < bucket ? L : bucket;
+}
+
 // Grid form for very large batches: grid (chunks, Hkv, B), one workgroup per
 // kChunk-key chunk of a plane; chunks at or beyond L_b exit at once, and chunk
 // 0 of a plane with no visible key writes the exact zero rows. Partial of
@@ -472,20 +480,20 @@ __global__ __launch_bounds__(kThreads, kWps) void attn_chunk_kernel(
     const void *__restrict__ q, const int8_t *__restrict__ kq, const int8_t *__restrict__ vq,
     const float *__restrict__ ks, const float *__restrict__ vs, const uint32_t *__restrict__ lens,
     float *__restrict__ part, void *__restrict__ out, uint32_t H, uint32_t Hkv, uint32_t G,
-    uint32_t bucket, uint32_t kChunk, uint32_t nchunks, float log2e_over_scale) {
+    uint32_t bucket, uint32_t kChunk, uint32_t nchunks, float log2e_over_scale, uint32_t q_rows) {
     __shared__ SegLds<D> lds;
-    const uint32_t b = blockIdx.z, kh = blockIdx.y, chunk = blockIdx.x;
-    uint32_t L = lens[b];
-    if (L > bucket) L = bucket;
+    const uint32_t v = blockIdx.z, kh = blockIdx.y, chunk = blockIdx.x;
+    const uint32_t b = v / q_rows;
+    const uint32_t L = visible_keys(lens[b], q_rows - 1 - v % q_rows, bucket);
     const uint32_t c0 = chunk * kChunk;
     if (c0 >= L) {
-        if (L == 0 && chunk == 0) zero_rows<kF32Q>(out, b, kh, H, G, D, threadIdx.x, kThreads);
+        if (L == 0 && chunk == 0) zero_rows<kF32Q>(out, v, kh, H, G, D, threadIdx.x, kThreads);
         return;
     }
     const uint32_t c1 = L - c0 < kChunk ? L : c0 + kChunk;
-    const uint64_t plane = uint64_t(b) * Hkv + kh;
-    float *dst = part + (plane * nchunks + chunk) * G * (D + 2);
-    attn_segment<D, kF32Q>(q, kq, vq, ks, vs, dst, out, b, kh, c0, c1, L <= kChunk, H, Hkv, G,
+    const uint64_t row_plane = uint64_t(v) * Hkv + kh;
+    float *dst = part + (row_plane * nchunks + chunk) * G * (D + 2);
+    attn_segment<D, kF32Q>(q, kq, vq, ks, vs, dst, out, b, v, kh, c0, c1, L <= kChunk, H, Hkv, G,
                            bucket, log2e_over_scale, lds);
 }
 
@@ -585,7 +593,7 @@ __global__ __launch_bounds__(kThreads, kWps) void attn_split_kernel(
         const bool single = x == ps && se == pe;
         const uint64_t p = uint64_t(b) * Hkv + kh;
         float *dst = part + (p + w) * G * (D + 2);
-        attn_segment<D, kF32Q>(q, kq, vq, ks, vs, dst, out, b, kh, c0, c1, single, H, Hkv, G,
+        attn_segment<D, kF32Q>(q, kq, vq, ks, vs, dst, out, b, b, kh, c0, c1, single, H, Hkv, G,
                                bucket, log2e_over_scale, lds);
         x = se;
         if (++kh == Hkv) {
@@ -664,16 +672,15 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restri
                                                           void *__restrict__ out, uint32_t H,
                                                           uint32_t Hkv, uint32_t G,
                                                           uint32_t bucket, uint32_t kChunk,
-                                                          uint32_t nchunks) {
+                                                          uint32_t nchunks, uint32_t q_rows) {
     __shared__ float wgt[kMaxSeg][16];
     __shared__ float inv_l[16];
-    const uint32_t kh = blockIdx.x, b = blockIdx.y;
-    uint32_t L = lens[b];
-    if (L > bucket) L = bucket;
+    const uint32_t kh = blockIdx.x, v = blockIdx.y;
+    const uint32_t L = visible_keys(lens[v / q_rows], q_rows - 1 - v % q_rows, bucket);
     const uint32_t nch = (L + kChunk - 1) / kChunk;
     if (nch <= 1) return;
-    const uint64_t plane = uint64_t(b) * Hkv + kh;
-    merge_partials<D, kF32Q>(part + plane * nchunks * G * (D + 2), nch, out, b, kh, H, G, wgt,
+    const uint64_t row_plane = uint64_t(v) * Hkv + kh;
+    merge_partials<D, kF32Q>(part + row_plane * nchunks * G * (D + 2), nch, out, v, kh, H, G, wgt,
                              inv_l);
 }
 
@@ -777,7 +784,7 @@ hipError_t run_t(const AttnI8Args &a, void *scratch, hipStream_t stream) {
     const uint32_t G = a.H / a.Hkv;
     float *part = static_cast<float *>(scratch);
     const float mul = kLog2e / a.score_scale;
-    if (use_split(a.B, a.Hkv, a.bucket)) {
+    if (a.q_rows == 1 && use_split(a.B, a.Hkv, a.bucket)) {
         const uint32_t P = split_wgs<D, kF32Q>();
         uint32_t *qoff = reinterpret_cast<uint32_t *>(part + split_part_floats(a.B, a.H, a.Hkv, D, P));
         hipLaunchKernelGGL((attn_split_kernel<D, kF32Q>), dim3(P), dim3(kThreads), 0, stream, a.q,
@@ -791,13 +798,14 @@ hipError_t run_t(const AttnI8Args &a, void *scratch, hipStream_t stream) {
     }
     const uint32_t ck = chunk_keys(a.bucket);
     const uint32_t nch = chunks_of(a.bucket);
-    hipLaunchKernelGGL((attn_chunk_kernel<D, kF32Q>), dim3(nch, a.Hkv, a.B), dim3(kThreads), 0,
+    const uint32_t rows = a.B * a.q_rows;
+    hipLaunchKernelGGL((attn_chunk_kernel<D, kF32Q>), dim3(nch, a.Hkv, rows), dim3(kThreads), 0,
                        stream, a.q, a.kq, a.vq, a.ks, a.vs, a.lens, part, a.out, a.H, a.Hkv, G,
-                       a.bucket, ck, nch, mul);
+                       a.bucket, ck, nch, mul, a.q_rows);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || nch == 1) return e;
-    hipLaunchKernelGGL((attn_combine_kernel<D, kF32Q>), dim3(a.Hkv, a.B), dim3(256), 0, stream,
-                       part, a.lens, a.out, a.H, a.Hkv, G, a.bucket, ck, nch);
+    hipLaunchKernelGGL((attn_combine_kernel<D, kF32Q>), dim3(a.Hkv, rows), dim3(256), 0, stream,
+                       part, a.lens, a.out, a.H, a.Hkv, G, a.bucket, ck, nch, a.q_rows);
     return hipGetLastError();
 }
 
@@ -807,20 +815,25 @@ hipError_t run(const AttnI8Args &a, void *scratch, hipStream_t stream) {
 }
 
 template <int D, bool kF32Q>
-size_t scratch_t(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t bucket) {
-    if (use_split(B, Hkv, bucket))
+size_t scratch_t(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t bucket, uint32_t q_rows) {
+    if (q_rows == 1 && use_split(B, Hkv, bucket))
         return split_part_floats(B, H, Hkv, D, split_wgs<D, kF32Q>()) * sizeof(float) +
                size_t(B + 1) * sizeof(uint32_t);
-    return size_t(B) * H * chunks_of(bucket) * (D + 2) * sizeof(float);
+    return size_t(B) * q_rows * H * chunks_of(bucket) * (D + 2) * sizeof(float);
 }
 
 }  // namespace
 
-size_t attn_i8_scratch_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t bucket, uint32_t D) {
+size_t attn_i8_scratch_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t bucket, uint32_t D,
+                             uint32_t q_rows) {
     // the larger of the bf16 and f32 instantiations' needs (their occupancy may differ)
     size_t n = 0;
-    if (D == 128) n = std::max(scratch_t<128, false>(B, H, Hkv, bucket), scratch_t<128, true>(B, H, Hkv, bucket));
-    if (D == 64) n = std::max(scratch_t<64, false>(B, H, Hkv, bucket), scratch_t<64, true>(B, H, Hkv, bucket));
+    if (D == 128)
+        n = std::max(scratch_t<128, false>(B, H, Hkv, bucket, q_rows),
+                     scratch_t<128, true>(B, H, Hkv, bucket, q_rows));
+    if (D == 64)
+        n = std::max(scratch_t<64, false>(B, H, Hkv, bucket, q_rows),
+                     scratch_t<64, true>(B, H, Hkv, bucket, q_rows));
     return n;
 }
 

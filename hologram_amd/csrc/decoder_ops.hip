@@ -268,6 +268,38 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const void *__restrict__ i
     }
 }
 
+// Transpose (transpose_float, src/cpu/float_kernels.rs:2980-3028): output
+// axis i is input axis perm[i]. The copy unit is a piece of an output row of
+// the last axis when that axis stays last (16 bytes when rows and bases allow,
+// else one element), one element otherwise; each thread finds its input
+// offset from the output coordinates.
+struct TransposeArgs {
+    const uint8_t *in;
+    uint8_t *out;
+    uint32_t lead;                 // output axes decomposed per unit
+    uint64_t out_dims[8];
+    uint64_t in_stride[8];         // bytes per step of output axis i in the input
+    uint64_t unit_bytes, units_per_row, units;
+};
+
+__global__ __launch_bounds__(256) void transpose_kernel(const TransposeArgs a) {
+    const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
+    for (uint64_t u = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; u < a.units; u += stride) {
+        const uint64_t row = u / a.units_per_row, piece = u % a.units_per_row;
+        uint64_t rem = row, src = piece * a.unit_bytes;
+        for (int i = int(a.lead) - 1; i >= 0; --i) {
+            src += (rem % a.out_dims[i]) * a.in_stride[i];
+            rem /= a.out_dims[i];
+        }
+        const uint8_t *s = a.in + src;
+        uint8_t *d = a.out + u * a.unit_bytes;
+        if (a.unit_bytes == 16)
+            *reinterpret_cast<u32x4 *>(d) = *reinterpret_cast<const u32x4 *>(s);
+        else
+            for (uint64_t b = 0; b < a.unit_bytes; ++b) d[b] = s[b];
+    }
+}
+
 unsigned grid_for(uint64_t work, unsigned cap = 4096) {
     const uint64_t g = (work + 255) / 256;
     return unsigned(g == 0 ? 1 : (g < cap ? g : cap));
@@ -335,6 +367,34 @@ hipError_t launch_gather(const void *data, const void *idx, void *out, uint64_t 
         hipLaunchKernelGGL((gather_kernel<false>), grid, dim3(256), 0, stream,
                            static_cast<const uint8_t *>(data), idx, static_cast<uint8_t *>(out),
                            axis_dim, num_idx, row_bytes, err);
+    return hipGetLastError();
+}
+
+hipError_t launch_transpose(const void *in, void *out, uint32_t rank, const uint32_t *dims,
+                            const uint8_t *perm, uint32_t es, hipStream_t stream) {
+    if (rank == 0 || rank > 8) return hipErrorInvalidValue;
+    uint64_t in_stride[8], total = 1;
+    for (int i = int(rank) - 1; i >= 0; --i) {
+        in_stride[i] = total * es;
+        total *= dims[i];
+    }
+    if (total == 0) return hipSuccess;
+    TransposeArgs a{};
+    a.in = static_cast<const uint8_t *>(in);
+    a.out = static_cast<uint8_t *>(out);
+    for (uint32_t i = 0; i < rank; ++i) {
+        a.out_dims[i] = dims[perm[i]];
+        a.in_stride[i] = in_stride[perm[i]];
+    }
+    const bool keep_last = perm[rank - 1] == rank - 1;
+    const uint64_t row_bytes = keep_last ? uint64_t(dims[rank - 1]) * es : es;
+    a.lead = keep_last ? rank - 1 : rank;
+    const bool vec = keep_last && row_bytes % 16 == 0 &&
+                     ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+    a.unit_bytes = vec ? 16 : es;
+    a.units_per_row = row_bytes / a.unit_bytes;
+    a.units = total * es / a.unit_bytes;
+    hipLaunchKernelGGL(transpose_kernel, dim3(grid_for(a.units, 16384)), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

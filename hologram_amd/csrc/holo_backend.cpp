@@ -528,7 +528,8 @@ int do_kv_quant(holo_backend *be, const SlotTable &st, const holo_kv_quant_appen
 
 // ---------------------------------------------------- DecodeAttnI8 -------
 // Refusals follow decode_attention_valid_float (src/cpu/float_kernels.rs:4192-4220).
-int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attention_i8_call &c) {
+int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attention_i8_call &c,
+               uint32_t q_rows = 1) {
     const char *op = "decode_attention_i8";
     if (c.batch == 0 || c.heads == 0 || c.head_dim == 0) return HOLO_OK;
     const uint32_t hkv = c.kv_heads == 0 ? c.heads : c.kv_heads;
@@ -542,7 +543,8 @@ int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attentio
                     "decode_attention_i8: head_dim must be 64 or 128, heads/kv_heads at most 16 "
                     "and bucket_rows * head_dim at most 2^30");
     const uint64_t es = dtype_size(c.dtype);
-    const uint64_t qn = uint64_t(c.batch) * c.heads * c.head_dim;
+    if (q_rows == 0) return fail(HOLO_ERR_UNSUPPORTED_OP, std::string(op) + ": q_rows must be >= 1");
+    const uint64_t qn = uint64_t(c.batch) * q_rows * c.heads * c.head_dim;
     const uint64_t rows = uint64_t(c.batch) * hkv * c.bucket_rows;
     holo_buffer_ref reads[6] = {c.q, c.k_cache, c.v_cache, c.k_scales, c.v_scales, c.lens};
     View rv[6], out;
@@ -555,8 +557,9 @@ int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attentio
     HOLO_TRY(need(rv[5], uint64_t(c.batch) * 4, c.lens.slot, op, "lens"));
     HOLO_TRY(need(out, qn * es, c.output.slot, op, "output"));
     // launch-shape limits of the kernels: grid (chunks, kv_heads, batch)
-    if (c.batch > 65535 || hkv > 65535)
-        return fail(HOLO_ERR_UNSUPPORTED_OP, "decode_attention_i8: batch and kv_heads must be <= 65535");
+    if (uint64_t(c.batch) * q_rows > 65535 || hkv > 65535)
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    std::string(op) + ": batch * q_rows and kv_heads must be <= 65535");
     // vector loads: 16-byte K/V rows, 4-byte scales/lens, element-aligned q/out
     if (!aligned(rv[1], 16) || !aligned(rv[2], 16) || !aligned(rv[3], 4) || !aligned(rv[4], 4) ||
         !aligned(rv[5], 4) || !aligned(rv[0], es) || !aligned(out, es))
@@ -574,7 +577,8 @@ int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attentio
         scale = sm > 0.0f ? 1.0f / sm : dflt;
     }
     HOLO_TRY(ensure_scratch(
-        be, holo::attn_i8_scratch_bytes(c.batch, c.heads, hkv, c.bucket_rows, c.head_dim), op));
+        be, holo::attn_i8_scratch_bytes(c.batch, c.heads, hkv, c.bucket_rows, c.head_dim, q_rows),
+        op));
     holo::AttnI8Args a;
     a.q = rv[0].base;
     a.kq = reinterpret_cast<const int8_t *>(rv[1].base);
@@ -590,6 +594,7 @@ int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attentio
     a.D = c.head_dim;
     a.score_scale = scale;
     a.dtype = c.dtype;
+    a.q_rows = q_rows;
     if (c.bucket_rows == 0) {
         // No key can be visible: the pinned zero vector (pinned_semantics.rs).
         return launched(holo::launch_fill_zero(out.base, qn * es, be->stream), op);
@@ -717,6 +722,37 @@ int do_gather(holo_backend *be, const SlotTable &st, const holo_gather_call &c) 
                     op);
 }
 
+// --------------------------------------------------------- Transpose -----
+// transpose_float (src/cpu/float_kernels.rs:2980-3028).
+int do_transpose(holo_backend *be, const SlotTable &st, const holo_transpose_call &c) {
+    const char *op = "transpose";
+    if (c.rank == 0 || c.rank > 8)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "transpose: rank must be 1..=8");
+    if (c.dtype != HOLO_DTYPE_F16 && c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F32)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "transpose: the device path serves f16, bf16 and f32");
+    uint32_t seen = 0;
+    for (uint32_t i = 0; i < c.rank; ++i) {
+        if (c.perm[i] >= c.rank || (seen >> c.perm[i]) & 1u)
+            return fail(HOLO_ERR_UNSUPPORTED_OP, "transpose: perm must be a permutation of 0..rank");
+        seen |= 1u << c.perm[i];
+    }
+    const uint64_t es = dtype_size(c.dtype);
+    uint64_t total = 1;
+    for (uint32_t i = 0; i < c.rank; ++i) total *= c.dims[i];
+    View in, out;
+    HOLO_TRY(split_borrow(st, &c.input, &in, 1, c.output, &out, op));
+    if (in.bytes < total * es || out.bytes < total * es)
+        return fail(HOLO_ERR_SLOT_OUT_OF_RANGE,
+                    "transpose: an operand is shorter than the tensor (slot " +
+                        std::to_string(c.output.slot) + ")");
+    if (!aligned(in, es) || !aligned(out, es))
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "transpose: operands must be element-aligned");
+    if (!be || total == 0) return HOLO_OK;
+    return launched(holo::launch_transpose(in.base, out.base, c.rank, c.dims, c.perm, uint32_t(es),
+                                           be->stream),
+                    op);
+}
+
 // ------------------------------------------------------------ ArgMax -----
 int do_argmax(holo_backend *be, const SlotTable &st, const holo_argmax_call &c) {
     const char *op = "argmax";
@@ -764,6 +800,9 @@ int dispatch_impl(holo_backend *be, const SlotTable &st, const holo_kernel_call 
         case HOLO_OP_KV_CACHE_WRITE: return do_kv_write(be, st, call->u.kv_write);
         case HOLO_OP_KV_QUANT_APPEND: return do_kv_quant(be, st, call->u.kv_quant_append);
         case HOLO_OP_DECODE_ATTN_I8: return do_attn_i8(be, st, call->u.attn_i8);
+        case HOLO_OP_ATTN_I8_ROWS:
+            return do_attn_i8(be, st, call->u.attn_i8_rows.attn, call->u.attn_i8_rows.q_rows);
+        case HOLO_OP_TRANSPOSE: return do_transpose(be, st, call->u.transpose);
         default:
             return fail(HOLO_ERR_UNSUPPORTED_OP,
                         "dispatch: kernel call tag " + std::to_string(call->tag) +
@@ -939,8 +978,9 @@ int decode_impl(const uint8_t *wire, size_t len, holo_kernel_call *out, size_t *
             c.dtype = r.get<uint8_t>();
             break;
         }
-        case HOLO_OP_DECODE_ATTN_I8: {  // field order of holo_decode_attention_i8_call
-            auto &c = out->u.attn_i8;
+        case HOLO_OP_DECODE_ATTN_I8:
+        case HOLO_OP_ATTN_I8_ROWS: {  // field order of holo_decode_attention_i8_call (+ q_rows)
+            auto &c = out->tag == HOLO_OP_ATTN_I8_ROWS ? out->u.attn_i8_rows.attn : out->u.attn_i8;
             c.q = r.buf();
             c.k_cache = r.buf();
             c.v_cache = r.buf();
@@ -954,6 +994,17 @@ int decode_impl(const uint8_t *wire, size_t len, holo_kernel_call *out, size_t *
             c.bucket_rows = r.get<uint32_t>();
             c.head_dim = r.get<uint32_t>();
             c.scale_bits = r.get<uint32_t>();
+            c.dtype = r.get<uint8_t>();
+            if (out->tag == HOLO_OP_ATTN_I8_ROWS) out->u.attn_i8_rows.q_rows = r.get<uint32_t>();
+            break;
+        }
+        case HOLO_OP_TRANSPOSE: {  // put_transpose :687-697
+            auto &c = out->u.transpose;
+            c.input = r.buf();
+            c.output = r.buf();
+            c.rank = r.get<uint8_t>();
+            for (auto &d : c.dims) d = r.get<uint32_t>();
+            for (auto &p : c.perm) p = r.get<uint8_t>();
             c.dtype = r.get<uint8_t>();
             break;
         }

@@ -41,8 +41,11 @@ struct AttnI8Args {
     uint32_t B, H, Hkv, bucket, D;
     float score_scale;      // the divisor: sqrtf(D) or 1/scale_multiplier
     uint8_t dtype;
+    uint32_t q_rows = 1;    // query rows per sequence (q/out [B, q_rows, H, D]); row t
+                            // sees min(lens[b] - (q_rows - 1 - t), bucket) keys
 };
-size_t attn_i8_scratch_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t bucket, uint32_t D);
+size_t attn_i8_scratch_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t bucket, uint32_t D,
+                             uint32_t q_rows = 1);
 bool attn_i8_supported(uint32_t H, uint32_t Hkv, uint32_t D, uint32_t bucket);
 hipError_t launch_attn_i8(const AttnI8Args &a, void *scratch, hipStream_t stream);
 
@@ -61,6 +64,10 @@ hipError_t launch_gather(const void *data, const void *idx, void *out, uint64_t 
                          int *err, hipStream_t stream);
 hipError_t launch_argmax(const void *in, int32_t *out, uint32_t rows, uint32_t cols, bool bf16,
                          hipStream_t stream);
+// Axis permutation of a row-major [dims[0], .., dims[rank-1]] tensor of es-byte
+// elements: output axis i is input axis perm[i] (perm a permutation of 0..rank-1).
+hipError_t launch_transpose(const void *in, void *out, uint32_t rank, const uint32_t *dims,
+                            const uint8_t *perm, uint32_t es, hipStream_t stream);
 
 // gemm.hip — C = A*B row-major, fp32 accumulation. dtype f32 or bf16 (bf16
 // result narrowed by truncation). `scratch` holds split-K partials of the

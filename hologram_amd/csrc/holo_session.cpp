@@ -144,8 +144,11 @@ void call_operands(const holo_kernel_call &c, std::vector<holo_buffer_ref> *read
             r(k.new_rows_buf); r(k.pos); r(k.cache); r(k.cache_scales);
             w(k.output); w(k.output_scales); break;
         }
-        case HOLO_OP_DECODE_ATTN_I8: {
-            const auto &a = c.u.attn_i8;
+        case HOLO_OP_TRANSPOSE:
+            r(c.u.transpose.input); w(c.u.transpose.output); break;
+        case HOLO_OP_DECODE_ATTN_I8:
+        case HOLO_OP_ATTN_I8_ROWS: {
+            const auto &a = c.tag == HOLO_OP_ATTN_I8_ROWS ? c.u.attn_i8_rows.attn : c.u.attn_i8;
             r(a.q); r(a.k_cache); r(a.v_cache); r(a.k_scales); r(a.v_scales); r(a.lens);
             w(a.output); break;
         }

@@ -34,9 +34,10 @@ from dataclasses import dataclass
 import numpy as np
 
 from .archive import ConstantEntry, HoloWriter, PortDescriptor
-from .kernel_call import (DTYPE_BF16, DTYPE_F32, DTYPE_I8, DTYPE_I32, ArgMaxCall, BinaryCall,
-                          BufferRef, DecodeAttentionI8Call, GatherCall, KernelCall,
-                          KvQuantAppendCall, MatMulCall, NormCall, RoPECall, UnaryCall)
+from .kernel_call import (DTYPE_BF16, DTYPE_F32, DTYPE_I8, DTYPE_I32, ArgMaxCall,
+                          AttentionI8RowsCall, BinaryCall, BufferRef, DecodeAttentionI8Call,
+                          GatherCall, KernelCall, KvQuantAppendCall, MatMulCall, NormCall, RoPECall,
+                          TransposeCall, UnaryCall)
 
 
 @dataclass(frozen=True)
@@ -114,9 +115,31 @@ class _Builder:
 
 def build_decode_step(cfg: DecoderConfig, weights: dict) -> bytes:
     """The `.holo` archive of one decode step (see the module docstring)."""
+    return _build(cfg, weights, 1)
+
+
+def build_prefill(cfg: DecoderConfig, weights: dict, rows: int) -> bytes:
+    """The `.holo` archive of a prompt pass: `rows` tokens of every sequence at
+    once, appended to the caches at ring rows pos .. pos + rows - 1.
+
+    Same weights and cache ports as the decode step. Per-row tensors are
+    token-major [B * rows, ...]; k and v go through Transpose
+    ([B, rows, Hkv, Dh] -> [B, Hkv, rows, Dh], the caches' row order) before the
+    append, and attention is AttentionI8Rows (row t sees lens[b] - (rows - 1 - t)
+    keys: causal). Only each sequence's last row continues past the layers
+    (Gather), so logits and the next token are [B] as in the decode step.
+    Inputs: tokens i32[B, rows], pos u32[1], lens u32[B] (= pos + rows),
+    cos_q/sin_q bf16[B, rows, H, Dh], cos_k/sin_k bf16[B, rows, Hkv, Dh], caches."""
+    if rows < 2:
+        raise ValueError("a prompt pass has at least two rows; one row is the decode step")
+    return _build(cfg, weights, rows)
+
+
+def _build(cfg: DecoderConfig, weights: dict, T: int) -> bytes:
     B, Dm, H, Hkv, Dh, F, V, S = (cfg.batch, cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim,
                                   cfg.ffn, cfg.vocab, cfg.bucket)
     P = cfg.planes
+    R = B * T           # rows through the layers
     g = _Builder()
     w = HoloWriter()
     bf = 2
@@ -126,23 +149,24 @@ def build_decode_step(cfg: DecoderConfig, weights: dict) -> bytes:
         (w.outputs if out else w.inputs).append(PortDescriptor(name, ref.slot, count, dtype,
                                                                list(shape)))
 
-    def const(body: bytes, dtype=DTYPE_BF16) -> BufferRef:
+    def const(body: bytes, dtype=DTYPE_BF16, inline=False) -> BufferRef:
         ref = g.slot(len(body))
-        w.constants.append(ConstantEntry(ref.slot, dtype, body, by_reference=True))
+        w.constants.append(ConstantEntry(ref.slot, dtype, body, by_reference=not inline))
         return ref
 
-    tokens = g.slot(4 * B)
+    tokens = g.slot(4 * R)
     pos = g.slot(4)
     lens = g.slot(4 * B)
-    cos_q, sin_q = g.slot(B * H * Dh * bf), g.slot(B * H * Dh * bf)
-    cos_k, sin_k = g.slot(B * Hkv * Dh * bf), g.slot(B * Hkv * Dh * bf)
-    port("tokens", tokens, B, DTYPE_I32, [B])
+    cos_q, sin_q = g.slot(R * H * Dh * bf), g.slot(R * H * Dh * bf)
+    cos_k, sin_k = g.slot(R * Hkv * Dh * bf), g.slot(R * Hkv * Dh * bf)
+    rshape = [B] if T == 1 else [B, T]
+    port("tokens", tokens, R, DTYPE_I32, rshape)
     port("pos", pos, 1, DTYPE_I32, [1])
     port("lens", lens, B, DTYPE_I32, [B])
-    port("cos_q", cos_q, B * H * Dh, DTYPE_BF16, [B, H, Dh])
-    port("sin_q", sin_q, B * H * Dh, DTYPE_BF16, [B, H, Dh])
-    port("cos_k", cos_k, B * Hkv * Dh, DTYPE_BF16, [B, Hkv, Dh])
-    port("sin_k", sin_k, B * Hkv * Dh, DTYPE_BF16, [B, Hkv, Dh])
+    port("cos_q", cos_q, R * H * Dh, DTYPE_BF16, rshape + [H, Dh])
+    port("sin_q", sin_q, R * H * Dh, DTYPE_BF16, rshape + [H, Dh])
+    port("cos_k", cos_k, R * Hkv * Dh, DTYPE_BF16, rshape + [Hkv, Dh])
+    port("sin_k", sin_k, R * Hkv * Dh, DTYPE_BF16, rshape + [Hkv, Dh])
     caches = []
     for layer in range(cfg.layers):
         kq, ks = g.slot(P * S * Dh), g.slot(P * S * 4)
@@ -155,50 +179,64 @@ def build_decode_step(cfg: DecoderConfig, weights: dict) -> bytes:
         caches.append((kq, ks, vq, vs))
 
     emb = const(weights["embedding"])
-    x = g.slot(B * Dm * bf)
-    g.add(KernelCall.Gather(GatherCall(emb, tokens, x, 1, V, Dm, B, DTYPE_I32, DTYPE_BF16)))
+    x = g.slot(R * Dm * bf)
+    g.add(KernelCall.Gather(GatherCall(emb, tokens, x, 1, V, Dm, R, DTYPE_I32, DTYPE_BF16)))
     new_caches = []
     for layer in range(cfg.layers):
         lw = weights[f"l{layer}"]
         kq, ks, vq, vs = caches[layer]
-        h = g.slot(B * Dm * bf)
-        g.add(KernelCall.RmsNorm(NormCall(x, const(lw["attn_norm"]), h, B, Dm, eps, DTYPE_BF16)))
-        q, k, v = g.slot(B * H * Dh * bf), g.slot(B * Hkv * Dh * bf), g.slot(B * Hkv * Dh * bf)
-        g.add(KernelCall.MatMul(MatMulCall(h, const(lw["wq"]), q, B, Dm, H * Dh, DTYPE_BF16)))
-        g.add(KernelCall.MatMul(MatMulCall(h, const(lw["wk"]), k, B, Dm, Hkv * Dh, DTYPE_BF16)))
-        g.add(KernelCall.MatMul(MatMulCall(h, const(lw["wv"]), v, B, Dm, Hkv * Dh, DTYPE_BF16)))
-        qr, kr = g.slot(B * H * Dh * bf), g.slot(B * Hkv * Dh * bf)
-        g.add(KernelCall.RotaryEmbedding(RoPECall(q, cos_q, sin_q, qr, Dh, B * H * Dh, DTYPE_BF16)))
-        g.add(KernelCall.RotaryEmbedding(RoPECall(k, cos_k, sin_k, kr, Dh, B * Hkv * Dh,
+        h = g.slot(R * Dm * bf)
+        g.add(KernelCall.RmsNorm(NormCall(x, const(lw["attn_norm"]), h, R, Dm, eps, DTYPE_BF16)))
+        q, k, v = g.slot(R * H * Dh * bf), g.slot(R * Hkv * Dh * bf), g.slot(R * Hkv * Dh * bf)
+        g.add(KernelCall.MatMul(MatMulCall(h, const(lw["wq"]), q, R, Dm, H * Dh, DTYPE_BF16)))
+        g.add(KernelCall.MatMul(MatMulCall(h, const(lw["wk"]), k, R, Dm, Hkv * Dh, DTYPE_BF16)))
+        g.add(KernelCall.MatMul(MatMulCall(h, const(lw["wv"]), v, R, Dm, Hkv * Dh, DTYPE_BF16)))
+        qr, kr = g.slot(R * H * Dh * bf), g.slot(R * Hkv * Dh * bf)
+        g.add(KernelCall.RotaryEmbedding(RoPECall(q, cos_q, sin_q, qr, Dh, R * H * Dh, DTYPE_BF16)))
+        g.add(KernelCall.RotaryEmbedding(RoPECall(k, cos_k, sin_k, kr, Dh, R * Hkv * Dh,
                                                   DTYPE_BF16)))
+        if T > 1:   # token-major rows -> the caches' [plane][row] order
+            kt, vt = g.slot(R * Hkv * Dh * bf), g.slot(R * Hkv * Dh * bf)
+            for src, dst in ((kr, kt), (v, vt)):
+                g.add(KernelCall.Transpose(TransposeCall(src, dst, (B, T, Hkv, Dh), (0, 2, 1, 3),
+                                                         DTYPE_BF16)))
+            kr, v = kt, vt
         kq2, ks2 = g.slot(P * S * Dh), g.slot(P * S * 4)
         vq2, vs2 = g.slot(P * S * Dh), g.slot(P * S * 4)
-        g.add(KernelCall.KvQuantAppend(KvQuantAppendCall(kr, pos, kq, ks, kq2, ks2, P, S, 1, Dh,
+        g.add(KernelCall.KvQuantAppend(KvQuantAppendCall(kr, pos, kq, ks, kq2, ks2, P, S, T, Dh,
                                                          DTYPE_BF16)))
-        g.add(KernelCall.KvQuantAppend(KvQuantAppendCall(v, pos, vq, vs, vq2, vs2, P, S, 1, Dh,
+        g.add(KernelCall.KvQuantAppend(KvQuantAppendCall(v, pos, vq, vs, vq2, vs2, P, S, T, Dh,
                                                          DTYPE_BF16)))
         new_caches.append((kq2, ks2, vq2, vs2))
-        a = g.slot(B * H * Dh * bf)
-        g.add(KernelCall.DecodeAttentionI8(DecodeAttentionI8Call(
-            qr, kq2, vq2, ks2, vs2, lens, a, B, H, Hkv, S, Dh, 0, DTYPE_BF16)))
-        o = g.slot(B * Dm * bf)
-        g.add(KernelCall.MatMul(MatMulCall(a, const(lw["wo"]), o, B, H * Dh, Dm, DTYPE_BF16)))
-        x2 = g.slot(B * Dm * bf)
-        g.add(KernelCall.Add(BinaryCall(x, o, x2, B * Dm, 16, DTYPE_BF16)))
-        h2 = g.slot(B * Dm * bf)
-        g.add(KernelCall.RmsNorm(NormCall(x2, const(lw["ffn_norm"]), h2, B, Dm, eps, DTYPE_BF16)))
-        gt, up = g.slot(B * F * bf), g.slot(B * F * bf)
-        g.add(KernelCall.MatMul(MatMulCall(h2, const(lw["wg"]), gt, B, Dm, F, DTYPE_BF16)))
-        g.add(KernelCall.MatMul(MatMulCall(h2, const(lw["wu"]), up, B, Dm, F, DTYPE_BF16)))
-        sg = g.slot(B * F * bf)
-        g.add(KernelCall.Silu(UnaryCall(gt, sg, B * F, 16, DTYPE_BF16)))
-        mm = g.slot(B * F * bf)
-        g.add(KernelCall.Mul(BinaryCall(sg, up, mm, B * F, 16, DTYPE_BF16)))
-        dn = g.slot(B * Dm * bf)
-        g.add(KernelCall.MatMul(MatMulCall(mm, const(lw["wd"]), dn, B, F, Dm, DTYPE_BF16)))
-        x3 = g.slot(B * Dm * bf)
-        g.add(KernelCall.Add(BinaryCall(x2, dn, x3, B * Dm, 16, DTYPE_BF16)))
+        a = g.slot(R * H * Dh * bf)
+        attn = DecodeAttentionI8Call(qr, kq2, vq2, ks2, vs2, lens, a, B, H, Hkv, S, Dh, 0,
+                                     DTYPE_BF16)
+        g.add(KernelCall.DecodeAttentionI8(attn) if T == 1
+              else KernelCall.AttentionI8Rows(AttentionI8RowsCall(attn, T)))
+        o = g.slot(R * Dm * bf)
+        g.add(KernelCall.MatMul(MatMulCall(a, const(lw["wo"]), o, R, H * Dh, Dm, DTYPE_BF16)))
+        x2 = g.slot(R * Dm * bf)
+        g.add(KernelCall.Add(BinaryCall(x, o, x2, R * Dm, 16, DTYPE_BF16)))
+        h2 = g.slot(R * Dm * bf)
+        g.add(KernelCall.RmsNorm(NormCall(x2, const(lw["ffn_norm"]), h2, R, Dm, eps, DTYPE_BF16)))
+        gt, up = g.slot(R * F * bf), g.slot(R * F * bf)
+        g.add(KernelCall.MatMul(MatMulCall(h2, const(lw["wg"]), gt, R, Dm, F, DTYPE_BF16)))
+        g.add(KernelCall.MatMul(MatMulCall(h2, const(lw["wu"]), up, R, Dm, F, DTYPE_BF16)))
+        sg = g.slot(R * F * bf)
+        g.add(KernelCall.Silu(UnaryCall(gt, sg, R * F, 16, DTYPE_BF16)))
+        mm = g.slot(R * F * bf)
+        g.add(KernelCall.Mul(BinaryCall(sg, up, mm, R * F, 16, DTYPE_BF16)))
+        dn = g.slot(R * Dm * bf)
+        g.add(KernelCall.MatMul(MatMulCall(mm, const(lw["wd"]), dn, R, F, Dm, DTYPE_BF16)))
+        x3 = g.slot(R * Dm * bf)
+        g.add(KernelCall.Add(BinaryCall(x2, dn, x3, R * Dm, 16, DTYPE_BF16)))
         x = x3
+    if T > 1:       # each sequence's last row
+        last = np.arange(1, B + 1, dtype=np.int32) * T - 1
+        xl = g.slot(B * Dm * bf)
+        g.add(KernelCall.Gather(GatherCall(x, const(last.tobytes(), DTYPE_I32, inline=True), xl, 1,
+                                           R, Dm, B, DTYPE_I32, DTYPE_BF16)))
+        x = xl
     hf = g.slot(B * Dm * bf)
     g.add(KernelCall.RmsNorm(NormCall(x, const(weights["final_norm"]), hf, B, Dm, eps,
                                       DTYPE_BF16)))
@@ -231,3 +269,13 @@ def rope_tables(cfg: DecoderConfig, positions: np.ndarray, heads: int) -> tuple:
     c = np.broadcast_to(np.cos(ang)[:, None, None, :], shape)
     s = np.broadcast_to(np.sin(ang)[:, None, None, :], shape)
     return bf16_bytes(c), bf16_bytes(s)
+
+
+def rope_tables_rows(cfg: DecoderConfig, positions: np.ndarray, heads: int) -> tuple:
+    """cos/sin for a prompt pass: bf16 bytes of shape [B, len(positions), heads, Dh]
+    (every sequence at the same positions), the token-major rows of build_prefill."""
+    c, s = rope_tables(cfg, positions, heads)
+    shape = (len(positions), cfg.batch, heads, cfg.head_dim)
+    tr = lambda b: np.ascontiguousarray(
+        np.frombuffer(b, np.uint16).reshape(shape).transpose(1, 0, 2, 3)).tobytes()
+    return tr(c), tr(s)

@@ -54,6 +54,8 @@ D_DAVL = 121
 D_KVQA = 122   # new: int8 quantize + append
 D_DAI8 = 123   # new: decode attention over an int8 cache
 D_ARGMAX = 124  # new: per-row argmax (the greedy pick of a decode step)
+D_AI8R = 125    # new: multi-row (prefill) form of D_DAI8
+D_TRANSPOSE = 61
 
 SLOT_ABSENT = 0xFFFFFFFF
 
@@ -300,11 +302,40 @@ class DecodeAttentionI8Call:
                               self.bucket_rows, self.head_dim, self.scale_bits, self.dtype))
 
 
+@dataclass(frozen=True)
+class AttentionI8RowsCall:
+    """New (discriminant 125): DecodeAttentionI8 over q_rows query rows per
+    sequence, row t seeing lens[b] - (q_rows - 1 - t) keys (include/holo_hip.h)."""
+    attn: DecodeAttentionI8Call
+    q_rows: int
+
+    def wire(self) -> bytes:
+        return self.attn.wire() + struct.pack("<I", self.q_rows)
+
+
+@dataclass(frozen=True)
+class TransposeCall:
+    """kernel_call.rs:487-499: output axis i is input axis perm[i]."""
+    input: BufferRef
+    output: BufferRef
+    dims: tuple
+    perm: tuple
+    dtype: int = DTYPE_BF16
+
+    def wire(self) -> bytes:  # put_transpose, kernel_codec.rs:687-697
+        rank = len(self.dims)
+        dims = list(self.dims) + [0] * (8 - rank)
+        perm = list(self.perm) + [0] * (8 - rank)
+        return (self.input.wire() + self.output.wire() + struct.pack("<B", rank)
+                + struct.pack("<8I", *dims) + struct.pack("<8B", *perm)
+                + struct.pack("<B", self.dtype))
+
+
 _NAMES = {D_ADD: "Add", D_MUL: "Mul", D_RN: "RmsNorm", D_ROTARY: "RotaryEmbedding",
           D_GATHER: "Gather", D_ARGMAX: "ArgMax", D_SIGMOID: "Sigmoid", D_TANH: "Tanh", D_GELU: "Gelu", D_SILU: "Silu", D_EXP: "Exp",
           D_MATMUL: "MatMul", D_MMA: "MatMulActivation", D_MMADD: "MatMulAdd",
           D_MMAA: "MatMulAddActivation", D_KVWR: "KvCacheWrite", D_KVQA: "KvQuantAppend",
-          D_DAI8: "DecodeAttentionI8"}
+          D_DAI8: "DecodeAttentionI8", D_AI8R: "AttentionI8Rows", D_TRANSPOSE: "Transpose"}
 
 
 @dataclass(frozen=True)
@@ -386,6 +417,14 @@ class KernelCall:
     def DecodeAttentionI8(cls, c: DecodeAttentionI8Call) -> "KernelCall":  # noqa: N802
         return cls(D_DAI8, c)
 
+    @classmethod
+    def AttentionI8Rows(cls, c: AttentionI8RowsCall) -> "KernelCall":  # noqa: N802
+        return cls(D_AI8R, c)
+
+    @classmethod
+    def Transpose(cls, c: TransposeCall) -> "KernelCall":  # noqa: N802
+        return cls(D_TRANSPOSE, c)
+
     @property
     def name(self) -> str:
         return _NAMES.get(self.tag, f"op{self.tag}")
@@ -434,6 +473,14 @@ class KernelCall:
             kc.u.kv_quant_append = _ffi.KvQuantAppendCallC(
                 p.new.c(), p.pos.c(), p.cache.c(), p.cache_scales.c(), p.output.c(),
                 p.output_scales.c(), p.planes, p.bucket_rows, p.new_rows, p.head_dim, p.dtype)
+        elif isinstance(p, AttentionI8RowsCall):
+            kc.u.attn_i8_rows = _ffi.AttentionI8RowsCallC(_attn_c(p.attn), p.q_rows)
+        elif isinstance(p, TransposeCall):
+            rank = len(p.dims)
+            kc.u.transpose = _ffi.TransposeCallC(
+                p.input.c(), p.output.c(), rank,
+                (ctypes.c_uint32 * 8)(*(list(p.dims) + [0] * (8 - rank))),
+                (ctypes.c_uint8 * 8)(*(list(p.perm) + [0] * (8 - rank))), p.dtype)
         elif isinstance(p, DecodeAttentionI8Call):
             kc.u.attn_i8 = _ffi.DecodeAttentionI8CallC(
                 p.q.c(), p.k_cache.c(), p.v_cache.c(), p.k_scales.c(), p.v_scales.c(),
@@ -442,6 +489,13 @@ class KernelCall:
         else:
             raise TypeError(f"no C form for payload {type(p).__name__}")
         return kc
+
+
+def _attn_c(p: DecodeAttentionI8Call) -> _ffi.DecodeAttentionI8CallC:
+    return _ffi.DecodeAttentionI8CallC(p.q.c(), p.k_cache.c(), p.v_cache.c(), p.k_scales.c(),
+                                       p.v_scales.c(), p.lens.c(), p.output.c(), p.batch,
+                                       p.heads, p.kv_heads, p.bucket_rows, p.head_dim,
+                                       p.scale_bits, p.dtype)
 
 
 def _mm_c(p: MatMulCall) -> _ffi.MatMulCallC:

@@ -82,6 +82,8 @@ typedef enum holo_status {
 #define HOLO_OP_KV_QUANT_APPEND 122u      /* new: int8 quantize + ring append   */
 #define HOLO_OP_DECODE_ATTN_I8 123u       /* new: GQA decode over an int8 cache */
 #define HOLO_OP_ARGMAX 124u               /* new: per-row argmax (greedy pick)  */
+#define HOLO_OP_ATTN_I8_ROWS 125u         /* new: multi-row (prefill) form of 123 */
+#define HOLO_OP_TRANSPOSE 61u             /* Transpose (kernel_codec.rs:80)     */
 
 /* BufferRef, crates/hologram-compute/src/workspace.rs:16-24.
  * length == 0 means "to the end of the slot"; slot == HOLO_SLOT_ABSENT marks an
@@ -258,6 +260,31 @@ typedef struct holo_decode_attention_i8_call {
     uint8_t dtype;
 } holo_decode_attention_i8_call;
 
+/* New (tag 125): the multi-row form of tag 123, a prompt's rows against the
+ * int8 cache they were appended to (prefill). q / output are
+ * [batch, q_rows, heads, head_dim]; lens[b] is the visible length of sequence
+ * b's last row, and row t sees the first lens[b] - (q_rows - 1 - t) rows of its
+ * planes (none when that is not positive), at most bucket_rows: the causal
+ * visibility of DecodeAttentionValid's new rows, past prefix then min(qi + 1, new)
+ * (src/cpu/float_kernels.rs:3926). q_rows = 1 is tag 123. */
+typedef struct holo_attention_i8_rows_call {
+    holo_decode_attention_i8_call attn;
+    uint32_t q_rows;
+} holo_attention_i8_rows_call;
+
+/* TransposeCall, kernel_call.rs:487-499 (transpose_float,
+ * src/cpu/float_kernels.rs:2980-3028): output axis i is input axis perm[i] of
+ * the row-major input of shape dims[0..rank). rank 1..8; f16/bf16/f32 elements;
+ * perm must be a permutation of 0..rank-1. */
+typedef struct holo_transpose_call {
+    holo_buffer_ref input;
+    holo_buffer_ref output;
+    uint8_t rank;
+    uint32_t dims[8];
+    uint8_t perm[8];
+    uint8_t dtype;
+} holo_transpose_call;
+
 /* KernelCall (kernel_call.rs:1146-1276): tag + the variant's payload. */
 typedef struct holo_kernel_call {
     uint32_t tag;
@@ -275,6 +302,8 @@ typedef struct holo_kernel_call {
         holo_kv_cache_write_call kv_write;
         holo_kv_quant_append_call kv_quant_append;
         holo_decode_attention_i8_call attn_i8;
+        holo_attention_i8_rows_call attn_i8_rows;
+        holo_transpose_call transpose;
     } u;
 } holo_kernel_call;
 

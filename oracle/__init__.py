@@ -168,6 +168,32 @@ def decode_attention_i8(q, kq, ks, vq, vs, lens, B, H, Hkv, bucket, D, scale) ->
     return out
 
 
+def attention_i8_rows(q, kq, ks, vq, vs, lens, B, T, H, Hkv, bucket, D, scale) -> np.ndarray:
+    """The multi-row (prefill) form over an int8 cache: q [B, T, H, D] (f32), row t
+    of sequence b a one-query decode over the first clamp(lens[b] - (T - 1 - t),
+    0, bucket) rows of its planes. With lens[b] >= T this is
+    DecodeAttentionValid{m = new = T, past = lens[b] - T} (float_kernels.rs:3926:
+    row qi sees the past prefix and min(qi + 1, new) new rows)."""
+    q = np.ascontiguousarray(q, np.float32).reshape(B, T, H, D)
+    out = np.zeros((B, T, H, D), np.float32)
+    pl, ps = Hkv * bucket * D, Hkv * bucket
+    for b in range(B):
+        planes = [np.ascontiguousarray(a) for a in (kq[b * pl:(b + 1) * pl], ks[b * ps:(b + 1) * ps],
+                                                   vq[b * pl:(b + 1) * pl], vs[b * ps:(b + 1) * ps])]
+        for t in range(T):
+            L = max(int(lens[b]) - (T - 1 - t), 0)
+            out[b, t] = decode_attention_i8(np.ascontiguousarray(q[b, t]).ravel(), *planes,
+                                            np.array([L], np.uint32), 1, H, Hkv, bucket, D,
+                                            scale).reshape(H, D)
+    return out.ravel()
+
+
+def transpose(x: np.ndarray, dims, perm) -> np.ndarray:
+    """transpose_float (float_kernels.rs:2980-3028): output axis i is input axis
+    perm[i] of the row-major input of shape dims."""
+    return np.ascontiguousarray(np.transpose(np.asarray(x).reshape(tuple(dims)), tuple(perm))).ravel()
+
+
 def fused_act_f32(act: int, x: np.ndarray) -> np.ndarray:
     """fused_act_fn (float_kernels.rs:768-780) over f32 values; act is a
     fused_activation id (kernel_call.rs:861-870)."""

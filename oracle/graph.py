@@ -79,6 +79,17 @@ def _decode_call(r: _R) -> tuple:
                          lens=r.buf(), output=r.buf(), batch=r.u("I"), heads=r.u("I"),
                          kv_heads=r.u("I"), bucket=r.u("I"), head_dim=r.u("I"),
                          scale_bits=r.u("I"), dtype=r.u("B"))
+    if tag == 125:                                   # multi-row int8 attention (new)
+        return tag, dict(q=r.buf(), kq=r.buf(), vq=r.buf(), ks=r.buf(), vs=r.buf(),
+                         lens=r.buf(), output=r.buf(), batch=r.u("I"), heads=r.u("I"),
+                         kv_heads=r.u("I"), bucket=r.u("I"), head_dim=r.u("I"),
+                         scale_bits=r.u("I"), dtype=r.u("B"), q_rows=r.u("I"))
+    if tag == 61:                                    # put_transpose
+        c = dict(input=r.buf(), output=r.buf(), rank=r.u("B"))
+        c["dims"] = [r.u("I") for _ in range(8)][:c["rank"]]
+        c["perm"] = [r.u("B") for _ in range(8)][:c["rank"]]
+        c["dtype"] = r.u("B")
+        return tag, c
     if tag == 124:                                   # argmax (new)
         return tag, dict(input=r.buf(), output=r.buf(), rows=r.u("I"), cols=r.u("I"),
                          dtype=r.u("B"))
@@ -253,6 +264,26 @@ class OracleSession:
             o = decode_attention_i8(q, kq, ks, vq, vs, lens, B, H, Hkv, S, D,
                                     attn_scale(D, c["scale_bits"]))
             self._out(c["output"], B * H * D * es)[:] = self._narrow(o, c["dtype"])
+        elif tag == 125:
+            B, T, H, Hkv = c["batch"], c["q_rows"], c["heads"], c["kv_heads"]
+            S, D = c["bucket"], c["head_dim"]
+            es = DT_BYTES[c["dtype"]]
+            q = self._f32(self._view(c["q"], B * T * H * D * es), c["dtype"])
+            kq = np.ascontiguousarray(self._view(c["kq"], B * Hkv * S * D)).view(np.int8)
+            vq = np.ascontiguousarray(self._view(c["vq"], B * Hkv * S * D)).view(np.int8)
+            ks = np.ascontiguousarray(self._view(c["ks"], B * Hkv * S * 4)).view(np.float32)
+            vs = np.ascontiguousarray(self._view(c["vs"], B * Hkv * S * 4)).view(np.float32)
+            lens = np.ascontiguousarray(self._view(c["lens"], B * 4)).view(np.uint32)
+            from . import attention_i8_rows, attn_scale
+            o = attention_i8_rows(q, kq, ks, vq, vs, lens, B, T, H, Hkv, S, D,
+                                  attn_scale(D, c["scale_bits"]))
+            self._out(c["output"], B * T * H * D * es)[:] = self._narrow(o, c["dtype"])
+        elif tag == 61:
+            es = DT_BYTES[c["dtype"]]
+            n = int(np.prod(c["dims"]))
+            x = np.ascontiguousarray(self._view(c["input"], n * es)).view(f"u{es}")
+            from . import transpose
+            self._out(c["output"], n * es)[:] = transpose(x, c["dims"], c["perm"]).view(np.uint8)
         elif tag == 124:
             es = DT_BYTES[c["dtype"]]
             x = np.ascontiguousarray(self._view(c["input"], c["rows"] * c["cols"] * es))

@@ -19,10 +19,7 @@
 // kernel it replaces (the partials summed sequentially in ks order as
 // skinny_reduce_kernel does, bf16 narrowed by truncation between ops), so a
 // fused walk gives the same bits as the unfused one.
-//
-// With ks == 0 the base value is read from `src` (the already-narrowed output
-// of a tiled MatMul) instead of partials: the in-place epilogue of a fused
-// MatMul call whose product took the tiled path.
+
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -42,52 +39,6 @@ constexpr uint32_t kEpiThreads = 64;
 __device__ __forceinline__ float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
 __device__ __forceinline__ uint32_t f2bf(float f) { return __float_as_uint(f) >> 16; }
 
-// exp_f32_det (src/cpu/simd.rs:4191-4239): clamp, k = trunc(x*log2e +- 1/2),
-// Cody-Waite reduction, degree-6 Horner, scale by 2^k.
-__device__ float exp_det(float x) {
-    const float LO = -87.33654f, HI = 88.0f;
-    const float LOG2E = 1.44269504088896340736f;
-    const float LN2_HI = __uint_as_float(0x3F318000u);
-    const float LN2_LO = -2.1219444e-4f;
-    const float C6 = 1.0f / 720.0f, C5 = 1.0f / 120.0f, C4 = 1.0f / 24.0f, C3 = 1.0f / 6.0f,
-                C2 = 0.5f;
-    if (x != x || x < LO) return 0.0f;
-    if (x > HI) x = HI;
-    const float t = x * LOG2E;
-    const int32_t k = t >= 0.0f ? int32_t(t + 0.5f) : int32_t(t - 0.5f);
-    const float kf = float(k);
-    const float r = (x - kf * LN2_HI) - kf * LN2_LO;
-    float p = C6;
-    p = p * r + C5;
-    p = p * r + C4;
-    p = p * r + C3;
-    p = p * r + C2;
-    p = p * r + 1.0f;
-    p = p * r + 1.0f;
-    uint32_t sb = uint32_t(k + 127) << 23;
-    if (sb > 0x7f000000u) sb = 0x7f000000u;
-    return p * __uint_as_float(sb);
-}
-
-// fused_activation ids (kernel_call.rs:861-870) served on f32.
-__device__ float act_f32(uint32_t act, float x) {
-    switch (act) {
-        case kFusedGelu: {
-            const float cube = ((0.044715f * x) * x) * x;
-            const float u = 0.7978846f * (x + cube);
-            const float e = exp_det(2.0f * u);
-            return (0.5f * x) * (1.0f + (e - 1.0f) / (e + 1.0f));
-        }
-        case kFusedSilu: return x * (1.0f / (1.0f + exp_det(-x)));
-        case kFusedSigmoid: return 1.0f / (1.0f + exp_det(-x));
-        case kFusedTanh: {
-            const float e = exp_det(2.0f * x);
-            return (e - 1.0f) / (e + 1.0f);
-        }
-        default: return x;
-    }
-}
-
 // Segment of this workgroup (workgroup-uniform, chosen with selects).
 __device__ __forceinline__ int pick(const EpiArgs &g, uint32_t *first_block) {
     int s = 0;
@@ -103,9 +54,8 @@ __device__ __forceinline__ int pick(const EpiArgs &g, uint32_t *first_block) {
 }
 
 // The product at (row m, column c) of P's column space: partials summed in
-// ks order (or the tiled output read back). Up to kBatch loads go out before
-// the first add, so a split of up to kBatch partials costs one memory round
-// trip; the adds keep ks order.
+// ks order. Up to kBatch loads go out before the first add, so a split of up
+// to kBatch partials costs one memory round trip; the adds keep ks order.
 constexpr uint32_t kBatch = 32;
 
 template <class T>
@@ -124,36 +74,15 @@ __device__ __forceinline__ T sum_partials(const T *p, uint64_t plane, uint32_t k
     return s;
 }
 
-template <bool kBf16>
-__device__ __forceinline__ float product(const EpiArgs &g, uint32_t m, uint32_t c) {
-    if (g.ks == 0) {
-        if constexpr (kBf16)
-            return bf2f(static_cast<const uint16_t *>(g.src)[uint64_t(m) * g.ntot + c]);
-        else
-            return static_cast<const float *>(g.src)[uint64_t(m) * g.ntot + c];
-    }
-    return sum_partials(g.P + uint64_t(m) * g.ntot + c, uint64_t(g.m) * g.ntot, g.ks);
-}
-
-// The same for 4 consecutive columns (c a multiple of 4), as 16-byte loads.
-template <bool kBf16>
+// 4 consecutive columns (c a multiple of 4), as 16-byte loads.
 __device__ __forceinline__ f32x4 product4(const EpiArgs &g, uint32_t m, uint32_t c) {
-    if (g.ks == 0)
-        return f32x4{product<kBf16>(g, m, c), product<kBf16>(g, m, c + 1),
-                     product<kBf16>(g, m, c + 2), product<kBf16>(g, m, c + 3)};
     return sum_partials(reinterpret_cast<const f32x4 *>(g.P + uint64_t(m) * g.ntot + c),
                         uint64_t(g.m) * g.ntot / 4, g.ks);
 }
 
 // Two columns (c, c + off) of one row, their partials in flight together.
-template <bool kBf16>
 __device__ __forceinline__ void product2(const EpiArgs &g, uint32_t m, uint32_t c, uint32_t off,
                                         float *x1, float *x2) {
-    if (g.ks == 0) {
-        *x1 = product<kBf16>(g, m, c);
-        *x2 = product<kBf16>(g, m, c + off);
-        return;
-    }
     const uint64_t plane = uint64_t(g.m) * g.ntot;
     const float *p = g.P + uint64_t(m) * g.ntot + c;
     float s1 = 0.0f, s2 = 0.0f;
@@ -245,11 +174,8 @@ __device__ void elem_segment(const EpiArgs &g, const EpiSeg &sg, const EpiSeg &p
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) rb[j] = load<kBf16>(pr.residual, e0 + j);
     f32x4 va, vb = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (g.ks == 0) {
-        va = product4<kBf16>(g, m, sg.col0 + c);
-        if (pair) vb = product4<kBf16>(g, m, pr.col0 + c);
-    } else if (!pair) {
-        va = product4<kBf16>(g, m, sg.col0 + c);
+    if (!pair) {
+        va = product4(g, m, sg.col0 + c);
     } else {
         // both segments' partials in flight together
         const uint64_t plane = uint64_t(g.m) * g.ntot / 4;
@@ -319,7 +245,7 @@ __device__ void head_segment(const EpiArgs &g, const EpiSeg &sg, uint32_t blk) {
             r2 = load<kBf16>(sg.residual, e1 + half);
         }
         float p1, p2;
-        product2<kBf16>(g, m, sg.col0 + c1, half, &p1, &p2);
+        product2(g, m, sg.col0 + c1, half, &p1, &p2);
         x1 = base_value<kBf16>(sg, p1, r1);
         x2 = base_value<kBf16>(sg, p2, r2);
         if (sg.out) {
@@ -388,6 +314,55 @@ __global__ __launch_bounds__(kEpiThreads) void epilogue_kernel(const EpiArgs g) 
 
 }  // namespace
 
+// In-place epilogue over a tiled MatMul's output: 8 bf16 (or 4 f32) per
+// thread as one 16-byte load and store when the operands allow, element by
+// element otherwise; grid-stride.
+template <bool kBf16, bool kVec>
+__global__ __launch_bounds__(256) void tile_epilogue_kernel(void *__restrict__ c,
+                                                           const void *__restrict__ res,
+                                                           const uint16_t *__restrict__ lut,
+                                                           uint64_t count, uint8_t kind,
+                                                           uint32_t act) {
+    constexpr uint32_t E = kVec ? (kBf16 ? 8 : 4) : 1;
+    const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
+    for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i * E < count; i += stride) {
+        float v[E], r[E];
+        if constexpr (kVec) {
+            const u32x4 x = reinterpret_cast<const u32x4 *>(c)[i];
+            const u32x4 y = kind >= 2 ? reinterpret_cast<const u32x4 *>(res)[i]
+                                      : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (uint32_t j = 0; j < E; ++j) {
+                if constexpr (kBf16) {
+                    v[j] = bf2f(j & 1 ? x[j / 2] >> 16 : x[j / 2] & 0xffffu);
+                    r[j] = bf2f(j & 1 ? y[j / 2] >> 16 : y[j / 2] & 0xffffu);
+                } else {
+                    v[j] = __uint_as_float(x[j]);
+                    r[j] = __uint_as_float(y[j]);
+                }
+            }
+        } else {
+            v[0] = load<kBf16>(c, i);
+            r[0] = kind >= 2 ? load<kBf16>(res, i) : 0.0f;
+        }
+        EpiSeg sg;
+        sg.base = kind;
+        sg.act = act;
+        sg.lut = lut;
+#pragma unroll
+        for (uint32_t j = 0; j < E; ++j) v[j] = base_value<kBf16>(sg, v[j], r[j]);
+        if constexpr (kVec) {
+            u32x4 o;
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j)
+                o[j] = kBf16 ? (f2bf(v[2 * j]) | (f2bf(v[2 * j + 1]) << 16)) : __float_as_uint(v[j]);
+            reinterpret_cast<u32x4 *>(c)[i] = o;
+        } else {
+            store<kBf16>(c, i, v[0]);
+        }
+    }
+}
+
 uint32_t epilogue_blocks(const EpiSeg &sg, uint32_t m) {
     if (sg.skip) return 0;
     if (sg.head_dim) {
@@ -397,6 +372,30 @@ uint32_t epilogue_blocks(const EpiSeg &sg, uint32_t m) {
     }
     const uint64_t threads = uint64_t(m) * sg.n / 4;
     return uint32_t((threads + kEpiThreads - 1) / kEpiThreads);
+}
+
+hipError_t launch_tile_epilogue(void *c, uint64_t count, bool bf16, const TileEpi &epi,
+                                hipStream_t stream) {
+    if (count == 0 || epi.kind == kEpiStore) return hipSuccess;
+    const uint64_t E = bf16 ? 8 : 4;
+    const bool vec = count % E == 0 && ((reinterpret_cast<uintptr_t>(c) |
+                                         reinterpret_cast<uintptr_t>(epi.residual)) & 15) == 0;
+    const uint64_t items = vec ? count / E : count;
+    uint64_t blocks = (items + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    const dim3 grid{unsigned(blocks)}, block{256u};
+#define HOLO_TILE_EPI(BF, VEC)                                                                   \
+    hipLaunchKernelGGL((tile_epilogue_kernel<BF, VEC>), grid, block, 0, stream, c, epi.residual, \
+                       epi.lut, count, epi.kind, epi.act)
+    if (bf16) {
+        if (vec) HOLO_TILE_EPI(true, true);
+        else HOLO_TILE_EPI(true, false);
+    } else {
+        if (vec) HOLO_TILE_EPI(false, true);
+        else HOLO_TILE_EPI(false, false);
+    }
+#undef HOLO_TILE_EPI
+    return hipGetLastError();
 }
 
 hipError_t launch_epilogue(EpiArgs g, hipStream_t stream) {

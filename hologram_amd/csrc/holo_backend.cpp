@@ -270,7 +270,7 @@ int do_matmul(holo_backend *be, const SlotTable &st, const holo_matmul_call &c) 
 // Every member's product in one few-row launch (fp32 partials), then one
 // epilogue launch that finishes each segment. A one-segment group with an
 // element-wise epilogue that the few-row kernels do not serve runs the tiled
-// MatMul into its output and the epilogue in place.
+// MatMul into its output and the epilogue over it in place.
 int dispatch_group_impl(holo_backend *be, const SlotTable &st, const holo::GroupDesc &g,
                         const char *op) {
     const size_t nseg = g.segs.size();
@@ -365,16 +365,20 @@ int dispatch_group_impl(holo_backend *be, const SlotTable &st, const holo::Group
             return fail(HOLO_ERR_DISPATCH,
                         std::string(op) + ": a fused group needs the few-row path (16-byte aligned "
                                           "operands, one common split)");
-        // the tiled product into the output, then the epilogue in place
+        // the tiled product into the output, then the epilogue over it in place
         HOLO_TRY(ensure_scratch(be, holo::matmul_scratch_bytes(g.m, g.k, s.n, g.dtype), op));
         HOLO_TRY(launched(holo::launch_matmul(a.base, ss[0].b, e.seg[0].out, g.m, g.k, s.n, g.dtype,
                                               be->scratch, be->stream),
                           op));
         if (s.base == holo::kEpiStore) return HOLO_OK;
-        e.ks = 0;
-        e.src = e.seg[0].out;
-        e.ntot = s.n;
-        return launched(holo::launch_epilogue(e, be->stream), op);
+        holo::TileEpi te;
+        te.kind = s.base;
+        te.act = s.act;
+        te.lut = e.seg[0].lut;
+        te.residual = e.seg[0].residual;
+        return launched(holo::launch_tile_epilogue(e.seg[0].out, uint64_t(g.m) * s.n, bf16, te,
+                                                   be->stream),
+                        op);
     }
     HOLO_TRY(ensure_scratch(be, size_t(plan.ks) * g.m * ntot * 4, op));
     e.P = static_cast<const float *>(be->scratch);

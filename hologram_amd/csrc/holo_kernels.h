@@ -73,6 +73,17 @@ hipError_t launch_transpose(const void *in, void *out, uint32_t rank, const uint
 // result narrowed by truncation). `scratch` holds split-K partials of the
 // few-row path, matmul_scratch_bytes() bytes (0: none needed). Calls sharing
 // one scratch must not overlap.
+// An element-wise epilogue over a tiled MatMul's output, in place (kind as
+// EpiSeg::base: 1 activation, 2 + residual, 3 + residual then activation); the
+// same arithmetic as the separate kernels.
+struct TileEpi {
+    uint8_t kind = 0;
+    uint32_t act = 0;                  // fused_activation id (f32, and bf16 kind 3)
+    const uint16_t *lut = nullptr;     // bf16 kind 1: the activation's table
+    const void *residual = nullptr;    // kinds 2, 3: [count], same dtype
+};
+hipError_t launch_tile_epilogue(void *c, uint64_t count, bool bf16, const TileEpi &epi,
+                                hipStream_t stream);
 size_t matmul_scratch_bytes(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype);
 hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint32_t k,
                          uint32_t n, uint8_t dtype, void *scratch, hipStream_t stream);
@@ -123,8 +134,7 @@ struct EpiSeg {
     bool skip = false;                 // consumed through another segment's pair; no blocks
 };
 struct EpiArgs {
-    const float *P = nullptr;          // [ks][m][ntot]
-    const void *src = nullptr;         // ks == 0: the tiled MatMul's output [m][ntot]
+    const float *P = nullptr;          // [ks][m][ntot], ks >= 1
     uint32_t m = 0, ks = 0, ntot = 0, nseg = 0;
     bool bf16 = true;
     EpiSeg seg[kSkinnyMaxSeg];

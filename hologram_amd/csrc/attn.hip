@@ -142,13 +142,21 @@ struct SegLds {
 // super-block's largest v-scale sets ve, shared by the four wavefronts:
 // P' = p * vscale / 2^ve <= 1 is fed to the f16 MFMA, and the softmax state is
 // kept in units of 2^-ve (p' = exp2(s - m - ve), l' = sum p').
-template <int D, bool kF32Q>
+//
+// kPack (prompt rows, whole-plane segments only): the 16 MFMA columns hold
+// `prow` consecutive query rows x G heads, column r = row r / G, head r % G,
+// each row with its own visible-key limit lim0 + r / G (clamped to
+// [0, bucket]); c1 is the largest. Keys past a column's limit score -inf, and
+// a column that has seen no visible key yet keeps exact zeros (its rescale
+// and weights are guarded); a row with no visible key at all is written as
+// zeros.
+template <int D, bool kF32Q, bool kPack = false>
 __device__ __forceinline__ void attn_segment(
     const void *__restrict__ q, const int8_t *__restrict__ kq, const int8_t *__restrict__ vq,
     const float *__restrict__ ks, const float *__restrict__ vs, float *__restrict__ dst,
     void *__restrict__ out, uint32_t b, uint32_t qrow, uint32_t kh, uint32_t c0, uint32_t c1,
     bool single, uint32_t H, uint32_t Hkv, uint32_t G, uint32_t bucket, float log2e_over_scale,
-    SegLds<D> &lds) {
+    SegLds<D> &lds, uint32_t prow = 1, int64_t lim0 = 0) {
     constexpr int KB = D / 4;          // K bytes per lane per key row (QK k-slots)
     constexpr int NKS = D / 64;        // i8 MFMA k-steps (64 dims each)
     constexpr int NDB = D / 16;        // 16-row dim blocks of O^T
@@ -230,8 +238,11 @@ __device__ __forceinline__ void attn_segment(
     const uint32_t nsb = (c1 - c0 + kSuper - 1) / kSuper;
     if (wv == 0) {
         float qv[KB];
-        const bool live = uint32_t(r) < G;
-        const uint64_t qi = (uint64_t(qrow) * H + kh * G + (live ? r : 0)) * D + KB * g;
+        const uint32_t cols = kPack ? G * prow : G;
+        const bool live = uint32_t(r) < cols;
+        const uint32_t col = live ? uint32_t(r) : 0u;
+        const uint64_t qi = kPack ? ((uint64_t(qrow) + col / G) * H + kh * G + col % G) * D + KB * g
+                                  : (uint64_t(qrow) * H + kh * G + col) * D + KB * g;
         if constexpr (kF32Q) {
             const u32x4 *src = reinterpret_cast<const u32x4 *>(static_cast<const float *>(q) + qi);
 #pragma unroll
@@ -307,6 +318,12 @@ __device__ __forceinline__ void attn_segment(
     store_sc(0, sreg);
     __syncthreads();
     const float smul = lds.smul[r];
+    // kPack: this lane's column limit, and the smallest limit (blocks ending
+    // past it need the per-key test)
+    int64_t lim_r = lim0 + int64_t(uint32_t(r) / (G ? G : 1));
+    lim_r = lim_r < 0 ? 0 : (lim_r > int64_t(bucket) ? int64_t(bucket) : lim_r);
+    const uint32_t lim_lane = kPack ? uint32_t(lim_r) : c1;
+    const uint32_t lim_min = kPack ? uint32_t(lim0 < 0 ? 0 : (lim0 > int64_t(bucket) ? int64_t(bucket) : lim0)) : c1;
 
     // One 32-key block: lane (r, g) holds keys 16mb + 4g + i for head r.
     // masked: keys at or beyond c1 are invisible (the segment's last block;
@@ -338,7 +355,7 @@ __device__ __forceinline__ void attn_segment(
         if (masked) {
 #pragma unroll
             for (int j = 0; j < 8; ++j)
-                if (blk + 16 * (j >> 2) + 4 * g + (j & 3) >= c1) sc[j] = -INFINITY;
+                if (blk + 16 * (j >> 2) + 4 * g + (j & 3) >= lim_lane) sc[j] = -INFINITY;
         }
         float m_blk = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
                             fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
@@ -350,7 +367,8 @@ __device__ __forceinline__ void attn_segment(
         }
         if (__any(m_blk > m_run)) {        // rescale only when some head's max grew
             const float m_new = fmaxf(m_run, m_blk);
-            const float alpha = exp2f(m_run - m_new);
+            // kPack: a column with no visible key so far stays at -inf, exact 0
+            const float alpha = kPack && m_new == -INFINITY ? 1.0f : exp2f(m_run - m_new);
             m_run = m_new;
             mv = m_run + float(ve);
             l_run *= alpha;
@@ -360,7 +378,8 @@ __device__ __forceinline__ void attn_segment(
         f16x8 pf;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float p = exp2f(sc[j] - mv);   // p * 2^-ve; masked keys: exp2(-inf) = 0
+            float p = exp2f(sc[j] - mv);         // p * 2^-ve; masked keys: exp2(-inf) = 0
+            if (kPack && sc[j] == -INFINITY) p = 0.0f;
             l_run += p;
             pf[j] = (_Float16)(p * vsc[j]);      // invisible keys carry scale 0
         }
@@ -408,7 +427,7 @@ __device__ __forceinline__ void attn_segment(
             if (nb < c1) load(nb, nxt);
             const uint32_t so = (it & 3) * kQuad + wv * kBlock;
             const float *skp = lds.sk[sb & 1] + so, *svp = lds.sv[sb & 1] + so;
-            block(blk + kBlock > c1, cur, blk, skp, svp);
+            block(blk + kBlock > lim_min, cur, blk, skp, svp);
             cur = nxt;
         }
         if ((it & 3) == 3) {
@@ -434,7 +453,8 @@ __device__ __forceinline__ void attn_segment(
     // The whole plane: the merged state is the answer (o / l does not depend on
     // the common 2^ve). Otherwise write the partial, scaled back by 2^ve.
     const float v_rescale = ldexpf(1.0f, ve);
-    for (uint32_t idx = tid; idx < G * D; idx += kThreads) {
+    const uint32_t ncol = kPack ? G * prow : G;
+    for (uint32_t idx = tid; idx < ncol * D; idx += kThreads) {
         const uint32_t h = idx / D, d = idx % D;
         float m = -INFINITY;
 #pragma unroll
@@ -447,11 +467,13 @@ __device__ __forceinline__ void attn_segment(
             l = fmaf(lds.red_l[w][h], sc, l);
         }
         if (single) {
-            const uint64_t oi = (uint64_t(qrow) * H + kh * G + h) * D + d;
+            const uint64_t oi = kPack ? ((uint64_t(qrow) + h / G) * H + kh * G + h % G) * D + d
+                                      : (uint64_t(qrow) * H + kh * G + h) * D + d;
+            const float res = kPack && l == 0.0f ? 0.0f : o / l;   // kPack: a row with no key
             if constexpr (kF32Q)
-                static_cast<float *>(out)[oi] = o / l;
+                static_cast<float *>(out)[oi] = res;
             else
-                static_cast<uint16_t *>(out)[oi] = uint16_t(__float_as_uint(o / l) >> 16);
+                static_cast<uint16_t *>(out)[oi] = uint16_t(__float_as_uint(res) >> 16);
             continue;
         }
         dst[h * (D + 2) + 2 + d] = o * v_rescale;
@@ -495,6 +517,33 @@ __global__ __launch_bounds__(kThreads, kWps) void attn_chunk_kernel(
     float *dst = part + (row_plane * nchunks + chunk) * G * (D + 2);
     attn_segment<D, kF32Q>(q, kq, vq, ks, vs, dst, out, b, v, kh, c0, c1, L <= kChunk, H, Hkv, G,
                            bucket, log2e_over_scale, lds);
+}
+
+// Packed prompt form: grid (1, Hkv, B * ceil(T / R)). A workgroup takes R
+// consecutive query rows of one sequence for one kv head (R * G <= 16 MFMA
+// columns), so each K/V byte of the plane is read once per R rows. Each plane
+// fits one chunk (the whole visible range is one segment; no merge).
+template <int D, bool kF32Q>
+__global__ __launch_bounds__(kThreads, kWps) void attn_rows_packed_kernel(
+    const void *__restrict__ q, const int8_t *__restrict__ kq, const int8_t *__restrict__ vq,
+    const float *__restrict__ ks, const float *__restrict__ vs, const uint32_t *__restrict__ lens,
+    void *__restrict__ out, uint32_t H, uint32_t Hkv, uint32_t G, uint32_t bucket,
+    float log2e_over_scale, uint32_t T, uint32_t R) {
+    __shared__ SegLds<D> lds;
+    const uint32_t nt = (T + R - 1) / R;
+    const uint32_t kh = blockIdx.y, b = blockIdx.z / nt, t0 = (blockIdx.z % nt) * R;
+    const uint32_t rows = T - t0 < R ? T - t0 : R;
+    const int64_t lim0 = int64_t(lens[b]) - int64_t(T - 1 - t0);    // first packed row
+    int64_t last = lim0 + rows - 1;
+    last = last < 0 ? 0 : (last > int64_t(bucket) ? int64_t(bucket) : last);
+    const uint32_t qrow = b * T + t0;
+    if (last == 0) {   // no packed row sees a key: exact zeros
+        for (uint32_t ro = 0; ro < rows; ++ro)
+            zero_rows<kF32Q>(out, qrow + ro, kh, H, G, D, threadIdx.x, kThreads);
+        return;
+    }
+    attn_segment<D, kF32Q, true>(q, kq, vq, ks, vs, nullptr, out, b, qrow, kh, 0, uint32_t(last),
+                                 true, H, Hkv, G, bucket, log2e_over_scale, lds, rows, lim0);
 }
 
 // Balanced form: the planes' 128-key quads laid end to end, plane (b, kh) in
@@ -798,6 +847,14 @@ hipError_t run_t(const AttnI8Args &a, void *scratch, hipStream_t stream) {
     }
     const uint32_t ck = chunk_keys(a.bucket);
     const uint32_t nch = chunks_of(a.bucket);
+    if (a.q_rows > 1 && nch == 1 && G <= 8) {
+        const uint32_t R = 16 / G;
+        const uint32_t nt = (a.q_rows + R - 1) / R;
+        hipLaunchKernelGGL((attn_rows_packed_kernel<D, kF32Q>), dim3(1, a.Hkv, a.B * nt),
+                           dim3(kThreads), 0, stream, a.q, a.kq, a.vq, a.ks, a.vs, a.lens, a.out,
+                           a.H, a.Hkv, G, a.bucket, mul, a.q_rows, R);
+        return hipGetLastError();
+    }
     const uint32_t rows = a.B * a.q_rows;
     hipLaunchKernelGGL((attn_chunk_kernel<D, kF32Q>), dim3(nch, a.Hkv, rows), dim3(kThreads), 0,
                        stream, a.q, a.kq, a.vq, a.ks, a.vs, a.lens, part, a.out, a.H, a.Hkv, G,

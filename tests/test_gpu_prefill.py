@@ -80,8 +80,10 @@ def run_rows(torch, backend, B, T, H, Hkv, D, S, lens, seed, q_rows_op=True):
 
 @pytest.mark.parametrize("H,Hkv,D", [(8, 2, 64), (16, 4, 128), (4, 4, 64)])
 def test_attention_rows_parity(torch_cuda, backend, H, Hkv, D):
-    B, T, S = 3, 9, 48
-    lens = [9, 40, 3]              # the last sequence is shorter than its prompt rows
+    B, T, S = 4, 9, 48
+    # the third sequence is shorter than its prompt rows; the fourth's rows run
+    # past the bucket (each row sees at most the bucket)
+    lens = [9, 40, 3, 53]
     got, want, _ = run_rows(torch_cuda, backend, B, T, H, Hkv, D, S, lens, seed=H + D)
     for b in range(B):
         for t in range(T):

@@ -280,6 +280,12 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(const float *__restr
 // slab's global loads are issued before the current slab's MFMAs.
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kBigM = 256, kBigN = 256, kBigK = 64, kLdk = kBigK + 8;
+// 256x256 tiles are used when there are at least this many of them. Measured
+// at M = 4096, N = 2048 (128 tiles, half the CUs): 68 us (K = 2048) and 229 us
+// (K = 8192) against 73 and 272 us for the 128x128 kernel on every CU.
+#ifndef HOLO_BIG_MIN_TILES
+#define HOLO_BIG_MIN_TILES 128
+#endif
 
 __device__ __forceinline__ void tile_coords(uint32_t wg, uint32_t nwg, uint32_t tiles_m,
                                             uint32_t tiles_n, uint32_t *tm, uint32_t *tn) {
@@ -533,12 +539,12 @@ hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint
         }                                                                                        \
     } while (0)
     if (dtype == 7) {
-        // large aligned problems: 256x256 tiles, at least one tile per CU, an
+        // large aligned problems: 256x256 tiles, at least HOLO_BIG_MIN_TILES of them, an
         // even number (>= 4) of 64-deep slabs, and 256 rows of A / 64 rows of
         // B within a 32-bit buffer range
         if ((al & 15) == 0 && m % kBigM == 0 && n % kBigN == 0 && k % (2 * kBigK) == 0 &&
             k >= 4 * kBigK && k < (1u << 22) && n < (1u << 24) &&
-            uint64_t(m / kBigM) * (n / kBigN) >= 256) {
+            uint64_t(m / kBigM) * (n / kBigN) >= HOLO_BIG_MIN_TILES) {
             hipLaunchKernelGGL(gemm_bf16_big_kernel, dim3((m / kBigM) * (n / kBigN)), dim3(256), 0,
                                stream, static_cast<const uint16_t *>(a),
                                static_cast<const uint16_t *>(b), static_cast<uint16_t *>(c), m, n, k);

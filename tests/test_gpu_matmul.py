@@ -97,7 +97,8 @@ def run_mm_rows(torch, backend, m, k, n, seed, rows):
 
 
 @pytest.mark.parametrize("m,k,n", [(4096, 256, 4096), (4096, 384, 4096), (4096, 320, 4096),
-                                   (8192, 8192, 8192), (2048, 1024, 8192)])
+                                   (8192, 8192, 8192), (2048, 1024, 8192), (4096, 2048, 2048),
+                                   (4096, 8192, 2048)])
 def test_matmul_large_tiles_sampled_rows(torch_cuda, backend, m, k, n):
     """The 256x256-tile path: every 256-row tile and every row residue mod 32
     appears among the sampled rows."""

@@ -104,7 +104,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const void *__restrict__ x
 
 // RmsNorm for bf16 rows of feature % 8 == 0, feature <= 8 * 256 * 4: one
 // workgroup per row, every 16-byte vector of x and gamma loaded once, up
-// front, and kept in registers through the reduction.
+// front, and kept in registers through the reduction (rmsnorm_vec_row).
 __global__ __launch_bounds__(256) void rmsnorm_bf16_vec_kernel(const uint16_t *__restrict__ x,
                                                                const uint16_t *__restrict__ gamma,
                                                                uint16_t *__restrict__ out,
@@ -123,36 +123,8 @@ __global__ __launch_bounds__(256) void rmsnorm_bf16_vec_kernel(const uint16_t *_
             gv[u] = gamma ? gr[v] : u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
         }
     }
-    float ss = 0.0f;
-#pragma unroll
-    for (int u = 0; u < kMaxVec; ++u)
-        if (threadIdx.x + 256u * u < nv)
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const float lo = __uint_as_float(xv[u][w] << 16), hi = __uint_as_float(xv[u][w] & 0xFFFF0000u);
-                ss = fmaf(lo, lo, ss);
-                ss = fmaf(hi, hi, ss);
-            }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    const float inv = 1.0f / sqrtf((part[0] + part[1] + part[2] + part[3]) / float(feature) + eps);
-    u32x4 *orow = reinterpret_cast<u32x4 *>(out + uint64_t(blockIdx.x) * feature);
-#pragma unroll
-    for (int u = 0; u < kMaxVec; ++u) {
-        const uint32_t v = threadIdx.x + 256u * u;
-        if (v >= nv) continue;
-        u32x4 r;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const float lo = (__uint_as_float(xv[u][w] << 16) * inv) * __uint_as_float(gv[u][w] << 16);
-            const float hi = (__uint_as_float(xv[u][w] & 0xFFFF0000u) * inv) *
-                             __uint_as_float(gv[u][w] & 0xFFFF0000u);
-            r[w] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
-        }
-        orow[v] = r;
-    }
+    rmsnorm_vec_row<kMaxVec>(xv, gv, nv, feature, eps, part,
+                             reinterpret_cast<u32x4 *>(out + uint64_t(blockIdx.x) * feature));
 }
 
 // Rotary embedding, rotate-half form over heads of head_dim elements.

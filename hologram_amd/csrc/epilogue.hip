@@ -297,6 +297,70 @@ __device__ void head_segment(const EpiArgs &g, const EpiSeg &sg, uint32_t blk) {
     if (d == 0) sg.cs[row] = amax / 127.0f;
 }
 
+// A group of one element-wise bf16 segment that also leaves the RmsNorm
+// statistics of each result row. The standalone bf16 RmsNorm kernel (one 256-thread workgroup per
+// row) has thread t sum the squares of its 16-byte vectors t + 256u in order,
+// then reduces each wave with a xor tree, then adds the four wave sums. Here
+// four one-wave workgroups per row each play one of those waves exactly: lane
+// l of wave w holds vectors 64w + l + 256u, computes the same per-lane sum and
+// the same tree, and stores the wave's sum; the reader adds the four in order.
+constexpr uint32_t kStatVec = 4;   // vectors per lane: n <= 8 * 256 * 4
+
+__global__ __launch_bounds__(kEpiThreads) void epilogue_stat_kernel(const EpiArgs g) {
+    const EpiSeg &sg = g.seg[0];
+    const uint32_t r = blockIdx.x / 4, w = blockIdx.x % 4, l = threadIdx.x;
+    const uint32_t nv = sg.n / 8;
+    const uint64_t plane = uint64_t(g.m) * g.ntot / 4;
+    const bool add = has_residual(sg);
+    float ss = 0.0f;
+#pragma unroll
+    for (uint32_t u = 0; u < kStatVec; ++u) {
+        const uint32_t v = 64 * w + l + 256 * u;
+        if (v >= nv) break;
+        const uint64_t e0 = uint64_t(r) * sg.n + 8ull * v;
+        const u32x4 res = add ? reinterpret_cast<const u32x4 *>(sg.residual)[e0 / 8]
+                              : u32x4{0u, 0u, 0u, 0u};
+        // columns 8v .. 8v+3 and 8v+4 .. 8v+7: both halves' partials in flight
+        // together, summed in ks order
+        const f32x4 *pa = reinterpret_cast<const f32x4 *>(g.P + uint64_t(r) * g.ntot + sg.col0 + 8 * v);
+        f32x4 va = pa[0], vb = pa[1];
+        for (uint32_t k0 = 1; k0 < g.ks; k0 += 8) {
+            f32x4 xa[8], xb[8];
+#pragma unroll
+            for (uint32_t i = 0; i < 8; ++i)
+                if (k0 + i < g.ks) {
+                    xa[i] = pa[(k0 + i) * plane];
+                    xb[i] = pa[(k0 + i) * plane + 1];
+                }
+#pragma unroll
+            for (uint32_t i = 0; i < 8; ++i)
+                if (k0 + i < g.ks) {
+                    va += xa[i];
+                    vb += xb[i];
+                }
+        }
+        u32x4 x;
+#pragma unroll
+        for (uint32_t h = 0; h < 4; ++h) {
+            const float p0 = h < 2 ? va[2 * h] : vb[2 * h - 4];
+            const float p1 = h < 2 ? va[2 * h + 1] : vb[2 * h - 3];
+            const float lo = base_value<true>(sg, p0, bf2f(res[h] & 0xffffu));
+            const float hi = base_value<true>(sg, p1, bf2f(res[h] >> 16));
+            x[h] = f2bf(lo) | (f2bf(hi) << 16);
+        }
+        if (sg.out) reinterpret_cast<u32x4 *>(sg.out)[e0 / 8] = x;
+#pragma unroll
+        for (uint32_t h = 0; h < 4; ++h) {
+            const float lo = bf2f(x[h] & 0xffffu), hi = __uint_as_float(x[h] & 0xFFFF0000u);
+            ss = fmaf(lo, lo, ss);
+            ss = fmaf(hi, hi, ss);
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if (l == 0) sg.ssq[4 * r + w] = ss;
+}
+
 template <bool kBf16>
 __global__ __launch_bounds__(kEpiThreads) void epilogue_kernel(const EpiArgs g) {
     uint32_t b0;
@@ -400,8 +464,19 @@ hipError_t launch_tile_epilogue(void *c, uint64_t count, bool bf16, const TileEp
 
 hipError_t launch_epilogue(EpiArgs g, hipStream_t stream) {
     if (g.nseg < 1 || g.nseg > uint32_t(kSkinnyMaxSeg)) return hipErrorInvalidValue;
+    if (g.seg[0].ssq) {
+        const EpiSeg &s = g.seg[0];
+        if (g.nseg != 1 || !g.bf16 || s.head_dim || s.pair >= 0 || s.skip || s.n % 8 != 0 ||
+            s.n > 8 * 256 * kStatVec || g.ntot != s.n || g.ks < 1 ||
+            ((reinterpret_cast<uintptr_t>(s.out) | reinterpret_cast<uintptr_t>(s.residual) |
+              reinterpret_cast<uintptr_t>(s.ssq)) & 15) != 0)
+            return hipErrorInvalidValue;
+        hipLaunchKernelGGL(epilogue_stat_kernel, dim3(4 * g.m), dim3(kEpiThreads), 0, stream, g);
+        return hipGetLastError();
+    }
     uint32_t total = 0;
     for (uint32_t i = 0; i < g.nseg; ++i) {
+        if (g.seg[i].ssq) return hipErrorInvalidValue;
         total += epilogue_blocks(g.seg[i], g.m);
         g.blk_end[i] = total;
     }

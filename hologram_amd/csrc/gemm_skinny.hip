@@ -63,6 +63,7 @@ struct SkinnyArgs {
     const void *b[kSkinnyMaxSeg];
     void *c[kSkinnyMaxSeg];
     uint32_t n[kSkinnyMaxSeg], col0[kSkinnyMaxSeg];
+    SkinnyNormA norm;                        // bf16: ssq non-null reads A as RmsNorm(A)
 };
 
 // Segment of this workgroup and its first strip (workgroup-uniform, picked
@@ -109,6 +110,26 @@ __global__ __launch_bounds__(256) void skinny_bf16_kernel(const SkinnyArgs g) {
     const auto ra = rsrc(A, M * K * 2u);   // rows >= M read zero
     const uint32_t bcol = n0 < N ? n0 * 2u : 0x80000000u;
 
+    // RmsNorm of A on the way in: the producer's four wave sums of each of
+    // this lane's rows and gamma at the lane's k values, loaded ahead of B
+    const bool norm = g.norm.ssq != nullptr;
+    f32x4 ssq[MT];
+    u32x4 gam[STEPS];
+    if (norm) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const uint32_t row = mt * 16 + q;
+            ssq[mt] = row < M ? reinterpret_cast<const f32x4 *>(g.norm.ssq)[row]
+                              : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int t = 0; t < STEPS; ++t) {
+            const uint32_t kr = uint32_t(t * kWaves + w) * 32;
+            gam[t] = u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+            if (kr < krows && g.norm.gamma)
+                gam[t] = *reinterpret_cast<const u32x4 *>(g.norm.gamma + kb0 + kr + 8 * grp);
+        }
+    }
     u32x4 b[STEPS][8], a[STEPS][MT];
 #pragma unroll
     for (int t = 0; t < STEPS; ++t) {
@@ -124,6 +145,14 @@ __global__ __launch_bounds__(256) void skinny_bf16_kernel(const SkinnyArgs g) {
                     ra, ((mt * 16 + q) * K + kb0 + kr + 8 * grp) * 2u, 0, 0);
         }
     }
+    // inv of each row: the four wave sums added in the standalone kernel's order
+    float inv[MT];
+    if (norm)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const f32x4 s = ssq[mt];
+            inv[mt] = 1.0f / sqrtf((s[0] + s[1] + s[2] + s[3]) / float(K) + g.norm.eps);
+        }
     f32x4 acc[MT][8];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -132,6 +161,21 @@ __global__ __launch_bounds__(256) void skinny_bf16_kernel(const SkinnyArgs g) {
 #pragma unroll
     for (int t = 0; t < STEPS; ++t) {
         if (uint32_t(t * kWaves + w) * 32 < krows) {
+            if (norm) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    u32x4 r;
+#pragma unroll
+                    for (int h = 0; h < 4; ++h) {
+                        const uint32_t x = a[t][mt][h], y = gam[t][h];
+                        const float lo = (__uint_as_float(x << 16) * inv[mt]) * __uint_as_float(y << 16);
+                        const float hi = (__uint_as_float(x & 0xFFFF0000u) * inv[mt]) *
+                                         __uint_as_float(y & 0xFFFF0000u);
+                        r[h] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+                    }
+                    a[t][mt] = r;
+                }
+            }
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
                 const u32x4 o = column8(b[t], c);
@@ -430,9 +474,11 @@ hipError_t launch_matmul_skinny(const void *a, const void *b, void *c, uint32_t 
 
 hipError_t launch_skinny_partials(const void *a, uint32_t m, uint32_t k, uint8_t dtype,
                                   const SkinnySegment *segs, int nseg, const SkinnyPlan &plan,
-                                  float *P, hipStream_t stream) {
+                                  float *P, hipStream_t stream, const SkinnyNormA *norm) {
     if (plan.mt == 0 || nseg < 1 || nseg > kSkinnyMaxSeg || P == nullptr) return hipErrorInvalidValue;
+    if (norm && norm->ssq && dtype != 7) return hipErrorInvalidValue;
     SkinnyArgs g{};
+    if (norm) g.norm = *norm;
     g.a = a;
     g.p = P;
     g.m = m;

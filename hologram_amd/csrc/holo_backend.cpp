@@ -356,8 +356,38 @@ int dispatch_group_impl(holo_backend *be, const SlotTable &st, const holo::Group
             d.mul_out = v.base;
         }
         d.skip = s.skip;
+        d.ssq = s.ssq;
+        if (s.ssq && (!bf16 || s.head_dim || s.pair >= 0 || s.skip || s.n % 8 != 0 || s.n > 8192 ||
+                      ((reinterpret_cast<uintptr_t>(d.out) | reinterpret_cast<uintptr_t>(d.residual)) & 15)))
+            return fail(HOLO_ERR_DISPATCH, std::string(op) + ": a norm-statistics epilogue needs a "
+                                                             "bf16 element-wise product of <= 8192 "
+                                                             "16-byte aligned columns");
     }
+    holo::SkinnyNormA na;
+    const bool a_norm = g.a_ssq != nullptr;
+    if (a_norm) {
+        if (!bf16) return fail(HOLO_ERR_DISPATCH, std::string(op) + ": a normalized A must be bf16");
+        na.ssq = g.a_ssq;
+        na.eps = g.a_eps;
+        if (g.a_gamma.slot != HOLO_SLOT_ABSENT) {
+            View gv;
+            if (!resolve(st, g.a_gamma, &gv))
+                return fail(HOLO_ERR_SLOT_OUT_OF_RANGE, std::string(op) + ": gamma slot unbound");
+            // affine_operand (float_kernels.rs:39-44): an empty gamma is the identity
+            if (gv.bytes > 0) {
+                HOLO_TRY(need(gv, uint64_t(g.k) * es, g.a_gamma.slot, op, "gamma"));
+                if (!aligned(gv, 16))
+                    return fail(HOLO_ERR_DISPATCH, std::string(op) + ": gamma must be 16-byte aligned");
+                na.gamma = reinterpret_cast<const uint16_t *>(gv.base);
+            }
+        }
+    }
+    bool stats = false;
+    for (size_t i = 0; i < nseg; ++i) stats = stats || g.segs[i].ssq;
     fast = fast && plan.mt != 0;
+    if (!fast && (a_norm || stats))
+        return fail(HOLO_ERR_DISPATCH, std::string(op) + ": a fused RmsNorm needs the few-row path "
+                                                         "(16-byte aligned operands)");
     if (!fast) {
         const holo::GroupSegDesc &s = g.segs[0];
         const bool elementwise = nseg == 1 && s.write_out && !s.head_dim && s.pair < 0;
@@ -385,7 +415,8 @@ int dispatch_group_impl(holo_backend *be, const SlotTable &st, const holo::Group
     e.ks = plan.ks;
     e.ntot = ntot;
     HOLO_TRY(launched(holo::launch_skinny_partials(a.base, g.m, g.k, g.dtype, ss, int(nseg), plan,
-                                                   static_cast<float *>(be->scratch), be->stream),
+                                                   static_cast<float *>(be->scratch), be->stream,
+                                                   a_norm ? &na : nullptr),
                       op));
     return launched(holo::launch_epilogue(e, be->stream), op);
 }

@@ -61,4 +61,53 @@ __device__ inline float act_f32(uint32_t act, float x) {
     }
 }
 
+// RmsNorm of one bf16 row held as 16-byte vectors: thread t of a 256-thread
+// group (waves 0-3 of its workgroup) holds vectors t + 256u (u < kMaxVec, v <
+// nv) of x and of gamma. Sum of squares: per thread in vector order with fmaf,
+// then a xor tree in each wave, then the four wave sums in order; then
+// out = (x * inv) * gamma narrowed by truncation (rms_norm_float,
+// src/cpu/float_kernels.rs:1683-1755). The standalone kernel and the fused
+// MatMul epilogue share this, so both give the same bits. `part` is 4 floats
+// of LDS; every thread of the workgroup must call it (it synchronises).
+template <int kMaxVec>
+__device__ __forceinline__ void rmsnorm_vec_row(const u32x4 (&xv)[kMaxVec],
+                                                const u32x4 (&gv)[kMaxVec], uint32_t nv,
+                                                uint32_t feature, float eps, float *part,
+                                                u32x4 *__restrict__ orow) {
+    const uint32_t t = threadIdx.x;
+    float ss = 0.0f;
+    if (t < 256) {
+#pragma unroll
+        for (int u = 0; u < kMaxVec; ++u)
+            if (t + 256u * u < nv)
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const float lo = __uint_as_float(xv[u][w] << 16),
+                                hi = __uint_as_float(xv[u][w] & 0xFFFF0000u);
+                    ss = fmaf(lo, lo, ss);
+                    ss = fmaf(hi, hi, ss);
+                }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if (t < 256 && (t & 63) == 0) part[t >> 6] = ss;
+    __syncthreads();
+    if (t >= 256) return;
+    const float inv = 1.0f / sqrtf((part[0] + part[1] + part[2] + part[3]) / float(feature) + eps);
+#pragma unroll
+    for (int u = 0; u < kMaxVec; ++u) {
+        const uint32_t v = t + 256u * u;
+        if (v >= nv) continue;
+        u32x4 r;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float lo = (__uint_as_float(xv[u][w] << 16) * inv) * __uint_as_float(gv[u][w] << 16);
+            const float hi = (__uint_as_float(xv[u][w] & 0xFFFF0000u) * inv) *
+                             __uint_as_float(gv[u][w] & 0xFFFF0000u);
+            r[w] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+        }
+        orow[v] = r;
+    }
+}
+
 }  // namespace holo

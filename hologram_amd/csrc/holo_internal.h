@@ -45,12 +45,18 @@ struct GroupSegDesc {
     bool rope = false, write_rope = true, quant = false, skip = false;
     uint32_t bucket = 0, new_rows = 0;
     int pair = -1;
+    float *ssq = nullptr;      // RmsNorm statistics of the rows (EpiSeg::ssq), session memory
 };
 struct GroupDesc {
     holo_buffer_ref a{};
     uint32_t m = 0, k = 0;
     uint8_t dtype = 0;
     std::vector<GroupSegDesc> segs;
+    // A read as RmsNorm(A) (SkinnyNormA): the statistics a producer group left
+    // in session memory, gamma (absent: identity) and epsilon
+    const float *a_ssq = nullptr;
+    holo_buffer_ref a_gamma{HOLO_SLOT_ABSENT, 0, 0};
+    float a_eps = 0.0f;
 };
 int dispatch_group(holo_backend *be, const std::vector<SlotRange> &slots, const GroupDesc &g);
 // The LUT activation id of a fused_activation id (-1: no table).

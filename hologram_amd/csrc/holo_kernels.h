@@ -132,6 +132,12 @@ struct EpiSeg {
     int pair = -1;                     // element-wise product with segment `pair`'s value
     void *mul_out = nullptr;
     bool skip = false;                 // consumed through another segment's pair; no blocks
+    // bf16, element-wise, n % 8 == 0, n <= 8192: also the RmsNorm statistics
+    // of each result row, [m][4] floats (the four wave sums of squares of the
+    // standalone bf16 RmsNorm kernel, in its order); out and residual must be
+    // 16-byte aligned. The normalization itself happens where the row is read
+    // (SkinnyNormA).
+    float *ssq = nullptr;
 };
 struct EpiArgs {
     const float *P = nullptr;          // [ks][m][ntot], ks >= 1
@@ -146,8 +152,17 @@ struct SkinnySegment {
     const void *b;
     uint32_t n;
 };
+// bf16 A read as RmsNorm(A) (feature = k): each element becomes
+// ((a * inv) * gamma) narrowed by truncation, inv = 1 / sqrt(sum / k + eps)
+// from the four wave sums an epilogue's `ssq` left for the row, the same bits
+// the standalone bf16 RmsNorm kernel writes. gamma null: the identity.
+struct SkinnyNormA {
+    const float *ssq = nullptr;        // [m][4], 16-byte aligned
+    const uint16_t *gamma = nullptr;   // [k], 16-byte aligned
+    float eps = 0.0f;
+};
 hipError_t launch_skinny_partials(const void *a, uint32_t m, uint32_t k, uint8_t dtype,
                                   const SkinnySegment *segs, int nseg, const SkinnyPlan &plan,
-                                  float *P, hipStream_t stream);
+                                  float *P, hipStream_t stream, const SkinnyNormA *norm = nullptr);
 
 }  // namespace holo

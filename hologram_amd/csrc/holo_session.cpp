@@ -34,6 +34,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <map>
 #include <memory>
 #include <string>
@@ -337,6 +338,7 @@ struct holo_session {
     uint32_t flags = 0;                           // HOLO_SESSION_* load options
     std::vector<Node> nodes;                      // the walk, in order
     std::vector<holo::GroupDesc> groups;          // fused few-row MatMul groups
+    float *norm_arena = nullptr;                  // RmsNorm statistics of fused norms
 };
 
 namespace {
@@ -601,10 +603,224 @@ void device_fusion(holo_session *s, const std::vector<uint8_t> &is_output,
     }
 }
 
+// ------------------------------------------------------------- norm fusion --
+// A bf16 RmsNorm between two few-row MatMuls (the decode step's norms: the
+// residual sum of Wo or Wd, normalized, read only by the next q/k/v, gate/up
+// or LM-head group) leaves the walk. The group that produces its input also
+// writes each row's sums of squares (the four wave sums of the standalone
+// kernel), and the group that reads its output reads the input instead and
+// normalizes A as it loads it. The normalized rows are never stored; every
+// value keeps the standalone kernel's bits.
+//
+// Conditions: the norm's input is the whole output of the nearest earlier
+// writer of its slot, an element-wise product of batch x feature; its output
+// is read by exactly one node, as that group's A, before its slot is written
+// again, and is no graph output; the producer is a group of one product; no node between the norm and that reader
+// writes the input or gamma; operands 16-byte aligned and not caller-bound.
+void node_slots(const holo_session *s, const Node &nd, std::vector<uint32_t> *rd,
+                std::vector<uint32_t> *wr) {
+    rd->clear();
+    wr->clear();
+    if (nd.group < 0) {
+        std::vector<holo_buffer_ref> r, w;
+        call_operands(s->calls[nd.call], &r, &w);
+        for (auto &x : r) rd->push_back(x.slot);
+        for (auto &x : w) wr->push_back(x.slot);
+        return;
+    }
+    const holo::GroupDesc &g = s->groups[size_t(nd.group)];
+    rd->push_back(g.a.slot);
+    if (g.a_gamma.slot != HOLO_SLOT_ABSENT) rd->push_back(g.a_gamma.slot);
+    std::vector<uint32_t> r, w;
+    for (const auto &sg : g.segs) {
+        seg_slots(sg, &r, &w);
+        rd->push_back(sg.b.slot);
+        rd->insert(rd->end(), r.begin(), r.end());
+        wr->insert(wr->end(), w.begin(), w.end());
+    }
+}
+
+bool has_slot(const std::vector<uint32_t> &v, uint32_t slot) {
+    return std::find(v.begin(), v.end(), slot) != v.end();
+}
+
+int norm_fusion(holo_session *s, const std::vector<uint8_t> &is_output,
+                const std::vector<uint8_t> &is_input) {
+    auto &nodes = s->nodes;
+    const size_t nn = nodes.size();
+    std::vector<std::vector<uint32_t>> R(nn), W(nn);
+    for (size_t i = 0; i < nn; ++i) node_slots(s, nodes[i], &R[i], &W[i]);
+    auto caller_bound = [&](uint32_t slot) { return slot >= is_input.size() || is_input[slot]; };
+    auto aligned16 = [&](const holo_buffer_ref &r) { return r.offset % 16 == 0 && !caller_bound(r.slot); };
+    // a plain MatMul-family call node as a group of one segment
+    auto as_group = [&](size_t i) -> holo::GroupDesc * {
+        Node &nd = nodes[i];
+        if (nd.group >= 0) return &s->groups[size_t(nd.group)];
+        MmView mv;
+        if (!matmul_family(s->calls[nd.call], &mv)) return nullptr;
+        holo::GroupDesc g;
+        g.a = mv.mm.a;
+        g.m = mv.mm.m;
+        g.k = mv.mm.k;
+        g.dtype = mv.mm.dtype;
+        holo::GroupSegDesc d;
+        d.b = mv.mm.b;
+        d.out = mv.mm.output;
+        d.n = mv.mm.n;
+        d.base = mv.base;
+        d.act = mv.act;
+        d.residual = mv.residual;
+        g.segs.push_back(d);
+        s->groups.push_back(std::move(g));
+        nd.group = int(s->groups.size() - 1);
+        return &s->groups.back();
+    };
+    // would-be group view of node i without converting it
+    auto view = [&](size_t i, holo::GroupDesc *tmp) -> const holo::GroupDesc * {
+        const Node &nd = nodes[i];
+        if (nd.group >= 0) return &s->groups[size_t(nd.group)];
+        MmView mv;
+        const holo_kernel_call &c = s->calls[nd.call];
+        if (!matmul_family(c, &mv) || mv.mm.b_packed) return nullptr;
+        tmp->a = mv.mm.a;
+        tmp->m = mv.mm.m;
+        tmp->k = mv.mm.k;
+        tmp->dtype = mv.mm.dtype;
+        tmp->segs.assign(1, holo::GroupSegDesc{});
+        tmp->segs[0].b = mv.mm.b;
+        tmp->segs[0].out = mv.mm.output;
+        tmp->segs[0].n = mv.mm.n;
+        tmp->segs[0].base = mv.base;
+        tmp->segs[0].residual = mv.residual;
+        return tmp;
+    };
+    auto few_row = [&](const holo::GroupDesc &g) {
+        if (g.dtype != HOLO_DTYPE_BF16 || (g.a.offset % 16) || caller_bound(g.a.slot)) return false;
+        const holo::SkinnyPlan pl = holo::matmul_skinny_plan(g.m, g.k, g.segs[0].n, g.dtype);
+        if (pl.mt == 0) return false;
+        for (const auto &sg : g.segs) {
+            const holo::SkinnyPlan p = holo::matmul_skinny_plan(g.m, g.k, sg.n, g.dtype);
+            if (p.mt != pl.mt || p.steps != pl.steps || p.ks != pl.ks || sg.b.offset % 16 ||
+                caller_bound(sg.b.slot))
+                return false;
+        }
+        return true;
+    };
+    std::vector<bool> drop(nn, false);
+    std::vector<std::pair<int, int>> links;   // (producer group, segment), consumer group
+    std::vector<int> link_cons;
+    auto linked_seg = [&](int grp, int seg) {
+        return grp >= 0 && std::find(links.begin(), links.end(), std::make_pair(grp, seg)) != links.end();
+    };
+    auto linked_cons = [&](int grp) {
+        return grp >= 0 && std::find(link_cons.begin(), link_cons.end(), grp) != link_cons.end();
+    };
+    for (size_t k = 0; k < nn; ++k) {
+        if (nodes[k].group >= 0 || s->calls[nodes[k].call].tag != HOLO_OP_RMS_NORM) continue;
+        const holo_norm_call &nc = s->calls[nodes[k].call].u.norm;
+        if (nc.dtype != HOLO_DTYPE_BF16 || nc.residual.slot != HOLO_SLOT_ABSENT || nc.channels ||
+            nc.num_groups || nc.batch == 0 || nc.feature % 8 || nc.feature > 8192 || nc.feature == 0)
+            continue;
+        float eps = 1e-9f;
+        if (nc.epsilon_bits != 0) {
+            const uint32_t eb = uint32_t(nc.epsilon_bits);
+            memcpy(&eps, &eb, 4);
+            if (!(std::isfinite(eps) && eps > 0.0f)) continue;
+        }
+        const holo_buffer_ref x = nc.x, y = nc.output;
+        const bool has_g = nc.gamma.slot != HOLO_SLOT_ABSENT;
+        if (x.slot == y.slot || !aligned16(x) || (has_g && !aligned16(nc.gamma)) ||
+            y.slot >= is_output.size() || is_output[y.slot])
+            continue;
+        // producer: the nearest earlier writer of x
+        size_t j = k;
+        while (j > 0 && !has_slot(W[j - 1], x.slot)) --j;
+        if (j == 0) continue;
+        --j;
+        holo::GroupDesc tp;
+        const holo::GroupDesc *pg = view(j, &tp);
+        if (!pg || pg->segs.size() != 1 || !few_row(*pg) || pg->m != nc.batch) continue;
+        int pseg = -1;
+        for (size_t t = 0; t < pg->segs.size(); ++t) {
+            const auto &sg = pg->segs[t];
+            if (same_ref(sg.out, x) && sg.write_out && sg.n == nc.feature && !sg.head_dim && !sg.rope &&
+                !sg.quant && sg.pair < 0 && !sg.skip && !sg.ssq && aligned16(sg.out) &&
+                (!(sg.base == holo::kEpiAdd || sg.base == holo::kEpiAddAct) || aligned16(sg.residual)))
+                pseg = int(t);
+        }
+        if (pseg < 0 || linked_seg(nodes[j].group, pseg)) continue;
+        // consumer: the one reader of y before y's slot is written again
+        size_t q = nn, readers = 0;
+        for (size_t t = k + 1; t < nn; ++t) {
+            if (has_slot(R[t], y.slot)) {
+                ++readers;
+                q = t;
+            }
+            if (has_slot(W[t], y.slot)) break;
+        }
+        if (readers != 1) continue;
+        holo::GroupDesc tc;
+        const holo::GroupDesc *cg = view(q, &tc);
+        if (!cg || !few_row(*cg) || linked_cons(nodes[q].group) || !same_ref(cg->a, y) ||
+            cg->m != nc.batch || cg->k != nc.feature)
+            continue;
+        {   // y read only as A
+            std::vector<uint32_t> r, w;
+            bool other = false;
+            for (const auto &sg : cg->segs) {
+                seg_slots(sg, &r, &w);
+                other = other || sg.b.slot == y.slot || has_slot(r, y.slot);
+            }
+            if (other) continue;
+        }
+        bool clobbered = false;
+        for (size_t t = k + 1; t < q && !clobbered; ++t)
+            clobbered = has_slot(W[t], x.slot) || (has_g && has_slot(W[t], nc.gamma.slot));
+        if (clobbered) continue;
+        // commit
+        as_group(j);
+        holo::GroupDesc *C = as_group(q);
+        C->a = x;
+        C->a_gamma = has_g ? nc.gamma : holo_buffer_ref{HOLO_SLOT_ABSENT, 0, 0};
+        C->a_eps = eps;
+        links.push_back({nodes[j].group, pseg});
+        link_cons.push_back(nodes[q].group);
+        drop[k] = true;
+        node_slots(s, nodes[j], &R[j], &W[j]);
+        node_slots(s, nodes[q], &R[q], &W[q]);
+        R[k].clear();
+        W[k].clear();
+    }
+    if (links.empty()) return HOLO_OK;
+    // the statistics: [64 rows][4] floats per fused norm, in session memory
+    // (a dry load has no device: the groups are only counted)
+    float *arena = nullptr;
+    if (s->be) {
+        if (hipMalloc(&arena, links.size() * 64 * 4 * sizeof(float)) != hipSuccess) {
+            (void)hipGetLastError();
+            return set_error(HOLO_ERR_INIT, "session_load: device allocation failed (norm statistics)");
+        }
+        s->norm_arena = arena;
+    }
+    for (size_t f = 0; f < links.size(); ++f) {
+        float *st = arena ? arena + f * 64 * 4 : nullptr;
+        holo::GroupDesc &pgd = s->groups[size_t(links[f].first)];
+        holo::GroupDesc &cgd = s->groups[size_t(link_cons[f])];
+        pgd.segs[size_t(links[f].second)].ssq = st;
+        cgd.a_ssq = st;
+    }
+    std::vector<Node> kept;
+    for (size_t i = 0; i < nn; ++i)
+        if (!drop[i]) kept.push_back(nodes[i]);
+    nodes.swap(kept);
+    return HOLO_OK;
+}
+
 void release(holo_session *s) {
     if (!s) return;
     if (s->stream) (void)hipStreamSynchronize(s->stream);
     if (s->graph) (void)hipGraphExecDestroy(s->graph);
+    if (s->norm_arena) (void)hipFree(s->norm_arena);
     if (s->const_arena) (void)hipFree(s->const_arena);
     if (s->work_arena) (void)hipFree(s->work_arena);
     if (s->stream) (void)hipStreamDestroy(s->stream);
@@ -855,6 +1071,10 @@ plan_moves:
             for (uint32_t ci : lv) s->nodes.push_back(Node{-1, ci});
     } else {
         device_fusion(s.get(), is_output, is_input);
+        if (!(flags & HOLO_SESSION_NO_NORM_FUSION)) {
+            const int rc = norm_fusion(s.get(), is_output, is_input);
+            if (rc != HOLO_OK) return rc;
+        }
     }
     *out = s.release();
     return HOLO_OK;

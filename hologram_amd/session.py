@@ -27,12 +27,14 @@ class Port:
 # load options (include/holo_hip.h)
 NO_EPILOGUE_FUSION = 1   # skip the reference loader's fuse_matmul_epilogue
 NO_DEVICE_FUSION = 2     # skip this backend's grouped few-row MatMuls and epilogues
+NO_NORM_FUSION = 4       # keep each RmsNorm between few-row MatMuls as its own launch
 
 
 class HipSession:
     """`backend=None` loads dry: parse, size and validate every call on the host,
     with no device (such a session reports ports and refuses to execute).
-    `flags` turns the load-time fusions off (NO_EPILOGUE_FUSION, NO_DEVICE_FUSION);
+    `flags` turns the load-time fusions off (NO_EPILOGUE_FUSION, NO_DEVICE_FUSION,
+    NO_NORM_FUSION);
     fused and unfused walks give the same bits."""
 
     def __init__(self, backend: HipBackend | None, archive: bytes, flags: int = 0):

@@ -367,9 +367,14 @@ int holo_hip_session_load(holo_backend *be, const uint8_t *archive, size_t len,
  * fusion: few-row MatMuls that share their A operand run as one launch, and
  * the ops that only consume such a product (rotary embedding, int8
  * quantize+append, the SwiGLU product) run inside the launch that finishes
- * it. Both give the same bits as the unfused walk; the flags turn them off. */
+ * it. A bf16 RmsNorm between two such MatMuls is split between them: the
+ * first leaves each row's sums of squares, the second normalizes its A as it
+ * reads it, and the norm's own launch and output go away. All of these give
+ * the same bits as the unfused walk; the flags turn them off
+ * (NO_DEVICE_FUSION also turns off the norm fusion). */
 #define HOLO_SESSION_NO_EPILOGUE_FUSION 1u
 #define HOLO_SESSION_NO_DEVICE_FUSION 2u
+#define HOLO_SESSION_NO_NORM_FUSION 4u
 int holo_hip_session_load_ex(holo_backend *be, const uint8_t *archive, size_t len, uint32_t flags,
                              holo_session **out);
 /* Steps of one walk after fusion (each a call or a fused MatMul group), and

@@ -15,10 +15,10 @@ import pytest
 
 from hologram_amd import (DTYPE_BF16, DTYPE_F32, BinaryCall, BufferRef, HipSession, HoloWriter,
                           KernelCall, MatMulActivationCall, MatMulAddActivationCall,
-                          MatMulAddCall, MatMulCall, PortDescriptor, SlotOutOfRange, UnaryCall,
+                          MatMulAddCall, MatMulCall, NormCall, PortDescriptor, SlotOutOfRange, UnaryCall,
                           UnsupportedOp, decode_call, fused_activation, validate)
 from hologram_amd.decoder_graph import DecoderConfig, build_decode_step, init_weights
-from hologram_amd.session import NO_DEVICE_FUSION, NO_EPILOGUE_FUSION
+from hologram_amd.session import NO_DEVICE_FUSION, NO_EPILOGUE_FUSION, NO_NORM_FUSION
 
 M, K, N = 4, 64, 32
 
@@ -132,7 +132,53 @@ def test_decoder_walk_counts():
     # per layer: RmsNorm, {q,k,v + 2 RoPE + 2 appends}, attention, Wo+Add, RmsNorm,
     # {gate+Silu, up, Mul}, Wd+Add
     assert full.n_calls == 1 + 15 * L + 3
-    assert full.n_nodes == 1 + 7 * L + 3 and full.n_groups == 2 * L
+    grouped = HipSession(None, a, flags=NO_NORM_FUSION)
+    assert grouped.n_nodes == 1 + 7 * L + 3 and grouped.n_groups == 2 * L
+    # the norms after Wo+Add and Wd+Add (the next layer's, or the final one)
+    # split between producer and reader: Wo+Add, Wd+Add and the LM head become
+    # groups of one; only layer 0's input norm (after the embedding) remains
+    assert full.n_nodes == 1 + 5 * L + 3 and full.n_groups == 4 * L + 1
+
+
+def norm(x, g, o, rows, feat, dt=DTYPE_BF16):
+    es = 2 if dt == DTYPE_BF16 else 4
+    return KernelCall.RmsNorm(NormCall(ref(x, rows * feat, es), ref(g, feat, es),
+                                       ref(o, rows * feat, es), rows, feat, dtype=dt))
+
+
+def norm_chain(dt=DTYPE_BF16, out_y=False, extra_reader=False, feat=K, clobber=False):
+    """X = A*B (slot 2); Y = RmsNorm(X) (slot 4, gamma slot 5); Z = Y*W (slot 6).
+    A, B, W and gamma are computed in-graph (sums of inputs), so no operand of
+    the MatMuls or the norm is caller-bound."""
+    calls = [add(10, 10, 0, dt, M * K), add(11, 11, 1, dt, K * feat),
+             add(12, 12, 3, dt, feat * N), add(13, 13, 5, dt, feat),
+             mm(0, 1, 2, dt, n=feat), norm(2, 5, 4, M, feat, dt)]
+    if clobber:
+        calls.append(add(10, 10, 2, dt, M * feat))
+    calls.append(mm(4, 3, 6, dt, k=feat))
+    outs = [(6, M * N, dt)]
+    if extra_reader:
+        calls.append(add(4, 4, 7, dt, M * feat))
+        outs.append((7, M * feat, dt))
+    if out_y:
+        outs.append((4, M * feat, dt))
+    inputs = [(10, M * K, dt), (11, K * feat, dt), (12, feat * N, dt), (13, feat, dt)]
+    return archive(calls, inputs, outs)
+
+
+def test_norm_between_few_row_matmuls_is_split():
+    s = HipSession(None, norm_chain())
+    assert s.n_calls == 7 and s.n_nodes == 6 and s.n_groups == 2
+    assert HipSession(None, norm_chain(), flags=NO_NORM_FUSION).n_nodes == 7
+
+
+@pytest.mark.parametrize("kw", [dict(dt=DTYPE_F32), dict(out_y=True), dict(extra_reader=True),
+                                dict(feat=K + 4), dict(clobber=True)])
+def test_norm_fusion_conditions(kw):
+    # f32; the norm's output a graph output or read twice; a feature that is
+    # not a multiple of 8; the input overwritten before the reader: standalone
+    s = HipSession(None, norm_chain(**kw))
+    assert s.n_nodes == s.n_calls, kw
 
 
 def test_members_that_depend_on_each_other_are_not_grouped():

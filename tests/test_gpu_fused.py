@@ -18,11 +18,12 @@ import pytest
 
 import oracle
 from conftest import from_dev, to_dev
-from hologram_amd import (DTYPE_BF16, DTYPE_F32, BufferRef, DeviceWorkspace, HipSession,
-                          KernelCall, MatMulActivationCall, MatMulAddActivationCall,
-                          MatMulAddCall, MatMulCall, fused_activation)
+from hologram_amd import (DTYPE_BF16, DTYPE_F32, BinaryCall, BufferRef, DeviceWorkspace,
+                          HipSession, HoloWriter, KernelCall, MatMulActivationCall,
+                          MatMulAddActivationCall, MatMulAddCall, MatMulCall, NormCall,
+                          PortDescriptor, fused_activation)
 from hologram_amd.decoder_graph import DecoderConfig, build_decode_step, init_weights, rope_tables
-from hologram_amd.session import NO_DEVICE_FUSION, NO_EPILOGUE_FUSION
+from hologram_amd.session import NO_DEVICE_FUSION, NO_EPILOGUE_FUSION, NO_NORM_FUSION
 
 pytestmark = pytest.mark.gpu
 
@@ -132,7 +133,7 @@ def test_session_fusion_is_bit_identical(torch_cuda, backend):
     archive = build_decode_step(CFG, init_weights(CFG, seed=21))
     base, base_counts = walk(backend, archive, NO_EPILOGUE_FUSION | NO_DEVICE_FUSION, 5)
     assert base_counts[2] == 0
-    for flags in (NO_DEVICE_FUSION, NO_EPILOGUE_FUSION, 0):
+    for flags in (NO_DEVICE_FUSION, NO_EPILOGUE_FUSION, NO_NORM_FUSION, 0):
         rec, counts = walk(backend, archive, flags, 5)
         if not flags & NO_DEVICE_FUSION:
             assert counts[2] > 0 and counts[1] < base_counts[1]
@@ -147,3 +148,72 @@ def test_fused_session_graph_replay_matches_eager(torch_cuda, backend):
     graph, _ = walk(backend, archive, 0, 6, graph=True)
     for step, (x, y) in enumerate(zip(eager, graph)):
         assert x == y, f"step {step}"
+
+
+def norm_archive(m, k0, feat, n, gamma, residual):
+    """h = A*B (+ R); y = RmsNorm(h) (gamma or none); z = y*W. A, B, W and gamma
+    are doubled in-graph, so the MatMuls' operands are session memory. Outputs
+    z and h."""
+    bf = DTYPE_BF16
+
+    def r(slot, elems):
+        return BufferRef(slot, 0, 2 * elems)
+
+    def add(a, b, o, elems):
+        return KernelCall.Add(BinaryCall(r(a, elems), r(b, elems), r(o, elems), elems, 16, bf))
+
+    calls = [add(20, 20, 0, m * k0), add(21, 21, 1, k0 * feat), add(22, 22, 3, feat * n)]
+    if gamma:
+        calls.append(add(23, 23, 5, feat))
+    if residual:
+        calls.append(add(24, 24, 9, m * feat))
+    calls.append(KernelCall.MatMul(MatMulCall(r(0, m * k0), r(1, k0 * feat), r(2, m * feat),
+                                              m, k0, feat, bf)))
+    h = 2
+    if residual:
+        calls.append(add(2, 9, 8, m * feat))
+        h = 8
+    calls.append(KernelCall.RmsNorm(NormCall(r(h, m * feat),
+                                             r(5, feat) if gamma else BufferRef(0xFFFFFFFF),
+                                             r(4, m * feat), m, feat, dtype=bf)))
+    calls.append(KernelCall.MatMul(MatMulCall(r(4, m * feat), r(3, feat * n), r(6, m * n),
+                                              m, feat, n, bf)))
+    w = HoloWriter()
+    w.kernel_calls = calls
+    w.exec_plan = [[i] for i in range(len(calls))]   # the residual is ready before the MatMul
+    for s, e in ((20, m * k0), (21, k0 * feat), (22, feat * n), (23, feat), (24, m * feat)):
+        w.inputs.append(PortDescriptor(f"in{s}", s, e, bf, [e]))
+    for s, e in ((6, m * n), (h, m * feat)):
+        w.outputs.append(PortDescriptor(f"out{s}", s, e, bf, [e]))
+    return w.finish()
+
+
+@pytest.mark.parametrize("m,feat,gamma,residual", [
+    (8, 2048, True, True), (3, 1056, True, True), (40, 4096, False, True),
+    (1, 8192, True, False), (17, 256, True, True)])
+def test_split_norm_is_bit_identical(torch_cuda, backend, m, feat, gamma, residual):
+    """The norm split between its producer's epilogue (row statistics) and its
+    reader's A load gives the standalone RmsNorm's bits: same z, same h.
+    Features cover one to four vectors per lane and partly filled waves."""
+    k0, n = 512, 384
+    rng = np.random.default_rng(m * 7 + feat)
+    data = [rng.standard_normal(m * k0) / np.sqrt(k0), rng.standard_normal(k0 * feat) * 0.5,
+            rng.standard_normal(feat * n) / np.sqrt(feat), 1 + 0.25 * rng.standard_normal(feat),
+            rng.standard_normal(m * feat)]
+    inputs = [narrow(x.astype(np.float32), DTYPE_BF16).tobytes() for x in data]
+    arch = norm_archive(m, k0, feat, n, gamma, residual)
+    got = {}
+    for flags in (0, NO_NORM_FUSION):
+        sess = HipSession(backend, arch, flags=flags)
+        for i, b in enumerate(inputs):
+            sess.write_input(i, b)
+        sess.run()
+        sess.synchronize()
+        got[flags] = ([sess.read_output(o) for o in range(len(sess.outputs))], sess.n_nodes)
+        sess.close()
+    (fused, n_fused), (plain, n_plain) = got[0], got[NO_NORM_FUSION]
+    assert n_fused == n_plain - 1, "the norm was not fused"
+    for o, (u, v) in enumerate(zip(fused, plain)):
+        a, b = np.frombuffer(u, np.uint16), np.frombuffer(v, np.uint16)
+        bad = np.flatnonzero(a != b)
+        assert bad.size == 0, f"output {o}: {bad.size} of {a.size} differ, first at {bad[:4]}"

@@ -286,6 +286,11 @@ constexpr int kBigM = 256, kBigN = 256, kBigK = 64, kLdk = kBigK + 8;
 #ifndef HOLO_BIG_MIN_TILES
 #define HOLO_BIG_MIN_TILES 128
 #endif
+// 1: large tiles run gemm_bf16_dma_kernel (LDS DMA, transposing B reads);
+// 0: gemm_bf16_big_kernel (register staging, B transposed with permutes)
+#ifndef HOLO_GEMM_DMA
+#define HOLO_GEMM_DMA 1
+#endif
 
 __device__ __forceinline__ void tile_coords(uint32_t wg, uint32_t nwg, uint32_t tiles_m,
                                             uint32_t tiles_n, uint32_t *tm, uint32_t *tn) {
@@ -500,6 +505,238 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_big_kernel(const uint16_t *_
         }
 }
 
+// ------------------------------------------- bf16, large tiles, LDS DMA ----
+// The same 256x256 tile and wave layout as gemm_bf16_big_kernel, 32-deep K
+// slabs in kDmaStages LDS stages. Both operands go from global memory into
+// LDS by DMA (buffer_load ... lds: lane l of a load writes the 16 bytes at
+// LDS base + 16 l) in their own layouts, A [m][k] and B [k][n], each 16-byte
+// chunk of a row at a swizzled place (chunk ^ f(row)) so fragment reads hit
+// distinct banks. The A operand is a 16-byte LDS read. The B operand (8
+// consecutive k of one column per lane) is two ds_read_b64_tr_b16: within
+// each 16-lane group, lane r addresses row k0 + r/4, columns n0 + 4(r%4) ..+3,
+// and lane j receives rows k0 .. k0+3 of column n0 + j. No operand passes
+// through registers on its way to LDS. One barrier per slab, placed between
+// the slab's two k-steps so the MFMAs already issued cover it. The MFMA order
+// per output tile is the same as gemm_bf16_big_kernel's, so the results are
+// identical.
+constexpr int kDmaK = 32, kDmaStages = 4;
+constexpr uint32_t kDmaStage = 32768, kDmaB = 16384;   // bytes per stage; B after A
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+__device__ __forceinline__ uint32_t swz_a(uint32_t row) { return ((row >> 1) ^ (row >> 2)) & 3u; }
+__device__ __forceinline__ uint32_t swz_b(uint32_t k) {
+    return 4u * ((k & 3u) | (((k >> 3) & 1u) << 2));
+}
+// s_waitcnt with vmcnt <= n and no wait on the other counters (gfx9 encoding)
+template <int n>
+__device__ __forceinline__ void wait_vm() {
+    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// The slab barrier: each wave has waited (wait_vm) for its own share of the
+// DMA loads the next reads need, and its reads of the stage about to be
+// refilled have been consumed by MFMAs already issued. __syncthreads' release
+// fence would also wait for the DMA loads still meant to be in flight, so the
+// barrier is bare, with compiler barriers on both sides.
+__device__ __forceinline__ void slab_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(const uint16_t *__restrict__ A,
+                                                              const uint16_t *__restrict__ B,
+                                                              uint16_t *__restrict__ C, uint32_t M,
+                                                              uint32_t N, uint32_t K) {
+    // one array per stage: the compiler then knows a DMA into one stage does
+    // not feed reads of another, and waits only where a read needs the data
+    __shared__ __attribute__((aligned(1024))) uint8_t lds0[kDmaStage], lds1[kDmaStage],
+        lds2[kDmaStage], lds3[kDmaStage];
+    auto stage = [&](auto st) -> lds_u8 * {
+        constexpr int kS = decltype(st)::value % kDmaStages;
+        return kS == 0 ? (lds_u8 *)lds0 : kS == 1 ? (lds_u8 *)lds1 : kS == 2 ? (lds_u8 *)lds2 : (lds_u8 *)lds3;
+    };
+    const uint32_t tiles_m = M / kBigM, tiles_n = N / kBigN;
+    uint32_t tm, tn;
+    tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, &tm, &tn);
+    const uint32_t m0 = tm * kBigM, n0 = tn * kBigN;
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
+    const int lr = lane & 31, lg = lane >> 5;
+
+    // DMA: load t (0..3) of a wave fills 1 KiB of a stage. A: rows
+    // 64 wave + 16 t + lane/4, physical chunk lane%4; B: k-rows
+    // 8 wave + 2 t + lane/32, physical chunk lane%32. Each lane fetches the
+    // logical chunk stored there.
+    const uint32_t arow = 64u * wave + lane / 4;
+    const uint32_t a_voff = (arow * K + 8u * ((lane & 3) ^ swz_a(arow))) * 2u;
+    uint32_t b_voff[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const uint32_t k = 8u * wave + 2u * t + lane / 32;
+        b_voff[t] = (k * N + 8u * ((lane & 31) ^ swz_b(k))) * 2u;
+    }
+    auto dma = [&](uint32_t slab, auto st) {
+        const uint32_t k0 = slab * kDmaK;
+        const auto ra = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t *>(A + uint64_t(m0) * K + k0), 0, int(512u * K), 0x00020000);
+        const auto rb = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t *>(B + uint64_t(k0) * N + n0), 0, int(64u * N), 0x00020000);
+        lds_u8 *sa = stage(st) + wave * 4096u;
+        lds_u8 *sb = sa + kDmaB;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, sa + 1024 * t, 16, a_voff, 32u * K * t, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, sb + 1024 * t, 16, b_voff[t], 0, 0, 0);
+    };
+
+    // fragment offsets within a stage. A: row wm + 32i + lr, logical chunk
+    // kk/8 + lg (the swizzle depends on lr only); B: per j, lane (g, r) of
+    // its 16-lane group addresses k-row 8(g/2) + r/4 (+ kk + 4h), column
+    // wn + 32j + 16(g%2) + 4(r%4) (the swizzle is the same for every kk, h)
+    const uint32_t a_frag = (wm + lr) * 64u + ((lg ^ swz_a(lr)) * 16u);
+    uint32_t b_frag[4];
+    {
+        const uint32_t g = lane >> 4, r = lane & 15;
+        const uint32_t k = 8u * (g >> 1) + (r >> 2);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t n = wn + 32u * j + 16u * (g & 1) + 4u * (r & 3);
+            b_frag[j] = kDmaB + k * 512u + (((n >> 3) ^ swz_b(k)) * 16u) + (n & 7u) * 2u;
+        }
+    }
+    bf16x8 af[2][4], bfr[2][4];
+    auto fload = [&](auto st, int kk, int fb) {
+        const lds_u8 *base = stage(st);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            af[fb][i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8 *>(
+                base + ((a_frag + 2048u * i) ^ (kk == 16 ? 32u : 0u)));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const lds_u8 *p = base + b_frag[j] + 512u * kk;
+            const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                reinterpret_cast<lds_v4i16 *>(const_cast<lds_u8 *>(p)));
+            const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                reinterpret_cast<lds_v4i16 *>(const_cast<lds_u8 *>(p + 2048)));
+            bfr[fb][j] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+    };
+
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    auto mfmas = [&](int fb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[fb][i], bfr[fb][j], acc[i][j], 0, 0, 0);
+    };
+    // 12 fragment reads, one after each of the first 12 MFMAs
+    auto mix_reads = [] {
+#pragma unroll
+        for (int i = 0; i < 12; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    };
+
+    // One slab s in stage s % kDmaStages. kNext: slab s+1 exists (wait for its
+    // DMA and pass the barrier mid-slab, then read its first fragments);
+    // kWait: the DMA loads allowed to stay in flight at that point; kLoad: slab
+    // s + kDmaStages - 1 exists (its DMA goes into the stage slab s-1 used).
+    auto slab = [&](uint32_t s, auto st, auto next, auto wait, auto load) {
+        constexpr bool kNext = decltype(next)::value, kLoad = decltype(load)::value;
+        constexpr int kWait = decltype(wait)::value, kS = decltype(st)::value;
+        fload(st, 16, 1);
+        mfmas(0);
+        mix_reads();
+        __builtin_amdgcn_sched_barrier(0);
+        if (kNext) {
+            wait_vm<kWait>();
+            slab_barrier();
+            if (kLoad) dma(s + kDmaStages - 1, std::integral_constant<int, kS + kDmaStages - 1>{});
+            fload(std::integral_constant<int, kS + 1>{}, 0, 0);
+        }
+        mfmas(1);
+        if (kNext) {
+            if (kLoad) {
+                // 12 fragment reads and 8 DMA loads over the 16 MFMAs
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+            } else {
+                mix_reads();
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    using yes = std::integral_constant<bool, true>;
+    using no = std::integral_constant<bool, false>;
+    // DMA loads per slab per wave: 8. While slab s+1 is awaited, the slabs
+    // issued after it (up to s + kDmaStages - 2) may stay in flight.
+    using w_steady = std::integral_constant<int, 8 * (kDmaStages - 3)>;
+    using w_drain = std::integral_constant<int, 0>;
+    static_assert(kDmaStages == 4, "the loop below is written for four stages");
+
+    using s0 = std::integral_constant<int, 0>;
+    using s1 = std::integral_constant<int, 1>;
+    using s2 = std::integral_constant<int, 2>;
+    using s3 = std::integral_constant<int, 3>;
+
+    const uint32_t nk = K / kDmaK;   // a multiple of 4, >= 8
+    dma(0, s0{});
+    dma(1, s1{});
+    dma(2, s2{});
+    wait_vm<16>();
+    slab_barrier();
+    fload(s0{}, 0, 0);
+    // slab s uses stage s % 4; every slab but the last three issues the DMA
+    // of slab s + 3
+    for (uint32_t s = 0; s + 4 < nk; s += 4) {
+        slab(s, s0{}, yes{}, w_steady{}, yes{});
+        slab(s + 1, s1{}, yes{}, w_steady{}, yes{});
+        slab(s + 2, s2{}, yes{}, w_steady{}, yes{});
+        slab(s + 3, s3{}, yes{}, w_steady{}, yes{});
+    }
+    slab(nk - 4, s0{}, yes{}, w_steady{}, yes{});
+    slab(nk - 3, s1{}, yes{}, w_steady{}, no{});
+    slab(nk - 2, s2{}, yes{}, w_drain{}, no{});
+    slab(nk - 1, s3{}, no{}, w_drain{}, no{});
+
+    uint16_t *cbase = C + uint64_t(m0 + wm + 4 * lg) * N + n0 + wn + lr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint16_t *ct = cbase + uint64_t(32 * i) * N + 32 * j;
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                ct[uint64_t(8 * (r >> 2) + (r & 3)) * N] = uint16_t(__float_as_uint(acc[i][j][r]) >> 16);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+}
+
 }  // namespace
 
 size_t matmul_scratch_bytes(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype) {
@@ -545,9 +782,15 @@ hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint
         if ((al & 15) == 0 && m % kBigM == 0 && n % kBigN == 0 && k % (2 * kBigK) == 0 &&
             k >= 4 * kBigK && k < (1u << 22) && n < (1u << 24) &&
             uint64_t(m / kBigM) * (n / kBigN) >= HOLO_BIG_MIN_TILES) {
+#if HOLO_GEMM_DMA
+            hipLaunchKernelGGL(gemm_bf16_dma_kernel, dim3((m / kBigM) * (n / kBigN)), dim3(256), 0,
+                               stream, static_cast<const uint16_t *>(a),
+                               static_cast<const uint16_t *>(b), static_cast<uint16_t *>(c), m, n, k);
+#else
             hipLaunchKernelGGL(gemm_bf16_big_kernel, dim3((m / kBigM) * (n / kBigN)), dim3(256), 0,
                                stream, static_cast<const uint16_t *>(a),
                                static_cast<const uint16_t *>(b), static_cast<uint16_t *>(c), m, n, k);
+#endif
             return hipGetLastError();
         }
         const bool fast = (al & 15) == 0 && k % BK16 == 0 && n % 8 == 0;

@@ -286,11 +286,16 @@ constexpr int kBigM = 256, kBigN = 256, kBigK = 64, kLdk = kBigK + 8;
 #ifndef HOLO_BIG_MIN_TILES
 #define HOLO_BIG_MIN_TILES 128
 #endif
-// 1: large tiles run gemm_bf16_dma_kernel (LDS DMA, transposing B reads);
+// 1: large tiles run gemm_bf16_dma256/128_kernel (LDS DMA, transposing B reads);
 // 0: gemm_bf16_big_kernel (register staging, B transposed with permutes)
 #ifndef HOLO_GEMM_DMA
 #define HOLO_GEMM_DMA 1
 #endif
+// the DMA kernel takes 256x128 tiles below this many 256x256 tiles
+#ifndef HOLO_DMA_NARROW_BELOW
+#define HOLO_DMA_NARROW_BELOW 256
+#endif
+constexpr uint64_t kDmaNarrowBelow = HOLO_DMA_NARROW_BELOW;
 
 __device__ __forceinline__ void tile_coords(uint32_t wg, uint32_t nwg, uint32_t tiles_m,
                                             uint32_t tiles_n, uint32_t *tm, uint32_t *tn) {
@@ -506,8 +511,9 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_big_kernel(const uint16_t *_
 }
 
 // ------------------------------------------- bf16, large tiles, LDS DMA ----
-// The same 256x256 tile and wave layout as gemm_bf16_big_kernel, 32-deep K
-// slabs in kDmaStages LDS stages. Both operands go from global memory into
+// 256 x BN workgroup tiles (BN = 256, or 128 when 256-wide tiles would leave
+// CUs idle), four wavefronts of 128 x BN/2 on v_mfma_f32_32x32x16_bf16, 32-deep
+// K slabs in kDmaStages LDS stages. Both operands go from global memory into
 // LDS by DMA (buffer_load ... lds: lane l of a load writes the 16 bytes at
 // LDS base + 16 l) in their own layouts, A [m][k] and B [k][n], each 16-byte
 // chunk of a row at a swizzled place (chunk ^ f(row)) so fragment reads hit
@@ -517,18 +523,22 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_big_kernel(const uint16_t *_
 // and lane j receives rows k0 .. k0+3 of column n0 + j. No operand passes
 // through registers on its way to LDS. One barrier per slab, placed between
 // the slab's two k-steps so the MFMAs already issued cover it. The MFMA order
-// per output tile is the same as gemm_bf16_big_kernel's, so the results are
-// identical.
+// per output element is the same as gemm_bf16_big_kernel's (k ascending in
+// steps of 16), so the results are identical.
 constexpr int kDmaK = 32, kDmaStages = 4;
-constexpr uint32_t kDmaStage = 32768, kDmaB = 16384;   // bytes per stage; B after A
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
 __device__ __forceinline__ uint32_t swz_a(uint32_t row) { return ((row >> 1) ^ (row >> 2)) & 3u; }
+// B rows of BN/8 chunks: the 4-chunk group of a chunk is XORed with a
+// function of the k-row, so the eight k-rows one transposing read touches
+// (k0..k0+3, k0+8..k0+11) spread over the banks
+template <int BN>
 __device__ __forceinline__ uint32_t swz_b(uint32_t k) {
-    return 4u * ((k & 3u) | (((k >> 3) & 1u) << 2));
+    if constexpr (BN == 256) return 4u * ((k & 3u) | (((k >> 3) & 1u) << 2));
+    else return 4u * (k & 3u);
 }
 // s_waitcnt with vmcnt <= n and no wait on the other counters (gfx9 encoding)
 template <int n>
@@ -546,38 +556,45 @@ __device__ __forceinline__ void slab_barrier() {
     asm volatile("" ::: "memory");
 }
 
-__global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(const uint16_t *__restrict__ A,
-                                                              const uint16_t *__restrict__ B,
-                                                              uint16_t *__restrict__ C, uint32_t M,
-                                                              uint32_t N, uint32_t K) {
+template <int BN>
+__device__ __forceinline__ void gemm_bf16_dma(const uint16_t *__restrict__ A,
+                                              const uint16_t *__restrict__ B,
+                                              uint16_t *__restrict__ C, uint32_t M, uint32_t N,
+                                              uint32_t K) {
+    constexpr int NJ = BN / 64;                  // 32-column MFMA blocks per wave
+    constexpr uint32_t kBytesB = 64u * BN;       // one stage of B: 32 k-rows
+    constexpr uint32_t kStage = 16384u + kBytesB, kOffB = 16384u;
+    constexpr int kLoadsB = BN / 64;             // 1 KiB DMA loads of B per wave per slab
+    constexpr int kLoads = 4 + kLoadsB;          // ... of A and B
+    constexpr int kMfma = 4 * NJ, kReads = 4 + 2 * NJ;   // per k-step
     // one array per stage: the compiler then knows a DMA into one stage does
     // not feed reads of another, and waits only where a read needs the data
-    __shared__ __attribute__((aligned(1024))) uint8_t lds0[kDmaStage], lds1[kDmaStage],
-        lds2[kDmaStage], lds3[kDmaStage];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds0[kStage], lds1[kStage], lds2[kStage],
+        lds3[kStage];
     auto stage = [&](auto st) -> lds_u8 * {
         constexpr int kS = decltype(st)::value % kDmaStages;
         return kS == 0 ? (lds_u8 *)lds0 : kS == 1 ? (lds_u8 *)lds1 : kS == 2 ? (lds_u8 *)lds2 : (lds_u8 *)lds3;
     };
-    const uint32_t tiles_m = M / kBigM, tiles_n = N / kBigN;
+    const uint32_t tiles_m = M / kBigM, tiles_n = N / BN;
     uint32_t tm, tn;
     tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, &tm, &tn);
-    const uint32_t m0 = tm * kBigM, n0 = tn * kBigN;
+    const uint32_t m0 = tm * kBigM, n0 = tn * BN;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
+    const int wm = (wave >> 1) * 128, wn = (wave & 1) * (BN / 2);
     const int lr = lane & 31, lg = lane >> 5;
 
-    // DMA: load t (0..3) of a wave fills 1 KiB of a stage. A: rows
-    // 64 wave + 16 t + lane/4, physical chunk lane%4; B: k-rows
-    // 8 wave + 2 t + lane/32, physical chunk lane%32. Each lane fetches the
-    // logical chunk stored there.
+    // DMA: each load of a wave fills 1 KiB of a stage. A (4 per wave): rows
+    // 64 wave + 16 t + lane/4, physical chunk lane%4. B (BN/64 per wave):
+    // k-rows of BN/8 chunks, lane/(BN/8) of 512/BN rows per load, physical
+    // chunk lane%(BN/8). Each lane fetches the logical chunk stored there.
     const uint32_t arow = 64u * wave + lane / 4;
     const uint32_t a_voff = (arow * K + 8u * ((lane & 3) ^ swz_a(arow))) * 2u;
-    uint32_t b_voff[4];
+    uint32_t b_voff[kLoadsB];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const uint32_t k = 8u * wave + 2u * t + lane / 32;
-        b_voff[t] = (k * N + 8u * ((lane & 31) ^ swz_b(k))) * 2u;
+    for (int t = 0; t < kLoadsB; ++t) {
+        const uint32_t k = (kLoadsB * wave + t) * (512u / BN) + lane / (BN / 8);
+        b_voff[t] = (k * N + 8u * ((lane % (BN / 8)) ^ swz_b<BN>(k))) * 2u;
     }
     auto dma = [&](uint32_t slab, auto st) {
         const uint32_t k0 = slab * kDmaK;
@@ -586,12 +603,12 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(const uint16_t *_
         const auto rb = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint16_t *>(B + uint64_t(k0) * N + n0), 0, int(64u * N), 0x00020000);
         lds_u8 *sa = stage(st) + wave * 4096u;
-        lds_u8 *sb = sa + kDmaB;
+        lds_u8 *sb = stage(st) + kOffB + wave * (1024u * kLoadsB);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, sa + 1024 * t, 16, a_voff, 32u * K * t, 0, 0);
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < kLoadsB; ++t)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, sb + 1024 * t, 16, b_voff[t], 0, 0, 0);
     };
 
@@ -600,17 +617,17 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(const uint16_t *_
     // its 16-lane group addresses k-row 8(g/2) + r/4 (+ kk + 4h), column
     // wn + 32j + 16(g%2) + 4(r%4) (the swizzle is the same for every kk, h)
     const uint32_t a_frag = (wm + lr) * 64u + ((lg ^ swz_a(lr)) * 16u);
-    uint32_t b_frag[4];
+    uint32_t b_frag[NJ];
     {
         const uint32_t g = lane >> 4, r = lane & 15;
         const uint32_t k = 8u * (g >> 1) + (r >> 2);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NJ; ++j) {
             const uint32_t n = wn + 32u * j + 16u * (g & 1) + 4u * (r & 3);
-            b_frag[j] = kDmaB + k * 512u + (((n >> 3) ^ swz_b(k)) * 16u) + (n & 7u) * 2u;
+            b_frag[j] = kOffB + k * (2u * BN) + (((n >> 3) ^ swz_b<BN>(k)) * 16u) + (n & 7u) * 2u;
         }
     }
-    bf16x8 af[2][4], bfr[2][4];
+    bf16x8 af[2][4], bfr[2][NJ];
     auto fload = [&](auto st, int kk, int fb) {
         const lds_u8 *base = stage(st);
 #pragma unroll
@@ -618,39 +635,43 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(const uint16_t *_
             af[fb][i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8 *>(
                 base + ((a_frag + 2048u * i) ^ (kk == 16 ? 32u : 0u)));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const lds_u8 *p = base + b_frag[j] + 512u * kk;
+        for (int j = 0; j < NJ; ++j) {
+            const lds_u8 *p = base + b_frag[j] + (2u * BN) * kk;
             const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 reinterpret_cast<lds_v4i16 *>(const_cast<lds_u8 *>(p)));
             const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                reinterpret_cast<lds_v4i16 *>(const_cast<lds_u8 *>(p + 2048)));
+                reinterpret_cast<lds_v4i16 *>(const_cast<lds_u8 *>(p + 8u * BN)));
             bfr[fb][j] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         }
     };
 
-    f32x16 acc[4][4];
+    f32x16 acc[4][NJ];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
     auto mfmas = [&](int fb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < NJ; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[fb][i], bfr[fb][j], acc[i][j], 0, 0, 0);
     };
-    // 12 fragment reads, one after each of the first 12 MFMAs
-    auto mix_reads = [] {
+    // interleave into the k-step's MFMAs: after each, one DMA load (while
+    // any are left) and one fragment read (while any are left)
+    auto mix = [](auto loads) {
+        constexpr int kL = decltype(loads)::value;
 #pragma unroll
-        for (int i = 0; i < 12; ++i) {
+        for (int i = 0; i < kMfma; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            if (i < kL) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            if (i < kReads) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     };
+    using n0_ = std::integral_constant<int, 0>;
+    using nl_ = std::integral_constant<int, kLoads>;
 
     // One slab s in stage s % kDmaStages. kNext: slab s+1 exists (wait for its
     // DMA and pass the barrier mid-slab, then read its first fragments);
@@ -661,7 +682,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(const uint16_t *_
         constexpr int kWait = decltype(wait)::value, kS = decltype(st)::value;
         fload(st, 16, 1);
         mfmas(0);
-        mix_reads();
+        mix(n0_{});
         __builtin_amdgcn_sched_barrier(0);
         if (kNext) {
             wait_vm<kWait>();
@@ -671,34 +692,18 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(const uint16_t *_
         }
         mfmas(1);
         if (kNext) {
-            if (kLoad) {
-                // 12 fragment reads and 8 DMA loads over the 16 MFMAs
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                }
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                }
-                __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-            } else {
-                mix_reads();
-            }
+            if (kLoad) mix(nl_{});
+            else mix(n0_{});
         }
         __builtin_amdgcn_sched_barrier(0);
     };
     using yes = std::integral_constant<bool, true>;
     using no = std::integral_constant<bool, false>;
-    // DMA loads per slab per wave: 8. While slab s+1 is awaited, the slabs
-    // issued after it (up to s + kDmaStages - 2) may stay in flight.
-    using w_steady = std::integral_constant<int, 8 * (kDmaStages - 3)>;
+    // While slab s+1 is awaited, the slabs issued after it (up to
+    // s + kDmaStages - 2) may stay in flight.
+    using w_steady = std::integral_constant<int, kLoads * (kDmaStages - 3)>;
     using w_drain = std::integral_constant<int, 0>;
     static_assert(kDmaStages == 4, "the loop below is written for four stages");
-
     using s0 = std::integral_constant<int, 0>;
     using s1 = std::integral_constant<int, 1>;
     using s2 = std::integral_constant<int, 2>;
@@ -708,7 +713,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(const uint16_t *_
     dma(0, s0{});
     dma(1, s1{});
     dma(2, s2{});
-    wait_vm<16>();
+    wait_vm<2 * kLoads>();
     slab_barrier();
     fload(s0{}, 0, 0);
     // slab s uses stage s % 4; every slab but the last three issues the DMA
@@ -724,17 +729,31 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(const uint16_t *_
     slab(nk - 2, s2{}, yes{}, w_drain{}, no{});
     slab(nk - 1, s3{}, no{}, w_drain{}, no{});
 
+    // 32x32 D layout: acc[r] is row 8(r/4) + 4*lg + r%4, column lr
     uint16_t *cbase = C + uint64_t(m0 + wm + 4 * lg) * N + n0 + wn + lr;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NJ; ++j) {
             uint16_t *ct = cbase + uint64_t(32 * i) * N + 32 * j;
 #pragma unroll
             for (int r = 0; r < 16; ++r)
                 ct[uint64_t(8 * (r >> 2) + (r & 3)) * N] = uint16_t(__float_as_uint(acc[i][j][r]) >> 16);
             __builtin_amdgcn_sched_barrier(0);
         }
+}
+
+__global__ __launch_bounds__(256, 1) void gemm_bf16_dma256_kernel(const uint16_t *__restrict__ A,
+                                                                 const uint16_t *__restrict__ B,
+                                                                 uint16_t *__restrict__ C, uint32_t M,
+                                                                 uint32_t N, uint32_t K) {
+    gemm_bf16_dma<256>(A, B, C, M, N, K);
+}
+__global__ __launch_bounds__(256, 1) void gemm_bf16_dma128_kernel(const uint16_t *__restrict__ A,
+                                                                 const uint16_t *__restrict__ B,
+                                                                 uint16_t *__restrict__ C, uint32_t M,
+                                                                 uint32_t N, uint32_t K) {
+    gemm_bf16_dma<128>(A, B, C, M, N, K);
 }
 
 }  // namespace
@@ -783,9 +802,18 @@ hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint
             k >= 4 * kBigK && k < (1u << 22) && n < (1u << 24) &&
             uint64_t(m / kBigM) * (n / kBigN) >= HOLO_BIG_MIN_TILES) {
 #if HOLO_GEMM_DMA
-            hipLaunchKernelGGL(gemm_bf16_dma_kernel, dim3((m / kBigM) * (n / kBigN)), dim3(256), 0,
-                               stream, static_cast<const uint16_t *>(a),
-                               static_cast<const uint16_t *>(b), static_cast<uint16_t *>(c), m, n, k);
+            // 256x128 tiles when 256x256 ones would not give every CU a workgroup
+            const uint64_t tiles256 = uint64_t(m / kBigM) * (n / kBigN);
+            if (tiles256 < kDmaNarrowBelow)
+                hipLaunchKernelGGL(gemm_bf16_dma128_kernel, dim3(uint32_t(2 * tiles256)), dim3(256),
+                                   0, stream, static_cast<const uint16_t *>(a),
+                                   static_cast<const uint16_t *>(b), static_cast<uint16_t *>(c), m,
+                                   n, k);
+            else
+                hipLaunchKernelGGL(gemm_bf16_dma256_kernel, dim3(uint32_t(tiles256)), dim3(256), 0,
+                                   stream, static_cast<const uint16_t *>(a),
+                                   static_cast<const uint16_t *>(b), static_cast<uint16_t *>(c), m,
+                                   n, k);
 #else
             hipLaunchKernelGGL(gemm_bf16_big_kernel, dim3((m / kBigM) * (n / kBigN)), dim3(256), 0,
                                stream, static_cast<const uint16_t *>(a),

@@ -280,11 +280,12 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(const float *__restr
 // slab's global loads are issued before the current slab's MFMAs.
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kBigM = 256, kBigN = 256, kBigK = 64, kLdk = kBigK + 8;
-// 256x256 tiles are used when there are at least this many of them. Measured
-// at M = 4096, N = 2048 (128 tiles, half the CUs): 68 us (K = 2048) and 229 us
-// (K = 8192) against 73 and 272 us for the 128x128 kernel on every CU.
+// The large-tile kernels are used from this many 256x256 tiles up. Measured
+// with the DMA kernel's 256x128 tiles against the 128x128 / 64x64 kernel:
+// 4096x2048x512 (32 tiles) 26.2 vs 34.4 us, 2048^3 (64 tiles) 28.1 vs 46.8 us;
+// at 16 tiles it no longer pays (2048x8192x512: 89.0 vs 83.9 us).
 #ifndef HOLO_BIG_MIN_TILES
-#define HOLO_BIG_MIN_TILES 128
+#define HOLO_BIG_MIN_TILES 32
 #endif
 // 1: large tiles run gemm_bf16_dma256/128_kernel (LDS DMA, transposing B reads);
 // 0: gemm_bf16_big_kernel (register staging, B transposed with permutes)
@@ -556,11 +557,21 @@ __device__ __forceinline__ void slab_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// A launch over up to kSkinnyMaxSeg products sharing A [M, K]: segment s has
+// B_s [K, n_s] and C_s [M, n_s]; the tile columns of every segment are laid
+// end to end (tiles_end: running totals of BN-wide columns) and each
+// workgroup's tile belongs to one segment.
+struct DmaGroup {
+    const uint16_t *a;
+    uint32_t m, k, nseg;
+    uint32_t tiles_end[kSkinnyMaxSeg];
+    const uint16_t *b[kSkinnyMaxSeg];
+    uint16_t *c[kSkinnyMaxSeg];
+    uint32_t n[kSkinnyMaxSeg];
+};
+
 template <int BN>
-__device__ __forceinline__ void gemm_bf16_dma(const uint16_t *__restrict__ A,
-                                              const uint16_t *__restrict__ B,
-                                              uint16_t *__restrict__ C, uint32_t M, uint32_t N,
-                                              uint32_t K) {
+__device__ __forceinline__ void gemm_bf16_dma(const DmaGroup &g) {
     constexpr int NJ = BN / 64;                  // 32-column MFMA blocks per wave
     constexpr uint32_t kBytesB = 64u * BN;       // one stage of B: 32 k-rows
     constexpr uint32_t kStage = 16384u + kBytesB, kOffB = 16384u;
@@ -575,10 +586,24 @@ __device__ __forceinline__ void gemm_bf16_dma(const uint16_t *__restrict__ A,
         constexpr int kS = decltype(st)::value % kDmaStages;
         return kS == 0 ? (lds_u8 *)lds0 : kS == 1 ? (lds_u8 *)lds1 : kS == 2 ? (lds_u8 *)lds2 : (lds_u8 *)lds3;
     };
-    const uint32_t tiles_m = M / kBigM, tiles_n = N / BN;
+    const uint16_t *__restrict__ A = g.a;
+    const uint32_t M = g.m, K = g.k;
+    const uint32_t tiles_m = M / kBigM, tiles_n = g.tiles_end[g.nseg - 1];
     uint32_t tm, tn;
     tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, &tm, &tn);
-    const uint32_t m0 = tm * kBigM, n0 = tn * BN;
+    // this tile's segment (workgroup-uniform, chosen with selects)
+    const uint16_t *__restrict__ B = g.b[0];
+    uint16_t *__restrict__ C = g.c[0];
+    uint32_t N = g.n[0], first = 0;
+#pragma unroll
+    for (int i = 1; i < kSkinnyMaxSeg; ++i)
+        if (uint32_t(i) < g.nseg && tn >= g.tiles_end[i - 1]) {
+            B = g.b[i];
+            C = g.c[i];
+            N = g.n[i];
+            first = g.tiles_end[i - 1];
+        }
+    const uint32_t m0 = tm * kBigM, n0 = (tn - first) * BN;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wm = (wave >> 1) * 128, wn = (wave & 1) * (BN / 2);
@@ -743,17 +768,39 @@ __device__ __forceinline__ void gemm_bf16_dma(const uint16_t *__restrict__ A,
         }
 }
 
-__global__ __launch_bounds__(256, 1) void gemm_bf16_dma256_kernel(const uint16_t *__restrict__ A,
-                                                                 const uint16_t *__restrict__ B,
-                                                                 uint16_t *__restrict__ C, uint32_t M,
-                                                                 uint32_t N, uint32_t K) {
-    gemm_bf16_dma<256>(A, B, C, M, N, K);
+__global__ __launch_bounds__(256, 1) void gemm_bf16_dma256_kernel(const DmaGroup g) {
+    gemm_bf16_dma<256>(g);
 }
-__global__ __launch_bounds__(256, 1) void gemm_bf16_dma128_kernel(const uint16_t *__restrict__ A,
-                                                                 const uint16_t *__restrict__ B,
-                                                                 uint16_t *__restrict__ C, uint32_t M,
-                                                                 uint32_t N, uint32_t K) {
-    gemm_bf16_dma<128>(A, B, C, M, N, K);
+__global__ __launch_bounds__(256, 1) void gemm_bf16_dma128_kernel(const DmaGroup g) {
+    gemm_bf16_dma<128>(g);
+}
+
+// Whether the DMA kernel takes a product (bf16, 16-byte aligned operands
+// checked by the caller): K a multiple of 128 and >= 256, at least
+// HOLO_BIG_MIN_TILES 256x256 tiles, and 256 rows of A / 32 rows of B within
+// a 32-bit buffer range.
+bool dma_applies(uint32_t m, uint32_t k, uint32_t n) {
+    return m % kBigM == 0 && n % kBigN == 0 && k % (2 * kBigK) == 0 && k >= 4 * kBigK &&
+           k < (1u << 22) && n < (1u << 24) &&
+           uint64_t(m / kBigM) * (n / kBigN) >= HOLO_BIG_MIN_TILES;
+}
+
+hipError_t launch_dma(DmaGroup g, hipStream_t stream) {
+    uint32_t wide = 0;
+    for (uint32_t i = 0; i < g.nseg; ++i) wide += g.n[i] / kBigN;
+    // 256x128 tiles when 256x256 ones would not give every CU a workgroup
+    const bool narrow = uint64_t(g.m / kBigM) * wide < kDmaNarrowBelow;
+    uint32_t cols = 0;
+    for (uint32_t i = 0; i < g.nseg; ++i) {
+        cols += g.n[i] / (narrow ? 128u : 256u);
+        g.tiles_end[i] = cols;
+    }
+    const dim3 grid{(g.m / kBigM) * cols}, block{256u};
+    if (narrow)
+        hipLaunchKernelGGL(gemm_bf16_dma128_kernel, grid, block, 0, stream, g);
+    else
+        hipLaunchKernelGGL(gemm_bf16_dma256_kernel, grid, block, 0, stream, g);
+    return hipGetLastError();
 }
 
 }  // namespace
@@ -795,25 +842,20 @@ hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint
         }                                                                                        \
     } while (0)
     if (dtype == 7) {
-        // large aligned problems: 256x256 tiles, at least HOLO_BIG_MIN_TILES of them, an
-        // even number (>= 4) of 64-deep slabs, and 256 rows of A / 64 rows of
-        // B within a 32-bit buffer range
-        if ((al & 15) == 0 && m % kBigM == 0 && n % kBigN == 0 && k % (2 * kBigK) == 0 &&
-            k >= 4 * kBigK && k < (1u << 22) && n < (1u << 24) &&
-            uint64_t(m / kBigM) * (n / kBigN) >= HOLO_BIG_MIN_TILES) {
+        // large aligned problems: at least HOLO_BIG_MIN_TILES 256x256 tiles, K a
+        // multiple of 128 and >= 256, and 256 rows of A / 64 rows of B within a
+        // 32-bit buffer range
+        if ((al & 15) == 0 && dma_applies(m, k, n)) {
 #if HOLO_GEMM_DMA
-            // 256x128 tiles when 256x256 ones would not give every CU a workgroup
-            const uint64_t tiles256 = uint64_t(m / kBigM) * (n / kBigN);
-            if (tiles256 < kDmaNarrowBelow)
-                hipLaunchKernelGGL(gemm_bf16_dma128_kernel, dim3(uint32_t(2 * tiles256)), dim3(256),
-                                   0, stream, static_cast<const uint16_t *>(a),
-                                   static_cast<const uint16_t *>(b), static_cast<uint16_t *>(c), m,
-                                   n, k);
-            else
-                hipLaunchKernelGGL(gemm_bf16_dma256_kernel, dim3(uint32_t(tiles256)), dim3(256), 0,
-                                   stream, static_cast<const uint16_t *>(a),
-                                   static_cast<const uint16_t *>(b), static_cast<uint16_t *>(c), m,
-                                   n, k);
+            DmaGroup g{};
+            g.a = static_cast<const uint16_t *>(a);
+            g.m = m;
+            g.k = k;
+            g.nseg = 1;
+            g.b[0] = static_cast<const uint16_t *>(b);
+            g.c[0] = static_cast<uint16_t *>(c);
+            g.n[0] = n;
+            return launch_dma(g, stream);
 #else
             hipLaunchKernelGGL(gemm_bf16_big_kernel, dim3((m / kBigM) * (n / kBigN)), dim3(256), 0,
                                stream, static_cast<const uint16_t *>(a),
@@ -831,6 +873,36 @@ hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint
     }
 #undef HOLO_GEMM_LAUNCH
     return hipGetLastError();
+}
+
+bool matmul_group_tiled_applies(uint32_t m, uint32_t k, const uint32_t *n, int nseg) {
+    if (!HOLO_GEMM_DMA || nseg < 1 || nseg > kSkinnyMaxSeg) return false;
+    for (int i = 0; i < nseg; ++i)
+        if (!dma_applies(m, k, n[i])) return false;
+    return true;
+}
+
+hipError_t launch_matmul_group_tiled(const void *a, uint32_t m, uint32_t k,
+                                     const SkinnySegment *segs, void *const *c, int nseg,
+                                     hipStream_t stream) {
+    uint32_t n[kSkinnyMaxSeg] = {};
+    uintptr_t al = reinterpret_cast<uintptr_t>(a);
+    for (int i = 0; i < nseg && i < kSkinnyMaxSeg; ++i) {
+        n[i] = segs[i].n;
+        al |= reinterpret_cast<uintptr_t>(segs[i].b) | reinterpret_cast<uintptr_t>(c[i]);
+    }
+    if ((al & 15) != 0 || !matmul_group_tiled_applies(m, k, n, nseg)) return hipErrorInvalidValue;
+    DmaGroup g{};
+    g.a = static_cast<const uint16_t *>(a);
+    g.m = m;
+    g.k = k;
+    g.nseg = uint32_t(nseg);
+    for (int i = 0; i < nseg; ++i) {
+        g.b[i] = static_cast<const uint16_t *>(segs[i].b);
+        g.c[i] = static_cast<uint16_t *>(c[i]);
+        g.n[i] = n[i];
+    }
+    return launch_dma(g, stream);
 }
 
 }  // namespace holo

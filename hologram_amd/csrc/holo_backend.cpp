@@ -388,6 +388,37 @@ int dispatch_group_impl(holo_backend *be, const SlotTable &st, const holo::Group
     if (!fast && (a_norm || stats))
         return fail(HOLO_ERR_DISPATCH, std::string(op) + ": a fused RmsNorm needs the few-row path "
                                                          "(16-byte aligned operands)");
+    if (!fast && nseg > 1 && bf16) {
+        // large M: one launch of the tiled kernel for every product, then
+        // each segment's element-wise epilogue in place
+        bool plain = true;
+        uint32_t ns[holo::kSkinnyMaxSeg];
+        void *cs[holo::kSkinnyMaxSeg];
+        for (size_t i = 0; i < nseg; ++i) {
+            const holo::GroupSegDesc &s = g.segs[i];
+            plain = plain && s.write_out && !s.head_dim && !s.rope && !s.quant && s.pair < 0 &&
+                    !s.skip && !s.ssq;
+            ns[i] = s.n;
+            cs[i] = e.seg[i].out;
+        }
+        if (plain && holo::matmul_group_tiled_applies(g.m, g.k, ns, int(nseg))) {
+            HOLO_TRY(launched(holo::launch_matmul_group_tiled(a.base, g.m, g.k, ss, cs, int(nseg),
+                                                              be->stream),
+                              op));
+            for (size_t i = 0; i < nseg; ++i) {
+                if (g.segs[i].base == holo::kEpiStore) continue;
+                holo::TileEpi te;
+                te.kind = g.segs[i].base;
+                te.act = g.segs[i].act;
+                te.lut = e.seg[i].lut;
+                te.residual = e.seg[i].residual;
+                HOLO_TRY(launched(holo::launch_tile_epilogue(cs[i], uint64_t(g.m) * ns[i], bf16, te,
+                                                             be->stream),
+                                  op));
+            }
+            return HOLO_OK;
+        }
+    }
     if (!fast) {
         const holo::GroupSegDesc &s = g.segs[0];
         const bool elementwise = nseg == 1 && s.write_out && !s.head_dim && s.pair < 0;

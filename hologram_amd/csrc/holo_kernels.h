@@ -161,6 +161,14 @@ struct SkinnyNormA {
     const uint16_t *gamma = nullptr;   // [k], 16-byte aligned
     float eps = 0.0f;
 };
+// Large-M bf16 products sharing A [m, k] (segment s: B_s [k, n_s] into c[s]),
+// one launch of the tiled DMA kernel. Applies when each product alone would
+// take that kernel (launch_matmul), so each result is bit for bit the single
+// call's. Operands 16-byte aligned.
+bool matmul_group_tiled_applies(uint32_t m, uint32_t k, const uint32_t *n, int nseg);
+hipError_t launch_matmul_group_tiled(const void *a, uint32_t m, uint32_t k,
+                                     const SkinnySegment *segs, void *const *c, int nseg,
+                                     hipStream_t stream);
 hipError_t launch_skinny_partials(const void *a, uint32_t m, uint32_t k, uint8_t dtype,
                                   const SkinnySegment *segs, int nseg, const SkinnyPlan &plan,
                                   float *P, hipStream_t stream, const SkinnyNormA *norm = nullptr);

@@ -458,9 +458,19 @@ void device_fusion(holo_session *s, const std::vector<uint8_t> &is_output,
         }
         return npos;
     };
+    // few-row products (the split-K kernel), or large-M bf16 products the
+    // tiled DMA kernel takes on their own (grouped, each result keeps the
+    // single call's bits)
+    auto tiled = [&](const MmView &m) {
+        const uint32_t n = m.mm.n;
+        return m.mm.dtype == HOLO_DTYPE_BF16 && m.mm.output.offset % 16 == 0 &&
+               m.mm.output.slot < is_input.size() && !is_input[m.mm.output.slot] &&
+               holo::matmul_group_tiled_applies(m.mm.m, m.mm.k, &n, 1);
+    };
     auto groupable = [&](const MmView &m) {
         if (m.mm.dtype != HOLO_DTYPE_BF16 && m.mm.dtype != HOLO_DTYPE_F32) return false;
-        if (m.mm.b_packed || holo::matmul_skinny_plan(m.mm.m, m.mm.k, m.mm.n, m.mm.dtype).mt == 0)
+        if (m.mm.b_packed) return false;
+        if (holo::matmul_skinny_plan(m.mm.m, m.mm.k, m.mm.n, m.mm.dtype).mt == 0 && !tiled(m))
             return false;
         if ((m.mm.a.offset | m.mm.b.offset) % 16 != 0) return false;
         if (m.mm.a.slot >= is_input.size() || m.mm.b.slot >= is_input.size()) return false;
@@ -503,6 +513,7 @@ void device_fusion(holo_session *s, const std::vector<uint8_t> &is_output,
                 continue;
             const holo::SkinnyPlan pj = holo::matmul_skinny_plan(mj.mm.m, mj.mm.k, mj.mm.n, mj.mm.dtype);
             if (pj.mt != pl.mt || pj.steps != pl.steps || pj.ks != pl.ks || !movable(q, p)) continue;
+            if (pl.mt == 0 && !tiled(mj)) continue;
             g.segs.push_back(seg_of(mj));
             if (!segments_disjoint(g.segs, g.a)) {
                 g.segs.pop_back();
@@ -511,9 +522,10 @@ void device_fusion(holo_session *s, const std::vector<uint8_t> &is_output,
             members.push_back(j);
             taken[j] = true;
         }
-        // pull each product's sole consumer into the epilogue
+        // pull each product's sole consumer into the epilogue (few-row
+        // groups: the tiled kernel writes plain products)
         std::vector<holo_buffer_ref> value(g.segs.size());
-        std::vector<bool> done(g.segs.size(), false);
+        std::vector<bool> done(g.segs.size(), pl.mt == 0);
         for (size_t t = 0; t < g.segs.size(); ++t) value[t] = g.segs[t].out;
         for (size_t t = 0; t < g.segs.size(); ++t) {
             while (!done[t]) {

@@ -98,10 +98,11 @@ def run_mm_rows(torch, backend, m, k, n, seed, rows):
 
 @pytest.mark.parametrize("m,k,n", [(4096, 256, 4096), (4096, 384, 4096), (4096, 320, 4096),
                                    (8192, 8192, 8192), (2048, 1024, 8192), (4096, 2048, 2048),
-                                   (4096, 8192, 2048)])
+                                   (4096, 8192, 2048), (4096, 2048, 512), (2048, 2048, 2048)])
 def test_matmul_large_tiles_sampled_rows(torch_cuda, backend, m, k, n):
-    """The 256x256-tile path: every 256-row tile and every row residue mod 32
-    appears among the sampled rows."""
+    """The large-tile paths (256x256 tiles from 256 of them up, 256x128 tiles
+    from 32): every 256-row tile and every row residue mod 32 appears among
+    the sampled rows, and every column is checked."""
     rows = sorted({(t * 256 + (t * 37) % 256) % m for t in range(m // 256)} | set(range(0, 64)))
     got, want = run_mm_rows(torch_cuda, backend, m, k, n, seed=m + n + k, rows=rows)
     err = oracle.max_rel_err(got, want)

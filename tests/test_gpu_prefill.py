@@ -22,6 +22,7 @@ from hologram_amd import (DTYPE_BF16, DTYPE_F32, AttentionI8RowsCall, BufferRef,
                           TransposeCall)
 from hologram_amd.decoder_graph import (DecoderConfig, build_decode_step, build_prefill,
                                         init_weights, rope_tables, rope_tables_rows)
+from hologram_amd.session import NO_DEVICE_FUSION
 from oracle.graph import OracleSession
 
 pytestmark = pytest.mark.gpu
@@ -215,3 +216,30 @@ def test_prefill_then_decode_tracks_decode_only(torch_cuda, backend):
         assert ok, (s, errs)
     for x in (ref, pre, dec):
         x.close()
+
+
+def test_prefill_grouped_products_are_bit_identical(torch_cuda, backend):
+    """At prompt-pass sizes (4096 rows, hidden 2048) q/k/v and gate/up run as
+    one launch each of the tiled kernel (one segment table per group); every
+    output (next tokens, logits, int8 caches and scales) matches the walk
+    without grouping bit for bit."""
+    cfg = DecoderConfig(layers=1, hidden=2048, heads=32, kv_heads=8, head_dim=64, ffn=8192,
+                        vocab=1024, batch=8, bucket=1024)
+    T = 512
+    archive = build_prefill(cfg, init_weights(cfg, seed=41), T)
+    prompt = np.random.default_rng(42).integers(0, cfg.vocab, (cfg.batch, T))
+    outs = {}
+    for flags in (0, NO_DEVICE_FUSION):
+        sess = HipSession(backend, archive, flags=flags)
+        if flags == 0:
+            assert sess.n_groups == 2 and sess.n_nodes == sess.n_calls - 3
+        zero_caches(sess.write_input, cfg)
+        for i, b in enumerate(prefill_inputs(cfg, T, prompt)):
+            sess.write_input(i, b)
+        sess.run()
+        sess.synchronize()
+        outs[flags] = [sess.read_output(o) for o in range(len(sess.outputs))]
+        sess.close()
+    for o, (u, v) in enumerate(zip(outs[0], outs[NO_DEVICE_FUSION])):
+        assert u == v, f"output {o} differs"
+

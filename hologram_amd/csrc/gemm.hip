@@ -561,6 +561,12 @@ __device__ __forceinline__ void slab_barrier() {
 // B_s [K, n_s] and C_s [M, n_s]; the tile columns of every segment are laid
 // end to end (tiles_end: running totals of BN-wide columns) and each
 // workgroup's tile belongs to one segment.
+// Pair form (one segment): b[0] and b[1] are two products' B of the same
+// shape [K, n[0]] (SwiGLU's gate and up); the workgroup tile is 256 rows x
+// 128 columns of both, and c[0] receives f(gate) * g(up) per element, each
+// product narrowed to bf16 and passed through its activation table lut[0] /
+// lut[1] when given, the product narrowed again (the standalone kernels'
+// arithmetic).
 struct DmaGroup {
     const uint16_t *a;
     uint32_t m, k, nseg;
@@ -568,11 +574,14 @@ struct DmaGroup {
     const uint16_t *b[kSkinnyMaxSeg];
     uint16_t *c[kSkinnyMaxSeg];
     uint32_t n[kSkinnyMaxSeg];
+    const uint16_t *lut[2];
 };
 
-template <int BN>
+template <int BN, bool kPair = false>
 __device__ __forceinline__ void gemm_bf16_dma(const DmaGroup &g) {
+    static_assert(!kPair || BN == 256, "the pair form fills a 256-wide tile from two B tiles");
     constexpr int NJ = BN / 64;                  // 32-column MFMA blocks per wave
+    constexpr int BW = kPair ? 128 : BN;         // columns of one B matrix in the tile
     constexpr uint32_t kBytesB = 64u * BN;       // one stage of B: 32 k-rows
     constexpr uint32_t kStage = 16384u + kBytesB, kOffB = 16384u;
     constexpr int kLoadsB = BN / 64;             // 1 KiB DMA loads of B per wave per slab
@@ -603,10 +612,12 @@ __device__ __forceinline__ void gemm_bf16_dma(const DmaGroup &g) {
             N = g.n[i];
             first = g.tiles_end[i - 1];
         }
-    const uint32_t m0 = tm * kBigM, n0 = (tn - first) * BN;
+    const uint32_t m0 = tm * kBigM, n0 = (tn - first) * BW;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int wm = (wave >> 1) * 128, wn = (wave & 1) * (BN / 2);
+    // wave tile: 128 rows x BN/2 columns; in the pair form its columns are
+    // 64 of gate and the same 64 of up
+    const int wm = (wave >> 1) * 128, wn = (wave & 1) * (BW / 2);
     const int lr = lane & 31, lg = lane >> 5;
 
     // DMA: each load of a wave fills 1 KiB of a stage. A (4 per wave): rows
@@ -615,26 +626,33 @@ __device__ __forceinline__ void gemm_bf16_dma(const DmaGroup &g) {
     // chunk lane%(BN/8). Each lane fetches the logical chunk stored there.
     const uint32_t arow = 64u * wave + lane / 4;
     const uint32_t a_voff = (arow * K + 8u * ((lane & 3) ^ swz_a(arow))) * 2u;
-    uint32_t b_voff[kLoadsB];
+    // (pair form: each of the two B matrices as a BW-wide tile, kLoadsB / 2
+    // loads each, gate's tile first)
+    constexpr int kLoadsM = kPair ? kLoadsB / 2 : kLoadsB;   // loads per B matrix
+    uint32_t b_voff[kLoadsM];
 #pragma unroll
-    for (int t = 0; t < kLoadsB; ++t) {
-        const uint32_t k = (kLoadsB * wave + t) * (512u / BN) + lane / (BN / 8);
-        b_voff[t] = (k * N + 8u * ((lane % (BN / 8)) ^ swz_b<BN>(k))) * 2u;
+    for (int t = 0; t < kLoadsM; ++t) {
+        const uint32_t k = (kLoadsM * wave + t) * (512u / BW) + lane / (BW / 8);
+        b_voff[t] = (k * N + 8u * ((lane % (BW / 8)) ^ swz_b<BW>(k))) * 2u;
     }
     auto dma = [&](uint32_t slab, auto st) {
         const uint32_t k0 = slab * kDmaK;
         const auto ra = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint16_t *>(A + uint64_t(m0) * K + k0), 0, int(512u * K), 0x00020000);
-        const auto rb = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint16_t *>(B + uint64_t(k0) * N + n0), 0, int(64u * N), 0x00020000);
         lds_u8 *sa = stage(st) + wave * 4096u;
-        lds_u8 *sb = stage(st) + kOffB + wave * (1024u * kLoadsB);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, sa + 1024 * t, 16, a_voff, 32u * K * t, 0, 0);
 #pragma unroll
-        for (int t = 0; t < kLoadsB; ++t)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, sb + 1024 * t, 16, b_voff[t], 0, 0, 0);
+        for (int mi = 0; mi < (kPair ? 2 : 1); ++mi) {
+            const uint16_t *Bm = kPair && mi == 1 ? g.b[1] : B;
+            const auto rb = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint16_t *>(Bm + uint64_t(k0) * N + n0), 0, int(64u * N), 0x00020000);
+            lds_u8 *sb = stage(st) + kOffB + mi * (64u * BW) + wave * (1024u * kLoadsM);
+#pragma unroll
+            for (int t = 0; t < kLoadsM; ++t)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, sb + 1024 * t, 16, b_voff[t], 0, 0, 0);
+        }
     };
 
     // fragment offsets within a stage. A: row wm + 32i + lr, logical chunk
@@ -648,8 +666,10 @@ __device__ __forceinline__ void gemm_bf16_dma(const DmaGroup &g) {
         const uint32_t k = 8u * (g >> 1) + (r >> 2);
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-            const uint32_t n = wn + 32u * j + 16u * (g & 1) + 4u * (r & 3);
-            b_frag[j] = kOffB + k * (2u * BN) + (((n >> 3) ^ swz_b<BN>(k)) * 16u) + (n & 7u) * 2u;
+            const int mi = kPair ? j / 2 : 0, jj = kPair ? j % 2 : j;
+            const uint32_t n = wn + 32u * jj + 16u * (g & 1) + 4u * (r & 3);
+            b_frag[j] = kOffB + mi * (64u * BW) + k * (2u * BW) +
+                        (((n >> 3) ^ swz_b<BW>(k)) * 16u) + (n & 7u) * 2u;
         }
     }
     bf16x8 af[2][4], bfr[2][NJ];
@@ -661,11 +681,11 @@ __device__ __forceinline__ void gemm_bf16_dma(const DmaGroup &g) {
                 base + ((a_frag + 2048u * i) ^ (kk == 16 ? 32u : 0u)));
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-            const lds_u8 *p = base + b_frag[j] + (2u * BN) * kk;
+            const lds_u8 *p = base + b_frag[j] + (2u * BW) * kk;
             const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 reinterpret_cast<lds_v4i16 *>(const_cast<lds_u8 *>(p)));
             const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                reinterpret_cast<lds_v4i16 *>(const_cast<lds_u8 *>(p + 8u * BN)));
+                reinterpret_cast<lds_v4i16 *>(const_cast<lds_u8 *>(p + 8u * BW)));
             bfr[fb][j] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         }
     };
@@ -756,16 +776,38 @@ __device__ __forceinline__ void gemm_bf16_dma(const DmaGroup &g) {
 
     // 32x32 D layout: acc[r] is row 8(r/4) + 4*lg + r%4, column lr
     uint16_t *cbase = C + uint64_t(m0 + wm + 4 * lg) * N + n0 + wn + lr;
+    if constexpr (kPair) {
+        // acc[i][jj] is gate and acc[i][jj + 2] up at the same element
+        const uint16_t *lg_ = g.lut[0], *lu_ = g.lut[1];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            uint16_t *ct = cbase + uint64_t(32 * i) * N + 32 * j;
+            for (int jj = 0; jj < 2; ++jj) {
+                uint16_t *ct = cbase + uint64_t(32 * i) * N + 32 * jj;
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                ct[uint64_t(8 * (r >> 2) + (r & 3)) * N] = uint16_t(__float_as_uint(acc[i][j][r]) >> 16);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+                for (int r = 0; r < 16; ++r) {
+                    uint32_t x = __float_as_uint(acc[i][jj][r]) >> 16;
+                    uint32_t y = __float_as_uint(acc[i][jj + 2][r]) >> 16;
+                    if (lg_) x = lg_[x];
+                    if (lu_) y = lu_[y];
+                    const float v = __uint_as_float(x << 16) * __uint_as_float(y << 16);
+                    ct[uint64_t(8 * (r >> 2) + (r & 3)) * N] = uint16_t(__float_as_uint(v) >> 16);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                uint16_t *ct = cbase + uint64_t(32 * i) * N + 32 * j;
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    ct[uint64_t(8 * (r >> 2) + (r & 3)) * N] =
+                        uint16_t(__float_as_uint(acc[i][j][r]) >> 16);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+    }
 }
 
 __global__ __launch_bounds__(256, 1) void gemm_bf16_dma256_kernel(const DmaGroup g) {
@@ -773,6 +815,9 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma256_kernel(const DmaGroup
 }
 __global__ __launch_bounds__(256, 1) void gemm_bf16_dma128_kernel(const DmaGroup g) {
     gemm_bf16_dma<128>(g);
+}
+__global__ __launch_bounds__(256, 1) void gemm_bf16_dma_pair_kernel(const DmaGroup g) {
+    gemm_bf16_dma<256, true>(g);
 }
 
 // Whether the DMA kernel takes a product (bf16, 16-byte aligned operands
@@ -872,6 +917,30 @@ hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint
         return hipErrorInvalidValue;
     }
 #undef HOLO_GEMM_LAUNCH
+    return hipGetLastError();
+}
+
+hipError_t launch_matmul_pair_tiled(const void *a, uint32_t m, uint32_t k, const void *b_gate,
+                                    const void *b_up, uint32_t n, void *out,
+                                    const uint16_t *lut_gate, const uint16_t *lut_up,
+                                    hipStream_t stream) {
+    const uintptr_t al = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b_gate) |
+                         reinterpret_cast<uintptr_t>(b_up) | reinterpret_cast<uintptr_t>(out);
+    if ((al & 15) != 0 || !matmul_group_tiled_applies(m, k, &n, 1)) return hipErrorInvalidValue;
+    DmaGroup g{};
+    g.a = static_cast<const uint16_t *>(a);
+    g.m = m;
+    g.k = k;
+    g.nseg = 1;
+    g.b[0] = static_cast<const uint16_t *>(b_gate);
+    g.b[1] = static_cast<const uint16_t *>(b_up);
+    g.c[0] = static_cast<uint16_t *>(out);
+    g.n[0] = n;
+    g.tiles_end[0] = n / 128;
+    g.lut[0] = lut_gate;
+    g.lut[1] = lut_up;
+    const dim3 grid{(m / kBigM) * (n / 128)}, block{256u};
+    hipLaunchKernelGGL(gemm_bf16_dma_pair_kernel, grid, block, 0, stream, g);
     return hipGetLastError();
 }
 

@@ -388,6 +388,24 @@ int dispatch_group_impl(holo_backend *be, const SlotTable &st, const holo::Group
     if (!fast && (a_norm || stats))
         return fail(HOLO_ERR_DISPATCH, std::string(op) + ": a fused RmsNorm needs the few-row path "
                                                          "(16-byte aligned operands)");
+    if (!fast && nseg == 2 && bf16 && (g.segs[0].pair == 1 || g.segs[1].pair == 0)) {
+        // large M, SwiGLU pair: both products and f(gate) * g(up) in one
+        // launch of the tiled kernel
+        const size_t gi = g.segs[0].pair == 1 ? 0 : 1, ui = 1 - gi;
+        const holo::GroupSegDesc &sg = g.segs[gi], &su = g.segs[ui];
+        auto table = [](const holo::GroupSegDesc &d) {
+            return d.base == holo::kEpiStore || d.base == holo::kEpiAct;
+        };
+        if (!table(sg) || !table(su) || sg.write_out || su.write_out || sg.head_dim || su.head_dim ||
+            sg.ssq || su.ssq || !su.skip)
+            return fail(HOLO_ERR_DISPATCH, std::string(op) + ": a tiled pair needs plain or "
+                                                             "table-activated products");
+        return launched(holo::launch_matmul_pair_tiled(
+                            a.base, g.m, g.k, ss[gi].b, ss[ui].b, sg.n, e.seg[gi].mul_out,
+                            sg.base == holo::kEpiAct ? e.seg[gi].lut : nullptr,
+                            su.base == holo::kEpiAct ? e.seg[ui].lut : nullptr, be->stream),
+                        op);
+    }
     if (!fast && nseg > 1 && bf16) {
         // large M: one launch of the tiled kernel for every product, then
         // each segment's element-wise epilogue in place

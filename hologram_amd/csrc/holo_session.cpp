@@ -522,10 +522,12 @@ void device_fusion(holo_session *s, const std::vector<uint8_t> &is_output,
             members.push_back(j);
             taken[j] = true;
         }
-        // pull each product's sole consumer into the epilogue (few-row
-        // groups: the tiled kernel writes plain products)
+        // pull each product's sole consumer into the epilogue (tiled groups:
+        // only the SwiGLU product of a group of exactly two, whose bases are
+        // the plain product or a table activation)
+        const bool tiled_group = pl.mt == 0;
         std::vector<holo_buffer_ref> value(g.segs.size());
-        std::vector<bool> done(g.segs.size(), pl.mt == 0);
+        std::vector<bool> done(g.segs.size(), tiled_group && g.segs.size() != 2);
         for (size_t t = 0; t < g.segs.size(); ++t) value[t] = g.segs[t].out;
         for (size_t t = 0; t < g.segs.size(); ++t) {
             while (!done[t]) {
@@ -539,6 +541,7 @@ void device_fusion(holo_session *s, const std::vector<uint8_t> &is_output,
                 std::vector<holo::GroupSegDesc> segs2 = g.segs;
                 bool ok = false, last = false;
                 int partner = -1;
+                if (tiled_group && cc.tag != HOLO_OP_MUL) break;
                 if (cc.tag == HOLO_OP_ROTARY && free_seg && !trial.rope) {
                     const auto &r = cc.u.rope;
                     if (same_ref(r.x, value[t]) && r.dtype == g.dtype && pow2_head(r.head_dim) &&
@@ -583,6 +586,13 @@ void device_fusion(holo_session *s, const std::vector<uint8_t> &is_output,
                         partner = int(u);
                         break;
                     }
+                    auto table_base = [](const holo::GroupSegDesc &d) {
+                        return d.base == holo::kEpiStore || d.base == holo::kEpiAct;
+                    };
+                    if (tiled_group && partner >= 0 &&
+                        !(table_base(trial) && table_base(g.segs[size_t(partner)]) &&
+                          b.output.offset % 16 == 0))
+                        partner = -1;
                     if (partner >= 0 && b.dtype == g.dtype && b.element_count == mn) {
                         trial.pair = partner;
                         trial.mul_out = b.output;

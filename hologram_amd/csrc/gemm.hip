@@ -292,11 +292,12 @@ constexpr int kBigM = 256, kBigN = 256, kBigK = 64, kLdk = kBigK + 8;
 #ifndef HOLO_GEMM_DMA
 #define HOLO_GEMM_DMA 1
 #endif
-// the DMA kernel takes 256x128 tiles below this many 256x256 tiles
-#ifndef HOLO_DMA_NARROW_BELOW
-#define HOLO_DMA_NARROW_BELOW 256
+// the DMA kernel takes 256x128 tiles when there are at most this many of them
+// (one per CU)
+#ifndef HOLO_DMA_NARROW_MAX
+#define HOLO_DMA_NARROW_MAX 256
 #endif
-constexpr uint64_t kDmaNarrowBelow = HOLO_DMA_NARROW_BELOW;
+constexpr uint64_t kDmaNarrowMax = HOLO_DMA_NARROW_MAX;
 
 __device__ __forceinline__ void tile_coords(uint32_t wg, uint32_t nwg, uint32_t tiles_m,
                                             uint32_t tiles_n, uint32_t *tm, uint32_t *tn) {
@@ -563,9 +564,9 @@ __device__ __forceinline__ void slab_barrier() {
 // workgroup's tile belongs to one segment.
 // Pair form (one segment): b[0] and b[1] are two products' B of the same
 // shape [K, n[0]] (SwiGLU's gate and up); the workgroup tile is 256 rows x
-// 128 columns of both, and c[0] receives f(gate) * g(up) per element, each
-// product narrowed to bf16 and passed through its activation table lut[0] /
-// lut[1] when given, the product narrowed again (the standalone kernels'
+// 128 columns of both, and c[0] receives f(gate) * up per element, each
+// product narrowed to bf16, gate passed through its activation table lut[0]
+// when given, the product narrowed again (the standalone kernels'
 // arithmetic).
 struct DmaGroup {
     const uint16_t *a;
@@ -574,7 +575,7 @@ struct DmaGroup {
     const uint16_t *b[kSkinnyMaxSeg];
     uint16_t *c[kSkinnyMaxSeg];
     uint32_t n[kSkinnyMaxSeg];
-    const uint16_t *lut[2];
+    const uint16_t *lut[1];
 };
 
 template <int BN, bool kPair = false>
@@ -777,8 +778,30 @@ __device__ __forceinline__ void gemm_bf16_dma(const DmaGroup &g) {
     // 32x32 D layout: acc[r] is row 8(r/4) + 4*lg + r%4, column lr
     uint16_t *cbase = C + uint64_t(m0 + wm + 4 * lg) * N + n0 + wn + lr;
     if constexpr (kPair) {
+        static_assert(kStage == 32768, "the table fills the four stages");
+        // gate's activation table (65536 bf16 = the four 32 KiB stages, which
+        // the last slab's reads have left) comes into LDS for the lookups:
+        // wave w fills stage w with entries 16384 w .. 16384 w + 16383
+        const uint16_t *lut = g.lut[0];
+        if (lut) {
+            slab_barrier();
+            const auto rl = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(lut), 0,
+                                                              131072, 0x00020000);
+            lds_u8 *dst = wave == 0 ? stage(s0{}) : wave == 1 ? stage(s1{}) : wave == 2 ? stage(s2{}) : stage(s3{});
+#pragma unroll
+            for (int t = 0; t < 32; ++t)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, dst + 1024 * t, 16, lane * 16u,
+                                                         wave * 32768u + t * 1024u, 0, 0);
+            wait_vm<0>();
+            slab_barrier();
+        }
+        auto lookup = [&](uint32_t x) -> uint32_t {
+            const uint32_t part = x >> 14, off = (x & 16383u) * 2u;
+            const lds_u8 *base = part == 0 ? stage(s0{}) : part == 1 ? stage(s1{})
+                               : part == 2 ? stage(s2{}) : stage(s3{});
+            return *reinterpret_cast<const __attribute__((address_space(3))) uint16_t *>(base + off);
+        };
         // acc[i][jj] is gate and acc[i][jj + 2] up at the same element
-        const uint16_t *lg_ = g.lut[0], *lu_ = g.lut[1];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -787,9 +810,8 @@ __device__ __forceinline__ void gemm_bf16_dma(const DmaGroup &g) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     uint32_t x = __float_as_uint(acc[i][jj][r]) >> 16;
-                    uint32_t y = __float_as_uint(acc[i][jj + 2][r]) >> 16;
-                    if (lg_) x = lg_[x];
-                    if (lu_) y = lu_[y];
+                    const uint32_t y = __float_as_uint(acc[i][jj + 2][r]) >> 16;
+                    if (lut) x = lookup(x);
                     const float v = __uint_as_float(x << 16) * __uint_as_float(y << 16);
                     ct[uint64_t(8 * (r >> 2) + (r & 3)) * N] = uint16_t(__float_as_uint(v) >> 16);
                 }
@@ -833,8 +855,11 @@ bool dma_applies(uint32_t m, uint32_t k, uint32_t n) {
 hipError_t launch_dma(DmaGroup g, hipStream_t stream) {
     uint32_t wide = 0;
     for (uint32_t i = 0; i < g.nseg; ++i) wide += g.n[i] / kBigN;
-    // 256x128 tiles when 256x256 ones would not give every CU a workgroup
-    const bool narrow = uint64_t(g.m / kBigM) * wide < kDmaNarrowBelow;
+    // 256x128 tiles when they all fit in one round of workgroups: a 256x128
+    // workgroup takes about 0.82 of a 256x256 one's time for half the work
+    // (4096x2048x2048: 40 us on 256 CUs vs 49 us on 128), so they pay only
+    // when twice as many tiles still need no second round
+    const bool narrow = 2 * uint64_t(g.m / kBigM) * wide <= kDmaNarrowMax;
     uint32_t cols = 0;
     for (uint32_t i = 0; i < g.nseg; ++i) {
         cols += g.n[i] / (narrow ? 128u : 256u);
@@ -922,8 +947,7 @@ hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint
 
 hipError_t launch_matmul_pair_tiled(const void *a, uint32_t m, uint32_t k, const void *b_gate,
                                     const void *b_up, uint32_t n, void *out,
-                                    const uint16_t *lut_gate, const uint16_t *lut_up,
-                                    hipStream_t stream) {
+                                    const uint16_t *lut_gate, hipStream_t stream) {
     const uintptr_t al = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b_gate) |
                          reinterpret_cast<uintptr_t>(b_up) | reinterpret_cast<uintptr_t>(out);
     if ((al & 15) != 0 || !matmul_group_tiled_applies(m, k, &n, 1)) return hipErrorInvalidValue;
@@ -938,7 +962,6 @@ hipError_t launch_matmul_pair_tiled(const void *a, uint32_t m, uint32_t k, const
     g.n[0] = n;
     g.tiles_end[0] = n / 128;
     g.lut[0] = lut_gate;
-    g.lut[1] = lut_up;
     const dim3 grid{(m / kBigM) * (n / 128)}, block{256u};
     hipLaunchKernelGGL(gemm_bf16_dma_pair_kernel, grid, block, 0, stream, g);
     return hipGetLastError();

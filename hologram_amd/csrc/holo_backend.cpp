@@ -393,17 +393,13 @@ int dispatch_group_impl(holo_backend *be, const SlotTable &st, const holo::Group
         // launch of the tiled kernel
         const size_t gi = g.segs[0].pair == 1 ? 0 : 1, ui = 1 - gi;
         const holo::GroupSegDesc &sg = g.segs[gi], &su = g.segs[ui];
-        auto table = [](const holo::GroupSegDesc &d) {
-            return d.base == holo::kEpiStore || d.base == holo::kEpiAct;
-        };
-        if (!table(sg) || !table(su) || sg.write_out || su.write_out || sg.head_dim || su.head_dim ||
-            sg.ssq || su.ssq || !su.skip)
-            return fail(HOLO_ERR_DISPATCH, std::string(op) + ": a tiled pair needs plain or "
-                                                             "table-activated products");
+        if (!(sg.base == holo::kEpiStore || sg.base == holo::kEpiAct) || su.base != holo::kEpiStore ||
+            sg.write_out || su.write_out || sg.head_dim || su.head_dim || sg.ssq || su.ssq || !su.skip)
+            return fail(HOLO_ERR_DISPATCH, std::string(op) + ": a tiled pair needs a plain or "
+                                                             "table-activated gate and a plain up");
         return launched(holo::launch_matmul_pair_tiled(
                             a.base, g.m, g.k, ss[gi].b, ss[ui].b, sg.n, e.seg[gi].mul_out,
-                            sg.base == holo::kEpiAct ? e.seg[gi].lut : nullptr,
-                            su.base == holo::kEpiAct ? e.seg[ui].lut : nullptr, be->stream),
+                            sg.base == holo::kEpiAct ? e.seg[gi].lut : nullptr, be->stream),
                         op);
     }
     if (!fast && nseg > 1 && bf16) {

@@ -169,15 +169,14 @@ bool matmul_group_tiled_applies(uint32_t m, uint32_t k, const uint32_t *n, int n
 hipError_t launch_matmul_group_tiled(const void *a, uint32_t m, uint32_t k,
                                      const SkinnySegment *segs, void *const *c, int nseg,
                                      hipStream_t stream);
-// SwiGLU-shaped pair on the tiled kernel: out = f(A*Bg) * g(A*Bu), each
-// product narrowed to bf16 and passed through its activation table when given
-// (the bf16 unary op's table), the product narrowed again. Applies where
-// matmul_group_tiled_applies does for [m, k] x [k, n]; bit for bit the two
-// single calls, their epilogues and the Mul.
+// SwiGLU-shaped pair on the tiled kernel: out = f(A*Bg) * (A*Bu), each
+// product narrowed to bf16, gate passed through its activation table when
+// given (the bf16 unary op's 65536-entry table), the product narrowed again.
+// Applies where matmul_group_tiled_applies does for [m, k] x [k, n]; bit for
+// bit the two single calls, gate's epilogue and the Mul.
 hipError_t launch_matmul_pair_tiled(const void *a, uint32_t m, uint32_t k, const void *b_gate,
                                     const void *b_up, uint32_t n, void *out,
-                                    const uint16_t *lut_gate, const uint16_t *lut_up,
-                                    hipStream_t stream);
+                                    const uint16_t *lut_gate, hipStream_t stream);
 hipError_t launch_skinny_partials(const void *a, uint32_t m, uint32_t k, uint8_t dtype,
                                   const SkinnySegment *segs, int nseg, const SkinnyPlan &plan,
                                   float *P, hipStream_t stream, const SkinnyNormA *norm = nullptr);

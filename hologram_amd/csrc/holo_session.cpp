@@ -523,8 +523,7 @@ void device_fusion(holo_session *s, const std::vector<uint8_t> &is_output,
             taken[j] = true;
         }
         // pull each product's sole consumer into the epilogue (tiled groups:
-        // only the SwiGLU product of a group of exactly two, whose bases are
-        // the plain product or a table activation)
+        // only the SwiGLU product of a group of exactly two)
         const bool tiled_group = pl.mt == 0;
         std::vector<holo_buffer_ref> value(g.segs.size());
         std::vector<bool> done(g.segs.size(), tiled_group && g.segs.size() != 2);
@@ -586,11 +585,10 @@ void device_fusion(holo_session *s, const std::vector<uint8_t> &is_output,
                         partner = int(u);
                         break;
                     }
-                    auto table_base = [](const holo::GroupSegDesc &d) {
-                        return d.base == holo::kEpiStore || d.base == holo::kEpiAct;
-                    };
+                    // tiled pair: a plain or table-activated gate, a plain up
                     if (tiled_group && partner >= 0 &&
-                        !(table_base(trial) && table_base(g.segs[size_t(partner)]) &&
+                        !((trial.base == holo::kEpiStore || trial.base == holo::kEpiAct) &&
+                          g.segs[size_t(partner)].base == holo::kEpiStore &&
                           b.output.offset % 16 == 0))
                         partner = -1;
                     if (partner >= 0 && b.dtype == g.dtype && b.element_count == mn) {

@@ -546,6 +546,223 @@ __global__ __launch_bounds__(kThreads, kWps) void attn_rows_packed_kernel(
                                  true, H, Hkv, G, bucket, log2e_over_scale, lds, rows, lim0);
 }
 
+// Prompt form for G = 4, D = 64, bf16 rows: grid (ceil(T / 64), Hkv, B).
+// A workgroup takes 64 consecutive query rows of one sequence; wave w owns
+// query head 4 kh + w. Each 64-key tile of the plane is staged in LDS once for
+// all four heads: K as bf16 [key][dim] (int8 values are exact) and V
+// transposed as f16 [dim][key] with the key's scale applied (v * vscale, an
+// f16 rounding of 2^-11 relative). Per tile and wave:
+//     S^T[64 keys x 64 rows] = K . Q^T   v_mfma_f32_32x32x16_bf16
+//     scale by kscale * log2e / scale, causal mask per row (only in tiles
+//     some row of the block does not fully see), online softmax (fp32, exp2;
+//     a row is a lane column, its keys in the lane and the lane 32 apart),
+//     p as f16
+//     O^T[64 dims x 64 rows] += V'^T . P^T   v_mfma_f32_32x32x16_f16
+// A lane's 8 scores of a 16-key step are exactly its B operand when the
+// step's keys are taken in the order the S^T layout holds them (rows
+// 4 lg + 0..3 and 8 + 4 lg + 0..3 of each 16); V^T is read in that order.
+// Row t sees the first clamp(lens[b] - (T - 1 - t), 0, bucket) keys; a row
+// that sees none is written as zeros. Later row blocks see more keys; the
+// upper half of the workgroups takes the blocks in reverse order, so the two
+// workgroups a CU holds at once tend to pair a long block with a short one.
+constexpr uint32_t kPT = 64;    // query rows per workgroup, keys per tile
+constexpr uint32_t kPLd = 72;   // LDS row stride of the staged tiles (16-bit elements)
+typedef __bf16 pbf16x8 __attribute__((ext_vector_type(8)));
+typedef float pf32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ uint32_t bf16_of_int(int v) {
+    return __float_as_uint(float(v)) >> 16;   // exact: |v| <= 128
+}
+__device__ __forceinline__ uint32_t f16_of_int(int v) {
+    const _Float16 h = _Float16(float(v));
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+__global__ __launch_bounds__(kThreads, 2) void attn_prompt_kernel(
+    const uint16_t *__restrict__ q, const int8_t *__restrict__ kq, const int8_t *__restrict__ vq,
+    const float *__restrict__ ks, const float *__restrict__ vs, const uint32_t *__restrict__ lens,
+    uint16_t *__restrict__ out, uint32_t H, uint32_t Hkv, uint32_t bucket, float mul, uint32_t T) {
+    __shared__ __attribute__((aligned(16))) uint16_t kl[kPT * kPLd];   // K tile, bf16 [key][dim]
+    __shared__ __attribute__((aligned(16))) uint16_t vt[kPT * kPLd];   // V tile, f16 [dim][key]
+    __shared__ float ksl[kPT];
+    const uint32_t nqb = gridDim.x;
+    const uint32_t lin = blockIdx.x + nqb * (blockIdx.y + gridDim.y * blockIdx.z);
+    const uint32_t xb = 2 * lin >= nqb * gridDim.y * gridDim.z ? nqb - 1 - blockIdx.x : blockIdx.x;
+    const uint32_t b = blockIdx.z, kh = blockIdx.y, t0 = xb * kPT;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, lg = lane >> 5;
+    const uint32_t h = kh * 4 + wave;
+    const uint64_t plane = uint64_t(b) * Hkv + kh;
+    const int8_t *kp = kq + plane * bucket * 64, *vp = vq + plane * bucket * 64;
+    const float *ksp = ks + plane * bucket, *vsp = vs + plane * bucket;
+    const int64_t len = lens[b];
+    auto visible = [&](uint32_t t) -> uint32_t {
+        const int64_t L = len - int64_t(T - 1 - t);
+        return L < 0 ? 0u : (L > int64_t(bucket) ? bucket : uint32_t(L));
+    };
+    const uint32_t tl = (t0 + kPT < T ? t0 + kPT : T) - 1;   // the block's last row sees most
+    const uint32_t kmax = visible(tl);
+    const uint32_t kmin = visible(t0);   // ... and its first row least: keys < kmin need no mask
+
+    // this lane's rows t0 + 32 qb + lr: their key limits and Q^T fragments
+    // (dims 16 kk + 8 lg .. +7)
+    uint32_t lim[2];
+    pbf16x8 qf[2][4];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        const uint32_t t = t0 + 32 * qb + lr;
+        lim[qb] = t < T ? visible(t) : 0u;
+        const uint16_t *qr = q + ((uint64_t(b) * T + t) * H + h) * 64 + 8 * lg;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            u32x4 v = u32x4{0u, 0u, 0u, 0u};
+            if (t < T) v = *reinterpret_cast<const u32x4 *>(qr + 16 * kk);
+            qf[qb][kk] = __builtin_bit_cast(pbf16x8, v);
+        }
+    }
+    pf32x16 o[2][2];
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[db][qb][r] = 0.0f;
+    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
+
+    for (uint32_t j0 = 0; j0 < kmax; j0 += kPT) {
+        __syncthreads();   // the previous tile's readers are done
+        {
+            // thread: key tid / 4, dims 16 (tid % 4) .. +15
+            const uint32_t key = tid >> 2, d0 = (tid & 3) * 16, j = j0 + key;
+            u32x4 kr = u32x4{0u, 0u, 0u, 0u}, vr = kr;
+            if (j < bucket) {
+                kr = *reinterpret_cast<const u32x4 *>(kp + uint64_t(j) * 64 + d0);
+                vr = *reinterpret_cast<const u32x4 *>(vp + uint64_t(j) * 64 + d0);
+            }
+            u32x4 k0, k1;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const uint32_t x = kr[w];
+                const uint32_t lo = bf16_of_int(int8_t(x & 0xff)) | (bf16_of_int(int8_t((x >> 8) & 0xff)) << 16);
+                const uint32_t hi = bf16_of_int(int8_t((x >> 16) & 0xff)) | (bf16_of_int(int8_t(x >> 24)) << 16);
+                if (w < 2) {
+                    k0[2 * w] = lo;
+                    k0[2 * w + 1] = hi;
+                } else {
+                    k1[2 * w - 4] = lo;
+                    k1[2 * w - 3] = hi;
+                }
+            }
+            *reinterpret_cast<u32x4 *>(kl + key * kPLd + d0) = k0;
+            *reinterpret_cast<u32x4 *>(kl + key * kPLd + d0 + 8) = k1;
+            const float vsc = j < bucket ? vsp[j] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const _Float16 vh = _Float16(float(int8_t((vr[i / 4] >> (8 * (i % 4))) & 0xff)) * vsc);
+                vt[(d0 + i) * kPLd + key] = __builtin_bit_cast(uint16_t, vh);
+            }
+            if (tid < int(kPT)) {
+                const uint32_t jj = j0 + tid;
+                ksl[tid] = jj < bucket ? ksp[jj] * mul : 0.0f;
+            }
+        }
+        __syncthreads();
+
+        // S^T for key blocks kb and row blocks qb
+        pf32x16 s[2][2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            pbf16x8 kf[4];
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+                kf[kk] = *reinterpret_cast<const pbf16x8 *>(kl + (32 * kb + lr) * kPLd + 16 * kk + 8 * lg);
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) s[kb][qb][r] = 0.0f;
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk)
+                    s[kb][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kk], qf[qb][kk], s[kb][qb], 0, 0, 0);
+            }
+        }
+        // scale, mask, online softmax; s becomes p
+        float ksc[2][16];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) ksc[kb][r] = ksl[32 * kb + 8 * (r >> 2) + 4 * lg + (r & 3)];
+        const bool full = j0 + kPT <= kmin;   // every row of the block sees the whole tile
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            float mt = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t kt = 32 * kb + 8 * (r >> 2) + 4 * lg + (r & 3);
+                    float x = s[kb][qb][r] * ksc[kb][r];
+                    if (!full) x = j0 + kt < lim[qb] ? x : -INFINITY;
+                    s[kb][qb][r] = x;
+                    mt = x > mt ? x : mt;
+                }
+            const float mo = __shfl_xor(mt, 32, 64);
+            mt = mo > mt ? mo : mt;
+            const float mn = m[qb] > mt ? m[qb] : mt;
+            // v_exp_f32 directly: it differs from exp2f only below 2^-126
+            const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[qb] - mn);
+            const float mref = mn == -INFINITY ? 0.0f : mn;   // all masked: exp2(-inf) = 0
+            float rs = 0.0f;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float p = __builtin_amdgcn_exp2f(s[kb][qb][r] - mref);
+                    rs += p;
+                    s[kb][qb][r] = p;
+                }
+            rs += __shfl_xor(rs, 32, 64);
+            l[qb] = l[qb] * alpha + rs;
+            m[qb] = mn;
+#pragma unroll
+            for (int db = 0; db < 2; ++db) o[db][qb] *= alpha;
+        }
+        // O^T += V^T . P'^T over four 16-key steps
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const int kb = st >> 1, hh = st & 1;
+            f16x8 pf[2];
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) pf[qb][i] = _Float16(s[kb][qb][8 * hh + i]);
+#pragma unroll
+            for (int db = 0; db < 2; ++db) {
+                const uint16_t *vrow = vt + (32 * db + lr) * kPLd + 32 * kb + 16 * hh + 4 * lg;
+                const uint2 lo = *reinterpret_cast<const uint2 *>(vrow);
+                const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + 8);
+                const u32x4 w = u32x4{lo.x, lo.y, hi.x, hi.y};
+                const f16x8 vf = __builtin_bit_cast(f16x8, w);
+#pragma unroll
+                for (int qb = 0; qb < 2; ++qb)
+                    o[db][qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[qb], o[db][qb], 0, 0, 0);
+            }
+        }
+    }
+    // O^T: lane holds dims 32 db + 8 (r/4) + 4 lg + r%4 of row t0 + 32 qb + lr
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        const uint32_t t = t0 + 32 * qb + lr;
+        if (t >= T) continue;
+        const float inv = l[qb] > 0.0f ? 1.0f / l[qb] : 0.0f;
+        uint16_t *orow = out + ((uint64_t(b) * T + t) * H + h) * 64;
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                orow[32 * db + 8 * (r >> 2) + 4 * lg + (r & 3)] =
+                    uint16_t(__float_as_uint(o[db][qb][r] * inv) >> 16);
+    }
+}
+
 // Balanced form: the planes' 128-key quads laid end to end, plane (b, kh) in
 // (b, kh) order, and cut into `P` equal shares, one per workgroup (P is the
 // number of workgroups the GPU holds at once, so the whole batch is one round
@@ -844,6 +1061,17 @@ hipError_t run_t(const AttnI8Args &a, void *scratch, hipStream_t stream) {
         hipLaunchKernelGGL((attn_merge_kernel<D, kF32Q>), dim3(a.Hkv, a.B), dim3(256), 0, stream,
                            part, qoff, a.lens, a.out, a.B, a.H, a.Hkv, G, a.bucket, P);
         return hipGetLastError();
+    }
+    if constexpr (D == 64 && !kF32Q) {
+        const uintptr_t al = reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.kq) |
+                             reinterpret_cast<uintptr_t>(a.vq) | reinterpret_cast<uintptr_t>(a.out);
+        if (a.q_rows > 1 && G == 4 && (al & 15) == 0) {
+            hipLaunchKernelGGL(attn_prompt_kernel, dim3((a.q_rows + kPT - 1) / kPT, a.Hkv, a.B),
+                               dim3(kThreads), 0, stream, static_cast<const uint16_t *>(a.q), a.kq,
+                               a.vq, a.ks, a.vs, a.lens, static_cast<uint16_t *>(a.out), a.H, a.Hkv,
+                               a.bucket, mul, a.q_rows);
+            return hipGetLastError();
+        }
     }
     const uint32_t ck = chunk_keys(a.bucket);
     const uint32_t nch = chunks_of(a.bucket);

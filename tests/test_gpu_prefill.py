@@ -95,6 +95,23 @@ def test_attention_rows_parity(torch_cuda, backend, H, Hkv, D):
                 assert err <= 1e-2, (b, t, err)
 
 
+@pytest.mark.parametrize("B,T,S,lens", [(4, 130, 256, [130, 250, 60, 7]), (2, 64, 64, [64, 64]),
+                                        (3, 200, 512, [512, 200, 1])])
+def test_attention_prompt_tiles_parity(torch_cuda, backend, B, T, S, lens):
+    """The tiled prompt form (G = 4, D = 64, bf16): several 64-row blocks and
+    64-key tiles, rows that see part of a tile, rows past the bucket, rows
+    that see no key."""
+    H, Hkv, D = 8, 2, 64
+    got, want, _ = run_rows(torch_cuda, backend, B, T, H, Hkv, D, S, lens, seed=T + S)
+    for b in range(B):
+        for t in range(T):
+            if lens[b] - (T - 1 - t) <= 0:
+                assert np.all(got[b, t] == 0), (b, t)
+            else:
+                err = np.max(np.abs(got[b, t] - want[b, t])) / (np.max(np.abs(want[b, t])) + 1e-9)
+                assert err <= 1e-2, (b, t, err)
+
+
 def test_attention_rows_one_row_is_op_123(torch_cuda, backend):
     args = (4, 1, 8, 2, 64, 64, [1, 17, 64, 30], 5)
     _, _, a = run_rows(torch_cuda, backend, *args, q_rows_op=True)

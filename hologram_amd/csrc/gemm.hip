@@ -575,6 +575,7 @@ struct DmaGroup {
     const uint16_t *b[kSkinnyMaxSeg];
     uint16_t *c[kSkinnyMaxSeg];
     uint32_t n[kSkinnyMaxSeg];
+    const uint16_t *res[kSkinnyMaxSeg];   // plain form: residual [M, n_s] added, or null
     const uint16_t *lut[1];
 };
 
@@ -604,12 +605,14 @@ __device__ __forceinline__ void gemm_bf16_dma(const DmaGroup &g) {
     // this tile's segment (workgroup-uniform, chosen with selects)
     const uint16_t *__restrict__ B = g.b[0];
     uint16_t *__restrict__ C = g.c[0];
+    const uint16_t *Rs = g.res[0];
     uint32_t N = g.n[0], first = 0;
 #pragma unroll
     for (int i = 1; i < kSkinnyMaxSeg; ++i)
         if (uint32_t(i) < g.nseg && tn >= g.tiles_end[i - 1]) {
             B = g.b[i];
             C = g.c[i];
+            Rs = g.res[i];
             N = g.n[i];
             first = g.tiles_end[i - 1];
         }
@@ -787,11 +790,12 @@ __device__ __forceinline__ void gemm_bf16_dma(const DmaGroup &g) {
             slab_barrier();
             const auto rl = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(lut), 0,
                                                               131072, 0x00020000);
-            lds_u8 *dst = wave == 0 ? stage(s0{}) : wave == 1 ? stage(s1{}) : wave == 2 ? stage(s2{}) : stage(s3{});
+            const uint32_t wu = __builtin_amdgcn_readfirstlane(wave);   // in an SGPR
+            lds_u8 *dst = wu == 0 ? stage(s0{}) : wu == 1 ? stage(s1{}) : wu == 2 ? stage(s2{}) : stage(s3{});
 #pragma unroll
             for (int t = 0; t < 32; ++t)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, dst + 1024 * t, 16, lane * 16u,
-                                                         wave * 32768u + t * 1024u, 0, 0);
+                                                         wu * 32768u + t * 1024u, 0, 0);
             wait_vm<0>();
             slab_barrier();
         }
@@ -818,17 +822,64 @@ __device__ __forceinline__ void gemm_bf16_dma(const DmaGroup &g) {
                 __builtin_amdgcn_sched_barrier(0);
             }
     } else {
+        // + residual (MatMulAdd): each wave brings the residual of its own
+        // 128 x BW/2 quadrant into its LDS stage (the main loop has left the
+        // stages; the one barrier waits out the last slab's reads), then adds
+        // it block row by block row as the loads land: product narrowed,
+        // residual added in f32, narrowed again (the standalone epilogue's
+        // arithmetic)
+        constexpr uint32_t kQc = BW / 2, kLanesRow = kQc / 8, kRows = 64 / kLanesRow;
+        constexpr uint32_t kLoadsI = 32 / kRows;   // 1 KiB loads per 32-row block row
+        const uint32_t wu = __builtin_amdgcn_readfirstlane(wave);   // the wave index, in an SGPR
+        lds_u8 *qres = wu == 0 ? stage(s0{}) : wu == 1 ? stage(s1{}) : wu == 2 ? stage(s2{}) : stage(s3{});
+        if (Rs) {
+            static_assert(128 * kQc * 2 <= kStage, "a stage holds a wave's residual quadrant");
+            slab_barrier();
+            const uint64_t q0 = uint64_t(m0 + (wu >> 1) * 128u) * N + n0 + (wu & 1u) * kQc;
+            const auto rr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(Rs + q0), 0,
+                                                              int(256u * N), 0x00020000);
+            const uint32_t voff = ((lane / kLanesRow) * N + 8u * (lane % kLanesRow)) * 2u;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+            for (uint32_t t = 0; t < 4 * kLoadsI; ++t)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, qres + 1024 * t, 16, voff, kRows * t * N * 2u, 0, 0);
+        }
+        auto res_at = [&](uint32_t qr, uint32_t qc) -> uint32_t {
+            return *reinterpret_cast<const __attribute__((address_space(3))) uint16_t *>(
+                qres + (qr * kQc + qc) * 2u);
+        };
+        if (Rs) {
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                uint16_t *ct = cbase + uint64_t(32 * i) * N + 32 * j;
+            for (int i = 0; i < 4; ++i) {
+                if (i == 0) wait_vm<3 * kLoadsI>();
+                else if (i == 1) wait_vm<2 * kLoadsI>();
+                else if (i == 2) wait_vm<kLoadsI>();
+                else wait_vm<0>();
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    ct[uint64_t(8 * (r >> 2) + (r & 3)) * N] =
-                        uint16_t(__float_as_uint(acc[i][j][r]) >> 16);
-                __builtin_amdgcn_sched_barrier(0);
+                for (int j = 0; j < NJ; ++j) {
+                    uint16_t *ct = cbase + uint64_t(32 * i) * N + 32 * j;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const uint32_t x = __float_as_uint(acc[i][j][r]) >> 16;
+                        const uint32_t y = res_at(32 * i + 8 * (r >> 2) + 4 * lg + (r & 3), 32 * j + lr);
+                        ct[uint64_t(8 * (r >> 2) + (r & 3)) * N] = uint16_t(
+                            __float_as_uint(__uint_as_float(x << 16) + __uint_as_float(y << 16)) >> 16);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    uint16_t *ct = cbase + uint64_t(32 * i) * N + 32 * j;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        ct[uint64_t(8 * (r >> 2) + (r & 3)) * N] =
+                            uint16_t(__float_as_uint(acc[i][j][r]) >> 16);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+        }
     }
 }
 
@@ -976,12 +1027,16 @@ bool matmul_group_tiled_applies(uint32_t m, uint32_t k, const uint32_t *n, int n
 
 hipError_t launch_matmul_group_tiled(const void *a, uint32_t m, uint32_t k,
                                      const SkinnySegment *segs, void *const *c, int nseg,
-                                     hipStream_t stream) {
+                                     hipStream_t stream, const void *const *res) {
     uint32_t n[kSkinnyMaxSeg] = {};
     uintptr_t al = reinterpret_cast<uintptr_t>(a);
     for (int i = 0; i < nseg && i < kSkinnyMaxSeg; ++i) {
         n[i] = segs[i].n;
         al |= reinterpret_cast<uintptr_t>(segs[i].b) | reinterpret_cast<uintptr_t>(c[i]);
+        if (res && res[i]) {
+            al |= reinterpret_cast<uintptr_t>(res[i]);
+            if (n[i] >= (1u << 21)) return hipErrorInvalidValue;   // 256 rows within 2^31 bytes
+        }
     }
     if ((al & 15) != 0 || !matmul_group_tiled_applies(m, k, n, nseg)) return hipErrorInvalidValue;
     DmaGroup g{};
@@ -993,6 +1048,7 @@ hipError_t launch_matmul_group_tiled(const void *a, uint32_t m, uint32_t k,
         g.b[i] = static_cast<const uint16_t *>(segs[i].b);
         g.c[i] = static_cast<uint16_t *>(c[i]);
         g.n[i] = n[i];
+        g.res[i] = res ? static_cast<const uint16_t *>(res[i]) : nullptr;
     }
     return launch_dma(g, stream);
 }

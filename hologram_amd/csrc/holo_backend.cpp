@@ -416,11 +416,15 @@ int dispatch_group_impl(holo_backend *be, const SlotTable &st, const holo::Group
             cs[i] = e.seg[i].out;
         }
         if (plain && holo::matmul_group_tiled_applies(g.m, g.k, ns, int(nseg))) {
+            // residual adds ride in the tiled kernel's store
+            const void *rs[holo::kSkinnyMaxSeg] = {};
+            for (size_t i = 0; i < nseg; ++i)
+                if (g.segs[i].base == holo::kEpiAdd) rs[i] = e.seg[i].residual;
             HOLO_TRY(launched(holo::launch_matmul_group_tiled(a.base, g.m, g.k, ss, cs, int(nseg),
-                                                              be->stream),
+                                                              be->stream, rs),
                               op));
             for (size_t i = 0; i < nseg; ++i) {
-                if (g.segs[i].base == holo::kEpiStore) continue;
+                if (g.segs[i].base == holo::kEpiStore || g.segs[i].base == holo::kEpiAdd) continue;
                 holo::TileEpi te;
                 te.kind = g.segs[i].base;
                 te.act = g.segs[i].act;
@@ -440,6 +444,17 @@ int dispatch_group_impl(holo_backend *be, const SlotTable &st, const holo::Group
             return fail(HOLO_ERR_DISPATCH,
                         std::string(op) + ": a fused group needs the few-row path (16-byte aligned "
                                           "operands, one common split)");
+        if (bf16 && s.base == holo::kEpiAdd && s.n < (1u << 21) &&
+            holo::matmul_group_tiled_applies(g.m, g.k, &s.n, 1) &&
+            ((reinterpret_cast<uintptr_t>(a.base) | reinterpret_cast<uintptr_t>(ss[0].b) |
+              reinterpret_cast<uintptr_t>(e.seg[0].out) |
+              reinterpret_cast<uintptr_t>(e.seg[0].residual)) & 15) == 0) {
+            // MatMulAdd at large M: the residual is added in the tiled kernel's store
+            void *cs[1] = {e.seg[0].out};
+            const void *rs[1] = {e.seg[0].residual};
+            return launched(holo::launch_matmul_group_tiled(a.base, g.m, g.k, ss, cs, 1, be->stream, rs),
+                            op);
+        }
         // the tiled product into the output, then the epilogue over it in place
         HOLO_TRY(ensure_scratch(be, holo::matmul_scratch_bytes(g.m, g.k, s.n, g.dtype), op));
         HOLO_TRY(launched(holo::launch_matmul(a.base, ss[0].b, e.seg[0].out, g.m, g.k, s.n, g.dtype,

@@ -164,11 +164,13 @@ struct SkinnyNormA {
 // Large-M bf16 products sharing A [m, k] (segment s: B_s [k, n_s] into c[s]),
 // one launch of the tiled DMA kernel. Applies when each product alone would
 // take that kernel (launch_matmul), so each result is bit for bit the single
-// call's. Operands 16-byte aligned.
+// call's. res (optional, per segment, null for none): a residual [m, n_s]
+// added as MatMulAdd does (product narrowed, added in f32, narrowed; n_s <
+// 2^21). Operands 16-byte aligned.
 bool matmul_group_tiled_applies(uint32_t m, uint32_t k, const uint32_t *n, int nseg);
 hipError_t launch_matmul_group_tiled(const void *a, uint32_t m, uint32_t k,
                                      const SkinnySegment *segs, void *const *c, int nseg,
-                                     hipStream_t stream);
+                                     hipStream_t stream, const void *const *res = nullptr);
 // SwiGLU-shaped pair on the tiled kernel: out = f(A*Bg) * (A*Bu), each
 // product narrowed to bf16, gate passed through its activation table when
 // given (the bf16 unary op's 65536-entry table), the product narrowed again.

@@ -92,6 +92,36 @@ def test_fused_matmul_bit_exact(torch_cuda, backend, m, kind, act, dtype):
     assert bad.size == 0, f"{bad.size} mismatches, first at {bad[:4]}: {got[bad[:4]]} vs {want[bad[:4]]}"
 
 
+@pytest.mark.parametrize("m,k,n", [(1024, 512, 2048), (4096, 256, 4096), (512, 1024, 4096)])
+def test_fused_add_large_m_bit_exact(torch_cuda, backend, m, k, n):
+    """bf16 MatMulAdd at large M adds the residual in the tiled kernel's store
+    (256x128 tiles for the first and last shapes, 256x256 for the second):
+    each element is the plain product narrowed, plus the residual in f32,
+    narrowed again."""
+    rng = np.random.default_rng(m + k + n)
+    a = narrow((rng.standard_normal(m * k) / np.sqrt(k)).astype(np.float32), DTYPE_BF16)
+    b = narrow(rng.standard_normal(k * n).astype(np.float32), DTYPE_BF16)
+    r = narrow(rng.standard_normal(m * n).astype(np.float32), DTYPE_BF16)
+    ws = DeviceWorkspace()
+    keep = [to_dev(torch_cuda, x) for x in (a, b, r)]
+    for s, t in enumerate(keep):
+        ws.bind(s, t)
+    prod = torch_cuda.zeros(m * n * 2, dtype=torch_cuda.uint8, device="cuda")
+    fused = torch_cuda.zeros(m * n * 2, dtype=torch_cuda.uint8, device="cuda")
+    ws.bind(3, prod)
+    ws.bind(4, fused)
+    backend.dispatch(KernelCall.MatMul(MatMulCall(BufferRef(0), BufferRef(1), BufferRef(3), m, k, n,
+                                                  DTYPE_BF16)), ws)
+    mmf = MatMulCall(BufferRef(0), BufferRef(1), BufferRef(4), m, k, n, DTYPE_BF16)
+    backend.dispatch(KernelCall.MatMulAdd(MatMulAddCall(mmf, BufferRef(2))), ws)
+    backend.synchronize()
+    p = from_dev(prod, np.uint16)
+    got = from_dev(fused, np.uint16)
+    want = narrow(widen(p, DTYPE_BF16) + widen(r, DTYPE_BF16), DTYPE_BF16)
+    bad = np.flatnonzero(got != want)
+    assert bad.size == 0, f"{bad.size} mismatches, first at {bad[:4]}: {got[bad[:4]]} vs {want[bad[:4]]}"
+
+
 CFG = DecoderConfig(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=1000,
                     batch=3, bucket=64)
 

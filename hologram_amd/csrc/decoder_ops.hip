@@ -148,6 +148,33 @@ __global__ __launch_bounds__(256) void rope_kernel(const void *__restrict__ x,
     }
 }
 
+// The bf16 form eight elements a lane (head_dim a multiple of 16, operands
+// 16-byte aligned, n a multiple of 8): the same per-element arithmetic, with
+// 16-byte loads of x, its rotate-half partner, cos and sin.
+__global__ __launch_bounds__(256) void rope_bf16_vec_kernel(const u32x4 *__restrict__ x,
+                                                            const u32x4 *__restrict__ cs,
+                                                            const u32x4 *__restrict__ sn,
+                                                            u32x4 *__restrict__ out, uint32_t head_dim,
+                                                            uint64_t n8) {
+    const uint32_t half8 = head_dim / 16, hd8 = head_dim / 8;
+    for (uint64_t e = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; e < n8;
+         e += uint64_t(gridDim.x) * blockDim.x) {
+        const bool lo = uint32_t(e % hd8) < half8;
+        const u32x4 xv = x[e], pv = x[lo ? e + half8 : e - half8], cv = cs[e], sv = sn[e];
+        u32x4 o;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t sh = (j & 1) * 16;
+            const float xe = bf2f((xv[j / 2] >> sh) & 0xffffu), xp = bf2f((pv[j / 2] >> sh) & 0xffffu);
+            const float ce = bf2f((cv[j / 2] >> sh) & 0xffffu), se = bf2f((sv[j / 2] >> sh) & 0xffffu);
+            const float v = lo ? xe * ce - xp * se : xe * ce + xp * se;
+            const uint32_t b = f2bf(v);
+            o[j / 2] = (j & 1) ? (o[j / 2] | (b << 16)) : b;
+        }
+        out[e] = o;
+    }
+}
+
 // Gather rows of `row_bytes` (a multiple of 4 when `words`): one workgroup per
 // (outer, index) row. An index outside [-axis_dim, axis_dim) zeroes its row
 // and raises *err.
@@ -319,6 +346,14 @@ hipError_t launch_rmsnorm(const void *x, const void *gamma, void *out, uint32_t 
 
 hipError_t launch_rope(const void *x, const void *cs, const void *sn, void *out, uint32_t head_dim,
                        uint64_t n, bool bf16, hipStream_t stream) {
+    if (bf16 && head_dim % 16 == 0 && n % 8 == 0 &&
+        ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(cs) |
+          reinterpret_cast<uintptr_t>(sn) | reinterpret_cast<uintptr_t>(out)) & 15) == 0) {
+        hipLaunchKernelGGL(rope_bf16_vec_kernel, dim3(grid_for(n / 8)), dim3(256), 0, stream,
+                           static_cast<const u32x4 *>(x), static_cast<const u32x4 *>(cs),
+                           static_cast<const u32x4 *>(sn), static_cast<u32x4 *>(out), head_dim, n / 8);
+        return hipGetLastError();
+    }
     const unsigned grid = grid_for(n);
     if (bf16)
         hipLaunchKernelGGL((rope_kernel<true>), dim3(grid), dim3(256), 0, stream, x, cs, sn, out, head_dim, n);

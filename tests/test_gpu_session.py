@@ -94,9 +94,11 @@ def test_rms_norm(torch_cuda, backend, dtype, tol, batch, feature):
 
 
 @pytest.mark.parametrize("dtype", [DTYPE_BF16, DTYPE_F32])
-def test_rope_bit_exact(torch_cuda, backend, dtype):
-    rng = np.random.default_rng(5)
-    heads, D = 37, 64
+@pytest.mark.parametrize("heads,D", [(37, 64), (5, 40), (80000, 128)])
+def test_rope_bit_exact(torch_cuda, backend, dtype, heads, D):
+    """bf16 with head_dim a multiple of 16 takes the eight-a-lane kernel (the
+    largest case also its grid-stride loop); head_dim 40 the scalar one."""
+    rng = np.random.default_rng(5 + heads)
     x32 = rng.standard_normal(heads * D).astype(np.float32)
     th = rng.uniform(-3, 3, (heads, D // 2))
     c32 = np.concatenate([np.cos(th), np.cos(th)], 1).astype(np.float32).ravel()

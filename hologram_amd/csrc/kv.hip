@@ -64,9 +64,15 @@ __global__ __launch_bounds__(kCopyThreads) void place_rows_kernel(const uint8_t 
     for (uint32_t c = threadIdx.x; c < row_bytes; c += kCopyThreads) out[dst + c] = nw[src + c];
 }
 
+__device__ __forceinline__ float widen16(uint32_t b, uint8_t dtype);
+
 __device__ __forceinline__ float widen(const void *base, uint8_t dtype, uint64_t i) {
     if (dtype == 8) return reinterpret_cast<const float *>(base)[i];
-    const uint32_t b = reinterpret_cast<const uint16_t *>(base)[i];
+    return widen16(reinterpret_cast<const uint16_t *>(base)[i], dtype);
+}
+
+// A 16-bit element (bf16, else f16) widened to f32.
+__device__ __forceinline__ float widen16(uint32_t b, uint8_t dtype) {
     if (dtype == 7) return __uint_as_float(b << 16);
     // f16 -> f32 by bits, as src/cpu/dtype.rs:94-118 (exact; NaN payload kept)
     const uint32_t s = (b >> 15) << 31, e = (b >> 10) & 0x1fu, m = b & 0x3ffu;
@@ -143,6 +149,53 @@ __global__ __launch_bounds__(256) void quant_append_kernel(const void *__restric
     if (lane == 0) cs[row] = amax / 127.0f;
 }
 
+// The same quantization for 16-bit rows of d = 8 kL elements (64 or 128):
+// kL lanes a row, eight elements a lane from one 16-byte load, the row max
+// over the kL lanes, eight int8 values stored at once.
+template <uint32_t kL>
+__global__ __launch_bounds__(256) void quant_append_vec_kernel(const u32x4 *__restrict__ nw,
+                                                              uint8_t dtype,
+                                                              const uint32_t *__restrict__ posp,
+                                                              int8_t *__restrict__ cq,
+                                                              float *__restrict__ cs, uint32_t planes,
+                                                              uint32_t bucket, uint32_t new_rows) {
+    constexpr uint32_t d = 8 * kL;
+    const uint64_t t = uint64_t(blockIdx.x) * 256u + threadIdx.x;
+    const uint64_t r = t / kL;
+    const uint32_t c = uint32_t(t % kL);
+    const bool live = r < uint64_t(planes) * new_rows;
+    const u32x4 v = live ? nw[t] : u32x4{0u, 0u, 0u, 0u};
+    float x[8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        x[e] = widen16((v[e / 2] >> ((e & 1) * 16)) & 0xffffu, dtype);
+        const float av = x[e] < 0.0f ? -x[e] : x[e];
+        if (av > amax) amax = av;
+    }
+#pragma unroll
+    for (uint32_t off = kL / 2; off >= 1; off >>= 1) {
+        const float o = __shfl_xor(amax, int(off), 64);
+        if (o > amax) amax = o;
+    }
+    if (!live) return;
+    const uint32_t p = uint32_t(r / new_rows), j = uint32_t(r % new_rows);
+    const uint64_t row = uint64_t(p) * bucket + (uint64_t(*posp % bucket) + j) % bucket;
+    uint32_t lo = 0, hi = 0;
+    if (amax != 0.0f) {
+        const float inv = 127.0f / amax;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float q = x[e] * inv;
+            const float rq = q >= 0.0f ? truncf(q + 0.5f) : truncf(q - 0.5f);
+            const uint32_t by = uint32_t(uint8_t(to_q(rq))) << (8 * (e & 3));
+            if (e < 4) lo |= by; else hi |= by;
+        }
+    }
+    reinterpret_cast<uint2 *>(cq + row * d)[c] = make_uint2(lo, hi);
+    if (c == 0) cs[row] = amax == 0.0f ? 0.0f : amax / 127.0f;
+}
+
 }  // namespace
 
 hipError_t launch_copy_bytes(const void *src, void *dst, uint64_t bytes, hipStream_t stream) {
@@ -191,6 +244,18 @@ hipError_t launch_kv_quant_append(const void *nw, uint8_t dtype, const uint32_t 
     const uint64_t blocks = (waves + 3) / 4;
     if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
     const dim3 g{unsigned(blocks), 1, 1}, b{256, 1, 1};
+    if (dtype != 8 && (d == 64 || d == 128) && (reinterpret_cast<uintptr_t>(nw) & 15) == 0 &&
+        (reinterpret_cast<uintptr_t>(cq) & 7) == 0) {
+        const uint64_t vblocks = (waves * (d / 8) + 255) / 256;
+        if (vblocks > 0x7fffffffull) return hipErrorInvalidValue;
+        if (d == 64)
+            hipLaunchKernelGGL(quant_append_vec_kernel<8>, dim3(unsigned(vblocks)), b, 0, stream,
+                               static_cast<const u32x4 *>(nw), dtype, pos, cq, cs, planes, bucket, new_rows);
+        else
+            hipLaunchKernelGGL(quant_append_vec_kernel<16>, dim3(unsigned(vblocks)), b, 0, stream,
+                               static_cast<const u32x4 *>(nw), dtype, pos, cq, cs, planes, bucket, new_rows);
+        return hipGetLastError();
+    }
     if (d <= 128)
         hipLaunchKernelGGL(quant_append_kernel<2>, g, b, 0, stream, nw, dtype, pos, cq, cs, planes,
                            bucket, new_rows, d);

@@ -81,10 +81,13 @@ def test_dtypes_dims_and_wrap(torch_cuda, backend, dtype, d):
     assert np.array_equal(gs.view(np.uint32), ws_.view(np.uint32))
 
 
-def test_special_rows(torch_cuda, backend):
+@pytest.mark.parametrize("dtype,d", [(DTYPE_F32, 128), (DTYPE_BF16, 128), (DTYPE_BF16, 64),
+                                     (DTYPE_F16, 64)])
+def test_special_rows(torch_cuda, backend, dtype, d):
     """all-zero row -> q 0, scale 0; NaN ignored by the max and quantized to 0;
-    an Inf row gives scale Inf; subnormal-only rows; half-way ties."""
-    d, planes, bucket = 128, 8, 4
+    an Inf row gives scale Inf; subnormal-only rows; half-way ties. The 16-bit
+    cases (rows narrowed from the same f32 values) take the eight-a-lane kernel."""
+    planes, bucket = 8, 4
     rows = np.zeros((planes, d), np.float32)
     rows[1, :] = np.float32(1e-40)                       # subnormal
     rows[2, :5] = [np.nan, 1.0, -2.0, 0.5, -0.0]
@@ -94,11 +97,16 @@ def test_special_rows(torch_cuda, backend):
     rows[5, :] = -0.0
     rows[6, 0] = -np.inf
     rows[7, :] = np.float32(3.4e38)
+    if dtype == DTYPE_BF16:
+        rows = (rows.view(np.uint32) >> 16).astype(np.uint16)
+    elif dtype == DTYPE_F16:
+        with np.errstate(over="ignore"):
+            rows = rows.astype(np.float16).view(np.uint16)
     cq = np.full(planes * bucket * d, 9, np.int8)
     cs = np.full(planes * bucket, 2.0, np.float32)
-    gq, gs = run_append(torch_cuda, backend, rows, DTYPE_F32, 2, cq, cs, planes, bucket, 1, d,
+    gq, gs = run_append(torch_cuda, backend, rows, dtype, 2, cq, cs, planes, bucket, 1, d,
                         False)
-    wq, ws_ = oracle.kv_quant_append(rows, DTYPE_F32, 2, cq, cs, planes, bucket, 1, d)
+    wq, ws_ = oracle.kv_quant_append(rows, dtype, 2, cq, cs, planes, bucket, 1, d)
     assert np.array_equal(gq, wq)
     assert np.array_equal(gs.view(np.uint32), ws_.view(np.uint32))
 

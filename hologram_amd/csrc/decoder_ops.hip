@@ -6,6 +6,7 @@
 // and Gather are bit-exact with the reference CPU kernels, and RmsNorm differs
 // only by the order of its sum of squares (a tree here, sequential there).
 #include <hip/hip_runtime.h>
+#include <type_traits>
 
 #include <math.h>
 
@@ -281,14 +282,19 @@ struct TransposeArgs {
     uint64_t unit_bytes, units_per_row, units;
 };
 
+// kNarrow: unit counts and output dims below 2^32, so the coordinates come
+// from 32-bit divisions (a 64-bit one is a long instruction sequence).
+template <bool kNarrow>
 __global__ __launch_bounds__(256) void transpose_kernel(const TransposeArgs a) {
+    using idx_t = typename std::conditional<kNarrow, uint32_t, uint64_t>::type;
     const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
     for (uint64_t u = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; u < a.units; u += stride) {
-        const uint64_t row = u / a.units_per_row, piece = u % a.units_per_row;
-        uint64_t rem = row, src = piece * a.unit_bytes;
+        const idx_t row = idx_t(u) / idx_t(a.units_per_row), piece = idx_t(u) % idx_t(a.units_per_row);
+        idx_t rem = row;
+        uint64_t src = uint64_t(piece) * a.unit_bytes;
         for (int i = int(a.lead) - 1; i >= 0; --i) {
-            src += (rem % a.out_dims[i]) * a.in_stride[i];
-            rem /= a.out_dims[i];
+            src += uint64_t(rem % idx_t(a.out_dims[i])) * a.in_stride[i];
+            rem /= idx_t(a.out_dims[i]);
         }
         const uint8_t *s = a.in + src;
         uint8_t *d = a.out + u * a.unit_bytes;
@@ -401,7 +407,12 @@ hipError_t launch_transpose(const void *in, void *out, uint32_t rank, const uint
     a.unit_bytes = vec ? 16 : es;
     a.units_per_row = row_bytes / a.unit_bytes;
     a.units = total * es / a.unit_bytes;
-    hipLaunchKernelGGL(transpose_kernel, dim3(grid_for(a.units, 16384)), dim3(256), 0, stream, a);
+    bool narrow = a.units < (1ull << 32) && a.units_per_row < (1ull << 32);
+    for (uint32_t i = 0; i < a.lead; ++i) narrow = narrow && a.out_dims[i] < (1ull << 32);
+    if (narrow)
+        hipLaunchKernelGGL(transpose_kernel<true>, dim3(grid_for(a.units, 16384)), dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL(transpose_kernel<false>, dim3(grid_for(a.units, 16384)), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -60,7 +60,13 @@ namespace {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWps = 3;  // wavefronts per SIMD the registers are budgeted for
+// Wavefronts per SIMD the registers are budgeted for. Two (about 176 VGPRs,
+// 512 workgroups in the balanced form) run config 4's decode attention 5-7%
+// faster than three (168 VGPRs, 768 workgroups): 133k vs 125-127k tok/s.
+#ifndef HOLO_ATTN_WPS
+#define HOLO_ATTN_WPS 2
+#endif
+constexpr int kWps = HOLO_ATTN_WPS;
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBlock = 32;     // keys per wavefront step

@@ -403,6 +403,12 @@ hipError_t launch_skinny(const SkinnyArgs &g, uint8_t dtype, int mt, int steps, 
 // wave, across the four waves, then across K ranges in ks order), so a call
 // and a grouped launch with the same plan give the same bits. mt = 0: the
 // few-row kernels do not apply.
+// Workgroups per CU the K split aims for. One gives config 5's decode step
+// 1.068 ms against 1.091 with two (fewer partials for the epilogues to sum)
+// and 1.128 with four.
+#ifndef HOLO_SKINNY_WG_PER_CU
+#define HOLO_SKINNY_WG_PER_CU 1
+#endif
 SkinnyPlan matmul_skinny_plan(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype) {
     SkinnyPlan p;
     if (m == 0 || m > 64 || k == 0 || n == 0) return p;
@@ -412,7 +418,7 @@ SkinnyPlan matmul_skinny_plan(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype)
     if (bf16 ? (n % 8 != 0 || k % 32 != 0) : (n % 4 != 0 || k % 16 != 0)) return p;
     p.mt = m <= 16 ? 1 : m <= 32 ? 2 : 4;
     p.strips = (n + (bf16 ? 127 : 63)) / (bf16 ? 128 : 64);
-    // k steps per wave: the most that still gives every CU two workgroups
+    // k steps per wave: the most that still gives every CU its workgroups
     // (a long K range per workgroup keeps its loads streaming; a short one
     // fills the GPU when B is small)
     const int kstep = bf16 ? 32 : 16;
@@ -420,7 +426,7 @@ SkinnyPlan matmul_skinny_plan(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype)
     p.steps = max_steps;
     while (p.steps > 1 &&
            uint64_t(p.strips) * ((k + kWaves * p.steps * kstep - 1) / (kWaves * p.steps * kstep)) <
-               2u * uint64_t(skinny_cus()))
+               uint64_t(HOLO_SKINNY_WG_PER_CU) * skinny_cus())
         p.steps /= 2;
     p.kc = kWaves * p.steps * kstep;
     // 32-bit buffer ranges: all of A, and KC rows of B (plus the out-of-range

@@ -47,30 +47,26 @@ def _run(cmd: list[str]) -> None:
                            f"{proc.stdout}\n{proc.stderr}")
 
 
-def _compile(src: Path, obj_dir: Path = OBJ, extra: tuple = ()) -> Path:
+def _compile(src: Path, obj_dir: Path = OBJ) -> Path:
     out = obj_dir / (src.name + ".o")
     inc = [f"-I{ROOT / 'include'}", f"-I{CSRC}", f"-I{ROCM / 'include'}"]
     if src.suffix == ".hip":
-        _run([str(HIPCC), *HIP_FLAGS, *extra, *inc, "-c", str(src), "-o", str(out)])
+        _run([str(HIPCC), *HIP_FLAGS, *inc, "-c", str(src), "-o", str(out)])
     else:
         _run(["g++", *CXX_FLAGS, *inc, "-c", str(src), "-o", str(out)])
     return out
 
 
-def build(verbose: bool = True, out: Path = LIB, hip_defines: tuple = ()) -> Path:
-    """Compile every source under csrc/ and link libholo_hip.so (always rebuilds).
-
-    `out` and `hip_defines` (e.g. ("-DHOLO_ATTN_RING=3",)) build a variant
-    library elsewhere, for tuning sweeps; the default is the product build.
-    """
+def build(verbose: bool = True) -> Path:
+    """Compile every source under csrc/ and link libholo_hip.so (always rebuilds)."""
     if not HIPCC.exists():
         raise RuntimeError(f"hipcc not found at {HIPCC}")
-    obj_dir = OBJ if out == LIB else out.parent / (out.stem + "_obj")
+    out, obj_dir = LIB, OBJ
     obj_dir.mkdir(parents=True, exist_ok=True)
     srcs = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
     jobs = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(jobs) as ex:
-        objs = list(ex.map(lambda p: _compile(p, obj_dir, tuple(hip_defines)), srcs))
+        objs = list(ex.map(lambda p: _compile(p, obj_dir), srcs))
     tmp = out.with_suffix(".so.tmp")
     _run([str(HIPCC), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs),
           "-o", str(tmp), f"-L{ROCM / 'lib'}", "-lamdhip64",

@@ -63,10 +63,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // Wavefronts per SIMD the registers are budgeted for. Two (about 176 VGPRs,
 // 512 workgroups in the balanced form) run config 4's decode attention 5-7%
 // faster than three (168 VGPRs, 768 workgroups): 133k vs 125-127k tok/s.
-#ifndef HOLO_ATTN_WPS
-#define HOLO_ATTN_WPS 2
-#endif
-constexpr int kWps = HOLO_ATTN_WPS;
+constexpr int kWps = 2;
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBlock = 32;     // keys per wavefront step
@@ -1027,8 +1024,7 @@ uint32_t split_wgs() {
     return n;
 }
 
-// HOLO_ATTN_FORM=grid forces the grid form (tuning and tests). Otherwise the
-// balanced form is taken whenever the batch fits its LDS scan, except when
+// The balanced form is taken whenever the batch fits its LDS scan, except when
 // every plane fits one chunk and there are enough planes to spread over the
 // GPU: then the grid form is one workgroup per plane and needs no merge
 // launch (a decode step's short contexts: 64 planes of <= 1024 keys run in
@@ -1038,11 +1034,7 @@ constexpr uint32_t kGridMinPlanes = 32;
 uint32_t chunks_of(uint32_t bucket);
 
 bool use_split(uint32_t B, uint32_t Hkv, uint32_t bucket) {
-    static const bool grid_forced = [] {
-        const char *e = getenv("HOLO_ATTN_FORM");
-        return e && strcmp(e, "grid") == 0;
-    }();
-    if (grid_forced || B > kScanMax) return false;
+    if (B > kScanMax) return false;
     return !(chunks_of(bucket) == 1 && uint64_t(B) * Hkv >= kGridMinPlanes);
 }
 

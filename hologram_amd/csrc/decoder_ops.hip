@@ -368,6 +368,23 @@ hipError_t launch_rope(const void *x, const void *cs, const void *sn, void *out,
     return hipGetLastError();
 }
 
+// The multi-row attention's precondition, checked where the lengths live: a
+// prompt's earlier rows need cache slots that a ring wrap (lens > bucket) has
+// already overwritten with later rows, so such a length raises bit 2 of *err.
+__global__ __launch_bounds__(256) void lens_within_kernel(const uint32_t *__restrict__ lens,
+                                                          uint32_t n, uint32_t bucket,
+                                                          int *__restrict__ err) {
+    bool bad = false;
+    for (uint32_t i = threadIdx.x; i < n; i += 256) bad = bad || lens[i] > bucket;
+    if (bad) atomicOr(err, 2);
+}
+
+hipError_t launch_lens_within(const uint32_t *lens, uint32_t n, uint32_t bucket, int *err,
+                              hipStream_t stream) {
+    hipLaunchKernelGGL(lens_within_kernel, dim3(1), dim3(256), 0, stream, lens, n, bucket, err);
+    return hipGetLastError();
+}
+
 hipError_t launch_gather(const void *data, const void *idx, void *out, uint64_t outer,
                          uint64_t axis_dim, uint64_t num_idx, uint64_t row_bytes, bool i64,
                          int *err, hipStream_t stream) {

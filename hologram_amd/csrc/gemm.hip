@@ -284,20 +284,10 @@ constexpr int kBigM = 256, kBigN = 256, kBigK = 64, kLdk = kBigK + 8;
 // with the DMA kernel's 256x128 tiles against the 128x128 / 64x64 kernel:
 // 4096x2048x512 (32 tiles) 26.2 vs 34.4 us, 2048^3 (64 tiles) 28.1 vs 46.8 us;
 // at 16 tiles it no longer pays (2048x8192x512: 89.0 vs 83.9 us).
-#ifndef HOLO_BIG_MIN_TILES
-#define HOLO_BIG_MIN_TILES 32
-#endif
-// 1: large tiles run gemm_bf16_dma256/128_kernel (LDS DMA, transposing B reads);
-// 0: gemm_bf16_big_kernel (register staging, B transposed with permutes)
-#ifndef HOLO_GEMM_DMA
-#define HOLO_GEMM_DMA 1
-#endif
+constexpr uint64_t kBigMinTiles = 32;
 // the DMA kernel takes 256x128 tiles when there are at most this many of them
 // (one per CU)
-#ifndef HOLO_DMA_NARROW_MAX
-#define HOLO_DMA_NARROW_MAX 256
-#endif
-constexpr uint64_t kDmaNarrowMax = HOLO_DMA_NARROW_MAX;
+constexpr uint64_t kDmaNarrowMax = 256;
 
 __device__ __forceinline__ void tile_coords(uint32_t wg, uint32_t nwg, uint32_t tiles_m,
                                             uint32_t tiles_n, uint32_t *tm, uint32_t *tn) {
@@ -314,204 +304,6 @@ __device__ __forceinline__ void tile_coords(uint32_t wg, uint32_t nwg, uint32_t 
     *tn = in_group / gsize;
 }
 
-__global__ __launch_bounds__(256, 1) void gemm_bf16_big_kernel(const uint16_t *__restrict__ A,
-                                                              const uint16_t *__restrict__ B,
-                                                              uint16_t *__restrict__ C, uint32_t M,
-                                                              uint32_t N, uint32_t K) {
-    __shared__ uint16_t lds[2][2][kBigM][kLdk];   // [stage][A | Bt][row][k]
-    const uint32_t tiles_m = M / kBigM, tiles_n = N / kBigN;
-    uint32_t tm, tn;
-    tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, &tm, &tn);
-    const uint32_t m0 = tm * kBigM, n0 = tn * kBigN;
-
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
-    const int lr = lane & 31, lg = lane >> 5;
-
-    // global -> register slab loads
-    const int arow = tid >> 3, akc = (tid & 7) * 8;           // A: 8 threads per 128-byte row
-    // B: an 8x8 block (k 8bkb.., n 8bnb..). kb varies fastest, so the 8 lanes an
-    // LDS store cycle serves write 8 different 16-byte chunks of one Bt row
-    // (rows 8 apart share banks once rows are 16-byte aligned).
-    const int bkb = tid & 7, bnb = tid >> 3;
-    // Buffer loads against a resource re-based at every slab: one VGPR offset
-    // per operand, row strides as scalar offsets, 32-bit offsets for any
-    // matrix size (the launcher keeps 256 rows of A and 64 rows of B below 2 GiB).
-    const uint32_t a_voff = (uint32_t(arow) * K + akc) * 2u;
-    const uint32_t b_voff = (uint32_t(8 * bkb) * N + 8 * bnb) * 2u;
-    // two register sets: set t & 1 stages slab t
-    u32x4 ra[2][8], rb[2][8];
-    auto gload = [&](int set, uint32_t k0) {
-        const auto rsa = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint16_t *>(A + uint64_t(m0) * K + k0), 0, int(512u * K), 0x00020000);
-        const auto rsb = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint16_t *>(B + uint64_t(k0) * N + n0), 0, int(128u * N), 0x00020000);
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            ra[set][i] = __builtin_amdgcn_raw_buffer_load_b128(rsa, a_voff, int(64u * K) * i, 0);
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            rb[set][j] = __builtin_amdgcn_raw_buffer_load_b128(rsb, b_voff, int(2u * N) * j, 0);
-    };
-    auto lstore = [&](int st, int set) {
-        const u32x4 *xb = rb[set];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4 *>(&lds[st][0][arow + 32 * i][akc]) = ra[set][i];
-        // transpose the 8x8 block: column c gets (k 0..7) as 4 dwords of k pairs
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
-            u32x4 o;
-            o.x = __builtin_amdgcn_perm(xb[1][c >> 1], xb[0][c >> 1], sel);
-            o.y = __builtin_amdgcn_perm(xb[3][c >> 1], xb[2][c >> 1], sel);
-            o.z = __builtin_amdgcn_perm(xb[5][c >> 1], xb[4][c >> 1], sel);
-            o.w = __builtin_amdgcn_perm(xb[7][c >> 1], xb[6][c >> 1], sel);
-            *reinterpret_cast<u32x4 *>(&lds[st][1][8 * bnb + c][8 * bkb]) = o;
-        }
-    };
-
-    f32x16 acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-    // Software pipeline per 64-deep slab s (LDS buffer s & 1), k-steps kk = 0..3.
-    // When slab s starts, register set (s+1) & 1 holds slab s+1 and set s & 1
-    // is receiving slab s+2. With one wave per SIMD nothing else fills the MFMA
-    // pipe, so every other instruction is placed in the shadow of a running
-    // MFMA (sched_group_barrier: 0x008 MFMA, 0x100 LDS read, 0x200 LDS write,
-    // 0x020 global read, 0x002 VALU):
-    //   kk = 0, 1: LDS fragments of kk+1, one read between MFMAs
-    //   kk = 2:    fragments of kk = 3, then slab s+1 goes into the other LDS
-    //              buffer (its last readers passed the previous barrier), its
-    //              stores spread over the first 12 MFMAs so the last 4 cover
-    //              their completion
-    //   barrier
-    //   kk = 3:    fragments of slab s+1's kk = 0, and the global loads of slab
-    //              s+3 into the set just stored (two slabs of MFMAs to land),
-    //              between the MFMAs
-    bf16x8 af[2][4], bfr[2][4];
-    auto fload = [&](int st, int kk, int fb) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            af[fb][i] = *reinterpret_cast<const bf16x8 *>(&lds[st][0][wm + 32 * i + lr][kk + 8 * lg]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            bfr[fb][j] = *reinterpret_cast<const bf16x8 *>(&lds[st][1][wn + 32 * j + lr][kk + 8 * lg]);
-    };
-    auto mfmas = [&](int fb) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[fb][i], bfr[fb][j], acc[i][j], 0, 0, 0);
-    };
-    // one fragment read after each of the first 8 MFMAs
-    auto mix_reads = [] {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-    };
-
-    // One slab. set: (s+1) & 1 as a constant. store: slab s+1 exists (store
-    // it, read its first fragments); load: slab s+3 exists (issue its global
-    // loads). In the main loop all three are constants, so the body is one
-    // basic block, which the interleaving needs.
-    auto slab = [&](uint32_t s, auto set, auto store, auto load) {
-        constexpr int kSet = decltype(set)::value;
-        const int cur = s & 1;
-        fload(cur, 16, 1);
-        mfmas(0);
-        mix_reads();
-        __builtin_amdgcn_sched_barrier(0);
-        fload(cur, 32, 0);
-        mfmas(1);
-        mix_reads();
-        __builtin_amdgcn_sched_barrier(0);
-        fload(cur, 48, 1);
-        mfmas(0);
-        if (store) {
-            lstore(cur ^ 1, kSet);
-            // 8 reads up front; A stores (plain) after MFMAs 1-4, B stores (4
-            // perms each) after MFMAs 5-12; MFMAs 13-16 cover completion
-            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-                __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        if (store) {
-            __syncthreads();
-            fload(cur ^ 1, 0, 0);
-        }
-        mfmas(1);
-        if (load) {
-            gload(kSet, (s + 3) * kBigK);
-            // 8 fragment reads then 16 global loads, two per MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    using yes = std::integral_constant<bool, true>;
-    using no = std::integral_constant<bool, false>;
-    using set0 = std::integral_constant<int, 0>;
-    using set1 = std::integral_constant<int, 1>;
-
-    const uint32_t nk = K / kBigK;   // even, >= 4
-    gload(0, 0);
-    gload(1, kBigK);
-    lstore(0, 0);
-    gload(0, 2 * kBigK);
-    __syncthreads();
-    fload(0, 0, 0);
-    uint32_t s = 0;
-    for (; s + 4 < nk; s += 2) {
-        slab(s, set1{}, yes{}, yes{});
-        slab(s + 1, set0{}, yes{}, yes{});
-    }
-    // the last four slabs (nk is even and >= 4, so s = nk - 4)
-    slab(s, set1{}, yes{}, yes{});
-    slab(s + 1, set0{}, yes{}, no{});
-    slab(s + 2, set1{}, yes{}, no{});
-    slab(s + 3, set0{}, no{}, no{});
-
-    // 32x32 D layout: acc[r] is row 8(r/4) + 4*lg + r%4, column lr. One base
-    // pointer per lane; the scheduling barrier keeps each tile's addresses local
-    // (hoisting all 256 of them would spill).
-    uint16_t *cbase = C + uint64_t(m0 + wm + 4 * lg) * N + n0 + wn + lr;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            uint16_t *ct = cbase + uint64_t(32 * i) * N + 32 * j;
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                ct[uint64_t(8 * (r >> 2) + (r & 3)) * N] = uint16_t(__float_as_uint(acc[i][j][r]) >> 16);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-}
-
 // ------------------------------------------- bf16, large tiles, LDS DMA ----
 // 256 x BN workgroup tiles (BN = 256, or 128 when 256-wide tiles would leave
 // CUs idle), four wavefronts of 128 x BN/2 on v_mfma_f32_32x32x16_bf16, 32-deep
@@ -525,8 +317,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_big_kernel(const uint16_t *_
 // and lane j receives rows k0 .. k0+3 of column n0 + j. No operand passes
 // through registers on its way to LDS. One barrier per slab, placed between
 // the slab's two k-steps so the MFMAs already issued cover it. The MFMA order
-// per output element is the same as gemm_bf16_big_kernel's (k ascending in
-// steps of 16), so the results are identical.
+// per output element is k ascending in steps of 16.
 constexpr int kDmaK = 32, kDmaStages = 4;
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
@@ -895,12 +686,12 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_pair_kernel(const DmaGro
 
 // Whether the DMA kernel takes a product (bf16, 16-byte aligned operands
 // checked by the caller): K a multiple of 128 and >= 256, at least
-// HOLO_BIG_MIN_TILES 256x256 tiles, and 256 rows of A / 32 rows of B within
+// kBigMinTiles 256x256 tiles, and 256 rows of A / 32 rows of B within
 // a 32-bit buffer range.
 bool dma_applies(uint32_t m, uint32_t k, uint32_t n) {
     return m % kBigM == 0 && n % kBigN == 0 && k % (2 * kBigK) == 0 && k >= 4 * kBigK &&
            k < (1u << 22) && n < (1u << 24) &&
-           uint64_t(m / kBigM) * (n / kBigN) >= HOLO_BIG_MIN_TILES;
+           uint64_t(m / kBigM) * (n / kBigN) >= kBigMinTiles;
 }
 
 hipError_t launch_dma(DmaGroup g, hipStream_t stream) {
@@ -963,11 +754,10 @@ hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint
         }                                                                                        \
     } while (0)
     if (dtype == 7) {
-        // large aligned problems: at least HOLO_BIG_MIN_TILES 256x256 tiles, K a
+        // large aligned problems: at least kBigMinTiles 256x256 tiles, K a
         // multiple of 128 and >= 256, and 256 rows of A / 64 rows of B within a
         // 32-bit buffer range
         if ((al & 15) == 0 && dma_applies(m, k, n)) {
-#if HOLO_GEMM_DMA
             DmaGroup g{};
             g.a = static_cast<const uint16_t *>(a);
             g.m = m;
@@ -977,12 +767,6 @@ hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint
             g.c[0] = static_cast<uint16_t *>(c);
             g.n[0] = n;
             return launch_dma(g, stream);
-#else
-            hipLaunchKernelGGL(gemm_bf16_big_kernel, dim3((m / kBigM) * (n / kBigN)), dim3(256), 0,
-                               stream, static_cast<const uint16_t *>(a),
-                               static_cast<const uint16_t *>(b), static_cast<uint16_t *>(c), m, n, k);
-#endif
-            return hipGetLastError();
         }
         const bool fast = (al & 15) == 0 && k % BK16 == 0 && n % 8 == 0;
         HOLO_GEMM_LAUNCH(gemm_bf16_kernel, uint16_t);
@@ -1019,7 +803,7 @@ hipError_t launch_matmul_pair_tiled(const void *a, uint32_t m, uint32_t k, const
 }
 
 bool matmul_group_tiled_applies(uint32_t m, uint32_t k, const uint32_t *n, int nseg) {
-    if (!HOLO_GEMM_DMA || nseg < 1 || nseg > kSkinnyMaxSeg) return false;
+    if (nseg < 1 || nseg > kSkinnyMaxSeg) return false;
     for (int i = 0; i < nseg; ++i)
         if (!dma_applies(m, k, n[i])) return false;
     return true;

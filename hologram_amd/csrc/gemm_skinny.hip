@@ -406,9 +406,7 @@ hipError_t launch_skinny(const SkinnyArgs &g, uint8_t dtype, int mt, int steps, 
 // Workgroups per CU the K split aims for. One gives config 5's decode step
 // 1.068 ms against 1.091 with two (fewer partials for the epilogues to sum)
 // and 1.128 with four.
-#ifndef HOLO_SKINNY_WG_PER_CU
-#define HOLO_SKINNY_WG_PER_CU 1
-#endif
+constexpr uint32_t kSkinnyWgPerCu = 1;
 SkinnyPlan matmul_skinny_plan(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype) {
     SkinnyPlan p;
     if (m == 0 || m > 64 || k == 0 || n == 0) return p;
@@ -426,7 +424,7 @@ SkinnyPlan matmul_skinny_plan(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype)
     p.steps = max_steps;
     while (p.steps > 1 &&
            uint64_t(p.strips) * ((k + kWaves * p.steps * kstep - 1) / (kWaves * p.steps * kstep)) <
-               uint64_t(HOLO_SKINNY_WG_PER_CU) * skinny_cus())
+               uint64_t(kSkinnyWgPerCu) * skinny_cus())
         p.steps /= 2;
     p.kc = kWaves * p.steps * kstep;
     // 32-bit buffer ranges: all of A, and KC rows of B (plus the out-of-range

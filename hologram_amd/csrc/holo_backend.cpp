@@ -97,7 +97,8 @@ bool resolve(const SlotTable &st, const holo_buffer_ref &r, View *v) {
     uint64_t len, key;
     if (!st.lookup(r.slot, &p, &len, &key)) return false;
     const uint64_t start = r.offset < len ? r.offset : len;
-    const uint64_t end = r.length == 0 ? len : (start + r.length < len ? start + r.length : len);
+    // (saturating: a length past the slot's end, however large, ends at len)
+    const uint64_t end = (r.length == 0 || r.length > len - start) ? len : start + r.length;
     v->base = p + start;
     v->bytes = end - start;
     v->key = key;
@@ -224,8 +225,14 @@ int do_unary(holo_backend *be, const SlotTable &st, uint32_t tag, const holo_una
 
 // The backend's split-K scratch grows to the largest request; the old buffer
 // is released only after the stream has drained (kernels may still read it).
+// Never under stream capture: a captured graph would hold the freed buffer
+// (a session's capture is preceded by an eager walk that sizes it).
 int ensure_scratch(holo_backend *be, size_t bytes, const char *op) {
     if (bytes <= be->scratch_bytes) return HOLO_OK;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(be->stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+        return fail(HOLO_ERR_DISPATCH,
+                    std::string(op) + ": scratch would grow under stream capture; walk once eagerly first");
     if (be->scratch) {
         (void)hipStreamSynchronize(be->stream);
         (void)hipFree(be->scratch);
@@ -415,16 +422,42 @@ int dispatch_group_impl(holo_backend *be, const SlotTable &st, const holo::Group
             ns[i] = s.n;
             cs[i] = e.seg[i].out;
         }
+        uintptr_t al = reinterpret_cast<uintptr_t>(a.base);
+        for (size_t i = 0; i < nseg; ++i)
+            al |= reinterpret_cast<uintptr_t>(ss[i].b) | reinterpret_cast<uintptr_t>(cs[i]);
+        if (plain && (al & 15) != 0) {
+            // operands the grouped kernel's 16-byte loads cannot take: each
+            // product on its own through the general MatMul, epilogue in place
+            for (size_t i = 0; i < nseg; ++i) {
+                HOLO_TRY(ensure_scratch(be, holo::matmul_scratch_bytes(g.m, g.k, ns[i], g.dtype), op));
+                HOLO_TRY(launched(holo::launch_matmul(a.base, ss[i].b, cs[i], g.m, g.k, ns[i], g.dtype,
+                                                      be->scratch, be->stream),
+                                  op));
+                if (g.segs[i].base == holo::kEpiStore) continue;
+                holo::TileEpi te;
+                te.kind = g.segs[i].base;
+                te.act = g.segs[i].act;
+                te.lut = e.seg[i].lut;
+                te.residual = e.seg[i].residual;
+                HOLO_TRY(launched(holo::launch_tile_epilogue(cs[i], uint64_t(g.m) * ns[i], bf16, te,
+                                                             be->stream),
+                                  op));
+            }
+            return HOLO_OK;
+        }
         if (plain && holo::matmul_group_tiled_applies(g.m, g.k, ns, int(nseg))) {
-            // residual adds ride in the tiled kernel's store
+            // residual adds ride in the tiled kernel's store where the
+            // residual suits its 16-byte loads; otherwise they run in place after
             const void *rs[holo::kSkinnyMaxSeg] = {};
             for (size_t i = 0; i < nseg; ++i)
-                if (g.segs[i].base == holo::kEpiAdd) rs[i] = e.seg[i].residual;
+                if (g.segs[i].base == holo::kEpiAdd && ns[i] < (1u << 21) &&
+                    (reinterpret_cast<uintptr_t>(e.seg[i].residual) & 15) == 0)
+                    rs[i] = e.seg[i].residual;
             HOLO_TRY(launched(holo::launch_matmul_group_tiled(a.base, g.m, g.k, ss, cs, int(nseg),
                                                               be->stream, rs),
                               op));
             for (size_t i = 0; i < nseg; ++i) {
-                if (g.segs[i].base == holo::kEpiStore || g.segs[i].base == holo::kEpiAdd) continue;
+                if (g.segs[i].base == holo::kEpiStore || rs[i]) continue;
                 holo::TileEpi te;
                 te.kind = g.segs[i].base;
                 te.act = g.segs[i].act;
@@ -694,6 +727,10 @@ int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attentio
         // No key can be visible: the pinned zero vector (pinned_semantics.rs).
         return launched(holo::launch_fill_zero(out.base, qn * es, be->stream), op);
     }
+    if (q_rows > 1)
+        HOLO_TRY(launched(holo::launch_lens_within(a.lens, c.batch, c.bucket_rows, be->dev_err,
+                                                   be->stream),
+                          op));
     return launched(holo::launch_attn_i8(a, be->scratch, be->stream), op);
 }
 
@@ -1159,6 +1196,10 @@ bool fused_act_supported(uint32_t act, uint8_t dtype, bool after_add) {
 hipStream_t backend_stream(const holo_backend *be) { return be->stream; }
 void set_backend_stream(holo_backend *be, hipStream_t s) { be->stream = s; }
 int backend_device(const holo_backend *be) { return be->device; }
+void swap_scratch(holo_backend *be, void **ptr, size_t *bytes) {
+    std::swap(be->scratch, *ptr);
+    std::swap(be->scratch_bytes, *bytes);
+}
 
 }  // namespace holo
 
@@ -1248,9 +1289,14 @@ int holo_hip_synchronize(holo_backend *be) {
     if (e != hipSuccess) return fail(HOLO_ERR_DISPATCH, std::string("synchronize: ") + hipGetErrorString(e));
     if (flag) {
         (void)hipMemcpy(be->dev_err, &kZero, sizeof(int), hipMemcpyHostToDevice);
-        return fail(HOLO_ERR_SLOT_OUT_OF_RANGE,
-                    "gather: an index is outside [-axis_dim, axis_dim) (reported by the device; "
-                    "its output row was zeroed)");
+        if (flag & 1)
+            return fail(HOLO_ERR_SLOT_OUT_OF_RANGE,
+                        "gather: an index is outside [-axis_dim, axis_dim) (reported by the device; "
+                        "its output row was zeroed)");
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    "attention_i8_rows: a length exceeds bucket_rows (reported by the device): "
+                    "after a ring wrap the earlier rows' keys are overwritten, so a causal "
+                    "multi-row result does not exist");
     }
     return HOLO_OK;
 }

@@ -31,6 +31,10 @@ int decode_call(const uint8_t *wire, size_t len, holo_kernel_call *out, size_t *
 hipStream_t backend_stream(const holo_backend *be);
 void set_backend_stream(holo_backend *be, hipStream_t s);
 int backend_device(const holo_backend *be);
+// Exchange the backend's split-K scratch (pointer, size) with the caller's.
+// A session swaps its own scratch in for its walk and back out after it, so
+// a captured walk's graph holds memory only that session grows or frees.
+void swap_scratch(holo_backend *be, void **ptr, size_t *bytes);
 // A fused few-row MatMul group (the session's device fusion): products that
 // share A, each finished by its epilogue (holo_kernels.h EpiSeg) in one more
 // launch. Operands stay BufferRefs, resolved through the slot table at

@@ -59,6 +59,9 @@ hipError_t launch_rmsnorm(const void *x, const void *gamma, void *out, uint32_t 
 hipError_t launch_rope(const void *x, const void *cs, const void *sn, void *out, uint32_t head_dim,
                        uint64_t n, bool bf16, hipStream_t stream);
 // Row gather; an out-of-range index zeroes its row and sets *err (device int).
+// Raise bit 2 of *err if any of lens[0..n) exceeds bucket (multi-row attention).
+hipError_t launch_lens_within(const uint32_t *lens, uint32_t n, uint32_t bucket, int *err,
+                              hipStream_t stream);
 hipError_t launch_gather(const void *data, const void *idx, void *out, uint64_t outer,
                          uint64_t axis_dim, uint64_t num_idx, uint64_t row_bytes, bool i64,
                          int *err, hipStream_t stream);

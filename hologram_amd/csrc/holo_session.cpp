@@ -92,6 +92,9 @@ struct Cursor {
 };
 
 // port_bytes_per_element (session.rs): the element width of a port's dtype.
+uint64_t sat_add(uint64_t a, uint64_t b) { return a > UINT64_MAX - b ? UINT64_MAX : a + b; }
+uint64_t sat_mul(uint64_t a, uint64_t b) { return b && a > UINT64_MAX / b ? UINT64_MAX : a * b; }
+
 uint64_t port_bytes(uint8_t dt) {
     switch (dt) {
         case 0: case 1: case HOLO_DTYPE_I8: return 1;   // bool, u8, i8
@@ -339,6 +342,12 @@ struct holo_session {
     std::vector<Node> nodes;                      // the walk, in order
     std::vector<holo::GroupDesc> groups;          // fused few-row MatMul groups
     float *norm_arena = nullptr;                  // RmsNorm statistics of fused norms
+    // split-K partials of this session's walks (few-row MatMuls, attention):
+    // its own, so no other session or direct dispatch on the same backend
+    // frees or shares what a captured graph of this walk reads and writes
+    void *scratch = nullptr;
+    size_t scratch_bytes = 0;
+    void *graph_scratch = nullptr;                // the scratch the graph was captured with
 };
 
 namespace {
@@ -841,6 +850,7 @@ void release(holo_session *s) {
     if (s->stream) (void)hipStreamSynchronize(s->stream);
     if (s->graph) (void)hipGraphExecDestroy(s->graph);
     if (s->norm_arena) (void)hipFree(s->norm_arena);
+    if (s->scratch) (void)hipFree(s->scratch);
     if (s->const_arena) (void)hipFree(s->const_arena);
     if (s->work_arena) (void)hipFree(s->work_arena);
     if (s->stream) (void)hipStreamDestroy(s->stream);
@@ -925,6 +935,25 @@ int load_impl(holo_backend *be, const uint8_t *bytes, size_t len, uint32_t flags
         for (size_t i = 0; i < all.size(); ++i) all[i] = uint32_t(i);
         s->plan.push_back(std::move(all));
     }
+    // --- slot ids are host-side indices from here on: every call's write
+    // operands and every port must name a real slot (an absent write, or a
+    // port on the absent sentinel, is a malformed archive, not an operand to skip)
+    {
+        std::vector<holo_buffer_ref> rd0, wr0;
+        for (size_t i = 0; i < s->calls.size(); ++i) {
+            call_operands(s->calls[i], &rd0, &wr0);
+            for (auto &b : wr0)
+                if (b.slot == HOLO_SLOT_ABSENT)
+                    return set_error(HOLO_ERR_SLOT_OUT_OF_RANGE,
+                                     "session_load: kernel call " + std::to_string(i) +
+                                         " writes the absent slot");
+        }
+        for (auto *ports : {&s->inputs, &s->outputs})
+            for (auto &p : *ports)
+                if (p.slot == HOLO_SLOT_ABSENT)
+                    return set_error(HOLO_ERR_SLOT_OUT_OF_RANGE,
+                                     "session_load: port '" + p.name + "' names the absent slot");
+    }
     // --- the loader's epilogue fusion (session.rs:493-509)
     if (!(flags & HOLO_SESSION_NO_EPILOGUE_FUSION)) fuse_matmul_epilogue(s->calls, s->plan, s->outputs);
     // --- weights (fingerprint -> body), constants
@@ -958,6 +987,9 @@ int load_impl(holo_backend *be, const uint8_t *bytes, size_t len, uint32_t flags
             const uint8_t tag = c.get<uint8_t>();
             const uint32_t slot = c.get<uint32_t>();
             (void)c.get<uint8_t>();   // dtype
+            if (c.ok && slot == HOLO_SLOT_ABSENT)
+                return set_error(HOLO_ERR_SLOT_OUT_OF_RANGE,
+                                 "session_load: constant " + std::to_string(i) + " names the absent slot");
             if (tag == 0) {
                 const uint32_t bl = c.get<uint32_t>();
                 const uint8_t *body = c.take(bl);
@@ -996,17 +1028,22 @@ int load_impl(holo_backend *be, const uint8_t *bytes, size_t len, uint32_t flags
     for (const auto &call : s->calls) {
         call_operands(call, &rd, &wr);
         for (auto *v : {&rd, &wr})
-            for (auto &b : *v) sz[b.slot] = std::max(sz[b.slot], b.offset + b.length);
+            for (auto &b : *v) sz[b.slot] = std::max(sz[b.slot], sat_add(b.offset, b.length));
     }
     for (auto *ports : {&s->inputs, &s->outputs})
-        for (auto &p : *ports) sz[p.slot] = std::max(sz[p.slot], p.count * port_bytes(p.dtype));
+        for (auto &p : *ports) sz[p.slot] = std::max(sz[p.slot], sat_mul(p.count, port_bytes(p.dtype)));
     for (auto &k : consts) {
         sz[k.slot] = std::max(sz[k.slot], k.len);
         is_const[k.slot] = 1;
     }
     for (auto &p : s->inputs) is_input[p.slot] = 1;
     for (auto &p : s->outputs) is_output[p.slot] = 1;
-    for (auto &v : sz) v = std::max<uint64_t>(v, 64), v = (v + 63) / 64 * 64;
+    for (auto &v : sz) {
+        // a slot no device could hold is refused here, before any rounding wraps
+        if (v > (uint64_t(1) << 46))
+            return set_error(HOLO_ERR_SLOT_OUT_OF_RANGE, "session_load: a slot is referenced beyond 2^46 bytes");
+        v = std::max<uint64_t>(v, 64), v = (v + 63) / 64 * 64;
+    }
     // --- device memory: one arena for constants, one for every other slot,
     // each slot 256-byte aligned
     uint64_t cbytes = 0, wbytes = 0;
@@ -1053,7 +1090,7 @@ plan_moves:
         if (call.tag == HOLO_OP_KV_CACHE_WRITE) {
             auto &k = call.u.kv_write;
             const uint32_t cs = k.cache.slot, os = k.output.slot;
-            if (cs == os || readers[cs] != 1 || is_output[cs] || is_const[cs] || k.cache.offset != 0 ||
+            if (cs == HOLO_SLOT_ABSENT || cs == os || readers[cs] != 1 || is_output[cs] || is_const[cs] || k.cache.offset != 0 ||
                 k.output.offset != 0)
                 continue;
             if (k.new_rows_buf.slot == cs || k.pos.slot == cs) continue;
@@ -1063,7 +1100,7 @@ plan_moves:
             auto &k = call.u.kv_quant_append;
             const uint32_t cq = k.cache.slot, cs = k.cache_scales.slot;
             const uint32_t oq = k.output.slot, os = k.output_scales.slot;
-            if (cq == oq || cs == os || cq == cs || readers[cq] != 1 || readers[cs] != 1 ||
+            if (cq == HOLO_SLOT_ABSENT || cs == HOLO_SLOT_ABSENT || cq == oq || cs == os || cq == cs || readers[cq] != 1 || readers[cs] != 1 ||
                 is_output[cq] || is_output[cs] || is_const[cq] || is_const[cs] ||
                 k.cache.offset != 0 || k.cache_scales.offset != 0 || k.output.offset != 0 ||
                 k.output_scales.offset != 0)
@@ -1106,6 +1143,7 @@ int walk(holo_session *s) {
     for (auto &a : s->aliases) s->slots[a.first] = s->slots[a.second];
     const hipStream_t saved = holo::backend_stream(s->be);
     holo::set_backend_stream(s->be, s->stream);
+    holo::swap_scratch(s->be, &s->scratch, &s->scratch_bytes);   // the session's scratch in
     int rc = HOLO_OK;
     for (const Node &nd : s->nodes) {
         rc = nd.group >= 0 ? holo::dispatch_group(s->be, s->slots, s->groups[size_t(nd.group)])
@@ -1117,6 +1155,7 @@ int walk(holo_session *s) {
             break;
         }
     }
+    holo::swap_scratch(s->be, &s->scratch, &s->scratch_bytes);   // and out again
     holo::set_backend_stream(s->be, saved);
     return rc;
 }
@@ -1289,6 +1328,7 @@ int holo_hip_session_capture(holo_session *s) {
         return set_error(HOLO_ERR_DISPATCH, "session_capture: graph instantiation failed");
     }
     s->graph_slots = s->slots;
+    s->graph_scratch = s->scratch;
     return HOLO_OK;
 }
 
@@ -1300,6 +1340,9 @@ int holo_hip_session_replay(holo_session *s) {
     if (!same_bindings(now, s->graph_slots))
         return set_error(HOLO_ERR_DISPATCH,
                          "session_replay: an input was rebound since the capture; capture again");
+    if (s->scratch != s->graph_scratch)
+        return set_error(HOLO_ERR_DISPATCH,
+                         "session_replay: the session's scratch was reallocated since the capture; capture again");
     if (hipGraphLaunch(s->graph, s->stream) != hipSuccess)
         return set_error(HOLO_ERR_DISPATCH, "session_replay: graph launch failed");
     return HOLO_OK;

@@ -128,26 +128,12 @@ hipError_t launch_lut_u16(const uint16_t *table, const uint16_t *in, uint16_t *o
     if (n == 0) return hipSuccess;
     const bool aligned = ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
     const uint64_t nvec = aligned ? n / 8 : 0;
-    // HOLO_LUT_CFG selects a launch shape for tuning sweeps (0 = default).
-    static const int cfg = [] {
-        const char *e = getenv("HOLO_LUT_CFG");
-        return e ? atoi(e) : 0;
-    }();
-    if (nvec && nvec <= kDirectMaxVec && cfg == 0) {
+    if (nvec && nvec <= kDirectMaxVec) {
         hipLaunchKernelGGL(lut_direct_kernel, dim3(unsigned((nvec + 255) / 256)), dim3(256), 0,
                            stream, table, in, out, n, nvec);
         return hipGetLastError();
     }
-    switch (cfg) {
-        case 1: return launch<1024, 1>(table, in, out, n, nvec, stream);
-        case 2: return launch<1024, 2>(table, in, out, n, nvec, stream);
-        case 3: return launch<512, 2>(table, in, out, n, nvec, stream);
-        case 4: return launch<512, 4>(table, in, out, n, nvec, stream);
-        case 5: return launch<256, 4>(table, in, out, n, nvec, stream);
-        case 6: return launch<512, 16>(table, in, out, n, nvec, stream);
-        case 7: return launch<1024, 4>(table, in, out, n, nvec, stream);
-        default: return launch<1024, 8>(table, in, out, n, nvec, stream);
-    }
+    return launch<1024, 8>(table, in, out, n, nvec, stream);
 }
 
 }  // namespace holo

@@ -266,7 +266,11 @@ typedef struct holo_decode_attention_i8_call {
  * b's last row, and row t sees the first lens[b] - (q_rows - 1 - t) rows of its
  * planes (none when that is not positive), at most bucket_rows: the causal
  * visibility of DecodeAttentionValid's new rows, past prefix then min(qi + 1, new)
- * (src/cpu/float_kernels.rs:3926). q_rows = 1 is tag 123. */
+ * (src/cpu/float_kernels.rs:3926). q_rows = 1 is tag 123. With q_rows > 1 every
+ * lens[b] must be at most bucket_rows: once a multi-row append wraps the ring,
+ * later rows have overwritten slots the earlier rows must see. The lengths
+ * live on the device, so a violation is reported (UnsupportedOp) by the next
+ * holo_hip_synchronize. */
 typedef struct holo_attention_i8_rows_call {
     holo_decode_attention_i8_call attn;
     uint32_t q_rows;

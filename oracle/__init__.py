@@ -173,7 +173,11 @@ def attention_i8_rows(q, kq, ks, vq, vs, lens, B, T, H, Hkv, bucket, D, scale) -
     of sequence b a one-query decode over the first clamp(lens[b] - (T - 1 - t),
     0, bucket) rows of its planes. With lens[b] >= T this is
     DecodeAttentionValid{m = new = T, past = lens[b] - T} (float_kernels.rs:3926:
-    row qi sees the past prefix and min(qi + 1, new) new rows)."""
+    row qi sees the past prefix and min(qi + 1, new) new rows). With T > 1 every
+    lens[b] must be at most bucket: past a ring wrap the earlier rows' keys are
+    overwritten, and no causal result exists."""
+    if T > 1 and np.any(np.asarray(lens, np.int64)[:B] > bucket):
+        raise ValueError("attention_i8_rows: a length exceeds the bucket (ring wrapped)")
     q = np.ascontiguousarray(q, np.float32).reshape(B, T, H, D)
     out = np.zeros((B, T, H, D), np.float32)
     pl, ps = Hkv * bucket * D, Hkv * bucket
@@ -211,6 +215,16 @@ def matmul_ref_f64(a, b, m, k, n) -> np.ndarray:
     out = np.zeros(m * n, np.float32)
     lib().or_matmul_ref_f64(_p(a), _p(b), _p(out), m, k, n)
     return out
+
+
+def matmul_f64_blas(a, b, m, k, n) -> np.ndarray:
+    """The same f64 reference as matmul_ref_f64 (products and sums in f64,
+    one rounding to f32 at the end) through numpy's f64 BLAS, for graph-sized
+    products the scalar loop would take minutes on; only the order of the f64
+    sums differs."""
+    a64 = np.ascontiguousarray(a, np.float32).reshape(m, k).astype(np.float64)
+    b64 = np.ascontiguousarray(b, np.float32).reshape(k, n).astype(np.float64)
+    return (a64 @ b64).astype(np.float32).ravel()
 
 
 def max_rel_err(got, want) -> float:

@@ -230,8 +230,9 @@ class OracleSession:
             es = DT_BYTES[dt]
             a = self._f32(self._view(c["a"], m * k * es), dt)
             b = self._f32(self._view(c["b"], k * n * es), dt)
-            from . import FUSED_TO_LUT, build_table, fused_act_f32, matmul_ref_f64
-            v = self._f32(self._narrow(matmul_ref_f64(a, b, m, k, n), dt), dt)
+            from . import FUSED_TO_LUT, build_table, fused_act_f32, matmul_f64_blas, matmul_ref_f64
+            ref = matmul_ref_f64 if m * k * n <= (1 << 24) else matmul_f64_blas
+            v = self._f32(self._narrow(ref(a, b, m, k, n), dt), dt)
             if tag in (107, 108):
                 v = v + self._f32(self._view(c["residual"], m * n * es), dt)
             if tag == 106 and dt == BF16:

@@ -163,3 +163,43 @@ def test_decode_step_refusals():
     with pytest.raises(SlotOutOfRange):          # short operand
         validate(KernelCall.MatMul(MatMulCall(BufferRef(1, 0, 64), BufferRef(2), BufferRef(3),
                                               8, 8, 8, DTYPE_F32)), sizes)
+
+
+def _one_add_archive(out_slot=2, in_port_slot=0, const_slot=1):
+    w = HoloWriter()
+    w.inputs = [PortDescriptor("a", in_port_slot, 16, DTYPE_F32, [16])]
+    w.outputs = [PortDescriptor("out", 2, 16, DTYPE_F32, [16])]
+    w.constants = [ConstantEntry(const_slot, DTYPE_F32, np.arange(16, dtype=np.float32).tobytes())]
+    w.kernel_calls = [KernelCall.Add(BinaryCall(BufferRef(0, 0, 64), BufferRef(1, 0, 64),
+                                                BufferRef(out_slot, 0, 64), 16, 32, DTYPE_F32))]
+    w.exec_plan = [[0]]
+    return w.finish()
+
+
+ABSENT = 0xFFFFFFFF
+
+
+@pytest.mark.parametrize("where", ["output", "port", "constant"])
+def test_dry_load_refuses_the_absent_slot(where):
+    """Slot ids from the archive index host tables at load: an absent write
+    operand, port or constant is a malformed archive and comes back as an
+    error, never as an out-of-range index."""
+    kw = {"output": dict(out_slot=ABSENT), "port": dict(in_port_slot=ABSENT),
+          "constant": dict(const_slot=ABSENT)}[where]
+    HipSession(None, _one_add_archive())          # the well-formed twin loads
+    with pytest.raises(SlotOutOfRange):
+        HipSession(None, _one_add_archive(**kw))
+
+
+def test_view_length_past_the_slot_saturates():
+    """buf_range clamps the end of a view to its slot (buffer.rs:312-335). A
+    length near 2^64 must clamp, not wrap round to a huge view that passes the
+    size check: 16 f32 at offset 8 of a 64-byte slot have only 56 bytes."""
+    sizes = [64] * 4
+    call = KernelCall.Add(BinaryCall(BufferRef(1, 8, (1 << 64) - 4), BufferRef(2), BufferRef(3),
+                                     16, 32, DTYPE_F32))
+    with pytest.raises(SlotOutOfRange):
+        validate(call, sizes)
+    ok = KernelCall.Add(BinaryCall(BufferRef(1, 8, (1 << 64) - 4), BufferRef(2), BufferRef(3),
+                                   14, 32, DTYPE_F32))
+    validate(ok, sizes)                           # 14 f32 = 56 bytes fit

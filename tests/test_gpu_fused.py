@@ -247,3 +247,48 @@ def test_split_norm_is_bit_identical(torch_cuda, backend, m, feat, gamma, residu
         a, b = np.frombuffer(u, np.uint16), np.frombuffer(v, np.uint16)
         bad = np.flatnonzero(a != b)
         assert bad.size == 0, f"output {o}: {bad.size} of {a.size} differ, first at {bad[:4]}"
+
+
+def two_residual_products_archive(res_offset):
+    """Two large-M bf16 MatMulAdds sharing A, their residuals at a byte offset
+    of one constant slot: device fusion groups them into one tiled launch."""
+    m, k, n = 2048, 512, 1024
+    rng = np.random.default_rng(41)
+    a = narrow(rng.standard_normal(m * k) / np.sqrt(k), DTYPE_BF16)
+    b1, b2 = (narrow(rng.standard_normal(k * n), DTYPE_BF16) for _ in range(2))
+    res = narrow(rng.standard_normal(2 * m * n + 8), DTYPE_BF16)
+    from hologram_amd import ConstantEntry
+    w = HoloWriter()
+    w.outputs = [PortDescriptor("y1", 4, m * n, DTYPE_BF16, [m, n]),
+                 PortDescriptor("y2", 5, m * n, DTYPE_BF16, [m, n])]
+    w.constants = [ConstantEntry(s, DTYPE_BF16, x.tobytes()) for s, x in
+                   ((0, a), (1, b1), (2, b2), (3, res))]
+    mn2 = m * n * 2
+    w.kernel_calls = [
+        KernelCall.MatMulAdd(MatMulAddCall(
+            MatMulCall(BufferRef(0), BufferRef(1), BufferRef(4), m, k, n, DTYPE_BF16),
+            BufferRef(3, res_offset, mn2))),
+        KernelCall.MatMulAdd(MatMulAddCall(
+            MatMulCall(BufferRef(0), BufferRef(2), BufferRef(5), m, k, n, DTYPE_BF16),
+            BufferRef(3, res_offset + mn2, mn2))),
+    ]
+    w.exec_plan = [[0, 1]]
+    return w.finish()
+
+
+@pytest.mark.parametrize("res_offset", [0, 2])
+def test_grouped_tiled_products_with_any_residual_alignment(torch_cuda, backend, res_offset):
+    """A residual the grouped kernel's 16-byte loads cannot take (2-byte offset)
+    is added in place after the product instead; either way the grouped walk
+    equals the unfused one bit for bit."""
+    arch = two_residual_products_archive(res_offset)
+    outs = []
+    for flags in (0, NO_DEVICE_FUSION):
+        s = HipSession(backend, arch, flags=flags)
+        if flags == 0:
+            assert s.n_groups == 1
+        s.run()
+        s.synchronize()
+        outs.append([s.read_output(0), s.read_output(1)])
+        s.close()
+    assert outs[0] == outs[1]

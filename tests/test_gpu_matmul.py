@@ -75,19 +75,20 @@ def test_packed_b_refused(torch_cuda, backend):
                                                       4, 4, 4, DTYPE_F32, True)), ws)
 
 
-def run_mm_rows(torch, backend, m, k, n, seed, rows):
-    """bf16 MatMul on the device; f64 reference only on the sampled rows."""
+def run_mm_rows(torch, backend, m, k, n, seed, rows, dtype=DTYPE_BF16):
+    """MatMul on the device; f64 reference only on the sampled rows."""
     g = torch.Generator().manual_seed(seed)
-    a = (torch.randn(m, k, generator=g) / np.sqrt(k)).to(torch.bfloat16)
-    b = (torch.randn(k, n, generator=g) / np.sqrt(k)).to(torch.bfloat16)
+    tdt = torch.bfloat16 if dtype == DTYPE_BF16 else torch.float32
+    a = (torch.randn(m, k, generator=g) / np.sqrt(k)).to(tdt)
+    b = (torch.randn(k, n, generator=g) / np.sqrt(k)).to(tdt)
     ad, bd = a.cuda(), b.cuda()
-    out = torch.zeros(m, n, dtype=torch.bfloat16, device="cuda")
+    out = torch.zeros(m, n, dtype=tdt, device="cuda")
     ws = DeviceWorkspace()
     ws.bind(0, ad)
     ws.bind(1, bd)
     ws.bind(2, out)
     backend.dispatch(KernelCall.MatMul(MatMulCall(BufferRef(0), BufferRef(1), BufferRef(2), m, k, n,
-                                                  DTYPE_BF16)), ws)
+                                                  dtype)), ws)
     backend.synchronize()
     got = out[rows].float().cpu().numpy().reshape(-1)
     a32 = a[rows].float().numpy().reshape(-1).copy()
@@ -107,6 +108,17 @@ def test_matmul_large_tiles_sampled_rows(torch_cuda, backend, m, k, n):
     got, want = run_mm_rows(torch_cuda, backend, m, k, n, seed=m + n + k, rows=rows)
     err = oracle.max_rel_err(got, want)
     assert err <= 1e-2, f"normalized error {err:.3g}"
+
+
+@pytest.mark.parametrize("m,k,n", [(4096, 4096, 4096), (8192, 8192, 8192), (1024, 1024, 1024)])
+def test_matmul_f32_config_shapes_sampled_rows(torch_cuda, backend, m, k, n):
+    """Config 2's f32 squares at full size (the 128-tile kernel the bench times
+    at 4096^3 and 8192^3): every 128-row tile is sampled once at a varying
+    residue, plus the first 64 rows; every column is checked, bound 1e-5."""
+    rows = sorted({(t * 128 + (t * 37) % 128) % m for t in range(m // 128)} | set(range(0, 64)))
+    got, want = run_mm_rows(torch_cuda, backend, m, k, n, seed=m + 3, rows=rows, dtype=DTYPE_F32)
+    err = oracle.max_rel_err(got, want)
+    assert err <= 1e-5, f"normalized error {err:.3g}"
 
 
 SKINNY = [(1, 4096, 4096), (7, 96, 136), (16, 512, 256), (16, 544, 264), (17, 1024, 512),

@@ -82,9 +82,9 @@ def run_rows(torch, backend, B, T, H, Hkv, D, S, lens, seed, q_rows_op=True):
 @pytest.mark.parametrize("H,Hkv,D", [(8, 2, 64), (16, 4, 128), (4, 4, 64)])
 def test_attention_rows_parity(torch_cuda, backend, H, Hkv, D):
     B, T, S = 4, 9, 48
-    # the third sequence is shorter than its prompt rows; the fourth's rows run
-    # past the bucket (each row sees at most the bucket)
-    lens = [9, 40, 3, 53]
+    # the third sequence is shorter than its prompt rows; the fourth fills the
+    # bucket exactly
+    lens = [9, 40, 3, 48]
     got, want, _ = run_rows(torch_cuda, backend, B, T, H, Hkv, D, S, lens, seed=H + D)
     for b in range(B):
         for t in range(T):
@@ -110,6 +110,16 @@ def test_attention_prompt_tiles_parity(torch_cuda, backend, B, T, S, lens):
             else:
                 err = np.max(np.abs(got[b, t] - want[b, t])) / (np.max(np.abs(want[b, t])) + 1e-9)
                 assert err <= 1e-2, (b, t, err)
+
+
+def test_attention_rows_past_the_bucket_is_refused(torch_cuda, backend):
+    """A multi-row call whose length exceeds the bucket (a wrapped ring) has no
+    causal result: the device raises it and synchronize reports UnsupportedOp,
+    then the flag is clear again."""
+    from hologram_amd import UnsupportedOp
+    with pytest.raises(UnsupportedOp):
+        run_rows(torch_cuda, backend, 2, 4, 8, 2, 64, 16, [16, 17], seed=3)
+    backend.synchronize()
 
 
 def test_attention_rows_one_row_is_op_123(torch_cuda, backend):

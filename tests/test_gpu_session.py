@@ -257,3 +257,58 @@ def test_session_capture_replay_matches_eager(torch_cuda, backend):
         sess.close()
     for a, b in zip(*outs):
         assert a == b
+
+
+def test_captured_walk_survives_other_work_on_its_backend(torch_cuda, backend):
+    """A captured walk keeps the split-K scratch it was recorded with: a larger
+    session and a large direct few-row MatMul on the same backend in between
+    (each needing more scratch than the first session) must not move or free
+    it. Every replay equals the eager walk of the same inputs."""
+    from hologram_amd import MatMulCall
+    cfg = CFG
+    archive = build_decode_step(cfg, init_weights(cfg, seed=21))
+    big = DecoderConfig(layers=1, hidden=1024, heads=8, kv_heads=2, head_dim=128, ffn=4096,
+                        vocab=4000, batch=4, bucket=128)
+    big_archive = build_decode_step(big, init_weights(big, seed=22))
+
+    def fresh(c, arch):
+        s = HipSession(backend, arch)
+        P, S, Dh = c.planes, c.bucket, c.head_dim
+        for layer in range(c.layers):
+            for j, z in enumerate([bytes(P * S * Dh), bytes(P * S * 4)] * 2):
+                s.write_input(7 + 4 * layer + j, z)
+        for i, b in enumerate(step_inputs(c, 0, np.arange(c.batch) * 5)):
+            s.write_input(i, b)
+        return s
+
+    eager = fresh(cfg, archive)
+    eager.run()
+    eager.synchronize()
+    want = eager.read_output(1)
+    eager.close()
+
+    sess = fresh(cfg, archive)
+    sess.capture()
+    sess.synchronize()
+    for rnd in range(3):
+        other = fresh(big, big_archive)          # larger few-row products, own scratch
+        other.run()
+        other.synchronize()
+        other.close()
+        m, k, n = 16, 8192, 8192                 # a direct call that grows the backend's scratch
+        a = to_dev(torch_cuda, bf(np.ones(m * k, np.float32)))
+        b = to_dev(torch_cuda, bf(np.full(k * n, 2 ** -13, np.float32)))
+        c = torch_cuda.zeros(m * n * 2, dtype=torch_cuda.uint8, device="cuda")
+        ws = DeviceWorkspace()
+        ws.bind(1, a), ws.bind(2, b), ws.bind(3, c)
+        backend.dispatch(KernelCall.MatMul(MatMulCall(BufferRef(1), BufferRef(2), BufferRef(3),
+                                                      m, k, n, DTYPE_BF16)), ws)
+        backend.synchronize()
+        assert np.all(unbf(c.cpu().numpy().view(np.uint16)) == 1.0)
+        # the same step's inputs again: the caches were appended at the same ring row
+        for i, bb in enumerate(step_inputs(cfg, 0, np.arange(cfg.batch) * 5)):
+            sess.write_input(i, bb)
+        sess.replay()
+        sess.synchronize()
+        assert sess.read_output(1) == want, rnd
+    sess.close()

@@ -14,6 +14,7 @@ import pytest
 import oracle
 
 BF16, F16, F32 = oracle.DTYPE_BF16, oracle.DTYPE_F16, oracle.DTYPE_F32
+DTYPE_BF16, DTYPE_F16, DTYPE_F32 = BF16, F16, F32
 L = oracle.lib()
 
 
@@ -209,6 +210,80 @@ def test_kv_cache_write_ring_placement_brute_force(pos, new_rows):
     assert np.array_equal(got, want.reshape(-1))
 
 
+def _widen_independently(bits, dtype):
+    """bf16 = bits << 16, f16 through numpy's IEEE half, f32 as is."""
+    if dtype == DTYPE_BF16:
+        return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+    if dtype == DTYPE_F16:
+        return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
+    return np.asarray(bits, np.float32)
+
+
+@pytest.mark.parametrize("dtype", [DTYPE_BF16, DTYPE_F16, DTYPE_F32])
+@pytest.mark.parametrize("pos,new_rows", [(0, 1), (6, 1), (7, 1), (5, 3), (2**32 - 1, 4), (13, 8)])
+def test_kv_quant_append_is_quantizer_plus_ring_placement(dtype, pos, new_rows):
+    """or_kv_quant_append = the golden-pinned row quantizer (quantize_row_i8,
+    simd.rs:4755-4785) applied to each new row, placed as KvCacheWrite places
+    rows (kernels.rs:489-499): new row j of plane p, laid out [planes][new_rows][D],
+    lands at ring row (pos + j) % bucket; every other row is untouched; an
+    all-zero row writes q = 0 and scale 0 over whatever the slot held. Checked
+    against a brute-force placement and against the composition of the two
+    pinned oracle functions (quantizer, then kv_cache_write on bytes and scales)."""
+    planes, bucket, D = 3, 8, 32
+    rng = np.random.default_rng(pos % 997 + 31 * new_rows + dtype)
+    x = rng.standard_normal((planes, new_rows, D)).astype(np.float32) * 4
+    x[1, 0] = 0.0                                     # an all-zero row
+    x[2, new_rows - 1, 5] *= 40                       # an outlier channel
+    if dtype == DTYPE_BF16:
+        new = (x.view(np.uint32) >> 16).astype(np.uint16)
+    elif dtype == DTYPE_F16:
+        new = x.astype(np.float16).view(np.uint16)
+    else:
+        new = x
+    old_q = rng.integers(-127, 128, planes * bucket * D).astype(np.int8)
+    old_s = rng.uniform(0.01, 1, planes * bucket).astype(np.float32)
+    got_q, got_s = oracle.kv_quant_append(new, dtype, pos, old_q, old_s, planes, bucket, new_rows, D)
+    vals = _widen_independently(new, dtype).reshape(planes, new_rows, D)
+    want_q = old_q.reshape(planes, bucket, D).copy()
+    want_s = old_s.reshape(planes, bucket).copy()
+    rows_q = np.zeros((planes, new_rows, D), np.int8)
+    rows_s = np.zeros((planes, new_rows), np.float32)
+    for p in range(planes):
+        for j in range(new_rows):
+            q, sc = oracle.quantize_row_i8(vals[p, j])
+            rows_q[p, j], rows_s[p, j] = q, sc
+            want_q[p, (pos + j) % bucket] = q
+            want_s[p, (pos + j) % bucket] = sc
+    assert np.array_equal(got_q, want_q.ravel())
+    assert np.array_equal(got_s.view(np.uint32), want_s.ravel().view(np.uint32))
+    # the zero row: q = 0, scale 0, regardless of the slot's old contents
+    zr = (pos + 0) % bucket
+    assert np.all(got_q.reshape(planes, bucket, D)[1, zr] == 0) and got_s.reshape(planes, bucket)[1, zr] == 0
+    # composition of the two pinned functions, byte for byte
+    cq = oracle.kv_cache_write(old_q.view(np.uint8), rows_q.view(np.uint8).ravel(), pos, planes,
+                               bucket, new_rows, D)
+    cs = oracle.kv_cache_write(old_s.view(np.uint8), rows_s.view(np.uint8).ravel(), pos, planes,
+                               bucket, new_rows, 4)
+    assert np.array_equal(got_q.view(np.uint8), cq) and np.array_equal(got_s.view(np.uint8), cs)
+
+
+def test_kv_quant_append_catches_a_placement_mistake():
+    """The brute force above discriminates: placing row j at (pos - j) or
+    reading the new rows [new_rows][planes] would not match."""
+    planes, bucket, D, pos, nr = 2, 8, 16, 6, 3
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((planes, nr, D)).astype(np.float32)
+    got_q, _ = oracle.kv_quant_append(x, DTYPE_F32, pos, np.zeros(planes * bucket * D, np.int8),
+                                      np.zeros(planes * bucket, np.float32), planes, bucket, nr, D)
+    got = got_q.reshape(planes, bucket, D)
+    swapped = x.reshape(nr, planes, D)                # the transposed reading of the new rows
+    q_wrong, _ = oracle.quantize_row_i8(swapped[1, 0])
+    q_right, _ = oracle.quantize_row_i8(x[0, 1])
+    assert np.array_equal(got[0, (pos + 1) % bucket], q_right)
+    assert not np.array_equal(got[0, (pos + 1) % bucket], q_wrong)
+    assert not np.array_equal(got[0, (pos - 1) % bucket], q_right)
+
+
 def test_kv_cache_write_refusals():
     with pytest.raises(ValueError):
         oracle.kv_cache_write(np.zeros(8, np.uint8), np.zeros(48, np.uint8), 0, 1, 2, 3, 4)
@@ -283,3 +358,17 @@ def test_matmul_reference_closed_forms():
                                want.astype(np.float32).reshape(-1), rtol=1e-6)
     assert oracle.max_rel_err(np.array([1.0, 2.0], np.float32),
                               np.array([1.0, 4.0], np.float32)) == pytest.approx(0.5)
+
+
+def test_blas_f64_product_is_the_f64_reference():
+    """The graph oracle's large products go through numpy's f64 BLAS: the same
+    f64 products and sums as or_matmul_ref_f64, in another order, so the f32
+    results agree to f64 rounding (well under one f32 ulp)."""
+    rng = np.random.default_rng(17)
+    m, k, n = 37, 1500, 70
+    a = rng.standard_normal(m * k).astype(np.float32)
+    b = rng.standard_normal(k * n).astype(np.float32)
+    x = oracle.matmul_ref_f64(a, b, m, k, n)
+    y = oracle.matmul_f64_blas(a, b, m, k, n)
+    ulps = np.abs(x.view(np.int32).astype(np.int64) - y.view(np.int32).astype(np.int64))
+    assert ulps.max() <= 1 and np.mean(ulps != 0) < 0.01

@@ -81,6 +81,36 @@ def test_attention_rows_oracle_is_the_valid_form():
         assert np.allclose(got[b], want, rtol=1e-5, atol=1e-6), b
 
 
+def test_attention_rows_oracle_brute_force_causal():
+    """Brute force in f64 over the dequantized, unwrapped positions: row t of a
+    T-row prompt ending at position lens[b] - 1 attends to positions
+    0 .. lens[b] - T + t, nothing later; a wrapped ring (lens > bucket) is refused."""
+    rng = np.random.default_rng(8)
+    B, T, H, Hkv, D, S = 2, 4, 4, 2, 64, 16
+    kq, ks = make_cache(rng, B * Hkv, S, D)
+    vq, vs = make_cache(rng, B * Hkv, S, D)
+    lens = np.array([16, 9], np.uint32)           # a full bucket and a partial one
+    q = rng.standard_normal(B * T * H * D).astype(np.float32)
+    scale = oracle.attn_scale(D)
+    got = oracle.attention_i8_rows(q, kq, ks, vq, vs, lens, B, T, H, Hkv, S, D, scale)
+    got = got.reshape(B, T, H, D)
+    kd = (kq.reshape(B, Hkv, S, D).astype(np.float64) * ks.reshape(B, Hkv, S, 1))
+    vd = (vq.reshape(B, Hkv, S, D).astype(np.float64) * vs.reshape(B, Hkv, S, 1))
+    qq = q.reshape(B, T, H, D).astype(np.float64)
+    for b in range(B):
+        for t in range(T):
+            last = int(lens[b]) - T + t           # the row's own position
+            for h in range(H):
+                kv = h // (H // Hkv)
+                s_ = kd[b, kv, :last + 1] @ qq[b, t, h] / scale
+                p = np.exp(s_ - s_.max())
+                want = (p / p.sum()) @ vd[b, kv, :last + 1]
+                assert np.allclose(got[b, t, h], want, rtol=1e-4, atol=1e-5), (b, t, h)
+    with pytest.raises(ValueError):
+        oracle.attention_i8_rows(q, kq, ks, vq, vs, np.array([17, 9], np.uint32), B, T, H, Hkv,
+                                 S, D, scale)
+
+
 def test_attention_rows_short_sequence_rows_are_zero():
     rng = np.random.default_rng(4)
     B, T, H, Hkv, D, S = 1, 6, 2, 1, 64, 16

@@ -110,7 +110,15 @@ def _ports(b: bytes) -> list:
 class OracleSession:
     """Load an archive and run it on the CPU oracle, step by step."""
 
-    def __init__(self, archive: bytes, verify_footer: bool = True):
+    def __init__(self, archive: bytes, verify_footer: bool = True, products: str = "f64"):
+        """products: "f64" sums every MatMul in f64 (the reference metric's
+        exact product, tests/conformance.rs:100-112); "f32" sums in f32
+        through numpy's BLAS (as the reference CPU engine accumulates in f32,
+        in another order). Two walks that differ only here measure how far
+        two correct bf16 walks of the same archive land apart."""
+        if products not in ("f64", "f32"):
+            raise ValueError(products)
+        self.products = products
         if archive[:4] != b"HOLO":
             raise ValueError("bad magic")
         ver, _flags, nsec = struct.unpack_from("<HHH", archive, 4)
@@ -231,8 +239,12 @@ class OracleSession:
             a = self._f32(self._view(c["a"], m * k * es), dt)
             b = self._f32(self._view(c["b"], k * n * es), dt)
             from . import FUSED_TO_LUT, build_table, fused_act_f32, matmul_f64_blas, matmul_ref_f64
-            ref = matmul_ref_f64 if m * k * n <= (1 << 24) else matmul_f64_blas
-            v = self._f32(self._narrow(ref(a, b, m, k, n), dt), dt)
+            if self.products == "f32":
+                prod = (a.reshape(m, k) @ b.reshape(k, n)).ravel()
+            else:
+                ref = matmul_ref_f64 if m * k * n <= (1 << 24) else matmul_f64_blas
+                prod = ref(a, b, m, k, n)
+            v = self._f32(self._narrow(prod, dt), dt)
             if tag in (107, 108):
                 v = v + self._f32(self._view(c["residual"], m * n * es), dt)
             if tag == 106 and dt == BF16:

@@ -14,7 +14,7 @@ from .backend import (BackendError, DeviceWorkspace, DispatchError, HipBackend, 
 from .kernel_call import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, DTYPE_I8, DTYPE_I32, DTYPE_I64,
                           NO_BUFFER, SLOT_ABSENT, ArgMaxCall, AttentionI8RowsCall, BinaryCall,
                           BufferRef,
-                          DecodeAttentionI8Call, GatherCall, KernelCall, KvCacheWriteCall,
+                          DecodeAttentionI8Call, DecodeAttentionValidCall, GatherCall, KernelCall, KvCacheWriteCall,
                           KvQuantAppendCall, MatMulActivationCall, MatMulAddActivationCall,
                           MatMulAddCall, MatMulCall, NormCall, RoPECall, TransposeCall, UnaryCall,
                           encode_calls, fused_activation, lut_act)
@@ -26,7 +26,7 @@ __all__ = [
     "ShapeMismatch", "SlotOutOfRange", "UnsupportedOp", "decode_call", "lut_table", "validate",
     "DTYPE_BF16", "DTYPE_F16", "DTYPE_F32", "DTYPE_I8", "DTYPE_I32", "DTYPE_I64",
     "NO_BUFFER", "SLOT_ABSENT", "ArgMaxCall", "AttentionI8RowsCall", "BinaryCall", "BufferRef",
-    "DecodeAttentionI8Call", "GatherCall", "KernelCall", "KvCacheWriteCall",
+    "DecodeAttentionI8Call", "DecodeAttentionValidCall", "GatherCall", "KernelCall", "KvCacheWriteCall",
     "KvQuantAppendCall", "MatMulActivationCall", "MatMulAddActivationCall", "MatMulAddCall",
     "MatMulCall", "NormCall", "RoPECall", "TransposeCall", "UnaryCall", "encode_calls",
     "fused_activation",

@@ -93,6 +93,16 @@ class KvQuantAppendCallC(ctypes.Structure):
                 ("head_dim", ctypes.c_uint32), ("dtype", ctypes.c_uint8)]
 
 
+class DecodeAttentionValidCallC(ctypes.Structure):
+    _fields_ = [("q", BufferRefC), ("k_past", BufferRefC), ("v_past", BufferRefC),
+                ("k_new", BufferRefC), ("v_new", BufferRefC), ("valid_len", BufferRefC),
+                ("output", BufferRefC), ("batch", ctypes.c_uint32), ("heads", ctypes.c_uint32),
+                ("kv_heads", ctypes.c_uint32), ("q_rows", ctypes.c_uint32),
+                ("past_len", ctypes.c_uint32), ("new_len", ctypes.c_uint32),
+                ("head_dim", ctypes.c_uint32), ("scale_bits", ctypes.c_uint32),
+                ("dtype", ctypes.c_uint8)]
+
+
 class DecodeAttentionI8CallC(ctypes.Structure):
     _fields_ = [("q", BufferRefC), ("k_cache", BufferRefC), ("v_cache", BufferRefC),
                 ("k_scales", BufferRefC), ("v_scales", BufferRefC), ("lens", BufferRefC),
@@ -118,7 +128,8 @@ class CallUnion(ctypes.Union):
                 ("matmul", MatMulCallC), ("matmul_act", MatMulActCallC),
                 ("matmul_add", MatMulAddCallC), ("matmul_add_act", MatMulAddActCallC),
                 ("kv_write", KvCacheWriteCallC),
-                ("kv_quant_append", KvQuantAppendCallC), ("attn_i8", DecodeAttentionI8CallC),
+                ("kv_quant_append", KvQuantAppendCallC), ("attn_valid", DecodeAttentionValidCallC),
+                ("attn_i8", DecodeAttentionI8CallC),
                 ("attn_i8_rows", AttentionI8RowsCallC), ("transpose", TransposeCallC)]
 
 

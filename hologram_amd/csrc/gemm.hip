@@ -163,7 +163,16 @@ __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(const uint16_t *__r
 constexpr int BK32 = 32;
 constexpr int APAD32 = 4, BPAD32 = 4;
 
-template <bool kFast, int WT>
+// kPacked: B is the reference's panel-packed weight (src/layout.rs:16-45),
+// [ceil(N/16)][K][16] with zero-padded columns: element (k, n) sits at
+// ((n / 16) * K + k) * 16 + n % 16, so four columns n..n+3 (n % 4 == 0) of one
+// k-row are still one 16-byte load, and a load past N reads panel padding.
+template <bool kPacked>
+__device__ __forceinline__ uint64_t b_index(uint32_t gk, uint32_t gn, uint32_t N, uint32_t K) {
+    return kPacked ? (uint64_t(gn >> 4) * K + gk) * 16 + (gn & 15) : uint64_t(gk) * N + gn;
+}
+
+template <bool kFast, int WT, bool kPacked = false>
 __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(const float *__restrict__ A,
                                                            const float *__restrict__ B,
                                                            float *__restrict__ C, uint32_t M,
@@ -208,13 +217,13 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(const float *__restr
             const int r = c / (BN / 4), nc = (c % (BN / 4)) * 4;
             const uint32_t gk = k0 + r, gn = n0 + nc;
             if (kFast) {
-                rb[i] = gn < N ? *reinterpret_cast<const float4 *>(B + uint64_t(gk) * N + gn)
+                rb[i] = gn < N ? *reinterpret_cast<const float4 *>(B + b_index<kPacked>(gk, gn, N, K))
                                : make_float4(0.f, 0.f, 0.f, 0.f);
             } else {
                 float v[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    v[e] = (gk < K && gn + e < N) ? B[uint64_t(gk) * N + gn + e] : 0.0f;
+                    v[e] = (gk < K && gn + e < N) ? B[b_index<kPacked>(gk, gn + e, N, K)] : 0.0f;
                 rb[i] = make_float4(v[0], v[1], v[2], v[3]);
             }
         }
@@ -777,6 +786,31 @@ hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint
         return hipErrorInvalidValue;
     }
 #undef HOLO_GEMM_LAUNCH
+    return hipGetLastError();
+}
+
+hipError_t launch_matmul_f32_packed(const float *a, const float *b_packed, float *c, uint32_t m,
+                                   uint32_t k, uint32_t n, hipStream_t stream) {
+    const uint64_t tiles128 = uint64_t((m + 127) / 128) * ((n + 127) / 128);
+    const bool small = tiles128 < 256;
+    const uint32_t bt = small ? 64 : 128;
+    const dim3 grid((n + bt - 1) / bt, (m + bt - 1) / bt);
+    // the fast loads need 16-byte aligned A and B rows and whole K slabs; the
+    // packed B's panel padding covers any n
+    const bool fast = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b_packed)) & 15) == 0 &&
+                      k % BK32 == 0;
+    if (fast && small)
+        hipLaunchKernelGGL((gemm_f32_kernel<true, 2, true>), grid, dim3(kThreads), 0, stream, a,
+                           b_packed, c, m, n, k);
+    else if (fast)
+        hipLaunchKernelGGL((gemm_f32_kernel<true, 4, true>), grid, dim3(kThreads), 0, stream, a,
+                           b_packed, c, m, n, k);
+    else if (small)
+        hipLaunchKernelGGL((gemm_f32_kernel<false, 2, true>), grid, dim3(kThreads), 0, stream, a,
+                           b_packed, c, m, n, k);
+    else
+        hipLaunchKernelGGL((gemm_f32_kernel<false, 4, true>), grid, dim3(kThreads), 0, stream, a,
+                           b_packed, c, m, n, k);
     return hipGetLastError();
 }
 

@@ -252,21 +252,29 @@ int do_matmul(holo_backend *be, const SlotTable &st, const holo_matmul_call &c) 
     if (c.m == 0 || c.k == 0 || c.n == 0) return HOLO_OK;
     if (c.dtype != HOLO_DTYPE_F32 && c.dtype != HOLO_DTYPE_BF16)
         return fail(HOLO_ERR_UNSUPPORTED_OP, "matmul: the device path serves f32 and bf16");
-    if (c.b_packed)
-        return fail(HOLO_ERR_UNSUPPORTED_OP,
-                    "matmul: panel-packed B (b_packed) is a CPU layout; bind the row-major weight");
+    // the compiler panel-packs constant f32 weights only (compiler.rs:590-613)
+    if (c.b_packed && c.dtype != HOLO_DTYPE_F32)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "matmul: a panel-packed B is served for f32 only");
     const uint64_t es = dtype_size(c.dtype);
     holo_buffer_ref reads[2] = {c.a, c.b};
     View rv[2], out;
     HOLO_TRY(split_borrow(st, reads, rv, 2, c.output, &out, op));
     HOLO_TRY(need(rv[0], uint64_t(c.m) * c.k * es, c.a.slot, op, "a"));
-    HOLO_TRY(need(rv[1], uint64_t(c.k) * c.n * es, c.b.slot, op, "b"));
+    // a packed weight spans layout::packed_len(k, n) elements (float_kernels.rs:317-324)
+    HOLO_TRY(need(rv[1], (c.b_packed ? holo::packed_len(c.k, c.n) : uint64_t(c.k) * c.n) * es,
+                  c.b.slot, op, "b"));
     HOLO_TRY(need(out, uint64_t(c.m) * c.n * es, c.output.slot, op, "output"));
     if (!aligned(rv[0], es) || !aligned(rv[1], es) || !aligned(out, es))
         return fail(HOLO_ERR_UNSUPPORTED_OP, "matmul: operands must be element-aligned");
     if ((uint64_t(c.m) + 127) / 128 > 65535)
         return fail(HOLO_ERR_UNSUPPORTED_OP, "matmul: m above 8388480");
     if (!be) return HOLO_OK;
+    if (c.b_packed)
+        return launched(holo::launch_matmul_f32_packed(
+                            reinterpret_cast<const float *>(rv[0].base),
+                            reinterpret_cast<const float *>(rv[1].base),
+                            reinterpret_cast<float *>(out.base), c.m, c.k, c.n, be->stream),
+                        op);
     HOLO_TRY(ensure_scratch(be, holo::matmul_scratch_bytes(c.m, c.k, c.n, c.dtype), op));
     return launched(holo::launch_matmul(rv[0].base, rv[1].base, out.base, c.m, c.k, c.n, c.dtype,
                                         be->scratch, be->stream),
@@ -538,6 +546,18 @@ int do_matmul_fused(holo_backend *be, const SlotTable &st, uint32_t tag, const h
             return fail(HOLO_ERR_UNSUPPORTED_OP, std::string(op) + ": residual must be element-aligned");
     }
     if (!be) return HOLO_OK;
+    if (c.b_packed) {
+        // the packed product into the output, then the epilogue over it in place
+        HOLO_TRY(do_matmul(be, st, c));
+        View o;
+        HOLO_TRY(split_borrow(st, nullptr, nullptr, 0, c.output, &o, op));
+        holo::TileEpi te;
+        te.kind = tag == HOLO_OP_MATMUL_ACT ? holo::kEpiAct
+                  : tag == HOLO_OP_MATMUL_ADD ? holo::kEpiAdd : holo::kEpiAddAct;
+        te.act = act;
+        te.residual = has_res ? rv[0].base : nullptr;
+        return launched(holo::launch_tile_epilogue(o.base, count, false, te, be->stream), op);
+    }
     holo::GroupDesc g;
     g.a = c.a;
     g.m = c.m;
@@ -732,6 +752,77 @@ int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attentio
                                                    be->stream),
                           op));
     return launched(holo::launch_attn_i8(a, be->scratch, be->stream), op);
+}
+
+// -------------------------------------------------- DecodeAttentionValid --
+// decode_attention_valid_float (src/cpu/float_kernels.rs:4192-4307): refusals
+// in the reference's order, then the split-K kernel of attn_valid.hip.
+int do_attn_valid(holo_backend *be, const SlotTable &st, const holo_decode_attention_valid_call &c) {
+    const char *op = "decode_attention_valid";
+    if (c.batch == 0 || c.heads == 0 || c.head_dim == 0) return HOLO_OK;
+    if (c.q_rows == 0 || c.q_rows != c.new_len)
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    "decode_attention_valid: q_rows must equal new_len and be at least 1 "
+                    "(the causal law pairs query row i with chunk key row i)");
+    const uint32_t hkv = c.kv_heads == 0 ? c.heads : c.kv_heads;
+    if (c.heads % hkv != 0)
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    "decode_attention_valid: heads must be a multiple of kv_heads (grouped-query)");
+    const uint64_t es = dtype_size(c.dtype);
+    if (es == 0 || c.dtype == HOLO_DTYPE_I8)
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    "decode_attention_valid: only f32/f16/bf16 are supported compute dtypes");
+    const uint64_t qn = uint64_t(c.batch) * c.heads * c.q_rows * c.head_dim;
+    const uint64_t pn = uint64_t(c.batch) * hkv * c.past_len * c.head_dim;
+    const uint64_t nn = uint64_t(c.batch) * hkv * c.new_len * c.head_dim;
+    holo_buffer_ref reads[6] = {c.q, c.k_past, c.v_past, c.k_new, c.v_new, c.valid_len};
+    View rv[6], out;
+    HOLO_TRY(split_borrow(st, reads, rv, 6, c.output, &out, op));
+    HOLO_TRY(need(rv[0], qn * es, c.q.slot, op, "q"));
+    HOLO_TRY(need(rv[1], pn * es, c.k_past.slot, op, "k_past"));
+    HOLO_TRY(need(rv[2], pn * es, c.v_past.slot, op, "v_past"));
+    HOLO_TRY(need(rv[3], nn * es, c.k_new.slot, op, "k_new"));
+    HOLO_TRY(need(rv[4], nn * es, c.v_new.slot, op, "v_new"));
+    HOLO_TRY(need(rv[5], 4, c.valid_len.slot, op, "valid_len"));
+    HOLO_TRY(need(out, qn * es, c.output.slot, op, "output"));
+    for (int i = 0; i < 5; ++i)
+        if (!aligned(rv[i], es))
+            return fail(HOLO_ERR_UNSUPPORTED_OP, std::string(op) + ": operands must be element-aligned");
+    if (!aligned(out, es))
+        return fail(HOLO_ERR_UNSUPPORTED_OP, std::string(op) + ": operands must be element-aligned");
+    if (!holo::attn_valid_supported(c.batch, c.heads, hkv, c.q_rows, c.head_dim))
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    std::string(op) + ": head_dim above 4096 or a grid beyond the launch limits");
+    if (!be) return HOLO_OK;
+    // score divisor (float_kernels.rs:4256-4266)
+    float scale = std::sqrt(static_cast<float>(c.head_dim));
+    if (scale < 1.0f) scale = 1.0f;
+    if (c.scale_bits != 0) {
+        float sm;
+        memcpy(&sm, &c.scale_bits, 4);
+        if (sm > 0.0f) scale = 1.0f / sm;
+    }
+    HOLO_TRY(ensure_scratch(be, holo::attn_valid_scratch_bytes(c.batch, c.heads, hkv, c.q_rows,
+                                                               c.past_len, c.new_len, c.head_dim),
+                            op));
+    holo::AttnValidArgs a;
+    a.q = rv[0].base;
+    a.kp = rv[1].base;
+    a.vp = rv[2].base;
+    a.kn = rv[3].base;
+    a.vn = rv[4].base;
+    a.valid_len = rv[5].base;
+    a.out = out.base;
+    a.B = c.batch;
+    a.H = c.heads;
+    a.Hkv = hkv;
+    a.M = c.q_rows;
+    a.past = c.past_len;
+    a.nnew = c.new_len;
+    a.D = c.head_dim;
+    a.scale = scale;
+    a.dtype = c.dtype;
+    return launched(holo::launch_attn_valid(a, be->scratch, be->stream), op);
 }
 
 // ------------------------------------------------------- Add / Mul -----
@@ -931,6 +1022,7 @@ int dispatch_impl(holo_backend *be, const SlotTable &st, const holo_kernel_call 
                                    call->u.matmul_add_act.residual, call->u.matmul_add_act.act);
         case HOLO_OP_KV_CACHE_WRITE: return do_kv_write(be, st, call->u.kv_write);
         case HOLO_OP_KV_QUANT_APPEND: return do_kv_quant(be, st, call->u.kv_quant_append);
+        case HOLO_OP_DECODE_ATTN_VALID: return do_attn_valid(be, st, call->u.attn_valid);
         case HOLO_OP_DECODE_ATTN_I8: return do_attn_i8(be, st, call->u.attn_i8);
         case HOLO_OP_ATTN_I8_ROWS:
             return do_attn_i8(be, st, call->u.attn_i8_rows.attn, call->u.attn_i8_rows.q_rows);
@@ -961,6 +1053,7 @@ struct Reader {
     }
     holo_buffer_ref buf() {
         holo_buffer_ref b;
+        memset(&b, 0, sizeof b);   // padding too: decoded calls compare byte for byte
         b.slot = get<uint32_t>();
         b.offset = get<uint64_t>();
         b.length = get<uint64_t>();
@@ -1107,6 +1200,26 @@ int decode_impl(const uint8_t *wire, size_t len, holo_kernel_call *out, size_t *
             c.bucket_rows = r.get<uint32_t>();
             c.new_rows = r.get<uint32_t>();
             c.head_dim = r.get<uint32_t>();
+            c.dtype = r.get<uint8_t>();
+            break;
+        }
+        case HOLO_OP_DECODE_ATTN_VALID: {  // put_davl :786-803
+            auto &c = out->u.attn_valid;
+            c.q = r.buf();
+            c.k_past = r.buf();
+            c.v_past = r.buf();
+            c.k_new = r.buf();
+            c.v_new = r.buf();
+            c.valid_len = r.buf();
+            c.output = r.buf();
+            c.batch = r.get<uint32_t>();
+            c.heads = r.get<uint32_t>();
+            c.kv_heads = r.get<uint32_t>();
+            c.q_rows = r.get<uint32_t>();
+            c.past_len = r.get<uint32_t>();
+            c.new_len = r.get<uint32_t>();
+            c.head_dim = r.get<uint32_t>();
+            c.scale_bits = r.get<uint32_t>();
             c.dtype = r.get<uint8_t>();
             break;
         }

@@ -12,6 +12,42 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ u32x4 ld_stream(const u32x4 *p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ void st_stream(u32x4 v, u32x4 *p) { __builtin_nontemporal_store(v, p); }
 
+// f16 -> f32 by bits (src/cpu/dtype.rs:94-118): exact, NaN payload kept.
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t b) {
+    const uint32_t s = (b >> 15) << 31, e = (b >> 10) & 0x1fu, m = b & 0x3ffu;
+    if (e == 0x1fu) return __uint_as_float(s | 0x7f800000u | (m << 13));
+    if (e != 0) return __uint_as_float(s | ((e + 112u) << 23) | (m << 13));
+    if (m == 0) return __uint_as_float(s);
+    const int sh = __clz(m) - 21;  // left shifts until the implicit bit (0x400) is set
+    return __uint_as_float(s | (uint32_t(113 - sh) << 23) | (((m << sh) & 0x3ffu) << 13));
+}
+
+// f32 -> f16 bits with the reference's rule (src/cpu/dtype.rs:121-153): the
+// magnitude rounded half up at the cut, overflow to Inf, NaN as the quiet
+// NaN of its sign, subnormals by the same half-up shift.
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
+    const uint32_t bits = __float_as_uint(v);
+    const uint32_t sign = (bits >> 31) & 1u;
+    const int32_t ex = int32_t((bits >> 23) & 0xffu);
+    const uint32_t mant = bits & 0x7fffffu;
+    if (ex == 0xff) return uint16_t((sign << 15) | (0x1fu << 10) | (mant != 0 ? 0x200u : 0u));
+    const int32_t ne = ex - 127 + 15;
+    if (ne >= 0x1f) return uint16_t((sign << 15) | (0x1fu << 10));
+    if (ne <= 0) {
+        if (ne < -10) return uint16_t(sign << 15);
+        const uint32_t m = mant | 0x800000u;
+        const uint32_t shift = uint32_t(1 - ne) + 13;
+        return uint16_t((sign << 15) | ((m + (1u << (shift - 1))) >> shift));
+    }
+    const uint32_t rm = (mant + 0x1000u) >> 13;
+    if (rm & 0x400u) {
+        const int32_t be = ne + 1;
+        if (be >= 0x1f) return uint16_t((sign << 15) | (0x1fu << 10));
+        return uint16_t((sign << 15) | (uint32_t(be) << 10));
+    }
+    return uint16_t((sign << 15) | (uint32_t(ne) << 10) | (rm & 0x3ffu));
+}
+
 // exp_f32_det (src/cpu/simd.rs:4191-4239): clamp, k = trunc(x*log2e +- 1/2),
 // Cody-Waite reduction, degree-6 Horner, scale by 2^k. IEEE basic operations
 // only; the files that include this are built without contraction.

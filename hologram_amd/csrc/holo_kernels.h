@@ -49,6 +49,22 @@ size_t attn_i8_scratch_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t buck
 bool attn_i8_supported(uint32_t H, uint32_t Hkv, uint32_t D, uint32_t bucket);
 hipError_t launch_attn_i8(const AttnI8Args &a, void *scratch, hipStream_t stream);
 
+// attn_valid.hip — DecodeAttentionValid (discriminant 121) over bf16/f16/f32
+// K/V: q/out [B, H, M, D], k/v_past [B, Hkv, past, D], k/v_new [B, Hkv, nnew, D]
+// (M == nnew), valid_len a 4-byte LE u32 on the device.
+struct AttnValidArgs {
+    const void *q, *kp, *vp, *kn, *vn;
+    const uint8_t *valid_len;
+    void *out;
+    uint32_t B, H, Hkv, M, past, nnew, D;
+    float scale;            // the divisor: sqrtf(D) (>= 1) or 1/scale_multiplier
+    uint8_t dtype;          // 7 bf16, 6 f16, 8 f32
+};
+bool attn_valid_supported(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t M, uint32_t D);
+size_t attn_valid_scratch_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t M, uint32_t past,
+                                uint32_t nnew, uint32_t D);
+hipError_t launch_attn_valid(const AttnValidArgs &a, void *scratch, hipStream_t stream);
+
 // decoder_ops.hip — the other ops of a decode step (bf16 or f32 operands).
 // op 0 = Add, 1 = Mul.
 hipError_t launch_binary(int op, const void *a, const void *b, void *out, uint64_t n, bool bf16,
@@ -90,6 +106,12 @@ hipError_t launch_tile_epilogue(void *c, uint64_t count, bool bf16, const TileEp
 size_t matmul_scratch_bytes(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype);
 hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint32_t k,
                          uint32_t n, uint8_t dtype, void *scratch, hipStream_t stream);
+// f32 C = A * B with B in the reference's panel-packed layout (src/layout.rs:
+// 16-45): [ceil(n/16)][k][16] floats, columns past n zero.
+hipError_t launch_matmul_f32_packed(const float *a, const float *b_packed, float *c, uint32_t m,
+                                   uint32_t k, uint32_t n, hipStream_t stream);
+// The packed layout's length in elements (layout::packed_len).
+inline uint64_t packed_len(uint32_t k, uint32_t n) { return uint64_t((n + 15) / 16) * k * 16; }
 
 // gemm_skinny.hip — the few-row (m <= 64) path that launch_matmul takes when
 // it applies (16-byte aligned operands required by the caller).

@@ -150,6 +150,11 @@ void call_operands(const holo_kernel_call &c, std::vector<holo_buffer_ref> *read
         }
         case HOLO_OP_TRANSPOSE:
             r(c.u.transpose.input); w(c.u.transpose.output); break;
+        case HOLO_OP_DECODE_ATTN_VALID: {
+            const auto &a = c.u.attn_valid;
+            r(a.q); r(a.k_past); r(a.v_past); r(a.k_new); r(a.v_new); r(a.valid_len);
+            w(a.output); break;
+        }
         case HOLO_OP_DECODE_ATTN_I8:
         case HOLO_OP_ATTN_I8_ROWS: {
             const auto &a = c.tag == HOLO_OP_ATTN_I8_ROWS ? c.u.attn_i8_rows.attn : c.u.attn_i8;
@@ -368,6 +373,17 @@ struct MmView {
     uint32_t act = 0;
     holo_buffer_ref residual{HOLO_SLOT_ABSENT, 0, 0};
 };
+
+// The MatMul payload of a MatMul-family call (46, 106-108), or null.
+holo_matmul_call *matmul_of(holo_kernel_call &c) {
+    switch (c.tag) {
+        case HOLO_OP_MATMUL: return &c.u.matmul;
+        case HOLO_OP_MATMUL_ACT: return &c.u.matmul_act.mm;
+        case HOLO_OP_MATMUL_ADD: return &c.u.matmul_add.mm;
+        case HOLO_OP_MATMUL_ADD_ACT: return &c.u.matmul_add_act.mm;
+        default: return nullptr;
+    }
+}
 
 bool matmul_family(const holo_kernel_call &c, MmView *v) {
     switch (c.tag) {
@@ -1007,6 +1023,58 @@ int load_impl(holo_backend *be, const uint8_t *bytes, size_t len, uint32_t flags
             }
         }
         if (!c.ok) return set_error(HOLO_ERR_DISPATCH, "session_load: truncated Constants section");
+    }
+    // --- panel-packed f32 weights (compiler.rs:590-613 packs every constant
+    // f32 MatMul weight for the CPU engine, layout.rs:16-45): a constant read
+    // only as the packed B of f32 MatMuls of one (k, n) is laid back out
+    // row-major here, once, so those calls take the device's own MatMul
+    // kernels (few-row, grouped). Any other packed B runs the packed kernel.
+    std::vector<std::vector<uint8_t>> unpacked;
+    {
+        std::map<uint32_t, std::vector<holo_matmul_call *>> users;   // const slot -> packed uses
+        std::map<uint32_t, bool> other;                              // read any other way
+        std::vector<holo_buffer_ref> rd0, wr0;
+        std::map<uint32_t, size_t> const_of;
+        for (size_t i = 0; i < consts.size(); ++i) const_of[consts[i].slot] = i;
+        for (auto &call : s->calls) {
+            holo_matmul_call *mm = matmul_of(call);
+            if (mm && mm->b_packed && mm->dtype == HOLO_DTYPE_F32 && mm->b.offset == 0 &&
+                const_of.count(mm->b.slot)) {
+                users[mm->b.slot].push_back(mm);
+                call_operands(call, &rd0, &wr0);
+                int n_b = 0;
+                for (auto &r : rd0) n_b += r.slot == mm->b.slot;
+                if (n_b != 1) other[mm->b.slot] = true;          // also read as A or residual
+                continue;
+            }
+            call_operands(call, &rd0, &wr0);
+            for (auto &r : rd0) other[r.slot] = true;
+            for (auto &w : wr0) other[w.slot] = true;
+        }
+        unpacked.reserve(users.size());   // bodies below point into these buffers
+        for (auto &u : users) {
+            if (other.count(u.first)) continue;
+            const uint32_t k = u.second[0]->k, n = u.second[0]->n;
+            bool same = true;
+            for (auto *mm : u.second) same = same && mm->k == k && mm->n == n;
+            Const &cst = consts[const_of[u.first]];
+            if (!same || cst.len < holo::packed_len(k, n) * 4) continue;
+            std::vector<uint8_t> rm(uint64_t(k) * n * 4);
+            const uint32_t np = (n + 15) / 16;
+            for (uint32_t pnl = 0; pnl < np; ++pnl) {
+                const uint32_t cols = n - pnl * 16 < 16 ? n - pnl * 16 : 16;
+                for (uint32_t kk = 0; kk < k; ++kk)
+                    memcpy(rm.data() + (uint64_t(kk) * n + pnl * 16) * 4,
+                           cst.body + ((uint64_t(pnl) * k + kk) * 16) * 4, cols * 4);
+            }
+            unpacked.push_back(std::move(rm));
+            cst.body = unpacked.back().data();
+            cst.len = unpacked.back().size();
+            for (auto *mm : u.second) {
+                mm->b_packed = 0;
+                mm->b.length = uint64_t(k) * n * 4;
+            }
+        }
     }
     // --- per-slot sizes (session.rs:544-623)
     size_t nslots = 0;

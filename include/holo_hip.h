@@ -79,6 +79,7 @@ typedef enum holo_status {
 #define HOLO_OP_ROTARY 75u
 #define HOLO_OP_GATHER 114u
 #define HOLO_OP_KV_CACHE_WRITE 120u
+#define HOLO_OP_DECODE_ATTN_VALID 121u    /* DecodeAttentionValid (kernel_codec.rs D_DAVL) */
 #define HOLO_OP_KV_QUANT_APPEND 122u      /* new: int8 quantize + ring append   */
 #define HOLO_OP_DECODE_ATTN_I8 123u       /* new: GQA decode over an int8 cache */
 #define HOLO_OP_ARGMAX 124u               /* new: per-row argmax (greedy pick)  */
@@ -217,6 +218,29 @@ typedef struct holo_kv_cache_write_call {
     uint32_t planes, bucket_rows, new_rows, row_bytes;
 } holo_kv_cache_write_call;
 
+/* DecodeAttentionValidCall, kernel_call.rs:691-716 (decode_attention_valid_float,
+ * src/cpu/float_kernels.rs:4192-4307), the reference's decode attention:
+ * q [batch, heads, q_rows, head_dim]; k/v_past [batch, kv_heads, past_len,
+ * head_dim] of which the first min(valid_len, past_len) rows are realized;
+ * k/v_new [batch, kv_heads, new_len, head_dim]; valid_len a 4-byte LE u32 read
+ * by the device (content, one graph serves every step); out like q. Query row
+ * qi of head h (kv head h / (heads / kv_heads)) sees the realized past rows,
+ * then new rows 0..min(qi + 1, new_len). Scores dot(q, k) / s with s =
+ * sqrtf(head_dim) (at least 1) or 1 / f32(scale_bits); f32 softmax; no
+ * visible key gives the zero row. dtype bf16, f16 or f32 (all operands);
+ * q_rows must equal new_len >= 1; kv_heads 0 means heads; head_dim <= 4096. */
+typedef struct holo_decode_attention_valid_call {
+    holo_buffer_ref q;
+    holo_buffer_ref k_past;
+    holo_buffer_ref v_past;
+    holo_buffer_ref k_new;
+    holo_buffer_ref v_new;
+    holo_buffer_ref valid_len;
+    holo_buffer_ref output;
+    uint32_t batch, heads, kv_heads, q_rows, past_len, new_len, head_dim, scale_bits;
+    uint8_t dtype;
+} holo_decode_attention_valid_call;
+
 /* New (tag 122): int8 KV quantize + append. Each new row (head_dim values of
  * `dtype` in {bf16, f16, f32}) is quantized with the reference's per-row
  * symmetric scheme (src/cpu/simd.rs:4755-4785: scale = max|x|/127,
@@ -305,6 +329,7 @@ typedef struct holo_kernel_call {
         holo_matmul_add_act_call matmul_add_act;
         holo_kv_cache_write_call kv_write;
         holo_kv_quant_append_call kv_quant_append;
+        holo_decode_attention_valid_call attn_valid;
         holo_decode_attention_i8_call attn_i8;
         holo_attention_i8_rows_call attn_i8_rows;
         holo_transpose_call transpose;

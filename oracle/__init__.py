@@ -45,6 +45,8 @@ _SIGS = {
                                           _U32]),
     "or_dequant_i8": (None, [_P, _P, _P, _S, _S]),
     "or_attn_scale": (_F, [_U32, _U32]),
+    "or_decode_attention_valid": (ctypes.c_int, [_P, _P, _P, _P, _P, _U32, _P] + [_U32] * 8
+                                  + [ctypes.c_int]),
     "or_decode_attention_valid_f32": (None, [_P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32,
                                              _U32, _U32, _U32, _F, _U32]),
     "or_decode_attention_i8": (None, [_P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32,
@@ -161,6 +163,21 @@ def decode_attention_valid_f32(q, kp, vp, kn, vn, b, h, hkv, m, past, new, d, sc
     return out
 
 
+def decode_attention_valid(q, kp, vp, kn, vn, valid_len, b, h, hkv, m, past, new, d,
+                           scale_bits, dtype) -> np.ndarray:
+    """DecodeAttentionValid (float_kernels.rs:4192-4307) on raw operand arrays
+    of `dtype` (bf16/f16 as u16 bits, f32); returns the output array of the
+    same element type. Raises ValueError where the reference refuses."""
+    es = 4 if dtype == DTYPE_F32 else 2
+    out = np.zeros(b * h * m * d, np.float32 if es == 4 else np.uint16)
+    args = [np.ascontiguousarray(x) for x in (q, kp, vp, kn, vn)]
+    rc = lib().or_decode_attention_valid(*[_p(x) for x in args], valid_len, _p(out), b, h, hkv,
+                                         m, past, new, d, scale_bits, dtype)
+    if rc != 0:
+        raise ValueError(f"decode_attention_valid refused ({rc})")
+    return out
+
+
 def decode_attention_i8(q, kq, ks, vq, vs, lens, B, H, Hkv, bucket, D, scale) -> np.ndarray:
     out = np.zeros(B * H * D, np.float32)
     lib().or_decode_attention_i8(_p(q), _p(kq), _p(ks), _p(vq), _p(vs), _p(lens), _p(out), B,
@@ -215,6 +232,30 @@ def matmul_ref_f64(a, b, m, k, n) -> np.ndarray:
     out = np.zeros(m * n, np.float32)
     lib().or_matmul_ref_f64(_p(a), _p(b), _p(out), m, k, n)
     return out
+
+
+PANEL = 16   # layout.rs: the panel width of a packed B
+
+
+def packed_len(k: int, n: int) -> int:
+    """layout::packed_len: ceil(n / 16) * k * 16 elements."""
+    return -(-n // PANEL) * k * PANEL
+
+
+def pack_b_panels(b: np.ndarray, k: int, n: int) -> np.ndarray:
+    """pack_b_panels (layout.rs:16-45): packed[(p*k + kk)*16 + c] = b[kk*n + p*16 + c],
+    zero where p*16 + c >= n."""
+    npan = -(-n // PANEL)
+    padded = np.zeros((k, npan * PANEL), np.asarray(b).dtype)
+    padded[:, :n] = np.asarray(b).reshape(k, n)
+    return np.ascontiguousarray(padded.reshape(k, npan, PANEL).transpose(1, 0, 2)).ravel()
+
+
+def unpack_b_panels(packed: np.ndarray, k: int, n: int) -> np.ndarray:
+    """The inverse of pack_b_panels: the row-major k x n weight."""
+    npan = -(-n // PANEL)
+    p = np.asarray(packed)[:npan * k * PANEL].reshape(npan, k, PANEL).transpose(1, 0, 2)
+    return np.ascontiguousarray(p.reshape(k, npan * PANEL)[:, :n]).ravel()
 
 
 def matmul_f64_blas(a, b, m, k, n) -> np.ndarray:

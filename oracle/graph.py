@@ -59,6 +59,11 @@ def _decode_call(r: _R) -> tuple:
         return tag, dict(data=r.buf(), idx=r.buf(), output=r.buf(), outer=r.u("Q"),
                          axis=r.u("Q"), inner=r.u("Q"), num=r.u("Q"), idx_dtype=r.u("B"),
                          dtype=r.u("B"))
+    if tag == 121:                                   # put_davl
+        return tag, dict(q=r.buf(), kp=r.buf(), vp=r.buf(), kn=r.buf(), vn=r.buf(),
+                         valid=r.buf(), output=r.buf(), batch=r.u("I"), heads=r.u("I"),
+                         kv_heads=r.u("I"), q_rows=r.u("I"), past=r.u("I"), new=r.u("I"),
+                         head_dim=r.u("I"), scale_bits=r.u("I"), dtype=r.u("B"))
     if tag == 46:                                    # put_matmul
         return tag, dict(a=r.buf(), b=r.buf(), output=r.buf(), m=r.u("I"), k=r.u("I"),
                          n=r.u("I"), dtype=r.u("B"), packed=r.u("B"))
@@ -237,7 +242,13 @@ class OracleSession:
             dt = c["dtype"]
             es = DT_BYTES[dt]
             a = self._f32(self._view(c["a"], m * k * es), dt)
-            b = self._f32(self._view(c["b"], k * n * es), dt)
+            if c["packed"]:                          # layout.rs:16-45 (f32 weights only)
+                if dt != F32:
+                    raise ValueError("a panel-packed B is an f32 layout")
+                from . import packed_len, unpack_b_panels
+                b = unpack_b_panels(self._f32(self._view(c["b"], packed_len(k, n) * 4), dt), k, n)
+            else:
+                b = self._f32(self._view(c["b"], k * n * es), dt)
             from . import FUSED_TO_LUT, build_table, fused_act_f32, matmul_f64_blas, matmul_ref_f64
             if self.products == "f32":
                 prod = (a.reshape(m, k) @ b.reshape(k, n)).ravel()
@@ -277,6 +288,18 @@ class OracleSession:
             o = decode_attention_i8(q, kq, ks, vq, vs, lens, B, H, Hkv, S, D,
                                     attn_scale(D, c["scale_bits"]))
             self._out(c["output"], B * H * D * es)[:] = self._narrow(o, c["dtype"])
+        elif tag == 121:
+            B, H, M, D = c["batch"], c["heads"], c["q_rows"], c["head_dim"]
+            hkv = H if c["kv_heads"] == 0 else c["kv_heads"]
+            es = DT_BYTES[c["dtype"]]
+            pn, nn = B * hkv * c["past"] * D * es, B * hkv * c["new"] * D * es
+            ops = [np.ascontiguousarray(self._view(c[k], n)) for k, n in
+                   (("q", B * H * M * D * es), ("kp", pn), ("vp", pn), ("kn", nn), ("vn", nn))]
+            valid = int(np.ascontiguousarray(self._view(c["valid"], 4)).view(np.uint32)[0])
+            from . import decode_attention_valid
+            o = decode_attention_valid(*ops, valid, B, H, c["kv_heads"], M, c["past"], c["new"],
+                                       D, c["scale_bits"], c["dtype"])
+            self._out(c["output"], o.nbytes)[:] = o.view(np.uint8)
         elif tag == 125:
             B, T, H, Hkv = c["batch"], c["q_rows"], c["heads"], c["kv_heads"]
             S, D = c["bucket"], c["head_dim"]

@@ -432,6 +432,41 @@ void or_decode_attention_valid_f32(const float *q, const float *kp, const float 
     free(sc);
 }
 
+static float *widen_all(const void *src, int dtype, size_t n)
+{
+    float *o = (float *)malloc(sizeof(float) * (n ? n : 1));
+    for (size_t i = 0; i < n; ++i) o[i] = widen(src, dtype, i);
+    return o;
+}
+
+int or_decode_attention_valid(const void *q, const void *k_past, const void *v_past,
+                              const void *k_new, const void *v_new, uint32_t valid_len, void *out,
+                              uint32_t b, uint32_t h, uint32_t hkv, uint32_t m, uint32_t past,
+                              uint32_t nnew, uint32_t d, uint32_t scale_bits, int dtype)
+{
+    /* :4199-4216: empty shapes, the q_rows == new_len >= 1 law, the GQA map */
+    if (b == 0 || h == 0 || d == 0) return 0;
+    if (m == 0 || m != nnew) return 3;
+    if (hkv == 0) hkv = h;
+    if (h % hkv != 0) return 3;
+    if (dtype != OR_DTYPE_F32 && dtype != OR_DTYPE_BF16 && dtype != OR_DTYPE_F16) return 3;
+    size_t qn = (size_t)b * h * m * d, pn = (size_t)b * hkv * past * d, nn = (size_t)b * hkv * nnew * d;
+    float *q32 = widen_all(q, dtype, qn), *kp = widen_all(k_past, dtype, pn);
+    float *vp = widen_all(v_past, dtype, pn), *kn = widen_all(k_new, dtype, nn);
+    float *vn = widen_all(v_new, dtype, nn);
+    float *o = (float *)malloc(sizeof(float) * qn);
+    uint32_t vis = valid_len < past ? valid_len : past;              /* :4254 */
+    or_decode_attention_valid_f32(q32, kp, vp, kn, vn, o, b, h, hkv, m, past, nnew, d,
+                                  or_attn_scale(d, scale_bits), vis);
+    for (size_t i = 0; i < qn; ++i) {
+        if (dtype == OR_DTYPE_F32) ((float *)out)[i] = o[i];
+        else if (dtype == OR_DTYPE_BF16) ((uint16_t *)out)[i] = or_f32_to_bf16(o[i]);
+        else ((uint16_t *)out)[i] = or_f32_to_f16(o[i]);
+    }
+    free(q32); free(kp); free(vp); free(kn); free(vn); free(o);
+    return 0;
+}
+
 void or_decode_attention_i8(const float *q, const int8_t *kq, const float *ks,
                             const int8_t *vq, const float *vs, const uint32_t *lens,
                             float *out, uint32_t B, uint32_t H, uint32_t Hkv,

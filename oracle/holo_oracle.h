@@ -95,6 +95,14 @@ void or_decode_attention_valid_f32(const float *q, const float *k_past, const fl
                                    uint32_t b, uint32_t h, uint32_t hkv, uint32_t m,
                                    uint32_t past, uint32_t nnew, uint32_t d, float scale,
                                    uint32_t vis_past);
+/* DecodeAttentionValid over any of bf16/f16/f32 (:4192-4307): the declared
+ * buffers widened whole, the f32 engine, the output narrowed. valid_len is
+ * the u32 operand's value. Returns 0, or 3 (UnsupportedOp) for q_rows !=
+ * new_len, q_rows == 0, heads % kv_heads != 0 or another dtype. */
+int or_decode_attention_valid(const void *q, const void *k_past, const void *v_past,
+                              const void *k_new, const void *v_new, uint32_t valid_len, void *out,
+                              uint32_t b, uint32_t h, uint32_t hkv, uint32_t m, uint32_t past,
+                              uint32_t nnew, uint32_t d, uint32_t scale_bits, int dtype);
 /* int8-cache decode attention (new op), stated as the reference's per-sequence
  * DecodeAttentionValid{b=1, past=L-1, valid=L-1, q=new=1} over the dequantized
  * rows.  q: [B,H,D] f32 (widened), caches [B,Hkv,bucket,D] int8 + [B,Hkv,bucket]

@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 
 from hologram_amd import (DTYPE_BF16, DTYPE_F32, DTYPE_I32, ArgMaxCall, BinaryCall, BufferRef,
+                          DecodeAttentionValidCall,
                           ConstantEntry, GatherCall, HipSession, HoloWriter, KernelCall,
                           MatMulCall, NormCall, PortDescriptor, RoPECall, UnsupportedOp,
                           DispatchError, SlotOutOfRange, blake3, decode_call, validate)
@@ -128,6 +129,9 @@ def test_decoder_archive_loads_dry_with_in_place_caches():
 
 
 @pytest.mark.parametrize("call", [
+    KernelCall.DecodeAttentionValid(DecodeAttentionValidCall(
+        *[BufferRef(i, 4 * i, 0) for i in range(7)], 2, 32, 8, 1, 4096, 1, 128, 0x3E000000,
+        DTYPE_BF16)),
     KernelCall.Add(BinaryCall(BufferRef(1, 8, 24), BufferRef(2), BufferRef(3), 7, 16, DTYPE_BF16)),
     KernelCall.Mul(BinaryCall(BufferRef(1), BufferRef(2), BufferRef(3), 9, 32, DTYPE_F32)),
     KernelCall.RmsNorm(NormCall(BufferRef(1), BufferRef(2), BufferRef(3), 4, 64, 0x3727C5AC,
@@ -203,3 +207,22 @@ def test_view_length_past_the_slot_saturates():
     ok = KernelCall.Add(BinaryCall(BufferRef(1, 8, (1 << 64) - 4), BufferRef(2), BufferRef(3),
                                    14, 32, DTYPE_F32))
     validate(ok, sizes)                           # 14 f32 = 56 bytes fit
+
+
+def test_decode_attention_valid_refusals():
+    """decode_attention_valid_float's refusals (float_kernels.rs:4199-4240)."""
+    sizes = [1 << 20] * 8
+    mk = lambda m, new, h=4, hkv=2, q_len=0, dtype=DTYPE_BF16: KernelCall.DecodeAttentionValid(
+        DecodeAttentionValidCall(BufferRef(0, 0, q_len), *[BufferRef(i) for i in range(1, 7)], 1,
+                                 h, hkv, m, 64, new, 64, 0, dtype))
+    validate(mk(1, 1), sizes)
+    with pytest.raises(UnsupportedOp):
+        validate(mk(2, 1), sizes)                # q_rows != new_len
+    with pytest.raises(UnsupportedOp):
+        validate(mk(0, 0), sizes)                # q_rows == 0
+    with pytest.raises(UnsupportedOp):
+        validate(mk(1, 1, h=6, hkv=4), sizes)    # heads % kv_heads
+    with pytest.raises(UnsupportedOp):
+        validate(mk(1, 1, dtype=2), sizes)       # int8 is no compute dtype here
+    with pytest.raises(SlotOutOfRange):
+        validate(mk(1, 1, q_len=16), sizes)      # q shorter than 4 x 64 bf16

@@ -94,8 +94,13 @@ def test_matmul_refusals():
         validate(mm(m=2, k=3, n=4, dtype=DTYPE_F32), [24, 47, 32])
     with pytest.raises(UnsupportedOp):
         validate(mm(m=2, k=3, n=4, dtype=DTYPE_F16), [24, 48, 32])
-    with pytest.raises(UnsupportedOp):
+    # a packed B spans layout::packed_len(k, n) = ceil(n/16)*k*16 elements
+    # (float_kernels.rs:317-324); the compiler packs f32 weights only
+    with pytest.raises(SlotOutOfRange):
         validate(mm(m=2, k=3, n=4, dtype=DTYPE_F32, b_packed=True), [24, 48, 32])
+    validate(mm(m=2, k=3, n=4, dtype=DTYPE_F32, b_packed=True), [24, 192, 32])
+    with pytest.raises(UnsupportedOp):
+        validate(mm(m=2, k=3, n=4, dtype=DTYPE_BF16, b_packed=True), [24, 96, 32])
     validate(mm(m=0, k=3, n=4, dtype=DTYPE_F32), [])
 
 

@@ -66,13 +66,87 @@ def test_bf16_truncates(torch_cuda, backend):
     assert int(from_dev(out, np.uint16)[0]) == 0x3FC1
 
 
-def test_packed_b_refused(torch_cuda, backend):
+@pytest.mark.parametrize("m,k,n", [(1, 64, 17), (16, 4096, 4096), (300, 1000, 257),
+                                   (1024, 1024, 1024), (77, 131, 45), (4096, 512, 1000)])
+def test_packed_b_matmul_parity(torch_cuda, backend, m, k, n):
+    """f32 MatMul with B panel-packed as the reference compiler packs constant
+    weights (src/layout.rs:16-45, compiler.rs:590-613): within 1e-5 of the f64
+    product of the unpacked weight."""
+    rng = np.random.default_rng(m + k + n)
+    a = (rng.standard_normal(m * k) / np.sqrt(k)).astype(np.float32)
+    b = (rng.standard_normal(k * n) / np.sqrt(k)).astype(np.float32)
+    bp = oracle.pack_b_panels(b, k, n)
+    out = torch_cuda.zeros(m * n * 4, dtype=torch_cuda.uint8, device="cuda")
+    ws = DeviceWorkspace()
+    ws.bind(0, to_dev(torch_cuda, a))
+    ws.bind(1, to_dev(torch_cuda, bp))
+    ws.bind(2, out)
+    backend.dispatch(KernelCall.MatMul(MatMulCall(BufferRef(0), BufferRef(1), BufferRef(2), m, k,
+                                                  n, DTYPE_F32, True)), ws)
+    backend.synchronize()
+    err = oracle.max_rel_err(from_dev(out, np.float32), oracle.matmul_ref_f64(a, b, m, k, n))
+    assert err <= 1e-5, f"normalized error {err:.3g}"
+
+
+def test_packed_b_refused_for_bf16(torch_cuda, backend):
     ws = DeviceWorkspace()
     for s in range(3):
         ws.bind(s, torch_cuda.zeros(4096, dtype=torch_cuda.uint8, device="cuda"))
     with pytest.raises(UnsupportedOp):
         backend.dispatch(KernelCall.MatMul(MatMulCall(BufferRef(0), BufferRef(1), BufferRef(2),
-                                                      4, 4, 4, DTYPE_F32, True)), ws)
+                                                      4, 4, 4, DTYPE_BF16, True)), ws)
+
+
+def packed_archive(m, k, n, weight_also_added):
+    """y = relu-free MatMulAdd(x, W_packed, r); with weight_also_added the
+    packed constant is also an Add operand, so it stays packed on the device."""
+    from hologram_amd import (BinaryCall, ConstantEntry, HoloWriter, MatMulAddCall,
+                              PortDescriptor)
+    rng = np.random.default_rng(9)
+    w = (rng.standard_normal(k * n) / np.sqrt(k)).astype(np.float32)
+    r = rng.standard_normal(m * n).astype(np.float32)
+    wp = oracle.pack_b_panels(w, k, n)
+    wr = HoloWriter()
+    wr.inputs = [PortDescriptor("x", 0, m * k, DTYPE_F32, [m, k])]
+    wr.outputs = [PortDescriptor("y", 3, m * n, DTYPE_F32, [m, n])]
+    wr.constants = [ConstantEntry(1, DTYPE_F32, wp.tobytes()), ConstantEntry(2, DTYPE_F32, r.tobytes())]
+    calls = [KernelCall.MatMulAdd(MatMulAddCall(
+        MatMulCall(BufferRef(0), BufferRef(1, 0, wp.nbytes), BufferRef(3), m, k, n, DTYPE_F32,
+                   True), BufferRef(2)))]
+    if weight_also_added:
+        wr.outputs.append(PortDescriptor("w2", 4, 16, DTYPE_F32, [16]))
+        calls.append(KernelCall.Add(BinaryCall(BufferRef(1, 0, 64), BufferRef(1, 64, 64),
+                                               BufferRef(4), 16, 32, DTYPE_F32)))
+    wr.kernel_calls = calls
+    wr.exec_plan = [list(range(len(calls)))]
+    return wr.finish()
+
+
+@pytest.mark.parametrize("m", [4, 256])
+@pytest.mark.parametrize("also_added", [False, True])
+def test_packed_weight_session_matches_oracle(torch_cuda, backend, m, also_added):
+    """A reference-style archive whose f32 weight is panel-packed: unpacked at
+    load when the MatMul is its only reader (the device's own kernels then run,
+    few-row included), the packed kernel otherwise; both within 1e-5 of the
+    oracle walk, which unpacks the weight itself."""
+    from hologram_amd import HipSession
+    from oracle.graph import OracleSession
+    k, n = 512, 272
+    arch = packed_archive(m, k, n, also_added)
+    x = np.random.default_rng(10).standard_normal(m * k).astype(np.float32)
+    sess = HipSession(backend, arch)
+    ref = OracleSession(arch)
+    sess.write_input(0, x.tobytes())
+    ref.set_input(0, x.tobytes())
+    sess.run()
+    sess.synchronize()
+    ref.run()
+    got = np.frombuffer(sess.read_output(0), np.float32)
+    err = oracle.max_rel_err(got, ref.output(0).view(np.float32))
+    assert err <= 1e-5, err
+    if also_added:
+        assert sess.read_output(1) == ref.output(1).tobytes()
+    sess.close()
 
 
 def run_mm_rows(torch, backend, m, k, n, seed, rows, dtype=DTYPE_BF16):

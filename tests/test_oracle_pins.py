@@ -372,3 +372,96 @@ def test_blas_f64_product_is_the_f64_reference():
     y = oracle.matmul_f64_blas(a, b, m, k, n)
     ulps = np.abs(x.view(np.int32).astype(np.int64) - y.view(np.int32).astype(np.int64))
     assert ulps.max() <= 1 and np.mean(ulps != 0) < 0.01
+
+
+# ------------------------------------------------- DecodeAttentionValid ----
+
+def _valid_attention_f64(q, kp, vp, kn, vn, valid, b, h, hkv, m, past, new, d, scale):
+    """The op's law in f64 (kernel_call.rs:691-716, float_kernels.rs:3834-3957):
+    row qi of head hi sees past rows [0, min(valid, past)) then new rows
+    [0, min(qi + 1, new)) of kv head hi // (h // hkv); softmax(q.k / scale) . v."""
+    q = q.reshape(b, h, m, d).astype(np.float64)
+    kp, vp = (x.reshape(b, hkv, past, d).astype(np.float64) for x in (kp, vp))
+    kn, vn = (x.reshape(b, hkv, new, d).astype(np.float64) for x in (kn, vn))
+    vis = min(valid, past)
+    out = np.zeros((b, h, m, d))
+    for bi in range(b):
+        for hi in range(h):
+            kv = hi // (h // hkv)
+            for qi in range(m):
+                K = np.concatenate([kp[bi, kv, :vis], kn[bi, kv, :min(qi + 1, new)]])
+                V = np.concatenate([vp[bi, kv, :vis], vn[bi, kv, :min(qi + 1, new)]])
+                if len(K) == 0:
+                    continue
+                s = K @ q[bi, hi, qi] / scale
+                p = np.exp(s - s.max())
+                out[bi, hi, qi] = (p / p.sum()) @ V
+    return out.ravel()
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16, F16])
+@pytest.mark.parametrize("b,h,hkv,m,past,valid,d", [
+    (2, 4, 2, 1, 9, 5, 16),       # decode: a realized prefix of the bucket
+    (1, 6, 3, 3, 7, 7, 8),        # chunked prefill: 3 causal new rows, GQA group 2
+    (2, 2, 0, 2, 5, 99, 12),      # kv_heads 0 = heads; valid_len beyond past clamps
+    (1, 4, 1, 1, 0, 0, 32),       # no past at all: the new row only
+])
+def test_decode_attention_valid_oracle_matches_f64_law(dtype, b, h, hkv, m, past, valid, d):
+    rng = np.random.default_rng(b * 100 + h * 10 + m + d)
+    hk = h if hkv == 0 else hkv
+    q, kp, vp, kn, vn = (rng.standard_normal(n).astype(np.float32) for n in
+                         (b * h * m * d, b * hk * past * d, b * hk * past * d,
+                          b * hk * m * d, b * hk * m * d))
+    if dtype == BF16:
+        enc = lambda x: (x.view(np.uint32) >> 16).astype(np.uint16)
+        dec = lambda u: (u.astype(np.uint32) << 16).view(np.float32)
+        tol = 2 ** -7
+    elif dtype == F16:
+        enc = lambda x: x.astype(np.float16).view(np.uint16)
+        dec = lambda u: u.view(np.float16).astype(np.float32)
+        tol = 2 ** -10
+    else:
+        enc = dec = lambda x: x
+        tol = 1e-6
+    ops = [enc(x) for x in (q, kp, vp, kn, vn)]
+    # unrealized past rows hold NaN: the op must never read them
+    if past > min(valid, past):
+        for i in (1, 2):
+            t = ops[i].reshape(b, hk, past, d).copy()
+            t[:, :, min(valid, past):] = enc(np.full(1, np.nan, np.float32))[0]
+            ops[i] = t.ravel()
+    got = dec(oracle.decode_attention_valid(*ops, valid, b, h, hkv, m, past, m, d, 0, dtype))
+    want = _valid_attention_f64(*[dec(x) for x in ops[:3]], *[dec(x) for x in ops[3:]], valid,
+                                b, h, hk, m, past, m, d, max(math.sqrt(d), 1.0))
+    assert np.all(np.isfinite(got))
+    assert np.max(np.abs(got - want)) <= tol * (np.max(np.abs(want)) + 1e-6) * 2
+
+
+def test_decode_attention_valid_oracle_refusals_and_scale_bits():
+    z = np.zeros(64, np.float32)
+    with pytest.raises(ValueError):     # q_rows != new_len (float_kernels.rs:4205-4209)
+        oracle.decode_attention_valid(z, z, z, z, z, 0, 1, 2, 2, 2, 1, 1, 4, 0, F32)
+    with pytest.raises(ValueError):     # heads % kv_heads (:4216)
+        oracle.decode_attention_valid(z, z, z, z, z, 0, 1, 3, 2, 1, 1, 1, 4, 0, F32)
+    # scale_bits: the multiplier; a one-key row returns that key's V row exactly
+    rng = np.random.default_rng(3)
+    q, k, v = (rng.standard_normal(8).astype(np.float32) for _ in range(3))
+    sb = int(np.float32(0.25).view(np.uint32))
+    out = oracle.decode_attention_valid(q, z[:0], z[:0], k, v, 0, 1, 1, 1, 1, 0, 1, 8, sb, F32)
+    assert np.array_equal(out, v)
+
+
+@pytest.mark.parametrize("k,n", [(1, 1), (3, 16), (5, 17), (7, 40), (64, 100)])
+def test_panel_packing_follows_the_layout_formula(k, n):
+    """layout.rs:16-45, element by element: packed[(p*k + kk)*16 + c] is
+    b[kk*n + p*16 + c], zero where p*16 + c >= n; packed_len = ceil(n/16)*k*16;
+    unpacking returns the weight."""
+    b = np.arange(1, k * n + 1, dtype=np.float32)
+    pk = oracle.pack_b_panels(b, k, n)
+    assert pk.size == oracle.packed_len(k, n) == -(-n // 16) * k * 16
+    for p in range(-(-n // 16)):
+        for kk in range(k):
+            for c in range(16):
+                want = b[kk * n + p * 16 + c] if p * 16 + c < n else 0.0
+                assert pk[(p * k + kk) * 16 + c] == want
+    assert np.array_equal(oracle.unpack_b_panels(pk, k, n), b)

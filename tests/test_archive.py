@@ -226,3 +226,25 @@ def test_decode_attention_valid_refusals():
         validate(mk(1, 1, dtype=2), sizes)       # int8 is no compute dtype here
     with pytest.raises(SlotOutOfRange):
         validate(mk(1, 1, q_len=16), sizes)      # q shorter than 4 x 64 bf16
+
+
+GOLDEN = __import__("pathlib").Path(__file__).resolve().parent / "golden"
+
+
+def kappa_of(data: bytes) -> str:
+    """address_bytes (address.rs:96-99): blake3:<lowercase hex digest>."""
+    return "blake3:" + blake3(data).hex()
+
+
+def test_reference_compiled_fixture_loads_and_labels():
+    """The reference compiler's own archive (tests/golden/README.md): the
+    library's reader verifies its BLAKE3 footer and loads it dry; the oracle
+    walk's output carries the κ the reference's engine recorded."""
+    arch = (GOLDEN / "reference_fixture.holo").read_bytes()
+    want = (GOLDEN / "reference_fixture.kappa").read_text().strip()
+    s = HipSession(None, arch)
+    assert s.fingerprint() == arch[-32:] == blake3(arch[:-32])
+    assert len(s.outputs) == 1 and s.outputs[0].dtype == DTYPE_F32
+    o = OracleSession(arch)
+    o.run()
+    assert kappa_of(o.output(0).tobytes()) == want

@@ -312,3 +312,19 @@ def test_captured_walk_survives_other_work_on_its_backend(torch_cuda, backend):
         sess.synchronize()
         assert sess.read_output(1) == want, rnd
     sess.close()
+
+
+def test_reference_compiled_fixture_runs_to_its_kappa(torch_cuda, backend):
+    """The reference's compiled fixture.holo (tests/golden/) through the device
+    session: the output's κ (blake3 of its bytes, address.rs:96-99) equals the
+    reference engine's recorded fixture.kappa."""
+    from pathlib import Path
+    from hologram_amd import blake3
+    golden = Path(__file__).resolve().parent / "golden"
+    arch = (golden / "reference_fixture.holo").read_bytes()
+    want = (golden / "reference_fixture.kappa").read_text().strip()
+    sess = HipSession(backend, arch)
+    sess.run()
+    sess.synchronize()
+    assert "blake3:" + blake3(sess.read_output(0)).hex() == want
+    sess.close()

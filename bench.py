@@ -58,7 +58,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--only", default="attn,lut,kv,gemm,e2e")
+    p.add_argument("--only", default="attn,lut,copy,kv,gemm,e2e")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--seed", type=int, default=1234)
     return p.parse_args()
@@ -102,6 +102,25 @@ def queued_ms(torch, fn, n):
     e.record()
     torch.cuda.synchronize()
     return s.elapsed_time(e) / n
+
+
+def cpu_time(fn, min_seconds):
+    """Seconds per call of fn() on the host, repeated until min_seconds pass."""
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        calls += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds:
+            return dt / calls, calls, dt
+
+
+def cpu_baseline_obj(value_multi, value_single, unit, threads, sample):
+    """The cpu_baseline record: the multi-threaded leg is `value` (cores =
+    its threads), the single-threaded leg beside it, and the host."""
+    import oracle
+    return {"value": value_multi, "unit": unit, "cores": threads, "kind": "port",
+            "sample": sample, "single_thread": value_single, "host": oracle.host_info()}
 
 
 def bf16_normal(torch, shape, gen, outlier_frac=0.0):
@@ -204,18 +223,15 @@ def cpu_attn(torch, kq, ks, vq, vs, q, lens, B, H, Hkv, bucket, D, min_seconds=1
     th = oracle.host_threads()
     lib = oracle.lib()
     p = lambda a: a.ctypes.data
-    passes, t0 = 0, time.perf_counter()
-    while True:
-        lib.cb_decode_attention_i8(p(q_h), p(kq_h), p(ks_h), p(vq_h), p(vs_h), p(l_h), p(out), B,
-                                   H, Hkv, bucket, D, oracle.attn_scale(D), th)
-        passes += 1
-        dt = time.perf_counter() - t0
-        if dt >= min_seconds:
-            break
-    return {"value": B * passes / dt, "unit": "tok/s", "cores": th, "kind": "port",
-            "sample": f"the full config-4 batch ({B} sequences, {int(lens.sum())} keys), "
-                      f"{passes} passes in {dt:.1f} s",
-            "seconds": dt}
+    run = lambda t: lambda: lib.cb_decode_attention_i8(
+        p(q_h), p(kq_h), p(ks_h), p(vq_h), p(vs_h), p(l_h), p(out), B, H, Hkv, bucket, D,
+        oracle.attn_scale(D), t)
+    sec, passes, dt = cpu_time(run(th), min_seconds)
+    sec1, passes1, dt1 = cpu_time(run(1), min_seconds / 2)
+    return cpu_baseline_obj(B / sec, B / sec1, "tok/s", th,
+                            f"the full config-4 batch ({B} sequences, {int(lens.sum())} keys): "
+                            f"{passes} passes in {dt:.1f} s on {th} threads, {passes1} in "
+                            f"{dt1:.1f} s on 1")
 
 
 # --------------------------------------------------------------- config 1 ----
@@ -250,55 +266,122 @@ def bench_lut(torch, be, args, rep):
         xs = ins[0].cpu().numpy().view(np.uint16)
         o = np.empty_like(xs)
         th = oracle.host_threads()
-        t0 = time.perf_counter()
-        reps = 0
-        while time.perf_counter() - t0 < 10.0:
-            oracle.lib().cb_lut(tab.ctypes.data, xs.ctypes.data, o.ctypes.data, n, th)
-            reps += 1
-        dt = (time.perf_counter() - t0) / reps
-        rep["lut_cpu"] = {"value": n / dt / 1e9, "unit": "Gelem/s", "cores": th, "kind": "port",
-                          "sample": f"GELU gather of the 16,777,216 elements x{reps}"}
+        run = lambda t: lambda: oracle.lib().cb_lut(tab.ctypes.data, xs.ctypes.data,
+                                                    o.ctypes.data, n, t)
+        sec, reps, _ = cpu_time(run(th), 6.0)
+        sec1, reps1, _ = cpu_time(run(1), 3.0)
+        rep["lut_cpu"] = cpu_baseline_obj(n / sec / 1e9, n / sec1 / 1e9, "Gelem/s", th,
+                                          f"GELU gather of the 16,777,216 elements: x{reps} on "
+                                          f"{th} threads, x{reps1} on 1")
     return res
 
 
 # --------------------------------------------------------------- config 3 ----
 def bench_kv(torch, be, args, rep):
+    """Config 3: one step appends one new token per sequence to the K and to the
+    V cache (two KvQuantAppend dispatches: 16 x 8 planes, bucket 4096, D 128,
+    pos 4095). In place (the executor's move) a step writes 2 x 49,668 bytes;
+    the honest-copy form (the reference kernel's contract) also copies both
+    caches and their scales, 2 x (2 x 64 MiB + 2 x 2 MiB) + the new rows, with
+    two sets of caches rotated (528 MiB). The empty-kernel launch floor is
+    timed the same way beside the in-place figure."""
+    import numpy as np
     from hologram_amd import DTYPE_BF16, BufferRef, DeviceWorkspace, KernelCall, KvQuantAppendCall
     planes, bucket, D = 16 * 8, 4096, 128
     gen = torch.Generator(device="cuda")
     gen.manual_seed(args.seed + 3)
     ws = DeviceWorkspace()
-    cq = torch.randint(-127, 128, (planes * bucket * D,), dtype=torch.int8, device="cuda",
-                       generator=gen)
-    cs = torch.rand(planes * bucket, device="cuda", generator=gen)
-    oq, os_ = torch.empty_like(cq), torch.empty_like(cs)
-    news = [bf16_normal(torch, (planes, 1, D), gen, 0.02) for _ in range(4)]
-    pos = torch.tensor([4095], dtype=torch.int32, device="cuda")
-    for s, t in enumerate([pos, cq, cs, oq, os_] + news):
-        ws.bind(s, t)
+    nset = 2                                   # copy-form rotation: 2 x 264 MiB
+    slot = iter(range(1000))
+    bind = lambda t: (lambda s_: (ws.bind(s_, t), s_)[1])(next(slot))
+    pos_s = bind(torch.tensor([4095], dtype=torch.int32, device="cuda"))
+    caches = []                                # per set: (K q, K s, K out q, K out s, V ...)
+    keep = []
+    for _ in range(nset):
+        c = []
+        for _kv in range(2):
+            cq = torch.randint(-127, 128, (planes * bucket * D,), dtype=torch.int8, device="cuda",
+                               generator=gen)
+            cs = torch.rand(planes * bucket, device="cuda", generator=gen)
+            oq, os_ = torch.empty_like(cq), torch.empty_like(cs)
+            keep += [cq, cs, oq, os_]
+            c.append(tuple(bind(t) for t in (cq, cs, oq, os_)))
+        caches.append(c)
+    news = []
+    for _ in range(4):
+        t = bf16_normal(torch, (planes, 1, D), gen, 0.02)
+        keep.append(t)
+        news.append(bind(t))
+
+    def step_calls(form, i):
+        out = []
+        for kv in range(2):
+            cq, cs, oq, os_ = caches[i % nset][kv]
+            tq, ts = (cq, cs) if form == "in_place" else (oq, os_)
+            out.append(KernelCall.KvQuantAppend(KvQuantAppendCall(
+                BufferRef(news[(2 * i + kv) % 4]), BufferRef(pos_s), BufferRef(cq), BufferRef(cs),
+                BufferRef(tq), BufferRef(ts), planes, bucket, 1, D, DTYPE_BF16)))
+        return out
+
     res = {}
     for form in ("in_place", "copy"):
-        out_q, out_s = (BufferRef(1), BufferRef(2)) if form == "in_place" else (BufferRef(3), BufferRef(4))
-        calls = [KernelCall.KvQuantAppend(KvQuantAppendCall(
-            BufferRef(5 + i), BufferRef(0), BufferRef(1), BufferRef(2), out_q, out_s, planes,
-            bucket, 1, D, DTYPE_BF16)) for i in range(4)]
+        steps = [step_calls(form, i) for i in range(4)]
+        run = lambda i: [be.dispatch(c, ws) for c in steps[i % 4]]
         for i in range(max(args.warmup, 1)):
-            be.dispatch(calls[i % 4], ws)
+            run(i)
         be.synchronize()
-        ms = queued_ms(torch, lambda i: be.dispatch(calls[i % 4], ws), args.steps * 4)
+        ms = queued_ms(torch, run, args.steps * 4)
         if form == "in_place":
-            alg = planes * D * 2 + planes * D + planes * 4 + 4
+            alg = 2 * (planes * D * 2 + planes * D + planes * 4) + 4
         else:
-            alg = 2 * (planes * bucket * D + planes * bucket * 4) + planes * D * 2
+            alg = 2 * (2 * (planes * bucket * D + planes * bucket * 4) + planes * D * 2)
         gbs = alg / (ms / 1e3) / 1e9
-        res[form] = {"us": ms * 1e3, "alg_bytes": alg, "hbm_gbs": gbs,
-                     "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+        res[form] = {"us_per_step": ms * 1e3, "dispatches_per_step": 2, "alg_bytes": alg,
+                     "hbm_gbs": gbs,
+                     "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s",
+                                          profiled_traffic(f"kv_{form}_config3"))}
+    # the launch floor: an empty kernel, queued back to back the same way
+    floor_ms = queued_ms(torch, lambda i: torch.cuda._sleep(0), args.steps * 8)
+    res["launch_floor_us_per_kernel"] = floor_ms * 1e3
+    res["in_place"]["vs_launch_floor"] = (res["in_place"]["us_per_step"] / 2) / (floor_ms * 1e3)
+    res["copy"]["rotation_bytes"] = nset * 2 * 2 * (planes * bucket * D + planes * bucket * 4)
     rep["kv"] = res
+    if not args.no_cpu:
+        import oracle
+        th = oracle.host_threads()
+        hq = [np.ascontiguousarray(keep[i].cpu().numpy()) for i in range(4)]
+        nw = np.ascontiguousarray(keep[4 * nset * 2].cpu().view(torch.int16).numpy())
+        lib = oracle.lib()
+        p = lambda a: a.ctypes.data
+        def copy_step(t):
+            def f():
+                for _ in range(2):   # K and V
+                    lib.cb_kv_quant_append_copy(p(nw), DTYPE_BF16, 4095, p(hq[0]), p(hq[1]),
+                                                p(hq[2]), p(hq[3]), planes, bucket, 1, D, t)
+            return f
+        sec, n1, _ = cpu_time(copy_step(th), 4.0)
+        sec1, n2, _ = cpu_time(copy_step(1), 3.0)
+        res["cpu_baseline"] = cpu_baseline_obj(
+            1.0 / sec, 1.0 / sec1, "steps/s", th,
+            f"honest-copy form of one config-3 step (K and V: copy 2 x 66 MiB, quantize and place "
+            f"the 128 new rows): x{n1} on {th} threads, x{n2} on 1")
+        def move_step():
+            for _ in range(2):
+                lib.or_kv_quant_append(p(nw), DTYPE_BF16, 4095, p(hq[0]), p(hq[1]), planes, bucket,
+                                       1, D)
+        sec_m, n3, _ = cpu_time(move_step, 2.0)
+        res["cpu_baseline"]["in_place_single_thread_steps_s"] = 1.0 / sec_m
     return res
 
 
 # --------------------------------------------------------------- config 2 ----
 def bench_gemm(torch, be, args, rep):
+    """Config 2: bf16 and f32 C = A.B at 1024^3, 4096^3, 8192^3 and 16x4096x4096.
+    Every shape rotates enough (A, B, C) sets to pass 512 MiB (at least two),
+    so no call finds its operands in the 256 MB Infinity Cache. CPU legs: the
+    reference engine restatement (cpu_baseline.c) on the host threads for
+    every shape, and on one thread for 1024^3 and the few-row shape."""
+    import numpy as np
     from hologram_amd import DTYPE_BF16, DTYPE_F32, BufferRef, DeviceWorkspace, KernelCall, MatMulCall
     shapes = [(1024, 1024, 1024), (4096, 4096, 4096), (8192, 8192, 8192), (16, 4096, 4096)]
     gen = torch.Generator(device="cuda")
@@ -308,13 +391,15 @@ def bench_gemm(torch, be, args, rep):
                           (DTYPE_F32, torch.float32, FP32_PEAK_TFLOPS)):
         for (m, n, k) in shapes:
             es = 2 if dt == DTYPE_BF16 else 4
-            nbuf = max(1, min(4, (512 << 20) // ((m * k + k * n + m * n) * es)))
+            set_bytes = (m * k + k * n + m * n) * es
+            nbuf = max(2, -(-(512 << 20) // set_bytes) + 1)
             ws = DeviceWorkspace()
-            calls = []
+            calls, keep = [], []
             for i in range(nbuf):
                 a = (torch.randn(m * k, generator=gen, device="cuda") / math.sqrt(k)).to(tdt)
                 b = (torch.randn(k * n, generator=gen, device="cuda") / math.sqrt(k)).to(tdt)
                 c = torch.empty(m * n, dtype=tdt, device="cuda")
+                keep.append((a, b))
                 ws.bind(3 * i, a)
                 ws.bind(3 * i + 1, b)
                 ws.bind(3 * i + 2, c)
@@ -327,17 +412,47 @@ def bench_gemm(torch, be, args, rep):
             ms = queued_ms(torch, lambda i: be.dispatch(calls[i % nbuf], ws), steps)
             tf = 2.0 * m * n * k / (ms / 1e3) / 1e12
             key = f"{'bf16' if dt == DTYPE_BF16 else 'f32'}_{m}x{n}x{k}"
-            gbs = (m * k + k * n + m * n) * es / (ms / 1e3) / 1e9
+            gbs = set_bytes / (ms / 1e3) / 1e9
             dname = "bf16" if dt == DTYPE_BF16 else "f32"
             tkey = f"gemm_{dname}_{m}c" if m == n == k else f"gemm_{dname}_{m}x{n}x{k}"
             if m <= 64:   # few rows: bandwidth-bound on B
                 rl = roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s", profiled_traffic(tkey))
             else:
                 rl = roofline("mfma", tf, peak, "TFLOP/s", profiled_traffic(tkey))
-            res[key] = {"tflops": tf, "ms": ms, "hbm_gbs": gbs, "roofline": rl}
-            del ws, calls
+            res[key] = {"tflops": tf, "ms": ms, "hbm_gbs": gbs, "roofline": rl,
+                        "rotation_bytes": nbuf * set_bytes}
+            if not args.no_cpu:
+                res[key]["cpu_baseline"] = cpu_gemm(keep[0], m, k, n, dt,
+                                                    single=(m == 1024 or m <= 64))
+            del ws, calls, keep
     rep["gemm"] = res
     return res
+
+
+def cpu_gemm(ab, m, k, n, dt, single):
+    """The reference MatMul engines restated (4x16 AVX2/FMA tiles under the 64^3
+    bisection; bf16: widen, f32 engine, truncate; few-row bf16 streamed) on
+    the host threads, and on one thread when `single`; TFLOP/s."""
+    import numpy as np
+    import oracle
+    from hologram_amd import DTYPE_BF16
+    import torch
+    a, b = (np.ascontiguousarray(x.cpu().view(torch.int16 if dt == DTYPE_BF16 else torch.float32)
+                                 .numpy()) for x in ab)
+    out = np.zeros(m * n, a.dtype)
+    lib = oracle.lib()
+    if dt == DTYPE_BF16:
+        fn = lib.cb_matmul_bf16_gemv if m <= 8 else lib.cb_matmul_bf16
+    else:
+        fn = lib.cb_matmul_f32
+    run = lambda t: lambda: fn(a.ctypes.data, b.ctypes.data, out.ctypes.data, m, k, n, t)
+    th = oracle.host_threads()
+    flops = 2.0 * m * n * k
+    sec, reps, _ = cpu_time(run(th), 2.0)
+    sec1, reps1 = (cpu_time(run(1), 2.0)[:2] if single else (None, 0))
+    return cpu_baseline_obj(flops / sec / 1e12, flops / sec1 / 1e12 if sec1 else None, "TFLOP/s",
+                            th, f"{m}x{n}x{k}: x{reps} on {th} threads"
+                                + (f", x{reps1} on 1" if single else ""))
 
 
 # --------------------------------------------------------------- config 5 ----
@@ -375,7 +490,7 @@ def bench_e2e(torch, be, args, rep):
     dec = HipSession(be, dec_archive)
     t_load = time.perf_counter() - t0
     archive_bytes = len(dec_archive)
-    del dec_archive, pre_archive
+    del pre_archive
     dev = lambda b: torch.frombuffer(bytearray(b), dtype=torch.uint8).cuda()
     gen = torch.Generator(device="cuda")
     gen.manual_seed(args.seed + 6)
@@ -487,7 +602,78 @@ def bench_e2e(torch, be, args, rep):
         "prefill_roofline": roofline("mfma", pre_tflops, BF16_PEAK_TFLOPS, "TFLOP/s",
                                      kernel="whole prompt pass (8 x 512 tokens)"),
     }
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_decode_step(cfg, dec_archive, int(mean_len))
+    del dec_archive
     rep["e2e"] = res
+    return res
+
+
+def cpu_decode_step(cfg, archive, length):
+    """One decode step of the same 16-layer archive walked on the host with the
+    reference CPU engines (oracle/graph.py's cpu_baseline mode: streamed
+    few-row bf16 MatMuls, two-pass attention rows, in-place int8 appends), at
+    the timed run's mean context length; tok/s = batch / step time."""
+    import numpy as np
+    import oracle
+    from oracle.graph import OracleSession
+    from hologram_amd.decoder_graph import rope_tables
+    th = oracle.host_threads()
+    P, S, Dh = cfg.planes, cfg.bucket, cfg.head_dim
+    walks = {}
+    for t in (th, 1):
+        o = OracleSession(archive, verify_footer=False, products="cpu_baseline", threads=t)
+        cq, sq = rope_tables(cfg, np.array([length - 1]), cfg.heads)
+        ck, sk = rope_tables(cfg, np.array([length - 1]), cfg.kv_heads)
+        ins = [np.arange(cfg.batch, dtype=np.int32).tobytes(), np.uint32(length - 1).tobytes(),
+               np.full(cfg.batch, length, np.uint32).tobytes(), cq, sq, ck, sk]
+        for i, b in enumerate(ins):
+            o.set_input(i, b)
+        for layer in range(cfg.layers):
+            for j, z in enumerate([P * S * Dh, P * S * 4] * 2):
+                o.set_input(7 + 4 * layer + j, bytes(z))
+        o.run()                                  # first walk: tables, first touches
+        walks[t] = cpu_time(o.run, 6.0 if t == th else 3.0)
+        del o
+    (sec, n, _), (sec1, n1, _) = walks[th], walks[1]
+    return cpu_baseline_obj(cfg.batch / sec, cfg.batch / sec1, "tok/s", th,
+                            f"decode steps of the full {cfg.layers}-layer archive at context "
+                            f"{length}: x{n} on {th} threads, x{n1} on 1")
+
+
+# ------------------------------------------------------- copy ceiling ----
+def bench_copy(torch, be, args, rep):
+    """The plain-copy ceiling for the LUT's bytes: 32 MiB read + 32 MiB written
+    per launch, 8 pairs rotated (512 MiB), through the backend's own copy
+    kernel (a KvCacheWrite honest copy with no new rows, one copy16_kernel
+    launch) and through torch's device copy (hipMemcpyAsync), timed like the
+    LUT (queued_ms)."""
+    from hologram_amd import BufferRef, DeviceWorkspace, KernelCall, KvCacheWriteCall
+    nbytes, nbuf = 32 << 20, 8
+    ws = DeviceWorkspace()
+    src = [torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device="cuda") for _ in range(nbuf)]
+    dst = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(nbuf)]
+    pos = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ws.bind(2 * nbuf, pos)
+    ws.bind(2 * nbuf + 1, torch.zeros(16, dtype=torch.uint8, device="cuda"))
+    calls = []
+    for i in range(nbuf):
+        ws.bind(2 * i, src[i])
+        ws.bind(2 * i + 1, dst[i])
+        calls.append(KernelCall.KvCacheWrite(KvCacheWriteCall(
+            BufferRef(2 * i), BufferRef(2 * nbuf + 1), BufferRef(2 * nbuf), BufferRef(2 * i + 1),
+            1, nbytes // 16, 0, 16)))
+    for i in range(max(args.warmup, 1)):
+        be.dispatch(calls[i % nbuf], ws)
+    be.synchronize()
+    ms = queued_ms(torch, lambda i: be.dispatch(calls[i % nbuf], ws), args.steps * 4)
+    ms_t = queued_ms(torch, lambda i: dst[i % nbuf].copy_(src[i % nbuf]), args.steps * 4)
+    res = {"bytes_per_launch": 2 * nbytes,
+           "copy16_kernel": {"us": ms * 1e3, "gbs": 2 * nbytes / (ms / 1e3) / 1e9},
+           "hip_memcpy_d2d": {"us": ms_t * 1e3, "gbs": 2 * nbytes / (ms_t / 1e3) / 1e9}}
+    res["copy16_kernel"]["roofline"] = roofline("hbm", res["copy16_kernel"]["gbs"], HBM_PEAK_GBS,
+                                                "GB/s", profiled_traffic("copy16_64M"))
+    rep["copy"] = res
     return res
 
 
@@ -511,6 +697,9 @@ def main():
         torch.cuda.empty_cache()
     if "lut" in only:
         bench_lut(torch, be, args, rep)
+        torch.cuda.empty_cache()
+    if "copy" in only:
+        bench_copy(torch, be, args, rep)
         torch.cuda.empty_cache()
     if "kv" in only:
         bench_kv(torch, be, args, rep)
@@ -540,7 +729,7 @@ def main():
     if attn:
         line["roofline"] = roofline(
             "hbm", attn["hbm_gbs"], HBM_PEAK_GBS, "GB/s", profiled_traffic("decode_attn_i8_config4"),
-            "attn_mfma_kernel + attn_combine_kernel (one DecodeAttentionI8 dispatch); "
+            "attn_split_kernel + attn_merge_kernel (one DecodeAttentionI8 dispatch); "
             f"algorithmic bytes {attn['alg_bytes']}")
     if "attn_cpu" in rep:
         c = rep["attn_cpu"]
@@ -555,6 +744,12 @@ def main():
             for k, v in rep["lut"].items()}
         if "lut_cpu" in rep:
             comps["lut_bf16_16M"]["cpu_baseline"] = rep["lut_cpu"]
+        if "copy" in rep:
+            cp = rep["copy"]["copy16_kernel"]["us"]
+            for k in rep["lut"]:
+                comps["lut_bf16_16M"][k]["vs_copy_ceiling"] = cp / rep["lut"][k]["us"]
+    if "copy" in rep:
+        comps["copy_ceiling_64MiB"] = rep["copy"]
     if "kv" in rep:
         comps["kv_quant_append"] = rep["kv"]
     if "gemm" in rep:

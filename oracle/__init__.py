@@ -63,6 +63,7 @@ _SIGS = {
     "cb_lut": (None, [_P, _P, _P, _S, ctypes.c_int]),
     "cb_matmul_f32": (None, [_P, _P, _P, _S, _S, _S, ctypes.c_int]),
     "cb_matmul_bf16": (None, [_P, _P, _P, _S, _S, _S, ctypes.c_int]),
+    "cb_matmul_bf16_gemv": (None, [_P, _P, _P, _S, _S, _S, ctypes.c_int]),
     "cb_kv_quant_append_copy": (ctypes.c_int, [_P, ctypes.c_int, _U32, _P, _P, _P, _P, _U32,
                                                _U32, _U32, _U32, ctypes.c_int]),
     "cb_decode_attention_i8": (None, [_P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32,
@@ -91,11 +92,19 @@ def _p(a: np.ndarray) -> int:
     return a.ctypes.data
 
 
+_TABLES: dict = {}
+
+
 def build_table(act: int, dtype: int = DTYPE_BF16) -> np.ndarray:
-    t = np.zeros(65536, np.uint16)
-    if lib().or_build_table(act, dtype, _p(t)) != 0:
-        raise ValueError("no oracle table for this activation/dtype")
-    return t
+    """The oracle's (act, dtype) table, built once per process (a copy is
+    returned, so callers may modify it)."""
+    key = (act, dtype)
+    if key not in _TABLES:
+        t = np.zeros(65536, np.uint16)
+        if lib().or_build_table(act, dtype, _p(t)) != 0:
+            raise ValueError("no oracle table for this activation/dtype")
+        _TABLES[key] = t
+    return _TABLES[key].copy()
 
 
 def unary_lut(table: np.ndarray, x: np.ndarray) -> np.ndarray:
@@ -275,9 +284,30 @@ def max_rel_err(got, want) -> float:
 
 
 def host_threads() -> int:
-    """Threads for the CPU baseline: this process's CPU share, at most 16."""
+    """Threads for the CPU baseline: this process's CPU share, at most 16 (the
+    GPU box allots 16 host cores to each GPU, whatever nproc shows there)."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
         n = os.cpu_count() or 1
     return max(1, min(16, n))
+
+
+def host_info() -> dict:
+    """The host the CPU baseline runs on: nproc, this process's affinity, the
+    CPU model, and the thread count the multi-threaded legs use."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except AttributeError:
+        aff = os.cpu_count() or 1
+    return {"nproc": os.cpu_count(), "affinity": aff, "cpu_model": model,
+            "threads_used": host_threads(),
+            "thread_cap": "16: the box's host-core share per GPU"}

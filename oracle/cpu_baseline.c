@@ -216,6 +216,63 @@ void cb_matmul_bf16(const uint16_t *a, const uint16_t *b, uint16_t *out, size_t 
     free(o32);
 }
 
+/* Few-row bf16 path (m <= 8, float_kernels.rs:369-379; matmul_lowp_gemv,
+ * simd.rs:3808-3858): B is streamed once and widened in registers, never
+ * materialized; a is widened up front; output truncated. Threads take
+ * 64-column blocks of B. */
+typedef struct { const float *a; const uint16_t *b; float *out; size_t m, k, n; } gemv_ctx;
+static void gemv_task(void *c, size_t lo, size_t hi)
+{
+    gemv_ctx *x = (gemv_ctx *)c;
+    for (size_t blk = lo; blk < hi; ++blk) {
+        size_t c0 = blk * 64, c1 = c0 + 64 < x->n ? c0 + 64 : x->n;
+        for (size_t j = c0; j < c1; j += 8) {
+            if (j + 8 <= c1) {
+                __m256 acc[8];
+                for (size_t r = 0; r < x->m; ++r) acc[r] = _mm256_setzero_ps();
+                for (size_t kk = 0; kk < x->k; ++kk) {
+                    __m128i h = _mm_loadu_si128((const __m128i *)(x->b + kk * x->n + j));
+                    __m256 bv = _mm256_castsi256_ps(_mm256_slli_epi32(_mm256_cvtepu16_epi32(h), 16));
+                    for (size_t r = 0; r < x->m; ++r)
+                        acc[r] = _mm256_fmadd_ps(_mm256_set1_ps(x->a[r * x->k + kk]), bv, acc[r]);
+                }
+                for (size_t r = 0; r < x->m; ++r) _mm256_storeu_ps(x->out + r * x->n + j, acc[r]);
+            } else {
+                for (size_t jj = j; jj < c1; ++jj)
+                    for (size_t r = 0; r < x->m; ++r) {
+                        float s = 0.0f;
+                        for (size_t kk = 0; kk < x->k; ++kk) {
+                            uint32_t u = (uint32_t)x->b[kk * x->n + jj] << 16;
+                            float bf;
+                            memcpy(&bf, &u, 4);
+                            s += x->a[r * x->k + kk] * bf;
+                        }
+                        x->out[r * x->n + jj] = s;
+                    }
+            }
+        }
+    }
+}
+void cb_matmul_bf16_gemv(const uint16_t *a, const uint16_t *b, uint16_t *out, size_t m, size_t k,
+                         size_t n, int threads)
+{
+    float *a32 = (float *)malloc(sizeof(float) * m * k);
+    float *o32 = (float *)malloc(sizeof(float) * m * n);
+    for (size_t i = 0; i < m * k; ++i) {
+        uint32_t u = (uint32_t)a[i] << 16;
+        memcpy(&a32[i], &u, 4);
+    }
+    gemv_ctx c = {a32, b, o32, m, k, n};
+    cb_parallel(gemv_task, &c, (n + 63) / 64, threads);
+    for (size_t i = 0; i < m * n; ++i) {
+        uint32_t u;
+        memcpy(&u, &o32[i], 4);
+        out[i] = (uint16_t)(u >> 16);
+    }
+    free(a32);
+    free(o32);
+}
+
 /* ----------------------------------------------------------------- KV --- */
 typedef struct { const uint8_t *src; uint8_t *dst; size_t chunk, total; } copy_ctx;
 static void copy_task(void *c, size_t lo, size_t hi)

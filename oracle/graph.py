@@ -115,15 +115,23 @@ def _ports(b: bytes) -> list:
 class OracleSession:
     """Load an archive and run it on the CPU oracle, step by step."""
 
-    def __init__(self, archive: bytes, verify_footer: bool = True, products: str = "f64"):
+    def __init__(self, archive: bytes, verify_footer: bool = True, products: str = "f64",
+                 threads: int = 1):
         """products: "f64" sums every MatMul in f64 (the reference metric's
         exact product, tests/conformance.rs:100-112); "f32" sums in f32
         through numpy's BLAS (as the reference CPU engine accumulates in f32,
         in another order). Two walks that differ only here measure how far
-        two correct bf16 walks of the same archive land apart."""
-        if products not in ("f64", "f32"):
+        two correct bf16 walks of the same archive land apart.
+        "cpu_baseline" times the reference CPU engines instead (bench.py's
+        CPU leg): MatMul through oracle/cpu_baseline.c's restatement of the
+        reference kernels (few-row bf16 streamed, simd.rs:3808-3858; else the
+        blocked f32 engine), decode attention through its two-pass rows, on
+        `threads` host threads, and int8 appends in place as the reference
+        executor's KV move does (session.rs:1313-1370)."""
+        if products not in ("f64", "f32", "cpu_baseline"):
             raise ValueError(products)
         self.products = products
+        self.threads = threads
         if archive[:4] != b"HOLO":
             raise ValueError("bad magic")
         ver, _flags, nsec = struct.unpack_from("<HHH", archive, 4)
@@ -241,18 +249,29 @@ class OracleSession:
             m, k, n = c["m"], c["k"], c["n"]
             dt = c["dtype"]
             es = DT_BYTES[dt]
-            a = self._f32(self._view(c["a"], m * k * es), dt)
-            if c["packed"]:                          # layout.rs:16-45 (f32 weights only)
-                if dt != F32:
-                    raise ValueError("a panel-packed B is an f32 layout")
-                from . import packed_len, unpack_b_panels
-                b = unpack_b_panels(self._f32(self._view(c["b"], packed_len(k, n) * 4), dt), k, n)
-            else:
-                b = self._f32(self._view(c["b"], k * n * es), dt)
+            def operands():
+                a = self._f32(self._view(c["a"], m * k * es), dt)
+                if c["packed"]:                      # layout.rs:16-45 (f32 weights only)
+                    if dt != F32:
+                        raise ValueError("a panel-packed B is an f32 layout")
+                    from . import packed_len, unpack_b_panels
+                    b = unpack_b_panels(self._f32(self._view(c["b"], packed_len(k, n) * 4), dt),
+                                        k, n)
+                else:
+                    b = self._f32(self._view(c["b"], k * n * es), dt)
+                return a, b
             from . import FUSED_TO_LUT, build_table, fused_act_f32, matmul_f64_blas, matmul_ref_f64
-            if self.products == "f32":
+            if self.products == "cpu_baseline" and dt == BF16:
+                raw_a = np.ascontiguousarray(self._view(c["a"], m * k * es))
+                raw_b = np.ascontiguousarray(self._view(c["b"], k * n * es))
+                prod = self._baseline_matmul(None, None, raw_a, raw_b, m, k, n, dt)
+            elif self.products == "cpu_baseline":
+                prod = self._baseline_matmul(*operands(), None, None, m, k, n, dt)
+            elif self.products == "f32":
+                a, b = operands()
                 prod = (a.reshape(m, k) @ b.reshape(k, n)).ravel()
             else:
+                a, b = operands()
                 ref = matmul_ref_f64 if m * k * n <= (1 << 24) else matmul_f64_blas
                 prod = ref(a, b, m, k, n)
             v = self._f32(self._narrow(prod, dt), dt)
@@ -264,6 +283,18 @@ class OracleSession:
             elif tag in (106, 108):
                 v = fused_act_f32(c["act"], v)
             self._out(c["output"], m * n * es)[:] = self._narrow(v, dt)
+        elif tag == 122 and self.products == "cpu_baseline":
+            # the executor's in-place move: the cache slots are updated and the
+            # output slots alias them (no honest copy of the whole cache)
+            P, S, R, Dh = c["planes"], c["bucket"], c["new_rows"], c["head_dim"]
+            es = DT_BYTES[c["dtype"]]
+            new = np.ascontiguousarray(self._view(c["new"], P * R * Dh * es))
+            pos = int(np.ascontiguousarray(self._view(c["pos"], 4)).view(np.uint32)[0])
+            cq, cs = self.slots[c["cache"][0]], self.slots[c["scales"][0]]
+            if L.or_kv_quant_append(_p(new), c["dtype"], pos, _p(cq), _p(cs), P, S, R, Dh) != 0:
+                raise ValueError("kv_quant_append refused")
+            self.slots[c["output"][0]] = cq
+            self.slots[c["output_scales"][0]] = cs
         elif tag == 122:
             P, S, R, Dh = c["planes"], c["bucket"], c["new_rows"], c["head_dim"]
             es = DT_BYTES[c["dtype"]]
@@ -285,8 +316,16 @@ class OracleSession:
             vs = np.ascontiguousarray(self._view(c["vs"], B * Hkv * S * 4)).view(np.float32)
             lens = np.ascontiguousarray(self._view(c["lens"], B * 4)).view(np.uint32)
             from . import attn_scale, decode_attention_i8
-            o = decode_attention_i8(q, kq, ks, vq, vs, lens, B, H, Hkv, S, D,
-                                    attn_scale(D, c["scale_bits"]))
+            if self.products == "cpu_baseline":
+                o = np.zeros(B * H * D, np.float32)
+                q = np.ascontiguousarray(q)
+                lens = np.ascontiguousarray(lens)
+                L.cb_decode_attention_i8(_p(q), _p(kq), _p(ks), _p(vq), _p(vs), _p(lens), _p(o),
+                                         B, H, Hkv, S, D, attn_scale(D, c["scale_bits"]),
+                                         self.threads)
+            else:
+                o = decode_attention_i8(q, kq, ks, vq, vs, lens, B, H, Hkv, S, D,
+                                        attn_scale(D, c["scale_bits"]))
             self._out(c["output"], B * H * D * es)[:] = self._narrow(o, c["dtype"])
         elif tag == 121:
             B, H, M, D = c["batch"], c["heads"], c["q_rows"], c["head_dim"]
@@ -328,6 +367,21 @@ class OracleSession:
             self._out(c["output"], 4 * c["rows"])[:] = o.view(np.uint8)
         else:
             raise ValueError(f"oracle graph: no restatement for discriminant {tag}")
+
+    def _baseline_matmul(self, a, b, raw_a, raw_b, m, k, n, dt) -> np.ndarray:
+        """The reference CPU MatMul engines (cpu_baseline.c), f32 result."""
+        L = lib()
+        th = self.threads
+        if dt == BF16 and raw_b is not None:
+            out = np.zeros(m * n, np.uint16)
+            fn = L.cb_matmul_bf16_gemv if m <= 8 else L.cb_matmul_bf16
+            fn(_p(raw_a), _p(raw_b), _p(out), m, k, n, th)
+            return (out.astype(np.uint32) << 16).view(np.float32)
+        out = np.zeros(m * n, np.float32)
+        a = np.ascontiguousarray(a, np.float32)
+        b = np.ascontiguousarray(b, np.float32)
+        L.cb_matmul_f32(_p(a), _p(b), _p(out), m, k, n, th)
+        return out
 
     @staticmethod
     def _f32(b: np.ndarray, dtype: int) -> np.ndarray:

@@ -146,6 +146,7 @@ SIGNATURES = {
     "holo_hip_slot_bind": (ctypes.c_int, [_P, ctypes.c_uint32, _P, ctypes.c_uint64]),
     "holo_hip_slot_unbind": (ctypes.c_int, [_P, ctypes.c_uint32]),
     "holo_hip_dispatch": (ctypes.c_int, [_P, ctypes.POINTER(KernelCallC)]),
+    "holo_hip_dispatch_noalloc": (ctypes.c_int, [_P, ctypes.POINTER(KernelCallC)]),
     "holo_hip_dispatch_encoded": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.c_size_t,
                                                  ctypes.POINTER(ctypes.c_size_t)]),
     "holo_hip_synchronize": (ctypes.c_int, [_P]),

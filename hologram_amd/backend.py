@@ -136,6 +136,13 @@ class HipBackend:
         kc = call.to_c()
         check(_ffi.lib().holo_hip_dispatch(self._h, ctypes.byref(kc)))
 
+    def dispatch_noalloc(self, call: KernelCall, workspace: DeviceWorkspace) -> None:
+        """holo_hip_dispatch_noalloc: decode attention (123 / 125) on the fixed
+        per-device scratch, with no device allocation (see include/holo_hip.h)."""
+        self._sync_slots(workspace)
+        kc = call.to_c()
+        check(_ffi.lib().holo_hip_dispatch_noalloc(self._h, ctypes.byref(kc)))
+
     def dispatch_encoded(self, wire: bytes, workspace: DeviceWorkspace) -> int:
         """Dispatch one call given in the archive wire format; returns its length."""
         self._sync_slots(workspace)

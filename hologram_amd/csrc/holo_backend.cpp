@@ -677,7 +677,7 @@ int do_kv_quant(holo_backend *be, const SlotTable &st, const holo_kv_quant_appen
 // ---------------------------------------------------- DecodeAttnI8 -------
 // Refusals follow decode_attention_valid_float (src/cpu/float_kernels.rs:4192-4220).
 int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attention_i8_call &c,
-               uint32_t q_rows = 1) {
+               uint32_t q_rows = 1, bool static_scratch = false) {
     const char *op = "decode_attention_i8";
     if (c.batch == 0 || c.heads == 0 || c.head_dim == 0) return HOLO_OK;
     const uint32_t hkv = c.kv_heads == 0 ? c.heads : c.kv_heads;
@@ -724,9 +724,23 @@ int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attentio
         memcpy(&sm, &c.scale_bits, 4);
         scale = sm > 0.0f ? 1.0f / sm : dflt;
     }
-    HOLO_TRY(ensure_scratch(
-        be, holo::attn_i8_scratch_bytes(c.batch, c.heads, hkv, c.bucket_rows, c.head_dim, q_rows),
-        op));
+    const size_t scratch_bytes =
+        holo::attn_i8_scratch_bytes(c.batch, c.heads, hkv, c.bucket_rows, c.head_dim, q_rows);
+    void *scratch = nullptr;
+    if (static_scratch) {
+        // the allocation-free form: the fixed per-device array, never grown
+        if (scratch_bytes > holo::kStaticScratchBytes)
+            return fail(HOLO_ERR_UNSUPPORTED_OP,
+                        std::string(op) + " (no-allocation form): needs " +
+                            std::to_string(scratch_bytes) + " bytes of scratch, above the fixed " +
+                            std::to_string(holo::kStaticScratchBytes) + "; use holo_hip_dispatch");
+        scratch = holo::static_scratch(be->device);
+        if (!scratch)
+            return fail(HOLO_ERR_INIT, std::string(op) + ": the static scratch has no device address");
+    } else {
+        HOLO_TRY(ensure_scratch(be, scratch_bytes, op));
+        scratch = be->scratch;
+    }
     holo::AttnI8Args a;
     a.q = rv[0].base;
     a.kq = reinterpret_cast<const int8_t *>(rv[1].base);
@@ -751,7 +765,7 @@ int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attentio
         HOLO_TRY(launched(holo::launch_lens_within(a.lens, c.batch, c.bucket_rows, be->dev_err,
                                                    be->stream),
                           op));
-    return launched(holo::launch_attn_i8(a, be->scratch, be->stream), op);
+    return launched(holo::launch_attn_i8(a, scratch, be->stream), op);
 }
 
 // -------------------------------------------------- DecodeAttentionValid --
@@ -1333,6 +1347,12 @@ int holo_hip_backend_create(int device, void *stream, holo_backend **out) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(HOLO_ERR_INIT, std::string("backend_create: built for gfx950, device is ") +
                                        prop.gcnArchName);
+    // this device's address of the static scratch (holo_hip_dispatch_noalloc),
+    // taken once per device while it is current
+    const hipError_t se = holo::static_scratch_init(device);
+    if (se != hipSuccess)
+        return fail(HOLO_ERR_INIT, std::string("backend_create: static scratch address: ") +
+                                       hipGetErrorString(se));
     auto *be = new holo_backend();
     be->device = device;
     be->stream = static_cast<hipStream_t>(stream);
@@ -1384,6 +1404,21 @@ int holo_hip_dispatch(holo_backend *be, const holo_kernel_call *call) {
     SlotTable st;
     st.be = be;
     return dispatch_impl(be, st, call);
+}
+
+int holo_hip_dispatch_noalloc(holo_backend *be, const holo_kernel_call *call) {
+    if (!be || !call) return fail(HOLO_ERR_INIT, "dispatch_noalloc: null argument");
+    SlotTable st;
+    st.be = be;
+    switch (call->tag) {
+        case HOLO_OP_DECODE_ATTN_I8: return do_attn_i8(be, st, call->u.attn_i8, 1, true);
+        case HOLO_OP_ATTN_I8_ROWS:
+            return do_attn_i8(be, st, call->u.attn_i8_rows.attn, call->u.attn_i8_rows.q_rows, true);
+        default:
+            return fail(HOLO_ERR_UNSUPPORTED_OP,
+                        "dispatch_noalloc: serves DecodeAttentionI8 (123) and AttentionI8Rows (125); "
+                        "use holo_hip_dispatch");
+    }
 }
 
 int holo_hip_dispatch_encoded(holo_backend *be, const uint8_t *wire, size_t len, size_t *consumed) {

@@ -29,6 +29,14 @@ hipError_t launch_kv_quant_append(const void *nw, uint8_t dtype, const uint32_t 
                                   uint32_t bucket, uint32_t new_rows, uint32_t head_dim,
                                   hipStream_t stream);
 
+// static_scratch.hip — the fixed device scratch of holo_hip_dispatch_noalloc:
+// kStaticScratchBytes per GPU, held until the process ends. init records this
+// device's address of the array (call with `device` current, once per device);
+// static_scratch returns it (nullptr before init).
+constexpr size_t kStaticScratchBytes = size_t(16) << 20;
+hipError_t static_scratch_init(int device);
+void *static_scratch(int device);
+
 // attn.hip — int8-KV GQA decode attention. `scratch` holds the split-K
 // partials; attn_i8_scratch_bytes() gives its size. Calls sharing one scratch
 // must not overlap.

@@ -358,6 +358,18 @@ int holo_hip_slot_unbind(holo_backend *be, uint32_t slot);
  * HOLO_ERR_UNSUPPORTED_OP so the caller can route the call elsewhere, as the
  * reference's GPU backends do (src/metal_backend/mod.rs:172-180). */
 int holo_hip_dispatch(holo_backend *be, const holo_kernel_call *call);
+/* No counterpart in the reference: the allocation-free variant of
+ * holo_hip_dispatch, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). It serves DecodeAttentionI8 (123) and AttentionI8Rows (125),
+ * whose kernels need split-K scratch, from a fixed 16 MiB device array per GPU
+ * (held until the process ends) instead of the backend's grown scratch; it
+ * calls no hipMalloc/hipFree. A call needing more scratch than 16 MiB is
+ * refused with HOLO_ERR_UNSUPPORTED_OP (config 4's batch needs about 2 MiB).
+ * All calls on one GPU share that array: calls that overlap in time on one
+ * GPU (other streams, other threads, other backends) race; serialize them.
+ * Results are bit-identical to holo_hip_dispatch of the same call. */
+int holo_hip_dispatch_noalloc(holo_backend *be, const holo_kernel_call *call);
 /* Same, from one call in the archive wire format (u16 LE discriminant + LE
  * payload, crates/hologram-archive/src/kernel_codec.rs:130-137, 557-813).
  * *consumed receives the encoded length. */

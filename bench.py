@@ -733,7 +733,8 @@ def main():
             f"algorithmic bytes {attn['alg_bytes']}")
     if "attn_cpu" in rep:
         c = rep["attn_cpu"]
-        line["cpu_baseline"] = {k: c[k] for k in ("value", "unit", "cores", "kind", "sample")}
+        line["cpu_baseline"] = {k: c[k] for k in ("value", "unit", "cores", "kind", "sample",
+                                                  "single_thread", "host")}
     comps = {}
     if "lut" in rep:
         comps["lut_bf16_16M"] = {

@@ -49,7 +49,7 @@ struct holo_backend {
     int device = 0;
     hipStream_t stream = nullptr;
     std::map<uint32_t, Range> slots;
-    uint16_t *lut_dev[5][2] = {};       // [act][0 = f16, 1 = bf16], uploaded once
+    uint16_t *lut_dev[9][2] = {};       // [table id][0 = f16, 1 = bf16], uploaded once
     void *scratch = nullptr;            // split-K partials (decode attention, few-row MatMul)
     size_t scratch_bytes = 0;
     int *dev_err = nullptr;             // device-side refusals (Gather's index range), read at sync
@@ -1308,15 +1308,20 @@ int lut_act_of_fused(uint32_t act) {
         case kFusedSigmoid: return HOLO_ACT_SIGMOID;
         case kFusedTanh: return HOLO_ACT_TANH;
         case kFusedExp: return HOLO_ACT_EXP;
+        case kFusedRelu: return kTableRelu;
+        case kFusedElu: return kTableElu;
+        case kFusedSelu: return kTableSelu;
         default: return -1;
     }
 }
 
+// Every fused_activation (kernel_call.rs:861-870) is served: 16-bit products
+// through the table of narrow(f(widen(x))), f32 products and every sum after a
+// residual add computed in f32 (act_f32).
 bool fused_act_supported(uint32_t act, uint8_t dtype, bool after_add) {
-    const bool computed = act == kFusedGelu || act == kFusedSilu || act == kFusedSigmoid ||
-                          act == kFusedTanh;
-    if (dtype == HOLO_DTYPE_BF16) return after_add ? computed : lut_act_of_fused(act) >= 0;
-    if (dtype == HOLO_DTYPE_F32) return computed;
+    const bool known = act >= 1 && act <= 8;
+    if (dtype == HOLO_DTYPE_BF16) return after_add ? known : lut_act_of_fused(act) >= 0;
+    if (dtype == HOLO_DTYPE_F32) return known;
     return false;
 }
 

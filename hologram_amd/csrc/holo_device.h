@@ -76,11 +76,76 @@ __device__ inline float exp_det(float x) {
     return p * __uint_as_float(sb);
 }
 
+// libm 0.2.16 expf (exp_f, src/cpu/float_kernels.rs:3498-3500): the
+// published FreeBSD e_expf.c reduction and rational approximation, then the
+// musl scalbnf scaling, with the same operation order as the host table
+// builder's restatement (IEEE basic operations, no contraction).
+__device__ inline float scale_by_pow2_dev(float y, int32_t n) {
+    const float two127 = __uint_as_float(0x7f000000u);
+    const float two_m102 = __uint_as_float(0x00800000u) * __uint_as_float(0x4b800000u);
+    for (int step = 0; step < 2; ++step) {
+        if (n > 127) {
+            y *= two127;
+            n -= 127;
+        } else if (n < -126) {
+            y *= two_m102;
+            n += 102;
+        } else {
+            break;
+        }
+    }
+    if (n > 127) n = 127;
+    if (n < -126) n = -126;
+    return y * __uint_as_float(uint32_t(0x7f + n) << 23);
+}
+
+__device__ inline int32_t trunc_sat_i32_dev(float v) {
+    if (v != v) return 0;
+    if (v >= 2147483648.0f) return 2147483647;
+    if (v < -2147483648.0f) return int32_t(-2147483647 - 1);
+    return int32_t(v);
+}
+
+__device__ inline float libm_expf_dev(float x) {
+    uint32_t ax = __float_as_uint(x);
+    const int neg = int(ax >> 31);
+    ax &= 0x7fffffffu;
+    if (ax >= 0x42aeac50u) {
+        if (ax > 0x7f800000u) return x;
+        if (!neg && ax >= 0x42b17218u) return x * __uint_as_float(0x7f000000u);
+        if (neg && ax >= 0x42cff1b5u) return 0.0f;
+    }
+    int32_t k = 0;
+    float hi = x, lo = 0.0f;
+    if (ax > 0x3eb17218u) {
+        k = ax > 0x3f851592u ? trunc_sat_i32_dev(1.4426950216e+00f * x + (neg ? -0.5f : 0.5f))
+                             : 1 - 2 * neg;
+        const float kf = float(k);
+        hi = x - kf * 6.9314575195e-01f;
+        lo = kf * 1.4286067653e-06f;
+        x = hi - lo;
+    } else if (ax <= 0x39000000u) {
+        return 1.0f + x;
+    }
+    const float xx = x * x;
+    const float c = x - xx * (1.6666625440e-1f + xx * -2.7667332906e-3f);
+    const float y = 1.0f + (((x * c) / (2.0f - c) - lo) + hi);
+    return k == 0 ? y : scale_by_pow2_dev(y, k);
+}
+
 // f32 activations of the fused MatMul epilogues, by fused_activation id
-// (kernel_call.rs:861-870): gelu_f, silu_f, sigmoid_f, tanh_f
-// (src/cpu/float_kernels.rs:3549-3566), same operation order.
+// (kernel_call.rs:861-870, fused_act_fn float_kernels.rs:768-780): relu_f
+// (:3448), gelu_f, silu_f, sigmoid_f, tanh_f (:3549-3566), elu_f and selu_f
+// (:3641-3656), exp_f (libm expf); same operation order.
 __device__ inline float act_f32(uint32_t act, float x) {
     switch (act) {
+        case 1: return x > 0.0f ? x : 0.0f;                  // RELU: x.max(0.0), NaN -> +0
+        case 6: return x >= 0.0f ? x : libm_expf_dev(x) - 1.0f;   // ELU
+        case 7: {                                            // SELU
+            const float alpha = 1.6732632f, scale = 1.050701f;
+            return x >= 0.0f ? scale * x : scale * alpha * (libm_expf_dev(x) - 1.0f);
+        }
+        case 8: return libm_expf_dev(x);                     // EXP
         case 2: {   // GELU
             const float cube = ((0.044715f * x) * x) * x;
             const float u = 0.7978846f * (x + cube);

@@ -146,6 +146,8 @@ constexpr uint8_t kEpiStore = 0, kEpiAct = 1, kEpiAdd = 2, kEpiAddAct = 3;
 // fused_activation ids (crates/hologram-compute/src/kernel_call.rs:861-870)
 constexpr uint32_t kFusedRelu = 1, kFusedGelu = 2, kFusedSilu = 3, kFusedSigmoid = 4,
                    kFusedTanh = 5, kFusedElu = 6, kFusedSelu = 7, kFusedExp = 8;
+// Table ids of the 16-bit fused Relu/Elu/Selu (beyond lut_act's 0-5).
+constexpr int kTableRelu = 6, kTableElu = 7, kTableSelu = 8;
 struct EpiSeg {
     uint32_t n = 0, col0 = 0;          // columns; first column in the partials' column space
     uint8_t base = kEpiStore;

@@ -104,6 +104,14 @@ float act_gelu(float x) {
     return (0.5f * x) * (1.0f + act_tanh(inner));
 }
 float act_silu(float x) { return x * act_sigmoid(x); }
+// relu_f, elu_f, selu_f (src/cpu/float_kernels.rs:3448, 3641-3656). relu is
+// x.max(0.0): a NaN or a zero of either sign gives +0.0.
+float act_relu(float x) { return x > 0.0f ? x : 0.0f; }
+float act_elu(float x) { return x >= 0.0f ? x : libm_expf(x) - 1.0f; }
+float act_selu(float x) {
+    const float alpha = 1.6732632f, scale = 1.050701f;
+    return x >= 0.0f ? scale * x : scale * alpha * (libm_expf(x) - 1.0f);
+}
 
 // IEEE binary16 -> binary32 (src/cpu/dtype.rs:94-118).
 float half_to_float(uint16_t h) {
@@ -144,7 +152,10 @@ uint16_t float_to_half(float f) {
 
 }  // namespace
 
-// Returns false for an activation id this build has no table for.
+// Returns false for an activation id this build has no table for. Ids 0-4
+// are lut_act's (kernel_call.rs:877-885); 6-8 are this backend's tables for
+// the fused epilogues' Relu, Elu and Selu on 16-bit products (the reference
+// computes narrow(f(widen(x))) per element, which is the table entry).
 bool build_lut_table(int act, bool f16, uint16_t *t) {
     float (*fn)(float) = nullptr;
     switch (act) {
@@ -153,6 +164,9 @@ bool build_lut_table(int act, bool f16, uint16_t *t) {
         case 2: fn = act_gelu; break;
         case 3: fn = act_silu; break;
         case 4: fn = libm_expf; break;
+        case 6: fn = act_relu; break;
+        case 7: fn = act_elu; break;
+        case 8: fn = act_selu; break;
         default: return false;
     }
     for (uint32_t b = 0; b < 65536u; ++b) {

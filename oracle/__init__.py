@@ -38,6 +38,7 @@ _SIGS = {
     "or_build_table": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _P]),
     "or_unary_lut": (None, [_P, _P, _P, _S]),
     "or_quantize_row_i8": (_F, [_P, _P, _S]),
+    "or_matmul_q_omajor": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, _P, _S, _S, _S]),
     "or_matmul_i8_pc_omajor": (None, [_P, _P, _P, _P, _S, _S, _S]),
     "or_fnv1a_f32": (ctypes.c_uint64, [_P, _S]),
     "or_kv_cache_write": (ctypes.c_int, [_P, _P, _U32, _P, _U32, _U32, _U32, _U32]),
@@ -123,6 +124,19 @@ def quantize_row_i8(a: np.ndarray) -> tuple:
 def matmul_i8_pc_omajor(a, bq, scales, m, k, n) -> np.ndarray:
     out = np.zeros(m * n, np.float32)
     lib().or_matmul_i8_pc_omajor(_p(a), _p(bq), _p(scales), _p(out), m, k, n)
+    return out
+
+
+def matmul_q_omajor(tier: int, a, bq, scales, m, k, n, codebook=None) -> np.ndarray:
+    """Output-major W8A8 GEMV for the i8 (2), i4 (10) and e8cb (11) tiers."""
+    out = np.zeros(m * n, np.float32)
+    a = np.ascontiguousarray(a, np.float32)
+    bq = np.ascontiguousarray(bq).view(np.uint8)
+    scales = np.ascontiguousarray(scales, np.float32)
+    cb = None if codebook is None else np.ascontiguousarray(codebook).view(np.int8)
+    if lib().or_matmul_q_omajor(tier, _p(a), _p(bq), _p(cb) if cb is not None else None,
+                                _p(scales), _p(out), m, k, n) != 0:
+        raise ValueError("matmul_q_omajor refused")
     return out
 
 

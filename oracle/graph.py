@@ -277,7 +277,10 @@ class OracleSession:
             v = self._f32(self._narrow(prod, dt), dt)
             if tag in (107, 108):
                 v = v + self._f32(self._view(c["residual"], m * n * es), dt)
-            if tag == 106 and dt == BF16:
+            if tag == 106 and dt == BF16 and c["act"] not in FUSED_TO_LUT:
+                # Relu/Elu/Selu on a 16-bit product: f on the widened value, narrowed
+                v = fused_act_f32(c["act"], v)
+            elif tag == 106 and dt == BF16:
                 t = build_table(FUSED_TO_LUT[c["act"]], dt)
                 v = self._f32(t[self._narrow(v, dt).view(np.uint16)].view(np.uint8), dt)
             elif tag in (106, 108):

@@ -10,6 +10,7 @@
 #include "holo_oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 /* ------------------------------------------------------------------------ */
@@ -204,10 +205,23 @@ float or_silu_f(float x) { return x * or_sigmoid_f(x); }
 /* fused_act_fn (src/cpu/float_kernels.rs:768-780) over a slice, the f32
  * epilogue of MatMulActivation / MatMulAddActivation. ids: fused_activation
  * (src/kernel_call.rs:861-870). Relu, Elu and Selu are not restated (-1). */
+/* relu_f (float_kernels.rs:3448, x.max(0.0): NaN and -0.0 give +0.0), elu_f
+ * and selu_f (:3641-3656) */
+static float relu_f(float x) { return x > 0.0f ? x : 0.0f; }
+static float elu_f(float x) { return x >= 0.0f ? x : or_libm_expf(x) - 1.0f; }
+static float selu_f(float x)
+{
+    const float alpha = 1.6732632f, scale = 1.050701f;
+    return x >= 0.0f ? scale * x : scale * alpha * (or_libm_expf(x) - 1.0f);
+}
+
 int or_fused_act_f32(int act, const float *in, float *out, size_t n)
 {
     for (size_t i = 0; i < n; ++i) {
         switch (act) {
+        case 1: out[i] = relu_f(in[i]); break;
+        case 6: out[i] = elu_f(in[i]); break;
+        case 7: out[i] = selu_f(in[i]); break;
         case 2: out[i] = or_gelu_f(in[i]); break;
         case 3: out[i] = or_silu_f(in[i]); break;
         case 4: out[i] = or_sigmoid_f(in[i]); break;
@@ -277,11 +291,31 @@ float or_quantize_row_i8(const float *a, int8_t *q, size_t k)
 
 /* simd.rs:5295-5480 with the portable inner of :5203-5215: exact i32 dot,
  * out = (acc as f32) * (scale_a * scales[j]); an all-zero row writes zeros. */
-void or_matmul_i8_pc_omajor(const float *a, const int8_t *bq, const float *scales,
-                            float *out, size_t m, size_t k, size_t n)
+/* The output-major weight's integer level at (column j, row kk), per tier:
+ * i8 one byte (quant_tier.rs I8); i4 packed nibbles, unit u = j*k + kk in the
+ * low nibble of byte u/2 when u is even, sign-extended from bit 3
+ * (omajor_repack :117-131, ScalarQuant::read float_kernels.rs:440-455); e8cb a
+ * codebook index per 8-row group, the level codebook[idx*8 + kk%8]
+ * (matmul_e8cb_omajor simd.rs:6867-6900). */
+static int32_t omajor_level(int tier, const uint8_t *bq, const int8_t *cb, size_t j, size_t kk,
+                            size_t k)
 {
-    int8_t q[4096];
-    if (k > sizeof q) return;
+    if (tier == OR_DTYPE_I4) {
+        size_t u = j * k + kk;
+        int32_t v = (u & 1) ? (bq[u >> 1] >> 4) : (bq[u >> 1] & 0x0F);
+        return v >= 8 ? v - 16 : v;
+    }
+    if (tier == OR_DTYPE_E8CB) return cb[(size_t)bq[j * (k / 8) + kk / 8] * 8 + kk % 8];
+    return (int8_t)bq[j * k + kk];
+}
+
+int or_matmul_q_omajor(int tier, const float *a, const uint8_t *bq, const int8_t *codebook,
+                       const float *scales, float *out, size_t m, size_t k, size_t n)
+{
+    if (tier != OR_DTYPE_I8 && tier != OR_DTYPE_I4 && tier != OR_DTYPE_E8CB) return 3;
+    if ((tier == OR_DTYPE_I4 && k % 2) || (tier == OR_DTYPE_E8CB && k % 8)) return 3;
+    if (k > OR_I8_DOT_K_MAX) return 3;
+    int8_t *q = (int8_t *)malloc(k ? k : 1);
     for (size_t i = 0; i < m; ++i) {
         memset(q, 0, k);
         float sa = or_quantize_row_i8(a + i * k, q, k);
@@ -290,12 +324,20 @@ void or_matmul_i8_pc_omajor(const float *a, const int8_t *bq, const float *scale
             continue;
         }
         for (size_t j = 0; j < n; ++j) {
-            const int8_t *row = bq + j * k;
             int32_t acc = 0;
-            for (size_t kk = 0; kk < k; ++kk) acc += (int32_t)q[kk] * (int32_t)row[kk];
+            for (size_t kk = 0; kk < k; ++kk)
+                acc += (int32_t)q[kk] * omajor_level(tier, bq, codebook, j, kk, k);
             out[i * n + j] = (float)acc * (sa * scales[j]);
         }
     }
+    free(q);
+    return 0;
+}
+
+void or_matmul_i8_pc_omajor(const float *a, const int8_t *bq, const float *scales,
+                            float *out, size_t m, size_t k, size_t n)
+{
+    or_matmul_q_omajor(OR_DTYPE_I8, a, (const uint8_t *)bq, NULL, scales, out, m, k, n);
 }
 
 /* FNV-1a over the LE bytes of each f32 (simd.rs:8237-8246). */

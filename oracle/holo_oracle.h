@@ -69,6 +69,16 @@ void or_unary_lut(const uint16_t *table, const uint16_t *in, uint16_t *out, size
 /* ---- int8 scheme: src/cpu/simd.rs:4755-4785 ---- */
 float or_quantize_row_i8(const float *a, int8_t *q, size_t k);
 /* W8A8 output-major GEMV, simd.rs:5295-5480 (golden carrier, simd.rs:8236-8259) */
+/* Output-major W8A8 GEMV for the i8 (2), i4 (10) and e8cb (11) tiers
+ * (simd.rs:5295-5480, :6172-6230, :6867-6950): per-token symmetric activation
+ * quantization, exact i32 dot, out = (acc as f32) * (scale_a * scales[j]).
+ * codebook: 256 x 8 i8 (e8cb only). Returns 3 for an unknown tier, a k the
+ * tier cannot split, or k above the exact-i32 bound. */
+#define OR_DTYPE_I4 10
+#define OR_DTYPE_E8CB 11
+#define OR_I8_DOT_K_MAX 133144   /* i32::MAX / (127 * 127), kernel_call.rs:103 */
+int or_matmul_q_omajor(int tier, const float *a, const uint8_t *bq, const int8_t *codebook,
+                       const float *scales, float *out, size_t m, size_t k, size_t n);
 void or_matmul_i8_pc_omajor(const float *a, const int8_t *bq, const float *scales,
                             float *out, size_t m, size_t k, size_t n);
 uint64_t or_fnv1a_f32(const float *v, size_t n);

@@ -108,11 +108,15 @@ def test_three_op_chain_is_f32_only():
         assert n_calls(a) == want, dt
 
 
-def test_unserved_activation_is_left_unfused():
-    # f32 Exp has no device form (libm expf), so the pair stays two calls
-    a = archive([mm(0, 1, 2, DTYPE_F32), unary(KernelCall.Exp, 2, 3, DTYPE_BF16)],
-                ins(DTYPE_F32), [(3, M * N, DTYPE_BF16)])
-    assert n_calls(a) == 2
+@pytest.mark.parametrize("dt", [DTYPE_F32, DTYPE_BF16])
+def test_every_activation_is_fused(dt):
+    """Every fused_activation the reference loader absorbs (kernel_call.rs:
+    861-870) has a device form, so matmul -> activation is always one call:
+    the table of narrow(f(widen(x))) for 16-bit products, f computed in f32
+    otherwise (f32 Exp through libm's expf restated, Relu/Elu/Selu too)."""
+    for ctor in (KernelCall.Exp, KernelCall.Gelu, KernelCall.Silu):
+        a = archive([mm(0, 1, 2, dt), unary(ctor, 2, 3, dt)], ins(dt), [(3, M * N, dt)])
+        assert n_calls(a) == 1, (ctor, dt)
 
 
 def decoder(layers=2):
@@ -211,16 +215,14 @@ def test_fused_codec_round_trip(call):
 def test_fused_refusals():
     sizes = [1 << 16] * 8
     base = MatMulCall(BufferRef(1), BufferRef(2), BufferRef(3), 8, 64, 64, DTYPE_BF16)
-    with pytest.raises(UnsupportedOp):       # Relu: no device form
-        validate(KernelCall.MatMulActivation(MatMulActivationCall(base, fused_activation.RELU)),
-                 sizes)
     f32 = MatMulCall(BufferRef(1), BufferRef(2), BufferRef(3), 8, 64, 64, DTYPE_F32)
-    with pytest.raises(UnsupportedOp):       # f32 Exp is libm expf: not served
-        validate(KernelCall.MatMulActivation(MatMulActivationCall(f32, fused_activation.EXP)),
+    for act in range(1, 9):                  # every fused_activation has a device form
+        validate(KernelCall.MatMulActivation(MatMulActivationCall(base, act)), sizes)
+        validate(KernelCall.MatMulActivation(MatMulActivationCall(f32, act)), sizes)
+        validate(KernelCall.MatMulAddActivation(MatMulAddActivationCall(base, BufferRef(4), act)),
                  sizes)
-    with pytest.raises(UnsupportedOp):       # bf16 activation of an f32 sum: computed forms only
-        validate(KernelCall.MatMulAddActivation(MatMulAddActivationCall(
-            base, BufferRef(4), fused_activation.EXP)), sizes)
+    with pytest.raises(UnsupportedOp):       # no such activation id
+        validate(KernelCall.MatMulActivation(MatMulActivationCall(f32, 9)), sizes)
     with pytest.raises(SlotOutOfRange):      # residual overlaps the output (split_borrow)
         validate(KernelCall.MatMulAdd(MatMulAddCall(base, BufferRef(3))), sizes)
     with pytest.raises(SlotOutOfRange):      # short residual

@@ -41,6 +41,27 @@ def test_int8_quantizer_reproduces_reference_golden():
     assert oracle.fnv1a_f32(out) == 0x787CCDC172029F9B
 
 
+def test_packed_i4_and_e8cb_gemvs_reproduce_reference_goldens():
+    """The same test's other two tiers (simd.rs:8261-8283): packed i4 (W4A8)
+    FNV 0x4c5123c024af97ae and e8cb (W1A8, an 8-D codebook block per index)
+    FNV 0x88ac55a91dd5aa0d, over the same activations and scales; and the i8
+    golden through the generic entry."""
+    a, bq, scales, m, k, n = golden_inputs()
+    o8 = oracle.matmul_q_omajor(2, a, bq, scales, m, k, n)
+    assert oracle.fnv1a_f32(o8) == 0x787CCDC172029F9B
+    bq4 = np.array([(i * 53 + 9) % 251 for i in range(k * n // 2)], np.uint8)
+    o4 = oracle.matmul_q_omajor(10, a, bq4, scales, m, k, n)
+    assert oracle.fnv1a_f32(o4) == 0x4C5123C024AF97AE
+    cb = np.array([(i * 37 + 11) % 255 - 127 for i in range(256 * 8)], np.int8)
+    bq8 = np.array([(i * 17 + 3) % 256 for i in range(n * (k // 8))], np.uint8)
+    oe = oracle.matmul_q_omajor(11, a, bq8, scales, m, k, n, codebook=cb)
+    assert oracle.fnv1a_f32(oe) == 0x88AC55A91DD5AA0D
+    # a nibble-order mistake (high nibble first) breaks the i4 golden
+    swapped = ((bq4 & 0x0F) << 4) | (bq4 >> 4)
+    assert oracle.fnv1a_f32(oracle.matmul_q_omajor(10, a, swapped, scales, m, k, n)) != \
+        0x4C5123C024AF97AE
+
+
 def _golden_with(quantize):
     """The golden's arithmetic with a substitute quantizer (numpy, CPU only)."""
     a, bq, scales, m, k, n = golden_inputs()
@@ -465,3 +486,26 @@ def test_panel_packing_follows_the_layout_formula(k, n):
                 want = b[kk * n + p * 16 + c] if p * 16 + c < n else 0.0
                 assert pk[(p * k + kk) * 16 + c] == want
     assert np.array_equal(oracle.unpack_b_panels(pk, k, n), b)
+
+
+def test_relu_elu_selu_exp_closed_forms():
+    """relu_f / elu_f / selu_f / exp_f (float_kernels.rs:3448, 3641-3656,
+    3498-3500) in the oracle against f64 closed forms on a dense sweep, and
+    their special values: relu(NaN) = relu(-0) = +0, elu(-inf) = -1,
+    selu(+inf) = +inf, elu and selu continuous at 0."""
+    x = np.concatenate([np.linspace(-30, 30, 20001), [-0.0, 0.0, 1e-30, -1e-30]]).astype(np.float32)
+    f = lambda act: oracle.fused_act_f32(act, x).astype(np.float64)
+    x64 = x.astype(np.float64)
+    assert np.array_equal(f(1), np.maximum(x64, 0.0))
+    elu = np.where(x64 >= 0, x64, np.expm1(x64))
+    assert np.max(np.abs(f(6) - elu)) <= 2e-7
+    a, s = float(np.float32(1.6732632)), float(np.float32(1.050701))
+    selu = np.where(x64 >= 0, s * x64, s * a * np.expm1(x64))
+    assert np.max(np.abs(f(7) - selu)) <= 5e-7 * np.maximum(1, np.abs(selu)).max()
+    e = f(8)
+    assert np.max(np.abs(e - np.exp(x64)) / np.exp(x64)) <= 2 ** -23
+    sp = np.array([np.nan, -0.0, -np.inf, np.inf], np.float32)
+    r = oracle.fused_act_f32(1, sp)
+    assert r[0] == 0 and r[1] == 0 and not np.signbit(r[0]) and not np.signbit(r[1])
+    assert oracle.fused_act_f32(6, sp)[2] == -1.0
+    assert oracle.fused_act_f32(7, sp)[3] == np.inf

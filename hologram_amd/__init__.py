@@ -11,24 +11,27 @@ libholo_hip.so (C ABI: include/holo_hip.h); this package is its host mirror.
 from .backend import (BackendError, DeviceWorkspace, DispatchError, HipBackend, InitError,
                       ShapeMismatch, SlotOutOfRange, UnsupportedOp, decode_call, lut_table,
                       validate)
-from .kernel_call import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, DTYPE_I8, DTYPE_I32, DTYPE_I64,
-                          NO_BUFFER, SLOT_ABSENT, ArgMaxCall, AttentionI8RowsCall, BinaryCall,
-                          BufferRef,
-                          DecodeAttentionI8Call, DecodeAttentionValidCall, GatherCall, KernelCall, KvCacheWriteCall,
-                          KvQuantAppendCall, MatMulActivationCall, MatMulAddActivationCall,
-                          MatMulAddCall, MatMulCall, NormCall, RoPECall, TransposeCall, UnaryCall,
-                          encode_calls, fused_activation, lut_act)
+from .kernel_call import (DTYPE_BF16, DTYPE_E8CB, DTYPE_F16, DTYPE_F32, DTYPE_I4, DTYPE_I8,
+                          DTYPE_I32, DTYPE_I64, DTYPE_U8, NO_BUFFER, SLOT_ABSENT, ArgMaxCall,
+                          AttentionI8RowsCall, BinaryCall, BufferRef, DecodeAttentionI8Call,
+                          DecodeAttentionValidCall, DequantActivationCall, DequantizeCall,
+                          GatherCall, KernelCall, KvCacheWriteCall, KvQuantAppendCall,
+                          MatMulActivationCall, MatMulAddActivationCall, MatMulAddCall,
+                          MatMulCall, MatMulDequantCall, NormCall, RoPECall, TransposeCall,
+                          UnaryCall, encode_calls, fused_activation, lut_act, mm_act_quant,
+                          weight_layout)
 from .archive import ConstantEntry, HoloWriter, PortDescriptor, blake3
 from .session import HipSession
 
 __all__ = [
     "BackendError", "DeviceWorkspace", "DispatchError", "HipBackend", "InitError",
     "ShapeMismatch", "SlotOutOfRange", "UnsupportedOp", "decode_call", "lut_table", "validate",
-    "DTYPE_BF16", "DTYPE_F16", "DTYPE_F32", "DTYPE_I8", "DTYPE_I32", "DTYPE_I64",
-    "NO_BUFFER", "SLOT_ABSENT", "ArgMaxCall", "AttentionI8RowsCall", "BinaryCall", "BufferRef",
-    "DecodeAttentionI8Call", "DecodeAttentionValidCall", "GatherCall", "KernelCall", "KvCacheWriteCall",
+    "DTYPE_BF16", "DTYPE_E8CB", "DTYPE_F16", "DTYPE_F32", "DTYPE_I4", "DTYPE_I8", "DTYPE_I32",
+    "DTYPE_I64", "DTYPE_U8", "NO_BUFFER", "SLOT_ABSENT", "ArgMaxCall", "AttentionI8RowsCall",
+    "BinaryCall", "BufferRef", "DecodeAttentionI8Call", "DecodeAttentionValidCall",
+    "DequantActivationCall", "DequantizeCall", "GatherCall", "KernelCall", "KvCacheWriteCall",
     "KvQuantAppendCall", "MatMulActivationCall", "MatMulAddActivationCall", "MatMulAddCall",
-    "MatMulCall", "NormCall", "RoPECall", "TransposeCall", "UnaryCall", "encode_calls",
-    "fused_activation",
-    "lut_act", "ConstantEntry", "HoloWriter", "PortDescriptor", "blake3", "HipSession",
+    "MatMulCall", "MatMulDequantCall", "NormCall", "RoPECall", "TransposeCall", "UnaryCall",
+    "encode_calls", "fused_activation", "lut_act", "mm_act_quant", "weight_layout",
+    "ConstantEntry", "HoloWriter", "PortDescriptor", "blake3", "HipSession",
 ]

@@ -122,6 +122,33 @@ class TransposeCallC(ctypes.Structure):
                 ("dtype", ctypes.c_uint8)]
 
 
+class DequantizeCallC(ctypes.Structure):
+    _fields_ = [("input", BufferRefC), ("scales", BufferRefC), ("zero_points", BufferRefC),
+                ("output", BufferRefC), ("element_count", ctypes.c_uint64),
+                ("channels", ctypes.c_uint32), ("inner", ctypes.c_uint32),
+                ("quant_dtype", ctypes.c_uint8), ("dtype", ctypes.c_uint8),
+                ("scale_bits", ctypes.c_uint32), ("zero_point", ctypes.c_int32),
+                ("codebook", BufferRefC), ("weight_layout", ctypes.c_uint8),
+                ("act_quant", ctypes.c_uint8)]
+
+
+class MatMulDequantCallC(ctypes.Structure):
+    _fields_ = [("a", BufferRefC), ("bq", BufferRefC), ("scales", BufferRefC),
+                ("zero_points", BufferRefC), ("output", BufferRefC),
+                ("m", ctypes.c_uint32), ("k", ctypes.c_uint32), ("n", ctypes.c_uint32),
+                ("channels", ctypes.c_uint32), ("inner", ctypes.c_uint32),
+                ("quant_dtype", ctypes.c_uint8), ("dtype", ctypes.c_uint8),
+                ("scale_bits", ctypes.c_uint32), ("zero_point", ctypes.c_int32),
+                ("bq_omajor", ctypes.c_uint8), ("act_quant", ctypes.c_uint8),
+                ("act", ctypes.c_uint8), ("residual", BufferRefC), ("codebook", BufferRefC)]
+
+
+class DequantActivationCallC(ctypes.Structure):
+    _fields_ = [("input", BufferRefC), ("output", BufferRefC), ("element_count", ctypes.c_uint64),
+                ("quant_dtype", ctypes.c_uint8), ("act", ctypes.c_uint8), ("dtype", ctypes.c_uint8),
+                ("scale_bits", ctypes.c_uint32), ("zero_point", ctypes.c_int32)]
+
+
 class CallUnion(ctypes.Union):
     _fields_ = [("unary", UnaryCallC), ("binary", BinaryCallC), ("norm", NormCallC),
                 ("rope", RopeCallC), ("gather", GatherCallC), ("argmax", ArgMaxCallC),
@@ -129,7 +156,8 @@ class CallUnion(ctypes.Union):
                 ("matmul_add", MatMulAddCallC), ("matmul_add_act", MatMulAddActCallC),
                 ("kv_write", KvCacheWriteCallC),
                 ("kv_quant_append", KvQuantAppendCallC), ("attn_valid", DecodeAttentionValidCallC),
-                ("attn_i8", DecodeAttentionI8CallC),
+                ("dequantize", DequantizeCallC), ("matmul_dequant", MatMulDequantCallC),
+                ("dequant_act", DequantActivationCallC), ("attn_i8", DecodeAttentionI8CallC),
                 ("attn_i8_rows", AttentionI8RowsCallC), ("transpose", TransposeCallC)]
 
 
@@ -162,6 +190,7 @@ SIGNATURES = {
                                                 ctypes.c_uint32, ctypes.POINTER(_P)]),
     "holo_hip_session_nodes": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_uint32),
                                               ctypes.POINTER(ctypes.c_uint32)]),
+    "holo_hip_session_call": (ctypes.c_int, [_P, ctypes.c_uint32, ctypes.POINTER(KernelCallC)]),
     "holo_hip_session_close": (ctypes.c_int, [_P]),
     "holo_hip_session_info": (ctypes.c_int, [_P] + [ctypes.POINTER(ctypes.c_uint32)] * 4),
     "holo_hip_session_port": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_uint32,

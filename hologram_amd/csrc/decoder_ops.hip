@@ -385,6 +385,25 @@ hipError_t launch_lens_within(const uint32_t *lens, uint32_t n, uint32_t bucket,
     return hipGetLastError();
 }
 
+// Unary activations over f32: the reference computes these per element
+// (unary_act, src/cpu/kernels.rs:1586-1598), with the same scalar functions.
+__global__ __launch_bounds__(256) void act_f32_kernel(const float *__restrict__ in,
+                                                      float *__restrict__ out, uint64_t n,
+                                                      uint32_t act) {
+    const uint64_t stride = uint64_t(gridDim.x) * 256;
+    for (uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride)
+        out[i] = act_f32(act, in[i]);
+}
+
+hipError_t launch_act_f32(const float *in, float *out, uint64_t n, uint32_t act,
+                          hipStream_t stream) {
+    if (n == 0) return hipSuccess;
+    const uint64_t b = (n + 255) / 256;
+    hipLaunchKernelGGL(act_f32_kernel, dim3(unsigned(b < 8192 ? b : 8192)), dim3(256), 0, stream,
+                       in, out, n, act);
+    return hipGetLastError();
+}
+
 hipError_t launch_gather(const void *data, const void *idx, void *out, uint64_t outer,
                          uint64_t axis_dim, uint64_t num_idx, uint64_t row_bytes, bool i64,
                          int *err, hipStream_t stream) {

@@ -19,6 +19,7 @@
 
 namespace holo {
 bool build_lut_table(int act, bool f16, uint16_t *t);
+bool lut_act_value(int act, float x, float *y);
 }
 
 namespace {
@@ -155,14 +156,18 @@ int launched(hipError_t e, const char *op) {
     return HOLO_OK;
 }
 
-int lut_act_of(uint32_t tag) {
+// The fused_activation id (kernel_call.rs:861-870) of a unary activation tag.
+uint32_t fused_of_unary(uint32_t tag) {
     switch (tag) {
-        case HOLO_OP_SIGMOID: return HOLO_ACT_SIGMOID;
-        case HOLO_OP_TANH: return HOLO_ACT_TANH;
-        case HOLO_OP_GELU: return HOLO_ACT_GELU;
-        case HOLO_OP_SILU: return HOLO_ACT_SILU;
-        case HOLO_OP_EXP: return HOLO_ACT_EXP;
-        default: return -1;
+        case HOLO_OP_RELU: return 1;
+        case HOLO_OP_GELU: return 2;
+        case HOLO_OP_SILU: return 3;
+        case HOLO_OP_SIGMOID: return 4;
+        case HOLO_OP_TANH: return 5;
+        case HOLO_OP_ELU: return 6;
+        case HOLO_OP_SELU: return 7;
+        case HOLO_OP_EXP: return 8;
+        default: return 0;
     }
 }
 
@@ -199,22 +204,29 @@ int lut_table(holo_backend *be, int act, bool f16, const uint16_t **out, const c
 
 // ---------------------------------------------------------------- LUT ----
 // unary_act -> unary_lut (src/cpu/kernels.rs:1586-1598, src/cpu/lut.rs:76-98).
+// 16-bit: the table of narrow(f(widen(x))); f32: f per element.
 int do_unary(holo_backend *be, const SlotTable &st, uint32_t tag, const holo_unary_call &c) {
     const char *op = "unary_lut";
-    const int act = lut_act_of(tag);
-    if (c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F16)
+    const uint32_t fa = fused_of_unary(tag);
+    const int act = holo::lut_act_of_fused(fa);
+    if (c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F16 && c.dtype != HOLO_DTYPE_F32)
         return fail(HOLO_ERR_UNSUPPORTED_OP,
-                    "unary_lut: the device path serves bf16/f16 (the 65536-entry table); "
-                    "route other dtypes to the CPU backend");
+                    "unary: the device path serves bf16/f16 (tables) and f32 (computed)");
     if (c.element_count == 0) return HOLO_OK;
     View in, out;
     HOLO_TRY(split_borrow(st, &c.input, &in, 1, c.output, &out, op));
-    const uint64_t bytes = c.element_count * 2;
+    const uint64_t es = c.dtype == HOLO_DTYPE_F32 ? 4 : 2;
+    const uint64_t bytes = c.element_count * es;
     HOLO_TRY(need(in, bytes, c.input.slot, op, "input"));
     HOLO_TRY(need(out, bytes, c.output.slot, op, "output"));
-    if (!aligned(in, 2) || !aligned(out, 2))
-        return fail(HOLO_ERR_UNSUPPORTED_OP, "unary_lut: operands must be 2-byte aligned");
+    if (!aligned(in, es) || !aligned(out, es))
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "unary: operands must be element-aligned");
     if (!be) return HOLO_OK;
+    if (c.dtype == HOLO_DTYPE_F32)
+        return launched(holo::launch_act_f32(reinterpret_cast<const float *>(in.base),
+                                             reinterpret_cast<float *>(out.base), c.element_count,
+                                             fa, be->stream),
+                        op);
     const uint16_t *tab = nullptr;
     HOLO_TRY(lut_table(be, act, c.dtype == HOLO_DTYPE_F16, &tab, op));
     return launched(holo::launch_lut_u16(tab, reinterpret_cast<const uint16_t *>(in.base),
@@ -839,6 +851,227 @@ int do_attn_valid(holo_backend *be, const SlotTable &st, const holo_decode_atten
     return launched(holo::launch_attn_valid(a, be->scratch, be->stream), op);
 }
 
+// ------------------------------------------------ quantized weights ----
+// The level width of a quantized tier (quant_tier.rs:137-178): stored bytes
+// of `count` elements, or 0 for a tier this op cannot read.
+uint64_t quant_bytes(uint8_t q, uint64_t count) {
+    switch (q) {
+        case HOLO_DTYPE_I8:
+        case HOLO_DTYPE_U8: return count;
+        case HOLO_DTYPE_I4: return (count + 1) / 2;
+        case HOLO_DTYPE_E8CB: return (count + 7) / 8;
+        default: return 0;
+    }
+}
+
+float f32_of_bits(uint32_t b) {
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+
+// dequantize (src/cpu/kernels.rs:185-296).
+int do_dequantize(holo_backend *be, const SlotTable &st, const holo_dequantize_call &c) {
+    const char *op = "dequantize";
+    const uint64_t n = c.element_count;
+    if (c.quant_dtype != HOLO_DTYPE_I8 && c.quant_dtype != HOLO_DTYPE_U8 && c.quant_dtype != HOLO_DTYPE_I4)
+        return fail(HOLO_ERR_SLOT_OUT_OF_RANGE,
+                    "dequantize: quant_dtype must be i8, u8 or i4 (slot " + std::to_string(c.input.slot) + ")");
+    const bool per_ch = c.channels > 0 && c.scales.slot != HOLO_SLOT_ABSENT;
+    holo_buffer_ref reads[3] = {c.input, c.scales, c.zero_points};
+    View rv[3], out;
+    HOLO_TRY(split_borrow(st, reads, rv, per_ch ? 3 : 1, c.output, &out, op));
+    HOLO_TRY(need(rv[0], quant_bytes(c.quant_dtype, n), c.input.slot, op, "input"));
+    uint64_t es = 0;
+    if (c.dtype == HOLO_DTYPE_F32) es = 4;
+    else if (c.dtype == HOLO_DTYPE_BF16 || c.dtype == HOLO_DTYPE_F16) es = 2;
+    else if (c.dtype == 9)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "dequantize: f64 output is not served on the device");
+    else
+        return fail(HOLO_ERR_SLOT_OUT_OF_RANGE,
+                    "dequantize: unknown output dtype (slot " + std::to_string(c.output.slot) + ")");
+    HOLO_TRY(need(out, n * es, c.output.slot, op, "output"));
+    if (per_ch) {
+        HOLO_TRY(need(rv[1], uint64_t(c.channels) * 4, c.scales.slot, op, "scales"));
+        HOLO_TRY(need(rv[2], uint64_t(c.channels) * 4, c.zero_points.slot, op, "zero points"));
+        if (!aligned(rv[1], 4) || !aligned(rv[2], 4))
+            return fail(HOLO_ERR_UNSUPPORTED_OP, "dequantize: scales / zero points must be 4-byte aligned");
+    }
+    if (!aligned(out, es)) return fail(HOLO_ERR_UNSUPPORTED_OP, "dequantize: output must be element-aligned");
+    if (!be || n == 0) return HOLO_OK;
+    holo::DequantArgs d;
+    d.in = rv[0].base;
+    d.scales = per_ch ? reinterpret_cast<const float *>(rv[1].base) : nullptr;
+    d.zps = per_ch ? reinterpret_cast<const int32_t *>(rv[2].base) : nullptr;
+    d.out = out.base;
+    d.n = n;
+    d.channels = c.channels;
+    d.inner = c.inner ? c.inner : 1;
+    d.quant = c.quant_dtype;
+    d.dtype = c.dtype;
+    d.scale = f32_of_bits(c.scale_bits);
+    d.zp = c.zero_point;
+    return launched(holo::launch_dequantize(d, be->stream), op);
+}
+
+// dequant_activation (src/cpu/kernels.rs:311-388): the table of f((q - zp) as
+// f32 * scale) over the quantized domain, built here on the host with the
+// reference's scalar f, then one lookup per element; the output is f32.
+int do_dequant_act(holo_backend *be, const SlotTable &st, const holo_dequant_activation_call &c) {
+    const char *op = "dequant_activation";
+    const uint64_t n = c.element_count;
+    if (c.quant_dtype != HOLO_DTYPE_I8 && c.quant_dtype != HOLO_DTYPE_U8 && c.quant_dtype != HOLO_DTYPE_I4)
+        return fail(HOLO_ERR_SLOT_OUT_OF_RANGE,
+                    "dequant_activation: quant_dtype must be i8, u8 or i4 (slot " +
+                        std::to_string(c.input.slot) + ")");
+    View in, out;
+    HOLO_TRY(split_borrow(st, &c.input, &in, 1, c.output, &out, op));
+    HOLO_TRY(need(in, quant_bytes(c.quant_dtype, n), c.input.slot, op, "input"));
+    HOLO_TRY(need(out, n * 4, c.output.slot, op, "output"));
+    if (!aligned(out, 4)) return fail(HOLO_ERR_UNSUPPORTED_OP, "dequant_activation: output must be 4-byte aligned");
+    float probe;
+    if (!holo::lut_act_value(c.act, 0.0f, &probe))
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    "dequant_activation: activation " + std::to_string(c.act) +
+                        " (Erf: libm erff) has no device table");
+    if (!be || n == 0) return HOLO_OK;
+    const float scale = f32_of_bits(c.scale_bits);
+    float table[256] = {};
+    const bool i4 = c.quant_dtype == HOLO_DTYPE_I4;
+    for (int raw = 0; raw < (i4 ? 16 : 256); ++raw) {
+        int32_t q = raw;
+        if (c.quant_dtype == HOLO_DTYPE_I8) q = int32_t(int8_t(uint8_t(raw)));
+        if (i4) q = raw >= 8 ? raw - 16 : raw;
+        const int32_t qz = int32_t(uint32_t(q) - uint32_t(c.zero_point));
+        holo::lut_act_value(c.act, float(qz) * scale, &table[raw]);
+    }
+    return launched(holo::launch_dequant_act(in.base, reinterpret_cast<float *>(out.base), n, i4,
+                                             table, be->stream),
+                    op);
+}
+
+// matmul_dequant_float + matmul_dequant_epilogue (src/cpu/float_kernels.rs:459-760).
+int do_matmul_dequant(holo_backend *be, const SlotTable &st, const holo_matmul_dequant_call &c) {
+    const char *op = "matmul_dequant";
+    if (c.m == 0 || c.k == 0 || c.n == 0) return HOLO_OK;
+    if (c.dtype != HOLO_DTYPE_F32)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "matmul_dequant: only f32 output is supported");
+    const uint64_t kn = uint64_t(c.k) * c.n;
+    const uint64_t in_bytes = quant_bytes(c.quant_dtype, kn);
+    if (!in_bytes) return fail(HOLO_ERR_UNSUPPORTED_OP, "matmul_dequant: unknown quantized weight tier");
+    const bool needs_cb = c.quant_dtype == HOLO_DTYPE_E8CB;
+    const bool has_cb = c.codebook.slot != HOLO_SLOT_ABSENT;
+    if (needs_cb != has_cb)
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    "matmul_dequant: codebook operand missing for a VQ tier (or present without one)");
+    const bool per_ch = c.channels > 0 && c.scales.slot != HOLO_SLOT_ABSENT;
+    const bool has_res = c.residual.slot != HOLO_SLOT_ABSENT;
+    // operands in buffers() order: a, bq[, scales, zero points][, codebook]; the
+    // epilogue's residual is its own borrow (float_kernels.rs:727-760)
+    holo_buffer_ref reads[5];
+    int nr = 0;
+    reads[nr++] = c.a;
+    reads[nr++] = c.bq;
+    if (per_ch) {
+        reads[nr++] = c.scales;
+        reads[nr++] = c.zero_points;
+    }
+    const int cb_idx = nr;
+    if (has_cb) reads[nr++] = c.codebook;
+    View rv[5], out;
+    HOLO_TRY(split_borrow(st, reads, rv, nr, c.output, &out, op));
+    HOLO_TRY(need(rv[0], uint64_t(c.m) * c.k * 4, c.a.slot, op, "a"));
+    HOLO_TRY(need(rv[1], in_bytes, c.bq.slot, op, "bq"));
+    HOLO_TRY(need(out, uint64_t(c.m) * c.n * 4, c.output.slot, op, "output"));
+    View res;
+    if (has_res) {
+        HOLO_TRY(split_borrow(st, &c.residual, &res, 1, c.output, &out, op));
+        HOLO_TRY(need(res, uint64_t(c.m) * c.n * 4, c.residual.slot, op, "residual"));
+    }
+    // an id past the table is the identity (float_kernels.rs:767-781)
+    const uint32_t act = c.act <= holo::kFusedExp ? c.act : 0;
+    if (!aligned(rv[0], 4) || !aligned(out, 4) || (has_res && !aligned(res, 4)))
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "matmul_dequant: f32 operands must be 4-byte aligned");
+    const bool omajor = c.bq_omajor != 0, w8a8 = c.act_quant == 1;
+    if (omajor || w8a8) {
+        if (!(omajor && w8a8))
+            return fail(HOLO_ERR_UNSUPPORTED_OP, "matmul_dequant: bq_omajor and W8A8 must be paired");
+        // symmetric per-channel i8 / i4 / e8cb within the exact-i32 k bound;
+        // the zero points' values are checked on the device
+        const bool tier_ok = c.quant_dtype == HOLO_DTYPE_I8 ||
+                             (c.quant_dtype == HOLO_DTYPE_I4 && c.k % 2 == 0) ||
+                             (c.quant_dtype == HOLO_DTYPE_E8CB && c.k % 8 == 0);
+        if (!(per_ch && tier_ok && c.channels == c.n && c.inner == 1) || c.k > holo::kI8DotKMax)
+            return fail(HOLO_ERR_UNSUPPORTED_OP,
+                        "matmul_dequant: W8A8 requires symmetric per-channel i8/i4/e8cb within the k bound");
+        // every whole i32 of the zero-point view must be zero (the symmetry
+        // test reads the view, not n entries of it)
+        HOLO_TRY(need(rv[2], uint64_t(c.n) * 4, c.scales.slot, op, "scales"));
+        if (has_cb) HOLO_TRY(need(rv[cb_idx], 256 * 8, c.codebook.slot, op, "codebook"));
+        if (!aligned(rv[2], 4))
+            return fail(HOLO_ERR_UNSUPPORTED_OP, "matmul_dequant: scales must be 4-byte aligned");
+        if ((uint64_t(c.n) + 15) / 16 > 0x7fffffffull || (uint64_t(c.m) + 63) / 64 > 65535)
+            return fail(HOLO_ERR_UNSUPPORTED_OP, "matmul_dequant: grid beyond the launch limits");
+        if (!be) return HOLO_OK;
+        HOLO_TRY(launched(holo::launch_zero_points_check(rv[3].base, rv[3].bytes / 4, be->dev_err,
+                                                         be->stream),
+                          op));
+        HOLO_TRY(ensure_scratch(be, holo::q_omajor_scratch_bytes(c.m, c.k), op));
+        holo::QOmajorArgs a;
+        a.a = reinterpret_cast<const float *>(rv[0].base);
+        a.bq = rv[1].base;
+        a.codebook = has_cb ? reinterpret_cast<const int8_t *>(rv[cb_idx].base) : nullptr;
+        a.scales = reinterpret_cast<const float *>(rv[2].base);
+        a.residual = has_res ? reinterpret_cast<const float *>(res.base) : nullptr;
+        a.out = reinterpret_cast<float *>(out.base);
+        a.m = c.m;
+        a.k = c.k;
+        a.n = c.n;
+        a.tier = c.quant_dtype;
+        a.act = act;
+        return launched(holo::launch_matmul_q_omajor(a, be->scratch, be->stream), op);
+    }
+    // W8A32: the [k, n] weight dequantized to an f32 panel, the f32 product,
+    // then the epilogue in place
+    if (c.quant_dtype == HOLO_DTYPE_E8CB)
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    "matmul_dequant: quant_dtype is not scalar-decodable (e8cb needs the fused omajor path)");
+    if (per_ch) {
+        HOLO_TRY(need(rv[2], uint64_t(c.channels) * 4, c.scales.slot, op, "scales"));
+        HOLO_TRY(need(rv[3], uint64_t(c.channels) * 4, c.zero_points.slot, op, "zero points"));
+        if (!aligned(rv[2], 4) || !aligned(rv[3], 4))
+            return fail(HOLO_ERR_UNSUPPORTED_OP, "matmul_dequant: scales / zero points must be 4-byte aligned");
+    }
+    if ((uint64_t(c.m) + 127) / 128 > 65535)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "matmul_dequant: m above 8388480");
+    if (!be) return HOLO_OK;
+    const uint64_t panel = (kn * 4 + 255) / 256 * 256;
+    HOLO_TRY(ensure_scratch(be, panel + holo::matmul_scratch_bytes(c.m, c.k, c.n, HOLO_DTYPE_F32), op));
+    holo::DequantArgs d;
+    d.in = rv[1].base;
+    d.scales = per_ch ? reinterpret_cast<const float *>(rv[2].base) : nullptr;
+    d.zps = per_ch ? reinterpret_cast<const int32_t *>(rv[3].base) : nullptr;
+    d.out = be->scratch;
+    d.n = kn;
+    d.channels = c.channels;
+    d.inner = c.inner ? c.inner : 1;
+    d.quant = c.quant_dtype;
+    d.dtype = HOLO_DTYPE_F32;
+    d.scale = f32_of_bits(c.scale_bits);
+    d.zp = c.zero_point;
+    HOLO_TRY(launched(holo::launch_dequantize(d, be->stream), op));
+    HOLO_TRY(launched(holo::launch_matmul(rv[0].base, be->scratch, out.base, c.m, c.k, c.n,
+                                          HOLO_DTYPE_F32, static_cast<uint8_t *>(be->scratch) + panel,
+                                          be->stream),
+                      op));
+    if (act == 0 && !has_res) return HOLO_OK;
+    holo::TileEpi te;
+    te.kind = has_res ? (act ? holo::kEpiAddAct : holo::kEpiAdd) : holo::kEpiAct;
+    te.act = act;
+    te.residual = has_res ? res.base : nullptr;
+    return launched(holo::launch_tile_epilogue(out.base, uint64_t(c.m) * c.n, false, te, be->stream), op);
+}
+
 // ------------------------------------------------------- Add / Mul -----
 // binary_float (src/cpu/float_kernels.rs:238-300).
 int do_binary(holo_backend *be, const SlotTable &st, uint32_t tag, const holo_binary_call &c) {
@@ -1017,7 +1250,13 @@ int dispatch_impl(holo_backend *be, const SlotTable &st, const holo_kernel_call 
         case HOLO_OP_TANH:
         case HOLO_OP_GELU:
         case HOLO_OP_SILU:
-        case HOLO_OP_EXP: return do_unary(be, st, call->tag, call->u.unary);
+        case HOLO_OP_EXP:
+        case HOLO_OP_RELU:
+        case HOLO_OP_ELU:
+        case HOLO_OP_SELU: return do_unary(be, st, call->tag, call->u.unary);
+        case HOLO_OP_DEQUANTIZE: return do_dequantize(be, st, call->u.dequantize);
+        case HOLO_OP_DEQUANT_ACT: return do_dequant_act(be, st, call->u.dequant_act);
+        case HOLO_OP_MATMUL_DEQUANT: return do_matmul_dequant(be, st, call->u.matmul_dequant);
         case HOLO_OP_ADD:
         case HOLO_OP_MUL: return do_binary(be, st, call->tag, call->u.binary);
         case HOLO_OP_RMS_NORM: return do_rmsnorm(be, st, call->u.norm);
@@ -1085,13 +1324,81 @@ int decode_impl(const uint8_t *wire, size_t len, holo_kernel_call *out, size_t *
         case HOLO_OP_TANH:
         case HOLO_OP_GELU:
         case HOLO_OP_SILU:
-        case HOLO_OP_EXP: {  // put_unary :575-581
+        case HOLO_OP_EXP:
+        case HOLO_OP_RELU:
+        case HOLO_OP_ELU:
+        case HOLO_OP_SELU: {  // put_unary :575-581
             auto &c = out->u.unary;
             c.input = r.buf();
             c.output = r.buf();
             c.element_count = r.get<uint64_t>();
             c.witt_bits = r.get<uint16_t>();
             c.dtype = r.get<uint8_t>();
+            break;
+        }
+        case HOLO_OP_DEQUANTIZE:
+        case 118: {  // put_dequantize :861-872; 118 adds layout, act quant, codebook (decoder.rs:166-176)
+            auto &c = out->u.dequantize;
+            c.input = r.buf();
+            c.scales = r.buf();
+            c.zero_points = r.buf();
+            c.output = r.buf();
+            c.element_count = r.get<uint64_t>();
+            c.channels = r.get<uint32_t>();
+            c.inner = r.get<uint32_t>();
+            c.quant_dtype = r.get<uint8_t>();
+            c.dtype = r.get<uint8_t>();
+            c.scale_bits = r.get<uint32_t>();
+            c.zero_point = int32_t(r.get<uint32_t>());
+            c.codebook.slot = HOLO_SLOT_ABSENT;
+            if (out->tag == 118) {
+                c.weight_layout = r.get<uint8_t>();
+                c.act_quant = r.get<uint8_t>();
+                c.codebook = r.buf();
+            }
+            out->tag = HOLO_OP_DEQUANTIZE;
+            break;
+        }
+        case HOLO_OP_MATMUL_DEQUANT:
+        case 116:
+        case 117: {  // put_matmul_dequant :835-850, then the 116 / 117 tails (decoder.rs:190-212)
+            auto &c = out->u.matmul_dequant;
+            c.a = r.buf();
+            c.bq = r.buf();
+            c.scales = r.buf();
+            c.zero_points = r.buf();
+            c.output = r.buf();
+            c.m = r.get<uint32_t>();
+            c.k = r.get<uint32_t>();
+            c.n = r.get<uint32_t>();
+            c.channels = r.get<uint32_t>();
+            c.inner = r.get<uint32_t>();
+            c.quant_dtype = r.get<uint8_t>();
+            c.dtype = r.get<uint8_t>();
+            c.scale_bits = r.get<uint32_t>();
+            c.zero_point = int32_t(r.get<uint32_t>());
+            c.residual.slot = HOLO_SLOT_ABSENT;
+            c.codebook.slot = HOLO_SLOT_ABSENT;
+            if (out->tag != HOLO_OP_MATMUL_DEQUANT) {
+                c.bq_omajor = r.get<uint8_t>() != 0;
+                c.act_quant = r.get<uint8_t>();
+                c.act = r.get<uint8_t>();
+                c.residual = r.buf();
+                if (out->tag == 117) c.codebook = r.buf();
+            }
+            out->tag = HOLO_OP_MATMUL_DEQUANT;
+            break;
+        }
+        case HOLO_OP_DEQUANT_ACT: {  // put_dequant_activation :851-860
+            auto &c = out->u.dequant_act;
+            c.input = r.buf();
+            c.output = r.buf();
+            c.element_count = r.get<uint64_t>();
+            c.quant_dtype = r.get<uint8_t>();
+            c.act = r.get<uint8_t>();
+            c.dtype = r.get<uint8_t>();
+            c.scale_bits = r.get<uint32_t>();
+            c.zero_point = int32_t(r.get<uint32_t>());
             break;
         }
         case HOLO_OP_ADD:
@@ -1436,7 +1743,9 @@ int holo_hip_synchronize(holo_backend *be) {
     if (!be) return fail(HOLO_ERR_INIT, "synchronize: null backend");
     hipError_t e = hipStreamSynchronize(be->stream);
     if (e != hipSuccess) return fail(HOLO_ERR_DISPATCH, std::string("synchronize: ") + hipGetErrorString(e));
-    // refusals the kernels could only see on the device (a Gather index out of range)
+    // refusals the kernels could only see on the device: bit 1 a Gather index out
+    // of range, bit 2 a multi-row attention length past the ring, bit 4 a nonzero
+    // W8A8 zero point
     int flag = 0;
     e = hipMemcpy(&flag, be->dev_err, sizeof(int), hipMemcpyDeviceToHost);
     if (e != hipSuccess) return fail(HOLO_ERR_DISPATCH, std::string("synchronize: ") + hipGetErrorString(e));
@@ -1446,6 +1755,11 @@ int holo_hip_synchronize(holo_backend *be) {
             return fail(HOLO_ERR_SLOT_OUT_OF_RANGE,
                         "gather: an index is outside [-axis_dim, axis_dim) (reported by the device; "
                         "its output row was zeroed)");
+        if (flag & 4)
+            return fail(HOLO_ERR_UNSUPPORTED_OP,
+                        "matmul_dequant: W8A8 requires symmetric per-channel i8/i4/e8cb within the k "
+                        "bound (a nonzero zero point, reported by the device; the output holds the "
+                        "symmetric product and must be discarded)");
         return fail(HOLO_ERR_UNSUPPORTED_OP,
                     "attention_i8_rows: a length exceeds bucket_rows (reported by the device): "
                     "after a ring wrap the earlier rows' keys are overwritten, so a causal "

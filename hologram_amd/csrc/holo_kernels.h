@@ -73,10 +73,52 @@ size_t attn_valid_scratch_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t M
                                 uint32_t nnew, uint32_t D);
 hipError_t launch_attn_valid(const AttnValidArgs &a, void *scratch, hipStream_t stream);
 
+// quant.hip — MatMulDequant's output-major W8A8 GEMM (f32 A quantized per
+// row on the device, exact int32 dots, (acc as f32) * (scale_a * scales[j]),
+// then + residual and the fused activation), Dequantize and
+// DequantActivation. `scratch` holds the quantized rows
+// (q_omajor_scratch_bytes).
+struct QOmajorArgs {
+    const float *a;           // [m][k] f32
+    const void *bq;           // output-major weight: i8 [n][k], i4 [n][k/2], e8cb [n][k/8]
+    const int8_t *codebook;   // e8cb: 256 x 8 i8
+    const float *scales;      // [n]
+    const float *residual;    // [m][n] f32 or null
+    float *out;               // [m][n] f32
+    uint32_t m, k, n;
+    uint8_t tier;             // 2 i8, 10 i4, 11 e8cb
+    uint32_t act;             // fused_activation id, 0 none
+};
+constexpr uint32_t kI8DotKMax = 133144;   // i32::MAX / (127 * 127), kernel_call.rs:103
+size_t q_omajor_scratch_bytes(uint32_t m, uint32_t k);
+hipError_t launch_matmul_q_omajor(const QOmajorArgs &a, void *scratch, hipStream_t stream);
+struct DequantArgs {
+    const void *in;           // i8 / u8 bytes, or i4 nibbles (low first)
+    const float *scales;      // per-channel [channels], or null (per-tensor)
+    const int32_t *zps;       // per-channel [channels]
+    void *out;                // n elements of dtype
+    uint64_t n;
+    uint32_t channels, inner;
+    uint8_t quant;            // 2 i8, 1 u8, 10 i4
+    uint8_t dtype;            // 8 f32, 7 bf16, 6 f16
+    float scale;
+    int32_t zp;
+};
+hipError_t launch_dequantize(const DequantArgs &a, hipStream_t stream);
+// Raise bit 4 of *err if any of the `count` little-endian i32 zero points at
+// zps (any alignment) is nonzero (W8A8 symmetry).
+hipError_t launch_zero_points_check(const void *zps, uint64_t count, int *err, hipStream_t stream);
+// out[i] = table[level(i)]: i8/u8 index by the raw byte, i4 by the nibble.
+hipError_t launch_dequant_act(const uint8_t *in, float *out, uint64_t n, bool i4,
+                              const float table[256], hipStream_t stream);
+
 // decoder_ops.hip — the other ops of a decode step (bf16 or f32 operands).
 // op 0 = Add, 1 = Mul.
 hipError_t launch_binary(int op, const void *a, const void *b, void *out, uint64_t n, bool bf16,
                          hipStream_t stream);
+// out[i] = f(in[i]) over f32, f = act_f32(act) (a fused_activation id).
+hipError_t launch_act_f32(const float *in, float *out, uint64_t n, uint32_t act,
+                          hipStream_t stream);
 // gamma == nullptr: no affine scale.
 hipError_t launch_rmsnorm(const void *x, const void *gamma, void *out, uint32_t batch,
                           uint32_t feature, float eps, bool bf16, hipStream_t stream);

@@ -105,6 +105,11 @@ uint64_t port_bytes(uint8_t dt) {
     }
 }
 
+// DequantizeCall::per_channel (kernel_call.rs:850-854).
+bool dequant_per_channel(const holo_dequantize_call &d) {
+    return d.channels > 0 && d.scales.slot != HOLO_SLOT_ABSENT;
+}
+
 // The BufferRefs a call reads and writes. Writes are the call's outputs
 // (two for KvQuantAppend: the int8 cache and its scales).
 void call_operands(const holo_kernel_call &c, std::vector<holo_buffer_ref> *reads,
@@ -117,8 +122,23 @@ void call_operands(const holo_kernel_call &c, std::vector<holo_buffer_ref> *read
     auto w = [&](const holo_buffer_ref &b) { writes->push_back(b); };
     switch (c.tag) {
         case HOLO_OP_SIGMOID: case HOLO_OP_TANH: case HOLO_OP_GELU: case HOLO_OP_SILU:
-        case HOLO_OP_EXP:
+        case HOLO_OP_EXP: case HOLO_OP_RELU: case HOLO_OP_ELU: case HOLO_OP_SELU:
             r(c.u.unary.input); w(c.u.unary.output); break;
+        case HOLO_OP_DEQUANTIZE: {   // buffers(), kernel_call.rs:1656-1657
+            const auto &d = c.u.dequantize;
+            r(d.input);
+            if (dequant_per_channel(d)) { r(d.scales); r(d.zero_points); }
+            w(d.output); break;
+        }
+        case HOLO_OP_DEQUANT_ACT:
+            r(c.u.dequant_act.input); w(c.u.dequant_act.output); break;
+        case HOLO_OP_MATMUL_DEQUANT: {   // buffers(), kernel_call.rs:1583-1601
+            const auto &d = c.u.matmul_dequant;
+            r(d.a); r(d.bq);
+            if (d.channels > 0 && d.scales.slot != HOLO_SLOT_ABSENT) { r(d.scales); r(d.zero_points); }
+            r(d.codebook); r(d.residual);
+            w(d.output); break;
+        }
         case HOLO_OP_ADD: case HOLO_OP_MUL:
             r(c.u.binary.a); r(c.u.binary.b); w(c.u.binary.output); break;
         case HOLO_OP_RMS_NORM:
@@ -193,116 +213,61 @@ uint32_t fused_activation(const holo_kernel_call &c) {
         case HOLO_OP_SIGMOID: return HOLO_FUSED_SIGMOID;
         case HOLO_OP_TANH: return HOLO_FUSED_TANH;
         case HOLO_OP_EXP: return HOLO_FUSED_EXP;
+        case HOLO_OP_RELU: return HOLO_FUSED_RELU;
+        case HOLO_OP_ELU: return HOLO_FUSED_ELU;
+        case HOLO_OP_SELU: return HOLO_FUSED_SELU;
         default: return 0;
     }
 }
 
-// fuse_matmul_epilogue (crates/hologram-exec/src/session.rs:2150-2373): a
-// MatMul whose output has one producer and one reader, and is no output port,
-// absorbs that reader when it is an activation (-> MatMulActivation) or a
-// residual Add whose other operand is ready no later than the MatMul's level
-// (-> MatMulAdd; for f32 a single activation reader of the sum is absorbed
-// too, -> MatMulAddActivation). Absorbed calls leave the call list and the
-// plan. One difference: a fusion whose activation this device does not serve
-// is skipped (the unfused calls give the same result).
-void fuse_matmul_epilogue(std::vector<holo_kernel_call> &calls,
-                          std::vector<std::vector<uint32_t>> &plan, const std::vector<Port> &outputs) {
-    const size_t n = calls.size();
-    std::map<uint32_t, uint32_t> prod_count, read_count;
+// The per-slot census the loader's fusion passes share (session.rs:1861-1876):
+// how many calls write and read each slot, the last reader, the output ports.
+struct Census {
+    std::map<uint32_t, uint32_t> prod, read;
     std::map<uint32_t, size_t> read_idx;
-    std::vector<holo_buffer_ref> rd, wr;
-    for (size_t i = 0; i < n; ++i) {
-        call_operands(calls[i], &rd, &wr);
-        for (auto &r : rd) {
-            read_count[r.slot]++;
-            read_idx[r.slot] = i;
-        }
-        for (auto &w : wr)
-            if (w.slot != HOLO_SLOT_ABSENT) prod_count[w.slot]++;
-    }
     std::vector<uint32_t> out_slots;
-    for (auto &p : outputs) out_slots.push_back(p.slot);
-    auto is_out = [&](uint32_t s) { return std::find(out_slots.begin(), out_slots.end(), s) != out_slots.end(); };
-    std::map<uint32_t, size_t> slot_level;
-    for (size_t li = 0; li < plan.size(); ++li)
-        for (uint32_t ci : plan[li]) {
-            call_operands(calls[ci], &rd, &wr);
-            if (!wr.empty() && wr.back().slot != HOLO_SLOT_ABSENT) slot_level[wr.back().slot] = li;
+
+    Census(const std::vector<holo_kernel_call> &calls, const std::vector<Port> &outputs) {
+        std::vector<holo_buffer_ref> rd, wr;
+        for (size_t i = 0; i < calls.size(); ++i) {
+            call_operands(calls[i], &rd, &wr);
+            for (auto &r : rd) {
+                read[r.slot]++;
+                read_idx[r.slot] = i;
+            }
+            for (auto &w : wr)
+                if (w.slot != HOLO_SLOT_ABSENT) prod[w.slot]++;
         }
-    auto count = [](const std::map<uint32_t, uint32_t> &m, uint32_t s) {
+        for (auto &p : outputs) out_slots.push_back(p.slot);
+    }
+    static uint32_t count(const std::map<uint32_t, uint32_t> &m, uint32_t s) {
         auto it = m.find(s);
         return it == m.end() ? 0u : it->second;
-    };
-    std::vector<bool> absorbed(n, false);
-    std::vector<holo_kernel_call> fused(calls);
-    std::vector<bool> is_fused(n, false);
-    for (size_t i = 0; i < n; ++i) {
-        if (calls[i].tag != HOLO_OP_MATMUL) continue;
-        const holo_matmul_call mm = calls[i].u.matmul;
-        if (mm.dtype != HOLO_DTYPE_F32 && mm.dtype != HOLO_DTYPE_BF16 && mm.dtype != HOLO_DTYPE_F16) continue;
-        const uint32_t s = mm.output.slot;
-        if (s == HOLO_SLOT_ABSENT || is_out(s)) continue;
-        if (count(prod_count, s) != 1 || count(read_count, s) != 1) continue;
-        const size_t j = read_idx[s];
-        if (j == i || absorbed[j]) continue;
-        std::vector<holo_buffer_ref> jins, jw;
-        call_operands(calls[j], &jins, &jw);
-        if (jw.size() != 1) continue;
-        const holo_buffer_ref jout = jw[0];
-        if (const uint32_t act = fused_activation(calls[j])) {
-            if (jins.size() != 1 || jins[0].slot != s) continue;
-            if (!holo::fused_act_supported(act, mm.dtype, false)) continue;
-            holo_kernel_call f{};
-            f.tag = HOLO_OP_MATMUL_ACT;
-            f.u.matmul_act.mm = mm;
-            f.u.matmul_act.mm.output = jout;
-            f.u.matmul_act.act = uint8_t(act);
-            fused[i] = f;
-            is_fused[i] = true;
-            absorbed[j] = true;
-        } else if (calls[j].tag == HOLO_OP_ADD) {
-            if (jins.size() != 2) continue;
-            holo_buffer_ref residual;
-            if (jins[0].slot == s) residual = jins[1];
-            else if (jins[1].slot == s) residual = jins[0];
-            else continue;
-            const auto rl = slot_level.find(residual.slot), ml = slot_level.find(s);
-            const bool ready = rl == slot_level.end() || ml == slot_level.end() || rl->second < ml->second;
-            if (!ready) continue;
-            // three-op chain matmul -> add -> activation, f32 only
-            const uint32_t add_out = jout.slot;
-            if (mm.dtype == HOLO_DTYPE_F32 && add_out != HOLO_SLOT_ABSENT && !is_out(add_out) &&
-                count(prod_count, add_out) == 1 && count(read_count, add_out) == 1) {
-                const size_t k = read_idx[add_out];
-                const uint32_t act = k != j && !absorbed[k] ? fused_activation(calls[k]) : 0;
-                std::vector<holo_buffer_ref> kins, kw;
-                call_operands(calls[k], &kins, &kw);
-                if (act && kins.size() == 1 && kins[0].slot == add_out && kw.size() == 1 &&
-                    holo::fused_act_supported(act, mm.dtype, true)) {
-                    holo_kernel_call f{};
-                    f.tag = HOLO_OP_MATMUL_ADD_ACT;
-                    f.u.matmul_add_act.mm = mm;
-                    f.u.matmul_add_act.mm.output = kw[0];
-                    f.u.matmul_add_act.residual = residual;
-                    f.u.matmul_add_act.act = uint8_t(act);
-                    fused[i] = f;
-                    is_fused[i] = true;
-                    absorbed[j] = true;
-                    absorbed[k] = true;
-                    continue;
-                }
-            }
-            holo_kernel_call f{};
-            f.tag = HOLO_OP_MATMUL_ADD;
-            f.u.matmul_add.mm = mm;
-            f.u.matmul_add.mm.output = jout;
-            f.u.matmul_add.residual = residual;
-            fused[i] = f;
-            is_fused[i] = true;
-            absorbed[j] = true;
-        }
     }
-    if (std::find(absorbed.begin(), absorbed.end(), true) == absorbed.end()) return;
+    bool is_out(uint32_t s) const {
+        return std::find(out_slots.begin(), out_slots.end(), s) != out_slots.end();
+    }
+    // Slot s, written by call i, is a private intermediate (one producer, one
+    // reader, no output port) whose reader is a call not yet absorbed: *j.
+    bool sole_reader(uint32_t s, size_t i, const std::vector<bool> &absorbed, size_t *j) const {
+        if (s == HOLO_SLOT_ABSENT || is_out(s)) return false;
+        if (count(prod, s) != 1 || count(read, s) != 1) return false;
+        *j = read_idx.at(s);
+        return *j != i && !absorbed[*j];
+    }
+};
+
+// Drop the absorbed calls, put each fused call in its producer's place, and
+// renumber the plan (empty levels vanish), as every reference pass does.
+void compact(std::vector<holo_kernel_call> &calls, std::vector<std::vector<uint32_t>> &plan,
+             const std::vector<bool> &absorbed, const std::vector<holo_kernel_call> &fused,
+             const std::vector<bool> &is_fused) {
+    const size_t n = calls.size();
+    if (std::find(absorbed.begin(), absorbed.end(), true) == absorbed.end()) {
+        for (size_t i = 0; i < n; ++i)
+            if (is_fused[i]) calls[i] = fused[i];
+        return;
+    }
     std::vector<holo_kernel_call> nc;
     std::vector<uint32_t> remap(n, HOLO_SLOT_ABSENT);
     for (size_t i = 0; i < n; ++i) {
@@ -319,6 +284,236 @@ void fuse_matmul_epilogue(std::vector<holo_kernel_call> &calls,
     }
     calls = std::move(nc);
     plan = std::move(np);
+}
+
+// fuse_dequant_matmul (crates/hologram-exec/src/session.rs:1853-2044): a
+// Dequantize whose output is a private intermediate read only as the B operand
+// of an unpacked f32 MatMul becomes one MatMulDequant in the MatMul's place.
+// A weight slot that declares the output-major W8A8 form (weight_layout 1 with
+// act_quant 1) is fused as the W8A8 GEMV when the tier and shape allow it; an
+// output-major declaration nothing can read ([n, k] bytes) refuses the load.
+int fuse_dequant_matmul(std::vector<holo_kernel_call> &calls, std::vector<std::vector<uint32_t>> &plan,
+                        const std::vector<Port> &outputs) {
+    const size_t n = calls.size();
+    const Census cs(calls, outputs);
+    std::vector<bool> absorbed(n, false), is_fused(n, false);
+    std::vector<holo_kernel_call> fused(calls);
+    for (size_t i = 0; i < n; ++i) {
+        if (calls[i].tag != HOLO_OP_DEQUANTIZE) continue;
+        const holo_dequantize_call dq = calls[i].u.dequantize;
+        size_t j;
+        if (!cs.sole_reader(dq.output.slot, i, absorbed, &j)) continue;
+        if (calls[j].tag != HOLO_OP_MATMUL) continue;
+        const holo_matmul_call mm = calls[j].u.matmul;
+        if (mm.dtype != HOLO_DTYPE_F32 || mm.b_packed || mm.b.slot != dq.output.slot) continue;
+        // the quant_tier registry (quant_tier.rs:137-178)
+        const uint8_t q = dq.quant_dtype;
+        if (q != HOLO_DTYPE_I8 && q != HOLO_DTYPE_U8 && q != HOLO_DTYPE_I4 && q != HOLO_DTYPE_E8CB) continue;
+        const bool needs_cb = q == HOLO_DTYPE_E8CB, has_cb = dq.codebook.slot != HOLO_SLOT_ABSENT;
+        const bool k_ok = q == HOLO_DTYPE_I8 || (q == HOLO_DTYPE_I4 && mm.k % 2 == 0) ||
+                          (q == HOLO_DTYPE_E8CB && mm.k % 8 == 0);
+        const bool declares = dq.weight_layout == 1 && dq.act_quant == 1;
+        const bool omajor_ok = declares && q != HOLO_DTYPE_U8 && k_ok && dequant_per_channel(dq) &&
+                               dq.inner == 1 && dq.channels == mm.n && mm.k <= holo::kI8DotKMax &&
+                               needs_cb == has_cb;
+        if (dq.weight_layout == 1 && !omajor_ok)
+            return set_error(HOLO_ERR_DISPATCH,
+                             "session_load: kernel call " + std::to_string(i) +
+                                 " declares an output-major weight that no kernel can read");
+        if (!omajor_ok && q == HOLO_DTYPE_E8CB) continue;   // not scalar-decodable: left unfused
+        holo_kernel_call f{};
+        f.tag = HOLO_OP_MATMUL_DEQUANT;
+        auto &md = f.u.matmul_dequant;
+        md.a = mm.a;
+        md.bq = dq.input;
+        md.scales = dq.scales;
+        md.zero_points = dq.zero_points;
+        md.output = mm.output;
+        md.m = mm.m;
+        md.k = mm.k;
+        md.n = mm.n;
+        md.channels = dq.channels;
+        md.inner = dq.inner;
+        md.quant_dtype = q;
+        md.dtype = mm.dtype;
+        md.scale_bits = dq.scale_bits;
+        md.zero_point = dq.zero_point;
+        md.bq_omajor = omajor_ok;
+        md.act_quant = omajor_ok ? 1 : 0;
+        md.act = 0;
+        md.residual = holo_buffer_ref{HOLO_SLOT_ABSENT, 0, 0};
+        md.codebook = omajor_ok ? dq.codebook : holo_buffer_ref{HOLO_SLOT_ABSENT, 0, 0};
+        fused[j] = f;
+        is_fused[j] = true;
+        absorbed[i] = true;
+    }
+    for (size_t i = 0; i < n; ++i)
+        if (!absorbed[i] && calls[i].tag == HOLO_OP_DEQUANTIZE && calls[i].u.dequantize.weight_layout == 1)
+            return set_error(HOLO_ERR_DISPATCH,
+                             "session_load: kernel call " + std::to_string(i) +
+                                 " declares an output-major weight that no kernel can read");
+    compact(calls, plan, absorbed, fused, is_fused);
+    return HOLO_OK;
+}
+
+// fuse_dequant_activation (crates/hologram-exec/src/session.rs:2061-2148): a
+// per-tensor f32 Dequantize read only by an f32 Sigmoid / Tanh / Gelu / Silu /
+// Exp / Erf becomes one DequantActivation (lut_act id) in the activation's place.
+void fuse_dequant_activation(std::vector<holo_kernel_call> &calls,
+                             std::vector<std::vector<uint32_t>> &plan, const std::vector<Port> &outputs) {
+    const size_t n = calls.size();
+    const Census cs(calls, outputs);
+    std::vector<bool> absorbed(n, false), is_fused(n, false);
+    std::vector<holo_kernel_call> fused(calls);
+    for (size_t i = 0; i < n; ++i) {
+        if (calls[i].tag != HOLO_OP_DEQUANTIZE) continue;
+        const holo_dequantize_call dq = calls[i].u.dequantize;
+        if (dequant_per_channel(dq) || dq.dtype != HOLO_DTYPE_F32) continue;
+        size_t j;
+        if (!cs.sole_reader(dq.output.slot, i, absorbed, &j)) continue;
+        int act = -1;   // dequant_act_id: the lut_act ids
+        switch (calls[j].tag) {
+            case HOLO_OP_SIGMOID: act = 0; break;
+            case HOLO_OP_TANH: act = 1; break;
+            case HOLO_OP_GELU: act = 2; break;
+            case HOLO_OP_SILU: act = 3; break;
+            case HOLO_OP_EXP: act = 4; break;
+            case HOLO_OP_ERF: act = 5; break;
+            default: break;
+        }
+        if (act < 0) continue;
+        const holo_unary_call ac = calls[j].u.unary;
+        if (ac.dtype != HOLO_DTYPE_F32 || ac.input.slot != dq.output.slot) continue;
+        holo_kernel_call f{};
+        f.tag = HOLO_OP_DEQUANT_ACT;
+        auto &da = f.u.dequant_act;
+        da.input = dq.input;
+        da.output = ac.output;
+        da.element_count = dq.element_count;
+        da.quant_dtype = dq.quant_dtype;
+        da.act = uint8_t(act);
+        da.dtype = HOLO_DTYPE_F32;
+        da.scale_bits = dq.scale_bits;
+        da.zero_point = dq.zero_point;
+        fused[j] = f;
+        is_fused[j] = true;
+        absorbed[i] = true;
+    }
+    compact(calls, plan, absorbed, fused, is_fused);
+}
+
+// fuse_matmul_epilogue (crates/hologram-exec/src/session.rs:2150-2373): a
+// MatMul (f32, bf16, f16) or an epilogue-free f32 MatMulDequant whose output
+// has one producer and one reader, and is no output port, absorbs that reader
+// when it is an activation (-> MatMulActivation) or a residual Add whose other
+// operand is ready no later than the producer's level (-> MatMulAdd; for an
+// f32 producer a single activation reader of the sum is absorbed too,
+// -> MatMulAddActivation); a MatMulDequant takes the same epilogue in its own
+// act / residual fields. Absorbed calls leave the call list and the plan. One
+// difference: a fusion whose activation this device does not serve is skipped
+// (the unfused calls give the same result).
+void fuse_matmul_epilogue(std::vector<holo_kernel_call> &calls,
+                          std::vector<std::vector<uint32_t>> &plan, const std::vector<Port> &outputs) {
+    const size_t n = calls.size();
+    const Census cs(calls, outputs);
+    std::vector<holo_buffer_ref> rd, wr;
+    std::map<uint32_t, size_t> slot_level;
+    for (size_t li = 0; li < plan.size(); ++li)
+        for (uint32_t ci : plan[li]) {
+            call_operands(calls[ci], &rd, &wr);
+            if (!wr.empty() && wr.back().slot != HOLO_SLOT_ABSENT) slot_level[wr.back().slot] = li;
+        }
+    std::vector<bool> absorbed(n, false), is_fused(n, false);
+    std::vector<holo_kernel_call> fused(calls);
+    for (size_t i = 0; i < n; ++i) {
+        const bool is_mmd = calls[i].tag == HOLO_OP_MATMUL_DEQUANT;
+        uint8_t dtype;
+        uint32_t s;
+        if (calls[i].tag == HOLO_OP_MATMUL) {
+            const holo_matmul_call &mm = calls[i].u.matmul;
+            if (mm.dtype != HOLO_DTYPE_F32 && mm.dtype != HOLO_DTYPE_BF16 && mm.dtype != HOLO_DTYPE_F16) continue;
+            dtype = mm.dtype;
+            s = mm.output.slot;
+        } else if (is_mmd) {
+            const holo_matmul_dequant_call &md = calls[i].u.matmul_dequant;
+            if (md.dtype != HOLO_DTYPE_F32 || md.act != 0 || md.residual.slot != HOLO_SLOT_ABSENT) continue;
+            dtype = HOLO_DTYPE_F32;
+            s = md.output.slot;
+        } else {
+            continue;
+        }
+        // the producer with its output moved to `out` and the epilogue set
+        auto make = [&](const holo_buffer_ref &out, const holo_buffer_ref *residual, uint32_t act) {
+            holo_kernel_call f{};
+            if (is_mmd) {
+                f.tag = HOLO_OP_MATMUL_DEQUANT;
+                f.u.matmul_dequant = calls[i].u.matmul_dequant;
+                f.u.matmul_dequant.output = out;
+                f.u.matmul_dequant.act = uint8_t(act);
+                if (residual) f.u.matmul_dequant.residual = *residual;
+                return f;
+            }
+            holo_matmul_call mm = calls[i].u.matmul;
+            mm.output = out;
+            if (!residual) {
+                f.tag = HOLO_OP_MATMUL_ACT;
+                f.u.matmul_act.mm = mm;
+                f.u.matmul_act.act = uint8_t(act);
+            } else if (!act) {
+                f.tag = HOLO_OP_MATMUL_ADD;
+                f.u.matmul_add.mm = mm;
+                f.u.matmul_add.residual = *residual;
+            } else {
+                f.tag = HOLO_OP_MATMUL_ADD_ACT;
+                f.u.matmul_add_act.mm = mm;
+                f.u.matmul_add_act.residual = *residual;
+                f.u.matmul_add_act.act = uint8_t(act);
+            }
+            return f;
+        };
+        size_t j;
+        if (!cs.sole_reader(s, i, absorbed, &j)) continue;
+        std::vector<holo_buffer_ref> jins, jw;
+        call_operands(calls[j], &jins, &jw);
+        if (jw.size() != 1) continue;
+        const holo_buffer_ref jout = jw[0];
+        if (const uint32_t act = fused_activation(calls[j])) {
+            if (jins.size() != 1 || jins[0].slot != s) continue;
+            if (!holo::fused_act_supported(act, dtype, false)) continue;
+            fused[i] = make(jout, nullptr, act);
+            is_fused[i] = true;
+            absorbed[j] = true;
+        } else if (calls[j].tag == HOLO_OP_ADD) {
+            if (jins.size() != 2) continue;
+            holo_buffer_ref residual;
+            if (jins[0].slot == s) residual = jins[1];
+            else if (jins[1].slot == s) residual = jins[0];
+            else continue;
+            const auto rl = slot_level.find(residual.slot), ml = slot_level.find(s);
+            const bool ready = rl == slot_level.end() || ml == slot_level.end() || rl->second < ml->second;
+            if (!ready) continue;
+            // three-op chain producer -> add -> activation, f32 only
+            const uint32_t add_out = jout.slot;
+            size_t k;
+            if (dtype == HOLO_DTYPE_F32 && cs.sole_reader(add_out, j, absorbed, &k)) {
+                const uint32_t act = fused_activation(calls[k]);
+                std::vector<holo_buffer_ref> kins, kw;
+                call_operands(calls[k], &kins, &kw);
+                if (act && kins.size() == 1 && kins[0].slot == add_out && kw.size() == 1 &&
+                    holo::fused_act_supported(act, dtype, true)) {
+                    fused[i] = make(kw[0], &residual, act);
+                    is_fused[i] = true;
+                    absorbed[j] = true;
+                    absorbed[k] = true;
+                    continue;
+                }
+            }
+            fused[i] = make(jout, &residual, 0);
+            is_fused[i] = true;
+            absorbed[j] = true;
+        }
+    }
+    compact(calls, plan, absorbed, fused, is_fused);
 }
 
 // A step of the walk: one call, or a fused group (index into groups).
@@ -970,8 +1165,21 @@ int load_impl(holo_backend *be, const uint8_t *bytes, size_t len, uint32_t flags
                     return set_error(HOLO_ERR_SLOT_OUT_OF_RANGE,
                                      "session_load: port '" + p.name + "' names the absent slot");
     }
-    // --- the loader's epilogue fusion (session.rs:493-509)
+    // --- the loader's fusion passes, in the reference's order (session.rs:
+    // 493-504): dequant -> MatMul first, so the quantized weight is read in
+    // place rather than traded for an epilogue fusion
+    if (!(flags & HOLO_SESSION_NO_DEQUANT_FUSION)) {
+        const int rc = fuse_dequant_matmul(s->calls, s->plan, s->outputs);
+        if (rc != HOLO_OK) return rc;
+    } else {
+        for (size_t i = 0; i < s->calls.size(); ++i)
+            if (s->calls[i].tag == HOLO_OP_DEQUANTIZE && s->calls[i].u.dequantize.weight_layout == 1)
+                return set_error(HOLO_ERR_DISPATCH,
+                                 "session_load: kernel call " + std::to_string(i) +
+                                     " declares an output-major weight that no kernel can read");
+    }
     if (!(flags & HOLO_SESSION_NO_EPILOGUE_FUSION)) fuse_matmul_epilogue(s->calls, s->plan, s->outputs);
+    if (!(flags & HOLO_SESSION_NO_DEQUANT_FUSION)) fuse_dequant_activation(s->calls, s->plan, s->outputs);
     // --- weights (fingerprint -> body), constants
     std::map<std::string, std::pair<const uint8_t *, uint64_t>> weights;
     if ((it = sec.find(kSecWeights)) != sec.end()) {
@@ -1256,6 +1464,14 @@ int holo_hip_session_nodes(const holo_session *s, uint32_t *n_nodes, uint32_t *n
     if (!s) return set_error(HOLO_ERR_INIT, "session_nodes: null session");
     if (n_nodes) *n_nodes = uint32_t(s->nodes.size());
     if (n_groups) *n_groups = uint32_t(s->groups.size());
+    return HOLO_OK;
+}
+
+int holo_hip_session_call(const holo_session *s, uint32_t index, holo_kernel_call *out) {
+    if (!s || !out) return set_error(HOLO_ERR_INIT, "session_call: null argument");
+    if (index >= s->calls.size())
+        return set_error(HOLO_ERR_SLOT_OUT_OF_RANGE, "session_call: index past the loaded calls");
+    *out = s->calls[index];
     return HOLO_OK;
 }
 

@@ -177,4 +177,17 @@ bool build_lut_table(int act, bool f16, uint16_t *t) {
     return true;
 }
 
+// f(x) for lut_act id `act` (lut_act_ref, src/cpu/float_kernels.rs:3628-3638):
+// the DequantActivation table's entries. False for an id with no restatement.
+bool lut_act_value(int act, float x, float *y) {
+    switch (act) {
+        case 0: *y = act_sigmoid(x); return true;
+        case 1: *y = act_tanh(x); return true;
+        case 2: *y = act_gelu(x); return true;
+        case 3: *y = act_silu(x); return true;
+        case 4: *y = libm_expf(x); return true;
+        default: return false;
+    }
+}
+
 }  // namespace holo

@@ -16,12 +16,15 @@ from dataclasses import dataclass, field
 from . import _ffi
 
 # dtype tags, crates/hologram-types/src/dtype_id.rs:52-61
+DTYPE_U8 = 1
 DTYPE_I8 = 2
 DTYPE_I32 = 4
 DTYPE_I64 = 5
 DTYPE_F16 = 6
 DTYPE_BF16 = 7
 DTYPE_F32 = 8
+DTYPE_I4 = 10     # two per byte, low nibble first (dtype_id.rs:150-161)
+DTYPE_E8CB = 11   # one codebook index per 8-element group
 
 
 class lut_act:  # noqa: N801 - the reference's module name (kernel_call.rs:877-885)
@@ -37,11 +40,21 @@ class lut_act:  # noqa: N801 - the reference's module name (kernel_call.rs:877-8
 # archive discriminants, kernel_codec.rs:18-128
 D_ADD = 5
 D_MUL = 7
+D_RELU = 11
 D_SIGMOID = 12
 D_TANH = 13
 D_GELU = 14
 D_SILU = 15
+D_ELU = 16
+D_SELU = 17
 D_EXP = 18
+D_ERF = 32      # decoded; not served on the device
+D_DEQ = 105     # Dequantize (118 on the wire when it declares anything)
+D_DEQ2 = 118
+D_MMDQ = 111    # MatMulDequant (116 with the extended fields, 117 with a codebook)
+D_MMDQ2 = 116
+D_MMDQ3 = 117
+D_DQACT = 113   # DequantActivation
 D_MATMUL = 46
 D_MMA = 106     # MatMulActivation (the loader's epilogue fusion)
 D_MMADD = 107   # MatMulAdd
@@ -115,6 +128,128 @@ class BinaryCall:
 
 
 NO_BUFFER = BufferRef(SLOT_ABSENT)
+
+
+class mm_act_quant:  # noqa: N801 - the reference's module (kernel_call.rs:66-104)
+    W8A32 = 0
+    W8A8_TOKEN_SYM = 1
+    K_MAX = 133144   # i32::MAX // (127 * 127): the exact-i32 dot bound
+
+
+class weight_layout:  # noqa: N801 - hologram-types dtype_id.rs:18-28
+    ROW_MAJOR = 0
+    OUTPUT_MAJOR = 1
+
+
+@dataclass(frozen=True)
+class DequantizeCall:
+    """kernel_call.rs:790-840: out[i] = ((q[i] - zp) as f32 * scale) as dtype;
+    per-channel when channels > 0 and scales is present (channel (i / inner) %
+    channels). The extended wire form (118) declares the weight slot's layout,
+    its activation treatment and a codebook."""
+    input: BufferRef
+    scales: BufferRef
+    zero_points: BufferRef
+    output: BufferRef
+    element_count: int
+    channels: int = 0
+    inner: int = 1
+    quant_dtype: int = DTYPE_I8
+    dtype: int = DTYPE_F32
+    scale_bits: int = 0
+    zero_point: int = 0
+    codebook: BufferRef = NO_BUFFER
+    weight_layout: int = 0
+    act_quant: int = 0
+
+    def per_channel(self) -> bool:
+        return self.channels > 0 and self.scales.slot != SLOT_ABSENT
+
+    def extended(self) -> bool:  # kernel_call.rs:837-839
+        return self.weight_layout != 0 or self.act_quant != 0 or self.codebook.slot != SLOT_ABSENT
+
+    def wire_tag(self) -> int:
+        return D_DEQ2 if self.extended() else D_DEQ
+
+    def wire(self) -> bytes:  # put_dequantize, kernel_codec.rs:861-872 (+ :497-506)
+        body = (self.input.wire() + self.scales.wire() + self.zero_points.wire()
+                + self.output.wire()
+                + struct.pack("<QIIBBIi", self.element_count, self.channels, self.inner,
+                              self.quant_dtype, self.dtype, self.scale_bits, self.zero_point))
+        if self.extended():
+            body += struct.pack("<BB", self.weight_layout, self.act_quant) + self.codebook.wire()
+        return body
+
+
+@dataclass(frozen=True)
+class MatMulDequantCall:
+    """kernel_call.rs:162-273: out = act(A . dequant(Bq) [+ residual]), f32.
+    bq_omajor with act_quant W8A8_TOKEN_SYM is the output-major W8A8 GEMV
+    (i8 / i4 / e8cb + codebook); otherwise the [k, n] weight is dequantized
+    (W8A32)."""
+    a: BufferRef
+    bq: BufferRef
+    scales: BufferRef
+    zero_points: BufferRef
+    output: BufferRef
+    m: int
+    k: int
+    n: int
+    channels: int = 0
+    inner: int = 1
+    quant_dtype: int = DTYPE_I8
+    dtype: int = DTYPE_F32
+    scale_bits: int = 0
+    zero_point: int = 0
+    bq_omajor: bool = False
+    act_quant: int = 0
+    act: int = 0
+    residual: BufferRef = NO_BUFFER
+    codebook: BufferRef = NO_BUFFER
+
+    def per_channel(self) -> bool:
+        return self.channels > 0 and self.scales.slot != SLOT_ABSENT
+
+    def extended(self) -> bool:  # kernel_call.rs:250-256
+        return (self.bq_omajor or self.act_quant != 0 or self.act != 0
+                or self.residual.slot != SLOT_ABSENT or self.codebook.slot != SLOT_ABSENT)
+
+    def wire_tag(self) -> int:
+        if self.codebook.slot != SLOT_ABSENT:
+            return D_MMDQ3
+        return D_MMDQ2 if self.extended() else D_MMDQ
+
+    def wire(self) -> bytes:  # put_matmul_dequant, kernel_codec.rs:835-850 (+ :525-546)
+        body = (self.a.wire() + self.bq.wire() + self.scales.wire() + self.zero_points.wire()
+                + self.output.wire()
+                + struct.pack("<IIIIIBBIi", self.m, self.k, self.n, self.channels, self.inner,
+                              self.quant_dtype, self.dtype, self.scale_bits, self.zero_point))
+        tag = self.wire_tag()
+        if tag != D_MMDQ:
+            body += (struct.pack("<BBB", int(self.bq_omajor), self.act_quant, self.act)
+                     + self.residual.wire())
+        if tag == D_MMDQ3:
+            body += self.codebook.wire()
+        return body
+
+
+@dataclass(frozen=True)
+class DequantActivationCall:
+    """kernel_call.rs:275-290: out[i] = f((q[i] - zp) as f32 * scale), f32,
+    f the lut_act function `act`; per-tensor."""
+    input: BufferRef
+    output: BufferRef
+    element_count: int
+    quant_dtype: int = DTYPE_I8
+    act: int = lut_act.GELU
+    dtype: int = DTYPE_F32
+    scale_bits: int = 0
+    zero_point: int = 0
+
+    def wire(self) -> bytes:  # put_dequant_activation, kernel_codec.rs:851-860
+        return (self.input.wire() + self.output.wire()
+                + struct.pack("<QBBBIi", self.element_count, self.quant_dtype, self.act,
+                              self.dtype, self.scale_bits, self.zero_point))
 
 
 @dataclass(frozen=True)
@@ -361,6 +496,8 @@ class TransposeCall:
 
 
 _NAMES = {D_ADD: "Add", D_MUL: "Mul", D_RN: "RmsNorm", D_ROTARY: "RotaryEmbedding",
+          D_RELU: "Relu", D_ELU: "Elu", D_SELU: "Selu", D_ERF: "Erf", D_DEQ: "Dequantize",
+          D_MMDQ: "MatMulDequant", D_DQACT: "DequantActivation",
           D_GATHER: "Gather", D_ARGMAX: "ArgMax", D_SIGMOID: "Sigmoid", D_TANH: "Tanh", D_GELU: "Gelu", D_SILU: "Silu", D_EXP: "Exp",
           D_MATMUL: "MatMul", D_MMA: "MatMulActivation", D_MMADD: "MatMulAdd",
           D_MMAA: "MatMulAddActivation", D_KVWR: "KvCacheWrite", D_KVQA: "KvQuantAppend",
@@ -393,6 +530,34 @@ class KernelCall:
     @classmethod
     def Exp(cls, c: UnaryCall) -> "KernelCall":  # noqa: N802
         return cls(D_EXP, c)
+
+    @classmethod
+    def Relu(cls, c: UnaryCall) -> "KernelCall":  # noqa: N802
+        return cls(D_RELU, c)
+
+    @classmethod
+    def Elu(cls, c: UnaryCall) -> "KernelCall":  # noqa: N802
+        return cls(D_ELU, c)
+
+    @classmethod
+    def Selu(cls, c: UnaryCall) -> "KernelCall":  # noqa: N802
+        return cls(D_SELU, c)
+
+    @classmethod
+    def Erf(cls, c: UnaryCall) -> "KernelCall":  # noqa: N802
+        return cls(D_ERF, c)
+
+    @classmethod
+    def Dequantize(cls, c: DequantizeCall) -> "KernelCall":  # noqa: N802
+        return cls(D_DEQ, c)
+
+    @classmethod
+    def MatMulDequant(cls, c: MatMulDequantCall) -> "KernelCall":  # noqa: N802
+        return cls(D_MMDQ, c)
+
+    @classmethod
+    def DequantActivation(cls, c: DequantActivationCall) -> "KernelCall":  # noqa: N802
+        return cls(D_DQACT, c)
 
     @classmethod
     def MatMul(cls, c: MatMulCall) -> "KernelCall":  # noqa: N802
@@ -463,8 +628,11 @@ class KernelCall:
         return _NAMES.get(self.tag, f"op{self.tag}")
 
     def encode(self) -> bytes:
-        """Archive wire form of this one call (kernel_codec.rs encode_one)."""
-        return struct.pack("<H", self.tag) + self.payload.wire()
+        """Archive wire form of this one call (kernel_codec.rs encode_one); a
+        variant with several wire forms picks its own discriminant."""
+        wire_tag = getattr(self.payload, "wire_tag", None)
+        tag = wire_tag() if wire_tag else self.tag
+        return struct.pack("<H", tag) + self.payload.wire()
 
     def to_c(self) -> _ffi.KernelCallC:
         kc = _ffi.KernelCallC()
@@ -524,6 +692,20 @@ class KernelCall:
                 p.q.c(), p.k_cache.c(), p.v_cache.c(), p.k_scales.c(), p.v_scales.c(),
                 p.lens.c(), p.output.c(), p.batch, p.heads, p.kv_heads, p.bucket_rows,
                 p.head_dim, p.scale_bits, p.dtype)
+        elif isinstance(p, DequantizeCall):
+            kc.u.dequantize = _ffi.DequantizeCallC(
+                p.input.c(), p.scales.c(), p.zero_points.c(), p.output.c(), p.element_count,
+                p.channels, p.inner, p.quant_dtype, p.dtype, p.scale_bits, p.zero_point,
+                p.codebook.c(), p.weight_layout, p.act_quant)
+        elif isinstance(p, MatMulDequantCall):
+            kc.u.matmul_dequant = _ffi.MatMulDequantCallC(
+                p.a.c(), p.bq.c(), p.scales.c(), p.zero_points.c(), p.output.c(), p.m, p.k, p.n,
+                p.channels, p.inner, p.quant_dtype, p.dtype, p.scale_bits, p.zero_point,
+                int(p.bq_omajor), p.act_quant, p.act, p.residual.c(), p.codebook.c())
+        elif isinstance(p, DequantActivationCall):
+            kc.u.dequant_act = _ffi.DequantActivationCallC(
+                p.input.c(), p.output.c(), p.element_count, p.quant_dtype, p.act, p.dtype,
+                p.scale_bits, p.zero_point)
         else:
             raise TypeError(f"no C form for payload {type(p).__name__}")
         return kc

@@ -28,13 +28,14 @@ class Port:
 NO_EPILOGUE_FUSION = 1   # skip the reference loader's fuse_matmul_epilogue
 NO_DEVICE_FUSION = 2     # skip this backend's grouped few-row MatMuls and epilogues
 NO_NORM_FUSION = 4       # keep each RmsNorm between few-row MatMuls as its own launch
+NO_DEQUANT_FUSION = 8    # skip the loader's fuse_dequant_matmul / fuse_dequant_activation
 
 
 class HipSession:
     """`backend=None` loads dry: parse, size and validate every call on the host,
     with no device (such a session reports ports and refuses to execute).
     `flags` turns the load-time fusions off (NO_EPILOGUE_FUSION, NO_DEVICE_FUSION,
-    NO_NORM_FUSION);
+    NO_NORM_FUSION, NO_DEQUANT_FUSION);
     fused and unfused walks give the same bits."""
 
     def __init__(self, backend: HipBackend | None, archive: bytes, flags: int = 0):
@@ -60,6 +61,20 @@ class HipSession:
                                                ctypes.byref(cnt), ctypes.byref(dt),
                                                ctypes.byref(nb)))
         return Port(i, slot.value, cnt.value, dt.value, nb.value)
+
+    def call_tags(self) -> list[int]:
+        """The in-memory tag of each loaded call after the loader's passes."""
+        tags = []
+        for i in range(self.n_calls):
+            kc = _ffi.KernelCallC()
+            _check(self._lib.holo_hip_session_call(self.handle, i, ctypes.byref(kc)))
+            tags.append(kc.tag)
+        return tags
+
+    def call(self, index: int) -> _ffi.KernelCallC:
+        kc = _ffi.KernelCallC()
+        _check(self._lib.holo_hip_session_call(self.handle, index, ctypes.byref(kc)))
+        return kc
 
     def fingerprint(self) -> bytes:
         out = ctypes.create_string_buffer(32)

@@ -42,6 +42,9 @@ typedef enum holo_status {
 
 #define HOLO_DTYPE_I32 4u
 #define HOLO_DTYPE_I64 5u
+#define HOLO_DTYPE_U8 1u
+#define HOLO_DTYPE_I4 10u     /* packed signed 4-bit, two per byte, low nibble first */
+#define HOLO_DTYPE_E8CB 11u   /* one u8 codebook index per 8-element group */
 
 /* lut_act ids, crates/hologram-compute/src/kernel_call.rs:877-885 */
 #define HOLO_ACT_SIGMOID 0
@@ -66,11 +69,18 @@ typedef enum holo_status {
  * capabilities and take new discriminants (kernel_codec.rs:124-128). */
 #define HOLO_OP_ADD 5u
 #define HOLO_OP_MUL 7u
+#define HOLO_OP_RELU 11u
 #define HOLO_OP_SIGMOID 12u
 #define HOLO_OP_TANH 13u
 #define HOLO_OP_GELU 14u
 #define HOLO_OP_SILU 15u
+#define HOLO_OP_ELU 16u
+#define HOLO_OP_SELU 17u
 #define HOLO_OP_EXP 18u
+#define HOLO_OP_ERF 32u                   /* Erf: decoded, not served (no libm erff restatement) */
+#define HOLO_OP_DEQUANTIZE 105u           /* Dequantize (wire 105; 118 carries the extended fields) */
+#define HOLO_OP_MATMUL_DEQUANT 111u       /* MatMulDequant (wire 111; 116 / 117 the extended forms) */
+#define HOLO_OP_DEQUANT_ACT 113u          /* DequantActivation */
 #define HOLO_OP_MATMUL 46u
 #define HOLO_OP_MATMUL_ACT 106u           /* MatMulActivation (kernel_codec.rs:102)    */
 #define HOLO_OP_MATMUL_ADD 107u           /* MatMulAdd (kernel_codec.rs:103)           */
@@ -97,7 +107,10 @@ typedef struct holo_buffer_ref {
 #define HOLO_SLOT_ABSENT 0xFFFFFFFFu
 
 /* UnaryCall, kernel_call.rs:28-36. Sigmoid/Tanh/Gelu/Silu/Exp over bf16/f16
- * run as a gather through the 65536-entry table (src/cpu/lut.rs:76-98). */
+ * run as a gather through the 65536-entry table (src/cpu/lut.rs:76-98); Relu,
+ * Elu and Selu over bf16/f16 through the same kind of table of
+ * narrow(f(widen(x))); every one of them over f32 is computed per element with
+ * the reference's scalar function (exp_f32_det, libm expf for Exp/Elu/Selu). */
 typedef struct holo_unary_call {
     holo_buffer_ref input;
     holo_buffer_ref output;
@@ -241,6 +254,73 @@ typedef struct holo_decode_attention_valid_call {
     uint8_t dtype;
 } holo_decode_attention_valid_call;
 
+/* DequantizeCall, kernel_call.rs:782-818 (dequantize, src/cpu/kernels.rs:185-296):
+ * out[i] = (q[i] - zp) as f32 * scale, per tensor (scale_bits, zero_point) or
+ * per channel (channels > 0 and scales present: channel (i / inner) % channels
+ * reads scales[ch] f32 and zero_points[ch] i32). quant_dtype i8, u8 or i4
+ * (nibbles, low first, sign-extended); dtype f32, bf16 or f16. The extended
+ * wire form (118) adds weight_layout, act_quant and codebook, which the
+ * loader's dequant -> matmul fusion reads; the standalone op ignores them. */
+typedef struct holo_dequantize_call {
+    holo_buffer_ref input;
+    holo_buffer_ref scales;
+    holo_buffer_ref zero_points;
+    holo_buffer_ref output;
+    uint64_t element_count;
+    uint32_t channels, inner;
+    uint8_t quant_dtype;
+    uint8_t dtype;
+    uint32_t scale_bits;
+    int32_t zero_point;
+    holo_buffer_ref codebook;   /* HOLO_SLOT_ABSENT unless 118 carries one */
+    uint8_t weight_layout;      /* 0 row-major [k,n], 1 output-major [n,k] */
+    uint8_t act_quant;          /* 0 W8A32, 1 W8A8 per-token symmetric */
+} holo_dequantize_call;
+
+/* MatMulDequantCall, kernel_call.rs:162-273 (matmul_dequant_float +
+ * matmul_dequant_epilogue, src/cpu/float_kernels.rs:459-760): out = act(A .
+ * dequant(Bq) [+ residual]), f32 A and output.
+ *   bq_omajor = 1 with act_quant = 1 (W8A8): Bq output-major, symmetric
+ *   per-channel (channels == n, inner == 1, zero points 0, which the device
+ *   checks and reports at the next holo_hip_synchronize), i8 / i4 / e8cb
+ *   (codebook: 256 x 8 i8); each A row quantized per token, exact int32 dots,
+ *   out = (acc as f32) * (scale_a * scales[j]): bit-exact.
+ *   otherwise (W8A32): Bq [k,n] i8 / u8 / i4, per tensor or per channel,
+ *   dequantized to f32 and multiplied in f32 (within 1e-5).
+ * act: fused_activation id (0 none); residual: HOLO_SLOT_ABSENT for none. */
+typedef struct holo_matmul_dequant_call {
+    holo_buffer_ref a;
+    holo_buffer_ref bq;
+    holo_buffer_ref scales;
+    holo_buffer_ref zero_points;
+    holo_buffer_ref output;
+    uint32_t m, k, n, channels, inner;
+    uint8_t quant_dtype;
+    uint8_t dtype;
+    uint32_t scale_bits;
+    int32_t zero_point;
+    uint8_t bq_omajor;
+    uint8_t act_quant;
+    uint8_t act;
+    holo_buffer_ref residual;
+    holo_buffer_ref codebook;
+} holo_matmul_dequant_call;
+
+/* DequantActivationCall, kernel_call.rs:275-290 (dequant_activation,
+ * src/cpu/kernels.rs:311-388): out[i] = f((q[i] - zp) as f32 * scale) as f32,
+ * the table of the <= 256 levels built once per call with the reference's
+ * scalar function f of lut_act id `act` (0-4). i8 / u8 / i4 input. */
+typedef struct holo_dequant_activation_call {
+    holo_buffer_ref input;
+    holo_buffer_ref output;
+    uint64_t element_count;
+    uint8_t quant_dtype;
+    uint8_t act;
+    uint8_t dtype;
+    uint32_t scale_bits;
+    int32_t zero_point;
+} holo_dequant_activation_call;
+
 /* New (tag 122): int8 KV quantize + append. Each new row (head_dim values of
  * `dtype` in {bf16, f16, f32}) is quantized with the reference's per-row
  * symmetric scheme (src/cpu/simd.rs:4755-4785: scale = max|x|/127,
@@ -330,6 +410,9 @@ typedef struct holo_kernel_call {
         holo_kv_cache_write_call kv_write;
         holo_kv_quant_append_call kv_quant_append;
         holo_decode_attention_valid_call attn_valid;
+        holo_dequantize_call dequantize;
+        holo_matmul_dequant_call matmul_dequant;
+        holo_dequant_activation_call dequant_act;
         holo_decode_attention_i8_call attn_i8;
         holo_attention_i8_rows_call attn_i8_rows;
         holo_transpose_call transpose;
@@ -403,8 +486,13 @@ typedef struct holo_session holo_session;
  * but nothing is allocated and the session cannot execute (host-only checks). */
 int holo_hip_session_load(holo_backend *be, const uint8_t *archive, size_t len,
                           holo_session **out);
-/* Load with options. By default a load runs the reference's epilogue fusion
- * (fuse_matmul_epilogue, session.rs:2150-2373) and then this backend's device
+/* Load with options. By default a load runs the reference's loader passes in
+ * its order (session.rs:493-504): fuse_dequant_matmul (a Dequantize read only
+ * as an f32 MatMul's B becomes a MatMulDequant; an output-major weight
+ * declaration nothing can read refuses the load), fuse_matmul_epilogue
+ * (session.rs:2150-2373), fuse_dequant_activation (a per-tensor f32 Dequantize
+ * read only by an f32 transcendental becomes a DequantActivation), and then
+ * this backend's device
  * fusion: few-row MatMuls that share their A operand run as one launch, and
  * the ops that only consume such a product (rotary embedding, int8
  * quantize+append, the SwiGLU product) run inside the launch that finishes
@@ -412,15 +500,21 @@ int holo_hip_session_load(holo_backend *be, const uint8_t *archive, size_t len,
  * first leaves each row's sums of squares, the second normalizes its A as it
  * reads it, and the norm's own launch and output go away. All of these give
  * the same bits as the unfused walk; the flags turn them off
- * (NO_DEVICE_FUSION also turns off the norm fusion). */
+ * (NO_DEVICE_FUSION also turns off the norm fusion; NO_DEQUANT_FUSION the two
+ * dequant passes). */
 #define HOLO_SESSION_NO_EPILOGUE_FUSION 1u
 #define HOLO_SESSION_NO_DEVICE_FUSION 2u
 #define HOLO_SESSION_NO_NORM_FUSION 4u
+#define HOLO_SESSION_NO_DEQUANT_FUSION 8u
 int holo_hip_session_load_ex(holo_backend *be, const uint8_t *archive, size_t len, uint32_t flags,
                              holo_session **out);
 /* Steps of one walk after fusion (each a call or a fused MatMul group), and
  * how many of them are fused groups. */
 int holo_hip_session_nodes(const holo_session *s, uint32_t *n_nodes, uint32_t *n_groups);
+/* The index-th kernel call of the loaded schedule, after the reference's
+ * loader passes (the calls the reference's Session counts with
+ * dequant_fused_count and its siblings, session.rs:1390-1437). */
+int holo_hip_session_call(const holo_session *s, uint32_t index, holo_kernel_call *out);
 int holo_hip_session_close(holo_session *s);
 int holo_hip_session_info(const holo_session *s, uint32_t *n_inputs, uint32_t *n_outputs,
                           uint32_t *n_calls, uint32_t *n_slots);

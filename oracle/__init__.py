@@ -41,6 +41,10 @@ _SIGS = {
     "or_matmul_q_omajor": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, _P, _S, _S, _S]),
     "or_matmul_i8_pc_omajor": (None, [_P, _P, _P, _P, _S, _S, _S]),
     "or_fnv1a_f32": (ctypes.c_uint64, [_P, _S]),
+    "or_dequantize": (ctypes.c_int, [_P, ctypes.c_uint64, ctypes.c_int, _P, _P, _U32, _U32, _F,
+                                     ctypes.c_int32, ctypes.c_int, _P]),
+    "or_dequant_activation": (ctypes.c_int, [_P, ctypes.c_uint64, ctypes.c_int, ctypes.c_int,
+                                             _F, ctypes.c_int32, _P]),
     "or_kv_cache_write": (ctypes.c_int, [_P, _P, _U32, _P, _U32, _U32, _U32, _U32]),
     "or_kv_quant_append": (ctypes.c_int, [_P, ctypes.c_int, _U32, _P, _P, _U32, _U32, _U32,
                                           _U32]),
@@ -137,6 +141,32 @@ def matmul_q_omajor(tier: int, a, bq, scales, m, k, n, codebook=None) -> np.ndar
     if lib().or_matmul_q_omajor(tier, _p(a), _p(bq), _p(cb) if cb is not None else None,
                                 _p(scales), _p(out), m, k, n) != 0:
         raise ValueError("matmul_q_omajor refused")
+    return out
+
+
+def dequantize(q, n: int, quant: int, dtype: int = DTYPE_F32, scale: float = 1.0, zp: int = 0,
+               scales=None, zps=None, channels: int = 0, inner: int = 1) -> np.ndarray:
+    """Dequantize (kernels.rs:185-296): f32 array, or the bf16/f16 bits as
+    uint16. Per-channel when `scales` is given and channels > 0."""
+    q = np.ascontiguousarray(q).view(np.uint8)
+    out = np.zeros(n, np.float32 if dtype == DTYPE_F32 else np.uint16)
+    sc = None if scales is None else np.ascontiguousarray(scales, np.float32)
+    zp_arr = None if zps is None else np.ascontiguousarray(zps, np.int32)
+    if lib().or_dequantize(_p(q), n, quant, _p(sc) if sc is not None else None,
+                           _p(zp_arr) if zp_arr is not None else None, channels, inner,
+                           float(np.float32(scale)), int(zp), dtype, _p(out)) != 0:
+        raise ValueError("dequantize refused")
+    return out
+
+
+def dequant_activation(q, n: int, quant: int, act: int, scale: float, zp: int) -> np.ndarray:
+    """DequantActivation (kernels.rs:311-388): the f32 table of the <= 256
+    levels through lut_act_ref(act), one lookup per element."""
+    q = np.ascontiguousarray(q).view(np.uint8)
+    out = np.zeros(n, np.float32)
+    if lib().or_dequant_activation(_p(q), n, quant, act, float(np.float32(scale)), int(zp),
+                                   _p(out)) != 0:
+        raise ValueError("dequant_activation refused")
     return out
 
 

@@ -340,6 +340,66 @@ void or_matmul_i8_pc_omajor(const float *a, const int8_t *bq, const float *scale
     or_matmul_q_omajor(OR_DTYPE_I8, a, (const uint8_t *)bq, NULL, scales, out, m, k, n);
 }
 
+/* ------------------------------------------------------------------------ */
+/* dequantize: src/cpu/kernels.rs:185-296; dequant_activation :311-388        */
+/* ------------------------------------------------------------------------ */
+/* The stored level of element i: i8 two's complement, u8 the raw byte, i4 a
+ * nibble (low first) sign-extended from bit 3 (kernels.rs:247-270). */
+static int32_t scalar_level(int quant, const uint8_t *in, uint64_t i)
+{
+    if (quant == OR_DTYPE_I8) return (int32_t)(int8_t)in[i];
+    if (quant == OR_DTYPE_U8) return (int32_t)in[i];
+    uint8_t nib = (i % 2 == 0) ? (in[i / 2] & 0x0f) : (in[i / 2] >> 4);
+    return nib >= 8 ? (int32_t)nib - 16 : (int32_t)nib;
+}
+
+/* (q - zp) in two's complement i32, as the reference's release build wraps */
+static int32_t wrap_sub(int32_t a, int32_t b) { return (int32_t)((uint32_t)a - (uint32_t)b); }
+
+int or_dequantize(const uint8_t *in, uint64_t n, int quant, const float *scales,
+                  const int32_t *zps, uint32_t channels, uint32_t inner, float scale,
+                  int32_t zp, int dtype, void *out)
+{
+    if (quant != OR_DTYPE_I8 && quant != OR_DTYPE_U8 && quant != OR_DTYPE_I4) return 1;
+    if (dtype != OR_DTYPE_F32 && dtype != OR_DTYPE_BF16 && dtype != OR_DTYPE_F16) return 1;
+    int per_ch = channels > 0 && scales != NULL;
+    uint64_t in_step = inner ? inner : 1;
+    for (uint64_t i = 0; i < n; ++i) {
+        float s = scale;
+        int32_t z = zp;
+        if (per_ch) {
+            uint64_t ch = (i / in_step) % channels;
+            s = scales[ch];
+            z = zps[ch];
+        }
+        float v = (float)wrap_sub(scalar_level(quant, in, i), z) * s;
+        if (dtype == OR_DTYPE_F32) ((float *)out)[i] = v;
+        else if (dtype == OR_DTYPE_BF16) ((uint16_t *)out)[i] = or_f32_to_bf16(v);
+        else ((uint16_t *)out)[i] = or_f32_to_f16(v);
+    }
+    return 0;
+}
+
+int or_dequant_activation(const uint8_t *in, uint64_t n, int quant, int act, float scale,
+                          int32_t zp, float *out)
+{
+    if (quant != OR_DTYPE_I8 && quant != OR_DTYPE_U8 && quant != OR_DTYPE_I4) return 1;
+    if (act < OR_ACT_SIGMOID || act > OR_ACT_EXP) return 3;   /* Erf: not restated */
+    float table[256];
+    int levels = quant == OR_DTYPE_I4 ? 16 : 256;
+    for (int raw = 0; raw < levels; ++raw) {
+        int32_t q = quant == OR_DTYPE_I8 ? (int32_t)(int8_t)(uint8_t)raw
+                  : quant == OR_DTYPE_U8 ? raw : (raw >= 8 ? raw - 16 : raw);
+        table[raw] = or_lut_act_ref(act, (float)wrap_sub(q, zp) * scale);
+    }
+    for (uint64_t i = 0; i < n; ++i) {
+        int raw = quant == OR_DTYPE_I4 ? ((i % 2 == 0) ? (in[i / 2] & 0x0f) : (in[i / 2] >> 4))
+                                       : in[i];
+        out[i] = table[raw];
+    }
+    return 0;
+}
+
 /* FNV-1a over the LE bytes of each f32 (simd.rs:8237-8246). */
 uint64_t or_fnv1a_f32(const float *v, size_t n)
 {

@@ -76,6 +76,18 @@ float or_quantize_row_i8(const float *a, int8_t *q, size_t k);
  * tier cannot split, or k above the exact-i32 bound. */
 #define OR_DTYPE_I4 10
 #define OR_DTYPE_E8CB 11
+#define OR_DTYPE_U8 1
+/* dequantize (src/cpu/kernels.rs:185-296): out[i] = ((q[i] - zp) as f32 * s)
+ * as dtype, per-channel (scales/zps [channels], channel (i / inner) %
+ * channels) when scales is non-null and channels > 0. 0, or 1 for an
+ * unknown quant/output dtype. */
+int or_dequantize(const uint8_t *in, uint64_t n, int quant, const float *scales,
+                  const int32_t *zps, uint32_t channels, uint32_t inner, float scale,
+                  int32_t zp, int dtype, void *out);
+/* dequant_activation (kernels.rs:311-388): f32 out[i] = f((q - zp) as f32 *
+ * scale), f = lut_act_ref(act) (acts 0-4; 3 for Erf, not restated). */
+int or_dequant_activation(const uint8_t *in, uint64_t n, int quant, int act, float scale,
+                          int32_t zp, float *out);
 #define OR_I8_DOT_K_MAX 133144   /* i32::MAX / (127 * 127), kernel_call.rs:103 */
 int or_matmul_q_omajor(int tier, const float *a, const uint8_t *bq, const int8_t *codebook,
                        const float *scales, float *out, size_t m, size_t k, size_t n);

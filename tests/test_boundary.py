@@ -49,6 +49,24 @@ def test_host_tables_equal_oracle(act, dtype):
     assert np.array_equal(lut_table(act, dtype), oracle.build_table(act, dtype))
 
 
+@pytest.mark.parametrize("table,fused", [(6, 1), (7, 6), (8, 7)])   # Relu, Elu, Selu
+@pytest.mark.parametrize("dtype", [DTYPE_BF16, DTYPE_F16])
+def test_host_relu_elu_selu_tables_are_widen_f_narrow(table, fused, dtype):
+    """16-bit Relu / Elu / Selu run unary_float (float_kernels.rs:170-233):
+    widen, the scalar f, narrow (bf16 truncation, f16 the reference's rule);
+    a table of that over all 65536 patterns is the same map."""
+    bits = np.arange(65536, dtype=np.uint16)
+    L = oracle.lib()
+    if dtype == DTYPE_BF16:
+        x = (bits.astype(np.uint32) << 16).view(np.float32)
+        want = (oracle.fused_act_f32(fused, x).view(np.uint32) >> 16).astype(np.uint16)
+    else:
+        x = np.array([L.or_f16_to_f32(int(b)) for b in bits], np.float32)
+        y = oracle.fused_act_f32(fused, x)
+        want = np.array([L.or_f32_to_f16(float(v)) for v in y], np.uint16)
+    assert np.array_equal(lut_table(table, dtype), want)
+
+
 def test_erf_table_not_built():
     with pytest.raises(UnsupportedOp):
         lut_table(5, DTYPE_BF16)
@@ -68,8 +86,11 @@ def test_unary_sizes():
         validate(unary(8), [16, 15])        # output short
     with pytest.raises(SlotOutOfRange):
         validate(unary(8), [16])            # output slot unbound
+    validate(unary(8, DTYPE_F32), [32, 32])  # f32: computed, not tabled
+    with pytest.raises(SlotOutOfRange):
+        validate(unary(8, DTYPE_F32), [32, 31])
     with pytest.raises(UnsupportedOp):
-        validate(unary(8, DTYPE_F32), [64, 64])
+        validate(unary(8, 2), [64, 64])     # the integer ring form is not served here
     validate(unary(0), [])                  # empty is a no-op before any lookup
 
 
@@ -193,3 +214,49 @@ def test_codec_truncated_payload():
     wire = KernelCall.Gelu(UnaryCall(BufferRef(0), BufferRef(1), 5)).encode()
     with pytest.raises(DispatchError):
         decode_call(wire[:-1])
+
+
+def test_ctypes_layouts_match_the_header(tmp_path):
+    """Every call struct the ctypes binding declares has the C header's size and
+    field offsets (a drift would hand the library garbage)."""
+    import shutil
+    import subprocess
+    if not shutil.which("gcc"):
+        pytest.skip("no C compiler")
+    pairs = [(name[:-1], cls) for name, cls in vars(_ffi).items()
+             if name.endswith("C") and isinstance(cls, type)
+             and issubclass(cls, ctypes.Structure) and name != "KernelCallC"]
+    cname = {"BufferRef": "holo_buffer_ref", "KernelCall": "holo_kernel_call"}
+
+    def c_name(py):
+        if py in cname:
+            return cname[py]
+        return "holo_" + re.sub(r"(?<!^)(?=[A-Z])", "_", py).lower()
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "holo_hip.h"', 'int main(void){']
+    checks = []
+    for py, cls in pairs + [("KernelCall", _ffi.KernelCallC)]:
+        c = {"MatMulActCall": "holo_matmul_act_call", "MatMulAddCall": "holo_matmul_add_call",
+             "MatMulAddActCall": "holo_matmul_add_act_call", "MatMulCall": "holo_matmul_call",
+             "MatMulDequantCall": "holo_matmul_dequant_call",
+             "DecodeAttentionI8Call": "holo_decode_attention_i8_call",
+             "AttentionI8RowsCall": "holo_attention_i8_rows_call",
+             "ArgMaxCall": "holo_argmax_call", "KvCacheWriteCall": "holo_kv_cache_write_call",
+             "KvQuantAppendCall": "holo_kv_quant_append_call",
+             "DecodeAttentionValidCall": "holo_decode_attention_valid_call",
+             "DequantActivationCall": "holo_dequant_activation_call",
+             "RopeCall": "holo_rope_call"}.get(py) or c_name(py)
+        lines.append(f'printf("%zu\\n", sizeof({c}));')
+        checks.append((py, "sizeof", ctypes.sizeof(cls)))
+        for f, _ in cls._fields_:
+            lines.append(f'printf("%zu\\n", offsetof({c}, {f}));')
+            checks.append((py, f, getattr(cls, f).offset))
+    lines.append("return 0;}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], check=True, capture_output=True,
+                                          text=True).stdout.split()]
+    assert len(got) == len(checks)
+    for (py, what, want), g in zip(checks, got):
+        assert g == want, f"{py}.{what}: C {g}, ctypes {want}"

@@ -103,6 +103,44 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const void *__restrict__ x
     }
 }
 
+// AddRmsNorm: one workgroup per row over v = x + residual, the sum taken in
+// f32 and never narrowed (add_rms_norm_float, float_kernels.rs:1566-1672).
+// The reference's f32 rows with a residual scale in place by (inv * g); every
+// other form writes (v * inv) * g; the sum of squares is in tree order.
+template <bool kBf16>
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(const void *__restrict__ x,
+                                                          const void *__restrict__ res,
+                                                          const void *__restrict__ gamma,
+                                                          void *__restrict__ out, uint32_t feature,
+                                                          float eps) {
+    __shared__ float part[4];
+    const uint64_t row = uint64_t(blockIdx.x) * feature;
+    float ss = 0.0f;
+    for (uint32_t j = threadIdx.x; j < feature; j += 256) {
+        float v = ld<kBf16>(x, row + j);
+        if (res) v = v + ld<kBf16>(res, row + j);
+        ss = fmaf(v, v, ss);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float sumsq = part[0] + part[1] + part[2] + part[3];
+    const float inv = 1.0f / sqrtf(sumsq / float(feature) + eps);
+    for (uint32_t j = threadIdx.x; j < feature; j += 256) {
+        float v = ld<kBf16>(x, row + j);
+        if (res) v = v + ld<kBf16>(res, row + j);
+        float o;
+        if (!kBf16 && res) {
+            o = gamma ? v * (inv * ld<kBf16>(gamma, j)) : v * inv;
+        } else {
+            o = v * inv;
+            if (gamma) o = o * ld<kBf16>(gamma, j);
+        }
+        st<kBf16>(out, row + j, o);
+    }
+}
+
 // RmsNorm for bf16 rows of feature % 8 == 0, feature <= 8 * 256 * 4: one
 // workgroup per row, every 16-byte vector of x and gamma loaded once, up
 // front, and kept in registers through the reduction (rmsnorm_vec_row).
@@ -329,6 +367,19 @@ hipError_t launch_binary(int op, const void *a, const void *b, void *out, uint64
         else
             hipLaunchKernelGGL((binary_kernel<false, kOpMul>), dim3(grid), dim3(256), 0, stream, a, b, out, n, nvec);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_add_rmsnorm(const void *x, const void *residual, const void *gamma, void *out,
+                              uint32_t batch, uint32_t feature, float eps, bool bf16,
+                              hipStream_t stream) {
+    if (batch == 0 || feature == 0) return hipSuccess;
+    if (bf16)
+        hipLaunchKernelGGL((add_rmsnorm_kernel<true>), dim3(batch), dim3(256), 0, stream, x, residual,
+                           gamma, out, feature, eps);
+    else
+        hipLaunchKernelGGL((add_rmsnorm_kernel<false>), dim3(batch), dim3(256), 0, stream, x, residual,
+                           gamma, out, feature, eps);
     return hipGetLastError();
 }
 

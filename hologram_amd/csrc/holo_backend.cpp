@@ -167,6 +167,7 @@ uint32_t fused_of_unary(uint32_t tag) {
         case HOLO_OP_ELU: return 6;
         case HOLO_OP_SELU: return 7;
         case HOLO_OP_EXP: return 8;
+        case HOLO_OP_ERF: return holo::kActErf;
         default: return 0;
     }
 }
@@ -932,8 +933,7 @@ int do_dequant_act(holo_backend *be, const SlotTable &st, const holo_dequant_act
     float probe;
     if (!holo::lut_act_value(c.act, 0.0f, &probe))
         return fail(HOLO_ERR_UNSUPPORTED_OP,
-                    "dequant_activation: activation " + std::to_string(c.act) +
-                        " (Erf: libm erff) has no device table");
+                    "dequant_activation: activation " + std::to_string(c.act) + " has no table");
     if (!be || n == 0) return HOLO_OK;
     const float scale = f32_of_bits(c.scale_bits);
     float table[256] = {};
@@ -1131,6 +1131,48 @@ int do_rmsnorm(holo_backend *be, const SlotTable &st, const holo_norm_call &c) {
                     op);
 }
 
+// add_rms_norm_float (src/cpu/float_kernels.rs:1566-1672): reads x, the
+// residual when present, gamma; channels / groups / beta are not used.
+int do_add_rmsnorm(holo_backend *be, const SlotTable &st, const holo_norm_call &c) {
+    const char *op = "add_rms_norm";
+    if (c.batch == 0 || c.feature == 0) return HOLO_OK;
+    if (c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F32)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "add_rms_norm: the device path serves bf16 and f32");
+    float eps = 1e-9f;
+    if (c.epsilon_bits != 0) {
+        const uint32_t eb = uint32_t(c.epsilon_bits);
+        memcpy(&eps, &eb, 4);
+        if (!(std::isfinite(eps) && eps > 0.0f))
+            return fail(HOLO_ERR_UNSUPPORTED_OP,
+                        "norm epsilon must be a positive finite f32 (0 selects the default)");
+    }
+    const uint64_t es = dtype_size(c.dtype), total = uint64_t(c.batch) * c.feature * es;
+    const bool has_r = c.residual.slot != HOLO_SLOT_ABSENT, has_g = c.gamma.slot != HOLO_SLOT_ABSENT;
+    holo_buffer_ref reads[3];
+    int nr = 0;
+    reads[nr++] = c.x;
+    if (has_r) reads[nr++] = c.residual;
+    const int gi = nr;
+    if (has_g) reads[nr++] = c.gamma;
+    View rv[3], out;
+    HOLO_TRY(split_borrow(st, reads, rv, nr, c.output, &out, op));
+    HOLO_TRY(need(rv[0], total, c.x.slot, op, "x"));
+    if (has_r) HOLO_TRY(need(rv[1], total, c.residual.slot, op, "residual"));
+    HOLO_TRY(need(out, total, c.output.slot, op, "output"));
+    // affine_operand (float_kernels.rs:39-44): an empty gamma is the identity
+    const bool use_g = has_g && rv[gi].bytes > 0;
+    if (use_g) HOLO_TRY(need(rv[gi], uint64_t(c.feature) * es, c.gamma.slot, op, "gamma"));
+    if (!aligned(rv[0], es) || !aligned(out, es) || (has_r && !aligned(rv[1], es)) ||
+        (use_g && !aligned(rv[gi], es)))
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "add_rms_norm: operands must be element-aligned");
+    if (c.batch > 0x7fffffffu) return fail(HOLO_ERR_UNSUPPORTED_OP, "add_rms_norm: batch too large");
+    if (!be) return HOLO_OK;
+    return launched(holo::launch_add_rmsnorm(rv[0].base, has_r ? rv[1].base : nullptr,
+                                             use_g ? rv[gi].base : nullptr, out.base, c.batch,
+                                             c.feature, eps, c.dtype == HOLO_DTYPE_BF16, be->stream),
+                    op);
+}
+
 // -------------------------------------------------------------- RoPE -----
 // rope_float (src/cpu/float_kernels.rs:3123-3186).
 int do_rope(holo_backend *be, const SlotTable &st, const holo_rope_call &c) {
@@ -1253,13 +1295,15 @@ int dispatch_impl(holo_backend *be, const SlotTable &st, const holo_kernel_call 
         case HOLO_OP_EXP:
         case HOLO_OP_RELU:
         case HOLO_OP_ELU:
-        case HOLO_OP_SELU: return do_unary(be, st, call->tag, call->u.unary);
+        case HOLO_OP_SELU:
+        case HOLO_OP_ERF: return do_unary(be, st, call->tag, call->u.unary);
         case HOLO_OP_DEQUANTIZE: return do_dequantize(be, st, call->u.dequantize);
         case HOLO_OP_DEQUANT_ACT: return do_dequant_act(be, st, call->u.dequant_act);
         case HOLO_OP_MATMUL_DEQUANT: return do_matmul_dequant(be, st, call->u.matmul_dequant);
         case HOLO_OP_ADD:
         case HOLO_OP_MUL: return do_binary(be, st, call->tag, call->u.binary);
         case HOLO_OP_RMS_NORM: return do_rmsnorm(be, st, call->u.norm);
+        case HOLO_OP_ADD_RMS_NORM: return do_add_rmsnorm(be, st, call->u.norm);
         case HOLO_OP_ROTARY: return do_rope(be, st, call->u.rope);
         case HOLO_OP_GATHER: return do_gather(be, st, call->u.gather);
         case HOLO_OP_ARGMAX: return do_argmax(be, st, call->u.argmax);
@@ -1327,7 +1371,8 @@ int decode_impl(const uint8_t *wire, size_t len, holo_kernel_call *out, size_t *
         case HOLO_OP_EXP:
         case HOLO_OP_RELU:
         case HOLO_OP_ELU:
-        case HOLO_OP_SELU: {  // put_unary :575-581
+        case HOLO_OP_SELU:
+        case HOLO_OP_ERF: {  // put_unary :575-581
             auto &c = out->u.unary;
             c.input = r.buf();
             c.output = r.buf();
@@ -1412,7 +1457,8 @@ int decode_impl(const uint8_t *wire, size_t len, holo_kernel_call *out, size_t *
             c.dtype = r.get<uint8_t>();
             break;
         }
-        case HOLO_OP_RMS_NORM: {  // put_norm :656-668
+        case HOLO_OP_RMS_NORM:
+        case HOLO_OP_ADD_RMS_NORM: {  // put_norm :656-668
             auto &c = out->u.norm;
             c.x = r.buf();
             c.gamma = r.buf();
@@ -1618,6 +1664,7 @@ int lut_act_of_fused(uint32_t act) {
         case kFusedRelu: return kTableRelu;
         case kFusedElu: return kTableElu;
         case kFusedSelu: return kTableSelu;
+        case kActErf: return HOLO_ACT_ERF;
         default: return -1;
     }
 }

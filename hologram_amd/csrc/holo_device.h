@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "holo_kernels.h"
+
 namespace holo {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -133,6 +135,72 @@ __device__ inline float libm_expf_dev(float x) {
     return k == 0 ? y : scale_by_pow2_dev(y, k);
 }
 
+// libm 0.2.16 erff (lut_act::ERF, float_kernels.rs:3534-3536; musl erff.c from
+// FreeBSD s_erff.c): the published fdlibm coefficients, nested as written.
+__device__ inline float erf_poly(const float *c, int n, float t) {
+    float v = c[n - 1];
+    for (int i = n - 2; i >= 0; --i) v = c[i] + t * v;
+    return v;
+}
+
+__device__ inline float libm_erff_dev(float x) {
+    constexpr float erx = 8.4506291151e-01f, efx8 = 1.0270333290e+00f;
+    const float pp[5] = {1.2837916613e-01f, -3.2504209876e-01f, -2.8481749818e-02f,
+                         -5.7702702470e-03f, -2.3763017452e-05f};
+    const float qq[5] = {3.9791721106e-01f, 6.5022252500e-02f, 5.0813062117e-03f,
+                         1.3249473704e-04f, -3.9602282413e-06f};
+    uint32_t ix = __float_as_uint(x);
+    const bool neg = (ix >> 31) != 0;
+    ix &= 0x7fffffffu;
+    if (ix >= 0x7f800000u) return 1.0f - 2.0f * (neg ? 1.0f : 0.0f) + 1.0f / x;
+    if (ix < 0x3f580000u) {                       // |x| < 0.84375
+        if (ix < 0x31800000u) return 0.125f * (8.0f * x + efx8 * x);
+        const float z = x * x;
+        const float y = erf_poly(pp, 5, z) / (1.0f + z * erf_poly(qq, 5, z));
+        return x + x * y;
+    }
+    if (ix >= 0x40c00000u) {                      // |x| >= 6: 1 - 2^-120
+        const float y = 1.0f - __uint_as_float(0x03800000u);
+        return neg ? -y : y;
+    }
+    float erfc;
+    if (ix < 0x3fa00000u) {                       // |x| < 1.25
+        const float pa[7] = {-2.3621185683e-03f, 4.1485610604e-01f, -3.7220788002e-01f,
+                             3.1834661961e-01f, -1.1089469492e-01f, 3.5478305072e-02f,
+                             -2.1663755178e-03f};
+        const float qa[6] = {1.0642088205e-01f, 5.4039794207e-01f, 7.1828655899e-02f,
+                             1.2617121637e-01f, 1.3637083583e-02f, 1.1984500103e-02f};
+        const float s = fabsf(x) - 1.0f;
+        erfc = 1.0f - erx - erf_poly(pa, 7, s) / (1.0f + s * erf_poly(qa, 6, s));
+    } else {
+        const float ax = fabsf(x), s = 1.0f / (ax * ax);
+        float r, big_s;
+        if (ix < 0x4036db6du) {                   // |x| < 1/0.35
+            const float ra[8] = {-9.8649440333e-03f, -6.9385856390e-01f, -1.0558626175e+01f,
+                                 -6.2375331879e+01f, -1.6239666748e+02f, -1.8460508728e+02f,
+                                 -8.1287437439e+01f, -9.8143291473e+00f};
+            const float sa[8] = {1.9651271820e+01f, 1.3765776062e+02f, 4.3456588745e+02f,
+                                 6.4538726807e+02f, 4.2900814819e+02f, 1.0863500214e+02f,
+                                 6.5702495575e+00f, -6.0424413532e-02f};
+            r = erf_poly(ra, 8, s);
+            big_s = 1.0f + s * erf_poly(sa, 8, s);
+        } else {
+            const float rb[7] = {-9.8649431020e-03f, -7.9928326607e-01f, -1.7757955551e+01f,
+                                 -1.6063638306e+02f, -6.3756646729e+02f, -1.0250950928e+03f,
+                                 -4.8351919556e+02f};
+            const float sb[7] = {3.0338060379e+01f, 3.2579251099e+02f, 1.5367296143e+03f,
+                                 3.1998581543e+03f, 2.5530502930e+03f, 4.7452853394e+02f,
+                                 -2.2440952301e+01f};
+            r = erf_poly(rb, 7, s);
+            big_s = 1.0f + s * erf_poly(sb, 7, s);
+        }
+        const float z = __uint_as_float(__float_as_uint(ax) & 0xffffe000u);
+        erfc = libm_expf_dev(-z * z - 0.5625f) * libm_expf_dev((z - ax) * (z + ax) + r / big_s) / ax;
+    }
+    const float y = 1.0f - erfc;
+    return neg ? -y : y;
+}
+
 // f32 activations of the fused MatMul epilogues, by fused_activation id
 // (kernel_call.rs:861-870, fused_act_fn float_kernels.rs:768-780): relu_f
 // (:3448), gelu_f, silu_f, sigmoid_f, tanh_f (:3549-3566), elu_f and selu_f
@@ -146,6 +214,7 @@ __device__ inline float act_f32(uint32_t act, float x) {
             return x >= 0.0f ? scale * x : scale * alpha * (libm_expf_dev(x) - 1.0f);
         }
         case 8: return libm_expf_dev(x);                     // EXP
+        case kActErf: return libm_erff_dev(x);               // the Erf unary (f32)
         case 2: {   // GELU
             const float cube = ((0.044715f * x) * x) * x;
             const float u = 0.7978846f * (x + cube);

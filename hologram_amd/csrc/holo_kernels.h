@@ -120,6 +120,10 @@ hipError_t launch_binary(int op, const void *a, const void *b, void *out, uint64
 hipError_t launch_act_f32(const float *in, float *out, uint64_t n, uint32_t act,
                           hipStream_t stream);
 // gamma == nullptr: no affine scale.
+// AddRmsNorm: rows of x + residual (residual may be null), in f32.
+hipError_t launch_add_rmsnorm(const void *x, const void *residual, const void *gamma, void *out,
+                              uint32_t batch, uint32_t feature, float eps, bool bf16,
+                              hipStream_t stream);
 hipError_t launch_rmsnorm(const void *x, const void *gamma, void *out, uint32_t batch,
                           uint32_t feature, float eps, bool bf16, hipStream_t stream);
 hipError_t launch_rope(const void *x, const void *cs, const void *sn, void *out, uint32_t head_dim,
@@ -188,6 +192,9 @@ constexpr uint8_t kEpiStore = 0, kEpiAct = 1, kEpiAdd = 2, kEpiAddAct = 3;
 // fused_activation ids (crates/hologram-compute/src/kernel_call.rs:861-870)
 constexpr uint32_t kFusedRelu = 1, kFusedGelu = 2, kFusedSilu = 3, kFusedSigmoid = 4,
                    kFusedTanh = 5, kFusedElu = 6, kFusedSelu = 7, kFusedExp = 8;
+// The f32 Erf unary's id in act_f32 (Erf has no fused_activation id, so no
+// fusion produces it).
+constexpr uint32_t kActErf = 9;
 // Table ids of the 16-bit fused Relu/Elu/Selu (beyond lut_act's 0-5).
 constexpr int kTableRelu = 6, kTableElu = 7, kTableSelu = 8;
 struct EpiSeg {

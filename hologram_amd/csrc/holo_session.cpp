@@ -122,7 +122,7 @@ void call_operands(const holo_kernel_call &c, std::vector<holo_buffer_ref> *read
     auto w = [&](const holo_buffer_ref &b) { writes->push_back(b); };
     switch (c.tag) {
         case HOLO_OP_SIGMOID: case HOLO_OP_TANH: case HOLO_OP_GELU: case HOLO_OP_SILU:
-        case HOLO_OP_EXP: case HOLO_OP_RELU: case HOLO_OP_ELU: case HOLO_OP_SELU:
+        case HOLO_OP_EXP: case HOLO_OP_RELU: case HOLO_OP_ELU: case HOLO_OP_SELU: case HOLO_OP_ERF:
             r(c.u.unary.input); w(c.u.unary.output); break;
         case HOLO_OP_DEQUANTIZE: {   // buffers(), kernel_call.rs:1656-1657
             const auto &d = c.u.dequantize;
@@ -141,7 +141,7 @@ void call_operands(const holo_kernel_call &c, std::vector<holo_buffer_ref> *read
         }
         case HOLO_OP_ADD: case HOLO_OP_MUL:
             r(c.u.binary.a); r(c.u.binary.b); w(c.u.binary.output); break;
-        case HOLO_OP_RMS_NORM:
+        case HOLO_OP_RMS_NORM: case HOLO_OP_ADD_RMS_NORM:
             r(c.u.norm.x); r(c.u.norm.gamma); r(c.u.norm.beta); r(c.u.norm.residual);
             w(c.u.norm.output); break;
         case HOLO_OP_ROTARY:

@@ -94,6 +94,78 @@ float libm_expf(float x) {
     return k == 0 ? y : scale_by_pow2(y, k);
 }
 
+// libm 0.2.16 erff (the lut_act::ERF entry, float_kernels.rs:3534-3536): musl's
+// erff.c, from FreeBSD's s_erff.c (fdlibm's rational approximations of erf in
+// float). Polynomials nest innermost-first as the source writes them.
+struct ErfCoeffs {
+    static constexpr float erx = 8.4506291151e-01f, efx8 = 1.0270333290e+00f;
+    static constexpr float pp[5] = {1.2837916613e-01f, -3.2504209876e-01f, -2.8481749818e-02f,
+                                    -5.7702702470e-03f, -2.3763017452e-05f};
+    static constexpr float qq[5] = {3.9791721106e-01f, 6.5022252500e-02f, 5.0813062117e-03f,
+                                    1.3249473704e-04f, -3.9602282413e-06f};
+    static constexpr float pa[7] = {-2.3621185683e-03f, 4.1485610604e-01f, -3.7220788002e-01f,
+                                    3.1834661961e-01f, -1.1089469492e-01f, 3.5478305072e-02f,
+                                    -2.1663755178e-03f};
+    static constexpr float qa[6] = {1.0642088205e-01f, 5.4039794207e-01f, 7.1828655899e-02f,
+                                    1.2617121637e-01f, 1.3637083583e-02f, 1.1984500103e-02f};
+    static constexpr float ra[8] = {-9.8649440333e-03f, -6.9385856390e-01f, -1.0558626175e+01f,
+                                    -6.2375331879e+01f, -1.6239666748e+02f, -1.8460508728e+02f,
+                                    -8.1287437439e+01f, -9.8143291473e+00f};
+    static constexpr float sa[8] = {1.9651271820e+01f, 1.3765776062e+02f, 4.3456588745e+02f,
+                                    6.4538726807e+02f, 4.2900814819e+02f, 1.0863500214e+02f,
+                                    6.5702495575e+00f, -6.0424413532e-02f};
+    static constexpr float rb[7] = {-9.8649431020e-03f, -7.9928326607e-01f, -1.7757955551e+01f,
+                                    -1.6063638306e+02f, -6.3756646729e+02f, -1.0250950928e+03f,
+                                    -4.8351919556e+02f};
+    static constexpr float sb[7] = {3.0338060379e+01f, 3.2579251099e+02f, 1.5367296143e+03f,
+                                    3.1998581543e+03f, 2.5530502930e+03f, 4.7452853394e+02f,
+                                    -2.2440952301e+01f};
+};
+
+template <int N>
+float poly(const float (&c)[N], float t) {
+    float v = c[N - 1];
+    for (int i = N - 2; i >= 0; --i) v = c[i] + t * v;
+    return v;
+}
+
+float libm_erff(float x) {
+    using C = ErfCoeffs;
+    uint32_t ix = bits_of(x);
+    const bool neg = (ix >> 31) != 0;
+    ix &= 0x7fffffffu;
+    if (ix >= 0x7f800000u) return 1.0f - 2.0f * (neg ? 1.0f : 0.0f) + 1.0f / x;
+    if (ix < 0x3f580000u) {                       // |x| < 0.84375
+        if (ix < 0x31800000u) return 0.125f * (8.0f * x + C::efx8 * x);
+        const float z = x * x;
+        const float y = poly(C::pp, z) / (1.0f + z * poly(C::qq, z));
+        return x + x * y;
+    }
+    float erfc;
+    if (ix >= 0x40c00000u) {                      // |x| >= 6
+        const float y = 1.0f - float_of(0x03800000u);
+        return neg ? -y : y;
+    }
+    if (ix < 0x3fa00000u) {                       // |x| < 1.25
+        const float s = std::fabs(x) - 1.0f;
+        erfc = 1.0f - C::erx - poly(C::pa, s) / (1.0f + s * poly(C::qa, s));
+    } else {
+        const float ax = std::fabs(x), s = 1.0f / (ax * ax);
+        float r, big_s;
+        if (ix < 0x4036db6du) {                   // |x| < 1/0.35
+            r = poly(C::ra, s);
+            big_s = 1.0f + s * poly(C::sa, s);
+        } else {
+            r = poly(C::rb, s);
+            big_s = 1.0f + s * poly(C::sb, s);
+        }
+        const float z = float_of(bits_of(ax) & 0xffffe000u);
+        erfc = libm_expf(-z * z - 0.5625f) * libm_expf((z - ax) * (z + ax) + r / big_s) / ax;
+    }
+    const float y = 1.0f - erfc;
+    return neg ? -y : y;
+}
+
 float act_sigmoid(float x) { return 1.0f / (1.0f + det_exp(-x)); }
 float act_tanh(float x) {
     const float e = det_exp(2.0f * x);
@@ -152,7 +224,7 @@ uint16_t float_to_half(float f) {
 
 }  // namespace
 
-// Returns false for an activation id this build has no table for. Ids 0-4
+// Returns false for an activation id this build has no table for. Ids 0-5
 // are lut_act's (kernel_call.rs:877-885); 6-8 are this backend's tables for
 // the fused epilogues' Relu, Elu and Selu on 16-bit products (the reference
 // computes narrow(f(widen(x))) per element, which is the table entry).
@@ -164,6 +236,7 @@ bool build_lut_table(int act, bool f16, uint16_t *t) {
         case 2: fn = act_gelu; break;
         case 3: fn = act_silu; break;
         case 4: fn = libm_expf; break;
+        case 5: fn = libm_erff; break;
         case 6: fn = act_relu; break;
         case 7: fn = act_elu; break;
         case 8: fn = act_selu; break;
@@ -178,7 +251,7 @@ bool build_lut_table(int act, bool f16, uint16_t *t) {
 }
 
 // f(x) for lut_act id `act` (lut_act_ref, src/cpu/float_kernels.rs:3628-3638):
-// the DequantActivation table's entries. False for an id with no restatement.
+// the DequantActivation table's entries; Erf for 5 and any id past it.
 bool lut_act_value(int act, float x, float *y) {
     switch (act) {
         case 0: *y = act_sigmoid(x); return true;
@@ -186,7 +259,10 @@ bool lut_act_value(int act, float x, float *y) {
         case 2: *y = act_gelu(x); return true;
         case 3: *y = act_silu(x); return true;
         case 4: *y = libm_expf(x); return true;
-        default: return false;
+        default:
+            if (act < 0) return false;
+            *y = libm_erff(x);
+            return true;
     }
 }
 

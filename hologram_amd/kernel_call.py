@@ -60,6 +60,7 @@ D_MMA = 106     # MatMulActivation (the loader's epilogue fusion)
 D_MMADD = 107   # MatMulAdd
 D_MMAA = 108    # MatMulAddActivation
 D_RN = 51
+D_ADDRMS = 54   # AddRmsNorm: rms_norm(x + residual)
 D_ROTARY = 75
 D_GATHER = 114
 D_KVWR = 120
@@ -495,7 +496,7 @@ class TransposeCall:
                 + struct.pack("<B", self.dtype))
 
 
-_NAMES = {D_ADD: "Add", D_MUL: "Mul", D_RN: "RmsNorm", D_ROTARY: "RotaryEmbedding",
+_NAMES = {D_ADD: "Add", D_MUL: "Mul", D_RN: "RmsNorm", D_ADDRMS: "AddRmsNorm", D_ROTARY: "RotaryEmbedding",
           D_RELU: "Relu", D_ELU: "Elu", D_SELU: "Selu", D_ERF: "Erf", D_DEQ: "Dequantize",
           D_MMDQ: "MatMulDequant", D_DQACT: "DequantActivation",
           D_GATHER: "Gather", D_ARGMAX: "ArgMax", D_SIGMOID: "Sigmoid", D_TANH: "Tanh", D_GELU: "Gelu", D_SILU: "Silu", D_EXP: "Exp",
@@ -586,6 +587,10 @@ class KernelCall:
     @classmethod
     def RmsNorm(cls, c: NormCall) -> "KernelCall":  # noqa: N802
         return cls(D_RN, c)
+
+    @classmethod
+    def AddRmsNorm(cls, c: NormCall) -> "KernelCall":  # noqa: N802
+        return cls(D_ADDRMS, c)
 
     @classmethod
     def RotaryEmbedding(cls, c: RoPECall) -> "KernelCall":  # noqa: N802

@@ -52,6 +52,7 @@ typedef enum holo_status {
 #define HOLO_ACT_GELU 2
 #define HOLO_ACT_SILU 3
 #define HOLO_ACT_EXP 4
+#define HOLO_ACT_ERF 5
 
 /* fused_activation ids of the fused MatMul epilogues,
  * crates/hologram-compute/src/kernel_call.rs:861-870 */
@@ -77,7 +78,7 @@ typedef enum holo_status {
 #define HOLO_OP_ELU 16u
 #define HOLO_OP_SELU 17u
 #define HOLO_OP_EXP 18u
-#define HOLO_OP_ERF 32u                   /* Erf: decoded, not served (no libm erff restatement) */
+#define HOLO_OP_ERF 32u                   /* Erf: libm erff (bf16/f16 table, f32 computed) */
 #define HOLO_OP_DEQUANTIZE 105u           /* Dequantize (wire 105; 118 carries the extended fields) */
 #define HOLO_OP_MATMUL_DEQUANT 111u       /* MatMulDequant (wire 111; 116 / 117 the extended forms) */
 #define HOLO_OP_DEQUANT_ACT 113u          /* DequantActivation */
@@ -86,6 +87,7 @@ typedef enum holo_status {
 #define HOLO_OP_MATMUL_ADD 107u           /* MatMulAdd (kernel_codec.rs:103)           */
 #define HOLO_OP_MATMUL_ADD_ACT 108u       /* MatMulAddActivation (kernel_codec.rs:104) */
 #define HOLO_OP_RMS_NORM 51u
+#define HOLO_OP_ADD_RMS_NORM 54u          /* AddRmsNorm: rms_norm(x + residual) */
 #define HOLO_OP_ROTARY 75u
 #define HOLO_OP_GATHER 114u
 #define HOLO_OP_KV_CACHE_WRITE 120u
@@ -135,7 +137,10 @@ typedef struct holo_binary_call {
  * 1683-1755): per row of `feature` values, out = x * (1 / sqrtf(mean(x^2) +
  * eps)) * gamma (gamma absent: 1). eps = f32(epsilon_bits), 0 selects 1e-9
  * (float_kernels.rs:1324-1336). beta and residual must be absent; channels and
- * num_groups must be 0. dtype bf16 or f32. */
+ * num_groups must be 0. dtype bf16 or f32.
+ * As AddRmsNorm (tag 54, add_rms_norm_float, float_kernels.rs:1566-1672): the
+ * rows are v = x + residual (residual optional), summed in f32 and never
+ * narrowed; beta, channels and num_groups are ignored. */
 typedef struct holo_norm_call {
     holo_buffer_ref x;
     holo_buffer_ref gamma;

@@ -16,7 +16,7 @@ HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libholo_oracle.so"
 
 DTYPE_I8, DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 2, 6, 7, 8
-ACT_SIGMOID, ACT_TANH, ACT_GELU, ACT_SILU, ACT_EXP = 0, 1, 2, 3, 4
+ACT_SIGMOID, ACT_TANH, ACT_GELU, ACT_SILU, ACT_EXP, ACT_ERF = 0, 1, 2, 3, 4, 5
 
 _P = ctypes.c_void_p
 _S = ctypes.c_size_t
@@ -29,6 +29,7 @@ _SIGS = {
     "or_f32_to_f16": (ctypes.c_uint16, [_F]),
     "or_exp_f32_det": (_F, [_F]),
     "or_libm_expf": (_F, [_F]),
+    "or_libm_erff": (_F, [_F]),
     "or_sigmoid_f": (_F, [_F]),
     "or_tanh_f": (_F, [_F]),
     "or_gelu_f": (_F, [_F]),
@@ -58,6 +59,7 @@ _SIGS = {
                                       _F]),
     "or_binary": (None, [ctypes.c_int, _P, _P, _P, _S, ctypes.c_int]),
     "or_rms_norm": (ctypes.c_int, [_P, _P, _P, _U32, _U32, ctypes.c_uint64, ctypes.c_int]),
+    "or_add_rms_norm": (ctypes.c_int, [_P, _P, _P, _P, _U32, _U32, ctypes.c_uint64, ctypes.c_int]),
     "or_rope": (ctypes.c_int, [_P, _P, _P, _P, _U32, _S, ctypes.c_int]),
     "or_gather": (ctypes.c_int, [_P, _P, _P, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64,
                                  ctypes.c_uint64, ctypes.c_int]),

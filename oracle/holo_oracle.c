@@ -233,6 +233,89 @@ int or_fused_act_f32(int act, const float *in, float *out, size_t n)
     return 0;
 }
 
+/* libm 0.2.16 erff (the lut_act::ERF entry, float_kernels.rs:3534-3536): the
+ * crate ports musl's src/math/erff.c, itself FreeBSD's s_erff.c (fdlibm's
+ * erf rational approximations in float). Four ranges of |x|: [0, 0.84375)
+ * x + x*P(x^2)/Q(x^2); [0.84375, 1.25) 1 - ((1 - erx) - P(s)/Q(s)) with
+ * s = |x| - 1; [1.25, 6) 1 - exp(-z^2 - 0.5625) exp((z - x)(z + x) + R/S) / x
+ * with z = x truncated to 11 mantissa bits and R/S in 1/x^2; beyond, 1 - 2^-120.
+ * The coefficients are the published ones (each also given as its bits). */
+static const float ERF_ERX = 8.4506291151e-01f;   /* 0x3f58560b */
+static const float ERF_EFX8 = 1.0270333290e+00f;  /* 0x3f8375d4 */
+static const float ERF_PP[5] = {1.2837916613e-01f, -3.2504209876e-01f, -2.8481749818e-02f,
+                                -5.7702702470e-03f, -2.3763017452e-05f};
+static const float ERF_QQ[5] = {3.9791721106e-01f, 6.5022252500e-02f, 5.0813062117e-03f,
+                                1.3249473704e-04f, -3.9602282413e-06f};
+static const float ERF_PA[7] = {-2.3621185683e-03f, 4.1485610604e-01f, -3.7220788002e-01f,
+                                3.1834661961e-01f, -1.1089469492e-01f, 3.5478305072e-02f,
+                                -2.1663755178e-03f};
+static const float ERF_QA[6] = {1.0642088205e-01f, 5.4039794207e-01f, 7.1828655899e-02f,
+                                1.2617121637e-01f, 1.3637083583e-02f, 1.1984500103e-02f};
+static const float ERF_RA[8] = {-9.8649440333e-03f, -6.9385856390e-01f, -1.0558626175e+01f,
+                                -6.2375331879e+01f, -1.6239666748e+02f, -1.8460508728e+02f,
+                                -8.1287437439e+01f, -9.8143291473e+00f};
+static const float ERF_SA[8] = {1.9651271820e+01f, 1.3765776062e+02f, 4.3456588745e+02f,
+                                6.4538726807e+02f, 4.2900814819e+02f, 1.0863500214e+02f,
+                                6.5702495575e+00f, -6.0424413532e-02f};
+static const float ERF_RB[7] = {-9.8649431020e-03f, -7.9928326607e-01f, -1.7757955551e+01f,
+                                -1.6063638306e+02f, -6.3756646729e+02f, -1.0250950928e+03f,
+                                -4.8351919556e+02f};
+static const float ERF_SB[7] = {3.0338060379e+01f, 3.2579251099e+02f, 1.5367296143e+03f,
+                                3.1998581543e+03f, 2.5530502930e+03f, 4.7452853394e+02f,
+                                -2.2440952301e+01f};
+
+/* c[0] + t*(c[1] + t*(... + t*c[n-1])), innermost first, as the source nests it */
+static float horner(const float *c, int n, float t)
+{
+    float v = c[n - 1];
+    for (int i = n - 2; i >= 0; --i) v = c[i] + t * v;
+    return v;
+}
+
+/* 1 + t*(c[0] + t*(c[1] + ...)) */
+static float horner1(const float *c, int n, float t) { return 1.0f + t * horner(c, n, t); }
+
+static float erfc_mid(float x)          /* |x| in [0.84375, 1.25) */
+{
+    float s = fabsf(x) - 1.0f;
+    float p = horner(ERF_PA, 7, s);
+    float q = horner1(ERF_QA, 6, s);
+    return 1.0f - ERF_ERX - p / q;
+}
+
+static float erfc_tail(uint32_t ix, float x)   /* |x| in [0.84375, 6) */
+{
+    if (ix < 0x3fa00000u) return erfc_mid(x);
+    x = fabsf(x);
+    float s = 1.0f / (x * x);
+    float r, big_s;
+    if (ix < 0x4036db6du) {             /* |x| < 1/0.35 */
+        r = horner(ERF_RA, 8, s);
+        big_s = horner1(ERF_SA, 8, s);
+    } else {
+        r = horner(ERF_RB, 7, s);
+        big_s = horner1(ERF_SB, 7, s);
+    }
+    float z = u2f(f2u(x) & 0xffffe000u);
+    return or_libm_expf(-z * z - 0.5625f) * or_libm_expf((z - x) * (z + x) + r / big_s) / x;
+}
+
+float or_libm_erff(float x)
+{
+    uint32_t ix = f2u(x);
+    int sign = (int)(ix >> 31);
+    ix &= 0x7fffffffu;
+    if (ix >= 0x7f800000u) return 1.0f - 2.0f * (float)sign + 1.0f / x;   /* NaN, +-Inf */
+    if (ix < 0x3f580000u) {             /* |x| < 0.84375 */
+        if (ix < 0x31800000u) return 0.125f * (8.0f * x + ERF_EFX8 * x);  /* |x| < 2^-28 */
+        float z = x * x;
+        float y = horner(ERF_PP, 5, z) / horner1(ERF_QQ, 5, z);
+        return x + x * y;
+    }
+    float y = ix < 0x40c00000u ? 1.0f - erfc_tail(ix, x) : 1.0f - u2f(0x03800000u);
+    return sign ? -y : y;
+}
+
 float or_lut_act_ref(int act, float x)
 {
     switch (act) {
@@ -241,7 +324,7 @@ float or_lut_act_ref(int act, float x)
     case OR_ACT_GELU: return or_gelu_f(x);
     case OR_ACT_SILU: return or_silu_f(x);
     case OR_ACT_EXP: return or_libm_expf(x);
-    default: return NAN;
+    default: return or_libm_erff(x);          /* lut_act::ERF and any other id */
     }
 }
 
@@ -250,7 +333,7 @@ float or_lut_act_ref(int act, float x)
 /* ------------------------------------------------------------------------ */
 int or_build_table(int act, int dtype, uint16_t *t)
 {
-    if (act < 0 || act > OR_ACT_EXP) return -1;
+    if (act < 0 || act > OR_ACT_ERF) return -1;
     if (dtype != OR_DTYPE_BF16 && dtype != OR_DTYPE_F16) return -1;
     for (uint32_t bits = 0; bits < 65536u; ++bits) {
         float x = dtype == OR_DTYPE_F16 ? or_f16_to_f32((uint16_t)bits)
@@ -384,7 +467,6 @@ int or_dequant_activation(const uint8_t *in, uint64_t n, int quant, int act, flo
                           int32_t zp, float *out)
 {
     if (quant != OR_DTYPE_I8 && quant != OR_DTYPE_U8 && quant != OR_DTYPE_I4) return 1;
-    if (act < OR_ACT_SIGMOID || act > OR_ACT_EXP) return 3;   /* Erf: not restated */
     float table[256];
     int levels = quant == OR_DTYPE_I4 ? 16 : 256;
     for (int raw = 0; raw < levels; ++raw) {
@@ -682,6 +764,39 @@ int or_rms_norm(const void *x, const void *gamma, void *out, uint32_t batch, uin
         for (uint32_t j = 0; j < feature; ++j) {
             const float g = gamma ? rd(gamma, j, dtype) : 1.0f;
             wr(out, row + j, rd(x, row + j, dtype) * inv_rms * g, dtype);
+        }
+    }
+    return 0;
+}
+
+/* add_rms_norm_float, src/cpu/float_kernels.rs:1566-1672: v = x + residual in
+ * f32 (never narrowed), sequential f32 sum of squares; the f32 rows with a
+ * residual scale in place by (inv * g) (:1625-1634), every other form writes
+ * (v * inv) * g (:1636-1650, 1656-1671). residual may be NULL. */
+int or_add_rms_norm(const void *x, const void *res, const void *gamma, void *out, uint32_t batch,
+                    uint32_t feature, uint64_t epsilon_bits, int dtype)
+{
+    float eps = 1e-9f;
+    if (epsilon_bits != 0) {
+        eps = u2f((uint32_t)epsilon_bits);
+        if (!(isfinite(eps) && eps > 0.0f)) return -1;
+    }
+    for (uint32_t bi = 0; bi < batch; ++bi) {
+        const size_t row = (size_t)bi * feature;
+        float sumsq = 0.0f;
+        for (uint32_t j = 0; j < feature; ++j) {
+            const float v = rd(x, row + j, dtype) + (res ? rd(res, row + j, dtype) : 0.0f);
+            sumsq += v * v;
+        }
+        const float inv = 1.0f / sqrtf(sumsq / (float)feature + eps);
+        for (uint32_t j = 0; j < feature; ++j) {
+            const float v = rd(x, row + j, dtype) + (res ? rd(res, row + j, dtype) : 0.0f);
+            float o;
+            if (dtype == OR_DTYPE_F32 && res)
+                o = gamma ? v * (inv * rd(gamma, j, dtype)) : v * inv;
+            else
+                o = v * inv * (gamma ? rd(gamma, j, dtype) : 1.0f);
+            wr(out, row + j, o, dtype);
         }
     }
     return 0;

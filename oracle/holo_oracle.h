@@ -44,7 +44,8 @@ extern "C" {
 /* dtype tags: crates/hologram-types/src/dtype_id.rs:52-61 */
 enum { OR_DTYPE_I8 = 2, OR_DTYPE_F16 = 6, OR_DTYPE_BF16 = 7, OR_DTYPE_F32 = 8 };
 /* lut_act ids: crates/hologram-compute/src/kernel_call.rs:877-885 */
-enum { OR_ACT_SIGMOID = 0, OR_ACT_TANH = 1, OR_ACT_GELU = 2, OR_ACT_SILU = 3, OR_ACT_EXP = 4 };
+enum { OR_ACT_SIGMOID = 0, OR_ACT_TANH = 1, OR_ACT_GELU = 2, OR_ACT_SILU = 3, OR_ACT_EXP = 4,
+       OR_ACT_ERF = 5 };
 
 /* ---- codecs: src/cpu/dtype.rs:69-153 ---- */
 float    or_bf16_to_f32(uint16_t b);
@@ -60,7 +61,8 @@ float or_tanh_f(float x);                  /* :3553-3558 */
 float or_gelu_f(float x);                  /* :3560-3562 */
 float or_silu_f(float x);                  /* :3564-3566 */
 int or_fused_act_f32(int act, const float *in, float *out, size_t n); /* fused_act_fn :768-780 */
-float or_lut_act_ref(int act, float x);    /* :3628-3638 (Erf not restated) */
+float or_libm_erff(float x);               /* libm 0.2.16 erff (musl erff.c, FreeBSD s_erff.c) */
+float or_lut_act_ref(int act, float x);    /* :3628-3638 */
 
 /* ---- LUT: src/cpu/lut.rs:43-67 (build) and :76-98 (gather) ---- */
 int  or_build_table(int act, int dtype, uint16_t *table /* [65536] */);
@@ -85,7 +87,7 @@ int or_dequantize(const uint8_t *in, uint64_t n, int quant, const float *scales,
                   const int32_t *zps, uint32_t channels, uint32_t inner, float scale,
                   int32_t zp, int dtype, void *out);
 /* dequant_activation (kernels.rs:311-388): f32 out[i] = f((q - zp) as f32 *
- * scale), f = lut_act_ref(act) (acts 0-4; 3 for Erf, not restated). */
+ * scale), f = lut_act_ref(act) (0-4, and erff for 5 and any other id). */
 int or_dequant_activation(const uint8_t *in, uint64_t n, int quant, int act, float scale,
                           int32_t zp, float *out);
 #define OR_I8_DOT_K_MAX 133144   /* i32::MAX / (127 * 127), kernel_call.rs:103 */
@@ -140,6 +142,8 @@ void or_binary(int op, const void *a, const void *b, void *out, size_t n, int dt
 /* rms_norm_float generic path, float_kernels.rs:1683-1755 (gamma NULL: none) */
 int or_rms_norm(const void *x, const void *gamma, void *out, uint32_t batch, uint32_t feature,
                 uint64_t epsilon_bits, int dtype);
+int or_add_rms_norm(const void *x, const void *res, const void *gamma, void *out, uint32_t batch,
+                    uint32_t feature, uint64_t epsilon_bits, int dtype);
 /* rope_float scalar path, float_kernels.rs:3123-3186 */
 int or_rope(const void *x, const void *cs, const void *sn, void *out, uint32_t head_dim, size_t n,
             int dtype);

@@ -14,7 +14,7 @@ import oracle
 from conftest import ROOT
 from hologram_amd import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, BufferRef, DecodeAttentionI8Call,
                           KernelCall, KvCacheWriteCall, KvQuantAppendCall, MatMulCall,
-                          SlotOutOfRange, UnaryCall, UnsupportedOp, decode_call, lut_table,
+                          NormCall, SlotOutOfRange, UnaryCall, UnsupportedOp, decode_call, lut_table,
                           validate)
 from hologram_amd import _ffi
 
@@ -43,7 +43,7 @@ def test_no_device_backend_create_fails_loudly():
         HipBackend(0)
 
 
-@pytest.mark.parametrize("act", range(5))
+@pytest.mark.parametrize("act", range(6))
 @pytest.mark.parametrize("dtype", [DTYPE_BF16, DTYPE_F16])
 def test_host_tables_equal_oracle(act, dtype):
     assert np.array_equal(lut_table(act, dtype), oracle.build_table(act, dtype))
@@ -67,9 +67,9 @@ def test_host_relu_elu_selu_tables_are_widen_f_narrow(table, fused, dtype):
     assert np.array_equal(lut_table(table, dtype), want)
 
 
-def test_erf_table_not_built():
+def test_unknown_table_not_built():
     with pytest.raises(UnsupportedOp):
-        lut_table(5, DTYPE_BF16)
+        lut_table(9, DTYPE_BF16)
 
 
 # ---- refusals (validate = dispatch's host checks, no device) -----------------
@@ -195,6 +195,9 @@ def test_codec_layout_matches_kernel_codec():
 
 @pytest.mark.parametrize("call", [
     KernelCall.Exp(UnaryCall(BufferRef(3), BufferRef(4, 16, 32), 99, 16, DTYPE_F16)),
+    KernelCall.Erf(UnaryCall(BufferRef(1), BufferRef(2), 7, 32, DTYPE_F32)),
+    KernelCall.AddRmsNorm(NormCall(BufferRef(0), BufferRef(1), BufferRef(2), 3, 64, 0x3727C5AC,
+                                   DTYPE_F32, residual=BufferRef(5, 8, 0))),
     KernelCall.KvCacheWrite(KvCacheWriteCall(BufferRef(0), BufferRef(1), BufferRef(2),
                                              BufferRef(3), 5, 6, 1, 128)),
     KernelCall.KvQuantAppend(KvQuantAppendCall(*[BufferRef(i) for i in range(6)], 128, 4096, 1,

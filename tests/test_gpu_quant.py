@@ -8,9 +8,9 @@
   1e-5 (normalized max error) of the f64 product of A and the oracle's
   dequantized weight.
 - Dequantize and DequantActivation: bit-exact against the oracle.
-- f32 Relu / Sigmoid / Tanh / Gelu / Silu / Elu / Selu / Exp: bit-exact
-  against the oracle's scalar functions; 16-bit Relu / Elu / Selu: bit-exact
-  on all 65536 patterns (unary_float's widen, f, narrow).
+- f32 Relu / Sigmoid / Tanh / Gelu / Silu / Elu / Selu / Exp / Erf: bit-exact
+  against the oracle's scalar functions; 16-bit Relu / Elu / Selu / Erf:
+  bit-exact on all 65536 patterns (unary_float's widen, f, narrow; the LUT).
 - Sessions: the loader's dequant fusions give the unfused walk's bits.
 """
 import struct
@@ -229,7 +229,7 @@ def test_dequantize_bit_exact(torch_cuda, backend, quant, dtype, per_ch):
 
 @pytest.mark.parametrize("quant", [DTYPE_I8, DTYPE_U8, DTYPE_I4])
 @pytest.mark.parametrize("act", [lut_act.SIGMOID, lut_act.TANH, lut_act.GELU, lut_act.SILU,
-                                 lut_act.EXP])
+                                 lut_act.EXP, lut_act.ERF])
 def test_dequant_activation_bit_exact(torch_cuda, backend, quant, act):
     rng = np.random.default_rng(quant * 10 + act)
     n = 100001
@@ -265,6 +265,35 @@ def test_f32_unary_bit_exact(torch_cuda, backend, name):
     backend.dispatch(ctor(UnaryCall(BufferRef(0), BufferRef(1), x.size, 32, DTYPE_F32)), ws)
     backend.synchronize()
     assert same_bits(from_dev(out, np.float32), oracle.fused_act_f32(UNARY[name], x))
+
+
+def test_f32_erf_bit_exact(torch_cuda, backend):
+    rng = np.random.default_rng(32)
+    x = np.concatenate([SPECIALS, rng.uniform(-7, 7, 100000).astype(np.float32),
+                        rng.uniform(-1.3, 1.3, 50000).astype(np.float32),
+                        (np.float32(2.0) ** rng.uniform(-40, 0, 20000)).astype(np.float32)])
+    ws = DeviceWorkspace()
+    ws.bind(0, to_dev(torch_cuda, x))
+    out = torch_cuda.zeros(x.size * 4, dtype=torch_cuda.uint8, device="cuda")
+    ws.bind(1, out)
+    backend.dispatch(KernelCall.Erf(UnaryCall(BufferRef(0), BufferRef(1), x.size, 32, DTYPE_F32)),
+                     ws)
+    backend.synchronize()
+    L = oracle.lib()
+    want = np.array([L.or_libm_erff(float(v)) for v in x], np.float32)
+    assert same_bits(from_dev(out, np.float32), want)
+
+
+@pytest.mark.parametrize("dtype", [DTYPE_BF16, DTYPE_F16])
+def test_16bit_erf_every_pattern(torch_cuda, backend, dtype):
+    bits = np.arange(65536, dtype=np.uint16)
+    ws = DeviceWorkspace()
+    ws.bind(0, to_dev(torch_cuda, bits))
+    out = torch_cuda.zeros(65536 * 2, dtype=torch_cuda.uint8, device="cuda")
+    ws.bind(1, out)
+    backend.dispatch(KernelCall.Erf(UnaryCall(BufferRef(0), BufferRef(1), 65536, 16, dtype)), ws)
+    backend.synchronize()
+    assert np.array_equal(from_dev(out, np.uint16), oracle.build_table(lut_act.ERF, dtype))
 
 
 @pytest.mark.parametrize("name", ["Relu", "Elu", "Selu"])

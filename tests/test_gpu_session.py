@@ -1,8 +1,9 @@
 """GPU parity of the decode-step ops and of the `.holo` session walk.
 
 Ops (vs the C oracle, oracle/holo_oracle.c): Add, Mul, RoPE, Gather and
-ArgMax bit-exact; RmsNorm within 1e-2 (bf16) / 1e-5 (f32) normalized error
-(its sum of squares is a tree here, sequential in the reference).
+ArgMax bit-exact; RmsNorm and AddRmsNorm within 1e-2 (bf16) / 1e-5 (f32)
+normalized error (the sum of squares is a tree here, sequential in the
+reference).
 Session (vs oracle/graph.py, the reference walk over the same archive on the
 CPU): a small Llama-style decoder stepped several tokens. Every op of the walk
 narrows to bf16 by truncation, so a value near a bf16 boundary can land one ulp
@@ -91,6 +92,35 @@ def test_rms_norm(torch_cuda, backend, dtype, tol, batch, feature):
         else:
             got_f, want_f = got.view(np.float32), want.view(np.float32)
         assert oracle.max_rel_err(got_f, want_f) <= tol
+
+
+@pytest.mark.parametrize("dtype,tol", [(DTYPE_BF16, 1e-2), (DTYPE_F32, 1e-5)])
+@pytest.mark.parametrize("batch,feature", [(1, 64), (8, 2048), (3, 1000)])
+def test_add_rms_norm(torch_cuda, backend, dtype, tol, batch, feature):
+    """AddRmsNorm (54): rms_norm(x + residual), the sum in f32; with and
+    without the residual and gamma, against or_add_rms_norm."""
+    rng = np.random.default_rng(feature + 1)
+    x32 = rng.standard_normal((batch, feature)).astype(np.float32) * 3
+    r32 = rng.standard_normal((batch, feature)).astype(np.float32)
+    g32 = rng.standard_normal(feature).astype(np.float32)
+    x, r, g = (bf(x32), bf(r32), bf(g32)) if dtype == DTYPE_BF16 else (x32, r32, g32)
+    es = x.itemsize
+    eps = f32_bits(1e-5)
+    absent = BufferRef(0xFFFFFFFF)
+    for with_r in (True, False):
+        for with_g in (True, False):
+            call = KernelCall.AddRmsNorm(NormCall(
+                BufferRef(1), BufferRef(2) if with_g else absent, BufferRef(3), batch, feature,
+                eps, dtype, residual=BufferRef(4) if with_r else absent))
+            got = run(torch_cuda, backend, call, {1: x, 2: g, 4: r}, x.size * es, 3)
+            want = np.zeros(x.size * es, np.uint8)
+            lib().or_add_rms_norm(_p(x), _p(r) if with_r else None, _p(g) if with_g else None,
+                                  _p(want), batch, feature, eps, dtype)
+            if dtype == DTYPE_BF16:
+                got_f, want_f = unbf(got.view(np.uint16)), unbf(want.view(np.uint16))
+            else:
+                got_f, want_f = got.view(np.float32), want.view(np.float32)
+            assert oracle.max_rel_err(got_f, want_f) <= tol, (with_r, with_g)
 
 
 @pytest.mark.parametrize("dtype", [DTYPE_BF16, DTYPE_F32])

@@ -2,6 +2,8 @@
 the mathematics fixes, independently of the restatement's own code:
   or_binary   numpy float32 add/mul then bf16 truncation (exact)
   or_rms_norm f64 closed form; a constant row maps to gamma exactly
+  or_add_rms_norm RmsNorm without a residual; bf16 = f32 RmsNorm of the
+              unnarrowed sum, truncated; f64 closed form
   or_rope     f64 rotation; angle 0 is the identity; norms are preserved
   or_gather   brute-force indexing with negative wrap; range refusal
   or_argmax   numpy argmax on NaN-free rows; lowest index on ties; NaN skipped
@@ -54,6 +56,42 @@ def test_rms_norm_closed_form():
     assert np.allclose(o[0], -g, rtol=1e-6)
     # invalid epsilon is refused (float_kernels.rs:1324-1336)
     assert lib().or_rms_norm(_p(c), None, _p(o), 1, F, 0xBF800000, F32) == -1
+
+
+def test_add_rms_norm_laws():
+    """or_add_rms_norm (float_kernels.rs:1566-1672): without a residual it is
+    RmsNorm bit for bit; a bf16 row is the f32 RmsNorm of the unnarrowed f32
+    sum x + r, truncated; f32 rows with a residual follow the f64 closed form."""
+    rng = np.random.default_rng(7)
+    B, F = 4, 520
+    x = rng.standard_normal((B, F)).astype(np.float32) * 2
+    r = rng.standard_normal((B, F)).astype(np.float32)
+    g = rng.standard_normal(F).astype(np.float32)
+    eps = int(np.float32(1e-5).view(np.uint32))
+    o1, o2 = np.zeros_like(x), np.zeros_like(x)
+    assert lib().or_add_rms_norm(_p(x), None, _p(g), _p(o1), B, F, eps, F32) == 0
+    lib().or_rms_norm(_p(x), _p(g), _p(o2), B, F, eps, F32)
+    assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32))
+    # bf16: v = widen(x) + widen(r) in f32, never narrowed before the norm
+    xb, rb, gb = bf(x), bf(r), bf(g)
+    ob = np.zeros_like(xb)
+    assert lib().or_add_rms_norm(_p(xb), _p(rb), _p(gb), _p(ob), B, F, eps, BF16) == 0
+    v = (unbf(xb) + unbf(rb)).astype(np.float32)
+    g32 = unbf(gb)                    # held: _p() takes no reference to its array
+    of = np.zeros_like(v)
+    lib().or_rms_norm(_p(v), _p(g32), _p(of), B, F, eps, F32)
+    assert np.array_equal(ob, bf(of))
+    # narrowing the sum first (Add then RmsNorm) is a different function
+    vn = unbf(bf(v))
+    lib().or_rms_norm(_p(vn), _p(g32), _p(of), B, F, eps, F32)
+    assert not np.array_equal(ob, bf(of))
+    # f32 with a residual: the f64 closed form
+    o3 = np.zeros_like(x)
+    lib().or_add_rms_norm(_p(x), _p(r), _p(g), _p(o3), B, F, eps, F32)
+    vd = x.astype(np.float64) + r
+    want = vd / np.sqrt((vd * vd).mean(axis=1, keepdims=True) + 1e-5) * g
+    assert np.max(np.abs(o3 - want)) <= 2e-6 * np.max(np.abs(want))
+    assert lib().or_add_rms_norm(_p(x), _p(r), None, _p(o3), B, F, 0xBF800000, F32) == -1
 
 
 def test_rope_is_a_rotation():

@@ -138,9 +138,14 @@ def test_dequant_activation_is_the_unfused_pair(act, quant):
     assert np.array_equal(fused.view(np.uint32), oracle.fused_act_f32(FA_OF_LUT[act], x).view(np.uint32))
 
 
-def test_dequant_activation_erf_is_not_restated():
-    with pytest.raises(ValueError):
-        oracle.dequant_activation(np.zeros(4, np.uint8), 4, DTYPE_I8, lut_act.ERF, 1.0, 0)
+@pytest.mark.parametrize("act", [lut_act.ERF, 9])
+def test_dequant_activation_erf_is_the_unfused_pair(act):
+    # lut_act_ref maps Erf, and any id past it, to libm erff (float_kernels.rs:3628-3638)
+    raw = np.arange(256, dtype=np.uint8)
+    fused = oracle.dequant_activation(raw, 256, DTYPE_I8, act, 0.021, -4)
+    x = oracle.dequantize(raw, 256, DTYPE_I8, scale=0.021, zp=-4)
+    L = oracle.lib()
+    assert np.array_equal(fused, np.array([L.or_libm_erff(float(v)) for v in x], np.float32))
 
 
 # ---- W8A32 reference ----------------------------------------------------------
@@ -271,8 +276,7 @@ def test_dequant_activation_refusals():
         validate(da(), [10, 39])
     with pytest.raises(SlotOutOfRange):
         validate(da(quant=DTYPE_E8CB), [10, 40])
-    with pytest.raises(UnsupportedOp):
-        validate(da(lut_act.ERF), [10, 40])
+    validate(da(lut_act.ERF), [10, 40])
 
 
 def mmd(m=2, k=16, n=8, **kw):
@@ -432,9 +436,10 @@ def test_dequant_activation_fuses_per_tensor_f32_only():
         [dq_weight(per_ch=per_ch), f32u(ctor, 10, 11, n=n)],
         QIN[:2] + (QIN[2:] if per_ch else []), [(11, n, DTYPE_F32)])
     for ctor in (KernelCall.Sigmoid, KernelCall.Tanh, KernelCall.Gelu, KernelCall.Silu,
-                 KernelCall.Exp):
+                 KernelCall.Exp, KernelCall.Erf):
         s = HipSession(None, one(ctor))
         assert s.call_tags() == [113]
+    assert HipSession(None, one(KernelCall.Erf)).call(0).u.dequant_act.act == lut_act.ERF
     assert HipSession(None, one(KernelCall.Gelu)).call(0).u.dequant_act.act == lut_act.GELU
     assert HipSession(None, one(KernelCall.Relu)).call_tags() == [105, 11]    # no table form
     assert HipSession(None, one(KernelCall.Gelu, per_ch=True)).call_tags() == [105, 14]

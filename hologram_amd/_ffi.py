@@ -191,6 +191,12 @@ SIGNATURES = {
     "holo_hip_session_nodes": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_uint32),
                                               ctypes.POINTER(ctypes.c_uint32)]),
     "holo_hip_session_call": (ctypes.c_int, [_P, ctypes.c_uint32, ctypes.POINTER(KernelCallC)]),
+    "holo_hip_session_output_labels": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.c_char_p]),
+    "holo_hip_session_execute_bytes": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_void_p),
+                                                      ctypes.POINTER(ctypes.c_uint64),
+                                                      ctypes.c_uint32,
+                                                      ctypes.POINTER(ctypes.c_int)]),
+    "holo_hip_session_set_memo": (ctypes.c_int, [_P, ctypes.c_int]),
     "holo_hip_session_close": (ctypes.c_int, [_P]),
     "holo_hip_session_info": (ctypes.c_int, [_P] + [ctypes.POINTER(ctypes.c_uint32)] * 4),
     "holo_hip_session_port": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_uint32,
@@ -210,6 +216,12 @@ SIGNATURES = {
                                                ctypes.POINTER(ctypes.c_uint64)]),
     "holo_hip_session_read_output": (ctypes.c_int, [_P, ctypes.c_uint32, _P, ctypes.c_uint64]),
     "holo_hip_blake3": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_size_t, ctypes.c_char_p]),
+    "holo_hip_address_bytes": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_uint64, ctypes.c_char_p]),
+    "holo_hip_derive_label": (ctypes.c_int, [ctypes.c_uint16, ctypes.c_char_p, ctypes.c_uint64,
+                                             ctypes.c_char_p, ctypes.c_uint64, ctypes.c_char_p]),
+    "holo_hip_op_signature": (ctypes.c_int, [ctypes.POINTER(KernelCallC),
+                                             ctypes.POINTER(ctypes.c_uint16), ctypes.c_char_p,
+                                             ctypes.POINTER(ctypes.c_uint32)]),
     "holo_hip_last_error_message": (ctypes.c_char_p, []),
 }
 

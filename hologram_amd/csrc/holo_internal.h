@@ -72,4 +72,15 @@ bool fused_act_supported(uint32_t act, uint8_t dtype, bool after_add);
 // BLAKE3 (default hash mode, 32-byte digest).
 void blake3_hash(const void *data, size_t len, uint8_t out[32]);
 
+// κ-labels (holo_kappa.cpp): "blake3:" + hex digest; a call's op signature
+// (opcode, LE params; false for a call this backend does not serve) and its
+// label operands (input slots in derivation order, output slots).
+std::string kappa_of_digest(const uint8_t d[32]);
+std::string address_bytes(const void *bytes, size_t len);
+std::string derive_label(uint16_t opcode, const uint8_t *params, size_t n_params,
+                         const std::vector<std::string> &inputs);
+bool op_signature(const holo_kernel_call &c, uint16_t *opcode, uint8_t params[64], uint32_t *len);
+bool label_operands(const holo_kernel_call &c, std::vector<uint32_t> *ins,
+                    std::vector<uint32_t> *outs, bool *commutative);
+
 }  // namespace holo

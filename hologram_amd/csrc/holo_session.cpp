@@ -34,6 +34,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <map>
 #include <memory>
@@ -548,6 +549,19 @@ struct holo_session {
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
     void *graph_scratch = nullptr;                // the scratch the graph was captured with
+    // κ-labels (address.rs): the calls and plan as the reference's loader
+    // passes leave them (before this backend's in-place moves and device
+    // fusion), and each constant's BLAKE3 digest
+    std::vector<holo_kernel_call> label_calls;
+    std::vector<std::vector<uint32_t>> label_plan;
+    std::vector<std::pair<uint32_t, std::array<uint8_t, 32>>> const_digests;
+    // the whole-graph memo of session.rs:841-905 over the byte boundary: the
+    // input labels of the last walk, valid while nothing else has touched the
+    // session's memory; per port, the last bytes hashed and their label
+    bool memo_enabled = true, memo_valid = false;
+    std::vector<std::string> memo_key;
+    std::vector<std::vector<uint8_t>> input_seen;
+    std::vector<std::string> input_seen_label;
 };
 
 namespace {
@@ -1180,6 +1194,8 @@ int load_impl(holo_backend *be, const uint8_t *bytes, size_t len, uint32_t flags
     }
     if (!(flags & HOLO_SESSION_NO_EPILOGUE_FUSION)) fuse_matmul_epilogue(s->calls, s->plan, s->outputs);
     if (!(flags & HOLO_SESSION_NO_DEQUANT_FUSION)) fuse_dequant_activation(s->calls, s->plan, s->outputs);
+    s->label_calls = s->calls;
+    s->label_plan = s->plan;
     // --- weights (fingerprint -> body), constants
     std::map<std::string, std::pair<const uint8_t *, uint64_t>> weights;
     if ((it = sec.find(kSecWeights)) != sec.end()) {
@@ -1217,7 +1233,12 @@ int load_impl(holo_backend *be, const uint8_t *bytes, size_t len, uint32_t flags
             if (tag == 0) {
                 const uint32_t bl = c.get<uint32_t>();
                 const uint8_t *body = c.take(bl);
-                if (c.ok) consts.push_back({slot, body, bl});
+                if (c.ok) {
+                    consts.push_back({slot, body, bl});
+                    std::array<uint8_t, 32> d;
+                    holo::blake3_hash(body, bl, d.data());   // address_bytes of the body
+                    s->const_digests.push_back({slot, d});
+                }
             } else if (tag == 1) {
                 const uint8_t *fp = c.take(32);
                 if (!c.ok) break;
@@ -1226,6 +1247,9 @@ int load_impl(holo_backend *be, const uint8_t *bytes, size_t len, uint32_t flags
                     return set_error(HOLO_ERR_DISPATCH,
                                      "session_load: constant references a weight the archive does not carry");
                 consts.push_back({slot, w->second.first, w->second.second});
+                std::array<uint8_t, 32> d;   // label_from_fingerprint: the verified digest
+                memcpy(d.data(), fp, 32);
+                s->const_digests.push_back({slot, d});
             } else {
                 return set_error(HOLO_ERR_DISPATCH, "session_load: unknown ConstantEntry tag");
             }
@@ -1511,6 +1535,7 @@ int holo_hip_session_fingerprint(const holo_session *s, uint8_t out32[32]) {
 
 int holo_hip_session_bind_input(holo_session *s, uint32_t index, void *dev_ptr, uint64_t bytes) {
     if (!s) return set_error(HOLO_ERR_INIT, "session_bind_input: null session");
+    s->memo_valid = false;
     if (index >= s->inputs.size())
         return set_error(HOLO_ERR_SLOT_OUT_OF_RANGE, "session_bind_input: index out of range");
     const Port &p = s->inputs[index];
@@ -1529,6 +1554,7 @@ int holo_hip_session_bind_input(holo_session *s, uint32_t index, void *dev_ptr, 
 
 int holo_hip_session_write_input(holo_session *s, uint32_t index, const void *host, uint64_t bytes) {
     if (!s || !host) return set_error(HOLO_ERR_INIT, "session_write_input: null argument");
+    s->memo_valid = false;
     if (index >= s->inputs.size())
         return set_error(HOLO_ERR_SLOT_OUT_OF_RANGE, "session_write_input: index out of range");
     const Port &p = s->inputs[index];
@@ -1543,7 +1569,127 @@ int holo_hip_session_write_input(holo_session *s, uint32_t index, const void *ho
 
 int holo_hip_session_execute(holo_session *s) {
     if (!s) return set_error(HOLO_ERR_INIT, "session_execute: null session");
+    s->memo_valid = false;
     return walk(s);
+}
+
+namespace {
+
+// The output ports' κ-labels for the given input-port labels: every slot's
+// label walked through the plan as compute_and_label derives it
+// (session.rs:1052-1120); a call whose operand has no label leaves its
+// outputs unlabelled. A call with two outputs (the int8 append's cache and
+// scales) labels output j with its params followed by the byte j.
+int derive_outputs(const holo_session *s, const std::vector<std::string> &in,
+                   std::vector<std::string> *out) {
+    std::vector<std::string> lab(s->slot_bytes.size());
+    for (const auto &cd : s->const_digests)
+        if (cd.first < lab.size()) lab[cd.first] = holo::kappa_of_digest(cd.second.data());
+    for (size_t i = 0; i < s->inputs.size(); ++i)
+        if (s->inputs[i].slot < lab.size()) lab[s->inputs[i].slot] = in[i];
+    std::vector<uint32_t> ins, outs;
+    std::vector<std::string> il;
+    for (const auto &level : s->label_plan)
+        for (uint32_t ci : level) {
+            const holo_kernel_call &c = s->label_calls[ci];
+            bool comm = false;
+            uint16_t op = 0;
+            uint8_t params[65];
+            uint32_t np = 0;
+            if (!holo::label_operands(c, &ins, &outs, &comm) || !holo::op_signature(c, &op, params, &np))
+                return set_error(HOLO_ERR_UNSUPPORTED_OP,
+                                 "session_output_labels: kernel call " + std::to_string(ci) + " has no signature");
+            bool ok = true;
+            il.clear();
+            for (uint32_t sl : ins) {
+                if (sl >= lab.size() || lab[sl].empty()) {
+                    ok = false;
+                    break;
+                }
+                il.push_back(lab[sl]);
+            }
+            if (comm) std::sort(il.begin(), il.end());
+            for (size_t j = 0; j < outs.size(); ++j) {
+                if (outs[j] >= lab.size()) continue;
+                if (!ok) {
+                    lab[outs[j]].clear();
+                    continue;
+                }
+                uint32_t n = np;
+                if (outs.size() > 1) params[n++] = uint8_t(j);
+                lab[outs[j]] = holo::derive_label(op, params, n, il);
+            }
+        }
+    out->clear();
+    for (const auto &p : s->outputs) {
+        if (p.slot >= lab.size() || lab[p.slot].empty())
+            return set_error(HOLO_ERR_UNSUPPORTED_OP,
+                             "session_output_labels: output '" + p.name + "' is not addressable");
+        out->push_back(lab[p.slot]);
+    }
+    return HOLO_OK;
+}
+
+}  // namespace
+
+int holo_hip_session_output_labels(const holo_session *s, const char *input_labels, char *out) {
+    if (!s || (!input_labels && !s->inputs.empty()) || (!out && !s->outputs.empty()))
+        return set_error(HOLO_ERR_INIT, "session_output_labels: null argument");
+    std::vector<std::string> in;
+    for (size_t i = 0; i < s->inputs.size(); ++i)
+        in.emplace_back(input_labels + i * HOLO_LABEL_LEN, HOLO_LABEL_LEN);
+    std::vector<std::string> labels;
+    const int rc = derive_outputs(s, in, &labels);
+    if (rc != HOLO_OK) return rc;
+    for (size_t i = 0; i < labels.size(); ++i) memcpy(out + i * HOLO_LABEL_LEN, labels[i].data(), HOLO_LABEL_LEN);
+    return HOLO_OK;
+}
+
+int holo_hip_session_set_memo(holo_session *s, int enabled) {
+    if (!s) return set_error(HOLO_ERR_INIT, "session_set_memo: null session");
+    s->memo_enabled = enabled != 0;
+    if (!s->memo_enabled) s->memo_valid = false;
+    return HOLO_OK;
+}
+
+int holo_hip_session_execute_bytes(holo_session *s, const void *const *inputs, const uint64_t *sizes,
+                                   uint32_t n, int *memo_hit) {
+    if (!s || (n && (!inputs || !sizes))) return set_error(HOLO_ERR_INIT, "session_execute_bytes: null argument");
+    if (memo_hit) *memo_hit = 0;
+    if (n != s->inputs.size())
+        return set_error(HOLO_ERR_SHAPE_MISMATCH,
+                         "session_execute_bytes: expected " + std::to_string(s->inputs.size()) + " inputs");
+    if (!s->be) return set_error(HOLO_ERR_INIT, "session_execute_bytes: a dry-loaded session cannot execute");
+    std::vector<std::string> key;
+    if (s->memo_enabled) {
+        s->input_seen.resize(n);
+        s->input_seen_label.resize(n);
+        for (uint32_t i = 0; i < n; ++i) {
+            const Port &p = s->inputs[i];
+            const uint64_t len = std::min<uint64_t>(sizes[i], sat_mul(p.count, port_bytes(p.dtype)));
+            const uint8_t *b = static_cast<const uint8_t *>(inputs[i]);
+            auto &seen = s->input_seen[i];
+            if (seen.size() != len || (len && memcmp(seen.data(), b, len) != 0) || s->input_seen_label[i].empty()) {
+                seen.assign(b, b + len);   // a repeated input is not hashed again
+                s->input_seen_label[i] = holo::address_bytes(b, len);
+            }
+            key.push_back(s->input_seen_label[i]);
+        }
+        // hit: the outputs of these inputs are still in the output slots
+        if (s->memo_valid && key == s->memo_key) {
+            if (memo_hit) *memo_hit = 1;
+            return HOLO_OK;
+        }
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        const int rc = holo_hip_session_write_input(s, i, inputs[i], sizes[i]);
+        if (rc != HOLO_OK) return rc;
+    }
+    const int rc = holo_hip_session_execute(s);
+    if (rc != HOLO_OK) return rc;
+    s->memo_key = std::move(key);
+    s->memo_valid = s->memo_enabled;
+    return HOLO_OK;
 }
 
 int holo_hip_session_output(const holo_session *s, uint32_t index, void **dev_ptr, uint64_t *bytes) {
@@ -1585,6 +1731,7 @@ int holo_hip_session_stream(const holo_session *s, void **stream) {
 
 int holo_hip_session_capture(holo_session *s) {
     if (!s) return set_error(HOLO_ERR_INIT, "session_capture: null session");
+    s->memo_valid = false;
     // An eager walk first: it sizes the backend's scratch (no allocation may
     // happen under capture) and surfaces any refusal with a message.
     int rc = walk(s);
@@ -1618,6 +1765,7 @@ int holo_hip_session_capture(holo_session *s) {
 
 int holo_hip_session_replay(holo_session *s) {
     if (!s) return set_error(HOLO_ERR_INIT, "session_replay: null session");
+    s->memo_valid = false;
     if (!s->graph) return set_error(HOLO_ERR_DISPATCH, "session_replay: no captured walk");
     std::vector<SlotRange> now = s->slots;
     for (auto &a : s->aliases) now[a.first] = now[a.second];

@@ -52,6 +52,7 @@ class HipSession:
         nn, ng = ctypes.c_uint32(), ctypes.c_uint32()
         _check(self._lib.holo_hip_session_nodes(self.handle, ctypes.byref(nn), ctypes.byref(ng)))
         self.n_nodes, self.n_groups = nn.value, ng.value
+        self.last_memo_hit = False
         self.inputs = [self._port(0, i) for i in range(ni.value)]
         self.outputs = [self._port(1, i) for i in range(no.value)]
 
@@ -128,14 +129,34 @@ class HipSession:
         return buf.raw
 
     def execute(self, inputs: list[bytes]) -> list[bytes]:
-        """session.rs execute: bytes per input port in, bytes per output port out."""
+        """session.rs execute: bytes per input port in, bytes per output port
+        out, with the whole-graph memo (a repeat of the last inputs, nothing
+        touched since, skips the walk; `last_memo_hit` says whether it did)."""
         if len(inputs) != len(self.inputs):
             raise ValueError(f"expected {len(self.inputs)} inputs, got {len(inputs)}")
-        for i, b in enumerate(inputs):
-            self.write_input(i, b)
-        self.run()
+        bufs = [ctypes.create_string_buffer(bytes(b), len(b)) for b in inputs]
+        ptrs = (ctypes.c_void_p * max(1, len(bufs)))(*[ctypes.addressof(b) for b in bufs])
+        sizes = (ctypes.c_uint64 * max(1, len(bufs)))(*[len(b) for b in inputs])
+        hit = ctypes.c_int()
+        _check(self._lib.holo_hip_session_execute_bytes(self.handle, ptrs, sizes, len(bufs),
+                                                        ctypes.byref(hit)))
+        self.last_memo_hit = bool(hit.value)
         self.synchronize()
         return [self.read_output(i) for i in range(len(self.outputs))]
+
+    def set_memo(self, enabled: bool) -> None:
+        """The memo's hits on (default) or off (every execute walks)."""
+        _check(self._lib.holo_hip_session_set_memo(self.handle, int(enabled)))
+
+    def output_labels(self, input_labels: list[str]) -> list[str]:
+        """The output ports' κ-labels for these input-port labels (works on a
+        dry load)."""
+        if len(input_labels) != len(self.inputs):
+            raise ValueError(f"expected {len(self.inputs)} labels")
+        out = ctypes.create_string_buffer(71 * max(1, len(self.outputs)))
+        _check(self._lib.holo_hip_session_output_labels(self.handle,
+                                                        "".join(input_labels).encode(), out))
+        return [out.raw[71 * i:71 * (i + 1)].decode() for i in range(len(self.outputs))]
 
     def close(self) -> None:
         if self.handle:

@@ -520,6 +520,27 @@ int holo_hip_session_nodes(const holo_session *s, uint32_t *n_nodes, uint32_t *n
  * loader passes (the calls the reference's Session counts with
  * dequant_fused_count and its siblings, session.rs:1390-1437). */
 int holo_hip_session_call(const holo_session *s, uint32_t index, holo_kernel_call *out);
+/* The output ports' κ-labels for the given input-port labels (n_inputs x
+ * HOLO_LABEL_LEN bytes in, n_outputs x HOLO_LABEL_LEN out), derived through
+ * the loaded schedule as the reference's compute_and_label does
+ * (session.rs:1052-1120): constants are labelled by their content, each call
+ * by derive_label over its op signature and its operands' labels (buffers()
+ * order, kernel_call.rs:1526-1660; Add and Mul sort theirs). Works on a dry
+ * load. */
+int holo_hip_session_output_labels(const holo_session *s, const char *input_labels, char *out);
+/* Execute from host bytes with the reference's whole-graph memo
+ * (session.rs:841-905): each input is labelled by its bytes (a port whose
+ * bytes repeat is not hashed again); when the labels equal the last walk's
+ * and nothing has touched the session since (no bind, write, execute,
+ * capture or replay in between), the outputs already in place are those of
+ * these inputs and the walk is skipped (*memo_hit = 1). Writing session
+ * memory through a pointer from holo_hip_session_output is outside what the
+ * memo sees: turn it off first. `sizes[i]` bytes of input i are used, at most
+ * its port's size. */
+int holo_hip_session_execute_bytes(holo_session *s, const void *const *inputs, const uint64_t *sizes,
+                                   uint32_t n, int *memo_hit);
+/* Turn the memo's hits on (the default) or off (benchmarks: every call walks). */
+int holo_hip_session_set_memo(holo_session *s, int enabled);
 int holo_hip_session_close(holo_session *s);
 int holo_hip_session_info(const holo_session *s, uint32_t *n_inputs, uint32_t *n_outputs,
                           uint32_t *n_calls, uint32_t *n_slots);
@@ -552,6 +573,24 @@ int holo_hip_session_read_output(holo_session *s, uint32_t index, void *host, ui
 /* BLAKE3 (default mode, 32-byte digest): the archive footer and weight
  * fingerprint hash (crates/hologram-archive/src/weight.rs WeightFingerprint). */
 int holo_hip_blake3(const void *data, size_t len, uint8_t out32[32]);
+
+/* κ-labels (crates/hologram-archive/src/address.rs): "blake3:" followed by the
+ * 64 lowercase hex digits of a BLAKE3 digest, HOLO_LABEL_LEN ASCII bytes
+ * (`out` receives them and a terminating NUL). */
+#define HOLO_LABEL_LEN 71
+/* address_bytes (address.rs:96-99): the label of opaque bytes. */
+int holo_hip_address_bytes(const void *bytes, uint64_t len, char out[72]);
+/* derive_label (address.rs:108-116): the label of a computed value, the digest
+ * of opcode (u16 LE) || params || each operand label in order; `labels` holds
+ * n_labels labels back to back (HOLO_LABEL_LEN bytes each). */
+int holo_hip_derive_label(uint16_t opcode, const uint8_t *params, uint64_t n_params,
+                          const char *labels, uint64_t n_labels, char out[72]);
+/* KernelCall::op_signature (crates/hologram-compute/src/kernel_call.rs:
+ * 1321-1500): the opcode and LE parameter bytes a call's label is derived
+ * with. The new calls (122-125) take their discriminant as opcode and their
+ * scalar fields in struct order. UnsupportedOp for a call not served here. */
+int holo_hip_op_signature(const holo_kernel_call *call, uint16_t *opcode, uint8_t params[64],
+                          uint32_t *n_params);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char *holo_hip_last_error_message(void);

@@ -358,3 +358,55 @@ def test_reference_compiled_fixture_runs_to_its_kappa(torch_cuda, backend):
     sess.synchronize()
     assert "blake3:" + blake3(sess.read_output(0)).hex() == want
     sess.close()
+
+
+def test_session_memo_skips_a_repeated_walk(torch_cuda, backend):
+    """The whole-graph memo (session.rs:841-905): the same input bytes again,
+    nothing touched in between, skip the walk and leave the same outputs; new
+    bytes, a direct write, or the memo switched off walk again."""
+    from hologram_amd import HoloWriter, PortDescriptor
+    n = 4099
+    w = HoloWriter()
+    w.kernel_calls = [KernelCall.Add(BinaryCall(BufferRef(0, 0, n * 4), BufferRef(1, 0, n * 4),
+                                                BufferRef(2, 0, n * 4), n, 32, DTYPE_F32))]
+    w.inputs = [PortDescriptor("a", 0, n, DTYPE_F32, [n]), PortDescriptor("b", 1, n, DTYPE_F32, [n])]
+    w.outputs = [PortDescriptor("y", 2, n, DTYPE_F32, [n])]
+    sess = HipSession(backend, w.finish())
+    rng = np.random.default_rng(3)
+    a, b, c = (rng.standard_normal(n).astype(np.float32) for _ in range(3))
+    y1 = sess.execute([a.tobytes(), b.tobytes()])[0]
+    assert not sess.last_memo_hit
+    assert np.array_equal(np.frombuffer(y1, np.float32), a + b)
+    assert sess.execute([a.tobytes(), b.tobytes()])[0] == y1 and sess.last_memo_hit
+    y2 = sess.execute([a.tobytes(), c.tobytes()])[0]
+    assert not sess.last_memo_hit and np.array_equal(np.frombuffer(y2, np.float32), a + c)
+    sess.write_input(1, b.tobytes())          # touched directly: the next call walks
+    assert sess.execute([a.tobytes(), c.tobytes()])[0] == y2 and not sess.last_memo_hit
+    sess.set_memo(False)
+    sess.execute([a.tobytes(), c.tobytes()])
+    assert not sess.last_memo_hit
+    sess.set_memo(True)
+    sess.execute([a.tobytes(), c.tobytes()])
+    assert not sess.last_memo_hit
+    assert sess.execute([a.tobytes(), c.tobytes()])[0] == y2 and sess.last_memo_hit
+    sess.close()
+
+
+def test_session_memo_with_in_place_caches(torch_cuda, backend):
+    """A decode step whose caches move in place: a memo hit leaves the outputs
+    of the last walk (its caches included) exactly as a fresh walk of the
+    same inputs produces them."""
+    cfg = CFG
+    archive = build_decode_step(cfg, init_weights(cfg, seed=11))
+    P, S, Dh = cfg.planes, cfg.bucket, cfg.head_dim
+    caches = [bytes(P * S * Dh), bytes(P * S * 4), bytes(P * S * Dh), bytes(P * S * 4)] * cfg.layers
+    ins = step_inputs(cfg, 0, np.arange(cfg.batch) * 7) + caches
+    sess = HipSession(backend, archive)
+    first = sess.execute(ins)
+    again = sess.execute(ins)
+    assert sess.last_memo_hit and again == first
+    fresh = HipSession(backend, archive)
+    fresh.set_memo(False)
+    assert fresh.execute(ins) == first
+    sess.close()
+    fresh.close()

@@ -1,14 +1,15 @@
 """Benchmark of the MI355X hot path on one GPU; prints ONE JSON line.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only attn,lut,kv,gemm,e2e]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only attn,lut,copy,kv,gemm,w8a8,e2e]
 
 Headline (`value`): int8-KV GQA decode attention
 (B=32, H=32, Hkv=8, D=128, ragged L_b ~ U[512, 32768], bucket 32768, Q bf16,
 cache filled by the int8 quantize+append op) in tokens/s = B / step time.
 A step is one DecodeAttentionI8 dispatch over the whole batch, inputs
 resident in HBM. The other configs are reported under "components":
-LUT Gelem/s (config 1), GEMM TFLOP/s (config 2), KV append (config 3) and the
-end-to-end decoder through the `.holo` session (config 5, decode/prefill tok/s).
+LUT Gelem/s (config 1), GEMM TFLOP/s (config 2), KV append (config 3), the
+end-to-end decoder through the `.holo` session (config 5, decode/prefill tok/s)
+and the quantized-weight W8A8 GEMV (GMAC/s).
 Every number comes from HIP events on the stream the kernels run on: per step
 for the headline, and around a batch of back-to-back calls for the components
 (queued_ms), whose kernels are short enough that per-call events would count
@@ -58,7 +59,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--only", default="attn,lut,copy,kv,gemm,e2e")
+    p.add_argument("--only", default="attn,lut,copy,kv,gemm,w8a8,e2e")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--seed", type=int, default=1234)
     return p.parse_args()
@@ -677,6 +678,79 @@ def bench_copy(torch, be, args, rep):
     return res
 
 
+# ------------------------------------------------- quantized-weight GEMV ----
+def bench_w8a8(torch, be, args, rep):
+    """MatMulDequant's output-major W8A8 GEMV (the decode projection over a
+    quantized weight) at the reference's DRAM-streaming decode shape
+    (crates/hologram-bench/examples/gemv_micro.rs: m=1, k=2048, n=262144;
+    the i8 weight is 537 MB), for the i8 / i4 / e8cb tiers, and the i8 tier
+    at m=16 over a 64 MB weight (BENCHMARKS.md's blocked-prefill table).
+    GMAC/s = m*k*n per second; HBM bytes = weight + A + scales + output.
+    Weights rotate over >= 512 MiB so the 256 MiB last-level cache holds none."""
+    import numpy as np
+    from hologram_amd import (DTYPE_E8CB, DTYPE_I4, DTYPE_I8, BufferRef, DeviceWorkspace,
+                              KernelCall, MatMulDequantCall)
+    res = {}
+    cases = [("i8_decode", DTYPE_I8, 1, 2048, 262144), ("i4_decode", DTYPE_I4, 1, 2048, 262144),
+             ("e8cb_decode", DTYPE_E8CB, 1, 2048, 262144), ("i8_m16_64MB", DTYPE_I8, 16, 2048, 32768)]
+    for name, tier, m, k, n in cases:
+        wbytes = {DTYPE_I8: k * n, DTYPE_I4: k * n // 2, DTYPE_E8CB: k * n // 8}[tier]
+        nbuf = max(1, -(-(512 << 20) // wbytes))
+        ws = DeviceWorkspace()
+        gen = torch.Generator(device="cuda").manual_seed(args.seed)
+        a = torch.randn(m * k, generator=gen, device="cuda", dtype=torch.float32)
+        scales = torch.rand(n, generator=gen, device="cuda", dtype=torch.float32) * 0.01
+        zps = torch.zeros(n, dtype=torch.int32, device="cuda")
+        cb = torch.randint(-127, 128, (2048,), generator=gen, device="cuda",
+                           dtype=torch.int32).to(torch.int8)
+        out = torch.empty(m * n, dtype=torch.float32, device="cuda")
+        for s_, t in ((0, a), (2, scales), (3, zps), (4, out), (5, cb)):
+            ws.bind(s_, t)
+        calls = []
+        for i in range(nbuf):
+            w = torch.randint(0, 256, (wbytes,), generator=gen, device="cuda",
+                              dtype=torch.int32).to(torch.uint8)
+            ws.bind(10 + i, w)
+            calls.append(KernelCall.MatMulDequant(MatMulDequantCall(
+                BufferRef(0), BufferRef(10 + i), BufferRef(2), BufferRef(3), BufferRef(4), m, k, n,
+                channels=n, inner=1, quant_dtype=tier, bq_omajor=True, act_quant=1,
+                codebook=BufferRef(5) if tier == DTYPE_E8CB else BufferRef(0xFFFFFFFF))))
+        for i in range(max(args.warmup, 1)):
+            be.dispatch(calls[i % nbuf], ws)
+        be.synchronize()
+        ms = queued_ms(torch, lambda i: be.dispatch(calls[i % nbuf], ws), args.steps * 2)
+        be.synchronize()
+        alg = wbytes + m * k * 4 + n * 4 + m * n * 4
+        gbs = alg / (ms / 1e3) / 1e9
+        res[name] = {"m": m, "k": k, "n": n, "us": ms * 1e3,
+                     "gmac_s": m * k * n / (ms / 1e3) / 1e9,
+                     "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s",
+                                          profiled_traffic(f"w8a8_{name}"),
+                                          f"quant_rows_kernel + gemm_q_omajor_kernel; "
+                                          f"algorithmic bytes {alg}")}
+        del calls, ws
+        torch.cuda.empty_cache()
+    res["reference_published"] = {"i8_decode_gmac_s": 14.4, "i4_decode_gmac_s": 13.1,
+                                  "e8cb_decode_gmac_s": 27.0,
+                                  "machine": "AMD EPYC 7763 4c/8t AVX2, single thread "
+                                             "(BENCHMARKS.md:30-37)"}
+    if not args.no_cpu:
+        import oracle
+        k, n = 2048, 262144 // 16               # a 1/16 column slice of the decode shape
+        rng = np.random.default_rng(args.seed)
+        a = rng.standard_normal(k).astype(np.float32)
+        w = rng.integers(-128, 128, k * n).astype(np.int8)
+        sc = rng.uniform(0, 0.01, n).astype(np.float32)
+        sec, reps, _ = cpu_time(lambda: oracle.matmul_i8_pc_omajor(a, w, sc, 1, k, n), 3.0)
+        g = k * n / sec / 1e9
+        res["cpu_baseline"] = {"value": g, "unit": "GMAC/s", "cores": 1, "kind": "port",
+                               "sample": f"i8 m=1 k={k} n={n} (1/16 of the decode columns) "
+                                         f"x{reps} through the scalar oracle",
+                               "host": oracle.host_info()}
+    rep["w8a8"] = res
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -706,6 +780,9 @@ def main():
         torch.cuda.empty_cache()
     if "gemm" in only:
         bench_gemm(torch, be, args, rep)
+        torch.cuda.empty_cache()
+    if "w8a8" in only:
+        bench_w8a8(torch, be, args, rep)
         torch.cuda.empty_cache()
     if "e2e" in only:
         bench_e2e(torch, be, args, rep)
@@ -755,6 +832,8 @@ def main():
         comps["kv_quant_append"] = rep["kv"]
     if "gemm" in rep:
         comps["gemm"] = rep["gemm"]
+    if "w8a8" in rep:
+        comps["matmul_dequant_w8a8"] = rep["w8a8"]
     if attn:
         comps["decode_attn_i8"] = {k: attn[k] for k in ("tok_s", "hbm_gbs", "ms", "gflops",
                                                         "wall_ms_per_step")}

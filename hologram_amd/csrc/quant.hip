@@ -197,6 +197,167 @@ __global__ __launch_bounds__(256) void gemm_q_omajor_kernel(QGemm g) {
     }
 }
 
+// ----------------------------------------------------- W8A8 decode GEMV ----
+// Few rows (m <= 4): the dot products on v_dot4c_i32_i8 instead of MFMA, so
+// the weight stream is fully coalesced: a wavefront owns kGemvCols columns
+// and its 64 lanes sweep each column's k-vector in consecutive chunks (lane
+// l takes chunks l, l + 64, ...), one 16-byte (e8cb: 8-byte) load per column
+// per chunk; the int32 sums are exact, so the order of the lanes' partial sums
+// and of the cross-lane reduction does not matter. Chunks: i8 16 levels
+// (16 bytes), i4 32 levels (16 bytes: word t holds levels 8t .. 8t+7, even
+// levels in the low nibbles), e8cb 64 levels (8 codebook indices).
+constexpr int kGemvCols = 8;
+// Workgroups of the GEMV: each loops over column blocks (4 waves x kGemvCols
+// columns) with a grid stride, so the e8cb codebook is staged once per
+// workgroup and every wavefront streams several blocks.
+constexpr uint32_t kGemvGrid = 2048;
+
+// Reduce-scatter of N int32 values (N a power of two, <= 64) over the 64
+// lanes: each xor step halves the values a lane holds (it keeps the half its
+// lane bit selects and adds its partner's copy of that half), then plain xor
+// sums finish the strides left. Lane l ends with the wavefront's total of
+// value `index` (the bits the halving steps selected); integer sums are exact,
+// so the result is the plain total.
+template <int N, int S>
+struct Scatter {
+    static __device__ __forceinline__ void run(int32_t *v, int lane, int &index) {
+        constexpr int H = N / 2;
+        const bool up = (lane & S) != 0;
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            const int32_t send = up ? v[i] : v[i + H];
+            const int32_t recv = __shfl_xor(send, S, 64);
+            v[i] = (up ? v[i + H] : v[i]) + recv;
+        }
+        if (up) index += H;
+        Scatter<H, S / 2>::run(v, lane, index);
+    }
+};
+template <int S>
+struct Scatter<1, S> {
+    static __device__ __forceinline__ void run(int32_t *v, int lane, int &index) {
+        v[0] += __shfl_xor(v[0], S, 64);
+        Scatter<1, S / 2>::run(v, lane, index);
+    }
+};
+template <>
+struct Scatter<1, 0> {
+    static __device__ __forceinline__ void run(int32_t *, int, int &) {}
+};
+
+template <int TIER>
+struct GemvChunk {
+    static constexpr uint32_t elems = TIER == 2 ? 16 : (TIER == 10 ? 32 : 64);
+    static constexpr uint32_t bytes = TIER == 11 ? 8 : 16;
+};
+
+template <int TIER, int M>
+__global__ __launch_bounds__(256) void gemv_q_omajor_kernel(QGemm g) {
+    using Ch = GemvChunk<TIER>;
+    __shared__ __attribute__((aligned(16))) int8_t cbb[TIER == 11 ? 256 * 8 : 16];
+    if constexpr (TIER == 11) {
+        for (int i = threadIdx.x; i < 256 * 8; i += 256) cbb[i] = g.codebook[i];
+        __syncthreads();
+    }
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t nchunk = g.k / Ch::elems;
+    const uint64_t col_bytes = uint64_t(g.k) * Ch::bytes / Ch::elems;
+    const uint32_t nblk = (g.n + 4 * kGemvCols - 1) / (4 * kGemvCols);
+    for (uint32_t blk = blockIdx.x; blk < nblk; blk += gridDim.x) {
+    const uint32_t j0 = (blk * 4 + wave) * kGemvCols;
+    int32_t acc[M][kGemvCols];
+    int32_t corr[M];   // i4: the sum of the activation levels (the nibble bias)
+#pragma unroll
+    for (int r = 0; r < M; ++r) {
+        corr[r] = 0;
+#pragma unroll
+        for (int c = 0; c < kGemvCols; ++c) acc[r][c] = 0;
+    }
+    for (uint32_t ch = lane; ch < nchunk; ch += 64) {
+        // every column's chunk first, so the loads are in flight together
+        u32x4 w[kGemvCols];
+        uint64_t wi[kGemvCols];
+#pragma unroll
+        for (int c = 0; c < kGemvCols; ++c) {
+            const uint32_t j = j0 + c < g.n ? j0 + c : g.n - 1;   // a clamped column is never stored
+            const uint8_t *p = g.bq + uint64_t(j) * col_bytes + uint64_t(ch) * Ch::bytes;
+            if constexpr (TIER == 11) wi[c] = *reinterpret_cast<const uint64_t *>(p);
+            else w[c] = ld_stream(reinterpret_cast<const u32x4 *>(p));
+        }
+#pragma unroll
+        for (int r = 0; r < M; ++r) {
+            const u32x4 *qa = reinterpret_cast<const u32x4 *>(g.q + uint64_t(r) * g.kpad +
+                                                             uint64_t(ch) * Ch::elems);
+            if constexpr (TIER == 2) {
+                const u32x4 x = qa[0];
+#pragma unroll
+                for (int c = 0; c < kGemvCols; ++c)
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        acc[r][c] = __builtin_amdgcn_sdot4(int(x[t]), int(w[c][t]), acc[r][c], false);
+            } else if constexpr (TIER == 10) {
+                const u32x4 x0 = qa[0], x1 = qa[1];
+                const uint32_t xa[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    // levels 8t .. 8t+7: even ones (low nibbles) and odd ones (high)
+                    const uint32_t lo = __builtin_amdgcn_perm(xa[2 * t + 1], xa[2 * t], 0x06040200u);
+                    const uint32_t hi = __builtin_amdgcn_perm(xa[2 * t + 1], xa[2 * t], 0x07050301u);
+                    corr[r] = __builtin_amdgcn_sdot4(int(xa[2 * t]), 0x01010101, corr[r], false);
+                    corr[r] = __builtin_amdgcn_sdot4(int(xa[2 * t + 1]), 0x01010101, corr[r], false);
+#pragma unroll
+                    for (int c = 0; c < kGemvCols; ++c) {
+                        // a nibble u, as (u ^ 8) in 0..15: its signed level is (u ^ 8) - 8
+                        const uint32_t b = w[c][t] ^ 0x88888888u;
+                        acc[r][c] = __builtin_amdgcn_sdot4(int(lo), int(b & 0x0F0F0F0Fu), acc[r][c], false);
+                        acc[r][c] = __builtin_amdgcn_sdot4(int(hi), int((b >> 4) & 0x0F0F0F0Fu), acc[r][c],
+                                                           false);
+                    }
+                }
+            } else {
+                const u32x4 x0 = qa[0], x1 = qa[1], x2 = qa[2], x3 = qa[3];
+                const uint32_t xa[16] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3],
+                                         x2[0], x2[1], x2[2], x2[3], x3[0], x3[1], x3[2], x3[3]};
+#pragma unroll
+                for (int c = 0; c < kGemvCols; ++c)
+#pragma unroll
+                    for (int h = 0; h < 8; ++h) {
+                        const uint32_t half = h < 4 ? uint32_t(wi[c]) : uint32_t(wi[c] >> 32);
+                        const uint32_t idx = (half >> (8 * (h & 3))) & 0xffu;
+                        const uint64_t v = *reinterpret_cast<const uint64_t *>(cbb + idx * 8);
+                        acc[r][c] = __builtin_amdgcn_sdot4(int(xa[2 * h]), int(uint32_t(v)), acc[r][c], false);
+                        acc[r][c] = __builtin_amdgcn_sdot4(int(xa[2 * h + 1]), int(uint32_t(v >> 32)),
+                                                           acc[r][c], false);
+                    }
+            }
+        }
+    }
+    // exact int32 totals over the wavefront (the i4 bias folded in first: the
+    // totals are linear in the lanes' sums); M = 3 is padded to four rows
+    constexpr int MP = M == 3 ? 4 : M;
+    int32_t v[MP * kGemvCols];
+#pragma unroll
+    for (int r = 0; r < MP; ++r)
+#pragma unroll
+        for (int c = 0; c < kGemvCols; ++c)
+            v[r * kGemvCols + c] = r < M ? (TIER == 10 ? acc[r][c] - 8 * corr[r] : acc[r][c]) : 0;
+    int index = 0;
+    Scatter<MP * kGemvCols, 32>::run(v, lane, index);
+    if ((lane & (64 / (MP * kGemvCols) - 1)) == 0) {
+        const int r = index / kGemvCols, c = index % kGemvCols;
+        const int32_t tot = v[0];
+        const uint32_t j = j0 + c;
+        if (uint32_t(r) < g.m && j < g.n) {
+            const float si = g.sa[r], sj = g.scales[j];
+            float o = si == 0.0f ? 0.0f : float(tot) * (si * sj);
+            if (g.residual) o = o + g.residual[uint64_t(r) * g.n + j];
+            if (g.act) o = act_f32(g.act, o);
+            g.out[uint64_t(r) * g.n + j] = o;
+        }
+    }
+    }
+}
+
 // ------------------------------------------------------------- Dequantize ----
 struct DqArgs {
     const uint8_t *in;
@@ -304,6 +465,32 @@ hipError_t launch_matmul_q_omajor(const QOmajorArgs &a, void *scratch, hipStream
     g.n = a.n;
     g.kpad = kpad;
     g.act = a.act;
+    // the decode GEMV when its whole chunks tile k and the loads are aligned
+    const uint32_t ce = a.tier == 2 ? 16 : (a.tier == 10 ? 32 : 64);
+    const uintptr_t bal = a.tier == 11 ? 7 : 15;
+    if (a.m <= 4 && a.k % ce == 0 && (reinterpret_cast<uintptr_t>(a.bq) & bal) == 0) {
+        const uint32_t nblk = (a.n + 4 * kGemvCols - 1) / (4 * kGemvCols);
+        const dim3 gg(nblk < kGemvGrid ? nblk : kGemvGrid);
+#define HOLO_QV(T, M) hipLaunchKernelGGL((gemv_q_omajor_kernel<T, M>), gg, dim3(256), 0, stream, g)
+#define HOLO_QVM(T)                         \
+    do {                                    \
+        switch (a.m) {                      \
+            case 1: HOLO_QV(T, 1); break;   \
+            case 2: HOLO_QV(T, 2); break;   \
+            case 3: HOLO_QV(T, 3); break;   \
+            default: HOLO_QV(T, 4); break;  \
+        }                                   \
+    } while (0)
+        switch (a.tier) {
+            case 2: HOLO_QVM(2); break;
+            case 10: HOLO_QVM(10); break;
+            case 11: HOLO_QVM(11); break;
+            default: return hipErrorInvalidValue;
+        }
+#undef HOLO_QVM
+#undef HOLO_QV
+        return hipGetLastError();
+    }
     const bool tall = a.m > 16;
     const dim3 grid((a.n + 15) / 16, tall ? (a.m + 63) / 64 : 1);
 #define HOLO_QG(T)                                                                            \

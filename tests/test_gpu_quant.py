@@ -82,8 +82,11 @@ def w8a8_operands(rng, tier, m, k, n):
     return a, bq, scales, cb
 
 
+# m <= 4 with whole chunks (k a multiple of 16 / 32 / 64 per tier) takes the
+# dot4 GEMV; the rest the MFMA GEMM
 W8A8_SHAPES = [(1, 896, 4864), (1, 4096, 64), (3, 64, 17), (16, 128, 16), (17, 256, 33),
-               (64, 512, 48), (70, 1024, 100), (5, 8, 3)]
+               (64, 512, 48), (70, 1024, 100), (5, 8, 3), (2, 2048, 1000), (4, 1024, 33),
+               (1, 64, 1), (1, 2048, 16385)]
 
 
 @pytest.mark.parametrize("tier", [DTYPE_I8, DTYPE_I4, DTYPE_E8CB])

@@ -39,6 +39,39 @@ constexpr uint32_t kEpiThreads = 64;
 __device__ __forceinline__ float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
 __device__ __forceinline__ uint32_t f2bf(float f) { return __float_as_uint(f) >> 16; }
 
+// Segment i, copied out of the kernel arguments field by field with
+// constant indices: a reference picked at run time makes the compiler copy
+// the whole argument block to scratch memory on entry.
+__device__ __forceinline__ EpiSeg seg_of(const EpiArgs &g, uint32_t i) {
+    EpiSeg s;
+#define HOLO_SEG_FIELD(F) \
+    s.F = i == 0 ? g.seg[0].F : i == 1 ? g.seg[1].F : i == 2 ? g.seg[2].F : g.seg[3].F
+    HOLO_SEG_FIELD(n);
+    HOLO_SEG_FIELD(col0);
+    HOLO_SEG_FIELD(base);
+    HOLO_SEG_FIELD(act);
+    HOLO_SEG_FIELD(lut);
+    HOLO_SEG_FIELD(residual);
+    HOLO_SEG_FIELD(out);
+    HOLO_SEG_FIELD(head_dim);
+    HOLO_SEG_FIELD(rope);
+    HOLO_SEG_FIELD(cos);
+    HOLO_SEG_FIELD(sin);
+    HOLO_SEG_FIELD(rope_out);
+    HOLO_SEG_FIELD(quant);
+    HOLO_SEG_FIELD(pos);
+    HOLO_SEG_FIELD(cq);
+    HOLO_SEG_FIELD(cs);
+    HOLO_SEG_FIELD(bucket);
+    HOLO_SEG_FIELD(new_rows);
+    HOLO_SEG_FIELD(pair);
+    HOLO_SEG_FIELD(mul_out);
+    HOLO_SEG_FIELD(skip);
+    HOLO_SEG_FIELD(ssq);
+#undef HOLO_SEG_FIELD
+    return s;
+}
+
 // Segment of this workgroup (workgroup-uniform, chosen with selects).
 __device__ __forceinline__ int pick(const EpiArgs &g, uint32_t *first_block) {
     int s = 0;
@@ -160,7 +193,7 @@ __device__ __forceinline__ int8_t to_q(float r) {
 // Element-wise segments: 4 consecutive columns of one row per thread. The
 // residual and both segments' partials are loaded before any arithmetic.
 template <bool kBf16>
-__device__ void elem_segment(const EpiArgs &g, const EpiSeg &sg, const EpiSeg &pr, uint32_t blk) {
+__device__ __forceinline__ void elem_segment(const EpiArgs &g, const EpiSeg &sg, const EpiSeg &pr, uint32_t blk) {
     const uint64_t i = (uint64_t(blk) * kEpiThreads + threadIdx.x) * 4;
     if (i >= uint64_t(g.m) * sg.n) return;
     const uint32_t m = uint32_t(i / sg.n), c = uint32_t(i % sg.n);
@@ -218,7 +251,7 @@ __device__ void elem_segment(const EpiArgs &g, const EpiSeg &sg, const EpiSeg &p
 // Head-wise segments (rope and/or quant): a head of D = head_dim columns is
 // D/2 lanes, lane d holding the rotate-half pair (d, d + D/2).
 template <bool kBf16>
-__device__ void head_segment(const EpiArgs &g, const EpiSeg &sg, uint32_t blk) {
+__device__ __forceinline__ void head_segment(const EpiArgs &g, const EpiSeg &sg, uint32_t blk) {
     const uint32_t D = sg.head_dim, half = D / 2;
     const uint32_t heads_per_block = kEpiThreads / half;
     const uint32_t hl = threadIdx.x / half, d = threadIdx.x % half;
@@ -365,13 +398,13 @@ template <bool kBf16>
 __global__ __launch_bounds__(kEpiThreads) void epilogue_kernel(const EpiArgs g) {
     uint32_t b0;
     const int s = pick(g, &b0);
-    const EpiSeg &sg = s == 0 ? g.seg[0] : s == 1 ? g.seg[1] : s == 2 ? g.seg[2] : g.seg[3];
+    const EpiSeg sg = seg_of(g, uint32_t(s));
     const uint32_t blk = blockIdx.x - b0;
     if (sg.head_dim) {
         head_segment<kBf16>(g, sg, blk);
     } else {
         const int p = sg.pair < 0 ? 0 : sg.pair;
-        const EpiSeg &pr = p == 0 ? g.seg[0] : p == 1 ? g.seg[1] : p == 2 ? g.seg[2] : g.seg[3];
+        const EpiSeg pr = seg_of(g, uint32_t(p));
         elem_segment<kBf16>(g, sg, pr, blk);
     }
 }

@@ -30,6 +30,24 @@
  *                                 preserve the pair's norm); angle 0 = identity
  *   or_gather .................. brute-force row indexing, negative wrap
  *   or_argmax .................. numpy argmax (NaN-free rows), first-index ties
+ *   or_libm_erff ............... correctly-rounded erf (<= 1 ulp on every finite
+ *                                 bf16 input and 450,000 sampled f32), odd
+ *                                 symmetry, special values
+ *   or_matmul_q_omajor ......... reference goldens for the i8, i4 and e8cb tiers
+ *                                 (simd.rs:8236-8283)
+ *   or_dequantize .............. reference known answers (conformance.rs:936-1009),
+ *                                 exact (q - zp) * scale, nibble order, i32 wrap
+ *   or_dequant_activation ...... the unfused pair (or_dequantize then the
+ *                                 activation) bit for bit; f64 GELU tracking
+ *   or_add_rms_norm ............ RmsNorm bit for bit without a residual; the
+ *                                 unnarrowed f32 sum; f64 closed form (f32)
+ *   or_decode_attention_valid .. f64 softmax law over the causal visible set
+ *   pack_b_panels (Python) ..... the layout formula (layout.rs:16-45)
+ *
+ * Parity unpinned: the 126 signaling-NaN inputs of the bf16/f16 SiLU tables
+ * and NaN payloads of the Exp table (IEEE quieting assumed); Erf table entries
+ * are pinned to within one ulp of the correctly rounded erf, not bit for bit
+ * against libm 0.2.16 (not vendored in the reference).
  */
 #ifndef HOLO_ORACLE_H
 #define HOLO_ORACLE_H

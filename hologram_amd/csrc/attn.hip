@@ -72,6 +72,16 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
+// A workgroup barrier over LDS only: each wave waits for its own LDS accesses
+// (lgkmcnt 0), then s_barrier, without __syncthreads' release fence, which
+// would also wait for every load in flight (the prefetched key blocks).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));   // lgkmcnt(0); vmcnt, expcnt untouched
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // V^T operand of the PV MFMA: dim t of the lane's 4-byte segment, for the
 // lane's 8 keys (words w[0..7], bytes already xor 0x80), as 8 exact f16.
 // Two byte permutes interleave a key pair, two more place each byte under the
@@ -306,11 +316,20 @@ __device__ __forceinline__ void attn_segment(
         if (g == 0) lds.smul[r] = ldexpf(1.0f, -qe);   // the k-scales carry log2(e)/scale
     }
     u32x4 sreg = load_sc(0);
-    // Wavefront wv takes every fourth 32-key block of the segment; one block is
-    // in flight (prefetched into registers) while the previous is computed.
-    const uint32_t first = c0 + wv * kBlock;
-    Blk cur;
-    if (first < c1) load(first, cur);
+    // Wavefront wv takes every fourth 32-key block of the segment, with its
+    // next PD - 1 blocks in flight while one is computed: at head_dim 64 a
+    // decode step's short contexts give a wavefront only a few blocks, which
+    // one block in flight would fetch one latency at a time. The blocks sit in
+    // a ring indexed by the block's position in its 4-block super-block pass,
+    // a constant once that loop is unrolled, so no register is moved while its
+    // load is in flight.
+    constexpr int PD = D <= 64 ? 4 : 2;
+    Blk ring[PD];
+#pragma unroll
+    for (int p = 0; p < PD - 1; ++p) {
+        const uint32_t bb = c0 + uint32_t(p) * kQuad + wv * kBlock;
+        if (bb < c1) load(bb, ring[p]);
+    }
 
     f32x4 acc_o[NDB];
 #pragma unroll
@@ -319,7 +338,7 @@ __device__ __forceinline__ void attn_segment(
     int ve = kVeMin;
 
     store_sc(0, sreg);
-    __syncthreads();
+    lds_barrier();   // Q operands and the first scales; the blocks stay in flight
     const float smul = lds.smul[r];
     // kPack: this lane's column limit, and the smallest limit (blocks ending
     // past it need the per-key test)
@@ -404,13 +423,11 @@ __device__ __forceinline__ void attn_segment(
         }
     };
 
-    // Every wavefront walks the same 4 * nsb quads (the barriers must match);
-    // its block of a quad past c1 is skipped.
-    for (uint32_t it = 0; it < 4 * nsb; ++it) {
-        const uint32_t sb = it >> 2;
-        if ((it & 3) == 0) {
-            if (sb + 1 < nsb) sreg = load_sc(sb + 1);
-            // 2^ve bounds every v-scale of this super-block (all wavefronts alike)
+    // Every wavefront walks the same nsb super-blocks of 4 quads (the barriers
+    // must match); its block of a quad past c1 is skipped.
+    for (uint32_t sb = 0; sb < nsb; ++sb) {
+        if (sb + 1 < nsb) sreg = load_sc(sb + 1);
+        {   // 2^ve bounds every v-scale of this super-block (all wavefronts alike)
             const float vb = fmaxf(lds.svmax[sb & 1][0], lds.svmax[sb & 1][1]);
             if (vb > ldexpf(1.0f, ve) && vb <= 3.0e38f) {
                 int ve_new;
@@ -423,20 +440,19 @@ __device__ __forceinline__ void attn_segment(
                 mv = m_run + float(ve);
             }
         }
-        const uint32_t blk = c0 + it * kQuad + wv * kBlock;
-        if (blk < c1) {
-            const uint32_t nb = blk + kQuad;
-            Blk nxt;
-            if (nb < c1) load(nb, nxt);
-            const uint32_t so = (it & 3) * kQuad + wv * kBlock;
-            const float *skp = lds.sk[sb & 1] + so, *svp = lds.sv[sb & 1] + so;
-            block(blk + kBlock > lim_min, cur, blk, skp, svp);
-            cur = nxt;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t blk = c0 + (4 * sb + uint32_t(i)) * kQuad + wv * kBlock;
+            if (blk < c1) {
+                const uint32_t nb = blk + (PD - 1) * kQuad;
+                if (nb < c1) load(nb, ring[(i + PD - 1) % PD]);
+                const uint32_t so = uint32_t(i) * kQuad + wv * kBlock;
+                const float *skp = lds.sk[sb & 1] + so, *svp = lds.sv[sb & 1] + so;
+                block(blk + kBlock > lim_min, ring[i % PD], blk, skp, svp);
+            }
         }
-        if ((it & 3) == 3) {
-            if (sb + 1 < nsb) store_sc(sb + 1, sreg);
-            __syncthreads();
-        }
+        if (sb + 1 < nsb) store_sc(sb + 1, sreg);
+        lds_barrier();
     }
 
     // ---- wavefront state -> LDS, merge the four wavefronts per head

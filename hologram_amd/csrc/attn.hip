@@ -199,9 +199,15 @@ __device__ __forceinline__ void attn_segment(
         uint32_t v[8][VW];
     };
     // The per-row constants ride in the scalar offset: only koff and voff stay
-    // in vector registers across the loop.
-    auto load = [&](uint32_t blk, Blk &o) {
-        const int kvs = int(blk * D);
+    // in vector registers across the loop. A block that is not `live` loads
+    // nothing: its scalar offset starts at the end of the plane's buffer range,
+    // where buffer loads return 0 without a memory access. So no load sits
+    // behind a branch, and the compiler keeps an exact count of the loads in
+    // flight (a branch around a load makes it wait for all of them at the
+    // join, and the prefetched block would be waited for at once).
+    const int kvs_none = int(bucket * D);
+    auto load = [&](uint32_t blk, bool live, Blk &o) {
+        const int kvs = live ? int(blk * D) : kvs_none;
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
@@ -221,9 +227,10 @@ __device__ __forceinline__ void attn_segment(
     };
     // Super-block scales: wavefronts 0-1 load the 512 k-scales, 2-3 the
     // v-scales, four keys per thread.
+    const uint32_t nsb = (c1 - c0 + kSuper - 1) / kSuper;
     const uint32_t st = uint32_t(tid) & 127u;
-    auto load_sc = [&](uint32_t sb) -> u32x4 {
-        const int so = int((c0 + sb * kSuper) * 4);
+    auto load_sc = [&](uint32_t sb) -> u32x4 {   // sb >= nsb loads nothing
+        const int so = sb < nsb ? int((c0 + sb * kSuper) * 4) : int(bucket * 4);
         return wv < 2 ? __builtin_amdgcn_raw_buffer_load_b128(rks, int(16 * st), so, 0)
                       : __builtin_amdgcn_raw_buffer_load_b128(rvs, int(16 * st), so, 0);
     };
@@ -248,7 +255,6 @@ __device__ __forceinline__ void attn_segment(
     // Wavefront 0 turns Q into the MFMA operands (in LDS, shared by the four
     // wavefronts); its loads go out first. Lanes of padding heads (r >= G)
     // read head 0 and zero it.
-    const uint32_t nsb = (c1 - c0 + kSuper - 1) / kSuper;
     if (wv == 0) {
         float qv[KB];
         const uint32_t cols = kPack ? G * prow : G;
@@ -328,7 +334,7 @@ __device__ __forceinline__ void attn_segment(
 #pragma unroll
     for (int p = 0; p < PD - 1; ++p) {
         const uint32_t bb = c0 + uint32_t(p) * kQuad + wv * kBlock;
-        if (bb < c1) load(bb, ring[p]);
+        load(bb, bb < c1, ring[p]);
     }
 
     f32x4 acc_o[NDB];
@@ -426,7 +432,7 @@ __device__ __forceinline__ void attn_segment(
     // Every wavefront walks the same nsb super-blocks of 4 quads (the barriers
     // must match); its block of a quad past c1 is skipped.
     for (uint32_t sb = 0; sb < nsb; ++sb) {
-        if (sb + 1 < nsb) sreg = load_sc(sb + 1);
+        sreg = load_sc(sb + 1);
         {   // 2^ve bounds every v-scale of this super-block (all wavefronts alike)
             const float vb = fmaxf(lds.svmax[sb & 1][0], lds.svmax[sb & 1][1]);
             if (vb > ldexpf(1.0f, ve) && vb <= 3.0e38f) {
@@ -443,9 +449,9 @@ __device__ __forceinline__ void attn_segment(
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t blk = c0 + (4 * sb + uint32_t(i)) * kQuad + wv * kBlock;
+            const uint32_t nb = blk + (PD - 1) * kQuad;
+            load(nb, nb < c1, ring[(i + PD - 1) % PD]);
             if (blk < c1) {
-                const uint32_t nb = blk + (PD - 1) * kQuad;
-                if (nb < c1) load(nb, ring[(i + PD - 1) % PD]);
                 const uint32_t so = uint32_t(i) * kQuad + wv * kBlock;
                 const float *skp = lds.sk[sb & 1] + so, *svp = lds.sv[sb & 1] + so;
                 block(blk + kBlock > lim_min, ring[i % PD], blk, skp, svp);

@@ -697,6 +697,151 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_pair_kernel(const DmaGro
 // checked by the caller): K a multiple of 128 and >= 256, at least
 // kBigMinTiles 256x256 tiles, and 256 rows of A / 32 rows of B within
 // a 32-bit buffer range.
+// ------------------------------------------- bf16, 64x64 tiles, LDS DMA ----
+// Mid-size products (fewer than 256 128x128 tiles, e.g. 1024^3): one 64x64
+// tile per workgroup, so 1024^3 runs 256 workgroups, one per CU. Each wave
+// owns a 32x32 block on v_mfma_f32_32x32x16_bf16. With so little MFMA work
+// per K step the tile is bound by how many operand bytes it keeps in flight,
+// so A [64][64 k] and B [64 k][64] slabs go by DMA into an 8-stage LDS ring
+// (16 KiB per stage, 128 KiB): seven slabs (112 KiB) are in flight while one
+// is multiplied. Slab layouts are the large-tile kernel's with 128-byte rows:
+// A row r holds its eight 16-byte k-chunks at chunk ^ ((r >> 1) & 7), so the
+// 16-byte fragment reads of 8 consecutive rows hit distinct banks; B k-row k
+// holds its eight column chunks at chunk ^ 4 ((k >> 1) & 1), so the
+// transposing reads of k-rows k0..k0+3 fill one 256-byte bank row. The loop is
+// unrolled by the ring depth (stage indices are constants, no load behind a
+// branch); a slab past K loads nothing (its buffer range is empty). MFMA order
+// per output element: k ascending in steps of 16.
+constexpr int kD64K = 64, kD64Stages = 8;
+constexpr uint32_t kD64Stage = 16384, kD64OffB = 8192;
+
+__device__ __forceinline__ uint32_t swz_a64(uint32_t row) { return (row >> 1) & 7u; }
+__device__ __forceinline__ uint32_t swz_b64(uint32_t k) { return 4u * ((k >> 1) & 1u); }
+
+__global__ __launch_bounds__(kThreads, 1) void gemm_bf16_dma64_kernel(const uint16_t *__restrict__ A,
+                                                                      const uint16_t *__restrict__ B,
+                                                                      uint16_t *__restrict__ C,
+                                                                      uint32_t M, uint32_t N,
+                                                                      uint32_t K) {
+    __shared__ __attribute__((aligned(1024))) uint8_t l0[kD64Stage], l1[kD64Stage], l2[kD64Stage],
+        l3[kD64Stage], l4[kD64Stage], l5[kD64Stage], l6[kD64Stage], l7[kD64Stage];
+    auto stage = [&](auto st) -> lds_u8 * {
+        constexpr int kS = decltype(st)::value % kD64Stages;
+        return kS == 0 ? (lds_u8 *)l0 : kS == 1 ? (lds_u8 *)l1 : kS == 2 ? (lds_u8 *)l2
+             : kS == 3 ? (lds_u8 *)l3 : kS == 4 ? (lds_u8 *)l4 : kS == 5 ? (lds_u8 *)l5
+             : kS == 6 ? (lds_u8 *)l6 : (lds_u8 *)l7;
+    };
+    uint32_t tm, tn;
+    tile_coords(blockIdx.x, gridDim.x, M / 64, N / 64, &tm, &tn);
+    const uint32_t m0 = tm * 64, n0 = tn * 64;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t wu = __builtin_amdgcn_readfirstlane(wave);
+    const int lr = lane & 31, lg = lane >> 5;
+
+    // DMA: per slab each wave fills 2 KiB of A (rows 16 w .. 16 w + 15) and
+    // 2 KiB of B (k-rows 16 w .. 16 w + 15), 8 rows of 8 chunks per load.
+    uint32_t a_voff[2], b_voff[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const uint32_t row = 16u * wave + 8u * t + lane / 8;
+        a_voff[t] = (row * K + 8u * ((lane & 7) ^ swz_a64(row))) * 2u;
+        b_voff[t] = (row * N + 8u * ((lane & 7) ^ swz_b64(row))) * 2u;
+    }
+    const uint32_t nk = K / kD64K;
+    auto dma = [&](uint32_t slab, auto st) {
+        const bool live = slab < nk;
+        const uint32_t k0 = live ? slab * kD64K : 0u;
+        const auto ra = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t *>(A + uint64_t(m0) * K + k0), 0, live ? int(128u * K) : 0, 0x00020000);
+        const auto rb = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t *>(B + uint64_t(k0) * N + n0), 0, live ? int(128u * N) : 0, 0x00020000);
+        lds_u8 *sa = stage(st) + wu * 2048u;
+        lds_u8 *sb = stage(st) + kD64OffB + wu * 2048u;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, sa + 1024 * t, 16, a_voff[t], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, sb + 1024 * t, 16, b_voff[t], 0, 0, 0);
+    };
+
+    // fragment offsets within a stage. A: row 32 (w / 2) + lr, logical chunk
+    // kk/8 + lg. B: lane (g, r) of its 16-lane group addresses k-row
+    // 8 (g / 2) + r / 4 (+ kk, and + 4 for the second read), column
+    // 32 (w % 2) + 16 (g % 2) + 4 (r % 4).
+    const uint32_t arow = 32u * (wave >> 1) + lr;
+    uint32_t a_frag[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) a_frag[q] = arow * 128u + (((2u * q + lg) ^ swz_a64(arow)) * 16u);
+    uint32_t b_frag;
+    {
+        const uint32_t g = lane >> 4, r = lane & 15;
+        const uint32_t k = 8u * (g >> 1) + (r >> 2);
+        const uint32_t n = 32u * (wave & 1) + 16u * (g & 1) + 4u * (r & 3);
+        b_frag = kD64OffB + k * 128u + (((n >> 3) ^ swz_b64(k)) * 16u) + (n & 7u) * 2u;
+    }
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+
+    // Slab s in stage s % 8: wait for its DMA (the six slabs issued after it
+    // may stay in flight), barrier (every wave's share landed, and every wave
+    // is done reading the stage refilled next), issue slab s + 7 into the
+    // stage slab s - 1 used, then four k-steps.
+    auto step = [&](uint32_t s, auto st) {
+        constexpr int kS = decltype(st)::value;
+        wait_vm<4 * (kD64Stages - 2)>();
+        slab_barrier();
+        dma(s + kD64Stages - 1, std::integral_constant<int, kS + kD64Stages - 1>{});
+        const lds_u8 *base = stage(st);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const bf16x8 af = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8 *>(base + a_frag[q]);
+            const lds_u8 *p = base + b_frag + 128u * 16u * q;
+            const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                reinterpret_cast<lds_v4i16 *>(const_cast<lds_u8 *>(p)));
+            const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                reinterpret_cast<lds_v4i16 *>(const_cast<lds_u8 *>(p + 512u)));
+            const bf16x8 bf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf, acc, 0, 0, 0);
+        }
+    };
+#pragma unroll
+    for (int p = 0; p < kD64Stages - 1; ++p) {
+        // prologue: slabs 0..6 (constant stage indices through the switch)
+        switch (p) {
+        case 0: dma(0, std::integral_constant<int, 0>{}); break;
+        case 1: dma(1, std::integral_constant<int, 1>{}); break;
+        case 2: dma(2, std::integral_constant<int, 2>{}); break;
+        case 3: dma(3, std::integral_constant<int, 3>{}); break;
+        case 4: dma(4, std::integral_constant<int, 4>{}); break;
+        case 5: dma(5, std::integral_constant<int, 5>{}); break;
+        default: dma(6, std::integral_constant<int, 6>{}); break;
+        }
+    }
+    for (uint32_t s = 0; s < nk; s += kD64Stages) {   // nk is a multiple of 8
+        step(s + 0, std::integral_constant<int, 0>{});
+        step(s + 1, std::integral_constant<int, 1>{});
+        step(s + 2, std::integral_constant<int, 2>{});
+        step(s + 3, std::integral_constant<int, 3>{});
+        step(s + 4, std::integral_constant<int, 4>{});
+        step(s + 5, std::integral_constant<int, 5>{});
+        step(s + 6, std::integral_constant<int, 6>{});
+        step(s + 7, std::integral_constant<int, 7>{});
+    }
+    // 32x32 D layout: acc[r] is row 8 (r / 4) + 4 lg + r % 4, column lr;
+    // bf16 by truncation
+    uint16_t *cb = C + uint64_t(m0 + 32u * (wave >> 1) + 4u * lg) * N + n0 + 32u * (wave & 1) + lr;
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+        cb[uint64_t(8 * (r >> 2) + (r & 3)) * N] = uint16_t(__float_as_uint(acc[r]) >> 16);
+}
+
+bool dma64_applies(uint32_t m, uint32_t k, uint32_t n) {
+    return m % 64 == 0 && n % 64 == 0 && k % (kD64K * kD64Stages) == 0 && k < (1u << 23) &&
+           n < (1u << 23) && m >= 64 && n >= 64;
+}
+
 bool dma_applies(uint32_t m, uint32_t k, uint32_t n) {
     return m % kBigM == 0 && n % kBigN == 0 && k % (2 * kBigK) == 0 && k >= 4 * kBigK &&
            k < (1u << 22) && n < (1u << 24) &&
@@ -776,6 +921,13 @@ hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint
             g.c[0] = static_cast<uint16_t *>(c);
             g.n[0] = n;
             return launch_dma(g, stream);
+        }
+        // mid-size aligned problems: 64x64 tiles fed by LDS DMA
+        if (small && ((al | reinterpret_cast<uintptr_t>(c)) & 15) == 0 && dma64_applies(m, k, n)) {
+            hipLaunchKernelGGL(gemm_bf16_dma64_kernel, dim3((m / 64) * (n / 64)), dim3(kThreads), 0,
+                               stream, static_cast<const uint16_t *>(a),
+                               static_cast<const uint16_t *>(b), static_cast<uint16_t *>(c), m, n, k);
+            return hipGetLastError();
         }
         const bool fast = (al & 15) == 0 && k % BK16 == 0 && n % 8 == 0;
         HOLO_GEMM_LAUNCH(gemm_bf16_kernel, uint16_t);

@@ -47,6 +47,17 @@ def test_matmul_parity(torch_cuda, backend, m, k, n, dtype, tol):
     assert err <= tol, f"normalized error {err:.3g}"
 
 
+@pytest.mark.parametrize("m,k,n", [(64, 512, 64), (192, 1024, 320), (1024, 2048, 512),
+                                   (512, 4096, 64), (960, 512, 1984)])
+def test_matmul_bf16_dma64_parity(torch_cuda, backend, m, k, n):
+    """Mid-size bf16 shapes taken by the 64x64-tile DMA kernel (m, n multiples of
+    64, k a multiple of 512, fewer than 256 128x128 tiles), including tile
+    counts that are not a multiple of the 8 XCDs and the shortest K (8 slabs)."""
+    got, want = run_mm(torch_cuda, backend, m, k, n, DTYPE_BF16, seed=m + 3 * n + k)
+    err = oracle.max_rel_err(got, want)
+    assert err <= 1e-2, f"normalized error {err:.3g}"
+
+
 def test_bf16_truncates(torch_cuda, backend):
     """bf16 narrowing is truncation (write_bf16, src/cpu/dtype.rs:75-79): the single
     exact product (1 + 2^-7) * 1.5 = 0x3FC18000 narrows to 0x3FC1, where rounding to

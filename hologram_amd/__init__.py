@@ -13,9 +13,9 @@ from .backend import (BackendError, DeviceWorkspace, DispatchError, HipBackend, 
                       validate)
 from .kernel_call import (DTYPE_BF16, DTYPE_E8CB, DTYPE_F16, DTYPE_F32, DTYPE_I4, DTYPE_I8,
                           DTYPE_I32, DTYPE_I64, DTYPE_U8, NO_BUFFER, SLOT_ABSENT, ArgMaxCall,
-                          AttentionI8RowsCall, BinaryCall, BufferRef, DecodeAttentionI8Call,
-                          DecodeAttentionValidCall, DequantActivationCall, DequantizeCall,
-                          GatherCall, KernelCall, KvCacheWriteCall, KvQuantAppendCall,
+                          AttentionI8RowsCall, BinaryCall, BufferRef, DecodeAttentionCall,
+                          DecodeAttentionI8Call, DecodeAttentionValidCall, DequantActivationCall,
+                          DequantizeCall, GatherCall, KernelCall, KvCacheWriteCall, KvQuantAppendCall,
                           MatMulActivationCall, MatMulAddActivationCall, MatMulAddCall,
                           MatMulCall, MatMulDequantCall, NormCall, RoPECall, TransposeCall,
                           UnaryCall, encode_calls, fused_activation, lut_act, mm_act_quant,
@@ -28,8 +28,8 @@ __all__ = [
     "ShapeMismatch", "SlotOutOfRange", "UnsupportedOp", "decode_call", "lut_table", "validate",
     "DTYPE_BF16", "DTYPE_E8CB", "DTYPE_F16", "DTYPE_F32", "DTYPE_I4", "DTYPE_I8", "DTYPE_I32",
     "DTYPE_I64", "DTYPE_U8", "NO_BUFFER", "SLOT_ABSENT", "ArgMaxCall", "AttentionI8RowsCall",
-    "BinaryCall", "BufferRef", "DecodeAttentionI8Call", "DecodeAttentionValidCall",
-    "DequantActivationCall", "DequantizeCall", "GatherCall", "KernelCall", "KvCacheWriteCall",
+    "BinaryCall", "BufferRef", "DecodeAttentionCall", "DecodeAttentionI8Call",
+    "DecodeAttentionValidCall", "DequantActivationCall", "DequantizeCall", "GatherCall", "KernelCall", "KvCacheWriteCall",
     "KvQuantAppendCall", "MatMulActivationCall", "MatMulAddActivationCall", "MatMulAddCall",
     "MatMulCall", "MatMulDequantCall", "NormCall", "RoPECall", "TransposeCall", "UnaryCall",
     "encode_calls", "fused_activation", "lut_act", "mm_act_quant", "weight_layout",

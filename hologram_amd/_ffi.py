@@ -103,6 +103,16 @@ class DecodeAttentionValidCallC(ctypes.Structure):
                 ("dtype", ctypes.c_uint8)]
 
 
+class DecodeAttentionCallC(ctypes.Structure):
+    _fields_ = [("q", BufferRefC), ("k_past", BufferRefC), ("v_past", BufferRefC),
+                ("k_new", BufferRefC), ("v_new", BufferRefC), ("mask", BufferRefC),
+                ("output", BufferRefC), ("batch", ctypes.c_uint32), ("heads", ctypes.c_uint32),
+                ("kv_heads", ctypes.c_uint32), ("q_rows", ctypes.c_uint32),
+                ("past_len", ctypes.c_uint32), ("new_len", ctypes.c_uint32),
+                ("head_dim", ctypes.c_uint32), ("scale_bits", ctypes.c_uint32),
+                ("dtype", ctypes.c_uint8)]
+
+
 class DecodeAttentionI8CallC(ctypes.Structure):
     _fields_ = [("q", BufferRefC), ("k_cache", BufferRefC), ("v_cache", BufferRefC),
                 ("k_scales", BufferRefC), ("v_scales", BufferRefC), ("lens", BufferRefC),
@@ -156,6 +166,7 @@ class CallUnion(ctypes.Union):
                 ("matmul_add", MatMulAddCallC), ("matmul_add_act", MatMulAddActCallC),
                 ("kv_write", KvCacheWriteCallC),
                 ("kv_quant_append", KvQuantAppendCallC), ("attn_valid", DecodeAttentionValidCallC),
+                ("attn_mask", DecodeAttentionCallC),
                 ("dequantize", DequantizeCallC), ("matmul_dequant", MatMulDequantCallC),
                 ("dequant_act", DequantActivationCallC), ("attn_i8", DecodeAttentionI8CallC),
                 ("attn_i8_rows", AttentionI8RowsCallC), ("transpose", TransposeCallC)]

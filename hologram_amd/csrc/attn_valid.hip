@@ -2,7 +2,12 @@
 // K/V: the reference's own decode-attention op, as its compiler lowers
 // attention (crates/hologram-compiler/src/lower.rs:817), with the semantics
 // of decode_attention_valid_float (src/cpu/float_kernels.rs:4192-4307) and its
-// row function (:3834-3957).
+// row function (:3834-3957). The same kernels serve the mask form,
+// DecodeAttention (discriminant 119, decode_attention_float :2482-2600, row
+// function :2420-2477): the list is every past row then every new row, and
+// query row qi adds mask[qi][j] (f32 [q_rows, past + new]) to the score of
+// list entry j; a key the mask erases (-inf) weighs exactly 0, and a row
+// whose every key is erased is the zero row.
 //
 // Visible keys of a plane (batch b, kv head) form one list: the realized past
 // prefix, rows [0, vis_past) of k_past / v_past (vis_past = min(valid_len,
@@ -86,7 +91,8 @@ __global__ __launch_bounds__(kThreads) void attn_valid_split_kernel(AttnValidArg
     const uint32_t r0 = tile * RT, nr = R - r0 < RT ? R - r0 : RT;
     const uint64_t qrow0 = (uint64_t(b) * a.H + uint64_t(kvh) * G) * a.M + r0;
 
-    uint32_t vis_past = read_u32_le(a.valid_len);
+    // mask form: every past row is in the list, visibility is the mask's
+    uint32_t vis_past = a.mask ? a.past : read_u32_le(a.valid_len);
     if (vis_past > a.past) vis_past = a.past;
     const uint32_t total = vis_past + a.nnew;
     const uint32_t share = (total + nsplit - 1) / nsplit;
@@ -126,7 +132,7 @@ __global__ __launch_bounds__(kThreads) void attn_valid_split_kernel(AttnValidArg
         for (uint32_t pi = tid; pi < nr * KB; pi += kThreads) {
             const uint32_t rr = pi / KB, key = pi % KB;
             const uint32_t qi = (r0 + rr) % a.M;
-            const uint32_t lim = vis_past + (qi + 1 < a.nnew ? qi + 1 : a.nnew);
+            const uint32_t lim = a.mask ? total : vis_past + (qi + 1 < a.nnew ? qi + 1 : a.nnew);
             float s = -INFINITY;
             if (key < nk && jb + key < lim) {
                 const float *qr = qs + rr * D, *kr = ks + key * Dp;
@@ -140,6 +146,7 @@ __global__ __launch_bounds__(kThreads) void attn_valid_split_kernel(AttnValidArg
                 }
                 for (; c < D; ++c) d0 = fmaf(qr[c], kr[c], d0);
                 s = ((d0 + d1) + (d2 + d3)) / a.scale;
+                if (a.mask) s = s + a.mask[uint64_t(qi) * total + jb + key];
             }
             sc[rr * KB + key] = s;
         }

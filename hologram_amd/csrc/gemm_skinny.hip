@@ -112,41 +112,46 @@ __global__ __launch_bounds__(256) void skinny_bf16_kernel(const SkinnyArgs g) {
 
     // RmsNorm of A on the way in: the producer's four wave sums of each of
     // this lane's rows and gamma at the lane's k values, loaded ahead of B
+    // No load sits behind a branch: a step past the range, a row past M or an
+    // absent gamma loads from an out-of-range offset (zero, no memory access),
+    // so the compiler counts the loads in flight exactly and each step waits
+    // only for its own.
     const bool norm = g.norm.ssq != nullptr;
     f32x4 ssq[MT];
     u32x4 gam[STEPS];
-    if (norm) {
+    {   // (empty ranges when there is no norm: nothing is read)
+        const auto rs = rsrc(g.norm.ssq, norm ? M * 16u : 0u);
+        const auto rg = rsrc(g.norm.gamma, norm && g.norm.gamma ? K * 2u : 0u);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const uint32_t row = mt * 16 + q;
-            ssq[mt] = row < M ? reinterpret_cast<const f32x4 *>(g.norm.ssq)[row]
-                              : f32x4{0.f, 0.f, 0.f, 0.f};
-        }
+        for (int mt = 0; mt < MT; ++mt)
+            ssq[mt] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    rs, (mt * 16 + q) * 16u, 0, 0));
 #pragma unroll
         for (int t = 0; t < STEPS; ++t) {
             const uint32_t kr = uint32_t(t * kWaves + w) * 32;
-            gam[t] = u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
-            if (kr < krows && g.norm.gamma)
-                gam[t] = *reinterpret_cast<const u32x4 *>(g.norm.gamma + kb0 + kr + 8 * grp);
+            gam[t] = __builtin_amdgcn_raw_buffer_load_b128(
+                rg, kr < krows ? (kb0 + kr + 8 * grp) * 2u : 0x80000000u, 0, 0);
         }
     }
     u32x4 b[STEPS][8], a[STEPS][MT];
 #pragma unroll
     for (int t = 0; t < STEPS; ++t) {
         const uint32_t kr = uint32_t(t * kWaves + w) * 32;   // step start within the range
-        if (kr < krows) {
-            const uint32_t vo = bcol + (kr + 8 * grp) * N * 2u;
+        const bool live = kr < krows;
+        const uint32_t vo = live ? bcol + (kr + 8 * grp) * N * 2u : 0x80000000u;
 #pragma unroll
-            for (int r = 0; r < 8; ++r)
-                b[t][r] = __builtin_amdgcn_raw_buffer_load_b128(rb, vo, int(N * 2u) * r, 0);
+        for (int r = 0; r < 8; ++r)
+            b[t][r] = __builtin_amdgcn_raw_buffer_load_b128(rb, vo, int(N * 2u) * r, 0);
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-                a[t][mt] = __builtin_amdgcn_raw_buffer_load_b128(
-                    ra, ((mt * 16 + q) * K + kb0 + kr + 8 * grp) * 2u, 0, 0);
-        }
+        for (int mt = 0; mt < MT; ++mt)
+            a[t][mt] = __builtin_amdgcn_raw_buffer_load_b128(
+                ra, live ? ((mt * 16 + q) * K + kb0 + kr + 8 * grp) * 2u : 0x80000000u, 0, 0);
     }
     // inv of each row: the four wave sums added in the standalone kernel's order
     float inv[MT];
+    if (norm && !g.norm.gamma)   // no gamma: scale 1
+#pragma unroll
+        for (int t = 0; t < STEPS; ++t) gam[t] = u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
     if (norm)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
@@ -251,20 +256,20 @@ __global__ __launch_bounds__(256) void skinny_f32_kernel(const SkinnyArgs g) {
     const auto ra = rsrc(A, M * K * 4u);
     const uint32_t bcol = n0 < N ? n0 * 4u : 0x80000000u;
 
+    // steps past the range load from an out-of-range offset (no branch)
     u32x4 b[STEPS][4], a[STEPS][MT];
 #pragma unroll
     for (int t = 0; t < STEPS; ++t) {
         const uint32_t kr = uint32_t(t * kWaves + w) * 16;
-        if (kr < krows) {
-            const uint32_t vo = bcol + (kr + 4 * grp) * N * 4u;
+        const bool live = kr < krows;
+        const uint32_t vo = live ? bcol + (kr + 4 * grp) * N * 4u : 0x80000000u;
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                b[t][r] = __builtin_amdgcn_raw_buffer_load_b128(rb, vo, int(N * 4u) * r, 0);
+        for (int r = 0; r < 4; ++r)
+            b[t][r] = __builtin_amdgcn_raw_buffer_load_b128(rb, vo, int(N * 4u) * r, 0);
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-                a[t][mt] = __builtin_amdgcn_raw_buffer_load_b128(
-                    ra, ((mt * 16 + q) * K + kb0 + kr + 4 * grp) * 4u, 0, 0);
-        }
+        for (int mt = 0; mt < MT; ++mt)
+            a[t][mt] = __builtin_amdgcn_raw_buffer_load_b128(
+                ra, live ? ((mt * 16 + q) * K + kb0 + kr + 4 * grp) * 4u : 0x80000000u, 0, 0);
     }
     f32x4 acc[MT][4];
 #pragma unroll
@@ -328,13 +333,12 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float *__restr
     const uint64_t step = plane / 4;
     f32x4 s = p[0];
     uint32_t ks = 1;
-    for (; ks + 4 <= KS; ks += 4) {   // four loads in flight, added in ks order
-        const f32x4 v0 = p[ks * step], v1 = p[(ks + 1) * step], v2 = p[(ks + 2) * step],
-                    v3 = p[(ks + 3) * step];
-        s += v0;
-        s += v1;
-        s += v2;
-        s += v3;
+    for (; ks + 8 <= KS; ks += 8) {   // eight loads in flight, added in ks order
+        f32x4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = p[(ks + u) * step];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
     }
     for (; ks < KS; ++ks) s += p[ks * step];
     if (kBf16) {

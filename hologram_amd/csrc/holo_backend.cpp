@@ -852,6 +852,79 @@ int do_attn_valid(holo_backend *be, const SlotTable &st, const holo_decode_atten
     return launched(holo::launch_attn_valid(a, be->scratch, be->stream), op);
 }
 
+// ----------------------------------------------------- DecodeAttention --
+// decode_attention_float (src/cpu/float_kernels.rs:2482-2600), the mask form:
+// refusals in the reference's order, then the kernels of attn_valid.hip with
+// the mask in place of valid_len.
+int do_attn_mask(holo_backend *be, const SlotTable &st, const holo_decode_attention_call &c) {
+    const char *op = "decode_attention";
+    if (c.batch == 0 || c.heads == 0 || c.q_rows == 0 || c.head_dim == 0) return HOLO_OK;
+    const uint64_t L = uint64_t(c.past_len) + c.new_len;
+    if (L == 0)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "decode_attention: past_len + new_len must be at least 1");
+    const uint32_t hkv = c.kv_heads == 0 ? c.heads : c.kv_heads;
+    if (c.heads % hkv != 0)
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    "decode_attention: heads must be a multiple of kv_heads (grouped-query)");
+    const uint64_t es = dtype_size(c.dtype);
+    if (es == 0) return fail(HOLO_ERR_UNSUPPORTED_OP, "decode_attention: unknown dtype");
+    const uint64_t qn = uint64_t(c.batch) * c.heads * c.q_rows * c.head_dim;
+    const uint64_t pn = uint64_t(c.batch) * hkv * c.past_len * c.head_dim;
+    const uint64_t nn = uint64_t(c.batch) * hkv * c.new_len * c.head_dim;
+    holo_buffer_ref reads[6] = {c.q, c.k_past, c.v_past, c.k_new, c.v_new, c.mask};
+    View rv[6], out;
+    HOLO_TRY(split_borrow(st, reads, rv, 6, c.output, &out, op));
+    HOLO_TRY(need(rv[0], qn * es, c.q.slot, op, "q"));
+    HOLO_TRY(need(rv[1], pn * es, c.k_past.slot, op, "k_past"));
+    HOLO_TRY(need(rv[2], pn * es, c.v_past.slot, op, "v_past"));
+    HOLO_TRY(need(rv[3], nn * es, c.k_new.slot, op, "k_new"));
+    HOLO_TRY(need(rv[4], nn * es, c.v_new.slot, op, "v_new"));
+    HOLO_TRY(need(rv[5], uint64_t(c.q_rows) * L * 4, c.mask.slot, op, "mask"));   // always f32
+    HOLO_TRY(need(out, qn * es, c.output.slot, op, "output"));
+    if (c.dtype != HOLO_DTYPE_F32 && c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F16)
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    "decode_attention: only f32/f16/bf16 are supported compute dtypes");
+    for (int i = 0; i < 5; ++i)
+        if (!aligned(rv[i], es))
+            return fail(HOLO_ERR_UNSUPPORTED_OP, std::string(op) + ": operands must be element-aligned");
+    if (!aligned(out, es) || !aligned(rv[5], 4))
+        return fail(HOLO_ERR_UNSUPPORTED_OP, std::string(op) + ": operands must be element-aligned");
+    if (L > 0xffffffffull || !holo::attn_valid_supported(c.batch, c.heads, hkv, c.q_rows, c.head_dim))
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    std::string(op) + ": head_dim above 4096 or a grid beyond the launch limits");
+    if (!be) return HOLO_OK;
+    // score divisor (float_kernels.rs:2545-2555)
+    float scale = std::sqrt(static_cast<float>(c.head_dim));
+    if (scale < 1.0f) scale = 1.0f;
+    if (c.scale_bits != 0) {
+        float sm;
+        memcpy(&sm, &c.scale_bits, 4);
+        if (sm > 0.0f) scale = 1.0f / sm;
+    }
+    HOLO_TRY(ensure_scratch(be, holo::attn_valid_scratch_bytes(c.batch, c.heads, hkv, c.q_rows,
+                                                               c.past_len, c.new_len, c.head_dim),
+                            op));
+    holo::AttnValidArgs a;
+    a.q = rv[0].base;
+    a.kp = rv[1].base;
+    a.vp = rv[2].base;
+    a.kn = rv[3].base;
+    a.vn = rv[4].base;
+    a.valid_len = nullptr;
+    a.mask = reinterpret_cast<const float *>(rv[5].base);
+    a.out = out.base;
+    a.B = c.batch;
+    a.H = c.heads;
+    a.Hkv = hkv;
+    a.M = c.q_rows;
+    a.past = c.past_len;
+    a.nnew = c.new_len;
+    a.D = c.head_dim;
+    a.scale = scale;
+    a.dtype = c.dtype;
+    return launched(holo::launch_attn_valid(a, be->scratch, be->stream), op);
+}
+
 // ------------------------------------------------ quantized weights ----
 // The level width of a quantized tier (quant_tier.rs:137-178): stored bytes
 // of `count` elements, or 0 for a tier this op cannot read.
@@ -1320,6 +1393,7 @@ int dispatch_impl(holo_backend *be, const SlotTable &st, const holo_kernel_call 
         case HOLO_OP_KV_CACHE_WRITE: return do_kv_write(be, st, call->u.kv_write);
         case HOLO_OP_KV_QUANT_APPEND: return do_kv_quant(be, st, call->u.kv_quant_append);
         case HOLO_OP_DECODE_ATTN_VALID: return do_attn_valid(be, st, call->u.attn_valid);
+        case HOLO_OP_DECODE_ATTN: return do_attn_mask(be, st, call->u.attn_mask);
         case HOLO_OP_DECODE_ATTN_I8: return do_attn_i8(be, st, call->u.attn_i8);
         case HOLO_OP_ATTN_I8_ROWS:
             return do_attn_i8(be, st, call->u.attn_i8_rows.attn, call->u.attn_i8_rows.q_rows);
@@ -1567,6 +1641,26 @@ int decode_impl(const uint8_t *wire, size_t len, holo_kernel_call *out, size_t *
             c.bucket_rows = r.get<uint32_t>();
             c.new_rows = r.get<uint32_t>();
             c.head_dim = r.get<uint32_t>();
+            c.dtype = r.get<uint8_t>();
+            break;
+        }
+        case HOLO_OP_DECODE_ATTN: {  // put_decattn :768-785 (put_davl's order, mask for valid_len)
+            auto &c = out->u.attn_mask;
+            c.q = r.buf();
+            c.k_past = r.buf();
+            c.v_past = r.buf();
+            c.k_new = r.buf();
+            c.v_new = r.buf();
+            c.mask = r.buf();
+            c.output = r.buf();
+            c.batch = r.get<uint32_t>();
+            c.heads = r.get<uint32_t>();
+            c.kv_heads = r.get<uint32_t>();
+            c.q_rows = r.get<uint32_t>();
+            c.past_len = r.get<uint32_t>();
+            c.new_len = r.get<uint32_t>();
+            c.head_dim = r.get<uint32_t>();
+            c.scale_bits = r.get<uint32_t>();
             c.dtype = r.get<uint8_t>();
             break;
         }

@@ -165,6 +165,13 @@ bool op_signature(const holo_kernel_call &c, uint16_t *opcode, uint8_t params[64
             op = 120;
             break;
         }
+        case HOLO_OP_DECODE_ATTN: {
+            const auto &a = c.u.attn_mask;
+            s.u32(a.batch).u32(a.heads).u32(a.kv_heads).u32(a.q_rows).u32(a.past_len).u32(a.new_len)
+                .u32(a.head_dim).u32(a.scale_bits).u8(a.dtype);
+            op = 119;
+            break;
+        }
         case HOLO_OP_DECODE_ATTN_VALID: {
             const auto &a = c.u.attn_valid;
             s.u32(a.batch).u32(a.heads).u32(a.kv_heads).u32(a.q_rows).u32(a.past_len).u32(a.new_len)
@@ -247,6 +254,11 @@ bool label_operands(const holo_kernel_call &c, std::vector<uint32_t> *ins,
         case HOLO_OP_KV_CACHE_WRITE: {
             const auto &k = c.u.kv_write;
             r(k.cache), r(k.new_rows_buf), r(k.pos), w(k.output);
+            break;
+        }
+        case HOLO_OP_DECODE_ATTN: {
+            const auto &a = c.u.attn_mask;
+            r(a.q), r(a.k_past), r(a.v_past), r(a.k_new), r(a.v_new), r(a.mask), w(a.output);
             break;
         }
         case HOLO_OP_DECODE_ATTN_VALID: {

@@ -62,7 +62,8 @@ hipError_t launch_attn_i8(const AttnI8Args &a, void *scratch, hipStream_t stream
 // (M == nnew), valid_len a 4-byte LE u32 on the device.
 struct AttnValidArgs {
     const void *q, *kp, *vp, *kn, *vn;
-    const uint8_t *valid_len;
+    const uint8_t *valid_len;   // 121; null in the mask form
+    const float *mask = nullptr;  // 119: f32 [M, past + nnew] added to the scores
     void *out;
     uint32_t B, H, Hkv, M, past, nnew, D;
     float scale;            // the divisor: sqrtf(D) (>= 1) or 1/scale_multiplier

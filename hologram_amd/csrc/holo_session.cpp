@@ -176,6 +176,11 @@ void call_operands(const holo_kernel_call &c, std::vector<holo_buffer_ref> *read
             r(a.q); r(a.k_past); r(a.v_past); r(a.k_new); r(a.v_new); r(a.valid_len);
             w(a.output); break;
         }
+        case HOLO_OP_DECODE_ATTN: {
+            const auto &a = c.u.attn_mask;
+            r(a.q); r(a.k_past); r(a.v_past); r(a.k_new); r(a.v_new); r(a.mask);
+            w(a.output); break;
+        }
         case HOLO_OP_DECODE_ATTN_I8:
         case HOLO_OP_ATTN_I8_ROWS: {
             const auto &a = c.tag == HOLO_OP_ATTN_I8_ROWS ? c.u.attn_i8_rows.attn : c.u.attn_i8;

@@ -63,6 +63,7 @@ D_RN = 51
 D_ADDRMS = 54   # AddRmsNorm: rms_norm(x + residual)
 D_ROTARY = 75
 D_GATHER = 114
+D_DECATTN = 119   # DecodeAttention, the mask form
 D_KVWR = 120
 D_DAVL = 121
 D_KVQA = 122   # new: int8 quantize + append
@@ -414,6 +415,36 @@ class KvQuantAppendCall:
 
 
 @dataclass(frozen=True)
+class DecodeAttentionCall:
+    """kernel_call.rs:632-656: decode attention with an additive f32 mask
+    [q_rows, past_len + new_len] (every past row, then every new row, is a
+    key; -inf erases one)."""
+    q: BufferRef
+    k_past: BufferRef
+    v_past: BufferRef
+    k_new: BufferRef
+    v_new: BufferRef
+    mask: BufferRef
+    output: BufferRef
+    batch: int
+    heads: int
+    kv_heads: int
+    q_rows: int
+    past_len: int
+    new_len: int
+    head_dim: int
+    scale_bits: int = 0
+    dtype: int = DTYPE_BF16
+
+    def wire(self) -> bytes:  # put_decattn, kernel_codec.rs:768-785
+        return (self.q.wire() + self.k_past.wire() + self.v_past.wire() + self.k_new.wire()
+                + self.v_new.wire() + self.mask.wire() + self.output.wire()
+                + struct.pack("<IIIIIIIIB", self.batch, self.heads, self.kv_heads, self.q_rows,
+                              self.past_len, self.new_len, self.head_dim, self.scale_bits,
+                              self.dtype))
+
+
+@dataclass(frozen=True)
 class DecodeAttentionValidCall:
     """kernel_call.rs:691-716: the reference's decode attention over 16-bit or
     f32 K/V (past prefix of valid_len realized rows, then new rows causally)."""
@@ -502,7 +533,7 @@ _NAMES = {D_ADD: "Add", D_MUL: "Mul", D_RN: "RmsNorm", D_ADDRMS: "AddRmsNorm", D
           D_GATHER: "Gather", D_ARGMAX: "ArgMax", D_SIGMOID: "Sigmoid", D_TANH: "Tanh", D_GELU: "Gelu", D_SILU: "Silu", D_EXP: "Exp",
           D_MATMUL: "MatMul", D_MMA: "MatMulActivation", D_MMADD: "MatMulAdd",
           D_MMAA: "MatMulAddActivation", D_KVWR: "KvCacheWrite", D_KVQA: "KvQuantAppend",
-          D_DAVL: "DecodeAttentionValid", D_DAI8: "DecodeAttentionI8", D_AI8R: "AttentionI8Rows", D_TRANSPOSE: "Transpose"}
+          D_DECATTN: "DecodeAttention", D_DAVL: "DecodeAttentionValid", D_DAI8: "DecodeAttentionI8", D_AI8R: "AttentionI8Rows", D_TRANSPOSE: "Transpose"}
 
 
 @dataclass(frozen=True)
@@ -613,6 +644,10 @@ class KernelCall:
         return cls(D_KVQA, c)
 
     @classmethod
+    def DecodeAttention(cls, c: DecodeAttentionCall) -> "KernelCall":  # noqa: N802
+        return cls(D_DECATTN, c)
+
+    @classmethod
     def DecodeAttentionValid(cls, c: DecodeAttentionValidCall) -> "KernelCall":  # noqa: N802
         return cls(D_DAVL, c)
 
@@ -687,6 +722,11 @@ class KernelCall:
                 p.input.c(), p.output.c(), rank,
                 (ctypes.c_uint32 * 8)(*(list(p.dims) + [0] * (8 - rank))),
                 (ctypes.c_uint8 * 8)(*(list(p.perm) + [0] * (8 - rank))), p.dtype)
+        elif isinstance(p, DecodeAttentionCall):
+            kc.u.attn_mask = _ffi.DecodeAttentionCallC(
+                p.q.c(), p.k_past.c(), p.v_past.c(), p.k_new.c(), p.v_new.c(), p.mask.c(),
+                p.output.c(), p.batch, p.heads, p.kv_heads, p.q_rows, p.past_len, p.new_len,
+                p.head_dim, p.scale_bits, p.dtype)
         elif isinstance(p, DecodeAttentionValidCall):
             kc.u.attn_valid = _ffi.DecodeAttentionValidCallC(
                 p.q.c(), p.k_past.c(), p.v_past.c(), p.k_new.c(), p.v_new.c(), p.valid_len.c(),

@@ -90,6 +90,7 @@ typedef enum holo_status {
 #define HOLO_OP_ADD_RMS_NORM 54u          /* AddRmsNorm: rms_norm(x + residual) */
 #define HOLO_OP_ROTARY 75u
 #define HOLO_OP_GATHER 114u
+#define HOLO_OP_DECODE_ATTN 119u          /* DecodeAttention, mask form (kernel_codec.rs D_DECATTN) */
 #define HOLO_OP_KV_CACHE_WRITE 120u
 #define HOLO_OP_DECODE_ATTN_VALID 121u    /* DecodeAttentionValid (kernel_codec.rs D_DAVL) */
 #define HOLO_OP_KV_QUANT_APPEND 122u      /* new: int8 quantize + ring append   */
@@ -259,6 +260,28 @@ typedef struct holo_decode_attention_valid_call {
     uint8_t dtype;
 } holo_decode_attention_valid_call;
 
+/* DecodeAttentionCall, kernel_call.rs:632-656 (decode_attention_float,
+ * src/cpu/float_kernels.rs:2482-2600, row function :2420-2477), the mask form
+ * of decode attention: the same operands as DecodeAttentionValid with the
+ * additive mask, f32 [q_rows, past_len + new_len] shared by batch and heads,
+ * in place of valid_len. Every past row, then every new row, is a key; query
+ * row qi scores key j as dot(q, k_j) / s + mask[qi][j] (s as in
+ * DecodeAttentionValid); f32 softmax; a row whose every score is -inf is the
+ * zero row. Any q_rows >= 1 and new_len >= 0 pair; past_len + new_len >= 1;
+ * dtype bf16, f16 or f32 for q, K, V and out; kv_heads 0 means heads;
+ * head_dim <= 4096. */
+typedef struct holo_decode_attention_call {
+    holo_buffer_ref q;
+    holo_buffer_ref k_past;
+    holo_buffer_ref v_past;
+    holo_buffer_ref k_new;
+    holo_buffer_ref v_new;
+    holo_buffer_ref mask;
+    holo_buffer_ref output;
+    uint32_t batch, heads, kv_heads, q_rows, past_len, new_len, head_dim, scale_bits;
+    uint8_t dtype;
+} holo_decode_attention_call;
+
 /* DequantizeCall, kernel_call.rs:782-818 (dequantize, src/cpu/kernels.rs:185-296):
  * out[i] = (q[i] - zp) as f32 * scale, per tensor (scale_bits, zero_point) or
  * per channel (channels > 0 and scales present: channel (i / inner) % channels
@@ -415,6 +438,7 @@ typedef struct holo_kernel_call {
         holo_kv_cache_write_call kv_write;
         holo_kv_quant_append_call kv_quant_append;
         holo_decode_attention_valid_call attn_valid;
+        holo_decode_attention_call attn_mask;
         holo_dequantize_call dequantize;
         holo_matmul_dequant_call matmul_dequant;
         holo_dequant_activation_call dequant_act;

@@ -55,6 +55,9 @@ _SIGS = {
                                   + [ctypes.c_int]),
     "or_decode_attention_valid_f32": (None, [_P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32,
                                              _U32, _U32, _U32, _F, _U32]),
+    "or_decode_attention": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P] + [_U32] * 8
+                            + [ctypes.c_int]),
+    "or_decode_attention_mask_f32": (None, [_P] * 7 + [_U32] * 7 + [_F]),
     "or_decode_attention_i8": (None, [_P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32,
                                       _F]),
     "or_binary": (None, [ctypes.c_int, _P, _P, _P, _S, ctypes.c_int]),
@@ -230,6 +233,23 @@ def decode_attention_valid(q, kp, vp, kn, vn, valid_len, b, h, hkv, m, past, new
                                          m, past, new, d, scale_bits, dtype)
     if rc != 0:
         raise ValueError(f"decode_attention_valid refused ({rc})")
+    return out
+
+
+def decode_attention(q, kp, vp, kn, vn, mask, b, h, hkv, m, past, new, d, scale_bits,
+                     dtype) -> np.ndarray:
+    """DecodeAttention, the mask form (float_kernels.rs:2482-2660), on raw
+    operand arrays of `dtype` (bf16/f16 as u16 bits, f32) and an f32 mask
+    [m, past + new]; returns the output array of the same element type.
+    Raises ValueError where the reference refuses."""
+    es = 4 if dtype == DTYPE_F32 else 2
+    out = np.zeros(b * h * m * d, np.float32 if es == 4 else np.uint16)
+    args = [np.ascontiguousarray(x) for x in (q, kp, vp, kn, vn)]
+    mk = np.ascontiguousarray(mask, dtype=np.float32)
+    rc = lib().or_decode_attention(*[_p(x) for x in args], _p(mk), _p(out), b, h, hkv, m, past,
+                                   new, d, scale_bits, dtype)
+    if rc != 0:
+        raise ValueError(f"decode_attention refused ({rc})")
     return out
 
 

@@ -59,6 +59,11 @@ def _decode_call(r: _R) -> tuple:
         return tag, dict(data=r.buf(), idx=r.buf(), output=r.buf(), outer=r.u("Q"),
                          axis=r.u("Q"), inner=r.u("Q"), num=r.u("Q"), idx_dtype=r.u("B"),
                          dtype=r.u("B"))
+    if tag == 119:                                   # put_decattn
+        return tag, dict(q=r.buf(), kp=r.buf(), vp=r.buf(), kn=r.buf(), vn=r.buf(),
+                         mask=r.buf(), output=r.buf(), batch=r.u("I"), heads=r.u("I"),
+                         kv_heads=r.u("I"), q_rows=r.u("I"), past=r.u("I"), new=r.u("I"),
+                         head_dim=r.u("I"), scale_bits=r.u("I"), dtype=r.u("B"))
     if tag == 121:                                   # put_davl
         return tag, dict(q=r.buf(), kp=r.buf(), vp=r.buf(), kn=r.buf(), vn=r.buf(),
                          valid=r.buf(), output=r.buf(), batch=r.u("I"), heads=r.u("I"),
@@ -341,6 +346,18 @@ class OracleSession:
             from . import decode_attention_valid
             o = decode_attention_valid(*ops, valid, B, H, c["kv_heads"], M, c["past"], c["new"],
                                        D, c["scale_bits"], c["dtype"])
+            self._out(c["output"], o.nbytes)[:] = o.view(np.uint8)
+        elif tag == 119:
+            B, H, M, D = c["batch"], c["heads"], c["q_rows"], c["head_dim"]
+            hkv = H if c["kv_heads"] == 0 else c["kv_heads"]
+            es = DT_BYTES[c["dtype"]]
+            pn, nn = B * hkv * c["past"] * D * es, B * hkv * c["new"] * D * es
+            ops = [np.ascontiguousarray(self._view(c[k], n)) for k, n in
+                   (("q", B * H * M * D * es), ("kp", pn), ("vp", pn), ("kn", nn), ("vn", nn))]
+            mask = np.ascontiguousarray(self._view(c["mask"], M * (c["past"] + c["new"]) * 4))
+            from . import decode_attention
+            o = decode_attention(*ops, mask.view(np.float32), B, H, c["kv_heads"], M, c["past"],
+                                 c["new"], D, c["scale_bits"], c["dtype"])
             self._out(c["output"], o.nbytes)[:] = o.view(np.uint8)
         elif tag == 125:
             B, T, H, Hkv = c["batch"], c["q_rows"], c["heads"], c["kv_heads"]

@@ -651,6 +651,85 @@ int or_decode_attention_valid(const void *q, const void *k_past, const void *v_p
     return 0;
 }
 
+/* DecodeAttention, the mask form. One (b, h, q-row), :2420-2477: scores over
+ * past then new keys, each dot / scale + the row's mask entry; a row whose
+ * largest score is -inf is the zero row; then max-shift, exp_f32_det, the
+ * sequential sum, denom = max(sum, 1e-30), out = sum_j (e_j / denom) v_j. */
+static void mask_row(const float *q, const float *kp, const float *vp, const float *kn,
+                     const float *vn, const float *mrow, float *out, size_t past, size_t nnew,
+                     size_t d, float scale, float *sc)
+{
+    size_t l = past + nnew;
+    for (size_t j = 0; j < l; ++j) {
+        const float *kr = j < past ? kp + j * d : kn + (j - past) * d;
+        float s = 0.0f;
+        for (size_t c = 0; c < d; ++c) s += q[c] * kr[c];
+        sc[j] = s / scale + mrow[j];
+    }
+    float mx = -INFINITY;
+    for (size_t j = 0; j < l; ++j) mx = fmaxf(mx, sc[j]);
+    for (size_t c = 0; c < d; ++c) out[c] = 0.0f;
+    if (mx == -INFINITY) return;
+    for (size_t j = 0; j < l; ++j) sc[j] = or_exp_f32_det(sc[j] - mx);
+    float sum = 0.0f;
+    for (size_t j = 0; j < l; ++j) sum += sc[j];
+    float denom = sum > 1e-30f ? sum : 1e-30f;
+    for (size_t j = 0; j < l; ++j) {
+        float p = sc[j] / denom;
+        const float *vr = j < past ? vp + j * d : vn + (j - past) * d;
+        for (size_t c = 0; c < d; ++c) out[c] += p * vr[c];
+    }
+}
+
+/* serial engine, :2606-2660: row r -> (bi, hi, qi), kv head bi*hkv + hi/group,
+ * mask row qi of [m][past + nnew] (shared by batch and heads) */
+void or_decode_attention_mask_f32(const float *q, const float *kp, const float *vp,
+                                  const float *kn, const float *vn, const float *mask, float *out,
+                                  uint32_t b, uint32_t h, uint32_t hkv, uint32_t m,
+                                  uint32_t past, uint32_t nnew, uint32_t d, float scale)
+{
+    if (hkv == 0) hkv = h;
+    size_t group = h / hkv, l = (size_t)past + nnew;
+    float *sc = (float *)malloc(sizeof(float) * (l + 1));
+    size_t rows = (size_t)b * h * m;
+    for (size_t r = 0; r < rows; ++r) {
+        size_t bi = r / ((size_t)h * m), hi = (r / m) % h, qi = r % m;
+        size_t kvh = bi * hkv + hi / group;
+        mask_row(q + r * d, kp + kvh * (size_t)past * d, vp + kvh * (size_t)past * d,
+                 kn + kvh * (size_t)nnew * d, vn + kvh * (size_t)nnew * d, mask + qi * l,
+                 out + r * d, past, nnew, d, scale, sc);
+    }
+    free(sc);
+}
+
+int or_decode_attention(const void *q, const void *k_past, const void *v_past, const void *k_new,
+                        const void *v_new, const float *mask, void *out, uint32_t b, uint32_t h,
+                        uint32_t hkv, uint32_t m, uint32_t past, uint32_t nnew, uint32_t d,
+                        uint32_t scale_bits, int dtype)
+{
+    /* :2489-2511 and :2576-2580: empty shapes, an empty key list, the GQA map,
+     * then the compute dtypes */
+    if (b == 0 || h == 0 || m == 0 || d == 0) return 0;
+    if ((size_t)past + nnew == 0) return 3;
+    if (hkv == 0) hkv = h;
+    if (h % hkv != 0) return 3;
+    if (dtype != OR_DTYPE_F32 && dtype != OR_DTYPE_BF16 && dtype != OR_DTYPE_F16) return 3;
+    size_t qn = (size_t)b * h * m * d, pn = (size_t)b * hkv * past * d, nn = (size_t)b * hkv * nnew * d;
+    float *q32 = widen_all(q, dtype, qn), *kp = widen_all(k_past, dtype, pn);
+    float *vp = widen_all(v_past, dtype, pn), *kn = widen_all(k_new, dtype, nn);
+    float *vn = widen_all(v_new, dtype, nn);
+    float *o = (float *)malloc(sizeof(float) * qn);
+    or_decode_attention_mask_f32(q32, kp, vp, kn, vn, mask, o, b, h, hkv, m, past, nnew, d,
+                                 or_attn_scale(d, scale_bits));
+    for (size_t i = 0; i < qn; ++i) {
+        if (dtype == OR_DTYPE_F32) ((float *)out)[i] = o[i];
+        else if (dtype == OR_DTYPE_BF16) ((uint16_t *)out)[i] = or_f32_to_bf16(o[i]);
+        else ((uint16_t *)out)[i] = or_f32_to_f16(o[i]);
+    }
+    free(q32); free(kp); free(vp); free(kn); free(vn); free(o);
+    return 0;
+}
+
 void or_decode_attention_i8(const float *q, const int8_t *kq, const float *ks,
                             const int8_t *vq, const float *vs, const uint32_t *lens,
                             float *out, uint32_t B, uint32_t H, uint32_t Hkv,

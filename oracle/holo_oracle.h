@@ -42,6 +42,11 @@
  *   or_add_rms_norm ............ RmsNorm bit for bit without a residual; the
  *                                 unnarrowed f32 sum; f64 closed form (f32)
  *   or_decode_attention_valid .. f64 softmax law over the causal visible set
+ *   or_decode_attention (mask) . bit-equal to or_decode_attention_valid when the
+ *                                 mask states the same visibility (0 / -inf over
+ *                                 finite K/V: decode_attention_valid.rs:1-13);
+ *                                 f64 softmax law with the mask added; a fully
+ *                                 masked row is exactly zero
  *   pack_b_panels (Python) ..... the layout formula (layout.rs:16-45)
  *
  * Parity unpinned: the 126 signaling-NaN inputs of the bf16/f16 SiLU tables
@@ -145,6 +150,20 @@ int or_decode_attention_valid(const void *q, const void *k_past, const void *v_p
                               const void *k_new, const void *v_new, uint32_t valid_len, void *out,
                               uint32_t b, uint32_t h, uint32_t hkv, uint32_t m, uint32_t past,
                               uint32_t nnew, uint32_t d, uint32_t scale_bits, int dtype);
+/* DecodeAttention, the mask form (:2420-2477 row, :2482-2660 call): every
+ * past row then every new row is a key, query row qi adds mask[qi][j]
+ * (f32 [m][past + nnew]) to the score of key j, a row with no finite score
+ * maximum (all -inf) is zero. or_decode_attention returns 0, or 3
+ * (UnsupportedOp) for past + nnew == 0, heads % kv_heads != 0 or another
+ * dtype. */
+void or_decode_attention_mask_f32(const float *q, const float *k_past, const float *v_past,
+                                  const float *k_new, const float *v_new, const float *mask,
+                                  float *out, uint32_t b, uint32_t h, uint32_t hkv, uint32_t m,
+                                  uint32_t past, uint32_t nnew, uint32_t d, float scale);
+int or_decode_attention(const void *q, const void *k_past, const void *v_past, const void *k_new,
+                        const void *v_new, const float *mask, void *out, uint32_t b, uint32_t h,
+                        uint32_t hkv, uint32_t m, uint32_t past, uint32_t nnew, uint32_t d,
+                        uint32_t scale_bits, int dtype);
 /* int8-cache decode attention (new op), stated as the reference's per-sequence
  * DecodeAttentionValid{b=1, past=L-1, valid=L-1, q=new=1} over the dequantized
  * rows.  q: [B,H,D] f32 (widened), caches [B,Hkv,bucket,D] int8 + [B,Hkv,bucket]

@@ -12,7 +12,8 @@ import pytest
 
 import oracle
 from conftest import ROOT
-from hologram_amd import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, BufferRef, DecodeAttentionI8Call,
+from hologram_amd import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, BufferRef, DecodeAttentionCall,
+                          DecodeAttentionI8Call,
                           KernelCall, KvCacheWriteCall, KvQuantAppendCall, MatMulCall,
                           NormCall, SlotOutOfRange, UnaryCall, UnsupportedOp, decode_call, lut_table,
                           validate)
@@ -169,6 +170,33 @@ def test_attn_refusals():
         validate(call(batch=B, heads=H, kv_heads=Hkv, bucket_rows=bucket, head_dim=D), short)
 
 
+def test_decode_attention_mask_form_refusals():
+    """decode_attention_float's refusals (float_kernels.rs:2489-2580): an empty
+    key list, kv_heads not dividing heads, a mask shorter than q_rows * (past +
+    new) f32, and a dtype other than f32/f16/bf16 after the buffer checks."""
+    def call(**k):
+        geo = dict(batch=2, heads=4, kv_heads=2, q_rows=3, past_len=5, new_len=2, head_dim=8,
+                   scale_bits=0, dtype=DTYPE_BF16)
+        geo.update(k)
+        return KernelCall.DecodeAttention(DecodeAttentionCall(
+            *[BufferRef(s) for s in range(7)], **geo))
+    es, B, H, Hkv, M, P, N, D = 2, 2, 4, 2, 3, 5, 2, 8
+    sizes = [B * H * M * D * es, B * Hkv * P * D * es, B * Hkv * P * D * es,
+             B * Hkv * N * D * es, B * Hkv * N * D * es, M * (P + N) * 4, B * H * M * D * es]
+    validate(call(), sizes)
+    validate(call(batch=0), sizes)
+    with pytest.raises(UnsupportedOp):
+        validate(call(past_len=0, new_len=0), sizes)
+    with pytest.raises(UnsupportedOp):
+        validate(call(kv_heads=3), sizes)
+    short = list(sizes)
+    short[5] -= 4
+    with pytest.raises(SlotOutOfRange):
+        validate(call(), short)
+    with pytest.raises(UnsupportedOp):
+        validate(call(dtype=2), [s // 2 if i != 5 else s for i, s in enumerate(sizes)])
+
+
 def test_unknown_tag_is_unsupported():
     kc = _ffi.KernelCallC()
     kc.tag = 64   # Softmax: no device kernel here
@@ -204,6 +232,9 @@ def test_codec_layout_matches_kernel_codec():
                                                128, DTYPE_BF16)),
     KernelCall.DecodeAttentionI8(DecodeAttentionI8Call(*[BufferRef(i) for i in range(7)], 32, 32,
                                                        8, 32768, 128, 0, DTYPE_BF16)),
+    KernelCall.DecodeAttention(DecodeAttentionCall(*[BufferRef(i, i, 2 * i) for i in range(7)], 1,
+                                                   32, 8, 4, 4096, 4, 128, 0x3E000000,
+                                                   DTYPE_F16)),
 ])
 def test_codec_round_trip(call):
     wire = call.encode()

@@ -512,6 +512,105 @@ def test_decode_attention_valid_oracle_refusals_and_scale_bits():
     assert np.array_equal(out, v)
 
 
+def _visibility_mask(m, past, new, valid):
+    """The valid form's law as an additive mask [m, past + new]: 0 on the
+    realized prefix and the causal new rows, -inf elsewhere."""
+    mask = np.full((m, past + new), -np.inf, np.float32)
+    for qi in range(m):
+        mask[qi, :min(valid, past)] = 0.0
+        mask[qi, past:past + min(qi + 1, new)] = 0.0
+    return mask
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16, F16])
+@pytest.mark.parametrize("b,h,hkv,m,past,valid,d", [
+    (2, 4, 2, 1, 9, 5, 16), (1, 6, 3, 3, 7, 7, 8), (2, 2, 0, 2, 5, 3, 12), (1, 4, 1, 1, 0, 0, 32)])
+def test_decode_attention_mask_form_equals_valid_form(dtype, b, h, hkv, m, past, valid, d):
+    """The reference's witness (tests/decode_attention_valid.rs:1-13): with
+    finite bytes in the erased rows, the mask form over the mask that states
+    the valid form's visibility is bit-identical to the valid form (an erased
+    key's exp is exactly 0 and its context term an exact no-op)."""
+    rng = np.random.default_rng(7 * b + h + m + d)
+    hk = h if hkv == 0 else hkv
+    raw = [rng.standard_normal(n).astype(np.float32) for n in
+           (b * h * m * d, b * hk * past * d, b * hk * past * d, b * hk * m * d, b * hk * m * d)]
+    if dtype == BF16:
+        ops = [(x.view(np.uint32) >> 16).astype(np.uint16) for x in raw]
+    elif dtype == F16:
+        ops = [x.astype(np.float16).view(np.uint16) for x in raw]
+    else:
+        ops = raw
+    mask = _visibility_mask(m, past, m, valid)
+    got = oracle.decode_attention(*ops, mask, b, h, hkv, m, past, m, d, 0, dtype)
+    want = oracle.decode_attention_valid(*ops, valid, b, h, hkv, m, past, m, d, 0, dtype)
+    assert np.array_equal(got.view(np.uint8), want.view(np.uint8))
+
+
+def _mask_attention_f64(q, kp, vp, kn, vn, mask, b, h, hkv, m, past, new, d, scale):
+    """The mask form's law in f64 (kernel_call.rs:600-656): every past row then
+    every new row of kv head hi // (h // hkv), score q.k / scale + mask[qi][j],
+    softmax over the finite scores; no finite score gives the zero row."""
+    q = q.reshape(b, h, m, d).astype(np.float64)
+    K = np.concatenate([kp.reshape(b, hkv, past, d), kn.reshape(b, hkv, new, d)], 2).astype(np.float64)
+    V = np.concatenate([vp.reshape(b, hkv, past, d), vn.reshape(b, hkv, new, d)], 2).astype(np.float64)
+    out = np.zeros((b, h, m, d))
+    for bi in range(b):
+        for hi in range(h):
+            kv = hi // (h // hkv)
+            for qi in range(m):
+                s = K[bi, kv] @ q[bi, hi, qi] / scale + mask[qi].astype(np.float64)
+                if not np.isfinite(s).any():
+                    continue
+                p = np.exp(s - s[np.isfinite(s)].max())
+                out[bi, hi, qi] = (p / p.sum()) @ V[bi, kv]
+    return out.ravel()
+
+
+@pytest.mark.parametrize("b,h,hkv,m,past,new,d", [
+    (2, 4, 2, 1, 9, 1, 16), (1, 6, 3, 3, 7, 2, 8), (1, 2, 1, 4, 5, 0, 12), (2, 4, 4, 2, 0, 3, 8)])
+def test_decode_attention_mask_form_matches_f64_law(b, h, hkv, m, past, new, d):
+    """Any q_rows / new_len pairing (decode, frozen cache, no past), a finite
+    additive bias on every key plus erased (-inf) entries; one row fully
+    erased, which the law pins to exact zeros."""
+    rng = np.random.default_rng(b + h * 3 + m * 5 + new)
+    q, kp, vp, kn, vn = (rng.standard_normal(n).astype(np.float32) for n in
+                         (b * h * m * d, b * hkv * past * d, b * hkv * past * d,
+                          b * hkv * new * d, b * hkv * new * d))
+    L = past + new
+    mask = (rng.standard_normal((m, L)) * 2).astype(np.float32)
+    mask[rng.random((m, L)) < 0.3] = -np.inf
+    mask[0, :] = -np.inf
+    got = oracle.decode_attention(q, kp, vp, kn, vn, mask, b, h, hkv, m, past, new, d, 0, F32)
+    want = _mask_attention_f64(q, kp, vp, kn, vn, mask, b, h, hkv, m, past, new, d,
+                               max(math.sqrt(d), 1.0))
+    assert np.max(np.abs(got - want)) <= 1e-6 * (np.max(np.abs(want)) + 1e-6) * 4
+    rows = got.reshape(b, h, m, d)
+    assert np.array_equal(rows[:, :, 0], np.zeros_like(rows[:, :, 0]))
+
+
+def test_decode_attention_mask_form_reads_every_row_and_refuses():
+    """The mask form reads the erased rows (a NaN in an erased V row reaches
+    the output through 0 * NaN, kernel_call.rs:682-685), and refuses an empty
+    key list, a kv_heads that does not divide heads, and integer dtypes."""
+    d = 8
+    rng = np.random.default_rng(1)
+    q, k, v = (rng.standard_normal(n).astype(np.float32) for n in (d, 2 * d, 2 * d))
+    v[d:] = np.nan
+    mask = np.array([[0.0, -np.inf]], np.float32)
+    out = oracle.decode_attention(q, k, v, k[:0], v[:0], mask, 1, 1, 1, 1, 2, 0, d, 0, F32)
+    assert np.isnan(out).all()
+    v[d:] = 0.5
+    out = oracle.decode_attention(q, k, v, k[:0], v[:0], mask, 1, 1, 1, 1, 2, 0, d, 0, F32)
+    assert np.array_equal(out, v[:d])
+    z = np.zeros(64, np.float32)
+    with pytest.raises(ValueError):
+        oracle.decode_attention(z, z, z, z, z, z, 1, 2, 2, 1, 0, 0, 4, 0, F32)
+    with pytest.raises(ValueError):
+        oracle.decode_attention(z, z, z, z, z, z, 1, 3, 2, 1, 1, 1, 4, 0, F32)
+    with pytest.raises(ValueError):
+        oracle.decode_attention(z, z, z, z, z, z, 1, 2, 2, 1, 1, 1, 4, 0, 2)
+
+
 @pytest.mark.parametrize("k,n", [(1, 1), (3, 16), (5, 17), (7, 40), (64, 100)])
 def test_panel_packing_follows_the_layout_formula(k, n):
     """layout.rs:16-45, element by element: packed[(p*k + kk)*16 + c] is

@@ -903,6 +903,7 @@ __global__ __launch_bounds__(kThreads, kWps) void attn_split_kernel(
 // first, then each (head, dim) output as one weighted sum whose loads are
 // issued eight at a time. nseg <= kMaxSeg.
 constexpr uint32_t kMaxSeg = 1024;
+constexpr uint32_t kFastSeg = 8;   // up to this many segments merge in one round trip
 
 template <int D, bool kF32Q>
 __device__ __forceinline__ void merge_partials(const float *__restrict__ src, uint32_t nseg,
@@ -911,6 +912,44 @@ __device__ __forceinline__ void merge_partials(const float *__restrict__ src, ui
                                                float (&inv_l)[16]) {
     const uint32_t tid = threadIdx.x;
     const uint64_t cstride = uint64_t(G) * (D + 2);
+    if (nseg <= kFastSeg && G * D <= 2 * 256) {
+        // Few segments: each thread loads m, l and O of every segment for its
+        // (head, dim) outputs in one go (one memory round trip instead of
+        // three), then weighs them in segment order. Clamped indices keep
+        // every load unconditional.
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const uint32_t idx = tid + 256u * t;
+            const uint32_t h = idx < G * D ? idx / D : 0u, d = idx % D;
+            float mc[kFastSeg], lc[kFastSeg], oc[kFastSeg];
+#pragma unroll
+            for (int c = 0; c < int(kFastSeg); ++c) {
+                const float *ps = src + (uint32_t(c) < nseg ? c : nseg - 1) * cstride + h * (D + 2);
+                mc[c] = ps[0];
+                lc[c] = ps[1];
+                oc[c] = ps[2 + d];
+            }
+            float m = -INFINITY;
+#pragma unroll
+            for (int c = 0; c < int(kFastSeg); ++c) m = uint32_t(c) < nseg ? fmaxf(m, mc[c]) : m;
+            float o = 0.0f, l = 0.0f;
+#pragma unroll
+            for (int c = 0; c < int(kFastSeg); ++c) {
+                if (uint32_t(c) >= nseg) continue;
+                const float w = mc[c] == -INFINITY ? 0.0f : exp2f(mc[c] - m);
+                o = fmaf(oc[c], w, o);
+                l = fmaf(lc[c], w, l);
+            }
+            if (idx >= G * D) continue;
+            const float res = o * (1.0f / l);
+            const uint64_t oi = (uint64_t(b) * H + kh * G + h) * D + d;
+            if constexpr (kF32Q)
+                static_cast<float *>(out)[oi] = res;
+            else
+                static_cast<uint16_t *>(out)[oi] = uint16_t(__float_as_uint(res) >> 16);
+        }
+        return;
+    }
     // per head: M = max_c m_c; wgt[c] = 2^(m_c - M); 1 / sum_c wgt[c] l_c
     if (tid < 64) {
         const uint32_t h = tid & 15, c4 = tid >> 4;    // 4 segment lanes per head

@@ -796,7 +796,8 @@ def main():
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": attn["ms"] if attn else None,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int8 KV, bf16 Q/out, fp32 softmax",
+        "dtype": ("int8 KV, bf16 Q/out, fp32 softmax; QK on int8 MFMA with Q as a 15-bit "
+                  "integer per head (exact int8 halves), P x V on f16 MFMA"),
         "data": "synthetic (seeded N(0,1) K/V with 2% x20 outlier channels, quantized by the "
                 "int8 append op; seeded ragged lengths)",
         "config": {"workload": "config 4: GQA decode attention over int8 KV", "batch": 32,

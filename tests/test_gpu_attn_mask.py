@@ -150,3 +150,37 @@ def test_mask_form_archive_session_matches_oracle_walk(torch_cuda, backend, dtyp
     r = dec(ref.output(0).view(np.float32 if es == 4 else np.uint16), dtype).reshape(-1, d)
     assert row_err(g, r) <= TOL[dtype]
     sess.close()
+
+
+@pytest.mark.parametrize("dtype", [DTYPE_BF16, DTYPE_F32])
+def test_mask_form_split_equals_precatenated_on_device(torch_cuda, backend, dtype):
+    """tests/decode_attention.rs:5-9 on the device, bit for bit: the same keys
+    split past || new, or precatenated as past with no new rows, give the same
+    bytes (the key list, its order and the work split depend on past + new
+    only)."""
+    b, h, hkv, m, past, new, d = 2, 8, 2, 2, 700, 3, 64
+    rng = np.random.default_rng(33)
+    es = 4 if dtype == DTYPE_F32 else 2
+    q = enc(rng.standard_normal(b * h * m * d), dtype)
+    kp, vp = (rng.standard_normal((b, hkv, past, d)) for _ in range(2))
+    kn, vn = (rng.standard_normal((b, hkv, new, d)) for _ in range(2))
+    mask = make_mask(rng, m, past, new, "random").ravel()
+
+    def run(kp_, vp_, kn_, vn_, p_, n_):
+        ws = DeviceWorkspace()
+        ops = [q, enc(kp_.ravel(), dtype), enc(vp_.ravel(), dtype), enc(kn_.ravel(), dtype),
+               enc(vn_.ravel(), dtype), mask]
+        for s_, x in enumerate(ops):
+            ws.bind(s_, to_dev(torch_cuda, x) if x.size else
+                    torch_cuda.zeros(64, dtype=torch_cuda.uint8, device="cuda"))
+        out = torch_cuda.zeros(b * h * m * d * es, dtype=torch_cuda.uint8, device="cuda")
+        ws.bind(6, out)
+        backend.dispatch(KernelCall.DecodeAttention(DecodeAttentionCall(
+            *[BufferRef(s_) for s_ in range(7)], b, h, hkv, m, p_, n_, d, 0, dtype)), ws)
+        backend.synchronize()
+        return out.cpu().numpy()
+
+    split = run(kp, vp, kn, vn, past, new)
+    cat = run(np.concatenate([kp, kn], 2), np.concatenate([vp, vn], 2), kn[:, :, :0],
+              vn[:, :, :0], past + new, 0)
+    assert np.array_equal(split, cat)

@@ -58,6 +58,33 @@ def test_matmul_bf16_dma64_parity(torch_cuda, backend, m, k, n):
     assert err <= 1e-2, f"normalized error {err:.3g}"
 
 
+@pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_BF16])
+@pytest.mark.parametrize("m,k,n", [(7, 65, 40), (16, 4096, 4096), (300, 1000, 257), (1024, 1024, 1024),
+                                   (77, 131, 45), (4096, 512, 1000)])
+def test_matmul_row_bytes_independent_of_row_index(torch_cuda, backend, m, k, n, dtype):
+    """simd.rs:8369 on the device: two rows of A with the same values, one in the
+    first tile and one in the last (ragged) tile, give the same output bytes."""
+    rng = np.random.default_rng(m + k + n)
+    a = (rng.standard_normal(m * k) / np.sqrt(k)).astype(np.float32).reshape(m, k)
+    a[m - 1] = a[0]
+    b = (rng.standard_normal(k * n) / np.sqrt(k)).astype(np.float32)
+    if dtype == DTYPE_BF16:
+        da, db, es, view = (a.view(np.uint32) >> 16).astype(np.uint16), \
+            (b.view(np.uint32) >> 16).astype(np.uint16), 2, np.uint16
+    else:
+        da, db, es, view = a, b, 4, np.float32
+    out = torch_cuda.zeros(m * n * es, dtype=torch_cuda.uint8, device="cuda")
+    ws = DeviceWorkspace()
+    ws.bind(0, to_dev(torch_cuda, da.ravel()))
+    ws.bind(1, to_dev(torch_cuda, db))
+    ws.bind(2, out)
+    backend.dispatch(KernelCall.MatMul(MatMulCall(BufferRef(0), BufferRef(1), BufferRef(2), m, k,
+                                                  n, dtype)), ws)
+    backend.synchronize()
+    c = from_dev(out, view).reshape(m, n)
+    assert np.array_equal(c[0], c[m - 1])
+
+
 def test_bf16_truncates(torch_cuda, backend):
     """bf16 narrowing is truncation (write_bf16, src/cpu/dtype.rs:75-79): the single
     exact product (1 + 2^-7) * 1.5 = 0x3FC18000 narrows to 0x3FC1, where rounding to

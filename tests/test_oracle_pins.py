@@ -588,6 +588,36 @@ def test_decode_attention_mask_form_matches_f64_law(b, h, hkv, m, past, new, d):
     assert np.array_equal(rows[:, :, 0], np.zeros_like(rows[:, :, 0]))
 
 
+def test_decode_attention_mask_form_split_and_padding_witnesses():
+    """The reference's witnesses for the mask form (tests/decode_attention.rs:
+    1-18), bit for bit on the oracle: keys split past || new equal the same
+    keys precatenated as past; and a bucket padded with finite rows the mask
+    erases (-inf) equals the tight call over the realized rows only."""
+    rng = np.random.default_rng(21)
+    b, h, hkv, m, d = 2, 4, 2, 3, 16
+    past, new, pad = 11, 3, 9
+    q = rng.standard_normal(b * h * m * d).astype(np.float32)
+    kp, vp = (rng.standard_normal((b, hkv, past, d)).astype(np.float32) for _ in range(2))
+    kn, vn = (rng.standard_normal((b, hkv, new, d)).astype(np.float32) for _ in range(2))
+    mask = (rng.standard_normal((m, past + new)) * 0.5).astype(np.float32)
+    mask[rng.random((m, past + new)) < 0.25] = -np.inf
+    split = oracle.decode_attention(q, kp.ravel(), vp.ravel(), kn.ravel(), vn.ravel(), mask, b, h,
+                                    hkv, m, past, new, d, 0, F32)
+    kc = np.concatenate([kp, kn], 2).ravel()
+    vc = np.concatenate([vp, vn], 2).ravel()
+    cat = oracle.decode_attention(q, kc, vc, kc[:0], vc[:0], mask, b, h, hkv, m, past + new, 0,
+                                  d, 0, F32)
+    assert np.array_equal(split.view(np.uint32), cat.view(np.uint32))
+    # padded bucket: pad extra finite past rows, erased by -inf in the mask
+    kpad = np.concatenate([kp, rng.standard_normal((b, hkv, pad, d)).astype(np.float32)], 2)
+    vpad = np.concatenate([vp, rng.standard_normal((b, hkv, pad, d)).astype(np.float32)], 2)
+    mpad = np.concatenate([mask[:, :past], np.full((m, pad), -np.inf, np.float32),
+                           mask[:, past:]], 1)
+    padded = oracle.decode_attention(q, kpad.ravel(), vpad.ravel(), kn.ravel(), vn.ravel(), mpad,
+                                     b, h, hkv, m, past + pad, new, d, 0, F32)
+    assert np.array_equal(padded.view(np.uint32), split.view(np.uint32))
+
+
 def test_decode_attention_mask_form_reads_every_row_and_refuses():
     """The mask form reads the erased rows (a NaN in an erased V row reaches
     the output through 0 * NaN, kernel_call.rs:682-685), and refuses an empty

@@ -89,7 +89,12 @@ __device__ __forceinline__ int pick(const EpiArgs &g, uint32_t *first_block) {
 // The product at (row m, column c) of P's column space: partials summed in
 // ks order. Up to kBatch loads go out before the first add, so a split of up
 // to kBatch partials costs one memory round trip; the adds keep ks order.
+// No load sits behind a branch: a batch past ks reloads partial ks - 1 (its
+// value is not added), since a branch around a load makes the compiler wait
+// for every load in flight where the branch joins.
 constexpr uint32_t kBatch = 32;
+
+__device__ __forceinline__ uint32_t clamp_ks(uint32_t k, uint32_t ks) { return k < ks ? k : ks - 1; }
 
 template <class T>
 __device__ __forceinline__ T sum_partials(const T *p, uint64_t plane, uint32_t ks) {
@@ -97,14 +102,28 @@ __device__ __forceinline__ T sum_partials(const T *p, uint64_t plane, uint32_t k
     for (uint32_t k0 = 0; k0 < ks; k0 += kBatch) {
         T v[kBatch];
 #pragma unroll
-        for (uint32_t u = 0; u < kBatch; ++u)
-            if (k0 + u < ks) v[u] = p[(k0 + u) * plane];
+        for (uint32_t u = 0; u < kBatch; ++u) v[u] = p[clamp_ks(k0 + u, ks) * plane];
         if (k0 == 0) s = v[0];
 #pragma unroll
         for (uint32_t u = 0; u < kBatch; ++u)
             if (k0 + u < ks && (k0 | u) != 0) s += v[u];
     }
     return s;
+}
+
+// An optional side operand (residual, cos, sin) read through a buffer range
+// that is empty when the operand is absent: the load then reads 0 without a
+// memory access, so it needs no branch.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t opt_rsrc(const void *p, bool present) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, present ? 0x7fffffff : 0,
+                                             0x00020000);
+}
+template <bool kBf16>
+__device__ __forceinline__ float opt_load(__amdgpu_buffer_rsrc_t r, uint64_t e) {
+    if constexpr (kBf16)
+        return bf2f(__builtin_amdgcn_raw_buffer_load_b16(r, uint32_t(e) * 2u, 0, 0));
+    else
+        return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, uint32_t(e) * 4u, 0, 0));
 }
 
 // 4 consecutive columns (c a multiple of 4), as 16-byte loads.
@@ -122,11 +141,11 @@ __device__ __forceinline__ void product2(const EpiArgs &g, uint32_t m, uint32_t 
     for (uint32_t k0 = 0; k0 < g.ks; k0 += kBatch / 2) {
         float v1[kBatch / 2], v2[kBatch / 2];
 #pragma unroll
-        for (uint32_t u = 0; u < kBatch / 2; ++u)
-            if (k0 + u < g.ks) {
-                v1[u] = p[(k0 + u) * plane];
-                v2[u] = p[(k0 + u) * plane + off];
-            }
+        for (uint32_t u = 0; u < kBatch / 2; ++u) {
+            const uint64_t kk = clamp_ks(k0 + u, g.ks);
+            v1[u] = p[kk * plane];
+            v2[u] = p[kk * plane + off];
+        }
         if (k0 == 0) {
             s1 = v1[0];
             s2 = v2[0];
@@ -198,14 +217,15 @@ __device__ __forceinline__ void elem_segment(const EpiArgs &g, const EpiSeg &sg,
     if (i >= uint64_t(g.m) * sg.n) return;
     const uint32_t m = uint32_t(i / sg.n), c = uint32_t(i % sg.n);
     const uint64_t e0 = uint64_t(m) * sg.n + c;
-    float ra[4] = {0.f, 0.f, 0.f, 0.f}, rb[4] = {0.f, 0.f, 0.f, 0.f};
-    if (has_residual(sg))
-#pragma unroll
-        for (uint32_t j = 0; j < 4; ++j) ra[j] = load<kBf16>(sg.residual, e0 + j);
+    float ra[4], rb[4];
     const bool pair = sg.pair >= 0;
-    if (pair && has_residual(pr))
+    const auto rra = opt_rsrc(sg.residual, has_residual(sg));
+    const auto rrb = opt_rsrc(pr.residual, pair && has_residual(pr));
 #pragma unroll
-        for (uint32_t j = 0; j < 4; ++j) rb[j] = load<kBf16>(pr.residual, e0 + j);
+    for (uint32_t j = 0; j < 4; ++j) {
+        ra[j] = opt_load<kBf16>(rra, e0 + j);
+        rb[j] = opt_load<kBf16>(rrb, e0 + j);
+    }
     f32x4 va, vb = f32x4{0.f, 0.f, 0.f, 0.f};
     if (!pair) {
         va = product4(g, m, sg.col0 + c);
@@ -217,11 +237,11 @@ __device__ __forceinline__ void elem_segment(const EpiArgs &g, const EpiSeg &sg,
         for (uint32_t k0 = 0; k0 < g.ks; k0 += kBatch / 2) {
             f32x4 xa[kBatch / 2], xb[kBatch / 2];
 #pragma unroll
-            for (uint32_t u = 0; u < kBatch / 2; ++u)
-                if (k0 + u < g.ks) {
-                    xa[u] = pa[(k0 + u) * plane];
-                    xb[u] = pb[(k0 + u) * plane];
-                }
+            for (uint32_t u = 0; u < kBatch / 2; ++u) {
+                const uint64_t kk = clamp_ks(k0 + u, g.ks);
+                xa[u] = pa[kk * plane];
+                xb[u] = pb[kk * plane];
+            }
             if (k0 == 0) {
                 va = xa[0];
                 vb = xb[0];
@@ -257,30 +277,25 @@ __device__ __forceinline__ void head_segment(const EpiArgs &g, const EpiSeg &sg,
     const uint32_t hl = threadIdx.x / half, d = threadIdx.x % half;
     const uint32_t heads_row = sg.n / D;
     const uint64_t head = uint64_t(blk) * heads_per_block + hl;
-    const bool live = head < uint64_t(g.m) * heads_row;
-    float x1 = 0.0f, x2 = 0.0f;
-    uint64_t e1 = 0;
+    const uint64_t nheads = uint64_t(g.m) * heads_row;
+    const bool live = head < nheads;
+    // every lane loads (a lane past the last head reads the last head), so no
+    // load sits behind a branch; only live lanes store
+    const uint64_t hc = live ? head : nheads - 1;
+    const uint32_t m = uint32_t(hc / heads_row), h = uint32_t(hc % heads_row);
+    const uint32_t c1 = h * D + d;
+    const uint64_t e1 = uint64_t(m) * sg.n + c1;
+    // side operands first: their loads overlap the partials'
+    const auto rc = opt_rsrc(sg.cos, sg.rope), rs = opt_rsrc(sg.sin, sg.rope);
+    const auto rr = opt_rsrc(sg.residual, has_residual(sg));
+    const float c1v = opt_load<kBf16>(rc, e1), s1v = opt_load<kBf16>(rs, e1);
+    const float c2v = opt_load<kBf16>(rc, e1 + half), s2v = opt_load<kBf16>(rs, e1 + half);
+    const float r1 = opt_load<kBf16>(rr, e1), r2 = opt_load<kBf16>(rr, e1 + half);
+    float p1, p2;
+    product2(g, m, sg.col0 + c1, half, &p1, &p2);
+    float x1 = base_value<kBf16>(sg, p1, r1);
+    float x2 = base_value<kBf16>(sg, p2, r2);
     if (live) {
-        const uint32_t m = uint32_t(head / heads_row), h = uint32_t(head % heads_row);
-        const uint32_t c1 = h * D + d;
-        e1 = uint64_t(m) * sg.n + c1;
-        // side operands first: their loads overlap the partials'
-        float c1v = 0.f, s1v = 0.f, c2v = 0.f, s2v = 0.f;
-        if (sg.rope) {
-            c1v = load<kBf16>(sg.cos, e1);
-            s1v = load<kBf16>(sg.sin, e1);
-            c2v = load<kBf16>(sg.cos, e1 + half);
-            s2v = load<kBf16>(sg.sin, e1 + half);
-        }
-        float r1 = 0.f, r2 = 0.f;
-        if (has_residual(sg)) {
-            r1 = load<kBf16>(sg.residual, e1);
-            r2 = load<kBf16>(sg.residual, e1 + half);
-        }
-        float p1, p2;
-        product2(g, m, sg.col0 + c1, half, &p1, &p2);
-        x1 = base_value<kBf16>(sg, p1, r1);
-        x2 = base_value<kBf16>(sg, p2, r2);
         if (sg.out) {
             store<kBf16>(sg.out, e1, x1);
             store<kBf16>(sg.out, e1 + half, x2);
@@ -338,6 +353,7 @@ __device__ __forceinline__ void head_segment(const EpiArgs &g, const EpiSeg &sg,
 // l of wave w holds vectors 64w + l + 256u, computes the same per-lane sum and
 // the same tree, and stores the wave's sum; the reader adds the four in order.
 constexpr uint32_t kStatVec = 4;   // vectors per lane: n <= 8 * 256 * 4
+constexpr uint32_t kStatBatch = 16;  // partials per column pair in flight at once
 
 __global__ __launch_bounds__(kEpiThreads) void epilogue_stat_kernel(const EpiArgs g) {
     const EpiSeg &sg = g.seg[0];
@@ -351,23 +367,27 @@ __global__ __launch_bounds__(kEpiThreads) void epilogue_stat_kernel(const EpiArg
         const uint32_t v = 64 * w + l + 256 * u;
         if (v >= nv) break;
         const uint64_t e0 = uint64_t(r) * sg.n + 8ull * v;
-        const u32x4 res = add ? reinterpret_cast<const u32x4 *>(sg.residual)[e0 / 8]
-                              : u32x4{0u, 0u, 0u, 0u};
-        // columns 8v .. 8v+3 and 8v+4 .. 8v+7: both halves' partials in flight
-        // together, summed in ks order
+        const u32x4 res = __builtin_amdgcn_raw_buffer_load_b128(
+            opt_rsrc(sg.residual, add), uint32_t(e0) * 2u, 0, 0);
+        // columns 8v .. 8v+3 and 8v+4 .. 8v+7: the residual and both halves'
+        // partials (up to 16 of each) in flight together, summed in ks order
         const f32x4 *pa = reinterpret_cast<const f32x4 *>(g.P + uint64_t(r) * g.ntot + sg.col0 + 8 * v);
-        f32x4 va = pa[0], vb = pa[1];
-        for (uint32_t k0 = 1; k0 < g.ks; k0 += 8) {
-            f32x4 xa[8], xb[8];
+        f32x4 va, vb;
+        for (uint32_t k0 = 0; k0 < g.ks; k0 += kStatBatch) {
+            f32x4 xa[kStatBatch], xb[kStatBatch];
 #pragma unroll
-            for (uint32_t i = 0; i < 8; ++i)
-                if (k0 + i < g.ks) {
-                    xa[i] = pa[(k0 + i) * plane];
-                    xb[i] = pa[(k0 + i) * plane + 1];
-                }
+            for (uint32_t i = 0; i < kStatBatch; ++i) {
+                const uint64_t kk = clamp_ks(k0 + i, g.ks);
+                xa[i] = pa[kk * plane];
+                xb[i] = pa[kk * plane + 1];
+            }
+            if (k0 == 0) {
+                va = xa[0];
+                vb = xb[0];
+            }
 #pragma unroll
-            for (uint32_t i = 0; i < 8; ++i)
-                if (k0 + i < g.ks) {
+            for (uint32_t i = 0; i < kStatBatch; ++i)
+                if (k0 + i < g.ks && (k0 | i) != 0) {
                     va += xa[i];
                     vb += xb[i];
                 }
@@ -497,6 +517,9 @@ hipError_t launch_tile_epilogue(void *c, uint64_t count, bool bf16, const TileEp
 
 hipError_t launch_epilogue(EpiArgs g, hipStream_t stream) {
     if (g.nseg < 1 || g.nseg > uint32_t(kSkinnyMaxSeg)) return hipErrorInvalidValue;
+    // side operands are read through 32-bit buffer offsets
+    for (uint32_t i = 0; i < g.nseg; ++i)
+        if (uint64_t(g.m) * g.seg[i].n * (g.bf16 ? 2 : 4) > 0x7fffffffull) return hipErrorInvalidValue;
     if (g.seg[0].ssq) {
         const EpiSeg &s = g.seg[0];
         if (g.nseg != 1 || !g.bf16 || s.head_dim || s.pair >= 0 || s.skip || s.n % 8 != 0 ||

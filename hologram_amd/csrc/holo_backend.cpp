@@ -333,6 +333,8 @@ int dispatch_group_impl(holo_backend *be, const SlotTable &st, const holo::Group
         ss[i] = holo::SkinnySegment{v.base, s.n};
         const holo::SkinnyPlan p = holo::matmul_skinny_plan(g.m, g.k, s.n, g.dtype);
         if (p.mt != plan.mt || p.steps != plan.steps || p.ks != plan.ks) fast = false;
+        // the few-row epilogue reads side operands through 32-bit offsets
+        if (mn * es > 0x7fffffffull) fast = false;
         d.n = s.n;
         d.col0 = ntot;
         ntot += s.n;

@@ -119,9 +119,8 @@ def cpu_time(fn, min_seconds):
 def cpu_baseline_obj(value_multi, value_single, unit, threads, sample):
     """The cpu_baseline record: the multi-threaded leg is `value` (cores =
     its threads), the single-threaded leg beside it, and the host."""
-    import oracle
     return {"value": value_multi, "unit": unit, "cores": threads, "kind": "port",
-            "sample": sample, "single_thread": value_single, "host": oracle.host_info()}
+            "sample": sample, "single_thread": value_single}
 
 
 def bf16_normal(torch, shape, gen, outlier_frac=0.0):
@@ -230,9 +229,8 @@ def cpu_attn(torch, kq, ks, vq, vs, q, lens, B, H, Hkv, bucket, D, min_seconds=1
     sec, passes, dt = cpu_time(run(th), min_seconds)
     sec1, passes1, dt1 = cpu_time(run(1), min_seconds / 2)
     return cpu_baseline_obj(B / sec, B / sec1, "tok/s", th,
-                            f"the full config-4 batch ({B} sequences, {int(lens.sum())} keys): "
-                            f"{passes} passes in {dt:.1f} s on {th} threads, {passes1} in "
-                            f"{dt1:.1f} s on 1")
+                            f"full batch ({B} seq, {int(lens.sum())} keys): x{passes} "
+                            f"{th}thr, x{passes1} 1thr")
 
 
 # --------------------------------------------------------------- config 1 ----
@@ -272,8 +270,7 @@ def bench_lut(torch, be, args, rep):
         sec, reps, _ = cpu_time(run(th), 6.0)
         sec1, reps1, _ = cpu_time(run(1), 3.0)
         rep["lut_cpu"] = cpu_baseline_obj(n / sec / 1e9, n / sec1 / 1e9, "Gelem/s", th,
-                                          f"GELU gather of the 16,777,216 elements: x{reps} on "
-                                          f"{th} threads, x{reps1} on 1")
+                                          f"16M GELU gather: x{reps} {th}thr, x{reps1} 1thr")
     return res
 
 
@@ -364,8 +361,7 @@ def bench_kv(torch, be, args, rep):
         sec1, n2, _ = cpu_time(copy_step(1), 3.0)
         res["cpu_baseline"] = cpu_baseline_obj(
             1.0 / sec, 1.0 / sec1, "steps/s", th,
-            f"honest-copy form of one config-3 step (K and V: copy 2 x 66 MiB, quantize and place "
-            f"the 128 new rows): x{n1} on {th} threads, x{n2} on 1")
+            f"copy-form step (K, V): x{n1} {th}thr, x{n2} 1thr")
         def move_step():
             for _ in range(2):
                 lib.or_kv_quant_append(p(nw), DTYPE_BF16, 4095, p(hq[0]), p(hq[1]), planes, bucket,
@@ -452,8 +448,8 @@ def cpu_gemm(ab, m, k, n, dt, single):
     sec, reps, _ = cpu_time(run(th), 2.0)
     sec1, reps1 = (cpu_time(run(1), 2.0)[:2] if single else (None, 0))
     return cpu_baseline_obj(flops / sec / 1e12, flops / sec1 / 1e12 if sec1 else None, "TFLOP/s",
-                            th, f"{m}x{n}x{k}: x{reps} on {th} threads"
-                                + (f", x{reps1} on 1" if single else ""))
+                            th, f"whole product x{reps} {th}thr"
+                                + (f", x{reps1} 1thr" if single else ""))
 
 
 # --------------------------------------------------------------- config 5 ----
@@ -599,9 +595,9 @@ def bench_e2e(torch, be, args, rep):
                    "generate": gen_len, "bucket": cfg.bucket, "kv": "int8",
                    "weights": "bf16 ~ N(0, 0.02), seeded", "vocab_note": "32,000 assumed"},
         "roofline": roofline("hbm", (w_bytes + kv_bytes) / (step_ms / 1e3) / 1e9, HBM_PEAK_GBS,
-                             "GB/s", kernel="whole decode step (weights + int8 KV per step)"),
+                             "GB/s", kernel="decode step: weights + int8 KV"),
         "prefill_roofline": roofline("mfma", pre_tflops, BF16_PEAK_TFLOPS, "TFLOP/s",
-                                     kernel="whole prompt pass (8 x 512 tokens)"),
+                                     kernel="prompt pass"),
     }
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_decode_step(cfg, dec_archive, int(mean_len))
@@ -638,8 +634,8 @@ def cpu_decode_step(cfg, archive, length):
         del o
     (sec, n, _), (sec1, n1, _) = walks[th], walks[1]
     return cpu_baseline_obj(cfg.batch / sec, cfg.batch / sec1, "tok/s", th,
-                            f"decode steps of the full {cfg.layers}-layer archive at context "
-                            f"{length}: x{n} on {th} threads, x{n1} on 1")
+                            f"{cfg.layers}-layer decode step at ctx {length}: x{n} {th}thr, "
+                            f"x{n1} 1thr")
 
 
 # ------------------------------------------------------- copy ceiling ----
@@ -725,9 +721,7 @@ def bench_w8a8(torch, be, args, rep):
         res[name] = {"m": m, "k": k, "n": n, "us": ms * 1e3,
                      "gmac_s": m * k * n / (ms / 1e3) / 1e9,
                      "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s",
-                                          profiled_traffic(f"w8a8_{name}"),
-                                          f"quant_rows_kernel + gemm_q_omajor_kernel; "
-                                          f"algorithmic bytes {alg}")}
+                                          profiled_traffic(f"w8a8_{name}"))}
         del calls, ws
         torch.cuda.empty_cache()
     res["reference_published"] = {"i8_decode_gmac_s": 14.4, "i4_decode_gmac_s": 13.1,
@@ -744,11 +738,75 @@ def bench_w8a8(torch, be, args, rep):
         sec, reps, _ = cpu_time(lambda: oracle.matmul_i8_pc_omajor(a, w, sc, 1, k, n), 3.0)
         g = k * n / sec / 1e9
         res["cpu_baseline"] = {"value": g, "unit": "GMAC/s", "cores": 1, "kind": "port",
-                               "sample": f"i8 m=1 k={k} n={n} (1/16 of the decode columns) "
-                                         f"x{reps} through the scalar oracle",
-                               "host": oracle.host_info()}
+                               "sample": f"i8 m=1 k={k} n={n} (1/16 of n): x{reps} 1thr"}
     rep["w8a8"] = res
     return res
+
+
+def rounded(x, sig=4):
+    """Floats rounded to `sig` significant digits, recursively, so the one
+    JSON line stays short enough for a log tail to hold it whole."""
+    if isinstance(x, float):
+        if x != x or x in (float("inf"), float("-inf")) or x == 0.0:
+            return x
+        return float(f"{x:.{sig}g}")
+    if isinstance(x, dict):
+        return {k: rounded(v, sig) for k, v in x.items()}
+    if isinstance(x, (list, tuple)):
+        return [rounded(v, sig) for v in x]
+    return x
+
+
+def compact_components(rep):
+    """One short record per config leg: the headline figure, its roofline
+    object and its cpu_baseline (figures only; the host is reported once)."""
+    comps = {}
+    if "lut" in rep:
+        cp = rep.get("copy", {}).get("copy16_kernel", {}).get("us")
+        lut = {}
+        for k, v in rep["lut"].items():
+            lut[k] = {"gelem_s": v["gelem_s"], "us": v["us"],
+                      "roofline": roofline("hbm", v["hbm_gbs"], HBM_PEAK_GBS, "GB/s",
+                                           profiled_traffic("lut_gather_bf16_16M"))}
+            if cp:
+                lut[k]["vs_copy"] = cp / v["us"]
+        if "lut_cpu" in rep:
+            lut["cpu_baseline"] = rep["lut_cpu"]
+        comps["c1_lut_bf16_16M"] = lut
+    if "copy" in rep:
+        c = rep["copy"]
+        comps["copy_ceiling_64MiB"] = {"us": c["copy16_kernel"]["us"],
+                                       "roofline": c["copy16_kernel"]["roofline"],
+                                       "hip_memcpy_us": c["hip_memcpy_d2d"]["us"]}
+    if "kv" in rep:
+        kv = rep["kv"]
+        comps["c3_kv_append"] = {
+            "copy": {k: kv["copy"][k] for k in ("us_per_step", "launches_per_step", "roofline")
+                     if k in kv["copy"]},
+            "in_place": {k: kv["in_place"][k] for k in ("us_per_step", "vs_launch_floor",
+                                                        "roofline")},
+            "launch_floor_us": kv["launch_floor_us_per_kernel"]}
+        if "cpu_baseline" in kv:
+            comps["c3_kv_append"]["cpu_baseline"] = kv["cpu_baseline"]
+    if "gemm" in rep:
+        g = {}
+        for k, v in rep["gemm"].items():
+            g[k] = {"us": v["ms"] * 1e3, "roofline": v["roofline"]}
+            if "cpu_baseline" in v:
+                g[k]["cpu_baseline"] = v["cpu_baseline"]
+        comps["c2_gemm"] = g
+    if "w8a8" in rep:
+        w = {k: {"us": v["us"], "gmac_s": v["gmac_s"], "roofline": v["roofline"]}
+             for k, v in rep["w8a8"].items() if isinstance(v, dict) and "us" in v}
+        if "cpu_baseline" in rep["w8a8"]:
+            w["cpu_baseline"] = rep["w8a8"]["cpu_baseline"]
+        comps["w8a8_gemv"] = w
+    if "e2e" in rep:
+        e = rep["e2e"]
+        comps["c5_e2e_1b"] = {k: e[k] for k in (
+            "decode_tok_s", "decode_ms_per_step", "prefill_tok_s", "prefill_ms", "roofline",
+            "prefill_roofline", "decode_walk", "cpu_baseline") if k in e}
+    return comps
 
 
 def main():
@@ -805,46 +863,21 @@ def main():
                    "len_dist": "U[512, 32768]", "sum_len": attn["sum_len"] if attn else None},
     }
     if attn:
-        line["roofline"] = roofline(
-            "hbm", attn["hbm_gbs"], HBM_PEAK_GBS, "GB/s", profiled_traffic("decode_attn_i8_config4"),
-            "attn_split_kernel + attn_merge_kernel (one DecodeAttentionI8 dispatch); "
-            f"algorithmic bytes {attn['alg_bytes']}")
+        line["roofline"] = roofline("hbm", attn["hbm_gbs"], HBM_PEAK_GBS, "GB/s",
+                                    profiled_traffic("decode_attn_i8_config4"),
+                                    "attn_split_kernel+attn_merge_kernel")
+        line["alg_bytes"] = attn["alg_bytes"]
     if "attn_cpu" in rep:
-        c = rep["attn_cpu"]
-        line["cpu_baseline"] = {k: c[k] for k in ("value", "unit", "cores", "kind", "sample",
-                                                  "single_thread", "host")}
-    comps = {}
-    if "lut" in rep:
-        comps["lut_bf16_16M"] = {
-            k: {"gelem_s": v["gelem_s"], "us": v["us"],
-                "roofline": roofline("hbm", v["hbm_gbs"], HBM_PEAK_GBS, "GB/s",
-                                     profiled_traffic("lut_gather_bf16_16M"),
-                                     "lut_gather_kernel; algorithmic bytes 67108864")}
-            for k, v in rep["lut"].items()}
-        if "lut_cpu" in rep:
-            comps["lut_bf16_16M"]["cpu_baseline"] = rep["lut_cpu"]
-        if "copy" in rep:
-            cp = rep["copy"]["copy16_kernel"]["us"]
-            for k in rep["lut"]:
-                comps["lut_bf16_16M"][k]["vs_copy_ceiling"] = cp / rep["lut"][k]["us"]
-    if "copy" in rep:
-        comps["copy_ceiling_64MiB"] = rep["copy"]
-    if "kv" in rep:
-        comps["kv_quant_append"] = rep["kv"]
-    if "gemm" in rep:
-        comps["gemm"] = rep["gemm"]
-    if "w8a8" in rep:
-        comps["matmul_dequant_w8a8"] = rep["w8a8"]
-    if attn:
-        comps["decode_attn_i8"] = {k: attn[k] for k in ("tok_s", "hbm_gbs", "ms", "gflops",
-                                                        "wall_ms_per_step")}
-    if "e2e" in rep:
-        comps["e2e_decoder_1b"] = rep["e2e"]
-    comps["timing"] = ("headline: HIP events per step; components: HIP events around "
-                       "back-to-back calls queued behind a spin kernel (GPU time per call)")
-    line["components"] = comps
+        line["cpu_baseline"] = rep["attn_cpu"]
+    if not args.no_cpu:
+        import oracle
+        line["host"] = oracle.host_info()
+    line["components"] = compact_components(rep)
+    line["timing"] = ("headline: HIP events per step; components: HIP events around "
+                      "back-to-back calls queued behind a spin kernel (GPU time per call)")
     line["bench_wall_s"] = time.perf_counter() - t_all
-    print(json.dumps(line))
+    line = rounded(line)
+    print(json.dumps(line, separators=(",", ":")))
 
 
 if __name__ == "__main__":

@@ -170,21 +170,33 @@ __global__ __launch_bounds__(kThreads) void attn_valid_split_kernel(AttnValidArg
             }
         }
         __syncthreads();
-        // PV: slot i of this thread is (row, column) = divmod(tid + 256 i, D)
+        // PV: slot i of this thread is (row, column) = divmod(tid + 256 i, D).
+        // A valid-form row's list ends at its causal limit: keys past it are
+        // not in the row's list at all (not even as 0 * v, which a non-finite
+        // v would turn into NaN). The mask form's list is every key.
 #pragma unroll
         for (int i = 0; i < kNacc; ++i) {
             const uint32_t idx = tid + kThreads * uint32_t(i);
             if (idx < nr * D) {
                 const uint32_t rr = idx / D, c = idx % D;
+                uint32_t kend = nk;
+                if (!a.mask) {
+                    const uint32_t qi = (r0 + rr) % a.M;
+                    const uint32_t lim = vis_past + (qi + 1 < a.nnew ? qi + 1 : a.nnew);
+                    const uint32_t room = lim > jb ? lim - jb : 0;
+                    kend = room < nk ? room : nk;
+                }
                 float x = acc[i] * alpha[rr];
                 const float *pr = sc + rr * KB;
-                for (uint32_t key = 0; key < nk; ++key) x = fmaf(pr[key], vs[key * D + c], x);
+                for (uint32_t key = 0; key < kend; ++key) x = fmaf(pr[key], vs[key * D + c], x);
                 acc[i] = x;
             }
         }
         __syncthreads();
     }
-    // a single share finishes the rows; several leave (m, l, acc) partials
+    // a single share finishes the rows; several leave (m, l, acc) partials.
+    // A row with no visible key (every score -inf) is the exact zero row
+    // (float_kernels.rs:2446-2453, :3849-3852), whatever its keys' v rows hold.
     if (nsplit == 1) {
 #pragma unroll
         for (int i = 0; i < kNacc; ++i) {
@@ -192,7 +204,8 @@ __global__ __launch_bounds__(kThreads) void attn_valid_split_kernel(AttnValidArg
             if (idx < nr * D) {
                 const uint32_t rr = idx / D;
                 const float l = lrow[rr];
-                st_elem<DT>(a.out, qrow0 * D + idx, acc[i] / (l > 1e-30f ? l : 1e-30f));
+                const float o = mrow[rr] == -INFINITY ? 0.0f : acc[i] / (l > 1e-30f ? l : 1e-30f);
+                st_elem<DT>(a.out, qrow0 * D + idx, o);
             }
         }
         return;
@@ -214,13 +227,16 @@ __global__ __launch_bounds__(kThreads) void attn_valid_split_kernel(AttnValidArg
 }
 
 // One workgroup per query row: the shares' weights exp(m_s - M) first (share
-// order), then out = sum_s w_s acc_s / max(sum_s w_s l_s, 1e-30).
+// order), then out = sum_s w_s acc_s / max(sum_s w_s l_s, 1e-30). Every share
+// enters the sum, so a share whose keys the row weighs 0 still passes on
+// 0 * v (a non-finite v reaches the output, as in the reference's axpy); a row
+// with no visible key in any share is the exact zero row.
 template <int DT>
 __global__ __launch_bounds__(kThreads) void attn_valid_merge_kernel(AttnValidArgs a, uint32_t RT,
                                                                     uint32_t nsplit, uint32_t ntiles,
                                                                     const float *__restrict__ part) {
     __shared__ float w[256];
-    __shared__ float denom;
+    __shared__ float denom, mxs;
     const uint32_t D = a.D, G = a.H / a.Hkv, R = G * a.M;
     const uint32_t plane = blockIdx.x / R, r = blockIdx.x % R;
     const uint32_t tile = r / RT, rr = r % RT;
@@ -241,12 +257,14 @@ __global__ __launch_bounds__(kThreads) void attn_valid_merge_kernel(AttnValidArg
             l = l + ws * row_of(s)[1];
         }
         denom = l > 1e-30f ? l : 1e-30f;
+        mxs = mx;
     }
     __syncthreads();
+    const bool none = mxs == -INFINITY;
     for (uint32_t c = threadIdx.x; c < D; c += kThreads) {
         float x = 0.0f;
-        for (uint32_t s = 0; s < nsplit; ++s)
-            if (w[s] != 0.0f) x = fmaf(w[s], row_of(s)[2 + c], x);
+        if (!none)
+            for (uint32_t s = 0; s < nsplit; ++s) x = fmaf(w[s], row_of(s)[2 + c], x);
         st_elem<DT>(a.out, qrow * D + c, x / denom);
     }
 }

@@ -26,10 +26,12 @@
 // removes the per-node host cost from a decode step (the reference's ~191 ns
 // per node is per-execute host work that a GPU walk must not serialize on).
 //
-// Not carried over: κ-label derivation per node and the graph memo (the
-// benchmarks run with memo hits disabled, and labels only key reuse), load-time
-// fusion passes (the archives this backend runs carry unfused ops), paged
-// weight providers, leases and warm-start sections (WarmStart is ignored).
+// Also here: the loader's fusion passes (fuse_dequant_matmul,
+// fuse_matmul_epilogue, fuse_dequant_activation, session.rs:493-509, 1853-2373)
+// and a device fusion of this backend's own; κ-labels derived for every node
+// (holo_kappa.cpp) and the whole-graph memo with its off switch.
+// Not carried over: paged weight providers, leases and warm-start sections
+// (WarmStart is ignored).
 #include <hip/hip_runtime.h>
 #include <string.h>
 

@@ -192,7 +192,8 @@ typedef struct holo_argmax_call {
 
 /* MatMulCall, kernel_call.rs:49-65. Row-major A[m,k] * B[k,n] -> C[m,n];
  * f32 or bf16 (fp32 accumulation, bf16 result narrowed by truncation,
- * src/cpu/float_kernels.rs:368-392). b_packed = 1 is refused (UnsupportedOp). */
+ * src/cpu/float_kernels.rs:368-392). b_packed = 1 (f32 only) reads B in the
+ * reference compiler's panel layout, f32[ceil(n/16)][k][16] (src/layout.rs:16-45). */
 typedef struct holo_matmul_call {
     holo_buffer_ref a;
     holo_buffer_ref b;

@@ -184,3 +184,47 @@ def test_mask_form_split_equals_precatenated_on_device(torch_cuda, backend, dtyp
     cat = run(np.concatenate([kp, kn], 2), np.concatenate([vp, vn], 2), kn[:, :, :0],
               vn[:, :, :0], past + new, 0)
     assert np.array_equal(split, cat)
+
+
+@pytest.mark.parametrize("b,h,hkv,m,past,new,d", [
+    (2, 2, 0, 2, 0, 5, 32),          # one share, no merge
+    (2, 32, 8, 1, 4096, 1, 128),     # split + merge
+])
+def test_mask_form_erased_row_is_zero_over_non_finite_v(torch_cuda, backend, b, h, hkv, m, past,
+                                                        new, d):
+    """A query row whose mask erases every key is the exact zero row
+    (float_kernels.rs:2446-2453) even where the v rows hold NaN and Inf; a row
+    that sees any key passes an erased key's NaN on as 0 * NaN, as the
+    reference's axpy does, and the oracle marks the same elements NaN."""
+    dtype = DTYPE_F32
+    rng = np.random.default_rng(21)
+    hk = h if hkv == 0 else hkv
+    L = past + new
+    q = rng.standard_normal(b * h * m * d).astype(np.float32)
+    kp, vp = (rng.standard_normal((b, hk, past, d)).astype(np.float32) for _ in range(2))
+    kn, vn = (rng.standard_normal((b, hk, new, d)).astype(np.float32) for _ in range(2))
+    mask = np.zeros((m, L), np.float32)
+    mask[:, L // 2] = -np.inf                    # erased for every row; its v is non-finite
+    mask[m - 1, :] = -np.inf                     # the last row sees nothing
+    vrow = L // 2
+    tgt = vp if vrow < past else vn
+    j = vrow if vrow < past else vrow - past
+    tgt[:, :, j, ::2] = np.nan
+    tgt[:, :, j, 1::2] = np.inf
+    ops = [q, kp.ravel(), vp.ravel(), kn.ravel(), vn.ravel()]
+    ws = DeviceWorkspace()
+    for s, x in enumerate(ops + [mask.ravel()]):
+        ws.bind(s, to_dev(torch_cuda, x) if x.size else
+                torch_cuda.zeros(64, dtype=torch_cuda.uint8, device="cuda"))
+    out = torch_cuda.full((b * h * m * d * 4,), 0x55, dtype=torch_cuda.uint8, device="cuda")
+    ws.bind(6, out)
+    backend.dispatch(KernelCall.DecodeAttention(DecodeAttentionCall(
+        *[BufferRef(s) for s in range(7)], b, h, hkv, m, past, new, d, 0, dtype)), ws)
+    backend.synchronize()
+    got = out.cpu().numpy().view(np.float32).reshape(b, h, m, d)
+    want = oracle.decode_attention(*ops, mask.ravel(), b, h, hkv, m, past, new, d, 0,
+                                   dtype).reshape(b, h, m, d)
+    assert np.array_equal(got[:, :, m - 1], np.zeros_like(got[:, :, m - 1]))
+    assert np.array_equal(want[:, :, m - 1], np.zeros_like(want[:, :, m - 1]))
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(np.isinf(got), np.isinf(want))

@@ -133,3 +133,40 @@ def test_decode_attention_valid_refuses_unpaired_rows(torch_cuda, backend):
     with pytest.raises(UnsupportedOp):            # q_rows != new_len (float_kernels.rs:4205)
         backend.dispatch(KernelCall.DecodeAttentionValid(DecodeAttentionValidCall(
             *[BufferRef(s) for s in range(7)], 1, 4, 2, 2, 16, 1, 64, 0, DTYPE_F32)), ws)
+
+
+@pytest.mark.parametrize("b,h,hkv,m,past,valid,d", [
+    (64, 8, 8, 4, 16, 16, 32),      # 512 planes: one share, no merge
+    (1, 8, 2, 4, 256, 100, 64),     # split + merge
+])
+def test_decode_attention_valid_non_finite_v_past_the_causal_limit(torch_cuda, backend, b, h, hkv,
+                                                                   m, past, valid, d):
+    """A new row past a query row's causal limit is not in that row's key list
+    (float_kernels.rs:3899-3957), so NaN and Inf in its v row reach only the
+    rows that see it, exactly where the oracle puts them."""
+    dtype = DTYPE_F32
+    rng = np.random.default_rng(9)
+    hk = h if hkv == 0 else hkv
+    q = rng.standard_normal(b * h * m * d).astype(np.float32)
+    kp = rng.standard_normal(b * hk * past * d).astype(np.float32)
+    vp = rng.standard_normal(b * hk * past * d).astype(np.float32)
+    kn = rng.standard_normal(b * hk * m * d).astype(np.float32)
+    vn = rng.standard_normal((b, hk, m, d)).astype(np.float32)
+    vn[:, :, m - 1, ::2] = np.nan                # the last new row: only row m-1 sees it
+    vn[:, :, m - 1, 1::2] = np.inf
+    ops = [q, kp, vp, kn, vn.ravel()]
+    ws = DeviceWorkspace()
+    for s, x in enumerate(ops + [np.array([valid], np.uint32)]):
+        ws.bind(s, to_dev(torch_cuda, x))
+    out = torch_cuda.zeros(b * h * m * d * 4, dtype=torch_cuda.uint8, device="cuda")
+    ws.bind(6, out)
+    backend.dispatch(KernelCall.DecodeAttentionValid(DecodeAttentionValidCall(
+        *[BufferRef(s) for s in range(7)], b, h, hkv, m, past, m, d, 0, dtype)), ws)
+    backend.synchronize()
+    got = out.cpu().numpy().view(np.float32).reshape(b, h, m, d)
+    want = oracle.decode_attention_valid(*ops, valid, b, h, hkv, m, past, m, d, 0,
+                                         dtype).reshape(b, h, m, d)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(np.isinf(got), np.isinf(want))
+    assert not np.isnan(got[:, :, :m - 1]).any()
+    assert row_err(got[:, :, :m - 1].reshape(-1, d), want[:, :, :m - 1].reshape(-1, d)) <= 1e-5

@@ -8,8 +8,11 @@ archive) finishes in seconds; every kernel shape and every fused group of the
 Checked against the oracle, with the fusions on (the product path):
 - the prompt pass: each sequence's last-row logits; the greedy pick equal up
   to a near-tie; the int8 K/V rows and scales appended for all 512 rows;
-- three decode steps continuing from those caches (both walks fed the
-  oracle's greedy tokens): the same logits bounds per step.
+- four decode steps continuing from those caches (both walks fed the
+  oracle's greedy tokens): the same logits bounds per step, and the device's
+  own greedy pick (its ArgMax output, the token the next step would read)
+  equal to the oracle's at every step and sequence, up to a near-tie (the
+  device's pick scores within the logits bound of the oracle's maximum).
 
 The logits bound. The logits are bf16, narrowed by truncation, and so is
 every activation before them. Two correct walks that sum in different orders
@@ -116,7 +119,8 @@ def test_config5_shape_prompt_and_decode_match_oracle(torch_cuda, backend):
                 d_.set_input(7 + 4 * layer + j, r.output(2 + 4 * layer + j).tobytes())
     del refs
     tokens = np.asarray([int(np.argmax(want[b])) for b in range(cfg.batch)], np.int32)
-    for s in range(3):
+    same = 0
+    for s in range(4):
         for i, b in enumerate(decode_inputs(cfg, T + s, tokens)):
             dec.write_input(i, b)
             for d_ in decs:
@@ -128,10 +132,16 @@ def test_config5_shape_prompt_and_decode_match_oracle(torch_cuda, backend):
         got = bf(dec.read_output(1)).reshape(cfg.batch, -1)
         want, want32 = (bf(d_.output(1).tobytes()).reshape(cfg.batch, -1) for d_ in decs)
         check_logits(got, want, want32, f"decode step {s} logits")
+        picks = np.frombuffer(dec.read_output(0), np.int32)[:cfg.batch]
+        scale = float(np.max(np.abs(want)))
+        for b in range(cfg.batch):
+            assert want[b, picks[b]] >= want[b].max() - TOL * scale, (s, b, picks[b])
+        same += int(np.sum(picks == np.argmax(want, axis=1)))
         for d_ in decs:
             for layer in range(cfg.layers):
                 for j in range(4):
                     d_.set_input(7 + 4 * layer + j, d_.output(2 + 4 * layer + j).tobytes())
         tokens = np.asarray([int(np.argmax(want[b])) for b in range(cfg.batch)], np.int32)
+    print(f"decode greedy picks equal to the oracle's: {same} of {4 * cfg.batch}")
     for x in (pre, dec):
         x.close()

@@ -79,3 +79,28 @@ def test_wire_encoded_dispatch(torch_cuda, backend):
     assert used == len(call.encode())
     want = oracle.unary_lut(oracle.build_table(lut_act.SILU, DTYPE_BF16), x)
     assert np.array_equal(from_dev(dst, np.uint16), want)
+
+
+@pytest.mark.parametrize("n,out_off", [(3_000_001, 0), (20_000_003, 0), (2_100_007, 16),
+                                       (1000003, 0)])
+def test_partial_spans_store_nothing_past_the_output(torch_cuda, backend, n, out_off):
+    """The gather's last span is a partial one: its lanes' stores past the
+    output are dropped by the buffer range (the per-unroll offset sits in the
+    instruction's scalar offset). Every byte before and after the output, over
+    more than one 128 KiB workgroup span, keeps its canary value; the partial
+    span of the grid's second pass (20,000,003 elements) is covered too."""
+    x = u16_patterns(n, seed=n + 1)
+    guard = 256 << 10
+    src = to_dev(torch_cuda, np.concatenate([x, np.zeros(guard // 2, np.uint16)]))
+    dst = torch_cuda.full((out_off + 2 * n + guard,), 0xA5, dtype=torch_cuda.uint8, device="cuda")
+    ws = DeviceWorkspace()
+    ws.bind(0, src)
+    ws.bind(1, dst)
+    backend.dispatch(KernelCall.Gelu(UnaryCall(BufferRef(0, 0, 2 * n), BufferRef(1, out_off, 2 * n),
+                                               n, 16, DTYPE_BF16)), ws)
+    backend.synchronize()
+    raw = from_dev(dst, np.uint8)
+    assert (raw[:out_off] == 0xA5).all()
+    assert (raw[out_off + 2 * n:] == 0xA5).all(), "a store landed past the output"
+    want = oracle.unary_lut(oracle.build_table(lut_act.GELU, DTYPE_BF16), x)
+    assert np.array_equal(raw[out_off:out_off + 2 * n].view(np.uint16), want)

@@ -60,7 +60,7 @@ def test_matmul_bf16_dma64_parity(torch_cuda, backend, m, k, n):
 
 @pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_BF16])
 @pytest.mark.parametrize("m,k,n", [(7, 65, 40), (16, 4096, 4096), (300, 1000, 257), (1024, 1024, 1024),
-                                   (77, 131, 45), (4096, 512, 1000)])
+                                   (77, 131, 45), (4096, 512, 1000), (4096, 4096, 4096)])
 def test_matmul_row_bytes_independent_of_row_index(torch_cuda, backend, m, k, n, dtype):
     """simd.rs:8369 on the device: two rows of A with the same values, one in the
     first tile and one in the last (ragged) tile, give the same output bytes."""
@@ -210,7 +210,8 @@ def run_mm_rows(torch, backend, m, k, n, seed, rows, dtype=DTYPE_BF16):
 
 
 @pytest.mark.parametrize("m,k,n", [(4096, 256, 4096), (4096, 384, 4096), (4096, 320, 4096),
-                                   (8192, 8192, 8192), (2048, 1024, 8192), (4096, 2048, 2048),
+                                   (4096, 4096, 4096), (8192, 8192, 8192), (2048, 1024, 8192),
+                                   (4096, 2048, 2048),
                                    (4096, 8192, 2048), (4096, 2048, 512), (2048, 2048, 2048)])
 def test_matmul_large_tiles_sampled_rows(torch_cuda, backend, m, k, n):
     """The large-tile paths (256x256 tiles from 256 of them up, 256x128 tiles

@@ -334,7 +334,8 @@ def bench_kv(torch, be, args, rep):
         else:
             alg = 2 * (2 * (planes * bucket * D + planes * bucket * 4) + planes * D * 2)
         gbs = alg / (ms / 1e3) / 1e9
-        res[form] = {"us_per_step": ms * 1e3, "dispatches_per_step": 2, "alg_bytes": alg,
+        res[form] = {"us_per_step": ms * 1e3, "dispatches_per_step": 2, "launches_per_step": 2,
+                     "alg_bytes": alg,
                      "hbm_gbs": gbs,
                      "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s",
                                           profiled_traffic(f"kv_{form}_config3"))}

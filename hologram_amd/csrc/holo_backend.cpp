@@ -676,6 +676,16 @@ int do_kv_quant(holo_backend *be, const SlotTable &st, const holo_kv_quant_appen
     if (uint64_t(c.planes) * c.new_rows > 0xffffffffull / 64)
         return fail(HOLO_ERR_UNSUPPORTED_OP, "kv_quant_append: planes * new_rows too large");
     if (!be) return HOLO_OK;
+    if (!in_place && c.planes != 0 &&
+        holo::kv_quant_copy_fusable(cq.base, cs.base, oq.base, os.base, c.planes, c.bucket_rows,
+                                    c.head_dim))
+        return launched(holo::launch_kv_quant_copy_append(
+                            nw.base, c.dtype, reinterpret_cast<const uint32_t *>(pos.base),
+                            reinterpret_cast<const int8_t *>(cq.base),
+                            reinterpret_cast<const float *>(cs.base),
+                            reinterpret_cast<int8_t *>(oq.base), reinterpret_cast<float *>(os.base),
+                            c.planes, c.bucket_rows, c.new_rows, c.head_dim, be->stream),
+                        op);
     if (!in_place) {
         HOLO_TRY(launched(holo::launch_copy_bytes(cq.base, oq.base, qbytes, be->stream), op));
         HOLO_TRY(launched(holo::launch_copy_bytes(cs.base, os.base, sbytes, be->stream), op));

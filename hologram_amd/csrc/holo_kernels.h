@@ -23,6 +23,15 @@ hipError_t launch_fill_zero(void *dst, uint64_t bytes, hipStream_t stream);
 hipError_t launch_kv_place_rows(const uint8_t *nw, const uint32_t *pos, uint8_t *out,
                                 uint32_t planes, uint32_t bucket, uint32_t new_rows,
                                 uint32_t row_bytes, hipStream_t stream);
+// kv.hip — the copy form of the int8 quantize + ring append in one launch:
+// caches copied to the outputs except the appended rows, which are quantized
+// into place (requires kv_quant_copy_fusable).
+bool kv_quant_copy_fusable(const void *cq, const void *cs, const void *oq, const void *os,
+                           uint32_t planes, uint32_t bucket, uint32_t d);
+hipError_t launch_kv_quant_copy_append(const void *nw, uint8_t dtype, const uint32_t *pos,
+                                       const int8_t *cq, const float *cs, int8_t *oq, float *os,
+                                       uint32_t planes, uint32_t bucket, uint32_t new_rows,
+                                       uint32_t d, hipStream_t stream);
 // kv.hip — int8 quantize + ring append into (cache_q, cache_s) in place.
 hipError_t launch_kv_quant_append(const void *nw, uint8_t dtype, const uint32_t *pos,
                                   int8_t *cache_q, float *cache_s, uint32_t planes,

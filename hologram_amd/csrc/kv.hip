@@ -112,17 +112,12 @@ __device__ __forceinline__ int8_t to_q(float r) {
 // correctly rounded IEEE ones and the file is built without contraction, so
 // t = x * inv and t +- 0.5 round exactly as the reference's two steps.
 template <int kMaxPerLane>
-__global__ __launch_bounds__(256) void quant_append_kernel(const void *__restrict__ nw, uint8_t dtype,
-                                                          const uint32_t *__restrict__ posp,
-                                                          int8_t *__restrict__ cq,
-                                                          float *__restrict__ cs, uint32_t planes,
-                                                          uint32_t bucket, uint32_t new_rows,
-                                                          uint32_t d) {
-    const uint32_t wave = (blockIdx.x * 256u + threadIdx.x) >> 6;
-    const uint32_t lane = threadIdx.x & 63u;
-    if (wave >= planes * new_rows) return;
+__device__ __forceinline__ void quant_row_wave(const void *__restrict__ nw, uint8_t dtype,
+                                               uint64_t pos, int8_t *__restrict__ cq,
+                                               float *__restrict__ cs, uint32_t wave,
+                                               uint32_t lane, uint32_t bucket, uint32_t new_rows,
+                                               uint32_t d) {
     const uint32_t p = wave / new_rows, j = wave % new_rows;
-    const uint64_t pos = *posp % bucket;
     const uint64_t row = uint64_t(p) * bucket + (pos + j) % bucket;
     const uint64_t src = (uint64_t(p) * new_rows + j) * d;
 
@@ -162,6 +157,19 @@ __global__ __launch_bounds__(256) void quant_append_kernel(const void *__restric
         }
     }
     if (lane == 0) cs[row] = amax / 127.0f;
+}
+
+template <int kMaxPerLane>
+__global__ __launch_bounds__(256) void quant_append_kernel(const void *__restrict__ nw, uint8_t dtype,
+                                                          const uint32_t *__restrict__ posp,
+                                                          int8_t *__restrict__ cq,
+                                                          float *__restrict__ cs, uint32_t planes,
+                                                          uint32_t bucket, uint32_t new_rows,
+                                                          uint32_t d) {
+    const uint32_t wave = (blockIdx.x * 256u + threadIdx.x) >> 6;
+    if (wave >= planes * new_rows) return;
+    quant_row_wave<kMaxPerLane>(nw, dtype, *posp % bucket, cq, cs, wave, threadIdx.x & 63u, bucket,
+                                new_rows, d);
 }
 
 // The same quantization for 16-bit rows of d = 8 kL elements (64 or 128):
@@ -211,6 +219,90 @@ __global__ __launch_bounds__(256) void quant_append_vec_kernel(const u32x4 *__re
     if (c == 0) cs[row] = amax == 0.0f ? 0.0f : amax / 127.0f;
 }
 
+// Buffer resource over `bytes` bytes (< 2^31) at `base`: loads past the range
+// read 0 and stores past it are dropped, so a skipped store is an offset out
+// of range rather than a branch (a branch around memory operations makes the
+// compiler wait for every load in flight where it joins).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, int(bytes), 0x00020000);
+}
+
+// The copy form of KvQuantAppend in one launch: the int8 planes and the scale
+// planes are copied to the outputs, except the rows being appended, which
+// the first workgroups quantize and place (one wavefront per new row, the
+// arithmetic above). No byte is written twice, so the three parts need no
+// order among themselves. Block roles, in block order:
+//   [0, qblocks)                      quantize + place the new rows
+//   [qblocks, + planes * runs)        int8 plane p, run r: kCopyRun vectors
+//   [.., + scale runs)                the scale planes, flat, 4 rows a vector
+// Requires d % 16 == 0, bucket % 4 == 0, 16-byte aligned caches and planes
+// under 2 GiB, so a 16-byte int8 vector lies in one row, a scale vector in
+// one plane, and a plane is one buffer range. vshift: log2(d / 16) when d / 16
+// is a power of two, else -1 (divide).
+constexpr uint32_t kNoStore = 0x80000000u;   // past every range below
+
+template <int kMaxPerLane>
+__global__ __launch_bounds__(kCopyThreads) void quant_copy_append_kernel(
+    const void *__restrict__ nw, uint8_t dtype, const uint32_t *__restrict__ posp,
+    const u32x4 *__restrict__ cq, const u32x4 *__restrict__ cs, int8_t *__restrict__ oq,
+    float *__restrict__ os, uint32_t planes, uint32_t bucket, uint32_t new_rows, uint32_t d,
+    uint32_t qblocks, uint32_t runs, uint32_t plane_vecs, uint32_t scale_vecs, int vshift) {
+    uint32_t bid = blockIdx.x;
+    if (bid < qblocks) {
+        const uint32_t wave = bid * 4u + (threadIdx.x >> 6);
+        if (wave < planes * new_rows)
+            quant_row_wave<kMaxPerLane>(nw, dtype, *posp % bucket, oq, os, wave, threadIdx.x & 63u,
+                                        bucket, new_rows, d);
+        return;
+    }
+    bid -= qblocks;
+    const uint32_t pos = *posp % bucket;
+    // row r of a plane is being appended when (r - pos) mod bucket < new_rows
+    auto appended = [&](uint32_t r) { return (r >= pos ? r - pos : r + bucket - pos) < new_rows; };
+    if (bid < planes * runs) {
+        const uint32_t p = bid / runs;
+        const uint32_t v0 = (bid % runs) * uint32_t(kCopyRun) + threadIdx.x;
+        const auto rs = rsrc_of(cq + uint64_t(p) * plane_vecs, plane_vecs * 16u);
+        const auto rd = rsrc_of(reinterpret_cast<u32x4 *>(oq) + uint64_t(p) * plane_vecs,
+                                plane_vecs * 16u);
+        u32x4 v[kCopyVec];
+#pragma unroll
+        for (int u = 0; u < kCopyVec; ++u)
+            v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, 16u * (v0 + uint32_t(u) * kCopyThreads),
+                                                         0, 0);
+        const uint32_t vpr = d / 16;
+#pragma unroll
+        for (int u = 0; u < kCopyVec; ++u) {
+            const uint32_t i = v0 + uint32_t(u) * kCopyThreads;
+            const uint32_t row = vshift >= 0 ? i >> vshift : i / vpr;
+            __builtin_amdgcn_raw_buffer_store_b128(v[u], rd, appended(row) ? kNoStore : 16u * i, 0, 2);
+        }
+        return;
+    }
+    bid -= planes * runs;
+    const uint32_t v0 = bid * uint32_t(kCopyRun) + threadIdx.x;
+    const auto rs = rsrc_of(cs, scale_vecs * 16u), rd = rsrc_of(os, scale_vecs * 16u);
+    u32x4 v[kCopyVec];
+#pragma unroll
+    for (int u = 0; u < kCopyVec; ++u)
+        v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, 16u * (v0 + uint32_t(u) * kCopyThreads), 0, 0);
+#pragma unroll
+    for (int u = 0; u < kCopyVec; ++u) {
+        const uint32_t i = v0 + uint32_t(u) * kCopyThreads;
+        const uint32_t r0 = (4u * i) % bucket;          // the vector's rows r0 .. r0 + 3
+        bool a[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a[e] = appended(r0 + uint32_t(e));
+        const bool any = a[0] || a[1] || a[2] || a[3];
+        // whole vector when no row of it is appended, else its other rows one by one
+        __builtin_amdgcn_raw_buffer_store_b128(v[u], rd, any ? kNoStore : 16u * i, 0, 2);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            __builtin_amdgcn_raw_buffer_store_b32(v[u][e], rd,
+                                                  any && !a[e] ? 16u * i + 4u * e : kNoStore, 0, 0);
+    }
+}
+
 }  // namespace
 
 hipError_t launch_copy_bytes(const void *src, void *dst, uint64_t bytes, hipStream_t stream) {
@@ -248,6 +340,44 @@ hipError_t launch_kv_place_rows(const uint8_t *nw, const uint32_t *pos, uint8_t 
     if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
     hipLaunchKernelGGL(place_rows_kernel, dim3(unsigned(blocks)), dim3(kCopyThreads), 0, stream, nw,
                        pos, out, bucket, new_rows, row_bytes);
+    return hipGetLastError();
+}
+
+bool kv_quant_copy_fusable(const void *cq, const void *cs, const void *oq, const void *os,
+                           uint32_t planes, uint32_t bucket, uint32_t d) {
+    const uintptr_t al = reinterpret_cast<uintptr_t>(cq) | reinterpret_cast<uintptr_t>(cs) |
+                         reinterpret_cast<uintptr_t>(oq) | reinterpret_cast<uintptr_t>(os);
+    return (al & 15) == 0 && d % 16 == 0 && d != 0 && d <= 8192 && bucket % 4 == 0 &&
+           uint64_t(bucket) * d < (1ull << 31) && uint64_t(planes) * bucket * 4 < (1ull << 31);
+}
+
+hipError_t launch_kv_quant_copy_append(const void *nw, uint8_t dtype, const uint32_t *pos,
+                                       const int8_t *cq, const float *cs, int8_t *oq, float *os,
+                                       uint32_t planes, uint32_t bucket, uint32_t new_rows,
+                                       uint32_t d, hipStream_t stream) {
+    if (!kv_quant_copy_fusable(cq, cs, oq, os, planes, bucket, d)) return hipErrorInvalidValue;
+    if (planes == 0) return hipSuccess;
+    const uint32_t plane_vecs = bucket * (d / 16);
+    const uint32_t runs = uint32_t((plane_vecs + kCopyRun - 1) / kCopyRun);
+    const uint32_t vpr = d / 16;
+    const int vshift = (vpr & (vpr - 1)) == 0 ? __builtin_ctz(vpr) : -1;
+    const uint32_t scale_vecs = planes * (bucket / 4);
+    const uint64_t qblocks = (uint64_t(planes) * new_rows + 3) / 4;
+    const uint64_t sblocks = (scale_vecs + kCopyRun - 1) / kCopyRun;
+    const uint64_t blocks = qblocks + uint64_t(planes) * runs + sblocks;
+    if (blocks > 0x7fffffffull || uint64_t(planes) * new_rows > 0xffffffffull / 64)
+        return hipErrorInvalidValue;
+    const auto *q4 = reinterpret_cast<const u32x4 *>(cq);
+    const auto *s4 = reinterpret_cast<const u32x4 *>(cs);
+#define HOLO_QCA(K)                                                                              \
+    hipLaunchKernelGGL(quant_copy_append_kernel<K>, dim3(unsigned(blocks)), dim3(kCopyThreads), 0, \
+                       stream, nw, dtype, pos, q4, s4, oq, os, planes, bucket, new_rows, d,       \
+                       uint32_t(qblocks), runs, plane_vecs, scale_vecs, vshift)
+    if (d <= 128) HOLO_QCA(2);
+    else if (d <= 512) HOLO_QCA(8);
+    else if (d <= 2048) HOLO_QCA(32);
+    else HOLO_QCA(128);
+#undef HOLO_QCA
     return hipGetLastError();
 }
 

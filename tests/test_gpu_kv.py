@@ -68,9 +68,14 @@ def test_config3_shape(torch_cuda, backend, pos, in_place):
 
 @pytest.mark.parametrize("dtype", [DTYPE_BF16, DTYPE_F16, DTYPE_F32])
 @pytest.mark.parametrize("d", [64, 128, 96, 300])
-def test_dtypes_dims_and_wrap(torch_cuda, backend, dtype, d):
-    planes, bucket, new_rows, pos = 6, 10, 4, 8   # rows 8, 9, 0, 1: wraps the ring
-    rng = np.random.default_rng(d + dtype)
+@pytest.mark.parametrize("bucket", [10, 12])
+def test_dtypes_dims_and_wrap(torch_cuda, backend, dtype, d, bucket):
+    """Rows bucket-2, bucket-1, 0, 1: the append wraps the ring. A bucket of 12
+    with d a multiple of 16 takes the one-launch copy form (copy everything but
+    the appended rows, whose 16-byte scale vectors are shared with copied
+    rows); a bucket of 10 or d = 300 the copy-then-append launches."""
+    planes, new_rows, pos = 6, 4, bucket - 2
+    rng = np.random.default_rng(d + dtype + bucket)
     cq = rng.integers(-127, 128, size=planes * bucket * d, dtype=np.int8)
     cs = rng.random(planes * bucket, dtype=np.float32)
     new = kv_rows(rng, planes, new_rows, d, dtype)
@@ -107,6 +112,23 @@ def test_special_rows(torch_cuda, backend, dtype, d):
     gq, gs = run_append(torch_cuda, backend, rows, dtype, 2, cq, cs, planes, bucket, 1, d,
                         False)
     wq, ws_ = oracle.kv_quant_append(rows, dtype, 2, cq, cs, planes, bucket, 1, d)
+    assert np.array_equal(gq, wq)
+    assert np.array_equal(gs.view(np.uint32), ws_.view(np.uint32))
+
+
+@pytest.mark.parametrize("new_rows,pos", [(0, 3), (16, 5), (16, 0), (7, 13)])
+def test_copy_form_all_or_no_rows_appended(torch_cuda, backend, new_rows, pos):
+    """The one-launch copy form at its edges: no new row (a pure copy of both
+    planes), every row of the bucket replaced (nothing copied), and a wrapping
+    run that ends on a 16-byte scale vector boundary."""
+    planes, bucket, d = 33, 16, 128
+    rng = np.random.default_rng(new_rows * 100 + pos)
+    cq = rng.integers(-127, 128, size=planes * bucket * d, dtype=np.int8)
+    cs = rng.random(planes * bucket, dtype=np.float32)
+    new = kv_rows(rng, planes, new_rows, d, DTYPE_BF16) if new_rows else np.zeros(8, np.uint16)
+    gq, gs = run_append(torch_cuda, backend, new, DTYPE_BF16, pos, cq, cs, planes, bucket,
+                        new_rows, d, False)
+    wq, ws_ = oracle.kv_quant_append(new, DTYPE_BF16, pos, cq, cs, planes, bucket, new_rows, d)
     assert np.array_equal(gq, wq)
     assert np.array_equal(gs.view(np.uint32), ws_.view(np.uint32))
 

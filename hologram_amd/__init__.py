@@ -17,7 +17,7 @@ from .kernel_call import (DTYPE_BF16, DTYPE_E8CB, DTYPE_F16, DTYPE_F32, DTYPE_I4
                           DecodeAttentionI8Call, DecodeAttentionValidCall, DequantActivationCall,
                           DequantizeCall, GatherCall, KernelCall, KvCacheWriteCall, KvQuantAppendCall,
                           MatMulActivationCall, MatMulAddActivationCall, MatMulAddCall,
-                          MatMulCall, MatMulDequantCall, NormCall, RoPECall, TransposeCall,
+                          MatMulCall, MatMulDequantCall, NormCall, RoPECall, TransposeCall, LayoutCall,
                           UnaryCall, encode_calls, fused_activation, lut_act, mm_act_quant,
                           weight_layout)
 from .archive import ConstantEntry, HoloWriter, PortDescriptor, blake3
@@ -31,7 +31,7 @@ __all__ = [
     "BinaryCall", "BufferRef", "DecodeAttentionCall", "DecodeAttentionI8Call",
     "DecodeAttentionValidCall", "DequantActivationCall", "DequantizeCall", "GatherCall", "KernelCall", "KvCacheWriteCall",
     "KvQuantAppendCall", "MatMulActivationCall", "MatMulAddActivationCall", "MatMulAddCall",
-    "MatMulCall", "MatMulDequantCall", "NormCall", "RoPECall", "TransposeCall", "UnaryCall",
+    "MatMulCall", "MatMulDequantCall", "NormCall", "RoPECall", "TransposeCall", "LayoutCall", "UnaryCall",
     "encode_calls", "fused_activation", "lut_act", "mm_act_quant", "weight_layout",
     "ConstantEntry", "HoloWriter", "PortDescriptor", "blake3", "HipSession",
 ]

@@ -132,6 +132,11 @@ class TransposeCallC(ctypes.Structure):
                 ("dtype", ctypes.c_uint8)]
 
 
+class LayoutCallC(ctypes.Structure):
+    _fields_ = [("input", BufferRefC), ("output", BufferRefC), ("element_count", ctypes.c_uint64),
+                ("dtype", ctypes.c_uint8)]
+
+
 class DequantizeCallC(ctypes.Structure):
     _fields_ = [("input", BufferRefC), ("scales", BufferRefC), ("zero_points", BufferRefC),
                 ("output", BufferRefC), ("element_count", ctypes.c_uint64),
@@ -169,7 +174,8 @@ class CallUnion(ctypes.Union):
                 ("attn_mask", DecodeAttentionCallC),
                 ("dequantize", DequantizeCallC), ("matmul_dequant", MatMulDequantCallC),
                 ("dequant_act", DequantActivationCallC), ("attn_i8", DecodeAttentionI8CallC),
-                ("attn_i8_rows", AttentionI8RowsCallC), ("transpose", TransposeCallC)]
+                ("attn_i8_rows", AttentionI8RowsCallC), ("transpose", TransposeCallC),
+                ("layout", LayoutCallC)]
 
 
 class KernelCallC(ctypes.Structure):
@@ -230,6 +236,11 @@ SIGNATURES = {
     "holo_hip_address_bytes": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_uint64, ctypes.c_char_p]),
     "holo_hip_derive_label": (ctypes.c_int, [ctypes.c_uint16, ctypes.c_char_p, ctypes.c_uint64,
                                              ctypes.c_char_p, ctypes.c_uint64, ctypes.c_char_p]),
+    "holo_hip_derive_label_boundary": (ctypes.c_int, [ctypes.c_uint16, ctypes.c_char_p,
+                                                      ctypes.c_uint64, ctypes.c_char_p,
+                                                      ctypes.c_uint64, ctypes.c_char_p]),
+    "holo_hip_session_last_walk": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_uint32),
+                                                  ctypes.POINTER(ctypes.c_uint32)]),
     "holo_hip_op_signature": (ctypes.c_int, [ctypes.POINTER(KernelCallC),
                                              ctypes.POINTER(ctypes.c_uint16), ctypes.c_char_p,
                                              ctypes.POINTER(ctypes.c_uint32)]),

@@ -1350,6 +1350,32 @@ int do_transpose(holo_backend *be, const SlotTable &st, const holo_transpose_cal
                     op);
 }
 
+// ---------------------------------------------------- Reshape / Slice ----
+// layout_float (src/cpu/float_kernels.rs:2939-2954) for f16/bf16/f32: the
+// first element_count elements; layout_copy (src/cpu/kernels.rs:688-701) for
+// every other dtype: the first element_count bytes (the byte domain). f64 is
+// refused as try_dispatch_float refuses it (kernels.rs:1611-1615). A session
+// runs this only for a Reshape or Slice that writes an output port; an
+// interior one is bound as a view of its input.
+int do_layout(holo_backend *be, const SlotTable &st, uint32_t tag, const holo_layout_call &c) {
+    const char *op = tag == HOLO_OP_RESHAPE ? "reshape" : "slice";
+    if (c.dtype == HOLO_DTYPE_F64)
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    "f64 is not a supported compute dtype (hologram computes in f16/bf16/f32)");
+    const bool flt = c.dtype == HOLO_DTYPE_F16 || c.dtype == HOLO_DTYPE_BF16 ||
+                     c.dtype == HOLO_DTYPE_F32;
+    const uint64_t es = flt ? dtype_size(c.dtype) : 1;
+    if (c.element_count > UINT64_MAX / es)
+        return fail(HOLO_ERR_SLOT_OUT_OF_RANGE, std::string(op) + ": element_count overflows");
+    const uint64_t bytes = c.element_count * es;
+    View in, out;
+    HOLO_TRY(split_borrow(st, &c.input, &in, 1, c.output, &out, op));
+    HOLO_TRY(need(in, bytes, c.input.slot, op, "input"));
+    HOLO_TRY(need(out, bytes, c.output.slot, op, "output"));
+    if (!be || bytes == 0) return HOLO_OK;
+    return launched(holo::launch_copy_bytes(in.base, out.base, bytes, be->stream), op);
+}
+
 // ------------------------------------------------------------ ArgMax -----
 int do_argmax(holo_backend *be, const SlotTable &st, const holo_argmax_call &c) {
     const char *op = "argmax";
@@ -1410,6 +1436,8 @@ int dispatch_impl(holo_backend *be, const SlotTable &st, const holo_kernel_call 
         case HOLO_OP_ATTN_I8_ROWS:
             return do_attn_i8(be, st, call->u.attn_i8_rows.attn, call->u.attn_i8_rows.q_rows);
         case HOLO_OP_TRANSPOSE: return do_transpose(be, st, call->u.transpose);
+        case HOLO_OP_RESHAPE:
+        case HOLO_OP_SLICE: return do_layout(be, st, call->tag, call->u.layout);
         default:
             return fail(HOLO_ERR_UNSUPPORTED_OP,
                         "dispatch: kernel call tag " + std::to_string(call->tag) +
@@ -1714,6 +1742,15 @@ int decode_impl(const uint8_t *wire, size_t len, holo_kernel_call *out, size_t *
             c.scale_bits = r.get<uint32_t>();
             c.dtype = r.get<uint8_t>();
             if (out->tag == HOLO_OP_ATTN_I8_ROWS) out->u.attn_i8_rows.q_rows = r.get<uint32_t>();
+            break;
+        }
+        case HOLO_OP_RESHAPE:
+        case HOLO_OP_SLICE: {  // put_layout :681-686
+            auto &c = out->u.layout;
+            c.input = r.buf();
+            c.output = r.buf();
+            c.element_count = r.get<uint64_t>();
+            c.dtype = r.get<uint8_t>();
             break;
         }
         case HOLO_OP_TRANSPOSE: {  // put_transpose :687-697

@@ -80,6 +80,11 @@ std::string address_bytes(const void *bytes, size_t len);
 std::string derive_label(uint16_t opcode, const uint8_t *params, size_t n_params,
                          const std::vector<std::string> &inputs);
 bool op_signature(const holo_kernel_call &c, uint16_t *opcode, uint8_t params[64], uint32_t *len);
+// derive_label_boundary (address.rs:197-221): the op's label (address_bytes of
+// opcode and params) composed in order with each operand label; false when a
+// label is not of the blake3 form
+bool derive_label_boundary(uint16_t opcode, const uint8_t *params, size_t n_params,
+                           const std::vector<std::string> &inputs, std::string *out);
 bool label_operands(const holo_kernel_call &c, std::vector<uint32_t> *ins,
                     std::vector<uint32_t> *outs, bool *commutative);
 

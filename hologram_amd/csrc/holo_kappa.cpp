@@ -90,6 +90,47 @@ std::string derive_label(uint16_t opcode, const uint8_t *params, size_t n_params
     return address_bytes(msg.data(), msg.size());
 }
 
+// The 32-byte digest a "blake3:<64 hex>" label names (compose.rs:108-128);
+// false for any other form.
+bool digest_of_label(const std::string &l, uint8_t d[32]) {
+    if (l.size() != 71 || l.compare(0, 7, "blake3:") != 0) return false;
+    auto nib = [](char c) -> int {
+        if (c >= '0' && c <= '9') return c - '0';
+        if (c >= 'a' && c <= 'f') return c - 'a' + 10;
+        if (c >= 'A' && c <= 'F') return c - 'A' + 10;
+        return -1;
+    };
+    for (int i = 0; i < 32; ++i) {
+        const int hi = nib(l[7 + 2 * i]), lo = nib(l[8 + 2 * i]);
+        if (hi < 0 || lo < 0) return false;
+        d[i] = uint8_t(hi << 4 | lo);
+    }
+    return true;
+}
+
+// compose_ordered_blake3_address (compose.rs:154-164): address_bytes of the
+// two digests, left then right.
+bool compose_ordered(const std::string &left, const std::string &right, std::string *out) {
+    uint8_t canon[64];
+    if (!digest_of_label(left, canon) || !digest_of_label(right, canon + 32)) return false;
+    *out = address_bytes(canon, 64);
+    return true;
+}
+
+bool derive_label_boundary(uint16_t opcode, const uint8_t *params, size_t n_params,
+                           const std::vector<std::string> &inputs, std::string *out) {
+    std::vector<uint8_t> pre(2 + n_params);
+    memcpy(pre.data(), &opcode, 2);
+    if (n_params) memcpy(pre.data() + 2, params, n_params);
+    const std::string op_label = address_bytes(pre.data(), pre.size());
+    std::string acc = op_label;
+    for (const auto &in : inputs)
+        if (!compose_ordered(acc, in, &acc)) return false;
+    if (inputs.empty()) return compose_ordered(op_label, op_label, out);
+    *out = acc;
+    return true;
+}
+
 bool op_signature(const holo_kernel_call &c, uint16_t *opcode, uint8_t params[64], uint32_t *len) {
     Sig s;
     uint16_t op = 0;
@@ -115,6 +156,8 @@ bool op_signature(const holo_kernel_call &c, uint16_t *opcode, uint8_t params[64
             op = 60;
             break;
         }
+        case HOLO_OP_RESHAPE: s.u64(c.u.layout.element_count).u8(c.u.layout.dtype), op = 59; break;
+        case HOLO_OP_SLICE: s.u64(c.u.layout.element_count).u8(c.u.layout.dtype), op = 62; break;
         case HOLO_OP_ROTARY: {
             const auto &r = c.u.rope;
             s.u64(r.element_count).u32(r.head_dim).u8(r.dtype);
@@ -232,6 +275,7 @@ bool label_operands(const holo_kernel_call &c, std::vector<uint32_t> *ins,
         case HOLO_OP_RMS_NORM: case HOLO_OP_ADD_RMS_NORM:   // the residual is not an operand here
             r(c.u.norm.x), r(c.u.norm.gamma), r(c.u.norm.beta), w(c.u.norm.output); break;
         case HOLO_OP_TRANSPOSE: r(c.u.transpose.input), w(c.u.transpose.output); break;
+        case HOLO_OP_RESHAPE: case HOLO_OP_SLICE: r(c.u.layout.input), w(c.u.layout.output); break;
         case HOLO_OP_ROTARY:
             r(c.u.rope.x), r(c.u.rope.cos), r(c.u.rope.sin), w(c.u.rope.output); break;
         case HOLO_OP_GATHER:
@@ -301,6 +345,21 @@ int holo_hip_derive_label(uint16_t opcode, const uint8_t *params, uint64_t n_par
     for (uint64_t i = 0; i < n_labels; ++i)
         in.emplace_back(labels + i * HOLO_LABEL_LEN, HOLO_LABEL_LEN);
     const std::string l = holo::derive_label(opcode, params, size_t(n_params), in);
+    memcpy(out, l.c_str(), l.size() + 1);
+    return HOLO_OK;
+}
+
+int holo_hip_derive_label_boundary(uint16_t opcode, const uint8_t *params, uint64_t n_params,
+                                   const char *labels, uint64_t n_labels, char out[72]) {
+    if ((!params && n_params) || (!labels && n_labels) || !out)
+        return holo::set_error(HOLO_ERR_INIT, "derive_label_boundary: null argument");
+    std::vector<std::string> in;
+    for (uint64_t i = 0; i < n_labels; ++i)
+        in.emplace_back(labels + i * HOLO_LABEL_LEN, HOLO_LABEL_LEN);
+    std::string l;
+    if (!holo::derive_label_boundary(opcode, params, size_t(n_params), in, &l))
+        return holo::set_error(HOLO_ERR_DISPATCH,
+                               "derive_label_boundary: an operand label is not a blake3 label");
     memcpy(out, l.c_str(), l.size() + 1);
     return HOLO_OK;
 }

@@ -173,6 +173,8 @@ void call_operands(const holo_kernel_call &c, std::vector<holo_buffer_ref> *read
         }
         case HOLO_OP_TRANSPOSE:
             r(c.u.transpose.input); w(c.u.transpose.output); break;
+        case HOLO_OP_RESHAPE: case HOLO_OP_SLICE:
+            r(c.u.layout.input); w(c.u.layout.output); break;
         case HOLO_OP_DECODE_ATTN_VALID: {
             const auto &a = c.u.attn_valid;
             r(a.q); r(a.k_past); r(a.v_past); r(a.k_new); r(a.v_new); r(a.valid_len);
@@ -542,6 +544,22 @@ struct holo_session {
     std::vector<SlotRange> slots;                 // current bindings
     std::vector<SlotRange> owned;                 // the session's own buffer per slot
     std::vector<std::pair<uint32_t, uint32_t>> aliases;   // (output slot, cache slot) moves
+    // slots bound to (a sub-range of) another slot's memory instead of being
+    // computed: interior Reshape / Slice (session.rs:1106-1150) and duplicates
+    // of an earlier call's value (resident reuse, :1121-1131); applied after
+    // the moves, in walk order
+    struct ViewAlias {
+        uint32_t out, in;
+        uint64_t off, len;   // len 0: to the end of the source
+    };
+    std::vector<ViewAlias> views;
+    uint32_t n_elided = 0;                        // calls bound instead of dispatched
+    // per walk step: the root slots it reads and writes (through moves and
+    // views), and whether it runs on every walk (in-place moves, output ports)
+    std::vector<std::vector<uint32_t>> node_rd, node_wr;
+    std::vector<uint8_t> node_always;
+    std::vector<uint32_t> root;
+    uint32_t last_dispatched = 0, last_skipped = 0;
     void *const_arena = nullptr, *work_arena = nullptr;
     uint8_t fingerprint[32] = {};
     hipGraphExec_t graph = nullptr;
@@ -1077,6 +1095,202 @@ int norm_fusion(holo_session *s, const std::vector<uint8_t> &is_output,
     return HOLO_OK;
 }
 
+// Every slot's label walked through the plan as compute_and_label derives it
+// (session.rs:1052-1289): constants by content, input ports by `in`, each
+// call by derive_label over its op signature and operand labels (Add and Mul
+// sort theirs), a Reshape by its input's label; a call whose operand has no
+// label leaves its outputs unlabelled. A call with two outputs (the int8
+// append's cache and scales) labels output j with its params followed by the
+// byte j. With `boundary`, a call writing an output port also gives that port
+// the boundary form (derive_label_boundary), which later calls do not see.
+int label_walk(const holo_session *s, const std::vector<std::string> &in, bool boundary,
+               std::vector<std::string> *lab_out, std::vector<std::string> *witnessed) {
+    std::vector<std::string> &lab = *lab_out;
+    lab.assign(s->slot_bytes.size(), std::string());
+    for (const auto &cd : s->const_digests)
+        if (cd.first < lab.size()) lab[cd.first] = holo::kappa_of_digest(cd.second.data());
+    for (size_t i = 0; i < s->inputs.size(); ++i)
+        if (s->inputs[i].slot < lab.size()) lab[s->inputs[i].slot] = in[i];
+    std::vector<uint8_t> is_out(lab.size(), 0);
+    for (const auto &p : s->outputs)
+        if (p.slot < is_out.size()) is_out[p.slot] = 1;
+    if (witnessed) witnessed->assign(lab.size(), std::string());
+    std::vector<uint32_t> ins, outs;
+    std::vector<std::string> il;
+    for (const auto &level : s->label_plan)
+        for (uint32_t ci : level) {
+            const holo_kernel_call &c = s->label_calls[ci];
+            bool comm = false;
+            uint16_t op = 0;
+            uint8_t params[65];
+            uint32_t np = 0;
+            if (!holo::label_operands(c, &ins, &outs, &comm) || !holo::op_signature(c, &op, params, &np))
+                return set_error(HOLO_ERR_UNSUPPORTED_OP,
+                                 "session_output_labels: kernel call " + std::to_string(ci) + " has no signature");
+            bool ok = true;
+            il.clear();
+            for (uint32_t sl : ins) {
+                if (sl >= lab.size() || lab[sl].empty()) {
+                    ok = false;
+                    break;
+                }
+                il.push_back(lab[sl]);
+            }
+            if (comm) std::sort(il.begin(), il.end());
+            for (size_t j = 0; j < outs.size(); ++j) {
+                if (outs[j] >= lab.size()) continue;
+                if (!ok) {
+                    lab[outs[j]].clear();
+                    if (witnessed) (*witnessed)[outs[j]].clear();
+                    continue;
+                }
+                uint32_t n = np;
+                if (outs.size() > 1) params[n++] = uint8_t(j);
+                if (boundary && witnessed && is_out[outs[j]]) {
+                    std::string w;
+                    if (!holo::derive_label_boundary(op, params, n, il, &w))
+                        return set_error(HOLO_ERR_DISPATCH, "session_output_labels: an operand label "
+                                                            "is not a blake3 label");
+                    (*witnessed)[outs[j]] = w;
+                }
+                // Reshape re-addresses: its value's label is its input's
+                lab[outs[j]] = c.tag == HOLO_OP_RESHAPE && !il.empty()
+                                   ? il[0] : holo::derive_label(op, params, n, il);
+            }
+        }
+    return HOLO_OK;
+}
+
+// ------------------------------------------------------- bound, not run --
+// After fusion, two kinds of walk step are bound instead of dispatched, as
+// compute_and_label binds them (session.rs:1106-1150):
+//  - an interior Reshape (its value's label is its input's, resident) or
+//    Slice (a view of the field its input operand names): the output slot is
+//    bound to the input's memory, nothing moves;
+//  - a step whose value some earlier step of the same walk already holds
+//    (equal κ-label, derived here with a token per input port so that the
+//    equality holds for every input): its output slot is bound to that
+//    step's memory (the resident reuse of :1121-1131).
+// A step writing an output port always runs (the reference dispatches it to
+// mint the port's boundary label), as does any step that touches a KV cache
+// (the in-place move mutates memory a binding would share). Then each kept
+// step's root slots (through moves and bindings), which memo-on reuse tracks.
+void elide_steps(holo_session *s, const std::vector<uint8_t> &is_output,
+                 const std::vector<uint8_t> &is_input, const std::vector<uint8_t> &is_const) {
+    const size_t nslots = is_output.size();
+    std::vector<std::string> tok, sym;
+    for (size_t i = 0; i < s->inputs.size(); ++i) tok.push_back("input port " + std::to_string(i));
+    if (label_walk(s, tok, false, &sym, nullptr) != HOLO_OK) sym.assign(nslots, std::string());
+    sym.resize(nslots);
+    auto &nodes = s->nodes;
+    const size_t nn = nodes.size();
+    std::vector<std::vector<uint32_t>> R(nn), W(nn);
+    for (size_t i = 0; i < nn; ++i) node_slots(s, nodes[i], &R[i], &W[i]);
+    std::vector<uint32_t> writers(nslots, 0);
+    std::vector<size_t> last_writer(nslots, 0);
+    for (size_t i = 0; i < nn; ++i)
+        for (uint32_t w : W[i])
+            if (w < nslots) writers[w]++, last_writer[w] = i;
+    std::vector<uint8_t> kv(nslots, 0);   // a KV op's cache operand, or a moved slot
+    auto mark = [&](const holo_buffer_ref &b) {
+        if (b.slot < nslots) kv[b.slot] = 1;
+    };
+    for (const auto &c : s->calls) {
+        if (c.tag == HOLO_OP_KV_CACHE_WRITE) mark(c.u.kv_write.cache), mark(c.u.kv_write.output);
+        if (c.tag == HOLO_OP_KV_QUANT_APPEND) {
+            const auto &k = c.u.kv_quant_append;
+            mark(k.cache), mark(k.cache_scales), mark(k.output), mark(k.output_scales);
+        }
+    }
+    for (const auto &a : s->aliases) {
+        if (a.first < nslots) kv[a.first] = 1;
+        if (a.second < nslots) kv[a.second] = 1;
+    }
+    auto is_kv_op = [](uint32_t tag) {
+        return tag == HOLO_OP_KV_CACHE_WRITE || tag == HOLO_OP_KV_QUANT_APPEND;
+    };
+    // a slot only this step writes, that no port, constant or KV op touches
+    auto plain = [&](uint32_t sl) {
+        return sl < nslots && !is_output[sl] && !is_input[sl] && !is_const[sl] && writers[sl] == 1 &&
+               !kv[sl];
+    };
+    // the slot holds its final value before step i (nothing at or after i writes it)
+    auto settled = [&](uint32_t sl, size_t i) {
+        return sl < nslots && (writers[sl] == 0 || last_writer[sl] < i);
+    };
+    auto bound = [&](uint32_t sl) { return sl < nslots && (is_input[sl] || is_const[sl] || writers[sl] > 0); };
+    std::vector<uint8_t> is_view(nslots, 0), drop(nn, 0);
+    std::map<std::string, uint32_t> held;   // label -> the slot holding that value
+    for (size_t i = 0; i < nn; ++i) {
+        const Node &nd = nodes[i];
+        if (nd.group < 0) {
+            const holo_kernel_call &c = s->calls[nd.call];
+            if (c.tag == HOLO_OP_RESHAPE || c.tag == HOLO_OP_SLICE) {
+                const holo_layout_call &l = c.u.layout;
+                const uint32_t o = l.output.slot, in = l.input.slot;
+                const bool reshape = c.tag == HOLO_OP_RESHAPE;
+                // a Reshape binds its input's resident value (not a view's)
+                const bool ok = plain(o) && !kv[in] && settled(in, i) && bound(in) &&
+                                (!reshape || !is_view[in]);
+                if (ok) {
+                    if (reshape) {
+                        s->views.push_back({o, in, 0, 0});
+                    } else {
+                        s->views.push_back({o, in, l.input.offset, l.input.length});
+                        is_view[o] = 1;
+                    }
+                    drop[i] = 1;
+                    if (reshape && !sym[o].empty()) held.emplace(sym[o], o);
+                    continue;
+                }
+            } else if (!is_kv_op(c.tag) && W[i].size() == 1 && plain(W[i][0]) && !sym[W[i][0]].empty()) {
+                const auto it = held.find(sym[W[i][0]]);
+                if (it != held.end() && it->second != W[i][0]) {
+                    s->views.push_back({W[i][0], it->second, 0, 0});
+                    drop[i] = 1;
+                    continue;
+                }
+            }
+        }
+        for (uint32_t w : W[i])
+            if (plain(w) && !sym[w].empty()) held.emplace(sym[w], w);
+    }
+    std::vector<Node> kept;
+    std::vector<std::vector<uint32_t>> kr, kw;
+    for (size_t i = 0; i < nn; ++i) {
+        if (drop[i]) {
+            s->n_elided++;
+            continue;
+        }
+        kept.push_back(nodes[i]);
+        kr.push_back(std::move(R[i]));
+        kw.push_back(std::move(W[i]));
+    }
+    nodes = std::move(kept);
+    // root slots: a moved output is its cache, a bound slot its source
+    s->root.resize(nslots);
+    for (size_t i = 0; i < nslots; ++i) s->root[i] = uint32_t(i);
+    auto find = [&](uint32_t x) {
+        while (x < nslots && s->root[x] != x) x = s->root[x];
+        return x;
+    };
+    for (const auto &a : s->aliases)
+        if (a.first < nslots && a.second < nslots) s->root[a.first] = find(a.second);
+    for (const auto &v : s->views) s->root[v.out] = find(v.in);
+    s->node_rd.assign(nodes.size(), {});
+    s->node_wr.assign(nodes.size(), {});
+    s->node_always.assign(nodes.size(), 0);
+    for (size_t i = 0; i < nodes.size(); ++i) {
+        for (uint32_t r : kr[i])
+            if (r < nslots) s->node_rd[i].push_back(find(r));
+        for (uint32_t w : kw[i]) {
+            if (w >= nslots) continue;
+            s->node_wr[i].push_back(find(w));
+            if (is_output[w] || kv[w]) s->node_always[i] = 1;
+        }
+    }
+}
+
 void release(holo_session *s) {
     if (!s) return;
     if (s->stream) (void)hipStreamSynchronize(s->stream);
@@ -1440,19 +1654,41 @@ plan_moves:
             if (rc != HOLO_OK) return rc;
         }
     }
+    elide_steps(s.get(), is_output, is_input, is_const);
     *out = s.release();
     return HOLO_OK;
 }
 
-// One walk: each level's nodes in order on the session stream.
-int walk(holo_session *s) {
+// The slot bindings a walk uses: each moved output is its cache's memory,
+// each bound slot (a view or a reused value) the range of its source.
+void apply_bindings(const holo_session *s, std::vector<SlotRange> &slots) {
+    for (const auto &a : s->aliases) slots[a.first] = slots[a.second];
+    for (const auto &v : s->views) {
+        const SlotRange src = slots[v.in];
+        const uint64_t start = std::min<uint64_t>(v.off, src.bytes);
+        const uint64_t len = v.len == 0 ? src.bytes - start : std::min<uint64_t>(v.len, src.bytes - start);
+        slots[v.out] = SlotRange{src.ptr ? src.ptr + start : nullptr, len};
+    }
+}
+
+// One walk: each level's nodes in order on the session stream; a step whose
+// `skip` entry is set is left out (its outputs already hold its value).
+int walk(holo_session *s, const std::vector<uint8_t> *skip = nullptr) {
     if (!s->be) return set_error(HOLO_ERR_INIT, "session_execute: loaded without a backend (dry load)");
-    for (auto &a : s->aliases) s->slots[a.first] = s->slots[a.second];
+    apply_bindings(s, s->slots);
     const hipStream_t saved = holo::backend_stream(s->be);
     holo::set_backend_stream(s->be, s->stream);
     holo::swap_scratch(s->be, &s->scratch, &s->scratch_bytes);   // the session's scratch in
     int rc = HOLO_OK;
-    for (const Node &nd : s->nodes) {
+    s->last_dispatched = 0;
+    s->last_skipped = s->n_elided;
+    for (size_t i = 0; i < s->nodes.size(); ++i) {
+        const Node &nd = s->nodes[i];
+        if (skip && (*skip)[i]) {
+            s->last_skipped++;
+            continue;
+        }
+        s->last_dispatched++;
         rc = nd.group >= 0 ? holo::dispatch_group(s->be, s->slots, s->groups[size_t(nd.group)])
                            : holo::dispatch_with_slots(s->be, s->slots, &s->calls[nd.call]);
         if (rc != HOLO_OK) {
@@ -1582,57 +1818,23 @@ int holo_hip_session_execute(holo_session *s) {
 
 namespace {
 
-// The output ports' κ-labels for the given input-port labels: every slot's
-// label walked through the plan as compute_and_label derives it
-// (session.rs:1052-1120); a call whose operand has no label leaves its
-// outputs unlabelled. A call with two outputs (the int8 append's cache and
-// scales) labels output j with its params followed by the byte j.
+// The output ports' κ-labels for the given input-port labels: the boundary
+// label a writing call gave the port, else (a port no call writes) the
+// label of the input or constant it holds.
 int derive_outputs(const holo_session *s, const std::vector<std::string> &in,
                    std::vector<std::string> *out) {
-    std::vector<std::string> lab(s->slot_bytes.size());
-    for (const auto &cd : s->const_digests)
-        if (cd.first < lab.size()) lab[cd.first] = holo::kappa_of_digest(cd.second.data());
-    for (size_t i = 0; i < s->inputs.size(); ++i)
-        if (s->inputs[i].slot < lab.size()) lab[s->inputs[i].slot] = in[i];
-    std::vector<uint32_t> ins, outs;
-    std::vector<std::string> il;
-    for (const auto &level : s->label_plan)
-        for (uint32_t ci : level) {
-            const holo_kernel_call &c = s->label_calls[ci];
-            bool comm = false;
-            uint16_t op = 0;
-            uint8_t params[65];
-            uint32_t np = 0;
-            if (!holo::label_operands(c, &ins, &outs, &comm) || !holo::op_signature(c, &op, params, &np))
-                return set_error(HOLO_ERR_UNSUPPORTED_OP,
-                                 "session_output_labels: kernel call " + std::to_string(ci) + " has no signature");
-            bool ok = true;
-            il.clear();
-            for (uint32_t sl : ins) {
-                if (sl >= lab.size() || lab[sl].empty()) {
-                    ok = false;
-                    break;
-                }
-                il.push_back(lab[sl]);
-            }
-            if (comm) std::sort(il.begin(), il.end());
-            for (size_t j = 0; j < outs.size(); ++j) {
-                if (outs[j] >= lab.size()) continue;
-                if (!ok) {
-                    lab[outs[j]].clear();
-                    continue;
-                }
-                uint32_t n = np;
-                if (outs.size() > 1) params[n++] = uint8_t(j);
-                lab[outs[j]] = holo::derive_label(op, params, n, il);
-            }
-        }
+    std::vector<std::string> lab, wit;
+    const int rc = label_walk(s, in, true, &lab, &wit);
+    if (rc != HOLO_OK) return rc;
     out->clear();
     for (const auto &p : s->outputs) {
-        if (p.slot >= lab.size() || lab[p.slot].empty())
+        const std::string *l = p.slot < wit.size() && !wit[p.slot].empty() ? &wit[p.slot]
+                               : p.slot < lab.size() && !lab[p.slot].empty() ? &lab[p.slot]
+                                                                              : nullptr;
+        if (!l)
             return set_error(HOLO_ERR_UNSUPPORTED_OP,
                              "session_output_labels: output '" + p.name + "' is not addressable");
-        out->push_back(lab[p.slot]);
+        out->push_back(*l);
     }
     return HOLO_OK;
 }
@@ -1685,14 +1887,38 @@ int holo_hip_session_execute_bytes(holo_session *s, const void *const *inputs, c
         // hit: the outputs of these inputs are still in the output slots
         if (s->memo_valid && key == s->memo_key) {
             if (memo_hit) *memo_hit = 1;
+            s->last_dispatched = 0;
+            s->last_skipped = uint32_t(s->nodes.size()) + s->n_elided;
             return HOLO_OK;
+        }
+    }
+    // resident reuse across walks (session.rs:1121-1131): a step none of
+    // whose operands changed since the last walk (labels derive from the
+    // inputs' labels, so equal inputs give equal labels) still holds its
+    // value and is skipped; steps on an in-place KV move or an output port
+    // always run
+    std::vector<uint8_t> skip;
+    if (s->memo_enabled && s->memo_valid && s->memo_key.size() == n && !s->root.empty()) {
+        std::vector<uint8_t> dirty(s->root.size(), 0);
+        for (uint32_t i = 0; i < n; ++i)
+            if (key[i] != s->memo_key[i] && s->inputs[i].slot < dirty.size())
+                dirty[s->root[s->inputs[i].slot]] = 1;
+        skip.assign(s->nodes.size(), 0);
+        for (size_t j = 0; j < s->nodes.size(); ++j) {
+            bool d = s->node_always[j] != 0;
+            for (uint32_t r : s->node_rd[j]) d = d || dirty[r];
+            if (d)
+                for (uint32_t w : s->node_wr[j]) dirty[w] = 1;
+            else
+                skip[j] = 1;
         }
     }
     for (uint32_t i = 0; i < n; ++i) {
         const int rc = holo_hip_session_write_input(s, i, inputs[i], sizes[i]);
         if (rc != HOLO_OK) return rc;
     }
-    const int rc = holo_hip_session_execute(s);
+    s->memo_valid = false;
+    const int rc = walk(s, skip.empty() ? nullptr : &skip);
     if (rc != HOLO_OK) return rc;
     s->memo_key = std::move(key);
     s->memo_valid = s->memo_enabled;
@@ -1775,7 +2001,7 @@ int holo_hip_session_replay(holo_session *s) {
     s->memo_valid = false;
     if (!s->graph) return set_error(HOLO_ERR_DISPATCH, "session_replay: no captured walk");
     std::vector<SlotRange> now = s->slots;
-    for (auto &a : s->aliases) now[a.first] = now[a.second];
+    apply_bindings(s, now);
     if (!same_bindings(now, s->graph_slots))
         return set_error(HOLO_ERR_DISPATCH,
                          "session_replay: an input was rebound since the capture; capture again");
@@ -1784,6 +2010,15 @@ int holo_hip_session_replay(holo_session *s) {
                          "session_replay: the session's scratch was reallocated since the capture; capture again");
     if (hipGraphLaunch(s->graph, s->stream) != hipSuccess)
         return set_error(HOLO_ERR_DISPATCH, "session_replay: graph launch failed");
+    s->last_dispatched = uint32_t(s->nodes.size());
+    s->last_skipped = s->n_elided;
+    return HOLO_OK;
+}
+
+int holo_hip_session_last_walk(const holo_session *s, uint32_t *dispatched, uint32_t *skipped) {
+    if (!s) return set_error(HOLO_ERR_INIT, "session_last_walk: null session");
+    if (dispatched) *dispatched = s->last_dispatched;
+    if (skipped) *skipped = s->last_skipped;
     return HOLO_OK;
 }
 

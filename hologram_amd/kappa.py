@@ -4,6 +4,8 @@ by the 64 hex digits of a BLAKE3 digest.
 
   address_bytes(data)                     address.rs:96-99
   derive_label(opcode, params, labels)    address.rs:108-116
+  derive_label_boundary(op, params, labels)  address.rs:197-221 (an output
+                                          port's label)
   op_signature(call)                      KernelCall::op_signature,
                                           kernel_call.rs:1321-1500
 """
@@ -31,6 +33,17 @@ def derive_label(opcode: int, params: bytes, labels: list[str]) -> str:
         raise ValueError("a κ-label is 71 ASCII bytes")
     params = bytes(params)
     _check(_ffi.lib().holo_hip_derive_label(opcode, params, len(params), joined, len(labels), out))
+    return out.value.decode()
+
+
+def derive_label_boundary(opcode: int, params: bytes, labels: list[str]) -> str:
+    out = ctypes.create_string_buffer(LABEL_LEN + 1)
+    joined = "".join(labels).encode()
+    if any(len(lbl) != LABEL_LEN for lbl in labels):
+        raise ValueError("a κ-label is 71 ASCII bytes")
+    params = bytes(params)
+    _check(_ffi.lib().holo_hip_derive_label_boundary(opcode, params, len(params), joined,
+                                                     len(labels), out))
     return out.value.decode()
 
 

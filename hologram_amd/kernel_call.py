@@ -71,6 +71,8 @@ D_DAI8 = 123   # new: decode attention over an int8 cache
 D_ARGMAX = 124  # new: per-row argmax (the greedy pick of a decode step)
 D_AI8R = 125    # new: multi-row (prefill) form of D_DAI8
 D_TRANSPOSE = 61
+D_RESHAPE = 60
+D_SLICE = 63
 
 SLOT_ABSENT = 0xFFFFFFFF
 
@@ -527,7 +529,22 @@ class TransposeCall:
                 + struct.pack("<B", self.dtype))
 
 
-_NAMES = {D_ADD: "Add", D_MUL: "Mul", D_RN: "RmsNorm", D_ADDRMS: "AddRmsNorm", D_ROTARY: "RotaryEmbedding",
+@dataclass(frozen=True)
+class LayoutCall:
+    """kernel_call.rs:479-485 (Reshape, Slice): the first element_count
+    elements of the input view, copied; a session binds an interior one as a
+    view of its input instead (session.rs:1106-1150)."""
+    input: BufferRef
+    output: BufferRef
+    element_count: int
+    dtype: int = DTYPE_BF16
+
+    def wire(self) -> bytes:  # put_layout, kernel_codec.rs:681-686
+        return (self.input.wire() + self.output.wire()
+                + struct.pack("<QB", self.element_count, self.dtype))
+
+
+_NAMES = {D_RESHAPE: "Reshape", D_SLICE: "Slice", D_ADD: "Add", D_MUL: "Mul", D_RN: "RmsNorm", D_ADDRMS: "AddRmsNorm", D_ROTARY: "RotaryEmbedding",
           D_RELU: "Relu", D_ELU: "Elu", D_SELU: "Selu", D_ERF: "Erf", D_DEQ: "Dequantize",
           D_MMDQ: "MatMulDequant", D_DQACT: "DequantActivation",
           D_GATHER: "Gather", D_ARGMAX: "ArgMax", D_SIGMOID: "Sigmoid", D_TANH: "Tanh", D_GELU: "Gelu", D_SILU: "Silu", D_EXP: "Exp",
@@ -663,6 +680,14 @@ class KernelCall:
     def Transpose(cls, c: TransposeCall) -> "KernelCall":  # noqa: N802
         return cls(D_TRANSPOSE, c)
 
+    @classmethod
+    def Reshape(cls, c: LayoutCall) -> "KernelCall":  # noqa: N802
+        return cls(D_RESHAPE, c)
+
+    @classmethod
+    def Slice(cls, c: LayoutCall) -> "KernelCall":  # noqa: N802
+        return cls(D_SLICE, c)
+
     @property
     def name(self) -> str:
         return _NAMES.get(self.tag, f"op{self.tag}")
@@ -722,6 +747,8 @@ class KernelCall:
                 p.input.c(), p.output.c(), rank,
                 (ctypes.c_uint32 * 8)(*(list(p.dims) + [0] * (8 - rank))),
                 (ctypes.c_uint8 * 8)(*(list(p.perm) + [0] * (8 - rank))), p.dtype)
+        elif isinstance(p, LayoutCall):
+            kc.u.layout = _ffi.LayoutCallC(p.input.c(), p.output.c(), p.element_count, p.dtype)
         elif isinstance(p, DecodeAttentionCall):
             kc.u.attn_mask = _ffi.DecodeAttentionCallC(
                 p.q.c(), p.k_past.c(), p.v_past.c(), p.k_new.c(), p.v_new.c(), p.mask.c(),

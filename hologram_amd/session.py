@@ -144,6 +144,17 @@ class HipSession:
         self.synchronize()
         return [self.read_output(i) for i in range(len(self.outputs))]
 
+    @property
+    def last_walk(self) -> tuple[int, int]:
+        """(steps dispatched, steps skipped) of the last walk (session.rs
+        last_dispatched / last_skipped): skipped counts the steps bound at
+        load (interior Reshape / Slice, repeats of a value the walk holds),
+        the steps a memo-on execute found unchanged, and every step of a
+        whole-graph memo hit."""
+        d, k = ctypes.c_uint32(), ctypes.c_uint32()
+        _check(self._lib.holo_hip_session_last_walk(self.handle, ctypes.byref(d), ctypes.byref(k)))
+        return d.value, k.value
+
     def set_memo(self, enabled: bool) -> None:
         """The memo's hits on (default) or off (every execute walks)."""
         _check(self._lib.holo_hip_session_set_memo(self.handle, int(enabled)))

@@ -42,6 +42,7 @@ typedef enum holo_status {
 
 #define HOLO_DTYPE_I32 4u
 #define HOLO_DTYPE_I64 5u
+#define HOLO_DTYPE_F64 9u     /* storage only: no op computes in it (kernels.rs:1611-1615) */
 #define HOLO_DTYPE_U8 1u
 #define HOLO_DTYPE_I4 10u     /* packed signed 4-bit, two per byte, low nibble first */
 #define HOLO_DTYPE_E8CB 11u   /* one u8 codebook index per 8-element group */
@@ -98,6 +99,8 @@ typedef enum holo_status {
 #define HOLO_OP_ARGMAX 124u               /* new: per-row argmax (greedy pick)  */
 #define HOLO_OP_ATTN_I8_ROWS 125u         /* new: multi-row (prefill) form of 123 */
 #define HOLO_OP_TRANSPOSE 61u             /* Transpose (kernel_codec.rs:80)     */
+#define HOLO_OP_RESHAPE 60u               /* Reshape (kernel_codec.rs:79, D_RESHAPE) */
+#define HOLO_OP_SLICE 63u                 /* Slice (kernel_codec.rs:82, D_SLICE)     */
 
 /* BufferRef, crates/hologram-compute/src/workspace.rs:16-24.
  * length == 0 means "to the end of the slot"; slot == HOLO_SLOT_ABSENT marks an
@@ -422,6 +425,22 @@ typedef struct holo_transpose_call {
     uint8_t dtype;
 } holo_transpose_call;
 
+/* LayoutCall, kernel_call.rs:479-485, as Reshape (tag 60) and Slice (tag 63):
+ * the first element_count elements of the input view copied to the output
+ * view — element_count x the element width bytes for f16/bf16/f32
+ * (layout_float, src/cpu/float_kernels.rs:2939-2954), element_count bytes for
+ * the byte-domain dtypes (layout_copy, src/cpu/kernels.rs:688-701); f64 is
+ * refused (kernels.rs:1611-1615). A Slice's input view is the field it
+ * projects. Inside a session an interior Reshape or Slice moves nothing: its
+ * output slot is bound to its input's memory (session.rs:1106-1150); only one
+ * that writes an output port copies. */
+typedef struct holo_layout_call {
+    holo_buffer_ref input;
+    holo_buffer_ref output;
+    uint64_t element_count;
+    uint8_t dtype;
+} holo_layout_call;
+
 /* KernelCall (kernel_call.rs:1146-1276): tag + the variant's payload. */
 typedef struct holo_kernel_call {
     uint32_t tag;
@@ -446,6 +465,7 @@ typedef struct holo_kernel_call {
         holo_decode_attention_i8_call attn_i8;
         holo_attention_i8_rows_call attn_i8_rows;
         holo_transpose_call transpose;
+        holo_layout_call layout;
     } u;
 } holo_kernel_call;
 
@@ -539,8 +559,15 @@ int holo_hip_session_load(holo_backend *be, const uint8_t *archive, size_t len,
 int holo_hip_session_load_ex(holo_backend *be, const uint8_t *archive, size_t len, uint32_t flags,
                              holo_session **out);
 /* Steps of one walk after fusion (each a call or a fused MatMul group), and
- * how many of them are fused groups. */
+ * how many of them are fused groups. Steps bound at load instead of run (an
+ * interior Reshape or Slice, a repeat of a value the walk already holds) are
+ * not counted. */
 int holo_hip_session_nodes(const holo_session *s, uint32_t *n_nodes, uint32_t *n_groups);
+/* The last walk's steps dispatched and skipped (last_dispatched /
+ * last_skipped, session.rs:1291-1310): skipped counts the steps bound at load,
+ * the steps a memo-on holo_hip_session_execute_bytes found unchanged since
+ * the previous walk, and every step on a whole-graph memo hit. */
+int holo_hip_session_last_walk(const holo_session *s, uint32_t *dispatched, uint32_t *skipped);
 /* The index-th kernel call of the loaded schedule, after the reference's
  * loader passes (the calls the reference's Session counts with
  * dequant_fused_count and its siblings, session.rs:1390-1437). */
@@ -548,10 +575,13 @@ int holo_hip_session_call(const holo_session *s, uint32_t index, holo_kernel_cal
 /* The output ports' κ-labels for the given input-port labels (n_inputs x
  * HOLO_LABEL_LEN bytes in, n_outputs x HOLO_LABEL_LEN out), derived through
  * the loaded schedule as the reference's compute_and_label does
- * (session.rs:1052-1120): constants are labelled by their content, each call
+ * (session.rs:1052-1289): constants are labelled by their content, each call
  * by derive_label over its op signature and its operands' labels (buffers()
- * order, kernel_call.rs:1526-1660; Add and Mul sort theirs). Works on a dry
- * load. */
+ * order, kernel_call.rs:1526-1660; Add and Mul sort theirs), a Reshape by its
+ * input's label; the call that writes an output port gives that port the
+ * boundary form, derive_label_boundary (address.rs:197-221), while later
+ * calls derive from its plain label; a port no call writes carries its
+ * input's or constant's label. Works on a dry load. */
 int holo_hip_session_output_labels(const holo_session *s, const char *input_labels, char *out);
 /* Execute from host bytes with the reference's whole-graph memo
  * (session.rs:841-905): each input is labelled by its bytes (a port whose
@@ -603,6 +633,13 @@ int holo_hip_blake3(const void *data, size_t len, uint8_t out32[32]);
  * 64 lowercase hex digits of a BLAKE3 digest, HOLO_LABEL_LEN ASCII bytes
  * (`out` receives them and a terminating NUL). */
 #define HOLO_LABEL_LEN 71
+/* derive_label_boundary (address.rs:197-221): the label an output port
+ * receives from the call that writes it: the op's own label (address_bytes of
+ * opcode u16 LE || params) composed left to right with each operand label,
+ * each composition address_bytes(digest(acc) || digest(operand))
+ * (compose.rs:154-164); with no operand, the op label composed with itself. */
+int holo_hip_derive_label_boundary(uint16_t opcode, const uint8_t *params, uint64_t n_params,
+                                   const char *labels, uint64_t n_labels, char out[72]);
 /* address_bytes (address.rs:96-99): the label of opaque bytes. */
 int holo_hip_address_bytes(const void *bytes, uint64_t len, char out[72]);
 /* derive_label (address.rs:108-116): the label of a computed value, the digest

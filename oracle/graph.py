@@ -100,6 +100,8 @@ def _decode_call(r: _R) -> tuple:
         c["perm"] = [r.u("B") for _ in range(8)][:c["rank"]]
         c["dtype"] = r.u("B")
         return tag, c
+    if tag in (60, 63):                              # put_layout (Reshape, Slice)
+        return tag, dict(input=r.buf(), output=r.buf(), n=r.u("Q"), dtype=r.u("B"))
     if tag == 124:                                   # argmax (new)
         return tag, dict(input=r.buf(), output=r.buf(), rows=r.u("I"), cols=r.u("I"),
                          dtype=r.u("B"))
@@ -379,6 +381,18 @@ class OracleSession:
             x = np.ascontiguousarray(self._view(c["input"], n * es)).view(f"u{es}")
             from . import transpose
             self._out(c["output"], n * es)[:] = transpose(x, c["dims"], c["perm"]).view(np.uint8)
+        elif tag in (60, 63):
+            # layout_float / layout_copy (float_kernels.rs:2939-2954, kernels.rs:688-701):
+            # element_count elements of a float dtype, element_count bytes otherwise;
+            # f64 refused (kernels.rs:1611-1615). The reference walk binds an interior
+            # Reshape / Slice as a view of its input: the same bytes.
+            if c["dtype"] == 9:
+                raise ValueError("f64 is not a supported compute dtype")
+            nb = c["n"] * (DT_BYTES[c["dtype"]] if c["dtype"] in (6, 7, 8) else 1)
+            x = self._view(c["input"])
+            if len(x) < nb:
+                raise ValueError("layout: input shorter than element_count")
+            self._out(c["output"], nb)[:] = x[:nb]
         elif tag == 124:
             es = DT_BYTES[c["dtype"]]
             x = np.ascontiguousarray(self._view(c["input"], c["rows"] * c["cols"] * es))

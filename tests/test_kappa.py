@@ -14,7 +14,7 @@ from conftest import ROOT
 from hologram_amd import (DTYPE_BF16, DTYPE_F32, BinaryCall, BufferRef, ConstantEntry, HipSession,
                           HoloWriter, KernelCall, MatMulCall, PortDescriptor, UnaryCall,
                           UnsupportedOp, fused_activation)
-from hologram_amd.kappa import address_bytes, derive_label, op_signature
+from hologram_amd.kappa import address_bytes, derive_label, derive_label_boundary, op_signature
 from oracle.blake3_ref import blake3 as blake3_spec
 from test_quant import frozen_calls
 
@@ -23,6 +23,20 @@ GOLDEN = ROOT / "tests" / "golden"
 
 def spec_label(data: bytes) -> str:
     return "blake3:" + blake3_spec(data).hex()
+
+
+def spec_boundary(op: int, params: bytes, labels: list) -> str:
+    """derive_label_boundary (address.rs:197-221) stated with the specification's
+    BLAKE3: the op's label composed in order with each operand label, a
+    composition being the label of the two digests end to end
+    (compose_ordered_blake3_address, compose.rs:154-164)."""
+    comp = lambda l, r: spec_label(bytes.fromhex(l[7:]) + bytes.fromhex(r[7:]))
+    acc = spec_label(struct.pack("<H", op) + params)
+    if not labels:
+        return comp(acc, acc)
+    for lbl in labels:
+        acc = comp(acc, lbl)
+    return acc
 
 
 def test_address_bytes_reproduces_the_reference_fixture_label():
@@ -51,6 +65,18 @@ def test_derive_label_is_the_digest_of_opcode_params_and_labels():
     assert derive_label(45, b"\x07", [a, b]) != derive_label(46, b"\x07", [a, b])
     assert derive_label(45, b"\x07", [a, b]) != derive_label(45, b"\x08", [a, b])
     assert derive_label(45, b"", []) == spec_label(struct.pack("<H", 45))
+
+
+def test_derive_label_boundary_composes_the_op_label_with_each_operand():
+    a, b = address_bytes(b"A" * 100), address_bytes(b"B" * 3000)
+    for op, params, labels in ((45, bytes([1, 2, 3]), [a, b]), (13, b"\x07", [a]),
+                               (4, b"", []), (59, struct.pack("<QB", 77, DTYPE_F32), [b])):
+        assert derive_label_boundary(op, params, labels) == spec_boundary(op, params, labels)
+    # ordered, and a different address from the plain derivation of the same call
+    assert derive_label_boundary(45, b"\x07", [a, b]) != derive_label_boundary(45, b"\x07", [b, a])
+    assert derive_label_boundary(45, b"\x07", [a, b]) != derive_label(45, b"\x07", [a, b])
+    with pytest.raises(Exception):       # an operand label of another axis cannot compose
+        derive_label_boundary(45, b"", ["sha256:" + "0" * 64])
 
 
 def test_op_signature_of_the_served_families():
@@ -94,7 +120,8 @@ def test_session_labels_a_commutative_op_by_sorted_operands():
     la, lb = address_bytes(b"a" * 64), address_bytes(b"b" * 64)
     sess = HipSession(None, archive([add(0, 1, 2)], [(0, N, 8), (1, N, 8)], [(2, N, 8)]))
     params = struct.pack("<QHB", N, 32, DTYPE_F32)
-    want = derive_label(4, params, sorted([la, lb]))
+    # the call writing an output port gives it the boundary label (session.rs:1236-1250)
+    want = spec_boundary(4, params, sorted([la, lb]))
     assert sess.output_labels([la, lb]) == [want]
     assert sess.output_labels([lb, la]) == [want]          # a+b and b+a: one label
 
@@ -114,15 +141,15 @@ def test_session_labels_chain_constants_and_fused_calls():
         lx = address_bytes(b"x" * (m * k * 4))
         mm_params = struct.pack("<IIIB", m, k, n, DTYPE_F32)
         # the fused call carries one derivation: MatMulActivation's signature
-        want = derive_label(105, mm_params + bytes([fused_activation.GELU]),
-                            [lx, address_bytes(w)])
+        want = spec_boundary(105, mm_params + bytes([fused_activation.GELU]),
+                             [lx, address_bytes(w)])
         assert sess.output_labels([lx]) == [want]
     # with the fusion off, the two calls derive in sequence
     from hologram_amd.session import NO_EPILOGUE_FUSION
     sess = HipSession(None, archive(calls, [(0, m * k, 8)], [(7, m * n, 8)],
                                     [ConstantEntry(5, DTYPE_F32, w)]), flags=NO_EPILOGUE_FUSION)
     inner = derive_label(45, mm_params, [lx, address_bytes(w)])
-    want = derive_label(13, struct.pack("<QHB", m * n, 32, DTYPE_F32), [inner])
+    want = spec_boundary(13, struct.pack("<QHB", m * n, 32, DTYPE_F32), [inner])
     assert sess.output_labels([lx]) == [want]
 
 

@@ -19,20 +19,34 @@ namespace {
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
 __device__ __forceinline__ uint16_t f2bf(float f) { return uint16_t(__float_as_uint(f) >> 16); }
 
-template <bool kBf16>
-__device__ __forceinline__ float ld(const void *p, uint64_t i) {
-    if constexpr (kBf16)
-        return bf2f(static_cast<const uint16_t *>(p)[i]);
-    else
-        return static_cast<const float *>(p)[i];
+// Element access by dtype tag (f16 6, bf16 7, f32 8): widen exactly; narrow
+// bf16 by truncation and f16 by the reference's rounding (read_float /
+// write_float, src/cpu/dtype.rs:69-153).
+constexpr int kF16 = 6, kBF16 = 7, kF32 = 8;
+
+template <int DT>
+__device__ __forceinline__ float wid(uint32_t h) {
+    return DT == kBF16 ? bf2f(uint16_t(h)) : f16_bits_to_f32(h);
+}
+template <int DT>
+__device__ __forceinline__ uint32_t nar(float v) {
+    return DT == kBF16 ? f2bf(v) : f32_to_f16_bits(v);
 }
 
-template <bool kBf16>
-__device__ __forceinline__ void st(void *p, uint64_t i, float v) {
-    if constexpr (kBf16)
-        static_cast<uint16_t *>(p)[i] = f2bf(v);
+template <int DT>
+__device__ __forceinline__ float ld(const void *p, uint64_t i) {
+    if constexpr (DT == kF32)
+        return static_cast<const float *>(p)[i];
     else
+        return wid<DT>(static_cast<const uint16_t *>(p)[i]);
+}
+
+template <int DT>
+__device__ __forceinline__ void st(void *p, uint64_t i, float v) {
+    if constexpr (DT == kF32)
         static_cast<float *>(p)[i] = v;
+    else
+        static_cast<uint16_t *>(p)[i] = uint16_t(nar<DT>(v));
 }
 
 constexpr int kOpAdd = 0, kOpMul = 1;
@@ -42,14 +56,14 @@ __device__ __forceinline__ float bin(float a, float b) {
     return kOp == kOpAdd ? a + b : a * b;
 }
 
-// Add / Mul: 16-byte vectors (8 bf16 or 4 f32 per lane) when every operand is
-// 16-byte aligned, element tail after; grid-stride.
-template <bool kBf16, int kOp>
+// Add / Mul: 16-byte vectors (8 bf16/f16 or 4 f32 per lane) when every
+// operand is 16-byte aligned, element tail after; grid-stride.
+template <int DT, int kOp>
 __global__ __launch_bounds__(256) void binary_kernel(const void *__restrict__ a,
                                                      const void *__restrict__ b,
                                                      void *__restrict__ out, uint64_t n,
                                                      uint64_t nvec) {
-    constexpr int E = kBf16 ? 8 : 4;
+    constexpr int E = DT == kF32 ? 4 : 8;
     const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
     const u32x4 *a4 = static_cast<const u32x4 *>(a);
     const u32x4 *b4 = static_cast<const u32x4 *>(b);
@@ -57,13 +71,20 @@ __global__ __launch_bounds__(256) void binary_kernel(const void *__restrict__ a,
     for (uint64_t v = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; v < nvec; v += stride) {
         const u32x4 x = a4[v], y = b4[v];
         u32x4 r;
-        if constexpr (kBf16) {
+        if constexpr (DT == kBF16) {
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
                 const float lo = bin<kOp>(__uint_as_float(x[w] << 16), __uint_as_float(y[w] << 16));
                 const float hi = bin<kOp>(__uint_as_float(x[w] & 0xFFFF0000u),
                                           __uint_as_float(y[w] & 0xFFFF0000u));
                 r[w] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+            }
+        } else if constexpr (DT == kF16) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float lo = bin<kOp>(wid<DT>(x[w] & 0xFFFFu), wid<DT>(y[w] & 0xFFFFu));
+                const float hi = bin<kOp>(wid<DT>(x[w] >> 16), wid<DT>(y[w] >> 16));
+                r[w] = nar<DT>(lo) | (nar<DT>(hi) << 16);
             }
         } else {
 #pragma unroll
@@ -73,12 +94,12 @@ __global__ __launch_bounds__(256) void binary_kernel(const void *__restrict__ a,
         o4[v] = r;
     }
     for (uint64_t i = nvec * E + uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
-        st<kBf16>(out, i, bin<kOp>(ld<kBf16>(a, i), ld<kBf16>(b, i)));
+        st<DT>(out, i, bin<kOp>(ld<DT>(a, i), ld<DT>(b, i)));
 }
 
 // RmsNorm: one workgroup per row. Sum of squares in f32 (tree order), then
 // out = (x * inv_rms) * gamma as the reference evaluates it.
-template <bool kBf16>
+template <int DT>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const void *__restrict__ x,
                                                       const void *__restrict__ gamma,
                                                       void *__restrict__ out, uint32_t feature,
@@ -87,7 +108,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const void *__restrict__ x
     const uint64_t row = uint64_t(blockIdx.x) * feature;
     float ss = 0.0f;
     for (uint32_t j = threadIdx.x; j < feature; j += 256) {
-        const float v = ld<kBf16>(x, row + j);
+        const float v = ld<DT>(x, row + j);
         ss = fmaf(v, v, ss);
     }
 #pragma unroll
@@ -97,9 +118,9 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const void *__restrict__ x
     const float sumsq = part[0] + part[1] + part[2] + part[3];
     const float inv = 1.0f / sqrtf(sumsq / float(feature) + eps);
     for (uint32_t j = threadIdx.x; j < feature; j += 256) {
-        float v = ld<kBf16>(x, row + j) * inv;
-        if (gamma) v = v * ld<kBf16>(gamma, j);
-        st<kBf16>(out, row + j, v);
+        float v = ld<DT>(x, row + j) * inv;
+        if (gamma) v = v * ld<DT>(gamma, j);
+        st<DT>(out, row + j, v);
     }
 }
 
@@ -107,7 +128,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const void *__restrict__ x
 // f32 and never narrowed (add_rms_norm_float, float_kernels.rs:1566-1672).
 // The reference's f32 rows with a residual scale in place by (inv * g); every
 // other form writes (v * inv) * g; the sum of squares is in tree order.
-template <bool kBf16>
+template <int DT>
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const void *__restrict__ x,
                                                           const void *__restrict__ res,
                                                           const void *__restrict__ gamma,
@@ -117,8 +138,8 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const void *__restrict
     const uint64_t row = uint64_t(blockIdx.x) * feature;
     float ss = 0.0f;
     for (uint32_t j = threadIdx.x; j < feature; j += 256) {
-        float v = ld<kBf16>(x, row + j);
-        if (res) v = v + ld<kBf16>(res, row + j);
+        float v = ld<DT>(x, row + j);
+        if (res) v = v + ld<DT>(res, row + j);
         ss = fmaf(v, v, ss);
     }
 #pragma unroll
@@ -128,16 +149,16 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const void *__restrict
     const float sumsq = part[0] + part[1] + part[2] + part[3];
     const float inv = 1.0f / sqrtf(sumsq / float(feature) + eps);
     for (uint32_t j = threadIdx.x; j < feature; j += 256) {
-        float v = ld<kBf16>(x, row + j);
-        if (res) v = v + ld<kBf16>(res, row + j);
+        float v = ld<DT>(x, row + j);
+        if (res) v = v + ld<DT>(res, row + j);
         float o;
-        if (!kBf16 && res) {
-            o = gamma ? v * (inv * ld<kBf16>(gamma, j)) : v * inv;
+        if (DT == kF32 && res) {
+            o = gamma ? v * (inv * ld<DT>(gamma, j)) : v * inv;
         } else {
             o = v * inv;
-            if (gamma) o = o * ld<kBf16>(gamma, j);
+            if (gamma) o = o * ld<DT>(gamma, j);
         }
-        st<kBf16>(out, row + j, o);
+        st<DT>(out, row + j, o);
     }
 }
 
@@ -167,7 +188,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bf16_vec_kernel(const uint16_t *_
 }
 
 // Rotary embedding, rotate-half form over heads of head_dim elements.
-template <bool kBf16>
+template <int DT>
 __global__ __launch_bounds__(256) void rope_kernel(const void *__restrict__ x,
                                                    const void *__restrict__ cs,
                                                    const void *__restrict__ sn,
@@ -177,13 +198,13 @@ __global__ __launch_bounds__(256) void rope_kernel(const void *__restrict__ x,
     for (uint64_t e = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; e < n;
          e += uint64_t(gridDim.x) * blockDim.x) {
         const uint32_t pos = uint32_t(e % head_dim);
-        const float xe = ld<kBf16>(x, e), ce = ld<kBf16>(cs, e), se = ld<kBf16>(sn, e);
+        const float xe = ld<DT>(x, e), ce = ld<DT>(cs, e), se = ld<DT>(sn, e);
         float v;
         if (pos < half)
-            v = xe * ce - ld<kBf16>(x, e + half) * se;
+            v = xe * ce - ld<DT>(x, e + half) * se;
         else
-            v = xe * ce + ld<kBf16>(x, e - half) * se;
-        st<kBf16>(out, e, v);
+            v = xe * ce + ld<DT>(x, e - half) * se;
+        st<DT>(out, e, v);
     }
 }
 
@@ -243,10 +264,11 @@ __global__ __launch_bounds__(256) void gather_kernel(const uint8_t *__restrict__
 // ArgMax per row: one workgroup per row; each thread keeps the first index of
 // its largest value, then a (value, index) reduction that prefers the lower
 // index on equal values. NaN never compares greater.
-template <bool kBf16>
+template <int DT>
 __global__ __launch_bounds__(1024) void argmax_kernel(const void *__restrict__ in,
                                                       int32_t *__restrict__ out, uint32_t cols) {
     constexpr int kW = 16;                       // wavefronts
+    constexpr bool kBf16 = DT == kBF16;
     constexpr int E = kBf16 ? 8 : 4;             // elements per 16-byte vector
     __shared__ float sv[kW];
     __shared__ int si[kW];
@@ -281,7 +303,7 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const void *__restrict__ i
         }
         j0 = nv * E;
     }
-    for (uint32_t j = j0 + threadIdx.x; j < cols; j += 1024) take(ld<kBf16>(in, row + j), int(j));
+    for (uint32_t j = j0 + threadIdx.x; j < cols; j += 1024) take(ld<DT>(in, row + j), int(j));
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
         const float ov = __shfl_xor(best, o, 64);
@@ -350,42 +372,56 @@ unsigned grid_for(uint64_t work, unsigned cap = 4096) {
 
 }  // namespace
 
-hipError_t launch_binary(int op, const void *a, const void *b, void *out, uint64_t n, bool bf16,
+hipError_t launch_binary(int op, const void *a, const void *b, void *out, uint64_t n, uint8_t dtype,
                          hipStream_t stream) {
     const bool vec = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
                        reinterpret_cast<uintptr_t>(out)) & 15) == 0;
-    const uint64_t nvec = vec ? n / (bf16 ? 8 : 4) : 0;
+    const uint64_t nvec = vec ? n / (dtype == kF32 ? 4 : 8) : 0;
     const unsigned grid = grid_for(nvec ? nvec : n);
-    if (bf16) {
-        if (op == 0)
-            hipLaunchKernelGGL((binary_kernel<true, kOpAdd>), dim3(grid), dim3(256), 0, stream, a, b, out, n, nvec);
-        else
-            hipLaunchKernelGGL((binary_kernel<true, kOpMul>), dim3(grid), dim3(256), 0, stream, a, b, out, n, nvec);
-    } else {
-        if (op == 0)
-            hipLaunchKernelGGL((binary_kernel<false, kOpAdd>), dim3(grid), dim3(256), 0, stream, a, b, out, n, nvec);
-        else
-            hipLaunchKernelGGL((binary_kernel<false, kOpMul>), dim3(grid), dim3(256), 0, stream, a, b, out, n, nvec);
+#define HOLO_BIN(D)                                                                              \
+    do {                                                                                         \
+        if (op == 0)                                                                             \
+            hipLaunchKernelGGL((binary_kernel<D, kOpAdd>), dim3(grid), dim3(256), 0, stream, a, b, \
+                               out, n, nvec);                                                    \
+        else                                                                                     \
+            hipLaunchKernelGGL((binary_kernel<D, kOpMul>), dim3(grid), dim3(256), 0, stream, a, b, \
+                               out, n, nvec);                                                    \
+    } while (0)
+    switch (dtype) {
+        case kBF16: HOLO_BIN(kBF16); break;
+        case kF16: HOLO_BIN(kF16); break;
+        case kF32: HOLO_BIN(kF32); break;
+        default: return hipErrorInvalidValue;
     }
+#undef HOLO_BIN
     return hipGetLastError();
 }
 
 hipError_t launch_add_rmsnorm(const void *x, const void *residual, const void *gamma, void *out,
-                              uint32_t batch, uint32_t feature, float eps, bool bf16,
+                              uint32_t batch, uint32_t feature, float eps, uint8_t dtype,
                               hipStream_t stream) {
     if (batch == 0 || feature == 0) return hipSuccess;
-    if (bf16)
-        hipLaunchKernelGGL((add_rmsnorm_kernel<true>), dim3(batch), dim3(256), 0, stream, x, residual,
-                           gamma, out, feature, eps);
-    else
-        hipLaunchKernelGGL((add_rmsnorm_kernel<false>), dim3(batch), dim3(256), 0, stream, x, residual,
-                           gamma, out, feature, eps);
+    switch (dtype) {
+        case kBF16:
+            hipLaunchKernelGGL((add_rmsnorm_kernel<kBF16>), dim3(batch), dim3(256), 0, stream, x,
+                               residual, gamma, out, feature, eps);
+            break;
+        case kF16:
+            hipLaunchKernelGGL((add_rmsnorm_kernel<kF16>), dim3(batch), dim3(256), 0, stream, x,
+                               residual, gamma, out, feature, eps);
+            break;
+        case kF32:
+            hipLaunchKernelGGL((add_rmsnorm_kernel<kF32>), dim3(batch), dim3(256), 0, stream, x,
+                               residual, gamma, out, feature, eps);
+            break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
 hipError_t launch_rmsnorm(const void *x, const void *gamma, void *out, uint32_t batch,
-                          uint32_t feature, float eps, bool bf16, hipStream_t stream) {
-    const bool vec = bf16 && feature % 8 == 0 && feature <= 8 * 256 * 4 &&
+                          uint32_t feature, float eps, uint8_t dtype, hipStream_t stream) {
+    const bool vec = dtype == kBF16 && feature % 8 == 0 && feature <= 8 * 256 * 4 &&
                      ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gamma) |
                        reinterpret_cast<uintptr_t>(out)) & 15) == 0;
     if (vec) {
@@ -394,16 +430,27 @@ hipError_t launch_rmsnorm(const void *x, const void *gamma, void *out, uint32_t 
                            static_cast<uint16_t *>(out), feature, eps);
         return hipGetLastError();
     }
-    if (bf16)
-        hipLaunchKernelGGL((rmsnorm_kernel<true>), dim3(batch), dim3(256), 0, stream, x, gamma, out, feature, eps);
-    else
-        hipLaunchKernelGGL((rmsnorm_kernel<false>), dim3(batch), dim3(256), 0, stream, x, gamma, out, feature, eps);
+    switch (dtype) {
+        case kBF16:
+            hipLaunchKernelGGL((rmsnorm_kernel<kBF16>), dim3(batch), dim3(256), 0, stream, x, gamma,
+                               out, feature, eps);
+            break;
+        case kF16:
+            hipLaunchKernelGGL((rmsnorm_kernel<kF16>), dim3(batch), dim3(256), 0, stream, x, gamma,
+                               out, feature, eps);
+            break;
+        case kF32:
+            hipLaunchKernelGGL((rmsnorm_kernel<kF32>), dim3(batch), dim3(256), 0, stream, x, gamma,
+                               out, feature, eps);
+            break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
 hipError_t launch_rope(const void *x, const void *cs, const void *sn, void *out, uint32_t head_dim,
-                       uint64_t n, bool bf16, hipStream_t stream) {
-    if (bf16 && head_dim % 16 == 0 && n % 8 == 0 &&
+                       uint64_t n, uint8_t dtype, hipStream_t stream) {
+    if (dtype == kBF16 && head_dim % 16 == 0 && n % 8 == 0 &&
         ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(cs) |
           reinterpret_cast<uintptr_t>(sn) | reinterpret_cast<uintptr_t>(out)) & 15) == 0) {
         hipLaunchKernelGGL(rope_bf16_vec_kernel, dim3(grid_for(n / 8)), dim3(256), 0, stream,
@@ -412,10 +459,21 @@ hipError_t launch_rope(const void *x, const void *cs, const void *sn, void *out,
         return hipGetLastError();
     }
     const unsigned grid = grid_for(n);
-    if (bf16)
-        hipLaunchKernelGGL((rope_kernel<true>), dim3(grid), dim3(256), 0, stream, x, cs, sn, out, head_dim, n);
-    else
-        hipLaunchKernelGGL((rope_kernel<false>), dim3(grid), dim3(256), 0, stream, x, cs, sn, out, head_dim, n);
+    switch (dtype) {
+        case kBF16:
+            hipLaunchKernelGGL((rope_kernel<kBF16>), dim3(grid), dim3(256), 0, stream, x, cs, sn, out,
+                               head_dim, n);
+            break;
+        case kF16:
+            hipLaunchKernelGGL((rope_kernel<kF16>), dim3(grid), dim3(256), 0, stream, x, cs, sn, out,
+                               head_dim, n);
+            break;
+        case kF32:
+            hipLaunchKernelGGL((rope_kernel<kF32>), dim3(grid), dim3(256), 0, stream, x, cs, sn, out,
+                               head_dim, n);
+            break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
@@ -444,6 +502,33 @@ __global__ __launch_bounds__(256) void act_f32_kernel(const float *__restrict__ 
     const uint64_t stride = uint64_t(gridDim.x) * 256;
     for (uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride)
         out[i] = act_f32(act, in[i]);
+}
+
+// The fused MatMul epilogues over an f16 product already in `c` (narrowed
+// with the reference's rounding), as matmul_activation_float /
+// matmul_add_float / matmul_add_activation_float compute 16-bit rows
+// (src/cpu/float_kernels.rs:816-935): v = widen(c[i]) (+ widen(res[i]) in
+// f32), the scalar fused activation on the f32 value, one narrowing.
+// kind: 1 = activation, 2 = residual add, 3 = add then activation.
+__global__ __launch_bounds__(256) void epilogue_f16_kernel(uint16_t *__restrict__ c,
+                                                           const uint16_t *__restrict__ res,
+                                                           uint64_t n, uint32_t kind, uint32_t act) {
+    const uint64_t stride = uint64_t(gridDim.x) * 256;
+    for (uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) {
+        float v = f16_bits_to_f32(c[i]);
+        if (kind >= 2) v = v + f16_bits_to_f32(res[i]);
+        if (kind != 2) v = act_f32(act, v);
+        c[i] = f32_to_f16_bits(v);
+    }
+}
+
+hipError_t launch_epilogue_f16(uint16_t *c, const uint16_t *res, uint64_t n, uint32_t kind,
+                               uint32_t act, hipStream_t stream) {
+    if (n == 0) return hipSuccess;
+    const uint64_t b = (n + 255) / 256;
+    hipLaunchKernelGGL(epilogue_f16_kernel, dim3(unsigned(b < 8192 ? b : 8192)), dim3(256), 0,
+                       stream, c, res, n, kind, act);
+    return hipGetLastError();
 }
 
 hipError_t launch_act_f32(const float *in, float *out, uint64_t n, uint32_t act,
@@ -506,9 +591,9 @@ hipError_t launch_transpose(const void *in, void *out, uint32_t rank, const uint
 hipError_t launch_argmax(const void *in, int32_t *out, uint32_t rows, uint32_t cols, bool bf16,
                          hipStream_t stream) {
     if (bf16)
-        hipLaunchKernelGGL((argmax_kernel<true>), dim3(rows), dim3(1024), 0, stream, in, out, cols);
+        hipLaunchKernelGGL((argmax_kernel<kBF16>), dim3(rows), dim3(1024), 0, stream, in, out, cols);
     else
-        hipLaunchKernelGGL((argmax_kernel<false>), dim3(rows), dim3(1024), 0, stream, in, out, cols);
+        hipLaunchKernelGGL((argmax_kernel<kF32>), dim3(rows), dim3(1024), 0, stream, in, out, cols);
     return hipGetLastError();
 }
 

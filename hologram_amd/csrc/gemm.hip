@@ -20,6 +20,7 @@ namespace holo {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
@@ -94,11 +95,15 @@ __device__ __forceinline__ void store_slab_bf16(uint16_t (*As)[BK16 + APAD16],
     }
 }
 
-template <bool kFast, int WT>
-__global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(const uint16_t *__restrict__ A,
-                                                            const uint16_t *__restrict__ B,
-                                                            uint16_t *__restrict__ C, uint32_t M,
-                                                            uint32_t N, uint32_t K) {
+// kF16: f16 operands on v_mfma_f32_16x16x32_f16 (products exact in f32, f32
+// accumulation), each result narrowed with the reference's f16 rounding
+// (write_float, src/cpu/dtype.rs:121-153); the lowp MatMul serves f16 as it
+// serves bf16 (float_kernels.rs:356-392).
+template <bool kFast, int WT, bool kF16>
+__device__ __forceinline__ void gemm16_tile(const uint16_t *__restrict__ A,
+                                            const uint16_t *__restrict__ B,
+                                            uint16_t *__restrict__ C, uint32_t M, uint32_t N,
+                                            uint32_t K) {
     constexpr int BM = 32 * WT, BN = BM;
     __shared__ uint16_t As[2][BM][BK16 + APAD16];
     __shared__ uint16_t Bs[2][BK16][BN + BPAD16];
@@ -139,8 +144,14 @@ __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(const uint16_t *__r
 #pragma unroll
             for (int i = 0; i < WT; ++i)
 #pragma unroll
-                for (int j = 0; j < WT; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < WT; ++j) {
+                    if constexpr (kF16)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            __builtin_bit_cast(f16x8, af[i]), __builtin_bit_cast(f16x8, bfr[j]),
+                            acc[i][j], 0, 0, 0);
+                    else
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+                }
         }
         if (s + 1 < nk) store_slab_bf16<BM>(As[cur ^ 1], Bs[cur ^ 1], ra, rb);
         __syncthreads();
@@ -155,8 +166,25 @@ __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(const uint16_t *__r
             for (int r = 0; r < 4; ++r) {
                 const uint32_t gm = m0 + wm + i * 16 + lg * 4 + r, gn = n0 + wn + j * 16 + lr;
                 if (gm < M && gn < N)
-                    C[uint64_t(gm) * N + gn] = uint16_t(__float_as_uint(acc[i][j][r]) >> 16);
+                    C[uint64_t(gm) * N + gn] = kF16 ? f32_to_f16_bits(acc[i][j][r])
+                                                    : uint16_t(__float_as_uint(acc[i][j][r]) >> 16);
             }
+}
+
+template <bool kFast, int WT>
+__global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(const uint16_t *__restrict__ A,
+                                                            const uint16_t *__restrict__ B,
+                                                            uint16_t *__restrict__ C, uint32_t M,
+                                                            uint32_t N, uint32_t K) {
+    gemm16_tile<kFast, WT, false>(A, B, C, M, N, K);
+}
+
+template <bool kFast, int WT>
+__global__ __launch_bounds__(kThreads) void gemm_f16_kernel(const uint16_t *__restrict__ A,
+                                                           const uint16_t *__restrict__ B,
+                                                           uint16_t *__restrict__ C, uint32_t M,
+                                                           uint32_t N, uint32_t K) {
+    gemm16_tile<kFast, WT, true>(A, B, C, M, N, K);
 }
 
 // ----------------------------------------------------------------- f32 ----
@@ -879,7 +907,8 @@ hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint
                          uint8_t dtype, void *scratch, hipStream_t stream) {
     const uintptr_t al = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b);
     // few rows: stream B once (16-byte aligned operands, output included)
-    if (((al | reinterpret_cast<uintptr_t>(c)) & 15) == 0 && matmul_skinny_applies(m, k, n, dtype))
+    if (dtype != 6 && ((al | reinterpret_cast<uintptr_t>(c)) & 15) == 0 &&
+        matmul_skinny_applies(m, k, n, dtype))
         return launch_matmul_skinny(a, b, c, m, k, n, dtype, scratch, stream);
     // 64-tiles when 128-tiles would not give every CU a workgroup
     const uint64_t tiles128 = uint64_t((m + 127) / 128) * ((n + 127) / 128);
@@ -934,6 +963,9 @@ hipError_t launch_matmul(const void *a, const void *b, void *c, uint32_t m, uint
     } else if (dtype == 8) {
         const bool fast = (al & 15) == 0 && k % BK32 == 0 && n % 4 == 0;
         HOLO_GEMM_LAUNCH(gemm_f32_kernel, float);
+    } else if (dtype == 6) {
+        const bool fast = (al & 15) == 0 && k % BK16 == 0 && n % 8 == 0;
+        HOLO_GEMM_LAUNCH(gemm_f16_kernel, uint16_t);
     } else {
         return hipErrorInvalidValue;
     }

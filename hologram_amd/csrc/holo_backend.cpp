@@ -263,8 +263,8 @@ int ensure_scratch(holo_backend *be, size_t bytes, const char *op) {
 int do_matmul(holo_backend *be, const SlotTable &st, const holo_matmul_call &c) {
     const char *op = "matmul";
     if (c.m == 0 || c.k == 0 || c.n == 0) return HOLO_OK;
-    if (c.dtype != HOLO_DTYPE_F32 && c.dtype != HOLO_DTYPE_BF16)
-        return fail(HOLO_ERR_UNSUPPORTED_OP, "matmul: the device path serves f32 and bf16");
+    if (c.dtype != HOLO_DTYPE_F32 && c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F16)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "matmul: the device path serves f32, bf16 and f16");
     // the compiler panel-packs constant f32 weights only (compiler.rs:590-613)
     if (c.b_packed && c.dtype != HOLO_DTYPE_F32)
         return fail(HOLO_ERR_UNSUPPORTED_OP, "matmul: a panel-packed B is served for f32 only");
@@ -561,6 +561,18 @@ int do_matmul_fused(holo_backend *be, const SlotTable &st, uint32_t tag, const h
             return fail(HOLO_ERR_UNSUPPORTED_OP, std::string(op) + ": residual must be element-aligned");
     }
     if (!be) return HOLO_OK;
+    if (c.dtype == HOLO_DTYPE_F16) {
+        // the f16 product into the output, then its epilogue in place
+        HOLO_TRY(do_matmul(be, st, c));
+        View o;
+        HOLO_TRY(split_borrow(st, nullptr, nullptr, 0, c.output, &o, op));
+        const uint32_t kind = tag == HOLO_OP_MATMUL_ACT ? 1u : tag == HOLO_OP_MATMUL_ADD ? 2u : 3u;
+        return launched(holo::launch_epilogue_f16(reinterpret_cast<uint16_t *>(o.base),
+                                                  has_res ? reinterpret_cast<const uint16_t *>(rv[0].base)
+                                                          : nullptr,
+                                                  count, kind, act, be->stream),
+                        op);
+    }
     if (c.b_packed) {
         // the packed product into the output, then the epilogue over it in place
         HOLO_TRY(do_matmul(be, st, c));
@@ -711,10 +723,16 @@ int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attentio
                     "decode_attention_i8: heads must be a multiple of kv_heads (grouped-query)");
     if (c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F32)
         return fail(HOLO_ERR_UNSUPPORTED_OP, "decode_attention_i8: q/output must be bf16 or f32");
-    if (!holo::attn_i8_supported(c.heads, hkv, c.head_dim, c.bucket_rows))
+    // the MFMA kernels take head_dim 64 / 128 with at most 16 query heads per
+    // kv head; every other shape takes the generic blocked kernel
+    const bool mfma = holo::attn_i8_supported(c.heads, hkv, c.head_dim, c.bucket_rows);
+    if (!mfma && !holo::attn_i8_any_supported(c.batch, c.heads, hkv, q_rows, c.head_dim))
         return fail(HOLO_ERR_UNSUPPORTED_OP,
-                    "decode_attention_i8: head_dim must be 64 or 128, heads/kv_heads at most 16 "
+                    "decode_attention_i8: head_dim must be at most 4096 (within the LDS plan) "
                     "and bucket_rows * head_dim at most 2^30");
+    if (uint64_t(c.bucket_rows) * c.head_dim > (uint64_t(1) << 30))
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    "decode_attention_i8: bucket_rows * head_dim must be at most 2^30");
     const uint64_t es = dtype_size(c.dtype);
     if (q_rows == 0) return fail(HOLO_ERR_UNSUPPORTED_OP, std::string(op) + ": q_rows must be >= 1");
     const uint64_t qn = uint64_t(c.batch) * q_rows * c.heads * c.head_dim;
@@ -750,7 +768,9 @@ int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attentio
         scale = sm > 0.0f ? 1.0f / sm : dflt;
     }
     const size_t scratch_bytes =
-        holo::attn_i8_scratch_bytes(c.batch, c.heads, hkv, c.bucket_rows, c.head_dim, q_rows);
+        mfma ? holo::attn_i8_scratch_bytes(c.batch, c.heads, hkv, c.bucket_rows, c.head_dim, q_rows)
+             : holo::attn_i8_any_scratch_bytes(c.batch, c.heads, hkv, q_rows, c.bucket_rows,
+                                               c.head_dim);
     void *scratch = nullptr;
     if (static_scratch) {
         // the allocation-free form: the fixed per-device array, never grown
@@ -790,7 +810,9 @@ int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attentio
         HOLO_TRY(launched(holo::launch_lens_within(a.lens, c.batch, c.bucket_rows, be->dev_err,
                                                    be->stream),
                           op));
-    return launched(holo::launch_attn_i8(a, scratch, be->stream), op);
+    return launched(mfma ? holo::launch_attn_i8(a, scratch, be->stream)
+                         : holo::launch_attn_i8_any(a, scratch, be->stream),
+                    op);
 }
 
 // -------------------------------------------------- DecodeAttentionValid --
@@ -1161,8 +1183,9 @@ int do_matmul_dequant(holo_backend *be, const SlotTable &st, const holo_matmul_d
 // binary_float (src/cpu/float_kernels.rs:238-300).
 int do_binary(holo_backend *be, const SlotTable &st, uint32_t tag, const holo_binary_call &c) {
     const char *op = tag == HOLO_OP_ADD ? "add" : "mul";
-    if (c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F32)
-        return fail(HOLO_ERR_UNSUPPORTED_OP, std::string(op) + ": the device path serves bf16 and f32");
+    if (c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F16 && c.dtype != HOLO_DTYPE_F32)
+        return fail(HOLO_ERR_UNSUPPORTED_OP,
+                    std::string(op) + ": the device path serves f16, bf16 and f32");
     if (c.element_count == 0) return HOLO_OK;
     const uint64_t es = dtype_size(c.dtype), bytes = c.element_count * es;
     holo_buffer_ref reads[2] = {c.a, c.b};
@@ -1175,7 +1198,7 @@ int do_binary(holo_backend *be, const SlotTable &st, uint32_t tag, const holo_bi
         return fail(HOLO_ERR_UNSUPPORTED_OP, std::string(op) + ": operands must be element-aligned");
     if (!be) return HOLO_OK;
     return launched(holo::launch_binary(tag == HOLO_OP_ADD ? 0 : 1, rv[0].base, rv[1].base, out.base,
-                                        c.element_count, c.dtype == HOLO_DTYPE_BF16, be->stream),
+                                        c.element_count, c.dtype, be->stream),
                     op);
 }
 
@@ -1184,8 +1207,8 @@ int do_binary(holo_backend *be, const SlotTable &st, uint32_t tag, const holo_bi
 int do_rmsnorm(holo_backend *be, const SlotTable &st, const holo_norm_call &c) {
     const char *op = "rms_norm";
     if (c.batch == 0 || c.feature == 0) return HOLO_OK;
-    if (c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F32)
-        return fail(HOLO_ERR_UNSUPPORTED_OP, "rms_norm: the device path serves bf16 and f32");
+    if (c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F16 && c.dtype != HOLO_DTYPE_F32)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "rms_norm: the device path serves f16, bf16 and f32");
     if (c.residual.slot != HOLO_SLOT_ABSENT || c.channels != 0 || c.num_groups != 0)
         return fail(HOLO_ERR_UNSUPPORTED_OP,
                     "rms_norm: residual / grouped forms are not served by the device path");
@@ -1212,7 +1235,7 @@ int do_rmsnorm(holo_backend *be, const SlotTable &st, const holo_norm_call &c) {
     if (c.batch > 0x7fffffffu) return fail(HOLO_ERR_UNSUPPORTED_OP, "rms_norm: batch too large");
     if (!be) return HOLO_OK;
     return launched(holo::launch_rmsnorm(rv[0].base, use_g ? rv[1].base : nullptr, out.base, c.batch,
-                                         c.feature, eps, c.dtype == HOLO_DTYPE_BF16, be->stream),
+                                         c.feature, eps, c.dtype, be->stream),
                     op);
 }
 
@@ -1221,8 +1244,8 @@ int do_rmsnorm(holo_backend *be, const SlotTable &st, const holo_norm_call &c) {
 int do_add_rmsnorm(holo_backend *be, const SlotTable &st, const holo_norm_call &c) {
     const char *op = "add_rms_norm";
     if (c.batch == 0 || c.feature == 0) return HOLO_OK;
-    if (c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F32)
-        return fail(HOLO_ERR_UNSUPPORTED_OP, "add_rms_norm: the device path serves bf16 and f32");
+    if (c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F16 && c.dtype != HOLO_DTYPE_F32)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "add_rms_norm: the device path serves f16, bf16 and f32");
     float eps = 1e-9f;
     if (c.epsilon_bits != 0) {
         const uint32_t eb = uint32_t(c.epsilon_bits);
@@ -1254,7 +1277,7 @@ int do_add_rmsnorm(holo_backend *be, const SlotTable &st, const holo_norm_call &
     if (!be) return HOLO_OK;
     return launched(holo::launch_add_rmsnorm(rv[0].base, has_r ? rv[1].base : nullptr,
                                              use_g ? rv[gi].base : nullptr, out.base, c.batch,
-                                             c.feature, eps, c.dtype == HOLO_DTYPE_BF16, be->stream),
+                                             c.feature, eps, c.dtype, be->stream),
                     op);
 }
 
@@ -1264,8 +1287,8 @@ int do_rope(holo_backend *be, const SlotTable &st, const holo_rope_call &c) {
     const char *op = "rope";
     if (c.head_dim == 0 || c.head_dim % 2 != 0 || c.element_count % c.head_dim != 0)
         return fail(HOLO_ERR_UNSUPPORTED_OP, "rope: head_dim must be even and divide the element count");
-    if (c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F32)
-        return fail(HOLO_ERR_UNSUPPORTED_OP, "rope: the device path serves bf16 and f32");
+    if (c.dtype != HOLO_DTYPE_BF16 && c.dtype != HOLO_DTYPE_F16 && c.dtype != HOLO_DTYPE_F32)
+        return fail(HOLO_ERR_UNSUPPORTED_OP, "rope: the device path serves f16, bf16 and f32");
     if (c.element_count == 0) return HOLO_OK;
     const uint64_t es = dtype_size(c.dtype), bytes = c.element_count * es;
     holo_buffer_ref reads[3] = {c.x, c.cos, c.sin};
@@ -1279,7 +1302,7 @@ int do_rope(holo_backend *be, const SlotTable &st, const holo_rope_call &c) {
         return fail(HOLO_ERR_UNSUPPORTED_OP, "rope: operands must be element-aligned");
     if (!be) return HOLO_OK;
     return launched(holo::launch_rope(rv[0].base, rv[1].base, rv[2].base, out.base, c.head_dim,
-                                      c.element_count, c.dtype == HOLO_DTYPE_BF16, be->stream),
+                                      c.element_count, c.dtype, be->stream),
                     op);
 }
 
@@ -1818,7 +1841,7 @@ int lut_act_of_fused(uint32_t act) {
 bool fused_act_supported(uint32_t act, uint8_t dtype, bool after_add) {
     const bool known = act >= 1 && act <= 8;
     if (dtype == HOLO_DTYPE_BF16) return after_add ? known : lut_act_of_fused(act) >= 0;
-    if (dtype == HOLO_DTYPE_F32) return known;
+    if (dtype == HOLO_DTYPE_F32 || dtype == HOLO_DTYPE_F16) return known;
     return false;
 }
 

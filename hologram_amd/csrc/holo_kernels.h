@@ -65,6 +65,13 @@ size_t attn_i8_scratch_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t buck
                              uint32_t q_rows = 1);
 bool attn_i8_supported(uint32_t H, uint32_t Hkv, uint32_t D, uint32_t bucket);
 hipError_t launch_attn_i8(const AttnI8Args &a, void *scratch, hipStream_t stream);
+// attn_valid.hip — the same op for every other head_dim (up to 4096) and any
+// query-head group: a blocked split-K walk with each K/V block dequantized
+// into LDS, then the merge of the shares.
+bool attn_i8_any_supported(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t q_rows, uint32_t D);
+size_t attn_i8_any_scratch_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t q_rows,
+                                 uint32_t bucket, uint32_t D);
+hipError_t launch_attn_i8_any(const AttnI8Args &a, void *scratch, hipStream_t stream);
 
 // attn_valid.hip — DecodeAttentionValid (discriminant 121) over bf16/f16/f32
 // K/V: q/out [B, H, M, D], k/v_past [B, Hkv, past, D], k/v_new [B, Hkv, nnew, D]
@@ -122,22 +129,26 @@ hipError_t launch_zero_points_check(const void *zps, uint64_t count, int *err, h
 hipError_t launch_dequant_act(const uint8_t *in, float *out, uint64_t n, bool i4,
                               const float table[256], hipStream_t stream);
 
-// decoder_ops.hip — the other ops of a decode step (bf16 or f32 operands).
-// op 0 = Add, 1 = Mul.
-hipError_t launch_binary(int op, const void *a, const void *b, void *out, uint64_t n, bool bf16,
+// decoder_ops.hip — the other ops of a decode step; `dtype` is the element
+// tag (f16 6, bf16 7, f32 8). op 0 = Add, 1 = Mul.
+hipError_t launch_binary(int op, const void *a, const void *b, void *out, uint64_t n, uint8_t dtype,
                          hipStream_t stream);
+// The fused MatMul epilogues over an f16 product in place: kind 1 = act,
+// 2 = + residual, 3 = act(+ residual), computed in f32, narrowed once.
+hipError_t launch_epilogue_f16(uint16_t *c, const uint16_t *res, uint64_t n, uint32_t kind,
+                               uint32_t act, hipStream_t stream);
 // out[i] = f(in[i]) over f32, f = act_f32(act) (a fused_activation id).
 hipError_t launch_act_f32(const float *in, float *out, uint64_t n, uint32_t act,
                           hipStream_t stream);
 // gamma == nullptr: no affine scale.
 // AddRmsNorm: rows of x + residual (residual may be null), in f32.
 hipError_t launch_add_rmsnorm(const void *x, const void *residual, const void *gamma, void *out,
-                              uint32_t batch, uint32_t feature, float eps, bool bf16,
+                              uint32_t batch, uint32_t feature, float eps, uint8_t dtype,
                               hipStream_t stream);
 hipError_t launch_rmsnorm(const void *x, const void *gamma, void *out, uint32_t batch,
-                          uint32_t feature, float eps, bool bf16, hipStream_t stream);
+                          uint32_t feature, float eps, uint8_t dtype, hipStream_t stream);
 hipError_t launch_rope(const void *x, const void *cs, const void *sn, void *out, uint32_t head_dim,
-                       uint64_t n, bool bf16, hipStream_t stream);
+                       uint64_t n, uint8_t dtype, hipStream_t stream);
 // Row gather; an out-of-range index zeroes its row and sets *err (device int).
 // Raise bit 2 of *err if any of lens[0..n) exceeds bucket (multi-row attention).
 hipError_t launch_lens_within(const uint32_t *lens, uint32_t n, uint32_t bucket, int *err,

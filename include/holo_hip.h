@@ -125,8 +125,9 @@ typedef struct holo_unary_call {
     uint8_t dtype;
 } holo_unary_call;
 
-/* BinaryCall, kernel_call.rs:38-46. Add / Mul over bf16 or f32: widen, one
- * IEEE f32 operation, narrow (bf16 by truncation) — binary_float,
+/* BinaryCall, kernel_call.rs:38-46. Add / Mul over f16, bf16 or f32: widen, one
+ * IEEE f32 operation, narrow (bf16 by truncation, f16 by the reference's
+ * rounding, src/cpu/dtype.rs:121-153) — binary_float,
  * src/cpu/float_kernels.rs:238-300. */
 typedef struct holo_binary_call {
     holo_buffer_ref a;
@@ -141,7 +142,7 @@ typedef struct holo_binary_call {
  * 1683-1755): per row of `feature` values, out = x * (1 / sqrtf(mean(x^2) +
  * eps)) * gamma (gamma absent: 1). eps = f32(epsilon_bits), 0 selects 1e-9
  * (float_kernels.rs:1324-1336). beta and residual must be absent; channels and
- * num_groups must be 0. dtype bf16 or f32.
+ * num_groups must be 0. dtype f16, bf16 or f32.
  * As AddRmsNorm (tag 54, add_rms_norm_float, float_kernels.rs:1566-1672): the
  * rows are v = x + residual (residual optional), summed in f32 and never
  * narrowed; beta, channels and num_groups are ignored. */
@@ -157,7 +158,8 @@ typedef struct holo_norm_call {
 } holo_norm_call;
 
 /* RoPECall, kernel_call.rs:500-515 (rope_float, float_kernels.rs:3123-3186):
- * rotate-half over heads of head_dim; cos/sin tables have x's element layout. */
+ * rotate-half over heads of head_dim; cos/sin tables have x's element layout;
+ * f16, bf16 or f32. */
 typedef struct holo_rope_call {
     holo_buffer_ref x;
     holo_buffer_ref cos;
@@ -194,7 +196,8 @@ typedef struct holo_argmax_call {
 } holo_argmax_call;
 
 /* MatMulCall, kernel_call.rs:49-65. Row-major A[m,k] * B[k,n] -> C[m,n];
- * f32 or bf16 (fp32 accumulation, bf16 result narrowed by truncation,
+ * f32, bf16 or f16 (fp32 accumulation; a bf16 result narrowed by truncation,
+ * an f16 one with the reference's rounding, src/cpu/dtype.rs:121-153;
  * src/cpu/float_kernels.rs:368-392). b_packed = 1 (f32 only) reads B in the
  * reference compiler's panel layout, f32[ceil(n/16)][k][16] (src/layout.rs:16-45). */
 typedef struct holo_matmul_call {

@@ -798,17 +798,22 @@ double or_max_rel_err(const float *got, const float *want, size_t n)
 }
 
 /* ------------------------------------------------------------------------ */
-/* Decode-step ops. Element access widens bf16 (exact) and narrows by       */
-/* truncation, as read_float / write_float do (src/cpu/dtype.rs:69-79).     */
+/* Decode-step ops. Element access widens bf16 and f16 (exact) and narrows  */
+/* bf16 by truncation and f16 by the reference's rounding, as read_float /  */
+/* write_float do (src/cpu/dtype.rs:69-153).                                */
 static float rd(const void *p, size_t i, int dtype)
 {
-    return dtype == OR_DTYPE_BF16 ? or_bf16_to_f32(((const uint16_t *)p)[i]) : ((const float *)p)[i];
+    if (dtype == OR_DTYPE_BF16) return or_bf16_to_f32(((const uint16_t *)p)[i]);
+    if (dtype == OR_DTYPE_F16) return or_f16_to_f32(((const uint16_t *)p)[i]);
+    return ((const float *)p)[i];
 }
 
 static void wr(void *p, size_t i, float v, int dtype)
 {
     if (dtype == OR_DTYPE_BF16)
         ((uint16_t *)p)[i] = or_f32_to_bf16(v);
+    else if (dtype == OR_DTYPE_F16)
+        ((uint16_t *)p)[i] = or_f32_to_f16(v);
     else
         ((float *)p)[i] = v;
 }

@@ -114,8 +114,11 @@ def test_matmul_refusals():
     validate(mm(m=2, k=3, n=4, dtype=DTYPE_F32), [24, 48, 32])
     with pytest.raises(SlotOutOfRange):
         validate(mm(m=2, k=3, n=4, dtype=DTYPE_F32), [24, 47, 32])
-    with pytest.raises(UnsupportedOp):
-        validate(mm(m=2, k=3, n=4, dtype=DTYPE_F16), [24, 48, 32])
+    validate(mm(m=2, k=3, n=4, dtype=DTYPE_F16), [12, 24, 16])    # f16 is served
+    with pytest.raises(SlotOutOfRange):
+        validate(mm(m=2, k=3, n=4, dtype=DTYPE_F16), [12, 23, 16])
+    with pytest.raises(UnsupportedOp):                                # i8 is no MatMul dtype
+        validate(mm(m=2, k=3, n=4, dtype=2), [24, 48, 32])
     # a packed B spans layout::packed_len(k, n) = ceil(n/16)*k*16 elements
     # (float_kernels.rs:317-324); the compiler packs f32 weights only
     with pytest.raises(SlotOutOfRange):
@@ -162,8 +165,12 @@ def test_attn_refusals():
     validate(call(batch=B, heads=H, kv_heads=Hkv, bucket_rows=bucket, head_dim=D), sizes)
     with pytest.raises(UnsupportedOp):
         validate(call(batch=B, heads=H, kv_heads=3, bucket_rows=bucket, head_dim=D), sizes)
+    # any head_dim up to 4096 is served (head_dim 96: the generic kernel)
+    d96 = [B * H * 96 * 2, rows * 96, rows * 96, rows * 4, rows * 4, B * 4, B * H * 96 * 2]
+    validate(call(batch=B, heads=H, kv_heads=Hkv, bucket_rows=bucket, head_dim=96), d96)
     with pytest.raises(UnsupportedOp):
-        validate(call(batch=B, heads=H, kv_heads=Hkv, bucket_rows=bucket, head_dim=96), sizes)
+        validate(call(batch=B, heads=H, kv_heads=Hkv, bucket_rows=bucket, head_dim=8192),
+                 [x * 64 for x in sizes])
     with pytest.raises(SlotOutOfRange):
         short = list(sizes)
         short[5] = 4

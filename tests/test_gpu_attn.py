@@ -72,6 +72,22 @@ def test_ragged_gqa(torch_cuda, backend, H, Hkv, D, dtype):
         assert norm_err(got[b], want[b]) <= TOL, f"sequence {b} (len {lens[b]})"
 
 
+@pytest.mark.parametrize("dtype", [DTYPE_BF16, DTYPE_F32])
+@pytest.mark.parametrize("H,Hkv,D", [(32, 8, 96), (16, 8, 256), (8, 2, 80), (32, 1, 64),
+                                     (4, 4, 32), (64, 2, 128)])
+def test_any_head_dim_and_group(torch_cuda, backend, H, Hkv, D, dtype):
+    """Shapes the MFMA kernels do not take (head_dim other than 64 / 128, or
+    more than 16 query heads per kv head) run the generic blocked kernel, to
+    the same bound, ragged lengths and a length past the bucket included."""
+    B, bucket = 4, 700
+    lens = [0, 1, 699, 5000]
+    got, want, _ = run_case(torch_cuda, backend, B, H, Hkv, D, bucket, lens, dtype, seed=H + D)
+    assert np.all(np.isfinite(got))
+    assert np.all(got[0] == 0)
+    for b in range(1, B):
+        assert norm_err(got[b], want[b]) <= TOL, f"sequence {b} (len {lens[b]})"
+
+
 def test_zero_length_is_exact_zero(torch_cuda, backend):
     got, want, _ = run_case(torch_cuda, backend, 3, 8, 2, 128, 64, [0, 64, 0], DTYPE_F32, seed=1)
     assert np.all(got[0] == 0) and np.all(got[2] == 0)

@@ -18,7 +18,7 @@ import pytest
 
 import oracle
 from conftest import from_dev, to_dev
-from hologram_amd import (DTYPE_BF16, DTYPE_F32, BinaryCall, BufferRef, DeviceWorkspace,
+from hologram_amd import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, BinaryCall, BufferRef, DeviceWorkspace,
                           HipSession, HoloWriter, KernelCall, MatMulActivationCall,
                           MatMulAddActivationCall, MatMulAddCall, MatMulCall, NormCall,
                           PortDescriptor, fused_activation)
@@ -33,11 +33,15 @@ FA = fused_activation
 def widen(bits, dtype):
     if dtype == DTYPE_BF16:
         return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+    if dtype == DTYPE_F16:
+        return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
     return np.asarray(bits).view(np.float32)
 
 
 def narrow(x, dtype):
     x = np.ascontiguousarray(x, np.float32)
+    if dtype == DTYPE_F16:   # the reference's rounding (dtype.rs:121-153), the oracle's codec
+        return np.array([oracle.lib().or_f32_to_f16(float(v)) for v in x.ravel()], np.uint16)
     return (x.view(np.uint32) >> 16).astype(np.uint16) if dtype == DTYPE_BF16 else x.view(np.uint32)
 
 
@@ -49,7 +53,11 @@ CASES = [("act", FA.SILU, DTYPE_BF16), ("act", FA.GELU, DTYPE_BF16), ("act", FA.
          ("act", FA.RELU, DTYPE_BF16), ("act", FA.ELU, DTYPE_BF16), ("act", FA.SELU, DTYPE_BF16),
          ("act", FA.RELU, DTYPE_F32), ("act", FA.ELU, DTYPE_F32), ("act", FA.SELU, DTYPE_F32),
          ("act", FA.EXP, DTYPE_F32), ("addact", FA.EXP, DTYPE_F32), ("addact", FA.SELU, DTYPE_BF16),
-         ("addact", FA.RELU, DTYPE_F32)]
+         ("addact", FA.RELU, DTYPE_F32),
+         # f16: the product narrowed with the reference's rounding, the scalar
+         # activation on its widened value (or on the f32 sum), one narrowing
+         ("act", FA.GELU, DTYPE_F16), ("act", FA.RELU, DTYPE_F16), ("add", 0, DTYPE_F16),
+         ("addact", FA.SILU, DTYPE_F16)]
 
 
 @pytest.mark.parametrize("m", [8, 100])
@@ -61,7 +69,7 @@ def test_fused_matmul_bit_exact(torch_cuda, backend, m, kind, act, dtype):
     b32 = rng.standard_normal(k * n).astype(np.float32)
     r32 = rng.standard_normal(m * n).astype(np.float32)
     a, b, r = (narrow(x, dtype) for x in (a32, b32, r32))
-    es = 2 if dtype == DTYPE_BF16 else 4
+    es = 4 if dtype == DTYPE_F32 else 2
     ws = DeviceWorkspace()
     keep = [to_dev(torch_cuda, x) for x in (a, b, r)]
     for s, t in enumerate(keep):
@@ -81,7 +89,7 @@ def test_fused_matmul_bit_exact(torch_cuda, backend, m, kind, act, dtype):
         call = KernelCall.MatMulAddActivation(MatMulAddActivationCall(mmf, BufferRef(2), act))
     backend.dispatch(call, ws)
     backend.synchronize()
-    bits_t = np.uint16 if dtype == DTYPE_BF16 else np.uint32
+    bits_t = np.uint32 if dtype == DTYPE_F32 else np.uint16
     p = from_dev(prod, bits_t)
     got = from_dev(fused, bits_t)
     v = widen(p, dtype)

@@ -5,7 +5,7 @@ import pytest
 
 import oracle
 from conftest import from_dev, to_dev
-from hologram_amd import (DTYPE_BF16, DTYPE_F32, BufferRef, DeviceWorkspace, KernelCall,
+from hologram_amd import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, BufferRef, DeviceWorkspace, KernelCall,
                           MatMulCall, UnsupportedOp)
 
 pytestmark = pytest.mark.gpu
@@ -45,6 +45,30 @@ def test_matmul_parity(torch_cuda, backend, m, k, n, dtype, tol):
     got, want = run_mm(torch_cuda, backend, m, k, n, dtype, seed=m * 7 + n)
     err = oracle.max_rel_err(got, want)
     assert err <= tol, f"normalized error {err:.3g}"
+
+
+@pytest.mark.parametrize("m,k,n", [(1024, 1024, 1024), (16, 4096, 4096), (77, 131, 45),
+                                   (300, 1000, 257), (1, 1, 1), (4096, 512, 1000), (5, 64, 24)])
+def test_matmul_f16_parity(torch_cuda, backend, m, k, n):
+    """f16 MatMul (the reference's lowp path serves f16 as bf16,
+    float_kernels.rs:356-392): f16 operands, f32 accumulation, each result
+    narrowed with the reference's rounding; within 1e-2 of the f64 product of
+    the same f16 values."""
+    rng = np.random.default_rng(m * 5 + n)
+    a = (rng.standard_normal(m * k) / np.sqrt(k)).astype(np.float16)
+    b = (rng.standard_normal(k * n) / np.sqrt(k)).astype(np.float16)
+    out = torch_cuda.zeros(m * n * 2, dtype=torch_cuda.uint8, device="cuda")
+    ws = DeviceWorkspace()
+    ws.bind(0, to_dev(torch_cuda, a.view(np.uint16)))
+    ws.bind(1, to_dev(torch_cuda, b.view(np.uint16)))
+    ws.bind(2, out)
+    backend.dispatch(KernelCall.MatMul(MatMulCall(BufferRef(0), BufferRef(1), BufferRef(2), m, k,
+                                                  n, DTYPE_F16)), ws)
+    backend.synchronize()
+    got = from_dev(out, np.uint16).view(np.float16).astype(np.float32)
+    want = oracle.matmul_ref_f64(a.astype(np.float32), b.astype(np.float32), m, k, n)
+    err = oracle.max_rel_err(got, want)
+    assert err <= 1e-2, f"normalized error {err:.3g}"
 
 
 @pytest.mark.parametrize("m,k,n", [(64, 512, 64), (192, 1024, 320), (1024, 2048, 512),

@@ -79,7 +79,8 @@ def run_rows(torch, backend, B, T, H, Hkv, D, S, lens, seed, q_rows_op=True):
     return got.reshape(B, T, H, D), want.reshape(B, T, H, D), from_dev(out, np.uint16)
 
 
-@pytest.mark.parametrize("H,Hkv,D", [(8, 2, 64), (16, 4, 128), (4, 4, 64)])
+@pytest.mark.parametrize("H,Hkv,D", [(8, 2, 64), (16, 4, 128), (4, 4, 64), (8, 2, 96),
+                                     (4, 2, 256), (40, 2, 64)])
 def test_attention_rows_parity(torch_cuda, backend, H, Hkv, D):
     B, T, S = 4, 9, 48
     # the third sequence is shorter than its prompt rows; the fourth fills the

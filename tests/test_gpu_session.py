@@ -20,7 +20,7 @@ import pytest
 
 import oracle
 from conftest import from_dev, to_dev
-from hologram_amd import (DTYPE_BF16, DTYPE_F32, DTYPE_I32, DTYPE_I64, ArgMaxCall, BinaryCall,
+from hologram_amd import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, DTYPE_I32, DTYPE_I64, ArgMaxCall, BinaryCall,
                           BufferRef, DeviceWorkspace, DispatchError, GatherCall, HipSession,
                           KernelCall, NormCall, RoPECall, SlotOutOfRange)
 from hologram_amd.decoder_graph import (DecoderConfig, build_decode_step, f32_bits,
@@ -53,13 +53,31 @@ def run(torch, backend, call, arrays, out_bytes, out_slot):
     return out.cpu().numpy()
 
 
-@pytest.mark.parametrize("dtype", [DTYPE_BF16, DTYPE_F32])
+def enc16(x32, dtype):
+    """f32 values as the operand dtype's array: bf16 / f16 bits, or f32."""
+    if dtype == DTYPE_BF16:
+        return bf(x32)
+    if dtype == DTYPE_F16:
+        return np.asarray(x32, np.float32).astype(np.float16).view(np.uint16)
+    return np.asarray(x32, np.float32)
+
+
+def dec16(raw, dtype):
+    """Output bytes of the dtype as f32 values."""
+    if dtype == DTYPE_BF16:
+        return unbf(raw.view(np.uint16))
+    if dtype == DTYPE_F16:
+        return raw.view(np.float16).astype(np.float32)
+    return raw.view(np.float32)
+
+
+@pytest.mark.parametrize("dtype", [DTYPE_BF16, DTYPE_F16, DTYPE_F32])
 @pytest.mark.parametrize("n", [1, 7, 4096, 100003])
 def test_add_mul_bit_exact(torch_cuda, backend, dtype, n):
     rng = np.random.default_rng(n)
     a32 = (rng.standard_normal(n) * 5).astype(np.float32)
     b32 = (rng.standard_normal(n) * 5).astype(np.float32)
-    a, b = (bf(a32), bf(b32)) if dtype == DTYPE_BF16 else (a32, b32)
+    a, b = enc16(a32, dtype), enc16(b32, dtype)
     es = a.itemsize
     for tag, op in ((KernelCall.Add, 0), (KernelCall.Mul, 1)):
         # an offset view of slot 1 exercises the unaligned path
@@ -71,13 +89,13 @@ def test_add_mul_bit_exact(torch_cuda, backend, dtype, n):
         assert np.array_equal(got, want)
 
 
-@pytest.mark.parametrize("dtype,tol", [(DTYPE_BF16, 1e-2), (DTYPE_F32, 1e-5)])
+@pytest.mark.parametrize("dtype,tol", [(DTYPE_BF16, 1e-2), (DTYPE_F16, 1e-2), (DTYPE_F32, 1e-5)])
 @pytest.mark.parametrize("batch,feature", [(1, 64), (8, 2048), (3, 1000)])
 def test_rms_norm(torch_cuda, backend, dtype, tol, batch, feature):
     rng = np.random.default_rng(feature)
     x32 = rng.standard_normal((batch, feature)).astype(np.float32) * 3
     g32 = rng.standard_normal(feature).astype(np.float32)
-    x, g = (bf(x32), bf(g32)) if dtype == DTYPE_BF16 else (x32, g32)
+    x, g = enc16(x32, dtype), enc16(g32, dtype)
     es = x.itemsize
     eps = f32_bits(1e-5)
     for with_g in (True, False):
@@ -87,14 +105,11 @@ def test_rms_norm(torch_cuda, backend, dtype, tol, batch, feature):
         got = run(torch_cuda, backend, call, {1: x, 2: g}, x.size * es, 3)
         want = np.zeros(x.size * es, np.uint8)
         lib().or_rms_norm(_p(x), _p(g) if with_g else None, _p(want), batch, feature, eps, dtype)
-        if dtype == DTYPE_BF16:
-            got_f, want_f = unbf(got.view(np.uint16)), unbf(want.view(np.uint16))
-        else:
-            got_f, want_f = got.view(np.float32), want.view(np.float32)
+        got_f, want_f = dec16(got, dtype), dec16(want, dtype)
         assert oracle.max_rel_err(got_f, want_f) <= tol
 
 
-@pytest.mark.parametrize("dtype,tol", [(DTYPE_BF16, 1e-2), (DTYPE_F32, 1e-5)])
+@pytest.mark.parametrize("dtype,tol", [(DTYPE_BF16, 1e-2), (DTYPE_F16, 1e-2), (DTYPE_F32, 1e-5)])
 @pytest.mark.parametrize("batch,feature", [(1, 64), (8, 2048), (3, 1000)])
 def test_add_rms_norm(torch_cuda, backend, dtype, tol, batch, feature):
     """AddRmsNorm (54): rms_norm(x + residual), the sum in f32; with and
@@ -103,7 +118,7 @@ def test_add_rms_norm(torch_cuda, backend, dtype, tol, batch, feature):
     x32 = rng.standard_normal((batch, feature)).astype(np.float32) * 3
     r32 = rng.standard_normal((batch, feature)).astype(np.float32)
     g32 = rng.standard_normal(feature).astype(np.float32)
-    x, r, g = (bf(x32), bf(r32), bf(g32)) if dtype == DTYPE_BF16 else (x32, r32, g32)
+    x, r, g = enc16(x32, dtype), enc16(r32, dtype), enc16(g32, dtype)
     es = x.itemsize
     eps = f32_bits(1e-5)
     absent = BufferRef(0xFFFFFFFF)
@@ -116,14 +131,11 @@ def test_add_rms_norm(torch_cuda, backend, dtype, tol, batch, feature):
             want = np.zeros(x.size * es, np.uint8)
             lib().or_add_rms_norm(_p(x), _p(r) if with_r else None, _p(g) if with_g else None,
                                   _p(want), batch, feature, eps, dtype)
-            if dtype == DTYPE_BF16:
-                got_f, want_f = unbf(got.view(np.uint16)), unbf(want.view(np.uint16))
-            else:
-                got_f, want_f = got.view(np.float32), want.view(np.float32)
+            got_f, want_f = dec16(got, dtype), dec16(want, dtype)
             assert oracle.max_rel_err(got_f, want_f) <= tol, (with_r, with_g)
 
 
-@pytest.mark.parametrize("dtype", [DTYPE_BF16, DTYPE_F32])
+@pytest.mark.parametrize("dtype", [DTYPE_BF16, DTYPE_F16, DTYPE_F32])
 @pytest.mark.parametrize("heads,D", [(37, 64), (5, 40), (80000, 128)])
 def test_rope_bit_exact(torch_cuda, backend, dtype, heads, D):
     """bf16 with head_dim a multiple of 16 takes the eight-a-lane kernel (the
@@ -133,7 +145,7 @@ def test_rope_bit_exact(torch_cuda, backend, dtype, heads, D):
     th = rng.uniform(-3, 3, (heads, D // 2))
     c32 = np.concatenate([np.cos(th), np.cos(th)], 1).astype(np.float32).ravel()
     s32 = np.concatenate([np.sin(th), np.sin(th)], 1).astype(np.float32).ravel()
-    x, c, s = (bf(x32), bf(c32), bf(s32)) if dtype == DTYPE_BF16 else (x32, c32, s32)
+    x, c, s = enc16(x32, dtype), enc16(c32, dtype), enc16(s32, dtype)
     es = x.itemsize
     call = KernelCall.RotaryEmbedding(RoPECall(BufferRef(1), BufferRef(2), BufferRef(3),
                                                BufferRef(4), D, x.size, dtype))

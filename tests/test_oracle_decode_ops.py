@@ -144,3 +144,49 @@ def test_argmax_rules():
     o = np.zeros(3, np.int32)
     lib().or_argmax(_p(t), _p(o), 3, 4, F32)
     assert list(o) == [1, 1, 0]
+
+
+F16 = 6
+
+
+def f16_narrow(x):
+    """The reference's f32 -> f16 rule (dtype.rs:121-153), through the pinned
+    scalar codec (test_oracle_pins.py checks it exhaustively)."""
+    return np.array([lib().or_f32_to_f16(float(v)) for v in np.ravel(x)], np.uint16)
+
+
+def unf16(b):
+    return np.asarray(b, np.uint16).view(np.float16).astype(np.float32)
+
+
+def test_f16_element_ops_widen_compute_in_f32_and_narrow_by_the_reference_rule():
+    """or_binary / or_rope / or_rms_norm over f16 (read_float / write_float,
+    dtype.rs:94-153): each element widened exactly, the f32 arithmetic of the
+    f32 path, then the reference's f16 narrowing."""
+    rng = np.random.default_rng(11)
+    a = (rng.standard_normal(2051) * 40).astype(np.float16).view(np.uint16)
+    b = (rng.standard_normal(2051) * 40).astype(np.float16).view(np.uint16)
+    for op, f in ((0, np.add), (1, np.multiply)):
+        out = np.zeros_like(a)
+        lib().or_binary(op, _p(a), _p(b), _p(out), a.size, F16)
+        assert np.array_equal(out, f16_narrow(f(unf16(a), unf16(b))))
+    heads, D = 5, 32
+    x = (rng.standard_normal(heads * D)).astype(np.float16).view(np.uint16)
+    th = rng.uniform(-3, 3, (heads, D // 2))
+    cs = np.concatenate([np.cos(th), np.cos(th)], 1).astype(np.float16).view(np.uint16).ravel()
+    sn = np.concatenate([np.sin(th), np.sin(th)], 1).astype(np.float16).view(np.uint16).ravel()
+    o16 = np.zeros_like(x)
+    assert lib().or_rope(_p(x), _p(cs), _p(sn), _p(o16), D, x.size, F16) == 0
+    x32, c32, s32 = unf16(x), unf16(cs), unf16(sn)
+    o32 = np.zeros_like(x32)
+    lib().or_rope(_p(x32), _p(c32), _p(s32), _p(o32), D, x.size, F32)
+    assert np.array_equal(o16, f16_narrow(o32))
+    B, F = 3, 96
+    xr = (rng.standard_normal(B * F) * 3).astype(np.float16).view(np.uint16)
+    g = rng.standard_normal(F).astype(np.float16).view(np.uint16)
+    o16 = np.zeros_like(xr)
+    assert lib().or_rms_norm(_p(xr), _p(g), _p(o16), B, F, 0, F16) == 0
+    xr32, g32 = unf16(xr), unf16(g)
+    o32 = np.zeros_like(xr32)
+    lib().or_rms_norm(_p(xr32), _p(g32), _p(o32), B, F, 0, F32)
+    assert np.array_equal(o16, f16_narrow(o32))

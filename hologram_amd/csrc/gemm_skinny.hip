@@ -6,13 +6,20 @@
 // crates/hologram-compute/src/cpu/float_kernels.rs:298-399): fp32 accumulate,
 // bf16 results narrowed by truncation (src/cpu/dtype.rs:75-79).
 //
-// Work split. A workgroup owns a strip of columns (128 for bf16, 64 for f32)
-// and a K range of KC rows; its four wavefronts interleave over that range in
-// k steps, each wave issuing all of its steps' B loads up front (about 128 KiB
-// in flight per workgroup). The waves' partial tiles are summed through LDS in
-// a fixed order. With more than one K range the workgroups write fp32 partials
-// [ks][M][N] and a second kernel sums them in ks order, so the result does not
-// depend on scheduling.
+// Summation order (bf16). K is cut into 32-deep steps; chain c = 0..63
+// accumulates the steps s = c, c + 64, c + 128, ... in ascending order on the
+// MFMA; group g = 0..15 adds its chains 4g .. 4g + 3 in order; the product is
+// the groups added in order. The order depends on K alone, so a call, a
+// grouped launch and the single-launch form over packed weights
+// (gemv_packed.hip) give the same bits.
+//
+// Work split (bf16). A workgroup owns a strip of 128 columns and one group:
+// its four wavefronts are the group's four chains, each issuing all of its
+// steps' B loads up front (up to four steps a batch), and their partial tiles
+// are added through LDS in chain order. Each group's fp32 partials go to
+// [group][M][N] and a second kernel adds the groups in order. f32 keeps
+// contiguous K ranges of KC rows, the four waves interleaving over a range in
+// k steps, the ranges summed in order by the same second kernel.
 //
 // B operand without LDS. B is row-major, the MFMA B operand wants consecutive
 // k per lane. A lane loads an 8 (k) x 8 (n) bf16 block as eight 16-byte rows
@@ -90,105 +97,103 @@ __device__ __forceinline__ SegPick pick_segment(const SkinnyArgs &g) {
 }
 
 // ---------------------------------------------------------------- bf16 ----
-// MT 16-row tiles of A, STEPS 32-deep k steps per wave: KC = 4 * STEPS * 32.
+// MT 16-row tiles of A; each wave (chain 4 * blockIdx.y + w) takes its steps
+// STEPS at a time, all of a batch's loads issued before its MFMAs.
 template <int MT, int STEPS>
 __global__ __launch_bounds__(256) void skinny_bf16_kernel(const SkinnyArgs g) {
-    constexpr uint32_t KC = kWaves * STEPS * 32;
     __shared__ f32x4 red[kWaves - 1][MT][8][64];
     const SegPick sg = pick_segment(g);
     const uint16_t *__restrict__ A = static_cast<const uint16_t *>(g.a);
     const uint16_t *__restrict__ B = static_cast<const uint16_t *>(sg.b);
-    const uint32_t M = g.m, N = sg.n, K = g.k;
+    const uint32_t M = g.m, N = sg.n, K = g.k, S = K / 32;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, grp = lane >> 4, q = lane & 15;
     const uint32_t n0 = sg.strip * 128 + 8 * q;
-    const uint32_t kb0 = blockIdx.y * KC;
-    const uint32_t krows = K - kb0 < KC ? K - kb0 : KC;
-    // This workgroup's rows of B as one buffer range; columns past N are sent
-    // out of range, where buffer loads return zero.
-    const auto rb = rsrc(B + uint64_t(kb0) * N, krows * N * 2u);
+    const uint32_t chain = 4 * blockIdx.y + w;
+    // steps of this chain: chain, chain + 64, ...
+    const uint32_t nsteps = chain < S ? (S - chain + 63) / 64 : 0;
+    // All of B as one buffer range; columns past N are sent out of range,
+    // where buffer loads return zero.
+    const auto rb = rsrc(B, K * N * 2u);
     const auto ra = rsrc(A, M * K * 2u);   // rows >= M read zero
     const uint32_t bcol = n0 < N ? n0 * 2u : 0x80000000u;
 
     // RmsNorm of A on the way in: the producer's four wave sums of each of
-    // this lane's rows and gamma at the lane's k values, loaded ahead of B
-    // No load sits behind a branch: a step past the range, a row past M or an
+    // this lane's rows and gamma at the lane's k values, loaded ahead of B.
+    // No load sits behind a branch: a step past the chain, a row past M or an
     // absent gamma loads from an out-of-range offset (zero, no memory access),
     // so the compiler counts the loads in flight exactly and each step waits
     // only for its own.
     const bool norm = g.norm.ssq != nullptr;
+    const auto rs = rsrc(g.norm.ssq, norm ? M * 16u : 0u);
+    const auto rg = rsrc(g.norm.gamma, norm && g.norm.gamma ? K * 2u : 0u);
     f32x4 ssq[MT];
-    u32x4 gam[STEPS];
-    {   // (empty ranges when there is no norm: nothing is read)
-        const auto rs = rsrc(g.norm.ssq, norm ? M * 16u : 0u);
-        const auto rg = rsrc(g.norm.gamma, norm && g.norm.gamma ? K * 2u : 0u);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-            ssq[mt] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                    rs, (mt * 16 + q) * 16u, 0, 0));
-#pragma unroll
-        for (int t = 0; t < STEPS; ++t) {
-            const uint32_t kr = uint32_t(t * kWaves + w) * 32;
-            gam[t] = __builtin_amdgcn_raw_buffer_load_b128(
-                rg, kr < krows ? (kb0 + kr + 8 * grp) * 2u : 0x80000000u, 0, 0);
-        }
-    }
-    u32x4 b[STEPS][8], a[STEPS][MT];
-#pragma unroll
-    for (int t = 0; t < STEPS; ++t) {
-        const uint32_t kr = uint32_t(t * kWaves + w) * 32;   // step start within the range
-        const bool live = kr < krows;
-        const uint32_t vo = live ? bcol + (kr + 8 * grp) * N * 2u : 0x80000000u;
-#pragma unroll
-        for (int r = 0; r < 8; ++r)
-            b[t][r] = __builtin_amdgcn_raw_buffer_load_b128(rb, vo, int(N * 2u) * r, 0);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-            a[t][mt] = __builtin_amdgcn_raw_buffer_load_b128(
-                ra, live ? ((mt * 16 + q) * K + kb0 + kr + 8 * grp) * 2u : 0x80000000u, 0, 0);
-    }
-    // inv of each row: the four wave sums added in the standalone kernel's order
-    float inv[MT];
-    if (norm && !g.norm.gamma)   // no gamma: scale 1
-#pragma unroll
-        for (int t = 0; t < STEPS; ++t) gam[t] = u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
-    if (norm)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const f32x4 s = ssq[mt];
-            inv[mt] = 1.0f / sqrtf((s[0] + s[1] + s[2] + s[3]) / float(K) + g.norm.eps);
-        }
+    for (int mt = 0; mt < MT; ++mt)
+        ssq[mt] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                rs, (mt * 16 + q) * 16u, 0, 0));
     f32x4 acc[MT][8];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int c = 0; c < 8; ++c) acc[mt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float inv[MT] = {};
+    for (uint32_t t0 = 0; t0 < nsteps; t0 += STEPS) {
+        u32x4 b[STEPS][8], a[STEPS][MT], gam[STEPS];
 #pragma unroll
-    for (int t = 0; t < STEPS; ++t) {
-        if (uint32_t(t * kWaves + w) * 32 < krows) {
-            if (norm) {
+        for (int t = 0; t < STEPS; ++t) {
+            const bool live = t0 + t < nsteps;
+            const uint32_t kr = (chain + 64 * (t0 + t)) * 32;   // the step's first row of B
+            gam[t] = __builtin_amdgcn_raw_buffer_load_b128(rg, live ? (kr + 8 * grp) * 2u : 0x80000000u,
+                                                           0, 0);
+            const uint32_t vo = live ? bcol + (kr + 8 * grp) * N * 2u : 0x80000000u;
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    u32x4 r;
+            for (int r = 0; r < 8; ++r)
+                b[t][r] = __builtin_amdgcn_raw_buffer_load_b128(rb, vo, int(N * 2u) * r, 0);
 #pragma unroll
-                    for (int h = 0; h < 4; ++h) {
-                        const uint32_t x = a[t][mt][h], y = gam[t][h];
-                        const float lo = (__uint_as_float(x << 16) * inv[mt]) * __uint_as_float(y << 16);
-                        const float hi = (__uint_as_float(x & 0xFFFF0000u) * inv[mt]) *
-                                         __uint_as_float(y & 0xFFFF0000u);
-                        r[h] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
-                    }
-                    a[t][mt] = r;
-                }
+            for (int mt = 0; mt < MT; ++mt)
+                a[t][mt] = __builtin_amdgcn_raw_buffer_load_b128(
+                    ra, live ? ((mt * 16 + q) * K + kr + 8 * grp) * 2u : 0x80000000u, 0, 0);
+        }
+        if (norm) {
+            // inv of each row: the four wave sums added in the standalone kernel's order
+            if (!g.norm.gamma)   // no gamma: scale 1
+#pragma unroll
+                for (int t = 0; t < STEPS; ++t)
+                    gam[t] = u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const f32x4 s = ssq[mt];
+                inv[mt] = 1.0f / sqrtf((s[0] + s[1] + s[2] + s[3]) / float(K) + g.norm.eps);
             }
+        }
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const u32x4 o = column8(b[t], c);
+        for (int t = 0; t < STEPS; ++t) {
+            if (t0 + t < nsteps) {
+                if (norm) {
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
-                    acc[mt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        __builtin_bit_cast(bf16x8, a[t][mt]), __builtin_bit_cast(bf16x8, o),
-                        acc[mt][c], 0, 0, 0);
+                    for (int mt = 0; mt < MT; ++mt) {
+                        u32x4 r;
+#pragma unroll
+                        for (int h = 0; h < 4; ++h) {
+                            const uint32_t x = a[t][mt][h], y = gam[t][h];
+                            const float lo = (__uint_as_float(x << 16) * inv[mt]) * __uint_as_float(y << 16);
+                            const float hi = (__uint_as_float(x & 0xFFFF0000u) * inv[mt]) *
+                                             __uint_as_float(y & 0xFFFF0000u);
+                            r[h] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+                        }
+                        a[t][mt] = r;
+                    }
+                }
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    const u32x4 o = column8(b[t], c);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+                        acc[mt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(bf16x8, a[t][mt]), __builtin_bit_cast(bf16x8, o),
+                            acc[mt][c], 0, 0, 0);
+                }
             }
         }
     }
@@ -403,28 +408,45 @@ hipError_t launch_skinny(const SkinnyArgs &g, uint8_t dtype, int mt, int steps, 
 }  // namespace
 
 // The split of a few-row MatMul: 16-row tiles of A, the k steps per wave and
-// the K ranges. It fixes the order of every fp32 sum of the product (within a
-// wave, across the four waves, then across K ranges in ks order), so a call
-// and a grouped launch with the same plan give the same bits. mt = 0: the
+// the K ranges (bf16: the groups of the summation order). For f32 it fixes
+// the order of every fp32 sum (within a wave, across the four waves, then
+// across K ranges in ks order), so a call and a grouped launch with the same
+// plan give the same bits; for bf16 the order depends on K alone. mt = 0: the
 // few-row kernels do not apply.
-// Workgroups per CU the K split aims for. One gives config 5's decode step
-// 1.068 ms against 1.091 with two (fewer partials for the epilogues to sum)
-// and 1.128 with four.
+// f32 workgroups per CU the K split aims for: one gave config 5's decode
+// step 1.068 ms against 1.091 with two (fewer partials for the epilogues to
+// sum) and 1.128 with four.
 constexpr uint32_t kSkinnyWgPerCu = 1;
 SkinnyPlan matmul_skinny_plan(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype) {
     SkinnyPlan p;
     if (m == 0 || m > 64 || k == 0 || n == 0) return p;
     const bool bf16 = dtype == 7;
     if (dtype != 7 && dtype != 8) return p;
-    const uint32_t es = bf16 ? 2 : 4;
     if (bf16 ? (n % 8 != 0 || k % 32 != 0) : (n % 4 != 0 || k % 16 != 0)) return p;
     p.mt = m <= 16 ? 1 : m <= 32 ? 2 : 4;
     p.strips = (n + (bf16 ? 127 : 63)) / (bf16 ? 128 : 64);
+    if (bf16) {
+        // 32-bit buffer ranges over all of A and all of B (plus the
+        // out-of-range column offset 2^31 on top of a row offset)
+        if (uint64_t(m) * k * 2 >= (1ull << 31) || uint64_t(k) * n * 2 >= (1ull << 31) ||
+            p.strips > (1u << 31)) {
+            p.mt = 0;
+            return p;
+        }
+        const uint32_t S = k / 32, per_chain = (S + 63) / 64;
+        const int max_steps = p.mt == 4 ? 2 : 4;
+        p.steps = 1;
+        while (p.steps < max_steps && uint32_t(p.steps) < per_chain) p.steps *= 2;
+        p.ks = S / 4 + (S % 4 != 0);
+        if (p.ks > 16) p.ks = 16;
+        p.kc = 0;
+        return p;
+    }
     // k steps per wave: the most that still gives every CU its workgroups
     // (a long K range per workgroup keeps its loads streaming; a short one
     // fills the GPU when B is small)
-    const int kstep = bf16 ? 32 : 16;
-    const int max_steps = bf16 ? (p.mt == 4 ? 2 : 4) : (p.mt == 4 ? 4 : 8);
+    const int kstep = 16;
+    const int max_steps = p.mt == 4 ? 4 : 8;
     p.steps = max_steps;
     while (p.steps > 1 &&
            uint64_t(p.strips) * ((k + kWaves * p.steps * kstep - 1) / (kWaves * p.steps * kstep)) <
@@ -433,7 +455,7 @@ SkinnyPlan matmul_skinny_plan(uint32_t m, uint32_t k, uint32_t n, uint8_t dtype)
     p.kc = kWaves * p.steps * kstep;
     // 32-bit buffer ranges: all of A, and KC rows of B (plus the out-of-range
     // column offset 2^31 on top of a row offset)
-    if (uint64_t(m) * k * es >= (1ull << 31) || uint64_t(p.kc) * n * es >= (1ull << 31)) {
+    if (uint64_t(m) * k * 4 >= (1ull << 31) || uint64_t(p.kc) * n * 4 >= (1ull << 31)) {
         p.mt = 0;
         return p;
     }

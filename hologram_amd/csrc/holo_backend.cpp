@@ -394,7 +394,9 @@ int dispatch_group_impl(holo_backend *be, const SlotTable &st, const holo::Group
                                                              "16-byte aligned columns");
     }
     holo::SkinnyNormA na;
-    const bool a_norm = g.a_ssq != nullptr;
+    const bool a_norm = g.a_norm;
+    if (a_norm && !g.packed && !g.a_ssq)
+        return fail(HOLO_ERR_DISPATCH, std::string(op) + ": a normalized A without row statistics");
     if (a_norm) {
         if (!bf16) return fail(HOLO_ERR_DISPATCH, std::string(op) + ": a normalized A must be bf16");
         na.ssq = g.a_ssq;
@@ -411,6 +413,31 @@ int dispatch_group_impl(holo_backend *be, const SlotTable &st, const holo::Group
                 na.gamma = reinterpret_cast<const uint16_t *>(gv.base);
             }
         }
+    }
+    if (g.packed && (aligned(a, 16) || (a_norm && !g.a_ssq))) {
+        // one launch over the fragment-order weights; a normalized A's
+        // statistics are taken in it (an A the launch's 16-byte loads cannot
+        // take, bound by the caller, goes the split-K way: same bits)
+        holo::PackedGroup pg;
+        pg.a = a.base;
+        pg.m = g.m;
+        pg.k = g.k;
+        pg.nseg = int(nseg);
+        pg.norm = a_norm;
+        pg.gamma = na.gamma;
+        pg.eps = na.eps;
+        pg.tw = g.packed_tw;
+        for (size_t i = 0; i < nseg; ++i) {
+            pg.bp[i] = g.segs[i].bp;
+            pg.seg[i] = e.seg[i];
+            pg.seg[i].ssq = nullptr;
+            if (!pg.bp[i])
+                return fail(HOLO_ERR_DISPATCH, std::string(op) + ": packed group without packed weights");
+        }
+        if (!bf16 || !aligned(a, 16) || !holo::packed_group_applies(g.m, g.k, pg.seg, int(nseg), a_norm))
+            return fail(HOLO_ERR_DISPATCH, std::string(op) + ": a packed group needs bf16, <= 16 rows of "
+                                                             "16-byte aligned A and 16-column tiles");
+        return launched(holo::launch_packed_group(pg, be->stream), op);
     }
     bool stats = false;
     for (size_t i = 0; i < nseg; ++i) stats = stats || g.segs[i].ssq;

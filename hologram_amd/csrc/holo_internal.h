@@ -50,17 +50,25 @@ struct GroupSegDesc {
     uint32_t bucket = 0, new_rows = 0;
     int pair = -1;
     float *ssq = nullptr;      // RmsNorm statistics of the rows (EpiSeg::ssq), session memory
+    const void *bp = nullptr;  // B in MFMA fragment order (session memory) when the group is packed
 };
 struct GroupDesc {
     holo_buffer_ref a{};
     uint32_t m = 0, k = 0;
     uint8_t dtype = 0;
     std::vector<GroupSegDesc> segs;
-    // A read as RmsNorm(A) (SkinnyNormA): the statistics a producer group left
-    // in session memory, gamma (absent: identity) and epsilon
+    // A read as RmsNorm(A) (SkinnyNormA): a_norm; the statistics a producer
+    // group left in session memory (split-K readers), gamma (absent:
+    // identity) and epsilon
+    bool a_norm = false;
     const float *a_ssq = nullptr;
     holo_buffer_ref a_gamma{HOLO_SLOT_ABSENT, 0, 0};
     float a_eps = 0.0f;
+    // every product and epilogue in one launch over each segment's `bp`
+    // (gemv_packed.hip); a normalized A's statistics are then taken in that
+    // launch, not read from a_ssq
+    bool packed = false;
+    uint32_t packed_tw = 16;   // element-wise tile width the weights were packed with
 };
 int dispatch_group(holo_backend *be, const std::vector<SlotRange> &slots, const GroupDesc &g);
 // The LUT activation id of a fused_activation id (-1: no table).

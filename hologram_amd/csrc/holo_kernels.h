@@ -253,6 +253,34 @@ struct EpiArgs {
 };
 hipError_t launch_epilogue(EpiArgs g, hipStream_t stream);
 
+// gemv_packed.hip — a few-row bf16 group (m <= 16) over weights packed into
+// MFMA fragment order (launch_pack_b): every product and its epilogue (the
+// EpiSeg fields, except `ssq`: a group that reads A through a fused RmsNorm
+// computes the statistics itself) in one launch, a workgroup per 16-column
+// tile, SwiGLU tile pair or head. Same bits as the split-K launch and
+// launch_epilogue over the same segments.
+struct PackedGroup {
+    const void *a = nullptr;               // [m, k] bf16, 16-byte aligned
+    const uint16_t *gamma = nullptr;       // norm: [k] (null: the identity)
+    float eps = 0.0f;
+    bool norm = false;                     // A read as RmsNorm(A) (SkinnyNormA's arithmetic)
+    uint32_t m = 0, k = 0;
+    int nseg = 0;
+    uint32_t tw = 16;                      // element-wise tile width (8 or 16): as the weights were packed
+    uint32_t tpu = 0;                      // tiles per element-wise workgroup (0: chosen)
+    int occupancy = 0;                     // workgroups a CU: 2 for one-tile units, else 1
+    const void *bp[kSkinnyMaxSeg] = {};   // B_s [k, n_s] in fragment order
+    EpiSeg seg[kSkinnyMaxSeg];
+};
+bool packed_group_applies(uint32_t m, uint32_t k, const EpiSeg *segs, int nseg, bool norm);
+hipError_t launch_packed_group(const PackedGroup &pg, hipStream_t stream);
+// B [k, n] row-major bf16 -> fragment order in tiles of tw = 8 or 16 columns
+// (k % 32 == 0, n % tw == 0): packed_b_bytes(k, n, tw) (= k * n * 2) bytes at bp.
+hipError_t launch_pack_b(const void *b, void *bp, uint32_t k, uint32_t n, uint32_t tw, hipStream_t stream);
+uint64_t packed_b_bytes(uint32_t k, uint32_t n, uint32_t tw);
+// The tile width a group's weights are packed with.
+uint32_t packed_tile_width(uint32_t m, uint32_t k, const EpiSeg *segs, int nseg);
+
 struct SkinnySegment {
     const void *b;
     uint32_t n;

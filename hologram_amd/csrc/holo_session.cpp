@@ -41,6 +41,7 @@
 #include <map>
 #include <memory>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "holo_hip.h"
@@ -568,6 +569,8 @@ struct holo_session {
     std::vector<Node> nodes;                      // the walk, in order
     std::vector<holo::GroupDesc> groups;          // fused few-row MatMul groups
     float *norm_arena = nullptr;                  // RmsNorm statistics of fused norms
+    void *packed_arena = nullptr;                 // weights of packed groups, fragment order
+    uint64_t packed_bytes = 0;
     // split-K partials of this session's walks (few-row MatMuls, attention):
     // its own, so no other session or direct dispatch on the same backend
     // frees or shares what a captured graph of this walk reads and writes
@@ -923,8 +926,45 @@ bool has_slot(const std::vector<uint32_t> &v, uint32_t slot) {
     return std::find(v.begin(), v.end(), slot) != v.end();
 }
 
+// Whether a group can run as one launch over packed weights
+// (gemv_packed.hip): bf16, at most 16 rows of a 16-byte aligned A in session
+// memory, every weight a constant, the segments' tiles and heads in reach of
+// the kernel.
+bool packable_group(const holo_session *s, const holo::GroupDesc &g, const std::vector<uint8_t> &is_input,
+                    const std::vector<uint8_t> &is_const) {
+    const size_t nslots = is_const.size();
+    auto caller_bound = [&](uint32_t slot) { return slot >= is_input.size() || is_input[slot]; };
+    auto aligned16 = [&](const holo_buffer_ref &r) { return r.offset % 16 == 0 && !caller_bound(r.slot); };
+    if (g.dtype != HOLO_DTYPE_BF16 || g.m == 0 || g.m > 16 || !aligned16(g.a) ||
+        (g.a_gamma.slot != HOLO_SLOT_ABSENT && !aligned16(g.a_gamma)) || g.segs.empty() ||
+        g.segs.size() > size_t(holo::kSkinnyMaxSeg))
+        return false;
+    holo::EpiSeg es[holo::kSkinnyMaxSeg];
+    for (size_t i = 0; i < g.segs.size(); ++i) {
+        const auto &d = g.segs[i];
+        if (d.b.slot >= nslots || !is_const[d.b.slot] || d.b.offset % 16 ||
+            s->slot_bytes[d.b.slot] < d.b.offset + uint64_t(g.k) * d.n * 2)
+            return false;
+        if ((d.base == holo::kEpiAct || d.base == holo::kEpiAddAct) &&
+            !holo::fused_act_supported(d.act, g.dtype, d.base == holo::kEpiAddAct))
+            return false;
+        holo::EpiSeg &e = es[i];
+        e.n = d.n;
+        e.base = d.base;
+        e.head_dim = d.head_dim;
+        e.rope = d.rope;
+        e.quant = d.quant;
+        e.bucket = d.bucket;
+        e.new_rows = d.new_rows;
+        e.pair = d.pair;
+        e.skip = d.skip;
+    }
+    return holo::packed_group_applies(g.m, g.k, es, int(g.segs.size()), g.a_norm);
+}
+
 int norm_fusion(holo_session *s, const std::vector<uint8_t> &is_output,
-                const std::vector<uint8_t> &is_input) {
+                const std::vector<uint8_t> &is_input, const std::vector<uint8_t> &is_const,
+                bool packing) {
     auto &nodes = s->nodes;
     const size_t nn = nodes.size();
     std::vector<std::vector<uint32_t>> R(nn), W(nn);
@@ -1011,23 +1051,26 @@ int norm_fusion(holo_session *s, const std::vector<uint8_t> &is_output,
         if (x.slot == y.slot || !aligned16(x) || (has_g && !aligned16(nc.gamma)) ||
             y.slot >= is_output.size() || is_output[y.slot])
             continue;
-        // producer: the nearest earlier writer of x
+        // producer: the nearest earlier writer of x, when it is a few-row
+        // product that can leave the statistics
         size_t j = k;
         while (j > 0 && !has_slot(W[j - 1], x.slot)) --j;
-        if (j == 0) continue;
-        --j;
-        holo::GroupDesc tp;
-        const holo::GroupDesc *pg = view(j, &tp);
-        if (!pg || pg->segs.size() != 1 || !few_row(*pg) || pg->m != nc.batch) continue;
         int pseg = -1;
-        for (size_t t = 0; t < pg->segs.size(); ++t) {
-            const auto &sg = pg->segs[t];
-            if (same_ref(sg.out, x) && sg.write_out && sg.n == nc.feature && !sg.head_dim && !sg.rope &&
-                !sg.quant && sg.pair < 0 && !sg.skip && !sg.ssq && aligned16(sg.out) &&
-                (!(sg.base == holo::kEpiAdd || sg.base == holo::kEpiAddAct) || aligned16(sg.residual)))
-                pseg = int(t);
+        if (j > 0) {
+            --j;
+            holo::GroupDesc tp;
+            const holo::GroupDesc *pg = view(j, &tp);
+            if (pg && pg->segs.size() == 1 && few_row(*pg) && pg->m == nc.batch) {
+                for (size_t t = 0; t < pg->segs.size(); ++t) {
+                    const auto &sg = pg->segs[t];
+                    if (same_ref(sg.out, x) && sg.write_out && sg.n == nc.feature && !sg.head_dim &&
+                        !sg.rope && !sg.quant && sg.pair < 0 && !sg.skip && !sg.ssq && aligned16(sg.out) &&
+                        (!(sg.base == holo::kEpiAdd || sg.base == holo::kEpiAddAct) || aligned16(sg.residual)))
+                        pseg = int(t);
+                }
+                if (pseg >= 0 && linked_seg(nodes[j].group, pseg)) pseg = -1;
+            }
         }
-        if (pseg < 0 || linked_seg(nodes[j].group, pseg)) continue;
         // consumer: the one reader of y before y's slot is written again
         size_t q = nn, readers = 0;
         for (size_t t = k + 1; t < nn; ++t) {
@@ -1040,9 +1083,23 @@ int norm_fusion(holo_session *s, const std::vector<uint8_t> &is_output,
         if (readers != 1) continue;
         holo::GroupDesc tc;
         const holo::GroupDesc *cg = view(q, &tc);
-        if (!cg || !few_row(*cg) || linked_cons(nodes[q].group) || !same_ref(cg->a, y) ||
-            cg->m != nc.batch || cg->k != nc.feature)
+        if (!cg || linked_cons(nodes[q].group) || !same_ref(cg->a, y) || cg->m != nc.batch ||
+            cg->k != nc.feature || cg->a_norm)
             continue;
+        // with no producer to leave the statistics, a reader that runs packed
+        // takes them itself
+        bool self_stats = false;
+        if (pseg < 0) {
+            if (!packing) continue;
+            holo::GroupDesc probe = *cg;
+            probe.a = x;
+            probe.a_gamma = has_g ? nc.gamma : holo_buffer_ref{HOLO_SLOT_ABSENT, 0, 0};
+            probe.a_norm = true;
+            if (!packable_group(s, probe, is_input, is_const)) continue;
+            self_stats = true;
+        } else if (!few_row(*cg)) {
+            continue;
+        }
         {   // y read only as A
             std::vector<uint32_t> r, w;
             bool other = false;
@@ -1057,19 +1114,26 @@ int norm_fusion(holo_session *s, const std::vector<uint8_t> &is_output,
             clobbered = has_slot(W[t], x.slot) || (has_g && has_slot(W[t], nc.gamma.slot));
         if (clobbered) continue;
         // commit
-        as_group(j);
+        if (!self_stats) as_group(j);
         holo::GroupDesc *C = as_group(q);
         C->a = x;
         C->a_gamma = has_g ? nc.gamma : holo_buffer_ref{HOLO_SLOT_ABSENT, 0, 0};
         C->a_eps = eps;
-        links.push_back({nodes[j].group, pseg});
-        link_cons.push_back(nodes[q].group);
+        C->a_norm = true;
+        if (!self_stats) {
+            links.push_back({nodes[j].group, pseg});
+            link_cons.push_back(nodes[q].group);
+            node_slots(s, nodes[j], &R[j], &W[j]);
+        }
         drop[k] = true;
-        node_slots(s, nodes[j], &R[j], &W[j]);
         node_slots(s, nodes[q], &R[q], &W[q]);
         R[k].clear();
         W[k].clear();
     }
+    std::vector<Node> kept;
+    for (size_t i = 0; i < nn; ++i)
+        if (!drop[i]) kept.push_back(nodes[i]);
+    nodes.swap(kept);
     if (links.empty()) return HOLO_OK;
     // the statistics: [64 rows][4] floats per fused norm, in session memory
     // (a dry load has no device: the groups are only counted)
@@ -1088,10 +1152,6 @@ int norm_fusion(holo_session *s, const std::vector<uint8_t> &is_output,
         pgd.segs[size_t(links[f].second)].ssq = st;
         cgd.a_ssq = st;
     }
-    std::vector<Node> kept;
-    for (size_t i = 0; i < nn; ++i)
-        if (!drop[i]) kept.push_back(nodes[i]);
-    nodes.swap(kept);
     return HOLO_OK;
 }
 
@@ -1291,11 +1351,127 @@ void elide_steps(holo_session *s, const std::vector<uint8_t> &is_output,
     }
 }
 
+// Few-row bf16 groups over constant weights run as one launch
+// (gemv_packed.hip): each weight is copied once, at load, into the matrix
+// cores' operand order. A plain few-row MatMul-family call over a constant
+// weight becomes a group of one for this. A packed group that reads A through
+// a fused RmsNorm takes the row statistics itself, so its producer stops
+// writing them; a producer whose reader stays split-K keeps writing them and
+// stays split-K too (a packed launch leaves no statistics).
+int pack_weights(holo_session *s, const std::vector<uint8_t> &is_input,
+                 const std::vector<uint8_t> &is_const) {
+    auto packable = [&](const holo::GroupDesc &g) { return packable_group(s, g, is_input, is_const); };
+    // plain few-row calls over a constant weight: groups of one
+    for (auto &nd : s->nodes) {
+        if (nd.group >= 0) continue;
+        MmView mv;
+        if (!matmul_family(s->calls[nd.call], &mv) || mv.mm.b_packed) continue;
+        holo::GroupDesc g;
+        g.a = mv.mm.a;
+        g.m = mv.mm.m;
+        g.k = mv.mm.k;
+        g.dtype = mv.mm.dtype;
+        holo::GroupSegDesc d;
+        d.b = mv.mm.b;
+        d.out = mv.mm.output;
+        d.n = mv.mm.n;
+        d.base = mv.base;
+        d.act = mv.act;
+        d.residual = mv.residual;
+        g.segs.push_back(d);
+        if (!packable(g)) continue;
+        s->groups.push_back(std::move(g));
+        nd.group = int(s->groups.size() - 1);
+    }
+    std::vector<uint8_t> live(s->groups.size(), 0);
+    for (const auto &nd : s->nodes)
+        if (nd.group >= 0) live[size_t(nd.group)] = 1;
+    for (size_t i = 0; i < s->groups.size(); ++i) s->groups[i].packed = live[i] && packable(s->groups[i]);
+    // fused norms: (producer group, segment) -> consumer group, by the shared
+    // statistics buffer
+    struct Link {
+        size_t p, seg, c;
+    };
+    std::vector<Link> links;
+    for (size_t c = 0; c < s->groups.size(); ++c) {
+        if (!s->groups[c].a_ssq) continue;
+        for (size_t p = 0; p < s->groups.size(); ++p)
+            for (size_t t = 0; t < s->groups[p].segs.size(); ++t)
+                if (s->groups[p].segs[t].ssq == s->groups[c].a_ssq) links.push_back({p, t, c});
+    }
+    for (bool changed = true; changed;) {
+        changed = false;
+        for (const auto &l : links)
+            if (!s->groups[l.c].packed && s->groups[l.p].packed) {
+                s->groups[l.p].packed = false;
+                changed = true;
+            }
+    }
+    for (const auto &l : links)
+        if (s->groups[l.c].packed) s->groups[l.p].segs[l.seg].ssq = nullptr;
+    for (size_t i = 0; i < s->groups.size(); ++i)
+        if (live[i] && s->groups[i].a_norm && !s->groups[i].a_ssq && s->be && !s->groups[i].packed)
+            return set_error(HOLO_ERR_INIT, "session_load: a fused RmsNorm's reader cannot run packed");
+    // the tile width each packed group's weights take
+    for (auto &g : s->groups) {
+        if (!g.packed) continue;
+        holo::EpiSeg es[holo::kSkinnyMaxSeg];
+        for (size_t i = 0; i < g.segs.size(); ++i) {
+            es[i].n = g.segs[i].n;
+            es[i].head_dim = g.segs[i].head_dim;
+            es[i].skip = g.segs[i].skip;
+        }
+        g.packed_tw = holo::packed_tile_width(g.m, g.k, es, int(g.segs.size()));
+    }
+    if (!s->be) return HOLO_OK;   // a dry load: decided, nothing to copy
+    // one fragment-order copy per distinct weight and tile width
+    auto seg_tw = [](const holo::GroupDesc &g, const holo::GroupSegDesc &d) {
+        return d.head_dim ? 16u : g.packed_tw;
+    };
+    std::map<std::tuple<uint32_t, uint64_t, uint32_t, uint32_t, uint32_t>, uint64_t> at;
+    uint64_t total = 0;
+    for (const auto &g : s->groups) {
+        if (!g.packed) continue;
+        for (const auto &d : g.segs) {
+            const auto key = std::make_tuple(d.b.slot, d.b.offset, g.k, d.n, seg_tw(g, d));
+            if (at.count(key)) continue;
+            at[key] = total;
+            total += (holo::packed_b_bytes(g.k, d.n, seg_tw(g, d)) + 255) / 256 * 256;
+        }
+    }
+    if (total == 0) return HOLO_OK;
+    if (hipMalloc(&s->packed_arena, total) != hipSuccess) {
+        (void)hipGetLastError();
+        s->packed_arena = nullptr;
+        return set_error(HOLO_ERR_INIT, "session_load: device allocation failed (packed weights, " +
+                                            std::to_string(total) + " bytes)");
+    }
+    s->packed_bytes = total;
+    uint8_t *base = static_cast<uint8_t *>(s->packed_arena);
+    for (const auto &kv : at) {
+        const uint32_t slot = std::get<0>(kv.first);
+        const uint64_t off = std::get<1>(kv.first);
+        if (holo::launch_pack_b(s->owned[slot].ptr + off, base + kv.second, std::get<2>(kv.first),
+                                std::get<3>(kv.first), std::get<4>(kv.first), s->stream) != hipSuccess) {
+            (void)hipGetLastError();
+            return set_error(HOLO_ERR_INIT, "session_load: weight packing launch failed");
+        }
+    }
+    if (hipStreamSynchronize(s->stream) != hipSuccess)
+        return set_error(HOLO_ERR_INIT, "session_load: weight packing failed");
+    for (auto &g : s->groups) {
+        if (!g.packed) continue;
+        for (auto &d : g.segs) d.bp = base + at[std::make_tuple(d.b.slot, d.b.offset, g.k, d.n, seg_tw(g, d))];
+    }
+    return HOLO_OK;
+}
+
 void release(holo_session *s) {
     if (!s) return;
     if (s->stream) (void)hipStreamSynchronize(s->stream);
     if (s->graph) (void)hipGraphExecDestroy(s->graph);
     if (s->norm_arena) (void)hipFree(s->norm_arena);
+    if (s->packed_arena) (void)hipFree(s->packed_arena);
     if (s->scratch) (void)hipFree(s->scratch);
     if (s->const_arena) (void)hipFree(s->const_arena);
     if (s->work_arena) (void)hipFree(s->work_arena);
@@ -1650,11 +1826,16 @@ plan_moves:
     } else {
         device_fusion(s.get(), is_output, is_input);
         if (!(flags & HOLO_SESSION_NO_NORM_FUSION)) {
-            const int rc = norm_fusion(s.get(), is_output, is_input);
+            const int rc = norm_fusion(s.get(), is_output, is_input, is_const,
+                                       !(flags & HOLO_SESSION_NO_WEIGHT_PACKING));
             if (rc != HOLO_OK) return rc;
         }
     }
     elide_steps(s.get(), is_output, is_input, is_const);
+    if (!(flags & (HOLO_SESSION_NO_DEVICE_FUSION | HOLO_SESSION_NO_WEIGHT_PACKING))) {
+        const int rc = pack_weights(s.get(), is_input, is_const);
+        if (rc != HOLO_OK) return rc;
+    }
     *out = s.release();
     return HOLO_OK;
 }
@@ -1739,6 +1920,18 @@ int holo_hip_session_call(const holo_session *s, uint32_t index, holo_kernel_cal
     if (index >= s->calls.size())
         return set_error(HOLO_ERR_SLOT_OUT_OF_RANGE, "session_call: index past the loaded calls");
     *out = s->calls[index];
+    return HOLO_OK;
+}
+
+int holo_hip_session_packed(const holo_session *s, uint32_t *groups, uint64_t *bytes) {
+    if (!s) return set_error(HOLO_ERR_INIT, "session_packed: null session");
+    uint32_t n = 0;
+    std::vector<uint8_t> live(s->groups.size(), 0);
+    for (const auto &nd : s->nodes)
+        if (nd.group >= 0) live[size_t(nd.group)] = 1;
+    for (size_t i = 0; i < s->groups.size(); ++i) n += live[i] && s->groups[i].packed;
+    if (groups) *groups = n;
+    if (bytes) *bytes = s->packed_bytes;
     return HOLO_OK;
 }
 

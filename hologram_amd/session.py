@@ -29,13 +29,14 @@ NO_EPILOGUE_FUSION = 1   # skip the reference loader's fuse_matmul_epilogue
 NO_DEVICE_FUSION = 2     # skip this backend's grouped few-row MatMuls and epilogues
 NO_NORM_FUSION = 4       # keep each RmsNorm between few-row MatMuls as its own launch
 NO_DEQUANT_FUSION = 8    # skip the loader's fuse_dequant_matmul / fuse_dequant_activation
+NO_WEIGHT_PACKING = 16   # keep few-row groups over constant weights on the split-K launches
 
 
 class HipSession:
     """`backend=None` loads dry: parse, size and validate every call on the host,
     with no device (such a session reports ports and refuses to execute).
     `flags` turns the load-time fusions off (NO_EPILOGUE_FUSION, NO_DEVICE_FUSION,
-    NO_NORM_FUSION, NO_DEQUANT_FUSION);
+    NO_NORM_FUSION, NO_DEQUANT_FUSION, NO_WEIGHT_PACKING);
     fused and unfused walks give the same bits."""
 
     def __init__(self, backend: HipBackend | None, archive: bytes, flags: int = 0):
@@ -154,6 +155,14 @@ class HipSession:
         d, k = ctypes.c_uint32(), ctypes.c_uint32()
         _check(self._lib.holo_hip_session_last_walk(self.handle, ctypes.byref(d), ctypes.byref(k)))
         return d.value, k.value
+
+    @property
+    def packed(self) -> tuple[int, int]:
+        """(groups run as one launch over packed weights, bytes of the packed
+        weight copies)."""
+        g, b = ctypes.c_uint32(), ctypes.c_uint64()
+        _check(self._lib.holo_hip_session_packed(self.handle, ctypes.byref(g), ctypes.byref(b)))
+        return g.value, b.value
 
     def set_memo(self, enabled: bool) -> None:
         """The memo's hits on (default) or off (every execute walks)."""

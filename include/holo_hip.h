@@ -554,11 +554,18 @@ int holo_hip_session_load(holo_backend *be, const uint8_t *archive, size_t len,
  * reads it, and the norm's own launch and output go away. All of these give
  * the same bits as the unfused walk; the flags turn them off
  * (NO_DEVICE_FUSION also turns off the norm fusion; NO_DEQUANT_FUSION the two
- * dequant passes). */
+ * dequant passes). A bf16 group of at most 16 rows whose weights are
+ * constants of the archive runs as one launch: at load each such weight is
+ * copied once into the matrix cores' operand order (the archive's own copy
+ * stays), a workgroup owns a 16-column tile (a SwiGLU tile pair, a head) over
+ * the whole of K, and a fused RmsNorm's statistics are taken in that launch;
+ * the few-row product's summation order is fixed by K alone, so this too is
+ * bit-identical. NO_WEIGHT_PACKING keeps the split-K launches. */
 #define HOLO_SESSION_NO_EPILOGUE_FUSION 1u
 #define HOLO_SESSION_NO_DEVICE_FUSION 2u
 #define HOLO_SESSION_NO_NORM_FUSION 4u
 #define HOLO_SESSION_NO_DEQUANT_FUSION 8u
+#define HOLO_SESSION_NO_WEIGHT_PACKING 16u
 int holo_hip_session_load_ex(holo_backend *be, const uint8_t *archive, size_t len, uint32_t flags,
                              holo_session **out);
 /* Steps of one walk after fusion (each a call or a fused MatMul group), and
@@ -571,6 +578,10 @@ int holo_hip_session_nodes(const holo_session *s, uint32_t *n_nodes, uint32_t *n
  * the steps a memo-on holo_hip_session_execute_bytes found unchanged since
  * the previous walk, and every step on a whole-graph memo hit. */
 int holo_hip_session_last_walk(const holo_session *s, uint32_t *dispatched, uint32_t *skipped);
+/* Fused groups that run as one launch over packed weights, and the device
+ * bytes the packed copies of their weights hold (no counterpart in the
+ * reference: its CPU kernels read weights in place). */
+int holo_hip_session_packed(const holo_session *s, uint32_t *groups, uint64_t *bytes);
 /* The index-th kernel call of the loaded schedule, after the reference's
  * loader passes (the calls the reference's Session counts with
  * dequant_fused_count and its siblings, session.rs:1390-1437). */

@@ -18,7 +18,8 @@ from hologram_amd import (DTYPE_BF16, DTYPE_F32, BinaryCall, BufferRef, HipSessi
                           MatMulAddCall, MatMulCall, NormCall, PortDescriptor, SlotOutOfRange, UnaryCall,
                           UnsupportedOp, decode_call, fused_activation, validate)
 from hologram_amd.decoder_graph import DecoderConfig, build_decode_step, init_weights
-from hologram_amd.session import NO_DEVICE_FUSION, NO_EPILOGUE_FUSION, NO_NORM_FUSION
+from hologram_amd.session import (NO_DEVICE_FUSION, NO_EPILOGUE_FUSION, NO_NORM_FUSION,
+                                  NO_WEIGHT_PACKING)
 
 M, K, N = 4, 64, 32
 
@@ -136,12 +137,23 @@ def test_decoder_walk_counts():
     # per layer: RmsNorm, {q,k,v + 2 RoPE + 2 appends}, attention, Wo+Add, RmsNorm,
     # {gate+Silu, up, Mul}, Wd+Add
     assert full.n_calls == 1 + 15 * L + 3
-    grouped = HipSession(None, a, flags=NO_NORM_FUSION)
+    grouped = HipSession(None, a, flags=NO_NORM_FUSION | NO_WEIGHT_PACKING)
     assert grouped.n_nodes == 1 + 7 * L + 3 and grouped.n_groups == 2 * L
+    # with packing, the plain few-row MatMuls over constant weights (Wo+Add,
+    # Wd+Add, the LM head) run as groups of one
+    packed = HipSession(None, a, flags=NO_NORM_FUSION)
+    assert packed.n_nodes == 1 + 7 * L + 3 and packed.n_groups == 4 * L + 1
+    assert packed.packed[0] == 4 * L + 1
     # the norms after Wo+Add and Wd+Add (the next layer's, or the final one)
     # split between producer and reader: Wo+Add, Wd+Add and the LM head become
-    # groups of one; only layer 0's input norm (after the embedding) remains
-    assert full.n_nodes == 1 + 5 * L + 3 and full.n_groups == 4 * L + 1
+    # groups of one; layer 0's input norm (after the embedding) stays on its
+    # own when the weights are not packed
+    split = HipSession(None, a, flags=NO_WEIGHT_PACKING)
+    assert split.n_nodes == 1 + 5 * L + 3 and split.n_groups == 4 * L + 1
+    assert split.packed[0] == 0
+    # packed, the q/k/v group takes layer 0's norm statistics itself
+    assert full.n_nodes == 5 * L + 3 and full.n_groups == 4 * L + 1
+    assert full.packed[0] == 4 * L + 1
 
 
 def norm(x, g, o, rows, feat, dt=DTYPE_BF16):

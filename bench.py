@@ -62,6 +62,8 @@ def parse():
     p.add_argument("--only", default="attn,lut,copy,kv,gemm,w8a8,e2e")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--seed", type=int, default=1234)
+    p.add_argument("--e2e-flags", type=int, default=0,
+                   help="HOLO_SESSION_* load flags of config 5's decode session (A/B of the fusions)")
     return p.parse_args()
 
 
@@ -485,7 +487,7 @@ def bench_e2e(torch, be, args, rep):
     t_build = time.perf_counter() - t0
     t0 = time.perf_counter()
     pre = HipSession(be, pre_archive)
-    dec = HipSession(be, dec_archive)
+    dec = HipSession(be, dec_archive, flags=args.e2e_flags)
     t_load = time.perf_counter() - t0
     archive_bytes = len(dec_archive)
     del pre_archive
@@ -514,12 +516,22 @@ def bench_e2e(torch, be, args, rep):
     tptr, tbytes = dec.output_ptr(0)
     tok = torch.as_tensor(_DevBytes(tptr, tbytes), device="cuda").view(torch.int32)
     dec.bind_input(0, (tptr, tbytes))
-    bufs = [torch.empty(1, dtype=torch.int32, device="cuda"),
-            torch.empty(B, dtype=torch.int32, device="cuda"),
-            torch.empty_like(cq[0]), torch.empty_like(sq[0]), torch.empty_like(ck[0]),
-            torch.empty_like(sk[0])]
-    for i, t in enumerate(bufs):
-        dec.bind_input(1 + i, t)
+    # the step's position, lengths and rotary rows, as one row per position of
+    # one table: a step's inputs are one device copy into one staging row, the
+    # session's six input ports bound to 256-byte aligned views of it
+    parts = [pos_tab.view(torch.uint8).view(npos, -1), lens_tab.view(torch.uint8).view(npos, -1),
+             cq.view(torch.uint8).view(npos, -1), sq.view(torch.uint8).view(npos, -1),
+             ck.view(torch.uint8).view(npos, -1), sk.view(torch.uint8).view(npos, -1)]
+    widths = [x.shape[1] for x in parts]
+    offs = [0]
+    for wdt in widths:
+        offs.append(offs[-1] + (wdt + 255) // 256 * 256)
+    table = torch.zeros((npos, offs[-1]), dtype=torch.uint8, device="cuda")
+    for o, wdt, x in zip(offs, widths, parts):
+        table[:, o:o + wdt] = x
+    staging = torch.zeros(offs[-1], dtype=torch.uint8, device="cuda")
+    for i, (o, wdt) in enumerate(zip(offs, widths)):
+        dec.bind_input(1 + i, staging[o:o + wdt])
     ext_pre = torch.cuda.ExternalStream(pre.stream())
     ext = torch.cuda.ExternalStream(dec.stream())
     torch.cuda.synchronize()
@@ -540,8 +552,7 @@ def bench_e2e(torch, be, args, rep):
 
     def set_step(p):
         with torch.cuda.stream(ext):
-            for dst, src in zip(bufs, (pos_tab[p], lens_tab[p], cq[p], sq[p], ck[p], sk[p])):
-                dst.copy_(src, non_blocking=True)
+            staging.copy_(table[p], non_blocking=True)
 
     # ---- decode: the prompt pass's greedy token at position 512 (the eager
     # step inside the capture), then 256 timed replays at 513 .. 768

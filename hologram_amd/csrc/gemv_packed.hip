@@ -125,62 +125,51 @@ __device__ __forceinline__ void gemv_packed_body(const PackedArgs &g) {
     const KSeg pr = &ka->seg[pi];
     const uint32_t head_dim = sg->head_dim;
     const uint32_t n = sg->n;
-    // B. A head-wise unit: the head's tiles, consecutive blocks of one
-    // segment (rb0). An element-wise unit: tpu consecutive tiles (rb0); for a
-    // pair, the up segment's tiles at the same columns follow (rb1). Tiles
-    // past the unit or the segment fall past the ranges.
-    // An element-wise tile of 8 columns is a 512-byte block a step (lanes q <
-    // 8 of the MFMA's B operand; the others read zero).
-    const uint32_t tpu = head_dim ? 0u : g.tpu;
-    const uint32_t tw = head_dim ? 16u : g.tw, blk = tw * 64u;   // columns, bytes a block
+    // A rotary head-wise segment runs in 16-column rope tiles: its weights are
+    // packed so that tile column q < 8 is head element 8t + q and q >= 8 its
+    // rotate-half partner 8t + q - 8 + D/2, so the pair meets in lanes q and
+    // q ^ 8 of one workgroup.
+    const bool rtile = head_dim != 0;
+    // B: tpu consecutive tiles of the segment (rb0); for a pair, the up
+    // segment's tiles at the same columns follow (rb1). Tiles past the unit or
+    // the segment fall past the ranges. An element-wise tile of 8 columns is a
+    // 512-byte block a step (lanes q < 8 of the MFMA's B operand; the others
+    // read zero).
+    const uint32_t tpu = rtile ? 1u : g.tpu;
+    const uint32_t tw = rtile ? 16u : g.tw, blk = tw * 64u;      // columns, bytes a block
     const uint32_t ts = S * blk;                                   // bytes a tile
-    const uint32_t first = head_dim ? unit * (head_dim / 16) : unit * tpu;
+    const uint32_t first = unit * tpu;
     const uint32_t left = n / tw - first;                          // the segment's tiles from `first`
-    const uint32_t own = head_dim ? head_dim / 16 : (left < tpu ? left : tpu);
+    const uint32_t own = left < tpu ? left : tpu;
     const auto rb0 = rsrc(reinterpret_cast<const uint8_t *>(ka->bp[si]) + uint64_t(first) * ts, own * ts);
     const auto rb1 = rsrc(reinterpret_cast<const uint8_t *>(ka->bp[pi]) + uint64_t(first) * ts,
                           pair >= 0 ? own * ts : 0u);
     const bool qin = uint32_t(q) < tw;                              // this lane's column is in the tile
     const auto ra = rsrc(g.a, M * K * 2u);   // rows >= M read zero
 
-    // (1) the epilogue's side operands. Element-wise unit: wave t < own
-    // finishes tile `first + t`, lane (grp, q) holding rows 4grp + i at its
-    // column q. Head-wise unit: thread (m, d) holds the rotate-half pair
-    // (d, d + D/2) of row m.
+    // (1) the epilogue's side operands: wave t < own finishes tile `first +
+    // t`, lane (grp, q) holding rows 4grp + i at its column ecol (a rope
+    // tile's columns are the head's pairs, see above). ra_: the residual; rb_:
+    // the pair's residual, or a rope tile's cos; rs_: a rope tile's sin (a
+    // rope tile has no pair).
     const EpiSeg vf = value_form(sg), pf = value_form(pr);
-    float ra_[4] = {}, rb_[4] = {};
+    const uint32_t rt_h = rtile ? unit / (head_dim / 16) : 0, rt_t = rtile ? unit % (head_dim / 16) : 0;
+    const uint32_t ecol = rtile ? rt_h * head_dim + 8 * rt_t + (q < 8 ? uint32_t(q) : uint32_t(q) - 8 + head_dim / 2)
+                                : tw * (first + uint32_t(w)) + uint32_t(q);
+    float ra_[4] = {}, rb_[4] = {}, rs_[4] = {};
     {
-        const bool mine = head_dim == 0 && uint32_t(w) < own && qin;
+        const bool mine = uint32_t(w) < own && qin;
         const auto rra = opt_rsrc(sg->residual, has_residual(vf) && mine);
-        const auto rrb = opt_rsrc(pr->residual, pair >= 0 && has_residual(pf) && mine);
-        const uint32_t col = tw * (first + uint32_t(w)) + uint32_t(q);
+        const auto rrb = rtile ? opt_rsrc(sg->cos, mine) : opt_rsrc(pr->residual, pair >= 0 && has_residual(pf) && mine);
+        const auto rrs = opt_rsrc(sg->sin, rtile && mine);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t m = 4 * grp + i;
-            const uint64_t e = m < M && qin ? uint64_t(m) * n + col : uint64_t(kNoLoad) / 2;
+            const uint64_t e = m < M && qin ? uint64_t(m) * n + ecol : uint64_t(kNoLoad) / 2;
             ra_[i] = opt_load<true>(rra, e);
             rb_[i] = opt_load<true>(rrb, e);
+            rs_[i] = opt_load<true>(rrs, e);
         }
-    }
-    const uint32_t D = head_dim ? head_dim : 2, half = D / 2;
-    const uint32_t hm = threadIdx.x / half, d = threadIdx.x % half;
-    const bool hlive = hm < M;
-    const uint32_t mrow = hlive ? hm : M - 1;
-    const uint64_t e1 = uint64_t(mrow) * n + unit * D + d;
-    const bool rope = sg->rope, quant = sg->quant;
-    float c1v = 0.f, s1v = 0.f, c2v = 0.f, s2v = 0.f, r1 = 0.f, r2 = 0.f;
-    uint32_t pos = 0;
-    {
-        const bool hw = head_dim != 0;
-        const auto rc = opt_rsrc(sg->cos, hw && rope), rs = opt_rsrc(sg->sin, hw && rope);
-        const auto rr = opt_rsrc(sg->residual, hw && has_residual(vf));
-        c1v = opt_load<true>(rc, e1);
-        s1v = opt_load<true>(rs, e1);
-        c2v = opt_load<true>(rc, e1 + half);
-        s2v = opt_load<true>(rs, e1 + half);
-        r1 = opt_load<true>(rr, e1);
-        r2 = opt_load<true>(rr, e1 + half);
-        pos = __builtin_amdgcn_raw_buffer_load_b32(rsrc(sg->pos, hw && quant ? 4u : 0u), 0u, 0, 0);
     }
 
     // (2) A. Staged: thread tau = 256p + t of pass p holds the vectors
@@ -193,14 +182,12 @@ __device__ __forceinline__ void gemv_packed_body(const PackedArgs &g) {
     const uint32_t t256 = threadIdx.x & 255, r0 = threadIdx.x >> 8;
     u32x4 xv[LDSA ? kPass : 1][kVec], gv[LDSA && NORM ? kVec : 1];
     u32x4 a[LDSA ? 1 : 4][SPC];
-    constexpr int kSplitA = !LDSA && SPC >= 4 ? 2 : 4;   // direct: chains whose A goes out first
-    auto load_a = [&](int c0, int c1) {
+    auto load_a = [&]() {
         if constexpr (!LDSA) {
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc)
 #pragma unroll
                 for (int i = 0; i < SPC; ++i) {
-                    if (cc < c0 || cc >= c1) continue;
                     const uint32_t s = uint32_t(4 * w + cc) + 64 * i;
                     a[cc][i] = __builtin_amdgcn_raw_buffer_load_b128(
                         ra, s < S ? (q * K + 32 * s + 8 * grp) * 2u : kNoLoad, 0, 0);
@@ -225,7 +212,7 @@ __device__ __forceinline__ void gemv_packed_body(const PackedArgs &g) {
             }
         }
     } else {
-        load_a(0, kSplitA);
+        load_a();
     }
     // (3) B at this wave's steps
     u32x4 b[4][SPC][NT];
@@ -310,13 +297,6 @@ __device__ __forceinline__ void gemv_packed_body(const PackedArgs &g) {
     f32x4 grp_sum[NT];
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) {
-        if constexpr (kSplitA < 4) {
-            if (cc == kSplitA) {
-                __builtin_amdgcn_sched_barrier(0);
-                load_a(kSplitA, 4);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
         u32x4 av[SPC];
 #pragma unroll
         for (int i = 0; i < SPC; ++i) {
@@ -349,7 +329,7 @@ __device__ __forceinline__ void gemv_packed_body(const PackedArgs &g) {
 
     // (6) the groups added in order, then the epilogue
     const uint32_t groups = S / 4 + (S % 4 != 0), G = groups > 16 ? 16 : groups;
-    if (head_dim == 0) {
+    {
         // wave t < own: tile `first + t` (and its up tile at t + tpu)
         if (uint32_t(w) >= own) return;
         const uint32_t wt = uint32_t(w) < NT ? uint32_t(w) : 0;
@@ -359,12 +339,27 @@ __device__ __forceinline__ void gemv_packed_body(const PackedArgs &g) {
             va += red[v][wt][lane];
             if (pair >= 0) vb += red[v][tu][lane];
         }
-        const uint32_t col = tw * (first + uint32_t(w)) + uint32_t(q);
+        if (rtile) {
+            // rotate-half: y = x c - x' s (first half), x c + x' s (second),
+            // x' the partner in lane q ^ 8, as the standalone rotary kernel
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t m = 4 * grp + i;
+                const float x = base_value<true>(vf, va[i], ra_[i]);
+                const float xp = __shfl_xor(x, 8, 64);
+                const float y = bf2f(f2bf(q < 8 ? x * rb_[i] - xp * rs_[i] : x * rb_[i] + xp * rs_[i]));
+                if (m >= M) continue;
+                const uint64_t e = uint64_t(m) * n + ecol;
+                if (sg->out) store<true>(sg->out, e, x);
+                if (sg->rope_out) store<true>(sg->rope_out, e, y);
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t m = 4 * grp + i;
             if (m >= M || !qin) continue;
-            const uint64_t e = uint64_t(m) * n + col;
+            const uint64_t e = uint64_t(m) * n + ecol;
             const float xa = base_value<true>(vf, va[i], ra_[i]);
             if (sg->out) store<true>(sg->out, e, xa);
             if (pair >= 0) {
@@ -375,68 +370,6 @@ __device__ __forceinline__ void gemv_packed_body(const PackedArgs &g) {
         }
         return;
     }
-
-    // head-wise: each tile's sum (wave t < own) into LDS as a [16 rows][D] f32
-    // tile over the first group's slot, then thread (m, d) finishes its pair
-    f32x4 fin = f32x4{0.f, 0.f, 0.f, 0.f};
-    const uint32_t wt = uint32_t(w) < own && uint32_t(w) < NT ? uint32_t(w) : 0;
-    if (uint32_t(w) < own) {
-        fin = red[0][wt][lane];
-        for (uint32_t v = 1; v < G; ++v) fin += red[v][wt][lane];
-    }
-    __syncthreads();
-    float *tile = reinterpret_cast<float *>(&red[0][0][0]);   // [16][D]
-    if (uint32_t(w) < own)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) tile[(4 * grp + i) * D + 16 * wt + q] = fin[i];
-    __syncthreads();
-    float x1 = base_value<true>(vf, tile[mrow * D + d], r1);
-    float x2 = base_value<true>(vf, tile[mrow * D + d + half], r2);
-    if (hlive) {
-        if (sg->out) {
-            store<true>(sg->out, e1, x1);
-            store<true>(sg->out, e1 + half, x2);
-        }
-        if (rope) {
-            const float y1 = bf2f(f2bf(x1 * c1v - x2 * s1v));
-            const float y2 = bf2f(f2bf(x2 * c2v + x1 * s2v));
-            x1 = y1;
-            x2 = y2;
-            if (sg->rope_out) {
-                store<true>(sg->rope_out, e1, x1);
-                store<true>(sg->rope_out, e1 + half, x2);
-            }
-        }
-    }
-    if (!quant) return;
-    // row max of |x| over the head's lanes (NaN never wins a `>`); exact, so
-    // the order of the reduction does not matter
-    float amax = 0.0f;
-    const float a1 = x1 < 0.0f ? -x1 : x1, a2 = x2 < 0.0f ? -x2 : x2;
-    if (a1 > amax) amax = a1;
-    if (a2 > amax) amax = a2;
-    for (uint32_t off = half / 2; off >= 1; off >>= 1) {
-        const float o = __shfl_xor(amax, int(off), 64);
-        if (o > amax) amax = o;
-    }
-    if (!hlive) return;
-    const uint64_t r = e1 / D;   // the row of the appended [planes, new_rows, D] block
-    const uint32_t new_rows = sg->new_rows, bucket = sg->bucket;
-    const uint32_t plane = uint32_t(r / new_rows), j = uint32_t(r % new_rows);
-    const uint64_t row = uint64_t(plane) * bucket + (uint64_t(pos % bucket) + j) % bucket;
-    int8_t *dst = sg->cq + row * D;
-    float *cs = sg->cs;
-    if (amax == 0.0f) {
-        dst[d] = 0;
-        dst[d + half] = 0;
-        if (d == 0) cs[row] = 0.0f;
-        return;
-    }
-    const float iv = 127.0f / amax;
-    const float t1 = x1 * iv, t2 = x2 * iv;
-    dst[d] = to_q(t1 >= 0.0f ? truncf(t1 + 0.5f) : truncf(t1 - 0.5f));
-    dst[d + half] = to_q(t2 >= 0.0f ? truncf(t2 + 0.5f) : truncf(t2 - 0.5f));
-    if (d == 0) cs[row] = amax / 127.0f;
 }
 
 // One workgroup of sixteen waves per CU at a time, or two (at most 64
@@ -453,10 +386,11 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8, 8))) vo
 
 // B [K, N] row-major -> fragment order; one 16-byte block lane per thread.
 // Tile width tw = 16: block (j, s) is 64 lanes (grp, q) holding B[32s + 8grp
-// + e][16j + q]; tw = 8: 32 lanes (grp, q < 8) holding B[32s + 8grp + e][8j + q].
+// + e][16j + q]; tw = 8: 32 lanes (grp, q < 8) holding B[32s + 8grp + e][8j + q];
+// rope_d > 0 (tw 16): the columns of rope tiles over heads of rope_d.
 __global__ __launch_bounds__(256) void pack_b_kernel(const uint16_t *__restrict__ B,
                                                      uint8_t *__restrict__ Bp, uint32_t K, uint32_t N,
-                                                     uint32_t tw) {
+                                                     uint32_t tw, uint32_t rope_d) {
     const uint32_t S = K / 32, lanes = 4 * tw;
     const uint64_t ts = uint64_t(S) * tw * 64;
     const uint64_t total = uint64_t(N / tw) * S * lanes;
@@ -465,7 +399,12 @@ __global__ __launch_bounds__(256) void pack_b_kernel(const uint16_t *__restrict_
         const uint32_t ln = uint32_t(idx % lanes), grp = ln / tw, q = ln % tw;
         const uint64_t js = idx / lanes;
         const uint64_t s = js % S, j = js / S;
-        const uint64_t col = uint64_t(tw) * j + q, row0 = 32 * s + 8 * grp;
+        // rope_d: tile j is rope tile t of head h, its columns the head's
+        // elements 8t + q (q < 8) and their rotate-half partners
+        const uint64_t hj = rope_d ? j / (rope_d / 16) : 0, tj = rope_d ? j % (rope_d / 16) : 0;
+        const uint64_t col = rope_d ? hj * rope_d + 8 * tj + (q < 8 ? q : q - 8 + rope_d / 2)
+                                    : uint64_t(tw) * j + q;
+        const uint64_t row0 = 32 * s + 8 * grp;
         u32x4 o;
 #pragma unroll
         for (int h = 0; h < 4; ++h)
@@ -481,12 +420,12 @@ __global__ __launch_bounds__(256) void pack_b_kernel(const uint16_t *__restrict_
 // units.
 uint32_t packed_unit_tiles(const EpiSeg &s, uint32_t tpu) {
     if (s.skip) return 0;
-    if (s.head_dim) return s.head_dim / 16;
+    if (s.head_dim) return 1;   // a rope tile
     return s.pair >= 0 ? 2 * tpu : tpu;
 }
 uint32_t packed_units(const EpiSeg &s, uint32_t tpu, uint32_t tw) {
     if (s.skip) return 0;
-    if (s.head_dim) return s.n / s.head_dim;
+    if (s.head_dim) return s.n / 16;
     return (s.n / tw + tpu - 1) / tpu;
 }
 
@@ -499,29 +438,33 @@ bool packed_group_applies(uint32_t m, uint32_t k, const EpiSeg *segs, int nseg, 
         return false;
     // the norm is taken on the LDS copy of A
     if (norm && packed_lds_bytes(m, k) > kMaxDynLds) return false;
-    const uint32_t spc = (k / 32 + 63) / 64;
-    const uint32_t spc_t = spc <= 1 ? 1 : spc <= 2 ? 2 : 4;
-    if (uint64_t(m) * k * 2 >= (1ull << 31)) return false;
-    uint32_t units = 0;
+    // Where a workgroup owning all of K loses to the split-K launch and its
+    // epilogue (measured per decode shape on one box, weights streamed from
+    // HBM): K beyond 4096 (Wd, 8192 x 2048: 12.2 against 11.5 us), more than
+    // 1024 sixteen-column tiles (an LM head of 32000 columns: 35.9 against
+    // 34.1 us), and the int8 append, whose row maximum needs a whole head in
+    // one workgroup (q/k/v: 11.3 against 9.7 us). It wins where the
+    // epilogue's launch is a large share: Wo + residual 6.5 against 7.7 us,
+    // gate/up + SwiGLU 20.4 against 21.3 us.
+    if (k > 4096 || uint64_t(m) * k * 2 >= (1ull << 31)) return false;
+    uint32_t units = 0, tiles = 0;
     for (int i = 0; i < nseg; ++i) {
         const EpiSeg &s = segs[i];
         if (s.n == 0 || s.n % 8 != 0 || uint64_t(k) * s.n * 2 >= (1ull << 31) ||
-            uint64_t(m) * s.n * 2 >= (1ull << 31))
+            uint64_t(m) * s.n * 2 >= (1ull << 31) || s.quant)
             return false;
-        if (s.head_dim) {
-            if (!(s.head_dim == 16 || s.head_dim == 32 || s.head_dim == 64 || s.head_dim == 128) ||
+        if (s.head_dim) {   // rope tiles
+            if (!s.rope || !(s.head_dim == 16 || s.head_dim == 32 || s.head_dim == 64 || s.head_dim == 128) ||
                 s.n % s.head_dim != 0 || s.pair >= 0)
                 return false;
-            if (s.quant && (s.new_rows == 0 || s.bucket == 0)) return false;
         }
         if (s.pair >= 0) {
             if (s.pair >= nseg || s.pair == i || segs[s.pair].n != s.n || segs[s.pair].head_dim) return false;
         }
-        const uint32_t nt = packed_unit_tiles(s, 1);
-        if (nt * spc_t > 4) return false;   // registers: B of every step in flight
         units += packed_units(s, 1, 16);
+        tiles += s.n / 16 + (s.n % 16 != 0);
     }
-    return units > 0;
+    return units > 0 && tiles <= 1024;
 }
 
 hipError_t launch_packed_group(const PackedGroup &pg, hipStream_t stream) {
@@ -612,8 +555,7 @@ hipError_t launch_packed_group(const PackedGroup &pg, hipStream_t stream) {
     using C4 = std::integral_constant<int, 4>;
     if (nt <= 1) {
         if (spc_t == 1) go(C1{}, C1{});
-        else if (spc_t == 2) go(C1{}, C2{});
-        else hipLaunchKernelGGL((gemv_packed_kernel<1, 4, false, false, 1>), grid, block, 0, stream, g);
+        else go(C1{}, C2{});
     } else if (nt <= 2) {
         if (spc_t == 1) go(C2{}, C1{});
         else go(C2{}, C2{});
@@ -623,13 +565,15 @@ hipError_t launch_packed_group(const PackedGroup &pg, hipStream_t stream) {
     return hipGetLastError();
 }
 
-hipError_t launch_pack_b(const void *b, void *bp, uint32_t k, uint32_t n, uint32_t tw, hipStream_t stream) {
+hipError_t launch_pack_b(const void *b, void *bp, uint32_t k, uint32_t n, uint32_t tw, uint32_t rope_d,
+                         hipStream_t stream) {
     if (k == 0 || n == 0 || k % 32 != 0 || (tw != 8 && tw != 16) || n % tw != 0) return hipErrorInvalidValue;
+    if (rope_d && (tw != 16 || rope_d % 16 != 0 || n % rope_d != 0)) return hipErrorInvalidValue;
     const uint64_t total = uint64_t(n / tw) * (k / 32) * 4 * tw;
     uint64_t blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     hipLaunchKernelGGL(pack_b_kernel, dim3(unsigned(blocks)), dim3(256), 0, stream,
-                       static_cast<const uint16_t *>(b), static_cast<uint8_t *>(bp), k, n, tw);
+                       static_cast<const uint16_t *>(b), static_cast<uint8_t *>(bp), k, n, tw, rope_d);
     return hipGetLastError();
 }
 

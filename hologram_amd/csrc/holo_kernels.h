@@ -276,7 +276,11 @@ bool packed_group_applies(uint32_t m, uint32_t k, const EpiSeg *segs, int nseg, 
 hipError_t launch_packed_group(const PackedGroup &pg, hipStream_t stream);
 // B [k, n] row-major bf16 -> fragment order in tiles of tw = 8 or 16 columns
 // (k % 32 == 0, n % tw == 0): packed_b_bytes(k, n, tw) (= k * n * 2) bytes at bp.
-hipError_t launch_pack_b(const void *b, void *bp, uint32_t k, uint32_t n, uint32_t tw, hipStream_t stream);
+// rope_d > 0: a rotary-only head-wise segment over heads of rope_d, packed in
+// rope tiles (tile column q < 8: head element 8t + q; q >= 8: its rotate-half
+// partner), the layout the launch expects for such a segment.
+hipError_t launch_pack_b(const void *b, void *bp, uint32_t k, uint32_t n, uint32_t tw, uint32_t rope_d,
+                         hipStream_t stream);
 uint64_t packed_b_bytes(uint32_t k, uint32_t n, uint32_t tw);
 // The tile width a group's weights are packed with.
 uint32_t packed_tile_width(uint32_t m, uint32_t k, const EpiSeg *segs, int nseg);

@@ -569,6 +569,12 @@ struct holo_session {
     std::vector<Node> nodes;                      // the walk, in order
     std::vector<holo::GroupDesc> groups;          // fused few-row MatMul groups
     float *norm_arena = nullptr;                  // RmsNorm statistics of fused norms
+    // each fused norm split between groups: (producer group, its segment,
+    // consumer group)
+    struct NormLink {
+        size_t p, seg, c;
+    };
+    std::vector<NormLink> norm_links;
     void *packed_arena = nullptr;                 // weights of packed groups, fragment order
     uint64_t packed_bytes = 0;
     // split-K partials of this session's walks (few-row MatMuls, attention):
@@ -1146,6 +1152,7 @@ int norm_fusion(holo_session *s, const std::vector<uint8_t> &is_output,
         s->norm_arena = arena;
     }
     for (size_t f = 0; f < links.size(); ++f) {
+        s->norm_links.push_back({size_t(links[f].first), size_t(links[f].second), size_t(link_cons[f])});
         float *st = arena ? arena + f * 64 * 4 : nullptr;
         holo::GroupDesc &pgd = s->groups[size_t(links[f].first)];
         holo::GroupDesc &cgd = s->groups[size_t(link_cons[f])];
@@ -1387,18 +1394,8 @@ int pack_weights(holo_session *s, const std::vector<uint8_t> &is_input,
     for (const auto &nd : s->nodes)
         if (nd.group >= 0) live[size_t(nd.group)] = 1;
     for (size_t i = 0; i < s->groups.size(); ++i) s->groups[i].packed = live[i] && packable(s->groups[i]);
-    // fused norms: (producer group, segment) -> consumer group, by the shared
-    // statistics buffer
-    struct Link {
-        size_t p, seg, c;
-    };
-    std::vector<Link> links;
-    for (size_t c = 0; c < s->groups.size(); ++c) {
-        if (!s->groups[c].a_ssq) continue;
-        for (size_t p = 0; p < s->groups.size(); ++p)
-            for (size_t t = 0; t < s->groups[p].segs.size(); ++t)
-                if (s->groups[p].segs[t].ssq == s->groups[c].a_ssq) links.push_back({p, t, c});
-    }
+    // fused norms split between a producer group and its reader
+    const auto &links = s->norm_links;
     for (bool changed = true; changed;) {
         changed = false;
         for (const auto &l : links)
@@ -1428,12 +1425,14 @@ int pack_weights(holo_session *s, const std::vector<uint8_t> &is_input,
     auto seg_tw = [](const holo::GroupDesc &g, const holo::GroupSegDesc &d) {
         return d.head_dim ? 16u : g.packed_tw;
     };
-    std::map<std::tuple<uint32_t, uint64_t, uint32_t, uint32_t, uint32_t>, uint64_t> at;
+    // a rotary-only head-wise segment is packed in rope tiles
+    auto seg_rope = [](const holo::GroupSegDesc &d) { return d.head_dim && d.rope && !d.quant ? d.head_dim : 0u; };
+    std::map<std::tuple<uint32_t, uint64_t, uint32_t, uint32_t, uint32_t, uint32_t>, uint64_t> at;
     uint64_t total = 0;
     for (const auto &g : s->groups) {
         if (!g.packed) continue;
         for (const auto &d : g.segs) {
-            const auto key = std::make_tuple(d.b.slot, d.b.offset, g.k, d.n, seg_tw(g, d));
+            const auto key = std::make_tuple(d.b.slot, d.b.offset, g.k, d.n, seg_tw(g, d), seg_rope(d));
             if (at.count(key)) continue;
             at[key] = total;
             total += (holo::packed_b_bytes(g.k, d.n, seg_tw(g, d)) + 255) / 256 * 256;
@@ -1452,7 +1451,8 @@ int pack_weights(holo_session *s, const std::vector<uint8_t> &is_input,
         const uint32_t slot = std::get<0>(kv.first);
         const uint64_t off = std::get<1>(kv.first);
         if (holo::launch_pack_b(s->owned[slot].ptr + off, base + kv.second, std::get<2>(kv.first),
-                                std::get<3>(kv.first), std::get<4>(kv.first), s->stream) != hipSuccess) {
+                                std::get<3>(kv.first), std::get<4>(kv.first), std::get<5>(kv.first),
+                                s->stream) != hipSuccess) {
             (void)hipGetLastError();
             return set_error(HOLO_ERR_INIT, "session_load: weight packing launch failed");
         }
@@ -1461,7 +1461,8 @@ int pack_weights(holo_session *s, const std::vector<uint8_t> &is_input,
         return set_error(HOLO_ERR_INIT, "session_load: weight packing failed");
     for (auto &g : s->groups) {
         if (!g.packed) continue;
-        for (auto &d : g.segs) d.bp = base + at[std::make_tuple(d.b.slot, d.b.offset, g.k, d.n, seg_tw(g, d))];
+        for (auto &d : g.segs)
+            d.bp = base + at[std::make_tuple(d.b.slot, d.b.offset, g.k, d.n, seg_tw(g, d), seg_rope(d))];
     }
     return HOLO_OK;
 }

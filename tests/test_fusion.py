@@ -140,10 +140,11 @@ def test_decoder_walk_counts():
     grouped = HipSession(None, a, flags=NO_NORM_FUSION | NO_WEIGHT_PACKING)
     assert grouped.n_nodes == 1 + 7 * L + 3 and grouped.n_groups == 2 * L
     # with packing, the plain few-row MatMuls over constant weights (Wo+Add,
-    # Wd+Add, the LM head) run as groups of one
+    # Wd+Add, the LM head) run as groups of one; every group but q/k/v (the
+    # int8 appends need whole heads) runs packed
     packed = HipSession(None, a, flags=NO_NORM_FUSION)
     assert packed.n_nodes == 1 + 7 * L + 3 and packed.n_groups == 4 * L + 1
-    assert packed.packed[0] == 4 * L + 1
+    assert packed.packed[0] == 3 * L + 1
     # the norms after Wo+Add and Wd+Add (the next layer's, or the final one)
     # split between producer and reader: Wo+Add, Wd+Add and the LM head become
     # groups of one; layer 0's input norm (after the embedding) stays on its
@@ -151,9 +152,10 @@ def test_decoder_walk_counts():
     split = HipSession(None, a, flags=NO_WEIGHT_PACKING)
     assert split.n_nodes == 1 + 5 * L + 3 and split.n_groups == 4 * L + 1
     assert split.packed[0] == 0
-    # packed, the q/k/v group takes layer 0's norm statistics itself
-    assert full.n_nodes == 5 * L + 3 and full.n_groups == 4 * L + 1
-    assert full.packed[0] == 4 * L + 1
+    # packed: Wo and gate/up per layer, the last Wd and the LM head; the
+    # other Wd + Add steps write the statistics a split-K q/k/v group reads
+    assert full.n_nodes == 1 + 5 * L + 3 and full.n_groups == 4 * L + 1
+    assert full.packed[0] == 2 * L + 2
 
 
 def norm(x, g, o, rows, feat, dt=DTYPE_BF16):

@@ -425,8 +425,58 @@ def bench_gemm(torch, be, args, rep):
                 res[key]["cpu_baseline"] = cpu_gemm(keep[0], m, k, n, dt,
                                                     single=(m == 1024 or m <= 64))
             del ws, calls, keep
+    res["bf16_16x4096x4096_packed"] = bench_fewrow_packed(torch, be, args, 16, 4096, 4096)
     rep["gemm"] = res
     return res
+
+
+def bench_fewrow_packed(torch, be, args, m, k, n):
+    """The few-row bf16 MatMul with its weight a constant of a compiled graph:
+    the session packs the weight at load and runs the product as one launch
+    (gemv_packed.hip) instead of split-K plus a reduce. One archive holds
+    `nbuf` such products over different weights (rotated past the 256 MB
+    Infinity Cache), A = 2x computed in-graph; the captured walk is replayed
+    and the time per product is the replay's GPU time over nbuf (the one Add
+    included)."""
+    import numpy as np
+    from hologram_amd import (DTYPE_BF16, BinaryCall, BufferRef, ConstantEntry, HipSession, HoloWriter,
+                              KernelCall, MatMulCall, PortDescriptor)
+    nbuf = max(2, -(-(512 << 20) // (k * n * 2)))
+    rng = np.random.default_rng(args.seed + 9)
+    r = lambda slot, elems: BufferRef(slot, 0, 2 * elems)
+    w = HoloWriter()
+    w.kernel_calls = [KernelCall.Add(BinaryCall(r(0, m * k), r(0, m * k), r(1, m * k), m * k, 16, DTYPE_BF16))]
+    for i in range(nbuf):
+        wt = (rng.standard_normal(k * n, dtype=np.float32) / np.float32(np.sqrt(k))).view(np.uint32) >> 16
+        w.constants.append(ConstantEntry(2 + 2 * i, DTYPE_BF16, wt.astype(np.uint16).tobytes()))
+        w.kernel_calls.append(KernelCall.MatMul(MatMulCall(r(1, m * k), r(2 + 2 * i, k * n), r(3 + 2 * i, m * n),
+                                                           m, k, n, DTYPE_BF16)))
+        w.outputs.append(PortDescriptor(f"y{i}", 3 + 2 * i, m * n, DTYPE_BF16, [m, n]))
+    w.inputs = [PortDescriptor("x", 0, m * k, DTYPE_BF16, [m, k])]
+    sess = HipSession(be, w.finish())
+    packed = sess.packed[0]
+    x = (rng.standard_normal(m * k, dtype=np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    sess.write_input(0, x.tobytes())
+    sess.capture()
+    sess.synchronize()
+    ext = torch.cuda.ExternalStream(sess.stream())
+    reps = max(3, args.steps)
+    for _ in range(2):
+        sess.replay()
+    sess.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    with torch.cuda.stream(ext):
+        ev[0].record()
+    for _ in range(reps):
+        sess.replay()
+    with torch.cuda.stream(ext):
+        ev[1].record()
+    sess.synchronize()
+    us = ev[0].elapsed_time(ev[1]) * 1e3 / (reps * nbuf)
+    gbs = (m * k + k * n + m * n) * 2 / (us / 1e6) / 1e9
+    sess.close()
+    return {"us": us, "launches_per_product": 1, "packed_groups": packed,
+            "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s", None)}
 
 
 def cpu_gemm(ab, m, k, n, dt, single):
@@ -803,7 +853,9 @@ def compact_components(rep):
     if "gemm" in rep:
         g = {}
         for k, v in rep["gemm"].items():
-            g[k] = {"us": v["ms"] * 1e3, "roofline": v["roofline"]}
+            g[k] = {"us": v["ms"] * 1e3 if "ms" in v else v["us"], "roofline": v["roofline"]}
+            if "launches_per_product" in v:
+                g[k]["launches_per_product"] = v["launches_per_product"]
             if "cpu_baseline" in v:
                 g[k]["cpu_baseline"] = v["cpu_baseline"]
         comps["c2_gemm"] = g

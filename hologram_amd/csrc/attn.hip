@@ -129,14 +129,17 @@ __device__ __forceinline__ void zero_rows(void *out, uint32_t b, uint32_t kh, ui
 
 // LDS of one workgroup's segment: the wavefront merge and the super-block
 // scale buffers. k-scales are stored pre-multiplied by log2(e)/scale.
-constexpr uint32_t kSuper = 4 * kQuad;   // keys per scale super-block (512)
+// W wavefronts per workgroup (4, or 8 for the grid form over few planes):
+// a pass of the wavefronts covers W * 32 keys, a scale super-block four passes.
+template <int W>
+constexpr uint32_t super_keys() { return 4u * W * kBlock; }
 
-template <int D>
+template <int D, int W = kWaves>
 struct SegLds {
-    float red_m[kWaves][16], red_l[kWaves][16];
-    float red_o[kWaves][16][D];
-    float sk[2][kSuper], sv[2][kSuper];
-    float svmax[2][2];
+    float red_m[W][16], red_l[W][16];
+    float red_o[W][16][D];
+    float sk[2][super_keys<W>()], sv[2][super_keys<W>()];
+    float svmax[2][W / 2];
     i32x4 qop[2][D / 64][64];   // Q int8 hi/lo MFMA operands, per lane of a wavefront
     float smul[16];             // 2^-qe per head
 };
@@ -163,13 +166,16 @@ struct SegLds {
 // a column that has seen no visible key yet keeps exact zeros (its rescale
 // and weights are guarded); a row with no visible key at all is written as
 // zeros.
-template <int D, bool kF32Q, bool kPack = false>
+template <int D, bool kF32Q, bool kPack = false, int W = kWaves>
 __device__ __forceinline__ void attn_segment(
     const void *__restrict__ q, const int8_t *__restrict__ kq, const int8_t *__restrict__ vq,
     const float *__restrict__ ks, const float *__restrict__ vs, float *__restrict__ dst,
     void *__restrict__ out, uint32_t b, uint32_t qrow, uint32_t kh, uint32_t c0, uint32_t c1,
     bool single, uint32_t H, uint32_t Hkv, uint32_t G, uint32_t bucket, float log2e_over_scale,
-    SegLds<D> &lds, uint32_t prow = 1, int64_t lim0 = 0) {
+    SegLds<D, W> &lds, uint32_t prow = 1, int64_t lim0 = 0) {
+    constexpr uint32_t kQ = W * kBlock;         // keys per pass of the wavefronts
+    constexpr uint32_t kS = super_keys<W>();    // keys per scale super-block
+    constexpr int kNT = 64 * W;
     constexpr int KB = D / 4;          // K bytes per lane per key row (QK k-slots)
     constexpr int NKS = D / 64;        // i8 MFMA k-steps (64 dims each)
     constexpr int NDB = D / 16;        // 16-row dim blocks of O^T
@@ -227,19 +233,19 @@ __device__ __forceinline__ void attn_segment(
     };
     // Super-block scales: wavefronts 0-1 load the 512 k-scales, 2-3 the
     // v-scales, four keys per thread.
-    const uint32_t nsb = (c1 - c0 + kSuper - 1) / kSuper;
-    const uint32_t st = uint32_t(tid) & 127u;
+    const uint32_t nsb = (c1 - c0 + kS - 1) / kS;
+    const uint32_t st = uint32_t(tid) & (32u * W - 1u);
     auto load_sc = [&](uint32_t sb) -> u32x4 {   // sb >= nsb loads nothing
-        const int so = sb < nsb ? int((c0 + sb * kSuper) * 4) : int(bucket * 4);
-        return wv < 2 ? __builtin_amdgcn_raw_buffer_load_b128(rks, int(16 * st), so, 0)
+        const int so = sb < nsb ? int((c0 + sb * kS) * 4) : int(bucket * 4);
+        return wv < W / 2 ? __builtin_amdgcn_raw_buffer_load_b128(rks, int(16 * st), so, 0)
                       : __builtin_amdgcn_raw_buffer_load_b128(rvs, int(16 * st), so, 0);
     };
     auto store_sc = [&](uint32_t sb, u32x4 v) {
-        const uint32_t key0 = c0 + sb * kSuper + 4 * st;
+        const uint32_t key0 = c0 + sb * kS + 4 * st;
         float f[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) f[t] = key0 + t < c1 ? __uint_as_float(v[t]) : 0.0f;
-        if (wv < 2) {
+        if (wv < W / 2) {
             *reinterpret_cast<float4 *>(&lds.sk[sb & 1][4 * st]) =
                 float4{f[0] * log2e_over_scale, f[1] * log2e_over_scale,
                        f[2] * log2e_over_scale, f[3] * log2e_over_scale};
@@ -248,7 +254,7 @@ __device__ __forceinline__ void attn_segment(
             float m = fmaxf(fmaxf(f[0], f[1]), fmaxf(f[2], f[3]));
 #pragma unroll
             for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-            if (lane == 0) lds.svmax[sb & 1][wv - 2] = m;
+            if (lane == 0) lds.svmax[sb & 1][wv - W / 2] = m;
         }
     };
 
@@ -333,7 +339,7 @@ __device__ __forceinline__ void attn_segment(
     Blk ring[PD];
 #pragma unroll
     for (int p = 0; p < PD - 1; ++p) {
-        const uint32_t bb = c0 + uint32_t(p) * kQuad + wv * kBlock;
+        const uint32_t bb = c0 + uint32_t(p) * kQ + wv * kBlock;
         load(bb, bb < c1, ring[p]);
     }
 
@@ -434,7 +440,9 @@ __device__ __forceinline__ void attn_segment(
     for (uint32_t sb = 0; sb < nsb; ++sb) {
         sreg = load_sc(sb + 1);
         {   // 2^ve bounds every v-scale of this super-block (all wavefronts alike)
-            const float vb = fmaxf(lds.svmax[sb & 1][0], lds.svmax[sb & 1][1]);
+            float vb = lds.svmax[sb & 1][0];
+#pragma unroll
+            for (int i = 1; i < W / 2; ++i) vb = fmaxf(vb, lds.svmax[sb & 1][i]);
             if (vb > ldexpf(1.0f, ve) && vb <= 3.0e38f) {
                 int ve_new;
                 (void)frexpf(vb, &ve_new);                     // vb < 2^ve_new
@@ -448,11 +456,11 @@ __device__ __forceinline__ void attn_segment(
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t blk = c0 + (4 * sb + uint32_t(i)) * kQuad + wv * kBlock;
-            const uint32_t nb = blk + (PD - 1) * kQuad;
+            const uint32_t blk = c0 + (4 * sb + uint32_t(i)) * kQ + wv * kBlock;
+            const uint32_t nb = blk + (PD - 1) * kQ;
             load(nb, nb < c1, ring[(i + PD - 1) % PD]);
             if (blk < c1) {
-                const uint32_t so = uint32_t(i) * kQuad + wv * kBlock;
+                const uint32_t so = uint32_t(i) * kQ + wv * kBlock;
                 const float *skp = lds.sk[sb & 1] + so, *svp = lds.sv[sb & 1] + so;
                 block(blk + kBlock > lim_min, ring[i % PD], blk, skp, svp);
             }
@@ -479,14 +487,14 @@ __device__ __forceinline__ void attn_segment(
     // the common 2^ve). Otherwise write the partial, scaled back by 2^ve.
     const float v_rescale = ldexpf(1.0f, ve);
     const uint32_t ncol = kPack ? G * prow : G;
-    for (uint32_t idx = tid; idx < ncol * D; idx += kThreads) {
+    for (uint32_t idx = tid; idx < ncol * D; idx += kNT) {
         const uint32_t h = idx / D, d = idx % D;
         float m = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) m = fmaxf(m, lds.red_m[w][h]);
+        for (int w = 0; w < W; ++w) m = fmaxf(m, lds.red_m[w][h]);
         float o = 0.0f, l = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
+        for (int w = 0; w < W; ++w) {
             const float sc = lds.red_m[w][h] == -INFINITY ? 0.0f : exp2f(lds.red_m[w][h] - m);
             o = fmaf(lds.red_o[w][h][d], sc, o);
             l = fmaf(lds.red_l[w][h], sc, l);
@@ -521,27 +529,30 @@ __device__ __forceinline__ uint32_t visible_keys(uint32_t len, uint32_t back, ui
 // Grid form for very large batches: grid (chunks, Hkv, B), one workgroup per
 // kChunk-key chunk of a plane; chunks at or beyond L_b exit at once, and chunk
 // 0 of a plane with no visible key writes the exact zero rows. Partial of
-// (plane, chunk) at index plane * nchunks + chunk.
-template <int D, bool kF32Q>
-__global__ __launch_bounds__(kThreads, kWps) void attn_chunk_kernel(
+// (plane, chunk) at index plane * nchunks + chunk. W wavefronts a workgroup:
+// 8 when the grid is too small to fill the GPU (a decode step's 64 planes of
+// one chunk each), so each wavefront walks an eighth of its plane, not a
+// quarter.
+template <int D, bool kF32Q, int W>
+__global__ __launch_bounds__(64 * W, W == kWaves ? kWps : 1) void attn_chunk_kernel(
     const void *__restrict__ q, const int8_t *__restrict__ kq, const int8_t *__restrict__ vq,
     const float *__restrict__ ks, const float *__restrict__ vs, const uint32_t *__restrict__ lens,
     float *__restrict__ part, void *__restrict__ out, uint32_t H, uint32_t Hkv, uint32_t G,
     uint32_t bucket, uint32_t kChunk, uint32_t nchunks, float log2e_over_scale, uint32_t q_rows) {
-    __shared__ SegLds<D> lds;
+    __shared__ SegLds<D, W> lds;
     const uint32_t v = blockIdx.z, kh = blockIdx.y, chunk = blockIdx.x;
     const uint32_t b = v / q_rows;
     const uint32_t L = visible_keys(lens[b], q_rows - 1 - v % q_rows, bucket);
     const uint32_t c0 = chunk * kChunk;
     if (c0 >= L) {
-        if (L == 0 && chunk == 0) zero_rows<kF32Q>(out, v, kh, H, G, D, threadIdx.x, kThreads);
+        if (L == 0 && chunk == 0) zero_rows<kF32Q>(out, v, kh, H, G, D, threadIdx.x, 64 * W);
         return;
     }
     const uint32_t c1 = L - c0 < kChunk ? L : c0 + kChunk;
     const uint64_t row_plane = uint64_t(v) * Hkv + kh;
     float *dst = part + (row_plane * nchunks + chunk) * G * (D + 2);
-    attn_segment<D, kF32Q>(q, kq, vq, ks, vs, dst, out, b, v, kh, c0, c1, L <= kChunk, H, Hkv, G,
-                           bucket, log2e_over_scale, lds);
+    attn_segment<D, kF32Q, false, W>(q, kq, vq, ks, vs, dst, out, b, v, kh, c0, c1, L <= kChunk, H,
+                                     Hkv, G, bucket, log2e_over_scale, lds);
 }
 
 // Packed prompt form: grid (1, Hkv, B * ceil(T / R)). A workgroup takes R
@@ -1092,6 +1103,11 @@ uint32_t split_wgs() {
 // 8-9 us against 11.5 + 4.4 us for split + merge).
 constexpr uint32_t kGridMinPlanes = 32;
 
+// A grid form of at most this many workgroups (fewer than the GPU's CUs) runs
+// them wide, kWideWaves wavefronts each.
+constexpr uint64_t kWideMaxWgs = 128;
+constexpr int kWideWaves = 8;
+
 uint32_t chunks_of(uint32_t bucket);
 
 bool use_split(uint32_t B, uint32_t Hkv, uint32_t bucket) {
@@ -1143,9 +1159,14 @@ hipError_t run_t(const AttnI8Args &a, void *scratch, hipStream_t stream) {
         return hipGetLastError();
     }
     const uint32_t rows = a.B * a.q_rows;
-    hipLaunchKernelGGL((attn_chunk_kernel<D, kF32Q>), dim3(nch, a.Hkv, rows), dim3(kThreads), 0,
-                       stream, a.q, a.kq, a.vq, a.ks, a.vs, a.lens, part, a.out, a.H, a.Hkv, G,
-                       a.bucket, ck, nch, mul, a.q_rows);
+    if (uint64_t(nch) * a.Hkv * rows <= kWideMaxWgs)
+        hipLaunchKernelGGL((attn_chunk_kernel<D, kF32Q, kWideWaves>), dim3(nch, a.Hkv, rows),
+                           dim3(64 * kWideWaves), 0, stream, a.q, a.kq, a.vq, a.ks, a.vs, a.lens,
+                           part, a.out, a.H, a.Hkv, G, a.bucket, ck, nch, mul, a.q_rows);
+    else
+        hipLaunchKernelGGL((attn_chunk_kernel<D, kF32Q, kWaves>), dim3(nch, a.Hkv, rows),
+                           dim3(kThreads), 0, stream, a.q, a.kq, a.vq, a.ks, a.vs, a.lens, part,
+                           a.out, a.H, a.Hkv, G, a.bucket, ck, nch, mul, a.q_rows);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || nch == 1) return e;
     hipLaunchKernelGGL((attn_combine_kernel<D, kF32Q>), dim3(a.Hkv, rows), dim3(256), 0, stream,

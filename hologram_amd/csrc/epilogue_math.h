@@ -76,12 +76,12 @@ __device__ __forceinline__ float base_value(const EpiSeg &sg, float v, float r) 
         if (sg.base == kEpiAdd || sg.base == kEpiAddAct) {
             const float s = bf2f(x) + r;
             // MatMulAddActivation applies f to the f32 sum before narrowing
-            x = f2bf(sg.base == kEpiAddAct ? act_f32(sg.act, s) : s);
+            x = f2bf(sg.base == kEpiAddAct ? act_f32_call(sg.act, s) : s);
         }
         return bf2f(x);
     } else {
         if (sg.base == kEpiAdd || sg.base == kEpiAddAct) v = v + r;
-        if (sg.base == kEpiAct || sg.base == kEpiAddAct) v = act_f32(sg.act, v);
+        if (sg.base == kEpiAct || sg.base == kEpiAddAct) v = act_f32_call(sg.act, v);
         return v;
     }
 }

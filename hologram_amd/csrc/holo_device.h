@@ -231,6 +231,15 @@ __device__ inline float act_f32(uint32_t act, float x) {
     }
 }
 
+// The same, out of line: for epilogues that unroll many elements, where an
+// inlined copy per element (the switch with its exp / expf / erff bodies)
+// would multiply the kernel's code size (tens of KiB per kernel, re-fetched
+// into the instruction cache at every launch) for a path most launches never
+// take. The call needs no stack.
+__device__ __attribute__((noinline)) inline float act_f32_call(uint32_t act, float x) {
+    return act_f32(act, x);
+}
+
 // RmsNorm of one bf16 row held as 16-byte vectors: thread t of a 256-thread
 // group (waves 0-3 of its workgroup) holds vectors t + 256u (u < kMaxVec, v <
 // nv) of x and of gamma. Sum of squares: per thread in vector order with fmaf,

@@ -191,7 +191,7 @@ __global__ __launch_bounds__(256) void gemm_q_omajor_kernel(QGemm g) {
             const float si = g.sa[i];
             float o = si == 0.0f ? 0.0f : float(v[e]) * (si * sj);
             if (g.residual) o = o + g.residual[uint64_t(i) * g.n + j];
-            if (g.act) o = act_f32(g.act, o);
+            if (g.act) o = act_f32_call(g.act, o);
             g.out[uint64_t(i) * g.n + j] = o;
         }
     }
@@ -351,7 +351,7 @@ __global__ __launch_bounds__(256) void gemv_q_omajor_kernel(QGemm g) {
             const float si = g.sa[r], sj = g.scales[j];
             float o = si == 0.0f ? 0.0f : float(tot) * (si * sj);
             if (g.residual) o = o + g.residual[uint64_t(r) * g.n + j];
-            if (g.act) o = act_f32(g.act, o);
+            if (g.act) o = act_f32_call(g.act, o);
             g.out[uint64_t(r) * g.n + j] = o;
         }
     }

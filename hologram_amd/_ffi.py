@@ -243,6 +243,7 @@ SIGNATURES = {
                                                   ctypes.POINTER(ctypes.c_uint32)]),
     "holo_hip_session_packed": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_uint32),
                                                ctypes.POINTER(ctypes.c_uint64)]),
+    "holo_hip_session_attn_prologues": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_uint32)]),
     "holo_hip_op_signature": (ctypes.c_int, [ctypes.POINTER(KernelCallC),
                                              ctypes.POINTER(ctypes.c_uint16), ctypes.c_char_p,
                                              ctypes.POINTER(ctypes.c_uint32)]),

@@ -51,6 +51,7 @@
 
 #include <algorithm>
 
+#include "epilogue_math.h"
 #include "holo_device.h"
 #include "holo_kernels.h"
 
@@ -553,6 +554,59 @@ __global__ __launch_bounds__(64 * W, W == kWaves ? kWps : 1) void attn_chunk_ker
     float *dst = part + (row_plane * nchunks + chunk) * G * (D + 2);
     attn_segment<D, kF32Q, false, W>(q, kq, vq, ks, vs, dst, out, b, v, kh, c0, c1, L <= kChunk, H,
                                      Hkv, G, bucket, log2e_over_scale, lds);
+}
+
+// The grid form of a decode step (one chunk a plane, one bf16 query row) with
+// the q/k/v group's split-K epilogue in front: workgroup (b, kh) first
+// finishes, from the partials, every head of the group's head-wise segments
+// that belongs to kv head kh of row b (segment s holds n_s / D heads a row,
+// n_s / (D Hkv) of them per kv head: its query heads, or its one k or v head),
+// storing the rotated q and the appended int8 k / v rows exactly as the
+// epilogue launch does (the same head_finish), then attends. A workgroup reads
+// back only what it stored itself (its plane's query heads and cache rows),
+// after its stores have completed (s_waitcnt) and a workgroup barrier, so no
+// other workgroup's order matters.
+template <int D, int W>
+__global__ __launch_bounds__(64 * W, W == kWaves ? kWps : 1) void attn_pro_kernel(
+    const uint16_t *__restrict__ q, const int8_t *__restrict__ kq, const int8_t *__restrict__ vq,
+    const float *__restrict__ ks, const float *__restrict__ vs, const uint32_t *__restrict__ lens,
+    void *__restrict__ out, uint32_t H, uint32_t Hkv, uint32_t G, uint32_t bucket,
+    float log2e_over_scale, const EpiArgs pro) {
+    __shared__ SegLds<D, W> lds;
+    const uint32_t b = blockIdx.z, kh = blockIdx.y;
+    const uint32_t len_b = lens[b];   // read before the prologue: it does not write lens
+    {
+        constexpr uint32_t half = D / 2, slots = 64 * W / half;
+        const uint32_t slot = threadIdx.x / half, d = threadIdx.x % half;
+        uint32_t hp[kSkinnyMaxSeg], total = 0;
+#pragma unroll
+        for (int s = 0; s < kSkinnyMaxSeg; ++s) {
+            hp[s] = uint32_t(s) < pro.nseg ? pro.seg[s].n / (D * Hkv) : 0u;
+            total += hp[s];
+        }
+        // a head's D/2 lanes take the same heads (the quantizer's shuffles)
+        for (uint32_t t = slot; t < total; t += slots) {
+            uint32_t si = 0, first = 0, acc = hp[0];
+#pragma unroll
+            for (int s = 1; s < kSkinnyMaxSeg; ++s)
+                if (t >= acc) {
+                    si = uint32_t(s);
+                    first = acc;
+                    acc += hp[s];
+                }
+            const EpiSeg sg = epi::seg_of(pro, si);
+            epi::head_finish<true>(pro, sg, b, kh * (sg.n / (D * Hkv)) + (t - first), d, true);
+        }
+        __builtin_amdgcn_s_waitcnt(0);   // every store of this workgroup has completed
+        __syncthreads();
+    }
+    const uint32_t L = visible_keys(len_b, 0, bucket);
+    if (L == 0) {
+        zero_rows<false>(out, b, kh, H, G, D, threadIdx.x, 64 * W);
+        return;
+    }
+    attn_segment<D, false, false, W>(q, kq, vq, ks, vs, nullptr, out, b, b, kh, 0, L, true, H, Hkv, G,
+                                     bucket, log2e_over_scale, lds);
 }
 
 // Packed prompt form: grid (1, Hkv, B * ceil(T / R)). A workgroup takes R
@@ -1211,6 +1265,44 @@ hipError_t launch_attn_i8(const AttnI8Args &a, void *scratch, hipStream_t stream
     if (a.D == 128) return run<128>(a, scratch, stream);
     if (a.D == 64) return run<64>(a, scratch, stream);
     return hipErrorInvalidValue;
+}
+
+bool attn_i8_pro_applies(const AttnI8Args &a, const EpiArgs &pro) {
+    if (a.q_rows != 1 || a.dtype == 8 || !attn_i8_supported(a.H, a.Hkv, a.D, a.bucket) ||
+        a.B == 0 || a.B > 65535 || a.Hkv > 65535 || use_split(a.B, a.Hkv, a.bucket) ||
+        chunks_of(a.bucket) != 1)
+        return false;
+    if (!pro.bf16 || pro.m != a.B || pro.ks == 0 || pro.nseg == 0 || pro.nseg > uint32_t(kSkinnyMaxSeg))
+        return false;
+    for (uint32_t i = 0; i < pro.nseg; ++i) {
+        const EpiSeg &s = pro.seg[i];
+        if (s.head_dim != a.D || s.pair >= 0 || s.skip || s.ssq || s.n % (a.D * a.Hkv) != 0 ||
+            (s.quant && s.new_rows != 1))
+            return false;
+    }
+    return true;
+}
+
+hipError_t launch_attn_i8_pro(const AttnI8Args &a, const EpiArgs &pro, hipStream_t stream) {
+    if (!attn_i8_pro_applies(a, pro)) return hipErrorInvalidValue;
+    const uint32_t G = a.H / a.Hkv;
+    const float mul = kLog2e / a.score_scale;
+    const bool wide = uint64_t(a.Hkv) * a.B <= kWideMaxWgs;
+    const auto *q = static_cast<const uint16_t *>(a.q);
+    const dim3 grid(1, a.Hkv, a.B);
+    if (a.D == 64 && wide)
+        hipLaunchKernelGGL((attn_pro_kernel<64, kWideWaves>), grid, dim3(64 * kWideWaves), 0, stream, q,
+                           a.kq, a.vq, a.ks, a.vs, a.lens, a.out, a.H, a.Hkv, G, a.bucket, mul, pro);
+    else if (a.D == 64)
+        hipLaunchKernelGGL((attn_pro_kernel<64, kWaves>), grid, dim3(kThreads), 0, stream, q, a.kq,
+                           a.vq, a.ks, a.vs, a.lens, a.out, a.H, a.Hkv, G, a.bucket, mul, pro);
+    else if (wide)
+        hipLaunchKernelGGL((attn_pro_kernel<128, kWideWaves>), grid, dim3(64 * kWideWaves), 0, stream, q,
+                           a.kq, a.vq, a.ks, a.vs, a.lens, a.out, a.H, a.Hkv, G, a.bucket, mul, pro);
+    else
+        hipLaunchKernelGGL((attn_pro_kernel<128, kWaves>), grid, dim3(kThreads), 0, stream, q, a.kq,
+                           a.vq, a.ks, a.vs, a.lens, a.out, a.H, a.Hkv, G, a.bucket, mul, pro);
+    return hipGetLastError();
 }
 
 }  // namespace holo

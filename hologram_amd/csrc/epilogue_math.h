@@ -113,5 +113,130 @@ __device__ __forceinline__ int8_t to_q(float r) {
     return static_cast<int8_t>(static_cast<int32_t>(r));
 }
 
+// The product at (row m, column c) of P's column space: partials summed in
+// ks order. Up to kBatch loads go out before the first add, so a split of up
+// to kBatch partials costs one memory round trip; the adds keep ks order.
+// No load sits behind a branch: a batch past ks reloads partial ks - 1 (its
+// value is not added), since a branch around a load makes the compiler wait
+// for every load in flight where the branch joins.
+constexpr uint32_t kBatch = 32;
+
+__device__ __forceinline__ uint32_t clamp_ks(uint32_t k, uint32_t ks) { return k < ks ? k : ks - 1; }
+
+template <class T>
+__device__ __forceinline__ T sum_partials(const T *p, uint64_t plane, uint32_t ks) {
+    T s{};
+    for (uint32_t k0 = 0; k0 < ks; k0 += kBatch) {
+        T v[kBatch];
+#pragma unroll
+        for (uint32_t u = 0; u < kBatch; ++u) v[u] = p[clamp_ks(k0 + u, ks) * plane];
+        if (k0 == 0) s = v[0];
+#pragma unroll
+        for (uint32_t u = 0; u < kBatch; ++u)
+            if (k0 + u < ks && (k0 | u) != 0) s += v[u];
+    }
+    return s;
+}
+
+// Two columns (c, c + off) of one row, their partials in flight together.
+__device__ __forceinline__ void product2(const EpiArgs &g, uint32_t m, uint32_t c, uint32_t off,
+                                        float *x1, float *x2) {
+    const uint64_t plane = uint64_t(g.m) * g.ntot;
+    const float *p = g.P + uint64_t(m) * g.ntot + c;
+    float s1 = 0.0f, s2 = 0.0f;
+    for (uint32_t k0 = 0; k0 < g.ks; k0 += kBatch / 2) {
+        float v1[kBatch / 2], v2[kBatch / 2];
+#pragma unroll
+        for (uint32_t u = 0; u < kBatch / 2; ++u) {
+            const uint64_t kk = clamp_ks(k0 + u, g.ks);
+            v1[u] = p[kk * plane];
+            v2[u] = p[kk * plane + off];
+        }
+        if (k0 == 0) {
+            s1 = v1[0];
+            s2 = v2[0];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kBatch / 2; ++u)
+            if (k0 + u < g.ks && (k0 | u) != 0) {
+                s1 += v1[u];
+                s2 += v2[u];
+            }
+    }
+    *x1 = s1;
+    *x2 = s2;
+}
+
+// One head of a head-wise segment (rope and/or quant) at row m, head h of the
+// row: lane d < D/2 of the head's D/2 consecutive lanes holds the rotate-half
+// pair (d, d + D/2). The head's lanes run this together (the int8 scale is a
+// shuffle reduction over them). `live` false: the lane loads and computes but
+// stores nothing.
+template <bool kBf16>
+__device__ __forceinline__ void head_finish(const EpiArgs &g, const EpiSeg &sg, uint32_t m, uint32_t h,
+                                            uint32_t d, bool live) {
+    const uint32_t D = sg.head_dim, half = D / 2;
+    const uint32_t c1 = h * D + d;
+    const uint64_t e1 = uint64_t(m) * sg.n + c1;
+    // side operands first: their loads overlap the partials'
+    const auto rc = opt_rsrc(sg.cos, sg.rope), rs = opt_rsrc(sg.sin, sg.rope);
+    const auto rr = opt_rsrc(sg.residual, has_residual(sg));
+    const float c1v = opt_load<kBf16>(rc, e1), s1v = opt_load<kBf16>(rs, e1);
+    const float c2v = opt_load<kBf16>(rc, e1 + half), s2v = opt_load<kBf16>(rs, e1 + half);
+    const float r1 = opt_load<kBf16>(rr, e1), r2 = opt_load<kBf16>(rr, e1 + half);
+    float p1, p2;
+    product2(g, m, sg.col0 + c1, half, &p1, &p2);
+    float x1 = base_value<kBf16>(sg, p1, r1);
+    float x2 = base_value<kBf16>(sg, p2, r2);
+    if (live) {
+        if (sg.out) {
+            store<kBf16>(sg.out, e1, x1);
+            store<kBf16>(sg.out, e1 + half, x2);
+        }
+        if (sg.rope) {
+            float y1 = x1 * c1v - x2 * s1v;
+            float y2 = x2 * c2v + x1 * s2v;
+            if constexpr (kBf16) {
+                y1 = bf2f(f2bf(y1));
+                y2 = bf2f(f2bf(y2));
+            }
+            x1 = y1;
+            x2 = y2;
+            if (sg.rope_out) {
+                store<kBf16>(sg.rope_out, e1, x1);
+                store<kBf16>(sg.rope_out, e1 + half, x2);
+            }
+        }
+    }
+    if (!sg.quant) return;
+    // row max of |x| over the head's lanes (NaN never wins a `>`); exact, so
+    // the order of the reduction does not matter
+    float amax = 0.0f;
+    const float a1 = x1 < 0.0f ? -x1 : x1, a2 = x2 < 0.0f ? -x2 : x2;
+    if (a1 > amax) amax = a1;
+    if (a2 > amax) amax = a2;
+    for (uint32_t off = half / 2; off >= 1; off >>= 1) {
+        const float o = __shfl_xor(amax, int(off), 64);
+        if (o > amax) amax = o;
+    }
+    if (!live) return;
+    const uint64_t r = e1 / D;   // the row of the appended [planes, new_rows, D] block
+    const uint32_t plane = uint32_t(r / sg.new_rows), j = uint32_t(r % sg.new_rows);
+    const uint64_t pos = *sg.pos % sg.bucket;
+    const uint64_t row = uint64_t(plane) * sg.bucket + (pos + j) % sg.bucket;
+    int8_t *dst = sg.cq + row * D;
+    if (amax == 0.0f) {
+        dst[d] = 0;
+        dst[d + half] = 0;
+        if (d == 0) sg.cs[row] = 0.0f;
+        return;
+    }
+    const float inv = 127.0f / amax;
+    const float t1 = x1 * inv, t2 = x2 * inv;
+    dst[d] = to_q(t1 >= 0.0f ? truncf(t1 + 0.5f) : truncf(t1 - 0.5f));
+    dst[d + half] = to_q(t2 >= 0.0f ? truncf(t2 + 0.5f) : truncf(t2 - 0.5f));
+    if (d == 0) sg.cs[row] = amax / 127.0f;
+}
+
 }  // namespace epi
 }  // namespace holo

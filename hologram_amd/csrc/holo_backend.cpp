@@ -300,7 +300,7 @@ int do_matmul(holo_backend *be, const SlotTable &st, const holo_matmul_call &c) 
 // element-wise epilogue that the few-row kernels do not serve runs the tiled
 // MatMul into its output and the epilogue over it in place.
 int dispatch_group_impl(holo_backend *be, const SlotTable &st, const holo::GroupDesc &g,
-                        const char *op) {
+                        const char *op, holo::EpiArgs *defer = nullptr) {
     const size_t nseg = g.segs.size();
     if (nseg == 0 || nseg > size_t(holo::kSkinnyMaxSeg))
         return fail(HOLO_ERR_DISPATCH, std::string(op) + ": fused group of " + std::to_string(nseg) +
@@ -561,6 +561,12 @@ int dispatch_group_impl(holo_backend *be, const SlotTable &st, const holo::Group
                                                    static_cast<float *>(be->scratch), be->stream,
                                                    a_norm ? &na : nullptr),
                       op));
+    if (defer) {
+        // the caller runs the epilogue with the next call (its partials stay
+        // in the scratch, which nothing may grow before then)
+        *defer = e;
+        return HOLO_OK;
+    }
     return launched(holo::launch_epilogue(e, be->stream), op);
 }
 
@@ -741,7 +747,8 @@ int do_kv_quant(holo_backend *be, const SlotTable &st, const holo_kv_quant_appen
 // ---------------------------------------------------- DecodeAttnI8 -------
 // Refusals follow decode_attention_valid_float (src/cpu/float_kernels.rs:4192-4220).
 int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attention_i8_call &c,
-               uint32_t q_rows = 1, bool static_scratch = false) {
+               uint32_t q_rows = 1, bool static_scratch = false, const holo::EpiArgs *pro = nullptr,
+               bool *pro_done = nullptr) {
     const char *op = "decode_attention_i8";
     if (c.batch == 0 || c.heads == 0 || c.head_dim == 0) return HOLO_OK;
     const uint32_t hkv = c.kv_heads == 0 ? c.heads : c.kv_heads;
@@ -794,6 +801,30 @@ int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attentio
         memcpy(&sm, &c.scale_bits, 4);
         scale = sm > 0.0f ? 1.0f / sm : dflt;
     }
+    holo::AttnI8Args a;
+    a.q = rv[0].base;
+    a.kq = reinterpret_cast<const int8_t *>(rv[1].base);
+    a.vq = reinterpret_cast<const int8_t *>(rv[2].base);
+    a.ks = reinterpret_cast<const float *>(rv[3].base);
+    a.vs = reinterpret_cast<const float *>(rv[4].base);
+    a.lens = reinterpret_cast<const uint32_t *>(rv[5].base);
+    a.out = out.base;
+    a.B = c.batch;
+    a.H = c.heads;
+    a.Hkv = hkv;
+    a.bucket = c.bucket_rows;
+    a.D = c.head_dim;
+    a.score_scale = scale;
+    a.dtype = c.dtype;
+    a.q_rows = q_rows;
+    if (pro) {
+        // the few-row group before this call left its split-K epilogue here:
+        // run it in front of the attention in one launch, or on its own first
+        *pro_done = true;
+        if (mfma && c.bucket_rows != 0 && holo::attn_i8_pro_applies(a, *pro))
+            return launched(holo::launch_attn_i8_pro(a, *pro, be->stream), op);
+        HOLO_TRY(launched(holo::launch_epilogue(*pro, be->stream), op));
+    }
     const size_t scratch_bytes =
         mfma ? holo::attn_i8_scratch_bytes(c.batch, c.heads, hkv, c.bucket_rows, c.head_dim, q_rows)
              : holo::attn_i8_any_scratch_bytes(c.batch, c.heads, hkv, q_rows, c.bucket_rows,
@@ -813,22 +844,6 @@ int do_attn_i8(holo_backend *be, const SlotTable &st, const holo_decode_attentio
         HOLO_TRY(ensure_scratch(be, scratch_bytes, op));
         scratch = be->scratch;
     }
-    holo::AttnI8Args a;
-    a.q = rv[0].base;
-    a.kq = reinterpret_cast<const int8_t *>(rv[1].base);
-    a.vq = reinterpret_cast<const int8_t *>(rv[2].base);
-    a.ks = reinterpret_cast<const float *>(rv[3].base);
-    a.vs = reinterpret_cast<const float *>(rv[4].base);
-    a.lens = reinterpret_cast<const uint32_t *>(rv[5].base);
-    a.out = out.base;
-    a.B = c.batch;
-    a.H = c.heads;
-    a.Hkv = hkv;
-    a.bucket = c.bucket_rows;
-    a.D = c.head_dim;
-    a.score_scale = scale;
-    a.dtype = c.dtype;
-    a.q_rows = q_rows;
     if (c.bucket_rows == 0) {
         // No key can be visible: the pinned zero vector (pinned_semantics.rs).
         return launched(holo::launch_fill_zero(out.base, qn * es, be->stream), op);
@@ -1841,10 +1856,29 @@ int decode_call(const uint8_t *wire, size_t len, holo_kernel_call *out, size_t *
     return decode_impl(wire, len, out, consumed);
 }
 
-int dispatch_group(holo_backend *be, const std::vector<SlotRange> &slots, const GroupDesc &g) {
+int dispatch_group(holo_backend *be, const std::vector<SlotRange> &slots, const GroupDesc &g,
+                   EpiArgs *defer) {
     SlotTable st;
     st.vec = &slots;
-    return dispatch_group_impl(be, st, g, "fused_group");
+    if (defer) defer->ks = 0;
+    return dispatch_group_impl(be, st, g, "fused_group", defer);
+}
+
+int launch_deferred_epilogue(holo_backend *be, const EpiArgs &e) {
+    return launched(launch_epilogue(e, be->stream), "fused_group");
+}
+
+int dispatch_with_epilogue(holo_backend *be, const std::vector<SlotRange> &slots,
+                           const holo_kernel_call *call, const EpiArgs &pro) {
+    SlotTable st;
+    st.vec = &slots;
+    if (call->tag == HOLO_OP_DECODE_ATTN_I8) {
+        bool done = false;
+        const int rc = do_attn_i8(be, st, call->u.attn_i8, 1, false, &pro, &done);
+        if (done || rc != HOLO_OK) return rc;
+    }
+    HOLO_TRY(launch_deferred_epilogue(be, pro));
+    return dispatch_impl(be, st, call);
 }
 
 int lut_act_of_fused(uint32_t act) {

@@ -70,7 +70,18 @@ struct GroupDesc {
     bool packed = false;
     uint32_t packed_tw = 16;   // element-wise tile width the weights were packed with
 };
-int dispatch_group(holo_backend *be, const std::vector<SlotRange> &slots, const GroupDesc &g);
+struct EpiArgs;
+// defer: a group that ends in the split-K epilogue launches only its product
+// and leaves the epilogue's arguments in *defer (ks > 0; ks == 0: nothing
+// deferred). The partials stay in the backend's scratch, so the deferred
+// epilogue must run before anything grows it: with the next call
+// (dispatch_with_epilogue), which takes it into a decode attention's launch
+// where that applies, or on its own (launch_deferred_epilogue).
+int dispatch_group(holo_backend *be, const std::vector<SlotRange> &slots, const GroupDesc &g,
+                   EpiArgs *defer = nullptr);
+int dispatch_with_epilogue(holo_backend *be, const std::vector<SlotRange> &slots,
+                           const holo_kernel_call *call, const EpiArgs &pro);
+int launch_deferred_epilogue(holo_backend *be, const EpiArgs &e);
 // The LUT activation id of a fused_activation id (-1: no table).
 int lut_act_of_fused(uint32_t act);
 // Whether the device serves fused activation `act` for dtype (bf16 table or f32 compute);

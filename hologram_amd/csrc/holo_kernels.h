@@ -65,6 +65,13 @@ size_t attn_i8_scratch_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t buck
                              uint32_t q_rows = 1);
 bool attn_i8_supported(uint32_t H, uint32_t Hkv, uint32_t D, uint32_t bucket);
 hipError_t launch_attn_i8(const AttnI8Args &a, void *scratch, hipStream_t stream);
+// The decode step's grid form with a few-row group's split-K epilogue in
+// front (attn_pro_kernel): every segment head-wise at head_dim D, its heads a
+// multiple of Hkv, one row per sequence, one appended row; q_rows 1, bf16, one
+// chunk a plane. Needs no scratch. Declared after EpiArgs below.
+struct EpiArgs;
+bool attn_i8_pro_applies(const AttnI8Args &a, const EpiArgs &pro);
+hipError_t launch_attn_i8_pro(const AttnI8Args &a, const EpiArgs &pro, hipStream_t stream);
 // attn_valid.hip — the same op for every other head_dim (up to 4096) and any
 // query-head group: a blocked split-K walk with each K/V block dequantized
 // into LDS, then the merge of the shares.

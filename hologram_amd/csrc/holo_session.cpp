@@ -531,6 +531,8 @@ void fuse_matmul_epilogue(std::vector<holo_kernel_call> &calls,
 struct Node {
     int group = -1;
     uint32_t call = 0;
+    // a group whose split-K epilogue the next node runs (attn_prologue_fusion)
+    bool epi_next = false;
 };
 
 }  // namespace
@@ -1365,6 +1367,67 @@ void elide_steps(holo_session *s, const std::vector<uint8_t> &is_output,
 // a fused RmsNorm takes the row statistics itself, so its producer stops
 // writing them; a producer whose reader stays split-K keeps writing them and
 // stays split-K too (a packed launch leaves no statistics).
+// The q/k/v group of a decode step hands its split-K epilogue to the decode
+// attention that follows it, which runs it in front of the attention in one
+// launch (attn_pro_kernel: each workgroup finishes the heads of its own plane,
+// then attends over them). Conditions: the group is bf16 and not packed; its
+// segments are all head-wise at the attention's head_dim, each with a multiple
+// of kv_heads heads a row and at most one appended row, with no SwiGLU pair and
+// no statistics; the next node is a DecodeAttentionI8 over batch = the group's
+// rows, whose q is a segment's stored output of heads x head_dim columns (the
+// rotated one for a rotary segment), whose k and v caches and scales are two
+// different quant segments' (through the in-place moves), and whose lengths and
+// output are no slot the group writes. A workgroup of the fused launch then
+// reads back only what its own prologue stored. Whether the launch applies
+// (the grid form, one chunk a plane) is decided at dispatch; where it does
+// not, the epilogue runs on its own before the attention.
+void attn_prologue_fusion(holo_session *s) {
+    auto root = [&](uint32_t slot) {
+        for (const auto &a : s->aliases)
+            if (a.first == slot) return a.second;
+        return slot;
+    };
+    auto same = [&](const holo_buffer_ref &a, const holo_buffer_ref &b) {
+        return root(a.slot) == root(b.slot) && a.offset == b.offset;
+    };
+    std::vector<uint32_t> rd, wr;
+    for (size_t i = 0; i + 1 < s->nodes.size(); ++i) {
+        Node &nd = s->nodes[i];
+        const Node &nx = s->nodes[i + 1];
+        if (nd.group < 0 || nx.group >= 0) continue;
+        const holo_kernel_call &c = s->calls[nx.call];
+        if (c.tag != HOLO_OP_DECODE_ATTN_I8) continue;
+        const holo_decode_attention_i8_call &at = c.u.attn_i8;
+        const holo::GroupDesc &g = s->groups[size_t(nd.group)];
+        const uint32_t hkv = at.kv_heads == 0 ? at.heads : at.kv_heads;
+        if (g.packed || g.dtype != HOLO_DTYPE_BF16 || at.dtype != HOLO_DTYPE_BF16 || g.m != at.batch ||
+            hkv == 0 || at.head_dim == 0 || g.segs.empty())
+            continue;
+        bool ok = true;
+        int qs = -1, ks = -1, vs = -1;
+        for (size_t j = 0; j < g.segs.size() && ok; ++j) {
+            const holo::GroupSegDesc &sg = g.segs[j];
+            ok = sg.head_dim == at.head_dim && sg.pair < 0 && !sg.skip && !sg.ssq &&
+                 sg.n % (uint64_t(at.head_dim) * hkv) == 0 && (!sg.quant || sg.new_rows == 1);
+            if (!ok) break;
+            const bool stored = sg.rope ? sg.write_rope : sg.write_out;
+            if (stored && uint64_t(sg.n) == uint64_t(at.heads) * at.head_dim &&
+                same(sg.rope ? sg.rope_out : sg.out, at.q))
+                qs = int(j);
+            if (sg.quant && uint64_t(sg.n) == uint64_t(hkv) * at.head_dim) {
+                if (same(sg.cq, at.k_cache) && same(sg.cs, at.k_scales)) ks = int(j);
+                if (same(sg.cq, at.v_cache) && same(sg.cs, at.v_scales)) vs = int(j);
+            }
+        }
+        if (!ok || qs < 0 || ks < 0 || vs < 0 || ks == vs) continue;
+        node_slots(s, nd, &rd, &wr);
+        bool clash = false;
+        for (uint32_t w : wr) clash = clash || root(w) == root(at.lens.slot) || root(w) == root(at.output.slot);
+        if (clash) continue;
+        nd.epi_next = true;
+    }
+}
+
 int pack_weights(holo_session *s, const std::vector<uint8_t> &is_input,
                  const std::vector<uint8_t> &is_const) {
     auto packable = [&](const holo::GroupDesc &g) { return packable_group(s, g, is_input, is_const); };
@@ -1837,6 +1900,8 @@ plan_moves:
         const int rc = pack_weights(s.get(), is_input, is_const);
         if (rc != HOLO_OK) return rc;
     }
+    if (!(flags & (HOLO_SESSION_NO_DEVICE_FUSION | HOLO_SESSION_NO_ATTN_PROLOGUE)))
+        attn_prologue_fusion(s.get());
     *out = s.release();
     return HOLO_OK;
 }
@@ -1864,15 +1929,32 @@ int walk(holo_session *s, const std::vector<uint8_t> *skip = nullptr) {
     int rc = HOLO_OK;
     s->last_dispatched = 0;
     s->last_skipped = s->n_elided;
+    // a group's deferred split-K epilogue, run by the next node dispatched
+    holo::EpiArgs pend;
+    bool pending = false;
     for (size_t i = 0; i < s->nodes.size(); ++i) {
         const Node &nd = s->nodes[i];
-        if (skip && (*skip)[i]) {
+        const bool skipped = skip && (*skip)[i];
+        if (pending && (skipped || nd.group >= 0)) {
+            pending = false;
+            rc = holo::launch_deferred_epilogue(s->be, pend);
+            if (rc != HOLO_OK) break;
+        }
+        if (skipped) {
             s->last_skipped++;
             continue;
         }
         s->last_dispatched++;
-        rc = nd.group >= 0 ? holo::dispatch_group(s->be, s->slots, s->groups[size_t(nd.group)])
-                           : holo::dispatch_with_slots(s->be, s->slots, &s->calls[nd.call]);
+        if (nd.group >= 0) {
+            rc = holo::dispatch_group(s->be, s->slots, s->groups[size_t(nd.group)],
+                                      nd.epi_next ? &pend : nullptr);
+            pending = rc == HOLO_OK && nd.epi_next && pend.ks != 0;
+        } else if (pending) {
+            pending = false;
+            rc = holo::dispatch_with_epilogue(s->be, s->slots, &s->calls[nd.call], pend);
+        } else {
+            rc = holo::dispatch_with_slots(s->be, s->slots, &s->calls[nd.call]);
+        }
         if (rc != HOLO_OK) {
             std::string m = holo_hip_last_error_message();
             set_error(rc, "session_execute: kernel call " + std::to_string(nd.call) +
@@ -1880,6 +1962,7 @@ int walk(holo_session *s, const std::vector<uint8_t> *skip = nullptr) {
             break;
         }
     }
+    if (rc == HOLO_OK && pending) rc = holo::launch_deferred_epilogue(s->be, pend);
     holo::swap_scratch(s->be, &s->scratch, &s->scratch_bytes);   // and out again
     holo::set_backend_stream(s->be, saved);
     return rc;
@@ -1933,6 +2016,14 @@ int holo_hip_session_packed(const holo_session *s, uint32_t *groups, uint64_t *b
     for (size_t i = 0; i < s->groups.size(); ++i) n += live[i] && s->groups[i].packed;
     if (groups) *groups = n;
     if (bytes) *bytes = s->packed_bytes;
+    return HOLO_OK;
+}
+
+int holo_hip_session_attn_prologues(const holo_session *s, uint32_t *n) {
+    if (!s || !n) return set_error(HOLO_ERR_INIT, "session_attn_prologues: null argument");
+    uint32_t c = 0;
+    for (const auto &nd : s->nodes) c += nd.group >= 0 && nd.epi_next;
+    *n = c;
     return HOLO_OK;
 }
 

@@ -30,13 +30,14 @@ NO_DEVICE_FUSION = 2     # skip this backend's grouped few-row MatMuls and epilo
 NO_NORM_FUSION = 4       # keep each RmsNorm between few-row MatMuls as its own launch
 NO_DEQUANT_FUSION = 8    # skip the loader's fuse_dequant_matmul / fuse_dequant_activation
 NO_WEIGHT_PACKING = 16   # keep few-row groups over constant weights on the split-K launches
+NO_ATTN_PROLOGUE = 32    # keep the q/k/v group's split-K epilogue out of the decode attention's launch
 
 
 class HipSession:
     """`backend=None` loads dry: parse, size and validate every call on the host,
     with no device (such a session reports ports and refuses to execute).
     `flags` turns the load-time fusions off (NO_EPILOGUE_FUSION, NO_DEVICE_FUSION,
-    NO_NORM_FUSION, NO_DEQUANT_FUSION, NO_WEIGHT_PACKING);
+    NO_NORM_FUSION, NO_DEQUANT_FUSION, NO_WEIGHT_PACKING, NO_ATTN_PROLOGUE);
     fused and unfused walks give the same bits."""
 
     def __init__(self, backend: HipBackend | None, archive: bytes, flags: int = 0):
@@ -163,6 +164,14 @@ class HipSession:
         g, b = ctypes.c_uint32(), ctypes.c_uint64()
         _check(self._lib.holo_hip_session_packed(self.handle, ctypes.byref(g), ctypes.byref(b)))
         return g.value, b.value
+
+    @property
+    def attn_prologues(self) -> int:
+        """Fused groups whose split-K epilogue runs in the decode attention's
+        launch after them (decided at load)."""
+        n = ctypes.c_uint32()
+        _check(self._lib.holo_hip_session_attn_prologues(self.handle, ctypes.byref(n)))
+        return n.value
 
     def set_memo(self, enabled: bool) -> None:
         """The memo's hits on (default) or off (every execute walks)."""

@@ -560,12 +560,18 @@ int holo_hip_session_load(holo_backend *be, const uint8_t *archive, size_t len,
  * stays), a workgroup owns a 16-column tile (a SwiGLU tile pair, a head) over
  * the whole of K, and a fused RmsNorm's statistics are taken in that launch;
  * the few-row product's summation order is fixed by K alone, so this too is
- * bit-identical. NO_WEIGHT_PACKING keeps the split-K launches. */
+ * bit-identical. NO_WEIGHT_PACKING keeps the split-K launches. A decode
+ * step's q/k/v group (every product head-wise: RoPE and / or the int8 append)
+ * followed by the int8 decode attention over what it wrote leaves its split-K
+ * epilogue to that attention's launch, each workgroup finishing its own
+ * plane's heads first (the same device code, so the same bits);
+ * NO_ATTN_PROLOGUE keeps the epilogue a launch of its own. */
 #define HOLO_SESSION_NO_EPILOGUE_FUSION 1u
 #define HOLO_SESSION_NO_DEVICE_FUSION 2u
 #define HOLO_SESSION_NO_NORM_FUSION 4u
 #define HOLO_SESSION_NO_DEQUANT_FUSION 8u
 #define HOLO_SESSION_NO_WEIGHT_PACKING 16u
+#define HOLO_SESSION_NO_ATTN_PROLOGUE 32u
 int holo_hip_session_load_ex(holo_backend *be, const uint8_t *archive, size_t len, uint32_t flags,
                              holo_session **out);
 /* Steps of one walk after fusion (each a call or a fused MatMul group), and
@@ -582,6 +588,12 @@ int holo_hip_session_last_walk(const holo_session *s, uint32_t *dispatched, uint
  * bytes the packed copies of their weights hold (no counterpart in the
  * reference: its CPU kernels read weights in place). */
 int holo_hip_session_packed(const holo_session *s, uint32_t *groups, uint64_t *bytes);
+/* Fused groups that leave their split-K epilogue to the int8 decode attention
+ * after them (NO_ATTN_PROLOGUE; no counterpart in the reference). Decided at
+ * load; a launch shape the fused kernel does not take (more than one chunk a
+ * plane, the balanced form, head_dim other than 64 / 128, f32) runs the
+ * epilogue on its own at dispatch. */
+int holo_hip_session_attn_prologues(const holo_session *s, uint32_t *n);
 /* The index-th kernel call of the loaded schedule, after the reference's
  * loader passes (the calls the reference's Session counts with
  * dequant_fused_count and its siblings, session.rs:1390-1437). */

@@ -18,7 +18,7 @@ from hologram_amd import (DTYPE_BF16, DTYPE_F32, BinaryCall, BufferRef, HipSessi
                           MatMulAddCall, MatMulCall, NormCall, PortDescriptor, SlotOutOfRange, UnaryCall,
                           UnsupportedOp, decode_call, fused_activation, validate)
 from hologram_amd.decoder_graph import DecoderConfig, build_decode_step, init_weights
-from hologram_amd.session import (NO_DEVICE_FUSION, NO_EPILOGUE_FUSION, NO_NORM_FUSION,
+from hologram_amd.session import (NO_ATTN_PROLOGUE, NO_DEVICE_FUSION, NO_EPILOGUE_FUSION, NO_NORM_FUSION,
                                   NO_WEIGHT_PACKING)
 
 M, K, N = 4, 64, 32
@@ -156,6 +156,12 @@ def test_decoder_walk_counts():
     # other Wd + Add steps write the statistics a split-K q/k/v group reads
     assert full.n_nodes == 1 + 5 * L + 3 and full.n_groups == 4 * L + 1
     assert full.packed[0] == 2 * L + 2
+    # each layer's q/k/v group leaves its split-K epilogue (RoPE, int8 appends)
+    # to the decode attention after it; the node count does not change
+    assert full.attn_prologues == L and split.attn_prologues == L
+    off = HipSession(None, a, flags=NO_ATTN_PROLOGUE)
+    assert off.attn_prologues == 0 and off.n_nodes == full.n_nodes
+    assert ref.attn_prologues == 0 and plain.attn_prologues == 0
 
 
 def norm(x, g, o, rows, feat, dt=DTYPE_BF16):

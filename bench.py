@@ -15,7 +15,8 @@ for the headline, and around a batch of back-to-back calls for the components
 (queued_ms), whose kernels are short enough that per-call events would count
 the host's dispatch latency. A component that rotates buffers (past the 256 MB
 last-level cache) first calls once on every set, untimed (at least W calls),
-so no timed call is a set's first touch.
+so no timed call is a set's first touch; each GEMM shape also runs a quarter
+second untimed first, so the clocks have ramped up after the host-side legs.
 """
 from __future__ import annotations
 
@@ -107,6 +108,18 @@ def queued_ms(torch, fn, n):
     e.record()
     torch.cuda.synchronize()
     return s.elapsed_time(e) / n
+
+
+def warm(torch, fn, seconds):
+    """Untimed calls of fn(i) for at least `seconds` of wall time: a GPU that
+    sat idle (behind a host-side leg) ramps its clocks back up before the
+    timed calls, instead of during them."""
+    t0, i = time.perf_counter(), 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(4):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
 
 
 def cpu_time(fn, min_seconds):
@@ -410,6 +423,7 @@ def bench_gemm(torch, be, args, rep):
             for i in range(max(args.warmup, nbuf)):
                 be.dispatch(calls[i % nbuf], ws)
             be.synchronize()
+            warm(torch, lambda i: be.dispatch(calls[i % nbuf], ws), 0.25)
             steps = args.steps if m * n * k < 8192 ** 3 else max(3, args.steps // 4)
             ms = queued_ms(torch, lambda i: be.dispatch(calls[i % nbuf], ws), steps)
             tf = 2.0 * m * n * k / (ms / 1e3) / 1e12
@@ -821,9 +835,40 @@ def rounded(x, sig=4):
     return x
 
 
+def slim_roofline(rl):
+    """A component's roofline in short form: achieved (in unit), the fraction
+    of MI355X's peak for that unit (bound and peak follow from the unit), and
+    the profiled HBM traffic when there is one."""
+    out = {"achieved": rl["achieved"], "unit": rl["unit"], "frac": rl["frac"]}
+    if rl.get("traffic"):
+        out["traffic"] = rl["traffic"]
+    return out
+
+
+def slim_cpu(cb):
+    """A component's cpu_baseline in short form (host threads and kind are the
+    top-level record's; the samples are listed in bench.py's legs)."""
+    return {"value": cb["value"], "unit": cb["unit"], "single_thread": cb.get("single_thread")}
+
+
 def compact_components(rep):
     """One short record per config leg: the headline figure, its roofline
-    object and its cpu_baseline (figures only; the host is reported once)."""
+    and its cpu_baseline in short form (figures only; the host is reported
+    once), so the whole line stays a few KB."""
+    comps = compact_full(rep)
+
+    def walk(o):
+        if isinstance(o, dict):
+            if "achieved" in o and "peak" in o and "frac" in o:
+                return slim_roofline(o)
+            if "kind" in o and "cores" in o and "value" in o:
+                return slim_cpu(o)
+            return {k: walk(v) for k, v in o.items()}
+        return o
+    return walk(comps)
+
+
+def compact_full(rep):
     comps = {}
     if "lut" in rep:
         cp = rep.get("copy", {}).get("copy16_kernel", {}).get("us")

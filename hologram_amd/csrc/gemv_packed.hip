@@ -434,19 +434,22 @@ constexpr uint32_t kMaxDynLds = 65536;
 uint32_t packed_lds_bytes(uint32_t m, uint32_t k) { return m * (k / 8 + 1) * 16; }
 
 bool packed_group_applies(uint32_t m, uint32_t k, const EpiSeg *segs, int nseg, bool norm) {
-    if (m == 0 || m > 16 || k == 0 || k % 32 != 0 || k > 8192 || nseg < 1 || nseg > kSkinnyMaxSeg)
+    // At most two 32-k steps a chain (K <= 4096): four (K = 8192, Wd) would
+    // hold a chain's B and A operands in 128 registers at 1024 threads only by
+    // spilling, and a workgroup owning all of such a K also reads the whole of
+    // A (as many bytes as its weights), so K beyond 4096 stays split-K.
+    if (m == 0 || m > 16 || k == 0 || k % 32 != 0 || k > 4096 || nseg < 1 || nseg > kSkinnyMaxSeg)
         return false;
     // the norm is taken on the LDS copy of A
     if (norm && packed_lds_bytes(m, k) > kMaxDynLds) return false;
     // Where a workgroup owning all of K loses to the split-K launch and its
     // epilogue (measured per decode shape on one box, weights streamed from
-    // HBM): K beyond 4096 (Wd, 8192 x 2048: 12.2 against 11.5 us), more than
-    // 1024 sixteen-column tiles (an LM head of 32000 columns: 35.9 against
-    // 34.1 us), and the int8 append, whose row maximum needs a whole head in
-    // one workgroup (q/k/v: 11.3 against 9.7 us). It wins where the
-    // epilogue's launch is a large share: Wo + residual 6.5 against 7.7 us,
-    // gate/up + SwiGLU 20.4 against 21.3 us.
-    if (k > 4096 || uint64_t(m) * k * 2 >= (1ull << 31)) return false;
+    // HBM): more than 1024 sixteen-column tiles (an LM head of 32000 columns:
+    // 35.9 against 34.1 us), and the int8 append, whose row maximum needs a
+    // whole head in one workgroup (q/k/v: 11.3 against 9.7 us). It wins where
+    // the epilogue's launch is a large share: Wo + residual 6.5 against 7.7
+    // us, gate/up + SwiGLU 20.4 against 21.3 us.
+    if (uint64_t(m) * k * 2 >= (1ull << 31)) return false;
     uint32_t units = 0, tiles = 0;
     for (int i = 0; i < nseg; ++i) {
         const EpiSeg &s = segs[i];
@@ -512,7 +515,8 @@ hipError_t launch_packed_group(const PackedGroup &pg, hipStream_t stream) {
         units += packed_units(s, tpu, tw);
         g.unit_end[i] = units;
     }
-    if (nt * spc_t > 4) return hipErrorInvalidValue;
+    // the kernels are instantiated for at most two steps a chain (K <= 4096)
+    if (spc_t > 2 || nt * spc_t > 4) return hipErrorInvalidValue;
     const uint32_t lds = packed_lds_bytes(pg.m, pg.k);
     const bool ldsa = lds <= kMaxDynLds && spc_t <= 2;
     if (g.norm && !ldsa) return hipErrorInvalidValue;

@@ -451,7 +451,8 @@ def bench_fewrow_packed(torch, be, args, m, k, n):
     the session packs the weight at load and runs the product as one launch
     (gemv_packed.hip) instead of split-K plus a reduce. One archive holds
     `nbuf` such products over different weights (rotated past the 256 MB
-    Infinity Cache), A = 2x computed in-graph; the captured walk is replayed
+    Infinity Cache), each over its own A (a slice of 2x, computed in-graph by
+    one Add), so no two products share a launch; the captured walk is replayed
     and the time per product is the replay's GPU time over nbuf (the one Add
     included)."""
     import numpy as np
@@ -461,17 +462,20 @@ def bench_fewrow_packed(torch, be, args, m, k, n):
     rng = np.random.default_rng(args.seed + 9)
     r = lambda slot, elems: BufferRef(slot, 0, 2 * elems)
     w = HoloWriter()
-    w.kernel_calls = [KernelCall.Add(BinaryCall(r(0, m * k), r(0, m * k), r(1, m * k), m * k, 16, DTYPE_BF16))]
+    mk = m * k
+    w.kernel_calls = [KernelCall.Add(BinaryCall(r(0, nbuf * mk), r(0, nbuf * mk), r(1, nbuf * mk),
+                                                nbuf * mk, 16, DTYPE_BF16))]
     for i in range(nbuf):
         wt = (rng.standard_normal(k * n, dtype=np.float32) / np.float32(np.sqrt(k))).view(np.uint32) >> 16
         w.constants.append(ConstantEntry(2 + 2 * i, DTYPE_BF16, wt.astype(np.uint16).tobytes()))
-        w.kernel_calls.append(KernelCall.MatMul(MatMulCall(r(1, m * k), r(2 + 2 * i, k * n), r(3 + 2 * i, m * n),
+        a_i = BufferRef(1, 2 * mk * i, 2 * mk)      # product i's own A: a slice of 2x
+        w.kernel_calls.append(KernelCall.MatMul(MatMulCall(a_i, r(2 + 2 * i, k * n), r(3 + 2 * i, m * n),
                                                            m, k, n, DTYPE_BF16)))
         w.outputs.append(PortDescriptor(f"y{i}", 3 + 2 * i, m * n, DTYPE_BF16, [m, n]))
-    w.inputs = [PortDescriptor("x", 0, m * k, DTYPE_BF16, [m, k])]
+    w.inputs = [PortDescriptor("x", 0, nbuf * mk, DTYPE_BF16, [nbuf * m, k])]
     sess = HipSession(be, w.finish())
     packed = sess.packed[0]
-    x = (rng.standard_normal(m * k, dtype=np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    x = (rng.standard_normal(nbuf * m * k, dtype=np.float32).view(np.uint32) >> 16).astype(np.uint16)
     sess.write_input(0, x.tobytes())
     sess.capture()
     sess.synchronize()
@@ -491,7 +495,8 @@ def bench_fewrow_packed(torch, be, args, m, k, n):
     us = ev[0].elapsed_time(ev[1]) * 1e3 / (reps * nbuf)
     gbs = (m * k + k * n + m * n) * 2 / (us / 1e6) / 1e9
     sess.close()
-    return {"us": us, "launches_per_product": 1, "packed_groups": packed,
+    # each packed group is one launch over one product's weights
+    return {"us": us, "launches_per_product": packed / nbuf, "packed_groups": packed,
             "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s", None)}
 
 

@@ -9,9 +9,9 @@ own (NO_ATTN_PROLOGUE) and of the unfused walk (NO_DEVICE_FUSION): tokens,
 logits, caches and scales over several steps.
 
 Shapes: head_dim 64 and 128 at 32 planes (eight waves a plane) and 160 planes
-(four); and shapes the fused launch does not take, where the epilogue runs on
-its own at dispatch: 8 planes (the balanced split form) and head_dim 32 (the
-generic kernel)."""
+(four); a bucket the appends wrap (12 steps over 8 rows); and shapes the fused
+launch does not take, where the epilogue runs on its own at dispatch: 8 planes
+(the balanced split form) and head_dim 32 (the generic kernel)."""
 import numpy as np
 import pytest
 
@@ -28,6 +28,10 @@ CFGS = {
                                    vocab=256, batch=8, bucket=128),
     "d64_160planes": DecoderConfig(layers=1, hidden=256, heads=8, kv_heads=4, head_dim=64, ffn=512,
                                    vocab=256, batch=40, bucket=64),
+    # a bucket of 8 rows walked for 12 steps: the appends wrap the ring (the
+    # appended row at pos % bucket, every row visible)
+    "d64_ring_wrap": DecoderConfig(layers=1, hidden=256, heads=8, kv_heads=4, head_dim=64, ffn=512,
+                                   vocab=256, batch=8, bucket=8),
     "split_form": DecoderConfig(layers=1, hidden=256, heads=4, kv_heads=2, head_dim=64, ffn=512,
                                 vocab=256, batch=4, bucket=64),
     "d32_generic": DecoderConfig(layers=1, hidden=256, heads=8, kv_heads=4, head_dim=32, ffn=512,
@@ -77,11 +81,12 @@ def decode(backend, cfg, archive, flags, steps, capture=False):
 @pytest.mark.parametrize("name", list(CFGS))
 def test_prologue_walk_bit_identical(torch_cuda, backend, name):
     cfg = CFGS[name]
+    steps = 12 if cfg.bucket < 12 else 5
     archive = build_decode_step(cfg, init_weights(cfg, seed=11))
-    fused, n = decode(backend, cfg, archive, 0, 5)
+    fused, n = decode(backend, cfg, archive, 0, steps)
     assert n == cfg.layers
     for flags in (NO_ATTN_PROLOGUE, NO_DEVICE_FUSION):
-        other, m = decode(backend, cfg, archive, flags, 5)
+        other, m = decode(backend, cfg, archive, flags, steps)
         assert m == 0
         for step, (x, y) in enumerate(zip(fused, other)):
             for o, (u, v) in enumerate(zip(x, y)):

@@ -4,8 +4,8 @@
  * The reference's operator API is the Rust trait
  *     Backend::dispatch(&mut self, &KernelCall, &mut Workspace) -> Result<(), BackendError>
  * (crates/hologram-compute/src/backend.rs:8-15). This header is that boundary as
- * a C ABI: a Rust `Backend` impl binds these functions one to one (the shim is
- * in INTEGRATION.md). Buffers are device-resident: the caller's content-addressed
+ * a C ABI: a Rust `Backend` impl binds these functions one to one, falling
+ * back to the CPU backend for UnsupportedOp. Buffers are device-resident: the caller's content-addressed
  * pool (crates/hologram-exec/src/buffer.rs:149-207) binds each slot to a device
  * allocation it owns, and kernels read/write the slots in place — no per-call
  * host round trip.

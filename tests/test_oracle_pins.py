@@ -234,7 +234,7 @@ def test_table_special_values_follow_x86_semantics():
     assert g[0x7F80] == 0x7F80          # GELU(+Inf) = +Inf
     assert s[0x7F80] == 0x7F80 and s[0xFF80] == 0xFF80
     assert g[0x7FC1] == 0x7FC1          # quiet NaN input propagates
-    assert s[0x7F81] == 0x7FC1          # signaling NaN is quieted (IEEE)
+    assert s[0x7F81] == 0x7FC1          # signaling NaN is quieted (IEEE arithmetic on it)
     e = oracle.build_table(oracle.ACT_EXP, BF16)
     assert e[0x0000] == 0x3F80 and e[0x8000] == 0x3F80   # exp(+-0) = 1
     assert e[0x7F81] == 0x7F81          # libm returns a NaN input unchanged

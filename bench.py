@@ -437,6 +437,17 @@ def bench_gemm(torch, be, args, rep):
                 rl = roofline("mfma", tf, peak, "TFLOP/s", profiled_traffic(tkey))
             res[key] = {"tflops": tf, "ms": ms, "hbm_gbs": gbs, "roofline": rl,
                         "rotation_bytes": nbuf * set_bytes}
+            if dt == DTYPE_BF16 and m == n == k:
+                # the vendor library on the same box and the same rotated
+                # operands (torch.matmul -> hipBLASLt), for comparison only
+                mats = [(keep[i][0].view(m, k), keep[i][1].view(k, n),
+                         torch.empty(m, n, dtype=tdt, device="cuda")) for i in range(nbuf)]
+                vend = lambda i: torch.matmul(mats[i % nbuf][0], mats[i % nbuf][1],
+                                              out=mats[i % nbuf][2])
+                warm(torch, vend, 0.25)
+                vms = queued_ms(torch, vend, steps)
+                res[key]["hipblaslt_tflops"] = 2.0 * m * n * k / (vms / 1e3) / 1e12
+                del mats
             if not args.no_cpu:
                 res[key]["cpu_baseline"] = cpu_gemm(keep[0], m, k, n, dt,
                                                     single=(m == 1024 or m <= 64))
@@ -908,6 +919,8 @@ def compact_full(rep):
             g[k] = {"us": v["ms"] * 1e3 if "ms" in v else v["us"], "roofline": v["roofline"]}
             if "launches_per_product" in v:
                 g[k]["launches_per_product"] = v["launches_per_product"]
+            if "hipblaslt_tflops" in v:
+                g[k]["hipblaslt_tflops"] = v["hipblaslt_tflops"]
             if "cpu_baseline" in v:
                 g[k]["cpu_baseline"] = v["cpu_baseline"]
         comps["c2_gemm"] = g

@@ -282,22 +282,37 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const void *__restrict__ i
         }
     };
     // 16-byte vectors when the row start is aligned; each thread's vectors are
-    // ascending in index, so a strict > keeps the first index of its maximum
-    const bool vec = ((reinterpret_cast<uintptr_t>(in) + row * (kBf16 ? 2 : 4)) & 15) == 0;
+    // ascending in index, so a strict > keeps the first index of its maximum.
+    // Four vectors a thread are loaded before any is compared (one memory
+    // round trip per 4096 vectors, not one per 1024); a vector past the row
+    // reads zero from its buffer range and is not compared.
+    const bool vec = ((reinterpret_cast<uintptr_t>(in) + row * (kBf16 ? 2 : 4)) & 15) == 0 &&
+                     uint64_t(cols / E) * 16u < (uint64_t(1) << 32);   // a 32-bit buffer range
     uint32_t j0 = 0;
     if (vec) {
-        const u32x4 *r4 = reinterpret_cast<const u32x4 *>(static_cast<const char *>(in) +
-                                                          row * (kBf16 ? 2 : 4));
         const uint32_t nv = cols / E;
-        for (uint32_t v = threadIdx.x; v < nv; v += 1024) {
-            const u32x4 x = r4[v];
+        const auto rr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<char *>(static_cast<const char *>(in) + row * (kBf16 ? 2 : 4)), 0,
+            int(nv * 16u), 0x00020000);
+        for (uint32_t v0 = threadIdx.x; v0 < nv; v0 += 4 * 1024) {
+            u32x4 x[4];
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                if constexpr (kBf16) {
-                    take(__uint_as_float(x[w] << 16), int(v * E + 2 * w));
-                    take(__uint_as_float(x[w] & 0xFFFF0000u), int(v * E + 2 * w + 1));
-                } else {
-                    take(__uint_as_float(x[w]), int(v * E + w));
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t v = v0 + 1024u * u;
+                x[u] = __builtin_amdgcn_raw_buffer_load_b128(rr, v < nv ? 16u * v : 0x80000000u, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t v = v0 + 1024u * u;
+                if (v >= nv) break;
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    if constexpr (kBf16) {
+                        take(__uint_as_float(x[u][w] << 16), int(v * E + 2 * w));
+                        take(__uint_as_float(x[u][w] & 0xFFFF0000u), int(v * E + 2 * w + 1));
+                    } else {
+                        take(__uint_as_float(x[u][w]), int(v * E + w));
+                    }
                 }
             }
         }

@@ -190,21 +190,28 @@ def test_gather_out_of_range_is_reported(torch_cuda, backend):
 
 
 @pytest.mark.parametrize("dtype", [DTYPE_BF16, DTYPE_F32])
-def test_argmax(torch_cuda, backend, dtype):
+@pytest.mark.parametrize("cols", [32000, 100003, 131072])
+def test_argmax(torch_cuda, backend, dtype, cols):
+    """Rows of one to several rounds of the kernel's four vectors a thread
+    (32768 bf16 / 16384 f32 elements a round), odd lengths whose later rows
+    start unaligned (the element loop), ties across rounds, NaN rows."""
     rng = np.random.default_rng(7)
-    rows, cols = 9, 32000
+    rows = 9
     x32 = rng.standard_normal((rows, cols)).astype(np.float32)
     x32[3, :] = 1.0                              # all equal: index 0
     x32[4, 100] = x32[4, 20000] = 50.0           # a tie: the lower index
     x32[5, :] = np.nan
     x32[6, 10] = np.nan
     x32[6, 11] = 60.0
+    x32[7, cols - 1] = x32[7, cols // 2 + 1] = 70.0   # a tie in later rounds
+    x32[8, cols - 1] = 80.0                      # the last element
     x = bf(x32) if dtype == DTYPE_BF16 else x32
     call = KernelCall.ArgMax(ArgMaxCall(BufferRef(1), BufferRef(2), rows, cols, dtype))
     got = run(torch_cuda, backend, call, {1: x}, rows * 4, 2).view(np.int32)
     want = np.zeros(rows, np.int32)
     lib().or_argmax(_p(x), _p(want), rows, cols, dtype)
     assert np.array_equal(got, want) and got[3] == 0 and got[4] == 100 and got[6] == 11
+    assert got[7] == cols // 2 + 1 and got[8] == cols - 1
 
 
 # ------------------------------------------------------------- session -----

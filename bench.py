@@ -201,6 +201,8 @@ def bench_attn(torch, be, args, rep):
     for i in range(args.warmup):
         be.dispatch(calls[i % nq], ws)
     be.synchronize()
+    # (1) each dispatch between its own pair of events, as the host issues
+    # them one at a time (the wall clock of the K steps is taken here)
     timer = Timer(torch)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -210,13 +212,18 @@ def bench_attn(torch, be, args, rep):
     be.synchronize()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms = timer.mean_ms()
+    ms_each = timer.mean_ms()
+    # (2) the headline: the same K steps queued back to back behind a spin
+    # kernel, events around the batch, so no step waits on the host's Python
+    # dispatch (a serving loop issues asynchronously)
+    ms = queued_ms(torch, lambda i: be.dispatch(calls[i % nq], ws), args.steps)
     sum_l = int(lens.sum())
     kv_bytes = sum_l * Hkv * (2 * D + 8)          # int8 K and V rows + two f32 scales
     alg_bytes = kv_bytes + B * H * D * 2 * 2 + B * 4
     flops = 4.0 * D * H * sum_l
     res = {
-        "tok_s": B / (ms / 1e3), "ms": ms, "wall_ms_per_step": wall * 1e3 / args.steps,
+        "tok_s": B / (ms / 1e3), "ms": ms, "ms_events_per_dispatch": ms_each,
+        "wall_ms_per_step": wall * 1e3 / args.steps,
         "hbm_gbs": alg_bytes / (ms / 1e3) / 1e9, "alg_bytes": alg_bytes, "sum_len": sum_l,
         "gflops": flops / 1e9, "lens_seed": args.seed,
     }
@@ -1002,8 +1009,11 @@ def main():
         import oracle
         line["host"] = oracle.host_info()
     line["components"] = compact_components(rep)
-    line["timing"] = ("headline: HIP events per step; components: HIP events around "
-                      "back-to-back calls queued behind a spin kernel (GPU time per call)")
+    line["timing"] = ("headline and components: HIP events around back-to-back calls queued "
+                      "behind a spin kernel (GPU time per call)")
+    if attn:
+        line["ms_events_per_dispatch"] = attn["ms_events_per_dispatch"]
+        line["wall_ms_per_step"] = attn["wall_ms_per_step"]
     line["bench_wall_s"] = time.perf_counter() - t_all
     line = rounded(line)
     print(json.dumps(line, separators=(",", ":")))

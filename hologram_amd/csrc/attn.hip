@@ -718,16 +718,28 @@ __global__ __launch_bounds__(kThreads, 2) void attn_prompt_kernel(
             for (int r = 0; r < 16; ++r) o[db][qb][r] = 0.0f;
     float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
 
+    // A tile's K, V and scales come into registers one tile ahead (branch-free
+    // buffer loads: a key past the bucket reads zero), so the loads of tile
+    // j0 + 64 are in flight while tile j0 is computed. Thread: key tid / 4,
+    // dims 16 (tid % 4) .. +15; threads below 64 also take one k-scale.
+    const auto rk = rsrc(kp, bucket * 64u), rv = rsrc(vp, bucket * 64u);
+    const auto rks = rsrc(ksp, bucket * 4u), rvs = rsrc(vsp, bucket * 4u);
+    const uint32_t fkey = uint32_t(tid) >> 2, fd0 = (uint32_t(tid) & 3u) * 16u;
+    u32x4 kr, vr;
+    float vsc, ksv;
+    auto fetch = [&](uint32_t j0) {
+        const uint32_t j = j0 + fkey;
+        kr = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, j * 64u + fd0, 0, 0));
+        vr = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, j * 64u + fd0, 0, 0));
+        vsc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rvs, j * 4u, 0, 0));
+        ksv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                            rks, tid < int(kPT) ? (j0 + uint32_t(tid)) * 4u : 0x80000000u, 0, 0));
+    };
+    fetch(0);
     for (uint32_t j0 = 0; j0 < kmax; j0 += kPT) {
         __syncthreads();   // the previous tile's readers are done
         {
-            // thread: key tid / 4, dims 16 (tid % 4) .. +15
-            const uint32_t key = tid >> 2, d0 = (tid & 3) * 16, j = j0 + key;
-            u32x4 kr = u32x4{0u, 0u, 0u, 0u}, vr = kr;
-            if (j < bucket) {
-                kr = *reinterpret_cast<const u32x4 *>(kp + uint64_t(j) * 64 + d0);
-                vr = *reinterpret_cast<const u32x4 *>(vp + uint64_t(j) * 64 + d0);
-            }
+            const uint32_t key = fkey, d0 = fd0;
             u32x4 k0, k1;
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
@@ -744,17 +756,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_prompt_kernel(
             }
             *reinterpret_cast<u32x4 *>(kl + key * kPLd + d0) = k0;
             *reinterpret_cast<u32x4 *>(kl + key * kPLd + d0 + 8) = k1;
-            const float vsc = j < bucket ? vsp[j] : 0.0f;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const _Float16 vh = _Float16(float(int8_t((vr[i / 4] >> (8 * (i % 4))) & 0xff)) * vsc);
                 vt[(d0 + i) * kPLd + key] = __builtin_bit_cast(uint16_t, vh);
             }
-            if (tid < int(kPT)) {
-                const uint32_t jj = j0 + tid;
-                ksl[tid] = jj < bucket ? ksp[jj] * mul : 0.0f;
-            }
+            if (tid < int(kPT)) ksl[tid] = ksv * mul;
         }
+        fetch(j0 + kPT);   // the next tile (past kmax: loads nobody stages)
         __syncthreads();
 
         // S^T for key blocks kb and row blocks qb

@@ -858,37 +858,92 @@ def rounded(x, sig=4):
     return x
 
 
-def slim_roofline(rl):
-    """A component's roofline in short form: achieved (in unit), the fraction
-    of MI355X's peak for that unit (bound and peak follow from the unit), and
-    the profiled HBM traffic when there is one."""
-    out = {"achieved": rl["achieved"], "unit": rl["unit"], "frac": rl["frac"]}
-    if rl.get("traffic"):
-        out["traffic"] = rl["traffic"]
-    return out
+def _n(x):
+    """Four significant digits, without an exponent for large figures."""
+    return f"{x:.0f}" if abs(x) >= 1e4 else f"{x:.4g}"
 
 
-def slim_cpu(cb):
-    """A component's cpu_baseline in short form (host threads and kind are the
-    top-level record's; the samples are listed in bench.py's legs)."""
-    return {"value": cb["value"], "unit": cb["unit"], "single_thread": cb.get("single_thread")}
+def _pct(rl):
+    return f"{100 * rl['frac']:.1f}%"
+
+
+def _tr(rl, alg):
+    """Profiled HBM bytes over algorithmic bytes, when a counter pass exists."""
+    t = rl.get("traffic")
+    return f" tr{t / alg:.2f}" if t and alg else ""
+
+
+def _cpu(cb):
+    st = cb.get("single_thread")
+    return f"{_n(cb['value'])}{cb['unit']}" + (f" ({_n(st)} 1thr)" if st else "")
 
 
 def compact_components(rep):
-    """One short record per config leg: the headline figure, its roofline
-    and its cpu_baseline in short form (figures only; the host is reported
-    once), so the whole line stays a few KB."""
+    """One short string per leg's figure: time per call, rate, the fraction of
+    MI355X's peak for its bound (HBM 8 TB/s, or dense MFMA), the profiled
+    traffic ratio (tr: HBM bytes / algorithmic bytes) and the cpu_baseline.
+    The whole record stays about 1.5 KB and is printed last on the line, so a
+    log tail of 2000 characters holds every leg."""
     comps = compact_full(rep)
-
-    def walk(o):
-        if isinstance(o, dict):
-            if "achieved" in o and "peak" in o and "frac" in o:
-                return slim_roofline(o)
-            if "kind" in o and "cores" in o and "value" in o:
-                return slim_cpu(o)
-            return {k: walk(v) for k, v in o.items()}
-        return o
-    return walk(comps)
+    out = {"key": "us/call, rate, % of peak (hbm 8 TB/s; mfma bf16 2.5 / f32 0.157 PF), "
+                  "tr = HBM/alg bytes, cpu = cpu_baseline (gemm: TF/s, 16 threads)"}
+    if "c1_lut_bf16_16M" in comps:
+        c = comps["c1_lut_bf16_16M"]
+        d = {k: f"{v['us']:.4g}us {_n(v['gelem_s'])}Gelem/s {_pct(v['roofline'])}hbm"
+                f"{_tr(v['roofline'], 2 * 16 * 2 ** 20 * 2)}"
+             for k, v in c.items() if k != "cpu_baseline"}
+        if "cpu_baseline" in c:
+            d["cpu"] = _cpu(c["cpu_baseline"])
+        out["c1_lut_bf16_16M"] = d
+    if "copy_ceiling_64MiB" in comps:
+        c = comps["copy_ceiling_64MiB"]
+        out["copy_64MiB"] = (f"{c['us']:.4g}us {_pct(c['roofline'])}hbm "
+                             f"hipMemcpy {c['hip_memcpy_us']:.4g}us")
+    if "c3_kv_append" in comps:
+        c = comps["c3_kv_append"]
+        d = {"copy": f"{c['copy']['us_per_step']:.4g}us/step {_pct(c['copy']['roofline'])}hbm",
+             "in_place": f"{c['in_place']['us_per_step']:.4g}us/step "
+                         f"{c['in_place']['vs_launch_floor']:.3g}x the {c['launch_floor_us']:.3g}us launch floor"}
+        if "cpu_baseline" in c:
+            d["cpu"] = _cpu(c["cpu_baseline"])
+        out["c3_kv_append"] = d
+    if "c2_gemm" in comps:
+        d = {}
+        for k, v in comps["c2_gemm"].items():
+            rl = v["roofline"]
+            parts = [f"{v['us']:.4g}us", f"{rl['achieved']:.4g}{'TF' if rl['unit'] == 'TFLOP/s' else 'GB/s'}",
+                     _pct(rl) + ("mfma" if rl["unit"] == "TFLOP/s" else "hbm")]
+            if "hipblaslt_tflops" in v:
+                parts.append(f"hipblaslt {v['hipblaslt_tflops']:.4g}TF")
+            if "launches_per_product" in v:
+                parts.append(f"{v['launches_per_product']:.3g} launch")
+            if "cpu_baseline" in v:
+                parts.append(f"cpu {_n(v['cpu_baseline']['value'])}")
+            d[k.replace("1024x1024x1024", "1024^3").replace("4096x4096x4096", "4096^3")
+               .replace("8192x8192x8192", "8192^3")] = " ".join(parts)
+        out["c2_gemm"] = d
+    if "w8a8_gemv" in comps:
+        c = comps["w8a8_gemv"]
+        d = {k: f"{v['us']:.4g}us {_n(v['gmac_s'])}GMAC/s {_pct(v['roofline'])}hbm"
+             for k, v in c.items() if k != "cpu_baseline"}
+        if "cpu_baseline" in c:
+            d["cpu"] = _cpu(c["cpu_baseline"])
+        out["w8a8_gemv"] = d
+    if "c5_e2e_1b" in comps:
+        c = comps["c5_e2e_1b"]
+        d = {}
+        if "decode_ms_per_step" in c:
+            d["decode"] = (f"{c['decode_ms_per_step']:.4g}ms/step {_n(c['decode_tok_s'])}tok/s "
+                           f"{_pct(c['roofline'])}hbm")
+        if "prefill_ms" in c:
+            d["prefill"] = (f"{c['prefill_ms']:.4g}ms {_n(c['prefill_tok_s'])}tok/s "
+                            f"{_pct(c['prefill_roofline'])}mfma")
+        if "decode_walk" in c:
+            d["walk"] = f"{c['decode_walk']['calls']} calls, {c['decode_walk']['fused_groups']} fused"
+        if "cpu_baseline" in c:
+            d["cpu"] = _cpu(c["cpu_baseline"])
+        out["c5_e2e_1b"] = d
+    return out
 
 
 def compact_full(rep):
@@ -1008,7 +1063,6 @@ def main():
     if not args.no_cpu:
         import oracle
         line["host"] = oracle.host_info()
-    line["components"] = compact_components(rep)
     line["timing"] = ("headline and components: HIP events around back-to-back calls queued "
                       "behind a spin kernel (GPU time per call)")
     if attn:
@@ -1016,6 +1070,7 @@ def main():
         line["wall_ms_per_step"] = attn["wall_ms_per_step"]
     line["bench_wall_s"] = time.perf_counter() - t_all
     line = rounded(line)
+    line["components"] = compact_components(rep)   # last: a log tail keeps every leg
     print(json.dumps(line, separators=(",", ":")))
 
 

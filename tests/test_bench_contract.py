@@ -1,7 +1,7 @@
 """CPU: bench.py's reporting contract, without a GPU. `--gpus` above 1 exits
 with a message (one GPU in this build); the component records are the short
-form (achieved, unit, frac, traffic; the cpu_baseline's value and single
-thread figure) and every leg keeps its headline figure; the rounding keeps
+form (one string per figure: time, rate, fraction of peak, traffic ratio,
+cpu_baseline) and every leg keeps its headline figure; the rounding keeps
 four significant digits."""
 import json
 import subprocess
@@ -61,21 +61,29 @@ def walk(o):
 
 
 def test_components_are_short_and_complete():
-    comps = bench.rounded(bench.compact_components(synthetic_report()))
-    assert set(comps) == {"c1_lut_bf16_16M", "copy_ceiling_64MiB", "c3_kv_append", "c2_gemm",
+    comps = bench.compact_components(bench.rounded(synthetic_report()))
+    assert set(comps) == {"key", "c1_lut_bf16_16M", "copy_64MiB", "c3_kv_append", "c2_gemm",
                           "w8a8_gemv", "c5_e2e_1b"}
-    for d in walk(comps):
-        assert "peak" not in d and "bound" not in d and "sample" not in d and "cores" not in d
-        if "frac" in d:
-            assert set(d) <= {"achieved", "unit", "frac", "traffic"} and d["unit"]
-    assert comps["c1_lut_bf16_16M"]["gelu"]["us"] == 11.6
-    assert comps["c1_lut_bf16_16M"]["gelu"]["vs_copy"] == round(10.9 / 11.6, 4)
-    assert comps["c2_gemm"]["bf16_8192x8192x8192"]["us"] == 100.0
-    assert comps["c2_gemm"]["bf16_8192x8192x8192"]["cpu_baseline"] == {
-        "value": 0.5, "unit": "x/s", "single_thread": 0.05}
-    assert comps["c2_gemm"]["bf16_16x4096x4096_packed"]["launches_per_product"] == 1.0
-    assert comps["c5_e2e_1b"]["decode_ms_per_step"] == 0.963
-    assert len(json.dumps(comps, separators=(",", ":"))) < 3000
+    # tr: the committed counter pass of the LUT kernel over its 64 MiB
+    assert comps["c1_lut_bf16_16M"]["gelu"] == "11.6us 1400Gelem/s 72.5%hbm tr1.02"
+    assert comps["c1_lut_bf16_16M"]["cpu"] == "30x/s (3 1thr)"
+    assert comps["copy_64MiB"] == "10.9us 76.2%hbm hipMemcpy 14us"
+    assert comps["c2_gemm"]["bf16_8192^3"] == "100us 1200TF 48.0%mfma cpu 0.5"
+    assert comps["c2_gemm"]["bf16_16x4096x4096_packed"] == "12.9us 2600GB/s 32.5%hbm 1 launch"
+    assert comps["c3_kv_append"]["in_place"] == "5.2us/step 1.7x the 1.55us launch floor"
+    assert comps["w8a8_gemv"]["i8_decode"] == "90us 6000GMAC/s 73.8%hbm"
+    assert comps["c5_e2e_1b"]["decode"] == "0.963ms/step 8300tok/s 28.1%hbm"
+    assert comps["c5_e2e_1b"]["prefill"] == "10.2ms 401000tok/s 31.8%mfma"
+    # every leg a real run reports, at full length, stays well inside a 2000-character tail
+    assert len(json.dumps(comps, separators=(",", ":"))) < 1500
+
+
+def test_traffic_ratio_is_reported():
+    rep = synthetic_report()
+    rep["lut"]["gelu"]["hbm_gbs"] = 5800.0
+    rl_ = rl(5800.0, 8000.0, "GB/s", 68185259)
+    assert bench._tr(rl_, 2 * 16 * 2 ** 20 * 2) == " tr1.02"
+    assert bench._tr(rl(1.0, 8000.0, "GB/s"), 100) == ""
 
 
 def test_rounding_keeps_four_digits():
